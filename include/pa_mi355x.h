@@ -1,0 +1,253 @@
+/*
+ * pa_mi355x.h — C ABI of the MI355X (gfx950) paged GQA KV-cache attention library.
+ *
+ * This is the seam the reference plugin EP crosses when it runs com.microsoft::PagedAttention:
+ * there the op handler builds an MLX graph (scatter into the flattened cache, page gather,
+ * SDPA, or a custom Metal vector kernel); here the same inputs are handed, as plain device
+ * pointers and sizes, to hand-written HIP kernels.  Nothing in this header uses torch, HIP or
+ * ORT types; hipStream_t is passed as the opaque `pa_stream_t`.
+ *
+ * Conventions
+ *   - Every entry point returns 0 on success or a PA_ERR_* code; pa_last_error() returns the
+ *     thread-local message of the last failure.  Messages raised while validating operator
+ *     metadata start with "PagedAttention:" like the reference's errors
+ *     (rust/src/ops/attention.rs:3938-3990).
+ *   - All tensor pointers are device pointers unless the field name starts with host_.
+ *   - No entry point allocates device memory except pa_pool_create; split-K partials live in
+ *     a caller-provided workspace sized by pa_attention_workspace_bytes.
+ *   - Work is enqueued on `stream`; nothing synchronises the host unless stated.
+ *
+ * Layouts (identical to the ORT operator contract the reference claims,
+ * rust/src/ops/attention.rs:4537-4560 and tests/ops/test_paged_attention.py:161-178):
+ *   query            [num_tokens, num_heads * head_dim]           activation dtype T
+ *   key, value       [num_tokens, kv_heads * head_dim]            T
+ *   key/value_cache  [num_blocks, block_size, kv_heads, head_dim] T (or e4m3 with per-(block,
+ *                    kv-head) fp32 scales for the fp8 cache, a build-defined extension)
+ *   cumulative_sequence_length [batch + 1] int32, past_seqlens [batch] int32,
+ *   block_table      [batch, max_blocks] int32, slot_mapping [num_tokens] int32 (-1 = skip)
+ *   cos/sin cache    [positions, rotary_dim / 2] T
+ *   output           [num_tokens, num_heads * head_dim] T
+ */
+#ifndef PA_MI355X_H
+#define PA_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* pa_stream_t; /* hipStream_t; NULL = the null stream */
+
+typedef enum pa_dtype {
+  PA_DTYPE_FLOAT16 = 1,
+  PA_DTYPE_BFLOAT16 = 2,
+  PA_DTYPE_FLOAT32 = 3,
+  PA_DTYPE_FP8_E4M3 = 4 /* OCP e4m3fn, cache storage only */
+} pa_dtype;
+
+#define PA_OK 0
+#define PA_ERR_INVALID_ARGUMENT 1
+#define PA_ERR_UNSUPPORTED 2
+#define PA_ERR_HIP 3
+#define PA_ERR_OUT_OF_MEMORY 4
+
+/* Thread-local text of the last failure on this thread ("" if none).
+ * Replaces the OrtStatus message path of the reference's FFI guard (rust/src/lib.rs:53-80). */
+const char* pa_last_error(void);
+const char* pa_version(void);
+
+/* ------------------------------------------------------------------------------------------ */
+/* Page pool: the HBM slab behind the cache tensors.  Replaces the MLX-backed "MLX" device
+ * OrtAllocator that hands out the cache tensors (rust/src/device.rs:415-486, created by
+ * factory.rs:266-286).  One hipMalloc per side, [num_blocks, block_size, kv_heads, head_dim]. */
+typedef struct pa_pool pa_pool;
+
+int pa_pool_create(int64_t num_blocks, int32_t block_size, int32_t kv_heads, int32_t head_dim,
+                   pa_dtype cache_dtype, pa_pool** out_pool);
+int pa_pool_destroy(pa_pool* pool);
+void* pa_pool_k_ptr(const pa_pool* pool);
+void* pa_pool_v_ptr(const pa_pool* pool);
+/* fp8 pools only: per-(block, kv-head) fp32 scales, [num_blocks, kv_heads]; NULL otherwise. */
+float* pa_pool_k_scale_ptr(const pa_pool* pool);
+float* pa_pool_v_scale_ptr(const pa_pool* pool);
+int64_t pa_pool_bytes(const pa_pool* pool);
+
+/* ------------------------------------------------------------------------------------------ */
+/* Descriptors shared by the kernel-level entry points. */
+
+/* A paged KV cache (inputs 3/4 of PagedAttention, attention.rs:3922-3932). */
+typedef struct pa_cache {
+  void* key_cache;
+  void* value_cache;
+  const float* k_scale; /* fp8 only, [num_blocks, kv_heads] */
+  const float* v_scale; /* fp8 only, [num_blocks, kv_heads] */
+  int64_t num_blocks;
+  int32_t block_size;
+  int32_t kv_heads;
+  int32_t head_dim;
+  pa_dtype dtype; /* storage dtype: T, or PA_DTYPE_FP8_E4M3 */
+} pa_cache;
+
+/* Packed var-length batch metadata (inputs 5/6/7/10, attention.rs:3934-3990). */
+typedef struct pa_batch {
+  const int32_t* cumulative_sequence_length; /* [batch + 1] */
+  const int32_t* past_seqlens;               /* [batch] */
+  const int32_t* block_table;                /* [batch, max_blocks] */
+  const int32_t* slot_mapping;               /* [num_tokens] or NULL */
+  int32_t batch;
+  int32_t max_blocks;
+  int32_t num_tokens;
+  /* Host-known upper bound of new tokens per sequence; selects decode vs prefill kernels
+   * without a device read.  0 means "unknown" and is treated as num_tokens. */
+  int32_t max_query_len;
+} pa_batch;
+
+/* Attention attributes (attention.rs:3857-3870, 4255-4311; attr_scale :448-453). */
+typedef struct pa_attn {
+  int32_t num_heads;
+  float scale;               /* 0 -> 1/sqrt(head_dim) */
+  float softcap;             /* 0 -> off; else softcap * tanh(s / softcap) */
+  int32_t local_window_size; /* -1 -> off; else keys >= row - window + 1 */
+  int32_t is_causal;         /* 1: key p visible to row r iff p <= past + r */
+  const void* head_sink;     /* [num_heads] in activation dtype, or NULL */
+} pa_attn;
+
+/* ------------------------------------------------------------------------------------------ */
+/* Kernel-level entry points (what the op handler calls once metadata is validated). */
+
+/* KV append, optionally fused with Q/K RMSNorm and rotary embedding (a4/a5/a6 of the path).
+ * Replaces the per-sequence rope_with_offset + mlx_scatter_single loop of
+ * attention.rs:4021-4120 (gqa_rope :459-503, cos_sin_row :523-535, slot rule :4064-4079).
+ *   query/key/value      [num_tokens, heads * head_dim] in act_dtype
+ *   q_out / k_out        rotated (and normalised) query/key rows, same layout; may alias
+ *                        query/key; may be NULL when no rotation/normalisation is requested
+ *   cos_cache/sin_cache  [rotary_positions, rotary_half] act_dtype, or NULL (no rotary)
+ *   q_norm/k_norm        [head_dim] act_dtype, or NULL
+ * Cache rows are written in token order: when two tokens target one slot, the later token's
+ * row is the one left in the cache (test_paged_attention.py:117-126, :605-659).  Every
+ * elementwise rotary/norm step rounds to act_dtype, as the reference's per-op MLX graph does. */
+int pa_rotary_append(const pa_cache* cache, const pa_batch* batch, int32_t num_heads,
+                     pa_dtype act_dtype, const void* query, const void* key, const void* value,
+                     void* q_out, void* k_out, const void* cos_cache, const void* sin_cache,
+                     int64_t rotary_positions, int32_t rotary_half, int32_t rotary_offset,
+                     int32_t rotary_interleaved, const void* q_norm, const void* k_norm,
+                     float norm_eps, pa_stream_t stream);
+
+/* Pure reshape_and_cache: bit copy of key/value rows into their slots (or fp8 quantisation
+ * x / scale, zero scale -> 0, RNE, saturate to +-448).  Same slot and ordering rules. */
+int pa_reshape_and_cache(const pa_cache* cache, const pa_batch* batch, pa_dtype act_dtype,
+                         const void* key, const void* value, pa_stream_t stream);
+
+/* Workspace (bytes) needed by pa_attention for split-K partials. */
+size_t pa_attention_workspace_bytes(const pa_cache* cache, const pa_batch* batch,
+                                    const pa_attn* attn);
+/* Workspace (bytes) needed by pa_attention_ex for the given kind / chunk. */
+size_t pa_attention_workspace_bytes_ex(const pa_cache* cache, const pa_batch* batch,
+                                       const pa_attn* attn, pa_dtype act_dtype, int32_t kind,
+                                       int32_t chunk_tokens);
+
+/* Attention over the paged cache after append.  Keys/values at positions < past come from the
+ * cache pages; positions >= past come from k_new/v_new (the rotated new rows), exactly as the
+ * reference's _paged_ref and its patched Metal kernel do (attention.rs:4161-4190,
+ * paged_attention.rs:46-74).  fp8 caches read every position from the pages (the quantised
+ * rule of attention.rs:4192-4194).  q: [num_tokens, num_heads*head_dim]; out likewise.
+ * Dispatch: decode kernel (split-K MFMA, one wavefront per (sequence, kv-head, chunk)) when
+ * (num_heads/kv_heads) * max_query_len <= 16; chunked-prefill MFMA kernel otherwise;
+ * fp32 activations use the VALU kernel. */
+int pa_attention(const pa_cache* cache, const pa_batch* batch, const pa_attn* attn,
+                 pa_dtype act_dtype, const void* q, const void* k_new, const void* v_new,
+                 void* out, void* workspace, size_t workspace_bytes, pa_stream_t stream);
+
+/* Same contract, forcing one kernel family (for parity tests and benchmarks).
+ * kind: 0 = automatic, 1 = decode (split-K MFMA), 2 = prefill (MFMA), 3 = generic VALU.
+ * chunk_tokens: split-K chunk (multiple of 32; 0 = automatic). */
+int pa_attention_ex(const pa_cache* cache, const pa_batch* batch, const pa_attn* attn,
+                    pa_dtype act_dtype, const void* q, const void* k_new, const void* v_new,
+                    void* out, void* workspace, size_t workspace_bytes, int32_t kind,
+                    int32_t chunk_tokens, pa_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------ */
+/* Operator-level entry: the Compute body of com.microsoft::PagedAttention
+ * (paged_attention_op, attention.rs:3857-4382), minus ORT tensor plumbing. */
+
+typedef struct pa_paged_attention_node {
+  int32_t num_heads;          /* "num_heads" */
+  int32_t kv_num_heads;       /* "kv_num_heads" */
+  float scale;                /* "scale" (0 = default) */
+  float softcap;              /* "softcap" */
+  int32_t local_window_size;  /* "local_window_size" (-1) */
+  int32_t do_rotary;          /* "do_rotary" */
+  int32_t rotary_interleaved; /* "rotary_interleaved" */
+  int32_t rotary_offset;      /* "rotary_offset" */
+  int32_t is_causal;          /* "is_causal" (1) */
+  float qk_norm_epsilon;      /* "qk_norm_epsilon" (1e-6) */
+} pa_paged_attention_node;
+
+typedef struct pa_paged_attention_io {
+  pa_dtype dtype;              /* T */
+  int32_t num_tokens;          /* query.shape[0] */
+  int32_t query_hidden;        /* query.shape[1]; packed QKV when key == value == NULL */
+  const void* query;           /* input 0 */
+  const void* key;             /* input 1 (NULL: packed) */
+  const void* value;           /* input 2 (NULL: packed) */
+  pa_cache cache;              /* inputs 3/4 (+14/15 for fp8 scales) */
+  const int32_t* cumulative_sequence_length; /* input 5, device */
+  const int32_t* past_seqlens; /* input 6, device */
+  const int32_t* block_table;  /* input 7, device */
+  int32_t batch;               /* input 5 length - 1 */
+  int32_t max_blocks;          /* input 7 shape[1] */
+  const void* cos_cache;       /* input 8 */
+  const void* sin_cache;       /* input 9 */
+  int64_t rotary_positions;    /* input 8 shape[0] */
+  int32_t rotary_half;         /* input 8 shape[1] */
+  const int32_t* slot_mapping; /* input 10, device, or NULL */
+  const void* head_sink;       /* input 11 or NULL */
+  const void* q_norm_weight;   /* input 12 or NULL */
+  const void* k_norm_weight;   /* input 13 or NULL */
+  /* Host copies of inputs 5/6/7/10.  The reference reads these on the host every step
+   * (read_int_input, attention.rs:3733-3753); when given they are validated with the
+   * reference's rules and error messages.  When NULL the device copies are trusted (kernels
+   * still clamp every index so malformed metadata cannot fault). */
+  const int32_t* host_cumulative_sequence_length;
+  const int32_t* host_past_seqlens;
+  const int32_t* host_block_table;
+  const int32_t* host_slot_mapping;
+  void* output;                /* output 0 */
+} pa_paged_attention_io;
+
+size_t pa_paged_attention_workspace_bytes(const pa_paged_attention_node* node,
+                                          const pa_paged_attention_io* io);
+int pa_paged_attention(const pa_paged_attention_node* node, const pa_paged_attention_io* io,
+                       void* workspace, size_t workspace_bytes, pa_stream_t stream);
+
+/* Claim predicate for a PagedAttention node (paged_attention_claim, attention.rs:4384-4645,
+ * plus kv_cache::claim kv_cache.rs:16-108), restricted to what this build executes.
+ * Host only; no device work.  Returns 1 (claimed) or 0 (declined, reason written). */
+typedef struct pa_node_info {
+  int32_t num_inputs;          /* 8..17 */
+  int32_t num_outputs;         /* 1..3 */
+  int32_t input_present[17];
+  int32_t input_dtype[17];     /* pa_dtype, or 10 for int32, 11 for int8/uint8 */
+  int32_t input_rank[17];
+  int64_t input_shape[17][4];
+  int32_t output_present[3];
+  int32_t output_dtype[3];
+  int32_t output_rank[3];
+  int64_t output_shape[3][4];
+  int32_t num_heads, kv_num_heads, v_head_size, rotary_offset, do_rotary, local_window_size;
+  int32_t is_causal, has_scale_attr;
+  float softcap;
+  int32_t kv_cache_layout_latent; /* "kv_cache_layout" == "LATENT" */
+} pa_node_info;
+#define PA_INT32_DTYPE 10
+#define PA_INT8_DTYPE 11
+
+int pa_paged_attention_claim(const pa_node_info* node, char* reason, size_t reason_len);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* PA_MI355X_H */

@@ -1,0 +1,661 @@
+// pa_api.cpp — host side of the C ABI declared in include/pa_mi355x.h.
+//
+// Mirrors the reference's PagedAttention operator surface (attention.rs:3857-4382 handler,
+// :4384-4645 claim) with its validation rules and "PagedAttention:" error messages, and
+// dispatches to the gfx950 kernels.  No torch, no ORT types; every device buffer is provided by
+// the caller except the page pool.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "pa_device.hpp"
+#include "pa_mi355x.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(PA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+size_t elem_size(pa_dtype d) {
+  switch (d) {
+    case PA_DTYPE_FLOAT16:
+    case PA_DTYPE_BFLOAT16: return 2;
+    case PA_DTYPE_FLOAT32: return 4;
+    case PA_DTYPE_FP8_E4M3: return 1;
+  }
+  return 0;
+}
+
+bool is_act(pa_dtype d) {
+  return d == PA_DTYPE_FLOAT16 || d == PA_DTYPE_BFLOAT16 || d == PA_DTYPE_FLOAT32;
+}
+
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+// ---------------------------------------------------------------------------- descriptor checks
+int check_cache(const pa_cache* c, pa_dtype act) {
+  if (!c) return fail(PA_ERR_INVALID_ARGUMENT, "cache descriptor is NULL");
+  if (c->num_blocks <= 0 || c->block_size <= 0)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "PagedAttention: caches require matching positive block geometry");
+  if (c->kv_heads <= 0 || c->head_dim <= 0 || c->head_dim > 256 || c->head_dim % 8 != 0)
+    return fail(PA_ERR_UNSUPPORTED, "head_dim %d unsupported (multiple of 8, <= 256)",
+                c->head_dim);
+  if (!c->key_cache || !c->value_cache)
+    return fail(PA_ERR_INVALID_ARGUMENT, "key_cache/value_cache pointers are NULL");
+  if (c->dtype == PA_DTYPE_FP8_E4M3) {
+    if (!c->k_scale || !c->v_scale)
+      return fail(PA_ERR_INVALID_ARGUMENT, "fp8 cache requires k_scale and v_scale");
+  } else if (c->dtype != act) {
+    return fail(PA_ERR_UNSUPPORTED, "cache dtype must equal the activation dtype or be fp8");
+  }
+  if (!is_act(act)) return fail(PA_ERR_UNSUPPORTED, "activation dtype must be fp16/bf16/fp32");
+  if (c->num_blocks * (int64_t)c->block_size > INT32_MAX)
+    return fail(PA_ERR_UNSUPPORTED, "cache has more than 2^31 slots");
+  return PA_OK;
+}
+
+int check_batch(const pa_batch* bt) {
+  if (!bt) return fail(PA_ERR_INVALID_ARGUMENT, "batch descriptor is NULL");
+  if (bt->batch < 1)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "PagedAttention: cumulative_sequence_length must have length batch+1");
+  if (bt->num_tokens < 0 || bt->max_blocks < 1)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "PagedAttention: inconsistent cumulative lengths, past lengths or block table");
+  if (!bt->cumulative_sequence_length || !bt->past_seqlens || !bt->block_table)
+    return fail(PA_ERR_INVALID_ARGUMENT, "metadata pointers are NULL");
+  return PA_OK;
+}
+
+// ---------------------------------------------------------------------------- attention plan
+struct Plan {
+  int kind;  // 1 decode MFMA, 2 prefill MFMA, 3 generic
+  int chunk;
+  int max_splits;
+};
+
+int max_ctx_bound(const pa_cache* c, const pa_batch* b) {
+  int64_t v = (int64_t)b->max_blocks * c->block_size;
+  return (int)std::min<int64_t>(v, INT32_MAX / 2);
+}
+
+Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype act, int kind,
+               int chunk) {
+  Plan pl{};
+  const int g = a->num_heads / c->kv_heads;
+  const int mq = b->max_query_len > 0 ? b->max_query_len : std::max(b->num_tokens, 1);
+  if (kind == 0) {
+    if (pa::decode_mfma_supported(c->head_dim, act, c->dtype) && (int64_t)g * mq <= 16)
+      kind = 1;
+    else if (pa::prefill_mfma_supported(c->head_dim, act, c->dtype))
+      kind = 2;
+    else if (pa::decode_mfma_supported(c->head_dim, act, c->dtype))
+      kind = 1;
+    else
+      kind = 3;
+  }
+  pl.kind = kind;
+  const int ctx = std::max(max_ctx_bound(c, b), 1);
+  if (chunk <= 0) {
+    if (kind == 2) {
+      chunk = 1 << 30;  // prefill kernel walks the whole context
+    } else {
+      // Aim for >= ~4096 work units (16 per CU) over the (sequence, kv-head) pairs.
+      int64_t pairs = (int64_t)b->batch * c->kv_heads;
+      int64_t splits = std::max<int64_t>(1, (4096 + pairs - 1) / pairs);
+      int64_t ch = (ctx + splits - 1) / splits;
+      ch = ((ch + 31) / 32) * 32;
+      chunk = (int)std::min<int64_t>(std::max<int64_t>(ch, 256), 1024);
+    }
+  }
+  if (kind != 2) chunk = std::max(32, std::min(chunk, 1024) / 32 * 32);
+  pl.chunk = chunk;
+  pl.max_splits = (int)std::max<int64_t>(1, ((int64_t)ctx + chunk - 1) / chunk);
+  return pl;
+}
+
+size_t workspace_for(const pa_cache* c, const pa_batch* b, const pa_attn* a, const Plan& pl) {
+  if (pl.max_splits <= 1) return 0;
+  size_t rows = (size_t)std::max(b->num_tokens, 0) * a->num_heads * pl.max_splits;
+  return align256(rows * c->head_dim * sizeof(float)) + align256(rows * 2 * sizeof(float));
+}
+
+int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype act,
+                  const void* q, const void* kn, const void* vn, void* out, void* ws,
+                  size_t ws_bytes, int kind, int chunk, hipStream_t s) {
+  int rc = check_cache(c, act);
+  if (rc) return rc;
+  if ((rc = check_batch(b))) return rc;
+  if (!a) return fail(PA_ERR_INVALID_ARGUMENT, "attention descriptor is NULL");
+  if (a->num_heads <= 0 || a->num_heads % c->kv_heads != 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "PagedAttention: bad num_heads/kv_num_heads");
+  if (b->num_tokens == 0) return PA_OK;
+  if (!q || !out || (!kn && c->dtype != PA_DTYPE_FP8_E4M3) ||
+      (!vn && c->dtype != PA_DTYPE_FP8_E4M3))
+    return fail(PA_ERR_INVALID_ARGUMENT, "q/k_new/v_new/out pointers are NULL");
+  if (kind < 0 || kind > 3) return fail(PA_ERR_INVALID_ARGUMENT, "unknown kernel kind %d", kind);
+  if (kind == 1 && !pa::decode_mfma_supported(c->head_dim, act, c->dtype))
+    return fail(PA_ERR_UNSUPPORTED, "decode MFMA kernel does not cover this dtype/head_dim");
+  if (kind == 2 && !pa::prefill_mfma_supported(c->head_dim, act, c->dtype))
+    return fail(PA_ERR_UNSUPPORTED, "prefill MFMA kernel does not cover this dtype/head_dim");
+  if (!(a->softcap >= 0.0f) || !std::isfinite(a->softcap))
+    return fail(PA_ERR_INVALID_ARGUMENT, "softcap must be finite and non-negative");
+  Plan pl = make_plan(c, b, a, act, kind, chunk);
+  size_t need = workspace_for(c, b, a, pl);
+  if (need > 0 && (!ws || ws_bytes < need))
+    return fail(PA_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes, got %zu", need,
+                ws_bytes);
+
+  pa::AttnParams p{};
+  p.q = q;
+  p.k_new = kn;
+  p.v_new = vn;
+  p.key_cache = c->key_cache;
+  p.value_cache = c->value_cache;
+  p.k_scale = c->k_scale;
+  p.v_scale = c->v_scale;
+  p.cum = b->cumulative_sequence_length;
+  p.past = b->past_seqlens;
+  p.block_table = b->block_table;
+  p.head_sink = a->head_sink;
+  p.out = out;
+  size_t rows = (size_t)b->num_tokens * a->num_heads * pl.max_splits;
+  p.part_o = need ? reinterpret_cast<float*>(ws) : nullptr;
+  p.part_ml = need ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) +
+                                              align256(rows * c->head_dim * sizeof(float)))
+                   : nullptr;
+  p.num_blocks = c->num_blocks;
+  p.block_size = c->block_size;
+  p.kv_heads = c->kv_heads;
+  p.head_dim = c->head_dim;
+  p.num_heads = a->num_heads;
+  p.batch = b->batch;
+  p.max_blocks = b->max_blocks;
+  p.num_tokens = b->num_tokens;
+  p.chunk = pl.chunk;
+  p.max_splits = pl.max_splits;
+  p.max_query_len = b->max_query_len > 0 ? b->max_query_len : b->num_tokens;
+  p.scale = a->scale != 0.0f ? a->scale : 1.0f / std::sqrt((float)c->head_dim);
+  p.scale_log2 = p.scale * pa::kLog2e;
+  p.softcap = a->softcap;
+  p.window = a->local_window_size;
+  p.causal = a->is_causal ? 1 : 0;
+  p.read_all_from_cache = c->dtype == PA_DTYPE_FP8_E4M3 ? 1 : 0;
+
+  hipError_t e;
+  switch (pl.kind) {
+    case 1: e = pa::launch_decode_mfma(p, act, c->dtype, s); break;
+    case 2: e = pa::launch_prefill_mfma(p, act, c->dtype, s); break;
+    default: e = pa::launch_attn_generic(p, act, c->dtype, s); break;
+  }
+  if (e != hipSuccess) return hip_fail(e, "attention kernel launch");
+  if (pl.max_splits > 1) {
+    e = pa::launch_split_reduce(p, act, s);
+    if (e != hipSuccess) return hip_fail(e, "split-K reduce launch");
+  }
+  return PA_OK;
+}
+
+}  // namespace
+
+// ============================================================================== C ABI
+extern "C" {
+
+const char* pa_last_error(void) { return g_last_error.c_str(); }
+
+const char* pa_version(void) { return "onnxruntime-ep-mlx_amd 0.1.0 (gfx950)"; }
+
+// ------------------------------------------------------------------------------ page pool
+struct pa_pool {
+  void* k;
+  void* v;
+  float* ks;
+  float* vs;
+  int64_t bytes;
+};
+
+int pa_pool_create(int64_t num_blocks, int32_t block_size, int32_t kv_heads, int32_t head_dim,
+                   pa_dtype cache_dtype, pa_pool** out_pool) {
+  if (!out_pool) return fail(PA_ERR_INVALID_ARGUMENT, "out_pool is NULL");
+  *out_pool = nullptr;
+  size_t es = elem_size(cache_dtype);
+  if (num_blocks <= 0 || block_size <= 0 || kv_heads <= 0 || head_dim <= 0 || es == 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "invalid pool geometry");
+  size_t side = (size_t)num_blocks * block_size * kv_heads * head_dim * es;
+  pa_pool* p = new pa_pool{};
+  hipError_t e = hipMalloc(&p->k, side);
+  if (e == hipSuccess) e = hipMalloc(&p->v, side);
+  if (e == hipSuccess && cache_dtype == PA_DTYPE_FP8_E4M3) {
+    size_t sb = (size_t)num_blocks * kv_heads * sizeof(float);
+    e = hipMalloc(&p->ks, sb);
+    if (e == hipSuccess) e = hipMalloc(&p->vs, sb);
+  }
+  if (e != hipSuccess) {
+    (void)hipFree(p->k);
+    (void)hipFree(p->v);
+    (void)hipFree(p->ks);
+    (void)hipFree(p->vs);
+    delete p;
+    return fail(PA_ERR_OUT_OF_MEMORY, "pool allocation of 2 x %zu bytes failed: %s", side,
+                hipGetErrorString(e));
+  }
+  p->bytes = (int64_t)(2 * side);
+  *out_pool = p;
+  return PA_OK;
+}
+
+int pa_pool_destroy(pa_pool* p) {
+  if (!p) return PA_OK;
+  (void)hipFree(p->k);
+  (void)hipFree(p->v);
+  (void)hipFree(p->ks);
+  (void)hipFree(p->vs);
+  delete p;
+  return PA_OK;
+}
+
+void* pa_pool_k_ptr(const pa_pool* p) { return p ? p->k : nullptr; }
+void* pa_pool_v_ptr(const pa_pool* p) { return p ? p->v : nullptr; }
+float* pa_pool_k_scale_ptr(const pa_pool* p) { return p ? p->ks : nullptr; }
+float* pa_pool_v_scale_ptr(const pa_pool* p) { return p ? p->vs : nullptr; }
+int64_t pa_pool_bytes(const pa_pool* p) { return p ? p->bytes : 0; }
+
+// ------------------------------------------------------------------------------ append
+static int rotary_append_impl(const pa_cache* c, const pa_batch* b, int32_t num_heads,
+                              pa_dtype act, const void* query, const void* key,
+                              const void* value, void* q_out, void* k_out, const void* cos,
+                              const void* sin, int64_t rot_pos, int32_t rot_half,
+                              int32_t rot_offset, int32_t interleaved, const void* qn,
+                              const void* kn, float eps, hipStream_t s) {
+  int rc = check_cache(c, act);
+  if (rc) return rc;
+  if ((rc = check_batch(b))) return rc;
+  if (b->num_tokens == 0) return PA_OK;
+  if (!key || !value) return fail(PA_ERR_INVALID_ARGUMENT, "key/value pointers are NULL");
+  const bool rotate = cos != nullptr;
+  if (rotate) {
+    if (!sin || rot_half <= 0 || rot_offset < 0 || rot_offset + 2 * rot_half > c->head_dim ||
+        rot_pos <= 0)
+      return fail(PA_ERR_INVALID_ARGUMENT,
+                  "rotary_offset + rotary_dim must not exceed head_size");
+  }
+  if ((qn == nullptr) != (kn == nullptr))
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "q_norm_weight and k_norm_weight must be provided together");
+  const bool transform = rotate || qn;
+  if (transform && num_heads > 0 && query && !q_out)
+    return fail(PA_ERR_INVALID_ARGUMENT, "q_out is required when rotating/normalising query");
+  pa::AppendParams p{};
+  p.query = query;
+  p.key = key;
+  p.value = value;
+  p.q_out = q_out;
+  p.k_out = k_out;
+  p.key_cache = c->key_cache;
+  p.value_cache = c->value_cache;
+  p.k_scale = c->k_scale;
+  p.v_scale = c->v_scale;
+  p.cos_cache = cos;
+  p.sin_cache = sin;
+  p.q_norm = qn;
+  p.k_norm = kn;
+  p.cum = b->cumulative_sequence_length;
+  p.past = b->past_seqlens;
+  p.block_table = b->block_table;
+  p.slot_mapping = b->slot_mapping;
+  p.num_blocks = c->num_blocks;
+  p.rotary_positions = rot_pos;
+  p.block_size = c->block_size;
+  p.kv_heads = c->kv_heads;
+  p.head_dim = c->head_dim;
+  p.num_heads = num_heads;
+  p.batch = b->batch;
+  p.max_blocks = b->max_blocks;
+  p.num_tokens = b->num_tokens;
+  p.rotary_half = rotate ? rot_half : 0;
+  p.rotary_offset = rotate ? rot_offset : 0;
+  p.rotary_interleaved = interleaved ? 1 : 0;
+  p.do_q = (query && q_out && num_heads > 0) ? 1 : 0;
+  p.norm_eps = eps;
+  hipError_t e = pa::launch_rotary_append(p, act, c->dtype, s);
+  if (e != hipSuccess) return hip_fail(e, "rotary/append kernel launch");
+  return PA_OK;
+}
+
+int pa_rotary_append(const pa_cache* cache, const pa_batch* batch, int32_t num_heads,
+                     pa_dtype act_dtype, const void* query, const void* key, const void* value,
+                     void* q_out, void* k_out, const void* cos_cache, const void* sin_cache,
+                     int64_t rotary_positions, int32_t rotary_half, int32_t rotary_offset,
+                     int32_t rotary_interleaved, const void* q_norm, const void* k_norm,
+                     float norm_eps, pa_stream_t stream) {
+  return rotary_append_impl(cache, batch, num_heads, act_dtype, query, key, value, q_out, k_out,
+                            cos_cache, sin_cache, rotary_positions, rotary_half, rotary_offset,
+                            rotary_interleaved, q_norm, k_norm, norm_eps,
+                            reinterpret_cast<hipStream_t>(stream));
+}
+
+int pa_reshape_and_cache(const pa_cache* cache, const pa_batch* batch, pa_dtype act_dtype,
+                         const void* key, const void* value, pa_stream_t stream) {
+  return rotary_append_impl(cache, batch, 0, act_dtype, nullptr, key, value, nullptr, nullptr,
+                            nullptr, nullptr, 0, 0, 0, 0, nullptr, nullptr, 0.0f,
+                            reinterpret_cast<hipStream_t>(stream));
+}
+
+// ------------------------------------------------------------------------------ attention
+size_t pa_attention_workspace_bytes(const pa_cache* cache, const pa_batch* batch,
+                                    const pa_attn* attn) {
+  if (!cache || !batch || !attn || cache->kv_heads <= 0 || batch->batch <= 0) return 0;
+  pa_dtype act = cache->dtype == PA_DTYPE_FP8_E4M3 ? PA_DTYPE_BFLOAT16 : cache->dtype;
+  return workspace_for(cache, batch, attn, make_plan(cache, batch, attn, act, 0, 0));
+}
+
+size_t pa_attention_workspace_bytes_ex(const pa_cache* cache, const pa_batch* batch,
+                                       const pa_attn* attn, pa_dtype act_dtype, int32_t kind,
+                                       int32_t chunk_tokens) {
+  if (!cache || !batch || !attn || cache->kv_heads <= 0 || batch->batch <= 0) return 0;
+  return workspace_for(cache, batch, attn,
+                       make_plan(cache, batch, attn, act_dtype, kind, chunk_tokens));
+}
+
+int pa_attention(const pa_cache* cache, const pa_batch* batch, const pa_attn* attn,
+                 pa_dtype act_dtype, const void* q, const void* k_new, const void* v_new,
+                 void* out, void* workspace, size_t workspace_bytes, pa_stream_t stream) {
+  return run_attention(cache, batch, attn, act_dtype, q, k_new, v_new, out, workspace,
+                       workspace_bytes, 0, 0, reinterpret_cast<hipStream_t>(stream));
+}
+
+int pa_attention_ex(const pa_cache* cache, const pa_batch* batch, const pa_attn* attn,
+                    pa_dtype act_dtype, const void* q, const void* k_new, const void* v_new,
+                    void* out, void* workspace, size_t workspace_bytes, int32_t kind,
+                    int32_t chunk_tokens, pa_stream_t stream) {
+  return run_attention(cache, batch, attn, act_dtype, q, k_new, v_new, out, workspace,
+                       workspace_bytes, kind, chunk_tokens, reinterpret_cast<hipStream_t>(stream));
+}
+
+// ------------------------------------------------------------------------------ operator level
+namespace {
+
+struct OpLayout {
+  int head, kv_hidden;
+  bool transform;
+  size_t q_bytes, k_bytes, attn_off, total;
+  pa_batch batch;
+  pa_attn attn;
+};
+
+int op_layout(const pa_paged_attention_node* n, const pa_paged_attention_io* io, OpLayout* L) {
+  if (!n || !io) return fail(PA_ERR_INVALID_ARGUMENT, "node/io is NULL");
+  if (n->num_heads <= 0 || n->kv_num_heads <= 0 || n->num_heads % n->kv_num_heads != 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "PagedAttention: bad num_heads/kv_num_heads");
+  const bool packed = io->key == nullptr && io->value == nullptr;
+  if (packed)
+    return fail(PA_ERR_UNSUPPORTED, "PagedAttention: packed QKV input is not supported");
+  if (io->query_hidden <= 0 || io->query_hidden % n->num_heads != 0)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "query must have rank 2 and a hidden size divisible by its head count");
+  L->head = io->query_hidden / n->num_heads;
+  L->kv_hidden = L->head * n->kv_num_heads;
+  if (io->cache.head_dim != L->head || io->cache.kv_heads != n->kv_num_heads)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "key_cache must be [num_blocks,block_size,kv_num_heads,head_size]");
+  L->transform = (n->do_rotary != 0) || io->q_norm_weight != nullptr;
+  size_t es = elem_size(io->dtype);
+  L->q_bytes = L->transform ? align256((size_t)io->num_tokens * io->query_hidden * es) : 0;
+  L->k_bytes = L->transform ? align256((size_t)io->num_tokens * L->kv_hidden * es) : 0;
+  L->attn_off = L->q_bytes + L->k_bytes;
+  pa_batch& b = L->batch;
+  b.cumulative_sequence_length = io->cumulative_sequence_length;
+  b.past_seqlens = io->past_seqlens;
+  b.block_table = io->block_table;
+  b.slot_mapping = io->slot_mapping;
+  b.batch = io->batch;
+  b.max_blocks = io->max_blocks;
+  b.num_tokens = io->num_tokens;
+  b.max_query_len = 0;
+  if (io->host_cumulative_sequence_length) {
+    int mq = 0;
+    for (int i = 0; i < io->batch; ++i)
+      mq = std::max(mq, io->host_cumulative_sequence_length[i + 1] -
+                            io->host_cumulative_sequence_length[i]);
+    b.max_query_len = std::max(mq, 1);
+  }
+  pa_attn& a = L->attn;
+  a.num_heads = n->num_heads;
+  a.scale = n->scale;
+  a.softcap = n->softcap;
+  a.local_window_size = n->local_window_size;
+  a.is_causal = n->is_causal;
+  a.head_sink = io->head_sink;
+  L->total = L->attn_off + pa_attention_workspace_bytes_ex(&io->cache, &b, &a, io->dtype, 0, 0);
+  return PA_OK;
+}
+
+// Host-side metadata validation, restating attention.rs:3934-3990 rule for rule.
+int validate_host_metadata(const pa_paged_attention_node* n, const pa_paged_attention_io* io) {
+  const int32_t* cum = io->host_cumulative_sequence_length;
+  const int32_t* past = io->host_past_seqlens;
+  const int32_t* bt = io->host_block_table;
+  const int B = io->batch;
+  if (B < 1)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "PagedAttention: cumulative_sequence_length must have length batch+1");
+  if (!past || !bt)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "PagedAttention: host metadata must include past_seqlens and block_table");
+  bool bad = cum[0] != 0 || cum[B] != io->num_tokens || io->max_blocks < 1;
+  for (int i = 0; i < B && !bad; ++i) bad = cum[i] < 0 || cum[i] > cum[i + 1];
+  for (int i = 0; i < B && !bad; ++i) bad = past[i] < 0;
+  if (bad)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "PagedAttention: inconsistent cumulative lengths, past lengths or block table");
+  const int64_t nb = io->cache.num_blocks, bs = io->cache.block_size;
+  if (io->slot_mapping) {
+    const int32_t* sm = io->host_slot_mapping;
+    if (!sm)
+      return fail(PA_ERR_INVALID_ARGUMENT,
+                  "PagedAttention: host slot_mapping is required with a device slot_mapping");
+    for (int t = 0; t < io->num_tokens; ++t)
+      if (sm[t] < -1 || (int64_t)sm[t] >= nb * bs)
+        return fail(PA_ERR_INVALID_ARGUMENT,
+                    "PagedAttention: slot_mapping must contain -1 or valid physical cache slots");
+  }
+  for (int i = 0; i < B; ++i) {
+    int64_t total = (int64_t)past[i] + cum[i + 1] - cum[i];
+    if (total > INT32_MAX || total > (int64_t)io->max_blocks * bs)
+      return fail(PA_ERR_INVALID_ARGUMENT,
+                  "PagedAttention: sequence exceeds block table capacity");
+    int64_t needed = (total + bs - 1) / bs;
+    for (int64_t j = 0; j < needed; ++j) {
+      int32_t blk = bt[(int64_t)i * io->max_blocks + j];
+      if (blk < 0 || blk >= nb)
+        return fail(PA_ERR_INVALID_ARGUMENT,
+                    "PagedAttention: block table contains an invalid physical block");
+    }
+    if (n->do_rotary) {
+      // cos_sin_row (attention.rs:523-535) slices rows [past, past + nq) of the cache.
+      int64_t nq = cum[i + 1] - cum[i];
+      if (nq > 0 && (past[i] > io->rotary_positions - nq))
+        return fail(PA_ERR_INVALID_ARGUMENT,
+                    "RotaryEmbedding: requested positions exceed the supplied cache");
+    }
+  }
+  return PA_OK;
+}
+
+}  // namespace
+
+size_t pa_paged_attention_workspace_bytes(const pa_paged_attention_node* node,
+                                          const pa_paged_attention_io* io) {
+  OpLayout L;
+  if (op_layout(node, io, &L)) return 0;
+  return L.total;
+}
+
+int pa_paged_attention(const pa_paged_attention_node* n, const pa_paged_attention_io* io,
+                       void* workspace, size_t workspace_bytes, pa_stream_t stream) {
+  OpLayout L;
+  int rc = op_layout(n, io, &L);
+  if (rc) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (io->host_cumulative_sequence_length && (rc = validate_host_metadata(n, io))) return rc;
+  if (n->local_window_size != -1 && n->local_window_size <= 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "local_window_size must be -1 or positive");
+  if (n->do_rotary && (!io->cos_cache || !io->sin_cache))
+    return fail(PA_ERR_INVALID_ARGUMENT, "do_rotary=1 requires cos_cache and sin_cache inputs");
+  if (n->do_rotary && n->rotary_offset % 8 != 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "rotary_offset must be a multiple of 8");
+  if (workspace_bytes < L.total || (L.total && !workspace))
+    return fail(PA_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes, got %zu",
+                L.total, workspace_bytes);
+  if (io->num_tokens == 0) return PA_OK;
+  char* ws = reinterpret_cast<char*>(workspace);
+  void* q_rot = L.transform ? ws : nullptr;
+  void* k_rot = L.transform ? ws + L.q_bytes : nullptr;
+  rc = rotary_append_impl(&io->cache, &L.batch, n->num_heads, io->dtype, io->query, io->key,
+                          io->value, q_rot, k_rot, n->do_rotary ? io->cos_cache : nullptr,
+                          n->do_rotary ? io->sin_cache : nullptr, io->rotary_positions,
+                          io->rotary_half, n->rotary_offset, n->rotary_interleaved,
+                          io->q_norm_weight, io->k_norm_weight, n->qk_norm_epsilon, s);
+  if (rc) return rc;
+  const void* q = L.transform ? q_rot : io->query;
+  const void* kn = L.transform ? k_rot : io->key;
+  return run_attention(&io->cache, &L.batch, &L.attn, io->dtype, q, kn, io->value, io->output,
+                       ws + L.attn_off, workspace_bytes - L.attn_off, 0, 0, s);
+}
+
+// ------------------------------------------------------------------------------ claim
+// paged_attention_claim (attention.rs:4384-4645) + kv_cache::claim (kv_cache.rs:16-108),
+// restricted to the forms this build executes; declined forms name the reason.
+int pa_paged_attention_claim(const pa_node_info* n, char* reason, size_t reason_len) {
+  auto deny = [&](const char* fmt, ...) {
+    if (reason && reason_len) {
+      va_list ap;
+      va_start(ap, fmt);
+      vsnprintf(reason, reason_len, fmt, ap);
+      va_end(ap);
+    }
+    return 0;
+  };
+  if (!n) return deny("node info is NULL");
+  if (reason && reason_len) reason[0] = 0;
+  const int T16 = PA_DTYPE_FLOAT16, TB16 = PA_DTYPE_BFLOAT16, I32 = PA_INT32_DTYPE;
+  if (n->is_causal != 0 && n->is_causal != 1) return deny("is_causal must be 0 or 1");
+  if (n->num_outputs < 1 || n->num_outputs > 3)
+    return deny("PagedAttention requires 1 to 3 outputs");
+  if (n->v_head_size < 0) return deny("v_head_size must be non-negative");
+  if (n->rotary_offset < 0) return deny("rotary_offset must be non-negative");
+  const int out_dt = n->output_dtype[0];
+  if (out_dt != T16 && out_dt != TB16)
+    return deny("PagedAttention is only supported for fp16/bf16 (T)");
+  if (n->num_inputs < 8 || n->num_inputs > 17)
+    return deny("expects 8 required inputs plus optional rotary, scheduling, normalization, "
+                "and scale inputs, got %d", n->num_inputs);
+  if (n->kv_cache_layout_latent) return deny("LATENT kv_cache_layout is not executed by this build");
+  auto present = [&](int i) { return i < n->num_inputs && n->input_present[i]; };
+  auto out_present = [&](int i) { return i < n->num_outputs && n->output_present[i]; };
+  const bool packed = !present(1) && !present(2);
+  if (packed) return deny("packed QKV input is not executed by this build");
+  for (int i : {0, 1, 2})
+    if (!present(i) || n->input_dtype[i] != out_dt)
+      return deny("input %d must be present and share the output float dtype", i);
+  for (int i : {5, 6, 7})
+    if (!present(i) || n->input_dtype[i] != I32) return deny("input %d must be int32", i);
+  const int64_t H = n->num_heads, KV = n->kv_num_heads;
+  if (!(H > 0 && KV > 0 && H % KV == 0))
+    return deny("num_heads (%lld) must be a positive multiple of kv_num_heads (%lld)",
+                (long long)H, (long long)KV);
+  if (n->input_rank[0] != 2 || n->input_shape[0][1] <= 0 || n->input_shape[0][1] % H != 0)
+    return deny("query must have rank 2 and a hidden size divisible by its separate or packed "
+                "head count");
+  const int64_t head = n->input_shape[0][1] / H;
+  if (head > 256 || head % 8 != 0) return deny("head_size %lld is not executed by this build",
+                                               (long long)head);
+  // Cache storage: the activation dtype, or (build-defined) fp8 e4m3 with fp32
+  // per-(block, kv-head) scales in inputs 14/15.  Integer caches are not executed yet.
+  const int cache_dt = present(3) ? n->input_dtype[3] : out_dt;
+  if (!present(3) || !present(4)) return deny("key_cache and value_cache must be present");
+  if (n->input_dtype[4] != cache_dt) return deny("key/value caches must share one storage dtype");
+  if (cache_dt == PA_INT8_DTYPE) return deny("integer KV caches are not executed by this build");
+  if (cache_dt == PA_DTYPE_FP8_E4M3) {
+    for (int i : {14, 15})
+      if (!present(i) || n->input_dtype[i] != PA_DTYPE_FLOAT32 || n->input_rank[i] != 2 ||
+          n->input_shape[i][1] != KV)
+        return deny("fp8 cache requires float32 %s_scale [num_blocks, kv_num_heads]",
+                    i == 14 ? "k" : "v");
+  } else if (cache_dt != out_dt) {
+    return deny("a non-integer cache must use the activation dtype");
+  }
+  const int64_t v_head = n->v_head_size == 0 ? head : n->v_head_size;
+  if (n->input_rank[1] != 2 || n->input_shape[1][1] != KV * head)
+    return deny("key must be [num_tokens,kv_num_heads*head_size]");
+  if (n->input_rank[2] != 2 || n->input_shape[2][1] != KV * v_head)
+    return deny("value must be [num_tokens,kv_num_heads*v_head_size]");
+  if (v_head != head) return deny("SEPARATE layout requires equal key and value head sizes");
+  for (int i : {3, 4})
+    if (n->input_rank[i] != 4 || n->input_shape[i][2] != KV || n->input_shape[i][3] != head)
+      return deny("%s must be [num_blocks,block_size,kv_num_heads,head_size]",
+                  i == 3 ? "key_cache" : "value_cache");
+  if (n->output_rank[0] != 2 ||
+      !(n->output_shape[0][1] < 0 || n->output_shape[0][1] == H * v_head))
+    return deny("output must be [num_tokens,num_heads*v_head_size]");
+  if (!(n->local_window_size == -1 || n->local_window_size > 0))
+    return deny("local_window_size must be -1 or positive");
+  if (!std::isfinite(n->softcap) || n->softcap < 0.0f)
+    return deny("softcap must be finite and non-negative");
+  if (n->do_rotary) {
+    if (!present(8) || !present(9))
+      return deny("do_rotary=1 requires cos_cache and sin_cache inputs");
+    if (n->input_dtype[8] != out_dt || n->input_dtype[9] != out_dt)
+      return deny("cos_cache/sin_cache must share the output float dtype");
+    if (n->input_rank[8] != 2 || n->input_rank[9] != 2 ||
+        n->input_shape[8][0] != n->input_shape[9][0] ||
+        n->input_shape[8][1] != n->input_shape[9][1] || n->input_shape[8][1] <= 0)
+      return deny("cos/sin caches must have matching [positions,rotary_dim/2] shapes");
+    const int64_t rot = n->input_shape[8][1] * 2;
+    if (n->rotary_offset + rot > head)
+      return deny("rotary_offset + rotary_dim must not exceed head_size");
+    if (n->rotary_offset % 8 != 0) return deny("rotary_offset must be a multiple of 8");
+  }
+  if (present(10) &&
+      !(n->input_dtype[10] == I32 && n->input_rank[10] == 1 &&
+        (n->input_shape[10][0] < 0 || n->input_shape[0][0] < 0 ||
+         n->input_shape[10][0] == n->input_shape[0][0])))
+    return deny("slot_mapping must be int32 [num_tokens]");
+  if (present(11) &&
+      !(n->input_dtype[11] == out_dt && n->input_rank[11] == 1 && n->input_shape[11][0] == H))
+    return deny("head_sink must be [num_heads] in activation dtype");
+  if (present(12) != present(13))
+    return deny("q_norm_weight and k_norm_weight must be provided together");
+  if (present(12))
+    for (int i : {12, 13})
+      if (!(n->input_dtype[i] == out_dt && n->input_rank[i] == 1 && n->input_shape[i][0] == head))
+        return deny("Q/K norm weight %d must be [head_size] in activation dtype", i);
+  if (present(16) && !(n->input_dtype[16] == I32 && n->input_rank[16] == 1 &&
+                       (n->input_shape[16][0] == 2 || n->input_shape[16][0] == 3)))
+    return deny("attention_metadata must be int32 [2] or [3]");
+  for (int i = 1; i < std::min(n->num_outputs, 3); ++i)
+    if (out_present(i) && n->output_dtype[i] != n->input_dtype[i + 2])
+      return deny("cache output %d must retain cache storage dtype", i);
+  return 1;
+}
+
+}  // extern "C"

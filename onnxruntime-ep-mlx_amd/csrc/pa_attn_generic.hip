@@ -1,0 +1,232 @@
+// pa_attn_generic.hip — VALU paged attention for every dtype/shape, plus the split-K reduce.
+//
+// One wavefront per (packed query token, query head, context chunk).  Lanes split head_dim;
+// each key costs one cross-lane sum.  This is the fp32 path (the ORT CPU GQA parity config)
+// and the fallback for shapes the MFMA kernels do not cover; it is not the hot path.
+//
+// Semantics restated from _paged_ref (test_paged_attention.py:127-155) and the dense
+// fallback (attention.rs:4192-4319): positions < past read the cache pages through the block
+// table, positions >= past read the new rows; causal keeps keys p <= past + row; a window keeps
+// p >= past + row - window + 1; softcap s -> c*tanh(s/c); a head sink adds exp(sink) to the
+// denominator only (attention_probs_with_sink :100-118).  Softmax runs in base 2 on
+// x = s*log2(e), which is the same function.
+#include "pa_device.hpp"
+
+namespace pa {
+
+namespace {
+
+template <typename CT>
+struct CacheRead;
+
+template <>
+struct CacheRead<TF16> {
+  __device__ static float at(const void* c, int64_t i, float) {
+    return f16_to_f32(reinterpret_cast<const uint16_t*>(c)[i]);
+  }
+};
+template <>
+struct CacheRead<TBF16> {
+  __device__ static float at(const void* c, int64_t i, float) {
+    return bf16_to_f32(reinterpret_cast<const uint16_t*>(c)[i]);
+  }
+};
+template <>
+struct CacheRead<TF32> {
+  __device__ static float at(const void* c, int64_t i, float) {
+    return reinterpret_cast<const float*>(c)[i];
+  }
+};
+struct Fp8Cache {};
+template <>
+struct CacheRead<Fp8Cache> {
+  __device__ static float at(const void* c, int64_t i, float scale) {
+    return e4m3_to_f32(reinterpret_cast<const uint8_t*>(c)[i]) * scale;
+  }
+};
+
+constexpr int kMaxLanesElems = 4;  // head_dim <= 256
+
+template <typename TT, typename CT>
+__global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
+  const int split = blockIdx.x, h = blockIdx.y, t = blockIdx.z;
+  const int lane = threadIdx.x;
+  const int D = p.head_dim;
+  const int b = seq_of_token(p.cum, p.batch, t);
+  const int s0 = p.cum[b];
+  const int nq = p.cum[b + 1] - s0;
+  const int64_t pastb = max(p.past[b], 0);
+  const int64_t total = pastb + nq;
+  const int64_t start = (int64_t)split * p.chunk;
+  if (nq <= 0 || start >= total) return;
+  const int64_t end = min(start + (int64_t)p.chunk, total);
+  const int g = p.num_heads / p.kv_heads;
+  const int kh = h / g;
+  const int64_t rp = pastb + (t - s0);
+  int64_t lo = start, hi = end;
+  if (p.causal) hi = min(hi, rp + 1);
+  if (p.window > 0) lo = max(lo, rp - p.window + 1);
+
+  const int64_t row = (int64_t)p.kv_heads * D;
+  float qv[kMaxLanesElems], o[kMaxLanesElems];
+#pragma unroll
+  for (int k = 0; k < kMaxLanesElems; ++k) {
+    int e = lane + 64 * k;
+    qv[k] = e < D ? TT::to_f32(reinterpret_cast<const typename TT::raw*>(
+                        p.q)[((int64_t)t * p.num_heads + h) * D + e])
+                  : 0.0f;
+    o[k] = 0.0f;
+  }
+  float m = kNegInf, l = 0.0f;
+  const float cap = p.softcap;
+  for (int64_t pos = lo; pos < hi; ++pos) {
+    const void *kb, *vb;
+    int64_t off;
+    float ks = 1.0f, vs = 1.0f;
+    bool from_cache = pos < pastb || p.read_all_from_cache;
+    if (from_cache) {
+      int64_t bi = pos / p.block_size;
+      int64_t blk = p.block_table[(int64_t)b * p.max_blocks + min(bi, (int64_t)p.max_blocks - 1)];
+      blk = min(max(blk, (int64_t)0), p.num_blocks - 1);
+      off = (blk * p.block_size + pos % p.block_size) * row + (int64_t)kh * D;
+      kb = p.key_cache;
+      vb = p.value_cache;
+      if (p.k_scale) {
+        ks = p.k_scale[blk * p.kv_heads + kh];
+        vs = p.v_scale[blk * p.kv_heads + kh];
+      }
+    } else {
+      int64_t tok = min(max((int64_t)s0 + (pos - pastb), (int64_t)0), (int64_t)p.num_tokens - 1);
+      off = tok * row + (int64_t)kh * D;
+      kb = p.k_new;
+      vb = p.v_new;
+    }
+    float part = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kMaxLanesElems; ++k) {
+      int e = lane + 64 * k;
+      if (e < D) {
+        float kv = from_cache ? CacheRead<CT>::at(kb, off + e, ks)
+                              : TT::to_f32(reinterpret_cast<const typename TT::raw*>(kb)[off + e]);
+        part += qv[k] * kv;
+      }
+    }
+    float s = wave_sum(part) * p.scale;
+    if (cap > 0.0f) s = cap * tanhf(s / cap);
+    float x = s * kLog2e;
+    float mn = fmaxf(m, x);
+    float alpha = (m == kNegInf) ? 0.0f : exp2f(m - mn);
+    float w = exp2f(x - mn);
+    l = l * alpha + w;
+#pragma unroll
+    for (int k = 0; k < kMaxLanesElems; ++k) {
+      int e = lane + 64 * k;
+      if (e < D) {
+        float vv = from_cache ? CacheRead<CT>::at(vb, off + e, vs)
+                              : TT::to_f32(reinterpret_cast<const typename TT::raw*>(vb)[off + e]);
+        o[k] = o[k] * alpha + w * vv;
+      }
+    }
+    m = mn;
+  }
+
+  const bool single = (start == 0 && end == total);
+  if (!single && p.part_o == nullptr) return;  // beyond planned capacity: nothing to write into
+  if (single) {
+    float f = finalize_factor(m, l, sink_logit<TT>(p, h));
+    typename TT::raw* out = reinterpret_cast<typename TT::raw*>(p.out);
+#pragma unroll
+    for (int k = 0; k < kMaxLanesElems; ++k) {
+      int e = lane + 64 * k;
+      if (e < D) out[((int64_t)t * p.num_heads + h) * D + e] = TT::from_f32(o[k] * f);
+    }
+  } else {
+    int64_t pi = ((int64_t)t * p.num_heads + h) * p.max_splits + split;
+#pragma unroll
+    for (int k = 0; k < kMaxLanesElems; ++k) {
+      int e = lane + 64 * k;
+      if (e < D) p.part_o[pi * D + e] = o[k];
+    }
+    if (lane == 0) {
+      p.part_ml[pi * 2 + 0] = m;
+      p.part_ml[pi * 2 + 1] = l;
+    }
+  }
+}
+
+// Merge the per-chunk partials of one (token, head): global max, rescaled sums, divide.
+template <typename TT>
+__global__ __launch_bounds__(64) void split_reduce_kernel(const AttnParams p) {
+  const int h = blockIdx.x, t = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int D = p.head_dim;
+  const int b = seq_of_token(p.cum, p.batch, t);
+  const int nq = p.cum[b + 1] - p.cum[b];
+  const int64_t total = (int64_t)max(p.past[b], 0) + nq;
+  if (nq <= 0) return;
+  const int nsplit = (int)min((total + p.chunk - 1) / p.chunk, (int64_t)p.max_splits);
+  if (nsplit <= 1) return;  // the attention kernel already wrote the final row
+  const int64_t base = ((int64_t)t * p.num_heads + h) * p.max_splits;
+  float M = kNegInf;
+  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, p.part_ml[(base + s) * 2]);
+  float L = 0.0f;
+  for (int s = 0; s < nsplit; ++s) {
+    float ms = p.part_ml[(base + s) * 2];
+    if (ms != kNegInf) L += p.part_ml[(base + s) * 2 + 1] * exp2f(ms - M);
+  }
+  const float f = finalize_factor(M, L, sink_logit<TT>(p, h));
+  typename TT::raw* out = reinterpret_cast<typename TT::raw*>(p.out);
+  for (int e = lane; e < D; e += 64) {
+    float acc = 0.0f;
+    for (int s = 0; s < nsplit; ++s) {
+      float ms = p.part_ml[(base + s) * 2];
+      if (ms != kNegInf) acc += p.part_o[(base + s) * D + e] * exp2f(ms - M);
+    }
+    out[((int64_t)t * p.num_heads + h) * D + e] = TT::from_f32(acc * f);
+  }
+}
+
+template <typename TT>
+hipError_t launch_generic_t(const AttnParams& p, pa_dtype cache_dtype, hipStream_t s) {
+  dim3 grid(p.max_splits, p.num_heads, p.num_tokens), block(64);
+  if (cache_dtype == PA_DTYPE_FP8_E4M3)
+    hipLaunchKernelGGL((attn_generic_kernel<TT, Fp8Cache>), grid, block, 0, s, p);
+  else
+    hipLaunchKernelGGL((attn_generic_kernel<TT, TT>), grid, block, 0, s, p);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_attn_generic(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
+                               hipStream_t s) {
+  if (p.num_tokens <= 0) return hipSuccess;
+  if (p.head_dim > 64 * kMaxLanesElems) return hipErrorInvalidValue;
+  switch (act) {
+    case PA_DTYPE_FLOAT16: return launch_generic_t<TF16>(p, cache_dtype, s);
+    case PA_DTYPE_BFLOAT16: return launch_generic_t<TBF16>(p, cache_dtype, s);
+    case PA_DTYPE_FLOAT32: return launch_generic_t<TF32>(p, cache_dtype, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_split_reduce(const AttnParams& p, pa_dtype act, hipStream_t s) {
+  if (p.num_tokens <= 0 || p.max_splits <= 1) return hipSuccess;
+  dim3 grid(p.num_heads, p.num_tokens), block(64);
+  switch (act) {
+    case PA_DTYPE_FLOAT16:
+      hipLaunchKernelGGL((split_reduce_kernel<TF16>), grid, block, 0, s, p);
+      break;
+    case PA_DTYPE_BFLOAT16:
+      hipLaunchKernelGGL((split_reduce_kernel<TBF16>), grid, block, 0, s, p);
+      break;
+    case PA_DTYPE_FLOAT32:
+      hipLaunchKernelGGL((split_reduce_kernel<TF32>), grid, block, 0, s, p);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace pa

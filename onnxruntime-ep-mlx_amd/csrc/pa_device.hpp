@@ -1,0 +1,224 @@
+// pa_device.hpp — device-side helpers shared by the gfx950 kernels: dtype traits, exact
+// conversions, MFMA wrappers and the kernel parameter blocks.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "pa_mi355x.h"
+
+namespace pa {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+// ------------------------------------------------------------------------------ conversions
+// Integer round-to-nearest-even conversions: the rotary/append path must produce the exact bits
+// of the CPU restatement, so these do not depend on instruction selection.
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __builtin_bit_cast(float, (uint32_t)h << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+// IEEE binary16 conversion of the hardware (v_cvt_f16_f32) is round-to-nearest-even.
+__device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// OCP e4m3fn (bias 7, no infinities, 0x7f/0xff NaN, max 448).
+__device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
+  uint32_t s = (c & 0x80u) << 24;
+  uint32_t e = (c >> 3) & 15u, m = c & 7u;
+  float v;
+  if (e == 0)
+    v = (float)m * 0.001953125f;  // m * 2^-9
+  else
+    v = __builtin_bit_cast(float, ((e + 120u) << 23) | (m << 20));
+  if (e == 15 && m == 7) v = __builtin_nanf("");
+  return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v) | s);
+}
+// Saturating round-to-nearest-even encode; same arithmetic as the CPU restatement.
+__device__ __forceinline__ uint32_t f32_to_e4m3_sat(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  uint32_t s = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return 0x7fu;
+  float af = __builtin_bit_cast(float, a);
+  if (af >= 448.0f) return s | 0x7eu;
+  if (a == 0) return s;
+  int E = (int)(a >> 23) - 127;  // floor(log2) for normals; subnormal fp32 clamps below
+  if (E < -6) E = -6;
+  float q = __builtin_rintf(__builtin_ldexpf(af, 3 - E));
+  if (q >= 16.0f) {
+    E += 1;
+    q = 8.0f;
+  }
+  uint32_t qi = (uint32_t)q;
+  if (qi < 8u) return s | qi;
+  return s | ((uint32_t)(E + 7) << 3) | (qi - 8u);
+}
+
+// ------------------------------------------------------------------------------ dtype traits
+struct TF16 {
+  using raw = uint16_t;
+  using vec8 = f16x8;
+  static constexpr int code = PA_DTYPE_FLOAT16;
+  __device__ static float to_f32(raw h) { return f16_to_f32(h); }
+  __device__ static raw from_f32(float f) { return f32_to_f16_rne(f); }
+  __device__ static f32x4 mfma(vec8 a, vec8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ static vec8 cvt8(const float* x) {
+    vec8 r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = (_Float16)x[i];
+    return r;
+  }
+  __device__ static float back(_Float16 v) { return (float)v; }
+};
+
+struct TBF16 {
+  using raw = uint16_t;
+  using vec8 = bf16x8;
+  static constexpr int code = PA_DTYPE_BFLOAT16;
+  __device__ static float to_f32(raw h) { return bf16_to_f32(h); }
+  __device__ static raw from_f32(float f) { return f32_to_bf16_rne(f); }
+  __device__ static f32x4 mfma(vec8 a, vec8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ static vec8 cvt8(const float* x) {
+    vec8 r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = (__bf16)x[i];
+    return r;
+  }
+  __device__ static float back(__bf16 v) { return (float)v; }
+};
+
+struct TF32 {
+  using raw = float;
+  static constexpr int code = PA_DTYPE_FLOAT32;
+  __device__ static float to_f32(raw h) { return h; }
+  __device__ static raw from_f32(float f) { return f; }
+};
+
+// ------------------------------------------------------------------------------ wave helpers
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Sequence index of packed token t: largest b with cum[b] <= t (cum monotone).
+__device__ __forceinline__ int seq_of_token(const int32_t* cum, int batch, int t) {
+  int lo = 0, hi = batch - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (__ldg(&cum[mid]) <= t)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  return lo;
+}
+
+// ------------------------------------------------------------------------------ parameters
+struct AppendParams {
+  const void* query;
+  const void* key;
+  const void* value;
+  void* q_out;
+  void* k_out;
+  void* key_cache;
+  void* value_cache;
+  const float* k_scale;
+  const float* v_scale;
+  const void* cos_cache;
+  const void* sin_cache;
+  const void* q_norm;
+  const void* k_norm;
+  const int32_t* cum;
+  const int32_t* past;
+  const int32_t* block_table;
+  const int32_t* slot_mapping;
+  int64_t num_blocks;
+  int64_t rotary_positions;
+  int32_t block_size, kv_heads, head_dim, num_heads;
+  int32_t batch, max_blocks, num_tokens;
+  int32_t rotary_half, rotary_offset, rotary_interleaved;
+  int32_t do_q;  // process query rows (rotary/norm) into q_out
+  float norm_eps;
+};
+
+struct AttnParams {
+  const void* q;
+  const void* k_new;
+  const void* v_new;
+  const void* key_cache;
+  const void* value_cache;
+  const float* k_scale;
+  const float* v_scale;
+  const int32_t* cum;
+  const int32_t* past;
+  const int32_t* block_table;
+  const void* head_sink;
+  void* out;
+  float* part_o;   // [num_tokens, H, max_splits, D]
+  float* part_ml;  // [num_tokens, H, max_splits, 2]  (m in log2 units, l)
+  int64_t num_blocks;
+  int32_t block_size, kv_heads, head_dim, num_heads;
+  int32_t batch, max_blocks, num_tokens;
+  int32_t chunk, max_splits;
+  int32_t max_query_len;  // host bound on new tokens per sequence (row-group count)
+  float scale;       // softmax scale applied to q.k
+  float scale_log2;  // scale * log2(e)
+  float softcap;     // 0 = off
+  int32_t window;    // <= 0 = off
+  int32_t causal;
+  int32_t read_all_from_cache;  // fp8 rule: every position from the pages
+};
+
+// Final normalisation shared by every attention kernel: the factor that turns an output
+// accumulated relative to running max m (log2 units) with running sum l into the result,
+// folding in an optional sink logit that only enters the denominator.
+__device__ __forceinline__ float finalize_factor(float m, float l, float sink_x) {
+  float mm = fmaxf(m, sink_x);
+  if (mm == kNegInf) return 0.0f;
+  float f = (m == kNegInf) ? 0.0f : exp2f(m - mm);
+  float lt = l * f + ((sink_x == kNegInf) ? 0.0f : exp2f(sink_x - mm));
+  return lt > 0.0f ? f / lt : 0.0f;
+}
+
+template <typename TT>
+__device__ __forceinline__ float sink_logit(const AttnParams& p, int h) {
+  if (!p.head_sink) return kNegInf;
+  return TT::to_f32(reinterpret_cast<const typename TT::raw*>(p.head_sink)[h]) * kLog2e;
+}
+
+// Launchers (defined in the .hip files).
+hipError_t launch_rotary_append(const AppendParams& p, pa_dtype act, pa_dtype cache_dtype,
+                                hipStream_t s);
+hipError_t launch_attn_generic(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
+                               hipStream_t s);
+hipError_t launch_decode_mfma(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
+                              hipStream_t s);
+hipError_t launch_prefill_mfma(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
+                               hipStream_t s);
+hipError_t launch_split_reduce(const AttnParams& p, pa_dtype act, hipStream_t s);
+bool decode_mfma_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype);
+bool prefill_mfma_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype);
+
+}  // namespace pa

@@ -1,0 +1,262 @@
+"""torch-facing mirror of the com.microsoft::PagedAttention operator on MI355X.
+
+``paged_attention`` takes the operator's inputs in the reference's order and meaning
+(query, key, value, key_cache, value_cache, cumulative_sequence_length, past_seqlens,
+block_table, cos_cache, sin_cache, slot_mapping, head_sink, q_norm_weight, k_norm_weight,
+k_scale, v_scale, attention_metadata; rust/src/ops/attention.rs:3857-4382) and its attributes
+(num_heads, kv_num_heads, scale, softcap, local_window_size, do_rotary, rotary_interleaved,
+rotary_offset, is_causal, qk_norm_epsilon).  Caches are updated in place, as the reference
+writes ORT's input buffers back (engine.rs:1212-1357); the return value is
+(output, key_cache, value_cache) so callers can bind the optional cache outputs to the same
+storage.  torch only provides device memory and the stream; all compute runs in
+libonnxruntime_ep_mlx_amd.so.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import torch
+
+from . import _capi as capi
+
+_DTYPES = {
+    torch.float16: capi.PA_DTYPE_FLOAT16,
+    torch.bfloat16: capi.PA_DTYPE_BFLOAT16,
+    torch.float32: capi.PA_DTYPE_FLOAT32,
+    torch.float8_e4m3fn: capi.PA_DTYPE_FP8_E4M3,
+}
+
+
+def pa_dtype(t: torch.dtype) -> int:
+    try:
+        return _DTYPES[t]
+    except KeyError:
+        raise TypeError(f"PagedAttention: unsupported dtype {t}") from None
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _need_cuda(name: str, t: torch.Tensor | None) -> None:
+    if t is not None and not t.is_cuda:
+        raise ValueError(f"PagedAttention: {name} must be a device tensor")
+
+
+def _contig(name: str, t: torch.Tensor | None) -> None:
+    if t is not None and not t.is_contiguous():
+        raise ValueError(f"PagedAttention: {name} must be contiguous")
+
+
+@dataclass
+class _Workspace:
+    buf: torch.Tensor | None = None
+
+    def get(self, nbytes: int, device: torch.device) -> torch.Tensor | None:
+        if nbytes == 0:
+            return None
+        if self.buf is None or self.buf.numel() < nbytes or self.buf.device != device:
+            self.buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        return self.buf
+
+
+_ws = _Workspace()
+
+
+def cache_desc(key_cache: torch.Tensor, value_cache: torch.Tensor,
+               k_scale: torch.Tensor | None = None,
+               v_scale: torch.Tensor | None = None) -> capi.PaCache:
+    if key_cache.dim() != 4 or key_cache.shape != value_cache.shape:
+        raise ValueError("key_cache must be [num_blocks,block_size,kv_num_heads,head_size]")
+    nb, bs, kv, d = key_cache.shape
+    return capi.PaCache(_ptr(key_cache), _ptr(value_cache), _ptr(k_scale), _ptr(v_scale),
+                        nb, bs, kv, d, pa_dtype(key_cache.dtype))
+
+
+def batch_desc(cum: torch.Tensor, past: torch.Tensor, block_table: torch.Tensor,
+               num_tokens: int, slot_mapping: torch.Tensor | None = None,
+               max_query_len: int = 0) -> capi.PaBatch:
+    for name, t in (("cumulative_sequence_length", cum), ("past_seqlens", past),
+                    ("block_table", block_table), ("slot_mapping", slot_mapping)):
+        if t is not None and t.dtype != torch.int32:
+            raise ValueError(f"input {name} must be int32")
+        _contig(name, t)
+    return capi.PaBatch(_ptr(cum), _ptr(past), _ptr(block_table), _ptr(slot_mapping),
+                        cum.numel() - 1, block_table.shape[1], num_tokens, max_query_len)
+
+
+def attn_desc(num_heads: int, scale: float = 0.0, softcap: float = 0.0,
+              local_window_size: int = -1, is_causal: int = 1,
+              head_sink: torch.Tensor | None = None) -> capi.PaAttn:
+    return capi.PaAttn(num_heads, scale, softcap, local_window_size, is_causal, _ptr(head_sink))
+
+
+class PagePool:
+    """HBM page pool behind the cache tensors (pa_pool_*); exposes K/V as torch views."""
+
+    def __init__(self, num_blocks: int, block_size: int, kv_heads: int, head_dim: int,
+                 dtype: torch.dtype, device: torch.device | str = "cuda"):
+        lib = capi.load()
+        self.device = torch.device(device)
+        self.shape = (num_blocks, block_size, kv_heads, head_dim)
+        self.dtype = dtype
+        h = C.c_void_p()
+        with torch.cuda.device(self.device):
+            capi.check(lib.pa_pool_create(num_blocks, block_size, kv_heads, head_dim,
+                                          pa_dtype(dtype), C.byref(h)))
+        self._h = h
+        self.key_cache = self._view(lib.pa_pool_k_ptr(h), self.shape, dtype)
+        self.value_cache = self._view(lib.pa_pool_v_ptr(h), self.shape, dtype)
+        self.k_scale = self.v_scale = None
+        if dtype == torch.float8_e4m3fn:
+            self.k_scale = self._view(lib.pa_pool_k_scale_ptr(h), (num_blocks, kv_heads),
+                                      torch.float32)
+            self.v_scale = self._view(lib.pa_pool_v_scale_ptr(h), (num_blocks, kv_heads),
+                                      torch.float32)
+
+    def _view(self, ptr: int, shape, dtype) -> torch.Tensor:
+        # Wrap the pool's device memory as a tensor without copying (DLPack-free: a
+        # storage from the raw pointer via torch's UntypedStorage is not public, so use
+        # the __cuda_array_interface__ protocol).
+        n = 1
+        for s in shape:
+            n *= s
+        itemsize = torch.empty((), dtype=dtype).element_size()
+        holder = _DevPtr(ptr, n * itemsize, self.device)
+        raw = torch.as_tensor(holder, device=self.device)
+        return raw.view(dtype).view(*shape)
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            torch.cuda.synchronize(self.device)
+            capi.load().pa_pool_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class _DevPtr:
+    """Minimal __cuda_array_interface__ exporter for a raw device allocation (uint8)."""
+
+    def __init__(self, ptr: int, nbytes: int, device: torch.device):
+        self.__cuda_array_interface__ = {
+            "shape": (nbytes,), "typestr": "|u1", "data": (ptr, False), "version": 3,
+            "strides": None, "stream": None,
+        }
+
+
+def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, key_cache: torch.Tensor,
+                      value_cache: torch.Tensor, cum: torch.Tensor, past: torch.Tensor,
+                      block_table: torch.Tensor, slot_mapping: torch.Tensor | None = None,
+                      k_scale: torch.Tensor | None = None,
+                      v_scale: torch.Tensor | None = None) -> None:
+    lib = capi.load()
+    for n, t in (("key", key), ("value", value), ("key_cache", key_cache)):
+        _need_cuda(n, t)
+        _contig(n, t)
+    cache = cache_desc(key_cache, value_cache, k_scale, v_scale)
+    batch = batch_desc(cum, past, block_table, key.shape[0], slot_mapping)
+    capi.check(lib.pa_reshape_and_cache(C.byref(cache), C.byref(batch), pa_dtype(key.dtype),
+                                        _ptr(key), _ptr(value), _stream(key.device)))
+
+
+def rotary_append(query, key, value, key_cache, value_cache, cum, past, block_table, *,
+                  num_heads, cos_cache=None, sin_cache=None, rotary_offset=0,
+                  rotary_interleaved=0, q_norm_weight=None, k_norm_weight=None,
+                  qk_norm_epsilon=1e-6, slot_mapping=None, k_scale=None, v_scale=None):
+    """Fused RMSNorm + RoPE + append.  Returns the transformed (query, key) rows."""
+    lib = capi.load()
+    cache = cache_desc(key_cache, value_cache, k_scale, v_scale)
+    batch = batch_desc(cum, past, block_table, key.shape[0], slot_mapping)
+    transform = cos_cache is not None or q_norm_weight is not None
+    q_out = torch.empty_like(query) if transform else query
+    k_out = torch.empty_like(key) if transform else key
+    rot_pos = cos_cache.shape[0] if cos_cache is not None else 0
+    rot_half = cos_cache.shape[1] if cos_cache is not None else 0
+    capi.check(lib.pa_rotary_append(
+        C.byref(cache), C.byref(batch), num_heads, pa_dtype(query.dtype), _ptr(query),
+        _ptr(key), _ptr(value), _ptr(q_out) if transform else None,
+        _ptr(k_out) if transform else None, _ptr(cos_cache), _ptr(sin_cache), rot_pos,
+        rot_half, rotary_offset, rotary_interleaved, _ptr(q_norm_weight), _ptr(k_norm_weight),
+        qk_norm_epsilon, _stream(query.device)))
+    return q_out, k_out
+
+
+def attention(q, k_new, v_new, key_cache, value_cache, cum, past, block_table, *, num_heads,
+              scale=0.0, softcap=0.0, local_window_size=-1, is_causal=1, head_sink=None,
+              k_scale=None, v_scale=None, max_query_len=0, kind=0, chunk=0, out=None):
+    """Attention over the (already appended) paged cache; kind/chunk force a kernel family."""
+    lib = capi.load()
+    cache = cache_desc(key_cache, value_cache, k_scale, v_scale)
+    batch = batch_desc(cum, past, block_table, q.shape[0], None, max_query_len)
+    attn = attn_desc(num_heads, scale, softcap, local_window_size, is_causal, head_sink)
+    act = pa_dtype(q.dtype)
+    nbytes = lib.pa_attention_workspace_bytes_ex(C.byref(cache), C.byref(batch), C.byref(attn),
+                                                 act, kind, chunk)
+    ws = _ws.get(nbytes, q.device)
+    if out is None:
+        out = torch.empty_like(q)
+    capi.check(lib.pa_attention_ex(C.byref(cache), C.byref(batch), C.byref(attn), act, _ptr(q),
+                                   _ptr(k_new), _ptr(v_new), _ptr(out), _ptr(ws), nbytes, kind,
+                                   chunk, _stream(q.device)))
+    return out
+
+
+def paged_attention(query, key, value, key_cache, value_cache, cumulative_sequence_length,
+                    past_seqlens, block_table, cos_cache=None, sin_cache=None,
+                    slot_mapping=None, head_sink=None, q_norm_weight=None, k_norm_weight=None,
+                    k_scale=None, v_scale=None, attention_metadata=None, *, num_heads,
+                    kv_num_heads, scale=0.0, softcap=0.0, local_window_size=-1, do_rotary=0,
+                    rotary_interleaved=0, rotary_offset=0, is_causal=1, qk_norm_epsilon=1e-6,
+                    validate=True, output=None):
+    """com.microsoft::PagedAttention on MI355X (operator-level entry, pa_paged_attention).
+
+    ``attention_metadata`` is accepted and ignored, like the reference
+    (test_attention_contracts.py:338-367).  With ``validate`` the int32 metadata is copied to
+    the host and checked with the reference's rules (attention.rs:3934-3990), which is what the
+    reference does every step; without it the device copies are trusted.
+    """
+    del attention_metadata
+    lib = capi.load()
+    if query.dim() != 2:
+        raise ValueError("query must have rank 2")
+    for n, t in (("query", query), ("key", key), ("value", value), ("key_cache", key_cache),
+                 ("value_cache", value_cache)):
+        _need_cuda(n, t)
+        _contig(n, t)
+    node = capi.PaNode(num_heads, kv_num_heads, scale, softcap, local_window_size, do_rotary,
+                       rotary_interleaved, rotary_offset, is_causal, qk_norm_epsilon)
+    host = {}
+    if validate:
+        for name, t in (("cum", cumulative_sequence_length), ("past", past_seqlens),
+                        ("bt", block_table), ("slots", slot_mapping)):
+            host[name] = None if t is None else t.detach().to("cpu").contiguous()
+    if output is None:
+        output = torch.empty_like(query)
+    cache = cache_desc(key_cache, value_cache, k_scale, v_scale)
+    io = capi.PaIO(
+        pa_dtype(query.dtype), query.shape[0], query.shape[1], _ptr(query), _ptr(key),
+        _ptr(value), cache, _ptr(cumulative_sequence_length), _ptr(past_seqlens),
+        _ptr(block_table), cumulative_sequence_length.numel() - 1, block_table.shape[1],
+        _ptr(cos_cache) if do_rotary else None, _ptr(sin_cache) if do_rotary else None,
+        cos_cache.shape[0] if (do_rotary and cos_cache is not None) else 0,
+        cos_cache.shape[1] if (do_rotary and cos_cache is not None) else 0,
+        _ptr(slot_mapping), _ptr(head_sink), _ptr(q_norm_weight), _ptr(k_norm_weight),
+        _ptr(host.get("cum")), _ptr(host.get("past")), _ptr(host.get("bt")),
+        _ptr(host.get("slots")), _ptr(output))
+    nbytes = lib.pa_paged_attention_workspace_bytes(C.byref(node), C.byref(io))
+    ws = _ws.get(nbytes, query.device)
+    capi.check(lib.pa_paged_attention(C.byref(node), C.byref(io), _ptr(ws), nbytes,
+                                      _stream(query.device)))
+    return output, key_cache, value_cache

@@ -1,0 +1,452 @@
+/*
+ * pa_oracle.c — CPU restatement of the reference's paged GQA KV-cache attention path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see pa_oracle.h).  Compiled with -ffp-contract=off so that every
+ * float operation rounds on its own, which the per-op rounding rules below depend on.
+ */
+#include "pa_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+static inline uint32_t f2u(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+static inline float u2f(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/* ---------------------------------------------------------------- converters (IEEE / OCP) */
+
+uint16_t orc_f32_to_bf16(float f) {
+  uint32_t u = f2u(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u); /* quiet NaN */
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+float orc_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+uint16_t orc_f32_to_f16(float f) {
+  uint32_t u = f2u(f);
+  uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));
+  if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520 rounds to inf */
+  if (a >= 0x38800000u) {                                   /* normal half: >= 2^-14 */
+    uint32_t r = a + 0xfffu + ((a >> 13) & 1u);
+    return (uint16_t)(sign | ((r - 0x38000000u) >> 13));
+  }
+  if (a <= 0x33000000u) return sign; /* <= 2^-25: rounds (ties-to-even) to zero */
+  uint32_t e = a >> 23;
+  uint32_t m = (a & 0x7fffffu) | 0x800000u;
+  uint32_t shift = 126u - e; /* value in units of 2^-24 is m >> shift */
+  uint32_t q = m >> shift;
+  uint32_t rem = m & ((1u << shift) - 1u);
+  uint32_t half = 1u << (shift - 1u);
+  if (rem > half || (rem == half && (q & 1u))) q++;
+  return (uint16_t)(sign | q);
+}
+
+float orc_f16_to_f32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  if (e == 0) {
+    float v = ldexpf((float)m, -24);
+    return sign ? -v : v;
+  }
+  if (e == 31) return u2f(sign | 0x7f800000u | (m << 13));
+  return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+float orc_e4m3_to_f32(uint8_t c) {
+  int s = c >> 7, e = (c >> 3) & 15, m = c & 7;
+  if (e == 15 && m == 7) return NAN;
+  float v = e == 0 ? ldexpf((float)m, -9) : ldexpf((float)(8 + m), e - 10);
+  return s ? -v : v;
+}
+
+uint8_t orc_f32_to_e4m3(float f) {
+  if (isnan(f)) return 0x7f;
+  uint8_t s = signbit(f) ? 0x80 : 0x00;
+  float a = fabsf(f);
+  if (a >= 448.0f) return s | 0x7e;
+  if (a == 0.0f) return s;
+  int e2;
+  frexpf(a, &e2);
+  int E = e2 - 1; /* floor(log2 a) */
+  if (E < -6) E = -6;
+  /* quantum 2^(E-3); dividing by a power of two is exact, rintf rounds ties to even */
+  float q = rintf(ldexpf(a, 3 - E));
+  if (q >= 16.0f) { /* rounded up into the next binade */
+    E += 1;
+    q = 8.0f;
+  }
+  if (q < 8.0f) return s | (uint8_t)q; /* subnormal (only possible when E == -6) */
+  return s | (uint8_t)(((E + 7) << 3) | ((int)q - 8));
+}
+
+static inline float ld(const void* p, int64_t i, int dt) {
+  switch (dt) {
+    case ORC_F16: return orc_f16_to_f32(((const uint16_t*)p)[i]);
+    case ORC_BF16: return orc_bf16_to_f32(((const uint16_t*)p)[i]);
+    case ORC_E4M3: return orc_e4m3_to_f32(((const uint8_t*)p)[i]);
+    default: return ((const float*)p)[i];
+  }
+}
+
+static inline void st(void* p, int64_t i, float v, int dt) {
+  switch (dt) {
+    case ORC_F16: ((uint16_t*)p)[i] = orc_f32_to_f16(v); break;
+    case ORC_BF16: ((uint16_t*)p)[i] = orc_f32_to_bf16(v); break;
+    case ORC_E4M3: ((uint8_t*)p)[i] = orc_f32_to_e4m3(v); break;
+    default: ((float*)p)[i] = v; break;
+  }
+}
+
+/* round a float to dtype and back (identity for fp32) */
+static inline float rd(float v, int dt) {
+  switch (dt) {
+    case ORC_F16: return orc_f16_to_f32(orc_f32_to_f16(v));
+    case ORC_BF16: return orc_bf16_to_f32(orc_f32_to_bf16(v));
+    default: return v;
+  }
+}
+
+static inline int esize(int dt) { return dt == ORC_F32 ? 4 : dt == ORC_E4M3 ? 1 : 2; }
+
+void orc_encode(const float* src, void* dst, int64_t n, int dtype) {
+  for (int64_t i = 0; i < n; ++i) st(dst, i, src[i], dtype);
+}
+
+void orc_decode(const void* src, float* dst, int64_t n, int dtype) {
+  for (int64_t i = 0; i < n; ++i) dst[i] = ld(src, i, dtype);
+}
+
+/* ------------------------------------------------------------------ RMSNorm (a4, optional) */
+/* attention.rs:4045-4049 calls mlx_fast_rms_norm(x, w, eps): fp32 sum of squares, then the
+ * normalised value is rounded to T and multiplied by the weight in T. */
+void orc_rms_norm_rows(void* x, int64_t rows, int heads, int head_dim, const void* weight,
+                       float eps, int dtype) {
+  for (int64_t r = 0; r < rows * heads; ++r) {
+    int64_t base = r * head_dim;
+    float acc = 0.0f;
+    for (int i = 0; i < head_dim; ++i) {
+      float v = ld(x, base + i, dtype);
+      acc += v * v;
+    }
+    float inv = 1.0f / sqrtf(acc / (float)head_dim + eps);
+    for (int i = 0; i < head_dim; ++i) {
+      float v = rd(ld(x, base + i, dtype) * inv, dtype);
+      st(x, base + i, v * ld(weight, i, dtype), dtype);
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------- RoPE (a5) */
+/* gqa_rope (attention.rs:459-503): non-interleaved o1 = x1*c - x2*s, o2 = x2*c + x1*s on the
+ * rotary slice [offset, offset + 2*half); interleaved on (even, odd) pairs; every multiply,
+ * subtract and add is a separate MLX op in the activation dtype, so each rounds to T.  The
+ * cos/sin rows are the supplied cache rows at absolute positions (cos_sin_row :523-535). */
+int orc_rope_rows(void* x, int64_t rows, int heads, int head_dim, const int32_t* positions,
+                  const void* cos_cache, const void* sin_cache, int64_t cos_rows, int half,
+                  int offset, int interleaved, int dtype) {
+  if (offset < 0 || offset + 2 * half > head_dim) return 1;
+  for (int64_t r = 0; r < rows; ++r) {
+    int64_t pos = positions[r];
+    if (pos < 0 || pos >= cos_rows) return 2;
+    for (int h = 0; h < heads; ++h) {
+      int64_t base = (r * heads + h) * (int64_t)head_dim + offset;
+      for (int i = 0; i < half; ++i) {
+        float c = ld(cos_cache, pos * half + i, dtype);
+        float s = ld(sin_cache, pos * half + i, dtype);
+        int64_t i1 = interleaved ? base + 2 * i : base + i;
+        int64_t i2 = interleaved ? base + 2 * i + 1 : base + half + i;
+        float a = ld(x, i1, dtype), b = ld(x, i2, dtype);
+        float o1 = rd(rd(a * c, dtype) - rd(b * s, dtype), dtype);
+        float o2 = rd(rd(b * c, dtype) + rd(a * s, dtype), dtype);
+        st(x, i1, o1, dtype);
+        st(x, i2, o2, dtype);
+      }
+    }
+  }
+  return 0;
+}
+
+/* ---------------------------------------------------------------- append / scatter (a6) */
+
+static int token_slot(const int32_t* cum, const int32_t* past, const int32_t* bt, int b,
+                      int max_blocks, const int32_t* slot_mapping, int j, int block_size,
+                      int64_t* slot) {
+  int64_t t = cum[b] + j;
+  if (slot_mapping) {
+    *slot = slot_mapping[t];
+    return 0;
+  }
+  int64_t logical = (int64_t)past[b] + j;
+  *slot = (int64_t)bt[(int64_t)b * max_blocks + logical / block_size] * block_size +
+          logical % block_size;
+  return 0;
+}
+
+/* Paged quantised encode, restating kv_cache.rs:170-192 (x / scale, zero scale -> 0) with the
+ * fp8 e4m3 saturating RNE cast in place of the int8 clip/round. */
+static uint8_t quant_e4m3(float x, float scale) {
+  if (scale == 0.0f) return 0;
+  return orc_f32_to_e4m3(x / scale);
+}
+
+int orc_reshape_and_cache(const void* key, const void* value, int act_dtype, void* key_cache,
+                          void* value_cache, int cache_dtype, const float* k_scale,
+                          const float* v_scale, const int32_t* cum, const int32_t* past,
+                          const int32_t* block_table, int batch, int max_blocks,
+                          const int32_t* slot_mapping, int64_t num_blocks, int block_size,
+                          int kv_heads, int head_dim) {
+  int64_t row = (int64_t)kv_heads * head_dim;
+  for (int b = 0; b < batch; ++b) {
+    int nq = cum[b + 1] - cum[b];
+    for (int j = 0; j < nq; ++j) {
+      int64_t slot;
+      token_slot(cum, past, block_table, b, max_blocks, slot_mapping, j, block_size, &slot);
+      if (slot < 0) continue;
+      if (slot >= num_blocks * block_size) return 3;
+      int64_t t = cum[b] + j;
+      if (cache_dtype == ORC_E4M3) {
+        int64_t blk = slot / block_size;
+        for (int kh = 0; kh < kv_heads; ++kh) {
+          float ks = k_scale[blk * kv_heads + kh], vs = v_scale[blk * kv_heads + kh];
+          for (int i = 0; i < head_dim; ++i) {
+            int64_t src = t * row + (int64_t)kh * head_dim + i;
+            int64_t dst = slot * row + (int64_t)kh * head_dim + i;
+            ((uint8_t*)key_cache)[dst] = quant_e4m3(ld(key, src, act_dtype), ks);
+            ((uint8_t*)value_cache)[dst] = quant_e4m3(ld(value, src, act_dtype), vs);
+          }
+        }
+      } else {
+        int es = esize(cache_dtype);
+        memcpy((char*)key_cache + slot * row * es, (const char*)key + t * row * es,
+               (size_t)(row * es));
+        memcpy((char*)value_cache + slot * row * es, (const char*)value + t * row * es,
+               (size_t)(row * es));
+      }
+    }
+  }
+  return 0;
+}
+
+/* ----------------------------------------------------------------------- attention (a8) */
+
+static double cache_elem(const void* cache, int cache_dtype, const float* scales, int64_t blk,
+                         int kv_heads, int kh, int64_t idx) {
+  if (cache_dtype == ORC_E4M3) {
+    float v = orc_e4m3_to_f32(((const uint8_t*)cache)[idx]) * scales[blk * kv_heads + kh];
+    return (double)v;
+  }
+  return (double)ld(cache, idx, cache_dtype);
+}
+
+int orc_paged_attention(const void* q, const void* k_new, const void* v_new, int act_dtype,
+                        const void* key_cache, const void* value_cache, int cache_dtype,
+                        const float* k_scale, const float* v_scale, const int32_t* cum,
+                        const int32_t* past, const int32_t* block_table, int batch,
+                        int max_blocks, int64_t num_blocks, int block_size, int num_heads,
+                        int kv_heads, int head_dim, float scale, float softcap, int window,
+                        int causal, const float* head_sink, double* out) {
+  (void)num_blocks;
+  int g = num_heads / kv_heads;
+  int d = head_dim;
+  int64_t row = (int64_t)kv_heads * d;
+  int quant = cache_dtype == ORC_E4M3;
+  double* scores = NULL;
+  size_t cap = 0;
+  for (int b = 0; b < batch; ++b) {
+    int s0 = cum[b], nq = cum[b + 1] - cum[b];
+    if (nq <= 0) continue;
+    int64_t pastb = past[b], total = pastb + nq;
+    if ((size_t)total > cap) {
+      cap = (size_t)total;
+      free(scores);
+      scores = (double*)malloc(cap * sizeof(double));
+      if (!scores) return 4;
+    }
+    for (int i = 0; i < nq; ++i) {
+      int64_t t = s0 + i, rp = pastb + i;
+      for (int h = 0; h < num_heads; ++h) {
+        int kh = h / g;
+        const int64_t qbase = (t * num_heads + h) * (int64_t)d;
+        double m = -INFINITY;
+        for (int64_t p = 0; p < total; ++p) {
+          int visible = (!causal || p <= rp) && (window <= 0 || p >= rp - window + 1);
+          if (!visible) {
+            scores[p] = -INFINITY;
+            continue;
+          }
+          double dot = 0.0;
+          if (p < pastb || quant) {
+            int64_t blk = block_table[(int64_t)b * max_blocks + p / block_size];
+            int64_t base = (blk * block_size + p % block_size) * row + (int64_t)kh * d;
+            for (int e = 0; e < d; ++e)
+              dot += (double)ld(q, qbase + e, act_dtype) *
+                     cache_elem(key_cache, cache_dtype, k_scale, blk, kv_heads, kh, base + e);
+          } else {
+            int64_t base = (s0 + (p - pastb)) * row + (int64_t)kh * d;
+            for (int e = 0; e < d; ++e)
+              dot += (double)ld(q, qbase + e, act_dtype) * (double)ld(k_new, base + e, act_dtype);
+          }
+          double s = (double)scale * dot;
+          if (softcap > 0.0f) s = (double)softcap * tanh(s / (double)softcap);
+          scores[p] = s;
+          if (s > m) m = s;
+        }
+        double sink = head_sink ? (double)head_sink[h] : -INFINITY;
+        double mm = m > sink ? m : sink;
+        double l = 0.0;
+        double* o = out + qbase;
+        for (int e = 0; e < d; ++e) o[e] = 0.0;
+        if (mm == -INFINITY) continue; /* nothing visible: the sum==0 guard leaves zeros */
+        for (int64_t p = 0; p < total; ++p) {
+          if (scores[p] == -INFINITY) continue;
+          double w = exp(scores[p] - mm);
+          l += w;
+          if (p < pastb || quant) {
+            int64_t blk = block_table[(int64_t)b * max_blocks + p / block_size];
+            int64_t base = (blk * block_size + p % block_size) * row + (int64_t)kh * d;
+            for (int e = 0; e < d; ++e)
+              o[e] += w * cache_elem(value_cache, cache_dtype, v_scale, blk, kv_heads, kh, base + e);
+          } else {
+            int64_t base = (s0 + (p - pastb)) * row + (int64_t)kh * d;
+            for (int e = 0; e < d; ++e) o[e] += w * (double)ld(v_new, base + e, act_dtype);
+          }
+        }
+        if (head_sink) l += exp(sink - mm);
+        if (l != 0.0)
+          for (int e = 0; e < d; ++e) o[e] /= l;
+      }
+    }
+  }
+  free(scores);
+  return 0;
+}
+
+int orc_paged_attention_op(int act_dtype, int cache_dtype, const void* query, const void* key,
+                           const void* value, int64_t num_tokens, void* key_cache,
+                           void* value_cache, const float* k_scale, const float* v_scale,
+                           int64_t num_blocks, int block_size, const int32_t* cum,
+                           const int32_t* past, const int32_t* block_table, int batch,
+                           int max_blocks, const void* cos_cache, const void* sin_cache,
+                           int64_t cos_rows, int rot_half, int rot_offset, int interleaved,
+                           const int32_t* slot_mapping, const float* head_sink,
+                           const void* q_norm, const void* k_norm, float norm_eps,
+                           int num_heads, int kv_heads, int head_dim, float scale,
+                           float softcap, int window, int causal, double* out, void* out_t) {
+  int es = esize(act_dtype);
+  size_t qbytes = (size_t)num_tokens * num_heads * head_dim * es;
+  size_t kbytes = (size_t)num_tokens * kv_heads * head_dim * es;
+  void* qr = malloc(qbytes ? qbytes : 1);
+  void* kr = malloc(kbytes ? kbytes : 1);
+  int32_t* pos = (int32_t*)malloc((size_t)(num_tokens ? num_tokens : 1) * sizeof(int32_t));
+  int rc = 0;
+  if (!qr || !kr || !pos) {
+    rc = 4;
+    goto done;
+  }
+  memcpy(qr, query, qbytes);
+  memcpy(kr, key, kbytes);
+  for (int b = 0; b < batch; ++b)
+    for (int t = cum[b]; t < cum[b + 1]; ++t) pos[t] = past[b] + (t - cum[b]);
+  if (q_norm) {
+    orc_rms_norm_rows(qr, num_tokens, num_heads, head_dim, q_norm, norm_eps, act_dtype);
+    orc_rms_norm_rows(kr, num_tokens, kv_heads, head_dim, k_norm, norm_eps, act_dtype);
+  }
+  if (cos_cache) {
+    rc = orc_rope_rows(qr, num_tokens, num_heads, head_dim, pos, cos_cache, sin_cache, cos_rows,
+                       rot_half, rot_offset, interleaved, act_dtype);
+    if (!rc)
+      rc = orc_rope_rows(kr, num_tokens, kv_heads, head_dim, pos, cos_cache, sin_cache,
+                         cos_rows, rot_half, rot_offset, interleaved, act_dtype);
+    if (rc) goto done;
+  }
+  rc = orc_reshape_and_cache(kr, value, act_dtype, key_cache, value_cache, cache_dtype, k_scale,
+                             v_scale, cum, past, block_table, batch, max_blocks, slot_mapping,
+                             num_blocks, block_size, kv_heads, head_dim);
+  if (rc) goto done;
+  rc = orc_paged_attention(qr, kr, value, act_dtype, key_cache, value_cache, cache_dtype, k_scale,
+                           v_scale, cum, past, block_table, batch, max_blocks, num_blocks,
+                           block_size, num_heads, kv_heads, head_dim, scale, softcap, window,
+                           causal, head_sink, out);
+  if (!rc && out_t) {
+    int64_t n = num_tokens * (int64_t)num_heads * head_dim;
+    for (int64_t i = 0; i < n; ++i) st(out_t, i, (float)out[i], act_dtype);
+  }
+done:
+  free(qr);
+  free(kr);
+  free(pos);
+  return rc;
+}
+
+/* ------------------------------------------------------------ contiguous GQA (C1 semantic) */
+/* test_gqa_position_cache.py:104-126: past_b = total_b - S with total_b = seqlens_k[b] + 1;
+ * new rows land at [past_b, total_b); row i attends to [max(0, end - window), end) with
+ * end = past_b + i + 1 when causal (else total_b); GQA head map kv = h / (H / KV). */
+int orc_gqa_contiguous(int dtype, const void* query, const void* key, const void* value,
+                       void* present_k, void* present_v, int batch, int seq, int num_heads,
+                       int kv_heads, int head_dim, int cap, const int32_t* seqlens_k,
+                       float scale, float softcap, int window, int causal, double* out) {
+  int g = num_heads / kv_heads, d = head_dim;
+  double* scores = (double*)malloc((size_t)(cap > 0 ? cap : 1) * sizeof(double));
+  if (!scores) return 4;
+  for (int b = 0; b < batch; ++b) {
+    int total = seqlens_k[b] + 1;
+    int pastb = total - seq;
+    if (pastb < 0 || total > cap) {
+      free(scores);
+      return 5;
+    }
+    for (int j = 0; j < seq; ++j)
+      for (int kh = 0; kh < kv_heads; ++kh)
+        for (int e = 0; e < d; ++e) {
+          int64_t src = (((int64_t)b * seq + j) * kv_heads + kh) * d + e;
+          int64_t dst = (((int64_t)b * kv_heads + kh) * cap + pastb + j) * d + e;
+          st(present_k, dst, ld(key, src, dtype), dtype);
+          st(present_v, dst, ld(value, src, dtype), dtype);
+        }
+    for (int i = 0; i < seq; ++i)
+      for (int h = 0; h < num_heads; ++h) {
+        int kh = h / g;
+        int end = causal ? pastb + i + 1 : total;
+        if (end > total) end = total;
+        int start = window > 0 ? (end - window > 0 ? end - window : 0) : 0;
+        int64_t qb = (((int64_t)b * seq + i) * num_heads + h) * d;
+        double m = -INFINITY;
+        for (int p = start; p < end; ++p) {
+          int64_t kb = (((int64_t)b * kv_heads + kh) * cap + p) * d;
+          double dot = 0.0;
+          for (int e = 0; e < d; ++e)
+            dot += (double)ld(query, qb + e, dtype) * (double)ld(present_k, kb + e, dtype);
+          double s = (double)scale * dot;
+          if (softcap > 0.0f) s = (double)softcap * tanh(s / (double)softcap);
+          scores[p] = s;
+          if (s > m) m = s;
+        }
+        double* o = out + qb;
+        for (int e = 0; e < d; ++e) o[e] = 0.0;
+        double l = 0.0;
+        for (int p = start; p < end; ++p) {
+          double w = exp(scores[p] - m);
+          l += w;
+          int64_t vb = (((int64_t)b * kv_heads + kh) * cap + p) * d;
+          for (int e = 0; e < d; ++e) o[e] += w * (double)ld(present_v, vb + e, dtype);
+        }
+        if (l != 0.0)
+          for (int e = 0; e < d; ++e) o[e] /= l;
+      }
+  }
+  free(scores);
+  return 0;
+}

@@ -1,0 +1,109 @@
+/*
+ * pa_oracle.h — CPU restatement of the reference's paged GQA KV-cache attention path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load this library, and only as the checker (or the timed CPU baseline).  The product
+ * (onnxruntime-ep-mlx_amd/) never links, loads or falls back to it.
+ *
+ * Every function cites the reference file:line it restates (paths relative to the reference
+ * root).  The reference itself (Rust + MLX + Metal) cannot be built here: no rustc/cargo, no
+ * ORT headers, no MLX, no Metal.
+ *
+ * Pins (what checks each function independently of its own formula) live in
+ * tests/test_oracle.py: numpy/torch dtype casts for the converters, torch-CPU bf16/fp16
+ * arithmetic evaluating the reference's rotate_half formulation for RoPE, byte invariants and
+ * the reference's duplicate-slot known answer for append, torch's fp64
+ * scaled_dot_product_attention plus closed forms for attention, and torch.float8_e4m3fn for
+ * the fp8 encoder.
+ */
+#ifndef PA_ORACLE_H
+#define PA_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ORC_F16 = 1, ORC_BF16 = 2, ORC_F32 = 3, ORC_E4M3 = 4 };
+
+/* Scalar converters (round-to-nearest-even from IEEE-754 / OCP FP8 definitions). */
+uint16_t orc_f32_to_bf16(float f);
+float orc_bf16_to_f32(uint16_t h);
+uint16_t orc_f32_to_f16(float f);
+float orc_f16_to_f32(uint16_t h);
+uint8_t orc_f32_to_e4m3(float f); /* RNE, saturating to +-448, NaN -> 0x7f */
+float orc_e4m3_to_f32(uint8_t c);
+
+/* Bulk converters between float32 and a storage dtype. */
+void orc_encode(const float* src, void* dst, int64_t n, int dtype);
+void orc_decode(const void* src, float* dst, int64_t n, int dtype);
+
+/* In-place RMSNorm over head_dim of rows [rows, heads, head_dim] (mlx_fast_rms_norm at
+ * attention.rs:4045-4049; numpy form test_paged_attention.py:101-103). */
+void orc_rms_norm_rows(void* x, int64_t rows, int heads, int head_dim, const void* weight,
+                       float eps, int dtype);
+
+/* In-place rotary embedding with per-op rounding to dtype (gqa_rope attention.rs:459-503,
+ * rope_with_offset :3812-3855, cos_sin_row :523-535). positions[rows]. */
+int orc_rope_rows(void* x, int64_t rows, int heads, int head_dim, const int32_t* positions,
+                  const void* cos_cache, const void* sin_cache, int64_t cos_rows, int half,
+                  int offset, int interleaved, int dtype);
+
+/* Slot rule + scatter (attention.rs:4064-4120; test_paged_attention.py:117-126).
+ * cache_dtype == ORC_E4M3 quantises x / scale[block, kv-head] (zero scale -> 0). */
+int orc_reshape_and_cache(const void* key, const void* value, int act_dtype, void* key_cache,
+                          void* value_cache, int cache_dtype, const float* k_scale,
+                          const float* v_scale, const int32_t* cum, const int32_t* past,
+                          const int32_t* block_table, int batch, int max_blocks,
+                          const int32_t* slot_mapping, int64_t num_blocks, int block_size,
+                          int kv_heads, int head_dim);
+
+/* Attention after append, in double (_paged_ref test_paged_attention.py:127-155, dense
+ * fallback attention.rs:4192-4319, sink/softcap :79-118). q/k_new/v_new are the rotated rows in
+ * act_dtype.  head_sink: fp32 [H] or NULL.  out: [num_tokens, H*head_dim] doubles. */
+int orc_paged_attention(const void* q, const void* k_new, const void* v_new, int act_dtype,
+                        const void* key_cache, const void* value_cache, int cache_dtype,
+                        const float* k_scale, const float* v_scale, const int32_t* cum,
+                        const int32_t* past, const int32_t* block_table, int batch,
+                        int max_blocks, int64_t num_blocks, int block_size, int num_heads,
+                        int kv_heads, int head_dim, float scale, float softcap, int window,
+                        int causal, const float* head_sink, double* out);
+
+/* Whole operator: norm + rope + append + attention (paged_attention_op attention.rs:3857-4382
+ * and _paged_ref test_paged_attention.py:63-157).  Caches are updated in place.
+ * out_t (may be NULL) receives the output rounded to act_dtype. */
+int orc_paged_attention_op(int act_dtype, int cache_dtype, const void* query, const void* key,
+                           const void* value, int64_t num_tokens, void* key_cache,
+                           void* value_cache, const float* k_scale, const float* v_scale,
+                           int64_t num_blocks, int block_size, const int32_t* cum,
+                           const int32_t* past, const int32_t* block_table, int batch,
+                           int max_blocks, const void* cos_cache, const void* sin_cache,
+                           int64_t cos_rows, int rot_half, int rot_offset, int interleaved,
+                           const int32_t* slot_mapping, const float* head_sink,
+                           const void* q_norm, const void* k_norm, float norm_eps,
+                           int num_heads, int kv_heads, int head_dim, float scale,
+                           float softcap, int window, int causal, double* out, void* out_t);
+
+/* Contiguous-cache GroupQueryAttention (ORT CPU semantics as restated by the reference's
+ * test_gqa_position_cache.py:88-126 and gqa_batched attention.rs:586-848):
+ * query [B,S,H*d], key/value [B,S,KV*d], present_k/v [B,KV,cap,d] (past in, present out),
+ * seqlens_k[b] = total_b - 1.  Computes in double.  out [B,S,H*d]. */
+int orc_gqa_contiguous(int dtype, const void* query, const void* key, const void* value,
+                       void* present_k, void* present_v, int batch, int seq, int num_heads,
+                       int kv_heads, int head_dim, int cap, const int32_t* seqlens_k,
+                       float scale, float softcap, int window, int causal, double* out);
+
+/* CPU baseline (pa_cpu_baseline.c): the same contiguous GQA decode in fp32 accumulation over
+ * all requested threads, one task per (sequence, kv-head).  k/v: [sum_b ctx_b, KV, d] packed
+ * per sequence at row offsets kv_offset[b]; q [B, H, d]; out [B, H, d] float. */
+int orc_cpu_gqa_decode(int dtype, const void* q, const void* k, const void* v,
+                       const int64_t* kv_offset, const int32_t* ctx, int batch, int num_heads,
+                       int kv_heads, int head_dim, float scale, float* out, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,186 @@
+"""ctypes access to the CPU oracle (oracle/build/libpa_oracle.so) for the test suite.
+
+Test infrastructure only: the oracle is the checker, never the thing measured or shipped.
+Arrays are numpy "raw storage" arrays: float16 for fp16, uint16 bit patterns for bf16,
+float32 for fp32, uint8 codes for fp8 e4m3.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent.parent
+ORACLE_DIR = ROOT / "oracle"
+LIB = ORACLE_DIR / "build" / "libpa_oracle.so"
+
+F16, BF16, F32, E4M3 = 1, 2, 3, 4
+RAW = {F16: np.float16, BF16: np.uint16, F32: np.float32, E4M3: np.uint8}
+NAMES = {F16: "fp16", BF16: "bf16", F32: "fp32", E4M3: "e4m3"}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            subprocess.run(["make", "-s", "-C", os.fspath(ORACLE_DIR)], check=True)
+        L = C.CDLL(os.fspath(LIB))
+        P, I32, I64, F = C.c_void_p, C.c_int, C.c_int64, C.c_float
+        L.orc_f32_to_bf16.restype = C.c_uint16
+        L.orc_f32_to_bf16.argtypes = [F]
+        L.orc_bf16_to_f32.restype = F
+        L.orc_bf16_to_f32.argtypes = [C.c_uint16]
+        L.orc_f32_to_f16.restype = C.c_uint16
+        L.orc_f32_to_f16.argtypes = [F]
+        L.orc_f16_to_f32.restype = F
+        L.orc_f16_to_f32.argtypes = [C.c_uint16]
+        L.orc_f32_to_e4m3.restype = C.c_uint8
+        L.orc_f32_to_e4m3.argtypes = [F]
+        L.orc_e4m3_to_f32.restype = F
+        L.orc_e4m3_to_f32.argtypes = [C.c_uint8]
+        L.orc_encode.argtypes = [P, P, I64, I32]
+        L.orc_decode.argtypes = [P, P, I64, I32]
+        L.orc_rms_norm_rows.argtypes = [P, I64, I32, I32, P, F, I32]
+        L.orc_rope_rows.restype = I32
+        L.orc_rope_rows.argtypes = [P, I64, I32, I32, P, P, P, I64, I32, I32, I32, I32]
+        L.orc_reshape_and_cache.restype = I32
+        L.orc_reshape_and_cache.argtypes = [P, P, I32, P, P, I32, P, P, P, P, P, I32, I32, P,
+                                            I64, I32, I32, I32]
+        L.orc_paged_attention.restype = I32
+        L.orc_paged_attention.argtypes = [P, P, P, I32, P, P, I32, P, P, P, P, P, I32, I32, I64,
+                                          I32, I32, I32, I32, F, F, I32, I32, P, P]
+        L.orc_paged_attention_op.restype = I32
+        L.orc_paged_attention_op.argtypes = [I32, I32, P, P, P, I64, P, P, P, P, I64, I32, P, P,
+                                             P, I32, I32, P, P, I64, I32, I32, I32, P, P, P, P,
+                                             F, I32, I32, I32, F, F, I32, I32, P, P]
+        L.orc_gqa_contiguous.restype = I32
+        L.orc_gqa_contiguous.argtypes = [I32, P, P, P, P, P, I32, I32, I32, I32, I32, I32, P, F,
+                                         F, I32, I32, P]
+        L.orc_cpu_gqa_decode.restype = I32
+        L.orc_cpu_gqa_decode.argtypes = [I32, P, P, P, P, P, I32, I32, I32, I32, F, P, I32]
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data
+
+
+def encode(x: np.ndarray, dtype: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, RAW[dtype])
+    lib().orc_encode(_p(x), _p(out), x.size, dtype)
+    return out
+
+
+def decode(raw: np.ndarray, dtype: int) -> np.ndarray:
+    raw = np.ascontiguousarray(raw)
+    out = np.empty(raw.shape, np.float32)
+    lib().orc_decode(_p(raw), _p(out), raw.size, dtype)
+    return out
+
+
+def rms_norm_rows(x: np.ndarray, heads: int, head_dim: int, weight: np.ndarray, eps: float,
+                  dtype: int) -> np.ndarray:
+    x = np.ascontiguousarray(x).copy()
+    rows = x.size // (heads * head_dim)
+    lib().orc_rms_norm_rows(_p(x), rows, heads, head_dim, _p(np.ascontiguousarray(weight)),
+                            eps, dtype)
+    return x
+
+
+def rope_rows(x: np.ndarray, heads: int, head_dim: int, positions: np.ndarray, cos: np.ndarray,
+              sin: np.ndarray, offset: int, interleaved: int, dtype: int) -> np.ndarray:
+    x = np.ascontiguousarray(x).copy()
+    pos = np.ascontiguousarray(positions, dtype=np.int32)
+    rc = lib().orc_rope_rows(_p(x), pos.size, heads, head_dim, _p(pos), _p(cos), _p(sin),
+                             cos.shape[0], cos.shape[1], offset, interleaved, dtype)
+    assert rc == 0, rc
+    return x
+
+
+def reshape_and_cache(key, value, act_dtype, kc, vc, cache_dtype, cum, past, bt,
+                      slot_mapping=None, k_scale=None, v_scale=None):
+    kc, vc = kc.copy(), vc.copy()
+    nb, bs, kv, d = kc.shape
+    rc = lib().orc_reshape_and_cache(
+        _p(key), _p(value), act_dtype, _p(kc), _p(vc), cache_dtype, _p(k_scale), _p(v_scale),
+        _p(cum), _p(past), _p(bt), len(cum) - 1, bt.shape[1], _p(slot_mapping), nb, bs, kv, d)
+    assert rc == 0, rc
+    return kc, vc
+
+
+def paged_attention_op(case: dict, *, return_cache=True):
+    """Run the whole operator on a case dict (see pa_cases.make_case)."""
+    c = case
+    kc, vc = c["key_cache"].copy(), c["value_cache"].copy()
+    nb, bs, kv, d = kc.shape
+    T = c["query"].shape[0]
+    H = c["num_heads"]
+    out = np.zeros((T, H * d), np.float64)
+    out_t = np.zeros((T, H * d), RAW[c["dtype"]])
+    cos, sin = c.get("cos_cache"), c.get("sin_cache")
+    sink = c.get("head_sink_f32")
+    rc = lib().orc_paged_attention_op(
+        c["dtype"], c["cache_dtype"], _p(c["query"]), _p(c["key"]), _p(c["value"]), T, _p(kc),
+        _p(vc), _p(c.get("k_scale")), _p(c.get("v_scale")), nb, bs, _p(c["cum"]), _p(c["past"]),
+        _p(c["block_table"]), len(c["cum"]) - 1, c["block_table"].shape[1], _p(cos), _p(sin),
+        0 if cos is None else cos.shape[0], 0 if cos is None else cos.shape[1],
+        c.get("rotary_offset", 0), c.get("rotary_interleaved", 0), _p(c.get("slot_mapping")),
+        _p(sink), _p(c.get("q_norm")), _p(c.get("k_norm")), c.get("qk_norm_epsilon", 1e-6), H,
+        kv, d, c.get("scale", 0.0) or float(np.float32(1.0) / np.sqrt(np.float32(d))),
+        c.get("softcap", 0.0), c.get("local_window_size", -1), c.get("is_causal", 1), _p(out),
+        _p(out_t))
+    assert rc == 0, rc
+    return out, out_t, kc, vc
+
+
+def paged_attention(q, k_new, v_new, act_dtype, kc, vc, cache_dtype, cum, past, bt, H, scale,
+                    softcap=0.0, window=-1, causal=1, head_sink=None, k_scale=None,
+                    v_scale=None):
+    nb, bs, kv, d = kc.shape
+    out = np.zeros((q.shape[0], H * d), np.float64)
+    rc = lib().orc_paged_attention(
+        _p(q), _p(k_new), _p(v_new), act_dtype, _p(kc), _p(vc), cache_dtype, _p(k_scale),
+        _p(v_scale), _p(cum), _p(past), _p(bt), len(cum) - 1, bt.shape[1], nb, bs, H, kv, d,
+        scale, softcap, window, causal, _p(head_sink), _p(out))
+    assert rc == 0, rc
+    return out
+
+
+def gqa_contiguous(dtype, q, k, v, pk, pv, seqlens_k, H, KV, d, scale, softcap=0.0, window=-1,
+                   causal=1):
+    B, S = q.shape[0], q.shape[1]
+    pk, pv = pk.copy(), pv.copy()
+    out = np.zeros((B, S, H * d), np.float64)
+    rc = lib().orc_gqa_contiguous(dtype, _p(q), _p(k), _p(v), _p(pk), _p(pv), B, S, H, KV, d,
+                                  pk.shape[2], _p(np.ascontiguousarray(seqlens_k, np.int32)),
+                                  scale, softcap, window, causal, _p(out))
+    assert rc == 0, rc
+    return out, pk, pv
+
+
+def cpu_gqa_decode(dtype, q, k, v, kv_offset, ctx, H, KV, d, scale, threads):
+    B = len(ctx)
+    out = np.zeros((B, H, d), np.float32)
+    rc = lib().orc_cpu_gqa_decode(dtype, _p(q), _p(k), _p(v),
+                                  _p(np.ascontiguousarray(kv_offset, np.int64)),
+                                  _p(np.ascontiguousarray(ctx, np.int32)), B, H, KV, d, scale,
+                                  _p(out), threads)
+    assert rc == 0, rc
+    return out
+
+
+def rel_l2(a, b) -> float:
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    den = np.linalg.norm(b)
+    return float(np.linalg.norm(a - b) / (den if den > 0 else 1.0))

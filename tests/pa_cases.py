@@ -1,0 +1,141 @@
+"""Seeded PagedAttention cases shared by the CPU and GPU tests.
+
+Shapes and draws follow the reference's own test inputs (tests/ops/test_paged_attention.py:
+182-208: numpy default_rng(seed), new lengths in [1, 4], past uniform within capacity, values
+N(0,1)*0.3, block_table = permutation of the pool), with the dtype and geometry as parameters.
+bf16 values are produced with the oracle's RNE encoder (pinned against torch in test_oracle).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+import _oracle as orc
+from _oracle import BF16, E4M3, F16, F32, RAW
+
+
+def rotary_cache(positions: int, rot_dim: int, theta: float, dtype: int):
+    """cos/sin [positions, rot_dim/2] built in float64 then rounded to dtype (the structured
+    cache the reference's tests and _models.rotary_caches build, _models.py:261-266)."""
+    half = rot_dim // 2
+    inv = 1.0 / (theta ** (np.arange(half, dtype=np.float64) / half))
+    ang = np.arange(positions, dtype=np.float64)[:, None] * inv[None, :]
+    return orc.encode(np.cos(ang), dtype), orc.encode(np.sin(ang), dtype)
+
+
+def fp8_pages(rng, shape, scale_mult=1.0):
+    """e4m3 pages with per-(block, kv-head) fp32 scales: x ~ N(0,1), scale = amax/448."""
+    nb, bs, kv, d = shape
+    x = rng.standard_normal(shape).astype(np.float32) * scale_mult
+    amax = np.abs(x).max(axis=(1, 3))  # [nb, kv]
+    scale = (amax / 448.0).astype(np.float32)
+    scale[scale == 0] = 1.0
+    codes = orc.encode(x / scale[:, None, :, None], E4M3)
+    return codes, scale
+
+
+def make_case(H, KV, d, nb, bs, batch, *, dtype=F16, cache_dtype=None, seed=0, new_lens=None,
+              past=None, max_blocks=None, do_rotary=0, interleaved=0, theta=10000.0,
+              rot_dim=None, rotary_offset=0, slot_mapping=None, head_sink=None, qk_norm=False,
+              softcap=0.0, window=-1, causal=1, scale=0.0, std=0.3, value_std=None):
+    rng = np.random.default_rng(seed)
+    cache_dtype = dtype if cache_dtype is None else cache_dtype
+    if max_blocks is None:
+        max_blocks = nb // batch
+    cap = max_blocks * bs
+    if new_lens is None:
+        new_lens = rng.integers(1, min(4, cap) + 1, size=batch)
+    new_lens = np.asarray(new_lens, np.int32)
+    if past is None:
+        past = np.array([rng.integers(0, cap - nl + 1) for nl in new_lens])
+    past = np.asarray(past, np.int32)
+    cum = np.concatenate([[0], np.cumsum(new_lens)]).astype(np.int32)
+    T = int(cum[-1])
+    vstd = std if value_std is None else value_std
+
+    def draw(shape, s):
+        return orc.encode(rng.standard_normal(shape) * s, dtype)
+
+    case = dict(num_heads=H, kv_num_heads=KV, head_dim=d, dtype=dtype, cache_dtype=cache_dtype,
+                cum=cum, past=past, softcap=softcap, local_window_size=window, is_causal=causal,
+                scale=scale)
+    case["query"] = draw((T, H * d), std)
+    case["key"] = draw((T, KV * d), std)
+    case["value"] = draw((T, KV * d), vstd)
+    if cache_dtype == E4M3:
+        case["key_cache"], case["k_scale"] = fp8_pages(rng, (nb, bs, KV, d))
+        case["value_cache"], case["v_scale"] = fp8_pages(rng, (nb, bs, KV, d))
+    else:
+        case["key_cache"] = draw((nb, bs, KV, d), std)
+        case["value_cache"] = draw((nb, bs, KV, d), vstd)
+    case["block_table"] = rng.permutation(nb)[: batch * max_blocks].astype(np.int32).reshape(
+        batch, max_blocks)
+    if do_rotary:
+        rd = d if rot_dim is None else rot_dim
+        case["cos_cache"], case["sin_cache"] = rotary_cache(cap + 8, rd, theta, dtype)
+        case["rotary_offset"] = rotary_offset
+        case["rotary_interleaved"] = interleaved
+    if slot_mapping is not None:
+        case["slot_mapping"] = np.asarray(slot_mapping, np.int32)
+    if head_sink is not None:
+        hs = orc.encode(np.asarray(head_sink, np.float32), dtype)
+        case["head_sink"] = hs
+        case["head_sink_f32"] = orc.decode(hs, dtype)
+    if qk_norm:
+        case["q_norm"] = orc.encode(np.linspace(0.75, 1.25, d), dtype)
+        case["k_norm"] = orc.encode(np.linspace(1.25, 0.75, d), dtype)
+        case["qk_norm_epsilon"] = 1e-5
+    return case
+
+
+# ----------------------------------------------------------------------------- torch bridging
+
+def torch_dtype(code: int):
+    import torch
+    return {F16: torch.float16, BF16: torch.bfloat16, F32: torch.float32,
+            E4M3: torch.float8_e4m3fn}[code]
+
+
+def to_torch(raw: np.ndarray, code: int, device="cuda"):
+    import torch
+    raw = np.ascontiguousarray(raw)
+    if code == BF16:
+        t = torch.from_numpy(raw.view(np.int16)).view(torch.bfloat16)
+    elif code == E4M3:
+        t = torch.from_numpy(raw).view(torch.float8_e4m3fn)
+    else:
+        t = torch.from_numpy(raw)
+    return t.to(device)
+
+
+def from_torch(t, code: int) -> np.ndarray:
+    import torch
+    t = t.detach().cpu().contiguous()
+    if code == BF16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    if code == E4M3:
+        return t.view(torch.uint8).numpy()
+    return t.numpy()
+
+
+def run_gpu_op(case: dict, validate=True, device="cuda"):
+    """Run the operator-level entry (pa_paged_attention) on the GPU for a case."""
+    import torch
+    import onnxruntime_ep_mlx_amd as ep
+    dt, cdt = case["dtype"], case["cache_dtype"]
+    T = lambda k, code=dt: None if case.get(k) is None else to_torch(case[k], code, device)
+    I = lambda k: None if case.get(k) is None else torch.from_numpy(
+        np.ascontiguousarray(case[k], np.int32)).to(device)
+    F = lambda k: None if case.get(k) is None else torch.from_numpy(case[k]).to(device)
+    kc, vc = T("key_cache", cdt), T("value_cache", cdt)
+    out, kc, vc = ep.paged_attention(
+        T("query"), T("key"), T("value"), kc, vc, I("cum"), I("past"), I("block_table"),
+        T("cos_cache"), T("sin_cache"), I("slot_mapping"), T("head_sink"), T("q_norm"),
+        T("k_norm"), F("k_scale"), F("v_scale"), None,
+        num_heads=case["num_heads"], kv_num_heads=case["kv_num_heads"],
+        scale=case.get("scale", 0.0), softcap=case.get("softcap", 0.0),
+        local_window_size=case.get("local_window_size", -1),
+        do_rotary=int("cos_cache" in case), rotary_interleaved=case.get("rotary_interleaved", 0),
+        rotary_offset=case.get("rotary_offset", 0), is_causal=case.get("is_causal", 1),
+        qk_norm_epsilon=case.get("qk_norm_epsilon", 1e-6), validate=validate)
+    torch.cuda.synchronize()
+    return from_torch(out, dt), from_torch(kc, cdt), from_torch(vc, cdt)

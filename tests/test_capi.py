@@ -1,0 +1,179 @@
+"""CPU tests of the C ABI: the library loads, exports every declared symbol, and the host
+logic (claim predicate, metadata validation with the reference's "PagedAttention:" errors)
+behaves like the reference -- all without launching device work."""
+from __future__ import annotations
+
+import ctypes as C
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import onnxruntime_ep_mlx_amd as ep
+from onnxruntime_ep_mlx_amd import _capi as capi
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def _declared_functions():
+    text = (ROOT / "include" / "pa_mi355x.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pa_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = capi.load()
+    declared = _declared_functions()
+    assert len(declared) >= 15
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert sorted(capi.EXPORTS) == declared
+
+
+def test_version_and_error_channel():
+    lib = capi.load()
+    assert b"gfx950" in lib.pa_version()
+    h = C.c_void_p()
+    rc = lib.pa_pool_create(0, 16, 8, 128, capi.PA_DTYPE_BFLOAT16, C.byref(h))
+    assert rc == capi.PA_ERR_INVALID_ARGUMENT
+    assert b"invalid pool geometry" in lib.pa_last_error()
+
+
+# ------------------------------------------------------------------------------ claim
+def _node(dtype=capi.PA_DTYPE_BFLOAT16, H=32, KV=8, d=128, nb=40000, bs=16, T=64, B=64,
+          mb=512, cache_dtype=None, rotary=True):
+    n = capi.PaNodeInfo()
+    cache_dtype = dtype if cache_dtype is None else cache_dtype
+    n.num_inputs, n.num_outputs = 10 if rotary else 8, 1
+    shapes = {0: [T, H * d], 1: [T, KV * d], 2: [T, KV * d], 3: [nb, bs, KV, d],
+              4: [nb, bs, KV, d], 5: [B + 1], 6: [B], 7: [B, mb], 8: [8200, d // 2],
+              9: [8200, d // 2]}
+    dts = {0: dtype, 1: dtype, 2: dtype, 3: cache_dtype, 4: cache_dtype, 5: 10, 6: 10, 7: 10,
+           8: dtype, 9: dtype}
+    for i in range(n.num_inputs):
+        n.input_present[i] = 1
+        n.input_dtype[i] = dts[i]
+        n.input_rank[i] = len(shapes[i])
+        for j, s in enumerate(shapes[i]):
+            n.input_shape[i][j] = s
+    n.output_present[0] = 1
+    n.output_dtype[0] = dtype
+    n.output_rank[0] = 2
+    n.output_shape[0][0], n.output_shape[0][1] = T, H * d
+    n.num_heads, n.kv_num_heads = H, KV
+    n.do_rotary = int(rotary)
+    n.local_window_size = -1
+    n.is_causal = 1
+    return n
+
+
+def _claim(n):
+    buf = C.create_string_buffer(256)
+    ok = capi.load().pa_paged_attention_claim(C.byref(n), buf, 256)
+    return ok, buf.value.decode()
+
+
+def test_claim_accepts_baseline_config3_node():
+    assert _claim(_node()) == (1, "")
+
+
+def test_claim_accepts_fp8_cache_with_block_scales():
+    n = _node(cache_dtype=capi.PA_DTYPE_FP8_E4M3, rotary=False)
+    n.num_inputs = 16
+    for i in (14, 15):
+        n.input_present[i] = 1
+        n.input_dtype[i] = capi.PA_DTYPE_FLOAT32
+        n.input_rank[i] = 2
+        n.input_shape[i][0], n.input_shape[i][1] = 40000, 8
+    assert _claim(n)[0] == 1
+    n.input_shape[15][1] = 4
+    assert "v_scale" in _claim(n)[1]
+
+
+@pytest.mark.parametrize("mutate,reason", [
+    (lambda n: setattr(n, "is_causal", 2), "is_causal must be 0 or 1"),
+    (lambda n: n.output_dtype.__setitem__(0, capi.PA_DTYPE_FLOAT32),
+     "only supported for fp16/bf16"),
+    (lambda n: setattr(n, "kv_num_heads", 5), "positive multiple of kv_num_heads"),
+    (lambda n: setattr(n, "local_window_size", 0), "local_window_size must be -1 or positive"),
+    (lambda n: setattr(n, "softcap", -1.0), "softcap must be finite and non-negative"),
+    (lambda n: (setattr(n, "rotary_offset", 4), n.input_shape[8].__setitem__(1, 32),
+                n.input_shape[9].__setitem__(1, 32)), "rotary_offset must be a multiple of 8"),
+    (lambda n: (n.input_shape[8].__setitem__(1, 80), n.input_shape[9].__setitem__(1, 80)),
+     "must not exceed head_size"),
+    (lambda n: n.input_shape[8].__setitem__(1, 80), "matching [positions,rotary_dim/2]"),
+    (lambda n: setattr(n, "kv_cache_layout_latent", 1), "LATENT"),
+    (lambda n: n.input_dtype.__setitem__(5, capi.PA_DTYPE_FLOAT32), "input 5 must be int32"),
+    (lambda n: n.input_present.__setitem__(9, 0), "requires cos_cache and sin_cache"),
+    (lambda n: n.input_dtype.__setitem__(3, capi.PA_INT8_DTYPE), "storage dtype"),
+    (lambda n: setattr(n, "num_inputs", 18), "expects 8 required inputs"),
+])
+def test_claim_declines_with_reference_reasons(mutate, reason):
+    n = _node()
+    mutate(n)
+    ok, why = _claim(n)
+    assert ok == 0 and reason in why, why
+
+
+# ------------------------------------------------------------------------------ validation
+def _io(cum, past, bt, slots=None, nb=8, bs=4, T=None, H=4, KV=2, d=8):
+    """PagedAttention io with fake (never dereferenced) device pointers and real host copies:
+    validation fails before any device work, so this runs without a GPU."""
+    T = int(cum[-1]) if T is None else T
+    keep = [np.ascontiguousarray(a, np.int32) for a in (cum, past, bt)]
+    keep.append(None if slots is None else np.ascontiguousarray(slots, np.int32))
+    fake = 0x1000
+    cache = capi.PaCache(fake, fake, None, None, nb, bs, KV, d, capi.PA_DTYPE_FLOAT16)
+    io = capi.PaIO(capi.PA_DTYPE_FLOAT16, T, H * d, fake, fake, fake, cache, fake, fake, fake,
+                   len(cum) - 1, keep[2].shape[1], None, None, 0, 0,
+                   fake if slots is not None else None, None, None, None,
+                   keep[0].ctypes.data, keep[1].ctypes.data, keep[2].ctypes.data,
+                   None if slots is None else keep[3].ctypes.data, fake)
+    node = capi.PaNode(H, KV, 0.0, 0.0, -1, 0, 0, 0, 1, 1e-6)
+    return node, io, keep
+
+
+def _run_validation(node, io):
+    lib = capi.load()
+    rc = lib.pa_paged_attention(C.byref(node), C.byref(io), C.c_void_p(0x2000), 1 << 40, None)
+    return rc, lib.pa_last_error().decode()
+
+
+# test_attention_contracts.py:369-392
+@pytest.mark.parametrize("invalid", ["cumulative", "negative_past", "too_long", "block", "slot"])
+def test_invalid_live_metadata_errors(invalid):
+    rng = np.random.default_rng(123)
+    cum = np.array([0, 2, 3], np.int32)
+    past = np.array([1, 2], np.int32)
+    bt = rng.permutation(8).astype(np.int32).reshape(2, 4)
+    slots = None
+    if invalid == "cumulative":
+        cum[1] = -1
+    elif invalid == "negative_past":
+        past[0] = -1
+    elif invalid == "too_long":
+        past[0] = 1000
+    elif invalid == "block":
+        bt.fill(-1)
+    else:
+        slots = np.full(3, 1000, np.int32)
+    node, io, keep = _io(cum, past, bt, slots)
+    rc, msg = _run_validation(node, io)
+    assert rc == capi.PA_ERR_INVALID_ARGUMENT
+    assert msg.startswith("PagedAttention:"), msg
+
+
+def test_bad_head_counts_error():
+    node, io, keep = _io(np.array([0, 1], np.int32), np.array([0], np.int32),
+                         np.zeros((1, 2), np.int32))
+    node.kv_num_heads = 3
+    rc, msg = _run_validation(node, io)
+    assert rc != 0 and msg == "PagedAttention: bad num_heads/kv_num_heads"
+
+
+def test_workspace_query_is_pure_host():
+    node, io, keep = _io(np.array([0, 1, 2], np.int32), np.array([100, 7], np.int32),
+                         np.zeros((2, 4096), np.int32), nb=128, bs=4)
+    n = capi.load().pa_paged_attention_workspace_bytes(C.byref(node), C.byref(io))
+    assert n > 0 and n % 256 == 0

@@ -1,0 +1,270 @@
+"""GPU parity: the HIP path through the C ABI against the CPU oracle on identical seeded inputs.
+
+Bars: cache bytes after append bit-exact; outputs within
+rel-L2 <= 2e-3 (fp16/bf16) or <= 1e-5 (fp32).  For fp16/bf16 the output is compared with the
+oracle's output rounded to the activation dtype (the reference returns T), and additionally
+with the unrounded float64 result at twice the bar.  Geometries mirror the reference's
+tests/ops/test_paged_attention.py cases (cited per test) plus the BASELINE configs.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import _oracle as orc
+from _oracle import BF16, E4M3, F16, F32
+from pa_cases import make_case, run_gpu_op
+
+pytestmark = pytest.mark.gpu
+
+TOL = {F16: 2e-3, BF16: 2e-3, F32: 1e-5}
+
+
+def check(case, validate=True, tol=None):
+    ref, ref_t, kc_ref, vc_ref = orc.paged_attention_op(case)
+    out, kc, vc = run_gpu_op(case, validate=validate)
+    assert np.array_equal(kc, kc_ref), "key cache differs from the oracle"
+    assert np.array_equal(vc, vc_ref), "value cache differs from the oracle"
+    dt = case["dtype"]
+    got = orc.decode(out, dt).astype(np.float64)
+    bar = TOL[dt] if tol is None else tol
+    if dt == F32:
+        err = orc.rel_l2(got, ref)
+        assert err <= bar, f"rel-L2 {err:.3e} > {bar}"
+    else:
+        err_t = orc.rel_l2(got, orc.decode(ref_t, dt))
+        err64 = orc.rel_l2(got, ref)
+        assert err_t <= bar, f"rel-L2 vs T-rounded oracle {err_t:.3e} > {bar}"
+        assert err64 <= 2 * bar, f"rel-L2 vs fp64 oracle {err64:.3e} > {2 * bar}"
+    return out
+
+
+# test_paged_attention.py:239-242 (GQA/MHA/MQA x batch 1/3, d=16, block 4)
+@pytest.mark.parametrize("H,KV", [(4, 2), (4, 4), (8, 2), (2, 1)], ids=["gqa", "mha", "gqa8", "mqa"])
+@pytest.mark.parametrize("batch", [1, 3])
+def test_core(H, KV, batch):
+    check(make_case(H, KV, 16, 8 * batch, 4, batch, dtype=F16, seed=H * 10 + KV + batch))
+
+
+# same geometries at MFMA-kernel head sizes, both activation dtypes
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("dtype", [F16, BF16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("H,KV", [(4, 2), (8, 2), (2, 1), (8, 8)])
+def test_core_mfma(d, dtype, H, KV):
+    check(make_case(H, KV, d, 32, 16, 3, dtype=dtype, seed=d + H + KV))
+
+
+# test_paged_attention.py:245-247 (head 256)
+@pytest.mark.parametrize("kv", [1, 4])
+def test_head256(kv):
+    check(make_case(24, kv, 256, 4, 64, 1, dtype=F16, seed=256 + kv))
+
+
+# test_paged_attention.py:250-280 (causal x window decode replay)
+@pytest.mark.parametrize("causal", [0, 1])
+@pytest.mark.parametrize("window", [-1, 1, 3])
+@pytest.mark.parametrize("d", [16, 64])
+def test_mask_variants(causal, window, d):
+    for nt in (3, 1, 2, 1):
+        check(make_case(4, 2, d, 4, 4, 1, dtype=F16, seed=943 + nt, new_lens=[nt], past=[5],
+                        causal=causal, window=window))
+
+
+# test_paged_attention.py:284-286 (multi-block gather)
+@pytest.mark.parametrize("blk", [2, 8, 16])
+def test_multiblock(blk):
+    check(make_case(8, 2, 32, 16, blk, 2, dtype=F16, seed=blk + 7))
+    check(make_case(8, 2, 64, 16, blk, 2, dtype=BF16, seed=blk + 8))
+
+
+# test_paged_attention.py:289-318 (long context x 1/5/8 queries)
+@pytest.mark.parametrize("past", [4095, 16383])
+@pytest.mark.parametrize("queries", [1, 5, 8])
+@pytest.mark.parametrize("geom", [(24, 4, 256, 256), (8, 2, 128, 16)], ids=["d256", "d128"])
+def test_long_context(past, queries, geom):
+    H, KV, d, blk = geom
+    blocks = (past + queries + blk - 1) // blk
+    check(make_case(H, KV, d, blocks, blk, 1, dtype=F16, seed=412, new_lens=[queries],
+                    past=[past]), tol=3e-3 if d == 256 else None)
+
+
+# test_paged_attention.py:321-376 (slot_mapping normal / overwrite / skip, caches exact)
+@pytest.mark.parametrize("causal", [1, 0])
+@pytest.mark.parametrize("mapping", ["normal", "overwrite", "skip"])
+@pytest.mark.parametrize("d", [64, 128])
+def test_cache_overlay(causal, mapping, d):
+    queries, past = 5, 1022
+    base = make_case(4, 2, d, 8, 256, 1, dtype=F16, seed=417, new_lens=[queries], past=[past],
+                     causal=causal)
+    slots = None
+    if mapping == "skip":
+        slots = np.full(queries, -1, np.int32)
+    elif mapping == "overwrite":
+        slots = (base["block_table"][0, 0] * 256 + np.arange(queries)).astype(np.int32)
+    if slots is not None:
+        base["slot_mapping"] = slots
+    check(base)
+
+
+# test_paged_attention.py:605-659 (duplicate slots: the last token's row stays)
+def test_duplicate_slots_known_answer():
+    case = make_case(1, 1, 64, 2, 16, 1, dtype=F16, seed=42, new_lens=[2], past=[0])
+    case["query"] = np.ones((2, 64), np.float16)
+    case["key"] = np.stack([np.full(64, 1), np.full(64, 2)]).astype(np.float16)
+    case["value"] = np.stack([np.full(64, 3), np.full(64, 4)]).astype(np.float16)
+    case["slot_mapping"] = np.array([0, 0], np.int32)
+    out, kc, vc = run_gpu_op(case)
+    assert np.all(kc[0, 0, 0] == np.float16(2)) and np.all(vc[0, 0, 0] == np.float16(4))
+    check(case)
+
+
+# test_paged_attention.py:663-666 (RoPE neox / gptj) + the BASELINE bf16 theta=500000 rotary
+@pytest.mark.parametrize("interleaved", [0, 1], ids=["neox", "gptj"])
+@pytest.mark.parametrize("H,KV,d,dtype", [(4, 2, 16, F16), (2, 1, 64, F16), (32, 8, 128, BF16)])
+def test_rotary(interleaved, H, KV, d, dtype):
+    check(make_case(H, KV, d, 16, 4 if d < 128 else 16, 2, dtype=dtype, do_rotary=1,
+                    interleaved=interleaved, theta=500000.0 if dtype == BF16 else 10000.0,
+                    seed=H + d + interleaved))
+
+
+@pytest.mark.parametrize("offset,rot", [(8, 16), (0, 32), (16, 32)])
+def test_partial_rotary_offset(offset, rot):
+    check(make_case(4, 2, 64, 16, 16, 2, dtype=BF16, do_rotary=1, rot_dim=rot,
+                    rotary_offset=offset, seed=offset + rot))
+
+
+# test_paged_attention.py:855-983 (slot_mapping, head_sink, q/k norm, attention_metadata)
+@pytest.mark.parametrize("dtype", [F16, BF16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("d", [8, 64])
+def test_optional_inputs(dtype, d):
+    case = make_case(4, 2, d, 4, 4, 1, dtype=dtype, seed=129, new_lens=[2], past=[3],
+                     slot_mapping=[3, 9], head_sink=[-0.5, 0.25, 1.0, -1.0], qk_norm=True,
+                     std=1.0)
+    case["block_table"] = np.array([[2, 0, 1, 3]], np.int32)
+    check(case)
+
+
+@pytest.mark.parametrize("softcap", [0.0, 5.0, 30.0])
+@pytest.mark.parametrize("d", [16, 128])
+def test_softcap_and_sink(softcap, d):
+    check(make_case(8, 2, d, 64, 16, 3, dtype=BF16, seed=77, softcap=softcap,
+                    head_sink=np.linspace(-1, 2, 8), std=1.0))
+
+
+# GroupQueryAttention decode, fp32, B=1, 8q/2kv, d=64, past 128 + 1 new,
+# no rotary, scale 1/8 -- the GPU paged path on the equivalent pages must agree with the
+# contiguous-KV (ORT CPU semantics) restatement to rel-L2 <= 1e-5.
+def test_c1_gqa_fp32_against_contiguous():
+    rng = np.random.default_rng(1)
+    H, KV, d, past = 8, 2, 64, 128
+    q = rng.standard_normal((1, 1, H * d)).astype(np.float32)
+    k = rng.standard_normal((1, 1, KV * d)).astype(np.float32)
+    v = rng.standard_normal((1, 1, KV * d)).astype(np.float32)
+    pk = rng.standard_normal((1, KV, past + 1, d)).astype(np.float32)
+    pv = rng.standard_normal((1, KV, past + 1, d)).astype(np.float32)
+    ref, _, _ = orc.gqa_contiguous(F32, q, k, v, pk, pv, np.array([past]), H, KV, d, 0.125)
+    bs = 16
+    nb = (past + 1 + bs - 1) // bs
+    kc = np.zeros((nb, bs, KV, d), np.float32)
+    vc = np.zeros_like(kc)
+    for p in range(past):
+        kc[p // bs, p % bs] = pk[0, :, p]
+        vc[p // bs, p % bs] = pv[0, :, p]
+    case = dict(num_heads=H, kv_num_heads=KV, head_dim=d, dtype=F32, cache_dtype=F32,
+                cum=np.array([0, 1], np.int32), past=np.array([past], np.int32),
+                block_table=np.arange(nb, dtype=np.int32)[None], query=q.reshape(1, H * d),
+                key=k.reshape(1, KV * d), value=v.reshape(1, KV * d), key_cache=kc,
+                value_cache=vc, scale=0.125, is_causal=1, local_window_size=-1, softcap=0.0)
+    import onnxruntime_ep_mlx_amd as ep
+    import torch
+    from pa_cases import to_torch, from_torch
+    t = {n: to_torch(case[n], F32) for n in ("query", "key", "value", "key_cache", "value_cache")}
+    I = lambda a: torch.from_numpy(a).cuda()
+    out, kc_t, vc_t = ep.paged_attention(
+        t["query"], t["key"], t["value"], t["key_cache"], t["value_cache"], I(case["cum"]),
+        I(case["past"]), I(case["block_table"]), num_heads=H, kv_num_heads=KV, scale=0.125)
+    torch.cuda.synchronize()
+    got = from_torch(out, F32).reshape(ref.shape)
+    err = orc.rel_l2(got, ref)
+    assert err <= 1e-5, err
+    # present cache rows equal the contiguous present rows
+    kc_g = from_torch(kc_t, F32)
+    assert np.array_equal(kc_g[past // bs, past % bs], k.reshape(KV, d))
+
+
+# BASELINE config 3 geometry (Llama-3-8B decode), reduced batch for the oracle
+@pytest.mark.parametrize("kind", [0, 3], ids=["auto", "generic"])
+def test_c3_geometry_reduced_batch(kind):
+    rng = np.random.default_rng(3)
+    B, bs = 8, 16
+    ctx = rng.integers(512, 8193, size=B)
+    max_blocks = int((ctx.max() + bs - 1) // bs)
+    case = make_case(32, 8, 128, B * max_blocks, bs, B, dtype=BF16, seed=3, new_lens=[1] * B,
+                     past=ctx - 1, max_blocks=max_blocks, do_rotary=1, theta=500000.0, std=1.0)
+    if kind == 0:
+        check(case)
+        return
+    # force the generic kernel through the kernel-level entry points
+    import torch
+    import onnxruntime_ep_mlx_amd as ep
+    from pa_cases import to_torch, from_torch
+    ref, ref_t, kc_ref, vc_ref = orc.paged_attention_op(case)
+    t = {n: to_torch(case[n], BF16) for n in ("query", "key", "value", "key_cache",
+                                              "value_cache", "cos_cache", "sin_cache")}
+    I = {n: torch.from_numpy(case[n]).cuda() for n in ("cum", "past", "block_table")}
+    qr, kr = ep.rotary_append(t["query"], t["key"], t["value"], t["key_cache"],
+                              t["value_cache"], I["cum"], I["past"], I["block_table"],
+                              num_heads=32, cos_cache=t["cos_cache"], sin_cache=t["sin_cache"])
+    out = ep.attention(qr, kr, t["value"], t["key_cache"], t["value_cache"], I["cum"],
+                       I["past"], I["block_table"], num_heads=32, max_query_len=1, kind=3)
+    torch.cuda.synchronize()
+    assert np.array_equal(from_torch(t["key_cache"], BF16), kc_ref)
+    err = orc.rel_l2(orc.decode(from_torch(out, BF16), BF16), orc.decode(ref_t, BF16))
+    assert err <= 2e-3, err
+
+
+# split-K invariance: every chunk size gives the oracle's answer
+@pytest.mark.parametrize("chunk", [32, 64, 256, 1024])
+@pytest.mark.parametrize("kind", [1, 3], ids=["mfma", "generic"])
+def test_split_k_chunks(chunk, kind):
+    import torch
+    import onnxruntime_ep_mlx_amd as ep
+    from pa_cases import to_torch, from_torch
+    rng = np.random.default_rng(11)
+    B, bs = 4, 16
+    ctx = rng.integers(100, 3000, size=B)
+    mb = int((ctx.max() + bs - 1) // bs)
+    case = make_case(16, 4, 128, B * mb, bs, B, dtype=BF16, seed=11, new_lens=[1] * B,
+                     past=ctx - 1, max_blocks=mb, std=1.0)
+    ref, ref_t, kc_ref, _ = orc.paged_attention_op(case)
+    t = {n: to_torch(case[n], BF16) for n in ("query", "key", "value", "key_cache",
+                                              "value_cache")}
+    I = {n: torch.from_numpy(case[n]).cuda() for n in ("cum", "past", "block_table")}
+    ep.reshape_and_cache(t["key"], t["value"], t["key_cache"], t["value_cache"], I["cum"],
+                         I["past"], I["block_table"])
+    out = ep.attention(t["query"], t["key"], t["value"], t["key_cache"], t["value_cache"],
+                       I["cum"], I["past"], I["block_table"], num_heads=16, max_query_len=1,
+                       kind=kind, chunk=chunk)
+    torch.cuda.synchronize()
+    err = orc.rel_l2(orc.decode(from_torch(out, BF16), BF16), orc.decode(ref_t, BF16))
+    assert err <= 2e-3, err
+
+
+# BASELINE config 4 geometry (Qwen2.5-7B chunked prefill), reduced
+@pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "fp16"])
+def test_c4_prefill_reduced(dtype):
+    rng = np.random.default_rng(4)
+    B, bs, chunk = 2, 16, 64
+    past = rng.integers(0, 700, size=B)
+    mb = int((past.max() + chunk + bs - 1) // bs)
+    check(make_case(28, 4, 128, B * mb, bs, B, dtype=dtype, seed=4, new_lens=[chunk] * B,
+                    past=past, max_blocks=mb, std=1.0))
+
+
+# BASELINE config 5 geometry (fp8 e4m3 pages, per-(block, kv-head) scales), reduced
+@pytest.mark.parametrize("ctx", [1, 300, 4096])
+def test_c5_fp8_reduced(ctx):
+    bs = 16
+    mb = (ctx + bs - 1) // bs
+    check(make_case(64, 8, 128, 2 * mb + 2, bs, 2, dtype=BF16, cache_dtype=E4M3, seed=5,
+                    new_lens=[1, 1], past=[ctx - 1, max(ctx - 5, 0)], max_blocks=mb, std=1.0))
