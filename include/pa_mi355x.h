@@ -161,8 +161,10 @@ int pa_attention(const pa_cache* cache, const pa_batch* batch, const pa_attn* at
                  void* out, void* workspace, size_t workspace_bytes, pa_stream_t stream);
 
 /* Same contract, forcing one kernel family (for parity tests and benchmarks).
- * kind: 0 = automatic, 1 = decode (split-K MFMA), 2 = prefill (MFMA), 3 = generic VALU.
- * chunk_tokens: split-K chunk (multiple of 32; 0 = automatic). */
+ * kind: 0 = automatic, 1 = decode MFMA (balanced segments when every sequence has at most 16
+ * grouped query rows, else chunked split-K), 2 = prefill (MFMA), 3 = generic VALU,
+ * 4 = decode MFMA with chunked split-K forced.
+ * chunk_tokens: split-K chunk for the chunked/generic kernels (multiple of 32; 0 = automatic). */
 int pa_attention_ex(const pa_cache* cache, const pa_batch* batch, const pa_attn* attn,
                     pa_dtype act_dtype, const void* q, const void* k_new, const void* v_new,
                     void* out, void* workspace, size_t workspace_bytes, int32_t kind,

@@ -6,6 +6,7 @@
 // the caller except the page pool.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -87,10 +88,14 @@ int check_batch(const pa_batch* bt) {
 }
 
 // ---------------------------------------------------------------------------- attention plan
+// kind: 1 decode MFMA (balanced segments when every sequence has <= 16 grouped query rows,
+// chunked otherwise), 2 prefill MFMA, 3 generic VALU, 4 decode MFMA forced chunked.
 struct Plan {
-  int kind;  // 1 decode MFMA, 2 prefill MFMA, 3 generic
+  int kind;
+  bool balanced;
   int chunk;
-  int max_splits;
+  int max_splits;    // chunk count (chunked/generic) or segment count (balanced)
+  size_t part_rows;  // rows of fp32 partials in the workspace
 };
 
 int max_ctx_bound(const pa_cache* c, const pa_batch* b) {
@@ -98,23 +103,47 @@ int max_ctx_bound(const pa_cache* c, const pa_batch* b) {
   return (int)std::min<int64_t>(v, INT32_MAX / 2);
 }
 
+// Compute units of the current device (256 when no device is visible: sizing only).
+int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    return 256;
+  cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
 Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype act, int kind,
                int chunk) {
   Plan pl{};
   const int g = a->num_heads / c->kv_heads;
   const int mq = b->max_query_len > 0 ? b->max_query_len : std::max(b->num_tokens, 1);
+  const bool mfma = pa::decode_mfma_supported(c->head_dim, act, c->dtype);
   if (kind == 0) {
-    if (pa::decode_mfma_supported(c->head_dim, act, c->dtype) && (int64_t)g * mq <= 16)
+    if (mfma && (int64_t)g * mq <= 16)
       kind = 1;
     else if (pa::prefill_mfma_supported(c->head_dim, act, c->dtype))
       kind = 2;
-    else if (pa::decode_mfma_supported(c->head_dim, act, c->dtype))
+    else if (mfma)
       kind = 1;
     else
       kind = 3;
   }
   pl.kind = kind;
+  pl.balanced = kind == 1 && (int64_t)g * mq <= 16;
+  if (kind == 4) pl.kind = 1;
   const int ctx = std::max(max_ctx_bound(c, b), 1);
+  if (pl.balanced) {
+    // One segment per group of kv_heads wavefronts, two wavefronts per SIMD on every CU.
+    pl.chunk = 32;
+    pl.max_splits = std::max(1, 8 * device_cus() / c->kv_heads);
+    pl.part_rows = (size_t)(pl.max_splits + b->batch) * c->kv_heads * 16;
+    return pl;
+  }
   if (chunk <= 0) {
     if (kind == 2) {
       chunk = 1 << 30;  // prefill kernel walks the whole context
@@ -127,16 +156,19 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
       chunk = (int)std::min<int64_t>(std::max<int64_t>(ch, 256), 1024);
     }
   }
-  if (kind != 2) chunk = std::max(32, std::min(chunk, 1024) / 32 * 32);
+  if (pl.kind != 2) chunk = std::max(32, std::min(chunk, 1024) / 32 * 32);
   pl.chunk = chunk;
   pl.max_splits = (int)std::max<int64_t>(1, ((int64_t)ctx + chunk - 1) / chunk);
+  pl.part_rows = pl.max_splits > 1
+                     ? (size_t)std::max(b->num_tokens, 0) * a->num_heads * pl.max_splits
+                     : 0;
   return pl;
 }
 
-size_t workspace_for(const pa_cache* c, const pa_batch* b, const pa_attn* a, const Plan& pl) {
-  if (pl.max_splits <= 1) return 0;
-  size_t rows = (size_t)std::max(b->num_tokens, 0) * a->num_heads * pl.max_splits;
-  return align256(rows * c->head_dim * sizeof(float)) + align256(rows * 2 * sizeof(float));
+size_t workspace_for(const pa_cache* c, const pa_batch*, const pa_attn*, const Plan& pl) {
+  if (pl.part_rows == 0) return 0;
+  return align256(pl.part_rows * c->head_dim * sizeof(float)) +
+         align256(pl.part_rows * 2 * sizeof(float));
 }
 
 int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype act,
@@ -152,8 +184,8 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
   if (!q || !out || (!kn && c->dtype != PA_DTYPE_FP8_E4M3) ||
       (!vn && c->dtype != PA_DTYPE_FP8_E4M3))
     return fail(PA_ERR_INVALID_ARGUMENT, "q/k_new/v_new/out pointers are NULL");
-  if (kind < 0 || kind > 3) return fail(PA_ERR_INVALID_ARGUMENT, "unknown kernel kind %d", kind);
-  if (kind == 1 && !pa::decode_mfma_supported(c->head_dim, act, c->dtype))
+  if (kind < 0 || kind > 4) return fail(PA_ERR_INVALID_ARGUMENT, "unknown kernel kind %d", kind);
+  if ((kind == 1 || kind == 4) && !pa::decode_mfma_supported(c->head_dim, act, c->dtype))
     return fail(PA_ERR_UNSUPPORTED, "decode MFMA kernel does not cover this dtype/head_dim");
   if (kind == 2 && !pa::prefill_mfma_supported(c->head_dim, act, c->dtype))
     return fail(PA_ERR_UNSUPPORTED, "prefill MFMA kernel does not cover this dtype/head_dim");
@@ -178,10 +210,9 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
   p.block_table = b->block_table;
   p.head_sink = a->head_sink;
   p.out = out;
-  size_t rows = (size_t)b->num_tokens * a->num_heads * pl.max_splits;
   p.part_o = need ? reinterpret_cast<float*>(ws) : nullptr;
   p.part_ml = need ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) +
-                                              align256(rows * c->head_dim * sizeof(float)))
+                                              align256(pl.part_rows * c->head_dim * sizeof(float)))
                    : nullptr;
   p.num_blocks = c->num_blocks;
   p.block_size = c->block_size;
@@ -202,6 +233,11 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
   p.read_all_from_cache = c->dtype == PA_DTYPE_FP8_E4M3 ? 1 : 0;
 
   hipError_t e;
+  if (pl.balanced) {
+    e = pa::launch_decode_balanced(p, act, c->dtype, s);  // attention + partial merge
+    if (e != hipSuccess) return hip_fail(e, "balanced decode launch");
+    return PA_OK;
+  }
   switch (pl.kind) {
     case 1: e = pa::launch_decode_mfma(p, act, c->dtype, s); break;
     case 2: e = pa::launch_prefill_mfma(p, act, c->dtype, s); break;

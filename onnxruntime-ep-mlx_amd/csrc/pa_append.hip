@@ -102,16 +102,19 @@ __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p
   const int D = p.head_dim;
   const bool transform = p.cos_cache != nullptr || p.q_norm != nullptr;
 
-  // 1. query rows -> q_out
-  if (p.do_q && transform) {
-    for (int h = wave; h < p.num_heads; h += 4) {
+  // Workgroups with blockIdx.y >= 1 take four query head rows each, one per wavefront, so
+  // every head row of every token is in flight at once.
+  if (blockIdx.y > 0) {
+    const int h = (blockIdx.y - 1) * 4 + wave;
+    if (p.do_q && transform && h < p.num_heads) {
       int64_t base = ((int64_t)t * p.num_heads + h) * D;
       process_row<TT>(p, p.query, base, p.q_out, base, nullptr, 0, nullptr, 0, 0.0f, p.q_norm,
                       pos, lane);
     }
+    return;
   }
 
-  // 2. cache slot and last-writer rule
+  // blockIdx.y == 0: this token's key/value rows.  Cache slot and last-writer rule first.
   int64_t slot = token_slot(p, t);
   if (slot >= p.num_blocks * p.block_size) slot = -1;
   bool later_dup = false;
@@ -177,7 +180,9 @@ __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p
 hipError_t launch_rotary_append(const AppendParams& p, pa_dtype act, pa_dtype cache_dtype,
                                 hipStream_t s) {
   if (p.num_tokens <= 0) return hipSuccess;
-  dim3 grid(p.num_tokens), block(256);
+  const bool transform = p.cos_cache != nullptr || p.q_norm != nullptr;
+  const int q_groups = (p.do_q && transform) ? (p.num_heads + 3) / 4 : 0;
+  dim3 grid(p.num_tokens, 1 + q_groups), block(256);
   const bool fp8 = cache_dtype == PA_DTYPE_FP8_E4M3;
   switch (act) {
     case PA_DTYPE_FLOAT16:

@@ -167,22 +167,44 @@ __global__ __launch_bounds__(64) void split_reduce_kernel(const AttnParams p) {
   const int nsplit = (int)min((total + p.chunk - 1) / p.chunk, (int64_t)p.max_splits);
   if (nsplit <= 1) return;  // the attention kernel already wrote the final row
   const int64_t base = ((int64_t)t * p.num_heads + h) * p.max_splits;
+  const float2* ml = reinterpret_cast<const float2*>(p.part_ml) + base;
+  // Lanes hold the (m, l) of splits lane, lane+64, ...: one parallel load instead of a chain.
   float M = kNegInf;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, p.part_ml[(base + s) * 2]);
+  for (int s = lane; s < nsplit; s += 64) M = fmaxf(M, ml[s].x);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
   float L = 0.0f;
-  for (int s = 0; s < nsplit; ++s) {
-    float ms = p.part_ml[(base + s) * 2];
-    if (ms != kNegInf) L += p.part_ml[(base + s) * 2 + 1] * exp2f(ms - M);
+  for (int s = lane; s < nsplit; s += 64) {
+    const float2 v = ml[s];
+    if (v.x != kNegInf) L += v.y * exp2f(v.x - M);
   }
+  L = wave_sum(L);
   const float f = finalize_factor(M, L, sink_logit<TT>(p, h));
   typename TT::raw* out = reinterpret_cast<typename TT::raw*>(p.out);
-  for (int e = lane; e < D; e += 64) {
-    float acc = 0.0f;
-    for (int s = 0; s < nsplit; ++s) {
-      float ms = p.part_ml[(base + s) * 2];
-      if (ms != kNegInf) acc += p.part_o[(base + s) * D + e] * exp2f(ms - M);
+  const float* po = p.part_o + base * D;
+  float acc[kMaxLanesElems] = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < nsplit; s0 += 64) {
+    // every lane stays active through the shuffles: split weights live one per lane
+    float wl = 0.0f;
+    if (s0 + lane < nsplit) {
+      const float ms = ml[s0 + lane].x;
+      wl = (ms == kNegInf) ? 0.0f : exp2f(ms - M);
     }
-    out[((int64_t)t * p.num_heads + h) * D + e] = TT::from_f32(acc * f);
+    const int n = min(64, nsplit - s0);
+    for (int k = 0; k < n; ++k) {
+      const float wk = __shfl(wl, k, 64);
+      const float* row = po + (int64_t)(s0 + k) * D;
+#pragma unroll
+      for (int q = 0; q < kMaxLanesElems; ++q) {
+        const int e = lane + 64 * q;
+        if (e < D) acc[q] += row[e] * wk;
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < kMaxLanesElems; ++q) {
+    const int e = lane + 64 * q;
+    if (e < D) out[((int64_t)t * p.num_heads + h) * D + e] = TT::from_f32(acc[q] * f);
   }
 }
 

@@ -4,14 +4,15 @@
 // (paged_attention.rs:31-143, launcher :229-334) and, for bf16, the dense gather + SDPA
 // fallback (attention.rs:4192-4319) that the reference takes for every non-fp16 decode.
 //
-// Work unit: one wavefront per (sequence, kv-head, context chunk).  The wavefront serves every
-// grouped query row of its kv-head — rows r = (query token i, head hh) with r = i*g + hh, up
-// to 16 at a time — from ONE pass over the pages, so each K/V byte is read from HBM once per
-// kv-head instead of once per query head (the reference re-reads it g times).
+// Work unit: one wavefront per (sequence, kv-head, 16-row group, context chunk).  The
+// wavefront serves every grouped query row of its kv-head -- rows r = (query token i, head hh)
+// with r = i*g + hh, up to 16 at a time -- from ONE pass over the pages, so each K/V byte is
+// read from HBM once per kv-head instead of once per query head (the reference re-reads it g
+// times).
 //
-// Per 32-token step (two 16-token tiles A and B):
-//   S^T = K_tile . Q^T   v_mfma_f32_16x16x32 (A = 16 keys x 32 dims straight from the page row,
-//                        16 bytes per lane; B = Q^T held in registers for the whole chunk).
+// Per 32-key step (two 16-key tiles A and B):
+//   S^T = K_tile . Q^T   v_mfma_f32_16x16x32 (A = 16 keys x 32 dims straight from the page
+//                        rows, 16 bytes per lane; B = Q^T held in registers for the chunk).
 //                        Lane l ends with S[key 4*(l/16)+i][row l%16], i = 0..3, per tile.
 //   online softmax       base 2, per row, lazy rescale: the running max only moves when a
 //                        score exceeds it by more than 2^8, so the O rescale (and its
@@ -23,11 +24,16 @@
 //                        assigning output column n of N-tile j to head dim DL*n + j.  P is
 //                        split into hi + lo 16-bit parts (two MFMAs) so the PV product keeps
 //                        ~16 mantissa bits; the reference accumulates PV in fp32.
-// Split-K: each chunk writes (m, l, O) partials; pa_attn_generic.hip's reduce merges them.
-// A sequence that fits one chunk writes its final rows directly.
 //
-// HBM traffic per step and kv-head: 16 KiB of K/V rows (bf16, d=128), each byte read once.
-// The next step's rows are loaded before the current step is computed (two register sets).
+// Memory pipeline: steps whose 32 keys all sit in cached pages (and whose 16-key tiles each lie
+// in one page, i.e. block_size % 16 == 0) run in a software-pipelined loop -- the next step's
+// 16 KiB (bf16, d=128) is loaded into a second register set while the current step computes,
+// with the page id taken from a register (v_readlane) so addresses are a scalar page base plus a
+// fixed lane offset.  The remaining steps (the ones holding the new tokens, or any step when the
+// block size is not a multiple of 16) take a per-lane addressed path without prefetch.
+//
+// Split-K: each chunk writes (m, l, O) partials; pa_attn_generic.hip's reduce merges them.  A
+// sequence that fits one chunk writes its final rows directly.
 #include <algorithm>
 
 #include "pa_device.hpp"
@@ -49,128 +55,337 @@ struct VRow<128> {
 };
 
 template <int D>
-__device__ __forceinline__ VRow<D> load_vrow(const uint16_t* ptr);
+__device__ __forceinline__ VRow<D> ld_vrow(const char* ptr);
 template <>
-__device__ __forceinline__ VRow<64> load_vrow<64>(const uint16_t* ptr) {
-  VRow<64> r;
-  r.w = *reinterpret_cast<const u32x2*>(ptr);
-  return r;
+__device__ __forceinline__ VRow<64> ld_vrow<64>(const char* ptr) {
+  return VRow<64>{*reinterpret_cast<const u32x2*>(ptr)};
 }
 template <>
-__device__ __forceinline__ VRow<128> load_vrow<128>(const uint16_t* ptr) {
-  VRow<128> r;
-  r.w = *reinterpret_cast<const u32x4*>(ptr);
-  return r;
+__device__ __forceinline__ VRow<128> ld_vrow<128>(const char* ptr) {
+  return VRow<128>{*reinterpret_cast<const u32x4*>(ptr)};
+}
+
+__device__ __forceinline__ u32x4 ld16(const char* ptr) {
+  return *reinterpret_cast<const u32x4*>(ptr);
 }
 
 template <int D>
 struct Step {
-  static constexpr int KS = D / 32;
-  u32x4 k[2][KS];  // tile A / tile B key rows, 8 dims per k-step
-  VRow<D> v[8];    // value rows: keys 4G+e of tile A (e<4) and of tile B (e>=4)
+  u32x4 k[2][D / 32];  // tile A / tile B key rows, 8 dims per k-step
+  VRow<D> v[8];        // value rows: keys 4G+e of tile A (e<4) and of tile B (e>=4)
 };
 
-template <typename TT, int D>
-struct DecodeCtx {
-  const AttnParams& p;
-  const uint16_t* kc;
-  const uint16_t* vc;
-  const uint16_t* kn;
-  const uint16_t* vn;
-  int b, kh, s0, nq;
-  int pastb, total, cache_limit;
-  int64_t row;  // elements between consecutive cache rows (kv_heads * D)
-  int c, G;
-  int first_bi;
-  int btv;      // lane i: block_table[b, first_bi + i]
-  bool aligned; // block_size % 16 == 0: a 16-key tile never straddles two pages
-
-  __device__ int64_t clamp_blk(int64_t blk) const {
-    return min(max(blk, (int64_t)0), p.num_blocks - 1);
-  }
-
-  // Element offset of key/value row `pos` (per-lane, any block size); `is_cache` tells the
-  // caller which base pointer applies.  Positions past the end clamp to the last real row.
-  __device__ int64_t row_offset(int pos, bool& is_cache) const {
-    if (pos >= total) pos = total - 1;
-    if (pos < cache_limit) {
-      is_cache = true;
-      int bi = min(pos / p.block_size, p.max_blocks - 1);
-      int64_t blk = clamp_blk(p.block_table[(int64_t)b * p.max_blocks + bi]);
-      return (blk * p.block_size + pos % p.block_size) * row + (int64_t)kh * D;
-    }
-    is_cache = false;
-    int64_t tok = min(max((int64_t)s0 + (pos - pastb), (int64_t)0), (int64_t)p.num_tokens - 1);
-    return tok * row + (int64_t)kh * D;
-  }
-
-  __device__ void load_generic(int t0, Step<D>& st) const {
-#pragma unroll
-    for (int tile = 0; tile < 2; ++tile) {
-      bool cache;
-      int64_t off = row_offset(t0 + 16 * tile + c, cache);
-      const uint16_t* base = (cache ? kc : kn) + off + 8 * G;
-#pragma unroll
-      for (int s = 0; s < Step<D>::KS; ++s)
-        st.k[tile][s] = *reinterpret_cast<const u32x4*>(base + 32 * s);
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      bool cache;
-      int pos = t0 + 16 * (e >> 2) + 4 * G + (e & 3);
-      int64_t off = row_offset(pos, cache);
-      st.v[e] = load_vrow<D>((cache ? vc : vn) + off + (D / 16) * c);
-    }
-  }
-
-  // All 32 keys are cached and each 16-key tile lies in one page: the page id is wave-uniform
-  // (read from a register with v_readlane), so addresses are a scalar base + lane offset.
-  __device__ void load_fast(int t0, Step<D>& st) const {
-#pragma unroll
-    for (int tile = 0; tile < 2; ++tile) {
-      int tp = t0 + 16 * tile;
-      int64_t blk = clamp_blk(__builtin_amdgcn_readlane(btv, tp / p.block_size - first_bi));
-      int64_t tbase = (blk * p.block_size + tp % p.block_size) * row + (int64_t)kh * D;
-      const uint16_t* kb = kc + tbase + (int64_t)c * row + 8 * G;
-#pragma unroll
-      for (int s = 0; s < Step<D>::KS; ++s)
-        st.k[tile][s] = *reinterpret_cast<const u32x4*>(kb + 32 * s);
-      const uint16_t* vb = vc + tbase + (int64_t)(4 * G) * row + (D / 16) * c;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) st.v[4 * tile + e] = load_vrow<D>(vb + (int64_t)e * row);
-    }
-  }
-
-  __device__ void load(int t0, Step<D>& st) const {
-    if (aligned && t0 + 32 <= cache_limit)
-      load_fast(t0, st);
-    else
-      load_generic(t0, st);
-  }
+// Wave-uniform description of the (sequence, kv-head, chunk) being processed.
+struct WaveInfo {
+  const char* kc;  // key cache (bytes)
+  const char* vc;
+  const char* kn;  // new key rows (bytes)
+  const char* vn;
+  int b, kh, s0, pastb, total, cache_limit;
+  int bs, bs_shift;  // block size, log2 if a power of two else -1
+  int max_blocks, num_tokens;
+  int64_t num_blocks;
+  int64_t rowb;      // bytes between consecutive cache rows (kv_heads * D * 2)
+  int first_bi;      // first block-table index of the chunk
+  const int32_t* bt; // this sequence's block-table row
 };
 
-// Regroup 8 value rows (lane holds DL dims of each) into DL MFMA B-operands of 8 keys x 1 dim.
+__device__ __forceinline__ int div_bs(int x, const WaveInfo& w) {
+  return w.bs_shift >= 0 ? (x >> w.bs_shift) : x / w.bs;
+}
+__device__ __forceinline__ int mod_bs(int x, const WaveInfo& w) {
+  return w.bs_shift >= 0 ? (x & (w.bs - 1)) : x % w.bs;
+}
+
+// Fast path: all 32 keys cached, 16-key tiles page-aligned.  The page id of each tile comes
+// from lane (tile_block - first_bi) of `btv` (this chunk's block-table entries, one per lane).
+template <int D>
+__device__ __forceinline__ void load_fast(const WaveInfo& w, int btv, uint32_t koff,
+                                          uint32_t voff, int t0, Step<D>& st) {
+#pragma unroll
+  for (int tile = 0; tile < 2; ++tile) {
+    const int tp = t0 + 16 * tile;
+    int64_t blk = __builtin_amdgcn_readlane(btv, div_bs(tp, w) - w.first_bi);
+    blk = min(max(blk, (int64_t)0), w.num_blocks - 1);
+    const int64_t tb = (blk * w.bs + mod_bs(tp, w)) * w.rowb + (int64_t)w.kh * D * 2;
+    const char* kb = w.kc + tb;
+    const char* vb = w.vc + tb;
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s) st.k[tile][s] = ld16(kb + koff + 64 * s);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) st.v[4 * tile + e] = ld_vrow<D>(vb + voff + e * w.rowb);
+  }
+}
+
+// Byte offset of key/value row `pos` for this lane (any block size), choosing the cache page
+// (positions < cache_limit) or the new rows.  Positions past the end clamp to the last real
+// row; block ids are clamped into the pool, so malformed metadata cannot fault.
+__device__ __forceinline__ const char* row_ptr(const WaveInfo& w, int pos, bool value, int D) {
+  if (pos >= w.total) pos = w.total - 1;
+  if (pos < w.cache_limit) {
+    const int bi = min(div_bs(pos, w), w.max_blocks - 1);
+    int64_t blk = w.bt[bi];
+    blk = min(max(blk, (int64_t)0), w.num_blocks - 1);
+    return (value ? w.vc : w.kc) + (blk * w.bs + mod_bs(pos, w)) * w.rowb + (int64_t)w.kh * D * 2;
+  }
+  int64_t tok = min(max((int64_t)w.s0 + (pos - w.pastb), (int64_t)0), (int64_t)w.num_tokens - 1);
+  return (value ? w.vn : w.kn) + tok * w.rowb + (int64_t)w.kh * D * 2;
+}
+
+template <int D>
+__device__ __forceinline__ void load_edge(const WaveInfo& w, int c, int G, int t0, Step<D>& st) {
+#pragma unroll
+  for (int tile = 0; tile < 2; ++tile) {
+    const char* kb = row_ptr(w, t0 + 16 * tile + c, false, D) + 16 * G;
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s) st.k[tile][s] = ld16(kb + 64 * s);
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int pos = t0 + 16 * (e >> 2) + 4 * G + (e & 3);
+    st.v[e] = ld_vrow<D>(row_ptr(w, pos, true, D) + (D / 16) * 2 * c);
+  }
+}
+
+// Regroup 8 value rows (lane holds DL dims of each) into the MFMA B-operand of N-tile j:
+// 8 keys x head dim DL*c + j.
 template <typename TT, int D>
 __device__ __forceinline__ typename TT::vec8 value_operand(const Step<D>& st, int j) {
   u32x4 w;
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    uint32_t lo = st.v[2 * m].word(j >> 1), hi = st.v[2 * m + 1].word(j >> 1);
+    const uint32_t lo = st.v[2 * m].word(j >> 1), hi = st.v[2 * m + 1].word(j >> 1);
     w[m] = (j & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
   }
   return __builtin_bit_cast(typename TT::vec8, w);
 }
 
+// Row state of one 16-row group.
 template <typename TT, int D>
-__global__ __launch_bounds__(64) void decode_mfma_kernel(const AttnParams p) {
-  constexpr int KS = D / 32;
-  constexpr int DL = D / 16;
-  using vec8 = typename TT::vec8;
-  const int split = blockIdx.x, b = blockIdx.z;
-  const int kh = blockIdx.y % p.kv_heads, rgroup = blockIdx.y / p.kv_heads;
-  const int ngroups = gridDim.y / p.kv_heads;
-  const int lane = threadIdx.x, c = lane & 15, G = lane >> 4;
+struct RowState {
+  typename TT::vec8 qv[D / 32];
+  f32x4 o[D / 16];
+  float m_run;   // running max of row c (log2 units); identical across the 4 lane groups
+  float l_part;  // this lane's share of the row-c denominator
+  int vis_lo, vis_hi;
+};
 
+template <typename TT, int D, bool CAP>
+__device__ __forceinline__ void compute_step(RowState<TT, D>& rs, const Step<D>& st, int t0,
+                                             int end, int G, float scale_log2, float scale,
+                                             float cap) {
+  using vec8 = typename TT::vec8;
+  constexpr int KS = D / 32, DL = D / 16;
+  f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    sa = TT::mfma(__builtin_bit_cast(vec8, st.k[0][s]), rs.qv[s], sa);
+    sb = TT::mfma(__builtin_bit_cast(vec8, st.k[1][s]), rs.qv[s], sb);
+  }
+  float x[8];
+  float lmax = kNegInf;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int pos = t0 + 16 * (e >> 2) + 4 * G + (e & 3);
+    const float sv = (e < 4) ? sa[e & 3] : sb[e & 3];
+    float xv;
+    if constexpr (CAP)
+      xv = cap * tanhf(sv * scale / cap) * kLog2e;
+    else
+      xv = sv * scale_log2;
+    const bool vis = pos < end && pos >= rs.vis_lo && pos < rs.vis_hi;
+    x[e] = vis ? xv : kNegInf;
+    lmax = fmaxf(lmax, x[e]);
+  }
+  if (__any(lmax > rs.m_run + 8.0f)) {
+    float rmax = fmaxf(lmax, __shfl_xor(lmax, 16, 64));
+    rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+    const float m_new = fmaxf(rs.m_run, rmax);
+    const float alpha = (m_new == kNegInf) ? 1.0f : exp2f(rs.m_run - m_new);
+    rs.l_part *= alpha;
+    rs.m_run = m_new;
+    float ar[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ar[i] = __shfl(alpha, 4 * G + i, 64);
+#pragma unroll
+    for (int j = 0; j < DL; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rs.o[j][i] *= ar[i];
+  }
+  const float msafe = (rs.m_run == kNegInf) ? 0.0f : rs.m_run;
+  float pv[8], plo[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    pv[e] = exp2f(x[e] - msafe);
+    rs.l_part += pv[e];
+  }
+  const vec8 phi = TT::cvt8(pv);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) plo[e] = pv[e] - TT::back(phi[e]);
+  const vec8 plo8 = TT::cvt8(plo);
+#pragma unroll
+  for (int j = 0; j < DL; ++j) {
+    const vec8 vb = value_operand<TT, D>(st, j);
+    rs.o[j] = TT::mfma(phi, vb, rs.o[j]);
+    rs.o[j] = TT::mfma(plo8, vb, rs.o[j]);
+  }
+}
+
+// ----------------------------------------------------------------------------- shared driver
+
+// Walk keys [t_begin, t_last) for one (sequence, kv-head) with the rows in `rs`; t_begin is a
+// multiple of 32.  Steps entirely inside cached pages go through the pipelined fast loop in
+// sub-ranges of at most 1024 keys (one block-table entry per lane covers a sub-range); the rest
+// take the per-lane addressed path.  `end` masks keys at or beyond it.
+template <typename TT, int D, bool CAP>
+__device__ __forceinline__ void run_range(WaveInfo w, RowState<TT, D>& rs, int t_begin,
+                                          int t_last, int end, int lane, int c, int G,
+                                          float scale_log2, float scale, float cap) {
+  const uint32_t koff = (uint32_t)(c * w.rowb + 16 * G);
+  const uint32_t voff = (uint32_t)(4 * G * w.rowb + (D / 16) * 2 * c);
+  const int fast_lim = (w.bs % 16 == 0) ? min(t_last, w.cache_limit) : t_begin;
+  int t0 = t_begin;
+  Step<D> sA, sB;
+  while (t0 + 32 <= fast_lim) {
+    const int nfast = (min(fast_lim, t0 + 1024) - t0) / 32;
+    w.first_bi = div_bs(t0, w);
+    const int btv = w.bt[min(w.first_bi + lane, w.max_blocks - 1)];
+    load_fast<D>(w, btv, koff, voff, t0, sA);
+    int k = 0;
+    while (k + 2 < nfast) {
+      load_fast<D>(w, btv, koff, voff, t0 + 32, sB);
+      compute_step<TT, D, CAP>(rs, sA, t0, end, G, scale_log2, scale, cap);
+      load_fast<D>(w, btv, koff, voff, t0 + 64, sA);
+      compute_step<TT, D, CAP>(rs, sB, t0 + 32, end, G, scale_log2, scale, cap);
+      t0 += 64;
+      k += 2;
+    }
+    if (k + 1 < nfast) {
+      load_fast<D>(w, btv, koff, voff, t0 + 32, sB);
+      compute_step<TT, D, CAP>(rs, sA, t0, end, G, scale_log2, scale, cap);
+      compute_step<TT, D, CAP>(rs, sB, t0 + 32, end, G, scale_log2, scale, cap);
+      t0 += 64;
+    } else {
+      compute_step<TT, D, CAP>(rs, sA, t0, end, G, scale_log2, scale, cap);
+      t0 += 32;
+    }
+  }
+  for (; t0 < t_last; t0 += 32) {
+    load_edge<D>(w, c, G, t0, sA);
+    compute_step<TT, D, CAP>(rs, sA, t0, end, G, scale_log2, scale, cap);
+  }
+}
+
+__device__ __forceinline__ WaveInfo make_wave(const AttnParams& p, int D, int b, int kh, int s0,
+                                              int pastb, int total) {
+  WaveInfo w;
+  w.kc = reinterpret_cast<const char*>(p.key_cache);
+  w.vc = reinterpret_cast<const char*>(p.value_cache);
+  w.kn = reinterpret_cast<const char*>(p.k_new);
+  w.vn = reinterpret_cast<const char*>(p.v_new);
+  w.b = b;
+  w.kh = kh;
+  w.s0 = s0;
+  w.pastb = pastb;
+  w.total = total;
+  w.cache_limit = p.read_all_from_cache ? total : pastb;
+  w.bs = p.block_size;
+  w.bs_shift = (p.block_size & (p.block_size - 1)) == 0 ? __builtin_ctz(p.block_size) : -1;
+  w.max_blocks = p.max_blocks;
+  w.num_tokens = p.num_tokens;
+  w.num_blocks = p.num_blocks;
+  w.rowb = (int64_t)p.kv_heads * D * 2;
+  w.first_bi = 0;
+  w.bt = p.block_table + (int64_t)b * p.max_blocks;
+  return w;
+}
+
+// Rows row0 .. row0+15 of kv-head kh: this lane's MFMA column is row r = row0 + c, i.e. query
+// token r / g and head kh*g + r % g.
+template <typename TT, int D>
+__device__ __forceinline__ void init_rows(RowState<TT, D>& rs, const AttnParams& p,
+                                          const WaveInfo& w, int row0, int R, int g, int c,
+                                          int G) {
+  using vec8 = typename TT::vec8;
+  const int r = row0 + c;
+  const bool rvalid = r < R;
+  const int qi = rvalid ? r / g : 0;
+  const int h = w.kh * g + (rvalid ? r % g : 0);
+  const int rpos = w.pastb + qi;
+  rs.vis_lo = p.window > 0 ? rpos - p.window + 1 : 0;
+  rs.vis_hi = rvalid ? (p.causal ? rpos + 1 : w.total) : -1;
+  const char* qrow = reinterpret_cast<const char*>(p.q) +
+                     (((int64_t)(w.s0 + qi) * p.num_heads + h) * D + 8 * G) * 2;
+#pragma unroll
+  for (int s = 0; s < D / 32; ++s) {
+    const u32x4 v = rvalid ? ld16(qrow + 64 * s) : u32x4{0, 0, 0, 0};
+    rs.qv[s] = __builtin_bit_cast(vec8, v);
+  }
+#pragma unroll
+  for (int j = 0; j < D / 16; ++j) rs.o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  rs.m_run = kNegInf;
+  rs.l_part = 0.0f;
+}
+
+// Epilogue: rows 4G+i of this lane's O registers.  final: normalise (with the sink) and write
+// the output row in T; otherwise write the fp32 partial (O, m, l) at part_index(row).
+template <typename TT, int D, typename PartIndex>
+__device__ __forceinline__ void store_rows(const RowState<TT, D>& rs, const AttnParams& p,
+                                           const WaveInfo& w, int row0, int R, int g, int c,
+                                           int G, bool final, PartIndex part_index) {
+  constexpr int DL = D / 16;
+  float l_row = rs.l_part + __shfl_xor(rs.l_part, 16, 64);
+  l_row += __shfl_xor(l_row, 32, 64);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int rr = row0 + 4 * G + i;
+    const float mi = __shfl(rs.m_run, 4 * G + i, 64);
+    const float li = __shfl(l_row, 4 * G + i, 64);
+    if (rr >= R) continue;
+    const int oqi = rr / g, oh = w.kh * g + rr % g;
+    const int64_t t = w.s0 + oqi;
+    if (final) {
+      const float f = finalize_factor(mi, li, sink_logit<TT>(p, oh));
+      typename TT::raw vals[DL];
+#pragma unroll
+      for (int j = 0; j < DL; ++j) vals[j] = TT::from_f32(rs.o[j][i] * f);
+      typename TT::raw* dst =
+          reinterpret_cast<typename TT::raw*>(p.out) + (t * p.num_heads + oh) * D + DL * c;
+      if constexpr (DL == 8) {
+        u32x4 pk;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          pk[m] = (uint32_t)vals[2 * m] | ((uint32_t)vals[2 * m + 1] << 16);
+        *reinterpret_cast<u32x4*>(dst) = pk;
+      } else {
+#pragma unroll
+        for (int j = 0; j < DL; ++j) dst[j] = vals[j];
+      }
+    } else {
+      const int64_t pi = part_index(t, oh, rr - row0);
+      float* dst = p.part_o + pi * D + DL * c;
+#pragma unroll
+      for (int j = 0; j < DL; ++j) dst[j] = rs.o[j][i];
+      if (c == 0) {
+        p.part_ml[pi * 2 + 0] = mi;
+        p.part_ml[pi * 2 + 1] = li;
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------- chunked kernel
+// One wavefront per (context chunk, kv-head, 16-row group, sequence); kv-head fastest in the
+// grid so the wavefronts reading the same pages run together.  Used when a sequence has more
+// than 16 grouped query rows (multi-token queries); partials at (token, head, chunk).
+// Two wavefronts per SIMD: the pipelined d=128 loop fits in 256 registers without spilling.
+template <typename TT, int D, bool CAP>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+decode_chunked_kernel(const AttnParams p) {
+  const int kh = blockIdx.x % p.kv_heads, rgroup = blockIdx.x / p.kv_heads;
+  const int ngroups = gridDim.x / p.kv_heads;
+  const int split = blockIdx.y, b = blockIdx.z;
+  const int lane = threadIdx.x, c = lane & 15, G = lane >> 4;
   const int s0 = min(max(p.cum[b], 0), p.num_tokens);
   const int s1 = min(max(p.cum[b + 1], s0), p.num_tokens);
   const int nq = s1 - s0;
@@ -182,189 +397,221 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(const AttnParams p) {
   const int end = min(start + p.chunk, total);
   const int g = p.num_heads / p.kv_heads;
   const int R = g * nq;
-
-  DecodeCtx<TT, D> ctx{p};
-  ctx.kc = reinterpret_cast<const uint16_t*>(p.key_cache);
-  ctx.vc = reinterpret_cast<const uint16_t*>(p.value_cache);
-  ctx.kn = reinterpret_cast<const uint16_t*>(p.k_new);
-  ctx.vn = reinterpret_cast<const uint16_t*>(p.v_new);
-  ctx.b = b;
-  ctx.kh = kh;
-  ctx.s0 = s0;
-  ctx.nq = nq;
-  ctx.pastb = pastb;
-  ctx.total = total;
-  ctx.cache_limit = p.read_all_from_cache ? total : pastb;
-  ctx.row = (int64_t)p.kv_heads * D;
-  ctx.c = c;
-  ctx.G = G;
-  ctx.aligned = (p.block_size % 16) == 0;
-  ctx.first_bi = start / p.block_size;
-  {
-    int bi = min(ctx.first_bi + lane, p.max_blocks - 1);
-    ctx.btv = p.block_table[(int64_t)b * p.max_blocks + bi];
-  }
-  const uint16_t* qp = reinterpret_cast<const uint16_t*>(p.q);
-  const float scale_log2 = p.scale_log2;
-  const float cap = p.softcap;
-
+  const WaveInfo w = make_wave(p, D, b, kh, s0, pastb, total);
+  const bool single = (start == 0 && end == total);
+  // Metadata beyond the planned capacity (total > max_blocks * block_size) leaves no partial
+  // buffer to write into; such rows are left unwritten rather than faulting.
+  if (!single && p.part_o == nullptr) return;
   for (int row0 = 16 * rgroup; row0 < R; row0 += 16 * ngroups) {
-    // This lane's MFMA column: query row r = row0 + c.
-    const int r = row0 + c;
-    const bool rvalid = r < R;
-    const int qi = rvalid ? r / g : 0;
-    const int h = kh * g + (rvalid ? r % g : 0);
-    const int rpos = pastb + qi;
-    int vis_lo = p.window > 0 ? rpos - p.window + 1 : 0;
-    int vis_hi = p.causal ? rpos + 1 : total;
-    if (!rvalid) vis_hi = -1;
-
-    vec8 qv[KS];
-    {
-      const uint16_t* qrow = qp + ((int64_t)(s0 + qi) * p.num_heads + h) * D + 8 * G;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        u32x4 w = rvalid ? *reinterpret_cast<const u32x4*>(qrow + 32 * s) : u32x4{0, 0, 0, 0};
-        qv[s] = __builtin_bit_cast(vec8, w);
-      }
-    }
-
-    f32x4 o[DL];
-#pragma unroll
-    for (int j = 0; j < DL; ++j) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run = kNegInf;  // running max of row c (log2 units); identical across G
-    float l_part = 0.0f;    // this lane's share of the row-c denominator
-
-    auto compute = [&](int t0, const Step<D>& st) {
-      f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        sa = TT::mfma(__builtin_bit_cast(vec8, st.k[0][s]), qv[s], sa);
-        sb = TT::mfma(__builtin_bit_cast(vec8, st.k[1][s]), qv[s], sb);
-      }
-      float x[8];
-      float lmax = kNegInf;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int pos = t0 + 16 * (e >> 2) + 4 * G + (e & 3);
-        float sv = (e < 4) ? sa[e & 3] : sb[e & 3];
-        float xv;
-        if (cap > 0.0f)
-          xv = cap * tanhf(sv * p.scale / cap) * kLog2e;
-        else
-          xv = sv * scale_log2;
-        const bool vis = pos < end && pos >= vis_lo && pos < vis_hi;
-        x[e] = vis ? xv : kNegInf;
-        lmax = fmaxf(lmax, x[e]);
-      }
-      if (__any(lmax > m_run + 8.0f)) {
-        float rmax = fmaxf(lmax, __shfl_xor(lmax, 16, 64));
-        rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
-        const float m_new = fmaxf(m_run, rmax);
-        const float alpha = (m_new == kNegInf) ? 1.0f : exp2f(m_run - m_new);
-        l_part *= alpha;
-        m_run = m_new;
-        float ar[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ar[i] = __shfl(alpha, 4 * G + i, 64);
-#pragma unroll
-        for (int j = 0; j < DL; ++j)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) o[j][i] *= ar[i];
-      }
-      const float msafe = (m_run == kNegInf) ? 0.0f : m_run;
-      float pv[8], plo[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        pv[e] = exp2f(x[e] - msafe);
-        l_part += pv[e];
-      }
-      vec8 phi = TT::cvt8(pv);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) plo[e] = pv[e] - TT::back(phi[e]);
-      vec8 plo8 = TT::cvt8(plo);
-#pragma unroll
-      for (int j = 0; j < DL; ++j) {
-        vec8 vb = value_operand<TT, D>(st, j);
-        o[j] = TT::mfma(phi, vb, o[j]);
-        o[j] = TT::mfma(plo8, vb, o[j]);
-      }
-    };
-
+    RowState<TT, D> rs;
+    init_rows<TT, D>(rs, p, w, row0, R, g, c, G);
     // Keys outside every row's causal/window range are skipped (whole 32-key steps).
-    int lo_any = rvalid ? vis_lo : INT32_MAX;
-    int hi_any = vis_hi;
+    int lo_any = (row0 + c < R) ? rs.vis_lo : INT32_MAX;
+    int hi_any = rs.vis_hi;
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) {
       lo_any = min(lo_any, __shfl_xor(lo_any, o, 64));
       hi_any = max(hi_any, __shfl_xor(hi_any, o, 64));
     }
     const int t_first = max(start, (lo_any / 32) * 32);
-    const int t_last = min(end, hi_any);  // exclusive
-    Step<D> sA, sB;
-    int t0 = t_first;
-    if (t0 < t_last) {
-      ctx.load(t0, sA);
-      while (true) {
-        if (t0 + 32 < t_last) ctx.load(t0 + 32, sB);
-        compute(t0, sA);
-        t0 += 32;
-        if (t0 >= t_last) break;
-        if (t0 + 32 < t_last) ctx.load(t0 + 32, sA);
-        compute(t0, sB);
-        t0 += 32;
-        if (t0 >= t_last) break;
-      }
-    }
-
-    // Row totals: sum the four lane groups' partial denominators of row c, then fetch the
-    // (m, l) of the rows this lane's O registers hold (rows 4G+i).
-    float l_row = l_part + __shfl_xor(l_part, 16, 64);
-    l_row += __shfl_xor(l_row, 32, 64);
-    const bool single = (start == 0 && end == total);
-    // Metadata beyond the planned capacity (total > max_blocks * block_size) leaves no
-    // partial buffer to write into; such rows are left unwritten rather than faulting.
-    if (!single && p.part_o == nullptr) continue;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int rr = row0 + 4 * G + i;
-      const float mi = __shfl(m_run, 4 * G + i, 64);
-      const float li = __shfl(l_row, 4 * G + i, 64);
-      if (rr >= R) continue;
-      const int oqi = rr / g, oh = kh * g + rr % g;
-      const int64_t t = s0 + oqi;
-      if (single) {
-        const float f = finalize_factor(mi, li, sink_logit<TT>(p, oh));
-        typename TT::raw vals[DL];
-#pragma unroll
-        for (int j = 0; j < DL; ++j) vals[j] = TT::from_f32(o[j][i] * f);
-        typename TT::raw* dst =
-            reinterpret_cast<typename TT::raw*>(p.out) + (t * p.num_heads + oh) * D + DL * c;
-#pragma unroll
-        for (int j = 0; j < DL; ++j) dst[j] = vals[j];
-      } else {
-        const int64_t pi = (t * p.num_heads + oh) * p.max_splits + split;
-        float* dst = p.part_o + pi * D + DL * c;
-#pragma unroll
-        for (int j = 0; j < DL; ++j) dst[j] = o[j][i];
-        if (c == 0) {
-          p.part_ml[pi * 2 + 0] = mi;
-          p.part_ml[pi * 2 + 1] = li;
-        }
-      }
-    }
+    const int t_last = min(end, hi_any);
+    run_range<TT, D, CAP>(w, rs, t_first, t_last, end, lane, c, G, p.scale_log2, p.scale,
+                          p.softcap);
+    store_rows<TT, D>(rs, p, w, row0, R, g, c, G, single, [&](int64_t t, int oh, int) {
+      return (t * p.num_heads + oh) * p.max_splits + split;
+    });
   }
 }
 
+// ----------------------------------------------------------------------------- balanced kernel
+// Decode with at most 16 grouped query rows per sequence.  Every sequence contributes
+// n_b = ceil((total_b - first_b) / 32) steps of 32 keys (first_b: first key any row can see);
+// the steps of all sequences, in order, are cut into `nseg` contiguous segments of equal length
+// (the last ones may be shorter or empty), and the
+// wavefront for (segment, kv-head) walks its segment across sequence boundaries.  Each
+// wavefront does the same work and the kv-heads of a segment are adjacent in the grid, so all
+// wavefronts finish together and the ones sharing pages read them together.  A sequence
+// covered by one segment is written directly; otherwise each covering segment s writes a
+// partial at slot s + b (unique: segments of b are consecutive and the next sequence starts in
+// the segment where b ends or in the next one), merged by balanced_reduce_kernel.
+
+struct SeqSteps {
+  int s0, nq, pastb, total, first, n;  // first: first key step start (multiple of 32)
+};
+
+__device__ __forceinline__ SeqSteps seq_steps(const AttnParams& p, int b) {
+  SeqSteps q{0, 0, 0, 0, 0, 0};
+  if (b >= p.batch) return q;
+  q.s0 = min(max(p.cum[b], 0), p.num_tokens);
+  const int s1 = min(max(p.cum[b + 1], q.s0), p.num_tokens);
+  q.nq = s1 - q.s0;
+  if (q.nq <= 0) return q;
+  q.pastb = max(p.past[b], 0);
+  q.total = q.pastb + q.nq;
+  q.first = p.window > 0 ? (max(0, q.pastb - p.window + 1) / 32) * 32 : 0;
+  q.n = (q.total - q.first + 31) / 32;
+  return q;
+}
+
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(v, o, 64);
+    if (lane >= o) v += u;
+  }
+  return v;
+}
+
+__device__ __forceinline__ int64_t total_steps(const AttnParams& p, int lane) {
+  int64_t S = 0;
+  for (int base = 0; base < p.batch; base += 64) {
+    const int n = seq_steps(p, base + lane).n;
+    S += __shfl(wave_incl_scan(n, lane), 63, 64);
+  }
+  return S;
+}
+
+// Segments are L = ceil(S / nseg) steps long, so empty segments can only trail the list and
+// every segment between the first and last one covering a sequence holds part of it.
+__device__ __forceinline__ int64_t seg_len(int64_t S, int nseg) { return (S + nseg - 1) / nseg; }
+
+template <typename TT, int D, bool CAP>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+decode_balanced_kernel(const AttnParams p) {
+  const int kh = blockIdx.x, seg = blockIdx.y, nseg = gridDim.y;
+  const int lane = threadIdx.x, c = lane & 15, G = lane >> 4;
+  const int g = p.num_heads / p.kv_heads;
+  const int64_t S = total_steps(p, lane);
+  if (S <= 0) return;
+  const int64_t L = seg_len(S, nseg);
+  const int64_t gs = min(S, L * seg), ge = min(S, L * (seg + 1));
+  if (gs >= ge) return;
+  int64_t carry = 0;
+  for (int base = 0; base < p.batch && carry < ge; base += 64) {
+    int excl, chunk_total;
+    uint64_t mask;
+    {
+      const int n_l = seq_steps(p, base + lane).n;
+      const int incl = wave_incl_scan(n_l, lane);
+      excl = incl - n_l;
+      chunk_total = __shfl(incl, 63, 64);
+      const int64_t P = carry + excl;
+      mask = __ballot(n_l > 0 && P < ge && P + n_l > gs);
+    }
+    while (mask) {
+      // The chosen sequence is wave-uniform: its metadata comes from scalar loads, so only
+      // `excl` stays live in vector registers across the key loop.
+      const int li = __builtin_ctzll(mask);
+      mask &= mask - 1;
+      const int b = base + li;
+      const SeqSteps q = seq_steps(p, b);
+      const int64_t Pb = carry + __builtin_amdgcn_readlane(excl, li);
+      const int n = q.n;
+      const int a = (int)(max(gs, Pb) - Pb), e = (int)(min(ge, Pb + n) - Pb);
+      const int t_begin = q.first + 32 * a;
+      const int t_end = min(q.total, q.first + 32 * e);
+      const WaveInfo w = make_wave(p, D, b, kh, q.s0, q.pastb, q.total);
+      const int R = g * q.nq;  // <= 16 (host dispatch)
+      RowState<TT, D> rs;
+      init_rows<TT, D>(rs, p, w, 0, R, g, c, G);
+      run_range<TT, D, CAP>(w, rs, t_begin, t_end, t_end, lane, c, G, p.scale_log2, p.scale,
+                            p.softcap);
+      const bool final = Pb / L == (Pb + n - 1) / L;
+      const int64_t slot = (int64_t)seg + b;
+      store_rows<TT, D>(rs, p, w, 0, R, g, c, G, final, [&](int64_t, int, int rloc) {
+        return (slot * p.kv_heads + kh) * 16 + rloc;
+      });
+    }
+    carry += chunk_total;
+  }
+}
+
+// Merge the partials of one (token, head) row written by decode_balanced_kernel.
 template <typename TT>
-hipError_t launch_t(const AttnParams& p, int row_groups, hipStream_t s) {
-  dim3 grid(p.max_splits, p.kv_heads * row_groups, p.batch), block(64);
-  switch (p.head_dim) {
-    case 64: hipLaunchKernelGGL((decode_mfma_kernel<TT, 64>), grid, block, 0, s, p); break;
-    case 128: hipLaunchKernelGGL((decode_mfma_kernel<TT, 128>), grid, block, 0, s, p); break;
-    default: return hipErrorInvalidValue;
+__global__ __launch_bounds__(64) void balanced_reduce_kernel(const AttnParams p) {
+  const int h = blockIdx.x, t = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int D = p.head_dim, nseg = p.max_splits;
+  const int g = p.num_heads / p.kv_heads, kh = h / g;
+  const int b = seq_of_token(p.cum, p.batch, t);
+  const int64_t S = total_steps(p, lane);
+  if (S <= 0) return;
+  int64_t carry = 0;
+  for (int base = 0; base < b - (b % 64); base += 64)
+    carry += __shfl(wave_incl_scan(seq_steps(p, base + lane).n, lane), 63, 64);
+  const int base = b - (b % 64);
+  const SeqSteps mine = seq_steps(p, base + lane);
+  const int incl = wave_incl_scan(mine.n, lane);
+  const int li = b - base;
+  const int64_t Pb = carry + __shfl(incl - mine.n, li, 64);
+  const SeqSteps q = seq_steps(p, b);
+  if (q.n <= 0) return;
+  const int64_t seg_l = seg_len(S, nseg);
+  const int f = (int)(Pb / seg_l), l = (int)((Pb + q.n - 1) / seg_l);
+  if (f == l) return;  // written directly by the attention kernel
+  const int rloc = (t - q.s0) * g + (h % g);
+  const int nparts = l - f + 1;
+  auto pidx = [&](int k) { return (((int64_t)f + k + b) * p.kv_heads + kh) * 16 + rloc; };
+  float M = kNegInf;
+  for (int k = lane; k < nparts; k += 64) M = fmaxf(M, p.part_ml[pidx(k) * 2]);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+  float L = 0.0f;
+  for (int k = lane; k < nparts; k += 64) {
+    const float ms = p.part_ml[pidx(k) * 2];
+    if (ms != kNegInf) L += p.part_ml[pidx(k) * 2 + 1] * exp2f(ms - M);
+  }
+  L = wave_sum(L);
+  const float fct = finalize_factor(M, L, sink_logit<TT>(p, h));
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int k0 = 0; k0 < nparts; k0 += 64) {
+    float wl = 0.0f;
+    if (k0 + lane < nparts) {
+      const float ms = p.part_ml[pidx(k0 + lane) * 2];
+      wl = (ms == kNegInf) ? 0.0f : exp2f(ms - M);
+    }
+    const int n = min(64, nparts - k0);
+    for (int k = 0; k < n; ++k) {
+      const float wk = __shfl(wl, k, 64);
+      const float* row = p.part_o + pidx(k0 + k) * D;
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int e = lane + 64 * qd;
+        if (e < D) acc[qd] += row[e] * wk;
+      }
+    }
+  }
+  typename TT::raw* out = reinterpret_cast<typename TT::raw*>(p.out);
+#pragma unroll
+  for (int qd = 0; qd < 4; ++qd) {
+    const int e = lane + 64 * qd;
+    if (e < D) out[((int64_t)t * p.num_heads + h) * D + e] = TT::from_f32(acc[qd] * fct);
+  }
+}
+
+template <typename TT, int D>
+hipError_t launch_d(const AttnParams& p, dim3 grid, bool balanced, hipStream_t s) {
+  if (balanced) {
+    if (p.softcap > 0.0f)
+      hipLaunchKernelGGL((decode_balanced_kernel<TT, D, true>), grid, dim3(64), 0, s, p);
+    else
+      hipLaunchKernelGGL((decode_balanced_kernel<TT, D, false>), grid, dim3(64), 0, s, p);
+  } else {
+    if (p.softcap > 0.0f)
+      hipLaunchKernelGGL((decode_chunked_kernel<TT, D, true>), grid, dim3(64), 0, s, p);
+    else
+      hipLaunchKernelGGL((decode_chunked_kernel<TT, D, false>), grid, dim3(64), 0, s, p);
   }
   return hipGetLastError();
+}
+
+template <typename TT>
+hipError_t launch_t(const AttnParams& p, dim3 grid, bool balanced, hipStream_t s) {
+  switch (p.head_dim) {
+    case 64: return launch_d<TT, 64>(p, grid, balanced, s);
+    case 128: return launch_d<TT, 128>(p, grid, balanced, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace
@@ -375,15 +622,36 @@ bool decode_mfma_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype) {
   return head_dim == 64 || head_dim == 128;
 }
 
+// Chunked launch (p.max_splits chunks of p.chunk keys): any number of query rows.
 hipError_t launch_decode_mfma(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
                               hipStream_t s) {
   if (!decode_mfma_supported(p.head_dim, act, cache_dtype)) return hipErrorInvalidValue;
   if (p.batch <= 0) return hipSuccess;
   const int g = p.num_heads / p.kv_heads;
   const int mq = p.max_query_len > 0 ? p.max_query_len : p.num_tokens;
-  const int row_groups = (int)std::min<int64_t>(((int64_t)g * mq + 15) / 16, 65535 / p.kv_heads);
-  if (act == PA_DTYPE_FLOAT16) return launch_t<TF16>(p, row_groups, s);
-  return launch_t<TBF16>(p, row_groups, s);
+  const int row_groups =
+      (int)std::min<int64_t>(((int64_t)g * mq + 15) / 16, (int64_t)(INT32_MAX / p.kv_heads));
+  dim3 grid(p.kv_heads * row_groups, p.max_splits, p.batch);
+  if (act == PA_DTYPE_FLOAT16) return launch_t<TF16>(p, grid, false, s);
+  return launch_t<TBF16>(p, grid, false, s);
+}
+
+// Balanced launch: p.max_splits holds the segment count; every sequence must have at most 16
+// grouped query rows (g * query length <= 16).
+hipError_t launch_decode_balanced(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
+                                  hipStream_t s) {
+  if (!decode_mfma_supported(p.head_dim, act, cache_dtype)) return hipErrorInvalidValue;
+  if (p.batch <= 0) return hipSuccess;
+  dim3 grid(p.kv_heads, p.max_splits);
+  hipError_t e = (act == PA_DTYPE_FLOAT16) ? launch_t<TF16>(p, grid, true, s)
+                                           : launch_t<TBF16>(p, grid, true, s);
+  if (e != hipSuccess || p.part_o == nullptr) return e;
+  dim3 rgrid(p.num_heads, p.num_tokens);
+  if (act == PA_DTYPE_FLOAT16)
+    hipLaunchKernelGGL((balanced_reduce_kernel<TF16>), rgrid, dim3(64), 0, s, p);
+  else
+    hipLaunchKernelGGL((balanced_reduce_kernel<TBF16>), rgrid, dim3(64), 0, s, p);
+  return hipGetLastError();
 }
 
 }  // namespace pa

@@ -215,6 +215,8 @@ hipError_t launch_attn_generic(const AttnParams& p, pa_dtype act, pa_dtype cache
                                hipStream_t s);
 hipError_t launch_decode_mfma(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
                               hipStream_t s);
+hipError_t launch_decode_balanced(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
+                                  hipStream_t s);
 hipError_t launch_prefill_mfma(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
                                hipStream_t s);
 hipError_t launch_split_reduce(const AttnParams& p, pa_dtype act, hipStream_t s);

@@ -10,7 +10,9 @@ import os
 from pathlib import Path
 
 PKG_ROOT = Path(__file__).resolve().parent.parent
-LIB_PATH = PKG_ROOT / "lib" / "libonnxruntime_ep_mlx_amd.so"
+# ONNXRUNTIME_EP_MLX_AMD_LIB selects another build of the same library (side-by-side builds).
+LIB_PATH = Path(os.environ.get("ONNXRUNTIME_EP_MLX_AMD_LIB",
+                               PKG_ROOT / "lib" / "libonnxruntime_ep_mlx_amd.so"))
 
 PA_DTYPE_FLOAT16 = 1
 PA_DTYPE_BFLOAT16 = 2
