@@ -138,9 +138,9 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
   if (kind == 4) pl.kind = 1;
   const int ctx = std::max(max_ctx_bound(c, b), 1);
   if (pl.balanced) {
-    // One segment per group of kv_heads wavefronts, two wavefronts per SIMD on every CU.
+    // One segment per group of kv_heads wavefronts, one wavefront per SIMD on every CU.
     pl.chunk = 32;
-    pl.max_splits = std::max(1, 8 * device_cus() / c->kv_heads);
+    pl.max_splits = std::max(1, 4 * device_cus() / c->kv_heads);
     pl.part_rows = (size_t)(pl.max_splits + b->batch) * c->kv_heads * 16;
     return pl;
   }

@@ -237,39 +237,40 @@ __device__ __forceinline__ void compute_step(RowState<TT, D>& rs, const Step<D>&
 // multiple of 32.  Steps entirely inside cached pages go through the pipelined fast loop in
 // sub-ranges of at most 1024 keys (one block-table entry per lane covers a sub-range); the rest
 // take the per-lane addressed path.  `end` masks keys at or beyond it.
-template <typename TT, int D, bool CAP>
+//
+// The fast loop keeps DEPTH steps in registers: DEPTH-1 steps are in flight while one
+// computes.  Loads are always issued (past the last step they re-read the last step, which the
+// caches serve), so every path through an iteration issues the same loads and the compiler's
+// vmcnt waits only drain the step about to be computed.
+template <typename TT, int D, bool CAP, int DEPTH>
 __device__ __forceinline__ void run_range(WaveInfo w, RowState<TT, D>& rs, int t_begin,
                                           int t_last, int end, int lane, int c, int G,
                                           float scale_log2, float scale, float cap) {
+  static_assert(DEPTH == 2 || DEPTH == 3, "pipeline depth");
   const uint32_t koff = (uint32_t)(c * w.rowb + 16 * G);
   const uint32_t voff = (uint32_t)(4 * G * w.rowb + (D / 16) * 2 * c);
   const int fast_lim = (w.bs % 16 == 0) ? min(t_last, w.cache_limit) : t_begin;
   int t0 = t_begin;
-  Step<D> sA, sB;
+  Step<D> ring[DEPTH];
   while (t0 + 32 <= fast_lim) {
     const int nfast = (min(fast_lim, t0 + 1024) - t0) / 32;
     w.first_bi = div_bs(t0, w);
     const int btv = w.bt[min(w.first_bi + lane, w.max_blocks - 1)];
-    load_fast<D>(w, btv, koff, voff, t0, sA);
-    int k = 0;
-    while (k + 2 < nfast) {
-      load_fast<D>(w, btv, koff, voff, t0 + 32, sB);
-      compute_step<TT, D, CAP>(rs, sA, t0, end, G, scale_log2, scale, cap);
-      load_fast<D>(w, btv, koff, voff, t0 + 64, sA);
-      compute_step<TT, D, CAP>(rs, sB, t0 + 32, end, G, scale_log2, scale, cap);
-      t0 += 64;
-      k += 2;
+    const int last = t0 + 32 * (nfast - 1);
+#pragma unroll
+    for (int i = 0; i < DEPTH - 1; ++i) load_fast<D>(w, btv, koff, voff, min(t0 + 32 * i, last), ring[i]);
+    for (int k = 0; k < nfast; k += DEPTH) {
+#pragma unroll
+      for (int i = 0; i < DEPTH; ++i) {
+        load_fast<D>(w, btv, koff, voff, min(t0 + 32 * (k + i + DEPTH - 1), last),
+                     ring[(i + DEPTH - 1) % DEPTH]);
+        if (k + i < nfast)
+          compute_step<TT, D, CAP>(rs, ring[i], t0 + 32 * (k + i), end, G, scale_log2, scale, cap);
+      }
     }
-    if (k + 1 < nfast) {
-      load_fast<D>(w, btv, koff, voff, t0 + 32, sB);
-      compute_step<TT, D, CAP>(rs, sA, t0, end, G, scale_log2, scale, cap);
-      compute_step<TT, D, CAP>(rs, sB, t0 + 32, end, G, scale_log2, scale, cap);
-      t0 += 64;
-    } else {
-      compute_step<TT, D, CAP>(rs, sA, t0, end, G, scale_log2, scale, cap);
-      t0 += 32;
-    }
+    t0 += 32 * nfast;
   }
+  Step<D>& sA = ring[0];
   for (; t0 < t_last; t0 += 32) {
     load_edge<D>(w, c, G, t0, sA);
     compute_step<TT, D, CAP>(rs, sA, t0, end, G, scale_log2, scale, cap);
@@ -415,7 +416,7 @@ decode_chunked_kernel(const AttnParams p) {
     }
     const int t_first = max(start, (lo_any / 32) * 32);
     const int t_last = min(end, hi_any);
-    run_range<TT, D, CAP>(w, rs, t_first, t_last, end, lane, c, G, p.scale_log2, p.scale,
+    run_range<TT, D, CAP, 2>(w, rs, t_first, t_last, end, lane, c, G, p.scale_log2, p.scale,
                           p.softcap);
     store_rows<TT, D>(rs, p, w, row0, R, g, c, G, single, [&](int64_t t, int oh, int) {
       return (t * p.num_heads + oh) * p.max_splits + split;
@@ -475,8 +476,10 @@ __device__ __forceinline__ int64_t total_steps(const AttnParams& p, int lane) {
 // every segment between the first and last one covering a sequence holds part of it.
 __device__ __forceinline__ int64_t seg_len(int64_t S, int nseg) { return (S + nseg - 1) / nseg; }
 
+// One wavefront per SIMD: the 3-deep register pipeline (two 16 KiB steps in flight per
+// wavefront at d=128) measured faster than two wavefronts per SIMD with a 2-deep pipeline.
 template <typename TT, int D, bool CAP>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 decode_balanced_kernel(const AttnParams p) {
   const int kh = blockIdx.x, seg = blockIdx.y, nseg = gridDim.y;
   const int lane = threadIdx.x, c = lane & 15, G = lane >> 4;
@@ -514,7 +517,7 @@ decode_balanced_kernel(const AttnParams p) {
       const int R = g * q.nq;  // <= 16 (host dispatch)
       RowState<TT, D> rs;
       init_rows<TT, D>(rs, p, w, 0, R, g, c, G);
-      run_range<TT, D, CAP>(w, rs, t_begin, t_end, t_end, lane, c, G, p.scale_log2, p.scale,
+      run_range<TT, D, CAP, 3>(w, rs, t_begin, t_end, t_end, lane, c, G, p.scale_log2, p.scale,
                             p.softcap);
       const bool final = Pb / L == (Pb + n - 1) / L;
       const int64_t slot = (int64_t)seg + b;
