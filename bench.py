@@ -1,13 +1,14 @@
 #!/usr/bin/env python3
 """Benchmark: paged GQA decode step at the Llama-3-8B shape.
 
-One step = the hot path over one batch: fused RoPE + KV append of the 64 new tokens
-(pa_rotary_append) followed by split-K paged decode attention (pa_attention: MFMA decode kernel +
-split-K reduce).  Inputs are synthetic (seeded N(0,1), bf16) and resident in HBM before timing.
+One step = the hot path over one batch through the operator entry pa_paged_attention: host
+validation of the int32 metadata, fused RoPE + KV append of the 64 new tokens, and the balanced
+split-K paged decode on matrix cores.  Inputs are synthetic (seeded N(0,1), bf16) and resident in
+HBM before timing.
 
   value      = algorithmic KV bytes per step / step time (GB/s); KV bytes = 4096 * sum(ctx)
-  roofline   = the attention launch (decode kernel + reduce, same stream) timed with events on
-               that stream: achieved GB/s of KV bytes vs the 8 TB/s HBM peak
+  roofline   = the attention launch (pa_attention: counter clear + balanced decode kernel, same
+               stream) timed with events on that stream: KV bytes / launch time vs 8 TB/s
   cpu_baseline = the oracle's threaded contiguous-KV GQA decode (ORT CPU semantics) on a
                bounded sample of the same sequences, scaled to the full batch by KV bytes
 
@@ -81,27 +82,54 @@ def build_workload(torch, ep, seed):
 
 
 class Step:
-    """Pre-built C-ABI argument blocks so the timed loop is two ctypes calls per step."""
+    """Pre-built C-ABI argument blocks so the timed loop is one ctypes call per step.
+
+    step()      : pa_paged_attention -- the operator entry (RoPE + append + attention), with
+                  the int32 metadata validated on the host every step as the reference does.
+    append() /
+    attention() : the same work through the kernel-level entries, used to time the attention
+                  launch on its own for the roofline.
+    """
 
     def __init__(self, torch, ep, w, chunk):
+        import numpy as np
         from onnxruntime_ep_mlx_amd import _capi as capi
         from onnxruntime_ep_mlx_amd.ops import attn_desc, batch_desc, cache_desc
         self.lib = capi.load()
         self.capi = capi
+        self.w = w
+        self.act = capi.PA_DTYPE_BFLOAT16
+        self.stream = torch.cuda.current_stream().cuda_stream
+        self.out = torch.empty_like(w["q"])
+        # operator-level blocks
+        self.host = {n: np.ascontiguousarray(w[n].cpu().numpy()) for n in ("cum", "past", "bt")}
+        self.node = capi.PaNode(w["H"], w["KV"], 0.0, 0.0, -1, 1, 0, 0, 1, 1e-6)
+        self.io = capi.PaIO(
+            self.act, w["B"], w["H"] * w["d"], w["q"].data_ptr(), w["k"].data_ptr(),
+            w["v"].data_ptr(), cache_desc(w["kc"], w["vc"]), w["cum"].data_ptr(),
+            w["past"].data_ptr(), w["bt"].data_ptr(), w["B"], w["bt"].shape[1],
+            w["cos"].data_ptr(), w["sin"].data_ptr(), w["cos"].shape[0], w["cos"].shape[1],
+            None, None, None, None, self.host["cum"].ctypes.data, self.host["past"].ctypes.data,
+            self.host["bt"].ctypes.data, None, self.out.data_ptr())
+        self.op_ws_bytes = self.lib.pa_paged_attention_workspace_bytes(C.byref(self.node),
+                                                                       C.byref(self.io))
+        self.op_ws = torch.empty(max(self.op_ws_bytes, 1), dtype=torch.uint8, device="cuda")
+        # kernel-level blocks
         self.cache = cache_desc(w["kc"], w["vc"])
-        self.batch = batch_desc(w["cum"], w["past"], w["bt"], w["B"], None, 1)
+        self.batch = batch_desc(w["cum"], w["past"], w["bt"], w["B"], None, 1,
+                                capi.PA_BATCH_NEW_ROWS_IN_CACHE)
         self.attn = attn_desc(w["H"])
         self.q_out = torch.empty_like(w["q"])
         self.k_out = torch.empty_like(w["k"])
-        self.out = torch.empty_like(w["q"])
-        act = capi.PA_DTYPE_BFLOAT16
         self.chunk = chunk
         self.ws_bytes = self.lib.pa_attention_workspace_bytes_ex(
-            C.byref(self.cache), C.byref(self.batch), C.byref(self.attn), act, 1, chunk)
+            C.byref(self.cache), C.byref(self.batch), C.byref(self.attn), self.act, 1, chunk)
         self.ws = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device="cuda")
-        self.stream = torch.cuda.current_stream().cuda_stream
-        self.w = w
-        self.act = act
+
+    def __call__(self):
+        rc = self.lib.pa_paged_attention(C.byref(self.node), C.byref(self.io),
+                                         self.op_ws.data_ptr(), self.op_ws_bytes, self.stream)
+        self.capi.check(rc)
 
     def append(self):
         w = self.w
@@ -119,10 +147,6 @@ class Step:
             self.q_out.data_ptr(), self.k_out.data_ptr(), w["v"].data_ptr(),
             self.out.data_ptr(), self.ws.data_ptr(), self.ws_bytes, 1, self.chunk, self.stream)
         self.capi.check(rc)
-
-    def __call__(self):
-        self.append()
-        self.attention()
 
 
 def cpu_baseline(torch, w, step, n_seq, seconds):
@@ -199,7 +223,7 @@ def main():
     torch.cuda.synchronize()
     ms_step = e0.elapsed_time(e1) / args.steps
 
-    # dominant launch: the attention call (decode kernel + split-K reduce) on the same stream
+    # dominant launch: the attention call on the same stream, timed per launch
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(args.steps)]
     for a, b in evs:
@@ -237,12 +261,12 @@ def main():
             "batch": w["B"], "num_heads": w["H"], "kv_heads": w["KV"], "head_dim": w["d"],
             "block_size": w["bs"], "pool_blocks": w["nb"], "ctx": "U[512,8192]",
             "sum_ctx": int(w["ctx"].sum()), "kv_bytes_per_step": int(kv_bytes),
-            "rotary_theta": 500000.0, "split_k_chunk": args.chunk or "auto",
+            "rotary_theta": 500000.0, "entry": "pa_paged_attention (host-validated metadata)",
         },
         "roofline": {
             "bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "pa_attention (decode_mfma_kernel + split_reduce_kernel)",
+            "kernel": "pa_attention (decode_balanced_kernel + balanced_merge_kernel)",
             "us_per_launch": round(attn_ms * 1e3, 1),
         },
         "cpu_baseline": cpu,

@@ -102,7 +102,19 @@ typedef struct pa_batch {
   /* Host-known upper bound of new tokens per sequence; selects decode vs prefill kernels
    * without a device read.  0 means "unknown" and is treated as num_tokens. */
   int32_t max_query_len;
+  uint32_t flags; /* PA_BATCH_* bits */
 } pa_batch;
+
+/* The caller guarantees that every new key/value row was written to its block-table slot on
+ * this stream before the attention call (pa_rotary_append / pa_reshape_and_cache without a
+ * slot_mapping) and that no two tokens share a slot, so new positions may be read from the
+ * pages.  pa_paged_attention sets this itself when its host metadata proves it. */
+#define PA_BATCH_NEW_ROWS_IN_CACHE 1u
+
+/* The caller guarantees that no two new tokens map to the same cache slot, so the append
+ * skips its last-writer-wins check (a scan over later tokens).  pa_paged_attention sets this
+ * itself when its host metadata proves it. */
+#define PA_BATCH_SLOTS_DISTINCT 2u
 
 /* Attention attributes (attention.rs:3857-3870, 4255-4311; attr_scale :448-453). */
 typedef struct pa_attn {

@@ -6,6 +6,7 @@
 // the caller except the page pool.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <cstdarg>
@@ -165,15 +166,21 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
   return pl;
 }
 
+// Workspace: [partial O (fp32) | partial (m, l)].
 size_t workspace_for(const pa_cache* c, const pa_batch*, const pa_attn*, const Plan& pl) {
   if (pl.part_rows == 0) return 0;
   return align256(pl.part_rows * c->head_dim * sizeof(float)) +
          align256(pl.part_rows * 2 * sizeof(float));
 }
 
+// Options of one attention call beyond the public descriptors.
+struct RunOpts {
+  bool new_rows_in_cache = false;  // new rows sit in their block-table slots (see AttnParams)
+};
+
 int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype act,
                   const void* q, const void* kn, const void* vn, void* out, void* ws,
-                  size_t ws_bytes, int kind, int chunk, hipStream_t s) {
+                  size_t ws_bytes, int kind, int chunk, hipStream_t s, RunOpts opts = RunOpts()) {
   int rc = check_cache(c, act);
   if (rc) return rc;
   if ((rc = check_batch(b))) return rc;
@@ -231,6 +238,10 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
   p.window = a->local_window_size;
   p.causal = a->is_causal ? 1 : 0;
   p.read_all_from_cache = c->dtype == PA_DTYPE_FP8_E4M3 ? 1 : 0;
+  p.new_rows_in_cache =
+      (opts.new_rows_in_cache || ((b->flags & PA_BATCH_NEW_ROWS_IN_CACHE) && !b->slot_mapping))
+          ? 1
+          : 0;
 
   hipError_t e;
   if (pl.balanced) {
@@ -372,6 +383,7 @@ static int rotary_append_impl(const pa_cache* c, const pa_batch* b, int32_t num_
   p.rotary_interleaved = interleaved ? 1 : 0;
   p.do_q = (query && q_out && num_heads > 0) ? 1 : 0;
   p.norm_eps = eps;
+  p.slots_distinct = (b->flags & PA_BATCH_SLOTS_DISTINCT) ? 1 : 0;
   hipError_t e = pa::launch_rotary_append(p, act, c->dtype, s);
   if (e != hipSuccess) return hip_fail(e, "rotary/append kernel launch");
   return PA_OK;
@@ -467,6 +479,7 @@ int op_layout(const pa_paged_attention_node* n, const pa_paged_attention_io* io,
   b.max_blocks = io->max_blocks;
   b.num_tokens = io->num_tokens;
   b.max_query_len = 0;
+  b.flags = 0;
   if (io->host_cumulative_sequence_length) {
     int mq = 0;
     for (int i = 0; i < io->batch; ++i)
@@ -537,6 +550,24 @@ int validate_host_metadata(const pa_paged_attention_node* n, const pa_paged_atte
   return PA_OK;
 }
 
+// True when every token's block-table slot is distinct, so after the append each new key/value
+// row sits in its own slot and the attention may read new positions from the pages.
+bool host_slots_distinct(const pa_paged_attention_io* io) {
+  const int32_t* cum = io->host_cumulative_sequence_length;
+  const int32_t* past = io->host_past_seqlens;
+  const int32_t* bt = io->host_block_table;
+  const int64_t bs = io->cache.block_size;
+  std::vector<int64_t> slots;
+  slots.reserve((size_t)std::max(io->num_tokens, 0));
+  for (int b = 0; b < io->batch; ++b)
+    for (int t = cum[b]; t < cum[b + 1]; ++t) {
+      const int64_t pos = (int64_t)past[b] + (t - cum[b]);
+      slots.push_back((int64_t)bt[(int64_t)b * io->max_blocks + pos / bs] * bs + pos % bs);
+    }
+  std::sort(slots.begin(), slots.end());
+  return std::adjacent_find(slots.begin(), slots.end()) == slots.end();
+}
+
 }  // namespace
 
 size_t pa_paged_attention_workspace_bytes(const pa_paged_attention_node* node,
@@ -566,6 +597,11 @@ int pa_paged_attention(const pa_paged_attention_node* n, const pa_paged_attentio
   char* ws = reinterpret_cast<char*>(workspace);
   void* q_rot = L.transform ? ws : nullptr;
   void* k_rot = L.transform ? ws + L.q_bytes : nullptr;
+  RunOpts opts;
+  const bool distinct = io->slot_mapping == nullptr &&
+                        io->host_cumulative_sequence_length != nullptr && host_slots_distinct(io);
+  if (distinct) L.batch.flags |= PA_BATCH_SLOTS_DISTINCT;
+  opts.new_rows_in_cache = distinct && io->cache.dtype == io->dtype;
   rc = rotary_append_impl(&io->cache, &L.batch, n->num_heads, io->dtype, io->query, io->key,
                           io->value, q_rot, k_rot, n->do_rotary ? io->cos_cache : nullptr,
                           n->do_rotary ? io->sin_cache : nullptr, io->rotary_positions,
@@ -575,7 +611,7 @@ int pa_paged_attention(const pa_paged_attention_node* n, const pa_paged_attentio
   const void* q = L.transform ? q_rot : io->query;
   const void* kn = L.transform ? k_rot : io->key;
   return run_attention(&io->cache, &L.batch, &L.attn, io->dtype, q, kn, io->value, io->output,
-                       ws + L.attn_off, workspace_bytes - L.attn_off, 0, 0, s);
+                       ws + L.attn_off, workspace_bytes - L.attn_off, 0, 0, s, opts);
 }
 
 // ------------------------------------------------------------------------------ claim

@@ -10,6 +10,7 @@
 // v_cvt_f16_f32 for fp16; contraction into FMA is disabled for the fp32 variant.
 // Duplicate slots: a token skips its write when any later token maps to the same slot, so the
 // cache ends up holding the last token's row, as sequential scatter does.
+
 #include "pa_device.hpp"
 
 #pragma clang fp contract(off)
@@ -30,15 +31,21 @@ __device__ __forceinline__ float rnd(float v) {
   return TT::to_f32(TT::from_f32(v));
 }
 
-__device__ __forceinline__ int64_t token_slot(const AppendParams& p, int t) {
-  if (p.slot_mapping) return (int64_t)p.slot_mapping[t];
-  int b = seq_of_token(p.cum, p.batch, t);
-  int64_t logical = (int64_t)max(p.past[b], 0) + (t - p.cum[b]);
-  int64_t bi = logical / p.block_size;
+// Cache slot of logical position `logical` of sequence b; -1 when its block-table entry is
+// out of range.
+__device__ __forceinline__ int64_t slot_at(const AppendParams& p, int b, int64_t logical) {
+  const int64_t bi = logical / p.block_size;
   if (bi < 0 || bi >= p.max_blocks) return -1;
-  int64_t blk = p.block_table[(int64_t)b * p.max_blocks + bi];
+  const int64_t blk = p.block_table[(int64_t)b * p.max_blocks + bi];
   if (blk < 0 || blk >= p.num_blocks) return -1;
   return blk * p.block_size + logical % p.block_size;
+}
+
+// Per-lane slot of token u (the last-writer scan; u differs between lanes).
+__device__ __forceinline__ int64_t token_slot_lane(const AppendParams& p, int u) {
+  if (p.slot_mapping) return (int64_t)p.slot_mapping[u];
+  const int b = seq_of_token_lane(p.cum, p.batch, u);
+  return slot_at(p, b, (int64_t)max(p.past[b], 0) + (u - p.cum[b]));
 }
 
 // Normalise + rotate one head row in place of `dst` (reads from src).  Executed by one wave.
@@ -97,10 +104,11 @@ template <typename TT, bool FP8>
 __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p) {
   const int t = blockIdx.x;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int b = seq_of_token(p.cum, p.batch, t);
-  const int64_t pos = (int64_t)max(p.past[b], 0) + (t - p.cum[b]);
+  const SeqPos sp = seq_pos_of_token(p.cum, p.past, p.batch, t);
+  const int64_t pos = (int64_t)max(sp.past, 0) + (t - sp.start);
   const int D = p.head_dim;
   const bool transform = p.cos_cache != nullptr || p.q_norm != nullptr;
+
 
   // Workgroups with blockIdx.y >= 1 take four query head rows each, one per wavefront, so
   // every head row of every token is in flight at once.
@@ -115,12 +123,12 @@ __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p
   }
 
   // blockIdx.y == 0: this token's key/value rows.  Cache slot and last-writer rule first.
-  int64_t slot = token_slot(p, t);
+  int64_t slot = p.slot_mapping ? (int64_t)p.slot_mapping[t] : slot_at(p, sp.b, pos);
   if (slot >= p.num_blocks * p.block_size) slot = -1;
   bool later_dup = false;
-  if (slot >= 0) {
+  if (slot >= 0 && !p.slots_distinct) {
     for (int u = t + 1 + threadIdx.x; u < p.num_tokens; u += blockDim.x)
-      if (token_slot(p, u) == slot) later_dup = true;
+      if (token_slot_lane(p, u) == slot) later_dup = true;
   }
   const bool write_cache = slot >= 0 && !__syncthreads_or(later_dup);
 

@@ -249,7 +249,13 @@ __device__ __forceinline__ void run_range(WaveInfo w, RowState<TT, D>& rs, int t
   static_assert(DEPTH == 2 || DEPTH == 3, "pipeline depth");
   const uint32_t koff = (uint32_t)(c * w.rowb + 16 * G);
   const uint32_t voff = (uint32_t)(4 * G * w.rowb + (D / 16) * 2 * c);
-  const int fast_lim = (w.bs % 16 == 0) ? min(t_last, w.cache_limit) : t_begin;
+  int fast_lim = t_begin;
+  if (w.bs % 16 == 0) {
+    fast_lim = min(t_last, w.cache_limit);
+    // Every key of the sequence is in the pages: the last (partial) step comes from the pages
+    // too, its keys past the end masked and its page ids clamped into the pool.
+    if (w.cache_limit >= w.total) fast_lim = t_begin + ((t_last - t_begin + 31) / 32) * 32;
+  }
   int t0 = t_begin;
   Step<D> ring[DEPTH];
   while (t0 + 32 <= fast_lim) {
@@ -289,7 +295,7 @@ __device__ __forceinline__ WaveInfo make_wave(const AttnParams& p, int D, int b,
   w.s0 = s0;
   w.pastb = pastb;
   w.total = total;
-  w.cache_limit = p.read_all_from_cache ? total : pastb;
+  w.cache_limit = (p.read_all_from_cache || p.new_rows_in_cache) ? total : pastb;
   w.bs = p.block_size;
   w.bs_shift = (p.block_size & (p.block_size - 1)) == 0 ? __builtin_ctz(p.block_size) : -1;
   w.max_blocks = p.max_blocks;
@@ -434,23 +440,27 @@ decode_chunked_kernel(const AttnParams p) {
 // wavefronts finish together and the ones sharing pages read them together.  A sequence
 // covered by one segment is written directly; otherwise each covering segment s writes a
 // partial at slot s + b (unique: segments of b are consecutive and the next sequence starts in
-// the segment where b ends or in the next one), merged by balanced_reduce_kernel.
+// the segment where b ends or in the next one), merged by balanced_merge_kernel.
 
 struct SeqSteps {
   int s0, nq, pastb, total, first, n;  // first: first key step start (multiple of 32)
 };
 
+// All three metadata loads are issued before any test (index clamped; p.batch >= 1), so a
+// lookup costs one memory round trip.
 __device__ __forceinline__ SeqSteps seq_steps(const AttnParams& p, int b) {
   SeqSteps q{0, 0, 0, 0, 0, 0};
-  if (b >= p.batch) return q;
-  q.s0 = min(max(p.cum[b], 0), p.num_tokens);
-  const int s1 = min(max(p.cum[b + 1], q.s0), p.num_tokens);
+  const int bb = min(b, p.batch - 1);
+  const int c0 = p.cum[bb], c1 = p.cum[bb + 1], pb = p.past[bb];
+  const bool live = b < p.batch;
+  q.s0 = live ? min(max(c0, 0), p.num_tokens) : 0;
+  const int s1 = live ? min(max(c1, q.s0), p.num_tokens) : 0;
   q.nq = s1 - q.s0;
-  if (q.nq <= 0) return q;
-  q.pastb = max(p.past[b], 0);
-  q.total = q.pastb + q.nq;
-  q.first = p.window > 0 ? (max(0, q.pastb - p.window + 1) / 32) * 32 : 0;
-  q.n = (q.total - q.first + 31) / 32;
+  const bool any = q.nq > 0;
+  q.pastb = any ? max(pb, 0) : 0;
+  q.total = any ? q.pastb + q.nq : 0;
+  q.first = (any && p.window > 0) ? (max(0, q.pastb - p.window + 1) / 32) * 32 : 0;
+  q.n = any ? (q.total - q.first + 31) / 32 : 0;
   return q;
 }
 
@@ -475,6 +485,70 @@ __device__ __forceinline__ int64_t total_steps(const AttnParams& p, int lane) {
 // Segments are L = ceil(S / nseg) steps long, so empty segments can only trail the list and
 // every segment between the first and last one covering a sequence holds part of it.
 __device__ __forceinline__ int64_t seg_len(int64_t S, int nseg) { return (S + nseg - 1) / nseg; }
+
+// Merge the nparts partials of (sequence b, kv-head kh), stored at slots f+b .. f+nparts-1+b,
+// into the final rows.  Lane l handles row l/4 and a quarter of the head dims.  Pieces are taken
+// four at a time with every load of a batch issued before any is used (indices clamped into
+// range, surplus pieces weighted zero), so a merge costs one memory round trip per batch.
+template <typename TT, int D>
+__device__ __forceinline__ void merge_pieces(const AttnParams& p, int b, int kh, int s0, int R,
+                                             int g, int f, int nparts, int lane) {
+  constexpr int DQ = D / 4;   // dims per lane
+  constexpr int NV = DQ / 4;  // float4 loads per lane and piece
+  constexpr int KB = 4;       // pieces per batch
+  const int r = lane >> 2, quarter = lane & 3;
+  if (r >= R) return;
+  float M = kNegInf, lsum = 0.0f;
+  f32x4 acc[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) acc[v] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int k0 = 0; k0 < nparts; k0 += KB) {
+    float2 ml[KB];
+    f32x4 o[KB][NV];
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+      const int k = min(k0 + j, nparts - 1);
+      const int64_t row = (((int64_t)f + k + b) * p.kv_heads + kh) * 16 + r;
+      ml[j] = *reinterpret_cast<const float2*>(p.part_ml + row * 2);
+      const f32x4* src = reinterpret_cast<const f32x4*>(p.part_o + row * D + quarter * DQ);
+#pragma unroll
+      for (int v = 0; v < NV; ++v) o[j][v] = src[v];
+    }
+    float mn = M;
+#pragma unroll
+    for (int j = 0; j < KB; ++j)
+      if (k0 + j < nparts) mn = fmaxf(mn, ml[j].x);
+    // mn == -inf (every piece so far saw only masked keys) leaves a = w = 0 below.
+    const float a = (M == kNegInf) ? 0.0f : exp2f(M - mn);
+    lsum *= a;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) acc[v] *= a;
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+      const float w = (k0 + j < nparts && ml[j].x != kNegInf) ? exp2f(ml[j].x - mn) : 0.0f;
+      lsum += ml[j].y * w;
+#pragma unroll
+      for (int v = 0; v < NV; ++v) acc[v] += o[j][v] * w;
+    }
+    M = mn;
+  }
+  const int h = kh * g + r % g;
+  const int64_t t = s0 + r / g;
+  const float fct = finalize_factor(M, lsum, sink_logit<TT>(p, h));
+  u32x4* out = reinterpret_cast<u32x4*>(reinterpret_cast<typename TT::raw*>(p.out) +
+                                        (t * p.num_heads + h) * D + quarter * DQ);
+#pragma unroll
+  for (int v = 0; v < NV; v += 2) {
+    u32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const f32x4 x = acc[v + e / 2];
+      const float lo = x[(e & 1) * 2] * fct, hi = x[(e & 1) * 2 + 1] * fct;
+      w[e] = (uint32_t)TT::from_f32(lo) | ((uint32_t)TT::from_f32(hi) << 16);
+    }
+    out[v / 2] = w;
+  }
+}
 
 // One wavefront per SIMD: the 3-deep register pipeline (two 16 KiB steps in flight per
 // wavefront at d=128) measured faster than two wavefronts per SIMD with a 2-deep pipeline.
@@ -519,9 +593,10 @@ decode_balanced_kernel(const AttnParams p) {
       init_rows<TT, D>(rs, p, w, 0, R, g, c, G);
       run_range<TT, D, CAP, 3>(w, rs, t_begin, t_end, t_end, lane, c, G, p.scale_log2, p.scale,
                             p.softcap);
-      const bool final = Pb / L == (Pb + n - 1) / L;
+      const int f = (int)(Pb / L);
+      const int nparts = (int)((Pb + n - 1) / L) - f + 1;
       const int64_t slot = (int64_t)seg + b;
-      store_rows<TT, D>(rs, p, w, 0, R, g, c, G, final, [&](int64_t, int, int rloc) {
+      store_rows<TT, D>(rs, p, w, 0, R, g, c, G, nparts == 1, [&](int64_t, int, int rloc) {
         return (slot * p.kv_heads + kh) * 16 + rloc;
       });
     }
@@ -529,67 +604,37 @@ decode_balanced_kernel(const AttnParams p) {
   }
 }
 
-// Merge the partials of one (token, head) row written by decode_balanced_kernel.
-template <typename TT>
-__global__ __launch_bounds__(64) void balanced_reduce_kernel(const AttnParams p) {
-  const int h = blockIdx.x, t = blockIdx.y;
+// Merge the partials of every (kv-head, sequence) split across segments (one workgroup each).
+// A device-scope fence per piece inside the decode kernel (to let the last piece merge) writes
+// back the XCD's L2 and measured far slower than this separate launch.
+template <typename TT, int D>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void
+balanced_merge_kernel(const AttnParams p) {
+  const int kh = blockIdx.x, b = blockIdx.y;
   const int lane = threadIdx.x;
-  const int D = p.head_dim, nseg = p.max_splits;
-  const int g = p.num_heads / p.kv_heads, kh = h / g;
-  const int b = seq_of_token(p.cum, p.batch, t);
-  const int64_t S = total_steps(p, lane);
-  if (S <= 0) return;
-  int64_t carry = 0;
-  for (int base = 0; base < b - (b % 64); base += 64)
-    carry += __shfl(wave_incl_scan(seq_steps(p, base + lane).n, lane), 63, 64);
-  const int base = b - (b % 64);
-  const SeqSteps mine = seq_steps(p, base + lane);
-  const int incl = wave_incl_scan(mine.n, lane);
-  const int li = b - base;
-  const int64_t Pb = carry + __shfl(incl - mine.n, li, 64);
-  const SeqSteps q = seq_steps(p, b);
-  if (q.n <= 0) return;
+  const int nseg = p.max_splits;
+  const int g = p.num_heads / p.kv_heads;
+  // Prefix of steps up to b, b's own metadata and the total, one parallel pass over sequences.
+  int64_t S = 0, Pb = 0;
+  int nb = 0, s0 = 0, nq = 0;
+  for (int base = 0; base < p.batch; base += 64) {
+    const SeqSteps q = seq_steps(p, base + lane);
+    const int incl = wave_incl_scan(q.n, lane);
+    if (b >= base && b < base + 64) {
+      const int src = b - base;
+      Pb = S + __shfl(incl - q.n, src, 64);
+      nb = __shfl(q.n, src, 64);
+      s0 = __shfl(q.s0, src, 64);
+      nq = __shfl(q.nq, src, 64);
+    }
+    S += __shfl(incl, 63, 64);
+  }
+  if (nb <= 0 || S <= 0) return;
   const int64_t seg_l = seg_len(S, nseg);
-  const int f = (int)(Pb / seg_l), l = (int)((Pb + q.n - 1) / seg_l);
-  if (f == l) return;  // written directly by the attention kernel
-  const int rloc = (t - q.s0) * g + (h % g);
-  const int nparts = l - f + 1;
-  auto pidx = [&](int k) { return (((int64_t)f + k + b) * p.kv_heads + kh) * 16 + rloc; };
-  float M = kNegInf;
-  for (int k = lane; k < nparts; k += 64) M = fmaxf(M, p.part_ml[pidx(k) * 2]);
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-  float L = 0.0f;
-  for (int k = lane; k < nparts; k += 64) {
-    const float ms = p.part_ml[pidx(k) * 2];
-    if (ms != kNegInf) L += p.part_ml[pidx(k) * 2 + 1] * exp2f(ms - M);
-  }
-  L = wave_sum(L);
-  const float fct = finalize_factor(M, L, sink_logit<TT>(p, h));
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int k0 = 0; k0 < nparts; k0 += 64) {
-    float wl = 0.0f;
-    if (k0 + lane < nparts) {
-      const float ms = p.part_ml[pidx(k0 + lane) * 2];
-      wl = (ms == kNegInf) ? 0.0f : exp2f(ms - M);
-    }
-    const int n = min(64, nparts - k0);
-    for (int k = 0; k < n; ++k) {
-      const float wk = __shfl(wl, k, 64);
-      const float* row = p.part_o + pidx(k0 + k) * D;
-#pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const int e = lane + 64 * qd;
-        if (e < D) acc[qd] += row[e] * wk;
-      }
-    }
-  }
-  typename TT::raw* out = reinterpret_cast<typename TT::raw*>(p.out);
-#pragma unroll
-  for (int qd = 0; qd < 4; ++qd) {
-    const int e = lane + 64 * qd;
-    if (e < D) out[((int64_t)t * p.num_heads + h) * D + e] = TT::from_f32(acc[qd] * fct);
-  }
+  const int f = (int)(Pb / seg_l);
+  const int nparts = (int)((Pb + nb - 1) / seg_l) - f + 1;
+  if (nparts <= 1) return;  // written directly by the decode kernel
+  merge_pieces<TT, D>(p, b, kh, s0, g * nq, g, f, nparts, lane);
 }
 
 template <typename TT, int D>
@@ -640,20 +685,25 @@ hipError_t launch_decode_mfma(const AttnParams& p, pa_dtype act, pa_dtype cache_
 }
 
 // Balanced launch: p.max_splits holds the segment count; every sequence must have at most 16
-// grouped query rows (g * query length <= 16).
+// grouped query rows (g * query length <= 16).  Launches the decode and the partial merge.
 hipError_t launch_decode_balanced(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
                                   hipStream_t s) {
   if (!decode_mfma_supported(p.head_dim, act, cache_dtype)) return hipErrorInvalidValue;
   if (p.batch <= 0) return hipSuccess;
   dim3 grid(p.kv_heads, p.max_splits);
+  if (p.part_o == nullptr) return hipErrorInvalidValue;
   hipError_t e = (act == PA_DTYPE_FLOAT16) ? launch_t<TF16>(p, grid, true, s)
                                            : launch_t<TBF16>(p, grid, true, s);
-  if (e != hipSuccess || p.part_o == nullptr) return e;
-  dim3 rgrid(p.num_heads, p.num_tokens);
-  if (act == PA_DTYPE_FLOAT16)
-    hipLaunchKernelGGL((balanced_reduce_kernel<TF16>), rgrid, dim3(64), 0, s, p);
-  else
-    hipLaunchKernelGGL((balanced_reduce_kernel<TBF16>), rgrid, dim3(64), 0, s, p);
+  if (e != hipSuccess) return e;
+  const dim3 mgrid(p.kv_heads, p.batch);
+  const bool f16 = act == PA_DTYPE_FLOAT16;
+  if (p.head_dim == 64) {
+    if (f16) hipLaunchKernelGGL((balanced_merge_kernel<TF16, 64>), mgrid, dim3(64), 0, s, p);
+    else hipLaunchKernelGGL((balanced_merge_kernel<TBF16, 64>), mgrid, dim3(64), 0, s, p);
+  } else {
+    if (f16) hipLaunchKernelGGL((balanced_merge_kernel<TF16, 128>), mgrid, dim3(64), 0, s, p);
+    else hipLaunchKernelGGL((balanced_merge_kernel<TBF16, 128>), mgrid, dim3(64), 0, s, p);
+  }
   return hipGetLastError();
 }
 

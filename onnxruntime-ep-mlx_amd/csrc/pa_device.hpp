@@ -122,11 +122,56 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// Sequence index of packed token t: largest b with cum[b] <= t (cum monotone).
+// Sequence index of packed token t: largest b with cum[b] <= t (cum monotone, cum[0] <= t).
+// A 64-way search run by the whole wavefront (t wave-uniform): each level has every lane test
+// one evenly spaced candidate, so batch <= 64 costs one memory round trip and batch <= 4096
+// two, where a binary search pays log2(batch) dependent loads.
 __device__ __forceinline__ int seq_of_token(const int32_t* cum, int batch, int t) {
+  const int lane = threadIdx.x & 63;
+  int lo = 0, n = batch;  // answer in [lo, lo + n)
+  while (n > 64) {
+    const int step = (n + 63) / 64;
+    const int j = lo + lane * step;
+    const uint64_t ok = __ballot(j < lo + n && __ldg(&cum[j]) <= t);
+    const int k = ok ? 63 - __builtin_clzll(ok) : 0;  // last candidate at or below t
+    const int nlo = lo + k * step;
+    n = min(step, lo + n - nlo);
+    lo = nlo;
+  }
+  const uint64_t ok = __ballot(lane < n && __ldg(&cum[lo + lane]) <= t);
+  return ok ? lo + 63 - __builtin_clzll(ok) : lo;
+}
+
+// seq_of_token plus cum[b] and past[b], fetched in the same round trip as the last level.
+struct SeqPos {
+  int b, start, past;
+};
+__device__ __forceinline__ SeqPos seq_pos_of_token(const int32_t* cum, const int32_t* past,
+                                                   int batch, int t) {
+  const int lane = threadIdx.x & 63;
+  int lo = 0, n = batch;
+  while (n > 64) {
+    const int step = (n + 63) / 64;
+    const int j = lo + lane * step;
+    const uint64_t ok = __ballot(j < lo + n && __ldg(&cum[j]) <= t);
+    const int k = ok ? 63 - __builtin_clzll(ok) : 0;
+    const int nlo = lo + k * step;
+    n = min(step, lo + n - nlo);
+    lo = nlo;
+  }
+  const bool in = lane < n;
+  const int cj = in ? __ldg(&cum[lo + lane]) : 0;
+  const int pj = in ? __ldg(&past[lo + lane]) : 0;
+  const uint64_t ok = __ballot(in && cj <= t);
+  const int k = ok ? 63 - __builtin_clzll(ok) : 0;
+  return SeqPos{lo + k, __shfl(cj, k, 64), __shfl(pj, k, 64)};
+}
+
+// Per-lane form (t may differ between lanes, or lanes may be inactive): binary search.
+__device__ __forceinline__ int seq_of_token_lane(const int32_t* cum, int batch, int t) {
   int lo = 0, hi = batch - 1;
   while (lo < hi) {
-    int mid = (lo + hi + 1) >> 1;
+    const int mid = (lo + hi + 1) >> 1;
     if (__ldg(&cum[mid]) <= t)
       lo = mid;
     else
@@ -161,6 +206,7 @@ struct AppendParams {
   int32_t rotary_half, rotary_offset, rotary_interleaved;
   int32_t do_q;  // process query rows (rotary/norm) into q_out
   float norm_eps;
+  int32_t slots_distinct;  // no two tokens share a slot: skip the last-writer check
 };
 
 struct AttnParams {
@@ -189,6 +235,9 @@ struct AttnParams {
   int32_t window;    // <= 0 = off
   int32_t causal;
   int32_t read_all_from_cache;  // fp8 rule: every position from the pages
+  // The append that ran before this call left every new key/value row in its cache slot
+  // (block-table slots, no duplicates), so new positions may be read from the pages.
+  int32_t new_rows_in_cache;
 };
 
 // Final normalisation shared by every attention kernel: the factor that turns an output

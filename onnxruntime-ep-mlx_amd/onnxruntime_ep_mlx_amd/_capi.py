@@ -53,8 +53,11 @@ class PaBatch(C.Structure):
         ("cumulative_sequence_length", C.c_void_p), ("past_seqlens", C.c_void_p),
         ("block_table", C.c_void_p), ("slot_mapping", C.c_void_p),
         ("batch", C.c_int32), ("max_blocks", C.c_int32), ("num_tokens", C.c_int32),
-        ("max_query_len", C.c_int32),
+        ("max_query_len", C.c_int32), ("flags", C.c_uint32),
     ]
+
+
+PA_BATCH_NEW_ROWS_IN_CACHE = 1
 
 
 class PaAttn(C.Structure):

@@ -82,14 +82,14 @@ def cache_desc(key_cache: torch.Tensor, value_cache: torch.Tensor,
 
 def batch_desc(cum: torch.Tensor, past: torch.Tensor, block_table: torch.Tensor,
                num_tokens: int, slot_mapping: torch.Tensor | None = None,
-               max_query_len: int = 0) -> capi.PaBatch:
+               max_query_len: int = 0, flags: int = 0) -> capi.PaBatch:
     for name, t in (("cumulative_sequence_length", cum), ("past_seqlens", past),
                     ("block_table", block_table), ("slot_mapping", slot_mapping)):
         if t is not None and t.dtype != torch.int32:
             raise ValueError(f"input {name} must be int32")
         _contig(name, t)
     return capi.PaBatch(_ptr(cum), _ptr(past), _ptr(block_table), _ptr(slot_mapping),
-                        cum.numel() - 1, block_table.shape[1], num_tokens, max_query_len)
+                        cum.numel() - 1, block_table.shape[1], num_tokens, max_query_len, flags)
 
 
 def attn_desc(num_heads: int, scale: float = 0.0, softcap: float = 0.0,
@@ -195,11 +195,14 @@ def rotary_append(query, key, value, key_cache, value_cache, cum, past, block_ta
 
 def attention(q, k_new, v_new, key_cache, value_cache, cum, past, block_table, *, num_heads,
               scale=0.0, softcap=0.0, local_window_size=-1, is_causal=1, head_sink=None,
-              k_scale=None, v_scale=None, max_query_len=0, kind=0, chunk=0, out=None):
-    """Attention over the (already appended) paged cache; kind/chunk force a kernel family."""
+              k_scale=None, v_scale=None, max_query_len=0, kind=0, chunk=0, out=None,
+              new_rows_in_cache=False):
+    """Attention over the (already appended) paged cache; kind/chunk force a kernel family.
+    new_rows_in_cache: the caller appended k_new/v_new into distinct block-table slots."""
     lib = capi.load()
     cache = cache_desc(key_cache, value_cache, k_scale, v_scale)
-    batch = batch_desc(cum, past, block_table, q.shape[0], None, max_query_len)
+    batch = batch_desc(cum, past, block_table, q.shape[0], None, max_query_len,
+                       capi.PA_BATCH_NEW_ROWS_IN_CACHE if new_rows_in_cache else 0)
     attn = attn_desc(num_heads, scale, softcap, local_window_size, is_causal, head_sink)
     act = pa_dtype(q.dtype)
     nbytes = lib.pa_attention_workspace_bytes_ex(C.byref(cache), C.byref(batch), C.byref(attn),

@@ -223,9 +223,9 @@ def test_c3_geometry_reduced_batch(kind):
     assert err <= 2e-3, err
 
 
-# split-K invariance: every chunk size gives the oracle's answer
+# split-K invariance: every chunk size gives the oracle's answer (chunked MFMA and VALU kernels)
 @pytest.mark.parametrize("chunk", [32, 64, 256, 1024])
-@pytest.mark.parametrize("kind", [1, 3], ids=["mfma", "generic"])
+@pytest.mark.parametrize("kind", [4, 3], ids=["mfma_chunked", "generic"])
 def test_split_k_chunks(chunk, kind):
     import torch
     import onnxruntime_ep_mlx_amd as ep
@@ -248,6 +248,52 @@ def test_split_k_chunks(chunk, kind):
     torch.cuda.synchronize()
     err = orc.rel_l2(orc.decode(from_torch(out, BF16), BF16), orc.decode(ref_t, BF16))
     assert err <= 2e-3, err
+
+
+# balanced decode kernel through the kernel-level entries: segments that split sequences,
+# sequences of one step, the separate partial merge, and both sources of the new rows
+@pytest.mark.parametrize("new_rows_in_cache", [False, True])
+@pytest.mark.parametrize("B,lo,hi", [(4, 100, 3000), (64, 1, 40), (37, 1, 9000)])
+def test_balanced_decode_kernel_level(new_rows_in_cache, B, lo, hi):
+    import torch
+    import onnxruntime_ep_mlx_amd as ep
+    from pa_cases import to_torch, from_torch
+    rng = np.random.default_rng(B + lo)
+    bs = 16
+    ctx = rng.integers(lo, hi + 1, size=B)
+    mb = int((ctx.max() + bs - 1) // bs)
+    case = make_case(32, 8, 128, B * mb, bs, B, dtype=BF16, seed=B + hi, new_lens=[1] * B,
+                     past=ctx - 1, max_blocks=mb, std=1.0)
+    ref, ref_t, kc_ref, _ = orc.paged_attention_op(case)
+    t = {n: to_torch(case[n], BF16) for n in ("query", "key", "value", "key_cache",
+                                              "value_cache")}
+    I = {n: torch.from_numpy(case[n]).cuda() for n in ("cum", "past", "block_table")}
+    ep.reshape_and_cache(t["key"], t["value"], t["key_cache"], t["value_cache"], I["cum"],
+                         I["past"], I["block_table"])
+    outs = []
+    for _ in range(2):  # twice: the workspace left by one call must not leak into the next
+        outs.append(ep.attention(t["query"], t["key"], t["value"], t["key_cache"],
+                                 t["value_cache"], I["cum"], I["past"], I["block_table"],
+                                 num_heads=32, max_query_len=1, kind=1,
+                                 new_rows_in_cache=new_rows_in_cache))
+    torch.cuda.synchronize()
+    for out in outs:
+        err = orc.rel_l2(orc.decode(from_torch(out, BF16), BF16), orc.decode(ref_t, BF16))
+        assert err <= 2e-3, err
+    assert torch.equal(outs[0], outs[1])
+
+
+# batches beyond one wavefront: the 64-way sequence search takes two levels (append, generic
+# kernel) and the balanced decode scans sequences in several 64-wide chunks; decode and mixed
+# decode/prefill, with rotary so the query rows go through the append kernel too
+@pytest.mark.parametrize("B,mixed", [(65, False), (300, False), (150, True)])
+def test_large_batch(B, mixed):
+    rng = np.random.default_rng(B)
+    bs, mb = 16, 12
+    new = rng.integers(1, 5, size=B) if mixed else np.ones(B, np.int64)
+    past = np.array([rng.integers(0, mb * bs - n + 1) for n in new])
+    check(make_case(8, 2, 128, B * mb, bs, B, dtype=BF16, seed=B, new_lens=new, past=past,
+                    max_blocks=mb, do_rotary=1, std=1.0))
 
 
 # BASELINE config 4 geometry (Qwen2.5-7B chunked prefill), reduced
