@@ -199,7 +199,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(decode shards by sequence or kv-head with no exchange; see DESIGN.md)",
+              "(decode shards by sequence or kv-head with no exchange between GPUs)",
               file=sys.stderr)
         sys.exit(2)
     import torch
@@ -256,7 +256,7 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) bf16 pages, q/k/v; random block tables)",
         "config": {
-            "workload": "paged GQA decode, Llama-3-8B shape (BASELINE config 3): RoPE + KV "
+            "workload": "paged GQA decode, Llama-3-8B shape (BASELINE.json config 3): RoPE + KV "
                         "append + split-K paged attention per step",
             "batch": w["B"], "num_heads": w["H"], "kv_heads": w["KV"], "head_dim": w["d"],
             "block_size": w["bs"], "pool_blocks": w["nb"], "ctx": "U[512,8192]",

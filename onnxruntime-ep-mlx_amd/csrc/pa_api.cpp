@@ -91,11 +91,19 @@ int check_batch(const pa_batch* bt) {
 // ---------------------------------------------------------------------------- attention plan
 // kind: 1 decode MFMA (balanced segments when every sequence has <= 16 grouped query rows,
 // chunked otherwise), 2 prefill MFMA, 3 generic VALU, 4 decode MFMA forced chunked.
+// Balanced decode: sub-segments per wavefront, each for the next kv-head.  Mixing kv-heads
+// within a wavefront evens out the different HBM speeds of the kv-heads' byte ranges.
+#ifndef PA_DECODE_MIX
+#define PA_DECODE_MIX 1
+#endif
+constexpr int kDecodeMix = PA_DECODE_MIX;
+
 struct Plan {
   int kind;
   bool balanced;
   int chunk;
-  int max_splits;    // chunk count (chunked/generic) or segment count (balanced)
+  int max_splits;    // chunk count (chunked/generic) or sub-segment count (balanced)
+  int mix;           // balanced: sub-segments per wavefront
   size_t part_rows;  // rows of fp32 partials in the workspace
 };
 
@@ -135,13 +143,17 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
       kind = 3;
   }
   pl.kind = kind;
-  pl.balanced = kind == 1 && (int64_t)g * mq <= 16;
+  // The balanced (streaming) decode addresses rows with 32-bit row indices and shifts.
+  const bool pow2_bs = (c->block_size & (c->block_size - 1)) == 0;
+  pl.balanced = kind == 1 && (int64_t)g * mq <= 16 && pow2_bs &&
+                (int64_t)c->num_blocks * c->block_size <= (int64_t)UINT32_MAX;
   if (kind == 4) pl.kind = 1;
   const int ctx = std::max(max_ctx_bound(c, b), 1);
   if (pl.balanced) {
-    // One segment per group of kv_heads wavefronts, one wavefront per SIMD on every CU.
+    // One wavefront per SIMD on every CU, each walking kDecodeMix sub-segments.
     pl.chunk = 32;
-    pl.max_splits = std::max(1, 4 * device_cus() / c->kv_heads);
+    pl.mix = std::min(kDecodeMix, c->kv_heads);
+    pl.max_splits = pl.mix * std::max(1, 4 * device_cus() / c->kv_heads);
     pl.part_rows = (size_t)(pl.max_splits + b->batch) * c->kv_heads * 16;
     return pl;
   }
@@ -231,6 +243,7 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
   p.num_tokens = b->num_tokens;
   p.chunk = pl.chunk;
   p.max_splits = pl.max_splits;
+  p.mix = pl.mix;
   p.max_query_len = b->max_query_len > 0 ? b->max_query_len : b->num_tokens;
   p.scale = a->scale != 0.0f ? a->scale : 1.0f / std::sqrt((float)c->head_dim);
   p.scale_log2 = p.scale * pa::kLog2e;

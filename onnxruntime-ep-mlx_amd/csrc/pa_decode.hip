@@ -337,9 +337,9 @@ __device__ __forceinline__ void init_rows(RowState<TT, D>& rs, const AttnParams&
 // Epilogue: rows 4G+i of this lane's O registers.  final: normalise (with the sink) and write
 // the output row in T; otherwise write the fp32 partial (O, m, l) at part_index(row).
 template <typename TT, int D, typename PartIndex>
-__device__ __forceinline__ void store_rows(const RowState<TT, D>& rs, const AttnParams& p,
-                                           const WaveInfo& w, int row0, int R, int g, int c,
-                                           int G, bool final, PartIndex part_index) {
+__device__ __forceinline__ void store_rows(const RowState<TT, D>& rs, const AttnParams& p, int kh,
+                                           int s0, int row0, int R, int g, int c, int G,
+                                           float sink_c, bool final, PartIndex part_index) {
   constexpr int DL = D / 16;
   float l_row = rs.l_part + __shfl_xor(rs.l_part, 16, 64);
   l_row += __shfl_xor(l_row, 32, 64);
@@ -348,11 +348,12 @@ __device__ __forceinline__ void store_rows(const RowState<TT, D>& rs, const Attn
     const int rr = row0 + 4 * G + i;
     const float mi = __shfl(rs.m_run, 4 * G + i, 64);
     const float li = __shfl(l_row, 4 * G + i, 64);
+    const float si = __shfl(sink_c, 4 * G + i, 64);  // sink logit of row rr (log2 units)
     if (rr >= R) continue;
-    const int oqi = rr / g, oh = w.kh * g + rr % g;
-    const int64_t t = w.s0 + oqi;
+    const int oqi = rr / g, oh = kh * g + rr % g;
+    const int64_t t = s0 + oqi;
     if (final) {
-      const float f = finalize_factor(mi, li, sink_logit<TT>(p, oh));
+      const float f = finalize_factor(mi, li, si);
       typename TT::raw vals[DL];
 #pragma unroll
       for (int j = 0; j < DL; ++j) vals[j] = TT::from_f32(rs.o[j][i] * f);
@@ -424,7 +425,9 @@ decode_chunked_kernel(const AttnParams p) {
     const int t_last = min(end, hi_any);
     run_range<TT, D, CAP, 2>(w, rs, t_first, t_last, end, lane, c, G, p.scale_log2, p.scale,
                           p.softcap);
-    store_rows<TT, D>(rs, p, w, row0, R, g, c, G, single, [&](int64_t t, int oh, int) {
+    const int rc = min(row0 + c, R - 1);
+    const float sink_c = sink_logit<TT>(p, kh * g + rc % g);
+    store_rows<TT, D>(rs, p, kh, s0, row0, R, g, c, G, sink_c, single, [&](int64_t t, int oh, int) {
       return (t * p.num_heads + oh) * p.max_splits + split;
     });
   }
@@ -473,11 +476,12 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
   return v;
 }
 
+// Wave-uniform (readlane, so the compiler keeps it in scalar registers).
 __device__ __forceinline__ int64_t total_steps(const AttnParams& p, int lane) {
   int64_t S = 0;
   for (int base = 0; base < p.batch; base += 64) {
     const int n = seq_steps(p, base + lane).n;
-    S += __shfl(wave_incl_scan(n, lane), 63, 64);
+    S += __builtin_amdgcn_readlane(wave_incl_scan(n, lane), 63);
   }
   return S;
 }
@@ -550,56 +554,307 @@ __device__ __forceinline__ void merge_pieces(const AttnParams& p, int b, int kh,
   }
 }
 
-// One wavefront per SIMD: the 3-deep register pipeline (two 16 KiB steps in flight per
-// wavefront at d=128) measured faster than two wavefronts per SIMD with a 2-deep pipeline.
-template <typename TT, int D, bool CAP>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
-decode_balanced_kernel(const AttnParams p) {
-  const int kh = blockIdx.x, seg = blockIdx.y, nseg = gridDim.y;
-  const int lane = threadIdx.x, c = lane & 15, G = lane >> 4;
+__device__ __forceinline__ int64_t readlane64(int64_t v, int l) {
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, l);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)v >> 32), l);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// Up to 64 consecutive sequences, lane l describing sequence base + l.
+struct SeqWin {
+  int base;
+  SeqSteps q;
+  int64_t P;  // first flattened step of this lane's sequence
+};
+
+// Wave-uniform position in the flattened step list.
+struct Cursor {
+  int64_t f;     // flattened step
+  int bl;        // window lane of the sequence holding step f
+  int64_t pend;  // one past that sequence's last step
+  int64_t u;     // sub-segment holding step f
+  int64_t ub;    // one past that sub-segment's last step
+};
+
+__device__ __forceinline__ Cursor cursor_at(const SeqWin& sw, int64_t f, int64_t L) {
+  Cursor c;
+  c.f = f;
+  const int64_t pend_l = sw.P + sw.q.n;
+  const uint64_t m = __ballot(sw.q.n > 0 && pend_l > f);
+  c.bl = m ? __builtin_ctzll(m) : 63;
+  c.pend = readlane64(pend_l, c.bl);
+  c.u = f / L;
+  c.ub = (c.u + 1) * L;
+  return c;
+}
+
+// Next step, or stay on the last one (hi - 1): look-ahead cursors re-read it.
+__device__ __forceinline__ void cursor_next(Cursor& c, const SeqWin& sw, int64_t hi, int64_t L) {
+  if (c.f + 1 >= hi) return;
+  ++c.f;
+  if (c.f >= c.pend) {
+    const int64_t pend_l = sw.P + sw.q.n;
+    const uint64_t m = __ballot(sw.q.n > 0 && pend_l > c.f);
+    c.bl = m ? __builtin_ctzll(m) : 63;
+    c.pend = readlane64(pend_l, c.bl);
+  }
+  if (c.f >= c.ub) {
+    ++c.u;
+    c.ub += L;
+  }
+}
+
+// Everything one step needs, read from the window lanes (wave-uniform).
+struct StepAt {
+  int b, kh, t, s0, nq, pastb, total, cache_limit;
+  int64_t P;
+  int n;
+};
+
+__device__ __forceinline__ StepAt step_at(const Cursor& c, const SeqWin& sw, const AttnParams& p,
+                                          int x, int64_t u0) {
+  StepAt s;
+  s.b = sw.base + c.bl;
+  s.P = readlane64(sw.P, c.bl);
+  s.n = __builtin_amdgcn_readlane(sw.q.n, c.bl);
+  s.t = __builtin_amdgcn_readlane(sw.q.first, c.bl) + 32 * (int)(c.f - s.P);
+  s.s0 = __builtin_amdgcn_readlane(sw.q.s0, c.bl);
+  s.nq = __builtin_amdgcn_readlane(sw.q.nq, c.bl);
+  s.pastb = __builtin_amdgcn_readlane(sw.q.pastb, c.bl);
+  s.total = __builtin_amdgcn_readlane(sw.q.total, c.bl);
+  s.cache_limit = (p.read_all_from_cache || p.new_rows_in_cache) ? s.total : s.pastb;
+  const int kh = x + (int)(c.u - u0);  // mix <= kv_heads
+  s.kh = kh >= p.kv_heads ? kh - p.kv_heads : kh;
+  return s;
+}
+
+// Block-table entries of a step: lane l holds the entry of key t + (l & 31) (index clamped into
+// the table row; entries past the sequence are never used for addressing).
+__device__ __forceinline__ int load_step_blocks(const AttnParams& p, const StepAt& s, int lane,
+                                                int bs_shift) {
+  const int bi = min((s.t + (lane & 31)) >> bs_shift, p.max_blocks - 1);
+  return p.block_table[(int64_t)s.b * p.max_blocks + bi];
+}
+
+// Address of key/value row `pos` (t <= pos < total) of a step, branch-free: a cache page when
+// pos < cache_limit (page id from lane pos - t of `btl`, clamped into the pool), else the new
+// row of the packed batch.
+__device__ __forceinline__ const char* stream_row(const AttnParams& p, const StepAt& s, int btl,
+                                                  int pos, const char* cache, const char* fresh,
+                                                  uint32_t rowb, uint32_t hoff, int bs_shift) {
+  const int blk = min(max(__shfl(btl, pos - s.t, 64), 0), (int)min(p.num_blocks - 1,
+                                                                      (int64_t)INT32_MAX));
+  const uint32_t crow = ((uint32_t)blk << bs_shift) + (uint32_t)(pos & (p.block_size - 1));
+  const uint32_t tok = (uint32_t)min(max(s.s0 + (pos - s.pastb), 0), p.num_tokens - 1);
+  const bool in_cache = pos < s.cache_limit;
+  const char* base = in_cache ? cache : fresh;
+  const uint64_t row = in_cache ? crow : tok;
+  return base + row * rowb + hoff;
+}
+
+// All loads of one step: K and V rows of both 16-key tiles and the query rows of the step's
+// (sequence, kv-head).  Straight-line code, so every iteration issues the same loads and the
+// compiler's vmcnt waits only drain the step about to be computed.  Rows past the sequence end
+// re-read the last row.
+template <typename TT, int D>
+__device__ __forceinline__ void load_stream_step(const AttnParams& p, const StepAt& s, int btl,
+                                                 int lane, int g, int bs_shift, Step<D>& st,
+                                                 u32x4 (&qv)[D / 32], typename TT::raw& sk) {
+  const int c = lane & 15, G = lane >> 4;
+  constexpr int DL = D / 16;
+  const uint32_t rowb = (uint32_t)p.kv_heads * D * 2;
+  const uint32_t hoff = (uint32_t)s.kh * D * 2;
+  const char* kc = reinterpret_cast<const char*>(p.key_cache);
+  const char* vc = reinterpret_cast<const char*>(p.value_cache);
+  const char* kn = reinterpret_cast<const char*>(p.k_new);
+  const char* vn = reinterpret_cast<const char*>(p.v_new);
+  const int last = s.total - 1;
+  if (bs_shift >= 4 && min(s.t + 31, last) < s.cache_limit) {
+    // Every row in the pages and each 16-key tile inside one page: scalar page base (page id
+    // read from a lane of `btl`), fixed lane offsets.  Rows past the end stay in the last page.
+#pragma unroll
+    for (int tile = 0; tile < 2; ++tile) {
+      const int tp = s.t + 16 * tile;
+      const int64_t blk = min(max((int64_t)__builtin_amdgcn_readlane(btl, 16 * tile), (int64_t)0),
+                              (int64_t)p.num_blocks - 1);
+      const char* kb = kc + (uint64_t)((blk << bs_shift) + (tp & (p.block_size - 1))) * rowb + hoff;
+      const char* vb = vc + (uint64_t)((blk << bs_shift) + (tp & (p.block_size - 1))) * rowb + hoff;
+#pragma unroll
+      for (int q = 0; q < D / 32; ++q) st.k[tile][q] = ld16(kb + c * rowb + 16 * G + 64 * q);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        st.v[4 * tile + e] = ld_vrow<D>(vb + (4 * G + e) * rowb + DL * 2 * c);
+    }
+  } else {
+#pragma unroll
+    for (int tile = 0; tile < 2; ++tile) {
+      const int tp = s.t + 16 * tile;
+      const char* kr = stream_row(p, s, btl, min(tp + c, last), kc, kn, rowb, hoff, bs_shift);
+#pragma unroll
+      for (int q = 0; q < D / 32; ++q) st.k[tile][q] = ld16(kr + 16 * G + 64 * q);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const char* vr =
+            stream_row(p, s, btl, min(tp + 4 * G + e, last), vc, vn, rowb, hoff, bs_shift);
+        st.v[4 * tile + e] = ld_vrow<D>(vr + DL * 2 * c);
+      }
+    }
+  }
+  // Query rows of this (sequence, kv-head): MFMA column c is row r = c (rows past R repeat the
+  // last one; their scores are masked).
+  const int r = min(c, g * s.nq - 1);
+  const char* qrow = reinterpret_cast<const char*>(p.q) +
+                     (((int64_t)(s.s0 + r / g) * p.num_heads + s.kh * g + r % g) * D + 8 * G) * 2;
+#pragma unroll
+  for (int q = 0; q < D / 32; ++q) qv[q] = ld16(qrow + 64 * q);
+  // Sink logit input of that row's head (a harmless read of the query when there is none).
+  const typename TT::raw* sp = p.head_sink ? reinterpret_cast<const typename TT::raw*>(p.head_sink)
+                                           : reinterpret_cast<const typename TT::raw*>(p.q);
+  sk = sp[p.head_sink ? s.kh * g + r % g : 0];
+}
+
+// Stream the flattened steps [lo, hi) of one window through a DEPTH-3 register ring.  Three
+// cursors run over the same step list: block-table entries are fetched four steps ahead of the
+// compute, key/value/query rows two steps ahead, so a sequence or kv-head boundary costs no
+// pipeline refill.  A piece (one sequence, one sub-segment) is finished when the compute cursor
+// leaves it: final rows when the piece covers its whole sequence, else a partial at slot u + b.
+template <typename TT, int D, bool CAP, int DEPTH>
+__device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& sw, int64_t lo,
+                                             int64_t hi, int64_t L, int x, int64_t u0,
+                                             int lane) {
+  using vec8 = typename TT::vec8;
+  const int c = lane & 15, G = lane >> 4;
   const int g = p.num_heads / p.kv_heads;
+  const int bs_shift = __builtin_ctz(p.block_size);  // power of two (host dispatch)
+  const int64_t K = hi - lo;
+
+  Cursor cc = cursor_at(sw, lo, L);
+  Cursor cd = cc, cb = cc;
+  Step<D> st[DEPTH];
+  u32x4 qr[DEPTH][D / 32];
+  typename TT::raw skr[DEPTH];
+  int btr[DEPTH];
+  // Prologue: block ids of steps 0 .. DEPTH-2, their rows, block ids of the next DEPTH-1 steps.
+#pragma unroll
+  for (int j = 0; j < DEPTH - 1; ++j) {
+    btr[j] = load_step_blocks(p, step_at(cb, sw, p, x, u0), lane, bs_shift);
+    cursor_next(cb, sw, hi, L);
+  }
+#pragma unroll
+  for (int j = 0; j < DEPTH - 1; ++j) {
+    load_stream_step<TT, D>(p, step_at(cd, sw, p, x, u0), btr[j], lane, g, bs_shift, st[j], qr[j],
+                            skr[j]);
+    cursor_next(cd, sw, hi, L);
+  }
+#pragma unroll
+  for (int j = DEPTH - 1; j < 2 * DEPTH - 2; ++j) {
+    btr[j % DEPTH] = load_step_blocks(p, step_at(cb, sw, p, x, u0), lane, bs_shift);
+    cursor_next(cb, sw, hi, L);
+  }
+
+  RowState<TT, D> rs;
+  int pc_bl = -1;
+  int64_t pc_u = -1;
+  StepAt pc{};  // the piece being computed
+  bool pc_final = false;
+  int pc_first = 0;
+  float pc_sink = kNegInf;  // sink logit of row c
+  auto finish = [&]() {
+    const int64_t slot = pc_u + pc.b;
+    store_rows<TT, D>(rs, p, pc.kh, pc.s0, 0, g * pc.nq, g, c, G, pc_sink, pc_final,
+                      [&](int64_t, int, int rloc) { return (slot * p.kv_heads + pc.kh) * 16 + rloc; });
+  };
+
+  for (int64_t k = 0; k < K; k += DEPTH) {
+#pragma unroll
+    for (int i = 0; i < DEPTH; ++i) {
+      // Rows of step k+i+DEPTH-1 (block ids fetched DEPTH-1 iterations ago), then the block ids
+      // of step k+i+2*(DEPTH-1).
+      const int sd_slot = (i + DEPTH - 1) % DEPTH, sb_slot = (i + DEPTH - 2) % DEPTH;
+      load_stream_step<TT, D>(p, step_at(cd, sw, p, x, u0), btr[sd_slot], lane, g, bs_shift,
+                              st[sd_slot], qr[sd_slot], skr[sd_slot]);
+      cursor_next(cd, sw, hi, L);
+      btr[sb_slot] = load_step_blocks(p, step_at(cb, sw, p, x, u0), lane, bs_shift);
+      cursor_next(cb, sw, hi, L);
+      if (k + i < K) {
+        if (cc.bl != pc_bl || cc.u != pc_u) {
+          if (pc_bl >= 0) finish();
+          pc = step_at(cc, sw, p, x, u0);
+          pc_bl = cc.bl;
+          pc_u = cc.u;
+          pc_final = pc.P >= cc.u * L && pc.P + pc.n <= cc.ub;
+          pc_first = __builtin_amdgcn_readlane(sw.q.first, cc.bl);
+          pc_sink = p.head_sink ? TT::to_f32(skr[i]) * kLog2e : kNegInf;
+          const int R = g * pc.nq;
+          const bool rvalid = c < R;
+          const int rpos = pc.pastb + (rvalid ? c / g : 0);
+          rs.vis_lo = p.window > 0 ? rpos - p.window + 1 : 0;
+          rs.vis_hi = rvalid ? (p.causal ? rpos + 1 : pc.total) : -1;
+#pragma unroll
+          for (int q = 0; q < D / 32; ++q) rs.qv[q] = __builtin_bit_cast(vec8, qr[i][q]);
+#pragma unroll
+          for (int j = 0; j < D / 16; ++j) rs.o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+          rs.m_run = kNegInf;
+          rs.l_part = 0.0f;
+        }
+        const int t0 = pc_first + 32 * (int)(cc.f - pc.P);
+        Step<D>& cur = st[i];
+        if (t0 + 32 > pc.total) {
+          // Value rows past the sequence end (re-read rows) take no part, even if non-finite.
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int pos = t0 + 16 * (e >> 2) + 4 * G + (e & 3);
+            if (pos >= pc.total) cur.v[e] = VRow<D>{};
+          }
+        }
+        compute_step<TT, D, CAP>(rs, cur, t0, pc.total, G, p.scale_log2, p.scale, p.softcap);
+        cursor_next(cc, sw, hi, L);
+      }
+    }
+  }
+  if (pc_bl >= 0) finish();
+}
+
+// Decode with at most 16 grouped query rows per sequence.  Every sequence contributes
+// n_b = ceil((total_b - first_b) / 32) steps of 32 keys (first_b: first key any row can see); the
+// steps of all sequences, in order, are cut into p.max_splits sub-segments of L = ceil(S /
+// max_splits) steps (empty ones only at the end).  Sub-segment u of kv-head h is walked by
+// wavefront (x, seg) with seg = u / mix and x = (h - u % mix) mod kv_heads: each wavefront walks
+// `mix` consecutive sub-segments, each for the next kv-head, so every wavefront reads the same
+// share of every kv-head's bytes (whose HBM speed differs by their address) and all finish
+// together.  A sequence inside one sub-segment is written directly; otherwise each covering
+// sub-segment u writes a partial at slot u + b (unique: the sub-segments of b are consecutive
+// and the next sequence starts in the one where b ends or later), merged by
+// balanced_merge_kernel.
+#ifndef PA_DECODE_DEPTH
+#define PA_DECODE_DEPTH 3
+#endif
+template <typename TT, int D, bool CAP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void
+decode_balanced_kernel(const AttnParams p) {
+  // Workgroup = W wavefronts (one per SIMD of a CU) for W consecutive kv-heads of one segment:
+  // the kv-head slices of each page row are then fetched through one CU together, which the
+  // memory system serves measurably faster than the same slices fetched from W different CUs.
+  const int W = blockDim.x >> 6;
+  const int x = blockIdx.x * W + (threadIdx.x >> 6), seg = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int M = p.mix;
   const int64_t S = total_steps(p, lane);
   if (S <= 0) return;
-  const int64_t L = seg_len(S, nseg);
-  const int64_t gs = min(S, L * seg), ge = min(S, L * (seg + 1));
+  const int64_t L = seg_len(S, p.max_splits);
+  const int64_t u0 = (int64_t)seg * M;
+  const int64_t gs = min(S, L * u0), ge = min(S, L * (u0 + M));
   if (gs >= ge) return;
   int64_t carry = 0;
   for (int base = 0; base < p.batch && carry < ge; base += 64) {
-    int excl, chunk_total;
-    uint64_t mask;
-    {
-      const int n_l = seq_steps(p, base + lane).n;
-      const int incl = wave_incl_scan(n_l, lane);
-      excl = incl - n_l;
-      chunk_total = __shfl(incl, 63, 64);
-      const int64_t P = carry + excl;
-      mask = __ballot(n_l > 0 && P < ge && P + n_l > gs);
-    }
-    while (mask) {
-      // The chosen sequence is wave-uniform: its metadata comes from scalar loads, so only
-      // `excl` stays live in vector registers across the key loop.
-      const int li = __builtin_ctzll(mask);
-      mask &= mask - 1;
-      const int b = base + li;
-      const SeqSteps q = seq_steps(p, b);
-      const int64_t Pb = carry + __builtin_amdgcn_readlane(excl, li);
-      const int n = q.n;
-      const int a = (int)(max(gs, Pb) - Pb), e = (int)(min(ge, Pb + n) - Pb);
-      const int t_begin = q.first + 32 * a;
-      const int t_end = min(q.total, q.first + 32 * e);
-      const WaveInfo w = make_wave(p, D, b, kh, q.s0, q.pastb, q.total);
-      const int R = g * q.nq;  // <= 16 (host dispatch)
-      RowState<TT, D> rs;
-      init_rows<TT, D>(rs, p, w, 0, R, g, c, G);
-      run_range<TT, D, CAP, 3>(w, rs, t_begin, t_end, t_end, lane, c, G, p.scale_log2, p.scale,
-                            p.softcap);
-      const int f = (int)(Pb / L);
-      const int nparts = (int)((Pb + n - 1) / L) - f + 1;
-      const int64_t slot = (int64_t)seg + b;
-      store_rows<TT, D>(rs, p, w, 0, R, g, c, G, nparts == 1, [&](int64_t, int, int rloc) {
-        return (slot * p.kv_heads + kh) * 16 + rloc;
-      });
-    }
+    SeqWin sw;
+    sw.base = base;
+    sw.q = seq_steps(p, base + lane);
+    const int incl = wave_incl_scan(sw.q.n, lane);
+    sw.P = carry + (incl - sw.q.n);
+    const int chunk_total = __builtin_amdgcn_readlane(incl, 63);
+    const int64_t lo = max(gs, carry), hi = min(ge, carry + chunk_total);
+    if (lo < hi) stream_range<TT, D, CAP, PA_DECODE_DEPTH>(p, sw, lo, hi, L, x, u0, lane);
     carry += chunk_total;
   }
 }
@@ -638,12 +893,12 @@ balanced_merge_kernel(const AttnParams p) {
 }
 
 template <typename TT, int D>
-hipError_t launch_d(const AttnParams& p, dim3 grid, bool balanced, hipStream_t s) {
+hipError_t launch_d(const AttnParams& p, dim3 grid, dim3 block, bool balanced, hipStream_t s) {
   if (balanced) {
     if (p.softcap > 0.0f)
-      hipLaunchKernelGGL((decode_balanced_kernel<TT, D, true>), grid, dim3(64), 0, s, p);
+      hipLaunchKernelGGL((decode_balanced_kernel<TT, D, true>), grid, block, 0, s, p);
     else
-      hipLaunchKernelGGL((decode_balanced_kernel<TT, D, false>), grid, dim3(64), 0, s, p);
+      hipLaunchKernelGGL((decode_balanced_kernel<TT, D, false>), grid, block, 0, s, p);
   } else {
     if (p.softcap > 0.0f)
       hipLaunchKernelGGL((decode_chunked_kernel<TT, D, true>), grid, dim3(64), 0, s, p);
@@ -654,10 +909,10 @@ hipError_t launch_d(const AttnParams& p, dim3 grid, bool balanced, hipStream_t s
 }
 
 template <typename TT>
-hipError_t launch_t(const AttnParams& p, dim3 grid, bool balanced, hipStream_t s) {
+hipError_t launch_t(const AttnParams& p, dim3 grid, dim3 block, bool balanced, hipStream_t s) {
   switch (p.head_dim) {
-    case 64: return launch_d<TT, 64>(p, grid, balanced, s);
-    case 128: return launch_d<TT, 128>(p, grid, balanced, s);
+    case 64: return launch_d<TT, 64>(p, grid, block, balanced, s);
+    case 128: return launch_d<TT, 128>(p, grid, block, balanced, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -680,8 +935,8 @@ hipError_t launch_decode_mfma(const AttnParams& p, pa_dtype act, pa_dtype cache_
   const int row_groups =
       (int)std::min<int64_t>(((int64_t)g * mq + 15) / 16, (int64_t)(INT32_MAX / p.kv_heads));
   dim3 grid(p.kv_heads * row_groups, p.max_splits, p.batch);
-  if (act == PA_DTYPE_FLOAT16) return launch_t<TF16>(p, grid, false, s);
-  return launch_t<TBF16>(p, grid, false, s);
+  if (act == PA_DTYPE_FLOAT16) return launch_t<TF16>(p, grid, dim3(64), false, s);
+  return launch_t<TBF16>(p, grid, dim3(64), false, s);
 }
 
 // Balanced launch: p.max_splits holds the segment count; every sequence must have at most 16
@@ -690,10 +945,12 @@ hipError_t launch_decode_balanced(const AttnParams& p, pa_dtype act, pa_dtype ca
                                   hipStream_t s) {
   if (!decode_mfma_supported(p.head_dim, act, cache_dtype)) return hipErrorInvalidValue;
   if (p.batch <= 0) return hipSuccess;
-  dim3 grid(p.kv_heads, p.max_splits);
-  if (p.part_o == nullptr) return hipErrorInvalidValue;
-  hipError_t e = (act == PA_DTYPE_FLOAT16) ? launch_t<TF16>(p, grid, true, s)
-                                           : launch_t<TBF16>(p, grid, true, s);
+  if (p.part_o == nullptr || p.mix < 1 || p.mix > p.kv_heads || p.max_splits % p.mix != 0)
+    return hipErrorInvalidValue;
+  const int W = p.kv_heads % 4 == 0 ? 4 : p.kv_heads % 2 == 0 ? 2 : 1;
+  dim3 grid(p.kv_heads / W, p.max_splits / p.mix), block(64 * W);
+  hipError_t e = (act == PA_DTYPE_FLOAT16) ? launch_t<TF16>(p, grid, block, true, s)
+                                           : launch_t<TBF16>(p, grid, block, true, s);
   if (e != hipSuccess) return e;
   const dim3 mgrid(p.kv_heads, p.batch);
   const bool f16 = act == PA_DTYPE_FLOAT16;

@@ -238,6 +238,7 @@ struct AttnParams {
   // The append that ran before this call left every new key/value row in its cache slot
   // (block-table slots, no duplicates), so new positions may be read from the pages.
   int32_t new_rows_in_cache;
+  int32_t mix;  // balanced decode: sub-segments (each for another kv-head) per wavefront
 };
 
 // Final normalisation shared by every attention kernel: the factor that turns an output

@@ -58,6 +58,7 @@ class PaBatch(C.Structure):
 
 
 PA_BATCH_NEW_ROWS_IN_CACHE = 1
+PA_BATCH_SLOTS_DISTINCT = 2
 
 
 class PaAttn(C.Structure):

@@ -160,13 +160,16 @@ def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, key_cache: torch.T
                       value_cache: torch.Tensor, cum: torch.Tensor, past: torch.Tensor,
                       block_table: torch.Tensor, slot_mapping: torch.Tensor | None = None,
                       k_scale: torch.Tensor | None = None,
-                      v_scale: torch.Tensor | None = None) -> None:
+                      v_scale: torch.Tensor | None = None, slots_distinct: bool = False) -> None:
+    """Append key/value rows to the pages (last writer wins on shared slots unless the caller
+    asserts `slots_distinct`, which skips that check)."""
     lib = capi.load()
     for n, t in (("key", key), ("value", value), ("key_cache", key_cache)):
         _need_cuda(n, t)
         _contig(n, t)
     cache = cache_desc(key_cache, value_cache, k_scale, v_scale)
-    batch = batch_desc(cum, past, block_table, key.shape[0], slot_mapping)
+    batch = batch_desc(cum, past, block_table, key.shape[0], slot_mapping, 0,
+                       capi.PA_BATCH_SLOTS_DISTINCT if slots_distinct else 0)
     capi.check(lib.pa_reshape_and_cache(C.byref(cache), C.byref(batch), pa_dtype(key.dtype),
                                         _ptr(key), _ptr(value), _stream(key.device)))
 
@@ -174,11 +177,13 @@ def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, key_cache: torch.T
 def rotary_append(query, key, value, key_cache, value_cache, cum, past, block_table, *,
                   num_heads, cos_cache=None, sin_cache=None, rotary_offset=0,
                   rotary_interleaved=0, q_norm_weight=None, k_norm_weight=None,
-                  qk_norm_epsilon=1e-6, slot_mapping=None, k_scale=None, v_scale=None):
+                  qk_norm_epsilon=1e-6, slot_mapping=None, k_scale=None, v_scale=None,
+                  slots_distinct=False):
     """Fused RMSNorm + RoPE + append.  Returns the transformed (query, key) rows."""
     lib = capi.load()
     cache = cache_desc(key_cache, value_cache, k_scale, v_scale)
-    batch = batch_desc(cum, past, block_table, key.shape[0], slot_mapping)
+    batch = batch_desc(cum, past, block_table, key.shape[0], slot_mapping, 0,
+                       capi.PA_BATCH_SLOTS_DISTINCT if slots_distinct else 0)
     transform = cos_cache is not None or q_norm_weight is not None
     q_out = torch.empty_like(query) if transform else query
     k_out = torch.empty_like(key) if transform else key

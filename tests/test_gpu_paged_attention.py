@@ -4,7 +4,7 @@ Bars: cache bytes after append bit-exact; output
 rel-L2 <= 2e-3 (fp16/bf16) or <= 1e-5 (fp32).  For fp16/bf16 the output is compared with the
 oracle's output rounded to the activation dtype (the reference returns T), and additionally
 with the unrounded float64 result at twice the bar.  Geometries mirror the reference's
-tests/ops/test_paged_attention.py cases (cited per test) plus the BASELINE configs.
+tests/ops/test_paged_attention.py cases (cited per test) plus the BASELINE.json configs.
 """
 from __future__ import annotations
 
@@ -118,7 +118,7 @@ def test_duplicate_slots_known_answer():
     check(case)
 
 
-# test_paged_attention.py:663-666 (RoPE neox / gptj) + the BASELINE bf16 theta=500000 rotary
+# test_paged_attention.py:663-666 (RoPE neox / gptj) + the BASELINE.json bf16 theta=500000 rotary
 @pytest.mark.parametrize("interleaved", [0, 1], ids=["neox", "gptj"])
 @pytest.mark.parametrize("H,KV,d,dtype", [(4, 2, 16, F16), (2, 1, 64, F16), (32, 8, 128, BF16)])
 def test_rotary(interleaved, H, KV, d, dtype):
@@ -151,7 +151,7 @@ def test_softcap_and_sink(softcap, d):
                     head_sink=np.linspace(-1, 2, 8), std=1.0))
 
 
-# BASELINE config 1: GroupQueryAttention decode, fp32, B=1, 8q/2kv, d=64, past 128 + 1 new,
+# BASELINE.json config 1: GroupQueryAttention decode, fp32, B=1, 8q/2kv, d=64, past 128 + 1 new,
 # no rotary, scale 1/8 -- the GPU paged path on the equivalent pages must agree with the
 # contiguous-KV (ORT CPU semantics) restatement to rel-L2 <= 1e-5.
 def test_c1_gqa_fp32_against_contiguous():
@@ -192,7 +192,7 @@ def test_c1_gqa_fp32_against_contiguous():
     assert np.array_equal(kc_g[past // bs, past % bs], k.reshape(KV, d))
 
 
-# BASELINE config 3 geometry (Llama-3-8B decode), reduced batch for the oracle
+# BASELINE.json config 3 geometry (Llama-3-8B decode), reduced batch for the oracle
 @pytest.mark.parametrize("kind", [0, 3], ids=["auto", "generic"])
 def test_c3_geometry_reduced_batch(kind):
     rng = np.random.default_rng(3)
@@ -296,7 +296,7 @@ def test_large_batch(B, mixed):
                     max_blocks=mb, do_rotary=1, std=1.0))
 
 
-# BASELINE config 4 geometry (Qwen2.5-7B chunked prefill), reduced
+# BASELINE.json config 4 geometry (Qwen2.5-7B chunked prefill), reduced
 @pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "fp16"])
 def test_c4_prefill_reduced(dtype):
     rng = np.random.default_rng(4)
@@ -307,7 +307,7 @@ def test_c4_prefill_reduced(dtype):
                     past=past, max_blocks=mb, std=1.0))
 
 
-# BASELINE config 5 geometry (fp8 e4m3 pages, per-(block, kv-head) scales), reduced
+# BASELINE.json config 5 geometry (fp8 e4m3 pages, per-(block, kv-head) scales), reduced
 @pytest.mark.parametrize("ctx", [1, 300, 4096])
 def test_c5_fp8_reduced(ctx):
     bs = 16
