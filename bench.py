@@ -40,7 +40,19 @@ def parse():
     ap.add_argument("--cpu-sample", type=int, default=16, help="sequences in the CPU sample")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run 1 GiB device copies (known bytes) to scale HBM counters")
     return ap.parse_args()
+
+
+def load_traffic():
+    """HBM bytes per attention launch from the committed counter summary, if present."""
+    path = ROOT / "profiles" / "decode_c3_traffic.json"
+    if not path.exists():
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    return t.get("hbm_bytes_per_launch")
 
 
 def build_workload(torch, ep, seed):
@@ -209,6 +221,17 @@ def main():
     step = Step(torch, ep, w, args.chunk)
     kv_bytes = 4096.0 * float(w["ctx"].sum())
 
+    if args.calibrate_copy:
+        # Plain copies of exactly 1 GiB (read 1 GiB, write 1 GiB): the reference dispatches
+        # for scaling FETCH_SIZE / WRITE_SIZE counter readings to bytes.
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -265,7 +288,8 @@ def main():
         },
         "roofline": {
             "bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+            "unit": "GB/s", "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
+            "traffic": load_traffic(),
             "kernel": "pa_attention (decode_balanced_kernel + balanced_merge_kernel)",
             "us_per_launch": round(attn_ms * 1e3, 1),
         },

@@ -165,17 +165,18 @@ size_t pa_attention_workspace_bytes_ex(const pa_cache* cache, const pa_batch* ba
  * reference's _paged_ref and its patched Metal kernel do (attention.rs:4161-4190,
  * paged_attention.rs:46-74).  fp8 caches read every position from the pages (the quantised
  * rule of attention.rs:4192-4194).  q: [num_tokens, num_heads*head_dim]; out likewise.
- * Dispatch: decode kernel (split-K MFMA, one wavefront per (sequence, kv-head, chunk)) when
- * (num_heads/kv_heads) * max_query_len <= 16; chunked-prefill MFMA kernel otherwise;
- * fp32 activations use the VALU kernel. */
+ * Dispatch: fp16/bf16 with head_dim 64 or 128 run on matrix cores: the balanced (stream-K)
+ * decode kernel when (num_heads/kv_heads) * max_query_len <= 16 and the block size is a power
+ * of two, else the chunked split-K kernel in 16-row groups (multi-token prefill chunks);
+ * fp32 activations, other head sizes and fp8 pages use the VALU kernel. */
 int pa_attention(const pa_cache* cache, const pa_batch* batch, const pa_attn* attn,
                  pa_dtype act_dtype, const void* q, const void* k_new, const void* v_new,
                  void* out, void* workspace, size_t workspace_bytes, pa_stream_t stream);
 
 /* Same contract, forcing one kernel family (for parity tests and benchmarks).
  * kind: 0 = automatic, 1 = decode MFMA (balanced segments when every sequence has at most 16
- * grouped query rows, else chunked split-K), 2 = prefill (MFMA), 3 = generic VALU,
- * 4 = decode MFMA with chunked split-K forced.
+ * grouped query rows, else chunked split-K), 2 = dedicated prefill kernel (not in this build:
+ * returns PA_ERR_UNSUPPORTED), 3 = generic VALU, 4 = decode MFMA with chunked split-K forced.
  * chunk_tokens: split-K chunk for the chunked/generic kernels (multiple of 32; 0 = automatic). */
 int pa_attention_ex(const pa_cache* cache, const pa_batch* batch, const pa_attn* attn,
                     pa_dtype act_dtype, const void* q, const void* k_new, const void* v_new,
