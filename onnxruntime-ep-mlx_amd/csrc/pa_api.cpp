@@ -132,8 +132,12 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
   const int g = a->num_heads / c->kv_heads;
   const int mq = b->max_query_len > 0 ? b->max_query_len : std::max(b->num_tokens, 1);
   const bool mfma = pa::decode_mfma_supported(c->head_dim, act, c->dtype);
+  // The balanced (streaming) decode addresses rows with 32-bit row indices and shifts.
+  const bool bal_ok = (int64_t)g * mq <= 16 &&
+                      pa::balanced_supported(c->head_dim, act, c->dtype, c->block_size) &&
+                      (int64_t)c->num_blocks * c->block_size <= (int64_t)UINT32_MAX;
   if (kind == 0) {
-    if (mfma && (int64_t)g * mq <= 16)
+    if (bal_ok || (mfma && (int64_t)g * mq <= 16))
       kind = 1;
     else if (pa::prefill_mfma_supported(c->head_dim, act, c->dtype))
       kind = 2;
@@ -143,10 +147,7 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
       kind = 3;
   }
   pl.kind = kind;
-  // The balanced (streaming) decode addresses rows with 32-bit row indices and shifts.
-  const bool pow2_bs = (c->block_size & (c->block_size - 1)) == 0;
-  pl.balanced = kind == 1 && (int64_t)g * mq <= 16 && pow2_bs &&
-                (int64_t)c->num_blocks * c->block_size <= (int64_t)UINT32_MAX;
+  pl.balanced = kind == 1 && bal_ok;
   if (kind == 4) pl.kind = 1;
   const int ctx = std::max(max_ctx_bound(c, b), 1);
   if (pl.balanced) {
@@ -204,8 +205,15 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
       (!vn && c->dtype != PA_DTYPE_FP8_E4M3))
     return fail(PA_ERR_INVALID_ARGUMENT, "q/k_new/v_new/out pointers are NULL");
   if (kind < 0 || kind > 4) return fail(PA_ERR_INVALID_ARGUMENT, "unknown kernel kind %d", kind);
-  if ((kind == 1 || kind == 4) && !pa::decode_mfma_supported(c->head_dim, act, c->dtype))
+  if (kind == 4 && !pa::decode_mfma_supported(c->head_dim, act, c->dtype))
     return fail(PA_ERR_UNSUPPORTED, "decode MFMA kernel does not cover this dtype/head_dim");
+  if (kind == 1 && !pa::decode_mfma_supported(c->head_dim, act, c->dtype)) {
+    const int g = a->num_heads / c->kv_heads;
+    const int mq = b->max_query_len > 0 ? b->max_query_len : std::max(b->num_tokens, 1);
+    if (!((int64_t)g * mq <= 16 &&
+          pa::balanced_supported(c->head_dim, act, c->dtype, c->block_size)))
+      return fail(PA_ERR_UNSUPPORTED, "decode MFMA kernel does not cover this dtype/head_dim");
+  }
   if (kind == 2 && !pa::prefill_mfma_supported(c->head_dim, act, c->dtype))
     return fail(PA_ERR_UNSUPPORTED, "prefill MFMA kernel does not cover this dtype/head_dim");
   if (!(a->softcap >= 0.0f) || !std::isfinite(a->softcap))

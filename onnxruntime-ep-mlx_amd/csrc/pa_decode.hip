@@ -35,6 +35,7 @@
 // Split-K: each chunk writes (m, l, O) partials; pa_attn_generic.hip's reduce merges them.  A
 // sequence that fits one chunk writes its final rows directly.
 #include <algorithm>
+#include <type_traits>
 
 #include "pa_device.hpp"
 
@@ -74,6 +75,72 @@ struct Step {
   u32x4 k[2][D / 32];  // tile A / tile B key rows, 8 dims per k-step
   VRow<D> v[8];        // value rows: keys 4G+e of tile A (e<4) and of tile B (e>=4)
 };
+
+// fp8 (e4m3) pages: the same rows as loaded, one byte per element.  Key chunk h of a lane holds
+// dims 64h + 16G .. +15 (k-steps 2h and 2h+1); value row e holds the lane's D/16 dims.
+template <int D>
+struct RawV8;
+template <>
+struct RawV8<64> {
+  uint32_t w;
+};
+template <>
+struct RawV8<128> {
+  u32x2 w;
+};
+template <int D>
+struct Step8 {
+  u32x4 k[2][D / 64];
+  RawV8<D> v[8];
+  float sc;  // lane l: scale of (l & 2 ? value : key) page of tile (l & 1)
+};
+
+// Four e4m3 codes -> four bf16 (exact: every e4m3 value is a bf16 value) as two packed words:
+// v_cvt_f32_fp8 per byte (gfx950 decodes OCP e4m3 exactly, all 256 codes checked), then the
+// high halves packed with v_perm.  The two-element v_cvt_pk_f32_fp8 form is avoided: this
+// compiler folds its second result into the first when the results are repacked.
+// For fp16 activations the same values are packed as fp16 (also exact: |x| <= 448, and the
+// e4m3 subnormals are fp16 normals), so the MFMA operands match the query's type.
+template <typename TT>
+__device__ __forceinline__ u32x2 e4m3x4_widen(uint32_t w) {
+  const float fa = __builtin_amdgcn_cvt_f32_fp8((int)w, 0);
+  const float fb = __builtin_amdgcn_cvt_f32_fp8((int)w, 1);
+  const float fc = __builtin_amdgcn_cvt_f32_fp8((int)w, 2);
+  const float fd = __builtin_amdgcn_cvt_f32_fp8((int)w, 3);
+  if constexpr (TT::code == PA_DTYPE_FLOAT16) {
+    return u32x2{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(fa, fb)),
+                 __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(fc, fd))};
+  } else {
+    const uint32_t a = __builtin_bit_cast(uint32_t, fa), b = __builtin_bit_cast(uint32_t, fb);
+    const uint32_t c = __builtin_bit_cast(uint32_t, fc), d = __builtin_bit_cast(uint32_t, fd);
+    return u32x2{__builtin_amdgcn_perm(b, a, 0x07060302u), __builtin_amdgcn_perm(d, c, 0x07060302u)};
+  }
+}
+
+template <typename TT, int D>
+__device__ __forceinline__ Step<D> widen_step(const Step8<D>& r) {
+  Step<D> o;
+#pragma unroll
+  for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+    for (int h = 0; h < D / 64; ++h)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const u32x2 a = e4m3x4_widen<TT>(r.k[tile][h][2 * t]);
+        const u32x2 b = e4m3x4_widen<TT>(r.k[tile][h][2 * t + 1]);
+        o.k[tile][2 * h + t] = u32x4{a[0], a[1], b[0], b[1]};
+      }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    if constexpr (D == 128) {
+      const u32x2 a = e4m3x4_widen<TT>(r.v[e].w[0]), b = e4m3x4_widen<TT>(r.v[e].w[1]);
+      o.v[e].w = u32x4{a[0], a[1], b[0], b[1]};
+    } else {
+      o.v[e].w = e4m3x4_widen<TT>(r.v[e].w);
+    }
+  }
+  return o;
+}
 
 // Wave-uniform description of the (sequence, kv-head, chunk) being processed.
 struct WaveInfo {
@@ -170,10 +237,13 @@ struct RowState {
   int vis_lo, vis_hi;
 };
 
-template <typename TT, int D, bool CAP>
+// SC: fp8 pages, whose key codes score as ks * (q . code) and whose value codes weigh in as
+// vs * code; ks/vs are the page scales of tile A (keys t0..t0+15) and tile B.
+template <typename TT, int D, bool CAP, bool SC = false>
 __device__ __forceinline__ void compute_step(RowState<TT, D>& rs, const Step<D>& st, int t0,
                                              int end, int G, float scale_log2, float scale,
-                                             float cap) {
+                                             float cap, float ksA = 1.f, float ksB = 1.f,
+                                             float vsA = 1.f, float vsB = 1.f) {
   using vec8 = typename TT::vec8;
   constexpr int KS = D / 32, DL = D / 16;
   f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
@@ -181,6 +251,10 @@ __device__ __forceinline__ void compute_step(RowState<TT, D>& rs, const Step<D>&
   for (int s = 0; s < KS; ++s) {
     sa = TT::mfma(__builtin_bit_cast(vec8, st.k[0][s]), rs.qv[s], sa);
     sb = TT::mfma(__builtin_bit_cast(vec8, st.k[1][s]), rs.qv[s], sb);
+  }
+  if constexpr (SC) {
+    sa *= ksA;
+    sb *= ksB;
   }
   float x[8];
   float lmax = kNegInf;
@@ -218,6 +292,10 @@ __device__ __forceinline__ void compute_step(RowState<TT, D>& rs, const Step<D>&
   for (int e = 0; e < 8; ++e) {
     pv[e] = exp2f(x[e] - msafe);
     rs.l_part += pv[e];
+  }
+  if constexpr (SC) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pv[e] *= (e < 4) ? vsA : vsB;  // l_part keeps the unscaled sum
   }
   const vec8 phi = TT::cvt8(pv);
 #pragma unroll
@@ -656,11 +734,52 @@ __device__ __forceinline__ const char* stream_row(const AttnParams& p, const Ste
 // (sequence, kv-head).  Straight-line code, so every iteration issues the same loads and the
 // compiler's vmcnt waits only drain the step about to be computed.  Rows past the sequence end
 // re-read the last row.
-template <typename TT, int D>
-__device__ __forceinline__ void load_stream_step(const AttnParams& p, const StepAt& s, int btl,
-                                                 int lane, int g, int bs_shift, Step<D>& st,
-                                                 u32x4 (&qv)[D / 32], typename TT::raw& sk) {
+template <typename TT, int D, bool F8>
+using RingStep = typename std::conditional<F8, Step8<D>, Step<D>>::type;
+
+// fp8 pages (every row in the pages, block size a multiple of 16): per tile D/64 16-byte key
+// chunks (dims 64h + 16G ..) and four D/16-byte value rows per lane, plus the page scales.
+template <int D>
+__device__ __forceinline__ void load_step8(const AttnParams& p, const StepAt& s, int btl, int lane,
+                                           int bs_shift, Step8<D>& st) {
   const int c = lane & 15, G = lane >> 4;
+  const uint32_t rowb = (uint32_t)p.kv_heads * D;
+  const uint32_t hoff = (uint32_t)s.kh * D;
+  const char* kc = reinterpret_cast<const char*>(p.key_cache);
+  const char* vc = reinterpret_cast<const char*>(p.value_cache);
+  int64_t blk[2];
+#pragma unroll
+  for (int tile = 0; tile < 2; ++tile) {
+    const int tp = s.t + 16 * tile;
+    blk[tile] = min(max((int64_t)__builtin_amdgcn_readlane(btl, 16 * tile), (int64_t)0),
+                    (int64_t)p.num_blocks - 1);
+    const uint64_t row0 = (uint64_t)((blk[tile] << bs_shift) + (tp & (p.block_size - 1)));
+    const char* kb = kc + row0 * rowb + hoff;
+    const char* vb = vc + row0 * rowb + hoff;
+#pragma unroll
+    for (int h = 0; h < D / 64; ++h) st.k[tile][h] = ld16(kb + c * rowb + 16 * G + 64 * h);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const char* vr = vb + (4 * G + e) * rowb + (D / 16) * c;
+      if constexpr (D == 128)
+        st.v[4 * tile + e].w = *reinterpret_cast<const u32x2*>(vr);
+      else
+        st.v[4 * tile + e].w = *reinterpret_cast<const uint32_t*>(vr);
+    }
+  }
+  const float* sp = (lane & 2) ? p.v_scale : p.k_scale;
+  st.sc = sp[((lane & 1) ? blk[1] : blk[0]) * p.kv_heads + s.kh];
+}
+
+template <typename TT, int D, bool F8>
+__device__ __forceinline__ void load_stream_step(const AttnParams& p, const StepAt& s, int btl,
+                                                 int lane, int g, int bs_shift,
+                                                 RingStep<TT, D, F8>& st, u32x4 (&qv)[D / 32],
+                                                 typename TT::raw& sk) {
+  const int c = lane & 15, G = lane >> 4;
+  if constexpr (F8) {
+    load_step8<D>(p, s, btl, lane, bs_shift, st);
+  } else {
   constexpr int DL = D / 16;
   const uint32_t rowb = (uint32_t)p.kv_heads * D * 2;
   const uint32_t hoff = (uint32_t)s.kh * D * 2;
@@ -700,13 +819,18 @@ __device__ __forceinline__ void load_stream_step(const AttnParams& p, const Step
       }
     }
   }
+  }
   // Query rows of this (sequence, kv-head): MFMA column c is row r = c (rows past R repeat the
-  // last one; their scores are masked).
+  // last one; their scores are masked).  k-step q covers dims 32q + 8G .. (bf16 pages) or
+  // 64(q/2) + 16G + 8(q%2) .. (fp8 pages, matching the key chunks).
   const int r = min(c, g * s.nq - 1);
   const char* qrow = reinterpret_cast<const char*>(p.q) +
-                     (((int64_t)(s.s0 + r / g) * p.num_heads + s.kh * g + r % g) * D + 8 * G) * 2;
+                     ((int64_t)(s.s0 + r / g) * p.num_heads + s.kh * g + r % g) * D * 2;
 #pragma unroll
-  for (int q = 0; q < D / 32; ++q) qv[q] = ld16(qrow + 64 * q);
+  for (int q = 0; q < D / 32; ++q) {
+    const int dim0 = F8 ? 64 * (q >> 1) + 16 * G + 8 * (q & 1) : 32 * q + 8 * G;
+    qv[q] = ld16(qrow + 2 * dim0);
+  }
   // Sink logit input of that row's head (a harmless read of the query when there is none).
   const typename TT::raw* sp = p.head_sink ? reinterpret_cast<const typename TT::raw*>(p.head_sink)
                                            : reinterpret_cast<const typename TT::raw*>(p.q);
@@ -718,7 +842,7 @@ __device__ __forceinline__ void load_stream_step(const AttnParams& p, const Step
 // compute, key/value/query rows two steps ahead, so a sequence or kv-head boundary costs no
 // pipeline refill.  A piece (one sequence, one sub-segment) is finished when the compute cursor
 // leaves it: final rows when the piece covers its whole sequence, else a partial at slot u + b.
-template <typename TT, int D, bool CAP, int DEPTH>
+template <typename TT, int D, bool CAP, bool F8, int DEPTH>
 __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& sw, int64_t lo,
                                              int64_t hi, int64_t L, int x, int64_t u0,
                                              int lane) {
@@ -730,7 +854,7 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
 
   Cursor cc = cursor_at(sw, lo, L);
   Cursor cd = cc, cb = cc;
-  Step<D> st[DEPTH];
+  RingStep<TT, D, F8> st[DEPTH];
   u32x4 qr[DEPTH][D / 32];
   typename TT::raw skr[DEPTH];
   int btr[DEPTH];
@@ -742,8 +866,8 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
   }
 #pragma unroll
   for (int j = 0; j < DEPTH - 1; ++j) {
-    load_stream_step<TT, D>(p, step_at(cd, sw, p, x, u0), btr[j], lane, g, bs_shift, st[j], qr[j],
-                            skr[j]);
+    load_stream_step<TT, D, F8>(p, step_at(cd, sw, p, x, u0), btr[j], lane, g, bs_shift, st[j],
+                                qr[j], skr[j]);
     cursor_next(cd, sw, hi, L);
   }
 #pragma unroll
@@ -771,8 +895,8 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
       // Rows of step k+i+DEPTH-1 (block ids fetched DEPTH-1 iterations ago), then the block ids
       // of step k+i+2*(DEPTH-1).
       const int sd_slot = (i + DEPTH - 1) % DEPTH, sb_slot = (i + DEPTH - 2) % DEPTH;
-      load_stream_step<TT, D>(p, step_at(cd, sw, p, x, u0), btr[sd_slot], lane, g, bs_shift,
-                              st[sd_slot], qr[sd_slot], skr[sd_slot]);
+      load_stream_step<TT, D, F8>(p, step_at(cd, sw, p, x, u0), btr[sd_slot], lane, g, bs_shift,
+                                  st[sd_slot], qr[sd_slot], skr[sd_slot]);
       cursor_next(cd, sw, hi, L);
       btr[sb_slot] = load_step_blocks(p, step_at(cb, sw, p, x, u0), lane, bs_shift);
       cursor_next(cb, sw, hi, L);
@@ -798,16 +922,31 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
           rs.l_part = 0.0f;
         }
         const int t0 = pc_first + 32 * (int)(cc.f - pc.P);
-        Step<D>& cur = st[i];
-        if (t0 + 32 > pc.total) {
-          // Value rows past the sequence end (re-read rows) take no part, even if non-finite.
+        auto run = [&](Step<D>& cur, float ksA, float ksB, float vsA, float vsB) {
+          if (t0 + 32 > pc.total) {
+            // Value rows past the sequence end (re-read rows) take no part, even if not finite.
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int pos = t0 + 16 * (e >> 2) + 4 * G + (e & 3);
-            if (pos >= pc.total) cur.v[e] = VRow<D>{};
+            for (int e = 0; e < 8; ++e) {
+              const int pos = t0 + 16 * (e >> 2) + 4 * G + (e & 3);
+              if (pos >= pc.total) cur.v[e] = VRow<D>{};
+            }
           }
+          compute_step<TT, D, CAP, F8>(rs, cur, t0, pc.total, G, p.scale_log2, p.scale, p.softcap,
+                                       ksA, ksB, vsA, vsB);
+        };
+        if constexpr (F8) {
+          // Page scales of tiles A and B (lanes 0..3); a tile wholly past the end weighs zero
+          // (its page id, and so its scale, is not a real one).
+          const int sc = __builtin_bit_cast(int, st[i].sc);
+          const bool b_live = t0 + 16 < pc.total;
+          Step<D> wide = widen_step<TT, D>(st[i]);
+          run(wide, __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc, 0)),
+              b_live ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc, 1)) : 0.f,
+              __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc, 2)),
+              b_live ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc, 3)) : 0.f);
+        } else {
+          run(st[i], 1.f, 1.f, 1.f, 1.f);
         }
-        compute_step<TT, D, CAP>(rs, cur, t0, pc.total, G, p.scale_log2, p.scale, p.softcap);
         cursor_next(cc, sw, hi, L);
       }
     }
@@ -829,7 +968,7 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
 #ifndef PA_DECODE_DEPTH
 #define PA_DECODE_DEPTH 3
 #endif
-template <typename TT, int D, bool CAP>
+template <typename TT, int D, bool CAP, bool F8>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 decode_balanced_kernel(const AttnParams p) {
   // Workgroup = W wavefronts (one per SIMD of a CU) for W consecutive kv-heads of one segment:
@@ -854,7 +993,7 @@ decode_balanced_kernel(const AttnParams p) {
     sw.P = carry + (incl - sw.q.n);
     const int chunk_total = __builtin_amdgcn_readlane(incl, 63);
     const int64_t lo = max(gs, carry), hi = min(ge, carry + chunk_total);
-    if (lo < hi) stream_range<TT, D, CAP, PA_DECODE_DEPTH>(p, sw, lo, hi, L, x, u0, lane);
+    if (lo < hi) stream_range<TT, D, CAP, F8, PA_DECODE_DEPTH>(p, sw, lo, hi, L, x, u0, lane);
     carry += chunk_total;
   }
 }
@@ -895,10 +1034,14 @@ balanced_merge_kernel(const AttnParams p) {
 template <typename TT, int D>
 hipError_t launch_d(const AttnParams& p, dim3 grid, dim3 block, bool balanced, hipStream_t s) {
   if (balanced) {
-    if (p.softcap > 0.0f)
-      hipLaunchKernelGGL((decode_balanced_kernel<TT, D, true>), grid, block, 0, s, p);
-    else
-      hipLaunchKernelGGL((decode_balanced_kernel<TT, D, false>), grid, block, 0, s, p);
+    const bool f8 = p.read_all_from_cache != 0;  // fp8 pages (host dispatch)
+    if (p.softcap > 0.0f) {
+      if (f8) hipLaunchKernelGGL((decode_balanced_kernel<TT, D, true, true>), grid, block, 0, s, p);
+      else hipLaunchKernelGGL((decode_balanced_kernel<TT, D, true, false>), grid, block, 0, s, p);
+    } else {
+      if (f8) hipLaunchKernelGGL((decode_balanced_kernel<TT, D, false, true>), grid, block, 0, s, p);
+      else hipLaunchKernelGGL((decode_balanced_kernel<TT, D, false, false>), grid, block, 0, s, p);
+    }
   } else {
     if (p.softcap > 0.0f)
       hipLaunchKernelGGL((decode_chunked_kernel<TT, D, true>), grid, dim3(64), 0, s, p);
@@ -918,6 +1061,14 @@ hipError_t launch_t(const AttnParams& p, dim3 grid, dim3 block, bool balanced, h
 }
 
 }  // namespace
+
+bool balanced_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype, int block_size) {
+  if (act != PA_DTYPE_FLOAT16 && act != PA_DTYPE_BFLOAT16) return false;
+  if (head_dim != 64 && head_dim != 128) return false;
+  if (block_size <= 0 || (block_size & (block_size - 1)) != 0) return false;
+  if (cache_dtype == act) return true;
+  return cache_dtype == PA_DTYPE_FP8_E4M3 && block_size >= 16;
+}
 
 bool decode_mfma_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype) {
   if (act != PA_DTYPE_FLOAT16 && act != PA_DTYPE_BFLOAT16) return false;
@@ -943,7 +1094,10 @@ hipError_t launch_decode_mfma(const AttnParams& p, pa_dtype act, pa_dtype cache_
 // grouped query rows (g * query length <= 16).  Launches the decode and the partial merge.
 hipError_t launch_decode_balanced(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
                                   hipStream_t s) {
-  if (!decode_mfma_supported(p.head_dim, act, cache_dtype)) return hipErrorInvalidValue;
+  if (!balanced_supported(p.head_dim, act, cache_dtype, p.block_size)) return hipErrorInvalidValue;
+  if ((cache_dtype == PA_DTYPE_FP8_E4M3) != (p.read_all_from_cache != 0)) return hipErrorInvalidValue;
+  if (cache_dtype == PA_DTYPE_FP8_E4M3 && (p.k_scale == nullptr || p.v_scale == nullptr))
+    return hipErrorInvalidValue;
   if (p.batch <= 0) return hipSuccess;
   if (p.part_o == nullptr || p.mix < 1 || p.mix > p.kv_heads || p.max_splits % p.mix != 0)
     return hipErrorInvalidValue;

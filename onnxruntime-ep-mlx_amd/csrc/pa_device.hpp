@@ -271,6 +271,9 @@ hipError_t launch_prefill_mfma(const AttnParams& p, pa_dtype act, pa_dtype cache
                                hipStream_t s);
 hipError_t launch_split_reduce(const AttnParams& p, pa_dtype act, hipStream_t s);
 bool decode_mfma_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype);
+// Balanced (streaming) decode: fp16/bf16 activations, d in {64, 128}, power-of-two pages,
+// pages in the activation dtype or fp8 e4m3 (then at least 16 rows per page).
+bool balanced_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype, int block_size);
 bool prefill_mfma_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype);
 
 }  // namespace pa

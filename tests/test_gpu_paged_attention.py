@@ -314,3 +314,47 @@ def test_c5_fp8_reduced(ctx):
     mb = (ctx + bs - 1) // bs
     check(make_case(64, 8, 128, 2 * mb + 2, bs, 2, dtype=BF16, cache_dtype=E4M3, seed=5,
                     new_lens=[1, 1], past=[ctx - 1, max(ctx - 5, 0)], max_blocks=mb, std=1.0))
+
+
+# fp8 pages on the matrix-core decode: both activation dtypes, d 64/128, softcap, two-token
+# queries (g * nq <= 16), page sizes 8 (VALU fallback), 16 and 32, many-way split sequences
+@pytest.mark.parametrize("dtype,d,bs,softcap,nq", [
+    (BF16, 128, 16, 0.0, 1), (F16, 128, 16, 0.0, 1), (BF16, 64, 16, 0.0, 1),
+    (BF16, 128, 32, 0.0, 1), (BF16, 128, 8, 0.0, 1), (BF16, 128, 16, 30.0, 1),
+    (F16, 128, 16, 0.0, 2)])
+def test_fp8_pages_decode(dtype, d, bs, softcap, nq):
+    rng = np.random.default_rng(d + bs + nq)
+    B = 5
+    ctx = rng.integers(40, 1500, size=B)
+    mb = int((ctx.max() + bs - 1) // bs)
+    check(make_case(16, 4, d, B * mb + 3, bs, B, dtype=dtype, cache_dtype=E4M3,
+                    seed=int(ctx.sum()), new_lens=[nq] * B, past=ctx - nq, max_blocks=mb,
+                    std=1.0, softcap=softcap))
+
+
+# fp8 decode at BASELINE.json config 5's per-sequence shape (64 q / 8 kv heads, 32768 keys),
+# two sequences: the fp8 streaming kernel against the VALU kernel on identical pages, plus the
+# oracle on one sequence
+def test_fp8_long_context_matches_valu():
+    import torch
+    import onnxruntime_ep_mlx_amd as ep
+    from pa_cases import to_torch, from_torch
+    bs, ctx, B = 16, 32768, 2
+    mb = ctx // bs
+    case = make_case(64, 8, 128, B * mb + 2, bs, B, dtype=BF16, cache_dtype=E4M3, seed=55,
+                     new_lens=[1] * B, past=[ctx - 1, ctx - 1001], max_blocks=mb, std=1.0)
+    ref, ref_t, kc_ref, vc_ref = orc.paged_attention_op(case)
+    t = {n: to_torch(case[n], BF16) for n in ("query", "key", "value")}
+    kc, vc = to_torch(case["key_cache"], E4M3), to_torch(case["value_cache"], E4M3)
+    ks, vs = (torch.from_numpy(case[n]).cuda() for n in ("k_scale", "v_scale"))
+    I = {n: torch.from_numpy(case[n]).cuda() for n in ("cum", "past", "block_table")}
+    ep.reshape_and_cache(t["key"], t["value"], kc, vc, I["cum"], I["past"], I["block_table"],
+                         k_scale=ks, v_scale=vs)
+    outs = [ep.attention(t["query"], t["key"], t["value"], kc, vc, I["cum"], I["past"],
+                         I["block_table"], num_heads=64, max_query_len=1, kind=kind,
+                         k_scale=ks, v_scale=vs) for kind in (1, 3)]
+    torch.cuda.synchronize()
+    assert np.array_equal(from_torch(kc, E4M3), kc_ref)
+    g1, g3 = (orc.decode(from_torch(o, BF16), BF16).astype(np.float64) for o in outs)
+    assert orc.rel_l2(g1, orc.decode(ref_t, BF16)) <= 2e-3
+    assert orc.rel_l2(g1, g3) <= 2e-3
