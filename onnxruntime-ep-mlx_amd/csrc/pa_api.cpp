@@ -104,6 +104,7 @@ struct Plan {
   int chunk;
   int max_splits;    // chunk count (chunked/generic) or sub-segment count (balanced)
   int mix;           // balanced: sub-segments per wavefront
+  int ng;            // chunked MFMA kernel: 16-row groups per wavefront
   size_t part_rows;  // rows of fp32 partials in the workspace
 };
 
@@ -158,19 +159,33 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
     pl.part_rows = (size_t)(pl.max_splits + b->batch) * c->kv_heads * 16;
     return pl;
   }
+  // Chunked MFMA kernel: several 16-row groups per wavefront once a sequence has >= 64 grouped
+  // query rows (prefill chunks), so each loaded key/value step serves more rows (4 groups at
+  // d=64, 2 at d=128: what fits the register file).
+  pl.ng = (pl.kind == 1 && (int64_t)g * mq >= 64) ? (c->head_dim == 64 ? 4 : 2) : 1;
   if (chunk <= 0) {
     if (kind == 2) {
       chunk = 1 << 30;  // prefill kernel walks the whole context
     } else {
-      // Aim for >= ~4096 work units (16 per CU) over the (sequence, kv-head) pairs.
-      int64_t pairs = (int64_t)b->batch * c->kv_heads;
-      int64_t splits = std::max<int64_t>(1, (4096 + pairs - 1) / pairs);
-      int64_t ch = (ctx + splits - 1) / splits;
-      ch = ((ch + 31) / 32) * 32;
-      chunk = (int)std::min<int64_t>(std::max<int64_t>(ch, 256), 1024);
+      // Work units without split-K: (sequence, kv-head, row groups) for the MFMA kernel,
+      // (token, head) for the VALU kernel.  Split the context only when they cannot fill the
+      // GPU (~2048 one-per-SIMD wavefronts for NG = 4, ~4096 otherwise).
+      const int64_t rows_pw = 16 * pl.ng;
+      const int64_t units =
+          pl.kind == 1 ? (int64_t)b->batch * c->kv_heads * (((int64_t)g * mq + rows_pw - 1) / rows_pw)
+                       : (int64_t)std::max(b->num_tokens, 1) * a->num_heads;
+      const int64_t target = pl.ng > 1 ? 2048 : 4096;
+      if (units >= target) {
+        chunk = (int)std::min<int64_t>(((int64_t)ctx + 31) / 32 * 32, INT32_MAX / 2);
+      } else {
+        const int64_t splits = (target + units - 1) / units;
+        int64_t ch = (ctx + splits - 1) / splits;
+        ch = ((ch + 31) / 32) * 32;
+        chunk = (int)std::min<int64_t>(std::max<int64_t>(ch, 256), 1024);
+      }
     }
   }
-  if (pl.kind != 2) chunk = std::max(32, std::min(chunk, 1024) / 32 * 32);
+  if (pl.kind != 2) chunk = std::max(32, chunk / 32 * 32);
   pl.chunk = chunk;
   pl.max_splits = (int)std::max<int64_t>(1, ((int64_t)ctx + chunk - 1) / chunk);
   pl.part_rows = pl.max_splits > 1
@@ -252,6 +267,7 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
   p.chunk = pl.chunk;
   p.max_splits = pl.max_splits;
   p.mix = pl.mix;
+  p.ng = pl.ng > 0 ? pl.ng : 1;
   p.max_query_len = b->max_query_len > 0 ? b->max_query_len : b->num_tokens;
   p.scale = a->scale != 0.0f ? a->scale : 1.0f / std::sqrt((float)c->head_dim);
   p.scale_log2 = p.scale * pa::kLog2e;

@@ -311,8 +311,19 @@ __device__ __forceinline__ void compute_step(RowState<TT, D>& rs, const Step<D>&
 
 // ----------------------------------------------------------------------------- shared driver
 
-// Walk keys [t_begin, t_last) for one (sequence, kv-head) with the rows in `rs`; t_begin is a
-// multiple of 32.  Steps entirely inside cached pages go through the pipelined fast loop in
+// Zero this lane's value rows of a step that lie at or past `total` (rows re-read past the
+// sequence end take no part even if their bytes are not finite).
+template <int D>
+__device__ __forceinline__ void clear_tail_rows(Step<D>& st, int t0, int total, int G) {
+  if (t0 + 32 <= total) return;
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (t0 + 16 * (e >> 2) + 4 * G + (e & 3) >= total) st.v[e] = VRow<D>{};
+}
+
+// Walk keys [t_begin, t_last) for one (sequence, kv-head) with NG 16-row groups `rs`; t_begin
+// is a multiple of 32.  Every loaded step serves all NG groups (NG x fewer key/value reads per
+// query row).  Steps entirely inside cached pages go through the pipelined fast loop in
 // sub-ranges of at most 1024 keys (one block-table entry per lane covers a sub-range); the rest
 // take the per-lane addressed path.  `end` masks keys at or beyond it.
 //
@@ -320,8 +331,8 @@ __device__ __forceinline__ void compute_step(RowState<TT, D>& rs, const Step<D>&
 // computes.  Loads are always issued (past the last step they re-read the last step, which the
 // caches serve), so every path through an iteration issues the same loads and the compiler's
 // vmcnt waits only drain the step about to be computed.
-template <typename TT, int D, bool CAP, int DEPTH>
-__device__ __forceinline__ void run_range(WaveInfo w, RowState<TT, D>& rs, int t_begin,
+template <typename TT, int D, bool CAP, int DEPTH, int NG>
+__device__ __forceinline__ void run_range(WaveInfo w, RowState<TT, D> (&rs)[NG], int t_begin,
                                           int t_last, int end, int lane, int c, int G,
                                           float scale_log2, float scale, float cap) {
   static_assert(DEPTH == 2 || DEPTH == 3, "pipeline depth");
@@ -348,8 +359,13 @@ __device__ __forceinline__ void run_range(WaveInfo w, RowState<TT, D>& rs, int t
       for (int i = 0; i < DEPTH; ++i) {
         load_fast<D>(w, btv, koff, voff, min(t0 + 32 * (k + i + DEPTH - 1), last),
                      ring[(i + DEPTH - 1) % DEPTH]);
-        if (k + i < nfast)
-          compute_step<TT, D, CAP>(rs, ring[i], t0 + 32 * (k + i), end, G, scale_log2, scale, cap);
+        if (k + i < nfast) {
+          const int ts = t0 + 32 * (k + i);
+          clear_tail_rows<D>(ring[i], ts, w.total, G);
+#pragma unroll
+          for (int j = 0; j < NG; ++j)
+            compute_step<TT, D, CAP>(rs[j], ring[i], ts, end, G, scale_log2, scale, cap);
+        }
       }
     }
     t0 += 32 * nfast;
@@ -357,7 +373,9 @@ __device__ __forceinline__ void run_range(WaveInfo w, RowState<TT, D>& rs, int t
   Step<D>& sA = ring[0];
   for (; t0 < t_last; t0 += 32) {
     load_edge<D>(w, c, G, t0, sA);
-    compute_step<TT, D, CAP>(rs, sA, t0, end, G, scale_log2, scale, cap);
+#pragma unroll
+    for (int j = 0; j < NG; ++j)
+      compute_step<TT, D, CAP>(rs[j], sA, t0, end, G, scale_log2, scale, cap);
   }
 }
 
@@ -461,12 +479,13 @@ __device__ __forceinline__ void store_rows(const RowState<TT, D>& rs, const Attn
 }
 
 // ----------------------------------------------------------------------------- chunked kernel
-// One wavefront per (context chunk, kv-head, 16-row group, sequence); kv-head fastest in the
+// One wavefront per (context chunk, kv-head, NG 16-row groups, sequence); kv-head fastest in the
 // grid so the wavefronts reading the same pages run together.  Used when a sequence has more
-// than 16 grouped query rows (multi-token queries); partials at (token, head, chunk).
-// Two wavefronts per SIMD: the pipelined d=128 loop fits in 256 registers without spilling.
-template <typename TT, int D, bool CAP>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+// than 16 grouped query rows (multi-token queries, chunked prefill); partials at (token, head,
+// chunk).  NG = 1: two wavefronts per SIMD (the d=128 ring fits 256 registers).  NG > 1
+// (prefill): every loaded key/value step serves 16 * NG query rows, one wavefront per SIMD.
+template <typename TT, int D, bool CAP, int NG>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NG == 1 ? 2 : 1, NG == 1 ? 2 : 1))) void
 decode_chunked_kernel(const AttnParams p) {
   const int kh = blockIdx.x % p.kv_heads, rgroup = blockIdx.x / p.kv_heads;
   const int ngroups = gridDim.x / p.kv_heads;
@@ -488,12 +507,16 @@ decode_chunked_kernel(const AttnParams p) {
   // Metadata beyond the planned capacity (total > max_blocks * block_size) leaves no partial
   // buffer to write into; such rows are left unwritten rather than faulting.
   if (!single && p.part_o == nullptr) return;
-  for (int row0 = 16 * rgroup; row0 < R; row0 += 16 * ngroups) {
-    RowState<TT, D> rs;
-    init_rows<TT, D>(rs, p, w, row0, R, g, c, G);
+  for (int row0 = 16 * NG * rgroup; row0 < R; row0 += 16 * NG * ngroups) {
+    RowState<TT, D> rs[NG];
     // Keys outside every row's causal/window range are skipped (whole 32-key steps).
-    int lo_any = (row0 + c < R) ? rs.vis_lo : INT32_MAX;
-    int hi_any = rs.vis_hi;
+    int lo_any = INT32_MAX, hi_any = -1;
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+      init_rows<TT, D>(rs[j], p, w, row0 + 16 * j, R, g, c, G);
+      if (row0 + 16 * j + c < R) lo_any = min(lo_any, rs[j].vis_lo);
+      hi_any = max(hi_any, rs[j].vis_hi);
+    }
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) {
       lo_any = min(lo_any, __shfl_xor(lo_any, o, 64));
@@ -501,13 +524,19 @@ decode_chunked_kernel(const AttnParams p) {
     }
     const int t_first = max(start, (lo_any / 32) * 32);
     const int t_last = min(end, hi_any);
-    run_range<TT, D, CAP, 2>(w, rs, t_first, t_last, end, lane, c, G, p.scale_log2, p.scale,
-                          p.softcap);
-    const int rc = min(row0 + c, R - 1);
-    const float sink_c = sink_logit<TT>(p, kh * g + rc % g);
-    store_rows<TT, D>(rs, p, kh, s0, row0, R, g, c, G, sink_c, single, [&](int64_t t, int oh, int) {
-      return (t * p.num_heads + oh) * p.max_splits + split;
-    });
+    run_range<TT, D, CAP, 2, NG>(w, rs, t_first, t_last, end, lane, c, G, p.scale_log2, p.scale,
+                                 p.softcap);
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+      const int r0 = row0 + 16 * j;
+      if (r0 >= R) break;
+      const int rc = min(r0 + c, R - 1);
+      const float sink_c = sink_logit<TT>(p, kh * g + rc % g);
+      store_rows<TT, D>(rs[j], p, kh, s0, r0, R, g, c, G, sink_c, single,
+                        [&](int64_t t, int oh, int) {
+                          return (t * p.num_heads + oh) * p.max_splits + split;
+                        });
+    }
   }
 }
 
@@ -968,6 +997,9 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
 #ifndef PA_DECODE_DEPTH
 #define PA_DECODE_DEPTH 3
 #endif
+#ifndef PA_DECODE_DEPTH8
+#define PA_DECODE_DEPTH8 3
+#endif
 template <typename TT, int D, bool CAP, bool F8>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 decode_balanced_kernel(const AttnParams p) {
@@ -993,7 +1025,9 @@ decode_balanced_kernel(const AttnParams p) {
     sw.P = carry + (incl - sw.q.n);
     const int chunk_total = __builtin_amdgcn_readlane(incl, 63);
     const int64_t lo = max(gs, carry), hi = min(ge, carry + chunk_total);
-    if (lo < hi) stream_range<TT, D, CAP, F8, PA_DECODE_DEPTH>(p, sw, lo, hi, L, x, u0, lane);
+    if (lo < hi)
+      stream_range<TT, D, CAP, F8, F8 ? PA_DECODE_DEPTH8 : PA_DECODE_DEPTH>(p, sw, lo, hi, L, x,
+                                                                           u0, lane);
     carry += chunk_total;
   }
 }
@@ -1042,11 +1076,18 @@ hipError_t launch_d(const AttnParams& p, dim3 grid, dim3 block, bool balanced, h
       if (f8) hipLaunchKernelGGL((decode_balanced_kernel<TT, D, false, true>), grid, block, 0, s, p);
       else hipLaunchKernelGGL((decode_balanced_kernel<TT, D, false, false>), grid, block, 0, s, p);
     }
+  } else if (p.ng > 1) {
+    // NG row groups per wavefront: 4 at d=64, 2 at d=128 (what fits the register file).
+    constexpr int NG = D == 64 ? 4 : 2;
+    if (p.softcap > 0.0f)
+      hipLaunchKernelGGL((decode_chunked_kernel<TT, D, true, NG>), grid, dim3(64), 0, s, p);
+    else
+      hipLaunchKernelGGL((decode_chunked_kernel<TT, D, false, NG>), grid, dim3(64), 0, s, p);
   } else {
     if (p.softcap > 0.0f)
-      hipLaunchKernelGGL((decode_chunked_kernel<TT, D, true>), grid, dim3(64), 0, s, p);
+      hipLaunchKernelGGL((decode_chunked_kernel<TT, D, true, 1>), grid, dim3(64), 0, s, p);
     else
-      hipLaunchKernelGGL((decode_chunked_kernel<TT, D, false>), grid, dim3(64), 0, s, p);
+      hipLaunchKernelGGL((decode_chunked_kernel<TT, D, false, 1>), grid, dim3(64), 0, s, p);
   }
   return hipGetLastError();
 }
@@ -1083,8 +1124,10 @@ hipError_t launch_decode_mfma(const AttnParams& p, pa_dtype act, pa_dtype cache_
   if (p.batch <= 0) return hipSuccess;
   const int g = p.num_heads / p.kv_heads;
   const int mq = p.max_query_len > 0 ? p.max_query_len : p.num_tokens;
-  const int row_groups =
-      (int)std::min<int64_t>(((int64_t)g * mq + 15) / 16, (int64_t)(INT32_MAX / p.kv_heads));
+  if (p.ng != 1 && p.ng != (p.head_dim == 64 ? 4 : 2)) return hipErrorInvalidValue;
+  const int rows_per_wave = 16 * p.ng;
+  const int row_groups = (int)std::min<int64_t>(((int64_t)g * mq + rows_per_wave - 1) / rows_per_wave,
+                                                (int64_t)(INT32_MAX / p.kv_heads));
   dim3 grid(p.kv_heads * row_groups, p.max_splits, p.batch);
   if (act == PA_DTYPE_FLOAT16) return launch_t<TF16>(p, grid, dim3(64), false, s);
   return launch_t<TBF16>(p, grid, dim3(64), false, s);

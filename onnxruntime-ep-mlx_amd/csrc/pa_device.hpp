@@ -239,6 +239,7 @@ struct AttnParams {
   // (block-table slots, no duplicates), so new positions may be read from the pages.
   int32_t new_rows_in_cache;
   int32_t mix;  // balanced decode: sub-segments (each for another kv-head) per wavefront
+  int32_t ng;   // chunked kernel: 16-row groups per wavefront (1 or 4)
 };
 
 // Final normalisation shared by every attention kernel: the factor that turns an output
