@@ -237,6 +237,57 @@ size_t pa_paged_attention_workspace_bytes(const pa_paged_attention_node* node,
 int pa_paged_attention(const pa_paged_attention_node* node, const pa_paged_attention_io* io,
                        void* workspace, size_t workspace_bytes, pa_stream_t stream);
 
+/* Operator-level entry: com.microsoft::GroupQueryAttention on contiguous caches
+ * (group_query_attention_op / gqa_batched, attention.rs:932-1454 and :586-848), for the
+ * shared-buffer contract: present_key/present_value are [batch, kv_heads, capacity, head]
+ * buffers that already hold each sequence's past rows (past_key/past_value alias them) and
+ * receive, in place, the seq new rows of batch b at [seqlens_k[b] + 1 - seq, seqlens_k[b] + 1).
+ * Query rows attend causally over [0, seqlens_k[b] + 1) (plus window / softcap / sink).
+ * RoPE (do_rotary) rotates the new query/key rows at those positions with the supplied cache
+ * rows, per operation in T like the reference.  fp16/bf16 with head 64/128 and
+ * (num_heads/kv_heads) * seq <= 16 run on the streaming matrix-core decode; everything else
+ * (fp32, prefill chunks, other head sizes) on the VALU kernel.  Messages of invalid lengths
+ * start with "GroupQueryAttention:" (attention.rs:625-631, :668-672). */
+typedef struct pa_gqa_node {
+  int32_t num_heads;          /* "num_heads" */
+  int32_t kv_num_heads;       /* "kv_num_heads" */
+  float scale;                /* "scale" (0 = 1/sqrt(head)) */
+  float softcap;              /* "softcap" */
+  int32_t local_window_size;  /* "local_window_size" (-1) */
+  int32_t do_rotary;          /* "do_rotary" */
+  int32_t rotary_interleaved; /* "rotary_interleaved" */
+  int32_t is_causal;          /* "causal" (1) */
+  float qk_norm_epsilon;      /* "qk_norm_epsilon" (1e-6) */
+} pa_gqa_node;
+
+typedef struct pa_gqa_io {
+  pa_dtype dtype;            /* T */
+  int32_t batch;             /* query.shape[0] */
+  int32_t seq;               /* query.shape[1] (new tokens per sequence) */
+  int32_t query_hidden;      /* query.shape[2] = num_heads * head */
+  int32_t capacity;          /* present_key.shape[2] */
+  const void* query;         /* input 0 [batch, seq, num_heads * head] */
+  const void* key;           /* input 1 [batch, seq, kv_heads * head] */
+  const void* value;         /* input 2 */
+  void* present_key;         /* inputs 3/outputs 1: [batch, kv_heads, capacity, head], in place */
+  void* present_value;       /* inputs 4/outputs 2 */
+  const int32_t* seqlens_k;  /* input 5 [batch], device */
+  const int32_t* host_seqlens_k; /* host copy of input 5 (enables validation) or NULL */
+  int64_t total_sequence_length; /* input 6 (host scalar; used for validation) */
+  const void* cos_cache;     /* input 7 [positions, rotary_dim / 2] */
+  const void* sin_cache;     /* input 8 */
+  int64_t rotary_positions;
+  int32_t rotary_half;
+  const void* head_sink;     /* input 11 [num_heads] or NULL */
+  const void* q_norm_weight; /* inputs 14/15 [head] or NULL */
+  const void* k_norm_weight;
+  void* output;              /* output 0 [batch, seq, num_heads * head] */
+} pa_gqa_io;
+
+size_t pa_group_query_attention_workspace_bytes(const pa_gqa_node* node, const pa_gqa_io* io);
+int pa_group_query_attention(const pa_gqa_node* node, const pa_gqa_io* io, void* workspace,
+                             size_t workspace_bytes, pa_stream_t stream);
+
 /* Claim predicate for a PagedAttention node (paged_attention_claim, attention.rs:4384-4645,
  * plus kv_cache::claim kv_cache.rs:16-108), restricted to what this build executes.
  * Host only; no device work.  Returns 1 (claimed) or 0 (declined, reason written). */

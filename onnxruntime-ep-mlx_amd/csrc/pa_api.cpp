@@ -128,7 +128,7 @@ int device_cus() {
 }
 
 Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype act, int kind,
-               int chunk) {
+               int chunk, bool linear = false) {
   Plan pl{};
   const int g = a->num_heads / c->kv_heads;
   const int mq = b->max_query_len > 0 ? b->max_query_len : std::max(b->num_tokens, 1);
@@ -137,6 +137,7 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
   const bool bal_ok = (int64_t)g * mq <= 16 &&
                       pa::balanced_supported(c->head_dim, act, c->dtype, c->block_size) &&
                       (int64_t)c->num_blocks * c->block_size <= (int64_t)UINT32_MAX;
+  if (kind == 0 && linear) kind = bal_ok ? 1 : 3;  // contiguous caches: streaming or VALU kernel
   if (kind == 0) {
     if (bal_ok || (mfma && (int64_t)g * mq <= 16))
       kind = 1;
@@ -204,6 +205,7 @@ size_t workspace_for(const pa_cache* c, const pa_batch*, const pa_attn*, const P
 // Options of one attention call beyond the public descriptors.
 struct RunOpts {
   bool new_rows_in_cache = false;  // new rows sit in their block-table slots (see AttnParams)
+  int linear_cap = 0;              // contiguous [batch, kv_heads, cap, d] caches (GQA present)
 };
 
 int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype act,
@@ -233,7 +235,9 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
     return fail(PA_ERR_UNSUPPORTED, "prefill MFMA kernel does not cover this dtype/head_dim");
   if (!(a->softcap >= 0.0f) || !std::isfinite(a->softcap))
     return fail(PA_ERR_INVALID_ARGUMENT, "softcap must be finite and non-negative");
-  Plan pl = make_plan(c, b, a, act, kind, chunk);
+  Plan pl = make_plan(c, b, a, act, kind, chunk, opts.linear_cap > 0);
+  if (opts.linear_cap > 0 && !(pl.balanced || pl.kind == 3))
+    return fail(PA_ERR_UNSUPPORTED, "contiguous caches run on the decode or VALU kernels only");
   size_t need = workspace_for(c, b, a, pl);
   if (need > 0 && (!ws || ws_bytes < need))
     return fail(PA_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes, got %zu", need,
@@ -267,6 +271,7 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
   p.chunk = pl.chunk;
   p.max_splits = pl.max_splits;
   p.mix = pl.mix;
+  p.linear_cap = opts.linear_cap;
   p.ng = pl.ng > 0 ? pl.ng : 1;
   p.max_query_len = b->max_query_len > 0 ? b->max_query_len : b->num_tokens;
   p.scale = a->scale != 0.0f ? a->scale : 1.0f / std::sqrt((float)c->head_dim);
@@ -364,12 +369,20 @@ float* pa_pool_v_scale_ptr(const pa_pool* p) { return p ? p->vs : nullptr; }
 int64_t pa_pool_bytes(const pa_pool* p) { return p ? p->bytes : 0; }
 
 // ------------------------------------------------------------------------------ append
+// Contiguous-cache (GroupQueryAttention) append: see AppendParams.
+struct GqaAppend {
+  int linear_cap, seq;
+  const int32_t* seqlens_k;
+  int32_t* meta_out;
+};
+
 static int rotary_append_impl(const pa_cache* c, const pa_batch* b, int32_t num_heads,
                               pa_dtype act, const void* query, const void* key,
                               const void* value, void* q_out, void* k_out, const void* cos,
                               const void* sin, int64_t rot_pos, int32_t rot_half,
                               int32_t rot_offset, int32_t interleaved, const void* qn,
-                              const void* kn, float eps, hipStream_t s) {
+                              const void* kn, float eps, hipStream_t s,
+                              const GqaAppend* gqa = nullptr) {
   int rc = check_cache(c, act);
   if (rc) return rc;
   if ((rc = check_batch(b))) return rc;
@@ -421,6 +434,12 @@ static int rotary_append_impl(const pa_cache* c, const pa_batch* b, int32_t num_
   p.do_q = (query && q_out && num_heads > 0) ? 1 : 0;
   p.norm_eps = eps;
   p.slots_distinct = (b->flags & PA_BATCH_SLOTS_DISTINCT) ? 1 : 0;
+  if (gqa) {
+    p.linear_cap = gqa->linear_cap;
+    p.gqa_seq = gqa->seq;
+    p.seqlens_k = gqa->seqlens_k;
+    p.meta_out = gqa->meta_out;
+  }
   hipError_t e = pa::launch_rotary_append(p, act, c->dtype, s);
   if (e != hipSuccess) return hip_fail(e, "rotary/append kernel launch");
   return PA_OK;
@@ -648,6 +667,147 @@ int pa_paged_attention(const pa_paged_attention_node* n, const pa_paged_attentio
   const void* q = L.transform ? q_rot : io->query;
   const void* kn = L.transform ? k_rot : io->key;
   return run_attention(&io->cache, &L.batch, &L.attn, io->dtype, q, kn, io->value, io->output,
+                       ws + L.attn_off, workspace_bytes - L.attn_off, 0, 0, s, opts);
+}
+
+// ------------------------------------------------------------------------------ GQA
+namespace {
+
+struct GqaLayout {
+  int head;
+  bool transform;
+  size_t q_bytes, k_bytes, meta_off, attn_off, total;
+  pa_cache cache;
+  pa_batch batch;
+  pa_attn attn;
+};
+
+// group_query_attention_op / gqa_batched (attention.rs:932-1454, :586-848) restricted to the
+// shared-buffer contract: present_key/value ([batch, kv_heads, capacity, head]) already hold the
+// past rows and receive the seq new rows of batch b at [seqlens_k[b] + 1 - seq, seqlens_k[b] + 1).
+int gqa_layout(const pa_gqa_node* n, const pa_gqa_io* io, GqaLayout* L) {
+  if (!n || !io) return fail(PA_ERR_INVALID_ARGUMENT, "node/io is NULL");
+  if (n->num_heads <= 0 || n->kv_num_heads <= 0 || n->num_heads % n->kv_num_heads != 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "GroupQueryAttention: bad num_heads/kv_num_heads");
+  if (io->key == nullptr || io->value == nullptr)
+    return fail(PA_ERR_UNSUPPORTED, "GroupQueryAttention: packed QKV input is not supported");
+  if (io->batch < 1 || io->seq < 1 || io->capacity < 1)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "GroupQueryAttention: batch, sequence and capacity must be positive");
+  if (io->query_hidden <= 0 || io->query_hidden % n->num_heads != 0)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "GroupQueryAttention: query hidden size is not divisible by num_heads");
+  if (!is_act(io->dtype))
+    return fail(PA_ERR_UNSUPPORTED, "activation dtype must be fp16/bf16/fp32");
+  if (!io->query || !io->present_key || !io->present_value || !io->seqlens_k || !io->output)
+    return fail(PA_ERR_INVALID_ARGUMENT, "GroupQueryAttention: required pointers are NULL");
+  if ((int64_t)io->batch * n->kv_num_heads * io->capacity > (int64_t)INT32_MAX)
+    return fail(PA_ERR_UNSUPPORTED, "GroupQueryAttention: present cache has more than 2^31 rows");
+  L->head = io->query_hidden / n->num_heads;
+  L->transform = (n->do_rotary != 0) || io->q_norm_weight != nullptr;
+  const int64_t T = (int64_t)io->batch * io->seq;
+  const size_t es = elem_size(io->dtype);
+  L->q_bytes = L->transform ? align256((size_t)T * io->query_hidden * es) : 0;
+  L->k_bytes = L->transform ? align256((size_t)T * n->kv_num_heads * L->head * es) : 0;
+  L->meta_off = L->q_bytes + L->k_bytes;
+  L->attn_off = L->meta_off + align256((size_t)(2 * io->batch + 1) * sizeof(int32_t));
+  pa_cache& c = L->cache;
+  c = pa_cache{};
+  c.key_cache = io->present_key;
+  c.value_cache = io->present_value;
+  c.block_size = 16;  // geometry for the plan only: rows are addressed contiguously
+  c.num_blocks = ((int64_t)io->batch * n->kv_num_heads * io->capacity + 15) / 16;
+  c.kv_heads = n->kv_num_heads;
+  c.head_dim = L->head;
+  c.dtype = io->dtype;
+  pa_batch& b = L->batch;
+  b = pa_batch{};
+  b.batch = io->batch;
+  b.max_blocks = 1;
+  b.num_tokens = (int32_t)T;
+  b.max_query_len = io->seq;
+  b.flags = PA_BATCH_NEW_ROWS_IN_CACHE | PA_BATCH_SLOTS_DISTINCT;
+  pa_attn& a = L->attn;
+  a = pa_attn{};
+  a.num_heads = n->num_heads;
+  a.scale = n->scale;
+  a.softcap = n->softcap;
+  a.local_window_size = n->local_window_size;
+  a.is_causal = n->is_causal;
+  a.head_sink = io->head_sink;
+  L->total = L->attn_off + pa_attention_workspace_bytes_ex(&c, &b, &a, io->dtype, 0, 0);
+  return PA_OK;
+}
+
+// gqa_batched's length rules (attention.rs:614-631, :665-672), plus the shared-buffer
+// requirement that every sequence holds all seq new rows inside the capacity.
+int validate_gqa_lengths(const pa_gqa_io* io) {
+  const int32_t* len = io->host_seqlens_k;
+  const int64_t total = io->total_sequence_length;
+  bool bad = total <= 0 || total > INT32_MAX;
+  int64_t mx = -1;
+  for (int b = 0; b < io->batch && !bad; ++b) {
+    const int64_t v = len[b];
+    if (v < 0 || v >= total || (total != io->seq && v + 1 < io->seq)) bad = true;
+    mx = std::max(mx, v);
+  }
+  if (bad || mx != total - 1)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "GroupQueryAttention: invalid per-batch or maximum sequence lengths");
+  for (int b = 0; b < io->batch; ++b)
+    if ((int64_t)len[b] + 1 < io->seq || (int64_t)len[b] + 1 > io->capacity)
+      return fail(PA_ERR_INVALID_ARGUMENT,
+                  "GroupQueryAttention: sequence length exceeds available past cache");
+  return PA_OK;
+}
+
+}  // namespace
+
+size_t pa_group_query_attention_workspace_bytes(const pa_gqa_node* node, const pa_gqa_io* io) {
+  GqaLayout L;
+  if (gqa_layout(node, io, &L)) return 0;
+  return L.total;
+}
+
+int pa_group_query_attention(const pa_gqa_node* n, const pa_gqa_io* io, void* workspace,
+                             size_t workspace_bytes, pa_stream_t stream) {
+  GqaLayout L;
+  int rc = gqa_layout(n, io, &L);
+  if (rc) return rc;
+  if (io->host_seqlens_k && (rc = validate_gqa_lengths(io))) return rc;
+  if (n->local_window_size != -1 && n->local_window_size <= 0)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "GroupQueryAttention: local_window_size must be -1 or positive");
+  if (n->do_rotary && (!io->cos_cache || !io->sin_cache))
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "GroupQueryAttention: do_rotary=1 requires cos_cache and sin_cache inputs");
+  if (n->do_rotary && (io->rotary_half <= 0 || 2 * io->rotary_half > L.head))
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "GroupQueryAttention: rotary dimension must not exceed head_size");
+  if (workspace_bytes < L.total || !workspace)
+    return fail(PA_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes, got %zu", L.total,
+                workspace_bytes);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  char* ws = reinterpret_cast<char*>(workspace);
+  int32_t* meta = reinterpret_cast<int32_t*>(ws + L.meta_off);
+  L.batch.cumulative_sequence_length = meta;
+  L.batch.past_seqlens = meta + io->batch + 1;
+  L.batch.block_table = meta;  // unused for contiguous caches
+  void* q_rot = L.transform ? ws : nullptr;
+  void* k_rot = L.transform ? ws + L.q_bytes : nullptr;
+  GqaAppend g{io->capacity, io->seq, io->seqlens_k, meta};
+  rc = rotary_append_impl(&L.cache, &L.batch, n->num_heads, io->dtype, io->query, io->key,
+                          io->value, q_rot, k_rot, n->do_rotary ? io->cos_cache : nullptr,
+                          n->do_rotary ? io->sin_cache : nullptr, io->rotary_positions,
+                          io->rotary_half, 0, n->rotary_interleaved, io->q_norm_weight,
+                          io->k_norm_weight, n->qk_norm_epsilon, s, &g);
+  if (rc) return rc;
+  RunOpts opts;
+  opts.new_rows_in_cache = true;
+  opts.linear_cap = io->capacity;
+  const void* q = L.transform ? q_rot : io->query;
+  const void* kn = L.transform ? k_rot : io->key;
+  return run_attention(&L.cache, &L.batch, &L.attn, io->dtype, q, kn, io->value, io->output,
                        ws + L.attn_off, workspace_bytes - L.attn_off, 0, 0, s, opts);
 }
 

@@ -104,8 +104,23 @@ template <typename TT, bool FP8>
 __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p) {
   const int t = blockIdx.x;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const SeqPos sp = seq_pos_of_token(p.cum, p.past, p.batch, t);
-  const int64_t pos = (int64_t)max(sp.past, 0) + (t - sp.start);
+  const bool linear = p.linear_cap > 0;
+  int seq_b;
+  int64_t pos;
+  if (linear) {
+    // GroupQueryAttention: [batch, seq] query rows; past_b = seqlens_k[b] + 1 - seq.
+    seq_b = t / p.gqa_seq;
+    pos = (int64_t)p.seqlens_k[seq_b] + 1 - p.gqa_seq + (t % p.gqa_seq);
+    if (p.meta_out && t == 0 && blockIdx.y == 0)
+      for (int i = threadIdx.x; i <= p.batch; i += blockDim.x) {
+        p.meta_out[i] = i * p.gqa_seq;  // cum
+        if (i < p.batch) p.meta_out[p.batch + 1 + i] = max(p.seqlens_k[i] + 1 - p.gqa_seq, 0);
+      }
+  } else {
+    const SeqPos sp = seq_pos_of_token(p.cum, p.past, p.batch, t);
+    seq_b = sp.b;
+    pos = (int64_t)max(sp.past, 0) + (t - sp.start);
+  }
   const int D = p.head_dim;
   const bool transform = p.cos_cache != nullptr || p.q_norm != nullptr;
 
@@ -123,10 +138,14 @@ __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p
   }
 
   // blockIdx.y == 0: this token's key/value rows.  Cache slot and last-writer rule first.
-  int64_t slot = p.slot_mapping ? (int64_t)p.slot_mapping[t] : slot_at(p, sp.b, pos);
-  if (slot >= p.num_blocks * p.block_size) slot = -1;
+  int64_t slot;
+  if (linear)
+    slot = (pos >= 0 && pos < p.linear_cap) ? pos : -1;  // rows of one (b, kv-head) are distinct
+  else
+    slot = p.slot_mapping ? (int64_t)p.slot_mapping[t] : slot_at(p, seq_b, pos);
+  if (!linear && slot >= p.num_blocks * p.block_size) slot = -1;
   bool later_dup = false;
-  if (slot >= 0 && !p.slots_distinct) {
+  if (slot >= 0 && !p.slots_distinct && !linear) {
     for (int u = t + 1 + threadIdx.x; u < p.num_tokens; u += blockDim.x)
       if (token_slot_lane(p, u) == slot) later_dup = true;
   }
@@ -136,7 +155,8 @@ __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p
   const int64_t row = (int64_t)p.kv_heads * D;
   for (int kh = wave; kh < p.kv_heads; kh += 4) {
     int64_t sbase = (int64_t)t * row + (int64_t)kh * D;
-    int64_t cbase = slot * row + (int64_t)kh * D;
+    int64_t cbase = linear ? (((int64_t)seq_b * p.kv_heads + kh) * p.linear_cap + slot) * D
+                           : slot * row + (int64_t)kh * D;
     if (!FP8) {
       if (transform) {
         void* k_dst = p.k_out ? p.k_out : (write_cache ? p.key_cache : nullptr);

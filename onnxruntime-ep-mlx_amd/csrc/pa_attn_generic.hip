@@ -83,8 +83,13 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
     const void *kb, *vb;
     int64_t off;
     float ks = 1.0f, vs = 1.0f;
-    bool from_cache = pos < pastb || p.read_all_from_cache;
-    if (from_cache) {
+    bool from_cache = pos < pastb || p.read_all_from_cache || p.linear_cap > 0;
+    if (p.linear_cap > 0) {
+      // contiguous [batch, kv_heads, cap, head_dim] cache holding the new rows too
+      off = (((int64_t)b * p.kv_heads + kh) * p.linear_cap + pos) * D;
+      kb = p.key_cache;
+      vb = p.value_cache;
+    } else if (from_cache) {
       int64_t bi = pos / p.block_size;
       int64_t blk = p.block_table[(int64_t)b * p.max_blocks + min(bi, (int64_t)p.max_blocks - 1)];
       blk = min(max(blk, (int64_t)0), p.num_blocks - 1);

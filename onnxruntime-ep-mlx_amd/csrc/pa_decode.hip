@@ -739,6 +739,9 @@ __device__ __forceinline__ StepAt step_at(const Cursor& c, const SeqWin& sw, con
 // the table row; entries past the sequence are never used for addressing).
 __device__ __forceinline__ int load_step_blocks(const AttnParams& p, const StepAt& s, int lane,
                                                 int bs_shift) {
+  // Contiguous caches have no block table: the load still happens (same count on every path)
+  // and its value is unused.
+  if (p.linear_cap > 0) return p.cum[0];
   const int bi = min((s.t + (lane & 31)) >> bs_shift, p.max_blocks - 1);
   return p.block_table[(int64_t)s.b * p.max_blocks + bi];
 }
@@ -817,7 +820,22 @@ __device__ __forceinline__ void load_stream_step(const AttnParams& p, const Step
   const char* kn = reinterpret_cast<const char*>(p.k_new);
   const char* vn = reinterpret_cast<const char*>(p.v_new);
   const int last = s.total - 1;
-  if (bs_shift >= 4 && min(s.t + 31, last) < s.cache_limit) {
+  if (p.linear_cap > 0) {
+    // Contiguous cache: rows of (b, kh) follow each other; rows past the end re-read the last.
+    const int64_t r0 = ((int64_t)s.b * p.kv_heads + s.kh) * p.linear_cap;
+    const uint32_t rs = (uint32_t)D * 2;
+#pragma unroll
+    for (int tile = 0; tile < 2; ++tile) {
+      const int tp = s.t + 16 * tile;
+      const char* kr = kc + (uint64_t)(r0 + min(tp + c, last)) * rs;
+#pragma unroll
+      for (int q = 0; q < D / 32; ++q) st.k[tile][q] = ld16(kr + 16 * G + 64 * q);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        st.v[4 * tile + e] =
+            ld_vrow<D>(vc + (uint64_t)(r0 + min(tp + 4 * G + e, last)) * rs + DL * 2 * c);
+    }
+  } else if (bs_shift >= 4 && min(s.t + 31, last) < s.cache_limit) {
     // Every row in the pages and each 16-key tile inside one page: scalar page base (page id
     // read from a lane of `btl`), fixed lane offsets.  Rows past the end stay in the last page.
 #pragma unroll
@@ -1066,9 +1084,9 @@ balanced_merge_kernel(const AttnParams p) {
 }
 
 template <typename TT, int D>
-hipError_t launch_d(const AttnParams& p, dim3 grid, dim3 block, bool balanced, hipStream_t s) {
+hipError_t launch_d(const AttnParams& p, dim3 grid, dim3 block, bool balanced, bool f8,
+                    hipStream_t s) {
   if (balanced) {
-    const bool f8 = p.read_all_from_cache != 0;  // fp8 pages (host dispatch)
     if (p.softcap > 0.0f) {
       if (f8) hipLaunchKernelGGL((decode_balanced_kernel<TT, D, true, true>), grid, block, 0, s, p);
       else hipLaunchKernelGGL((decode_balanced_kernel<TT, D, true, false>), grid, block, 0, s, p);
@@ -1093,10 +1111,11 @@ hipError_t launch_d(const AttnParams& p, dim3 grid, dim3 block, bool balanced, h
 }
 
 template <typename TT>
-hipError_t launch_t(const AttnParams& p, dim3 grid, dim3 block, bool balanced, hipStream_t s) {
+hipError_t launch_t(const AttnParams& p, dim3 grid, dim3 block, bool balanced, bool f8,
+                    hipStream_t s) {
   switch (p.head_dim) {
-    case 64: return launch_d<TT, 64>(p, grid, block, balanced, s);
-    case 128: return launch_d<TT, 128>(p, grid, block, balanced, s);
+    case 64: return launch_d<TT, 64>(p, grid, block, balanced, f8, s);
+    case 128: return launch_d<TT, 128>(p, grid, block, balanced, f8, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -1121,6 +1140,7 @@ bool decode_mfma_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype) {
 hipError_t launch_decode_mfma(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
                               hipStream_t s) {
   if (!decode_mfma_supported(p.head_dim, act, cache_dtype)) return hipErrorInvalidValue;
+  if (p.linear_cap > 0) return hipErrorInvalidValue;  // paged caches only
   if (p.batch <= 0) return hipSuccess;
   const int g = p.num_heads / p.kv_heads;
   const int mq = p.max_query_len > 0 ? p.max_query_len : p.num_tokens;
@@ -1129,8 +1149,8 @@ hipError_t launch_decode_mfma(const AttnParams& p, pa_dtype act, pa_dtype cache_
   const int row_groups = (int)std::min<int64_t>(((int64_t)g * mq + rows_per_wave - 1) / rows_per_wave,
                                                 (int64_t)(INT32_MAX / p.kv_heads));
   dim3 grid(p.kv_heads * row_groups, p.max_splits, p.batch);
-  if (act == PA_DTYPE_FLOAT16) return launch_t<TF16>(p, grid, dim3(64), false, s);
-  return launch_t<TBF16>(p, grid, dim3(64), false, s);
+  if (act == PA_DTYPE_FLOAT16) return launch_t<TF16>(p, grid, dim3(64), false, false, s);
+  return launch_t<TBF16>(p, grid, dim3(64), false, false, s);
 }
 
 // Balanced launch: p.max_splits holds the segment count; every sequence must have at most 16
@@ -1138,16 +1158,17 @@ hipError_t launch_decode_mfma(const AttnParams& p, pa_dtype act, pa_dtype cache_
 hipError_t launch_decode_balanced(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
                                   hipStream_t s) {
   if (!balanced_supported(p.head_dim, act, cache_dtype, p.block_size)) return hipErrorInvalidValue;
-  if ((cache_dtype == PA_DTYPE_FP8_E4M3) != (p.read_all_from_cache != 0)) return hipErrorInvalidValue;
-  if (cache_dtype == PA_DTYPE_FP8_E4M3 && (p.k_scale == nullptr || p.v_scale == nullptr))
+  const bool f8 = cache_dtype == PA_DTYPE_FP8_E4M3;
+  if (f8 != (p.read_all_from_cache != 0)) return hipErrorInvalidValue;
+  if (f8 && (p.k_scale == nullptr || p.v_scale == nullptr || p.linear_cap > 0))
     return hipErrorInvalidValue;
   if (p.batch <= 0) return hipSuccess;
   if (p.part_o == nullptr || p.mix < 1 || p.mix > p.kv_heads || p.max_splits % p.mix != 0)
     return hipErrorInvalidValue;
   const int W = p.kv_heads % 4 == 0 ? 4 : p.kv_heads % 2 == 0 ? 2 : 1;
   dim3 grid(p.kv_heads / W, p.max_splits / p.mix), block(64 * W);
-  hipError_t e = (act == PA_DTYPE_FLOAT16) ? launch_t<TF16>(p, grid, block, true, s)
-                                           : launch_t<TBF16>(p, grid, block, true, s);
+  hipError_t e = (act == PA_DTYPE_FLOAT16) ? launch_t<TF16>(p, grid, block, true, f8, s)
+                                           : launch_t<TBF16>(p, grid, block, true, f8, s);
   if (e != hipSuccess) return e;
   const dim3 mgrid(p.kv_heads, p.batch);
   const bool f16 = act == PA_DTYPE_FLOAT16;

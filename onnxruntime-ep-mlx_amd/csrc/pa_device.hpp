@@ -207,6 +207,13 @@ struct AppendParams {
   int32_t do_q;  // process query rows (rotary/norm) into q_out
   float norm_eps;
   int32_t slots_distinct;  // no two tokens share a slot: skip the last-writer check
+  // Contiguous (GroupQueryAttention) caches: [batch, kv_heads, linear_cap, head_dim]; token t is
+  // query row t % gqa_seq of sequence t / gqa_seq at position seqlens_k[b] + 1 - gqa_seq + row.
+  // meta_out (if set) receives cum [batch + 1] and past [batch] for the attention that follows.
+  int32_t linear_cap;  // 0: paged cache
+  int32_t gqa_seq;
+  const int32_t* seqlens_k;
+  int32_t* meta_out;
 };
 
 struct AttnParams {
@@ -240,6 +247,10 @@ struct AttnParams {
   int32_t new_rows_in_cache;
   int32_t mix;  // balanced decode: sub-segments (each for another kv-head) per wavefront
   int32_t ng;   // chunked kernel: 16-row groups per wavefront (1 or 4)
+  // Contiguous caches [batch, kv_heads, linear_cap, head_dim] (GroupQueryAttention present
+  // buffers; the new rows are already in them): position pos of (b, kv-head kh) is row
+  // (b * kv_heads + kh) * linear_cap + pos.  0: paged cache.
+  int32_t linear_cap;
 };
 
 // Final normalisation shared by every attention kernel: the factor that turns an output

@@ -6,12 +6,13 @@ importing it loads the library and fails loudly if it has not been built.
 """
 from . import _capi
 from ._capi import PagedAttentionError, load
-from .ops import (PagePool, attention, paged_attention, pa_dtype, reshape_and_cache,
-                  rotary_append)
+from .ops import (PagePool, attention, group_query_attention, paged_attention, pa_dtype,
+                  reshape_and_cache, rotary_append)
 
 load()
 
 __all__ = [
-    "PagePool", "PagedAttentionError", "attention", "load", "pa_dtype", "paged_attention",
+    "PagePool", "PagedAttentionError", "attention", "group_query_attention", "load", "pa_dtype",
+    "paged_attention",
     "reshape_and_cache", "rotary_append", "_capi",
 ]

@@ -36,6 +36,7 @@ EXPORTS = (
     "pa_attention_workspace_bytes", "pa_attention_workspace_bytes_ex",
     "pa_attention", "pa_attention_ex",
     "pa_paged_attention_workspace_bytes", "pa_paged_attention", "pa_paged_attention_claim",
+    "pa_group_query_attention_workspace_bytes", "pa_group_query_attention",
 )
 
 
@@ -90,6 +91,30 @@ class PaIO(C.Structure):
         ("q_norm_weight", C.c_void_p), ("k_norm_weight", C.c_void_p),
         ("host_cumulative_sequence_length", C.c_void_p), ("host_past_seqlens", C.c_void_p),
         ("host_block_table", C.c_void_p), ("host_slot_mapping", C.c_void_p),
+        ("output", C.c_void_p),
+    ]
+
+
+class PaGqaNode(C.Structure):
+    _fields_ = [
+        ("num_heads", C.c_int32), ("kv_num_heads", C.c_int32), ("scale", C.c_float),
+        ("softcap", C.c_float), ("local_window_size", C.c_int32), ("do_rotary", C.c_int32),
+        ("rotary_interleaved", C.c_int32), ("is_causal", C.c_int32),
+        ("qk_norm_epsilon", C.c_float),
+    ]
+
+
+class PaGqaIO(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_int), ("batch", C.c_int32), ("seq", C.c_int32),
+        ("query_hidden", C.c_int32), ("capacity", C.c_int32),
+        ("query", C.c_void_p), ("key", C.c_void_p), ("value", C.c_void_p),
+        ("present_key", C.c_void_p), ("present_value", C.c_void_p),
+        ("seqlens_k", C.c_void_p), ("host_seqlens_k", C.c_void_p),
+        ("total_sequence_length", C.c_int64),
+        ("cos_cache", C.c_void_p), ("sin_cache", C.c_void_p),
+        ("rotary_positions", C.c_int64), ("rotary_half", C.c_int32),
+        ("head_sink", C.c_void_p), ("q_norm_weight", C.c_void_p), ("k_norm_weight", C.c_void_p),
         ("output", C.c_void_p),
     ]
 
@@ -154,6 +179,10 @@ def load() -> C.CDLL:
         "pa_paged_attention_workspace_bytes": (SZ, [C.POINTER(PaNode), C.POINTER(PaIO)]),
         "pa_paged_attention": (C.c_int, [C.POINTER(PaNode), C.POINTER(PaIO), P, SZ, P]),
         "pa_paged_attention_claim": (C.c_int, [C.POINTER(PaNodeInfo), C.c_char_p, SZ]),
+        "pa_group_query_attention_workspace_bytes": (SZ, [C.POINTER(PaGqaNode),
+                                                          C.POINTER(PaGqaIO)]),
+        "pa_group_query_attention": (C.c_int, [C.POINTER(PaGqaNode), C.POINTER(PaGqaIO), P, SZ,
+                                               P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

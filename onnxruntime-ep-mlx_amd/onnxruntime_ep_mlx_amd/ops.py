@@ -268,3 +268,42 @@ def paged_attention(query, key, value, key_cache, value_cache, cumulative_sequen
     capi.check(lib.pa_paged_attention(C.byref(node), C.byref(io), _ptr(ws), nbytes,
                                       _stream(query.device)))
     return output, key_cache, value_cache
+
+
+def group_query_attention(query, key, value, present_key, present_value, seqlens_k,
+                          total_sequence_length, cos_cache=None, sin_cache=None, head_sink=None,
+                          q_norm_weight=None, k_norm_weight=None, *, num_heads, kv_num_heads,
+                          scale=0.0, softcap=0.0, local_window_size=-1, do_rotary=0,
+                          rotary_interleaved=0, is_causal=1, qk_norm_epsilon=1e-6,
+                          validate=True, output=None):
+    """com.microsoft::GroupQueryAttention on MI355X (pa_group_query_attention), shared-buffer
+    contract: present_key/present_value [B, kv_heads, capacity, head] hold the past rows and are
+    updated in place with the new rows at [seqlens_k[b] + 1 - S, seqlens_k[b] + 1).
+    Returns (output, present_key, present_value)."""
+    lib = capi.load()
+    if query.dim() != 3:
+        raise ValueError("query must have rank 3 [batch, sequence, hidden]")
+    for n, t in (("query", query), ("key", key), ("value", value),
+                 ("present_key", present_key), ("present_value", present_value)):
+        _need_cuda(n, t)
+        _contig(n, t)
+    if seqlens_k.dtype != torch.int32:
+        raise ValueError("input seqlens_k must be int32")
+    host = seqlens_k.detach().to("cpu").contiguous() if validate else None
+    if output is None:
+        output = torch.empty_like(query)
+    node = capi.PaGqaNode(num_heads, kv_num_heads, scale, softcap, local_window_size, do_rotary,
+                          rotary_interleaved, is_causal, qk_norm_epsilon)
+    io = capi.PaGqaIO(
+        pa_dtype(query.dtype), query.shape[0], query.shape[1], query.shape[2],
+        present_key.shape[2], _ptr(query), _ptr(key), _ptr(value), _ptr(present_key),
+        _ptr(present_value), _ptr(seqlens_k), _ptr(host), int(total_sequence_length),
+        _ptr(cos_cache) if do_rotary else None, _ptr(sin_cache) if do_rotary else None,
+        cos_cache.shape[0] if (do_rotary and cos_cache is not None) else 0,
+        cos_cache.shape[1] if (do_rotary and cos_cache is not None) else 0,
+        _ptr(head_sink), _ptr(q_norm_weight), _ptr(k_norm_weight), _ptr(output))
+    nbytes = lib.pa_group_query_attention_workspace_bytes(C.byref(node), C.byref(io))
+    ws = _ws.get(max(nbytes, 1), query.device)
+    capi.check(lib.pa_group_query_attention(C.byref(node), C.byref(io), _ptr(ws), nbytes,
+                                            _stream(query.device)))
+    return output, present_key, present_value

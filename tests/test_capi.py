@@ -177,3 +177,26 @@ def test_workspace_query_is_pure_host():
                          np.zeros((2, 4096), np.int32), nb=128, bs=4)
     n = capi.load().pa_paged_attention_workspace_bytes(C.byref(node), C.byref(io))
     assert n > 0 and n % 256 == 0
+
+
+# GroupQueryAttention length rules (gqa_batched, attention.rs:614-631, :665-672): host-side
+# checks that fail before any device work, so they run without a GPU
+@pytest.mark.parametrize("seqlens,total,msg", [
+    ([5, 9], 9, "invalid per-batch or maximum sequence lengths"),      # max != total - 1
+    ([5, -1], 6, "invalid per-batch or maximum sequence lengths"),     # negative
+    ([5, 40], 41, "exceeds available past cache"),                     # beyond capacity 32
+])
+def test_gqa_length_validation(seqlens, total, msg):
+    from onnxruntime_ep_mlx_amd import _capi as capi
+    lib = capi.load()
+    host = np.asarray(seqlens, np.int32)
+    node = capi.PaGqaNode(8, 2, 0.0, 0.0, -1, 0, 0, 1, 1e-6)
+    fake = 0x1000  # never dereferenced: validation fails first
+    io = capi.PaGqaIO(capi.PA_DTYPE_BFLOAT16, 2, 1, 8 * 64, 32, fake, fake, fake, fake, fake,
+                      fake, host.ctypes.data, total, None, None, 0, 0, None, None, None, fake)
+    nbytes = lib.pa_group_query_attention_workspace_bytes(C.byref(node), C.byref(io))
+    assert nbytes > 0
+    rc = lib.pa_group_query_attention(C.byref(node), C.byref(io), C.c_void_p(fake), nbytes, None)
+    assert rc != 0
+    err = lib.pa_last_error().decode()
+    assert err.startswith("GroupQueryAttention:") and msg in err, err
