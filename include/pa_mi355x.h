@@ -44,8 +44,17 @@ typedef enum pa_dtype {
   PA_DTYPE_FLOAT16 = 1,
   PA_DTYPE_BFLOAT16 = 2,
   PA_DTYPE_FLOAT32 = 3,
-  PA_DTYPE_FP8_E4M3 = 4 /* OCP e4m3fn, cache storage only */
+  PA_DTYPE_FP8_E4M3 = 4, /* OCP e4m3fn, cache storage only */
+  /* Integer cache storage (ORT int8 / uint8 "int4" caches, kv_cache.rs:110-256): */
+  PA_DTYPE_INT8 = 5, /* one signed code per channel */
+  PA_DTYPE_INT4 = 6  /* uint8 bytes of two (code + 8) nibbles: channel 2i low, 2i+1 high; an
+                        odd head's last high nibble is 8; a row is (head_dim + 1) / 2 bytes */
 } pa_dtype;
+
+/* Scale layout of one side of an integer cache ("k_quant_type" / "v_quant_type"). */
+#define PA_QUANT_NONE 0
+#define PA_QUANT_PER_TENSOR 1  /* one fp32 scale */
+#define PA_QUANT_PER_CHANNEL 2 /* fp32 [kv_heads, head_dim] */
 
 #define PA_OK 0
 #define PA_ERR_INVALID_ARGUMENT 1
@@ -61,7 +70,8 @@ const char* pa_version(void);
 /* ------------------------------------------------------------------------------------------ */
 /* Page pool: the HBM slab behind the cache tensors.  Replaces the MLX-backed "MLX" device
  * OrtAllocator that hands out the cache tensors (rust/src/device.rs:415-486, created by
- * factory.rs:266-286).  One hipMalloc per side, [num_blocks, block_size, kv_heads, head_dim]. */
+ * factory.rs:266-286).  One hipMalloc per side, [num_blocks, block_size, kv_heads, head_dim]
+ * elements ((head_dim + 1) / 2 bytes per kv-head row for PA_DTYPE_INT4). */
 typedef struct pa_pool pa_pool;
 
 int pa_pool_create(int64_t num_blocks, int32_t block_size, int32_t kv_heads, int32_t head_dim,
@@ -77,17 +87,22 @@ int64_t pa_pool_bytes(const pa_pool* pool);
 /* ------------------------------------------------------------------------------------------ */
 /* Descriptors shared by the kernel-level entry points. */
 
-/* A paged KV cache (inputs 3/4 of PagedAttention, attention.rs:3922-3932). */
+/* A paged KV cache (inputs 3/4 of PagedAttention, attention.rs:3922-3932).
+ * Integer caches (inputs 14/15 = k_scale/v_scale, QuantizedCache kv_cache.rs:110-256): a new
+ * row is stored as codes sat(RNE(x / scale)) (zero scale -> code 0) and every key/value the
+ * attention reads, the new rows included, is code * scale in fp32 read back from the pages. */
 typedef struct pa_cache {
   void* key_cache;
   void* value_cache;
-  const float* k_scale; /* fp8 only, [num_blocks, kv_heads] */
-  const float* v_scale; /* fp8 only, [num_blocks, kv_heads] */
+  const float* k_scale; /* fp8: [num_blocks, kv_heads]; int8/int4: see k_quant_type */
+  const float* v_scale; /* fp8: [num_blocks, kv_heads]; int8/int4: see v_quant_type */
   int64_t num_blocks;
   int32_t block_size;
   int32_t kv_heads;
-  int32_t head_dim;
-  pa_dtype dtype; /* storage dtype: T, or PA_DTYPE_FP8_E4M3 */
+  int32_t head_dim; /* logical head size (int4 rows hold (head_dim + 1) / 2 bytes) */
+  pa_dtype dtype;   /* storage dtype: T, PA_DTYPE_FP8_E4M3, PA_DTYPE_INT8 or PA_DTYPE_INT4 */
+  int32_t k_quant_type; /* PA_QUANT_*: integer caches only (PA_QUANT_NONE otherwise) */
+  int32_t v_quant_type;
 } pa_cache;
 
 /* Packed var-length batch metadata (inputs 5/6/7/10, attention.rs:3934-3990). */
@@ -148,7 +163,8 @@ int pa_rotary_append(const pa_cache* cache, const pa_batch* batch, int32_t num_h
                      float norm_eps, pa_stream_t stream);
 
 /* Pure reshape_and_cache: bit copy of key/value rows into their slots (or fp8 quantisation
- * x / scale, zero scale -> 0, RNE, saturate to +-448).  Same slot and ordering rules. */
+ * x / scale, zero scale -> 0, RNE, saturate to +-448; or integer codes, see pa_cache).  Same
+ * slot and ordering rules. */
 int pa_reshape_and_cache(const pa_cache* cache, const pa_batch* batch, pa_dtype act_dtype,
                          const void* key, const void* value, pa_stream_t stream);
 
@@ -163,12 +179,13 @@ size_t pa_attention_workspace_bytes_ex(const pa_cache* cache, const pa_batch* ba
 /* Attention over the paged cache after append.  Keys/values at positions < past come from the
  * cache pages; positions >= past come from k_new/v_new (the rotated new rows), exactly as the
  * reference's _paged_ref and its patched Metal kernel do (attention.rs:4161-4190,
- * paged_attention.rs:46-74).  fp8 caches read every position from the pages (the quantised
- * rule of attention.rs:4192-4194).  q: [num_tokens, num_heads*head_dim]; out likewise.
+ * paged_attention.rs:46-74).  fp8 and integer caches read every position from the pages (the
+ * quantised rule of attention.rs:4192-4194).  q: [num_tokens, num_heads*head_dim]; out
+ * likewise.
  * Dispatch: fp16/bf16 with head_dim 64 or 128 run on matrix cores: the balanced (stream-K)
  * decode kernel when (num_heads/kv_heads) * max_query_len <= 16 and the block size is a power
  * of two, else the chunked split-K kernel in 16-row groups (multi-token prefill chunks);
- * fp32 activations, other head sizes and fp8 pages use the VALU kernel. */
+ * fp32 activations, other head sizes and integer pages use the VALU kernel. */
 int pa_attention(const pa_cache* cache, const pa_batch* batch, const pa_attn* attn,
                  pa_dtype act_dtype, const void* q, const void* k_new, const void* v_new,
                  void* out, void* workspace, size_t workspace_bytes, pa_stream_t stream);
@@ -203,11 +220,12 @@ typedef struct pa_paged_attention_node {
 typedef struct pa_paged_attention_io {
   pa_dtype dtype;              /* T */
   int32_t num_tokens;          /* query.shape[0] */
-  int32_t query_hidden;        /* query.shape[1]; packed QKV when key == value == NULL */
+  int32_t query_hidden;        /* query.shape[1]; key == value == NULL: packed QKV, query is
+                                  [num_tokens, (num_heads + 2 * kv_num_heads) * head] */
   const void* query;           /* input 0 */
   const void* key;             /* input 1 (NULL: packed) */
   const void* value;           /* input 2 (NULL: packed) */
-  pa_cache cache;              /* inputs 3/4 (+14/15 for fp8 scales) */
+  pa_cache cache;              /* inputs 3/4 (+14/15 for fp8 / integer cache scales) */
   const int32_t* cumulative_sequence_length; /* input 5, device */
   const int32_t* past_seqlens; /* input 6, device */
   const int32_t* block_table;  /* input 7, device */
@@ -246,8 +264,11 @@ int pa_paged_attention(const pa_paged_attention_node* node, const pa_paged_atten
  * RoPE (do_rotary) rotates the new query/key rows at those positions with the supplied cache
  * rows, per operation in T like the reference.  fp16/bf16 with head 64/128 and
  * (num_heads/kv_heads) * seq <= 16 run on the streaming matrix-core decode; everything else
- * (fp32, prefill chunks, other head sizes) on the VALU kernel.  Messages of invalid lengths
- * start with "GroupQueryAttention:" (attention.rs:625-631, :668-672). */
+ * (fp32, prefill chunks, other head sizes, integer caches) on the VALU kernel.  Messages of
+ * invalid lengths start with "GroupQueryAttention:" (attention.rs:625-631, :668-672).
+ * Integer present caches (cache_dtype PA_DTYPE_INT8 / PA_DTYPE_INT4, "kv_cache_bit_width" 8 /
+ * 4) encode the new rows as sat(RNE(x * (1 / scale))) with a zero scale read as 1 (the MLAS
+ * reciprocal rule, kv_cache.rs:183-190) and attend over code * scale of every row. */
 typedef struct pa_gqa_node {
   int32_t num_heads;          /* "num_heads" */
   int32_t kv_num_heads;       /* "kv_num_heads" */
@@ -282,6 +303,11 @@ typedef struct pa_gqa_io {
   const void* q_norm_weight; /* inputs 14/15 [head] or NULL */
   const void* k_norm_weight;
   void* output;              /* output 0 [batch, seq, num_heads * head] */
+  pa_dtype cache_dtype;      /* present storage: 0 (= T), PA_DTYPE_INT8 or PA_DTYPE_INT4 */
+  const float* k_scale;      /* inputs 12/13 for integer caches, see pa_cache */
+  const float* v_scale;
+  int32_t k_quant_type;      /* PA_QUANT_* ("k_quant_type" / "v_quant_type") */
+  int32_t v_quant_type;
 } pa_gqa_io;
 
 size_t pa_group_query_attention_workspace_bytes(const pa_gqa_node* node, const pa_gqa_io* io);
@@ -295,7 +321,7 @@ typedef struct pa_node_info {
   int32_t num_inputs;          /* 8..17 */
   int32_t num_outputs;         /* 1..3 */
   int32_t input_present[17];
-  int32_t input_dtype[17];     /* pa_dtype, or 10 for int32, 11 for int8/uint8 */
+  int32_t input_dtype[17];     /* pa_dtype, or PA_INT32_DTYPE / PA_INT8_DTYPE / PA_UINT8_DTYPE */
   int32_t input_rank[17];
   int64_t input_shape[17][4];
   int32_t output_present[3];
@@ -306,9 +332,15 @@ typedef struct pa_node_info {
   int32_t is_causal, has_scale_attr;
   float softcap;
   int32_t kv_cache_layout_latent; /* "kv_cache_layout" == "LATENT" */
+  /* "k_quant_type"/"v_quant_type": PA_QUANT_* (absent = PA_QUANT_NONE, any other string -1) */
+  int32_t k_quant_type, v_quant_type;
+  /* "k_cache_dtype"/"v_cache_dtype": 0 when absent or empty, PA_DTYPE_FLOAT16 "float16",
+   * PA_DTYPE_BFLOAT16 "bfloat16", PA_DTYPE_INT8 "int8", PA_DTYPE_INT4 "int4", -1 otherwise */
+  int32_t k_cache_dtype, v_cache_dtype;
 } pa_node_info;
 #define PA_INT32_DTYPE 10
 #define PA_INT8_DTYPE 11
+#define PA_UINT8_DTYPE 12
 
 int pa_paged_attention_claim(const pa_node_info* node, char* reason, size_t reason_len);
 

@@ -41,9 +41,19 @@ size_t elem_size(pa_dtype d) {
     case PA_DTYPE_FLOAT16:
     case PA_DTYPE_BFLOAT16: return 2;
     case PA_DTYPE_FLOAT32: return 4;
-    case PA_DTYPE_FP8_E4M3: return 1;
+    case PA_DTYPE_FP8_E4M3:
+    case PA_DTYPE_INT8: return 1;
+    case PA_DTYPE_INT4: return 0;  // two channels per byte: use cache_head_bytes
   }
   return 0;
+}
+
+bool is_int_cache(pa_dtype d) { return d == PA_DTYPE_INT8 || d == PA_DTYPE_INT4; }
+
+// Bytes of one kv-head's row in a cache of storage dtype d.
+size_t cache_head_bytes(pa_dtype d, int head_dim) {
+  if (d == PA_DTYPE_INT4) return (size_t)(head_dim + 1) / 2;
+  return elem_size(d) * (size_t)head_dim;
 }
 
 bool is_act(pa_dtype d) {
@@ -58,16 +68,28 @@ int check_cache(const pa_cache* c, pa_dtype act) {
   if (c->num_blocks <= 0 || c->block_size <= 0)
     return fail(PA_ERR_INVALID_ARGUMENT,
                 "PagedAttention: caches require matching positive block geometry");
-  if (c->kv_heads <= 0 || c->head_dim <= 0 || c->head_dim > 256 || c->head_dim % 8 != 0)
-    return fail(PA_ERR_UNSUPPORTED, "head_dim %d unsupported (multiple of 8, <= 256)",
-                c->head_dim);
+  if (c->kv_heads <= 0 || c->head_dim <= 0 || c->head_dim > 256)
+    return fail(PA_ERR_UNSUPPORTED, "head_dim %d unsupported (1..256)", c->head_dim);
   if (!c->key_cache || !c->value_cache)
     return fail(PA_ERR_INVALID_ARGUMENT, "key_cache/value_cache pointers are NULL");
   if (c->dtype == PA_DTYPE_FP8_E4M3) {
     if (!c->k_scale || !c->v_scale)
       return fail(PA_ERR_INVALID_ARGUMENT, "fp8 cache requires k_scale and v_scale");
+  } else if (is_int_cache(c->dtype)) {
+    // kv_cache.rs:37-60: integer caches need PER_TENSOR / PER_CHANNEL fp32 scales.
+    for (int side = 0; side < 2; ++side) {
+      const int mode = side ? c->v_quant_type : c->k_quant_type;
+      if (mode != PA_QUANT_PER_TENSOR && mode != PA_QUANT_PER_CHANNEL)
+        return fail(PA_ERR_INVALID_ARGUMENT,
+                    "integer %s cache requires PER_TENSOR or PER_CHANNEL quantization",
+                    side ? "v" : "k");
+      if (!(side ? c->v_scale : c->k_scale))
+        return fail(PA_ERR_INVALID_ARGUMENT, "quantized %s cache requires a scale tensor",
+                    side ? "v" : "k");
+    }
   } else if (c->dtype != act) {
-    return fail(PA_ERR_UNSUPPORTED, "cache dtype must equal the activation dtype or be fp8");
+    return fail(PA_ERR_UNSUPPORTED,
+                "cache dtype must equal the activation dtype or be fp8 / int8 / int4");
   }
   if (!is_act(act)) return fail(PA_ERR_UNSUPPORTED, "activation dtype must be fp16/bf16/fp32");
   if (c->num_blocks * (int64_t)c->block_size > INT32_MAX)
@@ -218,8 +240,9 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
   if (a->num_heads <= 0 || a->num_heads % c->kv_heads != 0)
     return fail(PA_ERR_INVALID_ARGUMENT, "PagedAttention: bad num_heads/kv_num_heads");
   if (b->num_tokens == 0) return PA_OK;
-  if (!q || !out || (!kn && c->dtype != PA_DTYPE_FP8_E4M3) ||
-      (!vn && c->dtype != PA_DTYPE_FP8_E4M3))
+  // Quantised caches (fp8, int8, int4) read every position from the pages.
+  const bool quant = c->dtype == PA_DTYPE_FP8_E4M3 || is_int_cache(c->dtype);
+  if (!q || !out || (!quant && (!kn || !vn)))
     return fail(PA_ERR_INVALID_ARGUMENT, "q/k_new/v_new/out pointers are NULL");
   if (kind < 0 || kind > 4) return fail(PA_ERR_INVALID_ARGUMENT, "unknown kernel kind %d", kind);
   if (kind == 4 && !pa::decode_mfma_supported(c->head_dim, act, c->dtype))
@@ -279,7 +302,9 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
   p.softcap = a->softcap;
   p.window = a->local_window_size;
   p.causal = a->is_causal ? 1 : 0;
-  p.read_all_from_cache = c->dtype == PA_DTYPE_FP8_E4M3 ? 1 : 0;
+  p.read_all_from_cache = quant ? 1 : 0;
+  p.k_quant = c->k_quant_type;
+  p.v_quant = c->v_quant_type;
   p.new_rows_in_cache =
       (opts.new_rows_in_cache || ((b->flags & PA_BATCH_NEW_ROWS_IN_CACHE) && !b->slot_mapping))
           ? 1
@@ -326,10 +351,11 @@ int pa_pool_create(int64_t num_blocks, int32_t block_size, int32_t kv_heads, int
                    pa_dtype cache_dtype, pa_pool** out_pool) {
   if (!out_pool) return fail(PA_ERR_INVALID_ARGUMENT, "out_pool is NULL");
   *out_pool = nullptr;
-  size_t es = elem_size(cache_dtype);
-  if (num_blocks <= 0 || block_size <= 0 || kv_heads <= 0 || head_dim <= 0 || es == 0)
+  const size_t hb = head_dim > 0 ? cache_head_bytes(cache_dtype, head_dim) : 0;
+  if (num_blocks <= 0 || block_size <= 0 || kv_heads <= 0 || head_dim <= 0 || hb == 0)
     return fail(PA_ERR_INVALID_ARGUMENT, "invalid pool geometry");
-  size_t side = (size_t)num_blocks * block_size * kv_heads * head_dim * es;
+  // Integer pools hold codes only: their per-tensor / per-channel scales are operator inputs.
+  size_t side = (size_t)num_blocks * block_size * kv_heads * hb;
   pa_pool* p = new pa_pool{};
   hipError_t e = hipMalloc(&p->k, side);
   if (e == hipSuccess) e = hipMalloc(&p->v, side);
@@ -369,11 +395,17 @@ float* pa_pool_v_scale_ptr(const pa_pool* p) { return p ? p->vs : nullptr; }
 int64_t pa_pool_bytes(const pa_pool* p) { return p ? p->bytes : 0; }
 
 // ------------------------------------------------------------------------------ append
-// Contiguous-cache (GroupQueryAttention) append: see AppendParams.
-struct GqaAppend {
-  int linear_cap, seq;
-  const int32_t* seqlens_k;
-  int32_t* meta_out;
+// Operator-level append options beyond the kernel-level entry: contiguous (GroupQueryAttention)
+// caches, packed-QKV input strides with contiguous copies of the rows, and the integer encode
+// rule (see AppendParams).
+struct AppendExtra {
+  int linear_cap = 0, seq = 0;
+  const int32_t* seqlens_k = nullptr;
+  int32_t* meta_out = nullptr;
+  int64_t q_ld = 0, k_ld = 0, v_ld = 0;  // 0: contiguous rows
+  void* v_out = nullptr;
+  bool copy_rows = false;
+  bool quant_reciprocal = false;
 };
 
 static int rotary_append_impl(const pa_cache* c, const pa_batch* b, int32_t num_heads,
@@ -382,7 +414,7 @@ static int rotary_append_impl(const pa_cache* c, const pa_batch* b, int32_t num_
                               const void* sin, int64_t rot_pos, int32_t rot_half,
                               int32_t rot_offset, int32_t interleaved, const void* qn,
                               const void* kn, float eps, hipStream_t s,
-                              const GqaAppend* gqa = nullptr) {
+                              const AppendExtra& x = AppendExtra()) {
   int rc = check_cache(c, act);
   if (rc) return rc;
   if ((rc = check_batch(b))) return rc;
@@ -398,7 +430,7 @@ static int rotary_append_impl(const pa_cache* c, const pa_batch* b, int32_t num_
   if ((qn == nullptr) != (kn == nullptr))
     return fail(PA_ERR_INVALID_ARGUMENT,
                 "q_norm_weight and k_norm_weight must be provided together");
-  const bool transform = rotate || qn;
+  const bool transform = rotate || qn || x.copy_rows;
   if (transform && num_heads > 0 && query && !q_out)
     return fail(PA_ERR_INVALID_ARGUMENT, "q_out is required when rotating/normalising query");
   pa::AppendParams p{};
@@ -434,12 +466,18 @@ static int rotary_append_impl(const pa_cache* c, const pa_batch* b, int32_t num_
   p.do_q = (query && q_out && num_heads > 0) ? 1 : 0;
   p.norm_eps = eps;
   p.slots_distinct = (b->flags & PA_BATCH_SLOTS_DISTINCT) ? 1 : 0;
-  if (gqa) {
-    p.linear_cap = gqa->linear_cap;
-    p.gqa_seq = gqa->seq;
-    p.seqlens_k = gqa->seqlens_k;
-    p.meta_out = gqa->meta_out;
-  }
+  p.linear_cap = x.linear_cap;
+  p.gqa_seq = x.seq;
+  p.seqlens_k = x.seqlens_k;
+  p.meta_out = x.meta_out;
+  p.q_ld = x.q_ld ? x.q_ld : (int64_t)num_heads * c->head_dim;
+  p.k_ld = x.k_ld ? x.k_ld : (int64_t)c->kv_heads * c->head_dim;
+  p.v_ld = x.v_ld ? x.v_ld : (int64_t)c->kv_heads * c->head_dim;
+  p.v_out = x.v_out;
+  p.copy_rows = x.copy_rows ? 1 : 0;
+  p.k_quant = c->k_quant_type;
+  p.v_quant = c->v_quant_type;
+  p.quant_reciprocal = x.quant_reciprocal ? 1 : 0;
   hipError_t e = pa::launch_rotary_append(p, act, c->dtype, s);
   if (e != hipSuccess) return hip_fail(e, "rotary/append kernel launch");
   return PA_OK;
@@ -468,7 +506,10 @@ int pa_reshape_and_cache(const pa_cache* cache, const pa_batch* batch, pa_dtype 
 size_t pa_attention_workspace_bytes(const pa_cache* cache, const pa_batch* batch,
                                     const pa_attn* attn) {
   if (!cache || !batch || !attn || cache->kv_heads <= 0 || batch->batch <= 0) return 0;
-  pa_dtype act = cache->dtype == PA_DTYPE_FP8_E4M3 ? PA_DTYPE_BFLOAT16 : cache->dtype;
+  // Quantised storage does not name the activation dtype; the plan only needs a 16-bit one.
+  pa_dtype act = (cache->dtype == PA_DTYPE_FP8_E4M3 || is_int_cache(cache->dtype))
+                     ? PA_DTYPE_BFLOAT16
+                     : cache->dtype;
   return workspace_for(cache, batch, attn, make_plan(cache, batch, attn, act, 0, 0));
 }
 
@@ -500,8 +541,8 @@ namespace {
 
 struct OpLayout {
   int head, kv_hidden;
-  bool transform;
-  size_t q_bytes, k_bytes, attn_off, total;
+  bool packed, transform;
+  size_t q_bytes, k_bytes, v_bytes, attn_off, total;
   pa_batch batch;
   pa_attn attn;
 };
@@ -510,22 +551,29 @@ int op_layout(const pa_paged_attention_node* n, const pa_paged_attention_io* io,
   if (!n || !io) return fail(PA_ERR_INVALID_ARGUMENT, "node/io is NULL");
   if (n->num_heads <= 0 || n->kv_num_heads <= 0 || n->num_heads % n->kv_num_heads != 0)
     return fail(PA_ERR_INVALID_ARGUMENT, "PagedAttention: bad num_heads/kv_num_heads");
-  const bool packed = io->key == nullptr && io->value == nullptr;
-  if (packed)
-    return fail(PA_ERR_UNSUPPORTED, "PagedAttention: packed QKV input is not supported");
-  if (io->query_hidden <= 0 || io->query_hidden % n->num_heads != 0)
+  // attention.rs:4433: key and value absent together = packed [T, (H + 2 KV) * head] query.
+  L->packed = io->key == nullptr && io->value == nullptr;
+  if (!L->packed && (io->key == nullptr || io->value == nullptr))
     return fail(PA_ERR_INVALID_ARGUMENT,
-                "query must have rank 2 and a hidden size divisible by its head count");
-  L->head = io->query_hidden / n->num_heads;
+                "PagedAttention: key and value must both be present or both be absent");
+  const int qheads = L->packed ? n->num_heads + 2 * n->kv_num_heads : n->num_heads;
+  if (io->query_hidden <= 0 || io->query_hidden % qheads != 0)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "query must have rank 2 and a hidden size divisible by its separate or packed "
+                "head count");
+  L->head = io->query_hidden / qheads;
   L->kv_hidden = L->head * n->kv_num_heads;
   if (io->cache.head_dim != L->head || io->cache.kv_heads != n->kv_num_heads)
     return fail(PA_ERR_INVALID_ARGUMENT,
                 "key_cache must be [num_blocks,block_size,kv_num_heads,head_size]");
-  L->transform = (n->do_rotary != 0) || io->q_norm_weight != nullptr;
+  // Packed rows are copied out contiguously by the append kernel (rotated or not).
+  L->transform = (n->do_rotary != 0) || io->q_norm_weight != nullptr || L->packed;
   size_t es = elem_size(io->dtype);
-  L->q_bytes = L->transform ? align256((size_t)io->num_tokens * io->query_hidden * es) : 0;
-  L->k_bytes = L->transform ? align256((size_t)io->num_tokens * L->kv_hidden * es) : 0;
-  L->attn_off = L->q_bytes + L->k_bytes;
+  const size_t T = (size_t)std::max(io->num_tokens, 0);
+  L->q_bytes = L->transform ? align256(T * n->num_heads * L->head * es) : 0;
+  L->k_bytes = L->transform ? align256(T * L->kv_hidden * es) : 0;
+  L->v_bytes = L->packed ? align256(T * L->kv_hidden * es) : 0;
+  L->attn_off = L->q_bytes + L->k_bytes + L->v_bytes;
   pa_batch& b = L->batch;
   b.cumulative_sequence_length = io->cumulative_sequence_length;
   b.past_seqlens = io->past_seqlens;
@@ -653,20 +701,34 @@ int pa_paged_attention(const pa_paged_attention_node* n, const pa_paged_attentio
   char* ws = reinterpret_cast<char*>(workspace);
   void* q_rot = L.transform ? ws : nullptr;
   void* k_rot = L.transform ? ws + L.q_bytes : nullptr;
+  void* v_rows = L.packed ? ws + L.q_bytes + L.k_bytes : nullptr;
+  const void* key = io->key;
+  const void* value = io->value;
+  AppendExtra x;
+  if (L.packed) {
+    const size_t es = elem_size(io->dtype);
+    const char* qkv = reinterpret_cast<const char*>(io->query);
+    key = qkv + (size_t)n->num_heads * L.head * es;
+    value = qkv + (size_t)(n->num_heads + n->kv_num_heads) * L.head * es;
+    x.q_ld = x.k_ld = x.v_ld = io->query_hidden;
+    x.v_out = v_rows;
+    x.copy_rows = true;
+  }
   RunOpts opts;
   const bool distinct = io->slot_mapping == nullptr &&
                         io->host_cumulative_sequence_length != nullptr && host_slots_distinct(io);
   if (distinct) L.batch.flags |= PA_BATCH_SLOTS_DISTINCT;
   opts.new_rows_in_cache = distinct && io->cache.dtype == io->dtype;
-  rc = rotary_append_impl(&io->cache, &L.batch, n->num_heads, io->dtype, io->query, io->key,
-                          io->value, q_rot, k_rot, n->do_rotary ? io->cos_cache : nullptr,
+  rc = rotary_append_impl(&io->cache, &L.batch, n->num_heads, io->dtype, io->query, key, value,
+                          q_rot, k_rot, n->do_rotary ? io->cos_cache : nullptr,
                           n->do_rotary ? io->sin_cache : nullptr, io->rotary_positions,
                           io->rotary_half, n->rotary_offset, n->rotary_interleaved,
-                          io->q_norm_weight, io->k_norm_weight, n->qk_norm_epsilon, s);
+                          io->q_norm_weight, io->k_norm_weight, n->qk_norm_epsilon, s, x);
   if (rc) return rc;
   const void* q = L.transform ? q_rot : io->query;
-  const void* kn = L.transform ? k_rot : io->key;
-  return run_attention(&io->cache, &L.batch, &L.attn, io->dtype, q, kn, io->value, io->output,
+  const void* kn = L.transform ? k_rot : key;
+  const void* vn = L.packed ? v_rows : value;
+  return run_attention(&io->cache, &L.batch, &L.attn, io->dtype, q, kn, vn, io->output,
                        ws + L.attn_off, workspace_bytes - L.attn_off, 0, 0, s, opts);
 }
 
@@ -675,8 +737,8 @@ namespace {
 
 struct GqaLayout {
   int head;
-  bool transform;
-  size_t q_bytes, k_bytes, meta_off, attn_off, total;
+  bool packed, transform;
+  size_t q_bytes, k_bytes, v_bytes, meta_off, attn_off, total;
   pa_cache cache;
   pa_batch batch;
   pa_attn attn;
@@ -689,27 +751,32 @@ int gqa_layout(const pa_gqa_node* n, const pa_gqa_io* io, GqaLayout* L) {
   if (!n || !io) return fail(PA_ERR_INVALID_ARGUMENT, "node/io is NULL");
   if (n->num_heads <= 0 || n->kv_num_heads <= 0 || n->num_heads % n->kv_num_heads != 0)
     return fail(PA_ERR_INVALID_ARGUMENT, "GroupQueryAttention: bad num_heads/kv_num_heads");
-  if (io->key == nullptr || io->value == nullptr)
-    return fail(PA_ERR_UNSUPPORTED, "GroupQueryAttention: packed QKV input is not supported");
+  // Key and value absent together: packed [B, S, (H + 2 KV) * head] query (attention.rs:2487).
+  L->packed = io->key == nullptr && io->value == nullptr;
+  if (!L->packed && (io->key == nullptr || io->value == nullptr))
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "GroupQueryAttention: key and value must both be present or both be absent");
   if (io->batch < 1 || io->seq < 1 || io->capacity < 1)
     return fail(PA_ERR_INVALID_ARGUMENT,
                 "GroupQueryAttention: batch, sequence and capacity must be positive");
-  if (io->query_hidden <= 0 || io->query_hidden % n->num_heads != 0)
+  const int qheads = L->packed ? n->num_heads + 2 * n->kv_num_heads : n->num_heads;
+  if (io->query_hidden <= 0 || io->query_hidden % qheads != 0)
     return fail(PA_ERR_INVALID_ARGUMENT,
-                "GroupQueryAttention: query hidden size is not divisible by num_heads");
+                "GroupQueryAttention: query hidden size is not divisible by its head count");
   if (!is_act(io->dtype))
     return fail(PA_ERR_UNSUPPORTED, "activation dtype must be fp16/bf16/fp32");
   if (!io->query || !io->present_key || !io->present_value || !io->seqlens_k || !io->output)
     return fail(PA_ERR_INVALID_ARGUMENT, "GroupQueryAttention: required pointers are NULL");
   if ((int64_t)io->batch * n->kv_num_heads * io->capacity > (int64_t)INT32_MAX)
     return fail(PA_ERR_UNSUPPORTED, "GroupQueryAttention: present cache has more than 2^31 rows");
-  L->head = io->query_hidden / n->num_heads;
-  L->transform = (n->do_rotary != 0) || io->q_norm_weight != nullptr;
+  L->head = io->query_hidden / qheads;
+  L->transform = (n->do_rotary != 0) || io->q_norm_weight != nullptr || L->packed;
   const int64_t T = (int64_t)io->batch * io->seq;
   const size_t es = elem_size(io->dtype);
-  L->q_bytes = L->transform ? align256((size_t)T * io->query_hidden * es) : 0;
+  L->q_bytes = L->transform ? align256((size_t)T * n->num_heads * L->head * es) : 0;
   L->k_bytes = L->transform ? align256((size_t)T * n->kv_num_heads * L->head * es) : 0;
-  L->meta_off = L->q_bytes + L->k_bytes;
+  L->v_bytes = L->packed ? align256((size_t)T * n->kv_num_heads * L->head * es) : 0;
+  L->meta_off = L->q_bytes + L->k_bytes + L->v_bytes;
   L->attn_off = L->meta_off + align256((size_t)(2 * io->batch + 1) * sizeof(int32_t));
   pa_cache& c = L->cache;
   c = pa_cache{};
@@ -719,7 +786,17 @@ int gqa_layout(const pa_gqa_node* n, const pa_gqa_io* io, GqaLayout* L) {
   c.num_blocks = ((int64_t)io->batch * n->kv_num_heads * io->capacity + 15) / 16;
   c.kv_heads = n->kv_num_heads;
   c.head_dim = L->head;
-  c.dtype = io->dtype;
+  c.dtype = io->cache_dtype == 0 ? io->dtype : io->cache_dtype;
+  if (c.dtype != io->dtype && !is_int_cache(c.dtype))
+    return fail(PA_ERR_UNSUPPORTED,
+                "GroupQueryAttention: present caches must use the activation dtype, int8 or int4");
+  if (c.dtype == PA_DTYPE_INT4 && L->head % 2 != 0)
+    return fail(PA_ERR_UNSUPPORTED,
+                "GroupQueryAttention: packed INT4 requires an even logical head size");
+  c.k_scale = io->k_scale;
+  c.v_scale = io->v_scale;
+  c.k_quant_type = is_int_cache(c.dtype) ? io->k_quant_type : PA_QUANT_NONE;
+  c.v_quant_type = is_int_cache(c.dtype) ? io->v_quant_type : PA_QUANT_NONE;
   pa_batch& b = L->batch;
   b = pa_batch{};
   b.batch = io->batch;
@@ -795,19 +872,37 @@ int pa_group_query_attention(const pa_gqa_node* n, const pa_gqa_io* io, void* wo
   L.batch.block_table = meta;  // unused for contiguous caches
   void* q_rot = L.transform ? ws : nullptr;
   void* k_rot = L.transform ? ws + L.q_bytes : nullptr;
-  GqaAppend g{io->capacity, io->seq, io->seqlens_k, meta};
-  rc = rotary_append_impl(&L.cache, &L.batch, n->num_heads, io->dtype, io->query, io->key,
-                          io->value, q_rot, k_rot, n->do_rotary ? io->cos_cache : nullptr,
+  void* v_rows = L.packed ? ws + L.q_bytes + L.k_bytes : nullptr;
+  const void* key = io->key;
+  const void* value = io->value;
+  AppendExtra x;
+  x.linear_cap = io->capacity;
+  x.seq = io->seq;
+  x.seqlens_k = io->seqlens_k;
+  x.meta_out = meta;
+  x.quant_reciprocal = true;  // MLAS GQA encode: x * (1 / scale), zero scale read as 1
+  if (L.packed) {
+    const size_t es = elem_size(io->dtype);
+    const char* qkv = reinterpret_cast<const char*>(io->query);
+    key = qkv + (size_t)n->num_heads * L.head * es;
+    value = qkv + (size_t)(n->num_heads + n->kv_num_heads) * L.head * es;
+    x.q_ld = x.k_ld = x.v_ld = io->query_hidden;
+    x.v_out = v_rows;
+    x.copy_rows = true;
+  }
+  rc = rotary_append_impl(&L.cache, &L.batch, n->num_heads, io->dtype, io->query, key, value,
+                          q_rot, k_rot, n->do_rotary ? io->cos_cache : nullptr,
                           n->do_rotary ? io->sin_cache : nullptr, io->rotary_positions,
                           io->rotary_half, 0, n->rotary_interleaved, io->q_norm_weight,
-                          io->k_norm_weight, n->qk_norm_epsilon, s, &g);
+                          io->k_norm_weight, n->qk_norm_epsilon, s, x);
   if (rc) return rc;
   RunOpts opts;
   opts.new_rows_in_cache = true;
   opts.linear_cap = io->capacity;
   const void* q = L.transform ? q_rot : io->query;
-  const void* kn = L.transform ? k_rot : io->key;
-  return run_attention(&L.cache, &L.batch, &L.attn, io->dtype, q, kn, io->value, io->output,
+  const void* kn = L.transform ? k_rot : key;
+  const void* vn = L.packed ? v_rows : value;
+  return run_attention(&L.cache, &L.batch, &L.attn, io->dtype, q, kn, vn, io->output,
                        ws + L.attn_off, workspace_bytes - L.attn_off, 0, 0, s, opts);
 }
 
@@ -842,45 +937,84 @@ int pa_paged_attention_claim(const pa_node_info* n, char* reason, size_t reason_
   auto present = [&](int i) { return i < n->num_inputs && n->input_present[i]; };
   auto out_present = [&](int i) { return i < n->num_outputs && n->output_present[i]; };
   const bool packed = !present(1) && !present(2);
-  if (packed) return deny("packed QKV input is not executed by this build");
-  for (int i : {0, 1, 2})
+  for (int i : {0, 1, 2}) {
+    if (packed && i > 0) break;
     if (!present(i) || n->input_dtype[i] != out_dt)
       return deny("input %d must be present and share the output float dtype", i);
+  }
   for (int i : {5, 6, 7})
     if (!present(i) || n->input_dtype[i] != I32) return deny("input %d must be int32", i);
   const int64_t H = n->num_heads, KV = n->kv_num_heads;
   if (!(H > 0 && KV > 0 && H % KV == 0))
     return deny("num_heads (%lld) must be a positive multiple of kv_num_heads (%lld)",
                 (long long)H, (long long)KV);
-  if (n->input_rank[0] != 2 || n->input_shape[0][1] <= 0 || n->input_shape[0][1] % H != 0)
+  const int64_t qheads = packed ? H + 2 * KV : H;
+  if (n->input_rank[0] != 2 || n->input_shape[0][1] <= 0 || n->input_shape[0][1] % qheads != 0)
     return deny("query must have rank 2 and a hidden size divisible by its separate or packed "
                 "head count");
-  const int64_t head = n->input_shape[0][1] / H;
-  if (head > 256 || head % 8 != 0) return deny("head_size %lld is not executed by this build",
-                                               (long long)head);
-  // Cache storage: the activation dtype, or (build-defined) fp8 e4m3 with fp32
-  // per-(block, kv-head) scales in inputs 14/15.  Integer caches are not executed yet.
-  const int cache_dt = present(3) ? n->input_dtype[3] : out_dt;
+  const int64_t head = n->input_shape[0][1] / qheads;
+  if (head > 256) return deny("head_size %lld is not executed by this build", (long long)head);
+  // kv_cache::claim (kv_cache.rs:16-108): both caches share one storage dtype; integer caches
+  // need PER_TENSOR / PER_CHANNEL fp32 scales (inputs 14/15) and a matching *_cache_dtype; a
+  // floating cache uses the activation dtype, NONE quantization and no scale.  fp8 e4m3 pages
+  // with fp32 per-(block, kv-head) scales are this build's extension.
   if (!present(3) || !present(4)) return deny("key_cache and value_cache must be present");
-  if (n->input_dtype[4] != cache_dt) return deny("key/value caches must share one storage dtype");
-  if (cache_dt == PA_INT8_DTYPE) return deny("integer KV caches are not executed by this build");
-  if (cache_dt == PA_DTYPE_FP8_E4M3) {
-    for (int i : {14, 15})
-      if (!present(i) || n->input_dtype[i] != PA_DTYPE_FLOAT32 || n->input_rank[i] != 2 ||
-          n->input_shape[i][1] != KV)
-        return deny("fp8 cache requires float32 %s_scale [num_blocks, kv_num_heads]",
-                    i == 14 ? "k" : "v");
-  } else if (cache_dt != out_dt) {
-    return deny("a non-integer cache must use the activation dtype");
+  const int cache_dt = n->input_dtype[3];
+  const bool quantized = cache_dt == PA_INT8_DTYPE || cache_dt == PA_UINT8_DTYPE;
+  for (int side = 0; side < 2; ++side) {
+    const int cache_in = 3 + side, scale_in = 14 + side;
+    const char* nm = side ? "v" : "k";
+    if (n->input_dtype[cache_in] != cache_dt)
+      return deny("key/value caches must share one storage dtype");
+    const int mode = side ? n->v_quant_type : n->k_quant_type;
+    if (quantized) {
+      if (mode != PA_QUANT_PER_TENSOR && mode != PA_QUANT_PER_CHANNEL)
+        return deny("integer %s cache requires PER_TENSOR or PER_CHANNEL quantization", nm);
+      if (!present(scale_in)) return deny("quantized %s cache requires a scale tensor", nm);
+      if (n->input_dtype[scale_in] != PA_DTYPE_FLOAT32) return deny("%s_scale must be float32", nm);
+      const int rank = n->input_rank[scale_in];
+      int64_t count = 1;
+      bool known = rank >= 0 && rank <= 4;
+      for (int d = 0; known && d < rank; ++d) {
+        if (n->input_shape[scale_in][d] < 0) known = false;
+        else count *= n->input_shape[scale_in][d];
+      }
+      const int64_t expected = mode == PA_QUANT_PER_TENSOR ? 1 : KV * head;
+      if (known && count != expected)
+        return deny("%s_scale must contain %lld elements", nm, (long long)expected);
+      if (mode == PA_QUANT_PER_CHANNEL &&
+          !(rank > 0 && rank <= 4 &&
+            (n->input_shape[scale_in][rank - 1] < 0 || n->input_shape[scale_in][rank - 1] == head)))
+        return deny("PagedAttention per-channel scales must end in head_size");
+    } else if (cache_dt == PA_DTYPE_FP8_E4M3) {
+      if (!present(scale_in) || n->input_dtype[scale_in] != PA_DTYPE_FLOAT32 ||
+          n->input_rank[scale_in] != 2 || n->input_shape[scale_in][1] != KV)
+        return deny("fp8 cache requires float32 %s_scale [num_blocks, kv_num_heads]", nm);
+    } else if (!(cache_dt == out_dt && mode == PA_QUANT_NONE && !present(scale_in))) {
+      return deny("floating %s cache requires activation dtype, NONE quantization and no scale",
+                  nm);
+    }
+    const int logical = side ? n->v_cache_dtype : n->k_cache_dtype;
+    const int expected = cache_dt == PA_INT8_DTYPE    ? PA_DTYPE_INT8
+                         : cache_dt == PA_UINT8_DTYPE ? PA_DTYPE_INT4
+                         : cache_dt == T16            ? T16
+                         : cache_dt == TB16           ? TB16
+                                                      : 0;
+    if (!(logical == expected || (logical == 0 && expected != PA_DTYPE_INT4)))
+      return deny("%s_cache_dtype must agree with cache storage; uint8 requires explicit int4",
+                  nm);
   }
+  const int64_t cache_head = cache_dt == PA_UINT8_DTYPE ? (head + 1) / 2 : head;
   const int64_t v_head = n->v_head_size == 0 ? head : n->v_head_size;
-  if (n->input_rank[1] != 2 || n->input_shape[1][1] != KV * head)
-    return deny("key must be [num_tokens,kv_num_heads*head_size]");
-  if (n->input_rank[2] != 2 || n->input_shape[2][1] != KV * v_head)
-    return deny("value must be [num_tokens,kv_num_heads*v_head_size]");
+  if (!packed) {
+    if (n->input_rank[1] != 2 || n->input_shape[1][1] != KV * head)
+      return deny("key must be [num_tokens,kv_num_heads*head_size]");
+    if (n->input_rank[2] != 2 || n->input_shape[2][1] != KV * v_head)
+      return deny("value must be [num_tokens,kv_num_heads*v_head_size]");
+  }
   if (v_head != head) return deny("SEPARATE layout requires equal key and value head sizes");
   for (int i : {3, 4})
-    if (n->input_rank[i] != 4 || n->input_shape[i][2] != KV || n->input_shape[i][3] != head)
+    if (n->input_rank[i] != 4 || n->input_shape[i][2] != KV || n->input_shape[i][3] != cache_head)
       return deny("%s must be [num_blocks,block_size,kv_num_heads,head_size]",
                   i == 3 ? "key_cache" : "value_cache");
   if (n->output_rank[0] != 2 ||

@@ -10,6 +10,8 @@
 // v_cvt_f16_f32 for fp16; contraction into FMA is disabled for the fp32 variant.
 // Duplicate slots: a token skips its write when any later token maps to the same slot, so the
 // cache ends up holding the last token's row, as sequential scatter does.
+// Integer caches (int8, int4 nibble pairs) store sat(RNE(x / scale)) codes of the final T row
+// (QuantizedCache::encode, kv_cache.rs:170-219).
 
 #include "pa_device.hpp"
 
@@ -100,7 +102,94 @@ __device__ void process_row(const AppendParams& p, const void* src, int64_t src_
   }
 }
 
-template <typename TT, bool FP8>
+// Cache storage kinds of the append kernel.
+enum CacheKind { kCacheT = 0, kCacheFp8 = 1, kCacheI8 = 2, kCacheI4 = 3 };
+
+// Integer code of x (QuantizedCache::encode, kv_cache.rs:170-199): paged caches divide by the
+// scale and store 0 for a zero scale; GroupQueryAttention caches multiply by the fp32
+// reciprocal with a zero scale read as 1.  Then clip to the code range and round half to even
+// (the clip bounds are integers, so clip-then-round equals round-then-clip).  NaN -> 0.
+__device__ __forceinline__ int int_code(float x, float s, bool reciprocal, float lo, float hi) {
+  float y;
+  if (reciprocal) {
+    const float r = 1.0f / (s == 0.0f ? 1.0f : s);
+    y = x * r;
+  } else {
+    y = s == 0.0f ? 0.0f : x / s;
+  }
+  if (y != y) return 0;
+  return (int)__builtin_rintf(fminf(fmaxf(y, lo), hi));
+}
+
+// Integer-cache row writer.  Each output element's final value (normalised, rotated, rounded
+// to T exactly as process_row does) is recomputed by the lane that stores it, so an int4 byte
+// (two channels) needs no exchange between lanes.  out (may be null) receives the T row.
+template <typename TT, int CK>
+__device__ void int_row(const AppendParams& p, const void* src, int64_t sbase, void* out,
+                        int64_t obase, uint8_t* cache, int64_t cbase, const float* sc,
+                        bool per_channel, int kh, const void* norm_w, bool rotate,
+                        int64_t pos, int lane) {
+  const int D = p.head_dim;
+  float inv = 1.0f;
+  if (norm_w) {
+    float acc = 0.0f;
+    for (int e = lane; e < D; e += 64) {
+      float v = ldv<TT>(src, sbase + e);
+      acc += v * v;
+    }
+    acc = wave_sum(acc);
+    inv = 1.0f / __builtin_sqrtf(acc / (float)D + p.norm_eps);
+  }
+  const int half =
+      (rotate && p.cos_cache && pos >= 0 && pos < p.rotary_positions) ? p.rotary_half : 0;
+  const int off = p.rotary_offset;
+  auto fetch = [&](int e) -> float {
+    float v = ldv<TT>(src, sbase + e);
+    if (norm_w) v = rnd<TT>(rnd<TT>(v * inv) * ldv<TT>(norm_w, e));
+    return v;
+  };
+  auto value = [&](int e) -> float {
+    const int r = e - off;
+    if (r < 0 || r >= 2 * half) return fetch(e);
+    const bool first = p.rotary_interleaved ? (r & 1) == 0 : r < half;
+    const int i = p.rotary_interleaved ? (r >> 1) : (first ? r : r - half);
+    const int e1 = p.rotary_interleaved ? off + 2 * i : off + i;
+    const int e2 = p.rotary_interleaved ? off + 2 * i + 1 : off + half + i;
+    const float c = ldv<TT>(p.cos_cache, pos * half + i);
+    const float s = ldv<TT>(p.sin_cache, pos * half + i);
+    const float a = fetch(e1), b = fetch(e2);
+    return first ? rnd<TT>(rnd<TT>(a * c) - rnd<TT>(b * s))
+                 : rnd<TT>(rnd<TT>(b * c) + rnd<TT>(a * s));
+  };
+  const bool recip = p.quant_reciprocal != 0;
+  const float s0 = (cache && !per_channel) ? sc[0] : 0.0f;
+  auto scale_of = [&](int e) -> float { return per_channel ? sc[(int64_t)kh * D + e] : s0; };
+  if (CK == kCacheI4) {
+    const int W = (D + 1) >> 1;
+    for (int j = lane; j < W; j += 64) {
+      const int e0 = 2 * j, e1 = 2 * j + 1;
+      const float v0 = value(e0);
+      const float v1 = e1 < D ? value(e1) : 0.0f;
+      if (out) {
+        stv<TT>(out, obase + e0, v0);
+        if (e1 < D) stv<TT>(out, obase + e1, v1);
+      }
+      if (cache) {
+        const int c0 = int_code(v0, scale_of(e0), recip, -8.0f, 7.0f) + 8;
+        const int c1 = e1 < D ? int_code(v1, scale_of(e1), recip, -8.0f, 7.0f) + 8 : 8;
+        cache[cbase + j] = (uint8_t)(c0 | (c1 << 4));
+      }
+    }
+  } else {
+    for (int e = lane; e < D; e += 64) {
+      const float v = value(e);
+      if (out) stv<TT>(out, obase + e, v);
+      if (cache) cache[cbase + e] = (uint8_t)(int8_t)int_code(v, scale_of(e), recip, -128.0f, 127.0f);
+    }
+  }
+}
+
+template <typename TT, int CK>
 __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p) {
   const int t = blockIdx.x;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -122,18 +211,16 @@ __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p
     pos = (int64_t)max(sp.past, 0) + (t - sp.start);
   }
   const int D = p.head_dim;
-  const bool transform = p.cos_cache != nullptr || p.q_norm != nullptr;
-
+  const bool transform = p.cos_cache != nullptr || p.q_norm != nullptr || p.copy_rows;
 
   // Workgroups with blockIdx.y >= 1 take four query head rows each, one per wavefront, so
   // every head row of every token is in flight at once.
   if (blockIdx.y > 0) {
     const int h = (blockIdx.y - 1) * 4 + wave;
-    if (p.do_q && transform && h < p.num_heads) {
-      int64_t base = ((int64_t)t * p.num_heads + h) * D;
-      process_row<TT>(p, p.query, base, p.q_out, base, nullptr, 0, nullptr, 0, 0.0f, p.q_norm,
-                      pos, lane);
-    }
+    if (p.do_q && transform && h < p.num_heads)
+      process_row<TT>(p, p.query, (int64_t)t * p.q_ld + (int64_t)h * D, p.q_out,
+                      ((int64_t)t * p.num_heads + h) * D, nullptr, 0, nullptr, 0, 0.0f,
+                      p.q_norm, pos, lane);
     return;
   }
 
@@ -152,30 +239,39 @@ __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p
   const bool write_cache = slot >= 0 && !__syncthreads_or(later_dup);
 
   // 3. key rows: transform into k_out and/or the cache row; value rows: copy / quantise
-  const int64_t row = (int64_t)p.kv_heads * D;
+  // Cache row width per kv-head in storage units: int4 packs two channels per byte.
+  const int Dc = CK == kCacheI4 ? (D + 1) >> 1 : D;
+  const int64_t crow = (int64_t)p.kv_heads * Dc;
   for (int kh = wave; kh < p.kv_heads; kh += 4) {
-    int64_t sbase = (int64_t)t * row + (int64_t)kh * D;
-    int64_t cbase = linear ? (((int64_t)seq_b * p.kv_heads + kh) * p.linear_cap + slot) * D
-                           : slot * row + (int64_t)kh * D;
-    if (!FP8) {
+    const int64_t kbase = (int64_t)t * p.k_ld + (int64_t)kh * D;
+    const int64_t vbase = (int64_t)t * p.v_ld + (int64_t)kh * D;
+    const int64_t obase = ((int64_t)t * p.kv_heads + kh) * D;  // k_out / v_out rows
+    const int64_t cbase = linear ? (((int64_t)seq_b * p.kv_heads + kh) * p.linear_cap + slot) * Dc
+                                 : slot * crow + (int64_t)kh * Dc;
+    if (CK == kCacheT) {
       if (transform) {
         void* k_dst = p.k_out ? p.k_out : (write_cache ? p.key_cache : nullptr);
-        int64_t k_base = p.k_out ? sbase : cbase;
+        int64_t k_base = p.k_out ? obase : cbase;
         void* k_dst2 = (p.k_out && write_cache) ? p.key_cache : nullptr;
         if (k_dst)
-          process_row<TT>(p, p.key, sbase, k_dst, k_base, k_dst2, cbase, nullptr, 0, 0.0f,
+          process_row<TT>(p, p.key, kbase, k_dst, k_base, k_dst2, cbase, nullptr, 0, 0.0f,
                           p.k_norm, pos, lane);
       } else if (write_cache) {
         const typename TT::raw* ks = reinterpret_cast<const typename TT::raw*>(p.key);
         typename TT::raw* kd = reinterpret_cast<typename TT::raw*>(p.key_cache);
-        for (int e = lane; e < D; e += 64) kd[cbase + e] = ks[sbase + e];
+        for (int e = lane; e < D; e += 64) kd[cbase + e] = ks[kbase + e];
       }
-      if (write_cache) {
+      if (write_cache || p.v_out) {
         const typename TT::raw* vs = reinterpret_cast<const typename TT::raw*>(p.value);
         typename TT::raw* vd = reinterpret_cast<typename TT::raw*>(p.value_cache);
-        for (int e = lane; e < D; e += 64) vd[cbase + e] = vs[sbase + e];
+        typename TT::raw* vo = reinterpret_cast<typename TT::raw*>(p.v_out);
+        for (int e = lane; e < D; e += 64) {
+          const typename TT::raw x = vs[vbase + e];
+          if (write_cache) vd[cbase + e] = x;
+          if (vo) vo[obase + e] = x;
+        }
       }
-    } else {
+    } else if (CK == kCacheFp8) {
       // fp8 cache: the (rotated) key row goes to k_out when transforming and is quantised
       // from registers; values are quantised from the input rows.
       const int64_t blk = write_cache ? slot / p.block_size : 0;
@@ -185,54 +281,69 @@ __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p
       uint8_t* vd = reinterpret_cast<uint8_t*>(p.value_cache);
       if (transform) {
         if (p.k_out || kd)
-          process_row<TT>(p, p.key, sbase, p.k_out, sbase, nullptr, 0, kd, cbase, ks, p.k_norm,
+          process_row<TT>(p, p.key, kbase, p.k_out, obase, nullptr, 0, kd, cbase, ks, p.k_norm,
                           pos, lane);
       } else if (write_cache) {
         for (int e = lane; e < D; e += 64) {
-          float kx = ldv<TT>(p.key, sbase + e);
+          float kx = ldv<TT>(p.key, kbase + e);
           kd[cbase + e] = ks == 0.0f ? 0 : (uint8_t)f32_to_e4m3_sat(kx / ks);
         }
       }
-      if (write_cache) {
+      if (write_cache || p.v_out)
         for (int e = lane; e < D; e += 64) {
-          float vx = ldv<TT>(p.value, sbase + e);
-          vd[cbase + e] = vsc == 0.0f ? 0 : (uint8_t)f32_to_e4m3_sat(vx / vsc);
+          float vx = ldv<TT>(p.value, vbase + e);
+          if (write_cache) vd[cbase + e] = vsc == 0.0f ? 0 : (uint8_t)f32_to_e4m3_sat(vx / vsc);
+          if (p.v_out) stv<TT>(p.v_out, obase + e, vx);
         }
-      }
+    } else {
+      uint8_t* kd = write_cache ? reinterpret_cast<uint8_t*>(p.key_cache) : nullptr;
+      uint8_t* vd = write_cache ? reinterpret_cast<uint8_t*>(p.value_cache) : nullptr;
+      if (kd || (transform && p.k_out))
+        int_row<TT, CK>(p, p.key, kbase, transform ? p.k_out : nullptr, obase, kd, cbase,
+                        p.k_scale, p.k_quant == PA_QUANT_PER_CHANNEL, kh, p.k_norm, true, pos,
+                        lane);
+      if (vd || p.v_out)  // values are neither normalised nor rotated
+        int_row<TT, CK>(p, p.value, vbase, p.v_out, obase, vd, cbase, p.v_scale,
+                        p.v_quant == PA_QUANT_PER_CHANNEL, kh, nullptr, false, pos, lane);
     }
   }
 }
 
 }  // namespace
 
+template <typename TT>
+void launch_append_t(const AppendParams& p, pa_dtype cache_dtype, dim3 grid, dim3 block,
+                     hipStream_t s) {
+  switch (cache_dtype) {
+    case PA_DTYPE_FP8_E4M3:
+      hipLaunchKernelGGL((rotary_append_kernel<TT, kCacheFp8>), grid, block, 0, s, p);
+      break;
+    case PA_DTYPE_INT8:
+      hipLaunchKernelGGL((rotary_append_kernel<TT, kCacheI8>), grid, block, 0, s, p);
+      break;
+    case PA_DTYPE_INT4:
+      hipLaunchKernelGGL((rotary_append_kernel<TT, kCacheI4>), grid, block, 0, s, p);
+      break;
+    default:
+      hipLaunchKernelGGL((rotary_append_kernel<TT, kCacheT>), grid, block, 0, s, p);
+      break;
+  }
+}
+
 hipError_t launch_rotary_append(const AppendParams& p, pa_dtype act, pa_dtype cache_dtype,
                                 hipStream_t s) {
   if (p.num_tokens <= 0) return hipSuccess;
-  const bool transform = p.cos_cache != nullptr || p.q_norm != nullptr;
+  const bool transform = p.cos_cache != nullptr || p.q_norm != nullptr || p.copy_rows;
   const int q_groups = (p.do_q && transform) ? (p.num_heads + 3) / 4 : 0;
   dim3 grid(p.num_tokens, 1 + q_groups), block(256);
-  const bool fp8 = cache_dtype == PA_DTYPE_FP8_E4M3;
+  if (cache_dtype != act && cache_dtype != PA_DTYPE_FP8_E4M3 && cache_dtype != PA_DTYPE_INT8 &&
+      cache_dtype != PA_DTYPE_INT4)
+    return hipErrorInvalidValue;
   switch (act) {
-    case PA_DTYPE_FLOAT16:
-      if (fp8)
-        hipLaunchKernelGGL((rotary_append_kernel<TF16, true>), grid, block, 0, s, p);
-      else
-        hipLaunchKernelGGL((rotary_append_kernel<TF16, false>), grid, block, 0, s, p);
-      break;
-    case PA_DTYPE_BFLOAT16:
-      if (fp8)
-        hipLaunchKernelGGL((rotary_append_kernel<TBF16, true>), grid, block, 0, s, p);
-      else
-        hipLaunchKernelGGL((rotary_append_kernel<TBF16, false>), grid, block, 0, s, p);
-      break;
-    case PA_DTYPE_FLOAT32:
-      if (fp8)
-        hipLaunchKernelGGL((rotary_append_kernel<TF32, true>), grid, block, 0, s, p);
-      else
-        hipLaunchKernelGGL((rotary_append_kernel<TF32, false>), grid, block, 0, s, p);
-      break;
-    default:
-      return hipErrorInvalidValue;
+    case PA_DTYPE_FLOAT16: launch_append_t<TF16>(p, cache_dtype, grid, block, s); break;
+    case PA_DTYPE_BFLOAT16: launch_append_t<TBF16>(p, cache_dtype, grid, block, s); break;
+    case PA_DTYPE_FLOAT32: launch_append_t<TF32>(p, cache_dtype, grid, block, s); break;
+    default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }

@@ -2,7 +2,8 @@
 //
 // One wavefront per (packed query token, query head, context chunk).  Lanes split head_dim;
 // each key costs one cross-lane sum.  This is the fp32 path (the ORT CPU GQA parity config)
-// and the fallback for shapes the MFMA kernels do not cover; it is not the hot path.
+// and the fallback for shapes the MFMA kernels do not cover, including integer (int8/int4)
+// pages, whose keys/values are code * scale in fp32; it is not the hot path.
 //
 // Semantics restated from _paged_ref (test_paged_attention.py:127-155) and the dense
 // fallback (attention.rs:4192-4319): positions < past read the cache pages through the block
@@ -10,40 +11,67 @@
 // p >= past + row - window + 1; softcap s -> c*tanh(s/c); a head sink adds exp(sink) to the
 // denominator only (attention_probs_with_sink :100-118).  Softmax runs in base 2 on
 // x = s*log2(e), which is the same function.
+#include <type_traits>
+
 #include "pa_device.hpp"
 
 namespace pa {
 
 namespace {
 
+// Element e of a cache row starting at storage index `base`, widened to fp32.  `scale` is the
+// fp8 per-(block, kv-head) scale or the integer per-tensor / per-channel scale of element e.
 template <typename CT>
 struct CacheRead;
 
 template <>
 struct CacheRead<TF16> {
-  __device__ static float at(const void* c, int64_t i, float) {
-    return f16_to_f32(reinterpret_cast<const uint16_t*>(c)[i]);
+  __device__ static float at(const void* c, int64_t base, int e, float) {
+    return f16_to_f32(reinterpret_cast<const uint16_t*>(c)[base + e]);
   }
 };
 template <>
 struct CacheRead<TBF16> {
-  __device__ static float at(const void* c, int64_t i, float) {
-    return bf16_to_f32(reinterpret_cast<const uint16_t*>(c)[i]);
+  __device__ static float at(const void* c, int64_t base, int e, float) {
+    return bf16_to_f32(reinterpret_cast<const uint16_t*>(c)[base + e]);
   }
 };
 template <>
 struct CacheRead<TF32> {
-  __device__ static float at(const void* c, int64_t i, float) {
-    return reinterpret_cast<const float*>(c)[i];
+  __device__ static float at(const void* c, int64_t base, int e, float) {
+    return reinterpret_cast<const float*>(c)[base + e];
   }
 };
 struct Fp8Cache {};
 template <>
 struct CacheRead<Fp8Cache> {
-  __device__ static float at(const void* c, int64_t i, float scale) {
-    return e4m3_to_f32(reinterpret_cast<const uint8_t*>(c)[i]) * scale;
+  __device__ static float at(const void* c, int64_t base, int e, float scale) {
+    return e4m3_to_f32(reinterpret_cast<const uint8_t*>(c)[base + e]) * scale;
   }
 };
+// Integer caches: QuantizedCache::decode (kv_cache.rs:222-256), code * scale in fp32.
+struct I8Cache {};
+template <>
+struct CacheRead<I8Cache> {
+  __device__ static float at(const void* c, int64_t base, int e, float scale) {
+    return (float)reinterpret_cast<const int8_t*>(c)[base + e] * scale;
+  }
+};
+struct I4Cache {};
+template <>
+struct CacheRead<I4Cache> {
+  __device__ static float at(const void* c, int64_t base, int e, float scale) {
+    const uint32_t byte = reinterpret_cast<const uint8_t*>(c)[base + (e >> 1)];
+    return (float)((int)((byte >> ((e & 1) * 4)) & 15u) - 8) * scale;
+  }
+};
+
+template <typename CT>
+constexpr bool kIntCache = false;
+template <>
+constexpr bool kIntCache<I8Cache> = true;
+template <>
+constexpr bool kIntCache<I4Cache> = true;
 
 constexpr int kMaxLanesElems = 4;  // head_dim <= 256
 
@@ -68,7 +96,10 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
   if (p.window > 0) lo = max(lo, rp - p.window + 1);
 
   const int64_t row = (int64_t)p.kv_heads * D;
-  float qv[kMaxLanesElems], o[kMaxLanesElems];
+  // Cache rows in storage units: int4 holds two channels per byte.
+  const int Dc = std::is_same<CT, I4Cache>::value ? (D + 1) >> 1 : D;
+  const int64_t crow = (int64_t)p.kv_heads * Dc;
+  float qv[kMaxLanesElems], o[kMaxLanesElems], ksv[kMaxLanesElems], vsv[kMaxLanesElems];
 #pragma unroll
   for (int k = 0; k < kMaxLanesElems; ++k) {
     int e = lane + 64 * k;
@@ -76,6 +107,11 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
                         p.q)[((int64_t)t * p.num_heads + h) * D + e])
                   : 0.0f;
     o[k] = 0.0f;
+    ksv[k] = vsv[k] = 1.0f;
+    if (kIntCache<CT> && e < D) {
+      ksv[k] = p.k_scale[p.k_quant == PA_QUANT_PER_CHANNEL ? (int64_t)kh * D + e : 0];
+      vsv[k] = p.v_scale[p.v_quant == PA_QUANT_PER_CHANNEL ? (int64_t)kh * D + e : 0];
+    }
   }
   float m = kNegInf, l = 0.0f;
   const float cap = p.softcap;
@@ -86,17 +122,17 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
     bool from_cache = pos < pastb || p.read_all_from_cache || p.linear_cap > 0;
     if (p.linear_cap > 0) {
       // contiguous [batch, kv_heads, cap, head_dim] cache holding the new rows too
-      off = (((int64_t)b * p.kv_heads + kh) * p.linear_cap + pos) * D;
+      off = (((int64_t)b * p.kv_heads + kh) * p.linear_cap + pos) * Dc;
       kb = p.key_cache;
       vb = p.value_cache;
     } else if (from_cache) {
       int64_t bi = pos / p.block_size;
       int64_t blk = p.block_table[(int64_t)b * p.max_blocks + min(bi, (int64_t)p.max_blocks - 1)];
       blk = min(max(blk, (int64_t)0), p.num_blocks - 1);
-      off = (blk * p.block_size + pos % p.block_size) * row + (int64_t)kh * D;
+      off = (blk * p.block_size + pos % p.block_size) * crow + (int64_t)kh * Dc;
       kb = p.key_cache;
       vb = p.value_cache;
-      if (p.k_scale) {
+      if (std::is_same<CT, Fp8Cache>::value) {
         ks = p.k_scale[blk * p.kv_heads + kh];
         vs = p.v_scale[blk * p.kv_heads + kh];
       }
@@ -111,7 +147,7 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
     for (int k = 0; k < kMaxLanesElems; ++k) {
       int e = lane + 64 * k;
       if (e < D) {
-        float kv = from_cache ? CacheRead<CT>::at(kb, off + e, ks)
+        float kv = from_cache ? CacheRead<CT>::at(kb, off, e, kIntCache<CT> ? ksv[k] : ks)
                               : TT::to_f32(reinterpret_cast<const typename TT::raw*>(kb)[off + e]);
         part += qv[k] * kv;
       }
@@ -127,7 +163,7 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
     for (int k = 0; k < kMaxLanesElems; ++k) {
       int e = lane + 64 * k;
       if (e < D) {
-        float vv = from_cache ? CacheRead<CT>::at(vb, off + e, vs)
+        float vv = from_cache ? CacheRead<CT>::at(vb, off, e, kIntCache<CT> ? vsv[k] : vs)
                               : TT::to_f32(reinterpret_cast<const typename TT::raw*>(vb)[off + e]);
         o[k] = o[k] * alpha + w * vv;
       }
@@ -216,10 +252,21 @@ __global__ __launch_bounds__(64) void split_reduce_kernel(const AttnParams p) {
 template <typename TT>
 hipError_t launch_generic_t(const AttnParams& p, pa_dtype cache_dtype, hipStream_t s) {
   dim3 grid(p.max_splits, p.num_heads, p.num_tokens), block(64);
-  if (cache_dtype == PA_DTYPE_FP8_E4M3)
-    hipLaunchKernelGGL((attn_generic_kernel<TT, Fp8Cache>), grid, block, 0, s, p);
-  else
-    hipLaunchKernelGGL((attn_generic_kernel<TT, TT>), grid, block, 0, s, p);
+  switch (cache_dtype) {
+    case PA_DTYPE_FP8_E4M3:
+      hipLaunchKernelGGL((attn_generic_kernel<TT, Fp8Cache>), grid, block, 0, s, p);
+      break;
+    case PA_DTYPE_INT8:
+      hipLaunchKernelGGL((attn_generic_kernel<TT, I8Cache>), grid, block, 0, s, p);
+      break;
+    case PA_DTYPE_INT4:
+      hipLaunchKernelGGL((attn_generic_kernel<TT, I4Cache>), grid, block, 0, s, p);
+      break;
+    default:
+      if (cache_dtype != TT::code) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((attn_generic_kernel<TT, TT>), grid, block, 0, s, p);
+      break;
+  }
   return hipGetLastError();
 }
 

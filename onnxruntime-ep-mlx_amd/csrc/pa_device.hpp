@@ -214,6 +214,17 @@ struct AppendParams {
   int32_t gqa_seq;
   const int32_t* seqlens_k;
   int32_t* meta_out;
+  // Input row strides in elements (packed QKV rows are (H + 2 KV) * D wide).  With copy_rows
+  // the query/key rows go to q_out/k_out and the value rows to v_out (contiguous [T, heads * D])
+  // even when nothing rotates or normalises them.
+  int64_t q_ld, k_ld, v_ld;
+  void* v_out;
+  int32_t copy_rows;
+  // Integer caches: scale layout per side (PA_QUANT_PER_TENSOR / PA_QUANT_PER_CHANNEL) and the
+  // encode rule: 0 divides by the scale (zero scale -> code 0), 1 multiplies by its reciprocal
+  // (zero scale read as 1).
+  int32_t k_quant, v_quant;
+  int32_t quant_reciprocal;
 };
 
 struct AttnParams {
@@ -251,6 +262,7 @@ struct AttnParams {
   // buffers; the new rows are already in them): position pos of (b, kv-head kh) is row
   // (b * kv_heads + kh) * linear_cap + pos.  0: paged cache.
   int32_t linear_cap;
+  int32_t k_quant, v_quant;  // integer caches: PA_QUANT_PER_TENSOR / PA_QUANT_PER_CHANNEL
 };
 
 // Final normalisation shared by every attention kernel: the factor that turns an output

@@ -18,8 +18,17 @@ PA_DTYPE_FLOAT16 = 1
 PA_DTYPE_BFLOAT16 = 2
 PA_DTYPE_FLOAT32 = 3
 PA_DTYPE_FP8_E4M3 = 4
+PA_DTYPE_INT8 = 5
+PA_DTYPE_INT4 = 6
 PA_INT32_DTYPE = 10
 PA_INT8_DTYPE = 11
+PA_UINT8_DTYPE = 12
+
+PA_QUANT_NONE = 0
+PA_QUANT_PER_TENSOR = 1
+PA_QUANT_PER_CHANNEL = 2
+QUANT_TYPES = {"NONE": PA_QUANT_NONE, "PER_TENSOR": PA_QUANT_PER_TENSOR,
+               "PER_CHANNEL": PA_QUANT_PER_CHANNEL}
 
 PA_OK = 0
 PA_ERR_INVALID_ARGUMENT = 1
@@ -46,6 +55,7 @@ class PaCache(C.Structure):
         ("k_scale", C.c_void_p), ("v_scale", C.c_void_p),
         ("num_blocks", C.c_int64), ("block_size", C.c_int32), ("kv_heads", C.c_int32),
         ("head_dim", C.c_int32), ("dtype", C.c_int),
+        ("k_quant_type", C.c_int32), ("v_quant_type", C.c_int32),
     ]
 
 
@@ -116,6 +126,8 @@ class PaGqaIO(C.Structure):
         ("rotary_positions", C.c_int64), ("rotary_half", C.c_int32),
         ("head_sink", C.c_void_p), ("q_norm_weight", C.c_void_p), ("k_norm_weight", C.c_void_p),
         ("output", C.c_void_p),
+        ("cache_dtype", C.c_int), ("k_scale", C.c_void_p), ("v_scale", C.c_void_p),
+        ("k_quant_type", C.c_int32), ("v_quant_type", C.c_int32),
     ]
 
 
@@ -131,6 +143,8 @@ class PaNodeInfo(C.Structure):
         ("local_window_size", C.c_int32), ("is_causal", C.c_int32),
         ("has_scale_attr", C.c_int32), ("softcap", C.c_float),
         ("kv_cache_layout_latent", C.c_int32),
+        ("k_quant_type", C.c_int32), ("v_quant_type", C.c_int32),
+        ("k_cache_dtype", C.c_int32), ("v_cache_dtype", C.c_int32),
     ]
 
 

@@ -25,6 +25,9 @@ _DTYPES = {
     torch.bfloat16: capi.PA_DTYPE_BFLOAT16,
     torch.float32: capi.PA_DTYPE_FLOAT32,
     torch.float8_e4m3fn: capi.PA_DTYPE_FP8_E4M3,
+    # integer cache storage (kv_cache.rs:8-13): int8 codes, uint8 = two int4 codes per byte
+    torch.int8: capi.PA_DTYPE_INT8,
+    torch.uint8: capi.PA_DTYPE_INT4,
 }
 
 
@@ -70,14 +73,39 @@ class _Workspace:
 _ws = _Workspace()
 
 
+def _quant(mode) -> int:
+    if isinstance(mode, str):
+        if mode not in capi.QUANT_TYPES:
+            raise ValueError(f"unknown quantization type {mode!r}")
+        return capi.QUANT_TYPES[mode]
+    return int(mode)
+
+
 def cache_desc(key_cache: torch.Tensor, value_cache: torch.Tensor,
                k_scale: torch.Tensor | None = None,
-               v_scale: torch.Tensor | None = None) -> capi.PaCache:
+               v_scale: torch.Tensor | None = None, *, head_dim: int | None = None,
+               k_quant_type="NONE", v_quant_type="NONE") -> capi.PaCache:
+    """Cache descriptor.  Integer caches (torch.int8 / torch.uint8 = int4) take fp32 scales
+    with k_quant_type / v_quant_type "PER_TENSOR" ([1]) or "PER_CHANNEL" ([kv_heads, head]);
+    an int4 cache's last dimension is ceil(head / 2), so pass head_dim for odd heads."""
     if key_cache.dim() != 4 or key_cache.shape != value_cache.shape:
         raise ValueError("key_cache must be [num_blocks,block_size,kv_num_heads,head_size]")
-    nb, bs, kv, d = key_cache.shape
+    if key_cache.dtype != value_cache.dtype:
+        raise ValueError("key/value caches must share one storage dtype")
+    nb, bs, kv, width = key_cache.shape
+    dt = pa_dtype(key_cache.dtype)
+    if head_dim is None:
+        head_dim = 2 * width if dt == capi.PA_DTYPE_INT4 else width
+    elif (head_dim + 1) // 2 != width if dt == capi.PA_DTYPE_INT4 else head_dim != width:
+        raise ValueError("key_cache must be [num_blocks,block_size,kv_num_heads,head_size]")
+    for name, t in (("k_scale", k_scale), ("v_scale", v_scale)):
+        if t is not None:
+            if t.dtype != torch.float32:
+                raise ValueError(f"{name} must be float32")
+            _need_cuda(name, t)
+            _contig(name, t)
     return capi.PaCache(_ptr(key_cache), _ptr(value_cache), _ptr(k_scale), _ptr(v_scale),
-                        nb, bs, kv, d, pa_dtype(key_cache.dtype))
+                        nb, bs, kv, head_dim, dt, _quant(k_quant_type), _quant(v_quant_type))
 
 
 def batch_desc(cum: torch.Tensor, past: torch.Tensor, block_table: torch.Tensor,
@@ -105,7 +133,9 @@ class PagePool:
                  dtype: torch.dtype, device: torch.device | str = "cuda"):
         lib = capi.load()
         self.device = torch.device(device)
-        self.shape = (num_blocks, block_size, kv_heads, head_dim)
+        self.head_dim = head_dim
+        width = (head_dim + 1) // 2 if dtype == torch.uint8 else head_dim  # int4: two per byte
+        self.shape = (num_blocks, block_size, kv_heads, width)
         self.dtype = dtype
         h = C.c_void_p()
         with torch.cuda.device(self.device):
@@ -160,14 +190,18 @@ def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, key_cache: torch.T
                       value_cache: torch.Tensor, cum: torch.Tensor, past: torch.Tensor,
                       block_table: torch.Tensor, slot_mapping: torch.Tensor | None = None,
                       k_scale: torch.Tensor | None = None,
-                      v_scale: torch.Tensor | None = None, slots_distinct: bool = False) -> None:
+                      v_scale: torch.Tensor | None = None, slots_distinct: bool = False, *,
+                      k_quant_type="NONE", v_quant_type="NONE") -> None:
     """Append key/value rows to the pages (last writer wins on shared slots unless the caller
     asserts `slots_distinct`, which skips that check)."""
     lib = capi.load()
     for n, t in (("key", key), ("value", value), ("key_cache", key_cache)):
         _need_cuda(n, t)
         _contig(n, t)
-    cache = cache_desc(key_cache, value_cache, k_scale, v_scale)
+    kv = key_cache.shape[2]
+    cache = cache_desc(key_cache, value_cache, k_scale, v_scale,
+                       head_dim=key.shape[-1] // kv, k_quant_type=k_quant_type,
+                       v_quant_type=v_quant_type)
     batch = batch_desc(cum, past, block_table, key.shape[0], slot_mapping, 0,
                        capi.PA_BATCH_SLOTS_DISTINCT if slots_distinct else 0)
     capi.check(lib.pa_reshape_and_cache(C.byref(cache), C.byref(batch), pa_dtype(key.dtype),
@@ -178,10 +212,12 @@ def rotary_append(query, key, value, key_cache, value_cache, cum, past, block_ta
                   num_heads, cos_cache=None, sin_cache=None, rotary_offset=0,
                   rotary_interleaved=0, q_norm_weight=None, k_norm_weight=None,
                   qk_norm_epsilon=1e-6, slot_mapping=None, k_scale=None, v_scale=None,
-                  slots_distinct=False):
+                  slots_distinct=False, k_quant_type="NONE", v_quant_type="NONE"):
     """Fused RMSNorm + RoPE + append.  Returns the transformed (query, key) rows."""
     lib = capi.load()
-    cache = cache_desc(key_cache, value_cache, k_scale, v_scale)
+    cache = cache_desc(key_cache, value_cache, k_scale, v_scale,
+                       head_dim=key.shape[-1] // key_cache.shape[2], k_quant_type=k_quant_type,
+                       v_quant_type=v_quant_type)
     batch = batch_desc(cum, past, block_table, key.shape[0], slot_mapping, 0,
                        capi.PA_BATCH_SLOTS_DISTINCT if slots_distinct else 0)
     transform = cos_cache is not None or q_norm_weight is not None
@@ -201,11 +237,13 @@ def rotary_append(query, key, value, key_cache, value_cache, cum, past, block_ta
 def attention(q, k_new, v_new, key_cache, value_cache, cum, past, block_table, *, num_heads,
               scale=0.0, softcap=0.0, local_window_size=-1, is_causal=1, head_sink=None,
               k_scale=None, v_scale=None, max_query_len=0, kind=0, chunk=0, out=None,
-              new_rows_in_cache=False):
+              new_rows_in_cache=False, k_quant_type="NONE", v_quant_type="NONE"):
     """Attention over the (already appended) paged cache; kind/chunk force a kernel family.
     new_rows_in_cache: the caller appended k_new/v_new into distinct block-table slots."""
     lib = capi.load()
-    cache = cache_desc(key_cache, value_cache, k_scale, v_scale)
+    cache = cache_desc(key_cache, value_cache, k_scale, v_scale,
+                       head_dim=q.shape[-1] // num_heads, k_quant_type=k_quant_type,
+                       v_quant_type=v_quant_type)
     batch = batch_desc(cum, past, block_table, q.shape[0], None, max_query_len,
                        capi.PA_BATCH_NEW_ROWS_IN_CACHE if new_rows_in_cache else 0)
     attn = attn_desc(num_heads, scale, softcap, local_window_size, is_causal, head_sink)
@@ -227,13 +265,16 @@ def paged_attention(query, key, value, key_cache, value_cache, cumulative_sequen
                     k_scale=None, v_scale=None, attention_metadata=None, *, num_heads,
                     kv_num_heads, scale=0.0, softcap=0.0, local_window_size=-1, do_rotary=0,
                     rotary_interleaved=0, rotary_offset=0, is_causal=1, qk_norm_epsilon=1e-6,
-                    validate=True, output=None):
+                    k_quant_type="NONE", v_quant_type="NONE", validate=True, output=None):
     """com.microsoft::PagedAttention on MI355X (operator-level entry, pa_paged_attention).
 
     ``attention_metadata`` is accepted and ignored, like the reference
     (test_attention_contracts.py:338-367).  With ``validate`` the int32 metadata is copied to
     the host and checked with the reference's rules (attention.rs:3934-3990), which is what the
-    reference does every step; without it the device copies are trusted.
+    reference does every step; without it the device copies are trusted.  ``key`` and
+    ``value`` both None means packed QKV: ``query`` is [T, (num_heads + 2 kv_num_heads) * head].
+    Integer caches (torch.int8, torch.uint8 = int4) take ``k_scale``/``v_scale`` with
+    ``k_quant_type``/``v_quant_type`` "PER_TENSOR" or "PER_CHANNEL".
     """
     del attention_metadata
     lib = capi.load()
@@ -243,6 +284,8 @@ def paged_attention(query, key, value, key_cache, value_cache, cumulative_sequen
                  ("value_cache", value_cache)):
         _need_cuda(n, t)
         _contig(n, t)
+    packed = key is None and value is None
+    head = query.shape[1] // (num_heads + 2 * kv_num_heads if packed else num_heads)
     node = capi.PaNode(num_heads, kv_num_heads, scale, softcap, local_window_size, do_rotary,
                        rotary_interleaved, rotary_offset, is_causal, qk_norm_epsilon)
     host = {}
@@ -251,8 +294,9 @@ def paged_attention(query, key, value, key_cache, value_cache, cumulative_sequen
                         ("bt", block_table), ("slots", slot_mapping)):
             host[name] = None if t is None else t.detach().to("cpu").contiguous()
     if output is None:
-        output = torch.empty_like(query)
-    cache = cache_desc(key_cache, value_cache, k_scale, v_scale)
+        output = query.new_empty((query.shape[0], num_heads * head))
+    cache = cache_desc(key_cache, value_cache, k_scale, v_scale, head_dim=head,
+                       k_quant_type=k_quant_type, v_quant_type=v_quant_type)
     io = capi.PaIO(
         pa_dtype(query.dtype), query.shape[0], query.shape[1], _ptr(query), _ptr(key),
         _ptr(value), cache, _ptr(cumulative_sequence_length), _ptr(past_seqlens),
@@ -275,23 +319,32 @@ def group_query_attention(query, key, value, present_key, present_value, seqlens
                           q_norm_weight=None, k_norm_weight=None, *, num_heads, kv_num_heads,
                           scale=0.0, softcap=0.0, local_window_size=-1, do_rotary=0,
                           rotary_interleaved=0, is_causal=1, qk_norm_epsilon=1e-6,
+                          k_scale=None, v_scale=None, k_quant_type="NONE", v_quant_type="NONE",
                           validate=True, output=None):
     """com.microsoft::GroupQueryAttention on MI355X (pa_group_query_attention), shared-buffer
     contract: present_key/present_value [B, kv_heads, capacity, head] hold the past rows and are
     updated in place with the new rows at [seqlens_k[b] + 1 - S, seqlens_k[b] + 1).
+    ``key``/``value`` None: packed QKV query [B, S, (H + 2 KV) * head].  Integer present caches
+    (torch.int8, or torch.uint8 with [.., ceil(head / 2)] rows = int4, "kv_cache_bit_width" 4)
+    take ``k_scale``/``v_scale`` (inputs 12/13) with "PER_TENSOR" / "PER_CHANNEL" modes.
     Returns (output, present_key, present_value)."""
     lib = capi.load()
     if query.dim() != 3:
         raise ValueError("query must have rank 3 [batch, sequence, hidden]")
     for n, t in (("query", query), ("key", key), ("value", value),
-                 ("present_key", present_key), ("present_value", present_value)):
+                 ("present_key", present_key), ("present_value", present_value),
+                 ("k_scale", k_scale), ("v_scale", v_scale)):
         _need_cuda(n, t)
         _contig(n, t)
     if seqlens_k.dtype != torch.int32:
         raise ValueError("input seqlens_k must be int32")
+    packed = key is None and value is None
+    head = query.shape[2] // (num_heads + 2 * kv_num_heads if packed else num_heads)
     host = seqlens_k.detach().to("cpu").contiguous() if validate else None
     if output is None:
-        output = torch.empty_like(query)
+        output = query.new_empty((query.shape[0], query.shape[1], num_heads * head))
+    cache_dt = present_key.dtype
+    cache_code = 0 if cache_dt == query.dtype else pa_dtype(cache_dt)
     node = capi.PaGqaNode(num_heads, kv_num_heads, scale, softcap, local_window_size, do_rotary,
                           rotary_interleaved, is_causal, qk_norm_epsilon)
     io = capi.PaGqaIO(
@@ -301,7 +354,8 @@ def group_query_attention(query, key, value, present_key, present_value, seqlens
         _ptr(cos_cache) if do_rotary else None, _ptr(sin_cache) if do_rotary else None,
         cos_cache.shape[0] if (do_rotary and cos_cache is not None) else 0,
         cos_cache.shape[1] if (do_rotary and cos_cache is not None) else 0,
-        _ptr(head_sink), _ptr(q_norm_weight), _ptr(k_norm_weight), _ptr(output))
+        _ptr(head_sink), _ptr(q_norm_weight), _ptr(k_norm_weight), _ptr(output), cache_code,
+        _ptr(k_scale), _ptr(v_scale), _quant(k_quant_type), _quant(v_quant_type))
     nbytes = lib.pa_group_query_attention_workspace_bytes(C.byref(node), C.byref(io))
     ws = _ws.get(max(nbytes, 1), query.device)
     capi.check(lib.pa_group_query_attention(C.byref(node), C.byref(io), _ptr(ws), nbytes,

@@ -91,6 +91,61 @@ uint8_t orc_f32_to_e4m3(float f) {
   return s | (uint8_t)(((E + 7) << 3) | ((int)q - 8));
 }
 
+/* --------------------------------------------------------- integer caches (a11) */
+/* QuantizedCache::encode (kv_cache.rs:170-199): divisor = scale, or 1 where scale == 0; the
+ * paged rule divides and then writes 0 where scale == 0 (:186-188), the GQA rule multiplies by
+ * fp32(1 / divisor) (:189-191); then mlx_clip to the code range and mlx_round (half to even). */
+int orc_int_code(float x, float scale, int bits, int reciprocal) {
+  float divisor = scale == 0.0f ? 1.0f : scale;
+  float y;
+  if (reciprocal) {
+    float r = 1.0f / divisor;
+    y = x * r;
+  } else {
+    y = scale == 0.0f ? 0.0f : x / divisor;
+  }
+  if (isnan(y)) return 0;
+  float lo = bits == 4 ? -8.0f : -128.0f, hi = bits == 4 ? 7.0f : 127.0f;
+  if (y < lo) y = lo;
+  if (y > hi) y = hi;
+  return (int)rintf(y); /* default rounding mode: to nearest, ties to even */
+}
+
+/* int4 packing (kv_cache.rs:196-219): biased = code + 8, an odd row padded with 8, byte =
+ * low + 16 * high over (even, odd) channel pairs. */
+void orc_int_encode_row(const float* x, int head_dim, const float* scale, int per_channel,
+                        int bits, int reciprocal, uint8_t* dst) {
+  if (bits == 8) {
+    for (int e = 0; e < head_dim; ++e)
+      dst[e] = (uint8_t)(int8_t)orc_int_code(x[e], scale[per_channel ? e : 0], 8, reciprocal);
+    return;
+  }
+  for (int j = 0; j < (head_dim + 1) / 2; ++j) {
+    int e0 = 2 * j, e1 = 2 * j + 1;
+    int lo = orc_int_code(x[e0], scale[per_channel ? e0 : 0], 4, reciprocal) + 8;
+    int hi = e1 < head_dim ? orc_int_code(x[e1], scale[per_channel ? e1 : 0], 4, reciprocal) + 8
+                           : 8;
+    dst[j] = (uint8_t)(lo + 16 * hi);
+  }
+}
+
+/* QuantizedCache::decode (kv_cache.rs:222-256): int4 splits (byte & 15, byte >> 4), slices to
+ * head_dim and subtracts 8; both widths multiply by the scale in fp32. */
+void orc_int_decode_row(const uint8_t* src, int head_dim, const float* scale, int per_channel,
+                        int bits, float* out) {
+  for (int e = 0; e < head_dim; ++e) {
+    float code = bits == 8 ? (float)(int8_t)src[e]
+                           : (float)((e & 1 ? src[e / 2] >> 4 : src[e / 2] & 15) - 8);
+    out[e] = code * scale[per_channel ? e : 0];
+  }
+}
+
+static inline int is_int_dt(int dt) { return dt == ORC_I8 || dt == ORC_I4; }
+/* storage units (elements, or int4 bytes) of one kv-head row */
+static inline int cache_width(int dt, int head_dim) {
+  return dt == ORC_I4 ? (head_dim + 1) / 2 : head_dim;
+}
+
 static inline float ld(const void* p, int64_t i, int dt) {
   switch (dt) {
     case ORC_F16: return orc_f16_to_f32(((const uint16_t*)p)[i]);
@@ -203,20 +258,43 @@ static uint8_t quant_e4m3(float x, float scale) {
 
 int orc_reshape_and_cache(const void* key, const void* value, int act_dtype, void* key_cache,
                           void* value_cache, int cache_dtype, const float* k_scale,
-                          const float* v_scale, const int32_t* cum, const int32_t* past,
-                          const int32_t* block_table, int batch, int max_blocks,
-                          const int32_t* slot_mapping, int64_t num_blocks, int block_size,
-                          int kv_heads, int head_dim) {
+                          const float* v_scale, int k_mode, int v_mode, const int32_t* cum,
+                          const int32_t* past, const int32_t* block_table, int batch,
+                          int max_blocks, const int32_t* slot_mapping, int64_t num_blocks,
+                          int block_size, int kv_heads, int head_dim) {
   int64_t row = (int64_t)kv_heads * head_dim;
+  int width = cache_width(cache_dtype, head_dim);
+  float* tmp = NULL;
+  if (is_int_dt(cache_dtype)) {
+    tmp = (float*)malloc((size_t)head_dim * sizeof(float));
+    if (!tmp) return 4;
+  }
   for (int b = 0; b < batch; ++b) {
     int nq = cum[b + 1] - cum[b];
     for (int j = 0; j < nq; ++j) {
       int64_t slot;
       token_slot(cum, past, block_table, b, max_blocks, slot_mapping, j, block_size, &slot);
       if (slot < 0) continue;
-      if (slot >= num_blocks * block_size) return 3;
+      if (slot >= num_blocks * block_size) {
+        free(tmp);
+        return 3;
+      }
       int64_t t = cum[b] + j;
-      if (cache_dtype == ORC_E4M3) {
+      if (is_int_dt(cache_dtype)) {
+        int bits = cache_dtype == ORC_I8 ? 8 : 4;
+        for (int kh = 0; kh < kv_heads; ++kh)
+          for (int side = 0; side < 2; ++side) {
+            const void* src = side ? value : key;
+            const float* sc = side ? v_scale : k_scale;
+            int pc = (side ? v_mode : k_mode) == ORC_QUANT_PER_CHANNEL;
+            uint8_t* dst = (uint8_t*)(side ? value_cache : key_cache) +
+                           (slot * kv_heads + kh) * (int64_t)width;
+            for (int i = 0; i < head_dim; ++i)
+              tmp[i] = ld(src, t * row + (int64_t)kh * head_dim + i, act_dtype);
+            orc_int_encode_row(tmp, head_dim, pc ? sc + (int64_t)kh * head_dim : sc, pc, bits, 0,
+                               dst);
+          }
+      } else if (cache_dtype == ORC_E4M3) {
         int64_t blk = slot / block_size;
         for (int kh = 0; kh < kv_heads; ++kh) {
           float ks = k_scale[blk * kv_heads + kh], vs = v_scale[blk * kv_heads + kh];
@@ -236,32 +314,44 @@ int orc_reshape_and_cache(const void* key, const void* value, int act_dtype, voi
       }
     }
   }
+  free(tmp);
   return 0;
 }
 
 /* ----------------------------------------------------------------------- attention (a8) */
 
-static double cache_elem(const void* cache, int cache_dtype, const float* scales, int64_t blk,
-                         int kv_heads, int kh, int64_t idx) {
+/* Element e of the kv-head row at storage index `base` (block blk, kv-head kh), as the
+ * attention reads it: T, fp8 code * block scale, or integer code * scale (fp32). */
+static double cache_elem(const void* cache, int cache_dtype, const float* scales, int mode,
+                         int64_t blk, int kv_heads, int kh, int head_dim, int64_t base, int e) {
   if (cache_dtype == ORC_E4M3) {
-    float v = orc_e4m3_to_f32(((const uint8_t*)cache)[idx]) * scales[blk * kv_heads + kh];
+    float v = orc_e4m3_to_f32(((const uint8_t*)cache)[base + e]) * scales[blk * kv_heads + kh];
     return (double)v;
   }
-  return (double)ld(cache, idx, cache_dtype);
+  if (is_int_dt(cache_dtype)) {
+    const uint8_t* row = (const uint8_t*)cache + base;
+    float code = cache_dtype == ORC_I8 ? (float)(int8_t)row[e]
+                                       : (float)((e & 1 ? row[e / 2] >> 4 : row[e / 2] & 15) - 8);
+    float s = scales[mode == ORC_QUANT_PER_CHANNEL ? (int64_t)kh * head_dim + e : 0];
+    return (double)(code * s);
+  }
+  return (double)ld(cache, base + e, cache_dtype);
 }
 
 int orc_paged_attention(const void* q, const void* k_new, const void* v_new, int act_dtype,
                         const void* key_cache, const void* value_cache, int cache_dtype,
-                        const float* k_scale, const float* v_scale, const int32_t* cum,
-                        const int32_t* past, const int32_t* block_table, int batch,
-                        int max_blocks, int64_t num_blocks, int block_size, int num_heads,
-                        int kv_heads, int head_dim, float scale, float softcap, int window,
-                        int causal, const float* head_sink, double* out) {
+                        const float* k_scale, const float* v_scale, int k_mode, int v_mode,
+                        const int32_t* cum, const int32_t* past, const int32_t* block_table,
+                        int batch, int max_blocks, int64_t num_blocks, int block_size,
+                        int num_heads, int kv_heads, int head_dim, float scale, float softcap,
+                        int window, int causal, const float* head_sink, double* out) {
   (void)num_blocks;
   int g = num_heads / kv_heads;
   int d = head_dim;
   int64_t row = (int64_t)kv_heads * d;
-  int quant = cache_dtype == ORC_E4M3;
+  int width = cache_width(cache_dtype, d);
+  int64_t crow = (int64_t)kv_heads * width;
+  int quant = cache_dtype == ORC_E4M3 || is_int_dt(cache_dtype);
   double* scores = NULL;
   size_t cap = 0;
   for (int b = 0; b < batch; ++b) {
@@ -289,10 +379,11 @@ int orc_paged_attention(const void* q, const void* k_new, const void* v_new, int
           double dot = 0.0;
           if (p < pastb || quant) {
             int64_t blk = block_table[(int64_t)b * max_blocks + p / block_size];
-            int64_t base = (blk * block_size + p % block_size) * row + (int64_t)kh * d;
+            int64_t base = (blk * block_size + p % block_size) * crow + (int64_t)kh * width;
             for (int e = 0; e < d; ++e)
               dot += (double)ld(q, qbase + e, act_dtype) *
-                     cache_elem(key_cache, cache_dtype, k_scale, blk, kv_heads, kh, base + e);
+                     cache_elem(key_cache, cache_dtype, k_scale, k_mode, blk, kv_heads, kh, d,
+                                base, e);
           } else {
             int64_t base = (s0 + (p - pastb)) * row + (int64_t)kh * d;
             for (int e = 0; e < d; ++e)
@@ -315,9 +406,10 @@ int orc_paged_attention(const void* q, const void* k_new, const void* v_new, int
           l += w;
           if (p < pastb || quant) {
             int64_t blk = block_table[(int64_t)b * max_blocks + p / block_size];
-            int64_t base = (blk * block_size + p % block_size) * row + (int64_t)kh * d;
+            int64_t base = (blk * block_size + p % block_size) * crow + (int64_t)kh * width;
             for (int e = 0; e < d; ++e)
-              o[e] += w * cache_elem(value_cache, cache_dtype, v_scale, blk, kv_heads, kh, base + e);
+              o[e] += w * cache_elem(value_cache, cache_dtype, v_scale, v_mode, blk, kv_heads, kh,
+                                     d, base, e);
           } else {
             int64_t base = (s0 + (p - pastb)) * row + (int64_t)kh * d;
             for (int e = 0; e < d; ++e) o[e] += w * (double)ld(v_new, base + e, act_dtype);
@@ -336,7 +428,7 @@ int orc_paged_attention(const void* q, const void* k_new, const void* v_new, int
 int orc_paged_attention_op(int act_dtype, int cache_dtype, const void* query, const void* key,
                            const void* value, int64_t num_tokens, void* key_cache,
                            void* value_cache, const float* k_scale, const float* v_scale,
-                           int64_t num_blocks, int block_size, const int32_t* cum,
+                           int k_mode, int v_mode, int64_t num_blocks, int block_size, const int32_t* cum,
                            const int32_t* past, const int32_t* block_table, int batch,
                            int max_blocks, const void* cos_cache, const void* sin_cache,
                            int64_t cos_rows, int rot_half, int rot_offset, int interleaved,
@@ -372,13 +464,13 @@ int orc_paged_attention_op(int act_dtype, int cache_dtype, const void* query, co
     if (rc) goto done;
   }
   rc = orc_reshape_and_cache(kr, value, act_dtype, key_cache, value_cache, cache_dtype, k_scale,
-                             v_scale, cum, past, block_table, batch, max_blocks, slot_mapping,
-                             num_blocks, block_size, kv_heads, head_dim);
+                             v_scale, k_mode, v_mode, cum, past, block_table, batch, max_blocks,
+                             slot_mapping, num_blocks, block_size, kv_heads, head_dim);
   if (rc) goto done;
   rc = orc_paged_attention(qr, kr, value, act_dtype, key_cache, value_cache, cache_dtype, k_scale,
-                           v_scale, cum, past, block_table, batch, max_blocks, num_blocks,
-                           block_size, num_heads, kv_heads, head_dim, scale, softcap, window,
-                           causal, head_sink, out);
+                           v_scale, k_mode, v_mode, cum, past, block_table, batch, max_blocks,
+                           num_blocks, block_size, num_heads, kv_heads, head_dim, scale, softcap,
+                           window, causal, head_sink, out);
   if (!rc && out_t) {
     int64_t n = num_tokens * (int64_t)num_heads * head_dim;
     for (int64_t i = 0; i < n; ++i) st(out_t, i, (float)out[i], act_dtype);
@@ -397,25 +489,61 @@ done:
 int orc_gqa_contiguous(int dtype, const void* query, const void* key, const void* value,
                        void* present_k, void* present_v, int batch, int seq, int num_heads,
                        int kv_heads, int head_dim, int cap, const int32_t* seqlens_k,
-                       float scale, float softcap, int window, int causal, double* out) {
+                       float scale, float softcap, int window, int causal, double* out,
+                       int cache_dtype, const float* k_scale, const float* v_scale, int k_mode,
+                       int v_mode) {
   int g = num_heads / kv_heads, d = head_dim;
+  int quant = is_int_dt(cache_dtype);
+  int width = quant ? cache_width(cache_dtype, d) : d;
+  int bits = cache_dtype == ORC_I8 ? 8 : 4;
+  int kpc = k_mode == ORC_QUANT_PER_CHANNEL, vpc = v_mode == ORC_QUANT_PER_CHANNEL;
   double* scores = (double*)malloc((size_t)(cap > 0 ? cap : 1) * sizeof(double));
-  if (!scores) return 4;
-  for (int b = 0; b < batch; ++b) {
+  float* tmp = (float*)malloc((size_t)d * sizeof(float));
+  float* kd = (float*)malloc((size_t)d * sizeof(float));
+  if (!scores || !tmp || !kd) {
+    free(scores);
+    free(tmp);
+    free(kd);
+    return 4;
+  }
+  int rc = 0;
+  /* row p of (b, kh) of a present cache, widened as the attention reads it */
+  #define PRESENT_ROW(buf, sc, pc, p, outrow)                                                  \
+    do {                                                                                      \
+      int64_t r_ = ((int64_t)b * kv_heads + kh) * cap + (p);                                  \
+      if (quant)                                                                              \
+        orc_int_decode_row((const uint8_t*)(buf) + r_ * width, d,                             \
+                           (pc) ? (sc) + (int64_t)kh * d : (sc), (pc), bits, (outrow));       \
+      else                                                                                    \
+        for (int e_ = 0; e_ < d; ++e_) (outrow)[e_] = ld((buf), r_ * d + e_, dtype);          \
+    } while (0)
+  for (int b = 0; b < batch && !rc; ++b) {
     int total = seqlens_k[b] + 1;
     int pastb = total - seq;
     if (pastb < 0 || total > cap) {
-      free(scores);
-      return 5;
+      rc = 5;
+      break;
     }
     for (int j = 0; j < seq; ++j)
-      for (int kh = 0; kh < kv_heads; ++kh)
-        for (int e = 0; e < d; ++e) {
-          int64_t src = (((int64_t)b * seq + j) * kv_heads + kh) * d + e;
-          int64_t dst = (((int64_t)b * kv_heads + kh) * cap + pastb + j) * d + e;
-          st(present_k, dst, ld(key, src, dtype), dtype);
-          st(present_v, dst, ld(value, src, dtype), dtype);
+      for (int kh = 0; kh < kv_heads; ++kh) {
+        int64_t src = (((int64_t)b * seq + j) * kv_heads + kh) * d;
+        int64_t dst = ((int64_t)b * kv_heads + kh) * cap + pastb + j;
+        if (quant) {
+          for (int side = 0; side < 2; ++side) {
+            const void* in = side ? value : key;
+            const float* sc = side ? v_scale : k_scale;
+            int pc = side ? vpc : kpc;
+            for (int e = 0; e < d; ++e) tmp[e] = ld(in, src + e, dtype);
+            orc_int_encode_row(tmp, d, pc ? sc + (int64_t)kh * d : sc, pc, bits, 1,
+                               (uint8_t*)(side ? present_v : present_k) + dst * width);
+          }
+        } else {
+          for (int e = 0; e < d; ++e) {
+            st(present_k, dst * d + e, ld(key, src + e, dtype), dtype);
+            st(present_v, dst * d + e, ld(value, src + e, dtype), dtype);
+          }
         }
+      }
     for (int i = 0; i < seq; ++i)
       for (int h = 0; h < num_heads; ++h) {
         int kh = h / g;
@@ -425,10 +553,9 @@ int orc_gqa_contiguous(int dtype, const void* query, const void* key, const void
         int64_t qb = (((int64_t)b * seq + i) * num_heads + h) * d;
         double m = -INFINITY;
         for (int p = start; p < end; ++p) {
-          int64_t kb = (((int64_t)b * kv_heads + kh) * cap + p) * d;
+          PRESENT_ROW(present_k, k_scale, kpc, p, kd);
           double dot = 0.0;
-          for (int e = 0; e < d; ++e)
-            dot += (double)ld(query, qb + e, dtype) * (double)ld(present_k, kb + e, dtype);
+          for (int e = 0; e < d; ++e) dot += (double)ld(query, qb + e, dtype) * (double)kd[e];
           double s = (double)scale * dot;
           if (softcap > 0.0f) s = (double)softcap * tanh(s / (double)softcap);
           scores[p] = s;
@@ -440,13 +567,16 @@ int orc_gqa_contiguous(int dtype, const void* query, const void* key, const void
         for (int p = start; p < end; ++p) {
           double w = exp(scores[p] - m);
           l += w;
-          int64_t vb = (((int64_t)b * kv_heads + kh) * cap + p) * d;
-          for (int e = 0; e < d; ++e) o[e] += w * (double)ld(present_v, vb + e, dtype);
+          PRESENT_ROW(present_v, v_scale, vpc, p, kd);
+          for (int e = 0; e < d; ++e) o[e] += w * (double)kd[e];
         }
         if (l != 0.0)
           for (int e = 0; e < d; ++e) o[e] /= l;
       }
   }
+  #undef PRESENT_ROW
   free(scores);
-  return 0;
+  free(tmp);
+  free(kd);
+  return rc;
 }

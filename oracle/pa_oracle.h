@@ -26,7 +26,9 @@
 extern "C" {
 #endif
 
-enum { ORC_F16 = 1, ORC_BF16 = 2, ORC_F32 = 3, ORC_E4M3 = 4 };
+enum { ORC_F16 = 1, ORC_BF16 = 2, ORC_F32 = 3, ORC_E4M3 = 4, ORC_I8 = 5, ORC_I4 = 6 };
+/* Integer cache scale layouts (k_quant_type / v_quant_type): one scale, or [kv_heads, d]. */
+enum { ORC_QUANT_NONE = 0, ORC_QUANT_PER_TENSOR = 1, ORC_QUANT_PER_CHANNEL = 2 };
 
 /* Scalar converters (round-to-nearest-even from IEEE-754 / OCP FP8 definitions). */
 uint16_t orc_f32_to_bf16(float f);
@@ -35,6 +37,20 @@ uint16_t orc_f32_to_f16(float f);
 float orc_f16_to_f32(uint16_t h);
 uint8_t orc_f32_to_e4m3(float f); /* RNE, saturating to +-448, NaN -> 0x7f */
 float orc_e4m3_to_f32(uint8_t c);
+
+/* Integer KV code of one value (QuantizedCache::encode, kv_cache.rs:170-199; byte equations of
+ * test_quantized_kv.py:22-37): reciprocal = 0 is the paged rule x / scale with a zero scale
+ * giving 0; reciprocal = 1 is the GroupQueryAttention (MLAS) rule x * fp32(1 / scale) with a zero
+ * scale read as 1.  Clip to [-2^(bits-1), 2^(bits-1) - 1], round half to even.  NaN -> 0. */
+int orc_int_code(float x, float scale, int bits, int reciprocal);
+/* One kv-head row of head_dim values -> int8 codes, or int4 bytes (code + 8, channel 2i in the
+ * low nibble, 2i+1 in the high nibble, an odd row's last high nibble 8).  scale points at the
+ * single per-tensor scale or at this row's head_dim channel scales (per_channel). */
+void orc_int_encode_row(const float* x, int head_dim, const float* scale, int per_channel,
+                        int bits, int reciprocal, uint8_t* dst);
+/* QuantizedCache::decode (kv_cache.rs:222-256): code * scale in fp32. */
+void orc_int_decode_row(const uint8_t* src, int head_dim, const float* scale, int per_channel,
+                        int bits, float* out);
 
 /* Bulk converters between float32 and a storage dtype. */
 void orc_encode(const float* src, void* dst, int64_t n, int dtype);
@@ -52,20 +68,26 @@ int orc_rope_rows(void* x, int64_t rows, int heads, int head_dim, const int32_t*
                   int offset, int interleaved, int dtype);
 
 /* Slot rule + scatter (attention.rs:4064-4120; test_paged_attention.py:117-126).
- * cache_dtype == ORC_E4M3 quantises x / scale[block, kv-head] (zero scale -> 0). */
+ * cache_dtype == ORC_E4M3 quantises x / scale[block, kv-head] (zero scale -> 0); ORC_I8 / ORC_I4
+ * store integer codes (paged divide rule) with per-tensor or per-channel scales given by
+ * k_mode / v_mode (ORC_QUANT_*); int4 rows are (head_dim + 1) / 2 bytes. */
 int orc_reshape_and_cache(const void* key, const void* value, int act_dtype, void* key_cache,
                           void* value_cache, int cache_dtype, const float* k_scale,
-                          const float* v_scale, const int32_t* cum, const int32_t* past,
+                          const float* v_scale, int k_mode, int v_mode, const int32_t* cum,
+                          const int32_t* past,
                           const int32_t* block_table, int batch, int max_blocks,
                           const int32_t* slot_mapping, int64_t num_blocks, int block_size,
                           int kv_heads, int head_dim);
 
 /* Attention after append, in double (_paged_ref test_paged_attention.py:127-155, dense
  * fallback attention.rs:4192-4319, sink/softcap :79-118). q/k_new/v_new are the rotated rows in
- * act_dtype.  head_sink: fp32 [H] or NULL.  out: [num_tokens, H*head_dim] doubles. */
+ * act_dtype.  head_sink: fp32 [H] or NULL.  out: [num_tokens, H*head_dim] doubles.
+ * Quantised caches (fp8, int8, int4) read every position, new rows included, from the pages
+ * (attention.rs:4192-4195). */
 int orc_paged_attention(const void* q, const void* k_new, const void* v_new, int act_dtype,
                         const void* key_cache, const void* value_cache, int cache_dtype,
-                        const float* k_scale, const float* v_scale, const int32_t* cum,
+                        const float* k_scale, const float* v_scale, int k_mode, int v_mode,
+                        const int32_t* cum,
                         const int32_t* past, const int32_t* block_table, int batch,
                         int max_blocks, int64_t num_blocks, int block_size, int num_heads,
                         int kv_heads, int head_dim, float scale, float softcap, int window,
@@ -77,7 +99,7 @@ int orc_paged_attention(const void* q, const void* k_new, const void* v_new, int
 int orc_paged_attention_op(int act_dtype, int cache_dtype, const void* query, const void* key,
                            const void* value, int64_t num_tokens, void* key_cache,
                            void* value_cache, const float* k_scale, const float* v_scale,
-                           int64_t num_blocks, int block_size, const int32_t* cum,
+                           int k_mode, int v_mode, int64_t num_blocks, int block_size, const int32_t* cum,
                            const int32_t* past, const int32_t* block_table, int batch,
                            int max_blocks, const void* cos_cache, const void* sin_cache,
                            int64_t cos_rows, int rot_half, int rot_offset, int interleaved,
@@ -89,11 +111,15 @@ int orc_paged_attention_op(int act_dtype, int cache_dtype, const void* query, co
 /* Contiguous-cache GroupQueryAttention (ORT CPU semantics as restated by the reference's
  * test_gqa_position_cache.py:88-126 and gqa_batched attention.rs:586-848):
  * query [B,S,H*d], key/value [B,S,KV*d], present_k/v [B,KV,cap,d] (past in, present out),
- * seqlens_k[b] = total_b - 1.  Computes in double.  out [B,S,H*d]. */
+ * seqlens_k[b] = total_b - 1.  Computes in double.  out [B,S,H*d].
+ * cache_dtype ORC_I8 / ORC_I4 (0 = dtype): integer present caches [B,KV,cap,width] holding codes
+ * of the reciprocal (MLAS) rule; attention reads code * scale of every row. */
 int orc_gqa_contiguous(int dtype, const void* query, const void* key, const void* value,
                        void* present_k, void* present_v, int batch, int seq, int num_heads,
                        int kv_heads, int head_dim, int cap, const int32_t* seqlens_k,
-                       float scale, float softcap, int window, int causal, double* out);
+                       float scale, float softcap, int window, int causal, double* out,
+                       int cache_dtype, const float* k_scale, const float* v_scale, int k_mode,
+                       int v_mode);
 
 /* CPU baseline (pa_cpu_baseline.c): the same contiguous GQA decode in fp32 accumulation over
  * all requested threads, one task per (sequence, kv-head).  k/v: [sum_b ctx_b, KV, d] packed

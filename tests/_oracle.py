@@ -17,9 +17,11 @@ ROOT = Path(__file__).resolve().parent.parent
 ORACLE_DIR = ROOT / "oracle"
 LIB = ORACLE_DIR / "build" / "libpa_oracle.so"
 
-F16, BF16, F32, E4M3 = 1, 2, 3, 4
-RAW = {F16: np.float16, BF16: np.uint16, F32: np.float32, E4M3: np.uint8}
-NAMES = {F16: "fp16", BF16: "bf16", F32: "fp32", E4M3: "e4m3"}
+F16, BF16, F32, E4M3, I8, I4 = 1, 2, 3, 4, 5, 6
+RAW = {F16: np.float16, BF16: np.uint16, F32: np.float32, E4M3: np.uint8, I8: np.int8,
+       I4: np.uint8}
+NAMES = {F16: "fp16", BF16: "bf16", F32: "fp32", E4M3: "e4m3", I8: "int8", I4: "int4"}
+PER_TENSOR, PER_CHANNEL = 1, 2
 
 _lib = None
 
@@ -48,19 +50,23 @@ def lib() -> C.CDLL:
         L.orc_rms_norm_rows.argtypes = [P, I64, I32, I32, P, F, I32]
         L.orc_rope_rows.restype = I32
         L.orc_rope_rows.argtypes = [P, I64, I32, I32, P, P, P, I64, I32, I32, I32, I32]
+        L.orc_int_code.restype = I32
+        L.orc_int_code.argtypes = [F, F, I32, I32]
+        L.orc_int_encode_row.argtypes = [P, I32, P, I32, I32, I32, P]
+        L.orc_int_decode_row.argtypes = [P, I32, P, I32, I32, P]
         L.orc_reshape_and_cache.restype = I32
-        L.orc_reshape_and_cache.argtypes = [P, P, I32, P, P, I32, P, P, P, P, P, I32, I32, P,
-                                            I64, I32, I32, I32]
+        L.orc_reshape_and_cache.argtypes = [P, P, I32, P, P, I32, P, P, I32, I32, P, P, P, I32,
+                                            I32, P, I64, I32, I32, I32]
         L.orc_paged_attention.restype = I32
-        L.orc_paged_attention.argtypes = [P, P, P, I32, P, P, I32, P, P, P, P, P, I32, I32, I64,
-                                          I32, I32, I32, I32, F, F, I32, I32, P, P]
+        L.orc_paged_attention.argtypes = [P, P, P, I32, P, P, I32, P, P, I32, I32, P, P, P, I32,
+                                          I32, I64, I32, I32, I32, I32, F, F, I32, I32, P, P]
         L.orc_paged_attention_op.restype = I32
-        L.orc_paged_attention_op.argtypes = [I32, I32, P, P, P, I64, P, P, P, P, I64, I32, P, P,
-                                             P, I32, I32, P, P, I64, I32, I32, I32, P, P, P, P,
-                                             F, I32, I32, I32, F, F, I32, I32, P, P]
+        L.orc_paged_attention_op.argtypes = [I32, I32, P, P, P, I64, P, P, P, P, I32, I32, I64,
+                                             I32, P, P, P, I32, I32, P, P, I64, I32, I32, I32, P,
+                                             P, P, P, F, I32, I32, I32, F, F, I32, I32, P, P]
         L.orc_gqa_contiguous.restype = I32
         L.orc_gqa_contiguous.argtypes = [I32, P, P, P, P, P, I32, I32, I32, I32, I32, I32, P, F,
-                                         F, I32, I32, P]
+                                         F, I32, I32, P, I32, P, P, I32, I32]
         L.orc_cpu_gqa_decode.restype = I32
         L.orc_cpu_gqa_decode.argtypes = [I32, P, P, P, P, P, I32, I32, I32, I32, F, P, I32]
         _lib = L
@@ -107,13 +113,45 @@ def rope_rows(x: np.ndarray, heads: int, head_dim: int, positions: np.ndarray, c
     return x
 
 
+def int_code(x: float, scale: float, bits: int, reciprocal: bool = False) -> int:
+    return lib().orc_int_code(x, scale, bits, int(reciprocal))
+
+
+def int_encode_row(x, scale, bits, per_channel=False, reciprocal=False) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    scale = np.ascontiguousarray(scale, np.float32)
+    d = x.shape[-1]
+    out = np.empty(d if bits == 8 else (d + 1) // 2, np.uint8)
+    lib().orc_int_encode_row(_p(x), d, _p(scale), int(per_channel), bits, int(reciprocal),
+                             _p(out))
+    return out.view(np.int8) if bits == 8 else out
+
+
+def int_decode_row(codes, head_dim, scale, bits, per_channel=False) -> np.ndarray:
+    codes = np.ascontiguousarray(codes).view(np.uint8)
+    scale = np.ascontiguousarray(scale, np.float32)
+    out = np.empty(head_dim, np.float32)
+    lib().orc_int_decode_row(_p(codes), head_dim, _p(scale), int(per_channel), bits, _p(out))
+    return out
+
+
+def head_dim_of(cache: np.ndarray, cache_dtype: int, head_dim: int | None = None) -> int:
+    """Logical head size of a [nb, bs, KV, width] cache (int4 width = ceil(d / 2))."""
+    if head_dim is not None:
+        return head_dim
+    return cache.shape[3] * 2 if cache_dtype == I4 else cache.shape[3]
+
+
 def reshape_and_cache(key, value, act_dtype, kc, vc, cache_dtype, cum, past, bt,
-                      slot_mapping=None, k_scale=None, v_scale=None):
+                      slot_mapping=None, k_scale=None, v_scale=None, k_mode=0, v_mode=0,
+                      head_dim=None):
     kc, vc = kc.copy(), vc.copy()
-    nb, bs, kv, d = kc.shape
+    nb, bs, kv, _ = kc.shape
+    d = head_dim_of(kc, cache_dtype, head_dim)
     rc = lib().orc_reshape_and_cache(
         _p(key), _p(value), act_dtype, _p(kc), _p(vc), cache_dtype, _p(k_scale), _p(v_scale),
-        _p(cum), _p(past), _p(bt), len(cum) - 1, bt.shape[1], _p(slot_mapping), nb, bs, kv, d)
+        k_mode, v_mode, _p(cum), _p(past), _p(bt), len(cum) - 1, bt.shape[1], _p(slot_mapping),
+        nb, bs, kv, d)
     assert rc == 0, rc
     return kc, vc
 
@@ -122,7 +160,8 @@ def paged_attention_op(case: dict, *, return_cache=True):
     """Run the whole operator on a case dict (see pa_cases.make_case)."""
     c = case
     kc, vc = c["key_cache"].copy(), c["value_cache"].copy()
-    nb, bs, kv, d = kc.shape
+    nb, bs, kv, _ = kc.shape
+    d = head_dim_of(kc, c["cache_dtype"], c.get("head_dim"))
     T = c["query"].shape[0]
     H = c["num_heads"]
     out = np.zeros((T, H * d), np.float64)
@@ -131,7 +170,8 @@ def paged_attention_op(case: dict, *, return_cache=True):
     sink = c.get("head_sink_f32")
     rc = lib().orc_paged_attention_op(
         c["dtype"], c["cache_dtype"], _p(c["query"]), _p(c["key"]), _p(c["value"]), T, _p(kc),
-        _p(vc), _p(c.get("k_scale")), _p(c.get("v_scale")), nb, bs, _p(c["cum"]), _p(c["past"]),
+        _p(vc), _p(c.get("k_scale")), _p(c.get("v_scale")), c.get("k_quant", 0),
+        c.get("v_quant", 0), nb, bs, _p(c["cum"]), _p(c["past"]),
         _p(c["block_table"]), len(c["cum"]) - 1, c["block_table"].shape[1], _p(cos), _p(sin),
         0 if cos is None else cos.shape[0], 0 if cos is None else cos.shape[1],
         c.get("rotary_offset", 0), c.get("rotary_interleaved", 0), _p(c.get("slot_mapping")),
@@ -145,25 +185,27 @@ def paged_attention_op(case: dict, *, return_cache=True):
 
 def paged_attention(q, k_new, v_new, act_dtype, kc, vc, cache_dtype, cum, past, bt, H, scale,
                     softcap=0.0, window=-1, causal=1, head_sink=None, k_scale=None,
-                    v_scale=None):
-    nb, bs, kv, d = kc.shape
+                    v_scale=None, k_mode=0, v_mode=0, head_dim=None):
+    nb, bs, kv, _ = kc.shape
+    d = head_dim_of(kc, cache_dtype, head_dim)
     out = np.zeros((q.shape[0], H * d), np.float64)
     rc = lib().orc_paged_attention(
         _p(q), _p(k_new), _p(v_new), act_dtype, _p(kc), _p(vc), cache_dtype, _p(k_scale),
-        _p(v_scale), _p(cum), _p(past), _p(bt), len(cum) - 1, bt.shape[1], nb, bs, H, kv, d,
-        scale, softcap, window, causal, _p(head_sink), _p(out))
+        _p(v_scale), k_mode, v_mode, _p(cum), _p(past), _p(bt), len(cum) - 1, bt.shape[1], nb,
+        bs, H, kv, d, scale, softcap, window, causal, _p(head_sink), _p(out))
     assert rc == 0, rc
     return out
 
 
 def gqa_contiguous(dtype, q, k, v, pk, pv, seqlens_k, H, KV, d, scale, softcap=0.0, window=-1,
-                   causal=1):
+                   causal=1, cache_dtype=0, k_scale=None, v_scale=None, k_mode=0, v_mode=0):
     B, S = q.shape[0], q.shape[1]
     pk, pv = pk.copy(), pv.copy()
     out = np.zeros((B, S, H * d), np.float64)
     rc = lib().orc_gqa_contiguous(dtype, _p(q), _p(k), _p(v), _p(pk), _p(pv), B, S, H, KV, d,
                                   pk.shape[2], _p(np.ascontiguousarray(seqlens_k, np.int32)),
-                                  scale, softcap, window, causal, _p(out))
+                                  scale, softcap, window, causal, _p(out), cache_dtype,
+                                  _p(k_scale), _p(v_scale), k_mode, v_mode)
     assert rc == 0, rc
     return out, pk, pv
 

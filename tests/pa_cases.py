@@ -10,7 +10,7 @@ from __future__ import annotations
 import numpy as np
 
 import _oracle as orc
-from _oracle import BF16, E4M3, F16, F32, RAW
+from _oracle import BF16, E4M3, F16, F32, I4, I8, PER_CHANNEL, PER_TENSOR, RAW
 
 
 def rotary_cache(positions: int, rot_dim: int, theta: float, dtype: int):
@@ -33,10 +33,21 @@ def fp8_pages(rng, shape, scale_mult=1.0):
     return codes, scale
 
 
+def int_scales(KV, d, mode, side):
+    """Integer-cache scales as the reference's tests draw them (test_quantized_kv.py:73-78):
+    per-tensor 0.125 (k) / 0.25 (v); per-channel a cycle of eight values, zero included, rolled
+    by the side, shaped [KV, d]."""
+    if mode == PER_TENSOR:
+        return np.array([0.125 if side == 0 else 0.25], np.float32)
+    pattern = np.array([0.125, 0.25, 0.5, 1, 0.0625, 0.375, 2, 0], np.float32)
+    return np.roll(np.resize(pattern, (KV, 1, d)), side, axis=-1).reshape(KV, d).copy()
+
+
 def make_case(H, KV, d, nb, bs, batch, *, dtype=F16, cache_dtype=None, seed=0, new_lens=None,
               past=None, max_blocks=None, do_rotary=0, interleaved=0, theta=10000.0,
               rot_dim=None, rotary_offset=0, slot_mapping=None, head_sink=None, qk_norm=False,
-              softcap=0.0, window=-1, causal=1, scale=0.0, std=0.3, value_std=None):
+              softcap=0.0, window=-1, causal=1, scale=0.0, std=0.3, value_std=None,
+              int_modes=(PER_CHANNEL, PER_CHANNEL)):
     rng = np.random.default_rng(seed)
     cache_dtype = dtype if cache_dtype is None else cache_dtype
     if max_blocks is None:
@@ -64,6 +75,16 @@ def make_case(H, KV, d, nb, bs, batch, *, dtype=F16, cache_dtype=None, seed=0, n
     if cache_dtype == E4M3:
         case["key_cache"], case["k_scale"] = fp8_pages(rng, (nb, bs, KV, d))
         case["value_cache"], case["v_scale"] = fp8_pages(rng, (nb, bs, KV, d))
+    elif cache_dtype in (I8, I4):
+        # random resident codes (test_quantized_kv.py:357-359) and the reference's scales
+        width = d if cache_dtype == I8 else (d + 1) // 2
+        for side, name in enumerate(("key", "value")):
+            if cache_dtype == I8:
+                case[f"{name}_cache"] = rng.integers(-128, 128, (nb, bs, KV, width), dtype=np.int8)
+            else:
+                case[f"{name}_cache"] = rng.integers(0, 256, (nb, bs, KV, width), dtype=np.uint8)
+            case["kv"[side] + "_scale"] = int_scales(KV, d, int_modes[side], side)
+        case["k_quant"], case["v_quant"] = int_modes
     else:
         case["key_cache"] = draw((nb, bs, KV, d), std)
         case["value_cache"] = draw((nb, bs, KV, d), vstd)
@@ -92,7 +113,7 @@ def make_case(H, KV, d, nb, bs, batch, *, dtype=F16, cache_dtype=None, seed=0, n
 def torch_dtype(code: int):
     import torch
     return {F16: torch.float16, BF16: torch.bfloat16, F32: torch.float32,
-            E4M3: torch.float8_e4m3fn}[code]
+            E4M3: torch.float8_e4m3fn, I8: torch.int8, I4: torch.uint8}[code]
 
 
 def to_torch(raw: np.ndarray, code: int, device="cuda"):
@@ -117,8 +138,12 @@ def from_torch(t, code: int) -> np.ndarray:
     return t.numpy()
 
 
-def run_gpu_op(case: dict, validate=True, device="cuda"):
-    """Run the operator-level entry (pa_paged_attention) on the GPU for a case."""
+QUANT_NAMES = {0: "NONE", PER_TENSOR: "PER_TENSOR", PER_CHANNEL: "PER_CHANNEL"}
+
+
+def run_gpu_op(case: dict, validate=True, device="cuda", packed=False):
+    """Run the operator-level entry (pa_paged_attention) on the GPU for a case.  packed: hand
+    Q, K and V over as one [T, (H + 2 KV) * d] query with key = value = None."""
     import torch
     import onnxruntime_ep_mlx_amd as ep
     dt, cdt = case["dtype"], case["cache_dtype"]
@@ -127,8 +152,11 @@ def run_gpu_op(case: dict, validate=True, device="cuda"):
         np.ascontiguousarray(case[k], np.int32)).to(device)
     F = lambda k: None if case.get(k) is None else torch.from_numpy(case[k]).to(device)
     kc, vc = T("key_cache", cdt), T("value_cache", cdt)
+    q, k, v = T("query"), T("key"), T("value")
+    if packed:
+        q, k, v = torch.cat([q, k, v], dim=1).contiguous(), None, None
     out, kc, vc = ep.paged_attention(
-        T("query"), T("key"), T("value"), kc, vc, I("cum"), I("past"), I("block_table"),
+        q, k, v, kc, vc, I("cum"), I("past"), I("block_table"),
         T("cos_cache"), T("sin_cache"), I("slot_mapping"), T("head_sink"), T("q_norm"),
         T("k_norm"), F("k_scale"), F("v_scale"), None,
         num_heads=case["num_heads"], kv_num_heads=case["kv_num_heads"],
@@ -136,6 +164,8 @@ def run_gpu_op(case: dict, validate=True, device="cuda"):
         local_window_size=case.get("local_window_size", -1),
         do_rotary=int("cos_cache" in case), rotary_interleaved=case.get("rotary_interleaved", 0),
         rotary_offset=case.get("rotary_offset", 0), is_causal=case.get("is_causal", 1),
-        qk_norm_epsilon=case.get("qk_norm_epsilon", 1e-6), validate=validate)
+        qk_norm_epsilon=case.get("qk_norm_epsilon", 1e-6),
+        k_quant_type=QUANT_NAMES[case.get("k_quant", 0)],
+        v_quant_type=QUANT_NAMES[case.get("v_quant", 0)], validate=validate)
     torch.cuda.synchronize()
     return from_torch(out, dt), from_torch(kc, cdt), from_torch(vc, cdt)

@@ -106,12 +106,92 @@ def test_claim_accepts_fp8_cache_with_block_scales():
     (lambda n: setattr(n, "kv_cache_layout_latent", 1), "LATENT"),
     (lambda n: n.input_dtype.__setitem__(5, capi.PA_DTYPE_FLOAT32), "input 5 must be int32"),
     (lambda n: n.input_present.__setitem__(9, 0), "requires cos_cache and sin_cache"),
-    (lambda n: n.input_dtype.__setitem__(3, capi.PA_INT8_DTYPE), "storage dtype"),
+    (lambda n: n.input_dtype.__setitem__(4, capi.PA_INT8_DTYPE), "storage dtype"),
+    (lambda n: n.input_dtype.__setitem__(3, capi.PA_INT8_DTYPE),
+     "integer k cache requires PER_TENSOR or PER_CHANNEL"),
     (lambda n: setattr(n, "num_inputs", 18), "expects 8 required inputs"),
 ])
 def test_claim_declines_with_reference_reasons(mutate, reason):
     n = _node()
     mutate(n)
+    ok, why = _claim(n)
+    assert ok == 0 and reason in why, why
+
+
+def _int_node(bits=8, modes=(capi.PA_QUANT_PER_CHANNEL, capi.PA_QUANT_PER_CHANNEL), head=16,
+              KV=2, H=4):
+    """The reference's integer PagedAttention node (test_quantized_kv.py:344-392)."""
+    width = head if bits == 8 else (head + 1) // 2
+    storage = capi.PA_INT8_DTYPE if bits == 8 else capi.PA_UINT8_DTYPE
+    n = _node(dtype=capi.PA_DTYPE_FLOAT16, H=H, KV=KV, d=head, nb=6, bs=4, T=3, B=3, mb=2,
+              cache_dtype=storage, rotary=False)
+    for i in (3, 4):
+        n.input_shape[i][3] = width
+    n.num_inputs = 16
+    for side, i in enumerate((14, 15)):
+        n.input_present[i] = 1
+        n.input_dtype[i] = capi.PA_DTYPE_FLOAT32
+        if modes[side] == capi.PA_QUANT_PER_TENSOR:
+            n.input_rank[i] = 1
+            n.input_shape[i][0] = 1
+        else:
+            n.input_rank[i] = 2
+            n.input_shape[i][0], n.input_shape[i][1] = KV, head
+    n.k_quant_type, n.v_quant_type = modes
+    n.k_cache_dtype = n.v_cache_dtype = capi.PA_DTYPE_INT8 if bits == 8 else capi.PA_DTYPE_INT4
+    return n
+
+
+@pytest.mark.parametrize("bits,head", [(8, 16), (4, 16), (4, 7)])
+@pytest.mark.parametrize("modes", [(1, 1), (2, 2), (1, 2)])
+def test_claim_accepts_integer_caches(bits, head, modes):
+    assert _claim(_int_node(bits, modes, head)) == (1, "")
+
+
+def test_claim_int8_without_explicit_cache_dtype_and_packed_qkv():
+    n = _int_node(8)
+    n.k_cache_dtype = n.v_cache_dtype = 0  # int8 storage needs no explicit "int8"
+    assert _claim(n)[0] == 1
+    n = _node()
+    n.input_present[1] = n.input_present[2] = 0  # packed [T, (H + 2 KV) * d] query
+    n.input_shape[0][1] = (32 + 16) * 128
+    assert _claim(n) == (1, "")
+
+
+# test_quantized_kv.py:615-641 (paged=True): each broken static contract is declined.
+@pytest.mark.parametrize("bad,reason", [
+    ("mode", "requires PER_TENSOR or PER_CHANNEL"),
+    ("missing_scale", "requires a scale tensor"),
+    ("scale_dtype", "k_scale must be float32"),
+    ("scale_shape", "k_scale must contain 8 elements"),
+    ("scale_last", "per-channel scales must end in head_size"),
+    ("cache_dtype", "storage dtype"),
+    ("output_dtype", "retain cache storage dtype"),
+    ("packing", "uint8 requires explicit int4"),
+    ("packing_absent", "uint8 requires explicit int4"),
+])
+def test_claim_declines_broken_integer_contracts(bad, reason):
+    n = _int_node(4, head=4)
+    if bad == "mode":
+        n.k_quant_type = capi.PA_QUANT_NONE
+    elif bad == "missing_scale":
+        n.input_present[14] = 0
+    elif bad == "scale_dtype":
+        n.input_dtype[14] = capi.PA_DTYPE_FLOAT16
+    elif bad == "scale_shape":
+        n.input_shape[14][1] = 3
+    elif bad == "scale_last":
+        n.input_shape[14][0], n.input_shape[14][1] = 4, 2
+    elif bad == "cache_dtype":
+        n.input_dtype[4] = capi.PA_DTYPE_FLOAT16
+    elif bad == "output_dtype":
+        n.num_outputs = 2
+        n.output_present[1] = 1
+        n.output_dtype[1] = capi.PA_DTYPE_FLOAT16
+    elif bad == "packing":
+        n.k_cache_dtype = -1  # e.g. "float4e2m1"
+    else:
+        n.k_cache_dtype = 0
     ok, why = _claim(n)
     assert ok == 0 and reason in why, why
 
