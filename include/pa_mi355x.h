@@ -93,7 +93,8 @@ int64_t pa_pool_bytes(const pa_pool* pool);
  * attention reads, the new rows included, is code * scale in fp32 read back from the pages. */
 typedef struct pa_cache {
   void* key_cache;
-  void* value_cache;
+  void* value_cache; /* NULL: the LATENT layout, each position's value is the first
+                        v_head_size dims of its key row (attention.rs:4058-4062, :4210-4213) */
   const float* k_scale; /* fp8: [num_blocks, kv_heads]; int8/int4: see k_quant_type */
   const float* v_scale; /* fp8: [num_blocks, kv_heads]; int8/int4: see v_quant_type */
   int64_t num_blocks;
@@ -139,6 +140,8 @@ typedef struct pa_attn {
   int32_t local_window_size; /* -1 -> off; else keys >= row - window + 1 */
   int32_t is_causal;         /* 1: key p visible to row r iff p <= past + r */
   const void* head_sink;     /* [num_heads] in activation dtype, or NULL */
+  int32_t v_head_size;       /* 0 -> head_dim; smaller only for a LATENT cache; q/out rows are
+                                [num_heads * head_dim] / [num_heads * v_head_size] */
 } pa_attn;
 
 /* ------------------------------------------------------------------------------------------ */
@@ -215,6 +218,11 @@ typedef struct pa_paged_attention_node {
   int32_t rotary_offset;      /* "rotary_offset" */
   int32_t is_causal;          /* "is_causal" (1) */
   float qk_norm_epsilon;      /* "qk_norm_epsilon" (1e-6) */
+  int32_t v_head_size;        /* "v_head_size" (0 = head_size) */
+  /* "kv_cache_layout" == "LATENT": kv_num_heads 1, inputs 2/4 (value, value_cache) absent,
+   * values are the first v_head_size dims of the (rotated) key rows, output
+   * [num_tokens, num_heads * v_head_size]. */
+  int32_t kv_cache_layout_latent;
 } pa_paged_attention_node;
 
 typedef struct pa_paged_attention_io {
@@ -224,7 +232,7 @@ typedef struct pa_paged_attention_io {
                                   [num_tokens, (num_heads + 2 * kv_num_heads) * head] */
   const void* query;           /* input 0 */
   const void* key;             /* input 1 (NULL: packed) */
-  const void* value;           /* input 2 (NULL: packed) */
+  const void* value;           /* input 2 (NULL: packed, or LATENT) */
   pa_cache cache;              /* inputs 3/4 (+14/15 for fp8 / integer cache scales) */
   const int32_t* cumulative_sequence_length; /* input 5, device */
   const int32_t* past_seqlens; /* input 6, device */

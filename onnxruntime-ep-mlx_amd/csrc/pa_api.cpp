@@ -62,16 +62,22 @@ bool is_act(pa_dtype d) {
 
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
+// Largest head size any kernel serves (the VALU kernel; matrix cores take 64 and 128).
+constexpr int kMaxHeadDim = 640;
+
 // ---------------------------------------------------------------------------- descriptor checks
 int check_cache(const pa_cache* c, pa_dtype act) {
   if (!c) return fail(PA_ERR_INVALID_ARGUMENT, "cache descriptor is NULL");
   if (c->num_blocks <= 0 || c->block_size <= 0)
     return fail(PA_ERR_INVALID_ARGUMENT,
                 "PagedAttention: caches require matching positive block geometry");
-  if (c->kv_heads <= 0 || c->head_dim <= 0 || c->head_dim > 256)
-    return fail(PA_ERR_UNSUPPORTED, "head_dim %d unsupported (1..256)", c->head_dim);
-  if (!c->key_cache || !c->value_cache)
-    return fail(PA_ERR_INVALID_ARGUMENT, "key_cache/value_cache pointers are NULL");
+  if (c->kv_heads <= 0 || c->head_dim <= 0 || c->head_dim > kMaxHeadDim)
+    return fail(PA_ERR_UNSUPPORTED, "head_dim %d unsupported (1..%d)", c->head_dim,
+                kMaxHeadDim);
+  if (!c->key_cache) return fail(PA_ERR_INVALID_ARGUMENT, "key_cache pointer is NULL");
+  // value_cache == NULL is the LATENT layout (values read from the key rows).
+  if (!c->value_cache && c->dtype != act)
+    return fail(PA_ERR_UNSUPPORTED, "quantized LATENT cache contract is not supported");
   if (c->dtype == PA_DTYPE_FP8_E4M3) {
     if (!c->k_scale || !c->v_scale)
       return fail(PA_ERR_INVALID_ARGUMENT, "fp8 cache requires k_scale and v_scale");
@@ -152,6 +158,9 @@ int device_cus() {
 Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype act, int kind,
                int chunk, bool linear = false) {
   Plan pl{};
+  // The LATENT layout (values = leading dims of the key rows) runs on the VALU kernel.
+  if (c->value_cache == nullptr || (a->v_head_size > 0 && a->v_head_size != c->head_dim))
+    kind = 3;
   const int g = a->num_heads / c->kv_heads;
   const int mq = b->max_query_len > 0 ? b->max_query_len : std::max(b->num_tokens, 1);
   const bool mfma = pa::decode_mfma_supported(c->head_dim, act, c->dtype);
@@ -242,9 +251,17 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
   if (b->num_tokens == 0) return PA_OK;
   // Quantised caches (fp8, int8, int4) read every position from the pages.
   const bool quant = c->dtype == PA_DTYPE_FP8_E4M3 || is_int_cache(c->dtype);
-  if (!q || !out || (!quant && (!kn || !vn)))
+  const bool latent = c->value_cache == nullptr;
+  const int vd = a->v_head_size > 0 ? a->v_head_size : c->head_dim;
+  if (!latent && vd != c->head_dim)
+    return fail(PA_ERR_INVALID_ARGUMENT, "SEPARATE layout requires equal key and value head sizes");
+  if (vd > c->head_dim)
+    return fail(PA_ERR_INVALID_ARGUMENT, "LATENT v_head_size must not exceed head_size");
+  if (!q || !out || (!quant && (!kn || (!vn && !latent))))
     return fail(PA_ERR_INVALID_ARGUMENT, "q/k_new/v_new/out pointers are NULL");
   if (kind < 0 || kind > 4) return fail(PA_ERR_INVALID_ARGUMENT, "unknown kernel kind %d", kind);
+  if (latent && kind != 0 && kind != 3)
+    return fail(PA_ERR_UNSUPPORTED, "the LATENT layout runs on the VALU kernel only");
   if (kind == 4 && !pa::decode_mfma_supported(c->head_dim, act, c->dtype))
     return fail(PA_ERR_UNSUPPORTED, "decode MFMA kernel does not cover this dtype/head_dim");
   if (kind == 1 && !pa::decode_mfma_supported(c->head_dim, act, c->dtype)) {
@@ -305,6 +322,8 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
   p.read_all_from_cache = quant ? 1 : 0;
   p.k_quant = c->k_quant_type;
   p.v_quant = c->v_quant_type;
+  p.v_head_dim = vd;
+  p.v_from_key = latent ? 1 : 0;
   p.new_rows_in_cache =
       (opts.new_rows_in_cache || ((b->flags & PA_BATCH_NEW_ROWS_IN_CACHE) && !b->slot_mapping))
           ? 1
@@ -419,7 +438,8 @@ static int rotary_append_impl(const pa_cache* c, const pa_batch* b, int32_t num_
   if (rc) return rc;
   if ((rc = check_batch(b))) return rc;
   if (b->num_tokens == 0) return PA_OK;
-  if (!key || !value) return fail(PA_ERR_INVALID_ARGUMENT, "key/value pointers are NULL");
+  if (!key || (!value && c->value_cache))
+    return fail(PA_ERR_INVALID_ARGUMENT, "key/value pointers are NULL");
   const bool rotate = cos != nullptr;
   if (rotate) {
     if (!sin || rot_half <= 0 || rot_offset < 0 || rot_offset + 2 * rot_half > c->head_dim ||
@@ -540,7 +560,7 @@ int pa_attention_ex(const pa_cache* cache, const pa_batch* batch, const pa_attn*
 namespace {
 
 struct OpLayout {
-  int head, kv_hidden;
+  int head, v_head, kv_hidden;
   bool packed, transform;
   size_t q_bytes, k_bytes, v_bytes, attn_off, total;
   pa_batch batch;
@@ -551,11 +571,24 @@ int op_layout(const pa_paged_attention_node* n, const pa_paged_attention_io* io,
   if (!n || !io) return fail(PA_ERR_INVALID_ARGUMENT, "node/io is NULL");
   if (n->num_heads <= 0 || n->kv_num_heads <= 0 || n->num_heads % n->kv_num_heads != 0)
     return fail(PA_ERR_INVALID_ARGUMENT, "PagedAttention: bad num_heads/kv_num_heads");
-  // attention.rs:4433: key and value absent together = packed [T, (H + 2 KV) * head] query.
-  L->packed = io->key == nullptr && io->value == nullptr;
-  if (!L->packed && (io->key == nullptr || io->value == nullptr))
-    return fail(PA_ERR_INVALID_ARGUMENT,
-                "PagedAttention: key and value must both be present or both be absent");
+  // attention.rs:4434: key and value absent together = packed [T, (H + 2 KV) * head] query.
+  const bool latent = n->kv_cache_layout_latent != 0;
+  L->packed = !latent && io->key == nullptr && io->value == nullptr;
+  if (latent) {
+    // attention.rs:4452-4481: one kv-head, value and value_cache absent.
+    if (n->kv_num_heads != 1)
+      return fail(PA_ERR_INVALID_ARGUMENT, "PagedAttention: LATENT layout requires kv_num_heads=1");
+    if (!io->key || io->value || io->cache.value_cache)
+      return fail(PA_ERR_INVALID_ARGUMENT,
+                  "PagedAttention: LATENT layout aliases value to key and requires absent "
+                  "value/value_cache");
+  } else {
+    if (!L->packed && (io->key == nullptr || io->value == nullptr))
+      return fail(PA_ERR_INVALID_ARGUMENT,
+                  "PagedAttention: key and value must both be present or both be absent");
+    if (!io->cache.value_cache)
+      return fail(PA_ERR_INVALID_ARGUMENT, "PagedAttention: value_cache is required");
+  }
   const int qheads = L->packed ? n->num_heads + 2 * n->kv_num_heads : n->num_heads;
   if (io->query_hidden <= 0 || io->query_hidden % qheads != 0)
     return fail(PA_ERR_INVALID_ARGUMENT,
@@ -566,6 +599,12 @@ int op_layout(const pa_paged_attention_node* n, const pa_paged_attention_io* io,
   if (io->cache.head_dim != L->head || io->cache.kv_heads != n->kv_num_heads)
     return fail(PA_ERR_INVALID_ARGUMENT,
                 "key_cache must be [num_blocks,block_size,kv_num_heads,head_size]");
+  L->v_head = n->v_head_size > 0 ? n->v_head_size : L->head;
+  if (latent && L->v_head > L->head)
+    return fail(PA_ERR_INVALID_ARGUMENT, "PagedAttention: LATENT v_head_size must not exceed head_size");
+  if (!latent && L->v_head != L->head)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "PagedAttention: SEPARATE layout requires equal key and value head sizes");
   // Packed rows are copied out contiguously by the append kernel (rotated or not).
   L->transform = (n->do_rotary != 0) || io->q_norm_weight != nullptr || L->packed;
   size_t es = elem_size(io->dtype);
@@ -598,6 +637,7 @@ int op_layout(const pa_paged_attention_node* n, const pa_paged_attention_io* io,
   a.local_window_size = n->local_window_size;
   a.is_causal = n->is_causal;
   a.head_sink = io->head_sink;
+  a.v_head_size = L->v_head;
   L->total = L->attn_off + pa_attention_workspace_bytes_ex(&io->cache, &b, &a, io->dtype, 0, 0);
   return PA_OK;
 }
@@ -933,14 +973,23 @@ int pa_paged_attention_claim(const pa_node_info* n, char* reason, size_t reason_
   if (n->num_inputs < 8 || n->num_inputs > 17)
     return deny("expects 8 required inputs plus optional rotary, scheduling, normalization, "
                 "and scale inputs, got %d", n->num_inputs);
-  if (n->kv_cache_layout_latent) return deny("LATENT kv_cache_layout is not executed by this build");
   auto present = [&](int i) { return i < n->num_inputs && n->input_present[i]; };
   auto out_present = [&](int i) { return i < n->num_outputs && n->output_present[i]; };
-  const bool packed = !present(1) && !present(2);
-  for (int i : {0, 1, 2}) {
+  const bool latent = n->kv_cache_layout_latent != 0;
+  const int cache_dt = present(3) ? n->input_dtype[3] : out_dt;
+  const bool quantized = cache_dt == PA_INT8_DTYPE || cache_dt == PA_UINT8_DTYPE;
+  if (latent && quantized) return deny("quantized LATENT cache contract is not supported");
+  const bool packed = !latent && !present(1) && !present(2);
+  for (int i : {0, 1}) {
     if (packed && i > 0) break;
     if (!present(i) || n->input_dtype[i] != out_dt)
       return deny("input %d must be present and share the output float dtype", i);
+  }
+  if (latent) {
+    if (present(2) || present(4))
+      return deny("LATENT layout aliases value to key and requires absent value/value_cache");
+  } else if (!packed && (!present(2) || n->input_dtype[2] != out_dt)) {
+    return deny("input 2 must be present and share the output float dtype");
   }
   for (int i : {5, 6, 7})
     if (!present(i) || n->input_dtype[i] != I32) return deny("input %d must be int32", i);
@@ -948,24 +997,27 @@ int pa_paged_attention_claim(const pa_node_info* n, char* reason, size_t reason_
   if (!(H > 0 && KV > 0 && H % KV == 0))
     return deny("num_heads (%lld) must be a positive multiple of kv_num_heads (%lld)",
                 (long long)H, (long long)KV);
+  if (latent && KV != 1) return deny("LATENT layout requires kv_num_heads=1");
   const int64_t qheads = packed ? H + 2 * KV : H;
   if (n->input_rank[0] != 2 || n->input_shape[0][1] <= 0 || n->input_shape[0][1] % qheads != 0)
     return deny("query must have rank 2 and a hidden size divisible by its separate or packed "
                 "head count");
   const int64_t head = n->input_shape[0][1] / qheads;
-  if (head > 256) return deny("head_size %lld is not executed by this build", (long long)head);
+  if (head > kMaxHeadDim)
+    return deny("head_size %lld is not executed by this build", (long long)head);
   // kv_cache::claim (kv_cache.rs:16-108): both caches share one storage dtype; integer caches
   // need PER_TENSOR / PER_CHANNEL fp32 scales (inputs 14/15) and a matching *_cache_dtype; a
   // floating cache uses the activation dtype, NONE quantization and no scale.  fp8 e4m3 pages
   // with fp32 per-(block, kv-head) scales are this build's extension.
-  if (!present(3) || !present(4)) return deny("key_cache and value_cache must be present");
-  const int cache_dt = n->input_dtype[3];
-  const bool quantized = cache_dt == PA_INT8_DTYPE || cache_dt == PA_UINT8_DTYPE;
+  if (!present(3) || (!latent && !present(4)))
+    return deny("key_cache and value_cache must be present");
+  if (latent && cache_dt != out_dt)
+    return deny("a LATENT cache must use the activation dtype");
   for (int side = 0; side < 2; ++side) {
     const int cache_in = 3 + side, scale_in = 14 + side;
     const char* nm = side ? "v" : "k";
-    if (n->input_dtype[cache_in] != cache_dt)
-      return deny("key/value caches must share one storage dtype");
+    const int side_dt = present(cache_in) ? n->input_dtype[cache_in] : out_dt;
+    if (side_dt != cache_dt) return deny("key/value caches must share one storage dtype");
     const int mode = side ? n->v_quant_type : n->k_quant_type;
     if (quantized) {
       if (mode != PA_QUANT_PER_TENSOR && mode != PA_QUANT_PER_CHANNEL)
@@ -1006,17 +1058,24 @@ int pa_paged_attention_claim(const pa_node_info* n, char* reason, size_t reason_
   }
   const int64_t cache_head = cache_dt == PA_UINT8_DTYPE ? (head + 1) / 2 : head;
   const int64_t v_head = n->v_head_size == 0 ? head : n->v_head_size;
+  if (v_head <= 0) return deny("effective v_head_size must be positive");
   if (!packed) {
     if (n->input_rank[1] != 2 || n->input_shape[1][1] != KV * head)
       return deny("key must be [num_tokens,kv_num_heads*head_size]");
-    if (n->input_rank[2] != 2 || n->input_shape[2][1] != KV * v_head)
+    if (!latent && (n->input_rank[2] != 2 || n->input_shape[2][1] != KV * v_head))
       return deny("value must be [num_tokens,kv_num_heads*v_head_size]");
   }
-  if (v_head != head) return deny("SEPARATE layout requires equal key and value head sizes");
-  for (int i : {3, 4})
+  if (!latent && v_head != head)
+    return deny("SEPARATE layout requires equal key and value head sizes");
+  if (latent && v_head > head) return deny("LATENT v_head_size must not exceed head_size");
+  if (latent && v_head != head && !n->has_scale_attr)
+    return deny("LATENT layout with asymmetric value heads requires an explicit scale");
+  for (int i : {3, 4}) {
+    if (latent && i == 4) break;
     if (n->input_rank[i] != 4 || n->input_shape[i][2] != KV || n->input_shape[i][3] != cache_head)
       return deny("%s must be [num_blocks,block_size,kv_num_heads,head_size]",
                   i == 3 ? "key_cache" : "value_cache");
+  }
   if (n->output_rank[0] != 2 ||
       !(n->output_shape[0][1] < 0 || n->output_shape[0][1] == H * v_head))
     return deny("output must be [num_tokens,num_heads*v_head_size]");
@@ -1055,6 +1114,7 @@ int pa_paged_attention_claim(const pa_node_info* n, char* reason, size_t reason_
   if (present(16) && !(n->input_dtype[16] == I32 && n->input_rank[16] == 1 &&
                        (n->input_shape[16][0] == 2 || n->input_shape[16][0] == 3)))
     return deny("attention_metadata must be int32 [2] or [3]");
+  if (latent && out_present(2)) return deny("LATENT layout has no separate value cache output");
   for (int i = 1; i < std::min(n->num_outputs, 3); ++i)
     if (out_present(i) && n->output_dtype[i] != n->input_dtype[i + 2])
       return deny("cache output %d must retain cache storage dtype", i);

@@ -242,6 +242,9 @@ __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p
   // Cache row width per kv-head in storage units: int4 packs two channels per byte.
   const int Dc = CK == kCacheI4 ? (D + 1) >> 1 : D;
   const int64_t crow = (int64_t)p.kv_heads * Dc;
+  // LATENT layout: no value input and no value cache (values are read from the key rows).
+  const bool write_v = write_cache && p.value != nullptr && p.value_cache != nullptr;
+  void* const v_out = p.value != nullptr ? p.v_out : nullptr;
   for (int kh = wave; kh < p.kv_heads; kh += 4) {
     const int64_t kbase = (int64_t)t * p.k_ld + (int64_t)kh * D;
     const int64_t vbase = (int64_t)t * p.v_ld + (int64_t)kh * D;
@@ -261,13 +264,13 @@ __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p
         typename TT::raw* kd = reinterpret_cast<typename TT::raw*>(p.key_cache);
         for (int e = lane; e < D; e += 64) kd[cbase + e] = ks[kbase + e];
       }
-      if (write_cache || p.v_out) {
+      if (write_v || v_out) {
         const typename TT::raw* vs = reinterpret_cast<const typename TT::raw*>(p.value);
         typename TT::raw* vd = reinterpret_cast<typename TT::raw*>(p.value_cache);
-        typename TT::raw* vo = reinterpret_cast<typename TT::raw*>(p.v_out);
+        typename TT::raw* vo = reinterpret_cast<typename TT::raw*>(v_out);
         for (int e = lane; e < D; e += 64) {
           const typename TT::raw x = vs[vbase + e];
-          if (write_cache) vd[cbase + e] = x;
+          if (write_v) vd[cbase + e] = x;
           if (vo) vo[obase + e] = x;
         }
       }
@@ -289,21 +292,21 @@ __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p
           kd[cbase + e] = ks == 0.0f ? 0 : (uint8_t)f32_to_e4m3_sat(kx / ks);
         }
       }
-      if (write_cache || p.v_out)
+      if (write_v || v_out)
         for (int e = lane; e < D; e += 64) {
           float vx = ldv<TT>(p.value, vbase + e);
-          if (write_cache) vd[cbase + e] = vsc == 0.0f ? 0 : (uint8_t)f32_to_e4m3_sat(vx / vsc);
-          if (p.v_out) stv<TT>(p.v_out, obase + e, vx);
+          if (write_v) vd[cbase + e] = vsc == 0.0f ? 0 : (uint8_t)f32_to_e4m3_sat(vx / vsc);
+          if (v_out) stv<TT>(v_out, obase + e, vx);
         }
     } else {
       uint8_t* kd = write_cache ? reinterpret_cast<uint8_t*>(p.key_cache) : nullptr;
-      uint8_t* vd = write_cache ? reinterpret_cast<uint8_t*>(p.value_cache) : nullptr;
+      uint8_t* vd = write_v ? reinterpret_cast<uint8_t*>(p.value_cache) : nullptr;
       if (kd || (transform && p.k_out))
         int_row<TT, CK>(p, p.key, kbase, transform ? p.k_out : nullptr, obase, kd, cbase,
                         p.k_scale, p.k_quant == PA_QUANT_PER_CHANNEL, kh, p.k_norm, true, pos,
                         lane);
-      if (vd || p.v_out)  // values are neither normalised nor rotated
-        int_row<TT, CK>(p, p.value, vbase, p.v_out, obase, vd, cbase, p.v_scale,
+      if (vd || v_out)  // values are neither normalised nor rotated
+        int_row<TT, CK>(p, p.value, vbase, v_out, obase, vd, cbase, p.v_scale,
                         p.v_quant == PA_QUANT_PER_CHANNEL, kh, nullptr, false, pos, lane);
     }
   }

@@ -73,13 +73,13 @@ constexpr bool kIntCache<I8Cache> = true;
 template <>
 constexpr bool kIntCache<I4Cache> = true;
 
-constexpr int kMaxLanesElems = 4;  // head_dim <= 256
-
-template <typename TT, typename CT>
+// Elements per lane: NE = 4 covers head_dim <= 256, NE = 10 head_dim <= 640 (latent heads).
+template <typename TT, typename CT, int NE>
 __global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
   const int split = blockIdx.x, h = blockIdx.y, t = blockIdx.z;
   const int lane = threadIdx.x;
   const int D = p.head_dim;
+  const int VD = p.v_head_dim;  // value / output head size (< D only for the LATENT layout)
   const int b = seq_of_token(p.cum, p.batch, t);
   const int s0 = p.cum[b];
   const int nq = p.cum[b + 1] - s0;
@@ -99,9 +99,9 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
   // Cache rows in storage units: int4 holds two channels per byte.
   const int Dc = std::is_same<CT, I4Cache>::value ? (D + 1) >> 1 : D;
   const int64_t crow = (int64_t)p.kv_heads * Dc;
-  float qv[kMaxLanesElems], o[kMaxLanesElems], ksv[kMaxLanesElems], vsv[kMaxLanesElems];
+  float qv[NE], o[NE], ksv[NE], vsv[NE];
 #pragma unroll
-  for (int k = 0; k < kMaxLanesElems; ++k) {
+  for (int k = 0; k < NE; ++k) {
     int e = lane + 64 * k;
     qv[k] = e < D ? TT::to_f32(reinterpret_cast<const typename TT::raw*>(
                         p.q)[((int64_t)t * p.num_heads + h) * D + e])
@@ -124,14 +124,14 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
       // contiguous [batch, kv_heads, cap, head_dim] cache holding the new rows too
       off = (((int64_t)b * p.kv_heads + kh) * p.linear_cap + pos) * Dc;
       kb = p.key_cache;
-      vb = p.value_cache;
+      vb = p.v_from_key ? p.key_cache : p.value_cache;
     } else if (from_cache) {
       int64_t bi = pos / p.block_size;
       int64_t blk = p.block_table[(int64_t)b * p.max_blocks + min(bi, (int64_t)p.max_blocks - 1)];
       blk = min(max(blk, (int64_t)0), p.num_blocks - 1);
       off = (blk * p.block_size + pos % p.block_size) * crow + (int64_t)kh * Dc;
       kb = p.key_cache;
-      vb = p.value_cache;
+      vb = p.v_from_key ? p.key_cache : p.value_cache;
       if (std::is_same<CT, Fp8Cache>::value) {
         ks = p.k_scale[blk * p.kv_heads + kh];
         vs = p.v_scale[blk * p.kv_heads + kh];
@@ -140,11 +140,11 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
       int64_t tok = min(max((int64_t)s0 + (pos - pastb), (int64_t)0), (int64_t)p.num_tokens - 1);
       off = tok * row + (int64_t)kh * D;
       kb = p.k_new;
-      vb = p.v_new;
+      vb = p.v_from_key ? p.k_new : p.v_new;
     }
     float part = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kMaxLanesElems; ++k) {
+    for (int k = 0; k < NE; ++k) {
       int e = lane + 64 * k;
       if (e < D) {
         float kv = from_cache ? CacheRead<CT>::at(kb, off, e, kIntCache<CT> ? ksv[k] : ks)
@@ -160,9 +160,9 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
     float w = exp2f(x - mn);
     l = l * alpha + w;
 #pragma unroll
-    for (int k = 0; k < kMaxLanesElems; ++k) {
+    for (int k = 0; k < NE; ++k) {
       int e = lane + 64 * k;
-      if (e < D) {
+      if (e < VD) {
         float vv = from_cache ? CacheRead<CT>::at(vb, off, e, kIntCache<CT> ? vsv[k] : vs)
                               : TT::to_f32(reinterpret_cast<const typename TT::raw*>(vb)[off + e]);
         o[k] = o[k] * alpha + w * vv;
@@ -177,16 +177,16 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
     float f = finalize_factor(m, l, sink_logit<TT>(p, h));
     typename TT::raw* out = reinterpret_cast<typename TT::raw*>(p.out);
 #pragma unroll
-    for (int k = 0; k < kMaxLanesElems; ++k) {
+    for (int k = 0; k < NE; ++k) {
       int e = lane + 64 * k;
-      if (e < D) out[((int64_t)t * p.num_heads + h) * D + e] = TT::from_f32(o[k] * f);
+      if (e < VD) out[((int64_t)t * p.num_heads + h) * VD + e] = TT::from_f32(o[k] * f);
     }
   } else {
     int64_t pi = ((int64_t)t * p.num_heads + h) * p.max_splits + split;
 #pragma unroll
-    for (int k = 0; k < kMaxLanesElems; ++k) {
+    for (int k = 0; k < NE; ++k) {
       int e = lane + 64 * k;
-      if (e < D) p.part_o[pi * D + e] = o[k];
+      if (e < VD) p.part_o[pi * D + e] = o[k];
     }
     if (lane == 0) {
       p.part_ml[pi * 2 + 0] = m;
@@ -196,11 +196,13 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
 }
 
 // Merge the per-chunk partials of one (token, head): global max, rescaled sums, divide.
-template <typename TT>
+// Partial rows have stride head_dim; outputs hold v_head_dim values per head.
+template <typename TT, int NE>
 __global__ __launch_bounds__(64) void split_reduce_kernel(const AttnParams p) {
   const int h = blockIdx.x, t = blockIdx.y;
   const int lane = threadIdx.x;
   const int D = p.head_dim;
+  const int VD = p.v_head_dim;
   const int b = seq_of_token(p.cum, p.batch, t);
   const int nq = p.cum[b + 1] - p.cum[b];
   const int64_t total = (int64_t)max(p.past[b], 0) + nq;
@@ -223,7 +225,9 @@ __global__ __launch_bounds__(64) void split_reduce_kernel(const AttnParams p) {
   const float f = finalize_factor(M, L, sink_logit<TT>(p, h));
   typename TT::raw* out = reinterpret_cast<typename TT::raw*>(p.out);
   const float* po = p.part_o + base * D;
-  float acc[kMaxLanesElems] = {0.f, 0.f, 0.f, 0.f};
+  float acc[NE];
+#pragma unroll
+  for (int q = 0; q < NE; ++q) acc[q] = 0.0f;
   for (int s0 = 0; s0 < nsplit; s0 += 64) {
     // every lane stays active through the shuffles: split weights live one per lane
     float wl = 0.0f;
@@ -236,38 +240,58 @@ __global__ __launch_bounds__(64) void split_reduce_kernel(const AttnParams p) {
       const float wk = __shfl(wl, k, 64);
       const float* row = po + (int64_t)(s0 + k) * D;
 #pragma unroll
-      for (int q = 0; q < kMaxLanesElems; ++q) {
+      for (int q = 0; q < NE; ++q) {
         const int e = lane + 64 * q;
-        if (e < D) acc[q] += row[e] * wk;
+        if (e < VD) acc[q] += row[e] * wk;
       }
     }
   }
 #pragma unroll
-  for (int q = 0; q < kMaxLanesElems; ++q) {
+  for (int q = 0; q < NE; ++q) {
     const int e = lane + 64 * q;
-    if (e < D) out[((int64_t)t * p.num_heads + h) * D + e] = TT::from_f32(acc[q] * f);
+    if (e < VD) out[((int64_t)t * p.num_heads + h) * VD + e] = TT::from_f32(acc[q] * f);
   }
+}
+
+// Lanes hold head_dim / 64 elements: 4 up to 256, 10 up to 640.
+constexpr int kMaxHeadDim = 640;
+template <int NE>
+constexpr bool ne_covers(int d) { return d <= 64 * NE; }
+
+template <typename TT, int NE>
+hipError_t launch_generic_ne(const AttnParams& p, pa_dtype cache_dtype, hipStream_t s) {
+  dim3 grid(p.max_splits, p.num_heads, p.num_tokens), block(64);
+  switch (cache_dtype) {
+    case PA_DTYPE_FP8_E4M3:
+      hipLaunchKernelGGL((attn_generic_kernel<TT, Fp8Cache, NE>), grid, block, 0, s, p);
+      break;
+    case PA_DTYPE_INT8:
+      hipLaunchKernelGGL((attn_generic_kernel<TT, I8Cache, NE>), grid, block, 0, s, p);
+      break;
+    case PA_DTYPE_INT4:
+      hipLaunchKernelGGL((attn_generic_kernel<TT, I4Cache, NE>), grid, block, 0, s, p);
+      break;
+    default:
+      if (cache_dtype != TT::code) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((attn_generic_kernel<TT, TT, NE>), grid, block, 0, s, p);
+      break;
+  }
+  return hipGetLastError();
 }
 
 template <typename TT>
 hipError_t launch_generic_t(const AttnParams& p, pa_dtype cache_dtype, hipStream_t s) {
-  dim3 grid(p.max_splits, p.num_heads, p.num_tokens), block(64);
-  switch (cache_dtype) {
-    case PA_DTYPE_FP8_E4M3:
-      hipLaunchKernelGGL((attn_generic_kernel<TT, Fp8Cache>), grid, block, 0, s, p);
-      break;
-    case PA_DTYPE_INT8:
-      hipLaunchKernelGGL((attn_generic_kernel<TT, I8Cache>), grid, block, 0, s, p);
-      break;
-    case PA_DTYPE_INT4:
-      hipLaunchKernelGGL((attn_generic_kernel<TT, I4Cache>), grid, block, 0, s, p);
-      break;
-    default:
-      if (cache_dtype != TT::code) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((attn_generic_kernel<TT, TT>), grid, block, 0, s, p);
-      break;
-  }
-  return hipGetLastError();
+  return ne_covers<4>(p.head_dim) ? launch_generic_ne<TT, 4>(p, cache_dtype, s)
+                                  : launch_generic_ne<TT, 10>(p, cache_dtype, s);
+}
+
+template <typename TT>
+void launch_reduce_t(const AttnParams& p, hipStream_t s) {
+  dim3 grid(p.num_heads, p.num_tokens), block(64);
+  if (ne_covers<4>(p.head_dim))
+    hipLaunchKernelGGL((split_reduce_kernel<TT, 4>), grid, block, 0, s, p);
+  else
+    hipLaunchKernelGGL((split_reduce_kernel<TT, 10>), grid, block, 0, s, p);
 }
 
 }  // namespace
@@ -275,7 +299,8 @@ hipError_t launch_generic_t(const AttnParams& p, pa_dtype cache_dtype, hipStream
 hipError_t launch_attn_generic(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
                                hipStream_t s) {
   if (p.num_tokens <= 0) return hipSuccess;
-  if (p.head_dim > 64 * kMaxLanesElems) return hipErrorInvalidValue;
+  if (p.head_dim > kMaxHeadDim || p.v_head_dim < 1 || p.v_head_dim > p.head_dim)
+    return hipErrorInvalidValue;
   switch (act) {
     case PA_DTYPE_FLOAT16: return launch_generic_t<TF16>(p, cache_dtype, s);
     case PA_DTYPE_BFLOAT16: return launch_generic_t<TBF16>(p, cache_dtype, s);
@@ -286,19 +311,13 @@ hipError_t launch_attn_generic(const AttnParams& p, pa_dtype act, pa_dtype cache
 
 hipError_t launch_split_reduce(const AttnParams& p, pa_dtype act, hipStream_t s) {
   if (p.num_tokens <= 0 || p.max_splits <= 1) return hipSuccess;
-  dim3 grid(p.num_heads, p.num_tokens), block(64);
+  if (p.head_dim > kMaxHeadDim || p.v_head_dim < 1 || p.v_head_dim > p.head_dim)
+    return hipErrorInvalidValue;
   switch (act) {
-    case PA_DTYPE_FLOAT16:
-      hipLaunchKernelGGL((split_reduce_kernel<TF16>), grid, block, 0, s, p);
-      break;
-    case PA_DTYPE_BFLOAT16:
-      hipLaunchKernelGGL((split_reduce_kernel<TBF16>), grid, block, 0, s, p);
-      break;
-    case PA_DTYPE_FLOAT32:
-      hipLaunchKernelGGL((split_reduce_kernel<TF32>), grid, block, 0, s, p);
-      break;
-    default:
-      return hipErrorInvalidValue;
+    case PA_DTYPE_FLOAT16: launch_reduce_t<TF16>(p, s); break;
+    case PA_DTYPE_BFLOAT16: launch_reduce_t<TBF16>(p, s); break;
+    case PA_DTYPE_FLOAT32: launch_reduce_t<TF32>(p, s); break;
+    default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }

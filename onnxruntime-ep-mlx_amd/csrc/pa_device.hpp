@@ -263,6 +263,11 @@ struct AttnParams {
   // (b * kv_heads + kh) * linear_cap + pos.  0: paged cache.
   int32_t linear_cap;
   int32_t k_quant, v_quant;  // integer caches: PA_QUANT_PER_TENSOR / PA_QUANT_PER_CHANNEL
+  // LATENT layout (kv_heads == 1): the value of a position is the first v_head_dim dims of its
+  // key row (key cache / k_new); outputs are [T, H * v_head_dim].  v_head_dim == head_dim and
+  // v_from_key == 0 otherwise.
+  int32_t v_head_dim;
+  int32_t v_from_key;
 };
 
 // Final normalisation shared by every attention kernel: the factor that turns an output

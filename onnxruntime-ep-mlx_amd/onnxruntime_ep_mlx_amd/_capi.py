@@ -76,6 +76,7 @@ class PaAttn(C.Structure):
     _fields_ = [
         ("num_heads", C.c_int32), ("scale", C.c_float), ("softcap", C.c_float),
         ("local_window_size", C.c_int32), ("is_causal", C.c_int32), ("head_sink", C.c_void_p),
+        ("v_head_size", C.c_int32),
     ]
 
 
@@ -85,6 +86,7 @@ class PaNode(C.Structure):
         ("softcap", C.c_float), ("local_window_size", C.c_int32), ("do_rotary", C.c_int32),
         ("rotary_interleaved", C.c_int32), ("rotary_offset", C.c_int32),
         ("is_causal", C.c_int32), ("qk_norm_epsilon", C.c_float),
+        ("v_head_size", C.c_int32), ("kv_cache_layout_latent", C.c_int32),
     ]
 
 

@@ -88,9 +88,9 @@ def cache_desc(key_cache: torch.Tensor, value_cache: torch.Tensor,
     """Cache descriptor.  Integer caches (torch.int8 / torch.uint8 = int4) take fp32 scales
     with k_quant_type / v_quant_type "PER_TENSOR" ([1]) or "PER_CHANNEL" ([kv_heads, head]);
     an int4 cache's last dimension is ceil(head / 2), so pass head_dim for odd heads."""
-    if key_cache.dim() != 4 or key_cache.shape != value_cache.shape:
+    if key_cache.dim() != 4 or (value_cache is not None and key_cache.shape != value_cache.shape):
         raise ValueError("key_cache must be [num_blocks,block_size,kv_num_heads,head_size]")
-    if key_cache.dtype != value_cache.dtype:
+    if value_cache is not None and key_cache.dtype != value_cache.dtype:
         raise ValueError("key/value caches must share one storage dtype")
     nb, bs, kv, width = key_cache.shape
     dt = pa_dtype(key_cache.dtype)
@@ -265,7 +265,8 @@ def paged_attention(query, key, value, key_cache, value_cache, cumulative_sequen
                     k_scale=None, v_scale=None, attention_metadata=None, *, num_heads,
                     kv_num_heads, scale=0.0, softcap=0.0, local_window_size=-1, do_rotary=0,
                     rotary_interleaved=0, rotary_offset=0, is_causal=1, qk_norm_epsilon=1e-6,
-                    k_quant_type="NONE", v_quant_type="NONE", validate=True, output=None):
+                    k_quant_type="NONE", v_quant_type="NONE", v_head_size=0,
+                    kv_cache_layout="SEPARATE", validate=True, output=None):
     """com.microsoft::PagedAttention on MI355X (operator-level entry, pa_paged_attention).
 
     ``attention_metadata`` is accepted and ignored, like the reference
@@ -275,7 +276,13 @@ def paged_attention(query, key, value, key_cache, value_cache, cumulative_sequen
     ``value`` both None means packed QKV: ``query`` is [T, (num_heads + 2 kv_num_heads) * head].
     Integer caches (torch.int8, torch.uint8 = int4) take ``k_scale``/``v_scale`` with
     ``k_quant_type``/``v_quant_type`` "PER_TENSOR" or "PER_CHANNEL".
+    ``kv_cache_layout="LATENT"``: one kv head, ``value`` and ``value_cache`` None; the values are
+    the first ``v_head_size`` dims of the (rotated) key rows and the output is
+    [T, num_heads * v_head_size].
     """
+    if kv_cache_layout not in ("SEPARATE", "LATENT"):
+        raise ValueError("kv_cache_layout must be SEPARATE or LATENT")
+    latent = kv_cache_layout == "LATENT"
     del attention_metadata
     lib = capi.load()
     if query.dim() != 2:
@@ -284,17 +291,19 @@ def paged_attention(query, key, value, key_cache, value_cache, cumulative_sequen
                  ("value_cache", value_cache)):
         _need_cuda(n, t)
         _contig(n, t)
-    packed = key is None and value is None
+    packed = not latent and key is None and value is None
     head = query.shape[1] // (num_heads + 2 * kv_num_heads if packed else num_heads)
+    v_head = v_head_size or head
     node = capi.PaNode(num_heads, kv_num_heads, scale, softcap, local_window_size, do_rotary,
-                       rotary_interleaved, rotary_offset, is_causal, qk_norm_epsilon)
+                       rotary_interleaved, rotary_offset, is_causal, qk_norm_epsilon,
+                       v_head_size, int(latent))
     host = {}
     if validate:
         for name, t in (("cum", cumulative_sequence_length), ("past", past_seqlens),
                         ("bt", block_table), ("slots", slot_mapping)):
             host[name] = None if t is None else t.detach().to("cpu").contiguous()
     if output is None:
-        output = query.new_empty((query.shape[0], num_heads * head))
+        output = query.new_empty((query.shape[0], num_heads * v_head))
     cache = cache_desc(key_cache, value_cache, k_scale, v_scale, head_dim=head,
                        k_quant_type=k_quant_type, v_quant_type=v_quant_type)
     io = capi.PaIO(

@@ -283,7 +283,7 @@ int orc_reshape_and_cache(const void* key, const void* value, int act_dtype, voi
       if (is_int_dt(cache_dtype)) {
         int bits = cache_dtype == ORC_I8 ? 8 : 4;
         for (int kh = 0; kh < kv_heads; ++kh)
-          for (int side = 0; side < 2; ++side) {
+          for (int side = 0; side < (value_cache ? 2 : 1); ++side) {
             const void* src = side ? value : key;
             const float* sc = side ? v_scale : k_scale;
             int pc = (side ? v_mode : k_mode) == ORC_QUANT_PER_CHANNEL;
@@ -297,20 +297,23 @@ int orc_reshape_and_cache(const void* key, const void* value, int act_dtype, voi
       } else if (cache_dtype == ORC_E4M3) {
         int64_t blk = slot / block_size;
         for (int kh = 0; kh < kv_heads; ++kh) {
-          float ks = k_scale[blk * kv_heads + kh], vs = v_scale[blk * kv_heads + kh];
+          float ks = k_scale[blk * kv_heads + kh];
+          float vs = value_cache ? v_scale[blk * kv_heads + kh] : 0.0f;
           for (int i = 0; i < head_dim; ++i) {
             int64_t src = t * row + (int64_t)kh * head_dim + i;
             int64_t dst = slot * row + (int64_t)kh * head_dim + i;
             ((uint8_t*)key_cache)[dst] = quant_e4m3(ld(key, src, act_dtype), ks);
-            ((uint8_t*)value_cache)[dst] = quant_e4m3(ld(value, src, act_dtype), vs);
+            if (value_cache)
+              ((uint8_t*)value_cache)[dst] = quant_e4m3(ld(value, src, act_dtype), vs);
           }
         }
       } else {
         int es = esize(cache_dtype);
         memcpy((char*)key_cache + slot * row * es, (const char*)key + t * row * es,
                (size_t)(row * es));
-        memcpy((char*)value_cache + slot * row * es, (const char*)value + t * row * es,
-               (size_t)(row * es));
+        if (value_cache) /* LATENT: no value cache */
+          memcpy((char*)value_cache + slot * row * es, (const char*)value + t * row * es,
+                 (size_t)(row * es));
       }
     }
   }
@@ -344,10 +347,19 @@ int orc_paged_attention(const void* q, const void* k_new, const void* v_new, int
                         const int32_t* cum, const int32_t* past, const int32_t* block_table,
                         int batch, int max_blocks, int64_t num_blocks, int block_size,
                         int num_heads, int kv_heads, int head_dim, float scale, float softcap,
-                        int window, int causal, const float* head_sink, double* out) {
+                        int window, int causal, const float* head_sink, double* out,
+                        int v_head_dim) {
   (void)num_blocks;
   int g = num_heads / kv_heads;
   int d = head_dim;
+  /* LATENT (value_cache == NULL): values are the first vd dims of the key rows
+   * (attention.rs:4058-4062 for new rows, :4210-4213 for cached rows). */
+  int latent = value_cache == NULL;
+  int vd = v_head_dim > 0 ? v_head_dim : d;
+  if (latent) {
+    value_cache = key_cache;
+    v_new = k_new;
+  }
   int64_t row = (int64_t)kv_heads * d;
   int width = cache_width(cache_dtype, d);
   int64_t crow = (int64_t)kv_heads * width;
@@ -397,8 +409,8 @@ int orc_paged_attention(const void* q, const void* k_new, const void* v_new, int
         double sink = head_sink ? (double)head_sink[h] : -INFINITY;
         double mm = m > sink ? m : sink;
         double l = 0.0;
-        double* o = out + qbase;
-        for (int e = 0; e < d; ++e) o[e] = 0.0;
+        double* o = out + (t * num_heads + h) * (int64_t)vd;
+        for (int e = 0; e < vd; ++e) o[e] = 0.0;
         if (mm == -INFINITY) continue; /* nothing visible: the sum==0 guard leaves zeros */
         for (int64_t p = 0; p < total; ++p) {
           if (scores[p] == -INFINITY) continue;
@@ -407,17 +419,17 @@ int orc_paged_attention(const void* q, const void* k_new, const void* v_new, int
           if (p < pastb || quant) {
             int64_t blk = block_table[(int64_t)b * max_blocks + p / block_size];
             int64_t base = (blk * block_size + p % block_size) * crow + (int64_t)kh * width;
-            for (int e = 0; e < d; ++e)
+            for (int e = 0; e < vd; ++e)
               o[e] += w * cache_elem(value_cache, cache_dtype, v_scale, v_mode, blk, kv_heads, kh,
                                      d, base, e);
           } else {
             int64_t base = (s0 + (p - pastb)) * row + (int64_t)kh * d;
-            for (int e = 0; e < d; ++e) o[e] += w * (double)ld(v_new, base + e, act_dtype);
+            for (int e = 0; e < vd; ++e) o[e] += w * (double)ld(v_new, base + e, act_dtype);
           }
         }
         if (head_sink) l += exp(sink - mm);
         if (l != 0.0)
-          for (int e = 0; e < d; ++e) o[e] /= l;
+          for (int e = 0; e < vd; ++e) o[e] /= l;
       }
     }
   }
@@ -435,7 +447,8 @@ int orc_paged_attention_op(int act_dtype, int cache_dtype, const void* query, co
                            const int32_t* slot_mapping, const float* head_sink,
                            const void* q_norm, const void* k_norm, float norm_eps,
                            int num_heads, int kv_heads, int head_dim, float scale,
-                           float softcap, int window, int causal, double* out, void* out_t) {
+                           float softcap, int window, int causal, double* out, void* out_t,
+                           int v_head_dim) {
   int es = esize(act_dtype);
   size_t qbytes = (size_t)num_tokens * num_heads * head_dim * es;
   size_t kbytes = (size_t)num_tokens * kv_heads * head_dim * es;
@@ -470,9 +483,9 @@ int orc_paged_attention_op(int act_dtype, int cache_dtype, const void* query, co
   rc = orc_paged_attention(qr, kr, value, act_dtype, key_cache, value_cache, cache_dtype, k_scale,
                            v_scale, k_mode, v_mode, cum, past, block_table, batch, max_blocks,
                            num_blocks, block_size, num_heads, kv_heads, head_dim, scale, softcap,
-                           window, causal, head_sink, out);
+                           window, causal, head_sink, out, v_head_dim);
   if (!rc && out_t) {
-    int64_t n = num_tokens * (int64_t)num_heads * head_dim;
+    int64_t n = num_tokens * (int64_t)num_heads * (v_head_dim > 0 ? v_head_dim : head_dim);
     for (int64_t i = 0; i < n; ++i) st(out_t, i, (float)out[i], act_dtype);
   }
 done:

@@ -83,7 +83,8 @@ int orc_reshape_and_cache(const void* key, const void* value, int act_dtype, voi
  * fallback attention.rs:4192-4319, sink/softcap :79-118). q/k_new/v_new are the rotated rows in
  * act_dtype.  head_sink: fp32 [H] or NULL.  out: [num_tokens, H*head_dim] doubles.
  * Quantised caches (fp8, int8, int4) read every position, new rows included, from the pages
- * (attention.rs:4192-4195). */
+ * (attention.rs:4192-4195).  value_cache == NULL is the LATENT layout: values are the first
+ * v_head_dim (0 = head_dim) dims of the key rows and out is [num_tokens, H*v_head_dim]. */
 int orc_paged_attention(const void* q, const void* k_new, const void* v_new, int act_dtype,
                         const void* key_cache, const void* value_cache, int cache_dtype,
                         const float* k_scale, const float* v_scale, int k_mode, int v_mode,
@@ -91,7 +92,7 @@ int orc_paged_attention(const void* q, const void* k_new, const void* v_new, int
                         const int32_t* past, const int32_t* block_table, int batch,
                         int max_blocks, int64_t num_blocks, int block_size, int num_heads,
                         int kv_heads, int head_dim, float scale, float softcap, int window,
-                        int causal, const float* head_sink, double* out);
+                        int causal, const float* head_sink, double* out, int v_head_dim);
 
 /* Whole operator: norm + rope + append + attention (paged_attention_op attention.rs:3857-4382
  * and _paged_ref test_paged_attention.py:63-157).  Caches are updated in place.
@@ -106,7 +107,8 @@ int orc_paged_attention_op(int act_dtype, int cache_dtype, const void* query, co
                            const int32_t* slot_mapping, const float* head_sink,
                            const void* q_norm, const void* k_norm, float norm_eps,
                            int num_heads, int kv_heads, int head_dim, float scale,
-                           float softcap, int window, int causal, double* out, void* out_t);
+                           float softcap, int window, int causal, double* out, void* out_t,
+                           int v_head_dim);
 
 /* Contiguous-cache GroupQueryAttention (ORT CPU semantics as restated by the reference's
  * test_gqa_position_cache.py:88-126 and gqa_batched attention.rs:586-848):

@@ -59,11 +59,12 @@ def lib() -> C.CDLL:
                                             I32, P, I64, I32, I32, I32]
         L.orc_paged_attention.restype = I32
         L.orc_paged_attention.argtypes = [P, P, P, I32, P, P, I32, P, P, I32, I32, P, P, P, I32,
-                                          I32, I64, I32, I32, I32, I32, F, F, I32, I32, P, P]
+                                          I32, I64, I32, I32, I32, I32, F, F, I32, I32, P, P, I32]
         L.orc_paged_attention_op.restype = I32
         L.orc_paged_attention_op.argtypes = [I32, I32, P, P, P, I64, P, P, P, P, I32, I32, I64,
                                              I32, P, P, P, I32, I32, P, P, I64, I32, I32, I32, P,
-                                             P, P, P, F, I32, I32, I32, F, F, I32, I32, P, P]
+                                             P, P, P, F, I32, I32, I32, F, F, I32, I32, P, P,
+                                             I32]
         L.orc_gqa_contiguous.restype = I32
         L.orc_gqa_contiguous.argtypes = [I32, P, P, P, P, P, I32, I32, I32, I32, I32, I32, P, F,
                                          F, I32, I32, P, I32, P, P, I32, I32]
@@ -157,19 +158,22 @@ def reshape_and_cache(key, value, act_dtype, kc, vc, cache_dtype, cum, past, bt,
 
 
 def paged_attention_op(case: dict, *, return_cache=True):
-    """Run the whole operator on a case dict (see pa_cases.make_case)."""
+    """Run the whole operator on a case dict (see pa_cases.make_case).  A case without a
+    value_cache (and value) is the LATENT layout with v_head_size output dims."""
     c = case
-    kc, vc = c["key_cache"].copy(), c["value_cache"].copy()
+    kc = c["key_cache"].copy()
+    vc = None if c.get("value_cache") is None else c["value_cache"].copy()
     nb, bs, kv, _ = kc.shape
     d = head_dim_of(kc, c["cache_dtype"], c.get("head_dim"))
+    vd = c.get("v_head_size", 0) or d
     T = c["query"].shape[0]
     H = c["num_heads"]
-    out = np.zeros((T, H * d), np.float64)
-    out_t = np.zeros((T, H * d), RAW[c["dtype"]])
+    out = np.zeros((T, H * vd), np.float64)
+    out_t = np.zeros((T, H * vd), RAW[c["dtype"]])
     cos, sin = c.get("cos_cache"), c.get("sin_cache")
     sink = c.get("head_sink_f32")
     rc = lib().orc_paged_attention_op(
-        c["dtype"], c["cache_dtype"], _p(c["query"]), _p(c["key"]), _p(c["value"]), T, _p(kc),
+        c["dtype"], c["cache_dtype"], _p(c["query"]), _p(c["key"]), _p(c.get("value")), T, _p(kc),
         _p(vc), _p(c.get("k_scale")), _p(c.get("v_scale")), c.get("k_quant", 0),
         c.get("v_quant", 0), nb, bs, _p(c["cum"]), _p(c["past"]),
         _p(c["block_table"]), len(c["cum"]) - 1, c["block_table"].shape[1], _p(cos), _p(sin),
@@ -178,7 +182,7 @@ def paged_attention_op(case: dict, *, return_cache=True):
         _p(sink), _p(c.get("q_norm")), _p(c.get("k_norm")), c.get("qk_norm_epsilon", 1e-6), H,
         kv, d, c.get("scale", 0.0) or float(np.float32(1.0) / np.sqrt(np.float32(d))),
         c.get("softcap", 0.0), c.get("local_window_size", -1), c.get("is_causal", 1), _p(out),
-        _p(out_t))
+        _p(out_t), vd)
     assert rc == 0, rc
     return out, out_t, kc, vc
 
@@ -192,7 +196,7 @@ def paged_attention(q, k_new, v_new, act_dtype, kc, vc, cache_dtype, cum, past, 
     rc = lib().orc_paged_attention(
         _p(q), _p(k_new), _p(v_new), act_dtype, _p(kc), _p(vc), cache_dtype, _p(k_scale),
         _p(v_scale), k_mode, v_mode, _p(cum), _p(past), _p(bt), len(cum) - 1, bt.shape[1], nb,
-        bs, H, kv, d, scale, softcap, window, causal, _p(head_sink), _p(out))
+        bs, H, kv, d, scale, softcap, window, causal, _p(head_sink), _p(out), 0)
     assert rc == 0, rc
     return out
 

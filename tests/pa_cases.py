@@ -166,6 +166,19 @@ def run_gpu_op(case: dict, validate=True, device="cuda", packed=False):
         rotary_offset=case.get("rotary_offset", 0), is_causal=case.get("is_causal", 1),
         qk_norm_epsilon=case.get("qk_norm_epsilon", 1e-6),
         k_quant_type=QUANT_NAMES[case.get("k_quant", 0)],
-        v_quant_type=QUANT_NAMES[case.get("v_quant", 0)], validate=validate)
+        v_quant_type=QUANT_NAMES[case.get("v_quant", 0)],
+        v_head_size=case.get("v_head_size", 0),
+        kv_cache_layout="LATENT" if case.get("latent") else "SEPARATE", validate=validate)
     torch.cuda.synchronize()
-    return from_torch(out, dt), from_torch(kc, cdt), from_torch(vc, cdt)
+    return (from_torch(out, dt), from_torch(kc, cdt),
+            None if vc is None else from_torch(vc, cdt))
+
+
+def make_latent_case(H, d, vd, nb, bs, batch, **kw):
+    """LATENT layout case (kv_num_heads 1, no value input or value cache)."""
+    c = make_case(H, 1, d, nb, bs, batch, **kw)
+    c.pop("value")
+    c.pop("value_cache")
+    c["latent"] = True
+    c["v_head_size"] = vd
+    return c

@@ -158,6 +158,41 @@ def test_claim_int8_without_explicit_cache_dtype_and_packed_qkv():
     assert _claim(n) == (1, "")
 
 
+def _latent_node(d=16, vd=8, H=2):
+    """test_paged_attention.py:727-744: LATENT node, kv 1, value and value_cache absent."""
+    n = _node(dtype=capi.PA_DTYPE_FLOAT16, H=H, KV=1, d=d, nb=3, bs=4, T=2, B=1, mb=3,
+              rotary=True)
+    n.input_present[2] = n.input_present[4] = 0
+    n.input_shape[8][1] = n.input_shape[9][1] = 4
+    n.rotary_offset = 8
+    n.v_head_size = vd
+    n.has_scale_attr = 1
+    n.kv_cache_layout_latent = 1
+    n.output_shape[0][1] = H * vd
+    return n
+
+
+def test_claim_accepts_latent_layout():
+    assert _claim(_latent_node()) == (1, "")
+
+
+@pytest.mark.parametrize("mutate,reason", [
+    (lambda n: setattr(n, "kv_num_heads", 2), "LATENT layout requires kv_num_heads=1"),
+    (lambda n: n.input_present.__setitem__(4, 1), "requires absent value/value_cache"),
+    (lambda n: setattr(n, "has_scale_attr", 0), "asymmetric value heads requires an explicit"),
+    (lambda n: setattr(n, "v_head_size", 32), "v_head_size must not exceed head_size"),
+    (lambda n: n.input_dtype.__setitem__(3, capi.PA_INT8_DTYPE),
+     "quantized LATENT cache contract is not supported"),
+    (lambda n: (setattr(n, "num_outputs", 3), n.output_present.__setitem__(2, 1)),
+     "no separate value cache output"),
+])
+def test_claim_declines_broken_latent_nodes(mutate, reason):
+    n = _latent_node()
+    mutate(n)
+    ok, why = _claim(n)
+    assert ok == 0 and reason in why, why
+
+
 # test_quantized_kv.py:615-641 (paged=True): each broken static contract is declined.
 @pytest.mark.parametrize("bad,reason", [
     ("mode", "requires PER_TENSOR or PER_CHANNEL"),
