@@ -7,12 +7,18 @@ split-K paged decode on matrix cores.  Inputs are synthetic (seeded N(0,1), bf16
 HBM before timing.
 
   value      = algorithmic KV bytes per step / step time (GB/s); KV bytes = 4096 * sum(ctx)
-  roofline   = the attention launch (pa_attention: counter clear + balanced decode kernel, same
-               stream) timed with events on that stream: KV bytes / launch time vs 8 TB/s
+  roofline   = the attention launch (pa_attention_ex: balanced decode kernel + partial merge
+               kernel, same stream) timed with events on that stream: KV bytes / launch time vs
+               8 TB/s
   cpu_baseline = the oracle's threaded contiguous-KV GQA decode (ORT CPU semantics) on a
                bounded sample of the same sequences, scaled to the full batch by KV bytes
 
-Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10]
+--config c4 / c5 measure BASELINE.json configs 4 (chunked prefill, Qwen2.5-7B shape: value =
+TFLOP/s of the causal attention FLOPs, roofline vs the 2.5 PFLOP/s dense bf16 MFMA peak) and 5
+(fp8 e4m3 pages, B=16, ctx 32768: value = GB/s of fp8 KV bytes, roofline vs 8 TB/s) the same way;
+their lines carry their own metric names and no CPU baseline.
+
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--config c3|c4|c5]
 """
 from __future__ import annotations
 
@@ -42,12 +48,14 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run 1 GiB device copies (known bytes) to scale HBM counters")
+    ap.add_argument("--config", choices=("c3", "c4", "c5"), default="c3",
+                    help="c3 (default): BASELINE.json config 3; c4 / c5: configs 4 / 5")
     return ap.parse_args()
 
 
-def load_traffic():
+def load_traffic(name="decode_c3_traffic.json"):
     """HBM bytes per attention launch from the committed counter summary, if present."""
-    path = ROOT / "profiles" / "decode_c3_traffic.json"
+    path = ROOT / "profiles" / name
     if not path.exists():
         return None
     with open(path) as f:
@@ -85,10 +93,73 @@ def build_workload(torch, ep, seed):
     q = torch.randn((B, H * d), generator=g, device=dev).to(torch.bfloat16)
     k = torch.randn((B, KV * d), generator=g, device=dev).to(torch.bfloat16)
     v = torch.randn((B, KV * d), generator=g, device=dev).to(torch.bfloat16)
-    w = dict(B=B, H=H, KV=KV, d=d, bs=bs, nb=nb, ctx=ctx, bt_np=bt, kc=kc, vc=vc, cos=cos,
-             sin=sin, q=q, k=k, v=v)
+    w = dict(B=B, T=B, mq=1, H=H, KV=KV, d=d, bs=bs, nb=nb, ctx=ctx, bt_np=bt, kc=kc, vc=vc,
+             cos=cos, sin=sin, q=q, k=k, v=v, ks=None, vs=None)
     w["cum"] = torch.arange(B + 1, dtype=torch.int32, device=dev)
     w["past"] = torch.from_numpy(ctx - 1).to(dev)
+    w["bt"] = torch.from_numpy(bt).to(dev)
+    return w
+
+
+def build_prefill_workload(torch, seed=4):
+    """bf16, 8 sequences each appending a 512-token chunk over a cached
+    context U[0, 4096], 28 query / 4 kv heads, d 128, block 16, causal within the chunk, packed
+    cumulative_sequence_length, values N(0,1).  No rotary (the config names none)."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    B, H, KV, d, bs, chunk = 8, 28, 4, 128, 16, 512
+    past = rng.integers(0, 4097, size=B).astype(np.int32)
+    mb = (4096 + chunk + bs - 1) // bs
+    nb = B * mb
+    bt = rng.permutation(nb).astype(np.int32).reshape(B, mb)
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    kc = torch.randn((nb, bs, KV, d), generator=g, device=dev).to(torch.bfloat16)
+    vc = torch.randn((nb, bs, KV, d), generator=g, device=dev).to(torch.bfloat16)
+    T = B * chunk
+    w = dict(B=B, T=T, mq=chunk, H=H, KV=KV, d=d, bs=bs, nb=nb, ctx=past + chunk, bt_np=bt,
+             kc=kc, vc=vc, cos=None, sin=None, ks=None, vs=None,
+             q=torch.randn((T, H * d), generator=g, device=dev).to(torch.bfloat16),
+             k=torch.randn((T, KV * d), generator=g, device=dev).to(torch.bfloat16),
+             v=torch.randn((T, KV * d), generator=g, device=dev).to(torch.bfloat16))
+    w["cum"] = torch.arange(0, T + 1, chunk, dtype=torch.int32, device=dev)
+    w["past"] = torch.from_numpy(past).to(dev)
+    w["bt"] = torch.from_numpy(bt).to(dev)
+    # causal attention FLOPs: QK and PV, 2 * 2 * H * d per visible (query, key) pair
+    w["flops"] = sum(4.0 * H * d * (chunk * int(p) + chunk * (chunk + 1) / 2) for p in past)
+    return w
+
+
+def build_fp8_workload(torch, seed=5):
+    """e4m3 K/V pages with per-(block, kv-head) fp32 scales, bf16 query,
+    batch 16, 64 query / 8 kv heads, d 128, context 32768 per sequence, block 16, random block
+    tables, values N(0,1) quantised with scale amax/448 per (block, kv-head)."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    B, H, KV, d, bs, ctx = 16, 64, 8, 128, 16, 32768
+    nbs = ctx // bs
+    nb = B * nbs + 64
+    bt = rng.permutation(nb)[: B * nbs].astype(np.int32).reshape(B, nbs)
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    kc = torch.empty((nb, bs, KV, d), dtype=torch.float8_e4m3fn, device=dev)
+    vc = torch.empty_like(kc)
+    ks = torch.empty((nb, KV), dtype=torch.float32, device=dev)
+    vs = torch.empty_like(ks)
+    for t, sc in ((kc, ks), (vc, vs)):
+        for i in range(0, nb, 4096):  # slices bound the fp32 temporary
+            n = min(4096, nb - i)
+            x = torch.randn((n, bs, KV, d), generator=g, device=dev)
+            s_ = (x.abs().amax(dim=(1, 3)) / 448.0).clamp_min(1e-12)
+            sc[i:i + n] = s_
+            t[i:i + n] = (x / s_[:, None, :, None]).to(torch.float8_e4m3fn)
+    w = dict(B=B, T=B, mq=1, H=H, KV=KV, d=d, bs=bs, nb=nb, ctx=np.full(B, ctx, np.int32),
+             bt_np=bt, kc=kc, vc=vc, ks=ks, vs=vs, cos=None, sin=None,
+             q=torch.randn((B, H * d), generator=g, device=dev).to(torch.bfloat16),
+             k=torch.randn((B, KV * d), generator=g, device=dev).to(torch.bfloat16),
+             v=torch.randn((B, KV * d), generator=g, device=dev).to(torch.bfloat16))
+    w["cum"] = torch.arange(B + 1, dtype=torch.int32, device=dev)
+    w["past"] = torch.full((B,), ctx - 1, dtype=torch.int32, device=dev)
     w["bt"] = torch.from_numpy(bt).to(dev)
     return w
 
@@ -103,7 +174,7 @@ class Step:
                   launch on its own for the roofline.
     """
 
-    def __init__(self, torch, ep, w, chunk):
+    def __init__(self, torch, ep, w, chunk, kind=1):
         import numpy as np
         from onnxruntime_ep_mlx_amd import _capi as capi
         from onnxruntime_ep_mlx_amd.ops import attn_desc, batch_desc, cache_desc
@@ -113,29 +184,34 @@ class Step:
         self.act = capi.PA_DTYPE_BFLOAT16
         self.stream = torch.cuda.current_stream().cuda_stream
         self.out = torch.empty_like(w["q"])
+        rotary = w["cos"] is not None
+        ptr = lambda t: None if t is None else t.data_ptr()
         # operator-level blocks
         self.host = {n: np.ascontiguousarray(w[n].cpu().numpy()) for n in ("cum", "past", "bt")}
-        self.node = capi.PaNode(w["H"], w["KV"], 0.0, 0.0, -1, 1, 0, 0, 1, 1e-6)
+        self.node = capi.PaNode(w["H"], w["KV"], 0.0, 0.0, -1, int(rotary), 0, 0, 1, 1e-6)
         self.io = capi.PaIO(
-            self.act, w["B"], w["H"] * w["d"], w["q"].data_ptr(), w["k"].data_ptr(),
-            w["v"].data_ptr(), cache_desc(w["kc"], w["vc"]), w["cum"].data_ptr(),
-            w["past"].data_ptr(), w["bt"].data_ptr(), w["B"], w["bt"].shape[1],
-            w["cos"].data_ptr(), w["sin"].data_ptr(), w["cos"].shape[0], w["cos"].shape[1],
-            None, None, None, None, self.host["cum"].ctypes.data, self.host["past"].ctypes.data,
+            self.act, w["T"], w["H"] * w["d"], w["q"].data_ptr(), w["k"].data_ptr(),
+            w["v"].data_ptr(), cache_desc(w["kc"], w["vc"], w["ks"], w["vs"]),
+            w["cum"].data_ptr(), w["past"].data_ptr(), w["bt"].data_ptr(), w["B"],
+            w["bt"].shape[1], ptr(w["cos"]), ptr(w["sin"]), w["cos"].shape[0] if rotary else 0,
+            w["cos"].shape[1] if rotary else 0, None, None, None, None,
+            self.host["cum"].ctypes.data, self.host["past"].ctypes.data,
             self.host["bt"].ctypes.data, None, self.out.data_ptr())
         self.op_ws_bytes = self.lib.pa_paged_attention_workspace_bytes(C.byref(self.node),
                                                                        C.byref(self.io))
         self.op_ws = torch.empty(max(self.op_ws_bytes, 1), dtype=torch.uint8, device="cuda")
         # kernel-level blocks
-        self.cache = cache_desc(w["kc"], w["vc"])
-        self.batch = batch_desc(w["cum"], w["past"], w["bt"], w["B"], None, 1,
+        self.cache = cache_desc(w["kc"], w["vc"], w["ks"], w["vs"])
+        self.batch = batch_desc(w["cum"], w["past"], w["bt"], w["T"], None, w["mq"],
                                 capi.PA_BATCH_NEW_ROWS_IN_CACHE)
         self.attn = attn_desc(w["H"])
-        self.q_out = torch.empty_like(w["q"])
-        self.k_out = torch.empty_like(w["k"])
+        self.rotary = rotary
+        self.q_out = torch.empty_like(w["q"]) if rotary else w["q"]
+        self.k_out = torch.empty_like(w["k"]) if rotary else w["k"]
         self.chunk = chunk
+        self.kind = kind
         self.ws_bytes = self.lib.pa_attention_workspace_bytes_ex(
-            C.byref(self.cache), C.byref(self.batch), C.byref(self.attn), self.act, 1, chunk)
+            C.byref(self.cache), C.byref(self.batch), C.byref(self.attn), self.act, kind, chunk)
         self.ws = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device="cuda")
 
     def __call__(self):
@@ -145,11 +221,13 @@ class Step:
 
     def append(self):
         w = self.w
+        rot = self.rotary
         rc = self.lib.pa_rotary_append(
             C.byref(self.cache), C.byref(self.batch), w["H"], self.act, w["q"].data_ptr(),
-            w["k"].data_ptr(), w["v"].data_ptr(), self.q_out.data_ptr(), self.k_out.data_ptr(),
-            w["cos"].data_ptr(), w["sin"].data_ptr(), w["cos"].shape[0], w["cos"].shape[1], 0, 0,
-            None, None, 0.0, self.stream)
+            w["k"].data_ptr(), w["v"].data_ptr(), self.q_out.data_ptr() if rot else None,
+            self.k_out.data_ptr() if rot else None, w["cos"].data_ptr() if rot else None,
+            w["sin"].data_ptr() if rot else None, w["cos"].shape[0] if rot else 0,
+            w["cos"].shape[1] if rot else 0, 0, 0, None, None, 0.0, self.stream)
         self.capi.check(rc)
 
     def attention(self):
@@ -157,7 +235,8 @@ class Step:
         rc = self.lib.pa_attention_ex(
             C.byref(self.cache), C.byref(self.batch), C.byref(self.attn), self.act,
             self.q_out.data_ptr(), self.k_out.data_ptr(), w["v"].data_ptr(),
-            self.out.data_ptr(), self.ws.data_ptr(), self.ws_bytes, 1, self.chunk, self.stream)
+            self.out.data_ptr(), self.ws.data_ptr(), self.ws_bytes, self.kind, self.chunk,
+            self.stream)
         self.capi.check(rc)
 
 
@@ -207,6 +286,60 @@ def cpu_baseline(torch, w, step, n_seq, seconds):
     }
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def other_config_line(args, w, ms_step, attn_ms, kv_bytes):
+    """JSON line of BASELINE.json configs 4 and 5 (not the driver's default line)."""
+    common = {"n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+              "ms_per_step": round(ms_step, 4), "us_per_step": round(ms_step * 1e3, 1),
+              "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+              "cpu_baseline": None}
+    if args.config == "c4":
+        tf_step = w["flops"] / (ms_step * 1e-3) / 1e12
+        tf_attn = w["flops"] / (attn_ms * 1e-3) / 1e12
+        return {
+            "metric": "chunked-prefill paged attention TFLOP/s (causal QK+PV FLOPs)",
+            "value": round(tf_step, 2), "unit": "TFLOP/s", **common, "dtype": "bf16",
+            "data": "synthetic (seeded N(0,1) bf16 pages and q/k/v; random block tables)",
+            "config": {
+                "workload": "chunked prefill, Qwen2.5-7B shape (BASELINE.json config 4): append "
+                            "of 8 x 512 new tokens + causal paged attention over past "
+                            "U[0,4096]",
+                "batch": w["B"], "tokens": w["T"], "num_heads": w["H"], "kv_heads": w["KV"],
+                "head_dim": w["d"], "block_size": w["bs"], "pasts": [int(x) for x in
+                                                                     w["ctx"] - w["mq"]],
+                "flops_per_step": w["flops"], "kv_bytes_read": int(kv_bytes),
+                "entry": "pa_paged_attention (host-validated metadata)"},
+            "roofline": {
+                "bound": "mfma", "achieved": round(tf_attn, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(tf_attn / MFMA_BF16_PEAK_TFLOPS, 4),
+                "traffic": None, "kernel": "pa_attention (decode_chunked_kernel, NG row groups)",
+                "us_per_launch": round(attn_ms * 1e3, 1)},
+        }
+    gbs = kv_bytes / (ms_step * 1e-3) / 1e9
+    attn_gbs = kv_bytes / (attn_ms * 1e-3) / 1e9
+    return {
+        "metric": "fp8 paged GQA decode µs/step + achieved HBM GB/s (fp8 KV bytes), B=16, "
+                  "ctx 32768",
+        "value": round(gbs, 2), "unit": "GB/s", **common, "dtype": "bf16 x e4m3",
+        "tokens_per_s": round(w["B"] / (ms_step * 1e-3), 1),
+        "data": "synthetic (seeded N(0,1) quantised to e4m3 with amax/448 block scales)",
+        "config": {
+            "workload": "long-context fp8 paged decode (BASELINE.json config 5): append + "
+                        "split-K paged attention over e4m3 pages",
+            "batch": w["B"], "num_heads": w["H"], "kv_heads": w["KV"], "head_dim": w["d"],
+            "block_size": w["bs"], "ctx": 32768, "kv_bytes_per_step": int(kv_bytes),
+            "entry": "pa_paged_attention (host-validated metadata)"},
+        "roofline": {
+            "bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
+            "traffic": load_traffic("decode_fp8_c5_traffic.json"),
+            "kernel": "pa_attention (decode_balanced_kernel fp8 + balanced_merge_kernel)",
+            "us_per_launch": round(attn_ms * 1e3, 1)},
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -217,9 +350,17 @@ def main():
     import torch
     import onnxruntime_ep_mlx_amd as ep
     torch.cuda.set_device(0)
-    w = build_workload(torch, ep, args.seed)
-    step = Step(torch, ep, w, args.chunk)
-    kv_bytes = 4096.0 * float(w["ctx"].sum())
+    if args.config == "c3":
+        w = build_workload(torch, ep, args.seed)
+        step = Step(torch, ep, w, args.chunk, kind=1)
+    elif args.config == "c4":
+        w = build_prefill_workload(torch)
+        step = Step(torch, ep, w, args.chunk, kind=0)
+    else:
+        w = build_fp8_workload(torch)
+        step = Step(torch, ep, w, args.chunk, kind=0)
+    kv_elem = 1 if w["ks"] is not None else 2  # fp8 pages: one byte per element
+    kv_bytes = float(w["ctx"].sum()) * w["KV"] * w["d"] * 2 * kv_elem
 
     if args.calibrate_copy:
         # Plain copies of exactly 1 GiB (read 1 GiB, write 1 GiB): the reference dispatches
@@ -257,6 +398,10 @@ def main():
     torch.cuda.synchronize()
     attn_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
     attn_gbs = kv_bytes / (attn_ms * 1e-3) / 1e9
+
+    if args.config != "c3":
+        print(json.dumps(other_config_line(args, w, ms_step, attn_ms, kv_bytes)), flush=True)
+        return
 
     cpu = None
     if not args.no_cpu_baseline:

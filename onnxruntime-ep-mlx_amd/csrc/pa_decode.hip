@@ -1025,7 +1025,21 @@ decode_balanced_kernel(const AttnParams p) {
   // the kv-head slices of each page row are then fetched through one CU together, which the
   // memory system serves measurably faster than the same slices fetched from W different CUs.
   const int W = blockDim.x >> 6;
-  const int x = blockIdx.x * W + (threadIdx.x >> 6), seg = blockIdx.y;
+  const int nx = p.kv_heads / W;             // head groups
+  const int nseg = p.max_splits / p.mix;     // segments; the grid holds nx * nseg workgroups
+  // Workgroups go round-robin to the 8 XCDs (id % 8).  Runs of 8 consecutive ids share a head
+  // group, so every XCD serves every head group: with the head group as the fastest index the
+  // groups were tied to one XCD parity each, and the odd-XCD half finished ~5 us later.
+  const int id = blockIdx.x;
+  int hg, seg;
+  if (nseg % 8 == 0) {
+    hg = (id >> 3) % nx;
+    seg = ((id >> 3) / nx) * 8 + (id & 7);
+  } else {
+    hg = id % nx;
+    seg = id / nx;
+  }
+  const int x = hg * W + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int M = p.mix;
   const int64_t S = total_steps(p, lane);
@@ -1166,7 +1180,7 @@ hipError_t launch_decode_balanced(const AttnParams& p, pa_dtype act, pa_dtype ca
   if (p.part_o == nullptr || p.mix < 1 || p.mix > p.kv_heads || p.max_splits % p.mix != 0)
     return hipErrorInvalidValue;
   const int W = p.kv_heads % 4 == 0 ? 4 : p.kv_heads % 2 == 0 ? 2 : 1;
-  dim3 grid(p.kv_heads / W, p.max_splits / p.mix), block(64 * W);
+  dim3 grid((p.kv_heads / W) * (p.max_splits / p.mix)), block(64 * W);
   hipError_t e = (act == PA_DTYPE_FLOAT16) ? launch_t<TF16>(p, grid, block, true, f8, s)
                                            : launch_t<TBF16>(p, grid, block, true, f8, s);
   if (e != hipSuccess) return e;
