@@ -314,7 +314,7 @@ def other_config_line(args, w, ms_step, attn_ms, kv_bytes):
             "roofline": {
                 "bound": "mfma", "achieved": round(tf_attn, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(tf_attn / MFMA_BF16_PEAK_TFLOPS, 4),
-                "traffic": None, "kernel": "pa_attention (decode_chunked_kernel, NG row groups)",
+                "traffic": None, "kernel": "pa_attention (prefill_kernel, LDS-shared K/V steps)",
                 "us_per_launch": round(attn_ms * 1e3, 1)},
         }
     gbs = kv_bytes / (ms_step * 1e-3) / 1e9

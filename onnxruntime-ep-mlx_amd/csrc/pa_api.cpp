@@ -195,29 +195,39 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
   // query rows (prefill chunks), so each loaded key/value step serves more rows (4 groups at
   // d=64, 2 at d=128: what fits the register file).
   pl.ng = (pl.kind == 1 && (int64_t)g * mq >= 64) ? (c->head_dim == 64 ? 4 : 2) : 1;
-  if (chunk <= 0) {
-    if (kind == 2) {
-      chunk = 1 << 30;  // prefill kernel walks the whole context
+  if (chunk <= 0 && kind == 2) {
+    // Prefill workgroups (4 wavefronts, pa::kPrefillRows grouped query rows each): split the
+    // context only when they cannot fill two workgroups per CU.
+    const int64_t units = (int64_t)b->batch * c->kv_heads *
+                          (((int64_t)g * mq + pa::kPrefillRows - 1) / pa::kPrefillRows);
+    const int64_t target = 2 * (int64_t)device_cus();
+    if (units >= target) {
+      chunk = (int)std::min<int64_t>(((int64_t)ctx + 31) / 32 * 32, INT32_MAX / 2);
     } else {
-      // Work units without split-K: (sequence, kv-head, row groups) for the MFMA kernel,
-      // (token, head) for the VALU kernel.  Split the context only when they cannot fill the
-      // GPU (~2048 one-per-SIMD wavefronts for NG = 4, ~4096 otherwise).
-      const int64_t rows_pw = 16 * pl.ng;
-      const int64_t units =
-          pl.kind == 1 ? (int64_t)b->batch * c->kv_heads * (((int64_t)g * mq + rows_pw - 1) / rows_pw)
-                       : (int64_t)std::max(b->num_tokens, 1) * a->num_heads;
-      const int64_t target = pl.ng > 1 ? 2048 : 4096;
-      if (units >= target) {
-        chunk = (int)std::min<int64_t>(((int64_t)ctx + 31) / 32 * 32, INT32_MAX / 2);
-      } else {
-        const int64_t splits = (target + units - 1) / units;
-        int64_t ch = (ctx + splits - 1) / splits;
-        ch = ((ch + 31) / 32) * 32;
-        chunk = (int)std::min<int64_t>(std::max<int64_t>(ch, 256), 1024);
-      }
+      const int64_t splits = (target + units - 1) / units;
+      int64_t ch = (ctx + splits - 1) / splits;
+      chunk = (int)std::min<int64_t>(std::max<int64_t>((ch + 31) / 32 * 32, 256), INT32_MAX / 2);
     }
   }
-  if (pl.kind != 2) chunk = std::max(32, chunk / 32 * 32);
+  if (chunk <= 0) {
+    // Work units without split-K: (sequence, kv-head, row groups) for the MFMA kernel,
+    // (token, head) for the VALU kernel.  Split the context only when they cannot fill the
+    // GPU (~2048 one-per-SIMD wavefronts for NG = 4, ~4096 otherwise).
+    const int64_t rows_pw = 16 * pl.ng;
+    const int64_t units =
+        pl.kind == 1 ? (int64_t)b->batch * c->kv_heads * (((int64_t)g * mq + rows_pw - 1) / rows_pw)
+                     : (int64_t)std::max(b->num_tokens, 1) * a->num_heads;
+    const int64_t target = pl.ng > 1 ? 2048 : 4096;
+    if (units >= target) {
+      chunk = (int)std::min<int64_t>(((int64_t)ctx + 31) / 32 * 32, INT32_MAX / 2);
+    } else {
+      const int64_t splits = (target + units - 1) / units;
+      int64_t ch = (ctx + splits - 1) / splits;
+      ch = ((ch + 31) / 32) * 32;
+      chunk = (int)std::min<int64_t>(std::max<int64_t>(ch, 256), 1024);
+    }
+  }
+  chunk = std::max(32, chunk / 32 * 32);
   pl.chunk = chunk;
   pl.max_splits = (int)std::max<int64_t>(1, ((int64_t)ctx + chunk - 1) / chunk);
   pl.part_rows = pl.max_splits > 1

@@ -287,6 +287,11 @@ __device__ __forceinline__ float sink_logit(const AttnParams& p, int h) {
   return TT::to_f32(reinterpret_cast<const typename TT::raw*>(p.head_sink)[h]) * kLog2e;
 }
 
+// Prefill kernel geometry: 16-row groups per wavefront, and grouped query rows per workgroup
+// of 4 wavefronts.
+constexpr int kPrefillGroups = 2;
+constexpr int kPrefillRows = 64 * kPrefillGroups;
+
 // Launchers (defined in the .hip files).
 hipError_t launch_rotary_append(const AppendParams& p, pa_dtype act, pa_dtype cache_dtype,
                                 hipStream_t s);

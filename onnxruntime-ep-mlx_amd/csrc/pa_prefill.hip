@@ -1,16 +1,322 @@
-// pa_prefill.hip — chunked-prefill attention over the paged cache.
+// pa_prefill.hip — chunked-prefill attention over the paged cache on gfx950 matrix cores.
 //
-// Until the LDS-shared prefill kernel lands, multi-token queries run on the split-K MFMA decode
-// kernel, which parallelises over 16-row groups of (query token, head) rows and skips key tiles
-// outside every row's causal range.
-#include "pa_device.hpp"
+// Replaces the reference's prefill route, the dense fallback (attention.rs:4192-4319) that
+// gathers the pages, concatenates the new rows and runs SDPA with native GQA heads for more
+// than 8 query tokens (:4235-4253, paged_sdpa :3786-3809).
+//
+// Work unit: one workgroup of 4 wavefronts per (sequence, kv-head, block of 64*NG grouped query
+// rows, context chunk).  Rows r = (query token i, head hh) with r = i*g + hh, as in the decode
+// kernels; wavefront w owns rows row0 + 16*NG*w + 16*j, j < NG, and computes them with the
+// shared 16x16x32 tile step (pa_tiles.hpp).
+//
+// Every 32-key step is fetched from the pages once per workgroup, the four wavefronts taking a
+// quarter each (key tile A, key tile B, the first and the second half of the value dims), and
+// written to LDS as the per-lane MFMA operand images the tile step consumes -- value rows
+// already regrouped into the B-operand layout.  Each wavefront then reads its operands with
+// 16-byte LDS reads, consecutive lanes at consecutive addresses (conflict free).  Against every
+// wavefront streaming the step by itself this cuts the L2->CU bytes 4x and does the value
+// regroup once per workgroup instead of once per wavefront.
+//
+// Pipeline: two LDS buffers and one barrier per step.  In iteration k the wavefronts compute
+// step k from buffer k&1, then write step k+1 (whose global loads were issued one iteration
+// earlier) into buffer (k+1)&1 -- last read in iteration k-1, before the previous barrier --
+// and issue the global loads of step k+2.  Two workgroups share a CU (two wavefronts per SIMD),
+// so one computes while the other waits at its barrier.
+//
+// Keys come from the pages when the step lies below the cache limit and the block size is a
+// multiple of 16 (one page per 16-key tile, page ids from a block-table window held one entry
+// per lane); other steps (new rows not yet in the pages, odd block sizes) address every row on
+// its own.  Value rows at or past the sequence end are zeroed and their scores masked.
+#include "pa_tiles.hpp"
 
 namespace pa {
+namespace {
 
-bool prefill_mfma_supported(int, pa_dtype, pa_dtype) { return false; }
+// One wavefront's quarter of a step: 16-key tile T = role & 1 of the keys (roles 0, 1) or of the
+// values (roles 2, 3), loaded as 4 pieces of D/8 bytes per lane -- the same instruction
+// sequence for every role, only the bases and strides differ:
+//   key role:   row c of the tile, dims 8G..8G+7 of each 32-dim k-step (16 bytes per k-step);
+//   value role: rows 4G..4G+3 of the tile, the lane's DL = D/16 dims DL*c ..
+// r[] holds the pieces in order (key k-step s = 16-byte item s; value row e = words HW*e ..).
+template <int D>
+struct Quarter {
+  static constexpr int PW = D / 32;  // words per piece
+  uint32_t r[4 * PW];
+  __device__ u32x4 item(int s) const { return u32x4{r[4 * s], r[4 * s + 1], r[4 * s + 2], r[4 * s + 3]}; }
+  __device__ uint32_t vword(int e, int wi) const { return r[PW * e + wi]; }
+};
 
-hipError_t launch_prefill_mfma(const AttnParams&, pa_dtype, pa_dtype, hipStream_t) {
-  return hipErrorNotSupported;
+template <int D>
+__device__ __forceinline__ void load_piece(uint32_t* r, const char* ptr) {
+  if constexpr (D == 128) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(ptr);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = v[i];
+  } else {
+    const u32x2 v = *reinterpret_cast<const u32x2*>(ptr);
+    r[0] = v[0];
+    r[1] = v[1];
+  }
+}
+
+// Block-table window: lane i holds the page id of block first + i.
+struct PageWindow {
+  int first;
+  int ids;
+};
+
+__device__ __forceinline__ void window_at(PageWindow& pw, const WaveInfo& w, int bi, int lane) {
+  pw.first = bi;
+  pw.ids = w.bt[min(bi + lane, w.max_blocks - 1)];
+}
+
+// Byte offset (from the cache base) of the first row of the 16-key tile starting at key t.
+__device__ __forceinline__ int64_t tile_base(const WaveInfo& w, PageWindow& pw, int t, int lane,
+                                             int D) {
+  const int bi = min(div_bs(t, w), w.max_blocks - 1);
+  if (bi < pw.first || bi >= pw.first + 64) window_at(pw, w, bi, lane);
+  int64_t blk = __builtin_amdgcn_readlane(pw.ids, bi - pw.first);
+  blk = min(max(blk, (int64_t)0), w.num_blocks - 1);
+  return (blk * w.bs + mod_bs(t, w)) * w.rowb + (int64_t)w.kh * D * 2;
+}
+
+// Per-lane geometry of a role: piece s sits at row `row0 + s * row_step` of the tile and byte
+// `col0 + (s >> 1) * col_a + (s & 1) * col_b` of that row's kv-head slice.
+struct RoleGeom {
+  bool value;
+  int row0, row_step;
+  int col0, col_a, col_b;
+};
+
+template <int D>
+__device__ __forceinline__ RoleGeom role_geom(int role, int c, int G) {
+  RoleGeom g;
+  g.value = role >= 2;
+  if (g.value) {
+    g.row0 = 4 * G;
+    g.row_step = 1;
+    g.col0 = (D / 16) * 2 * c;
+    g.col_a = g.col_b = 0;
+  } else {
+    g.row0 = c;
+    g.row_step = 0;
+    g.col0 = 16 * G;
+    g.col_a = D == 128 ? 128 : 64;  // k-step pairs (d=128) / k-steps (d=64)
+    g.col_b = D == 128 ? 64 : 8;    // next k-step (d=128) / second half of a k-step (d=64)
+  }
+  return g;
+}
+
+// Issue this wavefront's loads of the step at key t0.
+template <int D>
+__device__ __forceinline__ void load_quarter(const WaveInfo& w, PageWindow& pw, const RoleGeom& rg,
+                                             int role, int t0, int lane, Quarter<D>& q) {
+  const int t = t0 + 16 * (role & 1);
+  // With every key in the pages the last (partial) step comes from them too: rows past the end
+  // are masked / zeroed and page ids are clamped into the pool.
+  const bool paged = w.bs % 16 == 0 && (t0 + 32 <= w.cache_limit || w.cache_limit >= w.total);
+  if (paged) {
+    const char* base = (rg.value ? w.vc : w.kc) + tile_base(w, pw, t, lane, D) +
+                       (int64_t)rg.row0 * w.rowb + rg.col0;
+    const int64_t rstep = rg.row_step * w.rowb;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      load_piece<D>(q.r + Quarter<D>::PW * s,
+                    base + s * rstep + (s >> 1) * rg.col_a + (s & 1) * rg.col_b);
+  } else {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      load_piece<D>(q.r + Quarter<D>::PW * s,
+                    row_ptr(w, t + rg.row0 + s * rg.row_step, rg.value, D) + rg.col0 +
+                        (s >> 1) * rg.col_a + (s & 1) * rg.col_b);
+  }
+}
+
+// Write this wavefront's quarter of the step at key t0 into LDS buffer `buf` ([item][lane]):
+// items 0 .. 2*KS-1 are the key operands (tile, k-step), items 2*KS + j the value operands of
+// N-tile j.  Word m of a value operand combines value rows 2m and 2m+1 of the step (rows 4G+i
+// of tile A for m < 2, of tile B for m >= 2), so value role T writes words 2T, 2T+1 of every
+// N-tile.
+template <int D>
+__device__ __forceinline__ void store_quarter(u32x4 (*buf)[64], Quarter<D>& q, int role, int t0,
+                                              int total, int lane, int G) {
+  constexpr int KS = D / 32, DL = D / 16;
+  const int T = role & 1;
+  if (role < 2) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) buf[T * KS + s][lane] = q.item(s);
+  } else {
+    if (t0 + 32 > total) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (t0 + 16 * T + 4 * G + e >= total)
+#pragma unroll
+          for (int i = 0; i < Quarter<D>::PW; ++i) q.r[Quarter<D>::PW * e + i] = 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < DL; ++j) {
+      u32x2 half;
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const uint32_t lo = q.vword(2 * m, j >> 1), hi = q.vword(2 * m + 1, j >> 1);
+        half[m] = (j & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+      }
+      reinterpret_cast<u32x2*>(&buf[2 * KS + j][lane])[T] = half;
+    }
+  }
+}
+
+template <typename TT, int D, bool CAP, int NG>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+prefill_kernel(const AttnParams p) {
+  using vec8 = typename TT::vec8;
+  constexpr int KS = D / 32, DL = D / 16, NI = 2 * KS + DL;
+  constexpr int ROWS = 64 * NG;  // grouped query rows per workgroup
+  __shared__ u32x4 lds[2][NI][64];
+  // Grid x: (row block, sequence, kv-head) with (sequence, kv-head) fastest and the row blocks
+  // in reverse, so the last blocks of each chunk (the most keys under the causal mask) start
+  // first.  Grid y: context chunk (split-K).
+  const int units = p.batch * p.kv_heads;
+  const int unit = blockIdx.x % units;
+  const int rb = (int)(gridDim.x / units) - 1 - (int)(blockIdx.x / units);
+  const int kh = unit % p.kv_heads, b = unit / p.kv_heads;
+  const int split = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, G = lane >> 4;
+  // Everything up to the first barrier is uniform over the workgroup.
+  const int s0 = min(max(p.cum[b], 0), p.num_tokens);
+  const int s1 = min(max(p.cum[b + 1], s0), p.num_tokens);
+  const int nq = s1 - s0;
+  const int g = p.num_heads / p.kv_heads;
+  const int R = g * nq;
+  const int row0 = rb * ROWS;
+  if (row0 >= R) return;
+  const int pastb = max(p.past[b], 0);
+  const int total = pastb + nq;
+  const int start = split * p.chunk;
+  if (start >= total) return;
+  const int end = start + min(p.chunk, total - start);
+  const bool single = start == 0 && end == total;
+  // Metadata beyond the planned capacity leaves no partial buffer: rows stay unwritten.
+  if (!single && p.part_o == nullptr) return;
+  // Keys any row of the workgroup can see.
+  const int r_last = min(row0 + ROWS, R) - 1;
+  const int hi = p.causal ? pastb + r_last / g + 1 : total;
+  const int lo = p.window > 0 ? max(0, pastb + row0 / g - p.window + 1) : 0;
+  const int t_first = max(start, (lo / 32) * 32);
+  const int t_last = min(end, hi);
+  const int nsteps = t_last > t_first ? (t_last - t_first + 31) / 32 : 0;
+
+  const WaveInfo w = make_wave(p, D, b, kh, s0, pastb, total);
+  // This wavefront's rows and the keys they can see (steps outside are not computed).
+  const int wrow0 = row0 + 16 * NG * wave;
+  RowState<TT, D> rs[NG];
+#pragma unroll
+  for (int j = 0; j < NG; ++j) init_rows<TT, D>(rs[j], p, w, wrow0 + 16 * j, R, g, c, G);
+  // Keys visible to some row [any_lo, any_hi) and to every row [all_lo, all_hi) of the wave.
+  int any_lo = 0, any_hi = -1, all_lo = 0, all_hi = -1;
+  if (wrow0 < R) {
+    const int qf = wrow0 / g, ql = (min(wrow0 + 16 * NG, R) - 1) / g;
+    any_hi = p.causal ? pastb + ql + 1 : total;
+    all_hi = min(end, p.causal ? pastb + qf + 1 : total);
+    any_lo = p.window > 0 ? pastb + qf - p.window + 1 : 0;
+    all_lo = p.window > 0 ? pastb + ql - p.window + 1 : 0;
+  }
+
+  PageWindow pw;
+  window_at(pw, w, min(div_bs(t_first, w), w.max_blocks - 1), lane);
+  const RoleGeom rg = role_geom<D>(wave, c, G);
+  Quarter<D> q;
+  if (nsteps > 0) {
+    load_quarter<D>(w, pw, rg, wave, t_first, lane, q);
+    store_quarter<D>(lds[0], q, wave, t_first, total, lane, G);
+    if (nsteps > 1) load_quarter<D>(w, pw, rg, wave, t_first + 32, lane, q);
+  }
+  __syncthreads();
+  for (int k = 0; k < nsteps; ++k) {
+    const int t0 = t_first + 32 * k;
+    if (t0 < any_hi && t0 + 32 > any_lo) {
+      u32x4 kop[2][KS];
+      u32x4 vop[DL];
+#pragma unroll
+      for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+        for (int s = 0; s < KS; ++s) kop[tile][s] = lds[k & 1][tile * KS + s][lane];
+#pragma unroll
+      for (int j = 0; j < DL; ++j) vop[j] = lds[k & 1][2 * KS + j][lane];
+      auto vb = [&](int n) { return __builtin_bit_cast(vec8, vop[n]); };
+      if (t0 >= all_lo && t0 + 32 <= all_hi) {
+#pragma unroll
+        for (int j = 0; j < NG; ++j)
+          attend_step<TT, D, CAP, false, false>(rs[j], kop, vb, t0, end, G, p.scale_log2,
+                                                p.scale, p.softcap, 1.f, 1.f, 1.f, 1.f);
+      } else {
+#pragma unroll
+        for (int j = 0; j < NG; ++j)
+          attend_step<TT, D, CAP, false, true>(rs[j], kop, vb, t0, end, G, p.scale_log2,
+                                               p.scale, p.softcap, 1.f, 1.f, 1.f, 1.f);
+      }
+    }
+    if (k + 1 < nsteps) store_quarter<D>(lds[(k + 1) & 1], q, wave, t0 + 32, total, lane, G);
+    if (k + 2 < nsteps) load_quarter<D>(w, pw, rg, wave, t0 + 64, lane, q);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int j = 0; j < NG; ++j) {
+    const int r0 = wrow0 + 16 * j;
+    if (r0 >= R) break;
+    const int rc = min(r0 + c, R - 1);
+    const float sink_c = sink_logit<TT>(p, kh * g + rc % g);
+    store_rows<TT, D>(rs[j], p, kh, s0, r0, R, g, c, G, sink_c, single,
+                      [&](int64_t t, int oh, int) {
+                        return (t * p.num_heads + oh) * p.max_splits + split;
+                      });
+  }
+}
+
+template <typename TT, int D>
+hipError_t launch_d(const AttnParams& p, dim3 grid, hipStream_t s) {
+  constexpr int NG = kPrefillGroups;
+  if (p.softcap > 0.0f)
+    hipLaunchKernelGGL((prefill_kernel<TT, D, true, NG>), grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((prefill_kernel<TT, D, false, NG>), grid, dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+template <typename TT>
+hipError_t launch_t(const AttnParams& p, dim3 grid, hipStream_t s) {
+  switch (p.head_dim) {
+    case 64: return launch_d<TT, 64>(p, grid, s);
+    case 128: return launch_d<TT, 128>(p, grid, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+bool prefill_mfma_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype) {
+  if (act != PA_DTYPE_FLOAT16 && act != PA_DTYPE_BFLOAT16) return false;
+  if (cache_dtype != act) return false;
+  return head_dim == 64 || head_dim == 128;
+}
+
+// Grid: one workgroup per (row block, sequence, kv-head) and context chunk (p.max_splits
+// chunks of p.chunk keys).
+hipError_t launch_prefill_mfma(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
+                               hipStream_t s) {
+  if (!prefill_mfma_supported(p.head_dim, act, cache_dtype)) return hipErrorInvalidValue;
+  if (p.linear_cap > 0) return hipErrorInvalidValue;  // paged caches only
+  if (p.batch <= 0) return hipSuccess;
+  if (p.chunk < 32 || p.chunk % 32 != 0 || p.max_splits < 1) return hipErrorInvalidValue;
+  const int g = p.num_heads / p.kv_heads;
+  const int mq = p.max_query_len > 0 ? p.max_query_len : p.num_tokens;
+  const int64_t rbs = ((int64_t)g * mq + kPrefillRows - 1) / kPrefillRows;
+  const int64_t units = (int64_t)p.batch * p.kv_heads;
+  if (rbs * units > INT32_MAX || p.max_splits > 65535) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(rbs * units), p.max_splits);
+  if (act == PA_DTYPE_FLOAT16) return launch_t<TF16>(p, grid, s);
+  return launch_t<TBF16>(p, grid, s);
 }
 
 }  // namespace pa

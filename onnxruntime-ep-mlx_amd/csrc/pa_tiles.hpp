@@ -1,0 +1,312 @@
+// pa_tiles.hpp — the 16x16x32 MFMA tile step shared by the paged decode and prefill kernels:
+// per-lane operand layouts, one 32-key step of online-softmax attention for a 16-row group,
+// and the row set-up / epilogue (final rows or split-K partials).
+//
+// Scores are computed transposed, S^T = K_tile . Q^T (A = 16 keys x 32 dims straight from the
+// page rows, B = Q^T held in registers), so lane l ends with S[key 4*(l/16)+i][row l%16] of each
+// 16-key tile -- exactly the A-operand layout that P needs for O += P . V.  The value operand
+// (8 keys x 1 dim per lane) is assembled from 8 value-row slices; output column n of N-tile j
+// is head dim DL*n + j.  P is split into hi + lo 16-bit parts (two MFMAs), so the PV product
+// keeps ~16 mantissa bits.
+#pragma once
+
+#include "pa_device.hpp"
+
+namespace pa {
+namespace {
+
+template <int D>
+struct VRow;  // one lane's slice of one value row: DL = D/16 elements
+template <>
+struct VRow<64> {
+  u32x2 w;
+  __device__ uint32_t word(int i) const { return w[i]; }
+};
+template <>
+struct VRow<128> {
+  u32x4 w;
+  __device__ uint32_t word(int i) const { return w[i]; }
+};
+
+template <int D>
+__device__ __forceinline__ VRow<D> ld_vrow(const char* ptr);
+template <>
+__device__ __forceinline__ VRow<64> ld_vrow<64>(const char* ptr) {
+  return VRow<64>{*reinterpret_cast<const u32x2*>(ptr)};
+}
+template <>
+__device__ __forceinline__ VRow<128> ld_vrow<128>(const char* ptr) {
+  return VRow<128>{*reinterpret_cast<const u32x4*>(ptr)};
+}
+
+__device__ __forceinline__ u32x4 ld16(const char* ptr) {
+  return *reinterpret_cast<const u32x4*>(ptr);
+}
+
+template <int D>
+struct Step {
+  u32x4 k[2][D / 32];  // tile A / tile B key rows, 8 dims per k-step
+  VRow<D> v[8];        // value rows: keys 4G+e of tile A (e<4) and of tile B (e>=4)
+};
+
+// Wave-uniform description of the (sequence, kv-head, chunk) being processed.
+struct WaveInfo {
+  const char* kc;  // key cache (bytes)
+  const char* vc;
+  const char* kn;  // new key rows (bytes)
+  const char* vn;
+  int b, kh, s0, pastb, total, cache_limit;
+  int bs, bs_shift;  // block size, log2 if a power of two else -1
+  int max_blocks, num_tokens;
+  int64_t num_blocks;
+  int64_t rowb;      // bytes between consecutive cache rows (kv_heads * D * 2)
+  int first_bi;      // first block-table index of the chunk
+  const int32_t* bt; // this sequence's block-table row
+};
+
+__device__ __forceinline__ int div_bs(int x, const WaveInfo& w) {
+  return w.bs_shift >= 0 ? (x >> w.bs_shift) : x / w.bs;
+}
+__device__ __forceinline__ int mod_bs(int x, const WaveInfo& w) {
+  return w.bs_shift >= 0 ? (x & (w.bs - 1)) : x % w.bs;
+}
+
+// Byte offset of key/value row `pos` for this lane (any block size), choosing the cache page
+// (positions < cache_limit) or the new rows.  Positions past the end clamp to the last real
+// row; block ids are clamped into the pool, so malformed metadata cannot fault.
+__device__ __forceinline__ const char* row_ptr(const WaveInfo& w, int pos, bool value, int D) {
+  if (pos >= w.total) pos = w.total - 1;
+  if (pos < w.cache_limit) {
+    const int bi = min(div_bs(pos, w), w.max_blocks - 1);
+    int64_t blk = w.bt[bi];
+    blk = min(max(blk, (int64_t)0), w.num_blocks - 1);
+    return (value ? w.vc : w.kc) + (blk * w.bs + mod_bs(pos, w)) * w.rowb + (int64_t)w.kh * D * 2;
+  }
+  int64_t tok = min(max((int64_t)w.s0 + (pos - w.pastb), (int64_t)0), (int64_t)w.num_tokens - 1);
+  return (value ? w.vn : w.kn) + tok * w.rowb + (int64_t)w.kh * D * 2;
+}
+
+// Regroup 8 value rows (lane holds DL dims of each) into the MFMA B-operand of N-tile j:
+// 8 keys x head dim DL*c + j.
+template <typename TT, int D>
+__device__ __forceinline__ typename TT::vec8 value_operand(const Step<D>& st, int j) {
+  u32x4 w;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const uint32_t lo = st.v[2 * m].word(j >> 1), hi = st.v[2 * m + 1].word(j >> 1);
+    w[m] = (j & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+  }
+  return __builtin_bit_cast(typename TT::vec8, w);
+}
+
+// Row state of one 16-row group.
+template <typename TT, int D>
+struct RowState {
+  typename TT::vec8 qv[D / 32];
+  f32x4 o[D / 16];
+  float m_run;   // running max of row c (log2 units); identical across the 4 lane groups
+  float l_part;  // this lane's share of the row-c denominator
+  int vis_lo, vis_hi;
+};
+
+// SC: fp8 pages, whose key codes score as ks * (q . code) and whose value codes weigh in as
+// vs * code; ks/vs are the page scales of tile A (keys t0..t0+15) and tile B.
+//
+// The key operand `k` holds the two 16-key tiles (A: keys t0..t0+15, B: t0+16..t0+31), 16 bytes
+// per lane and k-step; `vop(j)` returns the value operand of N-tile j (8 keys x head dim
+// DL*c + j, keys in the order the scores come out: 4G+i of tile A, then of tile B).
+//
+// MASK = false: the caller knows every key of the step is visible to every valid row of the
+// group (rows past the end of the sequence have zero queries and are never stored), so the
+// per-score position tests are skipped.
+//
+// Probabilities use the hardware base-2 exponential (v_exp_f32) without the denormal-range
+// rescaling of exp2f: arguments are <= 8 (lazy max) and a probability below 2^-126 of the row
+// maximum adds nothing to an fp32 sum that holds the maximum's own 1.
+template <typename TT, int D, bool CAP, bool SC, bool MASK = true, typename ValueOp>
+__device__ __forceinline__ void attend_step(RowState<TT, D>& rs, const u32x4 (&k)[2][D / 32],
+                                            ValueOp vop, int t0, int end, int G,
+                                            float scale_log2, float scale, float cap, float ksA,
+                                            float ksB, float vsA, float vsB) {
+  using vec8 = typename TT::vec8;
+  constexpr int KS = D / 32, DL = D / 16;
+  f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    sa = TT::mfma(__builtin_bit_cast(vec8, k[0][s]), rs.qv[s], sa);
+    sb = TT::mfma(__builtin_bit_cast(vec8, k[1][s]), rs.qv[s], sb);
+  }
+  if constexpr (SC) {
+    sa *= ksA;
+    sb *= ksB;
+  }
+  float x[8];
+  float lmax = kNegInf;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int pos = t0 + 16 * (e >> 2) + 4 * G + (e & 3);
+    const float sv = (e < 4) ? sa[e & 3] : sb[e & 3];
+    float xv;
+    if constexpr (CAP)
+      xv = cap * tanhf(sv * scale / cap) * kLog2e;
+    else
+      xv = sv * scale_log2;
+    if constexpr (MASK) {
+      const bool vis = pos < end && pos >= rs.vis_lo && pos < rs.vis_hi;
+      x[e] = vis ? xv : kNegInf;
+    } else {
+      (void)pos;
+      x[e] = xv;
+    }
+    lmax = fmaxf(lmax, x[e]);
+  }
+  if (__any(lmax > rs.m_run + 8.0f)) {
+    float rmax = fmaxf(lmax, __shfl_xor(lmax, 16, 64));
+    rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+    const float m_new = fmaxf(rs.m_run, rmax);
+    const float alpha = (m_new == kNegInf) ? 1.0f : exp2f(rs.m_run - m_new);
+    rs.l_part *= alpha;
+    rs.m_run = m_new;
+    float ar[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ar[i] = __shfl(alpha, 4 * G + i, 64);
+#pragma unroll
+    for (int j = 0; j < DL; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rs.o[j][i] *= ar[i];
+  }
+  const float msafe = (rs.m_run == kNegInf) ? 0.0f : rs.m_run;
+  float pv[8], plo[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    pv[e] = __builtin_amdgcn_exp2f(x[e] - msafe);
+    rs.l_part += pv[e];
+  }
+  if constexpr (SC) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pv[e] *= (e < 4) ? vsA : vsB;  // l_part keeps the unscaled sum
+  }
+  const vec8 phi = TT::cvt8(pv);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) plo[e] = pv[e] - TT::back(phi[e]);
+  const vec8 plo8 = TT::cvt8(plo);
+#pragma unroll
+  for (int j = 0; j < DL; ++j) {
+    const vec8 vb = vop(j);
+    rs.o[j] = TT::mfma(phi, vb, rs.o[j]);
+    rs.o[j] = TT::mfma(plo8, vb, rs.o[j]);
+  }
+}
+
+// One 32-key step held in registers as loaded (value rows regrouped here).
+template <typename TT, int D, bool CAP, bool SC = false>
+__device__ __forceinline__ void compute_step(RowState<TT, D>& rs, const Step<D>& st, int t0,
+                                             int end, int G, float scale_log2, float scale,
+                                             float cap, float ksA = 1.f, float ksB = 1.f,
+                                             float vsA = 1.f, float vsB = 1.f) {
+  attend_step<TT, D, CAP, SC>(
+      rs, st.k, [&](int j) { return value_operand<TT, D>(st, j); }, t0, end, G, scale_log2,
+      scale, cap, ksA, ksB, vsA, vsB);
+}
+
+__device__ __forceinline__ WaveInfo make_wave(const AttnParams& p, int D, int b, int kh, int s0,
+                                              int pastb, int total) {
+  WaveInfo w;
+  w.kc = reinterpret_cast<const char*>(p.key_cache);
+  w.vc = reinterpret_cast<const char*>(p.value_cache);
+  w.kn = reinterpret_cast<const char*>(p.k_new);
+  w.vn = reinterpret_cast<const char*>(p.v_new);
+  w.b = b;
+  w.kh = kh;
+  w.s0 = s0;
+  w.pastb = pastb;
+  w.total = total;
+  w.cache_limit = (p.read_all_from_cache || p.new_rows_in_cache) ? total : pastb;
+  w.bs = p.block_size;
+  w.bs_shift = (p.block_size & (p.block_size - 1)) == 0 ? __builtin_ctz(p.block_size) : -1;
+  w.max_blocks = p.max_blocks;
+  w.num_tokens = p.num_tokens;
+  w.num_blocks = p.num_blocks;
+  w.rowb = (int64_t)p.kv_heads * D * 2;
+  w.first_bi = 0;
+  w.bt = p.block_table + (int64_t)b * p.max_blocks;
+  return w;
+}
+
+// Rows row0 .. row0+15 of kv-head kh: this lane's MFMA column is row r = row0 + c, i.e. query
+// token r / g and head kh*g + r % g.
+template <typename TT, int D>
+__device__ __forceinline__ void init_rows(RowState<TT, D>& rs, const AttnParams& p,
+                                          const WaveInfo& w, int row0, int R, int g, int c,
+                                          int G) {
+  using vec8 = typename TT::vec8;
+  const int r = row0 + c;
+  const bool rvalid = r < R;
+  const int qi = rvalid ? r / g : 0;
+  const int h = w.kh * g + (rvalid ? r % g : 0);
+  const int rpos = w.pastb + qi;
+  rs.vis_lo = p.window > 0 ? rpos - p.window + 1 : 0;
+  rs.vis_hi = rvalid ? (p.causal ? rpos + 1 : w.total) : -1;
+  const char* qrow = reinterpret_cast<const char*>(p.q) +
+                     (((int64_t)(w.s0 + qi) * p.num_heads + h) * D + 8 * G) * 2;
+#pragma unroll
+  for (int s = 0; s < D / 32; ++s) {
+    const u32x4 v = rvalid ? ld16(qrow + 64 * s) : u32x4{0, 0, 0, 0};
+    rs.qv[s] = __builtin_bit_cast(vec8, v);
+  }
+#pragma unroll
+  for (int j = 0; j < D / 16; ++j) rs.o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  rs.m_run = kNegInf;
+  rs.l_part = 0.0f;
+}
+
+// Epilogue: rows 4G+i of this lane's O registers.  final: normalise (with the sink) and write
+// the output row in T; otherwise write the fp32 partial (O, m, l) at part_index(row).
+template <typename TT, int D, typename PartIndex>
+__device__ __forceinline__ void store_rows(const RowState<TT, D>& rs, const AttnParams& p, int kh,
+                                           int s0, int row0, int R, int g, int c, int G,
+                                           float sink_c, bool final, PartIndex part_index) {
+  constexpr int DL = D / 16;
+  float l_row = rs.l_part + __shfl_xor(rs.l_part, 16, 64);
+  l_row += __shfl_xor(l_row, 32, 64);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int rr = row0 + 4 * G + i;
+    const float mi = __shfl(rs.m_run, 4 * G + i, 64);
+    const float li = __shfl(l_row, 4 * G + i, 64);
+    const float si = __shfl(sink_c, 4 * G + i, 64);  // sink logit of row rr (log2 units)
+    if (rr >= R) continue;
+    const int oqi = rr / g, oh = kh * g + rr % g;
+    const int64_t t = s0 + oqi;
+    if (final) {
+      const float f = finalize_factor(mi, li, si);
+      typename TT::raw vals[DL];
+#pragma unroll
+      for (int j = 0; j < DL; ++j) vals[j] = TT::from_f32(rs.o[j][i] * f);
+      typename TT::raw* dst =
+          reinterpret_cast<typename TT::raw*>(p.out) + (t * p.num_heads + oh) * D + DL * c;
+      if constexpr (DL == 8) {
+        u32x4 pk;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          pk[m] = (uint32_t)vals[2 * m] | ((uint32_t)vals[2 * m + 1] << 16);
+        *reinterpret_cast<u32x4*>(dst) = pk;
+      } else {
+#pragma unroll
+        for (int j = 0; j < DL; ++j) dst[j] = vals[j];
+      }
+    } else {
+      const int64_t pi = part_index(t, oh, rr - row0);
+      float* dst = p.part_o + pi * D + DL * c;
+#pragma unroll
+      for (int j = 0; j < DL; ++j) dst[j] = rs.o[j][i];
+      if (c == 0) {
+        p.part_ml[pi * 2 + 0] = mi;
+        p.part_ml[pi * 2 + 1] = li;
+      }
+    }
+  }
+}
+
+}  // namespace
+}  // namespace pa

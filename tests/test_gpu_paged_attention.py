@@ -250,6 +250,46 @@ def test_split_k_chunks(chunk, kind):
     assert err <= 2e-3, err
 
 
+# LDS-shared prefill kernel through the kernel-level entries: ragged multi-token queries (one
+# sequence empty), split-K chunks, page sizes that do or do not hold whole 16-key tiles, new
+# rows read from the pages or from the caller's rows, windows and softcap
+@pytest.mark.parametrize("chunk", [0, 32, 96, 512])
+@pytest.mark.parametrize("new_rows_in_cache", [False, True])
+@pytest.mark.parametrize("bs,d,dtype,window,softcap", [
+    (16, 128, BF16, -1, 0.0), (8, 128, F16, -1, 0.0), (32, 64, BF16, 100, 0.0),
+    (16, 64, F16, -1, 20.0)], ids=["bs16_d128", "bs8_d128", "bs32_d64_window", "d64_softcap"])
+def test_prefill_kernel_level(chunk, new_rows_in_cache, bs, d, dtype, window, softcap):
+    import torch
+    import onnxruntime_ep_mlx_amd as ep
+    from pa_cases import to_torch, from_torch
+    rng = np.random.default_rng(20 + bs + d)
+    B, H, KV = 4, 14, 2
+    new_lens = [37, 0, 70, 5]
+    past = rng.integers(0, 600, size=B)
+    mb = int((past.max() + max(new_lens) + bs - 1) // bs)
+    case = make_case(H, KV, d, B * mb, bs, B, dtype=dtype, seed=20 + bs + d, new_lens=new_lens,
+                     past=past, max_blocks=mb, std=1.0, window=window, softcap=softcap)
+    ref, ref_t, _, _ = orc.paged_attention_op(case)
+    t = {n: to_torch(case[n], dtype) for n in ("query", "key", "value", "key_cache",
+                                               "value_cache")}
+    I = {n: torch.from_numpy(case[n]).cuda() for n in ("cum", "past", "block_table")}
+    ep.reshape_and_cache(t["key"], t["value"], t["key_cache"], t["value_cache"], I["cum"],
+                         I["past"], I["block_table"])
+    outs = {}
+    for kind in (2, 4):
+        outs[kind] = ep.attention(t["query"], t["key"], t["value"], t["key_cache"],
+                                  t["value_cache"], I["cum"], I["past"], I["block_table"],
+                                  num_heads=H, max_query_len=max(new_lens), kind=kind,
+                                  chunk=chunk, local_window_size=window, softcap=softcap,
+                                  new_rows_in_cache=new_rows_in_cache)
+    torch.cuda.synchronize()
+    for kind, out in outs.items():
+        got = orc.decode(from_torch(out, dtype), dtype)
+        err = orc.rel_l2(got, orc.decode(ref_t, dtype))
+        assert err <= 2e-3, (kind, err)
+        assert orc.rel_l2(got.astype(np.float64), ref) <= 4e-3, kind
+
+
 # balanced decode kernel through the kernel-level entries: segments that split sequences,
 # sequences of one step, the separate partial merge, and both sources of the new rows
 @pytest.mark.parametrize("new_rows_in_cache", [False, True])
