@@ -145,16 +145,6 @@ __device__ __forceinline__ void load_edge(const WaveInfo& w, int c, int G, int t
 
 // ----------------------------------------------------------------------------- shared driver
 
-// Zero this lane's value rows of a step that lie at or past `total` (rows re-read past the
-// sequence end take no part even if their bytes are not finite).
-template <int D>
-__device__ __forceinline__ void clear_tail_rows(Step<D>& st, int t0, int total, int G) {
-  if (t0 + 32 <= total) return;
-#pragma unroll
-  for (int e = 0; e < 8; ++e)
-    if (t0 + 16 * (e >> 2) + 4 * G + (e & 3) >= total) st.v[e] = VRow<D>{};
-}
-
 // Walk keys [t_begin, t_last) for one (sequence, kv-head) with NG 16-row groups `rs`; t_begin
 // is a multiple of 32.  Every loaded step serves all NG groups (NG x fewer key/value reads per
 // query row).  Steps entirely inside cached pages go through the pipelined fast loop in

@@ -244,17 +244,12 @@ prefill_kernel(const AttnParams p) {
 #pragma unroll
       for (int j = 0; j < DL; ++j) vop[j] = lds[k & 1][2 * KS + j][lane];
       auto vb = [&](int n) { return __builtin_bit_cast(vec8, vop[n]); };
-      if (t0 >= all_lo && t0 + 32 <= all_hi) {
-#pragma unroll
-        for (int j = 0; j < NG; ++j)
-          attend_step<TT, D, CAP, false, false>(rs[j], kop, vb, t0, end, G, p.scale_log2,
-                                                p.scale, p.softcap, 1.f, 1.f, 1.f, 1.f);
-      } else {
-#pragma unroll
-        for (int j = 0; j < NG; ++j)
-          attend_step<TT, D, CAP, false, true>(rs[j], kop, vb, t0, end, G, p.scale_log2,
-                                               p.scale, p.softcap, 1.f, 1.f, 1.f, 1.f);
-      }
+      if (t0 >= all_lo && t0 + 32 <= all_hi)
+        attend_groups<TT, D, CAP, false, NG>(rs, kop, vb, t0, end, G, p.scale_log2, p.scale,
+                                             p.softcap);
+      else
+        attend_groups<TT, D, CAP, true, NG>(rs, kop, vb, t0, end, G, p.scale_log2, p.scale,
+                                            p.softcap);
     }
     if (k + 1 < nsteps) store_quarter<D>(lds[(k + 1) & 1], q, wave, t0 + 32, total, lane, G);
     if (k + 2 < nsteps) load_quarter<D>(w, pw, rg, wave, t0 + 64, lane, q);

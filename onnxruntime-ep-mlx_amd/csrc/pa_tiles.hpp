@@ -99,6 +99,16 @@ __device__ __forceinline__ typename TT::vec8 value_operand(const Step<D>& st, in
   return __builtin_bit_cast(typename TT::vec8, w);
 }
 
+// Zero this lane's value rows of a step that lie at or past `total` (rows re-read past the
+// sequence end take no part even if their bytes are not finite).
+template <int D>
+__device__ __forceinline__ void clear_tail_rows(Step<D>& st, int t0, int total, int G) {
+  if (t0 + 32 <= total) return;
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (t0 + 16 * (e >> 2) + 4 * G + (e & 3) >= total) st.v[e] = VRow<D>{};
+}
+
 // Row state of one 16-row group.
 template <typename TT, int D>
 struct RowState {
@@ -120,16 +130,19 @@ struct RowState {
 // group (rows past the end of the sequence have zero queries and are never stored), so the
 // per-score position tests are skipped.
 //
-// Probabilities use the hardware base-2 exponential (v_exp_f32) without the denormal-range
-// rescaling of exp2f: arguments are <= 8 (lazy max) and a probability below 2^-126 of the row
-// maximum adds nothing to an fp32 sum that holds the maximum's own 1.
-template <typename TT, int D, bool CAP, bool SC, bool MASK = true, typename ValueOp>
-__device__ __forceinline__ void attend_step(RowState<TT, D>& rs, const u32x4 (&k)[2][D / 32],
-                                            ValueOp vop, int t0, int end, int G,
-                                            float scale_log2, float scale, float cap, float ksA,
-                                            float ksB, float vsA, float vsB) {
+// The step is split into three pieces -- scores, the (rare) lazy rescale, probabilities and
+// the PV product -- so that attend_groups can run the middle piece once for several row
+// groups and leave the exponentials of one group and the PV MFMAs of another in one basic
+// block for the scheduler to interleave.
+
+// Scores of the step in log2 units (masked to -inf where not visible); returns this lane's max.
+template <typename TT, int D, bool CAP, bool SC, bool MASK>
+__device__ __forceinline__ float step_scores(const RowState<TT, D>& rs,
+                                             const u32x4 (&k)[2][D / 32], int t0, int end, int G,
+                                             float scale_log2, float scale, float cap, float ksA,
+                                             float ksB, float (&x)[8]) {
   using vec8 = typename TT::vec8;
-  constexpr int KS = D / 32, DL = D / 16;
+  constexpr int KS = D / 32;
   f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
@@ -140,7 +153,6 @@ __device__ __forceinline__ void attend_step(RowState<TT, D>& rs, const u32x4 (&k
     sa *= ksA;
     sb *= ksB;
   }
-  float x[8];
   float lmax = kNegInf;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -160,21 +172,42 @@ __device__ __forceinline__ void attend_step(RowState<TT, D>& rs, const u32x4 (&k
     }
     lmax = fmaxf(lmax, x[e]);
   }
-  if (__any(lmax > rs.m_run + 8.0f)) {
-    float rmax = fmaxf(lmax, __shfl_xor(lmax, 16, 64));
-    rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
-    const float m_new = fmaxf(rs.m_run, rmax);
-    const float alpha = (m_new == kNegInf) ? 1.0f : exp2f(rs.m_run - m_new);
-    rs.l_part *= alpha;
-    rs.m_run = m_new;
-    float ar[4];
+  return lmax;
+}
+
+// Lazy rescale: the running max only moves when a score exceeds it by more than 2^8.
+template <typename TT, int D>
+__device__ __forceinline__ bool needs_rescale(const RowState<TT, D>& rs, float lmax) {
+  return lmax > rs.m_run + 8.0f;
+}
+
+template <typename TT, int D>
+__device__ __forceinline__ void rescale_rows(RowState<TT, D>& rs, float lmax, int G) {
+  constexpr int DL = D / 16;
+  float rmax = fmaxf(lmax, __shfl_xor(lmax, 16, 64));
+  rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+  const float m_new = fmaxf(rs.m_run, rmax);
+  const float alpha = (m_new == kNegInf) ? 1.0f : exp2f(rs.m_run - m_new);
+  rs.l_part *= alpha;
+  rs.m_run = m_new;
+  float ar[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ar[i] = __shfl(alpha, 4 * G + i, 64);
+  for (int i = 0; i < 4; ++i) ar[i] = __shfl(alpha, 4 * G + i, 64);
 #pragma unroll
-    for (int j = 0; j < DL; ++j)
+  for (int j = 0; j < DL; ++j)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) rs.o[j][i] *= ar[i];
-  }
+    for (int i = 0; i < 4; ++i) rs.o[j][i] *= ar[i];
+}
+
+// Probabilities of the step as the PV A operand, split into hi + lo 16-bit parts.
+//
+// They use the hardware base-2 exponential (v_exp_f32) without the denormal-range rescaling of
+// exp2f: arguments are <= 8 (lazy max) and a probability below 2^-126 of the row maximum adds
+// nothing to an fp32 sum that holds the maximum's own 1.
+template <typename TT, int D, bool SC>
+__device__ __forceinline__ void step_probs(RowState<TT, D>& rs, const float (&x)[8], float vsA,
+                                           float vsB, typename TT::vec8& phi,
+                                           typename TT::vec8& plo8) {
   const float msafe = (rs.m_run == kNegInf) ? 0.0f : rs.m_run;
   float pv[8], plo[8];
 #pragma unroll
@@ -186,15 +219,66 @@ __device__ __forceinline__ void attend_step(RowState<TT, D>& rs, const u32x4 (&k
 #pragma unroll
     for (int e = 0; e < 8; ++e) pv[e] *= (e < 4) ? vsA : vsB;  // l_part keeps the unscaled sum
   }
-  const vec8 phi = TT::cvt8(pv);
+  phi = TT::cvt8(pv);
 #pragma unroll
   for (int e = 0; e < 8; ++e) plo[e] = pv[e] - TT::back(phi[e]);
-  const vec8 plo8 = TT::cvt8(plo);
+  plo8 = TT::cvt8(plo);
+}
+
+template <typename TT, int D, bool CAP, bool SC, bool MASK = true, typename ValueOp>
+__device__ __forceinline__ void attend_step(RowState<TT, D>& rs, const u32x4 (&k)[2][D / 32],
+                                            ValueOp vop, int t0, int end, int G,
+                                            float scale_log2, float scale, float cap, float ksA,
+                                            float ksB, float vsA, float vsB) {
+  using vec8 = typename TT::vec8;
+  constexpr int DL = D / 16;
+  float x[8];
+  const float lmax = step_scores<TT, D, CAP, SC, MASK>(rs, k, t0, end, G, scale_log2, scale, cap,
+                                                       ksA, ksB, x);
+  if (__any(needs_rescale(rs, lmax))) rescale_rows(rs, lmax, G);
+  vec8 phi, plo8;
+  step_probs<TT, D, SC>(rs, x, vsA, vsB, phi, plo8);
 #pragma unroll
   for (int j = 0; j < DL; ++j) {
     const vec8 vb = vop(j);
     rs.o[j] = TT::mfma(phi, vb, rs.o[j]);
     rs.o[j] = TT::mfma(plo8, vb, rs.o[j]);
+  }
+}
+
+// NG row groups against the same step: all scores first, one branch for the rare rescale, then
+// every group's probabilities and PV MFMAs in one block, each value operand built once.
+template <typename TT, int D, bool CAP, bool MASK, int NG, typename ValueOp>
+__device__ __forceinline__ void attend_groups(RowState<TT, D> (&rs)[NG],
+                                              const u32x4 (&k)[2][D / 32], ValueOp vop, int t0,
+                                              int end, int G, float scale_log2, float scale,
+                                              float cap) {
+  using vec8 = typename TT::vec8;
+  constexpr int DL = D / 16;
+  float x[NG][8], lmax[NG];
+  bool any = false;
+#pragma unroll
+  for (int j = 0; j < NG; ++j) {
+    lmax[j] = step_scores<TT, D, CAP, false, MASK>(rs[j], k, t0, end, G, scale_log2, scale, cap,
+                                                   1.f, 1.f, x[j]);
+    any = any || needs_rescale(rs[j], lmax[j]);
+  }
+  if (__any(any)) {
+#pragma unroll
+    for (int j = 0; j < NG; ++j)
+      if (__any(needs_rescale(rs[j], lmax[j]))) rescale_rows(rs[j], lmax[j], G);
+  }
+  vec8 phi[NG], plo[NG];
+#pragma unroll
+  for (int j = 0; j < NG; ++j) step_probs<TT, D, false>(rs[j], x[j], 1.f, 1.f, phi[j], plo[j]);
+#pragma unroll
+  for (int n = 0; n < DL; ++n) {
+    const vec8 vb = vop(n);
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+      rs[j].o[n] = TT::mfma(phi[j], vb, rs[j].o[n]);
+      rs[j].o[n] = TT::mfma(plo[j], vb, rs[j].o[n]);
+    }
   }
 }
 
