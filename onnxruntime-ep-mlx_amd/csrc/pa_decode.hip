@@ -61,25 +61,19 @@ struct Step8 {
   float sc;  // lane l: scale of (l & 2 ? value : key) page of tile (l & 1)
 };
 
-// Four e4m3 codes -> four bf16 (exact: every e4m3 value is a bf16 value) as two packed words:
-// v_cvt_f32_fp8 per byte (gfx950 decodes OCP e4m3 exactly, all 256 codes checked), then the
-// high halves packed with v_perm.  The two-element v_cvt_pk_f32_fp8 form is avoided: this
-// compiler folds its second result into the first when the results are repacked.
-// For fp16 activations the same values are packed as fp16 (also exact: |x| <= 448, and the
-// e4m3 subnormals are fp16 normals), so the MFMA operands match the query's type.
+// Four e4m3 codes -> four bf16 (exact: every e4m3 value is a bf16 value) as two packed words,
+// one gfx950 v_cvt_scalef32_pk_bf16_fp8 per code pair (scale 1.0: no scaling; all 65536 code
+// pairs in both word positions checked on the device against an exact decode, NaN codes stay
+// NaN).  For fp16 activations the same values are packed as fp16 (also exact: |x| <= 448, and
+// the e4m3 subnormals are fp16 normals), so the MFMA operands match the query's type.
 template <typename TT>
 __device__ __forceinline__ u32x2 e4m3x4_widen(uint32_t w) {
-  const float fa = __builtin_amdgcn_cvt_f32_fp8((int)w, 0);
-  const float fb = __builtin_amdgcn_cvt_f32_fp8((int)w, 1);
-  const float fc = __builtin_amdgcn_cvt_f32_fp8((int)w, 2);
-  const float fd = __builtin_amdgcn_cvt_f32_fp8((int)w, 3);
   if constexpr (TT::code == PA_DTYPE_FLOAT16) {
-    return u32x2{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(fa, fb)),
-                 __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(fc, fd))};
+    return u32x2{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false)),
+                 __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true))};
   } else {
-    const uint32_t a = __builtin_bit_cast(uint32_t, fa), b = __builtin_bit_cast(uint32_t, fb);
-    const uint32_t c = __builtin_bit_cast(uint32_t, fc), d = __builtin_bit_cast(uint32_t, fd);
-    return u32x2{__builtin_amdgcn_perm(b, a, 0x07060302u), __builtin_amdgcn_perm(d, c, 0x07060302u)};
+    return u32x2{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false)),
+                 __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true))};
   }
 }
 
