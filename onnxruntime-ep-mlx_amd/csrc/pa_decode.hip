@@ -508,14 +508,14 @@ __device__ __forceinline__ void load_step8(const AttnParams& p, const StepAt& s,
     const char* kb = kc + row0 * rowb + hoff;
     const char* vb = vc + row0 * rowb + hoff;
 #pragma unroll
-    for (int h = 0; h < D / 64; ++h) st.k[tile][h] = ld16(kb + c * rowb + 16 * G + 64 * h);
+    for (int h = 0; h < D / 64; ++h) st.k[tile][h] = ld16s(kb + c * rowb + 16 * G + 64 * h);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const char* vr = vb + (4 * G + e) * rowb + (D / 16) * c;
       if constexpr (D == 128)
-        st.v[4 * tile + e].w = *reinterpret_cast<const u32x2*>(vr);
+        st.v[4 * tile + e].w = ld8s(vr);
       else
-        st.v[4 * tile + e].w = *reinterpret_cast<const uint32_t*>(vr);
+        st.v[4 * tile + e].w = ld4s(vr);
     }
   }
   const float* sp = (lane & 2) ? p.v_scale : p.k_scale;
@@ -548,11 +548,11 @@ __device__ __forceinline__ void load_stream_step(const AttnParams& p, const Step
       const int tp = s.t + 16 * tile;
       const char* kr = kc + (uint64_t)(r0 + min(tp + c, last)) * rs;
 #pragma unroll
-      for (int q = 0; q < D / 32; ++q) st.k[tile][q] = ld16(kr + 16 * G + 64 * q);
+      for (int q = 0; q < D / 32; ++q) st.k[tile][q] = ld16s(kr + 16 * G + 64 * q);
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         st.v[4 * tile + e] =
-            ld_vrow<D>(vc + (uint64_t)(r0 + min(tp + 4 * G + e, last)) * rs + DL * 2 * c);
+            ld_vrow_s<D>(vc + (uint64_t)(r0 + min(tp + 4 * G + e, last)) * rs + DL * 2 * c);
     }
   } else if (bs_shift >= 4 && min(s.t + 31, last) < s.cache_limit) {
     // Every row in the pages and each 16-key tile inside one page: scalar page base (page id
@@ -565,10 +565,10 @@ __device__ __forceinline__ void load_stream_step(const AttnParams& p, const Step
       const char* kb = kc + (uint64_t)((blk << bs_shift) + (tp & (p.block_size - 1))) * rowb + hoff;
       const char* vb = vc + (uint64_t)((blk << bs_shift) + (tp & (p.block_size - 1))) * rowb + hoff;
 #pragma unroll
-      for (int q = 0; q < D / 32; ++q) st.k[tile][q] = ld16(kb + c * rowb + 16 * G + 64 * q);
+      for (int q = 0; q < D / 32; ++q) st.k[tile][q] = ld16s(kb + c * rowb + 16 * G + 64 * q);
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        st.v[4 * tile + e] = ld_vrow<D>(vb + (4 * G + e) * rowb + DL * 2 * c);
+        st.v[4 * tile + e] = ld_vrow_s<D>(vb + (4 * G + e) * rowb + DL * 2 * c);
     }
   } else {
 #pragma unroll
@@ -576,12 +576,12 @@ __device__ __forceinline__ void load_stream_step(const AttnParams& p, const Step
       const int tp = s.t + 16 * tile;
       const char* kr = stream_row(p, s, btl, min(tp + c, last), kc, kn, rowb, hoff, bs_shift);
 #pragma unroll
-      for (int q = 0; q < D / 32; ++q) st.k[tile][q] = ld16(kr + 16 * G + 64 * q);
+      for (int q = 0; q < D / 32; ++q) st.k[tile][q] = ld16s(kr + 16 * G + 64 * q);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const char* vr =
             stream_row(p, s, btl, min(tp + 4 * G + e, last), vc, vn, rowb, hoff, bs_shift);
-        st.v[4 * tile + e] = ld_vrow<D>(vr + DL * 2 * c);
+        st.v[4 * tile + e] = ld_vrow_s<D>(vr + DL * 2 * c);
       }
     }
   }
