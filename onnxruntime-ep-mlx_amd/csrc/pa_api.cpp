@@ -156,7 +156,7 @@ int device_cus() {
 }
 
 Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype act, int kind,
-               int chunk, bool linear = false) {
+               int chunk, bool linear = false, int linear_cap = 0) {
   Plan pl{};
   // The LATENT layout (values = leading dims of the key rows) runs on the VALU kernel.
   if (c->value_cache == nullptr || (a->v_head_size > 0 && a->v_head_size != c->head_dim))
@@ -164,10 +164,14 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
   const int g = a->num_heads / c->kv_heads;
   const int mq = b->max_query_len > 0 ? b->max_query_len : std::max(b->num_tokens, 1);
   const bool mfma = pa::decode_mfma_supported(c->head_dim, act, c->dtype);
-  // The balanced (streaming) decode addresses rows with 32-bit row indices and shifts.
+  // The balanced (streaming) decode addresses rows with 32-bit row indices and shifts, and
+  // numbers the 32-key steps of the whole batch with 32-bit indices: every sequence is clamped
+  // to the cache capacity on the device, so batch * (capacity / 32 + 1) bounds the step count.
+  const int64_t cap = linear_cap > 0 ? linear_cap : (int64_t)b->max_blocks * c->block_size;
   const bool bal_ok = (int64_t)g * mq <= 16 &&
                       pa::balanced_supported(c->head_dim, act, c->dtype, c->block_size) &&
-                      (int64_t)c->num_blocks * c->block_size <= (int64_t)UINT32_MAX;
+                      (int64_t)c->num_blocks * c->block_size <= (int64_t)UINT32_MAX &&
+                      (int64_t)std::max(b->batch, 0) * (cap / 32 + 2) < (int64_t)INT32_MAX;
   if (kind == 0 && linear) kind = bal_ok ? 1 : 3;  // contiguous caches: streaming or VALU kernel
   if (kind == 0) {
     if (bal_ok || (mfma && (int64_t)g * mq <= 16))
@@ -285,7 +289,7 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
     return fail(PA_ERR_UNSUPPORTED, "prefill MFMA kernel does not cover this dtype/head_dim");
   if (!(a->softcap >= 0.0f) || !std::isfinite(a->softcap))
     return fail(PA_ERR_INVALID_ARGUMENT, "softcap must be finite and non-negative");
-  Plan pl = make_plan(c, b, a, act, kind, chunk, opts.linear_cap > 0);
+  Plan pl = make_plan(c, b, a, act, kind, chunk, opts.linear_cap > 0, opts.linear_cap);
   if (opts.linear_cap > 0 && !(pl.balanced || pl.kind == 3))
     return fail(PA_ERR_UNSUPPORTED, "contiguous caches run on the decode or VALU kernels only");
   size_t need = workspace_for(c, b, a, pl);

@@ -284,9 +284,14 @@ __device__ __forceinline__ SeqSteps seq_steps(const AttnParams& p, int b) {
   const bool live = b < p.batch;
   q.s0 = live ? min(max(c0, 0), p.num_tokens) : 0;
   const int s1 = live ? min(max(c1, q.s0), p.num_tokens) : 0;
-  q.nq = s1 - q.s0;
+  // Keys are clamped to the cache capacity (metadata the host checked never reaches it), which
+  // bounds the batch's step count for the 32-bit step indices of the streaming kernel.
+  const int cap = p.linear_cap > 0 ? p.linear_cap
+                                   : (int)min((int64_t)p.max_blocks * p.block_size,
+                                              (int64_t)(INT32_MAX / 2));
+  q.nq = min(s1 - q.s0, cap);
   const bool any = q.nq > 0;
-  q.pastb = any ? max(pb, 0) : 0;
+  q.pastb = any ? min(max(pb, 0), cap - q.nq) : 0;
   q.total = any ? q.pastb + q.nq : 0;
   q.first = (any && p.window > 0) ? (max(0, q.pastb - p.window + 1) / 32) * 32 : 0;
   q.n = any ? (q.total - q.first + 31) / 32 : 0;
@@ -380,246 +385,296 @@ __device__ __forceinline__ void merge_pieces(const AttnParams& p, int b, int kh,
   }
 }
 
-__device__ __forceinline__ int64_t readlane64(int64_t v, int l) {
-  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, l);
-  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)v >> 32), l);
-  return (int64_t)(((uint64_t)hi << 32) | lo);
-}
-
 // Up to 64 consecutive sequences, lane l describing sequence base + l.
 struct SeqWin {
   int base;
   SeqSteps q;
-  int64_t P;  // first flattened step of this lane's sequence
+  int P;  // first flattened step of this lane's sequence
 };
 
-// Wave-uniform position in the flattened step list.
+// Wave-uniform position in the flattened step list.  The sequence fields a cursor needs on every
+// step are read from the window lanes only when it enters a sequence, and the key position t
+// advances by 32 per step, so moving to the next step costs a few scalar instructions.  Step
+// indices are 32-bit: sequences are clamped to the cache capacity (seq_steps) and the host
+// bounds batch * (capacity / 32 + 1) below 2^31.
 struct Cursor {
-  int64_t f;     // flattened step
-  int bl;        // window lane of the sequence holding step f
-  int64_t pend;  // one past that sequence's last step
-  int64_t u;     // sub-segment holding step f
-  int64_t ub;    // one past that sub-segment's last step
+  int f;      // flattened step
+  int pend;   // one past the last step of the sequence holding step f
+  int u;      // sub-segment holding step f
+  int ub;     // one past that sub-segment's last step
+  int bl;     // window lane of the sequence
+  int t;      // first key position of step f
+  int kh;     // kv-head of sub-segment u
+  int total;  // keys of the sequence
+  int lim;    // keys below lim are read from the pages
 };
 
-__device__ __forceinline__ Cursor cursor_at(const SeqWin& sw, int64_t f, int64_t L) {
+__device__ __forceinline__ int sub_segment_kh(int u, int u0, int x, int kv_heads) {
+  const int kh = x + (u - u0);  // mix <= kv_heads
+  return kh >= kv_heads ? kh - kv_heads : kh;
+}
+
+__device__ __forceinline__ int lane_of(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+
+__device__ __forceinline__ void cursor_seq(Cursor& c, const SeqWin& sw, const AttnParams& p) {
+  const int pend_l = sw.P + sw.q.n;
+  const uint64_t m = __ballot(sw.q.n > 0 && pend_l > c.f);
+  c.bl = m ? __builtin_ctzll(m) : 63;
+  c.pend = lane_of(pend_l, c.bl);
+  c.total = lane_of(sw.q.total, c.bl);
+  c.lim = (p.read_all_from_cache || p.new_rows_in_cache) ? c.total : lane_of(sw.q.pastb, c.bl);
+  c.t = lane_of(sw.q.first, c.bl) + 32 * (c.f - lane_of(sw.P, c.bl));
+}
+
+__device__ __forceinline__ Cursor cursor_at(const SeqWin& sw, const AttnParams& p, int f, int L,
+                                            int x, int u0) {
   Cursor c;
   c.f = f;
-  const int64_t pend_l = sw.P + sw.q.n;
-  const uint64_t m = __ballot(sw.q.n > 0 && pend_l > f);
-  c.bl = m ? __builtin_ctzll(m) : 63;
-  c.pend = readlane64(pend_l, c.bl);
   c.u = f / L;
   c.ub = (c.u + 1) * L;
+  c.kh = sub_segment_kh(c.u, u0, x, p.kv_heads);
+  cursor_seq(c, sw, p);
   return c;
 }
 
-// Next step, or stay on the last one (hi - 1): look-ahead cursors re-read it.
-__device__ __forceinline__ void cursor_next(Cursor& c, const SeqWin& sw, int64_t hi, int64_t L) {
-  if (c.f + 1 >= hi) return;
+// Next step, or stay on the last one (hi - 1): look-ahead cursors re-read it.  Returns true
+// when the sequence or the kv-head changed.
+__device__ __forceinline__ bool cursor_next(Cursor& c, const SeqWin& sw, const AttnParams& p,
+                                            int hi, int L, int x, int u0) {
+  if (c.f + 1 >= hi) return false;
   ++c.f;
+  c.t += 32;
+  bool changed = false;
   if (c.f >= c.pend) {
-    const int64_t pend_l = sw.P + sw.q.n;
-    const uint64_t m = __ballot(sw.q.n > 0 && pend_l > c.f);
-    c.bl = m ? __builtin_ctzll(m) : 63;
-    c.pend = readlane64(pend_l, c.bl);
+    cursor_seq(c, sw, p);
+    changed = true;
   }
   if (c.f >= c.ub) {
     ++c.u;
     c.ub += L;
+    c.kh = sub_segment_kh(c.u, u0, x, p.kv_heads);
+    changed = true;
   }
-}
-
-// Everything one step needs, read from the window lanes (wave-uniform).
-struct StepAt {
-  int b, kh, t, s0, nq, pastb, total, cache_limit;
-  int64_t P;
-  int n;
-};
-
-__device__ __forceinline__ StepAt step_at(const Cursor& c, const SeqWin& sw, const AttnParams& p,
-                                          int x, int64_t u0) {
-  StepAt s;
-  s.b = sw.base + c.bl;
-  s.P = readlane64(sw.P, c.bl);
-  s.n = __builtin_amdgcn_readlane(sw.q.n, c.bl);
-  s.t = __builtin_amdgcn_readlane(sw.q.first, c.bl) + 32 * (int)(c.f - s.P);
-  s.s0 = __builtin_amdgcn_readlane(sw.q.s0, c.bl);
-  s.nq = __builtin_amdgcn_readlane(sw.q.nq, c.bl);
-  s.pastb = __builtin_amdgcn_readlane(sw.q.pastb, c.bl);
-  s.total = __builtin_amdgcn_readlane(sw.q.total, c.bl);
-  s.cache_limit = (p.read_all_from_cache || p.new_rows_in_cache) ? s.total : s.pastb;
-  const int kh = x + (int)(c.u - u0);  // mix <= kv_heads
-  s.kh = kh >= p.kv_heads ? kh - p.kv_heads : kh;
-  return s;
+  return changed;
 }
 
 // Block-table entries of a step: lane l holds the entry of key t + (l & 31) (index clamped into
 // the table row; entries past the sequence are never used for addressing).
-__device__ __forceinline__ int load_step_blocks(const AttnParams& p, const StepAt& s, int lane,
-                                                int bs_shift) {
+__device__ __forceinline__ int load_step_blocks(const AttnParams& p, const SeqWin& sw,
+                                                const Cursor& c, int lane, int bs_shift) {
   // Contiguous caches have no block table: the load still happens (same count on every path)
   // and its value is unused.
   if (p.linear_cap > 0) return p.cum[0];
-  const int bi = min((s.t + (lane & 31)) >> bs_shift, p.max_blocks - 1);
-  return p.block_table[(int64_t)s.b * p.max_blocks + bi];
+  const int bi = min((c.t + (lane & 31)) >> bs_shift, p.max_blocks - 1);
+  return p.block_table[(int64_t)(sw.base + c.bl) * p.max_blocks + bi];
 }
 
 // Address of key/value row `pos` (t <= pos < total) of a step, branch-free: a cache page when
-// pos < cache_limit (page id from lane pos - t of `btl`, clamped into the pool), else the new
-// row of the packed batch.
-__device__ __forceinline__ const char* stream_row(const AttnParams& p, const StepAt& s, int btl,
-                                                  int pos, const char* cache, const char* fresh,
-                                                  uint32_t rowb, uint32_t hoff, int bs_shift) {
-  const int blk = min(max(__shfl(btl, pos - s.t, 64), 0), (int)min(p.num_blocks - 1,
+// pos < lim (page id from lane pos - t of `btl`, clamped into the pool), else the new row of the
+// packed batch (token s0 + pos - pastb).
+__device__ __forceinline__ const char* stream_row(const AttnParams& p, const Cursor& c, int btl,
+                                                  int pos, int s0, int pastb, const char* cache,
+                                                  const char* fresh, uint32_t rowb, uint32_t hoff,
+                                                  int bs_shift) {
+  const int blk = min(max(__shfl(btl, pos - c.t, 64), 0), (int)min(p.num_blocks - 1,
                                                                       (int64_t)INT32_MAX));
   const uint32_t crow = ((uint32_t)blk << bs_shift) + (uint32_t)(pos & (p.block_size - 1));
-  const uint32_t tok = (uint32_t)min(max(s.s0 + (pos - s.pastb), 0), p.num_tokens - 1);
-  const bool in_cache = pos < s.cache_limit;
+  const uint32_t tok = (uint32_t)min(max(s0 + (pos - pastb), 0), p.num_tokens - 1);
+  const bool in_cache = pos < c.lim;
   const char* base = in_cache ? cache : fresh;
   const uint64_t row = in_cache ? crow : tok;
   return base + row * rowb + hoff;
 }
 
-// All loads of one step: K and V rows of both 16-key tiles and the query rows of the step's
-// (sequence, kv-head).  Straight-line code, so every iteration issues the same loads and the
-// compiler's vmcnt waits only drain the step about to be computed.  Rows past the sequence end
-// re-read the last row.
+// Page rows through buffer loads: one scalar descriptor per 16-row tile (base address in
+// SGPRs) and offsets fixed per lane, so addressing a step costs scalar instructions only.
+// Streaming (nt) loads, like ld16s.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const char* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, -1, 0x00020000);
+}
+__device__ __forceinline__ u32x4 bld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 2));
+}
+__device__ __forceinline__ u32x2 bld8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 2));
+}
+__device__ __forceinline__ uint32_t bld4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 2);
+}
+
+// Page id of tile `tile` of a step (lane 16 * tile of `btl`), clamped into the pool, and the
+// byte offset of the tile's first row from the pool base.
+__device__ __forceinline__ uint64_t tile_row_bytes(const AttnParams& p, const Cursor& c, int btl,
+                                                   int tile, int bs_shift, uint32_t rowb,
+                                                   int64_t& blk) {
+  blk = min(max((int64_t)__builtin_amdgcn_readlane(btl, 16 * tile), (int64_t)0),
+            (int64_t)p.num_blocks - 1);
+  const uint64_t row0 =
+      (uint64_t)((blk << bs_shift) + ((c.t + 16 * tile) & (p.block_size - 1)));
+  return row0 * rowb;
+}
+
 template <typename TT, int D, bool F8>
 using RingStep = typename std::conditional<F8, Step8<D>, Step<D>>::type;
+
+// Per-lane constants of the streaming loads.
+struct LaneOffs {
+  uint32_t koff, voff;  // key / value offsets of this lane inside a 16-row tile (bytes)
+  uint32_t rowb;        // bytes per cache row
+};
+
+// Per-lane pointers of the query row and sink logit the data cursor's (sequence, kv-head)
+// needs; recomputed only when that cursor changes sequence or kv-head.  MFMA column c is row
+// r = c (rows past R repeat the last one; their scores never reach an output).  Query k-step q
+// covers dims 32q + 8G .. (bf16 pages) or 64(q/2) + 16G + 8(q%2) .. (fp8 pages, matching the
+// key chunks); the lane part of that offset is folded in here, the q part is a constant.
+struct QueryPtrs {
+  const char* q;
+  const char* sink;
+};
+template <int D, bool F8>
+__device__ __forceinline__ QueryPtrs query_ptrs(const AttnParams& p, const SeqWin& sw,
+                                                const Cursor& c, int g, int lane) {
+  const int cl = lane & 15, G = lane >> 4;
+  const int s0 = lane_of(sw.q.s0, c.bl), nq = lane_of(sw.q.nq, c.bl);
+  const int r = min(cl, g * nq - 1);
+  const int rq = r / g, rh = r - rq * g;
+  QueryPtrs o;
+  o.q = reinterpret_cast<const char*>(p.q) +
+        ((int64_t)(s0 + rq) * p.num_heads + c.kh * g + rh) * D * 2 + (F8 ? 32 : 16) * G;
+  // Sink logit input of that row's head (a harmless read of the query when there is none).
+  o.sink = p.head_sink ? reinterpret_cast<const char*>(p.head_sink) + (c.kh * g + rh) * 2
+                       : reinterpret_cast<const char*>(p.q);
+  return o;
+}
 
 // fp8 pages (every row in the pages, block size a multiple of 16): per tile D/64 16-byte key
 // chunks (dims 64h + 16G ..) and four D/16-byte value rows per lane, plus the page scales.
 template <int D>
-__device__ __forceinline__ void load_step8(const AttnParams& p, const StepAt& s, int btl, int lane,
-                                           int bs_shift, Step8<D>& st) {
-  const int c = lane & 15, G = lane >> 4;
-  const uint32_t rowb = (uint32_t)p.kv_heads * D;
-  const uint32_t hoff = (uint32_t)s.kh * D;
+__device__ __forceinline__ void load_step8(const AttnParams& p, const Cursor& c, int btl, int lane,
+                                           int bs_shift, const LaneOffs& lo, Step8<D>& st) {
+  const uint32_t hoff = (uint32_t)c.kh * D;
   const char* kc = reinterpret_cast<const char*>(p.key_cache);
   const char* vc = reinterpret_cast<const char*>(p.value_cache);
   int64_t blk[2];
 #pragma unroll
   for (int tile = 0; tile < 2; ++tile) {
-    const int tp = s.t + 16 * tile;
-    blk[tile] = min(max((int64_t)__builtin_amdgcn_readlane(btl, 16 * tile), (int64_t)0),
-                    (int64_t)p.num_blocks - 1);
-    const uint64_t row0 = (uint64_t)((blk[tile] << bs_shift) + (tp & (p.block_size - 1)));
-    const char* kb = kc + row0 * rowb + hoff;
-    const char* vb = vc + row0 * rowb + hoff;
+    const uint64_t off = tile_row_bytes(p, c, btl, tile, bs_shift, lo.rowb, blk[tile]) + hoff;
+    const __amdgpu_buffer_rsrc_t rk = rows_rsrc(kc + off), rv = rows_rsrc(vc + off);
 #pragma unroll
-    for (int h = 0; h < D / 64; ++h) st.k[tile][h] = ld16s(kb + c * rowb + 16 * G + 64 * h);
+    for (int h = 0; h < D / 64; ++h) st.k[tile][h] = bld16(rk, lo.koff + 64 * h, 0);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const char* vr = vb + (4 * G + e) * rowb + (D / 16) * c;
       if constexpr (D == 128)
-        st.v[4 * tile + e].w = ld8s(vr);
+        st.v[4 * tile + e].w = bld8(rv, lo.voff, e * lo.rowb);
       else
-        st.v[4 * tile + e].w = ld4s(vr);
+        st.v[4 * tile + e].w = bld4(rv, lo.voff, e * lo.rowb);
     }
   }
   const float* sp = (lane & 2) ? p.v_scale : p.k_scale;
-  st.sc = sp[((lane & 1) ? blk[1] : blk[0]) * p.kv_heads + s.kh];
+  st.sc = sp[((lane & 1) ? blk[1] : blk[0]) * p.kv_heads + c.kh];
 }
 
+// All loads of one step: K and V rows of both 16-key tiles and the query rows of the step's
+// (sequence, kv-head).  Every path issues the same number of loads, so the compiler's vmcnt
+// waits only drain the step about to be computed.  Rows past the sequence end re-read the last
+// row (or stay in the last page).
 template <typename TT, int D, bool F8>
-__device__ __forceinline__ void load_stream_step(const AttnParams& p, const StepAt& s, int btl,
-                                                 int lane, int g, int bs_shift,
+__device__ __forceinline__ void load_stream_step(const AttnParams& p, const SeqWin& sw,
+                                                 const Cursor& c, int btl, int lane, int bs_shift,
+                                                 const LaneOffs& lo, const QueryPtrs& qp,
                                                  RingStep<TT, D, F8>& st, u32x4 (&qv)[D / 32],
                                                  typename TT::raw& sk) {
-  const int c = lane & 15, G = lane >> 4;
+  const int cl = lane & 15, G = lane >> 4;
   if constexpr (F8) {
-    load_step8<D>(p, s, btl, lane, bs_shift, st);
+    load_step8<D>(p, c, btl, lane, bs_shift, lo, st);
   } else {
-  constexpr int DL = D / 16;
-  const uint32_t rowb = (uint32_t)p.kv_heads * D * 2;
-  const uint32_t hoff = (uint32_t)s.kh * D * 2;
-  const char* kc = reinterpret_cast<const char*>(p.key_cache);
-  const char* vc = reinterpret_cast<const char*>(p.value_cache);
-  const char* kn = reinterpret_cast<const char*>(p.k_new);
-  const char* vn = reinterpret_cast<const char*>(p.v_new);
-  const int last = s.total - 1;
-  if (p.linear_cap > 0) {
-    // Contiguous cache: rows of (b, kh) follow each other; rows past the end re-read the last.
-    const int64_t r0 = ((int64_t)s.b * p.kv_heads + s.kh) * p.linear_cap;
-    const uint32_t rs = (uint32_t)D * 2;
+    constexpr int DL = D / 16;
+    const uint32_t hoff = (uint32_t)c.kh * D * 2;
+    const char* kc = reinterpret_cast<const char*>(p.key_cache);
+    const char* vc = reinterpret_cast<const char*>(p.value_cache);
+    const int last = c.total - 1;
+    if (p.linear_cap > 0) {
+      // Contiguous cache: rows of (b, kh) follow each other; rows past the end re-read the last.
+      const int64_t r0 = ((int64_t)(sw.base + c.bl) * p.kv_heads + c.kh) * p.linear_cap;
+      const uint32_t rs = (uint32_t)D * 2;
 #pragma unroll
-    for (int tile = 0; tile < 2; ++tile) {
-      const int tp = s.t + 16 * tile;
-      const char* kr = kc + (uint64_t)(r0 + min(tp + c, last)) * rs;
+      for (int tile = 0; tile < 2; ++tile) {
+        const int tp = c.t + 16 * tile;
+        const char* kr = kc + (uint64_t)(r0 + min(tp + cl, last)) * rs;
 #pragma unroll
-      for (int q = 0; q < D / 32; ++q) st.k[tile][q] = ld16s(kr + 16 * G + 64 * q);
+        for (int q = 0; q < D / 32; ++q) st.k[tile][q] = ld16s(kr + 16 * G + 64 * q);
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        st.v[4 * tile + e] =
-            ld_vrow_s<D>(vc + (uint64_t)(r0 + min(tp + 4 * G + e, last)) * rs + DL * 2 * c);
-    }
-  } else if (bs_shift >= 4 && min(s.t + 31, last) < s.cache_limit) {
-    // Every row in the pages and each 16-key tile inside one page: scalar page base (page id
-    // read from a lane of `btl`), fixed lane offsets.  Rows past the end stay in the last page.
+        for (int e = 0; e < 4; ++e)
+          st.v[4 * tile + e] =
+              ld_vrow_s<D>(vc + (uint64_t)(r0 + min(tp + 4 * G + e, last)) * rs + DL * 2 * cl);
+      }
+    } else if (bs_shift >= 4 && min(c.t + 31, last) < c.lim) {
+      // Every row in the pages and each 16-key tile inside one page.
 #pragma unroll
-    for (int tile = 0; tile < 2; ++tile) {
-      const int tp = s.t + 16 * tile;
-      const int64_t blk = min(max((int64_t)__builtin_amdgcn_readlane(btl, 16 * tile), (int64_t)0),
-                              (int64_t)p.num_blocks - 1);
-      const char* kb = kc + (uint64_t)((blk << bs_shift) + (tp & (p.block_size - 1))) * rowb + hoff;
-      const char* vb = vc + (uint64_t)((blk << bs_shift) + (tp & (p.block_size - 1))) * rowb + hoff;
+      for (int tile = 0; tile < 2; ++tile) {
+        int64_t blk;
+        const uint64_t off = tile_row_bytes(p, c, btl, tile, bs_shift, lo.rowb, blk) + hoff;
+        const __amdgpu_buffer_rsrc_t rk = rows_rsrc(kc + off), rv = rows_rsrc(vc + off);
 #pragma unroll
-      for (int q = 0; q < D / 32; ++q) st.k[tile][q] = ld16s(kb + c * rowb + 16 * G + 64 * q);
+        for (int q = 0; q < D / 32; ++q) st.k[tile][q] = bld16(rk, lo.koff + 64 * q, 0);
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        st.v[4 * tile + e] = ld_vrow_s<D>(vb + (4 * G + e) * rowb + DL * 2 * c);
-    }
-  } else {
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (D == 128)
+            st.v[4 * tile + e] = VRow<D>{bld16(rv, lo.voff, e * lo.rowb)};
+          else
+            st.v[4 * tile + e] = VRow<D>{bld8(rv, lo.voff, e * lo.rowb)};
+        }
+      }
+    } else {
+      const char* kn = reinterpret_cast<const char*>(p.k_new);
+      const char* vn = reinterpret_cast<const char*>(p.v_new);
+      const int s0 = lane_of(sw.q.s0, c.bl), pastb = lane_of(sw.q.pastb, c.bl);
 #pragma unroll
-    for (int tile = 0; tile < 2; ++tile) {
-      const int tp = s.t + 16 * tile;
-      const char* kr = stream_row(p, s, btl, min(tp + c, last), kc, kn, rowb, hoff, bs_shift);
+      for (int tile = 0; tile < 2; ++tile) {
+        const int tp = c.t + 16 * tile;
+        const char* kr = stream_row(p, c, btl, min(tp + cl, last), s0, pastb, kc, kn, lo.rowb,
+                                    hoff, bs_shift);
 #pragma unroll
-      for (int q = 0; q < D / 32; ++q) st.k[tile][q] = ld16s(kr + 16 * G + 64 * q);
+        for (int q = 0; q < D / 32; ++q) st.k[tile][q] = ld16s(kr + 16 * G + 64 * q);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const char* vr =
-            stream_row(p, s, btl, min(tp + 4 * G + e, last), vc, vn, rowb, hoff, bs_shift);
-        st.v[4 * tile + e] = ld_vrow_s<D>(vr + DL * 2 * c);
+        for (int e = 0; e < 4; ++e) {
+          const char* vr = stream_row(p, c, btl, min(tp + 4 * G + e, last), s0, pastb, vc, vn,
+                                      lo.rowb, hoff, bs_shift);
+          st.v[4 * tile + e] = ld_vrow_s<D>(vr + DL * 2 * cl);
+        }
       }
     }
   }
-  }
-  // Query rows of this (sequence, kv-head): MFMA column c is row r = c (rows past R repeat the
-  // last one; their scores are masked).  k-step q covers dims 32q + 8G .. (bf16 pages) or
-  // 64(q/2) + 16G + 8(q%2) .. (fp8 pages, matching the key chunks).
-  const int r = min(c, g * s.nq - 1);
-  const char* qrow = reinterpret_cast<const char*>(p.q) +
-                     ((int64_t)(s.s0 + r / g) * p.num_heads + s.kh * g + r % g) * D * 2;
 #pragma unroll
-  for (int q = 0; q < D / 32; ++q) {
-    const int dim0 = F8 ? 64 * (q >> 1) + 16 * G + 8 * (q & 1) : 32 * q + 8 * G;
-    qv[q] = ld16(qrow + 2 * dim0);
-  }
-  // Sink logit input of that row's head (a harmless read of the query when there is none).
-  const typename TT::raw* sp = p.head_sink ? reinterpret_cast<const typename TT::raw*>(p.head_sink)
-                                           : reinterpret_cast<const typename TT::raw*>(p.q);
-  sk = sp[p.head_sink ? s.kh * g + r % g : 0];
+  for (int q = 0; q < D / 32; ++q)
+    qv[q] = ld16(qp.q + (F8 ? 128 * (q >> 1) + 16 * (q & 1) : 64 * q));
+  sk = *reinterpret_cast<const typename TT::raw*>(qp.sink);
 }
 
-// Stream the flattened steps [lo, hi) of one window through a DEPTH-3 register ring.  Three
-// cursors run over the same step list: block-table entries are fetched four steps ahead of the
-// compute, key/value/query rows two steps ahead, so a sequence or kv-head boundary costs no
-// pipeline refill.  A piece (one sequence, one sub-segment) is finished when the compute cursor
-// leaves it: final rows when the piece covers its whole sequence, else a partial at slot u + b.
+// Stream the flattened steps [lo, hi) of one window through a DEPTH-deep register ring.  Three
+// cursors run over the same step list: block-table entries are fetched 2 * (DEPTH - 1) steps
+// ahead of the compute, key/value/query rows DEPTH - 1 steps ahead, so a sequence or kv-head
+// boundary costs no pipeline refill.  A piece (one sequence, one sub-segment) is finished when
+// the compute cursor leaves it: final rows when the piece covers its whole sequence, else a
+// partial at slot u + b.  Steps whose keys are visible to every row of the piece skip the
+// per-score position tests.
 template <typename TT, int D, bool CAP, bool F8, int DEPTH>
-__device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& sw, int64_t lo,
-                                             int64_t hi, int64_t L, int x, int64_t u0,
-                                             int lane) {
+__device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& sw, int lo, int hi,
+                                             int L, int x, int u0, int lane) {
   using vec8 = typename TT::vec8;
   const int c = lane & 15, G = lane >> 4;
   const int g = p.num_heads / p.kv_heads;
   const int bs_shift = __builtin_ctz(p.block_size);  // power of two (host dispatch)
-  const int64_t K = hi - lo;
+  const int K = hi - lo;
+  LaneOffs lofs;
+  lofs.rowb = (uint32_t)p.kv_heads * D * (F8 ? 1 : 2);
+  lofs.koff = (uint32_t)c * lofs.rowb + 16 * G;
+  lofs.voff = (uint32_t)(4 * G) * lofs.rowb + (uint32_t)(D / 16) * (F8 ? 1 : 2) * c;
 
-  Cursor cc = cursor_at(sw, lo, L);
+  Cursor cc = cursor_at(sw, p, lo, L, x, u0);
   Cursor cd = cc, cb = cc;
+  QueryPtrs qp = query_ptrs<D, F8>(p, sw, cd, g, lane);
   RingStep<TT, D, F8> st[DEPTH];
   u32x4 qr[DEPTH][D / 32];
   typename TT::raw skr[DEPTH];
@@ -627,59 +682,64 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
   // Prologue: block ids of steps 0 .. DEPTH-2, their rows, block ids of the next DEPTH-1 steps.
 #pragma unroll
   for (int j = 0; j < DEPTH - 1; ++j) {
-    btr[j] = load_step_blocks(p, step_at(cb, sw, p, x, u0), lane, bs_shift);
-    cursor_next(cb, sw, hi, L);
+    btr[j] = load_step_blocks(p, sw, cb, lane, bs_shift);
+    cursor_next(cb, sw, p, hi, L, x, u0);
   }
 #pragma unroll
   for (int j = 0; j < DEPTH - 1; ++j) {
-    load_stream_step<TT, D, F8>(p, step_at(cd, sw, p, x, u0), btr[j], lane, g, bs_shift, st[j],
-                                qr[j], skr[j]);
-    cursor_next(cd, sw, hi, L);
+    load_stream_step<TT, D, F8>(p, sw, cd, btr[j], lane, bs_shift, lofs, qp, st[j], qr[j], skr[j]);
+    if (cursor_next(cd, sw, p, hi, L, x, u0)) qp = query_ptrs<D, F8>(p, sw, cd, g, lane);
   }
 #pragma unroll
   for (int j = DEPTH - 1; j < 2 * DEPTH - 2; ++j) {
-    btr[j % DEPTH] = load_step_blocks(p, step_at(cb, sw, p, x, u0), lane, bs_shift);
-    cursor_next(cb, sw, hi, L);
+    btr[j % DEPTH] = load_step_blocks(p, sw, cb, lane, bs_shift);
+    cursor_next(cb, sw, p, hi, L, x, u0);
   }
 
   RowState<TT, D> rs;
-  int pc_bl = -1;
-  int64_t pc_u = -1;
-  StepAt pc{};  // the piece being computed
-  bool pc_final = false;
-  int pc_first = 0;
-  float pc_sink = kNegInf;  // sink logit of row c
+  int pc_bl = -1, pc_u = -1;  // the piece being computed
+  int pc_kh = 0, pc_total = 0;
+  int full_lo = 0, full_hi = 0;  // steps [t, t + 32) inside [full_lo, full_hi) need no masks
+  float pc_sink = kNegInf;       // sink logit of row c
   auto finish = [&]() {
-    const int64_t slot = pc_u + pc.b;
-    store_rows<TT, D>(rs, p, pc.kh, pc.s0, 0, g * pc.nq, g, c, G, pc_sink, pc_final,
-                      [&](int64_t, int, int rloc) { return (slot * p.kv_heads + pc.kh) * 16 + rloc; });
+    const int b = sw.base + pc_bl;
+    const int P = lane_of(sw.P, pc_bl), n = lane_of(sw.q.n, pc_bl);
+    const bool final = P >= pc_u * L && P + n <= (pc_u + 1) * L;
+    const int64_t slot = (int64_t)pc_u + b;
+    store_rows<TT, D>(rs, p, pc_kh, lane_of(sw.q.s0, pc_bl), 0, g * lane_of(sw.q.nq, pc_bl), g, c,
+                      G, pc_sink, final,
+                      [&](int64_t, int, int rloc) { return (slot * p.kv_heads + pc_kh) * 16 + rloc; });
   };
 
-  for (int64_t k = 0; k < K; k += DEPTH) {
+  for (int k = 0; k < K; k += DEPTH) {
 #pragma unroll
     for (int i = 0; i < DEPTH; ++i) {
       // Rows of step k+i+DEPTH-1 (block ids fetched DEPTH-1 iterations ago), then the block ids
       // of step k+i+2*(DEPTH-1).
       const int sd_slot = (i + DEPTH - 1) % DEPTH, sb_slot = (i + DEPTH - 2) % DEPTH;
-      load_stream_step<TT, D, F8>(p, step_at(cd, sw, p, x, u0), btr[sd_slot], lane, g, bs_shift,
-                                  st[sd_slot], qr[sd_slot], skr[sd_slot]);
-      cursor_next(cd, sw, hi, L);
-      btr[sb_slot] = load_step_blocks(p, step_at(cb, sw, p, x, u0), lane, bs_shift);
-      cursor_next(cb, sw, hi, L);
+      load_stream_step<TT, D, F8>(p, sw, cd, btr[sd_slot], lane, bs_shift, lofs, qp, st[sd_slot],
+                                  qr[sd_slot], skr[sd_slot]);
+      if (cursor_next(cd, sw, p, hi, L, x, u0)) qp = query_ptrs<D, F8>(p, sw, cd, g, lane);
+      btr[sb_slot] = load_step_blocks(p, sw, cb, lane, bs_shift);
+      cursor_next(cb, sw, p, hi, L, x, u0);
       if (k + i < K) {
         if (cc.bl != pc_bl || cc.u != pc_u) {
           if (pc_bl >= 0) finish();
-          pc = step_at(cc, sw, p, x, u0);
           pc_bl = cc.bl;
           pc_u = cc.u;
-          pc_final = pc.P >= cc.u * L && pc.P + pc.n <= cc.ub;
-          pc_first = __builtin_amdgcn_readlane(sw.q.first, cc.bl);
+          pc_kh = cc.kh;
+          pc_total = cc.total;
           pc_sink = p.head_sink ? TT::to_f32(skr[i]) * kLog2e : kNegInf;
-          const int R = g * pc.nq;
+          const int nq = lane_of(sw.q.nq, cc.bl), pastb = lane_of(sw.q.pastb, cc.bl);
+          const int R = g * nq;
           const bool rvalid = c < R;
-          const int rpos = pc.pastb + (rvalid ? c / g : 0);
+          const int rpos = pastb + (rvalid ? c / g : 0);
           rs.vis_lo = p.window > 0 ? rpos - p.window + 1 : 0;
-          rs.vis_hi = rvalid ? (p.causal ? rpos + 1 : pc.total) : -1;
+          rs.vis_hi = rvalid ? (p.causal ? rpos + 1 : pc_total) : -1;
+          // Every valid row (positions pastb .. pastb + nq - 1) sees keys [full_lo, full_hi):
+          // its window and, when causal, the keys up to itself.
+          full_lo = p.window > 0 ? pastb + nq - p.window : 0;
+          full_hi = p.causal ? pastb + 1 : pc_total;
 #pragma unroll
           for (int q = 0; q < D / 32; ++q) rs.qv[q] = __builtin_bit_cast(vec8, qr[i][q]);
 #pragma unroll
@@ -687,24 +747,25 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
           rs.m_run = kNegInf;
           rs.l_part = 0.0f;
         }
-        const int t0 = pc_first + 32 * (int)(cc.f - pc.P);
+        const int t0 = cc.t;
+        const bool masked = !(t0 >= full_lo && t0 + 32 <= full_hi);
         auto run = [&](Step<D>& cur, float ksA, float ksB, float vsA, float vsB) {
-          if (t0 + 32 > pc.total) {
+          if (t0 + 32 > pc_total) {
             // Value rows past the sequence end (re-read rows) take no part, even if not finite.
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
               const int pos = t0 + 16 * (e >> 2) + 4 * G + (e & 3);
-              if (pos >= pc.total) cur.v[e] = VRow<D>{};
+              if (pos >= pc_total) cur.v[e] = VRow<D>{};
             }
           }
-          compute_step<TT, D, CAP, F8>(rs, cur, t0, pc.total, G, p.scale_log2, p.scale, p.softcap,
-                                       ksA, ksB, vsA, vsB);
+          compute_step<TT, D, CAP, F8>(rs, cur, t0, pc_total, G, p.scale_log2, p.scale,
+                                       p.softcap, ksA, ksB, vsA, vsB, masked);
         };
         if constexpr (F8) {
           // Page scales of tiles A and B (lanes 0..3); a tile wholly past the end weighs zero
           // (its page id, and so its scale, is not a real one).
           const int sc = __builtin_bit_cast(int, st[i].sc);
-          const bool b_live = t0 + 16 < pc.total;
+          const bool b_live = t0 + 16 < pc_total;
           Step<D> wide = widen_step<TT, D>(st[i]);
           run(wide, __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc, 0)),
               b_live ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc, 1)) : 0.f,
@@ -713,7 +774,7 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
         } else {
           run(st[i], 1.f, 1.f, 1.f, 1.f);
         }
-        cursor_next(cc, sw, hi, L);
+        cursor_next(cc, sw, p, hi, L, x, u0);
       }
     }
   }
@@ -758,16 +819,20 @@ decode_balanced_kernel(const AttnParams p) {
     hg = id % nx;
     seg = id / nx;
   }
-  const int x = hg * W + (threadIdx.x >> 6);
+  // The wavefront index is wave-uniform; readfirstlane tells the compiler, so the kv-head and
+  // every page address derived from it stay in scalar registers.
+  const int x = __builtin_amdgcn_readfirstlane(hg * W + (int)(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
   const int M = p.mix;
+  // Step counts fit 32 bits: sequences are clamped to the cache capacity and the host bounds
+  // batch * (capacity / 32 + 1) below 2^31.
   const int64_t S = total_steps(p, lane);
   if (S <= 0) return;
-  const int64_t L = seg_len(S, p.max_splits);
-  const int64_t u0 = (int64_t)seg * M;
-  const int64_t gs = min(S, L * u0), ge = min(S, L * (u0 + M));
+  const int L = (int)seg_len(S, p.max_splits);
+  const int u0 = seg * M;
+  const int gs = (int)min(S, (int64_t)L * u0), ge = (int)min(S, (int64_t)L * (u0 + M));
   if (gs >= ge) return;
-  int64_t carry = 0;
+  int carry = 0;
   for (int base = 0; base < p.batch && carry < ge; base += 64) {
     SeqWin sw;
     sw.base = base;
@@ -775,7 +840,7 @@ decode_balanced_kernel(const AttnParams p) {
     const int incl = wave_incl_scan(sw.q.n, lane);
     sw.P = carry + (incl - sw.q.n);
     const int chunk_total = __builtin_amdgcn_readlane(incl, 63);
-    const int64_t lo = max(gs, carry), hi = min(ge, carry + chunk_total);
+    const int lo = max(gs, carry), hi = min(ge, carry + chunk_total);
     if (lo < hi)
       stream_range<TT, D, CAP, F8, F8 ? PA_DECODE_DEPTH8 : PA_DECODE_DEPTH>(p, sw, lo, hi, L, x,
                                                                            u0, lane);

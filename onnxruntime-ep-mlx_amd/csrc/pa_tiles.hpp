@@ -114,7 +114,8 @@ __device__ __forceinline__ typename TT::vec8 value_operand(const Step<D>& st, in
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     const uint32_t lo = st.v[2 * m].word(j >> 1), hi = st.v[2 * m + 1].word(j >> 1);
-    w[m] = (j & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+    // One byte permute: low halves (even j) or high halves (odd j) of the two rows.
+    w[m] = __builtin_amdgcn_perm(hi, lo, (j & 1) ? 0x07060302u : 0x05040100u);
   }
   return __builtin_bit_cast(typename TT::vec8, w);
 }
@@ -160,7 +161,7 @@ template <typename TT, int D, bool CAP, bool SC, bool MASK>
 __device__ __forceinline__ float step_scores(const RowState<TT, D>& rs,
                                              const u32x4 (&k)[2][D / 32], int t0, int end, int G,
                                              float scale_log2, float scale, float cap, float ksA,
-                                             float ksB, float (&x)[8]) {
+                                             float ksB, float (&x)[8], bool masked = true) {
   using vec8 = typename TT::vec8;
   constexpr int KS = D / 32;
   f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
@@ -173,25 +174,29 @@ __device__ __forceinline__ float step_scores(const RowState<TT, D>& rs,
     sa *= ksA;
     sb *= ksB;
   }
-  float lmax = kNegInf;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const int pos = t0 + 16 * (e >> 2) + 4 * G + (e & 3);
     const float sv = (e < 4) ? sa[e & 3] : sb[e & 3];
-    float xv;
     if constexpr (CAP)
-      xv = cap * tanhf(sv * scale / cap) * kLog2e;
+      x[e] = cap * tanhf(sv * scale / cap) * kLog2e;
     else
-      xv = sv * scale_log2;
-    if constexpr (MASK) {
-      const bool vis = pos < end && pos >= rs.vis_lo && pos < rs.vis_hi;
-      x[e] = vis ? xv : kNegInf;
-    } else {
-      (void)pos;
-      x[e] = xv;
-    }
-    lmax = fmaxf(lmax, x[e]);
+      x[e] = sv * scale_log2;
   }
+  // `masked` (wave-uniform) is false when the caller knows every key of the step is visible to
+  // every valid row: one scalar branch instead of the per-score position tests.
+  if constexpr (MASK) {
+    if (masked) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int pos = t0 + 16 * (e >> 2) + 4 * G + (e & 3);
+        const bool vis = pos < end && pos >= rs.vis_lo && pos < rs.vis_hi;
+        x[e] = vis ? x[e] : kNegInf;
+      }
+    }
+  }
+  float lmax = kNegInf;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) lmax = fmaxf(lmax, x[e]);
   return lmax;
 }
 
@@ -249,12 +254,12 @@ template <typename TT, int D, bool CAP, bool SC, bool MASK = true, typename Valu
 __device__ __forceinline__ void attend_step(RowState<TT, D>& rs, const u32x4 (&k)[2][D / 32],
                                             ValueOp vop, int t0, int end, int G,
                                             float scale_log2, float scale, float cap, float ksA,
-                                            float ksB, float vsA, float vsB) {
+                                            float ksB, float vsA, float vsB, bool masked = true) {
   using vec8 = typename TT::vec8;
   constexpr int DL = D / 16;
   float x[8];
   const float lmax = step_scores<TT, D, CAP, SC, MASK>(rs, k, t0, end, G, scale_log2, scale, cap,
-                                                       ksA, ksB, x);
+                                                       ksA, ksB, x, masked);
   if (__any(needs_rescale(rs, lmax))) rescale_rows(rs, lmax, G);
   vec8 phi, plo8;
   step_probs<TT, D, SC>(rs, x, vsA, vsB, phi, plo8);
@@ -307,10 +312,11 @@ template <typename TT, int D, bool CAP, bool SC = false>
 __device__ __forceinline__ void compute_step(RowState<TT, D>& rs, const Step<D>& st, int t0,
                                              int end, int G, float scale_log2, float scale,
                                              float cap, float ksA = 1.f, float ksB = 1.f,
-                                             float vsA = 1.f, float vsB = 1.f) {
+                                             float vsA = 1.f, float vsB = 1.f,
+                                             bool masked = true) {
   attend_step<TT, D, CAP, SC>(
       rs, st.k, [&](int j) { return value_operand<TT, D>(st, j); }, t0, end, G, scale_log2,
-      scale, cap, ksA, ksB, vsA, vsB);
+      scale, cap, ksA, ksB, vsA, vsB, masked);
 }
 
 __device__ __forceinline__ WaveInfo make_wave(const AttnParams& p, int D, int b, int kh, int s0,
