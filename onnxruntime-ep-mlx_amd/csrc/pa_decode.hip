@@ -792,8 +792,12 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
 // sub-segment u writes a partial at slot u + b (unique: the sub-segments of b are consecutive
 // and the next sequence starts in the one where b ends or later), merged by
 // balanced_merge_kernel.
+// Ring depth (steps held in registers) of the streaming decode.  bf16/fp16 pages: 2 -- each step
+// is 16 KiB per wavefront, and the smaller ring needs fewer registers (C3 attention launch
+// 179 us against 185 us at depth 3).  fp8 pages: 3 (8 KiB steps; depths 2-5 measured within
+// noise of each other).
 #ifndef PA_DECODE_DEPTH
-#define PA_DECODE_DEPTH 3
+#define PA_DECODE_DEPTH 2
 #endif
 #ifndef PA_DECODE_DEPTH8
 #define PA_DECODE_DEPTH8 3
