@@ -77,29 +77,40 @@ __device__ __forceinline__ u32x2 e4m3x4_widen(uint32_t w) {
   }
 }
 
+// Key operand of k-step s of tile `tile`, widened from the codes as it is needed: chunk h = s/2
+// of the lane's key codes holds k-steps 2h (words 0, 1) and 2h + 1 (words 2, 3).
 template <typename TT, int D>
-__device__ __forceinline__ Step<D> widen_step(const Step8<D>& r) {
-  Step<D> o;
+__device__ __forceinline__ typename TT::vec8 key_operand8(const Step8<D>& r, int tile, int s) {
+  const u32x4& w = r.k[tile][s >> 1];
+  const int t = s & 1;
+  const u32x2 a = e4m3x4_widen<TT>(w[2 * t]), b = e4m3x4_widen<TT>(w[2 * t + 1]);
+  return __builtin_bit_cast(typename TT::vec8, u32x4{a[0], a[1], b[0], b[1]});
+}
+
+// Value operand of N-tile j (8 keys x head dim (D/16)*c + j) straight from the code rows: one
+// byte permute gathers dims j and j + 1 (j even) of value rows 2m and 2m + 1, and one
+// conversion per N-tile turns a code pair into word m.  The permute of j and j + 1 is the same
+// expression, so the two N-tiles share it.
+template <typename TT, int D>
+__device__ __forceinline__ typename TT::vec8 value_operand8(const Step8<D>& r, int j) {
+  u32x4 w;
 #pragma unroll
-  for (int tile = 0; tile < 2; ++tile)
-#pragma unroll
-    for (int h = 0; h < D / 64; ++h)
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const u32x2 a = e4m3x4_widen<TT>(r.k[tile][h][2 * t]);
-        const u32x2 b = e4m3x4_widen<TT>(r.k[tile][h][2 * t + 1]);
-        o.k[tile][2 * h + t] = u32x4{a[0], a[1], b[0], b[1]};
-      }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
+  for (int m = 0; m < 4; ++m) {
+    uint32_t lo, hi;
     if constexpr (D == 128) {
-      const u32x2 a = e4m3x4_widen<TT>(r.v[e].w[0]), b = e4m3x4_widen<TT>(r.v[e].w[1]);
-      o.v[e].w = u32x4{a[0], a[1], b[0], b[1]};
+      lo = r.v[2 * m].w[j >> 2];
+      hi = r.v[2 * m + 1].w[j >> 2];
     } else {
-      o.v[e].w = e4m3x4_widen<TT>(r.v[e].w);
+      lo = r.v[2 * m].w;
+      hi = r.v[2 * m + 1].w;
     }
+    // Bytes (row 2m, dim j'), (row 2m+1, dim j'), (row 2m, dim j'+1), (row 2m+1, dim j'+1) with
+    // j' = j & ~1 within the word.
+    const uint32_t pair = __builtin_amdgcn_perm(hi, lo, (j & 2) ? 0x07030602u : 0x05010400u);
+    const u32x2 both = e4m3x4_widen<TT>(pair);  // (j & 1) picks one; the other folds away
+    w[m] = (j & 1) ? both[1] : both[0];
   }
-  return o;
+  return __builtin_bit_cast(typename TT::vec8, w);
 }
 
 // Fast path: all 32 keys cached, 16-key tiles page-aligned.  The page id of each tile comes
@@ -583,8 +594,8 @@ template <typename TT, int D, bool F8>
 __device__ __forceinline__ void load_stream_step(const AttnParams& p, const SeqWin& sw,
                                                  const Cursor& c, int btl, int lane, int bs_shift,
                                                  const LaneOffs& lo, const QueryPtrs& qp,
-                                                 RingStep<TT, D, F8>& st, u32x4 (&qv)[D / 32],
-                                                 typename TT::raw& sk) {
+                                                 bool qload, RingStep<TT, D, F8>& st,
+                                                 u32x4 (&qv)[D / 32], typename TT::raw& sk) {
   const int cl = lane & 15, G = lane >> 4;
   if constexpr (F8) {
     load_step8<D>(p, c, btl, lane, bs_shift, lo, st);
@@ -646,10 +657,14 @@ __device__ __forceinline__ void load_stream_step(const AttnParams& p, const SeqW
       }
     }
   }
+  // Query rows and sink only for a step that starts a piece (the compute cursor takes them
+  // there and nowhere else).
+  if (qload) {
 #pragma unroll
-  for (int q = 0; q < D / 32; ++q)
-    qv[q] = ld16(qp.q + (F8 ? 128 * (q >> 1) + 16 * (q & 1) : 64 * q));
-  sk = *reinterpret_cast<const typename TT::raw*>(qp.sink);
+    for (int q = 0; q < D / 32; ++q)
+      qv[q] = ld16(qp.q + (F8 ? 128 * (q >> 1) + 16 * (q & 1) : 64 * q));
+    sk = *reinterpret_cast<const typename TT::raw*>(qp.sink);
+  }
 }
 
 // Stream the flattened steps [lo, hi) of one window through a DEPTH-deep register ring.  Three
@@ -685,10 +700,13 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
     btr[j] = load_step_blocks(p, sw, cb, lane, bs_shift);
     cursor_next(cb, sw, p, hi, L, x, u0);
   }
+  bool qload = true;  // the data cursor's step starts a piece
 #pragma unroll
   for (int j = 0; j < DEPTH - 1; ++j) {
-    load_stream_step<TT, D, F8>(p, sw, cd, btr[j], lane, bs_shift, lofs, qp, st[j], qr[j], skr[j]);
-    if (cursor_next(cd, sw, p, hi, L, x, u0)) qp = query_ptrs<D, F8>(p, sw, cd, g, lane);
+    load_stream_step<TT, D, F8>(p, sw, cd, btr[j], lane, bs_shift, lofs, qp, qload, st[j], qr[j],
+                                skr[j]);
+    qload = cursor_next(cd, sw, p, hi, L, x, u0);
+    if (qload) qp = query_ptrs<D, F8>(p, sw, cd, g, lane);
   }
 #pragma unroll
   for (int j = DEPTH - 1; j < 2 * DEPTH - 2; ++j) {
@@ -717,9 +735,10 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
       // Rows of step k+i+DEPTH-1 (block ids fetched DEPTH-1 iterations ago), then the block ids
       // of step k+i+2*(DEPTH-1).
       const int sd_slot = (i + DEPTH - 1) % DEPTH, sb_slot = (i + DEPTH - 2) % DEPTH;
-      load_stream_step<TT, D, F8>(p, sw, cd, btr[sd_slot], lane, bs_shift, lofs, qp, st[sd_slot],
-                                  qr[sd_slot], skr[sd_slot]);
-      if (cursor_next(cd, sw, p, hi, L, x, u0)) qp = query_ptrs<D, F8>(p, sw, cd, g, lane);
+      load_stream_step<TT, D, F8>(p, sw, cd, btr[sd_slot], lane, bs_shift, lofs, qp, qload,
+                                  st[sd_slot], qr[sd_slot], skr[sd_slot]);
+      qload = cursor_next(cd, sw, p, hi, L, x, u0);
+      if (qload) qp = query_ptrs<D, F8>(p, sw, cd, g, lane);
       btr[sb_slot] = load_step_blocks(p, sw, cb, lane, bs_shift);
       cursor_next(cb, sw, p, hi, L, x, u0);
       if (k + i < K) {
@@ -764,13 +783,25 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
         if constexpr (F8) {
           // Page scales of tiles A and B (lanes 0..3); a tile wholly past the end weighs zero
           // (its page id, and so its scale, is not a real one).
-          const int sc = __builtin_bit_cast(int, st[i].sc);
+          Step8<D>& cur = st[i];
+          const int sc = __builtin_bit_cast(int, cur.sc);
           const bool b_live = t0 + 16 < pc_total;
-          Step<D> wide = widen_step<TT, D>(st[i]);
-          run(wide, __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc, 0)),
+          if (t0 + 32 > pc_total) {
+            // Value rows past the sequence end (re-read rows) take no part, even if not finite.
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const int pos = t0 + 16 * (e >> 2) + 4 * G + (e & 3);
+              if (pos >= pc_total) cur.v[e] = RawV8<D>{};
+            }
+          }
+          attend_step_ops<TT, D, CAP, true>(
+              rs, [&](int tile, int s) { return key_operand8<TT, D>(cur, tile, s); },
+              [&](int j) { return value_operand8<TT, D>(cur, j); }, t0, pc_total, G,
+              p.scale_log2, p.scale, p.softcap,
+              __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc, 0)),
               b_live ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc, 1)) : 0.f,
               __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc, 2)),
-              b_live ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc, 3)) : 0.f);
+              b_live ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc, 3)) : 0.f, masked);
         } else {
           run(st[i], 1.f, 1.f, 1.f, 1.f);
         }

@@ -157,30 +157,33 @@ struct RowState {
 // block for the scheduler to interleave.
 
 // Scores of the step in log2 units (masked to -inf where not visible); returns this lane's max.
-template <typename TT, int D, bool CAP, bool SC, bool MASK>
-__device__ __forceinline__ float step_scores(const RowState<TT, D>& rs,
-                                             const u32x4 (&k)[2][D / 32], int t0, int end, int G,
-                                             float scale_log2, float scale, float cap, float ksA,
-                                             float ksB, float (&x)[8], bool masked = true) {
-  using vec8 = typename TT::vec8;
+//
+// `kop(tile, s)` returns the key operand of k-step s of tile 0 (keys t0..t0+15) or 1.
+template <typename TT, int D, bool CAP, bool SC, bool MASK, typename KeyOp>
+__device__ __forceinline__ float step_scores(const RowState<TT, D>& rs, KeyOp kop, int t0,
+                                             int end, int G, float scale_log2, float scale,
+                                             float cap, float ksA, float ksB, float (&x)[8],
+                                             bool masked = true) {
   constexpr int KS = D / 32;
   f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    sa = TT::mfma(__builtin_bit_cast(vec8, k[0][s]), rs.qv[s], sa);
-    sb = TT::mfma(__builtin_bit_cast(vec8, k[1][s]), rs.qv[s], sb);
+    sa = TT::mfma(kop(0, s), rs.qv[s], sa);
+    sb = TT::mfma(kop(1, s), rs.qv[s], sb);
   }
-  if constexpr (SC) {
+  if constexpr (SC && CAP) {
     sa *= ksA;
     sb *= ksB;
   }
+  // Page scales (SC) fold into the log2-domain score scale: one product per tile.
+  const float xa = SC ? ksA * scale_log2 : scale_log2, xb = SC ? ksB * scale_log2 : scale_log2;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float sv = (e < 4) ? sa[e & 3] : sb[e & 3];
     if constexpr (CAP)
       x[e] = cap * tanhf(sv * scale / cap) * kLog2e;
     else
-      x[e] = sv * scale_log2;
+      x[e] = sv * ((e < 4) ? xa : xb);
   }
   // `masked` (wave-uniform) is false when the caller knows every key of the step is visible to
   // every valid row: one scalar branch instead of the per-score position tests.
@@ -250,16 +253,17 @@ __device__ __forceinline__ void step_probs(RowState<TT, D>& rs, const float (&x)
   plo8 = TT::cvt8(plo);
 }
 
-template <typename TT, int D, bool CAP, bool SC, bool MASK = true, typename ValueOp>
-__device__ __forceinline__ void attend_step(RowState<TT, D>& rs, const u32x4 (&k)[2][D / 32],
-                                            ValueOp vop, int t0, int end, int G,
-                                            float scale_log2, float scale, float cap, float ksA,
-                                            float ksB, float vsA, float vsB, bool masked = true) {
+template <typename TT, int D, bool CAP, bool SC, bool MASK = true, typename KeyOp,
+          typename ValueOp>
+__device__ __forceinline__ void attend_step_ops(RowState<TT, D>& rs, KeyOp kop, ValueOp vop,
+                                                int t0, int end, int G, float scale_log2,
+                                                float scale, float cap, float ksA, float ksB,
+                                                float vsA, float vsB, bool masked = true) {
   using vec8 = typename TT::vec8;
   constexpr int DL = D / 16;
   float x[8];
-  const float lmax = step_scores<TT, D, CAP, SC, MASK>(rs, k, t0, end, G, scale_log2, scale, cap,
-                                                       ksA, ksB, x, masked);
+  const float lmax = step_scores<TT, D, CAP, SC, MASK>(rs, kop, t0, end, G, scale_log2, scale,
+                                                       cap, ksA, ksB, x, masked);
   if (__any(needs_rescale(rs, lmax))) rescale_rows(rs, lmax, G);
   vec8 phi, plo8;
   step_probs<TT, D, SC>(rs, x, vsA, vsB, phi, plo8);
@@ -271,6 +275,17 @@ __device__ __forceinline__ void attend_step(RowState<TT, D>& rs, const u32x4 (&k
   }
 }
 
+template <typename TT, int D, bool CAP, bool SC, bool MASK = true, typename ValueOp>
+__device__ __forceinline__ void attend_step(RowState<TT, D>& rs, const u32x4 (&k)[2][D / 32],
+                                            ValueOp vop, int t0, int end, int G,
+                                            float scale_log2, float scale, float cap, float ksA,
+                                            float ksB, float vsA, float vsB, bool masked = true) {
+  using vec8 = typename TT::vec8;
+  attend_step_ops<TT, D, CAP, SC, MASK>(
+      rs, [&](int tile, int s) { return __builtin_bit_cast(vec8, k[tile][s]); }, vop, t0, end, G,
+      scale_log2, scale, cap, ksA, ksB, vsA, vsB, masked);
+}
+
 // NG row groups against the same step: all scores first, one branch for the rare rescale, then
 // every group's probabilities and PV MFMAs in one block, each value operand built once.
 template <typename TT, int D, bool CAP, bool MASK, int NG, typename ValueOp>
@@ -280,11 +295,12 @@ __device__ __forceinline__ void attend_groups(RowState<TT, D> (&rs)[NG],
                                               float cap) {
   using vec8 = typename TT::vec8;
   constexpr int DL = D / 16;
+  auto kop = [&](int tile, int s) { return __builtin_bit_cast(vec8, k[tile][s]); };
   float x[NG][8], lmax[NG];
   bool any = false;
 #pragma unroll
   for (int j = 0; j < NG; ++j) {
-    lmax[j] = step_scores<TT, D, CAP, false, MASK>(rs[j], k, t0, end, G, scale_log2, scale, cap,
+    lmax[j] = step_scores<TT, D, CAP, false, MASK>(rs[j], kop, t0, end, G, scale_log2, scale, cap,
                                                    1.f, 1.f, x[j]);
     any = any || needs_rescale(rs[j], lmax[j]);
   }
