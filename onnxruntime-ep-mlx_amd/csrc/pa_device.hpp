@@ -88,6 +88,20 @@ struct TF16 {
     return r;
   }
   __device__ static float back(_Float16 v) { return (float)v; }
+  // x = hi + lo with hi and lo fp16 (probabilities split for the P.V product).  hi rounds toward
+  // zero (one packed conversion per pair), so x - hi is exact in fp32; lo rounds the same way,
+  // leaving an error below 2^-20 of x.
+  __device__ static void split8(const float (&x)[8], vec8& hi, vec8& lo) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const auto h = __builtin_amdgcn_cvt_pkrtz(x[2 * m], x[2 * m + 1]);
+      const auto l = __builtin_amdgcn_cvt_pkrtz(x[2 * m] - (float)h[0], x[2 * m + 1] - (float)h[1]);
+      hi[2 * m] = h[0];
+      hi[2 * m + 1] = h[1];
+      lo[2 * m] = l[0];
+      lo[2 * m + 1] = l[1];
+    }
+  }
 };
 
 struct TBF16 {
@@ -106,6 +120,25 @@ struct TBF16 {
     return r;
   }
   __device__ static float back(__bf16 v) { return (float)v; }
+  // x = hi + lo with hi and lo bf16 (probabilities split for the P.V product): hi is x rounded
+  // to nearest even (one packed conversion per pair), read back exactly from its bit pattern,
+  // and lo = round(x - hi).  Writing the read-back as bit operations keeps the compiler from
+  // re-deriving each hi element with a conversion of its own.
+  __device__ static void split8(const float (&x)[8], vec8& hi, vec8& lo) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const bf16x2 h = __builtin_convertvector(f32x2{x[2 * m], x[2 * m + 1]}, bf16x2);
+      const uint32_t w = __builtin_bit_cast(uint32_t, h);
+      const float h0 = __builtin_bit_cast(float, w << 16), h1 = __builtin_bit_cast(float, w & 0xffff0000u);
+      const bf16x2 l = __builtin_convertvector(f32x2{x[2 * m] - h0, x[2 * m + 1] - h1}, bf16x2);
+      hi[2 * m] = h[0];
+      hi[2 * m + 1] = h[1];
+      lo[2 * m] = l[0];
+      lo[2 * m + 1] = l[1];
+    }
+  }
 };
 
 struct TF32 {

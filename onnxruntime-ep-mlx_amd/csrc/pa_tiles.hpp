@@ -237,7 +237,7 @@ __device__ __forceinline__ void step_probs(RowState<TT, D>& rs, const float (&x)
                                            float vsB, typename TT::vec8& phi,
                                            typename TT::vec8& plo8) {
   const float msafe = (rs.m_run == kNegInf) ? 0.0f : rs.m_run;
-  float pv[8], plo[8];
+  float pv[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     pv[e] = __builtin_amdgcn_exp2f(x[e] - msafe);
@@ -247,10 +247,7 @@ __device__ __forceinline__ void step_probs(RowState<TT, D>& rs, const float (&x)
 #pragma unroll
     for (int e = 0; e < 8; ++e) pv[e] *= (e < 4) ? vsA : vsB;  // l_part keeps the unscaled sum
   }
-  phi = TT::cvt8(pv);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) plo[e] = pv[e] - TT::back(phi[e]);
-  plo8 = TT::cvt8(plo);
+  TT::split8(pv, phi, plo8);
 }
 
 template <typename TT, int D, bool CAP, bool SC, bool MASK = true, typename KeyOp,
