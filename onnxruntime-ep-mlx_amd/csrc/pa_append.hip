@@ -245,7 +245,34 @@ __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p
   // LATENT layout: no value input and no value cache (values are read from the key rows).
   const bool write_v = write_cache && p.value != nullptr && p.value_cache != nullptr;
   void* const v_out = p.value != nullptr ? p.v_out : nullptr;
-  for (int kh = wave; kh < p.kv_heads; kh += 4) {
+  // Plain copies (no rotary/norm, cache in the activation dtype, paged): the token's key row
+  // and value row -- all kv-heads, contiguous in the input and in the slot -- move 16 bytes per
+  // lane across the whole workgroup when every address is 16-byte aligned.
+  bool copied = false;
+  if (CK == kCacheT && !transform && !linear) {
+    using raw = typename TT::raw;
+    const int64_t row_bytes = (int64_t)p.kv_heads * D * (int64_t)sizeof(raw);
+    const char* ks = reinterpret_cast<const char*>(p.key) + (int64_t)t * p.k_ld * sizeof(raw);
+    const char* vs = p.value ? reinterpret_cast<const char*>(p.value) + (int64_t)t * p.v_ld * sizeof(raw)
+                             : nullptr;
+    char* kd = write_cache ? reinterpret_cast<char*>(p.key_cache) + slot * row_bytes : nullptr;
+    char* vd = write_v ? reinterpret_cast<char*>(p.value_cache) + slot * row_bytes : nullptr;
+    char* vo = v_out ? reinterpret_cast<char*>(v_out) + (int64_t)t * row_bytes : nullptr;
+    const uintptr_t align = (uintptr_t)row_bytes | (uintptr_t)ks | (uintptr_t)vs | (uintptr_t)kd |
+                            (uintptr_t)vd | (uintptr_t)vo;
+    if ((align & 15) == 0) {
+      for (int64_t o = (int64_t)threadIdx.x * 16; o < row_bytes; o += (int64_t)blockDim.x * 16) {
+        if (kd) *reinterpret_cast<u32x4*>(kd + o) = *reinterpret_cast<const u32x4*>(ks + o);
+        if (vd || vo) {
+          const u32x4 x = *reinterpret_cast<const u32x4*>(vs + o);
+          if (vd) *reinterpret_cast<u32x4*>(vd + o) = x;
+          if (vo) *reinterpret_cast<u32x4*>(vo + o) = x;
+        }
+      }
+      copied = true;
+    }
+  }
+  for (int kh = wave; kh < p.kv_heads && !copied; kh += 4) {
     const int64_t kbase = (int64_t)t * p.k_ld + (int64_t)kh * D;
     const int64_t vbase = (int64_t)t * p.v_ld + (int64_t)kh * D;
     const int64_t obase = ((int64_t)t * p.kv_heads + kh) * D;  // k_out / v_out rows
