@@ -134,6 +134,9 @@ struct Plan {
   int mix;           // balanced: sub-segments per wavefront
   int ng;            // chunked MFMA kernel: 16-row groups per wavefront
   size_t part_rows;  // rows of fp32 partials in the workspace
+  // Planned prefill: items (sequence, row block, kv-head), row blocks per sequence.
+  int64_t plan_items = 0;
+  int plan_rbs = 0;
 };
 
 int max_ctx_bound(const pa_cache* c, const pa_batch* b) {
@@ -202,10 +205,19 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
   if (chunk <= 0 && kind == 2) {
     // Prefill workgroups (4 wavefronts, pa::kPrefillRows grouped query rows each): split the
     // context only when they cannot fill two workgroups per CU.
-    const int64_t units = (int64_t)b->batch * c->kv_heads *
-                          (((int64_t)g * mq + pa::kPrefillRows - 1) / pa::kPrefillRows);
+    const int64_t rbs = ((int64_t)g * mq + pa::kPrefillRows - 1) / pa::kPrefillRows;
+    const int64_t units = (int64_t)b->batch * c->kv_heads * rbs;
     const int64_t target = 2 * (int64_t)device_cus();
-    if (units >= target) {
+    if (units >= target && units <= (int64_t)INT32_MAX / 4) {
+      // Enough workgroups for every slot: planned units, longest first, long items split in two
+      // (the tail of uneven row blocks otherwise idles ~28% of the slots at the C4 shape).
+      pl.chunk = (int)std::min<int64_t>(((int64_t)ctx + 31) / 32 * 32, INT32_MAX / 2);
+      pl.max_splits = 1;
+      pl.plan_items = units;
+      pl.plan_rbs = (int)rbs;
+      pl.part_rows = (size_t)units * 2 * pa::kPrefillRows;
+      return pl;
+    } else if (units >= target) {
       chunk = (int)std::min<int64_t>(((int64_t)ctx + 31) / 32 * 32, INT32_MAX / 2);
     } else {
       const int64_t splits = (target + units - 1) / units;
@@ -241,10 +253,15 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
 }
 
 // Workspace: [partial O (fp32) | partial (m, l)].
+// Planned prefill adds [unit list (2 per item, 4 int32 each) | unit count | split flag per item].
 size_t workspace_for(const pa_cache* c, const pa_batch*, const pa_attn*, const Plan& pl) {
   if (pl.part_rows == 0) return 0;
-  return align256(pl.part_rows * c->head_dim * sizeof(float)) +
-         align256(pl.part_rows * 2 * sizeof(float));
+  size_t n = align256(pl.part_rows * c->head_dim * sizeof(float)) +
+             align256(pl.part_rows * 2 * sizeof(float));
+  if (pl.plan_items > 0)
+    n += align256((size_t)pl.plan_items * 2 * 4 * sizeof(int32_t)) + 256 +
+         align256((size_t)pl.plan_items * sizeof(int32_t));
+  return n;
 }
 
 // Options of one attention call beyond the public descriptors.
@@ -314,6 +331,17 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
   p.part_ml = need ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) +
                                               align256(pl.part_rows * c->head_dim * sizeof(float)))
                    : nullptr;
+  if (pl.plan_items > 0) {
+    char* base = reinterpret_cast<char*>(ws) + align256(pl.part_rows * c->head_dim * sizeof(float)) +
+                 align256(pl.part_rows * 2 * sizeof(float));
+    p.plan = reinterpret_cast<int32_t*>(base);
+    base += align256((size_t)pl.plan_items * 2 * 4 * sizeof(int32_t));
+    p.plan_info = reinterpret_cast<int32_t*>(base);
+    p.plan_split = reinterpret_cast<int32_t*>(base + 256);
+    p.plan_items = (int32_t)pl.plan_items;
+    p.plan_rbs = pl.plan_rbs;
+    p.plan_slots = 2 * device_cus();
+  }
   p.num_blocks = c->num_blocks;
   p.block_size = c->block_size;
   p.kv_heads = c->kv_heads;
@@ -351,7 +379,10 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
   }
   switch (pl.kind) {
     case 1: e = pa::launch_decode_mfma(p, act, c->dtype, s); break;
-    case 2: e = pa::launch_prefill_mfma(p, act, c->dtype, s); break;
+    case 2:
+      e = pl.plan_items > 0 ? pa::launch_prefill_planned(p, act, c->dtype, s)
+                            : pa::launch_prefill_mfma(p, act, c->dtype, s);
+      break;
     default: e = pa::launch_attn_generic(p, act, c->dtype, s); break;
   }
   if (e != hipSuccess) return hip_fail(e, "attention kernel launch");

@@ -301,6 +301,15 @@ struct AttnParams {
   // v_from_key == 0 otherwise.
   int32_t v_head_dim;
   int32_t v_from_key;
+  // Planned prefill (plan_items > 0): item i = (sequence, row block, kv-head) with
+  // i = (b * plan_rbs + rb) * kv_heads + kh.  The plan kernel writes the work units longest first
+  // -- plan[4u .. 4u+3] = (item, part, first key, end key), part 0 a whole item, 1 / 2 the halves
+  // of an item split in two -- the unit count at plan_info[0] and plan_split[i] = 1 for split
+  // items, whose halves leave fp32 partials at rows (2 i + part - 1) * kPrefillRows + row.
+  int32_t plan_items, plan_rbs, plan_slots;
+  int32_t* plan;
+  int32_t* plan_info;
+  int32_t* plan_split;
 };
 
 // Final normalisation shared by every attention kernel: the factor that turns an output
@@ -336,6 +345,9 @@ hipError_t launch_decode_balanced(const AttnParams& p, pa_dtype act, pa_dtype ca
                                   hipStream_t s);
 hipError_t launch_prefill_mfma(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
                                hipStream_t s);
+// Planned prefill: plan kernel, prefill kernel over the planned units, merge of split items.
+hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
+                                  hipStream_t s);
 hipError_t launch_split_reduce(const AttnParams& p, pa_dtype act, hipStream_t s);
 bool decode_mfma_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype);
 // Balanced (streaming) decode: fp16/bf16 activations, d in {64, 128}, power-of-two pages,

@@ -176,11 +176,26 @@ prefill_kernel(const AttnParams p) {
   // Grid x: (row block, sequence, kv-head) with (sequence, kv-head) fastest and the row blocks
   // in reverse, so the last blocks of each chunk (the most keys under the causal mask) start
   // first.  Grid y: context chunk (split-K).
-  const int units = p.batch * p.kv_heads;
-  const int unit = blockIdx.x % units;
-  const int rb = (int)(gridDim.x / units) - 1 - (int)(blockIdx.x / units);
-  const int kh = unit % p.kv_heads, b = unit / p.kv_heads;
-  const int split = blockIdx.y;
+  int rb, kh, b, split = blockIdx.y, part = 0, item = 0, ustart = 0, uend = 0;
+  if (p.plan_items > 0) {
+    // Planned: this workgroup's unit, longest first (both loads in one round trip).
+    const int nunits = p.plan_info[0];
+    const int4 u = reinterpret_cast<const int4*>(p.plan)[min((int)blockIdx.x, p.plan_items * 2 - 1)];
+    if ((int)blockIdx.x >= nunits) return;
+    item = u.x;
+    part = u.y;
+    ustart = u.z;
+    uend = u.w;
+    kh = item % p.kv_heads;
+    rb = (item / p.kv_heads) % p.plan_rbs;
+    b = item / (p.kv_heads * p.plan_rbs);
+  } else {
+    const int units = p.batch * p.kv_heads;
+    const int unit = blockIdx.x % units;
+    rb = (int)(gridDim.x / units) - 1 - (int)(blockIdx.x / units);
+    kh = unit % p.kv_heads;
+    b = unit / p.kv_heads;
+  }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, G = lane >> 4;
   // Everything up to the first barrier is uniform over the workgroup.
   const int s0 = min(max(p.cum[b], 0), p.num_tokens);
@@ -192,10 +207,18 @@ prefill_kernel(const AttnParams p) {
   if (row0 >= R) return;
   const int pastb = max(p.past[b], 0);
   const int total = pastb + nq;
-  const int start = split * p.chunk;
-  if (start >= total) return;
-  const int end = start + min(p.chunk, total - start);
-  const bool single = start == 0 && end == total;
+  int start, end;
+  bool single;
+  if (p.plan_items > 0) {
+    start = ustart;
+    end = max(ustart, min(uend, total));
+    single = part == 0;
+  } else {
+    start = split * p.chunk;
+    if (start >= total) return;
+    end = start + min(p.chunk, total - start);
+    single = start == 0 && end == total;
+  }
   // Metadata beyond the planned capacity leaves no partial buffer: rows stay unwritten.
   if (!single && p.part_o == nullptr) return;
   // Keys any row of the workgroup can see.
@@ -263,9 +286,137 @@ prefill_kernel(const AttnParams p) {
     const int rc = min(r0 + c, R - 1);
     const float sink_c = sink_logit<TT>(p, kh * g + rc % g);
     store_rows<TT, D>(rs[j], p, kh, s0, r0, R, g, c, G, sink_c, single,
-                      [&](int64_t t, int oh, int) {
+                      [&](int64_t t, int oh, int rloc) {
+                        if (p.plan_items > 0)
+                          return ((int64_t)item * 2 + part - 1) * ROWS + (r0 - row0) + rloc;
                         return (t * p.num_heads + oh) * p.max_splits + split;
                       });
+  }
+}
+
+// ----------------------------------------------------------------------------- planned prefill
+// Visible key range [first, end) of item i (the keys some row of the row block can see), the
+// same bounds the prefill kernel derives; end < 0 when the row block holds no rows.
+struct ItemKeys {
+  int first, end;
+};
+__device__ __forceinline__ ItemKeys item_keys(const AttnParams& p, int i) {
+  const int g = p.num_heads / p.kv_heads;
+  const int rb = (i / p.kv_heads) % p.plan_rbs, b = i / (p.kv_heads * p.plan_rbs);
+  const int s0 = min(max(p.cum[b], 0), p.num_tokens);
+  const int s1 = min(max(p.cum[b + 1], s0), p.num_tokens);
+  const int R = g * (s1 - s0);
+  const int row0 = rb * kPrefillRows;
+  if (row0 >= R) return ItemKeys{0, -1};
+  const int pastb = max(p.past[b], 0);
+  const int total = pastb + (s1 - s0);
+  const int r_last = min(row0 + kPrefillRows, R) - 1;
+  const int hi = p.causal ? pastb + r_last / g + 1 : total;
+  const int lo = p.window > 0 ? max(0, pastb + row0 / g - p.window + 1) : 0;
+  const int first = (lo / 32) * 32;
+  return ItemKeys{first, max(first, min(total, hi))};
+}
+
+// One workgroup: the work units of every item, longest first.  An item whose visible keys
+// exceed ~0.6 of a slot's even share of all keys (plan_slots workgroup slots) is split into two
+// halves at a 32-key boundary.  Units are ordered by a counting sort on their 32-key step count
+// (LDS histogram, descending); the order inside a bucket is whatever the atomics give, which
+// changes nothing in the results (every unit writes its own rows or partial).
+template <int NT>
+__global__ __launch_bounds__(NT) void prefill_plan_kernel(const AttnParams p) {
+  constexpr int NB = 1024;  // buckets of 32-key steps (the last one holds everything longer)
+  __shared__ int hist[NB];
+  __shared__ unsigned long long total_keys;
+  const int tid = threadIdx.x;
+  for (int i = tid; i < NB; i += NT) hist[i] = 0;
+  if (tid == 0) total_keys = 0;
+  __syncthreads();
+  unsigned long long mine = 0;
+  for (int i = tid; i < p.plan_items; i += NT) {
+    const ItemKeys k = item_keys(p, i);
+    if (k.end >= 0) mine += (unsigned long long)(k.end - k.first);
+  }
+  atomicAdd(&total_keys, mine);
+  __syncthreads();
+  const long long thr = max(2048LL, (long long)(total_keys * 6 / 10) / max(p.plan_slots, 1));
+  auto bucket = [&](int len) { return NB - 1 - min((len + 31) / 32, NB - 1); };
+  auto split_of = [&](const ItemKeys& k) { return k.end - k.first > thr && k.end - k.first >= 64; };
+  for (int i = tid; i < p.plan_items; i += NT) {
+    const ItemKeys k = item_keys(p, i);
+    if (k.end < 0) {
+      p.plan_split[i] = 0;
+      continue;
+    }
+    const bool sp = split_of(k);
+    p.plan_split[i] = sp ? 1 : 0;
+    if (sp) {
+      const int mid = k.first + (((k.end - k.first + 31) / 32 + 1) / 2) * 32;
+      atomicAdd(&hist[bucket(mid - k.first)], 1);
+      atomicAdd(&hist[bucket(k.end - mid)], 1);
+    } else {
+      atomicAdd(&hist[bucket(k.end - k.first)], 1);
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {  // exclusive scan; NB is small
+    int run = 0;
+    for (int j = 0; j < NB; ++j) {
+      const int c = hist[j];
+      hist[j] = run;
+      run += c;
+    }
+    p.plan_info[0] = run;
+  }
+  __syncthreads();
+  int4* plan = reinterpret_cast<int4*>(p.plan);
+  for (int i = tid; i < p.plan_items; i += NT) {
+    const ItemKeys k = item_keys(p, i);
+    if (k.end < 0) continue;
+    if (split_of(k)) {
+      const int mid = k.first + (((k.end - k.first + 31) / 32 + 1) / 2) * 32;
+      plan[atomicAdd(&hist[bucket(mid - k.first)], 1)] = int4{i, 1, k.first, mid};
+      plan[atomicAdd(&hist[bucket(k.end - mid)], 1)] = int4{i, 2, mid, k.end};
+    } else {
+      plan[atomicAdd(&hist[bucket(k.end - k.first)], 1)] = int4{i, 0, k.first, k.end};
+    }
+  }
+}
+
+// Merge the two halves of each split item (one workgroup per item): rows of the item's row
+// block, D/4 lanes per row, one 16-byte load per half and lane.
+template <typename TT, int D>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnParams p) {
+  constexpr int QPR = D / 4;  // float4 quads per row
+  const int i = blockIdx.x;
+  if (!p.plan_split[i]) return;
+  const int g = p.num_heads / p.kv_heads;
+  const int kh = i % p.kv_heads, rb = (i / p.kv_heads) % p.plan_rbs;
+  const int b = i / (p.kv_heads * p.plan_rbs);
+  const int s0 = min(max(p.cum[b], 0), p.num_tokens);
+  const int s1 = min(max(p.cum[b + 1], s0), p.num_tokens);
+  const int R = g * (s1 - s0);
+  const int row0 = rb * kPrefillRows;
+  const int rows = min(kPrefillRows, R - row0);
+  const int q = threadIdx.x % QPR;
+  for (int r = threadIdx.x / QPR; r < rows; r += 256 / QPR) {
+    const int64_t r0 = ((int64_t)i * 2) * kPrefillRows + r, r1 = r0 + kPrefillRows;
+    const float2 a = reinterpret_cast<const float2*>(p.part_ml)[r0];
+    const float2 c = reinterpret_cast<const float2*>(p.part_ml)[r1];
+    const f32x4 oa = reinterpret_cast<const f32x4*>(p.part_o + r0 * D)[q];
+    const f32x4 oc = reinterpret_cast<const f32x4*>(p.part_o + r1 * D)[q];
+    const float M = fmaxf(a.x, c.x);
+    const float wa = (a.x == kNegInf) ? 0.0f : exp2f(a.x - M);
+    const float wc = (c.x == kNegInf) ? 0.0f : exp2f(c.x - M);
+    const int rr = row0 + r;
+    const int h = kh * g + rr % g;
+    const int64_t t = s0 + rr / g;
+    const float f = finalize_factor(M, a.y * wa + c.y * wc, sink_logit<TT>(p, h));
+    typename TT::raw* out = reinterpret_cast<typename TT::raw*>(p.out) + (t * p.num_heads + h) * D + 4 * q;
+    const f32x4 o = (oa * wa + oc * wc) * f;
+    u32x2 pk;
+    pk[0] = (uint32_t)TT::from_f32(o[0]) | ((uint32_t)TT::from_f32(o[1]) << 16);
+    pk[1] = (uint32_t)TT::from_f32(o[2]) | ((uint32_t)TT::from_f32(o[3]) << 16);
+    *reinterpret_cast<u32x2*>(out) = pk;
   }
 }
 
@@ -289,6 +440,30 @@ hipError_t launch_t(const AttnParams& p, dim3 grid, hipStream_t s) {
 }
 
 }  // namespace
+
+// Planned prefill: plan (one workgroup), the prefill kernel over 2 * plan_items unit slots
+// (workgroups past the planned count exit at once), then the merge of the split items.
+hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
+                                  hipStream_t s) {
+  if (!prefill_mfma_supported(p.head_dim, act, cache_dtype)) return hipErrorInvalidValue;
+  if (p.linear_cap > 0 || p.plan_items <= 0 || p.plan_rbs <= 0 || !p.plan || !p.plan_info ||
+      !p.plan_split || !p.part_o || !p.part_ml || p.max_splits != 1)
+    return hipErrorInvalidValue;
+  if ((int64_t)p.plan_items * 2 > INT32_MAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((prefill_plan_kernel<1024>), dim3(1), dim3(1024), 0, s, p);
+  const dim3 grid(2 * p.plan_items, 1);
+  hipError_t e = act == PA_DTYPE_FLOAT16 ? launch_t<TF16>(p, grid, s) : launch_t<TBF16>(p, grid, s);
+  if (e != hipSuccess) return e;
+  const dim3 mgrid(p.plan_items);
+  if (p.head_dim == 64) {
+    if (act == PA_DTYPE_FLOAT16) hipLaunchKernelGGL((prefill_merge_kernel<TF16, 64>), mgrid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((prefill_merge_kernel<TBF16, 64>), mgrid, dim3(256), 0, s, p);
+  } else {
+    if (act == PA_DTYPE_FLOAT16) hipLaunchKernelGGL((prefill_merge_kernel<TF16, 128>), mgrid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((prefill_merge_kernel<TBF16, 128>), mgrid, dim3(256), 0, s, p);
+  }
+  return hipGetLastError();
+}
 
 bool prefill_mfma_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype) {
   if (act != PA_DTYPE_FLOAT16 && act != PA_DTYPE_BFLOAT16) return false;

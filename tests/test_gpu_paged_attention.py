@@ -290,6 +290,45 @@ def test_prefill_kernel_level(chunk, new_rows_in_cache, bs, d, dtype, window, so
         assert orc.rel_l2(got.astype(np.float64), ref) <= 4e-3, kind
 
 
+# planned prefill (library-chosen plan with at least two workgroups per CU, 512 items here on a
+# 256-CU MI355X): units ordered longest first, items past the split threshold run as two halves
+# merged afterwards, one sequence without new tokens (no items), and a sink logit that only the
+# merge of the split items folds in for those rows
+@pytest.mark.parametrize("d,dtype,sink", [(64, BF16, False), (128, F16, True)],
+                         ids=["d64_bf16", "d128_f16_sink"])
+def test_prefill_planned(d, dtype, sink):
+    import torch
+    import onnxruntime_ep_mlx_amd as ep
+    from pa_cases import to_torch, from_torch
+    rng = np.random.default_rng(71 + d)
+    B, H, KV, bs, nq = 64, 32, 8, 16, 16
+    new_lens = np.full(B, nq)
+    new_lens[5] = 0
+    past = rng.integers(0, 300, size=B)
+    past[[17, 63]] = [2600, 3500]  # items longer than the 2048-key threshold
+    mb = int((past.max() + nq + bs - 1) // bs)
+    case = make_case(H, KV, d, B * mb, bs, B, dtype=dtype, seed=71 + d, new_lens=new_lens,
+                     past=past, max_blocks=mb, std=1.0,
+                     head_sink=(rng.standard_normal(H) if sink else None))
+    ref, ref_t, _, _ = orc.paged_attention_op(case)
+    t = {n: to_torch(case[n], dtype) for n in ("query", "key", "value", "key_cache",
+                                               "value_cache")}
+    I = {n: torch.from_numpy(case[n]).cuda() for n in ("cum", "past", "block_table")}
+    ep.reshape_and_cache(t["key"], t["value"], t["key_cache"], t["value_cache"], I["cum"],
+                         I["past"], I["block_table"])
+    hs = to_torch(case["head_sink"], dtype) if sink else None
+    outs = [ep.attention(t["query"], t["key"], t["value"], t["key_cache"], t["value_cache"],
+                         I["cum"], I["past"], I["block_table"], num_heads=H, max_query_len=nq,
+                         kind=2, head_sink=hs, new_rows_in_cache=True) for _ in range(2)]
+    torch.cuda.synchronize()
+    for out in outs:
+        got = orc.decode(from_torch(out, dtype), dtype)
+        assert orc.rel_l2(got, orc.decode(ref_t, dtype)) <= 2e-3
+        assert orc.rel_l2(got.astype(np.float64), ref) <= 4e-3
+    # the unit order inside a histogram bucket may differ between calls; the rows may not
+    assert torch.equal(outs[0], outs[1])
+
+
 # balanced decode kernel through the kernel-level entries: segments that split sequences,
 # sequences of one step, the separate partial merge, and both sources of the new rows
 @pytest.mark.parametrize("new_rows_in_cache", [False, True])
