@@ -295,6 +295,16 @@ prefill_kernel(const AttnParams p) {
 }
 
 // ----------------------------------------------------------------------------- planned prefill
+// Split threshold of the plan: items with more visible keys than PA_PLAN_SPLIT_PCT percent of a
+// slot's even share of all keys (and at least PA_PLAN_SPLIT_MIN keys) run as two halves.
+// C4 attention launch by threshold: 25 % 393 us, 35 % 392-395, 45 % 372-382, 60 % 391-396,
+// 80 % 388-389, 100 % 384-389.
+#ifndef PA_PLAN_SPLIT_PCT
+#define PA_PLAN_SPLIT_PCT 45
+#endif
+#ifndef PA_PLAN_SPLIT_MIN
+#define PA_PLAN_SPLIT_MIN 2048
+#endif
 // Visible key range [first, end) of item i (the keys some row of the row block can see), the
 // same bounds the prefill kernel derives; end < 0 when the row block holds no rows.
 struct ItemKeys {
@@ -318,7 +328,8 @@ __device__ __forceinline__ ItemKeys item_keys(const AttnParams& p, int i) {
 }
 
 // One workgroup: the work units of every item, longest first.  An item whose visible keys
-// exceed ~0.6 of a slot's even share of all keys (plan_slots workgroup slots) is split into two
+// exceed PA_PLAN_SPLIT_PCT % of a slot's even share of all keys (plan_slots workgroup slots) is
+// split into two
 // halves at a 32-key boundary.  Units are ordered by a counting sort on their 32-key step count
 // (LDS histogram, descending); the order inside a bucket is whatever the atomics give, which
 // changes nothing in the results (every unit writes its own rows or partial).
@@ -338,7 +349,8 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(const AttnParams p) {
   }
   atomicAdd(&total_keys, mine);
   __syncthreads();
-  const long long thr = max(2048LL, (long long)(total_keys * 6 / 10) / max(p.plan_slots, 1));
+  const long long thr = max((long long)PA_PLAN_SPLIT_MIN,
+                           (long long)(total_keys * PA_PLAN_SPLIT_PCT / 100) / max(p.plan_slots, 1));
   auto bucket = [&](int len) { return NB - 1 - min((len + 31) / 32, NB - 1); };
   auto split_of = [&](const ItemKeys& k) { return k.end - k.first > thr && k.end - k.first >= 64; };
   for (int i = tid; i < p.plan_items; i += NT) {
