@@ -370,14 +370,32 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(const AttnParams p) {
     }
   }
   __syncthreads();
-  if (tid == 0) {  // exclusive scan; NB is small
-    int run = 0;
-    for (int j = 0; j < NB; ++j) {
-      const int c = hist[j];
-      hist[j] = run;
-      run += c;
+  {  // exclusive scan of the histogram, one bucket per thread: wave scans, then the wave sums
+    static_assert(NT == NB && NT % 64 == 0 && NT / 64 <= 64, "one bucket per thread");
+    __shared__ int wsum[NT / 64];
+    const int lane = tid & 63, wave = tid >> 6;
+    const int c = hist[tid];
+    int x = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
     }
-    p.plan_info[0] = run;
+    if (lane == 63) wsum[wave] = x;
+    __syncthreads();
+    if (wave == 0) {
+      int v = lane < NT / 64 ? wsum[lane] : 0;
+#pragma unroll
+      for (int o = 1; o < NT / 64; o <<= 1) {
+        const int y = __shfl_up(v, o, 64);
+        if (lane >= o) v += y;
+      }
+      if (lane < NT / 64) wsum[lane] = v;
+    }
+    __syncthreads();
+    const int excl = x - c + (wave > 0 ? wsum[wave - 1] : 0);
+    hist[tid] = excl;
+    if (tid == NT - 1) p.plan_info[0] = excl + c;
   }
   __syncthreads();
   int4* plan = reinterpret_cast<int4*>(p.plan);
@@ -394,12 +412,18 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(const AttnParams p) {
   }
 }
 
-// Merge the two halves of each split item (one workgroup per item): rows of the item's row
-// block, D/4 lanes per row, one 16-byte load per half and lane.
+// Merge the two halves of each split item: one workgroup per kPrefillMergeRows rows of an
+// item's row block, D/4 lanes per row; every load of the workgroup's rows is issued before the
+// first is used, so the merge costs one memory latency, not one per row pass.
+constexpr int kPrefillMergeRows = 32;
 template <typename TT, int D>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnParams p) {
-  constexpr int QPR = D / 4;  // float4 quads per row
-  const int i = blockIdx.x;
+  constexpr int QPR = D / 4;              // float4 quads per row
+  constexpr int RPP = 256 / QPR;          // rows per pass
+  constexpr int NP = kPrefillMergeRows / RPP;
+  static_assert(kPrefillRows % kPrefillMergeRows == 0 && kPrefillMergeRows % RPP == 0, "merge tiling");
+  constexpr int CH = kPrefillRows / kPrefillMergeRows;
+  const int i = blockIdx.x / CH;
   if (!p.plan_split[i]) return;
   const int g = p.num_heads / p.kv_heads;
   const int kh = i % p.kv_heads, rb = (i / p.kv_heads) % p.plan_rbs;
@@ -409,22 +433,33 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnParams p) 
   const int R = g * (s1 - s0);
   const int row0 = rb * kPrefillRows;
   const int rows = min(kPrefillRows, R - row0);
+  if ((blockIdx.x % CH) * kPrefillMergeRows >= rows) return;
   const int q = threadIdx.x % QPR;
-  for (int r = threadIdx.x / QPR; r < rows; r += 256 / QPR) {
+  const int rbase = (blockIdx.x % CH) * kPrefillMergeRows + threadIdx.x / QPR;
+  float2 a[NP], c[NP];
+  f32x4 oa[NP], oc[NP];
+#pragma unroll
+  for (int j = 0; j < NP; ++j) {
+    const int r = min(rbase + j * RPP, rows - 1);  // clamped rows load a valid row, store nothing
     const int64_t r0 = ((int64_t)i * 2) * kPrefillRows + r, r1 = r0 + kPrefillRows;
-    const float2 a = reinterpret_cast<const float2*>(p.part_ml)[r0];
-    const float2 c = reinterpret_cast<const float2*>(p.part_ml)[r1];
-    const f32x4 oa = reinterpret_cast<const f32x4*>(p.part_o + r0 * D)[q];
-    const f32x4 oc = reinterpret_cast<const f32x4*>(p.part_o + r1 * D)[q];
-    const float M = fmaxf(a.x, c.x);
-    const float wa = (a.x == kNegInf) ? 0.0f : exp2f(a.x - M);
-    const float wc = (c.x == kNegInf) ? 0.0f : exp2f(c.x - M);
+    a[j] = reinterpret_cast<const float2*>(p.part_ml)[r0];
+    c[j] = reinterpret_cast<const float2*>(p.part_ml)[r1];
+    oa[j] = reinterpret_cast<const f32x4*>(p.part_o + r0 * D)[q];
+    oc[j] = reinterpret_cast<const f32x4*>(p.part_o + r1 * D)[q];
+  }
+#pragma unroll
+  for (int j = 0; j < NP; ++j) {
+    const int r = rbase + j * RPP;
+    if (r >= rows) continue;
+    const float M = fmaxf(a[j].x, c[j].x);
+    const float wa = (a[j].x == kNegInf) ? 0.0f : exp2f(a[j].x - M);
+    const float wc = (c[j].x == kNegInf) ? 0.0f : exp2f(c[j].x - M);
     const int rr = row0 + r;
     const int h = kh * g + rr % g;
     const int64_t t = s0 + rr / g;
-    const float f = finalize_factor(M, a.y * wa + c.y * wc, sink_logit<TT>(p, h));
+    const float f = finalize_factor(M, a[j].y * wa + c[j].y * wc, sink_logit<TT>(p, h));
     typename TT::raw* out = reinterpret_cast<typename TT::raw*>(p.out) + (t * p.num_heads + h) * D + 4 * q;
-    const f32x4 o = (oa * wa + oc * wc) * f;
+    const f32x4 o = (oa[j] * wa + oc[j] * wc) * f;
     u32x2 pk;
     pk[0] = (uint32_t)TT::from_f32(o[0]) | ((uint32_t)TT::from_f32(o[1]) << 16);
     pk[1] = (uint32_t)TT::from_f32(o[2]) | ((uint32_t)TT::from_f32(o[3]) << 16);
@@ -461,12 +496,12 @@ hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype ca
   if (p.linear_cap > 0 || p.plan_items <= 0 || p.plan_rbs <= 0 || !p.plan || !p.plan_info ||
       !p.plan_split || !p.part_o || !p.part_ml || p.max_splits != 1)
     return hipErrorInvalidValue;
-  if ((int64_t)p.plan_items * 2 > INT32_MAX) return hipErrorInvalidValue;
+  if ((int64_t)p.plan_items * (kPrefillRows / kPrefillMergeRows) > INT32_MAX) return hipErrorInvalidValue;
   hipLaunchKernelGGL((prefill_plan_kernel<1024>), dim3(1), dim3(1024), 0, s, p);
   const dim3 grid(2 * p.plan_items, 1);
   hipError_t e = act == PA_DTYPE_FLOAT16 ? launch_t<TF16>(p, grid, s) : launch_t<TBF16>(p, grid, s);
   if (e != hipSuccess) return e;
-  const dim3 mgrid(p.plan_items);
+  const dim3 mgrid(p.plan_items * (kPrefillRows / kPrefillMergeRows));
   if (p.head_dim == 64) {
     if (act == PA_DTYPE_FLOAT16) hipLaunchKernelGGL((prefill_merge_kernel<TF16, 64>), mgrid, dim3(256), 0, s, p);
     else hipLaunchKernelGGL((prefill_merge_kernel<TBF16, 64>), mgrid, dim3(256), 0, s, p);
