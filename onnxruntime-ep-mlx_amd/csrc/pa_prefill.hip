@@ -232,9 +232,13 @@ prefill_kernel(const AttnParams p) {
   const WaveInfo w = make_wave(p, D, b, kh, s0, pastb, total);
   // This wavefront's rows and the keys they can see (steps outside are not computed).
   const int wrow0 = row0 + 16 * NG * wave;
+  // A negative softmax scale moves its sign into the query operands (attend_groups takes a
+  // scale that is not negative).
+  const uint32_t qxor = p.scale < 0.0f ? 0x80008000u : 0u;
+  const float scale = fabsf(p.scale), scale_log2 = fabsf(p.scale_log2);
   RowState<TT, D> rs[NG];
 #pragma unroll
-  for (int j = 0; j < NG; ++j) init_rows<TT, D>(rs[j], p, w, wrow0 + 16 * j, R, g, c, G);
+  for (int j = 0; j < NG; ++j) init_rows<TT, D>(rs[j], p, w, wrow0 + 16 * j, R, g, c, G, qxor);
   // Keys visible to some row [any_lo, any_hi) and to every row [all_lo, all_hi) of the wave.
   int any_lo = 0, any_hi = -1, all_lo = 0, all_hi = -1;
   if (wrow0 < R) {
@@ -268,10 +272,10 @@ prefill_kernel(const AttnParams p) {
       for (int j = 0; j < DL; ++j) vop[j] = lds[k & 1][2 * KS + j][lane];
       auto vb = [&](int n) { return __builtin_bit_cast(vec8, vop[n]); };
       if (t0 >= all_lo && t0 + 32 <= all_hi)
-        attend_groups<TT, D, CAP, false, NG>(rs, kop, vb, t0, end, G, p.scale_log2, p.scale,
+        attend_groups<TT, D, CAP, false, NG>(rs, kop, vb, t0, end, G, scale_log2, scale,
                                              p.softcap);
       else
-        attend_groups<TT, D, CAP, true, NG>(rs, kop, vb, t0, end, G, p.scale_log2, p.scale,
+        attend_groups<TT, D, CAP, true, NG>(rs, kop, vb, t0, end, G, scale_log2, scale,
                                             p.softcap);
     }
     if (k + 1 < nsteps) store_quarter<D>(lds[(k + 1) & 1], q, wave, t0 + 32, total, lane, G);

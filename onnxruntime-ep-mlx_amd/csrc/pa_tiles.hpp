@@ -159,7 +159,7 @@ struct RowState {
 // Scores of the step in log2 units (masked to -inf where not visible); returns this lane's max.
 //
 // `kop(tile, s)` returns the key operand of k-step s of tile 0 (keys t0..t0+15) or 1.
-template <typename TT, int D, bool CAP, bool SC, bool MASK, typename KeyOp>
+template <typename TT, int D, bool CAP, bool SC, bool MASK, bool FOLD = false, typename KeyOp>
 __device__ __forceinline__ float step_scores(const RowState<TT, D>& rs, KeyOp kop, int t0,
                                              int end, int G, float scale_log2, float scale,
                                              float cap, float ksA, float ksB, float (&x)[8],
@@ -175,13 +175,18 @@ __device__ __forceinline__ float step_scores(const RowState<TT, D>& rs, KeyOp ko
     sa *= ksA;
     sb *= ksB;
   }
-  // Page scales (SC) fold into the log2-domain score scale: one product per tile.
+  // Page scales (SC) fold into the log2-domain score scale: one product per tile.  FOLD (no
+  // softcap, no page scales, scale_log2 >= 0): x keeps the raw products, the scale multiplies
+  // only their maximum here and enters each exponent through one FMA in step_probs.
+  static_assert(!FOLD || (!CAP && !SC), "FOLD takes plain scaled scores");
   const float xa = SC ? ksA * scale_log2 : scale_log2, xb = SC ? ksB * scale_log2 : scale_log2;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float sv = (e < 4) ? sa[e & 3] : sb[e & 3];
     if constexpr (CAP)
       x[e] = cap * tanhf(sv * scale / cap) * kLog2e;
+    else if constexpr (FOLD)
+      x[e] = sv;
     else
       x[e] = sv * ((e < 4) ? xa : xb);
   }
@@ -200,6 +205,7 @@ __device__ __forceinline__ float step_scores(const RowState<TT, D>& rs, KeyOp ko
   float lmax = kNegInf;
 #pragma unroll
   for (int e = 0; e < 8; ++e) lmax = fmaxf(lmax, x[e]);
+  if constexpr (FOLD) lmax *= scale_log2;
   return lmax;
 }
 
@@ -232,15 +238,16 @@ __device__ __forceinline__ void rescale_rows(RowState<TT, D>& rs, float lmax, in
 // They use the hardware base-2 exponential (v_exp_f32) without the denormal-range rescaling of
 // exp2f: arguments are <= 8 (lazy max) and a probability below 2^-126 of the row maximum adds
 // nothing to an fp32 sum that holds the maximum's own 1.
-template <typename TT, int D, bool SC>
-__device__ __forceinline__ void step_probs(RowState<TT, D>& rs, const float (&x)[8], float vsA,
-                                           float vsB, typename TT::vec8& phi,
-                                           typename TT::vec8& plo8) {
+template <typename TT, int D, bool FOLD, bool SC>
+__device__ __forceinline__ void step_probs(RowState<TT, D>& rs, const float (&x)[8],
+                                           float scale_log2, float vsA, float vsB,
+                                           typename TT::vec8& phi, typename TT::vec8& plo8) {
+  // FOLD: x holds the raw scores of step_scores<..., FOLD = true>
   const float msafe = (rs.m_run == kNegInf) ? 0.0f : rs.m_run;
   float pv[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    pv[e] = __builtin_amdgcn_exp2f(x[e] - msafe);
+    pv[e] = __builtin_amdgcn_exp2f(FOLD ? __builtin_fmaf(x[e], scale_log2, -msafe) : x[e] - msafe);
     rs.l_part += pv[e];
   }
   if constexpr (SC) {
@@ -263,7 +270,7 @@ __device__ __forceinline__ void attend_step_ops(RowState<TT, D>& rs, KeyOp kop, 
                                                        cap, ksA, ksB, x, masked);
   if (__any(needs_rescale(rs, lmax))) rescale_rows(rs, lmax, G);
   vec8 phi, plo8;
-  step_probs<TT, D, SC>(rs, x, vsA, vsB, phi, plo8);
+  step_probs<TT, D, false, SC>(rs, x, scale_log2, vsA, vsB, phi, plo8);
 #pragma unroll
   for (int j = 0; j < DL; ++j) {
     const vec8 vb = vop(j);
@@ -285,6 +292,8 @@ __device__ __forceinline__ void attend_step(RowState<TT, D>& rs, const u32x4 (&k
 
 // NG row groups against the same step: all scores first, one branch for the rare rescale, then
 // every group's probabilities and PV MFMAs in one block, each value operand built once.
+// Without softcap the scale folds into the exponents (step_scores FOLD), which takes
+// scale_log2 >= 0: the caller moves the sign of a negative scale into the query operands.
 template <typename TT, int D, bool CAP, bool MASK, int NG, typename ValueOp>
 __device__ __forceinline__ void attend_groups(RowState<TT, D> (&rs)[NG],
                                               const u32x4 (&k)[2][D / 32], ValueOp vop, int t0,
@@ -297,8 +306,8 @@ __device__ __forceinline__ void attend_groups(RowState<TT, D> (&rs)[NG],
   bool any = false;
 #pragma unroll
   for (int j = 0; j < NG; ++j) {
-    lmax[j] = step_scores<TT, D, CAP, false, MASK>(rs[j], kop, t0, end, G, scale_log2, scale, cap,
-                                                   1.f, 1.f, x[j]);
+    lmax[j] = step_scores<TT, D, CAP, false, MASK, !CAP>(rs[j], kop, t0, end, G, scale_log2,
+                                                         scale, cap, 1.f, 1.f, x[j]);
     any = any || needs_rescale(rs[j], lmax[j]);
   }
   if (__any(any)) {
@@ -308,7 +317,8 @@ __device__ __forceinline__ void attend_groups(RowState<TT, D> (&rs)[NG],
   }
   vec8 phi[NG], plo[NG];
 #pragma unroll
-  for (int j = 0; j < NG; ++j) step_probs<TT, D, false>(rs[j], x[j], 1.f, 1.f, phi[j], plo[j]);
+  for (int j = 0; j < NG; ++j)
+    step_probs<TT, D, !CAP, false>(rs[j], x[j], scale_log2, 1.f, 1.f, phi[j], plo[j]);
 #pragma unroll
   for (int n = 0; n < DL; ++n) {
     const vec8 vb = vop(n);
@@ -357,11 +367,12 @@ __device__ __forceinline__ WaveInfo make_wave(const AttnParams& p, int D, int b,
 }
 
 // Rows row0 .. row0+15 of kv-head kh: this lane's MFMA column is row r = row0 + c, i.e. query
-// token r / g and head kh*g + r % g.
+// token r / g and head kh*g + r % g.  `qxor` is XORed into every query word (0x80008000 flips
+// the sign of every element).
 template <typename TT, int D>
 __device__ __forceinline__ void init_rows(RowState<TT, D>& rs, const AttnParams& p,
                                           const WaveInfo& w, int row0, int R, int g, int c,
-                                          int G) {
+                                          int G, uint32_t qxor = 0) {
   using vec8 = typename TT::vec8;
   const int r = row0 + c;
   const bool rvalid = r < R;
@@ -374,7 +385,7 @@ __device__ __forceinline__ void init_rows(RowState<TT, D>& rs, const AttnParams&
                      (((int64_t)(w.s0 + qi) * p.num_heads + h) * D + 8 * G) * 2;
 #pragma unroll
   for (int s = 0; s < D / 32; ++s) {
-    const u32x4 v = rvalid ? ld16(qrow + 64 * s) : u32x4{0, 0, 0, 0};
+    const u32x4 v = rvalid ? (ld16(qrow + 64 * s) ^ qxor) : u32x4{0, 0, 0, 0};
     rs.qv[s] = __builtin_bit_cast(vec8, v);
   }
 #pragma unroll

@@ -151,6 +151,23 @@ def test_softcap_and_sink(softcap, d):
                     head_sink=np.linspace(-1, 2, 8), std=1.0))
 
 
+# a negative softmax scale (an attribute value the reference passes through unchanged): the
+# kernels take |scale| and move the sign into the query operands -- MFMA decode, the prefill
+# kernel, the VALU kernel (d 16), softcap, and fp8 pages
+@pytest.mark.parametrize("d,dtype,cache,nq,softcap", [
+    (128, BF16, None, 1, 0.0), (128, F16, None, 40, 0.0), (16, F16, None, 3, 0.0),
+    (128, BF16, None, 1, 5.0), (128, BF16, E4M3, 1, 0.0)],
+    ids=["decode", "prefill", "valu", "softcap", "fp8"])
+def test_negative_scale(d, dtype, cache, nq, softcap):
+    rng = np.random.default_rng(d + nq)
+    B, bs = 3, 16
+    past = rng.integers(100, 900, size=B)
+    mb = int((past.max() + nq + bs - 1) // bs)
+    check(make_case(8, 2, d, B * mb + 2, bs, B, dtype=dtype, cache_dtype=cache, seed=d + nq,
+                    new_lens=[nq] * B, past=past, max_blocks=mb, std=1.0, softcap=softcap,
+                    scale=-0.11))
+
+
 # GroupQueryAttention decode, fp32, B=1, 8q/2kv, d=64, past 128 + 1 new,
 # no rotary, scale 1/8 -- the GPU paged path on the equivalent pages must agree with the
 # contiguous-KV (ORT CPU semantics) restatement to rel-L2 <= 1e-5.
