@@ -294,7 +294,8 @@ prefill_kernel(const AttnParams p) {
                         if (p.plan_items > 0)
                           return ((int64_t)item * 2 + part - 1) * ROWS + (r0 - row0) + rloc;
                         return (t * p.num_heads + oh) * p.max_splits + split;
-                      });
+                      },
+                      p.plan_items > 0);
   }
 }
 
@@ -418,7 +419,9 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(const AttnParams p) {
 
 // Merge the two halves of each split item: one workgroup per kPrefillMergeRows rows of an
 // item's row block, D/4 lanes per row; every load of the workgroup's rows is issued before the
-// first is used, so the merge costs one memory latency, not one per row pass.
+// first is used, so the merge costs one memory latency, not one per row pass.  The halves'
+// partials are fp16 rows scaled by a power of two folded into their (m, l) (store_rows with
+// half_part): the log-sum-exp merge below takes them as they are.
 constexpr int kPrefillMergeRows = 32;
 template <typename TT, int D>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnParams p) {
@@ -441,16 +444,23 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnParams p) 
   const int q = threadIdx.x % QPR;
   const int rbase = (blockIdx.x % CH) * kPrefillMergeRows + threadIdx.x / QPR;
   float2 a[NP], c[NP];
-  f32x4 oa[NP], oc[NP];
+  u32x2 ha[NP], hc[NP];  // fp16 partial rows, 4 elements per lane (store_rows, half_part)
 #pragma unroll
   for (int j = 0; j < NP; ++j) {
     const int r = min(rbase + j * RPP, rows - 1);  // clamped rows load a valid row, store nothing
     const int64_t r0 = ((int64_t)i * 2) * kPrefillRows + r, r1 = r0 + kPrefillRows;
     a[j] = reinterpret_cast<const float2*>(p.part_ml)[r0];
     c[j] = reinterpret_cast<const float2*>(p.part_ml)[r1];
-    oa[j] = reinterpret_cast<const f32x4*>(p.part_o + r0 * D)[q];
-    oc[j] = reinterpret_cast<const f32x4*>(p.part_o + r1 * D)[q];
+    ha[j] = reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(p.part_o) + r0 * D * 2)[q];
+    hc[j] = reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(p.part_o) + r1 * D * 2)[q];
   }
+  auto widen = [](u32x2 h) {
+    f32x4 f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      f[e] = (float)__builtin_bit_cast(_Float16, (uint16_t)(h[e >> 1] >> (16 * (e & 1))));
+    return f;
+  };
 #pragma unroll
   for (int j = 0; j < NP; ++j) {
     const int r = rbase + j * RPP;
@@ -463,7 +473,7 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnParams p) 
     const int64_t t = s0 + rr / g;
     const float f = finalize_factor(M, a[j].y * wa + c[j].y * wc, sink_logit<TT>(p, h));
     typename TT::raw* out = reinterpret_cast<typename TT::raw*>(p.out) + (t * p.num_heads + h) * D + 4 * q;
-    const f32x4 o = (oa[j] * wa + oc[j] * wc) * f;
+    const f32x4 o = (widen(ha[j]) * wa + widen(hc[j]) * wc) * f;
     u32x2 pk;
     pk[0] = (uint32_t)TT::from_f32(o[0]) | ((uint32_t)TT::from_f32(o[1]) << 16);
     pk[1] = (uint32_t)TT::from_f32(o[2]) | ((uint32_t)TT::from_f32(o[3]) << 16);

@@ -395,14 +395,32 @@ __device__ __forceinline__ void init_rows(RowState<TT, D>& rs, const AttnParams&
 }
 
 // Epilogue: rows 4G+i of this lane's O registers.  final: normalise (with the sink) and write
-// the output row in T; otherwise write the fp32 partial (O, m, l) at part_index(row).
+// the output row in T; otherwise write the partial (O, m, l) at part_index(row): fp32, or with
+// `half_part` fp16 rows scaled by 2^-e (e from the row's largest |O|, clamped to [-64, 100], so
+// every element fits) with e folded into the row's (m, l) as (m + e, l * 2^-e).  A log-sum-exp
+// merge over (m, l, O) gives the same result for either form: the factors 2^e cancel between
+// the weighted O and the denominator, the sink term included.
 template <typename TT, int D, typename PartIndex>
 __device__ __forceinline__ void store_rows(const RowState<TT, D>& rs, const AttnParams& p, int kh,
                                            int s0, int row0, int R, int g, int c, int G,
-                                           float sink_c, bool final, PartIndex part_index) {
+                                           float sink_c, bool final, PartIndex part_index,
+                                           bool half_part = false) {
   constexpr int DL = D / 16;
   float l_row = rs.l_part + __shfl_xor(rs.l_part, 16, 64);
   l_row += __shfl_xor(l_row, 32, 64);
+  int ex[4] = {0, 0, 0, 0};
+  if (!final && half_part) {
+    // Row 4G+i lives in the 16 lanes of group G (DL dims each): max over j, then over c.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float mx = 0.0f;
+#pragma unroll
+      for (int j = 0; j < DL; ++j) mx = fmaxf(mx, fabsf(rs.o[j][i]));
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+      ex[i] = min(max(__builtin_amdgcn_frexp_expf(mx), -64), 100);
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int rr = row0 + 4 * G + i;
@@ -428,6 +446,25 @@ __device__ __forceinline__ void store_rows(const RowState<TT, D>& rs, const Attn
       } else {
 #pragma unroll
         for (int j = 0; j < DL; ++j) dst[j] = vals[j];
+      }
+    } else if (half_part) {
+      const int64_t pi = part_index(t, oh, rr - row0);
+      uint32_t w[DL / 2];
+#pragma unroll
+      for (int m = 0; m < DL / 2; ++m) {
+        const _Float16 a = (_Float16)__builtin_ldexpf(rs.o[2 * m][i], -ex[i]);
+        const _Float16 b = (_Float16)__builtin_ldexpf(rs.o[2 * m + 1][i], -ex[i]);
+        w[m] = (uint32_t)__builtin_bit_cast(uint16_t, a) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+      }
+      char* dst = reinterpret_cast<char*>(p.part_o) + (pi * D + DL * c) * 2;
+      if constexpr (DL == 8)
+        *reinterpret_cast<u32x4*>(dst) = u32x4{w[0], w[1], w[2], w[3]};
+      else
+        *reinterpret_cast<u32x2*>(dst) = u32x2{w[0], w[1]};
+      if (c == 0) {
+        p.part_ml[pi * 2 + 0] = mi + (float)ex[i];
+        p.part_ml[pi * 2 + 1] = __builtin_ldexpf(li, -ex[i]);
       }
     } else {
       const int64_t pi = part_index(t, oh, rr - row0);

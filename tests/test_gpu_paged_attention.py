@@ -310,10 +310,13 @@ def test_prefill_kernel_level(chunk, new_rows_in_cache, bs, d, dtype, window, so
 # planned prefill (library-chosen plan with at least two workgroups per CU, 512 items here on a
 # 256-CU MI355X): units ordered longest first, items past the split threshold run as two halves
 # merged afterwards, one sequence without new tokens (no items), and a sink logit that only the
-# merge of the split items folds in for those rows
-@pytest.mark.parametrize("d,dtype,sink", [(64, BF16, False), (128, F16, True)],
-                         ids=["d64_bf16", "d128_f16_sink"])
-def test_prefill_planned(d, dtype, sink):
+# merge of the split items folds in for those rows.  The halves' partials are fp16 rows scaled
+# by a power of two per row: values far outside the fp16 range (bf16 values ~1e6) and far below
+# its normal range (~1e-6) must merge within the same bar.
+@pytest.mark.parametrize("d,dtype,sink,vstd", [(64, BF16, False, None), (128, F16, True, None),
+                                               (128, BF16, True, 1e6), (64, BF16, False, 1e-6)],
+                         ids=["d64_bf16", "d128_f16_sink", "d128_bf16_large_v", "d64_bf16_tiny_v"])
+def test_prefill_planned(d, dtype, sink, vstd):
     import torch
     import onnxruntime_ep_mlx_amd as ep
     from pa_cases import to_torch, from_torch
@@ -325,7 +328,7 @@ def test_prefill_planned(d, dtype, sink):
     past[[17, 63]] = [2600, 3500]  # items longer than the 2048-key threshold
     mb = int((past.max() + nq + bs - 1) // bs)
     case = make_case(H, KV, d, B * mb, bs, B, dtype=dtype, seed=71 + d, new_lens=new_lens,
-                     past=past, max_blocks=mb, std=1.0,
+                     past=past, max_blocks=mb, std=1.0, value_std=vstd,
                      head_sink=(rng.standard_normal(H) if sink else None))
     ref, ref_t, _, _ = orc.paged_attention_op(case)
     t = {n: to_torch(case[n], dtype) for n in ("query", "key", "value", "key_cache",
