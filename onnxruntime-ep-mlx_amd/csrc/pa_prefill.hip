@@ -303,7 +303,8 @@ prefill_kernel(const AttnParams p) {
 // Split threshold of the plan: items with more visible keys than PA_PLAN_SPLIT_PCT percent of a
 // slot's even share of all keys (and at least PA_PLAN_SPLIT_MIN keys) run as two halves.
 // C4 attention launch by threshold: 25 % 393 us, 35 % 392-395, 45 % 372-382, 60 % 391-396,
-// 80 % 388-389, 100 % 384-389.
+// 80 % 388-389, 100 % 384-389; with the fp16 partials: 30 % 354-357, 38 % 356, 45 % 340-344,
+// 55 % 342-343.
 #ifndef PA_PLAN_SPLIT_PCT
 #define PA_PLAN_SPLIT_PCT 45
 #endif
@@ -352,7 +353,10 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(const AttnParams p) {
     const ItemKeys k = item_keys(p, i);
     if (k.end >= 0) mine += (unsigned long long)(k.end - k.first);
   }
-  atomicAdd(&total_keys, mine);
+  // Wave sums first: one LDS atomic per wavefront instead of one per thread on one address.
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) mine += __shfl_xor(mine, o, 64);
+  if ((tid & 63) == 0) atomicAdd(&total_keys, mine);
   __syncthreads();
   const long long thr = max((long long)PA_PLAN_SPLIT_MIN,
                            (long long)(total_keys * PA_PLAN_SPLIT_PCT / 100) / max(p.plan_slots, 1));
