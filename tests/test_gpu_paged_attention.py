@@ -313,10 +313,13 @@ def test_prefill_kernel_level(chunk, new_rows_in_cache, bs, d, dtype, window, so
 # merge of the split items folds in for those rows.  The halves' partials are fp16 rows scaled
 # by a power of two per row: values far outside the fp16 range (bf16 values ~1e6) and far below
 # its normal range (~1e-6) must merge within the same bar.
-@pytest.mark.parametrize("d,dtype,sink,vstd", [(64, BF16, False, None), (128, F16, True, None),
-                                               (128, BF16, True, 1e6), (64, BF16, False, 1e-6)],
-                         ids=["d64_bf16", "d128_f16_sink", "d128_bf16_large_v", "d64_bf16_tiny_v"])
-def test_prefill_planned(d, dtype, sink, vstd):
+@pytest.mark.parametrize("d,dtype,sink,vstd,softcap,window", [
+    (64, BF16, False, None, 0.0, -1), (128, F16, True, None, 0.0, -1),
+    (128, BF16, True, 1e6, 0.0, -1), (64, BF16, False, 1e-6, 0.0, -1),
+    (128, BF16, True, None, 30.0, 2900)],
+    ids=["d64_bf16", "d128_f16_sink", "d128_bf16_large_v", "d64_bf16_tiny_v",
+         "d128_bf16_softcap_window"])
+def test_prefill_planned(d, dtype, sink, vstd, softcap, window):
     import torch
     import onnxruntime_ep_mlx_amd as ep
     from pa_cases import to_torch, from_torch
@@ -328,8 +331,8 @@ def test_prefill_planned(d, dtype, sink, vstd):
     past[[17, 63]] = [2600, 3500]  # items longer than the 2048-key threshold
     mb = int((past.max() + nq + bs - 1) // bs)
     case = make_case(H, KV, d, B * mb, bs, B, dtype=dtype, seed=71 + d, new_lens=new_lens,
-                     past=past, max_blocks=mb, std=1.0, value_std=vstd,
-                     head_sink=(rng.standard_normal(H) if sink else None))
+                     past=past, max_blocks=mb, std=1.0, value_std=vstd, softcap=softcap,
+                     window=window, head_sink=(rng.standard_normal(H) if sink else None))
     ref, ref_t, _, _ = orc.paged_attention_op(case)
     t = {n: to_torch(case[n], dtype) for n in ("query", "key", "value", "key_cache",
                                                "value_cache")}
@@ -339,7 +342,8 @@ def test_prefill_planned(d, dtype, sink, vstd):
     hs = to_torch(case["head_sink"], dtype) if sink else None
     outs = [ep.attention(t["query"], t["key"], t["value"], t["key_cache"], t["value_cache"],
                          I["cum"], I["past"], I["block_table"], num_heads=H, max_query_len=nq,
-                         kind=2, head_sink=hs, new_rows_in_cache=True) for _ in range(2)]
+                         kind=2, head_sink=hs, softcap=softcap, local_window_size=window,
+                         new_rows_in_cache=True) for _ in range(2)]
     torch.cuda.synchronize()
     for out in outs:
         got = orc.decode(from_torch(out, dtype), dtype)
