@@ -339,6 +339,43 @@ __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p
   }
 }
 
+// Plain append: no rotary or norm, cache in the activation dtype, paged, every token's slot
+// distinct (no last-writer rule) and every row 16-byte aligned.  One wavefront per token: the
+// key and value rows (all kv-heads, contiguous in the input and in the slot) are loaded 16
+// bytes per lane before the slot lookup resolves, then stored; up to kCopyChunks * 1 KiB per row.
+constexpr int kCopyChunks = 4;
+__global__ __launch_bounds__(256) void copy_append_kernel(const AppendParams p, int row_bytes) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= p.num_tokens) return;  // whole wavefront
+  const char* ks = reinterpret_cast<const char*>(p.key) + (int64_t)t * p.k_ld * 2;
+  const char* vs = reinterpret_cast<const char*>(p.value) + (int64_t)t * p.v_ld * 2;
+  u32x4 kr[kCopyChunks], vr[kCopyChunks];
+#pragma unroll
+  for (int i = 0; i < kCopyChunks; ++i) {
+    const int o = (i * 64 + lane) * 16;
+    if (o < row_bytes) {
+      kr[i] = *reinterpret_cast<const u32x4*>(ks + o);
+      vr[i] = *reinterpret_cast<const u32x4*>(vs + o);
+    }
+  }
+  const SeqPos sp = seq_pos_of_token(p.cum, p.past, p.batch, t);
+  const int64_t pos = (int64_t)max(sp.past, 0) + (t - sp.start);
+  int64_t slot = p.slot_mapping ? (int64_t)p.slot_mapping[t] : slot_at(p, sp.b, pos);
+  if (slot >= p.num_blocks * p.block_size) slot = -1;
+  if (slot < 0) return;
+  char* kd = reinterpret_cast<char*>(p.key_cache) + slot * row_bytes;
+  char* vd = reinterpret_cast<char*>(p.value_cache) + slot * row_bytes;
+#pragma unroll
+  for (int i = 0; i < kCopyChunks; ++i) {
+    const int o = (i * 64 + lane) * 16;
+    if (o < row_bytes) {
+      *reinterpret_cast<u32x4*>(kd + o) = kr[i];
+      *reinterpret_cast<u32x4*>(vd + o) = vr[i];
+    }
+  }
+}
+
 }  // namespace
 
 template <typename TT>
@@ -369,6 +406,19 @@ hipError_t launch_rotary_append(const AppendParams& p, pa_dtype act, pa_dtype ca
   if (cache_dtype != act && cache_dtype != PA_DTYPE_FP8_E4M3 && cache_dtype != PA_DTYPE_INT8 &&
       cache_dtype != PA_DTYPE_INT4)
     return hipErrorInvalidValue;
+  if (cache_dtype == act && act != PA_DTYPE_FLOAT32 && !transform && p.linear_cap <= 0 &&
+      p.slots_distinct && p.key && p.value && p.key_cache && p.value_cache && !p.v_out) {
+    // 16-bit elements: every row start (input stride, slot stride) must be 16-byte aligned.
+    const int64_t row_bytes = (int64_t)p.kv_heads * p.head_dim * 2;
+    const uintptr_t align = (uintptr_t)p.key | (uintptr_t)p.value | (uintptr_t)p.key_cache |
+                            (uintptr_t)p.value_cache | (uintptr_t)(p.k_ld * 2) |
+                            (uintptr_t)(p.v_ld * 2) | (uintptr_t)row_bytes;
+    if ((align & 15) == 0 && row_bytes <= kCopyChunks * 64 * 16) {
+      hipLaunchKernelGGL(copy_append_kernel, dim3((p.num_tokens + 3) / 4), dim3(256), 0, s, p,
+                         (int)row_bytes);
+      return hipGetLastError();
+    }
+  }
   switch (act) {
     case PA_DTYPE_FLOAT16: launch_append_t<TF16>(p, cache_dtype, grid, block, s); break;
     case PA_DTYPE_BFLOAT16: launch_append_t<TBF16>(p, cache_dtype, grid, block, s); break;
