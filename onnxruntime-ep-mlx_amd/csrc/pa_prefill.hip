@@ -159,7 +159,8 @@ __device__ __forceinline__ void store_quarter(u32x4 (*buf)[64], Quarter<D>& q, i
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
         const uint32_t lo = q.vword(2 * m, j >> 1), hi = q.vword(2 * m + 1, j >> 1);
-        half[m] = (j & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+        // one byte permute: the low (even j) or high (odd j) halves of the two rows
+        half[m] = __builtin_amdgcn_perm(hi, lo, (j & 1) ? 0x07060302u : 0x05040100u);
       }
       reinterpret_cast<u32x2*>(&buf[2 * KS + j][lane])[T] = half;
     }
