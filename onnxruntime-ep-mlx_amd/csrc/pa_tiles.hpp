@@ -396,8 +396,9 @@ __device__ __forceinline__ void init_rows(RowState<TT, D>& rs, const AttnParams&
 
 // Epilogue: rows 4G+i of this lane's O registers.  final: normalise (with the sink) and write
 // the output row in T; otherwise write the partial (O, m, l) at part_index(row): fp32, or with
-// `half_part` fp16 rows scaled by 2^-e (e from the row's largest |O|, clamped to [-64, 100], so
-// every element fits) with e folded into the row's (m, l) as (m + e, l * 2^-e).  A log-sum-exp
+// `half_part` fp16 rows scaled by 2^-e (e from the row's largest |O|, clamped to [-64, 126]: every
+// element of a finite fp32 row fits, and l * 2^-e stays a normal float since l >= 1 for a row
+// with any visible key) with e folded into the row's (m, l) as (m + e, l * 2^-e).  A log-sum-exp
 // merge over (m, l, O) gives the same result for either form: the factors 2^e cancel between
 // the weighted O and the denominator, the sink term included.
 template <typename TT, int D, typename PartIndex>
@@ -418,7 +419,7 @@ __device__ __forceinline__ void store_rows(const RowState<TT, D>& rs, const Attn
       for (int j = 0; j < DL; ++j) mx = fmaxf(mx, fabsf(rs.o[j][i]));
 #pragma unroll
       for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-      ex[i] = min(max(__builtin_amdgcn_frexp_expf(mx), -64), 100);
+      ex[i] = min(max(__builtin_amdgcn_frexp_expf(mx), -64), 126);
     }
   }
 #pragma unroll
