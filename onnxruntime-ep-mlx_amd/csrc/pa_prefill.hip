@@ -423,14 +423,14 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(const AttnParams p) {
 }
 
 // Merge the two halves of each split item: one workgroup per kPrefillMergeRows rows of an
-// item's row block, D/4 lanes per row; every load of the workgroup's rows is issued before the
-// first is used, so the merge costs one memory latency, not one per row pass.  The halves'
+// item's row block, D/8 lanes per row (16 bytes of fp16 each); every load of the workgroup is
+// issued before the first is used, so the merge costs one memory latency after the split flag.  The halves'
 // partials are fp16 rows scaled by a power of two folded into their (m, l) (store_rows with
 // half_part): the log-sum-exp merge below takes them as they are.
 constexpr int kPrefillMergeRows = 32;
 template <typename TT, int D>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnParams p) {
-  constexpr int QPR = D / 4;              // float4 quads per row
+  constexpr int QPR = D / 8;              // lanes per row, 8 elements (16 bytes of fp16) each
   constexpr int RPP = 256 / QPR;          // rows per pass
   constexpr int NP = kPrefillMergeRows / RPP;
   static_assert(kPrefillRows % kPrefillMergeRows == 0 && kPrefillMergeRows % RPP == 0, "merge tiling");
@@ -440,31 +440,30 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnParams p) 
   const int g = p.num_heads / p.kv_heads;
   const int kh = i % p.kv_heads, rb = (i / p.kv_heads) % p.plan_rbs;
   const int b = i / (p.kv_heads * p.plan_rbs);
-  const int s0 = min(max(p.cum[b], 0), p.num_tokens);
-  const int s1 = min(max(p.cum[b + 1], s0), p.num_tokens);
-  const int R = g * (s1 - s0);
   const int row0 = rb * kPrefillRows;
-  const int rows = min(kPrefillRows, R - row0);
-  if ((blockIdx.x % CH) * kPrefillMergeRows >= rows) return;
   const int q = threadIdx.x % QPR;
   const int rbase = (blockIdx.x % CH) * kPrefillMergeRows + threadIdx.x / QPR;
+  // Every load in one round trip: the sequence bounds, both halves' (m, l) and rows, the sink.
+  // Rows past the block's last row read in-bounds workspace rows and store nothing.
+  const int cb0 = p.cum[b], cb1 = p.cum[b + 1];
   float2 a[NP], c[NP];
-  u32x2 ha[NP], hc[NP];  // fp16 partial rows, 4 elements per lane (store_rows, half_part)
+  u32x4 ha[NP], hc[NP];  // fp16 partial rows (store_rows, half_part)
+  float sk[NP];
 #pragma unroll
   for (int j = 0; j < NP; ++j) {
-    const int r = min(rbase + j * RPP, rows - 1);  // clamped rows load a valid row, store nothing
+    const int r = rbase + j * RPP;
     const int64_t r0 = ((int64_t)i * 2) * kPrefillRows + r, r1 = r0 + kPrefillRows;
     a[j] = reinterpret_cast<const float2*>(p.part_ml)[r0];
     c[j] = reinterpret_cast<const float2*>(p.part_ml)[r1];
-    ha[j] = reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(p.part_o) + r0 * D * 2)[q];
-    hc[j] = reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(p.part_o) + r1 * D * 2)[q];
+    ha[j] = reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(p.part_o) + r0 * D * 2)[q];
+    hc[j] = reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(p.part_o) + r1 * D * 2)[q];
+    sk[j] = sink_logit<TT>(p, kh * g + (row0 + r) % g);
   }
-  auto widen = [](u32x2 h) {
-    f32x4 f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      f[e] = (float)__builtin_bit_cast(_Float16, (uint16_t)(h[e >> 1] >> (16 * (e & 1))));
-    return f;
+  const int s0 = min(max(cb0, 0), p.num_tokens);
+  const int s1 = min(max(cb1, s0), p.num_tokens);
+  const int rows = min(kPrefillRows, g * (s1 - s0) - row0);
+  auto widen = [](uint32_t w2, int e) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w2 >> (16 * e)));
   };
 #pragma unroll
   for (int j = 0; j < NP; ++j) {
@@ -476,13 +475,16 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnParams p) 
     const int rr = row0 + r;
     const int h = kh * g + rr % g;
     const int64_t t = s0 + rr / g;
-    const float f = finalize_factor(M, a[j].y * wa + c[j].y * wc, sink_logit<TT>(p, h));
-    typename TT::raw* out = reinterpret_cast<typename TT::raw*>(p.out) + (t * p.num_heads + h) * D + 4 * q;
-    const f32x4 o = (widen(ha[j]) * wa + widen(hc[j]) * wc) * f;
-    u32x2 pk;
-    pk[0] = (uint32_t)TT::from_f32(o[0]) | ((uint32_t)TT::from_f32(o[1]) << 16);
-    pk[1] = (uint32_t)TT::from_f32(o[2]) | ((uint32_t)TT::from_f32(o[3]) << 16);
-    *reinterpret_cast<u32x2*>(out) = pk;
+    const float f = finalize_factor(M, a[j].y * wa + c[j].y * wc, sk[j]);
+    u32x4 pk;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const float lo = (widen(ha[j][m], 0) * wa + widen(hc[j][m], 0) * wc) * f;
+      const float hi = (widen(ha[j][m], 1) * wa + widen(hc[j][m], 1) * wc) * f;
+      pk[m] = (uint32_t)TT::from_f32(lo) | ((uint32_t)TT::from_f32(hi) << 16);
+    }
+    *reinterpret_cast<u32x4*>(reinterpret_cast<typename TT::raw*>(p.out) +
+                              (t * p.num_heads + h) * D + 8 * q) = pk;
   }
 }
 
