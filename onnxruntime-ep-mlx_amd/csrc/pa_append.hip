@@ -50,6 +50,71 @@ __device__ __forceinline__ int64_t token_slot_lane(const AppendParams& p, int u)
   return slot_at(p, b, (int64_t)max(p.past[b], 0) + (u - p.cum[b]));
 }
 
+// Last-writer rule without a slot mapping: whether a later token writes `slot` (block blk =
+// slot / bs, offset slot % bs) of token position `pos` in sequence b.  A later token u can only
+// be a new position of sequence b (after pos) or of a later sequence whose block-table entry
+// for u's block is blk, at offset slot % bs of that block -- so the workgroup scans the
+// block-table entries that cover the new positions of sequences b.. (O(T / bs + B) per token)
+// instead of every later token.  Called by the whole workgroup (256 threads).
+__device__ bool later_block_dup(const AppendParams& p, int b, int64_t pos, int64_t slot) {
+  constexpr int NT = 256;
+  __shared__ int pre[NT + 1];   // prefix of block-entry counts over a chunk of sequences
+  __shared__ int k0s[NT];       // first block index of each sequence's new positions
+  __shared__ int64_t ps_s[NT];  // first new position (past, clamped at 0)
+  __shared__ int n_s[NT];       // new-token count
+  __shared__ int wsum[NT / 64];
+  const int tid = threadIdx.x;
+  const int64_t bs = p.block_size;
+  const int64_t blk = slot / bs, off = slot % bs;
+  bool dup = false;
+  for (int base = b; base < p.batch; base += NT) {
+    const int sq = base + tid;
+    int k0 = 0, nk = 0, n = 0;
+    int64_t ps = 0;
+    if (sq < p.batch) {
+      n = p.cum[sq + 1] - p.cum[sq];
+      ps = (int64_t)max(p.past[sq], 0);
+      if (n > 0) {
+        const int64_t k1 = min((ps + n - 1) / bs, (int64_t)p.max_blocks - 1);
+        k0 = (int)min(ps / bs, (int64_t)p.max_blocks);
+        nk = k1 >= k0 ? (int)(k1 - k0 + 1) : 0;
+      }
+    }
+    k0s[tid] = k0;
+    ps_s[tid] = ps;
+    n_s[tid] = n;
+    // Inclusive scan of nk: wave scans, then the totals of the earlier wavefronts.
+    int x = nk;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if ((tid & 63) >= o) x += y;
+    }
+    if ((tid & 63) == 63) wsum[tid >> 6] = x;
+    __syncthreads();
+    for (int w = 0; w < (tid >> 6); ++w) x += wsum[w];
+    pre[tid + 1] = x;
+    if (tid == 0) pre[0] = 0;
+    __syncthreads();
+    const int total = pre[NT];
+    for (int j = tid; j < total; j += NT) {
+      int lo = 0, hi = NT - 1;  // sequence i of entry j: pre[i] <= j < pre[i + 1]
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (pre[mid] <= j) lo = mid; else hi = mid - 1;
+      }
+      const int sq2 = base + lo;
+      const int k = k0s[lo] + (j - pre[lo]);
+      if ((int64_t)p.block_table[(int64_t)sq2 * p.max_blocks + k] == blk) {
+        const int64_t pp = (int64_t)k * bs + off;
+        if (pp >= ps_s[lo] && pp < ps_s[lo] + n_s[lo] && (sq2 > b || pp > pos)) dup = true;
+      }
+    }
+    __syncthreads();  // the next chunk rewrites the tables
+  }
+  return __syncthreads_or(dup);
+}
+
 // Normalise + rotate one head row in place of `dst` (reads from src).  Executed by one wave.
 // Destinations: dst/dst2 receive the row in T (either may be null); q8 (may be null) receives
 // the fp8 code e4m3_sat(x / q8_scale), zero scale -> 0.
@@ -233,8 +298,12 @@ __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p
   if (!linear && slot >= p.num_blocks * p.block_size) slot = -1;
   bool later_dup = false;
   if (slot >= 0 && !p.slots_distinct && !linear) {
-    for (int u = t + 1 + threadIdx.x; u < p.num_tokens; u += blockDim.x)
-      if (token_slot_lane(p, u) == slot) later_dup = true;
+    if (p.slot_mapping) {
+      for (int u = t + 1 + threadIdx.x; u < p.num_tokens; u += blockDim.x)
+        if ((int64_t)p.slot_mapping[u] == slot) later_dup = true;
+    } else {
+      later_dup = later_block_dup(p, seq_b, pos, slot);
+    }
   }
   const bool write_cache = slot >= 0 && !__syncthreads_or(later_dup);
 

@@ -118,6 +118,19 @@ def test_duplicate_slots_known_answer():
     check(case)
 
 
+# duplicate slots through the block table (no slot mapping): sequence 2's new positions land on
+# the block sequence 0 writes, at overlapping offsets, and sequence 1's row names one block twice,
+# so its later positions overwrite its earlier ones.  The last writer in token order must win
+# (sequential scatter); the host metadata shows the slots are not distinct, so the append runs
+# its block-table last-writer check.
+@pytest.mark.parametrize("dtype", [F16, BF16], ids=["fp16", "bf16"])
+def test_block_table_duplicate_slots(dtype):
+    case = make_case(4, 2, 64, 12, 16, 3, dtype=dtype, seed=91, new_lens=[5, 20, 7],
+                     past=[3, 10, 3], max_blocks=4, std=1.0)
+    case["block_table"] = np.array([[0, 1, 2, 3], [4, 4, 5, 6], [0, 8, 9, 10]], np.int32)
+    check(case)
+
+
 # test_paged_attention.py:663-666 (RoPE neox / gptj) + the BASELINE.json bf16 theta=500000 rotary
 @pytest.mark.parametrize("interleaved", [0, 1], ids=["neox", "gptj"])
 @pytest.mark.parametrize("H,KV,d,dtype", [(4, 2, 16, F16), (2, 1, 64, F16), (32, 8, 128, BF16)])
