@@ -187,16 +187,20 @@ size_t pa_attention_workspace_bytes_ex(const pa_cache* cache, const pa_batch* ba
  * likewise.
  * Dispatch: fp16/bf16 with head_dim 64 or 128 run on matrix cores: the balanced (stream-K)
  * decode kernel when (num_heads/kv_heads) * max_query_len <= 16 and the block size is a power
- * of two, else the chunked split-K kernel in 16-row groups (multi-token prefill chunks);
- * fp32 activations, other head sizes and integer pages use the VALU kernel. */
+ * of two (fp8 pages too); otherwise, with cache dtype = T, the LDS-shared prefill kernel
+ * (128 grouped query rows per workgroup; planned longest-first units with split halves once the
+ * batch has at least two row blocks per compute unit); fp32 activations, other head sizes and
+ * integer pages use the VALU kernel.  batch->max_query_len = 0 is read as num_tokens. */
 int pa_attention(const pa_cache* cache, const pa_batch* batch, const pa_attn* attn,
                  pa_dtype act_dtype, const void* q, const void* k_new, const void* v_new,
                  void* out, void* workspace, size_t workspace_bytes, pa_stream_t stream);
 
 /* Same contract, forcing one kernel family (for parity tests and benchmarks).
  * kind: 0 = automatic, 1 = decode MFMA (balanced segments when every sequence has at most 16
- * grouped query rows, else chunked split-K), 2 = dedicated prefill kernel (not in this build:
- * returns PA_ERR_UNSUPPORTED), 3 = generic VALU, 4 = decode MFMA with chunked split-K forced.
+ * grouped query rows, else chunked split-K), 2 = LDS-shared prefill kernel (planned launch when
+ * the batch fills the GPU and chunk_tokens is 0, else split-K chunks), 3 = generic VALU,
+ * 4 = decode MFMA with chunked split-K forced.  A kind that does not cover the dtype / head size
+ * returns PA_ERR_UNSUPPORTED.
  * chunk_tokens: split-K chunk for the chunked/generic kernels (multiple of 32; 0 = automatic). */
 int pa_attention_ex(const pa_cache* cache, const pa_batch* batch, const pa_attn* attn,
                     pa_dtype act_dtype, const void* q, const void* k_new, const void* v_new,
@@ -256,8 +260,26 @@ typedef struct pa_paged_attention_io {
   const int32_t* host_block_table;
   const int32_t* host_slot_mapping;
   void* output;                /* output 0 */
+  /* Outputs 1/2 (key_cache_out / value_cache_out).  The input caches are always updated in
+   * place.  NULL (output omitted) or the input cache's own address (the output bound onto the
+   * input, ORT's shared-buffer binding): nothing more is written.  A distinct buffer of the
+   * cache's shape and dtype receives a copy of the whole updated cache (engine.rs:110-126
+   * full-copy path, attention.rs:4336-4380).  value_cache_out must be NULL for LATENT. */
+  void* key_cache_out;
+  void* value_cache_out;
+  /* Host-known bound on the new tokens of any one sequence (max of cum[b+1] - cum[b]); 0 =
+   * unknown.  It selects the kernel family and sizes the workspace without a device read.
+   * With host_cumulative_sequence_length it must be >= the largest query length there (else
+   * PA_ERR_INVALID_ARGUMENT); without it the caller guarantees the bound, and query rows beyond
+   * it are left unwritten (no access outside the buffers).  0 without host metadata: the bound
+   * is num_tokens. */
+  int32_t max_query_len;
 } pa_paged_attention_io;
 
+/* Workspace bytes for one call.  The size depends on the shapes (num_tokens, batch,
+ * max_blocks, heads, head size, dtypes, block size) and on the query-length bound (io's
+ * max_query_len, else the host cumulative lengths, else num_tokens); a caller that always passes
+ * the same max_query_len (its largest chunk) may size the workspace once per shape. */
 size_t pa_paged_attention_workspace_bytes(const pa_paged_attention_node* node,
                                           const pa_paged_attention_io* io);
 int pa_paged_attention(const pa_paged_attention_node* node, const pa_paged_attention_io* io,

@@ -252,12 +252,18 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
   return pl;
 }
 
-// Workspace: [partial O (fp32) | partial (m, l)].
+// Bytes of the partial rows: fp32 elements, except the planned prefill's halves, which are
+// stored as fp16 rows scaled by a power of two (store_rows with half_part).
+size_t part_o_bytes(const pa_cache* c, const Plan& pl) {
+  const size_t es = pl.plan_items > 0 ? 2 : sizeof(float);
+  return align256(pl.part_rows * c->head_dim * es);
+}
+
+// Workspace: [partial O | partial (m, l)].
 // Planned prefill adds [unit list (2 per item, 4 int32 each) | unit count | split flag per item].
 size_t workspace_for(const pa_cache* c, const pa_batch*, const pa_attn*, const Plan& pl) {
   if (pl.part_rows == 0) return 0;
-  size_t n = align256(pl.part_rows * c->head_dim * sizeof(float)) +
-             align256(pl.part_rows * 2 * sizeof(float));
+  size_t n = part_o_bytes(c, pl) + align256(pl.part_rows * 2 * sizeof(float));
   if (pl.plan_items > 0)
     n += align256((size_t)pl.plan_items * 2 * 4 * sizeof(int32_t)) + 256 +
          align256((size_t)pl.plan_items * sizeof(int32_t));
@@ -328,11 +334,10 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
   p.head_sink = a->head_sink;
   p.out = out;
   p.part_o = need ? reinterpret_cast<float*>(ws) : nullptr;
-  p.part_ml = need ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) +
-                                              align256(pl.part_rows * c->head_dim * sizeof(float)))
+  p.part_ml = need ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + part_o_bytes(c, pl))
                    : nullptr;
   if (pl.plan_items > 0) {
-    char* base = reinterpret_cast<char*>(ws) + align256(pl.part_rows * c->head_dim * sizeof(float)) +
+    char* base = reinterpret_cast<char*>(ws) + part_o_bytes(c, pl) +
                  align256(pl.part_rows * 2 * sizeof(float));
     p.plan = reinterpret_cast<int32_t*>(base);
     base += align256((size_t)pl.plan_items * 2 * 4 * sizeof(int32_t));
@@ -666,15 +671,19 @@ int op_layout(const pa_paged_attention_node* n, const pa_paged_attention_io* io,
   b.batch = io->batch;
   b.max_blocks = io->max_blocks;
   b.num_tokens = io->num_tokens;
-  b.max_query_len = 0;
   b.flags = 0;
-  if (io->host_cumulative_sequence_length) {
+  // Query-length bound: the caller's, else the host cumulative lengths, else num_tokens.
+  if (io->max_query_len < 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "max_query_len must be non-negative");
+  b.max_query_len = std::min(io->max_query_len, std::max(io->num_tokens, 1));
+  if (b.max_query_len == 0 && io->host_cumulative_sequence_length) {
     int mq = 0;
     for (int i = 0; i < io->batch; ++i)
       mq = std::max(mq, io->host_cumulative_sequence_length[i + 1] -
                             io->host_cumulative_sequence_length[i]);
     b.max_query_len = std::max(mq, 1);
   }
+  if (b.max_query_len == 0) b.max_query_len = std::max(io->num_tokens, 1);
   pa_attn& a = L->attn;
   a.num_heads = n->num_heads;
   a.scale = n->scale;
@@ -705,6 +714,12 @@ int validate_host_metadata(const pa_paged_attention_node* n, const pa_paged_atte
   if (bad)
     return fail(PA_ERR_INVALID_ARGUMENT,
                 "PagedAttention: inconsistent cumulative lengths, past lengths or block table");
+  if (io->max_query_len > 0)
+    for (int i = 0; i < B; ++i)
+      if (cum[i + 1] - cum[i] > io->max_query_len)
+        return fail(PA_ERR_INVALID_ARGUMENT,
+                    "PagedAttention: a sequence has more new tokens (%d) than max_query_len (%d)",
+                    cum[i + 1] - cum[i], io->max_query_len);
   const int64_t nb = io->cache.num_blocks, bs = io->cache.block_size;
   if (io->slot_mapping) {
     const int32_t* sm = io->host_slot_mapping;
@@ -759,6 +774,36 @@ bool host_slots_distinct(const pa_paged_attention_io* io) {
 
 }  // namespace
 
+namespace {
+
+// Bytes of one side of the paged cache ([num_blocks, block_size, kv_heads, row bytes]).
+size_t cache_side_bytes(const pa_cache& c) {
+  return (size_t)c.num_blocks * c.block_size * c.kv_heads * cache_head_bytes(c.dtype, c.head_dim);
+}
+
+// Outputs 1/2 bound to buffers of their own receive the updated caches (the input caches were
+// updated in place; an output bound onto its input needs nothing more).
+int check_cache_outputs(const pa_paged_attention_node* n, const pa_paged_attention_io* io) {
+  if (n->kv_cache_layout_latent && io->value_cache_out)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "PagedAttention: LATENT layout has no separate value cache output");
+  return PA_OK;
+}
+
+int copy_cache_outputs(const pa_paged_attention_io* io, hipStream_t s) {
+  const size_t bytes = cache_side_bytes(io->cache);
+  const void* src[2] = {io->cache.key_cache, io->cache.value_cache};
+  void* dst[2] = {io->key_cache_out, io->value_cache_out};
+  for (int i = 0; i < 2; ++i) {
+    if (!dst[i] || dst[i] == src[i] || !src[i]) continue;
+    hipError_t e = hipMemcpyAsync(dst[i], src[i], bytes, hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) return hip_fail(e, "cache output copy");
+  }
+  return PA_OK;
+}
+
+}  // namespace
+
 size_t pa_paged_attention_workspace_bytes(const pa_paged_attention_node* node,
                                           const pa_paged_attention_io* io) {
   OpLayout L;
@@ -782,7 +827,8 @@ int pa_paged_attention(const pa_paged_attention_node* n, const pa_paged_attentio
   if (workspace_bytes < L.total || (L.total && !workspace))
     return fail(PA_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes, got %zu",
                 L.total, workspace_bytes);
-  if (io->num_tokens == 0) return PA_OK;
+  if ((rc = check_cache_outputs(n, io))) return rc;
+  if (io->num_tokens == 0) return copy_cache_outputs(io, s);
   char* ws = reinterpret_cast<char*>(workspace);
   void* q_rot = L.transform ? ws : nullptr;
   void* k_rot = L.transform ? ws + L.q_bytes : nullptr;
@@ -813,8 +859,10 @@ int pa_paged_attention(const pa_paged_attention_node* n, const pa_paged_attentio
   const void* q = L.transform ? q_rot : io->query;
   const void* kn = L.transform ? k_rot : key;
   const void* vn = L.packed ? v_rows : value;
-  return run_attention(&io->cache, &L.batch, &L.attn, io->dtype, q, kn, vn, io->output,
-                       ws + L.attn_off, workspace_bytes - L.attn_off, 0, 0, s, opts);
+  rc = run_attention(&io->cache, &L.batch, &L.attn, io->dtype, q, kn, vn, io->output,
+                     ws + L.attn_off, workspace_bytes - L.attn_off, 0, 0, s, opts);
+  if (rc) return rc;
+  return copy_cache_outputs(io, s);
 }
 
 // ------------------------------------------------------------------------------ GQA

@@ -225,7 +225,7 @@ decode_chunked_kernel(const AttnParams p) {
   const int s1 = min(max(p.cum[b + 1], s0), p.num_tokens);
   const int nq = s1 - s0;
   if (nq <= 0) return;
-  const int pastb = max(p.past[b], 0);
+  const int pastb = clamped_past(p, b, nq);
   const int total = pastb + nq;
   const int start = split * p.chunk;
   if (start >= total) return;

@@ -206,7 +206,7 @@ prefill_kernel(const AttnParams p) {
   const int R = g * nq;
   const int row0 = rb * ROWS;
   if (row0 >= R) return;
-  const int pastb = max(p.past[b], 0);
+  const int pastb = clamped_past(p, b, nq);
   const int total = pastb + nq;
   int start, end;
   bool single;
@@ -325,7 +325,7 @@ __device__ __forceinline__ ItemKeys item_keys(const AttnParams& p, int i) {
   const int R = g * (s1 - s0);
   const int row0 = rb * kPrefillRows;
   if (row0 >= R) return ItemKeys{0, -1};
-  const int pastb = max(p.past[b], 0);
+  const int pastb = clamped_past(p, b, s1 - s0);
   const int total = pastb + (s1 - s0);
   const int r_last = min(row0 + kPrefillRows, R) - 1;
   const int hi = p.causal ? pastb + r_last / g + 1 : total;

@@ -342,6 +342,16 @@ __device__ __forceinline__ void compute_step(RowState<TT, D>& rs, const Step<D>&
       scale, cap, ksA, ksB, vsA, vsB, masked);
 }
 
+// Past length of sequence b, clamped so that past + nq stays within the cache capacity.  The host
+// rejects such metadata when it validates; trusted device metadata then cannot push 32-bit key
+// positions past the capacity (or overflow them), and valid metadata is unchanged.
+__device__ __forceinline__ int clamped_past(const AttnParams& p, int b, int nq) {
+  const int cap = p.linear_cap > 0
+                      ? p.linear_cap
+                      : (int)min((int64_t)p.max_blocks * p.block_size, (int64_t)(INT32_MAX / 2));
+  return min(max(p.past[b], 0), max(cap - nq, 0));
+}
+
 __device__ __forceinline__ WaveInfo make_wave(const AttnParams& p, int D, int b, int kh, int s0,
                                               int pastb, int total) {
   WaveInfo w;

@@ -103,7 +103,8 @@ class PaIO(C.Structure):
         ("q_norm_weight", C.c_void_p), ("k_norm_weight", C.c_void_p),
         ("host_cumulative_sequence_length", C.c_void_p), ("host_past_seqlens", C.c_void_p),
         ("host_block_table", C.c_void_p), ("host_slot_mapping", C.c_void_p),
-        ("output", C.c_void_p),
+        ("output", C.c_void_p), ("key_cache_out", C.c_void_p), ("value_cache_out", C.c_void_p),
+        ("max_query_len", C.c_int32),
     ]
 
 

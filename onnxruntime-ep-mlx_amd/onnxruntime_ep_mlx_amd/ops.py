@@ -266,7 +266,8 @@ def paged_attention(query, key, value, key_cache, value_cache, cumulative_sequen
                     kv_num_heads, scale=0.0, softcap=0.0, local_window_size=-1, do_rotary=0,
                     rotary_interleaved=0, rotary_offset=0, is_causal=1, qk_norm_epsilon=1e-6,
                     k_quant_type="NONE", v_quant_type="NONE", v_head_size=0,
-                    kv_cache_layout="SEPARATE", validate=True, output=None):
+                    kv_cache_layout="SEPARATE", validate=True, output=None,
+                    key_cache_out=None, value_cache_out=None, max_query_len=0):
     """com.microsoft::PagedAttention on MI355X (operator-level entry, pa_paged_attention).
 
     ``attention_metadata`` is accepted and ignored, like the reference
@@ -279,6 +280,11 @@ def paged_attention(query, key, value, key_cache, value_cache, cumulative_sequen
     ``kv_cache_layout="LATENT"``: one kv head, ``value`` and ``value_cache`` None; the values are
     the first ``v_head_size`` dims of the (rotated) key rows and the output is
     [T, num_heads * v_head_size].
+    Outputs 1/2: the input caches are always updated in place; ``key_cache_out`` /
+    ``value_cache_out`` given as tensors of their own receive a copy of the updated caches
+    (outputs bound onto the inputs need nothing), and are returned in place of the inputs.
+    ``max_query_len`` (0 = derive it) bounds every sequence's new tokens: it picks the kernel
+    family without a device read when ``validate`` is False.
     """
     if kv_cache_layout not in ("SEPARATE", "LATENT"):
         raise ValueError("kv_cache_layout must be SEPARATE or LATENT")
@@ -288,9 +294,15 @@ def paged_attention(query, key, value, key_cache, value_cache, cumulative_sequen
     if query.dim() != 2:
         raise ValueError("query must have rank 2")
     for n, t in (("query", query), ("key", key), ("value", value), ("key_cache", key_cache),
-                 ("value_cache", value_cache)):
+                 ("value_cache", value_cache), ("key_cache_out", key_cache_out),
+                 ("value_cache_out", value_cache_out)):
         _need_cuda(n, t)
         _contig(n, t)
+    for n, out_t, in_t in (("key_cache_out", key_cache_out, key_cache),
+                           ("value_cache_out", value_cache_out, value_cache)):
+        if out_t is not None and (in_t is None or out_t.shape != in_t.shape
+                                  or out_t.dtype != in_t.dtype):
+            raise ValueError(f"PagedAttention: {n} must match its cache's shape and dtype")
     packed = not latent and key is None and value is None
     head = query.shape[1] // (num_heads + 2 * kv_num_heads if packed else num_heads)
     v_head = v_head_size or head
@@ -315,12 +327,14 @@ def paged_attention(query, key, value, key_cache, value_cache, cumulative_sequen
         cos_cache.shape[1] if (do_rotary and cos_cache is not None) else 0,
         _ptr(slot_mapping), _ptr(head_sink), _ptr(q_norm_weight), _ptr(k_norm_weight),
         _ptr(host.get("cum")), _ptr(host.get("past")), _ptr(host.get("bt")),
-        _ptr(host.get("slots")), _ptr(output))
+        _ptr(host.get("slots")), _ptr(output), _ptr(key_cache_out), _ptr(value_cache_out),
+        max_query_len)
     nbytes = lib.pa_paged_attention_workspace_bytes(C.byref(node), C.byref(io))
     ws = _ws.get(nbytes, query.device)
     capi.check(lib.pa_paged_attention(C.byref(node), C.byref(io), _ptr(ws), nbytes,
                                       _stream(query.device)))
-    return output, key_cache, value_cache
+    return (output, key_cache if key_cache_out is None else key_cache_out,
+            value_cache if value_cache_out is None else value_cache_out)
 
 
 def group_query_attention(query, key, value, present_key, present_value, seqlens_k,

@@ -364,23 +364,26 @@ int orc_paged_attention(const void* q, const void* k_new, const void* v_new, int
   int width = cache_width(cache_dtype, d);
   int64_t crow = (int64_t)kv_heads * width;
   int quant = cache_dtype == ORC_E4M3 || is_int_dt(cache_dtype);
-  double* scores = NULL;
-  size_t cap = 0;
+  int failed = 0;
   for (int b = 0; b < batch; ++b) {
     int s0 = cum[b], nq = cum[b + 1] - cum[b];
     if (nq <= 0) continue;
     int64_t pastb = past[b], total = pastb + nq;
-    if ((size_t)total > cap) {
-      cap = (size_t)total;
-      free(scores);
-      scores = (double*)malloc(cap * sizeof(double));
-      if (!scores) return 4;
-    }
+    /* Every (query row, head) pair is computed on its own, in the same sequential order
+     * whichever thread takes it, so the results do not depend on the thread count. */
+#pragma omp parallel reduction(| : failed)
+    {
+      double* scores = (double*)malloc((size_t)total * sizeof(double));
+      double* qrow = (double*)malloc((size_t)d * sizeof(double));
+      if (!scores || !qrow) failed = 1;
+#pragma omp for collapse(2) schedule(dynamic, 1)
     for (int i = 0; i < nq; ++i) {
-      int64_t t = s0 + i, rp = pastb + i;
       for (int h = 0; h < num_heads; ++h) {
+        if (!scores || !qrow) continue;
+        int64_t t = s0 + i, rp = pastb + i;
         int kh = h / g;
         const int64_t qbase = (t * num_heads + h) * (int64_t)d;
+        for (int e = 0; e < d; ++e) qrow[e] = (double)ld(q, qbase + e, act_dtype);
         double m = -INFINITY;
         for (int64_t p = 0; p < total; ++p) {
           int visible = (!causal || p <= rp) && (window <= 0 || p >= rp - window + 1);
@@ -393,13 +396,11 @@ int orc_paged_attention(const void* q, const void* k_new, const void* v_new, int
             int64_t blk = block_table[(int64_t)b * max_blocks + p / block_size];
             int64_t base = (blk * block_size + p % block_size) * crow + (int64_t)kh * width;
             for (int e = 0; e < d; ++e)
-              dot += (double)ld(q, qbase + e, act_dtype) *
-                     cache_elem(key_cache, cache_dtype, k_scale, k_mode, blk, kv_heads, kh, d,
-                                base, e);
+              dot += qrow[e] * cache_elem(key_cache, cache_dtype, k_scale, k_mode, blk,
+                                          kv_heads, kh, d, base, e);
           } else {
             int64_t base = (s0 + (p - pastb)) * row + (int64_t)kh * d;
-            for (int e = 0; e < d; ++e)
-              dot += (double)ld(q, qbase + e, act_dtype) * (double)ld(k_new, base + e, act_dtype);
+            for (int e = 0; e < d; ++e) dot += qrow[e] * (double)ld(k_new, base + e, act_dtype);
           }
           double s = (double)scale * dot;
           if (softcap > 0.0f) s = (double)softcap * tanh(s / (double)softcap);
@@ -432,9 +433,11 @@ int orc_paged_attention(const void* q, const void* k_new, const void* v_new, int
           for (int e = 0; e < vd; ++e) o[e] /= l;
       }
     }
+      free(scores);
+      free(qrow);
+    }
   }
-  free(scores);
-  return 0;
+  return failed ? 4 : 0;
 }
 
 int orc_paged_attention_op(int act_dtype, int cache_dtype, const void* query, const void* key,

@@ -141,9 +141,14 @@ def from_torch(t, code: int) -> np.ndarray:
 QUANT_NAMES = {0: "NONE", PER_TENSOR: "PER_TENSOR", PER_CHANNEL: "PER_CHANNEL"}
 
 
-def run_gpu_op(case: dict, validate=True, device="cuda", packed=False):
+def run_gpu_op(case: dict, validate=True, device="cuda", packed=False, max_query_len=0,
+               cache_outputs="omitted"):
     """Run the operator-level entry (pa_paged_attention) on the GPU for a case.  packed: hand
-    Q, K and V over as one [T, (H + 2 KV) * d] query with key = value = None."""
+    Q, K and V over as one [T, (H + 2 KV) * d] query with key = value = None.
+    cache_outputs: "omitted" (outputs 1/2 absent), "aliased" (bound onto the input caches) or
+    "separate" (buffers of their own, pre-filled with a garbage pattern); with "separate" the
+    return value also holds the input caches after the call: (out, kc_out, vc_out, kc_in, vc_in).
+    """
     import torch
     import onnxruntime_ep_mlx_amd as ep
     dt, cdt = case["dtype"], case["cache_dtype"]
@@ -155,6 +160,13 @@ def run_gpu_op(case: dict, validate=True, device="cuda", packed=False):
     q, k, v = T("query"), T("key"), T("value")
     if packed:
         q, k, v = torch.cat([q, k, v], dim=1).contiguous(), None, None
+    kco = vco = None
+    if cache_outputs == "aliased":
+        kco, vco = kc, vc
+    elif cache_outputs == "separate":
+        kco = torch.full_like(kc.view(torch.uint8), 0x5A).view(kc.dtype)
+        vco = None if vc is None else torch.full_like(vc.view(torch.uint8), 0xA5).view(vc.dtype)
+    kc_in, vc_in = kc, vc
     out, kc, vc = ep.paged_attention(
         q, k, v, kc, vc, I("cum"), I("past"), I("block_table"),
         T("cos_cache"), T("sin_cache"), I("slot_mapping"), T("head_sink"), T("q_norm"),
@@ -168,10 +180,13 @@ def run_gpu_op(case: dict, validate=True, device="cuda", packed=False):
         k_quant_type=QUANT_NAMES[case.get("k_quant", 0)],
         v_quant_type=QUANT_NAMES[case.get("v_quant", 0)],
         v_head_size=case.get("v_head_size", 0),
-        kv_cache_layout="LATENT" if case.get("latent") else "SEPARATE", validate=validate)
+        kv_cache_layout="LATENT" if case.get("latent") else "SEPARATE", validate=validate,
+        key_cache_out=kco, value_cache_out=vco, max_query_len=max_query_len)
     torch.cuda.synchronize()
-    return (from_torch(out, dt), from_torch(kc, cdt),
-            None if vc is None else from_torch(vc, cdt))
+    res = (from_torch(out, dt), from_torch(kc, cdt), None if vc is None else from_torch(vc, cdt))
+    if cache_outputs == "separate":
+        res += (from_torch(kc_in, cdt), None if vc_in is None else from_torch(vc_in, cdt))
+    return res
 
 
 def make_latent_case(H, d, vd, nb, bs, batch, **kw):

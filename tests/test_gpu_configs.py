@@ -139,3 +139,128 @@ def test_c3_full_batch_sampled_oracle_and_properties():
     out3 = _run(ep, torch, c, kc, vc, rows=sample)
     err = orc.rel_l2(orc.decode(out3, BF16), orc.decode(out[sample], BF16))
     assert err <= 1e-3, err
+
+
+def _bench():
+    """bench.py's workload builders, so these tests run exactly the inputs the bench times."""
+    import sys
+    from pathlib import Path
+    root = str(Path(__file__).resolve().parent.parent)
+    if root not in sys.path:
+        sys.path.insert(0, root)
+    import bench
+    return bench
+
+
+def _gather(torch, pool, bt_row, n):
+    ids = torch.from_numpy(np.asarray(bt_row[:n], np.int64)).cuda()
+    return pool.index_select(0, ids)
+
+
+def test_c4_full_workload_planned_prefill():
+    """BASELINE.json config 4 at its workload (bench.py --config c4: seed 4, 8 x 512-token chunks,
+    past U[0,4096], 28q/4kv, d 128, block 16, bf16) through pa_paged_attention, which takes the
+    planned prefill (896 row-block items >= 2 per CU, items over the split threshold run as two
+    halves).  Checks: the whole pool bit-exact after the append; the sequences with the shortest
+    and the longest past fully (28 heads x 512 rows) against the oracle; every sequence against
+    the independent chunked decode kernel (kind 4); two calls bit-identical."""
+    import torch
+    import onnxruntime_ep_mlx_amd as ep
+    bench = _bench()
+    w = bench.build_prefill_workload(torch, seed=4)
+    B, H, KV, d, bs, T = w["B"], w["H"], w["KV"], w["d"], w["bs"], w["T"]
+    past = w["ctx"] - w["mq"]
+    cum = w["cum"].cpu().numpy()
+    q, k, v = (from_torch(w[n], BF16) for n in ("q", "k", "v"))
+    kc0, vc0 = from_torch(w["kc"], BF16), from_torch(w["vc"], BF16)
+    kc_ref, vc_ref = orc.reshape_and_cache(k, v, BF16, kc0, vc0, BF16, cum,
+                                           past.astype(np.int32), w["bt_np"])
+    outs = []
+    for _ in range(2):
+        out, _, _ = ep.paged_attention(w["q"], w["k"], w["v"], w["kc"], w["vc"], w["cum"],
+                                       w["past"], w["bt"], num_heads=H, kv_num_heads=KV)
+        torch.cuda.synchronize()
+        outs.append(out.clone())
+        if len(outs) == 1:
+            assert np.array_equal(from_torch(w["kc"], BF16), kc_ref)
+            assert np.array_equal(from_torch(w["vc"], BF16), vc_ref)
+    assert torch.equal(outs[0], outs[1])
+    got = orc.decode(from_torch(outs[0], BF16), BF16).astype(np.float64)
+    # the independent chunked MFMA decode kernel over the same (appended) pages, every sequence
+    alt = ep.attention(w["q"], w["k"], w["v"], w["kc"], w["vc"], w["cum"], w["past"], w["bt"],
+                       num_heads=H, max_query_len=w["mq"], kind=4, new_rows_in_cache=True)
+    torch.cuda.synchronize()
+    alt = orc.decode(from_torch(alt, BF16), BF16).astype(np.float64)
+    for b in range(B):
+        rows = slice(int(cum[b]), int(cum[b + 1]))
+        assert orc.rel_l2(got[rows], alt[rows]) <= 2e-3, b
+    # shortest and longest past against the oracle (pages gathered from the pre-step pool)
+    for b in (int(np.argmin(past)), int(np.argmax(past))):
+        n = (int(w["ctx"][b]) + bs - 1) // bs
+        ids = np.asarray(w["bt_np"][b, :n])
+        rows = slice(int(cum[b]), int(cum[b + 1]))
+        sub = dict(num_heads=H, kv_num_heads=KV, head_dim=d, dtype=BF16, cache_dtype=BF16,
+                   cum=np.array([0, w["mq"]], np.int32), past=np.array([past[b]], np.int32),
+                   block_table=np.arange(n, dtype=np.int32)[None], query=q[rows], key=k[rows],
+                   value=v[rows], key_cache=kc0[ids].copy(), value_cache=vc0[ids].copy())
+        ref, ref_t, _, _ = orc.paged_attention_op(sub)
+        assert orc.rel_l2(got[rows], orc.decode(ref_t, BF16)) <= 2e-3, b
+        assert orc.rel_l2(got[rows], ref) <= 4e-3, b
+
+
+def test_c5_full_batch_fp8():
+    """BASELINE.json config 5 at its batch (bench.py --config c5: B=16, 64q/8kv, d 128, ctx
+    32768, e4m3 pages with per-(block, kv-head) scales) through pa_paged_attention.  Three sampled
+    sequences against the oracle (pages and scales gathered before the step, the appended row
+    bytes included); the full batch through properties: only the 16 appended rows of the pages
+    changed, two calls bit-identical, the sampled sequences re-run as their own batch agree."""
+    import torch
+    import onnxruntime_ep_mlx_amd as ep
+    from _oracle import E4M3
+    bench = _bench()
+    w = bench.build_fp8_workload(torch, seed=5)
+    B, H, KV, d, bs = w["B"], w["H"], w["KV"], w["d"], w["bs"]
+    past = w["past"].cpu().numpy()
+    sample = [0, 7, 15]
+    n = (int(w["ctx"][0]) + bs - 1) // bs
+    pages = {b: tuple(from_torch(_gather(torch, w[p].view(torch.uint8), w["bt_np"][b], n), E4M3)
+                      for p in ("kc", "vc")) +
+                tuple(_gather(torch, w[s], w["bt_np"][b], n).cpu().numpy() for s in ("ks", "vs"))
+             for b in sample}
+    kc0 = w["kc"].view(torch.uint8).clone()
+
+    def run(rows=None):
+        sel = np.arange(B) if rows is None else np.asarray(rows)
+        m = len(sel)
+        idx = torch.from_numpy(sel.astype(np.int64)).cuda()
+        out, _, _ = ep.paged_attention(
+            w["q"].index_select(0, idx), w["k"].index_select(0, idx),
+            w["v"].index_select(0, idx), w["kc"], w["vc"],
+            torch.arange(m + 1, dtype=torch.int32, device="cuda"), w["past"].index_select(0, idx),
+            w["bt"].index_select(0, idx).contiguous(), k_scale=w["ks"], v_scale=w["vs"],
+            num_heads=H, kv_num_heads=KV)
+        torch.cuda.synchronize()
+        return from_torch(out, BF16)
+
+    out = run()
+    q, k, v = (from_torch(w[t], BF16) for t in ("q", "k", "v"))
+    for b in sample:
+        kb, vb, ksb, vsb = pages[b]
+        sub = dict(num_heads=H, kv_num_heads=KV, head_dim=d, dtype=BF16, cache_dtype=E4M3,
+                   cum=np.array([0, 1], np.int32), past=past[b:b + 1].copy(),
+                   block_table=np.arange(n, dtype=np.int32)[None], query=q[b:b + 1],
+                   key=k[b:b + 1], value=v[b:b + 1], key_cache=kb.copy(), value_cache=vb.copy(),
+                   k_scale=ksb.copy(), v_scale=vsb.copy())
+        ref, ref_t, kc_ref, vc_ref = orc.paged_attention_op(sub)
+        assert orc.rel_l2(orc.decode(out[b:b + 1], BF16), orc.decode(ref_t, BF16)) <= 2e-3, b
+        got_k = from_torch(_gather(torch, w["kc"].view(torch.uint8), w["bt_np"][b], n), E4M3)
+        got_v = from_torch(_gather(torch, w["vc"].view(torch.uint8), w["bt_np"][b], n), E4M3)
+        assert np.array_equal(got_k, kc_ref) and np.array_equal(got_v, vc_ref), b
+    # only the appended rows changed
+    diff = (w["kc"].view(torch.uint8) != kc0).reshape(-1, KV * d)
+    changed = set(torch.nonzero(diff.any(dim=1)).flatten().cpu().numpy().tolist())
+    expect = {int(w["bt_np"][b, int(past[b]) // bs]) * bs + int(past[b]) % bs for b in range(B)}
+    assert changed <= expect
+    assert np.array_equal(run(), out)
+    err = orc.rel_l2(orc.decode(run(sample), BF16), orc.decode(out[sample], BF16))
+    assert err <= 1e-3, err
