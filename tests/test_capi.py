@@ -31,6 +31,21 @@ def test_library_exports_every_declared_symbol():
     assert sorted(capi.EXPORTS) == declared
 
 
+def test_library_exports_only_declared_symbols():
+    """The version script keeps every internal helper local: the dynamic symbol table holds the
+    header's functions and nothing else of ours."""
+    import shutil
+    import subprocess
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm is not available")
+    out = subprocess.run([nm, "-D", "--defined-only", str(capi.LIB_PATH)], check=True,
+                         capture_output=True, text=True).stdout
+    names = {line.split()[-1] for line in out.splitlines() if line.split()[1:2] in (["T"], ["B"], ["D"])}
+    ours = {n for n in names if not n.startswith("_")}
+    assert ours == set(_declared_functions()), sorted(ours ^ set(_declared_functions()))
+
+
 def test_version_and_error_channel():
     lib = capi.load()
     assert b"gfx950" in lib.pa_version()
