@@ -285,6 +285,20 @@ size_t pa_paged_attention_workspace_bytes(const pa_paged_attention_node* node,
 int pa_paged_attention(const pa_paged_attention_node* node, const pa_paged_attention_io* io,
                        void* workspace, size_t workspace_bytes, pa_stream_t stream);
 
+/* Allocation-free variant of pa_paged_attention.  It has no counterpart in the reference; it is
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same contract as pa_paged_attention, except that the
+ * workspace is a scratch buffer of PA_STATIC_SCRATCH_BYTES inside the library's code object on
+ * each GPU (a file-scope __device__ array, resident until the process ends): a call whose
+ * workspace (pa_paged_attention_workspace_bytes) exceeds it returns PA_ERR_UNSUPPORTED before
+ * any device work.  No hipMalloc / hipFree or other allocating routine is called.  Every call
+ * on one GPU shares that GPU's scratch: calls that overlap on one GPU (different streams, or
+ * host threads) race and must be serialised by the caller; calls in stream order do not.  The
+ * kernels need no cleared scratch (everything they read is written earlier in the same call). */
+#define PA_STATIC_SCRATCH_BYTES ((size_t)64 << 20)
+int pa_paged_attention_static(const pa_paged_attention_node* node,
+                              const pa_paged_attention_io* io, pa_stream_t stream);
+
 /* Operator-level entry: com.microsoft::GroupQueryAttention on contiguous caches
  * (group_query_attention_op / gqa_batched, attention.rs:932-1454 and :586-848), for the
  * shared-buffer contract: present_key/present_value are [batch, kv_heads, capacity, head]

@@ -12,6 +12,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -863,6 +864,53 @@ int pa_paged_attention(const pa_paged_attention_node* n, const pa_paged_attentio
                      ws + L.attn_off, workspace_bytes - L.attn_off, 0, 0, s, opts);
   if (rc) return rc;
   return copy_cache_outputs(io, s);
+}
+
+// ------------------------------------------------------------------------------ no-alloc entry
+// The scratch of pa_paged_attention_static: one array per GPU in the library's code object.  In
+// host code its name is only a host-side stand-in; the device address comes from
+// hipGetSymbolAddress, looked up once per device and kept in g_scratch_ptr.
+namespace {
+
+static __device__ __align__(256) unsigned char scratch[PA_STATIC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int static_scratch(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(PA_ERR_UNSUPPORTED, "device %d is beyond the %d devices served", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(PA_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PA_OK;
+}
+
+}  // namespace
+
+int pa_paged_attention_static(const pa_paged_attention_node* n, const pa_paged_attention_io* io,
+                              pa_stream_t stream) {
+  OpLayout L;
+  int rc = op_layout(n, io, &L);
+  if (rc) return rc;
+  if (L.total > PA_STATIC_SCRATCH_BYTES)
+    return fail(PA_ERR_UNSUPPORTED,
+                "pa_paged_attention_static: the call needs %zu bytes of workspace, more than the "
+                "%zu-byte static scratch",
+                L.total, (size_t)PA_STATIC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if ((rc = static_scratch(&ws))) return rc;
+  return pa_paged_attention(n, io, ws, PA_STATIC_SCRATCH_BYTES, stream);
 }
 
 // ------------------------------------------------------------------------------ GQA

@@ -30,6 +30,8 @@ PA_QUANT_PER_CHANNEL = 2
 QUANT_TYPES = {"NONE": PA_QUANT_NONE, "PER_TENSOR": PA_QUANT_PER_TENSOR,
                "PER_CHANNEL": PA_QUANT_PER_CHANNEL}
 
+PA_STATIC_SCRATCH_BYTES = 64 << 20  # include/pa_mi355x.h
+
 PA_OK = 0
 PA_ERR_INVALID_ARGUMENT = 1
 PA_ERR_UNSUPPORTED = 2
@@ -44,7 +46,8 @@ EXPORTS = (
     "pa_rotary_append", "pa_reshape_and_cache",
     "pa_attention_workspace_bytes", "pa_attention_workspace_bytes_ex",
     "pa_attention", "pa_attention_ex",
-    "pa_paged_attention_workspace_bytes", "pa_paged_attention", "pa_paged_attention_claim",
+    "pa_paged_attention_workspace_bytes", "pa_paged_attention", "pa_paged_attention_static",
+    "pa_paged_attention_claim",
     "pa_group_query_attention_workspace_bytes", "pa_group_query_attention",
 )
 
@@ -195,6 +198,7 @@ def load() -> C.CDLL:
                                       C.c_int, P, P, P, P, P, SZ, I32, I32, P]),
         "pa_paged_attention_workspace_bytes": (SZ, [C.POINTER(PaNode), C.POINTER(PaIO)]),
         "pa_paged_attention": (C.c_int, [C.POINTER(PaNode), C.POINTER(PaIO), P, SZ, P]),
+        "pa_paged_attention_static": (C.c_int, [C.POINTER(PaNode), C.POINTER(PaIO), P]),
         "pa_paged_attention_claim": (C.c_int, [C.POINTER(PaNodeInfo), C.c_char_p, SZ]),
         "pa_group_query_attention_workspace_bytes": (SZ, [C.POINTER(PaGqaNode),
                                                           C.POINTER(PaGqaIO)]),

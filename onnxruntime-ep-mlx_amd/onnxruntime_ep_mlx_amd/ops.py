@@ -267,7 +267,8 @@ def paged_attention(query, key, value, key_cache, value_cache, cumulative_sequen
                     rotary_interleaved=0, rotary_offset=0, is_causal=1, qk_norm_epsilon=1e-6,
                     k_quant_type="NONE", v_quant_type="NONE", v_head_size=0,
                     kv_cache_layout="SEPARATE", validate=True, output=None,
-                    key_cache_out=None, value_cache_out=None, max_query_len=0):
+                    key_cache_out=None, value_cache_out=None, max_query_len=0,
+                    static_scratch=False):
     """com.microsoft::PagedAttention on MI355X (operator-level entry, pa_paged_attention).
 
     ``attention_metadata`` is accepted and ignored, like the reference
@@ -285,6 +286,8 @@ def paged_attention(query, key, value, key_cache, value_cache, cumulative_sequen
     (outputs bound onto the inputs need nothing), and are returned in place of the inputs.
     ``max_query_len`` (0 = derive it) bounds every sequence's new tokens: it picks the kernel
     family without a device read when ``validate`` is False.
+    ``static_scratch``: call pa_paged_attention_static, which allocates nothing (its workspace
+    is the library's per-GPU static scratch, shared by every call on that GPU).
     """
     if kv_cache_layout not in ("SEPARATE", "LATENT"):
         raise ValueError("kv_cache_layout must be SEPARATE or LATENT")
@@ -329,10 +332,14 @@ def paged_attention(query, key, value, key_cache, value_cache, cumulative_sequen
         _ptr(host.get("cum")), _ptr(host.get("past")), _ptr(host.get("bt")),
         _ptr(host.get("slots")), _ptr(output), _ptr(key_cache_out), _ptr(value_cache_out),
         max_query_len)
-    nbytes = lib.pa_paged_attention_workspace_bytes(C.byref(node), C.byref(io))
-    ws = _ws.get(nbytes, query.device)
-    capi.check(lib.pa_paged_attention(C.byref(node), C.byref(io), _ptr(ws), nbytes,
-                                      _stream(query.device)))
+    if static_scratch:
+        capi.check(lib.pa_paged_attention_static(C.byref(node), C.byref(io),
+                                                 _stream(query.device)))
+    else:
+        nbytes = lib.pa_paged_attention_workspace_bytes(C.byref(node), C.byref(io))
+        ws = _ws.get(nbytes, query.device)
+        capi.check(lib.pa_paged_attention(C.byref(node), C.byref(io), _ptr(ws), nbytes,
+                                          _stream(query.device)))
     return (output, key_cache if key_cache_out is None else key_cache_out,
             value_cache if value_cache_out is None else value_cache_out)
 
