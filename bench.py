@@ -16,7 +16,8 @@ HBM before timing.
 --config c4 / c5 measure BASELINE.json configs 4 (chunked prefill, Qwen2.5-7B shape: value =
 TFLOP/s of the causal attention FLOPs, roofline vs the 2.5 PFLOP/s dense bf16 MFMA peak) and 5
 (fp8 e4m3 pages, B=16, ctx 32768: value = GB/s of fp8 KV bytes, roofline vs 8 TB/s) the same way;
-their lines carry their own metric names and no CPU baseline.
+their lines carry their own metric names; their CPU baselines are the same CPU path on one
+sequence (causal prefill chunk / fp8 pages dequantised to fp32).
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--config c3|c4|c5]
 """
@@ -240,61 +241,149 @@ class Step:
         self.capi.check(rc)
 
 
-def cpu_baseline(torch, w, step, n_seq, seconds):
+def cpu_info():
+    """Threads the CPU path may use and the host's CPU model.  The threads are the CPUs this
+    process may run on (its affinity mask), capped by OMP_NUM_THREADS when the job sets it: a GPU
+    box grants each GPU's job a share of the host's cores and states it that way."""
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except AttributeError:
+        allowed = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    threads = min(allowed, int(env)) if env.isdigit() and int(env) > 0 else allowed
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return max(threads, 1), model, os.cpu_count() or 1
+
+
+def _timed(fn, seconds, max_reps=10000):
+    fn()  # warm
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= max_reps:
+            return el / reps, reps, el
+
+
+def _host_pages(torch, w, sample):
+    """The sampled sequences' pages copied to the host as a small paged pool (their blocks in
+    block-table order) plus each sequence's block ids in it: the input of the CPU gather."""
+    import numpy as np
+    bs = w["bs"]
+    ids, local, base = [], [], 0
+    for b in sample:
+        n = (int(w["ctx"][b]) + bs - 1) // bs
+        ids.append(w["bt_np"][b, :n].astype(np.int64))
+        local.append(np.arange(base, base + n))
+        base += n
+    sel = torch.from_numpy(np.concatenate(ids)).cuda()
+    raw = lambda t: t.view(torch.uint8) if t.element_size() == 1 else t.view(torch.int16)
+    kp = raw(w["kc"]).index_select(0, sel).cpu().numpy()
+    vp = raw(w["vc"]).index_select(0, sel).cpu().numpy()
+    sc = None
+    if w["ks"] is not None:
+        sc = (w["ks"].index_select(0, sel).cpu().numpy(), w["vs"].index_select(0, sel).cpu().numpy())
+    return kp, vp, sc, local
+
+
+def _gather(w, kp, vp, sc, local, sample):
+    """CPU page -> contiguous gather of the sampled sequences ([sum ctx, KV, d] K and V); fp8
+    pages are dequantised to fp32 (code * block scale) on the way, as a CPU GQA needs."""
+    import numpy as np
+    bs, KV, d = w["bs"], w["KV"], w["d"]
+    ks, vs, offs, off = [], [], [], 0
+    for b, blk in zip(sample, local):
+        c = int(w["ctx"][b])
+        kk = kp[blk].reshape(-1, KV, d)[:c]
+        vv = vp[blk].reshape(-1, KV, d)[:c]
+        if sc is not None:
+            import _oracle as orc
+            kscale = np.repeat(sc[0][blk], bs, axis=0)[:c, :, None]
+            vscale = np.repeat(sc[1][blk], bs, axis=0)[:c, :, None]
+            kk = orc.decode(np.ascontiguousarray(kk), orc.E4M3) * kscale
+            vv = orc.decode(np.ascontiguousarray(vv), orc.E4M3) * vscale
+        ks.append(kk)
+        vs.append(vv)
+        offs.append(off)
+        off += c
+    return (np.ascontiguousarray(np.concatenate(ks)), np.ascontiguousarray(np.concatenate(vs)),
+            offs)
+
+
+def cpu_baseline(torch, w, step, n_seq, seconds, config="c3"):
+    """The CPU path (the oracle directory's threaded contiguous-KV GQA, ORT CPU semantics, fp32
+    accumulation) on a bounded sample of the same workload, on this host's cores.  The page ->
+    contiguous gather it needs is timed on its own and reported beside it, not inside value."""
     import numpy as np
     sys.path.insert(0, os.fspath(ROOT / "tests"))
     import _oracle as orc
-    B, KV, d, bs = w["B"], w["KV"], w["d"], w["bs"]
+    threads, model, host_cpus = cpu_info()
+    B, H, KV, d = w["B"], w["H"], w["KV"], w["d"]
     sample = list(range(min(n_seq, B)))
-    ks, vs, offs, ctxs = [], [], [], []
-    off = 0
-    for b in sample:
-        c = int(w["ctx"][b])
-        n = (c + bs - 1) // bs
-        ids = torch.from_numpy(w["bt_np"][b, :n].astype(np.int64)).cuda()
-        kb = w["kc"].index_select(0, ids).reshape(n * bs, KV, d)[:c]
-        vb = w["vc"].index_select(0, ids).reshape(n * bs, KV, d)[:c]
-        ks.append(kb.view(torch.int16).cpu().numpy().view(np.uint16))
-        vs.append(vb.view(torch.int16).cpu().numpy().view(np.uint16))
-        offs.append(off)
-        ctxs.append(c)
-        off += c
-    k = np.ascontiguousarray(np.concatenate(ks))
-    v = np.ascontiguousarray(np.concatenate(vs))
-    q = step.q_out[sample].view(torch.int16).cpu().numpy().view(np.uint16).reshape(
-        len(sample), w["H"], d).copy()
-    threads = max(1, min(16, os.cpu_count() or 1))
+    kp, vp, sc, local = _host_pages(torch, w, sample)
+    k, v, offs = _gather(w, kp, vp, sc, local, sample)
+    gather_s, _, _ = _timed(lambda: _gather(w, kp, vp, sc, local, sample), min(seconds, 3.0), 50)
+    dt = orc.F32 if sc is not None else orc.BF16
+    if dt == orc.F32:
+        k, v = k.astype(np.float32), v.astype(np.float32)
     scale = float(1.0 / np.sqrt(np.float32(d)))
-    orc.cpu_gqa_decode(orc.BF16, q, k, v, offs, ctxs, w["H"], KV, d, scale, threads)  # warm
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        orc.cpu_gqa_decode(orc.BF16, q, k, v, offs, ctxs, w["H"], KV, d, scale, threads)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or reps >= 10000:
-            break
-    per = el / reps
-    sample_bytes = 4096.0 * sum(ctxs)
-    full_bytes = 4096.0 * float(w["ctx"].sum())
-    gbs = sample_bytes / per / 1e9
-    return {
-        "value": round(gbs, 3), "unit": "GB/s (KV bytes)", "cores": threads, "kind": "port",
-        "us_per_step_full_batch": round(per * full_bytes / sample_bytes * 1e6, 1),
-        "sample": (f"first {len(sample)} of {B} sequences (sum ctx {sum(ctxs)}), "
-                   f"{reps} reps in {el:.1f} s, contiguous bf16 KV gathered from the pages "
-                   f"(gather not timed), fp32 accumulation, {threads} threads"),
-    }
+    ctxs = [int(w["ctx"][b]) for b in sample]
+    if config == "c4":
+        mq = w["mq"]
+        q = step.q_out[: len(sample) * mq].view(torch.int16).cpu().numpy().view(np.uint16)
+        q = np.ascontiguousarray(q)
+        past = [c - mq for c in ctxs]
+        starts = [i * mq for i in range(len(sample))]
+        run = lambda: orc.cpu_gqa_prefill(dt, q, k, v, offs, starts, [mq] * len(sample), past,
+                                          H, KV, d, scale, threads)
+    else:
+        q = step.q_out[sample].view(torch.int16).cpu().numpy().view(np.uint16).reshape(
+            len(sample), H, d).copy()
+        if dt == orc.F32:
+            q = orc.decode(q, orc.BF16)
+        run = lambda: orc.cpu_gqa_decode(dt, q, k, v, offs, ctxs, H, KV, d, scale, threads)
+    per, reps, el = _timed(run, seconds)
+    what = {"c3": "contiguous bf16 KV", "c4": "contiguous bf16 KV, causal 512-row chunks",
+            "c5": "contiguous KV dequantised from e4m3 pages to fp32"}[config]
+    info = {"cores": threads, "kind": "port", "cpu_model": model, "host_cpus": host_cpus,
+            "gather_ms_sample": round(gather_s * 1e3, 2)}
+    desc = (f"first {len(sample)} of {B} sequences (sum ctx {sum(ctxs)}), {reps} reps in "
+            f"{el:.1f} s, {what} gathered from the pages (gather timed apart: "
+            f"{gather_s * 1e3:.1f} ms for the sample), fp32 accumulation, {threads} threads")
+    if config == "c4":
+        fl = sum(4.0 * H * d * (w["mq"] * (c - w["mq"]) + w["mq"] * (w["mq"] + 1) / 2)
+                 for c in ctxs)
+        return {"value": round(fl / per / 1e12, 4), "unit": "TFLOP/s", **info,
+                "ms_per_step_full_batch": round(per * w["flops"] / fl * 1e3, 1),
+                "sample": desc}
+    elem = 1 if config == "c5" else 2
+    sample_bytes = float(sum(ctxs)) * KV * d * 2 * elem
+    full_bytes = float(w["ctx"].sum()) * KV * d * 2 * elem
+    return {"value": round(sample_bytes / per / 1e9, 3),
+            "unit": "GB/s (fp8 KV bytes)" if config == "c5" else "GB/s (KV bytes)", **info,
+            "us_per_step_full_batch": round(per * full_bytes / sample_bytes * 1e6, 1),
+            "gather_us_full_batch": round(gather_s * full_bytes / sample_bytes * 1e6, 1),
+            "sample": desc}
 
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
-def other_config_line(args, w, ms_step, attn_ms, kv_bytes):
+def other_config_line(args, w, ms_step, attn_ms, kv_bytes, cpu=None):
     """JSON line of BASELINE.json configs 4 and 5 (not the driver's default line)."""
     common = {"n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
               "ms_per_step": round(ms_step, 4), "us_per_step": round(ms_step * 1e3, 1),
               "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-              "cpu_baseline": None}
+              "cpu_baseline": cpu}
     if args.config == "c4":
         tf_step = w["flops"] / (ms_step * 1e-3) / 1e12
         tf_attn = w["flops"] / (attn_ms * 1e-3) / 1e12
@@ -399,13 +488,14 @@ def main():
     attn_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
     attn_gbs = kv_bytes / (attn_ms * 1e-3) / 1e9
 
-    if args.config != "c3":
-        print(json.dumps(other_config_line(args, w, ms_step, attn_ms, kv_bytes)), flush=True)
-        return
-
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(torch, w, step, args.cpu_sample, args.cpu_seconds)
+        n_seq = {"c3": args.cpu_sample, "c4": 1, "c5": 1}[args.config]
+        cpu = cpu_baseline(torch, w, step, n_seq, args.cpu_seconds, args.config)
+
+    if args.config != "c3":
+        print(json.dumps(other_config_line(args, w, ms_step, attn_ms, kv_bytes, cpu)), flush=True)
+        return
 
     gbs = kv_bytes / (ms_step * 1e-3) / 1e9
     line = {

@@ -130,6 +130,14 @@ int orc_cpu_gqa_decode(int dtype, const void* q, const void* k, const void* v,
                        const int64_t* kv_offset, const int32_t* ctx, int batch, int num_heads,
                        int kv_heads, int head_dim, float scale, float* out, int threads);
 
+/* The CPU path for chunked prefill (bench.py config 4): causal GQA over contiguous K/V
+ * ([past + nq, kv_heads, head_dim] per sequence at kv_offset), query rows q_start[b] ..
+ * q_start[b] + nq[b] - 1 at positions past[b] .., fp32 accumulation, `threads` pthreads. */
+int orc_cpu_gqa_prefill(int dtype, const void* q, const void* k, const void* v,
+                        const int64_t* kv_offset, const int32_t* q_start, const int32_t* nq,
+                        const int32_t* past, int batch, int num_heads, int kv_heads,
+                        int head_dim, float scale, float* out, int threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -70,15 +70,20 @@ def lib() -> C.CDLL:
                                          F, I32, I32, P, I32, P, P, I32, I32]
         L.orc_cpu_gqa_decode.restype = I32
         L.orc_cpu_gqa_decode.argtypes = [I32, P, P, P, P, P, I32, I32, I32, I32, F, P, I32]
+        L.orc_cpu_gqa_prefill.restype = I32
+        L.orc_cpu_gqa_prefill.argtypes = [I32, P, P, P, P, P, P, P, I32, I32, I32, I32, F, P,
+                                          I32]
         _lib = L
     return _lib
 
 
 def _p(a):
+    """Pointer argument for a C call.  data_as keeps a reference to the array, so a temporary
+    made inline in the call's argument list stays alive until the call returns."""
     if a is None:
         return None
     assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
-    return a.ctypes.data
+    return a.ctypes.data_as(C.c_void_p)
 
 
 def encode(x: np.ndarray, dtype: int) -> np.ndarray:
@@ -230,3 +235,17 @@ def rel_l2(a, b) -> float:
     b = np.asarray(b, np.float64)
     den = np.linalg.norm(b)
     return float(np.linalg.norm(a - b) / (den if den > 0 else 1.0))
+
+
+def cpu_gqa_prefill(dtype, q, k, v, kv_offset, q_start, nq, past, H, KV, d, scale, threads):
+    """CPU path of chunked prefill (causal GQA over contiguous K/V); q is [T, H * d]."""
+    B = len(nq)
+    out = np.zeros((q.shape[0], H, d), np.float32)
+    rc = lib().orc_cpu_gqa_prefill(dtype, _p(q), _p(k), _p(v),
+                                   _p(np.ascontiguousarray(kv_offset, np.int64)),
+                                   _p(np.ascontiguousarray(q_start, np.int32)),
+                                   _p(np.ascontiguousarray(nq, np.int32)),
+                                   _p(np.ascontiguousarray(past, np.int32)), B, H, KV, d, scale,
+                                   _p(out), threads)
+    assert rc == 0, rc
+    return out

@@ -462,3 +462,34 @@ def test_cpu_baseline_matches_fp64_restatement():
                                         np.ascontiguousarray(pv[0, :, -1]).reshape(1, 1, -1),
                                         pk, pv, np.array([ctx[b] - 1]), H, KV, d, 0.125)
         assert orc.rel_l2(got[b].reshape(-1), want.reshape(-1)) < 1e-5
+
+
+# The CPU path timed beside the GPU (pa_cpu_baseline.c): the same attention over contiguous K/V
+# gathered from the pages after the append, in fp32 accumulation -- equal to the oracle's fp64
+# result to fp32 rounding, for decode (one row per sequence) and causal prefill chunks.
+@pytest.mark.parametrize("new", [[1, 1, 1], [5, 17, 1]], ids=["decode", "prefill"])
+def test_cpu_baseline_matches_oracle(new):
+    from pa_cases import make_case
+    B, bs, mb = 3, 16, 6
+    case = make_case(8, 2, 64, B * mb, bs, B, dtype=orc.BF16, seed=12, new_lens=new,
+                     past=[40, 9, 70], max_blocks=mb, std=1.0)
+    ref, _, kc, vc = orc.paged_attention_op(case)
+    cum, past = case["cum"], case["past"]
+    ks, vs, offs, off = [], [], [], 0
+    for b in range(B):
+        total = int(past[b] + cum[b + 1] - cum[b])
+        pos = np.arange(total)
+        slots = case["block_table"][b, pos // bs] * bs + pos % bs
+        ks.append(kc.reshape(-1, 2, 64)[slots])
+        vs.append(vc.reshape(-1, 2, 64)[slots])
+        offs.append(off)
+        off += total
+    k, v = np.ascontiguousarray(np.concatenate(ks)), np.ascontiguousarray(np.concatenate(vs))
+    scale = float(1.0 / np.sqrt(np.float32(64)))
+    if max(new) == 1:
+        q = case["query"].reshape(B, 8, 64).copy()
+        out = orc.cpu_gqa_decode(orc.BF16, q, k, v, offs, past + 1, 8, 2, 64, scale, 3)
+    else:
+        out = orc.cpu_gqa_prefill(orc.BF16, case["query"], k, v, offs, cum[:-1],
+                                  np.diff(cum), past, 8, 2, 64, scale, 3)
+    assert orc.rel_l2(out.reshape(ref.shape), ref) <= 1e-5
