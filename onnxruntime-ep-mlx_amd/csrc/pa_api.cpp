@@ -223,7 +223,9 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
     } else {
       const int64_t splits = (target + units - 1) / units;
       int64_t ch = (ctx + splits - 1) / splits;
-      chunk = (int)std::min<int64_t>(std::max<int64_t>((ch + 31) / 32 * 32, 256), INT32_MAX / 2);
+      const int64_t step = pa::prefill_key_step(c->head_dim);
+      chunk = (int)std::min<int64_t>(std::max<int64_t>((ch + step - 1) / step * step, 256),
+                                     INT32_MAX / 2);
     }
   }
   if (chunk <= 0) {
@@ -347,6 +349,7 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
     p.plan_items = (int32_t)pl.plan_items;
     p.plan_rbs = pl.plan_rbs;
     p.plan_slots = 2 * device_cus();
+    p.plan_step = pa::prefill_key_step(c->head_dim);
   }
   p.num_blocks = c->num_blocks;
   p.block_size = c->block_size;

@@ -305,8 +305,10 @@ struct AttnParams {
   // i = (b * plan_rbs + rb) * kv_heads + kh.  The plan kernel writes the work units longest first
   // -- plan[4u .. 4u+3] = (item, part, first key, end key), part 0 a whole item, 1 / 2 the halves
   // of an item split in two -- the unit count at plan_info[0] and plan_split[i] = 1 for split
-  // items, whose halves leave fp32 partials at rows (2 i + part - 1) * kPrefillRows + row.
-  int32_t plan_items, plan_rbs, plan_slots;
+  // items, whose halves leave fp16 partials (rows scaled by a power of two) at rows
+  // (2 i + part - 1) * kPrefillRows + row.  plan_step: the prefill kernel's key step (32 or 64);
+  // item key ranges start and split at multiples of it.
+  int32_t plan_items, plan_rbs, plan_slots, plan_step;
   int32_t* plan;
   int32_t* plan_info;
   int32_t* plan_split;
@@ -333,6 +335,10 @@ __device__ __forceinline__ float sink_logit(const AttnParams& p, int h) {
 // of 4 wavefronts.
 constexpr int kPrefillGroups = 2;
 constexpr int kPrefillRows = 64 * kPrefillGroups;
+
+// Keys per step of the prefill kernel for a head size: 64 for the head-128 kernel on 32x32
+// tiles, 32 for the head-64 kernel on 16x16 tiles.
+inline int prefill_key_step(int head_dim) { return head_dim == 128 ? 64 : 32; }
 
 // Launchers (defined in the .hip files).
 hipError_t launch_rotary_append(const AppendParams& p, pa_dtype act, pa_dtype cache_dtype,

@@ -300,6 +300,486 @@ prefill_kernel(const AttnParams p) {
   }
 }
 
+// ----------------------------------------------------------------------------- d = 128 kernel
+// The head-128 prefill kernel on 32x32x16 matrix-core tiles, 64 keys per step.
+//
+// Workgroup: 4 wavefronts, 128 grouped query rows of one (sequence, kv-head) -- wavefront w owns
+// rows row0 + 32 w + c, c = lane % 32 -- over a key range, two workgroups per CU.  Both products
+// run transposed, so every lane holds one query row:
+//   scores  S^T[key][row] = K . Q^T   (A = 32 keys x 16 dims from LDS, B = Q^T in registers):
+//           lane l gets row c, keys 8 i + 4 h + j (h = l / 32, register 4 i + j) of a 32-key block;
+//   output  O^T[dim][row] = V^T . P^T (A = 32 dims x 16 keys from LDS, B = P^T in registers):
+//           lane l accumulates row c, dims 8 i + 4 h + j of each 32-dim tile.
+// The probabilities of key slice t (keys 16 t .. 16 t + 15) are then registers 8 (t % 2) .. + 7
+// of score block t / 2 as they come out of the score product, in the key order
+// {4 h + j, 8 + 4 h + j} that the value images are written in.  Row maxima, sums and the lazy
+// rescale need no cross-lane traffic except one swap between the lane halves.
+//
+// P . V runs in fp16: probabilities are <= 2^8 (lazy maximum) and convert with round to nearest
+// even; bf16 value rows convert exactly to fp16 after a power-of-two scale 2^-s per 32-dim
+// quarter, chosen from the largest value seen so far in that quarter (s = exponent - 15, so the
+// largest converted value lies in [2^14, 2^15)).  When a step raises a quarter's s the output
+// accumulated for that quarter is scaled by the exact power of two 2^(s_old - s_new); the
+// epilogue multiplies by 2^s.  Values below 2^-29 of their quarter's maximum lose precision (fp16
+// subnormal range), far below the rounding of the fp32 sums.  fp16 activations use their value
+// rows as they are.
+//
+// Steps are fetched once per workgroup: wavefront w loads keys 16 w .. 16 w + 15 of the step (one
+// page when the block size is a multiple of 16) and the values of dims 32 w .. 32 w + 31 for all
+// 64 keys, converts and regroups them in registers and writes the per-lane MFMA operand images to
+// LDS.  Two LDS buffers, one barrier per step, the global loads of step k + 2 in flight while step
+// k computes.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+
+constexpr int kMxKeys = 64;  // keys per step
+
+template <typename TT>
+__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c);
+template <>
+__device__ __forceinline__ f32x16 mfma32<TBF16>(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x16 mfma32<TF16>(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// Both lane halves' value of x (lanes l and l ^ 32 hold the same query row).
+__device__ __forceinline__ float other_half(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x),
+                                                  __builtin_bit_cast(uint32_t, x), false, false);
+  // lanes 0..31: r[1] is lane l + 32's x; lanes 32..63: r[0] is lane l - 32's x
+  return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+}
+
+// Maximum of a non-negative value over the wavefront (DPP row steps, then the row broadcasts).
+__device__ __forceinline__ int wave_max_nonneg(int v) {
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false));  // row_mirror
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x142, 0xA, 0xF, false));  // row_bcast:15
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x143, 0xC, 0xF, false));  // row_bcast:31
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
+// One LDS buffer: the operand images of a 64-key step.
+//   k[kb][ks][lane]: key 32 kb + lane % 32, dims 16 ks + 8 (lane / 32) .. + 7 (score A operand)
+//   v[t][nt][slot]:  slot mx_vslot(lane) holds dim 32 nt + lane % 32, keys
+//                    16 t + {4 h + e, 8 + 4 h + e}, h = lane / 32 (output A operand, fp16)
+//   vs[nt]:          the value scale exponent s of quarter nt for this step
+// Every staging write and every operand read touches 16 distinct 16-byte bank groups per
+// 16 lanes (the value slots are XOR-swizzled for the staging writes; mx_vslot keeps the reads a
+// permutation of the image).
+struct MxBuf {
+  u32x4 k[2][8][64];
+  u32x4 v[4][4][64];
+  int vs[4];
+  int pad[12];
+};
+
+__device__ __forceinline__ int mx_vslot(int lane) { return lane ^ ((lane >> 4) & 3); }
+
+// This wavefront's share of a step's rows, as loaded.
+//   keys:   key 16 w + lane % 16, bytes 64 i + 16 (lane / 16) .. + 15 of its row slice, i < 4
+//   values: keys 16 t + 4 hh + e and 16 t + 8 + 4 hh + e (e < 4; t = lane / 16,
+//           hh = lane / 8 % 2), dims 32 w + 4 (lane % 8) .. + 3
+struct MxStage {
+  u32x4 k[4];
+  u32x2 v[8];
+};
+
+// Issue the loads of the step at key t0.  Page rows come straight from the pages when the step
+// lies below the cache limit (or every key is in the pages) and the block size is a multiple of
+// 16: the 16 keys of a group then share one page.  Other steps address every row on its own.
+// Value rows at or past the end are zeroed when stored (mx_store).
+template <typename TT>
+__device__ __forceinline__ void mx_load(const WaveInfo& w, PageWindow& pw, int wave, int lane,
+                                        int t0, MxStage& st) {
+  constexpr int D = 128;
+  const int kr = lane & 15, cq = lane >> 4;
+  const int dg = lane & 7, hh = (lane >> 3) & 1, t = lane >> 4;
+  const int64_t koff = (int64_t)w.kh * D * 2 + 16 * cq;
+  const int64_t voff = (int64_t)w.kh * D * 2 + (32 * wave + 4 * dg) * 2;
+  const bool paged = w.bs % 16 == 0 && (t0 + kMxKeys <= w.cache_limit || w.cache_limit >= w.total);
+  if (paged) {
+    // pool row of the first key of each 16-key group (wave-uniform), from the block-table window
+    int64_t grp[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int bi = min(div_bs(t0 + 16 * q, w), w.max_blocks - 1);
+      if (bi < pw.first || bi >= pw.first + 64) window_at(pw, w, bi, lane);
+      int64_t blk = __builtin_amdgcn_readlane(pw.ids, bi - pw.first);
+      blk = min(max(blk, (int64_t)0), w.num_blocks - 1);
+      grp[q] = blk * w.bs + mod_bs(t0 + 16 * q, w);
+    }
+    const char* kb = w.kc + (grp[wave] + kr) * w.rowb + koff;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st.k[i] = ld16(kb + 64 * i);
+    const int64_t vrow = (t == 0 ? grp[0] : t == 1 ? grp[1] : t == 2 ? grp[2] : grp[3]) + 4 * hh;
+    const char* vb = w.vc + vrow * w.rowb + voff;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      st.v[e] = *reinterpret_cast<const u32x2*>(vb + (e + 4 * (e >> 2)) * w.rowb);
+  } else {
+    const char* kb = row_ptr(w, t0 + 16 * wave + kr, false, D) + 16 * cq;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st.k[i] = ld16(kb + 64 * i);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int key = 16 * t + 4 * hh + (e & 3) + 8 * (e >> 2);
+      st.v[e] = *reinterpret_cast<const u32x2*>(row_ptr(w, t0 + key, true, D) +
+                                                (32 * wave + 4 * dg) * 2);
+    }
+  }
+}
+
+// Convert (bf16 values: to fp16 under this quarter's running scale) and regroup this
+// wavefront's share of the step at t0 into LDS buffer `buf`.  s_run: the quarter's running scale
+// exponent (wave-uniform), updated here.
+template <typename TT>
+__device__ __forceinline__ void mx_store(MxBuf& buf, MxStage& st, int wave, int lane, int t0,
+                                         int total, int& s_run) {
+  const int kr = lane & 15, cq = lane >> 4;
+  const int dg = lane & 7, hh = (lane >> 3) & 1, t = lane >> 4;
+  // keys: bytes 64 i + 16 cq = 16-byte chunk dc = 4 i + cq -> slice dc / 2, half dc % 2
+  const int kk = 16 * wave + kr;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int dc = 4 * i + cq;
+    buf.k[kk >> 5][dc >> 1][32 * (dc & 1) + (kk & 31)] = st.k[i];
+  }
+  // values: rows at or past the end take no part (their bytes may be anything): a row mask
+  // folded into the conversion (no branch, so the staging interleaves with the MFMAs)
+  uint32_t keep[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    keep[e] = (t0 + 16 * t + 4 * hh + (e & 3) + 8 * (e >> 2) < total) ? 0xffffffffu : 0u;
+  if constexpr (!std::is_same<TT, TBF16>::value) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) st.v[e] = u32x2{st.v[e][0] & keep[e], st.v[e][1] & keep[e]};
+  } else {
+    // largest biased exponent of the quarter's step, then s = max(s_run, exponent - 141): the
+    // largest value maps into [2^14, 2^15) of fp16 (bf16 exponent e -> fp16 exponent e - 112 - s)
+    uint32_t mx = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const u16x2 a = __builtin_bit_cast(u16x2, st.v[e][m] & (keep[e] & 0x7fff7fffu));
+        mx = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, mx), a));
+      }
+    const int emax = wave_max_nonneg((int)(max(mx & 0xffffu, mx >> 16) >> 7));
+    s_run = max(s_run, max(emax - 141, -112));
+    const unsigned short bias = (unsigned short)((112 + s_run) << 7);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const uint32_t x = st.v[e][m] & keep[e];
+        u16x2 a = __builtin_bit_cast(u16x2, x & 0x7fff7fffu);
+        a = __builtin_elementwise_sub_sat(a, u16x2{bias, bias});
+        a = a << (unsigned short)3;
+        st.v[e][m] = (x & 0x80008000u) | __builtin_bit_cast(uint32_t, a);
+      }
+  }
+  // regroup: dims 4 dg + 2 m (+1) of the 8 keys -> full slots of image (t, nt = wave), lane'
+  // 32 hh + 4 dg + 2 m (+1); element e' of a slot is row e' (keys 4 hh + e', then 8 + 4 hh + ...)
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    u32x4 lo, hi;
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) {
+      lo[e2] = __builtin_amdgcn_perm(st.v[2 * e2 + 1][m], st.v[2 * e2][m], 0x05040100u);
+      hi[e2] = __builtin_amdgcn_perm(st.v[2 * e2 + 1][m], st.v[2 * e2][m], 0x07060302u);
+    }
+    const int lp = 32 * hh + 4 * dg + 2 * m;
+    buf.v[t][wave][mx_vslot(lp)] = lo;
+    buf.v[t][wave][mx_vslot(lp + 1)] = hi;
+  }
+  buf.vs[wave] = s_run;  // every lane writes the same word: no branch
+}
+
+template <typename TT, bool CAP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+prefill_mx_kernel(const AttnParams p) {
+  constexpr int D = 128, ROWS = kPrefillRows;
+  static_assert(ROWS == 128, "four wavefronts of 32 rows");
+  __shared__ MxBuf lds[2];
+  int rb, kh, b, split = blockIdx.y, part = 0, item = 0, ustart = 0, uend = 0;
+  if (p.plan_items > 0) {
+    const int nunits = p.plan_info[0];
+    const int4 u = reinterpret_cast<const int4*>(p.plan)[min((int)blockIdx.x, p.plan_items * 2 - 1)];
+    if ((int)blockIdx.x >= nunits) return;
+    item = u.x;
+    part = u.y;
+    ustart = u.z;
+    uend = u.w;
+    kh = item % p.kv_heads;
+    rb = (item / p.kv_heads) % p.plan_rbs;
+    b = item / (p.kv_heads * p.plan_rbs);
+  } else {
+    const int units = p.batch * p.kv_heads;
+    const int unit = blockIdx.x % units;
+    rb = (int)(gridDim.x / units) - 1 - (int)(blockIdx.x / units);
+    kh = unit % p.kv_heads;
+    b = unit / p.kv_heads;
+  }
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
+  const int s0 = min(max(p.cum[b], 0), p.num_tokens);
+  const int s1 = min(max(p.cum[b + 1], s0), p.num_tokens);
+  const int nq = s1 - s0;
+  const int g = p.num_heads / p.kv_heads;
+  const int R = g * nq;
+  const int row0 = rb * ROWS;
+  if (row0 >= R) return;
+  const int pastb = clamped_past(p, b, nq);
+  const int total = pastb + nq;
+  int start, end;
+  bool single;
+  if (p.plan_items > 0) {
+    start = ustart;
+    end = max(ustart, min(uend, total));
+    single = part == 0;
+  } else {
+    start = split * p.chunk;
+    if (start >= total) return;
+    end = start + min(p.chunk, total - start);
+    single = start == 0 && end == total;
+  }
+  if (!single && p.part_o == nullptr) return;
+  const int r_last = min(row0 + ROWS, R) - 1;
+  const int hi_all = p.causal ? pastb + r_last / g + 1 : total;
+  const int lo_all = p.window > 0 ? max(0, pastb + row0 / g - p.window + 1) : 0;
+  const int t_first = max(start, (lo_all / kMxKeys) * kMxKeys);
+  const int t_last = min(end, hi_all);
+  const int nsteps = t_last > t_first ? (t_last - t_first + kMxKeys - 1) / kMxKeys : 0;
+
+  const WaveInfo w = make_wave(p, D, b, kh, s0, pastb, total);
+  // This lane's query row and the keys it sees.
+  const int r = row0 + 32 * wave + c;
+  const bool rvalid = r < R;
+  const int qi = rvalid ? r / g : 0, head = kh * g + (rvalid ? r % g : 0);
+  const int rpos = pastb + qi;
+  const int vis_lo = p.window > 0 ? rpos - p.window + 1 : 0;
+  const int vis_hi = rvalid ? (p.causal ? rpos + 1 : total) : -1;
+  const uint32_t qxor = p.scale < 0.0f ? 0x80008000u : 0u;
+  const float scale = fabsf(p.scale), scale_log2 = fabsf(p.scale_log2);
+  u32x4 qv[8];
+  {
+    const char* qrow = reinterpret_cast<const char*>(p.q) +
+                       (((int64_t)(s0 + qi) * p.num_heads + head) * D + 8 * h) * 2;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+      qv[ks] = rvalid ? (ld16(qrow + 32 * ks) ^ qxor) : u32x4{0u, 0u, 0u, 0u};
+  }
+  // Keys visible to some row [any_lo, any_hi) and to every row [all_lo, all_hi) of the wave.
+  int any_lo = 0, any_hi = -1, all_lo = 0, all_hi = -1;
+  {
+    const int wr0 = row0 + 32 * wave;
+    if (wr0 < R) {
+      const int qf = wr0 / g, ql = (min(wr0 + 32, R) - 1) / g;
+      any_hi = p.causal ? pastb + ql + 1 : total;
+      all_hi = min(end, p.causal ? pastb + qf + 1 : total);
+      any_lo = p.window > 0 ? pastb + qf - p.window + 1 : 0;
+      all_lo = p.window > 0 ? pastb + ql - p.window + 1 : 0;
+    }
+  }
+  f32x16 o[4];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[nt][i] = 0.0f;
+  float m_run = kNegInf, l_part = 0.0f;
+  // Value scale exponents the output quarters are accumulated in, and this wavefront's running
+  // scale of the quarter it stages (bf16 values; fp16 values are used unscaled).
+  constexpr int kS0 = std::is_same<TT, TBF16>::value ? -112 : 0;
+  int sv[4] = {kS0, kS0, kS0, kS0};
+  int s_stage = kS0;
+
+  PageWindow pw;
+  window_at(pw, w, min(div_bs(t_first, w), w.max_blocks - 1), lane);
+  MxStage st;
+  if (nsteps > 0) {
+    mx_load<TT>(w, pw, wave, lane, t_first, st);
+    mx_store<TT>(lds[0], st, wave, lane, t_first, total, s_stage);
+    if (nsteps > 1) mx_load<TT>(w, pw, wave, lane, t_first + kMxKeys, st);
+  }
+  __syncthreads();
+  for (int k = 0; k < nsteps; ++k) {
+    const int t0 = t_first + kMxKeys * k;
+    MxBuf& cur = lds[k & 1];
+    if (t0 < any_hi && t0 + kMxKeys > any_lo) {
+      // scores: two 32-key blocks, their accumulation chains interleaved
+      f32x16 sc[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sc[kb][i] = 0.0f;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) sc[kb] = mfma32<TT>(cur.k[kb][ks][lane], qv[ks], sc[kb]);
+      float x[2][16];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          float v = sc[kb][i];
+          if constexpr (CAP) v = p.softcap * tanhf(v * scale / p.softcap) * kLog2e;
+          x[kb][i] = v;
+        }
+      // per-score position tests only on steps some row does not see whole (one scalar branch)
+      if (!(t0 >= all_lo && t0 + kMxKeys <= all_hi)) {
+        const int base = t0 + 4 * h;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int pos = base + 32 * kb + 8 * (i >> 2) + (i & 3);
+            x[kb][i] = (pos < end && pos >= vis_lo && pos < vis_hi) ? x[kb][i] : kNegInf;
+          }
+      }
+      float lmax = kNegInf;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) lmax = fmaxf(lmax, x[kb][i]);
+      lmax = fmaxf(lmax, other_half(lmax));
+      if constexpr (!CAP) lmax *= scale_log2;
+      if (__any(lmax > m_run + 8.0f)) {
+        const float m_new = fmaxf(m_run, lmax);
+        const float alpha = (m_run == kNegInf || m_new == kNegInf) ? 1.0f : exp2f(m_run - m_new);
+        l_part *= alpha;
+        m_run = m_new;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) o[nt] *= alpha;
+      }
+      // value scales of this step: the output quarters follow a raised s exactly
+      {
+        const int4 vs4 = *reinterpret_cast<const int4*>(cur.vs);
+        const int vsn[4] = {__builtin_amdgcn_readfirstlane(vs4.x),
+                            __builtin_amdgcn_readfirstlane(vs4.y),
+                            __builtin_amdgcn_readfirstlane(vs4.z),
+                            __builtin_amdgcn_readfirstlane(vs4.w)};
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+          if (vsn[nt] != sv[nt]) {
+            const float f = __builtin_ldexpf(1.0f, sv[nt] - vsn[nt]);
+            o[nt] *= f;
+            sv[nt] = vsn[nt];
+          }
+      }
+      const float msafe = (m_run == kNegInf) ? 0.0f : m_run;
+      u32x4 pb[4];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        float pv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          pv[i] = __builtin_amdgcn_exp2f(CAP ? x[kb][i] - msafe
+                                             : __builtin_fmaf(x[kb][i], scale_log2, -msafe));
+          l_part += pv[i];
+        }
+#pragma unroll
+        for (int half = 0; half < 2; ++half)
+#pragma unroll
+          for (int m = 0; m < 4; ++m)
+            pb[2 * kb + half][m] = __builtin_bit_cast(
+                uint32_t, __builtin_convertvector(
+                              f32x2v{pv[8 * half + 2 * m], pv[8 * half + 2 * m + 1]}, f16x2v));
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+          o[nt] = mfma32<TF16>(cur.v[t][nt][mx_vslot(lane)], pb[t], o[nt]);
+    }
+    if (k + 1 < nsteps) mx_store<TT>(lds[(k + 1) & 1], st, wave, lane, t0 + kMxKeys, total, s_stage);
+    if (k + 2 < nsteps) mx_load<TT>(w, pw, wave, lane, t0 + 2 * kMxKeys, st);
+    __syncthreads();
+  }
+
+  // Epilogue: row r's output in true units is o[nt] * 2^sv[nt]; lanes l and l ^ 32 hold dims
+  // 8 i + 4 h + j of each quarter.
+  const float l_row = l_part + other_half(l_part);
+  if (!rvalid) return;
+  const int64_t tok = s0 + qi;
+  const float sink_c = sink_logit<TT>(p, head);
+  if (single) {
+    const float f = finalize_factor(m_run, l_row, sink_c);
+    typename TT::raw* dst = reinterpret_cast<typename TT::raw*>(p.out) + (tok * p.num_heads + head) * D;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const float fq = __builtin_ldexpf(f, sv[nt]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        u32x2 pk;
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+          pk[m] = (uint32_t)TT::from_f32(o[nt][4 * i + 2 * m] * fq) |
+                  ((uint32_t)TT::from_f32(o[nt][4 * i + 2 * m + 1] * fq) << 16);
+        *reinterpret_cast<u32x2*>(dst + 32 * nt + 8 * i + 4 * h) = pk;
+      }
+    }
+  } else if (p.plan_items == 0) {
+    // split-K chunk of the grid-order launch: fp32 partial (O, m, l) for split_reduce_kernel
+    const int64_t pi = (tok * p.num_heads + head) * p.max_splits + split;
+    float* dstf = p.part_o + pi * D;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f32x4 v4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v4[j] = __builtin_ldexpf(o[nt][4 * i + j], sv[nt]);
+        *reinterpret_cast<f32x4*>(dstf + 32 * nt + 8 * i + 4 * h) = v4;
+      }
+    if (h == 0) {
+      p.part_ml[pi * 2 + 0] = m_run;
+      p.part_ml[pi * 2 + 1] = l_row;
+    }
+  } else {
+    // fp16 partial row scaled by 2^-e (e from the row's largest |O|), e folded into (m, l)
+    float mx = 0.0f;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      float q = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) q = fmaxf(q, fabsf(o[nt][i]));
+      mx = fmaxf(mx, __builtin_ldexpf(q, sv[nt]));
+    }
+    mx = fmaxf(mx, other_half(mx));
+    const int ex = min(max(__builtin_amdgcn_frexp_expf(mx), -64), 126);
+    const int64_t pi = ((int64_t)item * 2 + part - 1) * ROWS + (r - row0);
+    char* dstb = reinterpret_cast<char*>(p.part_o) + pi * D * 2;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        u32x2 pk;
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          const _Float16 a = (_Float16)__builtin_ldexpf(o[nt][4 * i + 2 * m], sv[nt] - ex);
+          const _Float16 bb = (_Float16)__builtin_ldexpf(o[nt][4 * i + 2 * m + 1], sv[nt] - ex);
+          pk[m] = (uint32_t)__builtin_bit_cast(uint16_t, a) |
+                  ((uint32_t)__builtin_bit_cast(uint16_t, bb) << 16);
+        }
+        *reinterpret_cast<u32x2*>(dstb + (32 * nt + 8 * i + 4 * h) * 2) = pk;
+      }
+    if (h == 0) {
+      p.part_ml[pi * 2 + 0] = m_run + (float)ex;
+      p.part_ml[pi * 2 + 1] = __builtin_ldexpf(l_row, -ex);
+    }
+  }
+}
+
 // ----------------------------------------------------------------------------- planned prefill
 // Split threshold of the plan: items with more visible keys than PA_PLAN_SPLIT_PCT percent of a
 // slot's even share of all keys (and at least PA_PLAN_SPLIT_MIN keys) run as two halves.
@@ -330,7 +810,7 @@ __device__ __forceinline__ ItemKeys item_keys(const AttnParams& p, int i) {
   const int r_last = min(row0 + kPrefillRows, R) - 1;
   const int hi = p.causal ? pastb + r_last / g + 1 : total;
   const int lo = p.window > 0 ? max(0, pastb + row0 / g - p.window + 1) : 0;
-  const int first = (lo / 32) * 32;
+  const int first = (lo / p.plan_step) * p.plan_step;
   return ItemKeys{first, max(first, min(total, hi))};
 }
 
@@ -361,8 +841,15 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(const AttnParams p) {
   __syncthreads();
   const long long thr = max((long long)PA_PLAN_SPLIT_MIN,
                            (long long)(total_keys * PA_PLAN_SPLIT_PCT / 100) / max(p.plan_slots, 1));
-  auto bucket = [&](int len) { return NB - 1 - min((len + 31) / 32, NB - 1); };
-  auto split_of = [&](const ItemKeys& k) { return k.end - k.first > thr && k.end - k.first >= 64; };
+  const int step = p.plan_step;
+  auto bucket = [&](int len) { return NB - 1 - min((len + step - 1) / step, NB - 1); };
+  auto split_of = [&](const ItemKeys& k) {
+    return k.end - k.first > thr && k.end - k.first >= 2 * step;
+  };
+  // Halves split at a key-step boundary.
+  auto mid_of = [&](const ItemKeys& k) {
+    return k.first + (((k.end - k.first + step - 1) / step + 1) / 2) * step;
+  };
   for (int i = tid; i < p.plan_items; i += NT) {
     const ItemKeys k = item_keys(p, i);
     if (k.end < 0) {
@@ -372,7 +859,7 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(const AttnParams p) {
     const bool sp = split_of(k);
     p.plan_split[i] = sp ? 1 : 0;
     if (sp) {
-      const int mid = k.first + (((k.end - k.first + 31) / 32 + 1) / 2) * 32;
+      const int mid = mid_of(k);
       atomicAdd(&hist[bucket(mid - k.first)], 1);
       atomicAdd(&hist[bucket(k.end - mid)], 1);
     } else {
@@ -413,7 +900,7 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(const AttnParams p) {
     const ItemKeys k = item_keys(p, i);
     if (k.end < 0) continue;
     if (split_of(k)) {
-      const int mid = k.first + (((k.end - k.first + 31) / 32 + 1) / 2) * 32;
+      const int mid = mid_of(k);
       plan[atomicAdd(&hist[bucket(mid - k.first)], 1)] = int4{i, 1, k.first, mid};
       plan[atomicAdd(&hist[bucket(k.end - mid)], 1)] = int4{i, 2, mid, k.end};
     } else {
@@ -491,6 +978,13 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnParams p) 
 template <typename TT, int D>
 hipError_t launch_d(const AttnParams& p, dim3 grid, hipStream_t s) {
   constexpr int NG = kPrefillGroups;
+  if constexpr (D == 128) {
+    if (p.softcap > 0.0f)
+      hipLaunchKernelGGL((prefill_mx_kernel<TT, true>), grid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((prefill_mx_kernel<TT, false>), grid, dim3(256), 0, s, p);
+    return hipGetLastError();
+  }
   if (p.softcap > 0.0f)
     hipLaunchKernelGGL((prefill_kernel<TT, D, true, NG>), grid, dim3(256), 0, s, p);
   else
