@@ -300,19 +300,32 @@ int pa_paged_attention_static(const pa_paged_attention_node* node,
                               const pa_paged_attention_io* io, pa_stream_t stream);
 
 /* Operator-level entry: com.microsoft::GroupQueryAttention on contiguous caches
- * (group_query_attention_op / gqa_batched, attention.rs:932-1454 and :586-848), for the
- * shared-buffer contract: present_key/present_value are [batch, kv_heads, capacity, head]
- * buffers that already hold each sequence's past rows (past_key/past_value alias them) and
- * receive, in place, the seq new rows of batch b at [seqlens_k[b] + 1 - seq, seqlens_k[b] + 1).
- * Query rows attend causally over [0, seqlens_k[b] + 1) (plus window / softcap / sink).
- * RoPE (do_rotary) rotates the new query/key rows at those positions with the supplied cache
- * rows, per operation in T like the reference.  fp16/bf16 with head 64/128 and
- * (num_heads/kv_heads) * seq <= 16 run on the streaming matrix-core decode; everything else
- * (fp32, prefill chunks, other head sizes, integer caches) on the VALU kernel.  Messages of
- * invalid lengths start with "GroupQueryAttention:" (attention.rs:625-631, :668-672).
- * Integer present caches (cache_dtype PA_DTYPE_INT8 / PA_DTYPE_INT4, "kv_cache_bit_width" 8 /
- * 4) encode the new rows as sat(RNE(x * (1 / scale))) with a zero scale read as 1 (the MLAS
- * reciprocal rule, kv_cache.rs:183-190) and attend over code * scale of every row. */
+ * (group_query_attention_op / gqa_batched, attention.rs:932-1454 and :586-848).
+ * Per sequence b, with length = seqlens_k[b] + 1 (the reference's rules, attention.rs:614-672):
+ *   query_past = max(length - seq, 0); the seq query rows sit at positions query_past + i;
+ *   kv_seq == seq: the first length - query_past new key/value rows are stored at
+ *   [query_past, length) (a ragged first prompt, total_sequence_length == seq, stores only
+ *   `length` rows); kv_seq == 0: no new rows, the past already holds all `length` keys.
+ *   Row i attends keys [0, length) with the top-left causal rule p <= query_past + i, the
+ *   window rule p >= min(query_past + i, length - 1) - window + 1, an optional additive bias,
+ *   softcap, and a sink logit (head_sink, or 0 for smooth_softmax) in the denominator only.
+ *   present = [the length stored rows | past rows [length, past_capacity) | zero codes up to
+ *   present_capacity] (int4 zero codes are 0x88 bytes).
+ * Caches: present_key == past_key (the shared-buffer binding): updated in place, capacity
+ * past_capacity.  present_key of its own ([batch, kv_heads, present_capacity, head] with
+ * present_capacity = max(past_capacity, total_sequence_length), the growing present): past rows
+ * are copied in first.  present_key NULL (output omitted): the present lives in the workspace.
+ * past_key NULL (no past inputs): every sequence must be a first prompt.
+ * RoPE (do_rotary) rotates the query rows and the stored key rows at their positions with the
+ * supplied cache rows, each operation rounded to T like the reference's composed graph; with
+ * position_ids (input 9: first prompt, total_sequence_length == seq: rows pid[0] + i of every
+ * sequence; later calls: pid_flat[b * seq + i]) or kv_seq == 0 the rotation runs in fp32 and
+ * rounds once (gqa_rope_f32, attention.rs:506-521).  Messages of invalid inputs start with
+ * "GroupQueryAttention:".  Integer present caches (cache_dtype PA_DTYPE_INT8 / PA_DTYPE_INT4,
+ * "kv_cache_bit_width" 8 / 4) encode the new rows as sat(RNE(x * (1 / scale))) with a zero scale
+ * read as 1 (the MLAS reciprocal rule, kv_cache.rs:183-190) and attend over code * scale.
+ * fp16/bf16 head 64/128 decode batches (num_heads/kv_heads * seq <= 16) without a bias run on the
+ * streaming matrix-core decode; everything else on the VALU kernel. */
 typedef struct pa_gqa_node {
   int32_t num_heads;          /* "num_heads" */
   int32_t kv_num_heads;       /* "kv_num_heads" */
@@ -323,26 +336,39 @@ typedef struct pa_gqa_node {
   int32_t rotary_interleaved; /* "rotary_interleaved" */
   int32_t is_causal;          /* "causal" (1) */
   float qk_norm_epsilon;      /* "qk_norm_epsilon" (1e-6) */
+  int32_t smooth_softmax;     /* "smooth_softmax" == 1: a zero sink logit for every head */
 } pa_gqa_node;
 
 typedef struct pa_gqa_io {
   pa_dtype dtype;            /* T */
   int32_t batch;             /* query.shape[0] */
-  int32_t seq;               /* query.shape[1] (new tokens per sequence) */
-  int32_t query_hidden;      /* query.shape[2] = num_heads * head */
-  int32_t capacity;          /* present_key.shape[2] */
-  const void* query;         /* input 0 [batch, seq, num_heads * head] */
-  const void* key;           /* input 1 [batch, seq, kv_heads * head] */
+  int32_t seq;               /* query.shape[1] (query rows per sequence) */
+  int32_t query_hidden;      /* query.shape[2] = num_heads * head (packed: (H + 2 KV) * head) */
+  int32_t kv_seq;            /* key.shape[1]: seq, or 0 (no new rows; needs a past) */
+  const void* query;         /* input 0 [batch, seq, query_hidden] */
+  const void* key;           /* input 1 [batch, kv_seq, kv_heads * head] (NULL with value NULL
+                                and kv_seq == seq: packed QKV; unread when kv_seq == 0) */
   const void* value;         /* input 2 */
-  void* present_key;         /* inputs 3/outputs 1: [batch, kv_heads, capacity, head], in place */
-  void* present_value;       /* inputs 4/outputs 2 */
+  const void* past_key;      /* input 3 [batch, kv_heads, past_capacity, stored head] or NULL */
+  const void* past_value;    /* input 4 */
+  int32_t past_capacity;     /* input 3 shape[2] (0 when absent) */
+  void* present_key;         /* output 1 (== past_key, a buffer of its own, or NULL) */
+  void* present_value;       /* output 2 */
+  int32_t present_capacity;  /* output 1 shape[2] (ignored when present_key is NULL) */
   const int32_t* seqlens_k;  /* input 5 [batch], device */
   const int32_t* host_seqlens_k; /* host copy of input 5 (enables validation) or NULL */
-  int64_t total_sequence_length; /* input 6 (host scalar; used for validation) */
+  int64_t total_sequence_length; /* input 6 (host scalar) */
   const void* cos_cache;     /* input 7 [positions, rotary_dim / 2] */
   const void* sin_cache;     /* input 8 */
   int64_t rotary_positions;
   int32_t rotary_half;
+  const int64_t* position_ids;      /* input 9 [batch, position_cols] int64, device, or NULL */
+  const int64_t* host_position_ids; /* host copy of input 9 (validation) or NULL */
+  int32_t position_cols;
+  const void* attention_bias; /* input 10 [bias_batch, bias_heads, seq, total_sequence_length]
+                                 in T (additive, after scale and softcap), or NULL */
+  int32_t bias_batch;         /* 1 or batch */
+  int32_t bias_heads;         /* 1 or num_heads */
   const void* head_sink;     /* input 11 [num_heads] or NULL */
   const void* q_norm_weight; /* inputs 14/15 [head] or NULL */
   const void* k_norm_weight;
@@ -387,6 +413,33 @@ typedef struct pa_node_info {
 #define PA_UINT8_DTYPE 12
 
 int pa_paged_attention_claim(const pa_node_info* node, char* reason, size_t reason_len);
+
+/* Claim predicate for a GroupQueryAttention node (group_query_attention_claim,
+ * attention.rs:2407-2754, plus kv_cache::claim kv_cache.rs:16-108 for the present caches),
+ * restricted to what pa_group_query_attention executes: sliding_window_cache and the output_qk
+ * diagnostics (output 3) are declined with their reason.  Host only.  Returns 1 (claimed) or 0
+ * (declined, reason written). */
+typedef struct pa_gqa_node_info {
+  int32_t num_inputs;          /* 7..16 */
+  int32_t num_outputs;         /* 1..4 */
+  int32_t input_present[16];
+  int32_t input_dtype[16];     /* pa_dtype, or PA_INT32_DTYPE / PA_INT8_DTYPE / PA_UINT8_DTYPE /
+                                  PA_INT64_DTYPE */
+  int32_t input_rank[16];
+  int64_t input_shape[16][4];  /* -1: unknown (symbolic) dimension */
+  int32_t output_present[4];
+  int32_t output_dtype[4];
+  int32_t output_rank[4];
+  int64_t output_shape[4][4];
+  int32_t num_heads, kv_num_heads, do_rotary, is_causal, local_window_size;
+  int32_t sliding_window_cache, kv_cache_bit_width, smooth_softmax, qk_output;
+  float softcap;
+  /* "k_quant_type"/"v_quant_type": PA_QUANT_* (absent = PA_QUANT_NONE, any other string -1) */
+  int32_t k_quant_type, v_quant_type;
+} pa_gqa_node_info;
+#define PA_INT64_DTYPE 13
+
+int pa_group_query_attention_claim(const pa_gqa_node_info* node, char* reason, size_t reason_len);
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -190,7 +190,9 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
   pl.kind = kind;
   pl.balanced = kind == 1 && bal_ok;
   if (kind == 4) pl.kind = 1;
-  const int ctx = std::max(max_ctx_bound(c, b), 1);
+  // Longest context a sequence can have: the contiguous capacity, or the block table's.
+  const int ctx = std::max(
+      linear_cap > 0 ? std::min(linear_cap, INT32_MAX / 2) : max_ctx_bound(c, b), 1);
   if (pl.balanced) {
     // One wavefront per SIMD on every CU, each walking kDecodeMix sub-segments.
     pl.chunk = 32;
@@ -277,7 +279,16 @@ size_t workspace_for(const pa_cache* c, const pa_batch*, const pa_attn*, const P
 struct RunOpts {
   bool new_rows_in_cache = false;  // new rows sit in their block-table slots (see AttnParams)
   int linear_cap = 0;              // contiguous [batch, kv_heads, cap, d] caches (GQA present)
+  // GroupQueryAttention forms (see AttnParams): per-sequence key counts, additive bias, zero sink
+  const int32_t* key_limit = nullptr;
+  const void* bias = nullptr;
+  int bias_b = 0, bias_h = 0, bias_rows = 0, bias_cols = 0;
+  bool smooth_softmax = false;
 };
+
+// The kernel family a call with these options runs: a bias or per-sequence key counts beyond
+// what the decode kernels take send it to the VALU kernel.
+int effective_kind(int kind, const RunOpts& o) { return o.bias ? 3 : kind; }
 
 int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype act,
                   const void* q, const void* kn, const void* vn, void* out, void* ws,
@@ -315,6 +326,7 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
     return fail(PA_ERR_UNSUPPORTED, "prefill MFMA kernel does not cover this dtype/head_dim");
   if (!(a->softcap >= 0.0f) || !std::isfinite(a->softcap))
     return fail(PA_ERR_INVALID_ARGUMENT, "softcap must be finite and non-negative");
+  kind = effective_kind(kind, opts);
   Plan pl = make_plan(c, b, a, act, kind, chunk, opts.linear_cap > 0, opts.linear_cap);
   if (opts.linear_cap > 0 && !(pl.balanced || pl.kind == 3))
     return fail(PA_ERR_UNSUPPORTED, "contiguous caches run on the decode or VALU kernels only");
@@ -379,6 +391,13 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
       (opts.new_rows_in_cache || ((b->flags & PA_BATCH_NEW_ROWS_IN_CACHE) && !b->slot_mapping))
           ? 1
           : 0;
+  p.key_limit = opts.key_limit;
+  p.bias = opts.bias;
+  p.bias_b = opts.bias_b;
+  p.bias_h = opts.bias_h;
+  p.bias_rows = opts.bias_rows;
+  p.bias_cols = opts.bias_cols;
+  p.smooth_softmax = opts.smooth_softmax ? 1 : 0;
 
   hipError_t e;
   if (pl.balanced) {
@@ -473,12 +492,16 @@ int64_t pa_pool_bytes(const pa_pool* p) { return p ? p->bytes : 0; }
 // rule (see AppendParams).
 struct AppendExtra {
   int linear_cap = 0, seq = 0;
+  bool kv_rows = true;  // GroupQueryAttention: the call has new key/value rows
   const int32_t* seqlens_k = nullptr;
   int32_t* meta_out = nullptr;
   int64_t q_ld = 0, k_ld = 0, v_ld = 0;  // 0: contiguous rows
   void* v_out = nullptr;
   bool copy_rows = false;
   bool quant_reciprocal = false;
+  const int64_t* position_ids = nullptr;
+  bool pos_offset_form = false;
+  bool rope_fp32 = false;
 };
 
 static int rotary_append_impl(const pa_cache* c, const pa_batch* b, int32_t num_heads,
@@ -492,7 +515,7 @@ static int rotary_append_impl(const pa_cache* c, const pa_batch* b, int32_t num_
   if (rc) return rc;
   if ((rc = check_batch(b))) return rc;
   if (b->num_tokens == 0) return PA_OK;
-  if (!key || (!value && c->value_cache))
+  if (x.kv_rows && (!key || (!value && c->value_cache)))
     return fail(PA_ERR_INVALID_ARGUMENT, "key/value pointers are NULL");
   const bool rotate = cos != nullptr;
   if (rotate) {
@@ -542,6 +565,10 @@ static int rotary_append_impl(const pa_cache* c, const pa_batch* b, int32_t num_
   p.slots_distinct = (b->flags & PA_BATCH_SLOTS_DISTINCT) ? 1 : 0;
   p.linear_cap = x.linear_cap;
   p.gqa_seq = x.seq;
+  p.gqa_kv_rows = x.kv_rows ? 1 : 0;
+  p.position_ids = x.position_ids;
+  p.pos_offset_form = x.pos_offset_form ? 1 : 0;
+  p.rope_fp32 = x.rope_fp32 ? 1 : 0;
   p.seqlens_k = x.seqlens_k;
   p.meta_out = x.meta_out;
   p.q_ld = x.q_ld ? x.q_ld : (int64_t)num_heads * c->head_dim;
@@ -919,57 +946,103 @@ int pa_paged_attention_static(const pa_paged_attention_node* n, const pa_paged_a
 // ------------------------------------------------------------------------------ GQA
 namespace {
 
+// Workspace bytes of run_attention for these descriptors and options (the same plan).
+size_t attention_ws(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype act,
+                    const RunOpts& o) {
+  return workspace_for(c, b, a,
+                       make_plan(c, b, a, act, effective_kind(0, o), 0, o.linear_cap > 0,
+                                 o.linear_cap));
+}
+
 struct GqaLayout {
   int head;
   bool packed, transform;
-  size_t q_bytes, k_bytes, v_bytes, meta_off, attn_off, total;
+  bool shared;      // present == past: updated in place
+  bool in_ws;       // present omitted: it lives in the workspace
+  int cap_in;       // past capacity (0 without a past)
+  int cap_p;        // present capacity
+  size_t row_bytes; // bytes of one stored row of one kv-head
+  size_t q_bytes, k_bytes, v_bytes, meta_off, pres_off, pres_side, attn_off, total;
   pa_cache cache;
   pa_batch batch;
   pa_attn attn;
+  RunOpts opts;
 };
 
-// group_query_attention_op / gqa_batched (attention.rs:932-1454, :586-848) restricted to the
-// shared-buffer contract: present_key/value ([batch, kv_heads, capacity, head]) already hold the
-// past rows and receive the seq new rows of batch b at [seqlens_k[b] + 1 - seq, seqlens_k[b] + 1).
+// group_query_attention_op / gqa_batched (attention.rs:932-1454, :586-848): shapes, caches and the
+// workspace [rotated q | rotated k | packed v | metadata | present (when omitted) | attention].
 int gqa_layout(const pa_gqa_node* n, const pa_gqa_io* io, GqaLayout* L) {
   if (!n || !io) return fail(PA_ERR_INVALID_ARGUMENT, "node/io is NULL");
   if (n->num_heads <= 0 || n->kv_num_heads <= 0 || n->num_heads % n->kv_num_heads != 0)
     return fail(PA_ERR_INVALID_ARGUMENT, "GroupQueryAttention: bad num_heads/kv_num_heads");
   // Key and value absent together: packed [B, S, (H + 2 KV) * head] query (attention.rs:2487).
-  L->packed = io->key == nullptr && io->value == nullptr;
-  if (!L->packed && (io->key == nullptr || io->value == nullptr))
+  // With kv_seq == 0 the (empty) key/value pointers are not read.
+  L->packed = io->kv_seq > 0 && io->key == nullptr && io->value == nullptr;
+  if (!L->packed && io->kv_seq > 0 && (io->key == nullptr || io->value == nullptr))
     return fail(PA_ERR_INVALID_ARGUMENT,
                 "GroupQueryAttention: key and value must both be present or both be absent");
-  if (io->batch < 1 || io->seq < 1 || io->capacity < 1)
+  if (io->batch < 1 || io->seq < 1)
     return fail(PA_ERR_INVALID_ARGUMENT,
-                "GroupQueryAttention: batch, sequence and capacity must be positive");
+                "GroupQueryAttention: batch and sequence length must be positive");
+  if ((io->kv_seq != io->seq && io->kv_seq != 0) ||
+      (io->kv_seq == 0 && (L->packed || io->past_key == nullptr)))
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "GroupQueryAttention: K/V must match Q sequence or be empty with paired "
+                "non-sliding past");
+  if ((io->past_key == nullptr) != (io->past_value == nullptr))
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "GroupQueryAttention: past_key and past_value must be provided together");
+  if ((io->present_key == nullptr) != (io->present_value == nullptr))
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "GroupQueryAttention: present_key and present_value must both be provided or "
+                "both omitted");
   const int qheads = L->packed ? n->num_heads + 2 * n->kv_num_heads : n->num_heads;
   if (io->query_hidden <= 0 || io->query_hidden % qheads != 0)
     return fail(PA_ERR_INVALID_ARGUMENT,
                 "GroupQueryAttention: query hidden size is not divisible by its head count");
   if (!is_act(io->dtype))
     return fail(PA_ERR_UNSUPPORTED, "activation dtype must be fp16/bf16/fp32");
-  if (!io->query || !io->present_key || !io->present_value || !io->seqlens_k || !io->output)
+  if (!io->query || !io->seqlens_k || !io->output)
     return fail(PA_ERR_INVALID_ARGUMENT, "GroupQueryAttention: required pointers are NULL");
-  if ((int64_t)io->batch * n->kv_num_heads * io->capacity > (int64_t)INT32_MAX)
+  const int64_t total = io->total_sequence_length;
+  if (total <= 0 || total > INT32_MAX)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "GroupQueryAttention: invalid per-batch or maximum sequence lengths");
+  L->cap_in = io->past_key ? io->past_capacity : 0;
+  if (io->past_key && io->past_capacity < 1)
+    return fail(PA_ERR_INVALID_ARGUMENT, "GroupQueryAttention: past cache capacity must be positive");
+  L->shared = io->present_key && io->present_key == io->past_key;
+  if (L->shared != (io->present_value && io->present_value == io->past_value))
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "GroupQueryAttention: present_key and present_value must both alias the past "
+                "or neither");
+  L->in_ws = io->present_key == nullptr;
+  const int64_t grown = std::max<int64_t>(L->cap_in, total);
+  if (L->shared) {
+    L->cap_p = L->cap_in;
+  } else if (!L->in_ws) {
+    if (io->present_capacity != grown)
+      return fail(PA_ERR_INVALID_ARGUMENT,
+                  "GroupQueryAttention: present must be [batch,kv_num_heads,max(past capacity,"
+                  "total_sequence_length),head]");
+    L->cap_p = io->present_capacity;
+  } else {
+    L->cap_p = (int)grown;
+  }
+  if ((int64_t)io->batch * n->kv_num_heads * L->cap_p > (int64_t)INT32_MAX)
     return fail(PA_ERR_UNSUPPORTED, "GroupQueryAttention: present cache has more than 2^31 rows");
   L->head = io->query_hidden / qheads;
   L->transform = (n->do_rotary != 0) || io->q_norm_weight != nullptr || L->packed;
   const int64_t T = (int64_t)io->batch * io->seq;
   const size_t es = elem_size(io->dtype);
+  const bool kv_rows = io->kv_seq != 0;
   L->q_bytes = L->transform ? align256((size_t)T * n->num_heads * L->head * es) : 0;
-  L->k_bytes = L->transform ? align256((size_t)T * n->kv_num_heads * L->head * es) : 0;
+  L->k_bytes = (L->transform && kv_rows) ? align256((size_t)T * n->kv_num_heads * L->head * es) : 0;
   L->v_bytes = L->packed ? align256((size_t)T * n->kv_num_heads * L->head * es) : 0;
   L->meta_off = L->q_bytes + L->k_bytes + L->v_bytes;
-  L->attn_off = L->meta_off + align256((size_t)(2 * io->batch + 1) * sizeof(int32_t));
+  L->pres_off = L->meta_off + align256((size_t)(3 * io->batch + 1) * sizeof(int32_t));
   pa_cache& c = L->cache;
   c = pa_cache{};
-  c.key_cache = io->present_key;
-  c.value_cache = io->present_value;
-  c.block_size = 16;  // geometry for the plan only: rows are addressed contiguously
-  c.num_blocks = ((int64_t)io->batch * n->kv_num_heads * io->capacity + 15) / 16;
-  c.kv_heads = n->kv_num_heads;
-  c.head_dim = L->head;
   c.dtype = io->cache_dtype == 0 ? io->dtype : io->cache_dtype;
   if (c.dtype != io->dtype && !is_int_cache(c.dtype))
     return fail(PA_ERR_UNSUPPORTED,
@@ -977,6 +1050,16 @@ int gqa_layout(const pa_gqa_node* n, const pa_gqa_io* io, GqaLayout* L) {
   if (c.dtype == PA_DTYPE_INT4 && L->head % 2 != 0)
     return fail(PA_ERR_UNSUPPORTED,
                 "GroupQueryAttention: packed INT4 requires an even logical head size");
+  L->row_bytes = cache_head_bytes(c.dtype, L->head);
+  L->pres_side = L->in_ws ? align256((size_t)io->batch * n->kv_num_heads * L->cap_p * L->row_bytes) : 0;
+  L->attn_off = L->pres_off + 2 * L->pres_side;
+  // The cache pointers are set per call (the present may live in the workspace).
+  c.key_cache = io->present_key ? io->present_key : const_cast<void*>(io->query);
+  c.value_cache = io->present_value ? io->present_value : const_cast<void*>(io->query);
+  c.block_size = 16;  // geometry for the plan only: rows are addressed contiguously
+  c.num_blocks = ((int64_t)io->batch * n->kv_num_heads * L->cap_p + 15) / 16;
+  c.kv_heads = n->kv_num_heads;
+  c.head_dim = L->head;
   c.k_scale = io->k_scale;
   c.v_scale = io->v_scale;
   c.k_quant_type = is_int_cache(c.dtype) ? io->k_quant_type : PA_QUANT_NONE;
@@ -996,16 +1079,25 @@ int gqa_layout(const pa_gqa_node* n, const pa_gqa_io* io, GqaLayout* L) {
   a.local_window_size = n->local_window_size;
   a.is_causal = n->is_causal;
   a.head_sink = io->head_sink;
-  L->total = L->attn_off + pa_attention_workspace_bytes_ex(&c, &b, &a, io->dtype, 0, 0);
+  RunOpts& o = L->opts;
+  o = RunOpts{};
+  o.new_rows_in_cache = true;
+  o.linear_cap = L->cap_p;
+  o.bias = io->attention_bias;
+  o.bias_b = io->bias_batch;
+  o.bias_h = io->bias_heads;
+  o.bias_rows = io->seq;
+  o.bias_cols = (int)total;
+  o.smooth_softmax = n->smooth_softmax == 1;
+  L->total = L->attn_off + attention_ws(&c, &b, &a, io->dtype, o);
   return PA_OK;
 }
 
-// gqa_batched's length rules (attention.rs:614-631, :665-672), plus the shared-buffer
-// requirement that every sequence holds all seq new rows inside the capacity.
-int validate_gqa_lengths(const pa_gqa_io* io) {
+// gqa_batched's length rules (attention.rs:614-631, :665-672) and its cache bound (:695-700).
+int validate_gqa_lengths(const pa_gqa_io* io, const GqaLayout& L) {
   const int32_t* len = io->host_seqlens_k;
   const int64_t total = io->total_sequence_length;
-  bool bad = total <= 0 || total > INT32_MAX;
+  bool bad = false;
   int64_t mx = -1;
   for (int b = 0; b < io->batch && !bad; ++b) {
     const int64_t v = len[b];
@@ -1015,10 +1107,46 @@ int validate_gqa_lengths(const pa_gqa_io* io) {
   if (bad || mx != total - 1)
     return fail(PA_ERR_INVALID_ARGUMENT,
                 "GroupQueryAttention: invalid per-batch or maximum sequence lengths");
-  for (int b = 0; b < io->batch; ++b)
-    if ((int64_t)len[b] + 1 < io->seq || (int64_t)len[b] + 1 > io->capacity)
+  for (int b = 0; b < io->batch; ++b) {
+    const int64_t length = (int64_t)len[b] + 1;
+    const int64_t qp = std::max<int64_t>(length - io->seq, 0);
+    const int64_t past = io->kv_seq == 0 ? length : qp;
+    if (past > L.cap_in || (!io->past_key && past != 0) || length > L.cap_p)
       return fail(PA_ERR_INVALID_ARGUMENT,
                   "GroupQueryAttention: sequence length exceeds available past cache");
+  }
+  return PA_OK;
+}
+
+// Rotary rows the call reads: positions query_past + i (cos_sin_row, attention.rs:523-535), or
+// the position ids (gqa_rotary_rows :538-584).
+int validate_gqa_rotary(const pa_gqa_io* io) {
+  const int64_t rows = io->rotary_positions, S = io->seq;
+  if (io->position_ids) {
+    if (io->position_cols < S)
+      return fail(PA_ERR_INVALID_ARGUMENT,
+                  "GroupQueryAttention: position_ids must be int64 [batch,>=sequence]");
+    const int64_t* pid = io->host_position_ids;
+    if (!pid) return PA_OK;  // device ids: kernels leave rows outside the cache unrotated
+    if (io->total_sequence_length == S) {
+      if (pid[0] < 0 || pid[0] > rows - S)
+        return fail(PA_ERR_INVALID_ARGUMENT,
+                    "GroupQueryAttention: position_ids exceed the supplied cache");
+    } else {
+      for (int64_t i = 0; i < (int64_t)io->batch * S; ++i)
+        if (pid[i] < 0 || pid[i] >= rows)
+          return fail(PA_ERR_INVALID_ARGUMENT,
+                      "GroupQueryAttention: position_ids exceed the supplied cache");
+    }
+    return PA_OK;
+  }
+  if (!io->host_seqlens_k) return PA_OK;
+  for (int b = 0; b < io->batch; ++b) {
+    const int64_t qp = std::max<int64_t>((int64_t)io->host_seqlens_k[b] + 1 - S, 0);
+    if (qp > rows - S)
+      return fail(PA_ERR_INVALID_ARGUMENT,
+                  "RotaryEmbedding: requested positions exceed the supplied cache");
+  }
   return PA_OK;
 }
 
@@ -1035,7 +1163,7 @@ int pa_group_query_attention(const pa_gqa_node* n, const pa_gqa_io* io, void* wo
   GqaLayout L;
   int rc = gqa_layout(n, io, &L);
   if (rc) return rc;
-  if (io->host_seqlens_k && (rc = validate_gqa_lengths(io))) return rc;
+  if (io->host_seqlens_k && (rc = validate_gqa_lengths(io, L))) return rc;
   if (n->local_window_size != -1 && n->local_window_size <= 0)
     return fail(PA_ERR_INVALID_ARGUMENT,
                 "GroupQueryAttention: local_window_size must be -1 or positive");
@@ -1045,6 +1173,13 @@ int pa_group_query_attention(const pa_gqa_node* n, const pa_gqa_io* io, void* wo
   if (n->do_rotary && (io->rotary_half <= 0 || 2 * io->rotary_half > L.head))
     return fail(PA_ERR_INVALID_ARGUMENT,
                 "GroupQueryAttention: rotary dimension must not exceed head_size");
+  if (n->do_rotary && (rc = validate_gqa_rotary(io))) return rc;
+  if (io->attention_bias &&
+      !((io->bias_batch == 1 || io->bias_batch == io->batch) &&
+        (io->bias_heads == 1 || io->bias_heads == n->num_heads)))
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "GroupQueryAttention: attention_bias must broadcast to "
+                "[batch,heads,sequence,total]");
   if (workspace_bytes < L.total || !workspace)
     return fail(PA_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes, got %zu", L.total,
                 workspace_bytes);
@@ -1054,17 +1189,48 @@ int pa_group_query_attention(const pa_gqa_node* n, const pa_gqa_io* io, void* wo
   L.batch.cumulative_sequence_length = meta;
   L.batch.past_seqlens = meta + io->batch + 1;
   L.batch.block_table = meta;  // unused for contiguous caches
+  L.opts.key_limit = meta + 2 * io->batch + 1;
+  if (L.in_ws) {
+    L.cache.key_cache = ws + L.pres_off;
+    L.cache.value_cache = ws + L.pres_off + L.pres_side;
+  }
+  // The present starts as [past rows | zero codes] unless it is the past buffer itself
+  // (gqa_batched builds [stored | past tail | zeros], attention.rs:790-818).
+  if (!L.shared) {
+    const size_t pitch = (size_t)L.cap_p * L.row_bytes;
+    const size_t keep = (size_t)std::min(L.cap_in, L.cap_p) * L.row_bytes;
+    const size_t rows = (size_t)io->batch * n->kv_num_heads;
+    const int zero = L.cache.dtype == PA_DTYPE_INT4 ? 0x88 : 0;
+    for (int side = 0; side < 2; ++side) {
+      char* dst = reinterpret_cast<char*>(side ? L.cache.value_cache : L.cache.key_cache);
+      const void* src = side ? io->past_value : io->past_key;
+      hipError_t e = hipSuccess;
+      if (src && keep > 0)
+        e = hipMemcpy2DAsync(dst, pitch, src, (size_t)L.cap_in * L.row_bytes, keep, rows,
+                             hipMemcpyDeviceToDevice, s);
+      if (e == hipSuccess && pitch > keep)
+        e = hipMemset2DAsync(dst + keep, pitch, zero, pitch - keep, rows, s);
+      if (e != hipSuccess) return hip_fail(e, "present cache set-up");
+    }
+  }
   void* q_rot = L.transform ? ws : nullptr;
-  void* k_rot = L.transform ? ws + L.q_bytes : nullptr;
+  void* k_rot = L.k_bytes ? ws + L.q_bytes : nullptr;
   void* v_rows = L.packed ? ws + L.q_bytes + L.k_bytes : nullptr;
-  const void* key = io->key;
-  const void* value = io->value;
+  const void* key = io->kv_seq ? io->key : nullptr;
+  const void* value = io->kv_seq ? io->value : nullptr;
   AppendExtra x;
-  x.linear_cap = io->capacity;
+  x.linear_cap = L.cap_p;
   x.seq = io->seq;
+  x.kv_rows = io->kv_seq != 0;
   x.seqlens_k = io->seqlens_k;
   x.meta_out = meta;
   x.quant_reciprocal = true;  // MLAS GQA encode: x * (1 / scale), zero scale read as 1
+  if (n->do_rotary && io->position_ids) {
+    x.position_ids = io->position_ids;
+    x.pos_offset_form = io->total_sequence_length == io->seq;
+  }
+  // gqa_rope_f32 for position ids or an empty key/value (attention.rs:716-720)
+  x.rope_fp32 = n->do_rotary && (io->position_ids != nullptr || io->kv_seq == 0);
   if (L.packed) {
     const size_t es = elem_size(io->dtype);
     const char* qkv = reinterpret_cast<const char*>(io->query);
@@ -1080,14 +1246,11 @@ int pa_group_query_attention(const pa_gqa_node* n, const pa_gqa_io* io, void* wo
                           io->rotary_half, 0, n->rotary_interleaved, io->q_norm_weight,
                           io->k_norm_weight, n->qk_norm_epsilon, s, x);
   if (rc) return rc;
-  RunOpts opts;
-  opts.new_rows_in_cache = true;
-  opts.linear_cap = io->capacity;
   const void* q = L.transform ? q_rot : io->query;
-  const void* kn = L.transform ? k_rot : key;
-  const void* vn = L.packed ? v_rows : value;
+  const void* kn = k_rot ? k_rot : (key ? key : io->query);
+  const void* vn = L.packed ? v_rows : (value ? value : io->query);
   return run_attention(&L.cache, &L.batch, &L.attn, io->dtype, q, kn, vn, io->output,
-                       ws + L.attn_off, workspace_bytes - L.attn_off, 0, 0, s, opts);
+                       ws + L.attn_off, workspace_bytes - L.attn_off, 0, 0, s, L.opts);
 }
 
 // ------------------------------------------------------------------------------ claim
@@ -1262,6 +1425,181 @@ int pa_paged_attention_claim(const pa_node_info* n, char* reason, size_t reason_
   for (int i = 1; i < std::min(n->num_outputs, 3); ++i)
     if (out_present(i) && n->output_dtype[i] != n->input_dtype[i + 2])
       return deny("cache output %d must retain cache storage dtype", i);
+  return 1;
+}
+
+// group_query_attention_claim (attention.rs:2407-2628) + kv_cache::claim for contiguous caches
+// (kv_cache.rs:16-108, scales at inputs 12/13), restricted to what pa_group_query_attention
+// executes: sliding_window_cache and the output_qk diagnostics are declined.
+int pa_group_query_attention_claim(const pa_gqa_node_info* n, char* reason, size_t reason_len) {
+  auto deny = [&](const char* fmt, ...) {
+    if (reason && reason_len) {
+      va_list ap;
+      va_start(ap, fmt);
+      vsnprintf(reason, reason_len, fmt, ap);
+      va_end(ap);
+    }
+    return 0;
+  };
+  if (!n) return deny("node info is NULL");
+  if (reason && reason_len) reason[0] = 0;
+  auto present = [&](int i) { return i < n->num_inputs && n->input_present[i] != 0; };
+  auto out_present = [&](int i) { return i < n->num_outputs && n->output_present[i] != 0; };
+  auto shape = [&](int i, int d) { return n->input_shape[i][d]; };
+  const int I32 = PA_INT32_DTYPE;
+  if (n->num_outputs < 1 || n->num_outputs > 4) return deny("requires 1 to 4 outputs");
+  if (out_present(1) != out_present(2))
+    return deny("present_key and present_value must both be provided or both omitted");
+  const bool sliding = n->sliding_window_cache != 0;
+  if (n->is_causal != 0 && n->is_causal != 1) return deny("causal must be 0 or 1");
+  const int window = n->local_window_size;
+  if (!(window == -1 || window > 0)) return deny("local_window_size must be -1 or positive");
+  if (n->is_causal == 0 && window != -1)
+    return deny("bidirectional GroupQueryAttention requires local_window_size=-1");
+  if (present(3) != present(4)) return deny("past_key and past_value must be provided together");
+  const int out_dt = n->output_dtype[0];
+  if (!out_present(0) || !is_act((pa_dtype)out_dt))
+    return deny("output must have an MLX float dtype");
+  if (n->num_inputs < 7 || n->num_inputs > 16)
+    return deny("expects 7 required inputs plus optional rotary/bias/QK-norm inputs, got %d",
+                n->num_inputs);
+  const bool has_bias = present(10), do_rotary = n->do_rotary != 0;
+  if (n->num_inputs == 7 && do_rotary)
+    return deny("7-input GroupQueryAttention requires do_rotary=0 because cos/sin caches are "
+                "absent");
+  if (sliding) return deny("sliding_window_cache is not executed by this build");
+  const bool packed = present(0) && !present(1) && !present(2);
+  if (!packed && !(present(0) && present(1) && present(2)))
+    return deny("Q/K/V must be either all separate or packed in input 0 with inputs 1 and 2 "
+                "absent");
+  const bool quantized =
+      present(3) && (n->input_dtype[3] == PA_INT8_DTYPE || n->input_dtype[3] == PA_UINT8_DTYPE);
+  int float_idx[10], nf = 0;
+  float_idx[nf++] = 0;
+  if (!packed) float_idx[nf++] = 1, float_idx[nf++] = 2;
+  if (present(3) && !quantized) float_idx[nf++] = 3, float_idx[nf++] = 4;
+  if (do_rotary) float_idx[nf++] = 7, float_idx[nf++] = 8;
+  if (has_bias) float_idx[nf++] = 10;
+  if (present(14)) float_idx[nf++] = 14, float_idx[nf++] = 15;
+  for (int k = 0; k < nf; ++k) {
+    const int i = float_idx[k];
+    if (!present(i)) return deny("input %d lacks tensor type/shape info", i);
+    if (n->input_dtype[i] != out_dt) return deny("input %d must have the output dtype", i);
+  }
+  for (int i = 1; i < std::min(n->num_outputs, 3); ++i)
+    if (out_present(i) && n->output_dtype[i] != (present(i + 2) ? n->input_dtype[i + 2] : out_dt))
+      return deny("output %d must retain its cache dtype", i);
+  for (int i : {5, 6})
+    if (!present(i) || n->input_dtype[i] != I32) return deny("input %d must have int32 dtype", i);
+  if (has_bias && n->input_rank[10] != 4)
+    return deny("attention_bias (input 10) must have rank 4, got rank %d", n->input_rank[10]);
+  const int64_t nh = n->num_heads, kvh = n->kv_num_heads;
+  if (!(nh > 0 && kvh > 0 && nh % kvh == 0))
+    return deny("num_heads (%lld) must be a positive multiple of kv_num_heads (%lld)",
+                (long long)nh, (long long)kvh);
+  if (n->input_rank[0] != 3 || shape(0, 2) <= 0)
+    return deny("query must have rank 3 and a positive static hidden size");
+  const int64_t total_heads = packed ? nh + 2 * kvh : nh;
+  if (shape(0, 2) % total_heads != 0) return deny("query hidden size must match head count");
+  const int64_t head = shape(0, 2) / total_heads;
+  if (head > kMaxHeadDim)
+    return deny("head_size %lld is not executed by this build", (long long)head);
+  // kv_cache::claim: one storage dtype; integer caches need PER_TENSOR/PER_CHANNEL fp32 scales.
+  const int cache_dt = present(3) ? n->input_dtype[3] : out_dt;
+  for (int side = 0; side < 2; ++side) {
+    const int cache_in = 3 + side, scale_in = 12 + side;
+    const char* nm = side ? "v" : "k";
+    const int dt = present(cache_in) ? n->input_dtype[cache_in] : out_dt;
+    if (dt != cache_dt) return deny("key/value caches must share one storage dtype");
+    const int mode = side ? n->v_quant_type : n->k_quant_type;
+    if (quantized) {
+      if (mode != PA_QUANT_PER_TENSOR && mode != PA_QUANT_PER_CHANNEL)
+        return deny("integer %s cache requires PER_TENSOR or PER_CHANNEL quantization", nm);
+      if (!present(scale_in)) return deny("quantized %s cache requires a scale tensor", nm);
+      if (n->input_dtype[scale_in] != PA_DTYPE_FLOAT32) return deny("%s_scale must be float32", nm);
+      const int rank = n->input_rank[scale_in];
+      int64_t count = 1;
+      bool known = rank >= 0 && rank <= 4;
+      for (int d = 0; known && d < rank; ++d) {
+        if (shape(scale_in, d) < 0) known = false;
+        else count *= shape(scale_in, d);
+      }
+      const int64_t expected = mode == PA_QUANT_PER_TENSOR ? 1 : kvh * head;
+      if (known && count != expected)
+        return deny("%s_scale must contain %lld elements", nm, (long long)expected);
+    } else if (!(dt == out_dt && mode == PA_QUANT_NONE && !present(scale_in))) {
+      return deny("floating %s cache requires activation dtype, NONE quantization and no scale",
+                  nm);
+    }
+    if (out_present(1 + side) && n->output_dtype[1 + side] != dt)
+      return deny("present %s cache must retain its input storage dtype", nm);
+  }
+  const int bits_expected =
+      cache_dt == PA_INT8_DTYPE ? 8 : cache_dt == PA_UINT8_DTYPE ? 4 : 0;
+  if (n->kv_cache_bit_width != bits_expected)
+    return deny("kv_cache_bit_width must agree with cache storage");
+  if (n->kv_cache_bit_width == 4 && head % 2 != 0)
+    return deny("GQA packed INT4 requires an even logical head size (pinned CheckPast byte "
+                "geometry)");
+  const int64_t cache_head = n->kv_cache_bit_width == 4 ? (head + 1) / 2 : head;
+  const int64_t qb = shape(0, 0), qs = shape(0, 1);
+  if (has_bias &&
+      !((shape(10, 0) < 0 || shape(10, 0) == 1 || qb < 0 || shape(10, 0) == qb) &&
+        (shape(10, 1) < 0 || shape(10, 1) == 1 || shape(10, 1) == nh) &&
+        (shape(10, 2) < 0 || qs < 0 || shape(10, 2) == qs)))
+    return deny("attention_bias must broadcast to "
+                "[batch,num_heads,sequence_length,total_sequence_length]");
+  if (!packed) {
+    for (int i : {1, 2}) {
+      const int64_t kb = shape(i, 0), ks = shape(i, 1);
+      if (!(n->input_rank[i] == 3 && shape(i, 2) == kvh * head &&
+            (kb < 0 || qb < 0 || kb == qb) &&
+            (ks < 0 || qs < 0 || ks == qs || (ks == 0 && present(3)))))
+        return deny("key/value must match query batch, sequence length and KV head geometry");
+    }
+    for (int d = 0; d < 3; ++d)
+      if (shape(1, d) != shape(2, d)) return deny("key/value shapes must match");
+  }
+  for (int i : {3, 4}) {
+    if (!present(i)) continue;
+    if (!(n->input_rank[i] == 4 && shape(i, 1) == kvh && shape(i, 3) == cache_head &&
+          (shape(i, 0) < 0 || qb < 0 || shape(i, 0) == qb)))
+      return deny("past cache must be [batch,kv_num_heads,capacity,stored_head_size]");
+  }
+  if (present(3))
+    for (int d = 0; d < 4; ++d)
+      if (shape(3, d) != shape(4, d)) return deny("past key/value cache shapes must match");
+  if (!(n->input_rank[5] == 1 && (shape(5, 0) < 0 || qb < 0 || shape(5, 0) == qb)))
+    return deny("seqlens_k must be [batch]");
+  if (!(n->input_rank[6] == 0 || (n->input_rank[6] == 1 && shape(6, 0) == 1)))
+    return deny("total_sequence_length must be scalar or [1]");
+  if (do_rotary &&
+      !(n->input_rank[7] == 2 && n->input_rank[8] == 2 && shape(7, 0) == shape(8, 0) &&
+        shape(7, 1) == shape(8, 1) && shape(7, 1) > 0 && 2 * shape(7, 1) <= head))
+    return deny("rotary caches must have matching [positions,rotary_dim/2] shapes within the "
+                "head");
+  if (present(9) && do_rotary &&
+      !(n->input_dtype[9] == PA_INT64_DTYPE && n->input_rank[9] == 2 &&
+        (shape(9, 0) < 0 || qb < 0 || shape(9, 0) == qb) &&
+        (shape(9, 1) < 0 || qs < 0 || shape(9, 1) >= qs)))
+    return deny("position_ids must be int64 [batch,>=sequence_length]");
+  if (present(11) &&
+      !(n->input_dtype[11] == out_dt && n->input_rank[11] == 1 && shape(11, 0) == nh))
+    return deny("head_sink must be [num_heads] in activation dtype");
+  if (present(14) != present(15))
+    return deny("q_norm_weight and k_norm_weight must be provided together");
+  if (present(14))
+    for (int i : {14, 15})
+      if (!(n->input_rank[i] == 1 && shape(i, 0) == head))
+        return deny("Q/K norm weight %d must have shape [head_size=%lld]", i, (long long)head);
+  if (n->smooth_softmax < -1 || n->smooth_softmax > 1)
+    return deny("smooth_softmax must be -1 (schema default), 0 or 1");
+  const int qk = n->qk_output;
+  if (!(qk >= 0 && qk <= 2 && (qk != 0) == out_present(3)))
+    return deny("qk_output must be 0, 1 or 2 and enabled exactly when output_qk is present");
+  if (qk != 0) return deny("output_qk diagnostics are not executed by this build");
+  if (!std::isfinite(n->softcap) || n->softcap < 0.0f)
+    return deny("softcap must be finite and non-negative");
   return 1;
 }
 

@@ -126,14 +126,7 @@ __device__ void process_row(const AppendParams& p, const void* src, int64_t src_
   const int D = p.head_dim;
   float inv = 1.0f;
   if (norm_w) {
-    float acc = 0.0f;
-    for (int e = lane; e < D; e += 64) {
-      float v = ldv<TT>(src, src_base + e);
-      acc += v * v;
-    }
-    // Reduction order differs from a sequential sum; fp32 sums of <=256 squares of values that
-    // are already in T agree with the sequential order to well under one T ulp of the result.
-    acc = wave_sum(acc);
+    const float acc = sum_squares([&](int e) { return ldv<TT>(src, src_base + e); }, D, lane);
     inv = 1.0f / __builtin_sqrtf(acc / (float)D + p.norm_eps);
   }
   auto fetch = [&](int e) -> float {
@@ -156,8 +149,14 @@ __device__ void process_row(const AppendParams& p, const void* src, int64_t src_
     int e1 = p.rotary_interleaved ? off + 2 * i : off + i;
     int e2 = p.rotary_interleaved ? off + 2 * i + 1 : off + half + i;
     float a = fetch(e1), b = fetch(e2);
-    float o1 = rnd<TT>(rnd<TT>(a * c) - rnd<TT>(b * s));
-    float o2 = rnd<TT>(rnd<TT>(b * c) + rnd<TT>(a * s));
+    float o1, o2;
+    if (p.rope_fp32) {  // each operation rounded to fp32, one rounding to T (gqa_rope_f32)
+      o1 = rnd<TT>(__fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s)));
+      o2 = rnd<TT>(__fadd_rn(__fmul_rn(b, c), __fmul_rn(a, s)));
+    } else {
+      o1 = rnd<TT>(rnd<TT>(a * c) - rnd<TT>(b * s));
+      o2 = rnd<TT>(rnd<TT>(b * c) + rnd<TT>(a * s));
+    }
     put(e1, o1);
     put(e2, o2);
   }
@@ -197,12 +196,7 @@ __device__ void int_row(const AppendParams& p, const void* src, int64_t sbase, v
   const int D = p.head_dim;
   float inv = 1.0f;
   if (norm_w) {
-    float acc = 0.0f;
-    for (int e = lane; e < D; e += 64) {
-      float v = ldv<TT>(src, sbase + e);
-      acc += v * v;
-    }
-    acc = wave_sum(acc);
+    const float acc = sum_squares([&](int e) { return ldv<TT>(src, sbase + e); }, D, lane);
     inv = 1.0f / __builtin_sqrtf(acc / (float)D + p.norm_eps);
   }
   const int half =
@@ -223,6 +217,9 @@ __device__ void int_row(const AppendParams& p, const void* src, int64_t sbase, v
     const float c = ldv<TT>(p.cos_cache, pos * half + i);
     const float s = ldv<TT>(p.sin_cache, pos * half + i);
     const float a = fetch(e1), b = fetch(e2);
+    if (p.rope_fp32)
+      return first ? rnd<TT>(__fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s)))
+                   : rnd<TT>(__fadd_rn(__fmul_rn(b, c), __fmul_rn(a, s)));
     return first ? rnd<TT>(rnd<TT>(a * c) - rnd<TT>(b * s))
                  : rnd<TT>(rnd<TT>(b * c) + rnd<TT>(a * s));
   };
@@ -260,20 +257,35 @@ __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const bool linear = p.linear_cap > 0;
   int seq_b;
-  int64_t pos;
+  int64_t pos, rpos;      // storage position, rotary position
+  bool kv_store = true;   // GroupQueryAttention: this row is one of the stored new rows
   if (linear) {
-    // GroupQueryAttention: [batch, seq] query rows; past_b = seqlens_k[b] + 1 - seq.
+    // GroupQueryAttention: [batch, seq] query rows at query_past + j, query_past =
+    // max(length - seq, 0); the first length - query_past key/value rows are stored there.
     seq_b = t / p.gqa_seq;
-    pos = (int64_t)p.seqlens_k[seq_b] + 1 - p.gqa_seq + (t % p.gqa_seq);
+    const int j = t % p.gqa_seq;
+    const int len = p.seqlens_k[seq_b] + 1;
+    const int qp = max(len - p.gqa_seq, 0);
+    pos = (int64_t)qp + j;
+    kv_store = p.gqa_kv_rows != 0 && j < len - qp;
+    rpos = pos;
+    if (p.position_ids)
+      rpos = p.pos_offset_form ? p.position_ids[0] + j
+                               : p.position_ids[(int64_t)seq_b * p.gqa_seq + j];
     if (p.meta_out && t == 0 && blockIdx.y == 0)
       for (int i = threadIdx.x; i <= p.batch; i += blockDim.x) {
         p.meta_out[i] = i * p.gqa_seq;  // cum
-        if (i < p.batch) p.meta_out[p.batch + 1 + i] = max(p.seqlens_k[i] + 1 - p.gqa_seq, 0);
+        if (i < p.batch) {
+          const int li = p.seqlens_k[i] + 1;
+          p.meta_out[p.batch + 1 + i] = max(li - p.gqa_seq, 0);  // past (query_past)
+          p.meta_out[2 * p.batch + 1 + i] = li;                   // key count
+        }
       }
   } else {
     const SeqPos sp = seq_pos_of_token(p.cum, p.past, p.batch, t);
     seq_b = sp.b;
     pos = (int64_t)max(sp.past, 0) + (t - sp.start);
+    rpos = pos;
   }
   const int D = p.head_dim;
   const bool transform = p.cos_cache != nullptr || p.q_norm != nullptr || p.copy_rows;
@@ -285,14 +297,15 @@ __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p
     if (p.do_q && transform && h < p.num_heads)
       process_row<TT>(p, p.query, (int64_t)t * p.q_ld + (int64_t)h * D, p.q_out,
                       ((int64_t)t * p.num_heads + h) * D, nullptr, 0, nullptr, 0, 0.0f,
-                      p.q_norm, pos, lane);
+                      p.q_norm, rpos, lane);
     return;
   }
+  if (linear && p.gqa_kv_rows == 0) return;  // no new key/value rows in this call
 
   // blockIdx.y == 0: this token's key/value rows.  Cache slot and last-writer rule first.
   int64_t slot;
-  if (linear)
-    slot = (pos >= 0 && pos < p.linear_cap) ? pos : -1;  // rows of one (b, kv-head) are distinct
+  if (linear)  // rows of one (b, kv-head) are distinct
+    slot = (kv_store && pos >= 0 && pos < p.linear_cap) ? pos : -1;
   else
     slot = p.slot_mapping ? (int64_t)p.slot_mapping[t] : slot_at(p, seq_b, pos);
   if (!linear && slot >= p.num_blocks * p.block_size) slot = -1;
@@ -354,7 +367,7 @@ __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p
         void* k_dst2 = (p.k_out && write_cache) ? p.key_cache : nullptr;
         if (k_dst)
           process_row<TT>(p, p.key, kbase, k_dst, k_base, k_dst2, cbase, nullptr, 0, 0.0f,
-                          p.k_norm, pos, lane);
+                          p.k_norm, rpos, lane);
       } else if (write_cache) {
         const typename TT::raw* ks = reinterpret_cast<const typename TT::raw*>(p.key);
         typename TT::raw* kd = reinterpret_cast<typename TT::raw*>(p.key_cache);
@@ -381,7 +394,7 @@ __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p
       if (transform) {
         if (p.k_out || kd)
           process_row<TT>(p, p.key, kbase, p.k_out, obase, nullptr, 0, kd, cbase, ks, p.k_norm,
-                          pos, lane);
+                          rpos, lane);
       } else if (write_cache) {
         for (int e = lane; e < D; e += 64) {
           float kx = ldv<TT>(p.key, kbase + e);
@@ -399,7 +412,7 @@ __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p
       uint8_t* vd = write_v ? reinterpret_cast<uint8_t*>(p.value_cache) : nullptr;
       if (kd || (transform && p.k_out))
         int_row<TT, CK>(p, p.key, kbase, transform ? p.k_out : nullptr, obase, kd, cbase,
-                        p.k_scale, p.k_quant == PA_QUANT_PER_CHANNEL, kh, p.k_norm, true, pos,
+                        p.k_scale, p.k_quant == PA_QUANT_PER_CHANNEL, kh, p.k_norm, true, rpos,
                         lane);
       if (vd || v_out)  // values are neither normalised nor rotated
         int_row<TT, CK>(p, p.value, vbase, v_out, obase, vd, cbase, p.v_scale,

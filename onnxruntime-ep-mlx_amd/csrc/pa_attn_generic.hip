@@ -66,6 +66,15 @@ struct CacheRead<I4Cache> {
   }
 };
 
+// Keys of sequence b: past + query rows, bounded by key_limit[b] when given (GroupQueryAttention
+// sequences shorter than the query rows of a ragged first prompt) and by the capacity of a
+// contiguous cache (unvalidated lengths never address another sequence's rows).
+__device__ __forceinline__ int64_t seq_keys(const AttnParams& p, int b, int64_t pastb, int nq) {
+  int64_t t = pastb + nq;
+  if (p.key_limit) t = min(t, (int64_t)max(p.key_limit[b], 0));
+  return p.linear_cap > 0 ? min(t, (int64_t)p.linear_cap) : t;
+}
+
 template <typename CT>
 constexpr bool kIntCache = false;
 template <>
@@ -84,7 +93,7 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
   const int s0 = p.cum[b];
   const int nq = p.cum[b + 1] - s0;
   const int64_t pastb = max(p.past[b], 0);
-  const int64_t total = pastb + nq;
+  const int64_t total = seq_keys(p, b, pastb, nq);
   const int64_t start = (int64_t)split * p.chunk;
   if (nq <= 0 || start >= total) return;
   const int64_t end = min(start + (int64_t)p.chunk, total);
@@ -93,7 +102,14 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
   const int64_t rp = pastb + (t - s0);
   int64_t lo = start, hi = end;
   if (p.causal) hi = min(hi, rp + 1);
-  if (p.window > 0) lo = max(lo, rp - p.window + 1);
+  // window end point: the row's position, or the last key for rows past it (a right-padded
+  // first prompt, causal_window_mask attention.rs:328-353)
+  if (p.window > 0) lo = max(lo, min(rp, total - 1) - p.window + 1);
+  const typename TT::raw* bias_row =
+      p.bias ? reinterpret_cast<const typename TT::raw*>(p.bias) +
+                   ((((int64_t)(p.bias_b == 1 ? 0 : b) * p.bias_h + (p.bias_h == 1 ? 0 : h)) *
+                         p.bias_rows + (t - s0)) * p.bias_cols)
+             : nullptr;
 
   const int64_t row = (int64_t)p.kv_heads * D;
   // Cache rows in storage units: int4 holds two channels per byte.
@@ -154,6 +170,7 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
     }
     float s = wave_sum(part) * p.scale;
     if (cap > 0.0f) s = cap * tanhf(s / cap);
+    if (bias_row) s += TT::to_f32(bias_row[pos]);
     float x = s * kLog2e;
     float mn = fmaxf(m, x);
     float alpha = (m == kNegInf) ? 0.0f : exp2f(m - mn);
@@ -205,7 +222,7 @@ __global__ __launch_bounds__(64) void split_reduce_kernel(const AttnParams p) {
   const int VD = p.v_head_dim;
   const int b = seq_of_token(p.cum, p.batch, t);
   const int nq = p.cum[b + 1] - p.cum[b];
-  const int64_t total = (int64_t)max(p.past[b], 0) + nq;
+  const int64_t total = seq_keys(p, b, max(p.past[b], 0), nq);
   if (nq <= 0) return;
   const int nsplit = (int)min((total + p.chunk - 1) / p.chunk, (int64_t)p.max_splits);
   if (nsplit <= 1) return;  // the attention kernel already wrote the final row

@@ -748,7 +748,7 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
           pc_u = cc.u;
           pc_kh = cc.kh;
           pc_total = cc.total;
-          pc_sink = p.head_sink ? TT::to_f32(skr[i]) * kLog2e : kNegInf;
+          pc_sink = p.head_sink ? TT::to_f32(skr[i]) * kLog2e : (p.smooth_softmax ? 0.0f : kNegInf);
           const int nq = lane_of(sw.q.nq, cc.bl), pastb = lane_of(sw.q.pastb, cc.bl);
           const int R = g * nq;
           const bool rvalid = c < R;

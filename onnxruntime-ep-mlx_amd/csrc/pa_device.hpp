@@ -155,6 +155,20 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Sum of squares of a D-element row with one fixed rounding order (restated by the CPU oracle,
+// orc_rms_norm_rows): lane l folds elements l, l + 64, ... with fused multiply-adds in that order,
+// then the 64 lane sums meet in an XOR butterfly over lane distances 32, 16, ..., 1 (both lanes of
+// a pair add the same two values, so every lane ends with the same sum).
+template <typename Load>
+__device__ __forceinline__ float sum_squares(Load ld, int D, int lane) {
+  float acc = 0.0f;
+  for (int e = lane; e < D; e += 64) {
+    const float v = ld(e);
+    acc = __builtin_fmaf(v, v, acc);
+  }
+  return wave_sum(acc);
+}
+
 // Sequence index of packed token t: largest b with cum[b] <= t (cum monotone, cum[0] <= t).
 // A 64-way search run by the whole wavefront (t wave-uniform): each level has every lane test
 // one evenly spaced candidate, so batch <= 64 costs one memory round trip and batch <= 4096
@@ -241,12 +255,22 @@ struct AppendParams {
   float norm_eps;
   int32_t slots_distinct;  // no two tokens share a slot: skip the last-writer check
   // Contiguous (GroupQueryAttention) caches: [batch, kv_heads, linear_cap, head_dim]; token t is
-  // query row t % gqa_seq of sequence t / gqa_seq at position seqlens_k[b] + 1 - gqa_seq + row.
-  // meta_out (if set) receives cum [batch + 1] and past [batch] for the attention that follows.
+  // query row j = t % gqa_seq of sequence b = t / gqa_seq, length = seqlens_k[b] + 1, at position
+  // query_past + j with query_past = max(length - gqa_seq, 0); its key/value row is stored there
+  // when j < length - query_past (and gqa_kv_rows, i.e. the call has new key/value rows).
+  // meta_out (if set) receives cum [batch + 1], past = query_past [batch] and the key count
+  // length [batch] for the attention that follows.
   int32_t linear_cap;  // 0: paged cache
   int32_t gqa_seq;
+  int32_t gqa_kv_rows;
   const int32_t* seqlens_k;
   int32_t* meta_out;
+  // Rotary position overrides (GroupQueryAttention position_ids, int64 [batch, pos_cols]): row j
+  // of sequence b rotates at pid[0] + j (pos_offset_form: a first prompt) or at pid[b * gqa_seq
+  // + j] (the flattened ids).  rope_fp32: rotate in fp32 and round once (gqa_rope_f32).
+  const int64_t* position_ids;
+  int32_t pos_offset_form;
+  int32_t rope_fp32;
   // Input row strides in elements (packed QKV rows are (H + 2 KV) * D wide).  With copy_rows
   // the query/key rows go to q_out/k_out and the value rows to v_out (contiguous [T, heads * D])
   // even when nothing rotates or normalises them.
@@ -309,6 +333,15 @@ struct AttnParams {
   // (2 i + part - 1) * kPrefillRows + row.  plan_step: the prefill kernel's key step (32 or 64);
   // item key ranges start and split at multiples of it.
   int32_t plan_items, plan_rbs, plan_slots, plan_step;
+  // GroupQueryAttention forms (VALU kernel; the others take none of them): key_limit[b] bounds
+  // the keys of sequence b (its length, below past + query rows for a ragged first prompt); bias
+  // [bias_b, bias_h, bias_rows, bias_cols] in T is added to the scaled (softcapped) score of row i
+  // of sequence b, head h, key p at ((b | 0) * bias_h + (h | 0)) * bias_rows + i) * bias_cols + p;
+  // smooth_softmax: a zero sink logit when head_sink is NULL.
+  const int32_t* key_limit;
+  const void* bias;
+  int32_t bias_b, bias_h, bias_rows, bias_cols;
+  int32_t smooth_softmax;
   int32_t* plan;
   int32_t* plan_info;
   int32_t* plan_split;
@@ -327,7 +360,7 @@ __device__ __forceinline__ float finalize_factor(float m, float l, float sink_x)
 
 template <typename TT>
 __device__ __forceinline__ float sink_logit(const AttnParams& p, int h) {
-  if (!p.head_sink) return kNegInf;
+  if (!p.head_sink) return p.smooth_softmax ? 0.0f : kNegInf;
   return TT::to_f32(reinterpret_cast<const typename TT::raw*>(p.head_sink)[h]) * kLog2e;
 }
 

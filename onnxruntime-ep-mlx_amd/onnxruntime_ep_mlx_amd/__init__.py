@@ -6,13 +6,15 @@ importing it loads the library and fails loudly if it has not been built.
 """
 from . import _capi
 from ._capi import PagedAttentionError, load
-from .ops import (PagePool, attention, group_query_attention, paged_attention, pa_dtype,
+from .ops import (PagePool, attention, group_query_attention, group_query_attention_claim,
+                  paged_attention, pa_dtype,
                   reshape_and_cache, rotary_append)
 
 load()
 
 __all__ = [
-    "PagePool", "PagedAttentionError", "attention", "group_query_attention", "load", "pa_dtype",
+    "PagePool", "PagedAttentionError", "attention", "group_query_attention",
+    "group_query_attention_claim", "load", "pa_dtype",
     "paged_attention",
     "reshape_and_cache", "rotary_append", "_capi",
 ]

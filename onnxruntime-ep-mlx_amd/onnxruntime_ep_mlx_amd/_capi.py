@@ -23,6 +23,7 @@ PA_DTYPE_INT4 = 6
 PA_INT32_DTYPE = 10
 PA_INT8_DTYPE = 11
 PA_UINT8_DTYPE = 12
+PA_INT64_DTYPE = 13
 
 PA_QUANT_NONE = 0
 PA_QUANT_PER_TENSOR = 1
@@ -49,6 +50,7 @@ EXPORTS = (
     "pa_paged_attention_workspace_bytes", "pa_paged_attention", "pa_paged_attention_static",
     "pa_paged_attention_claim",
     "pa_group_query_attention_workspace_bytes", "pa_group_query_attention",
+    "pa_group_query_attention_claim",
 )
 
 
@@ -116,23 +118,43 @@ class PaGqaNode(C.Structure):
         ("num_heads", C.c_int32), ("kv_num_heads", C.c_int32), ("scale", C.c_float),
         ("softcap", C.c_float), ("local_window_size", C.c_int32), ("do_rotary", C.c_int32),
         ("rotary_interleaved", C.c_int32), ("is_causal", C.c_int32),
-        ("qk_norm_epsilon", C.c_float),
+        ("qk_norm_epsilon", C.c_float), ("smooth_softmax", C.c_int32),
     ]
 
 
 class PaGqaIO(C.Structure):
     _fields_ = [
         ("dtype", C.c_int), ("batch", C.c_int32), ("seq", C.c_int32),
-        ("query_hidden", C.c_int32), ("capacity", C.c_int32),
+        ("query_hidden", C.c_int32), ("kv_seq", C.c_int32),
         ("query", C.c_void_p), ("key", C.c_void_p), ("value", C.c_void_p),
+        ("past_key", C.c_void_p), ("past_value", C.c_void_p), ("past_capacity", C.c_int32),
         ("present_key", C.c_void_p), ("present_value", C.c_void_p),
+        ("present_capacity", C.c_int32),
         ("seqlens_k", C.c_void_p), ("host_seqlens_k", C.c_void_p),
         ("total_sequence_length", C.c_int64),
         ("cos_cache", C.c_void_p), ("sin_cache", C.c_void_p),
         ("rotary_positions", C.c_int64), ("rotary_half", C.c_int32),
+        ("position_ids", C.c_void_p), ("host_position_ids", C.c_void_p),
+        ("position_cols", C.c_int32),
+        ("attention_bias", C.c_void_p), ("bias_batch", C.c_int32), ("bias_heads", C.c_int32),
         ("head_sink", C.c_void_p), ("q_norm_weight", C.c_void_p), ("k_norm_weight", C.c_void_p),
         ("output", C.c_void_p),
         ("cache_dtype", C.c_int), ("k_scale", C.c_void_p), ("v_scale", C.c_void_p),
+        ("k_quant_type", C.c_int32), ("v_quant_type", C.c_int32),
+    ]
+
+
+class PaGqaNodeInfo(C.Structure):
+    _fields_ = [
+        ("num_inputs", C.c_int32), ("num_outputs", C.c_int32),
+        ("input_present", C.c_int32 * 16), ("input_dtype", C.c_int32 * 16),
+        ("input_rank", C.c_int32 * 16), ("input_shape", (C.c_int64 * 4) * 16),
+        ("output_present", C.c_int32 * 4), ("output_dtype", C.c_int32 * 4),
+        ("output_rank", C.c_int32 * 4), ("output_shape", (C.c_int64 * 4) * 4),
+        ("num_heads", C.c_int32), ("kv_num_heads", C.c_int32), ("do_rotary", C.c_int32),
+        ("is_causal", C.c_int32), ("local_window_size", C.c_int32),
+        ("sliding_window_cache", C.c_int32), ("kv_cache_bit_width", C.c_int32),
+        ("smooth_softmax", C.c_int32), ("qk_output", C.c_int32), ("softcap", C.c_float),
         ("k_quant_type", C.c_int32), ("v_quant_type", C.c_int32),
     ]
 
@@ -204,6 +226,7 @@ def load() -> C.CDLL:
                                                           C.POINTER(PaGqaIO)]),
         "pa_group_query_attention": (C.c_int, [C.POINTER(PaGqaNode), C.POINTER(PaGqaIO), P, SZ,
                                                P]),
+        "pa_group_query_attention_claim": (C.c_int, [C.POINTER(PaGqaNodeInfo), C.c_char_p, SZ]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

@@ -344,50 +344,107 @@ def paged_attention(query, key, value, key_cache, value_cache, cumulative_sequen
             value_cache if value_cache_out is None else value_cache_out)
 
 
-def group_query_attention(query, key, value, present_key, present_value, seqlens_k,
-                          total_sequence_length, cos_cache=None, sin_cache=None, head_sink=None,
-                          q_norm_weight=None, k_norm_weight=None, *, num_heads, kv_num_heads,
-                          scale=0.0, softcap=0.0, local_window_size=-1, do_rotary=0,
-                          rotary_interleaved=0, is_causal=1, qk_norm_epsilon=1e-6,
-                          k_scale=None, v_scale=None, k_quant_type="NONE", v_quant_type="NONE",
-                          validate=True, output=None):
-    """com.microsoft::GroupQueryAttention on MI355X (pa_group_query_attention), shared-buffer
-    contract: present_key/present_value [B, kv_heads, capacity, head] hold the past rows and are
-    updated in place with the new rows at [seqlens_k[b] + 1 - S, seqlens_k[b] + 1).
-    ``key``/``value`` None: packed QKV query [B, S, (H + 2 KV) * head].  Integer present caches
-    (torch.int8, or torch.uint8 with [.., ceil(head / 2)] rows = int4, "kv_cache_bit_width" 4)
-    take ``k_scale``/``v_scale`` (inputs 12/13) with "PER_TENSOR" / "PER_CHANNEL" modes.
+def group_query_attention(query, key, value, past_key, past_value, seqlens_k,
+                          total_sequence_length, cos_cache=None, sin_cache=None,
+                          position_ids=None, attention_bias=None, head_sink=None, k_scale=None,
+                          v_scale=None, q_norm_weight=None, k_norm_weight=None, *, num_heads,
+                          kv_num_heads, scale=0.0, softcap=0.0, local_window_size=-1,
+                          do_rotary=0, rotary_interleaved=0, is_causal=1, qk_norm_epsilon=1e-6,
+                          smooth_softmax=0, k_quant_type="NONE", v_quant_type="NONE",
+                          present="new", present_key=None, present_value=None, validate=True,
+                          output=None):
+    """com.microsoft::GroupQueryAttention on MI355X (pa_group_query_attention), inputs in the
+    operator's order (query, key, value, past_key, past_value, seqlens_k,
+    total_sequence_length, cos_cache, sin_cache, position_ids, attention_bias, head_sink,
+    k_scale, v_scale, q_norm_weight, k_norm_weight; attention.rs:932-1454).
+
+    ``key``/``value`` None: packed QKV query [B, S, (H + 2 KV) * head].  ``key``/``value`` with
+    a zero-length sequence axis: no new rows (the past is attended as is).  ``past_key`` None:
+    the first prompt, no past.  Integer caches (torch.int8, or torch.uint8 = int4 rows of
+    ceil(head / 2) bytes) take ``k_scale``/``v_scale`` with "PER_TENSOR" / "PER_CHANNEL".
+    ``present`` selects outputs 1/2: "new" allocates [B, KV, max(past capacity, total), row]
+    (the operator's own contract), "shared" updates ``past_key``/``past_value`` in place
+    (outputs bound onto the inputs: capacity stays), "omitted" returns None for both;
+    ``present_key``/``present_value`` given explicitly are used as the "new" buffers.
+    ``validate``: copy seqlens_k (and position_ids) to the host for the reference's checks.
     Returns (output, present_key, present_value)."""
     lib = capi.load()
     if query.dim() != 3:
         raise ValueError("query must have rank 3 [batch, sequence, hidden]")
-    for n, t in (("query", query), ("key", key), ("value", value),
-                 ("present_key", present_key), ("present_value", present_value),
-                 ("k_scale", k_scale), ("v_scale", v_scale)):
+    if present not in ("new", "shared", "omitted"):
+        raise ValueError("present must be 'new', 'shared' or 'omitted'")
+    for n, t in (("query", query), ("key", key), ("value", value), ("past_key", past_key),
+                 ("past_value", past_value), ("k_scale", k_scale), ("v_scale", v_scale),
+                 ("position_ids", position_ids), ("attention_bias", attention_bias),
+                 ("present_key", present_key), ("present_value", present_value)):
         _need_cuda(n, t)
         _contig(n, t)
     if seqlens_k.dtype != torch.int32:
         raise ValueError("input seqlens_k must be int32")
+    if position_ids is not None and position_ids.dtype != torch.int64:
+        raise ValueError("GroupQueryAttention: position_ids must be int64 [batch,>=sequence]")
+    B, S = query.shape[0], query.shape[1]
     packed = key is None and value is None
     head = query.shape[2] // (num_heads + 2 * kv_num_heads if packed else num_heads)
+    kv_seq = S if packed else key.shape[1]
+    total = int(total_sequence_length)
+    # without a past the caches use the activation dtype (kv_cache.rs:24)
+    cache_dt = past_key.dtype if past_key is not None else query.dtype
+    width = (head + 1) // 2 if cache_dt == torch.uint8 else head
+    past_cap = past_key.shape[2] if past_key is not None else 0
+    if present == "shared":
+        if past_key is None:
+            raise ValueError("GroupQueryAttention: present='shared' needs past_key/past_value")
+        present_key, present_value = past_key, past_value
+    elif present == "new" and present_key is None:
+        shape = (B, kv_num_heads, max(past_cap, total), width)
+        present_key = torch.empty(shape, dtype=cache_dt, device=query.device)
+        present_value = torch.empty(shape, dtype=cache_dt, device=query.device)
+    elif present == "omitted":
+        present_key = present_value = None
     host = seqlens_k.detach().to("cpu").contiguous() if validate else None
+    host_pid = (position_ids.detach().to("cpu").contiguous()
+                if validate and position_ids is not None else None)
     if output is None:
-        output = query.new_empty((query.shape[0], query.shape[1], num_heads * head))
-    cache_dt = present_key.dtype
+        output = query.new_empty((B, S, num_heads * head))
     cache_code = 0 if cache_dt == query.dtype else pa_dtype(cache_dt)
     node = capi.PaGqaNode(num_heads, kv_num_heads, scale, softcap, local_window_size, do_rotary,
-                          rotary_interleaved, is_causal, qk_norm_epsilon)
+                          rotary_interleaved, is_causal, qk_norm_epsilon, smooth_softmax)
+    rot = do_rotary and cos_cache is not None
     io = capi.PaGqaIO(
-        pa_dtype(query.dtype), query.shape[0], query.shape[1], query.shape[2],
-        present_key.shape[2], _ptr(query), _ptr(key), _ptr(value), _ptr(present_key),
-        _ptr(present_value), _ptr(seqlens_k), _ptr(host), int(total_sequence_length),
-        _ptr(cos_cache) if do_rotary else None, _ptr(sin_cache) if do_rotary else None,
-        cos_cache.shape[0] if (do_rotary and cos_cache is not None) else 0,
-        cos_cache.shape[1] if (do_rotary and cos_cache is not None) else 0,
-        _ptr(head_sink), _ptr(q_norm_weight), _ptr(k_norm_weight), _ptr(output), cache_code,
-        _ptr(k_scale), _ptr(v_scale), _quant(k_quant_type), _quant(v_quant_type))
+        dtype=pa_dtype(query.dtype), batch=B, seq=S, query_hidden=query.shape[2], kv_seq=kv_seq,
+        query=_ptr(query), key=_ptr(key), value=_ptr(value), past_key=_ptr(past_key),
+        past_value=_ptr(past_value), past_capacity=past_cap, present_key=_ptr(present_key),
+        present_value=_ptr(present_value),
+        present_capacity=present_key.shape[2] if present_key is not None else 0,
+        seqlens_k=_ptr(seqlens_k), host_seqlens_k=_ptr(host), total_sequence_length=total,
+        cos_cache=_ptr(cos_cache) if do_rotary else None,
+        sin_cache=_ptr(sin_cache) if do_rotary else None,
+        rotary_positions=cos_cache.shape[0] if rot else 0,
+        rotary_half=cos_cache.shape[1] if rot else 0,
+        position_ids=_ptr(position_ids), host_position_ids=_ptr(host_pid),
+        position_cols=position_ids.shape[1] if position_ids is not None else 0,
+        attention_bias=_ptr(attention_bias),
+        bias_batch=attention_bias.shape[0] if attention_bias is not None else 0,
+        bias_heads=attention_bias.shape[1] if attention_bias is not None else 0,
+        head_sink=_ptr(head_sink), q_norm_weight=_ptr(q_norm_weight),
+        k_norm_weight=_ptr(k_norm_weight), output=_ptr(output), cache_dtype=cache_code,
+        k_scale=_ptr(k_scale), v_scale=_ptr(v_scale), k_quant_type=_quant(k_quant_type),
+        v_quant_type=_quant(v_quant_type))
+    if attention_bias is not None and (attention_bias.dim() != 4
+                                       or attention_bias.shape[2] != S
+                                       or attention_bias.shape[3] != total):
+        raise ValueError("GroupQueryAttention: attention_bias must broadcast to "
+                         "[batch,heads,sequence,total]")
     nbytes = lib.pa_group_query_attention_workspace_bytes(C.byref(node), C.byref(io))
     ws = _ws.get(max(nbytes, 1), query.device)
     capi.check(lib.pa_group_query_attention(C.byref(node), C.byref(io), _ptr(ws), nbytes,
                                             _stream(query.device)))
     return output, present_key, present_value
+
+
+def group_query_attention_claim(info: "capi.PaGqaNodeInfo") -> tuple[bool, str]:
+    """pa_group_query_attention_claim: (claimed, reason)."""
+    buf = C.create_string_buffer(512)
+    ok = capi.load().pa_group_query_attention_claim(C.byref(info), buf, len(buf))
+    return bool(ok), buf.value.decode()

@@ -185,16 +185,39 @@ void orc_decode(const void* src, float* dst, int64_t n, int dtype) {
 
 /* ------------------------------------------------------------------ RMSNorm (a4, optional) */
 /* attention.rs:4045-4049 calls mlx_fast_rms_norm(x, w, eps): fp32 sum of squares, then the
- * normalised value is rounded to T and multiplied by the weight in T. */
+ * normalised value is rounded to T and multiplied by the weight in T.  The sum of squares has
+ * one fixed rounding order, the device's: 64 partial sums p[l] fold elements l, l + 64, ...
+ * with fused multiply-adds in that order, then an XOR butterfly over distances 32, 16, ..., 1
+ * replaces p[l] by p[l] + p[l ^ o] (a sum MLX leaves unspecified; any fp32 order is within its
+ * contract, this one makes the normalised rows bit-exact). */
+static float orc_sum_squares_f(const float* v, int head_dim) {
+  float p[64], q[64];
+  for (int l = 0; l < 64; ++l) {
+    float acc = 0.0f;
+    for (int e = l; e < head_dim; e += 64) acc = fmaf(v[e], v[e], acc);
+    p[l] = acc;
+  }
+  for (int o = 32; o >= 1; o >>= 1) {
+    for (int l = 0; l < 64; ++l) q[l] = p[l] + p[l ^ o];
+    memcpy(p, q, sizeof p);
+  }
+  return p[0];
+}
+
+float orc_sum_squares(const void* x, int64_t base, int head_dim, int dtype) {
+  float* v = (float*)malloc((size_t)(head_dim > 0 ? head_dim : 1) * sizeof(float));
+  if (!v) return NAN;
+  for (int e = 0; e < head_dim; ++e) v[e] = ld(x, base + e, dtype);
+  float r = orc_sum_squares_f(v, head_dim);
+  free(v);
+  return r;
+}
+
 void orc_rms_norm_rows(void* x, int64_t rows, int heads, int head_dim, const void* weight,
                        float eps, int dtype) {
   for (int64_t r = 0; r < rows * heads; ++r) {
     int64_t base = r * head_dim;
-    float acc = 0.0f;
-    for (int i = 0; i < head_dim; ++i) {
-      float v = ld(x, base + i, dtype);
-      acc += v * v;
-    }
+    float acc = orc_sum_squares(x, base, head_dim, dtype);
     float inv = 1.0f / sqrtf(acc / (float)head_dim + eps);
     for (int i = 0; i < head_dim; ++i) {
       float v = rd(ld(x, base + i, dtype) * inv, dtype);
@@ -594,5 +617,175 @@ int orc_gqa_contiguous(int dtype, const void* query, const void* key, const void
   free(scores);
   free(tmp);
   free(kd);
+  return rc;
+}
+
+/* ------------------------------------------------------------ GroupQueryAttention (all forms) */
+/* RMSNorm of one row held as T values in floats (orc_rms_norm_rows on a single row). */
+static void norm_row(float* v, int d, const void* weight, float eps, int dtype) {
+  float acc = orc_sum_squares_f(v, d);
+  float inv = 1.0f / sqrtf(acc / (float)d + eps);
+  for (int i = 0; i < d; ++i) v[i] = rd(rd(v[i] * inv, dtype) * ld(weight, i, dtype), dtype);
+}
+
+/* gqa_rope (per-op T rounding) or gqa_rope_f32 (fp32 ops, one rounding) of one row at cos/sin
+ * row pos (attention.rs:459-521). */
+static void rope_row(float* v, int64_t pos, const void* cos, const void* sin, int half,
+                     int interleaved, int f32, int dtype) {
+  for (int i = 0; i < half; ++i) {
+    float c = ld(cos, pos * half + i, dtype), s = ld(sin, pos * half + i, dtype);
+    int i1 = interleaved ? 2 * i : i, i2 = interleaved ? 2 * i + 1 : half + i;
+    float a = v[i1], b = v[i2];
+    if (f32) {
+      float ac = a * c, bs = b * s, bc = b * c, as = a * s;
+      v[i1] = rd(ac - bs, dtype);
+      v[i2] = rd(bc + as, dtype);
+    } else {
+      v[i1] = rd(rd(a * c, dtype) - rd(b * s, dtype), dtype);
+      v[i2] = rd(rd(b * c, dtype) + rd(a * s, dtype), dtype);
+    }
+  }
+}
+
+int orc_gqa_batched(const orc_gqa_args* a, double* out) {
+  const int B = a->batch, S = a->seq, H = a->num_heads, KV = a->kv_heads, d = a->head_dim;
+  const int dt = a->dtype, g = H / KV;
+  const int cdt = a->cache_dtype ? a->cache_dtype : dt;
+  const int quant = is_int_dt(cdt), bits = cdt == ORC_I8 ? 8 : 4;
+  const int w = quant ? cache_width(cdt, d) : d;
+  const size_t row_bytes = quant ? (size_t)w : (size_t)w * esize(dt);
+  const int Pc = a->present_cap, C0 = a->past_k ? a->past_cap : 0;
+  const int f32rope = a->position_ids != NULL || a->kv_seq == 0;
+  const int kpc = a->k_mode == ORC_QUANT_PER_CHANNEL, vpc = a->v_mode == ORC_QUANT_PER_CHANNEL;
+  float* row = (float*)malloc((size_t)(d > 0 ? d : 1) * sizeof(float));
+  float* qrow = (float*)malloc((size_t)(d > 0 ? d : 1) * sizeof(float));
+  double* sc = (double*)malloc((size_t)(Pc > 0 ? Pc : 1) * sizeof(double));
+  if (!row || !qrow || !sc) {
+    free(row);
+    free(qrow);
+    free(sc);
+    return 4;
+  }
+  int rc = 0;
+  for (int b = 0; b < B && !rc; ++b) {
+    const int length = a->seqlens_k[b] + 1;
+    const int qp = length - S > 0 ? length - S : 0;
+    const int past = a->kv_seq == 0 ? length : qp;
+    const int new_rows = a->kv_seq == 0 ? 0 : length - past;
+    if (past > C0 || length > Pc) {
+      rc = 5;
+      break;
+    }
+    /* present = [past rows | new rows | past tail | zero codes] */
+    for (int kh = 0; kh < KV; ++kh)
+      for (int side = 0; side < 2; ++side) {
+        const uint8_t* src = (const uint8_t*)(side ? a->past_v : a->past_k);
+        uint8_t* dst = (uint8_t*)(side ? a->present_v : a->present_k);
+        for (int r = 0; r < Pc; ++r) {
+          uint8_t* o = dst + (((size_t)b * KV + kh) * Pc + r) * row_bytes;
+          if (r < C0 && !(r >= past && r < length))
+            memcpy(o, src + (((size_t)b * KV + kh) * C0 + r) * row_bytes, row_bytes);
+          else
+            memset(o, cdt == ORC_I4 ? 0x88 : 0, row_bytes);
+        }
+      }
+    for (int j = 0; j < S; ++j) {
+      int64_t rp = qp + j;
+      if (a->position_ids)
+        rp = a->total == S ? a->position_ids[0] + j : a->position_ids[(int64_t)b * S + j];
+      if (a->cos_cache && (rp < 0 || rp >= a->cos_rows)) {
+        rc = 6;
+        break;
+      }
+      if (j >= new_rows) continue;
+      for (int kh = 0; kh < KV; ++kh) {
+        const int64_t src = (((int64_t)b * a->kv_seq + j) * KV + kh) * d;
+        const int64_t dst_row = ((int64_t)b * KV + kh) * Pc + past + j;
+        for (int side = 0; side < 2; ++side) {
+          const void* in = side ? a->value : a->key;
+          for (int e = 0; e < d; ++e) row[e] = ld(in, src + e, dt);
+          if (!side && a->k_norm) norm_row(row, d, a->k_norm, a->norm_eps, dt);
+          if (!side && a->cos_cache)
+            rope_row(row, rp, a->cos_cache, a->sin_cache, a->rot_half, a->interleaved, f32rope,
+                     dt);
+          void* pres = side ? a->present_v : a->present_k;
+          if (quant) {
+            const float* s = side ? a->v_scale : a->k_scale;
+            const int pc = side ? vpc : kpc;
+            orc_int_encode_row(row, d, pc ? s + (int64_t)kh * d : s, pc, bits, 1,
+                               (uint8_t*)pres + dst_row * w);
+          } else {
+            for (int e = 0; e < d; ++e) st(pres, dst_row * d + e, row[e], dt);
+          }
+        }
+      }
+    }
+    if (rc) break;
+    for (int i = 0; i < S; ++i) {
+      int64_t rp = qp + i;
+      if (a->position_ids)
+        rp = a->total == S ? a->position_ids[0] + i : a->position_ids[(int64_t)b * S + i];
+      /* visible keys [lo, hi) of this row (causal_mask_topleft / causal_window_mask) */
+      int hi = a->causal ? qp + i + 1 : length;
+      if (hi > length) hi = length;
+      int lo = 0;
+      if (a->window > 0) {
+        int l1 = qp + i - a->window + 1, l2 = length - a->window;
+        lo = l1 < l2 ? l1 : l2;
+        if (lo < 0) lo = 0;
+      }
+      for (int h = 0; h < H; ++h) {
+        const int kh = h / g;
+        const int64_t qb = (((int64_t)b * S + i) * H + h) * d;
+        for (int e = 0; e < d; ++e) qrow[e] = ld(a->query, qb + e, dt);
+        if (a->q_norm) norm_row(qrow, d, a->q_norm, a->norm_eps, dt);
+        if (a->cos_cache)
+          rope_row(qrow, rp, a->cos_cache, a->sin_cache, a->rot_half, a->interleaved, f32rope,
+                   dt);
+        double m = -INFINITY;
+        for (int p = lo; p < hi; ++p) {
+          const int64_t r = ((int64_t)b * KV + kh) * Pc + p;
+          if (quant)
+            orc_int_decode_row((const uint8_t*)a->present_k + r * w, d,
+                               kpc ? a->k_scale + (int64_t)kh * d : a->k_scale, kpc, bits, row);
+          else
+            for (int e = 0; e < d; ++e) row[e] = ld(a->present_k, r * d + e, dt);
+          double dot = 0.0;
+          for (int e = 0; e < d; ++e) dot += (double)qrow[e] * (double)row[e];
+          double s = (double)a->scale * dot;
+          if (a->softcap > 0.0f) s = (double)a->softcap * tanh(s / (double)a->softcap);
+          if (a->bias) {
+            const int bb = a->bias_b == 1 ? 0 : b, bh = a->bias_h == 1 ? 0 : h;
+            s += (double)ld(a->bias, (((int64_t)bb * a->bias_h + bh) * S + i) * a->total + p, dt);
+          }
+          sc[p] = s;
+          if (s > m) m = s;
+        }
+        double sink = -INFINITY;
+        if (a->head_sink) sink = (double)ld(a->head_sink, h, dt);
+        else if (a->smooth) sink = 0.0;
+        if (sink > m) m = sink;
+        double* o = out + qb;
+        for (int e = 0; e < d; ++e) o[e] = 0.0;
+        double l = sink == -INFINITY ? 0.0 : exp(sink - m);
+        for (int p = lo; p < hi; ++p) {
+          const double wgt = exp(sc[p] - m);
+          l += wgt;
+          const int64_t r = ((int64_t)b * KV + kh) * Pc + p;
+          if (quant)
+            orc_int_decode_row((const uint8_t*)a->present_v + r * w, d,
+                               vpc ? a->v_scale + (int64_t)kh * d : a->v_scale, vpc, bits, row);
+          else
+            for (int e = 0; e < d; ++e) row[e] = ld(a->present_v, r * d + e, dt);
+          for (int e = 0; e < d; ++e) o[e] += wgt * (double)row[e];
+        }
+        if (l != 0.0)
+          for (int e = 0; e < d; ++e) o[e] /= l;
+      }
+    }
+  }
+  free(row);
+  free(qrow);
+  free(sc);
   return rc;
 }

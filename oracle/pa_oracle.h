@@ -57,7 +57,9 @@ void orc_encode(const float* src, void* dst, int64_t n, int dtype);
 void orc_decode(const void* src, float* dst, int64_t n, int dtype);
 
 /* In-place RMSNorm over head_dim of rows [rows, heads, head_dim] (mlx_fast_rms_norm at
- * attention.rs:4045-4049; numpy form test_paged_attention.py:101-103). */
+ * attention.rs:4045-4049; numpy form test_paged_attention.py:101-103), with the sum of squares
+ * of orc_sum_squares (64 fma partials over a stride of 64, then an XOR butterfly 32..1). */
+float orc_sum_squares(const void* x, int64_t base, int head_dim, int dtype);
 void orc_rms_norm_rows(void* x, int64_t rows, int heads, int head_dim, const void* weight,
                        float eps, int dtype);
 
@@ -122,6 +124,51 @@ int orc_gqa_contiguous(int dtype, const void* query, const void* key, const void
                        float scale, float softcap, int window, int causal, double* out,
                        int cache_dtype, const float* k_scale, const float* v_scale, int k_mode,
                        int v_mode);
+
+/* GroupQueryAttention on contiguous caches, every form of gqa_batched (attention.rs:586-848,
+ * reached from group_query_attention_op :932-1454): per sequence length = seqlens_k[b] + 1,
+ * query_past = max(length - seq, 0), past = kv_seq == 0 ? length : query_past; query rows sit
+ * at query_past + i (ragged first prompts: right-padded rows beyond the length); RMSNorm of q/k
+ * (qk norm), then RoPE at query_past + i or at the position ids (first prompt, total == seq:
+ * pid[0] + i; later: pid_flat[b * seq + i]) — in fp32 with one rounding when position ids are
+ * given or kv_seq == 0 (gqa_rope_f32), per-op T rounding otherwise (gqa_rope); the present is
+ * [past rows | new rows | past tail | zero codes] of present_cap rows; attention over the
+ * present's first length rows with the top-left causal rule key <= query_past + i, the window
+ * lower bound min(query_past + i - w + 1, length - w) (:328-359), scale, softcap, + bias
+ * [b|1, h|1, i, key], and a sink logit (head_sink, or 0 for smooth_softmax) in the denominator
+ * only (:100-118).  Computes in double; out [B, S, H * d]. */
+typedef struct orc_gqa_args {
+  int dtype, batch, seq, kv_seq, num_heads, kv_heads, head_dim;
+  const void* query;   /* [B, S, H * d] */
+  const void* key;     /* [B, kv_seq, KV * d] (unused when kv_seq == 0) */
+  const void* value;
+  const void* past_k;  /* [B, KV, past_cap, w] or NULL (no past) */
+  const void* past_v;
+  int past_cap;
+  void* present_k;     /* out [B, KV, present_cap, w] */
+  void* present_v;
+  int present_cap;
+  const int32_t* seqlens_k;
+  int64_t total;
+  const void* cos_cache; /* [cos_rows, rot_half] or NULL (no rotary) */
+  const void* sin_cache;
+  int64_t cos_rows;
+  int rot_half, interleaved;
+  const int64_t* position_ids; /* flattened [B, >= S] or NULL */
+  const void* bias;            /* [bias_b, bias_h, S, total] in T or NULL */
+  int bias_b, bias_h;
+  const void* head_sink;       /* [H] in T or NULL */
+  int smooth;
+  const void* q_norm;          /* [d] in T or NULL */
+  const void* k_norm;
+  float norm_eps, scale, softcap;
+  int window, causal;
+  int cache_dtype;             /* 0 (= dtype), ORC_I8 or ORC_I4 */
+  const float* k_scale;
+  const float* v_scale;
+  int k_mode, v_mode;
+} orc_gqa_args;
+int orc_gqa_batched(const orc_gqa_args* a, double* out);
 
 /* CPU baseline (pa_cpu_baseline.c): the same contiguous GQA decode in fp32 accumulation over
  * all requested threads, one task per (sequence, kv-head).  k/v: [sum_b ctx_b, KV, d] packed

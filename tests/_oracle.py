@@ -26,6 +26,25 @@ PER_TENSOR, PER_CHANNEL = 1, 2
 _lib = None
 
 
+class GqaArgs(C.Structure):
+    """orc_gqa_args (oracle/pa_oracle.h)."""
+    _fields_ = [(n, C.c_int) for n in ("dtype", "batch", "seq", "kv_seq", "num_heads",
+                                       "kv_heads", "head_dim")] + [
+        ("query", C.c_void_p), ("key", C.c_void_p), ("value", C.c_void_p),
+        ("past_k", C.c_void_p), ("past_v", C.c_void_p), ("past_cap", C.c_int),
+        ("present_k", C.c_void_p), ("present_v", C.c_void_p), ("present_cap", C.c_int),
+        ("seqlens_k", C.c_void_p), ("total", C.c_int64),
+        ("cos_cache", C.c_void_p), ("sin_cache", C.c_void_p), ("cos_rows", C.c_int64),
+        ("rot_half", C.c_int), ("interleaved", C.c_int),
+        ("position_ids", C.c_void_p), ("bias", C.c_void_p), ("bias_b", C.c_int),
+        ("bias_h", C.c_int), ("head_sink", C.c_void_p), ("smooth", C.c_int),
+        ("q_norm", C.c_void_p), ("k_norm", C.c_void_p), ("norm_eps", C.c_float),
+        ("scale", C.c_float), ("softcap", C.c_float), ("window", C.c_int), ("causal", C.c_int),
+        ("cache_dtype", C.c_int), ("k_scale", C.c_void_p), ("v_scale", C.c_void_p),
+        ("k_mode", C.c_int), ("v_mode", C.c_int),
+    ]
+
+
 def lib() -> C.CDLL:
     global _lib
     if _lib is None:
@@ -68,6 +87,10 @@ def lib() -> C.CDLL:
         L.orc_gqa_contiguous.restype = I32
         L.orc_gqa_contiguous.argtypes = [I32, P, P, P, P, P, I32, I32, I32, I32, I32, I32, P, F,
                                          F, I32, I32, P, I32, P, P, I32, I32]
+        L.orc_gqa_batched.restype = I32
+        L.orc_gqa_batched.argtypes = [C.POINTER(GqaArgs), P]
+        L.orc_sum_squares.restype = F
+        L.orc_sum_squares.argtypes = [P, I64, I32, I32]
         L.orc_cpu_gqa_decode.restype = I32
         L.orc_cpu_gqa_decode.argtypes = [I32, P, P, P, P, P, I32, I32, I32, I32, F, P, I32]
         L.orc_cpu_gqa_prefill.restype = I32
@@ -217,6 +240,58 @@ def gqa_contiguous(dtype, q, k, v, pk, pv, seqlens_k, H, KV, d, scale, softcap=0
                                   _p(k_scale), _p(v_scale), k_mode, v_mode)
     assert rc == 0, rc
     return out, pk, pv
+
+
+def sum_squares(x: np.ndarray, dtype: int) -> float:
+    """orc_sum_squares of one row (the fixed RMSNorm reduction order)."""
+    x = np.ascontiguousarray(x)
+    return float(lib().orc_sum_squares(_p(x), 0, x.size, dtype))
+
+
+def gqa_batched(dtype, q, k, v, past_k, past_v, seqlens_k, total, H, KV, d, *, scale,
+                present_cap=None, softcap=0.0, window=-1, causal=1, cos=None, sin=None,
+                interleaved=0, position_ids=None, bias=None, head_sink=None, smooth=0,
+                q_norm=None, k_norm=None, norm_eps=1e-6, cache_dtype=0, k_scale=None,
+                v_scale=None, k_mode=0, v_mode=0):
+    """orc_gqa_batched: every GroupQueryAttention form on contiguous caches.  q [B, S, H*d];
+    k/v [B, kv_seq, KV*d] or None (kv_seq 0); past_k/v [B, KV, cap, w] or None.
+    Returns (out float64 [B, S, H*d], present_k, present_v)."""
+    B, S = q.shape[0], q.shape[1]
+    kv_seq = 0 if k is None else k.shape[1]
+    cap = 0 if past_k is None else past_k.shape[2]
+    if present_cap is None:
+        present_cap = max(cap, int(total))
+    w = d if not cache_dtype else (d if cache_dtype == I8 else (d + 1) // 2)
+    raw = RAW[cache_dtype or dtype]
+    pres_k = np.zeros((B, KV, present_cap, w), raw)
+    pres_v = np.zeros((B, KV, present_cap, w), raw)
+    out = np.zeros((B, S, H * d), np.float64)
+    keep = []
+
+    def ptr(x, dt=None):
+        if x is None:
+            return None
+        x = np.ascontiguousarray(x, dt) if dt is not None else np.ascontiguousarray(x)
+        keep.append(x)
+        return x.ctypes.data
+
+    a = GqaArgs(dtype=dtype, batch=B, seq=S, kv_seq=kv_seq, num_heads=H, kv_heads=KV,
+                head_dim=d, query=ptr(q), key=ptr(k), value=ptr(v), past_k=ptr(past_k),
+                past_v=ptr(past_v), past_cap=cap, present_k=pres_k.ctypes.data,
+                present_v=pres_v.ctypes.data, present_cap=present_cap,
+                seqlens_k=ptr(seqlens_k, np.int32), total=int(total), cos_cache=ptr(cos),
+                sin_cache=ptr(sin), cos_rows=0 if cos is None else cos.shape[0],
+                rot_half=0 if cos is None else cos.shape[1], interleaved=interleaved,
+                position_ids=ptr(position_ids, np.int64), bias=ptr(bias),
+                bias_b=0 if bias is None else bias.shape[0],
+                bias_h=0 if bias is None else bias.shape[1], head_sink=ptr(head_sink),
+                smooth=smooth, q_norm=ptr(q_norm), k_norm=ptr(k_norm), norm_eps=norm_eps,
+                scale=scale, softcap=softcap, window=window, causal=causal,
+                cache_dtype=cache_dtype, k_scale=ptr(k_scale, np.float32),
+                v_scale=ptr(v_scale, np.float32), k_mode=k_mode, v_mode=v_mode)
+    rc = lib().orc_gqa_batched(C.byref(a), out.ctypes.data)
+    assert rc == 0, rc
+    return out, pres_k, pres_v
 
 
 def cpu_gqa_decode(dtype, q, k, v, kv_offset, ctx, H, KV, d, scale, threads):

@@ -31,10 +31,8 @@ MIRRORS = {
     "pa_gqa_node": capi.PaGqaNode,
     "pa_gqa_io": capi.PaGqaIO,
     "pa_node_info": capi.PaNodeInfo,
+    "pa_gqa_node_info": capi.PaGqaNodeInfo,
 }
-for _name in ("PaGqaNodeInfo",):
-    if hasattr(capi, _name):
-        MIRRORS["pa_gqa_node_info"] = getattr(capi, _name)
 
 # header struct -> Rust mirror name in INTEGRATION.md
 RUST_MIRRORS = {

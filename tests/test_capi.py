@@ -320,10 +320,13 @@ def test_gqa_length_validation(seqlens, total, msg):
     from onnxruntime_ep_mlx_amd import _capi as capi
     lib = capi.load()
     host = np.asarray(seqlens, np.int32)
-    node = capi.PaGqaNode(8, 2, 0.0, 0.0, -1, 0, 0, 1, 1e-6)
+    node = capi.PaGqaNode(8, 2, 0.0, 0.0, -1, 0, 0, 1, 1e-6, 0)
     fake = 0x1000  # never dereferenced: validation fails first
-    io = capi.PaGqaIO(capi.PA_DTYPE_BFLOAT16, 2, 1, 8 * 64, 32, fake, fake, fake, fake, fake,
-                      fake, host.ctypes.data, total, None, None, 0, 0, None, None, None, fake)
+    io = capi.PaGqaIO(dtype=capi.PA_DTYPE_BFLOAT16, batch=2, seq=1, query_hidden=8 * 64,
+                      kv_seq=1, query=fake, key=fake, value=fake, past_key=fake,
+                      past_value=fake + 64, past_capacity=32, present_key=fake,
+                      present_value=fake + 64, seqlens_k=fake, host_seqlens_k=host.ctypes.data,
+                      total_sequence_length=total, output=fake)
     nbytes = lib.pa_group_query_attention_workspace_bytes(C.byref(node), C.byref(io))
     assert nbytes > 0
     rc = lib.pa_group_query_attention(C.byref(node), C.byref(io), C.c_void_p(fake), nbytes, None)

@@ -31,10 +31,11 @@ def run_gqa(c, dtype, H, KV, **kw):
     T = {n: to_torch(c[n], dtype) for n in ("q", "k", "v", "pk", "pv")}
     sl = torch.from_numpy(c["seqlens"]).cuda()
     extra = {n: to_torch(c[n], dtype) for n in ("cos", "sin", "sink") if n in c}
+    kw.setdefault("present", "shared")
     out, pk, pv = ep.group_query_attention(
         T["q"], T["k"], T["v"], T["pk"], T["pv"], sl, int(c["seqlens"].max()) + 1,
-        extra.get("cos"), extra.get("sin"), extra.get("sink"), num_heads=H, kv_num_heads=KV,
-        do_rotary=int("cos" in c), **kw)
+        cos_cache=extra.get("cos"), sin_cache=extra.get("sin"), head_sink=extra.get("sink"),
+        num_heads=H, kv_num_heads=KV, do_rotary=int("cos" in c), **kw)
     torch.cuda.synchronize()
     return from_torch(out, dtype), from_torch(pk, dtype), from_torch(pv, dtype)
 

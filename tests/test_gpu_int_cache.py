@@ -241,7 +241,8 @@ def run_gqa_int(c, dtype, packed=False, **kw):
         num_heads=c["H"], kv_num_heads=c["KV"], scale=float(1 / np.sqrt(c["d"])),
         k_scale=torch.from_numpy(c["k_scale"]).cuda(),
         v_scale=torch.from_numpy(c["v_scale"]).cuda(),
-        k_quant_type=QUANT_NAMES[c["modes"][0]], v_quant_type=QUANT_NAMES[c["modes"][1]], **kw)
+        k_quant_type=QUANT_NAMES[c["modes"][0]], v_quant_type=QUANT_NAMES[c["modes"][1]],
+        present=kw.pop("present", "shared"), **kw)
     torch.cuda.synchronize()
     return from_torch(out, dtype), from_torch(pk, cd), from_torch(pv, cd)
 

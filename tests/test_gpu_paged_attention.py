@@ -474,3 +474,17 @@ def test_fp8_long_context_matches_valu():
     g1, g3 = (orc.decode(from_torch(o, BF16), BF16).astype(np.float64) for o in outs)
     assert orc.rel_l2(g1, orc.decode(ref_t, BF16)) <= 2e-3
     assert orc.rel_l2(g1, g3) <= 2e-3
+
+
+# q/k RMSNorm on the C3 decode batch shape (bf16, 64 sequences, 32 / 8 heads, d 128, RoPE theta
+# 500000): the normalised and rotated key rows in the pages are bit-exact, since the device and
+# the oracle sum the squares in one fixed order (64 fma partials, then an XOR butterfly)
+def test_qk_norm_c3_decode_batch():
+    rng = np.random.default_rng(3)
+    B, bs = 64, 16
+    ctx = rng.integers(512, 2049, size=B)
+    mb = int((ctx.max() + bs - 1) // bs)
+    case = make_case(32, 8, 128, B * mb, bs, B, dtype=BF16, seed=3, new_lens=[1] * B,
+                     past=ctx - 1, max_blocks=mb, do_rotary=1, theta=500000.0, qk_norm=True,
+                     std=1.0)
+    check(case)
