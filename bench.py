@@ -51,6 +51,8 @@ def parse():
                     help="also run 1 GiB device copies (known bytes) to scale HBM counters")
     ap.add_argument("--config", choices=("c3", "c4", "c5"), default="c3",
                     help="c3 (default): BASELINE.json config 3; c4 / c5: configs 4 / 5")
+    ap.add_argument("--head-dim", type=int, default=128, choices=(64, 96, 128, 256),
+                    help="c3 only: the same decode batch at another head size (128 = config 3)")
     return ap.parse_args()
 
 
@@ -64,10 +66,10 @@ def load_traffic(name="decode_c3_traffic.json"):
     return t.get("hbm_bytes_per_launch")
 
 
-def build_workload(torch, ep, seed):
+def build_workload(torch, ep, seed, d=128):
     import numpy as np
     rng = np.random.default_rng(seed)
-    B, H, KV, d, bs, nb = 64, 32, 8, 128, 16, 40000
+    B, H, KV, bs, nb = 64, 32, 8, 16, 40000
     ctx = rng.integers(512, 8193, size=B).astype(np.int32)
     mb = 8192 // bs
     perm = rng.permutation(nb).astype(np.int32)
@@ -440,7 +442,7 @@ def main():
     import onnxruntime_ep_mlx_amd as ep
     torch.cuda.set_device(0)
     if args.config == "c3":
-        w = build_workload(torch, ep, args.seed)
+        w = build_workload(torch, ep, args.seed, args.head_dim)
         step = Step(torch, ep, w, args.chunk, kind=1)
     elif args.config == "c4":
         w = build_prefill_workload(torch)
@@ -524,12 +526,16 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
-            "traffic": load_traffic(),
+            "traffic": load_traffic() if w["d"] == 128 else None,
             "kernel": "pa_attention (decode_balanced_kernel + balanced_merge_kernel)",
             "us_per_launch": round(attn_ms * 1e3, 1),
         },
         "cpu_baseline": cpu,
     }
+    if w["d"] != 128:  # not config 3 itself: say so in the line
+        line["metric"] += f" (head_dim {w['d']} variant of config 3)"
+        line["config"]["workload"] = (f"config 3 decode batch at head_dim {w['d']}: RoPE + KV "
+                                      "append + split-K paged attention per step")
     print(json.dumps(line), flush=True)
 
 

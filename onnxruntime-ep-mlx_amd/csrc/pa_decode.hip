@@ -341,7 +341,7 @@ __device__ __forceinline__ void merge_pieces(const AttnParams& p, int b, int kh,
                                              int g, int f, int nparts, int lane) {
   constexpr int DQ = D / 4;   // dims per lane
   constexpr int NV = DQ / 4;  // float4 loads per lane and piece
-  constexpr int KB = 4;       // pieces per batch
+  constexpr int KB = D > 128 ? 2 : 4;  // pieces per batch (register budget)
   const int r = lane >> 2, quarter = lane & 3;
   if (r >= R) return;
   float M = kNegInf, lsum = 0.0f;
@@ -513,6 +513,35 @@ __device__ __forceinline__ uint32_t bld4(__amdgpu_buffer_rsrc_t r, uint32_t voff
   return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 2);
 }
 
+// One lane's value-row slice (D/8 bytes at voff of the row at soff) through buffer loads.
+template <int D>
+__device__ __forceinline__ VRow<D> bld_vrow(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                            uint32_t soff) {
+  if constexpr (D == 64) {
+    return VRow<64>{bld8(r, voff, soff)};
+  } else if constexpr (D == 128) {
+    return VRow<128>{bld16(r, voff, soff)};
+  } else if constexpr (D % 128 == 0) {
+    VRow<D> v;
+#pragma unroll
+    for (int i = 0; i < D / 128; ++i) {
+      const u32x4 x = bld16(r, voff + 16 * i, soff);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v.w[4 * i + k] = x[k];
+    }
+    return v;
+  } else if constexpr (D == 96) {  // one dwordx3 load (4-byte aligned slice)
+    const u32x3 x =
+        __builtin_bit_cast(u32x3, __builtin_amdgcn_raw_buffer_load_b96(r, voff, soff, 2));
+    return VRow<D>{{x[0], x[1], x[2]}};
+  } else {
+    VRow<D> v;
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) v.w[i] = bld4(r, voff + 4 * i, soff);
+    return v;
+  }
+}
+
 // Page id of tile `tile` of a step (lane 16 * tile of `btl`), clamped into the pool, and the
 // byte offset of the tile's first row from the pool base.
 __device__ __forceinline__ uint64_t tile_row_bytes(const AttnParams& p, const Cursor& c, int btl,
@@ -630,12 +659,7 @@ __device__ __forceinline__ void load_stream_step(const AttnParams& p, const SeqW
 #pragma unroll
         for (int q = 0; q < D / 32; ++q) st.k[tile][q] = bld16(rk, lo.koff + 64 * q, 0);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if constexpr (D == 128)
-            st.v[4 * tile + e] = VRow<D>{bld16(rv, lo.voff, e * lo.rowb)};
-          else
-            st.v[4 * tile + e] = VRow<D>{bld8(rv, lo.voff, e * lo.rowb)};
-        }
+        for (int e = 0; e < 4; ++e) st.v[4 * tile + e] = bld_vrow<D>(rv, lo.voff, e * lo.rowb);
       }
     } else {
       const char* kn = reinterpret_cast<const char*>(p.k_new);
@@ -687,30 +711,37 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
   lofs.koff = (uint32_t)c * lofs.rowb + 16 * G;
   lofs.voff = (uint32_t)(4 * G) * lofs.rowb + (uint32_t)(D / 16) * (F8 ? 1 : 2) * c;
 
+  // Block ids run BA steps ahead of the compute in a ring of NBT entries: 2 * (DEPTH - 1) ahead
+  // in DEPTH entries, or, with a one-step ring (rows loaded in the step that uses them), one
+  // step ahead in two entries.  The loop body is unrolled U times so every ring index is a
+  // compile-time constant.
+  constexpr int BA = DEPTH > 1 ? 2 * (DEPTH - 1) : 1;
+  constexpr int NBT = DEPTH > 1 ? DEPTH : 2;
+  constexpr int U = DEPTH > 1 ? DEPTH : 2;
   Cursor cc = cursor_at(sw, p, lo, L, x, u0);
   Cursor cd = cc, cb = cc;
   QueryPtrs qp = query_ptrs<D, F8>(p, sw, cd, g, lane);
   RingStep<TT, D, F8> st[DEPTH];
   u32x4 qr[DEPTH][D / 32];
   typename TT::raw skr[DEPTH];
-  int btr[DEPTH];
-  // Prologue: block ids of steps 0 .. DEPTH-2, their rows, block ids of the next DEPTH-1 steps.
+  int btr[NBT];
+  // Prologue: block ids of steps 0 .. DEPTH-2, their rows, block ids of steps DEPTH-1 .. BA-1.
 #pragma unroll
   for (int j = 0; j < DEPTH - 1; ++j) {
-    btr[j] = load_step_blocks(p, sw, cb, lane, bs_shift);
+    btr[j % NBT] = load_step_blocks(p, sw, cb, lane, bs_shift);
     cursor_next(cb, sw, p, hi, L, x, u0);
   }
   bool qload = true;  // the data cursor's step starts a piece
 #pragma unroll
   for (int j = 0; j < DEPTH - 1; ++j) {
-    load_stream_step<TT, D, F8>(p, sw, cd, btr[j], lane, bs_shift, lofs, qp, qload, st[j], qr[j],
-                                skr[j]);
+    load_stream_step<TT, D, F8>(p, sw, cd, btr[j % NBT], lane, bs_shift, lofs, qp, qload, st[j],
+                                qr[j], skr[j]);
     qload = cursor_next(cd, sw, p, hi, L, x, u0);
     if (qload) qp = query_ptrs<D, F8>(p, sw, cd, g, lane);
   }
 #pragma unroll
-  for (int j = DEPTH - 1; j < 2 * DEPTH - 2; ++j) {
-    btr[j % DEPTH] = load_step_blocks(p, sw, cb, lane, bs_shift);
+  for (int j = DEPTH - 1; j < BA; ++j) {
+    btr[j % NBT] = load_step_blocks(p, sw, cb, lane, bs_shift);
     cursor_next(cb, sw, p, hi, L, x, u0);
   }
 
@@ -729,17 +760,19 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
                       [&](int64_t, int, int rloc) { return (slot * p.kv_heads + pc_kh) * 16 + rloc; });
   };
 
-  for (int k = 0; k < K; k += DEPTH) {
+  for (int k = 0; k < K; k += U) {
 #pragma unroll
-    for (int i = 0; i < DEPTH; ++i) {
-      // Rows of step k+i+DEPTH-1 (block ids fetched DEPTH-1 iterations ago), then the block ids
-      // of step k+i+2*(DEPTH-1).
-      const int sd_slot = (i + DEPTH - 1) % DEPTH, sb_slot = (i + DEPTH - 2) % DEPTH;
-      load_stream_step<TT, D, F8>(p, sw, cd, btr[sd_slot], lane, bs_shift, lofs, qp, qload,
+    for (int i = 0; i < U; ++i) {
+      // Rows of step k+i+DEPTH-1 (block ids fetched BA-DEPTH+1 iterations ago), then the block
+      // ids of step k+i+BA.
+      const int sd_slot = (i + DEPTH - 1) % DEPTH;
+      const int bt_use = (i + DEPTH - 1) % NBT, bt_load = (i + BA) % NBT;
+      const int cs = i % DEPTH;  // ring slot of the step computed now
+      load_stream_step<TT, D, F8>(p, sw, cd, btr[bt_use], lane, bs_shift, lofs, qp, qload,
                                   st[sd_slot], qr[sd_slot], skr[sd_slot]);
       qload = cursor_next(cd, sw, p, hi, L, x, u0);
       if (qload) qp = query_ptrs<D, F8>(p, sw, cd, g, lane);
-      btr[sb_slot] = load_step_blocks(p, sw, cb, lane, bs_shift);
+      btr[bt_load] = load_step_blocks(p, sw, cb, lane, bs_shift);
       cursor_next(cb, sw, p, hi, L, x, u0);
       if (k + i < K) {
         if (cc.bl != pc_bl || cc.u != pc_u) {
@@ -748,7 +781,7 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
           pc_u = cc.u;
           pc_kh = cc.kh;
           pc_total = cc.total;
-          pc_sink = p.head_sink ? TT::to_f32(skr[i]) * kLog2e : (p.smooth_softmax ? 0.0f : kNegInf);
+          pc_sink = p.head_sink ? TT::to_f32(skr[cs]) * kLog2e : (p.smooth_softmax ? 0.0f : kNegInf);
           const int nq = lane_of(sw.q.nq, cc.bl), pastb = lane_of(sw.q.pastb, cc.bl);
           const int R = g * nq;
           const bool rvalid = c < R;
@@ -760,7 +793,7 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
           full_lo = p.window > 0 ? pastb + nq - p.window : 0;
           full_hi = p.causal ? pastb + 1 : pc_total;
 #pragma unroll
-          for (int q = 0; q < D / 32; ++q) rs.qv[q] = __builtin_bit_cast(vec8, qr[i][q]);
+          for (int q = 0; q < D / 32; ++q) rs.qv[q] = __builtin_bit_cast(vec8, qr[cs][q]);
 #pragma unroll
           for (int j = 0; j < D / 16; ++j) rs.o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
           rs.m_run = kNegInf;
@@ -783,7 +816,7 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
         if constexpr (F8) {
           // Page scales of tiles A and B (lanes 0..3); a tile wholly past the end weighs zero
           // (its page id, and so its scale, is not a real one).
-          Step8<D>& cur = st[i];
+          Step8<D>& cur = st[cs];
           const int sc = __builtin_bit_cast(int, cur.sc);
           const bool b_live = t0 + 16 < pc_total;
           if (t0 + 32 > pc_total) {
@@ -803,7 +836,7 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
               __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc, 2)),
               b_live ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc, 3)) : 0.f, masked);
         } else {
-          run(st[i], 1.f, 1.f, 1.f, 1.f);
+          run(st[cs], 1.f, 1.f, 1.f, 1.f);
         }
         cursor_next(cc, sw, p, hi, L, x, u0);
       }
@@ -825,8 +858,9 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
 // balanced_merge_kernel.
 // Ring depth (steps held in registers) of the streaming decode.  bf16/fp16 pages: 2 -- each step
 // is 16 KiB per wavefront, and the smaller ring needs fewer registers (C3 attention launch
-// 179 us against 185 us at depth 3).  fp8 pages: 3 (8 KiB steps; depths 2-5 measured within
-// noise of each other).
+// 179 us against 185 us at depth 3).  Head 256: 1 (a 32 KiB step; depth 2 spills ~80 registers
+// and measured 378 us against 359 us on the C3 batch at head 256).  fp8 pages: 3 (8 KiB steps;
+// depths 2-5 measured within noise of each other).
 #ifndef PA_DECODE_DEPTH
 #define PA_DECODE_DEPTH 2
 #endif
@@ -877,7 +911,7 @@ decode_balanced_kernel(const AttnParams p) {
     const int chunk_total = __builtin_amdgcn_readlane(incl, 63);
     const int lo = max(gs, carry), hi = min(ge, carry + chunk_total);
     if (lo < hi)
-      stream_range<TT, D, CAP, F8, F8 ? PA_DECODE_DEPTH8 : PA_DECODE_DEPTH>(p, sw, lo, hi, L, x,
+      stream_range<TT, D, CAP, F8, F8 ? PA_DECODE_DEPTH8 : (D > 128 ? 1 : PA_DECODE_DEPTH)>(p, sw, lo, hi, L, x,
                                                                            u0, lane);
     carry += chunk_total;
   }
@@ -919,7 +953,15 @@ balanced_merge_kernel(const AttnParams p) {
 template <typename TT, int D>
 hipError_t launch_d(const AttnParams& p, dim3 grid, dim3 block, bool balanced, bool f8,
                     hipStream_t s) {
-  if (balanced) {
+  if constexpr (D != 64 && D != 128) {
+    // Heads 96 / 256: the streaming decode on pages in the activation dtype only.
+    if (!balanced || f8) return hipErrorInvalidValue;
+    if (p.softcap > 0.0f)
+      hipLaunchKernelGGL((decode_balanced_kernel<TT, D, true, false>), grid, block, 0, s, p);
+    else
+      hipLaunchKernelGGL((decode_balanced_kernel<TT, D, false, false>), grid, block, 0, s, p);
+    return hipGetLastError();
+  } else if (balanced) {
     if (p.softcap > 0.0f) {
       if (f8) hipLaunchKernelGGL((decode_balanced_kernel<TT, D, true, true>), grid, block, 0, s, p);
       else hipLaunchKernelGGL((decode_balanced_kernel<TT, D, true, false>), grid, block, 0, s, p);
@@ -948,7 +990,9 @@ hipError_t launch_t(const AttnParams& p, dim3 grid, dim3 block, bool balanced, b
                     hipStream_t s) {
   switch (p.head_dim) {
     case 64: return launch_d<TT, 64>(p, grid, block, balanced, f8, s);
+    case 96: return launch_d<TT, 96>(p, grid, block, balanced, f8, s);
     case 128: return launch_d<TT, 128>(p, grid, block, balanced, f8, s);
+    case 256: return launch_d<TT, 256>(p, grid, block, balanced, f8, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -957,10 +1001,11 @@ hipError_t launch_t(const AttnParams& p, dim3 grid, dim3 block, bool balanced, b
 
 bool balanced_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype, int block_size) {
   if (act != PA_DTYPE_FLOAT16 && act != PA_DTYPE_BFLOAT16) return false;
-  if (head_dim != 64 && head_dim != 128) return false;
+  if (head_dim != 64 && head_dim != 96 && head_dim != 128 && head_dim != 256) return false;
   if (block_size <= 0 || (block_size & (block_size - 1)) != 0) return false;
   if (cache_dtype == act) return true;
-  return cache_dtype == PA_DTYPE_FP8_E4M3 && block_size >= 16;
+  return cache_dtype == PA_DTYPE_FP8_E4M3 && block_size >= 16 &&
+         (head_dim == 64 || head_dim == 128);
 }
 
 bool decode_mfma_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype) {
@@ -986,6 +1031,20 @@ hipError_t launch_decode_mfma(const AttnParams& p, pa_dtype act, pa_dtype cache_
   return launch_t<TBF16>(p, grid, dim3(64), false, false, s);
 }
 
+// The partial merge of the balanced decode, for the head size of the decode launch.
+template <typename TT>
+hipError_t launch_merge(const AttnParams& p, hipStream_t s) {
+  const dim3 grid(p.kv_heads, p.batch), block(64);
+  switch (p.head_dim) {
+    case 64: hipLaunchKernelGGL((balanced_merge_kernel<TT, 64>), grid, block, 0, s, p); break;
+    case 96: hipLaunchKernelGGL((balanced_merge_kernel<TT, 96>), grid, block, 0, s, p); break;
+    case 128: hipLaunchKernelGGL((balanced_merge_kernel<TT, 128>), grid, block, 0, s, p); break;
+    case 256: hipLaunchKernelGGL((balanced_merge_kernel<TT, 256>), grid, block, 0, s, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 // Balanced launch: p.max_splits holds the segment count; every sequence must have at most 16
 // grouped query rows (g * query length <= 16).  Launches the decode and the partial merge.
 hipError_t launch_decode_balanced(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
@@ -1003,16 +1062,7 @@ hipError_t launch_decode_balanced(const AttnParams& p, pa_dtype act, pa_dtype ca
   hipError_t e = (act == PA_DTYPE_FLOAT16) ? launch_t<TF16>(p, grid, block, true, f8, s)
                                            : launch_t<TBF16>(p, grid, block, true, f8, s);
   if (e != hipSuccess) return e;
-  const dim3 mgrid(p.kv_heads, p.batch);
-  const bool f16 = act == PA_DTYPE_FLOAT16;
-  if (p.head_dim == 64) {
-    if (f16) hipLaunchKernelGGL((balanced_merge_kernel<TF16, 64>), mgrid, dim3(64), 0, s, p);
-    else hipLaunchKernelGGL((balanced_merge_kernel<TBF16, 64>), mgrid, dim3(64), 0, s, p);
-  } else {
-    if (f16) hipLaunchKernelGGL((balanced_merge_kernel<TF16, 128>), mgrid, dim3(64), 0, s, p);
-    else hipLaunchKernelGGL((balanced_merge_kernel<TBF16, 128>), mgrid, dim3(64), 0, s, p);
-  }
-  return hipGetLastError();
+  return act == PA_DTYPE_FLOAT16 ? launch_merge<TF16>(p, s) : launch_merge<TBF16>(p, s);
 }
 
 }  // namespace pa

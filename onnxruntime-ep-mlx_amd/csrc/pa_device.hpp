@@ -14,6 +14,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
@@ -389,8 +390,8 @@ hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype ca
                                   hipStream_t s);
 hipError_t launch_split_reduce(const AttnParams& p, pa_dtype act, hipStream_t s);
 bool decode_mfma_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype);
-// Balanced (streaming) decode: fp16/bf16 activations, d in {64, 128}, power-of-two pages,
-// pages in the activation dtype or fp8 e4m3 (then at least 16 rows per page).
+// Balanced (streaming) decode: fp16/bf16 activations, d in {64, 96, 128, 256}, power-of-two
+// pages, pages in the activation dtype or (d 64 / 128) fp8 e4m3 with at least 16 rows per page.
 bool balanced_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype, int block_size);
 bool prefill_mfma_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype);
 

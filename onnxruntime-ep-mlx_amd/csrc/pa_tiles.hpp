@@ -15,8 +15,12 @@
 namespace pa {
 namespace {
 
+// One lane's slice of one value row: DL = D/16 elements (D/32 words); 64 and 128 as vectors.
 template <int D>
-struct VRow;  // one lane's slice of one value row: DL = D/16 elements
+struct VRow {
+  uint32_t w[D / 32];
+  __device__ uint32_t word(int i) const { return w[i]; }
+};
 template <>
 struct VRow<64> {
   u32x2 w;
@@ -57,10 +61,29 @@ __device__ __forceinline__ uint32_t ld4s(const char* ptr) {
 }
 template <int D>
 __device__ __forceinline__ VRow<D> ld_vrow_s(const char* ptr) {
-  if constexpr (D == 64)
+  if constexpr (D == 64) {
     return VRow<64>{ld8s(ptr)};
-  else
+  } else if constexpr (D == 128) {
     return VRow<128>{ld16s(ptr)};
+  } else if constexpr (D % 128 == 0) {  // 16-byte pieces (the slice is 16-byte aligned)
+    VRow<D> r;
+#pragma unroll
+    for (int i = 0; i < D / 128; ++i) {
+      const u32x4 v = ld16s(ptr + 16 * i);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) r.w[4 * i + k] = v[k];
+    }
+    return r;
+  } else if constexpr (D == 96) {  // 12-byte slices, 4-byte aligned: one dwordx3 load
+    VRow<D> r;
+    __builtin_memcpy(r.w, __builtin_assume_aligned(ptr, 4), 12);
+    return r;
+  } else {  // 4-byte words
+    VRow<D> r;
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) r.w[i] = ld4s(ptr + 4 * i);
+    return r;
+  }
 }
 
 template <int D>
