@@ -211,7 +211,8 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
     const int64_t rbs = ((int64_t)g * mq + pa::kPrefillRows - 1) / pa::kPrefillRows;
     const int64_t units = (int64_t)b->batch * c->kv_heads * rbs;
     const int64_t target = 2 * (int64_t)device_cus();
-    if (units >= target && units <= (int64_t)INT32_MAX / 4) {
+    if (units >= target && units <= (int64_t)INT32_MAX / 4 &&
+        pa::prefill_planned_supported(c->head_dim)) {
       // Enough workgroups for every slot: planned units, longest first, long items split in two
       // (the tail of uneven row blocks otherwise idles ~28% of the slots at the C4 shape).
       pl.chunk = (int)std::min<int64_t>(((int64_t)ctx + 31) / 32 * 32, INT32_MAX / 2);

@@ -107,6 +107,21 @@ __device__ __forceinline__ RoleGeom role_geom(int role, int c, int G) {
   return g;
 }
 
+// PW words of one value row slice at ptr (4-byte aligned; 16-byte aligned when PW % 4 == 0).
+template <int PW>
+__device__ __forceinline__ void load_words(uint32_t* r, const char* ptr) {
+  if constexpr (PW % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < PW / 4; ++i) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(ptr + 16 * i);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) r[4 * i + k] = v[k];
+    }
+  } else {
+    __builtin_memcpy(r, __builtin_assume_aligned(ptr, 4), 4 * PW);
+  }
+}
+
 // Issue this wavefront's loads of the step at key t0.
 template <int D>
 __device__ __forceinline__ void load_quarter(const WaveInfo& w, PageWindow& pw, const RoleGeom& rg,
@@ -115,6 +130,30 @@ __device__ __forceinline__ void load_quarter(const WaveInfo& w, PageWindow& pw, 
   // With every key in the pages the last (partial) step comes from them too: rows past the end
   // are masked / zeroed and page ids are clamped into the pool.
   const bool paged = w.bs % 16 == 0 && (t0 + 32 <= w.cache_limit || w.cache_limit >= w.total);
+  if constexpr (D != 64 && D != 128) {
+    // Other heads: key role = KS 16-byte k-step items of row c; value role = the lane's D/8
+    // bytes of rows 4G .. 4G+3.
+    constexpr int KS = D / 32, PW = D / 32;
+    const int c = lane & 15, G = lane >> 4;
+    const int64_t tb = paged ? tile_base(w, pw, t, lane, D) : 0;
+    if (!rg.value) {
+      const char* rp = paged ? w.kc + tb + (int64_t)c * w.rowb : row_ptr(w, t + c, false, D);
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const u32x4 v = ld16(rp + 16 * G + 64 * s);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) q.r[4 * s + k] = v[k];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const char* rp = paged ? w.vc + tb + (int64_t)(4 * G + e) * w.rowb
+                               : row_ptr(w, t + 4 * G + e, true, D);
+        load_words<PW>(q.r + PW * e, rp + (D / 16) * 2 * c);
+      }
+    }
+    return;
+  }
   if (paged) {
     const char* base = (rg.value ? w.vc : w.kc) + tile_base(w, pw, t, lane, D) +
                        (int64_t)rg.row0 * w.rowb + rg.col0;
@@ -167,8 +206,11 @@ __device__ __forceinline__ void store_quarter(u32x4 (*buf)[64], Quarter<D>& q, i
   }
 }
 
+// Two workgroups per CU; one at head 256, whose row state and step operands need the larger
+// register budget.
 template <typename TT, int D, bool CAP, int NG>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D > 128 ? 1 : 2,
+                                                                     D > 128 ? 1 : 2))) void
 prefill_kernel(const AttnParams p) {
   using vec8 = typename TT::vec8;
   constexpr int KS = D / 32, DL = D / 16, NI = 2 * KS + DL;
@@ -262,7 +304,23 @@ prefill_kernel(const AttnParams p) {
   __syncthreads();
   for (int k = 0; k < nsteps; ++k) {
     const int t0 = t_first + 32 * k;
-    if (t0 < any_hi && t0 + 32 > any_lo) {
+    if constexpr (D > 128) {
+      // Heads above 128: operands read from LDS where they are used (the row state of two
+      // groups already takes most of the register file).
+      if (t0 < any_hi && t0 + 32 > any_lo) {
+        const int bsel = k & 1;
+        auto kl = [&](int tile, int s) {
+          return __builtin_bit_cast(vec8, lds[bsel][tile * KS + s][lane]);
+        };
+        auto vl = [&](int n) { return __builtin_bit_cast(vec8, lds[bsel][2 * KS + n][lane]); };
+        if (t0 >= all_lo && t0 + 32 <= all_hi)
+          attend_groups_ops<TT, D, CAP, false, NG>(rs, kl, vl, t0, end, G, scale_log2, scale,
+                                                   p.softcap);
+        else
+          attend_groups_ops<TT, D, CAP, true, NG>(rs, kl, vl, t0, end, G, scale_log2, scale,
+                                                  p.softcap);
+      }
+    } else if (t0 < any_hi && t0 + 32 > any_lo) {
       u32x4 kop[2][KS];
       u32x4 vop[DL];
 #pragma unroll
@@ -996,9 +1054,24 @@ template <typename TT>
 hipError_t launch_t(const AttnParams& p, dim3 grid, hipStream_t s) {
   switch (p.head_dim) {
     case 64: return launch_d<TT, 64>(p, grid, s);
+    case 96: return launch_d<TT, 96>(p, grid, s);
     case 128: return launch_d<TT, 128>(p, grid, s);
+    case 256: return launch_d<TT, 256>(p, grid, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+// The merge of the planned prefill's split items (heads whose rows tile the merge workgroup).
+template <typename TT>
+hipError_t launch_prefill_merge(const AttnParams& p, hipStream_t s) {
+  const dim3 grid(p.plan_items * (kPrefillRows / kPrefillMergeRows)), block(256);
+  switch (p.head_dim) {
+    case 64: hipLaunchKernelGGL((prefill_merge_kernel<TT, 64>), grid, block, 0, s, p); break;
+    case 128: hipLaunchKernelGGL((prefill_merge_kernel<TT, 128>), grid, block, 0, s, p); break;
+    case 256: hipLaunchKernelGGL((prefill_merge_kernel<TT, 256>), grid, block, 0, s, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -1007,7 +1080,8 @@ hipError_t launch_t(const AttnParams& p, dim3 grid, hipStream_t s) {
 // (workgroups past the planned count exit at once), then the merge of the split items.
 hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
                                   hipStream_t s) {
-  if (!prefill_mfma_supported(p.head_dim, act, cache_dtype)) return hipErrorInvalidValue;
+  if (!prefill_mfma_supported(p.head_dim, act, cache_dtype) || !prefill_planned_supported(p.head_dim))
+    return hipErrorInvalidValue;
   if (p.linear_cap > 0 || p.plan_items <= 0 || p.plan_rbs <= 0 || !p.plan || !p.plan_info ||
       !p.plan_split || !p.part_o || !p.part_ml || p.max_splits != 1)
     return hipErrorInvalidValue;
@@ -1016,21 +1090,19 @@ hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype ca
   const dim3 grid(2 * p.plan_items, 1);
   hipError_t e = act == PA_DTYPE_FLOAT16 ? launch_t<TF16>(p, grid, s) : launch_t<TBF16>(p, grid, s);
   if (e != hipSuccess) return e;
-  const dim3 mgrid(p.plan_items * (kPrefillRows / kPrefillMergeRows));
-  if (p.head_dim == 64) {
-    if (act == PA_DTYPE_FLOAT16) hipLaunchKernelGGL((prefill_merge_kernel<TF16, 64>), mgrid, dim3(256), 0, s, p);
-    else hipLaunchKernelGGL((prefill_merge_kernel<TBF16, 64>), mgrid, dim3(256), 0, s, p);
-  } else {
-    if (act == PA_DTYPE_FLOAT16) hipLaunchKernelGGL((prefill_merge_kernel<TF16, 128>), mgrid, dim3(256), 0, s, p);
-    else hipLaunchKernelGGL((prefill_merge_kernel<TBF16, 128>), mgrid, dim3(256), 0, s, p);
-  }
-  return hipGetLastError();
+  return act == PA_DTYPE_FLOAT16 ? launch_prefill_merge<TF16>(p, s)
+                                 : launch_prefill_merge<TBF16>(p, s);
 }
 
 bool prefill_mfma_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype) {
   if (act != PA_DTYPE_FLOAT16 && act != PA_DTYPE_BFLOAT16) return false;
   if (cache_dtype != act) return false;
-  return head_dim == 64 || head_dim == 128;
+  return head_dim == 64 || head_dim == 96 || head_dim == 128 || head_dim == 256;
+}
+
+// The planned launch merges split items with D/8 lanes per row: heads whose rows tile that.
+bool prefill_planned_supported(int head_dim) {
+  return head_dim == 64 || head_dim == 128 || head_dim == 256;
 }
 
 // Grid: one workgroup per (row block, sequence, kv-head) and context chunk (p.max_splits

@@ -317,14 +317,12 @@ __device__ __forceinline__ void attend_step(RowState<TT, D>& rs, const u32x4 (&k
 // every group's probabilities and PV MFMAs in one block, each value operand built once.
 // Without softcap the scale folds into the exponents (step_scores FOLD), which takes
 // scale_log2 >= 0: the caller moves the sign of a negative scale into the query operands.
-template <typename TT, int D, bool CAP, bool MASK, int NG, typename ValueOp>
-__device__ __forceinline__ void attend_groups(RowState<TT, D> (&rs)[NG],
-                                              const u32x4 (&k)[2][D / 32], ValueOp vop, int t0,
-                                              int end, int G, float scale_log2, float scale,
-                                              float cap) {
+template <typename TT, int D, bool CAP, bool MASK, int NG, typename KeyOp, typename ValueOp>
+__device__ __forceinline__ void attend_groups_ops(RowState<TT, D> (&rs)[NG], KeyOp kop,
+                                                  ValueOp vop, int t0, int end, int G,
+                                                  float scale_log2, float scale, float cap) {
   using vec8 = typename TT::vec8;
   constexpr int DL = D / 16;
-  auto kop = [&](int tile, int s) { return __builtin_bit_cast(vec8, k[tile][s]); };
   float x[NG][8], lmax[NG];
   bool any = false;
 #pragma unroll
@@ -351,6 +349,17 @@ __device__ __forceinline__ void attend_groups(RowState<TT, D> (&rs)[NG],
       rs[j].o[n] = TT::mfma(plo[j], vb, rs[j].o[n]);
     }
   }
+}
+
+template <typename TT, int D, bool CAP, bool MASK, int NG, typename ValueOp>
+__device__ __forceinline__ void attend_groups(RowState<TT, D> (&rs)[NG],
+                                              const u32x4 (&k)[2][D / 32], ValueOp vop, int t0,
+                                              int end, int G, float scale_log2, float scale,
+                                              float cap) {
+  using vec8 = typename TT::vec8;
+  attend_groups_ops<TT, D, CAP, MASK, NG>(
+      rs, [&](int tile, int s) { return __builtin_bit_cast(vec8, k[tile][s]); }, vop, t0, end, G,
+      scale_log2, scale, cap);
 }
 
 // One 32-key step held in registers as loaded (value rows regrouped here).
@@ -492,10 +501,16 @@ __device__ __forceinline__ void store_rows(const RowState<TT, D>& rs, const Attn
                ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
       }
       char* dst = reinterpret_cast<char*>(p.part_o) + (pi * D + DL * c) * 2;
-      if constexpr (DL == 8)
-        *reinterpret_cast<u32x4*>(dst) = u32x4{w[0], w[1], w[2], w[3]};
-      else
+      if constexpr (DL % 8 == 0) {
+#pragma unroll
+        for (int m = 0; m < DL / 8; ++m)
+          reinterpret_cast<u32x4*>(dst)[m] = u32x4{w[4 * m], w[4 * m + 1], w[4 * m + 2], w[4 * m + 3]};
+      } else if constexpr (DL == 4) {
         *reinterpret_cast<u32x2*>(dst) = u32x2{w[0], w[1]};
+      } else {
+#pragma unroll
+        for (int m = 0; m < DL / 2; ++m) reinterpret_cast<uint32_t*>(dst)[m] = w[m];
+      }
       if (c == 0) {
         p.part_ml[pi * 2 + 0] = mi + (float)ex[i];
         p.part_ml[pi * 2 + 1] = __builtin_ldexpf(li, -ex[i]);

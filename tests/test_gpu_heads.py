@@ -1,12 +1,14 @@
-"""Heads 96 and 256 on the streaming matrix-core decode (decode_balanced_kernel<T, 96 | 256>).
+"""Heads 96 and 256 on the matrix cores: the streaming decode (decode_balanced_kernel<T, 96 | 256>)
+and the LDS-shared prefill kernel (prefill_kernel<T, 96 | 256>).
 
 The reference's direct kernel takes heads 64/96/128/256 (attention.rs:4140); its head-256 tests
 (test_paged_attention.py:245-247, :289-318) are mirrored in test_gpu_paged_attention.py and now
 reach this kernel for their decode-shaped batches.  Here: ragged decode batches in both dtypes,
 rotary, softcap + sink, local window, page sizes 16/32/64, two query tokens per sequence
-(g * nq <= 16), long contexts split over many segments (merged), a negative scale, and the
+(g * nq <= 16), long contexts split over many segments (merged), a negative scale, the
 kernel-level entry forced to the streaming decode (kind 1), which fails for a head size the
-kernel does not take.
+kernel does not take, and multi-token batches on the prefill kernel (the planned launch at
+head 256 is in test_gpu_paged_attention.py::test_prefill_planned).
 
 Bars as everywhere: caches bit-exact, outputs rel-L2 <= 2e-3 against the T-rounded oracle
 (<= 4e-3 against its fp64 output).
@@ -68,13 +70,11 @@ def test_decode_heads(d, dtype, variant):
 # long contexts: one sequence far longer than the others, split over many segments
 @pytest.mark.parametrize("d", [96, 256])
 def test_decode_heads_long_context(d):
-    rng = np.random.default_rng(d)
     B, bs = 4, 16
     ctx = np.array([12000, 300, 4100, 77])
     mb = int((ctx.max() + bs - 1) // bs)
     case = make_case(8, 1, d, B * mb, bs, B, dtype=BF16, seed=d, new_lens=[1] * B,
                      past=ctx - 1, max_blocks=mb, std=1.0, do_rotary=1, theta=500000.0)
-    del rng
     check(case)
 
 
@@ -99,3 +99,27 @@ def test_kernel_level_streaming_decode(d):
     assert np.array_equal(a, b)
     got = orc.decode(a, BF16).astype(np.float64)
     assert orc.rel_l2(got, orc.decode(ref_t, BF16)) <= 2e-3
+
+
+# multi-token batches (more than 16 grouped rows: the LDS-shared prefill kernel): ragged chunks,
+# an empty sequence, causal / window / softcap / sink, both dtypes
+@pytest.mark.parametrize("d", [96, 256])
+@pytest.mark.parametrize("dtype,variant", [(BF16, "plain"), (F16, "plain"), (BF16, "window"),
+                                           (F16, "softcap_sink"), (BF16, "non_causal"),
+                                           (BF16, "block32")])
+def test_prefill_heads(d, dtype, variant):
+    rng = np.random.default_rng(d + len(variant))
+    B, H, KV = 4, 16, 4
+    bs = 32 if variant == "block32" else 16
+    new_lens = [37, 0, 70, 5]
+    past = rng.integers(0, 600, size=B)
+    mb = int((past.max() + max(new_lens) + bs - 1) // bs)
+    kw = {}
+    if variant == "window":
+        kw = dict(window=50)
+    elif variant == "softcap_sink":
+        kw = dict(softcap=20.0, head_sink=np.linspace(-1, 1, H))
+    elif variant == "non_causal":
+        kw = dict(causal=0)
+    check(make_case(H, KV, d, B * mb + 5, bs, B, dtype=dtype, seed=d + len(variant),
+                    new_lens=new_lens, past=past, max_blocks=mb, std=1.0, **kw))

@@ -329,9 +329,10 @@ def test_prefill_kernel_level(chunk, new_rows_in_cache, bs, d, dtype, window, so
 @pytest.mark.parametrize("d,dtype,sink,vstd,softcap,window", [
     (64, BF16, False, None, 0.0, -1), (128, F16, True, None, 0.0, -1),
     (128, BF16, True, 1e6, 0.0, -1), (64, BF16, False, 1e-6, 0.0, -1),
-    (128, BF16, True, None, 30.0, 2900)],
+    (128, BF16, True, None, 30.0, 2900), (256, BF16, True, None, 0.0, -1),
+    (96, F16, False, None, 30.0, 2900)],
     ids=["d64_bf16", "d128_f16_sink", "d128_bf16_large_v", "d64_bf16_tiny_v",
-         "d128_bf16_softcap_window"])
+         "d128_bf16_softcap_window", "d256_bf16_sink", "d96_f16_softcap_window_grid"])
 def test_prefill_planned(d, dtype, sink, vstd, softcap, window):
     import torch
     import onnxruntime_ep_mlx_amd as ep
