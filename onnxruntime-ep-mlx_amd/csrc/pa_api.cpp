@@ -176,7 +176,9 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
                       pa::balanced_supported(c->head_dim, act, c->dtype, c->block_size) &&
                       (int64_t)c->num_blocks * c->block_size <= (int64_t)UINT32_MAX &&
                       (int64_t)std::max(b->batch, 0) * (cap / 32 + 2) < (int64_t)INT32_MAX;
-  if (kind == 0 && linear) kind = bal_ok ? 1 : 3;  // contiguous caches: streaming or VALU kernel
+  // Contiguous caches: the streaming decode, the LDS-shared prefill kernels, or VALU.
+  if (kind == 0 && linear)
+    kind = bal_ok ? 1 : pa::prefill_mfma_supported(c->head_dim, act, c->dtype) ? 2 : 3;
   if (kind == 0) {
     if (bal_ok || (mfma && (int64_t)g * mq <= 16))
       kind = 1;
@@ -287,9 +289,9 @@ struct RunOpts {
   bool smooth_softmax = false;
 };
 
-// The kernel family a call with these options runs: a bias or per-sequence key counts beyond
-// what the decode kernels take send it to the VALU kernel.
-int effective_kind(int kind, const RunOpts& o) { return o.bias ? 3 : kind; }
+// The kernel family a call with these options runs: a bias or per-sequence key counts (which
+// only the VALU kernel takes) send it to the VALU kernel.
+int effective_kind(int kind, const RunOpts& o) { return (o.bias || o.key_limit) ? 3 : kind; }
 
 int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype act,
                   const void* q, const void* kn, const void* vn, void* out, void* ws,
@@ -329,8 +331,9 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
     return fail(PA_ERR_INVALID_ARGUMENT, "softcap must be finite and non-negative");
   kind = effective_kind(kind, opts);
   Plan pl = make_plan(c, b, a, act, kind, chunk, opts.linear_cap > 0, opts.linear_cap);
-  if (opts.linear_cap > 0 && !(pl.balanced || pl.kind == 3))
-    return fail(PA_ERR_UNSUPPORTED, "contiguous caches run on the decode or VALU kernels only");
+  if (opts.linear_cap > 0 && !(pl.balanced || pl.kind == 2 || pl.kind == 3))
+    return fail(PA_ERR_UNSUPPORTED,
+                "contiguous caches run on the streaming decode, prefill or VALU kernels only");
   size_t need = workspace_for(c, b, a, pl);
   if (need > 0 && (!ws || ws_bytes < need))
     return fail(PA_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes, got %zu", need,
@@ -960,6 +963,7 @@ struct GqaLayout {
   bool packed, transform;
   bool shared;      // present == past: updated in place
   bool in_ws;       // present omitted: it lives in the workspace
+  bool ragged;      // some sequence may be shorter than the query rows (per-sequence key counts)
   int cap_in;       // past capacity (0 without a past)
   int cap_p;        // present capacity
   size_t row_bytes; // bytes of one stored row of one kv-head
@@ -1084,6 +1088,16 @@ int gqa_layout(const pa_gqa_node* n, const pa_gqa_io* io, GqaLayout* L) {
   o = RunOpts{};
   o.new_rows_in_cache = true;
   o.linear_cap = L->cap_p;
+  // A first prompt (total == seq) may hold sequences shorter than the query rows (right-padded
+  // rows): their key counts come from seqlens_k (VALU kernel).  Otherwise every sequence has
+  // query_past + seq keys and any kernel family serves it.  The pointer is set per call.
+  L->ragged = total == io->seq;
+  if (L->ragged && io->host_seqlens_k) {
+    L->ragged = false;
+    for (int b = 0; b < io->batch; ++b) L->ragged |= io->host_seqlens_k[b] + 1 < io->seq;
+  }
+  static const int32_t kPlanOnly = 0;  // non-null marker for planning; replaced before running
+  o.key_limit = L->ragged ? &kPlanOnly : nullptr;
   o.bias = io->attention_bias;
   o.bias_b = io->bias_batch;
   o.bias_h = io->bias_heads;
@@ -1190,7 +1204,7 @@ int pa_group_query_attention(const pa_gqa_node* n, const pa_gqa_io* io, void* wo
   L.batch.cumulative_sequence_length = meta;
   L.batch.past_seqlens = meta + io->batch + 1;
   L.batch.block_table = meta;  // unused for contiguous caches
-  L.opts.key_limit = meta + 2 * io->batch + 1;
+  L.opts.key_limit = L.ragged ? meta + 2 * io->batch + 1 : nullptr;
   if (L.in_ws) {
     L.cache.key_cache = ws + L.pres_off;
     L.cache.value_cache = ws + L.pres_off + L.pres_side;

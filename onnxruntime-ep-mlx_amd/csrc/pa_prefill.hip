@@ -73,11 +73,12 @@ __device__ __forceinline__ void window_at(PageWindow& pw, const WaveInfo& w, int
 // Byte offset (from the cache base) of the first row of the 16-key tile starting at key t.
 __device__ __forceinline__ int64_t tile_base(const WaveInfo& w, PageWindow& pw, int t, int lane,
                                              int D) {
+  if (w.lin_row0 >= 0) return (w.lin_row0 + t) * w.rowb;  // contiguous cache
   const int bi = min(div_bs(t, w), w.max_blocks - 1);
   if (bi < pw.first || bi >= pw.first + 64) window_at(pw, w, bi, lane);
   int64_t blk = __builtin_amdgcn_readlane(pw.ids, bi - pw.first);
   blk = min(max(blk, (int64_t)0), w.num_blocks - 1);
-  return (blk * w.bs + mod_bs(t, w)) * w.rowb + (int64_t)w.kh * D * 2;
+  return (blk * w.bs + mod_bs(t, w)) * w.rowb + w.hoff;
 }
 
 // Per-lane geometry of a role: piece s sits at row `row0 + s * row_step` of the tile and byte
@@ -129,7 +130,9 @@ __device__ __forceinline__ void load_quarter(const WaveInfo& w, PageWindow& pw, 
   const int t = t0 + 16 * (role & 1);
   // With every key in the pages the last (partial) step comes from them too: rows past the end
   // are masked / zeroed and page ids are clamped into the pool.
-  const bool paged = w.bs % 16 == 0 && (t0 + 32 <= w.cache_limit || w.cache_limit >= w.total);
+  // (Contiguous caches: only steps whose 32 rows all lie inside the capacity.)
+  const bool paged = w.bs % 16 == 0 && (t0 + 32 <= w.cache_limit || w.cache_limit >= w.total) &&
+                     (w.lin_row0 < 0 || t0 + 32 <= w.lin_cap);
   if constexpr (D != 64 && D != 128) {
     // Other heads: key role = KS 16-byte k-step items of row c; value role = the lane's D/8
     // bytes of rows 4G .. 4G+3.
@@ -462,14 +465,20 @@ __device__ __forceinline__ void mx_load(const WaveInfo& w, PageWindow& pw, int w
   constexpr int D = 128;
   const int kr = lane & 15, cq = lane >> 4;
   const int dg = lane & 7, hh = (lane >> 3) & 1, t = lane >> 4;
-  const int64_t koff = (int64_t)w.kh * D * 2 + 16 * cq;
-  const int64_t voff = (int64_t)w.kh * D * 2 + (32 * wave + 4 * dg) * 2;
-  const bool paged = w.bs % 16 == 0 && (t0 + kMxKeys <= w.cache_limit || w.cache_limit >= w.total);
+  const int64_t koff = w.hoff + 16 * cq;
+  const int64_t voff = w.hoff + (32 * wave + 4 * dg) * 2;
+  const bool paged = w.bs % 16 == 0 && (t0 + kMxKeys <= w.cache_limit || w.cache_limit >= w.total) &&
+                     (w.lin_row0 < 0 || t0 + kMxKeys <= w.lin_cap);
   if (paged) {
     // pool row of the first key of each 16-key group (wave-uniform), from the block-table window
+    // (contiguous caches: consecutive rows)
     int64_t grp[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
+      if (w.lin_row0 >= 0) {
+        grp[q] = w.lin_row0 + t0 + 16 * q;
+        continue;
+      }
       const int bi = min(div_bs(t0 + 16 * q, w), w.max_blocks - 1);
       if (bi < pw.first || bi >= pw.first + 64) window_at(pw, w, bi, lane);
       int64_t blk = __builtin_amdgcn_readlane(pw.ids, bi - pw.first);
@@ -1082,7 +1091,7 @@ hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype ca
                                   hipStream_t s) {
   if (!prefill_mfma_supported(p.head_dim, act, cache_dtype) || !prefill_planned_supported(p.head_dim))
     return hipErrorInvalidValue;
-  if (p.linear_cap > 0 || p.plan_items <= 0 || p.plan_rbs <= 0 || !p.plan || !p.plan_info ||
+  if (p.plan_items <= 0 || p.plan_rbs <= 0 || !p.plan || !p.plan_info ||
       !p.plan_split || !p.part_o || !p.part_ml || p.max_splits != 1)
     return hipErrorInvalidValue;
   if ((int64_t)p.plan_items * (kPrefillRows / kPrefillMergeRows) > INT32_MAX) return hipErrorInvalidValue;
@@ -1110,7 +1119,6 @@ bool prefill_planned_supported(int head_dim) {
 hipError_t launch_prefill_mfma(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
                                hipStream_t s) {
   if (!prefill_mfma_supported(p.head_dim, act, cache_dtype)) return hipErrorInvalidValue;
-  if (p.linear_cap > 0) return hipErrorInvalidValue;  // paged caches only
   if (p.batch <= 0) return hipSuccess;
   if (p.chunk < 32 || p.chunk % 32 != 0 || p.max_splits < 1) return hipErrorInvalidValue;
   const int g = p.num_heads / p.kv_heads;

@@ -102,9 +102,14 @@ struct WaveInfo {
   int bs, bs_shift;  // block size, log2 if a power of two else -1
   int max_blocks, num_tokens;
   int64_t num_blocks;
-  int64_t rowb;      // bytes between consecutive cache rows (kv_heads * D * 2)
+  int64_t rowb;      // bytes between consecutive cache rows (kv_heads * D * 2; contiguous: D * 2)
   int first_bi;      // first block-table index of the chunk
   const int32_t* bt; // this sequence's block-table row
+  int64_t hoff;      // byte offset of the kv-head's slice in a row (contiguous caches: 0)
+  // Contiguous [batch, kv_heads, cap, D] caches (GroupQueryAttention present): row of key 0 of
+  // this (sequence, kv-head), and cap; lin_row0 < 0 for pages.
+  int64_t lin_row0;
+  int lin_cap;
 };
 
 __device__ __forceinline__ int div_bs(int x, const WaveInfo& w) {
@@ -119,14 +124,16 @@ __device__ __forceinline__ int mod_bs(int x, const WaveInfo& w) {
 // row; block ids are clamped into the pool, so malformed metadata cannot fault.
 __device__ __forceinline__ const char* row_ptr(const WaveInfo& w, int pos, bool value, int D) {
   if (pos >= w.total) pos = w.total - 1;
+  if (w.lin_row0 >= 0)  // contiguous cache holding every key (total <= cap)
+    return (value ? w.vc : w.kc) + (w.lin_row0 + max(pos, 0)) * w.rowb;
   if (pos < w.cache_limit) {
     const int bi = min(div_bs(pos, w), w.max_blocks - 1);
     int64_t blk = w.bt[bi];
     blk = min(max(blk, (int64_t)0), w.num_blocks - 1);
-    return (value ? w.vc : w.kc) + (blk * w.bs + mod_bs(pos, w)) * w.rowb + (int64_t)w.kh * D * 2;
+    return (value ? w.vc : w.kc) + (blk * w.bs + mod_bs(pos, w)) * w.rowb + w.hoff;
   }
   int64_t tok = min(max((int64_t)w.s0 + (pos - w.pastb), (int64_t)0), (int64_t)w.num_tokens - 1);
-  return (value ? w.vn : w.kn) + tok * w.rowb + (int64_t)w.kh * D * 2;
+  return (value ? w.vn : w.kn) + tok * w.rowb + w.hoff;
 }
 
 // Regroup 8 value rows (lane holds DL dims of each) into the MFMA B-operand of N-tile j:
@@ -405,6 +412,18 @@ __device__ __forceinline__ WaveInfo make_wave(const AttnParams& p, int D, int b,
   w.rowb = (int64_t)p.kv_heads * D * 2;
   w.first_bi = 0;
   w.bt = p.block_table + (int64_t)b * p.max_blocks;
+  w.hoff = (int64_t)kh * D * 2;
+  w.lin_row0 = -1;
+  w.lin_cap = 0;
+  if (p.linear_cap > 0) {
+    w.rowb = (int64_t)D * 2;
+    w.hoff = 0;
+    w.lin_row0 = ((int64_t)b * p.kv_heads + kh) * p.linear_cap;
+    w.lin_cap = p.linear_cap;
+    w.bs = 16;  // rows of 16-key tiles are consecutive
+    w.bs_shift = 4;
+    w.cache_limit = total;
+  }
   return w;
 }
 

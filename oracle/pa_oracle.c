@@ -647,8 +647,8 @@ static void rope_row(float* v, int64_t pos, const void* cos, const void* sin, in
   }
 }
 
-int orc_gqa_batched(const orc_gqa_args* a, double* out) {
-  const int B = a->batch, S = a->seq, H = a->num_heads, KV = a->kv_heads, d = a->head_dim;
+static int gqa_one_sequence(const orc_gqa_args* a, int b, double* out) {
+  const int S = a->seq, H = a->num_heads, KV = a->kv_heads, d = a->head_dim;
   const int dt = a->dtype, g = H / KV;
   const int cdt = a->cache_dtype ? a->cache_dtype : dt;
   const int quant = is_int_dt(cdt), bits = cdt == ORC_I8 ? 8 : 4;
@@ -667,7 +667,7 @@ int orc_gqa_batched(const orc_gqa_args* a, double* out) {
     return 4;
   }
   int rc = 0;
-  for (int b = 0; b < B && !rc; ++b) {
+  do {
     const int length = a->seqlens_k[b] + 1;
     const int qp = length - S > 0 ? length - S : 0;
     const int past = a->kv_seq == 0 ? length : qp;
@@ -783,9 +783,20 @@ int orc_gqa_batched(const orc_gqa_args* a, double* out) {
           for (int e = 0; e < d; ++e) o[e] /= l;
       }
     }
-  }
+  } while (0);
   free(row);
   free(qrow);
   free(sc);
+  return rc;
+}
+
+int orc_gqa_batched(const orc_gqa_args* a, double* out) {
+  int rc = 0;
+  /* sequences are independent (each writes its own present rows and output rows) */
+  #pragma omp parallel for schedule(dynamic, 1) reduction(max : rc)
+  for (int b = 0; b < a->batch; ++b) {
+    int r = gqa_one_sequence(a, b, out);
+    if (r > rc) rc = r;
+  }
   return rc;
 }

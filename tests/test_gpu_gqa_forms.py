@@ -145,3 +145,35 @@ def test_attention_bias_on_a_decode_batch():
     c = gqa_case(F16, 4, 1, 16, 4, 128, [300, 17, 511, 64], cap=512, seed=13,
                  bias_shape=(4, 16, 1, 512))
     check(c, present="shared")
+
+
+# Multi-token GroupQueryAttention on the LDS-shared prefill kernels in contiguous-cache addressing
+# (head 128: prefill_mx_kernel, other heads: prefill_kernel): chunks over a past, growing and
+# shared presents, a window, a sink, capacities that are not multiples of the key step (the
+# last steps read row by row), and a first prompt with every sequence full length.
+@pytest.mark.parametrize("d", [64, 96, 128, 256])
+@pytest.mark.parametrize("variant", ["chunk_new", "chunk_shared", "window_sink", "first_full"])
+def test_multi_token_prefill_kernels(d, variant):
+    rng = np.random.default_rng(d + len(variant))
+    B, S, H, KV = 3, 48, 16, 4
+    if variant == "first_full":
+        c = gqa_case(BF16, B, S, H, KV, d, [S - 1] * B, seed=d, rotary=True, theta=500000.0)
+        check(c)
+        return
+    seqlens = rng.integers(S, 500, size=B)
+    kw = dict(cap=517, rotary=True, theta=500000.0)
+    if variant == "window_sink":
+        kw.update(window=77, sink=True)
+    c = gqa_case(F16 if variant == "window_sink" else BF16, B, S, H, KV, d, seqlens,
+                 seed=d + 1, **kw)
+    check(c, present="shared" if variant == "chunk_shared" else "new")
+
+
+# enough (sequence, kv-head, 128-row block) items for the planned launch (split halves merged)
+def test_multi_token_prefill_planned_launch():
+    rng = np.random.default_rng(77)
+    B, S, H, KV, d = 16, 128, 32, 8, 128
+    seqlens = rng.integers(S, 400, size=B)
+    seqlens[3] = 2999  # one long item that splits
+    c = gqa_case(BF16, B, S, H, KV, d, seqlens, cap=3000, seed=77, rotary=True, theta=500000.0)
+    check(c, present="shared")
