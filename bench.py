@@ -53,6 +53,9 @@ def parse():
                     help="c3 (default): BASELINE.json config 3; c4 / c5: configs 4 / 5")
     ap.add_argument("--head-dim", type=int, default=128, choices=(64, 96, 128, 256),
                     help="c3 / c4: the same batch at another head size (128 = the config)")
+    ap.add_argument("--cache-dtype", default="bf16", choices=("bf16", "int8", "int4"),
+                    help="c3 only: the same decode batch over int8 / int4 pages with per-channel "
+                         "fp32 scales (bf16 = config 3)")
     return ap.parse_args()
 
 
@@ -66,7 +69,7 @@ def load_traffic(name="decode_c3_traffic.json"):
     return t.get("hbm_bytes_per_launch")
 
 
-def build_workload(torch, ep, seed, d=128):
+def build_workload(torch, ep, seed, d=128, cache="bf16"):
     import numpy as np
     rng = np.random.default_rng(seed)
     B, H, KV, bs, nb = 64, 32, 8, 16, 40000
@@ -82,12 +85,22 @@ def build_workload(torch, ep, seed, d=128):
         used += n
     dev = torch.device("cuda", 0)
     g = torch.Generator(device=dev).manual_seed(seed)
-    kc = torch.empty((nb, bs, KV, d), dtype=torch.bfloat16, device=dev)
-    vc = torch.empty_like(kc)
-    for t in (kc, vc):  # fill in slices to bound the fp32 temporary
-        for i in range(0, nb, 5000):
-            t[i:i + 5000] = torch.randn((min(5000, nb - i), bs, KV, d), generator=g,
-                                        device=dev).to(torch.bfloat16)
+    ks = vs = None
+    if cache == "bf16":
+        kc = torch.empty((nb, bs, KV, d), dtype=torch.bfloat16, device=dev)
+        vc = torch.empty_like(kc)
+        for t in (kc, vc):  # fill in slices to bound the fp32 temporary
+            for i in range(0, nb, 5000):
+                t[i:i + 5000] = torch.randn((min(5000, nb - i), bs, KV, d), generator=g,
+                                            device=dev).to(torch.bfloat16)
+    else:
+        # integer codes uniform over the code range, per-channel scales [KV, d] of N(0,1) / 64
+        width, dt = (d, torch.int8) if cache == "int8" else ((d + 1) // 2, torch.uint8)
+        lo, hi = (-128, 128) if cache == "int8" else (0, 256)
+        kc = torch.randint(lo, hi, (nb, bs, KV, width), generator=g, device=dev, dtype=dt)
+        vc = torch.randint(lo, hi, (nb, bs, KV, width), generator=g, device=dev, dtype=dt)
+        ks = (torch.rand((KV, d), generator=g, device=dev) + 0.5) / 64.0
+        vs = (torch.rand((KV, d), generator=g, device=dev) + 0.5) / 64.0
     half = d // 2
     inv = 1.0 / (500000.0 ** (torch.arange(half, dtype=torch.float64) / half))
     ang = torch.arange(8192 + 8, dtype=torch.float64)[:, None] * inv[None, :]
@@ -97,7 +110,8 @@ def build_workload(torch, ep, seed, d=128):
     k = torch.randn((B, KV * d), generator=g, device=dev).to(torch.bfloat16)
     v = torch.randn((B, KV * d), generator=g, device=dev).to(torch.bfloat16)
     w = dict(B=B, T=B, mq=1, H=H, KV=KV, d=d, bs=bs, nb=nb, ctx=ctx, bt_np=bt, kc=kc, vc=vc,
-             cos=cos, sin=sin, q=q, k=k, v=v, ks=None, vs=None)
+             cos=cos, sin=sin, q=q, k=k, v=v, ks=ks, vs=vs, cache=cache,
+             quant="NONE" if cache == "bf16" else "PER_CHANNEL")
     w["cum"] = torch.arange(B + 1, dtype=torch.int32, device=dev)
     w["past"] = torch.from_numpy(ctx - 1).to(dev)
     w["bt"] = torch.from_numpy(bt).to(dev)
@@ -194,7 +208,9 @@ class Step:
         self.node = capi.PaNode(w["H"], w["KV"], 0.0, 0.0, -1, int(rotary), 0, 0, 1, 1e-6)
         self.io = capi.PaIO(
             self.act, w["T"], w["H"] * w["d"], w["q"].data_ptr(), w["k"].data_ptr(),
-            w["v"].data_ptr(), cache_desc(w["kc"], w["vc"], w["ks"], w["vs"]),
+            w["v"].data_ptr(), cache_desc(w["kc"], w["vc"], w["ks"], w["vs"], head_dim=w["d"],
+                                          k_quant_type=w.get("quant", "NONE"),
+                                          v_quant_type=w.get("quant", "NONE")),
             w["cum"].data_ptr(), w["past"].data_ptr(), w["bt"].data_ptr(), w["B"],
             w["bt"].shape[1], ptr(w["cos"]), ptr(w["sin"]), w["cos"].shape[0] if rotary else 0,
             w["cos"].shape[1] if rotary else 0, None, None, None, None,
@@ -204,7 +220,9 @@ class Step:
                                                                        C.byref(self.io))
         self.op_ws = torch.empty(max(self.op_ws_bytes, 1), dtype=torch.uint8, device="cuda")
         # kernel-level blocks
-        self.cache = cache_desc(w["kc"], w["vc"], w["ks"], w["vs"])
+        self.cache = cache_desc(w["kc"], w["vc"], w["ks"], w["vs"], head_dim=w["d"],
+                                k_quant_type=w.get("quant", "NONE"),
+                                v_quant_type=w.get("quant", "NONE"))
         self.batch = batch_desc(w["cum"], w["past"], w["bt"], w["T"], None, w["mq"],
                                 capi.PA_BATCH_NEW_ROWS_IN_CACHE)
         self.attn = attn_desc(w["H"])
@@ -442,15 +460,16 @@ def main():
     import onnxruntime_ep_mlx_amd as ep
     torch.cuda.set_device(0)
     if args.config == "c3":
-        w = build_workload(torch, ep, args.seed, args.head_dim)
-        step = Step(torch, ep, w, args.chunk, kind=1)
+        w = build_workload(torch, ep, args.seed, args.head_dim, args.cache_dtype)
+        step = Step(torch, ep, w, args.chunk, kind=1 if args.cache_dtype == "bf16" else 0)
     elif args.config == "c4":
         w = build_prefill_workload(torch, d=args.head_dim)
         step = Step(torch, ep, w, args.chunk, kind=0)
     else:
         w = build_fp8_workload(torch)
         step = Step(torch, ep, w, args.chunk, kind=0)
-    kv_elem = 1 if w["ks"] is not None else 2  # fp8 pages: one byte per element
+    # bytes per K or V element: fp8 / int8 pages 1, int4 pages 1/2, bf16 2
+    kv_elem = {"int8": 1, "int4": 0.5}.get(w.get("cache"), 1 if w["ks"] is not None else 2)
     kv_bytes = float(w["ctx"].sum()) * w["KV"] * w["d"] * 2 * kv_elem
 
     if args.calibrate_copy:
@@ -491,7 +510,7 @@ def main():
     attn_gbs = kv_bytes / (attn_ms * 1e-3) / 1e9
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and w.get("cache", "bf16") == "bf16":
         n_seq = {"c3": args.cpu_sample, "c4": 1, "c5": 1}[args.config]
         cpu = cpu_baseline(torch, w, step, n_seq, args.cpu_seconds, args.config)
 
@@ -529,16 +548,21 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
-            "traffic": load_traffic() if w["d"] == 128 else None,
+            "traffic": load_traffic() if (w["d"] == 128 and w["cache"] == "bf16") else None,
             "kernel": "pa_attention (decode_balanced_kernel + balanced_merge_kernel)",
             "us_per_launch": round(attn_ms * 1e3, 1),
         },
         "cpu_baseline": cpu,
     }
-    if w["d"] != 128:  # not config 3 itself: say so in the line
-        line["metric"] += f" (head_dim {w['d']} variant of config 3)"
-        line["config"]["workload"] = (f"config 3 decode batch at head_dim {w['d']}: RoPE + KV "
-                                      "append + split-K paged attention per step")
+    if w["d"] != 128 or w["cache"] != "bf16":  # not config 3 itself: say so in the line
+        what = f"head_dim {w['d']}" + ("" if w["cache"] == "bf16" else f", {w['cache']} pages")
+        line["metric"] += f" ({what} variant of config 3)"
+        line["config"]["workload"] = (f"config 3 decode batch at {what}: RoPE + KV append + "
+                                      "split-K paged attention per step")
+        line["config"]["cache_dtype"] = w["cache"]
+        if w["cache"] != "bf16":
+            line["roofline"]["kernel"] = "pa_attention (attn_generic_kernel + split_reduce_kernel)"
+            line["dtype"] = f"bf16 x {w['cache']}"
     print(json.dumps(line), flush=True)
 
 
