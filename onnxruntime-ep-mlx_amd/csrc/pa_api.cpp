@@ -172,8 +172,10 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
   // numbers the 32-key steps of the whole batch with 32-bit indices: every sequence is clamped
   // to the cache capacity on the device, so batch * (capacity / 32 + 1) bounds the step count.
   const int64_t cap = linear_cap > 0 ? linear_cap : (int64_t)b->max_blocks * c->block_size;
+  // (contiguous caches: pages in the activation dtype only)
   const bool bal_ok = (int64_t)g * mq <= 16 &&
                       pa::balanced_supported(c->head_dim, act, c->dtype, c->block_size) &&
+                      !(linear && c->dtype != act) &&
                       (int64_t)c->num_blocks * c->block_size <= (int64_t)UINT32_MAX &&
                       (int64_t)std::max(b->batch, 0) * (cap / 32 + 2) < (int64_t)INT32_MAX;
   // Contiguous caches: the streaming decode, the LDS-shared prefill kernels, or VALU.

@@ -113,6 +113,135 @@ __device__ __forceinline__ typename TT::vec8 value_operand8(const Step8<D>& r, i
   return __builtin_bit_cast(typename TT::vec8, w);
 }
 
+// Integer pages (kv_cache.rs:222-256: values are code x scale).  The products run in fp16 on the
+// exact codes: 0x64XX is the fp16 value 1024 + XX, so a biased code byte XX becomes its code with
+// one packed subtraction -- int8: XX = code ^ 0x80, minus 1152; int4: XX = nibble = code + 8,
+// minus 1032 (both exact: the results are small integers).  The scales enter outside the
+// products: per-tensor key scales in the score scale, per-channel ones in the query operands,
+// value scales in the epilogue (balanced_merge_kernel for split rows).
+typedef _Float16 f16x2c __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t f16pair_sub(uint32_t w, float bias) {
+  const f16x2c v = __builtin_bit_cast(f16x2c, w) - f16x2c{(_Float16)bias, (_Float16)bias};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// int8 pages: Step8 layout (one byte per code).  Key operand of k-step s: words 2 (s & 1) and
+// 2 (s & 1) + 1 of chunk s / 2, as in key_operand8.
+template <int D>
+__device__ __forceinline__ f16x8 key_operand_i8(const Step8<D>& r, int tile, int s) {
+  const u32x4& w = r.k[tile][s >> 1];
+  const int t = s & 1;
+  const uint32_t a = w[2 * t] ^ 0x80808080u, b = w[2 * t + 1] ^ 0x80808080u;
+  u32x4 o;
+  o[0] = f16pair_sub(__builtin_amdgcn_perm(0x64646464u, a, 0x04010400u), 1152.f);
+  o[1] = f16pair_sub(__builtin_amdgcn_perm(0x64646464u, a, 0x04030402u), 1152.f);
+  o[2] = f16pair_sub(__builtin_amdgcn_perm(0x64646464u, b, 0x04010400u), 1152.f);
+  o[3] = f16pair_sub(__builtin_amdgcn_perm(0x64646464u, b, 0x04030402u), 1152.f);
+  return __builtin_bit_cast(f16x8, o);
+}
+
+// Value operand of N-tile j (8 keys x head dim (D/16) c + j): word m pairs dim j of value rows
+// 2m and 2m + 1 (byte j & 3 of word j >> 2 of each row slice).
+template <int D>
+__device__ __forceinline__ f16x8 value_operand_i8(const Step8<D>& r, int j) {
+  const uint32_t sel = 0x0c000c00u | ((uint32_t)(4 + (j & 3)) << 16) | (uint32_t)(j & 3);
+  u32x4 o;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    uint32_t lo, hi;
+    if constexpr (D == 128) {
+      lo = r.v[2 * m].w[j >> 2];
+      hi = r.v[2 * m + 1].w[j >> 2];
+    } else {
+      lo = r.v[2 * m].w;
+      hi = r.v[2 * m + 1].w;
+    }
+    o[m] = f16pair_sub(__builtin_amdgcn_perm(hi, lo, sel) ^ 0x64806480u, 1152.f);
+  }
+  return __builtin_bit_cast(f16x8, o);
+}
+
+// int4 pages: rows of D/2 bytes, byte i = dims 2i (low nibble) and 2i + 1 (high nibble).  Key
+// chunk h of a lane: dims 64h + 16G .. +15 in 8 bytes; value row e: the lane's D/16 dims in
+// D/32 bytes (D = 64: two bytes in the low half of the word).
+template <int D>
+struct Step4 {
+  u32x2 k[2][D / 64];
+  uint32_t v[8];
+};
+
+template <int D>
+__device__ __forceinline__ f16x8 key_operand_i4(const Step4<D>& r, int tile, int s) {
+  const uint32_t x = r.k[tile][s >> 1][s & 1];
+  const uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
+  u32x4 o;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const uint32_t sel = 0x0c000c00u | ((uint32_t)(4 + m) << 16) | (uint32_t)m;
+    o[m] = f16pair_sub(__builtin_amdgcn_perm(hi, lo, sel) | 0x64006400u, 1032.f);
+  }
+  return __builtin_bit_cast(f16x8, o);
+}
+
+template <int D>
+__device__ __forceinline__ f16x8 value_operand_i4(const Step4<D>& r, int j) {
+  const int sh = 4 * (j & 1), byte = j >> 1;
+  const uint32_t sel = 0x0c000c00u | ((uint32_t)(4 + byte) << 16) | (uint32_t)byte;
+  u32x4 o;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const uint32_t lo = (r.v[2 * m] >> sh) & 0x0F0F0F0Fu, hi = (r.v[2 * m + 1] >> sh) & 0x0F0F0F0Fu;
+    o[m] = f16pair_sub(__builtin_amdgcn_perm(hi, lo, sel) | 0x64006400u, 1032.f);
+  }
+  return __builtin_bit_cast(f16x8, o);
+}
+
+// Integer pages: a piece's query rows as fp16 operands.  Per-channel key scales multiply the
+// query dims they meet (q_d * s_d, fp32); the row is then scaled by 2^(14 - e), e the exponent
+// of its largest |value| (so the row fits fp16 and keeps 11 bits), and the returned factor
+// 2^(e - 14) -- times a per-tensor key scale -- restores the scores.  Lanes c, c + 16, c + 32,
+// c + 48 hold row c; the lane's dims of k-step q are 64 (q / 2) + 16 G + 8 (q % 2) .. + 7.
+template <typename TT, int D>
+__device__ __forceinline__ float int_query(RowState<TF16, D>& rs, const u32x4 (&qr)[D / 32],
+                                           const AttnParams& p, int kh, int G) {
+  const bool pc = p.k_quant == PA_QUANT_PER_CHANNEL;
+  float qf[D / 32][8];
+  float mx = 0.0f;
+#pragma unroll
+  for (int q = 0; q < D / 32; ++q) {
+    float sc[8];
+    if (pc) {
+      const float* sp = p.k_scale + (int64_t)kh * D + 64 * (q >> 1) + 16 * G + 8 * (q & 1);
+      const f32x4 a = *reinterpret_cast<const f32x4*>(sp);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(sp + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sc[i] = a[i];
+        sc[4 + i] = b[i];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t w = qr[q][e >> 1];
+      const float v = TT::to_f32((typename TT::raw)((e & 1) ? (w >> 16) : (w & 0xffffu)));
+      qf[q][e] = pc ? v * sc[e] : v;
+      mx = fmaxf(mx, fabsf(qf[q][e]));
+    }
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const int ex = mx > 0.0f ? max(__builtin_amdgcn_frexp_expf(mx), -100) : 0;
+  const float up = __builtin_ldexpf(1.0f, 14 - ex);
+#pragma unroll
+  for (int q = 0; q < D / 32; ++q) {
+    float t[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = qf[q][e] * up;
+    rs.qv[q] = TF16::cvt8(t);
+  }
+  return __builtin_ldexpf(1.0f, ex - 14) * (pc ? 1.0f : p.k_scale[0]);
+}
+
 // Fast path: all 32 keys cached, 16-key tiles page-aligned.  The page id of each tile comes
 // from lane (tile_block - first_bi) of `btv` (this chunk's block-table entries, one per lane).
 template <int D>
@@ -381,6 +510,15 @@ __device__ __forceinline__ void merge_pieces(const AttnParams& p, int b, int kh,
   const int h = kh * g + r % g;
   const int64_t t = s0 + r / g;
   const float fct = finalize_factor(M, lsum, sink_logit<TT>(p, h));
+  if (p.v_quant == PA_QUANT_PER_TENSOR || p.v_quant == PA_QUANT_PER_CHANNEL) {
+    // integer pages: the partials are in code units; scale each output dim
+    const bool pc = p.v_quant == PA_QUANT_PER_CHANNEL;
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        acc[v][e] *= pc ? p.v_scale[(int64_t)kh * D + quarter * DQ + 4 * v + e] : p.v_scale[0];
+  }
   u32x4* out = reinterpret_cast<u32x4*>(reinterpret_cast<typename TT::raw*>(p.out) +
                                         (t * p.num_heads + h) * D + quarter * DQ);
 #pragma unroll
@@ -554,8 +692,12 @@ __device__ __forceinline__ uint64_t tile_row_bytes(const AttnParams& p, const Cu
   return row0 * rowb;
 }
 
-template <typename TT, int D, bool F8>
-using RingStep = typename std::conditional<F8, Step8<D>, Step<D>>::type;
+// Cache kinds of the streaming decode: pages in the activation dtype, fp8 e4m3, int8, int4.
+enum DecodeCache { kDcT = 0, kDcFp8 = 1, kDcI8 = 2, kDcI4 = 3 };
+
+template <typename TT, int D, int CK>
+using RingStep = typename std::conditional<
+    CK == kDcT, Step<D>, typename std::conditional<CK == kDcI4, Step4<D>, Step8<D>>::type>::type;
 
 // Per-lane constants of the streaming loads.
 struct LaneOffs {
@@ -572,7 +714,7 @@ struct QueryPtrs {
   const char* q;
   const char* sink;
 };
-template <int D, bool F8>
+template <int D, bool F8>  // F8: the query layout of byte-coded pages (fp8, int8, int4)
 __device__ __forceinline__ QueryPtrs query_ptrs(const AttnParams& p, const SeqWin& sw,
                                                 const Cursor& c, int g, int lane) {
   const int cl = lane & 15, G = lane >> 4;
@@ -590,7 +732,7 @@ __device__ __forceinline__ QueryPtrs query_ptrs(const AttnParams& p, const SeqWi
 
 // fp8 pages (every row in the pages, block size a multiple of 16): per tile D/64 16-byte key
 // chunks (dims 64h + 16G ..) and four D/16-byte value rows per lane, plus the page scales.
-template <int D>
+template <int D, bool SCALES = true>
 __device__ __forceinline__ void load_step8(const AttnParams& p, const Cursor& c, int btl, int lane,
                                            int bs_shift, const LaneOffs& lo, Step8<D>& st) {
   const uint32_t hoff = (uint32_t)c.kh * D;
@@ -611,23 +753,53 @@ __device__ __forceinline__ void load_step8(const AttnParams& p, const Cursor& c,
         st.v[4 * tile + e].w = bld4(rv, lo.voff, e * lo.rowb);
     }
   }
-  const float* sp = (lane & 2) ? p.v_scale : p.k_scale;
-  st.sc = sp[((lane & 1) ? blk[1] : blk[0]) * p.kv_heads + c.kh];
+  if constexpr (SCALES) {
+    const float* sp = (lane & 2) ? p.v_scale : p.k_scale;
+    st.sc = sp[((lane & 1) ? blk[1] : blk[0]) * p.kv_heads + c.kh];
+  }
+}
+
+// int4 pages: per tile D/64 8-byte key chunks and four D/32-byte value row slices per lane.
+template <int D>
+__device__ __forceinline__ void load_step4(const AttnParams& p, const Cursor& c, int btl, int lane,
+                                           int bs_shift, const LaneOffs& lo, Step4<D>& st) {
+  const uint32_t hoff = (uint32_t)c.kh * (D / 2);
+  const char* kc = reinterpret_cast<const char*>(p.key_cache);
+  const char* vc = reinterpret_cast<const char*>(p.value_cache);
+#pragma unroll
+  for (int tile = 0; tile < 2; ++tile) {
+    int64_t blk;
+    const uint64_t off = tile_row_bytes(p, c, btl, tile, bs_shift, lo.rowb, blk) + hoff;
+    const __amdgpu_buffer_rsrc_t rk = rows_rsrc(kc + off), rv = rows_rsrc(vc + off);
+#pragma unroll
+    for (int h = 0; h < D / 64; ++h) st.k[tile][h] = bld8(rk, lo.koff + 32 * h, 0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if constexpr (D == 128)
+        st.v[4 * tile + e] = bld4(rv, lo.voff, e * lo.rowb);
+      else
+        st.v[4 * tile + e] =
+            (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rv, lo.voff, e * lo.rowb, 2);
+    }
+  }
 }
 
 // All loads of one step: K and V rows of both 16-key tiles and the query rows of the step's
 // (sequence, kv-head).  Every path issues the same number of loads, so the compiler's vmcnt
 // waits only drain the step about to be computed.  Rows past the sequence end re-read the last
 // row (or stay in the last page).
-template <typename TT, int D, bool F8>
+template <typename TT, int D, int CK>
 __device__ __forceinline__ void load_stream_step(const AttnParams& p, const SeqWin& sw,
                                                  const Cursor& c, int btl, int lane, int bs_shift,
                                                  const LaneOffs& lo, const QueryPtrs& qp,
-                                                 bool qload, RingStep<TT, D, F8>& st,
+                                                 bool qload, RingStep<TT, D, CK>& st,
                                                  u32x4 (&qv)[D / 32], typename TT::raw& sk) {
+  constexpr bool F8 = CK != kDcT;  // byte-coded pages: the fp8 query layout
   const int cl = lane & 15, G = lane >> 4;
-  if constexpr (F8) {
-    load_step8<D>(p, c, btl, lane, bs_shift, lo, st);
+  if constexpr (CK == kDcFp8 || CK == kDcI8) {
+    load_step8<D, CK == kDcFp8>(p, c, btl, lane, bs_shift, lo, st);
+  } else if constexpr (CK == kDcI4) {
+    load_step4<D>(p, c, btl, lane, bs_shift, lo, st);
   } else {
     constexpr int DL = D / 16;
     const uint32_t hoff = (uint32_t)c.kh * D * 2;
@@ -698,18 +870,23 @@ __device__ __forceinline__ void load_stream_step(const AttnParams& p, const SeqW
 // the compute cursor leaves it: final rows when the piece covers its whole sequence, else a
 // partial at slot u + b.  Steps whose keys are visible to every row of the piece skip the
 // per-score position tests.
-template <typename TT, int D, bool CAP, bool F8, int DEPTH>
+template <typename TT, int D, bool CAP, int CK, int DEPTH>
 __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& sw, int lo, int hi,
                                              int L, int x, int u0, int lane) {
-  using vec8 = typename TT::vec8;
+  constexpr bool F8 = CK != kDcT;        // byte-coded pages (fp8 query layout)
+  constexpr bool INT = CK >= kDcI8;      // integer codes: fp16 products
+  using MT = typename std::conditional<INT, TF16, TT>::type;  // the products' type
+  using vec8 = typename MT::vec8;
   const int c = lane & 15, G = lane >> 4;
   const int g = p.num_heads / p.kv_heads;
   const int bs_shift = __builtin_ctz(p.block_size);  // power of two (host dispatch)
   const int K = hi - lo;
+  // bytes per row of one kv-head, and of one key chunk / value slice unit
+  constexpr int RB = CK == kDcT ? 2 * D : CK == kDcI4 ? D / 2 : D;
   LaneOffs lofs;
-  lofs.rowb = (uint32_t)p.kv_heads * D * (F8 ? 1 : 2);
-  lofs.koff = (uint32_t)c * lofs.rowb + 16 * G;
-  lofs.voff = (uint32_t)(4 * G) * lofs.rowb + (uint32_t)(D / 16) * (F8 ? 1 : 2) * c;
+  lofs.rowb = (uint32_t)p.kv_heads * RB;
+  lofs.koff = (uint32_t)c * lofs.rowb + (CK == kDcI4 ? 8 : 16) * G;
+  lofs.voff = (uint32_t)(4 * G) * lofs.rowb + (uint32_t)(RB / 16) * c;
 
   // Block ids run BA steps ahead of the compute in a ring of NBT entries: 2 * (DEPTH - 1) ahead
   // in DEPTH entries, or, with a one-step ring (rows loaded in the step that uses them), one
@@ -721,7 +898,7 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
   Cursor cc = cursor_at(sw, p, lo, L, x, u0);
   Cursor cd = cc, cb = cc;
   QueryPtrs qp = query_ptrs<D, F8>(p, sw, cd, g, lane);
-  RingStep<TT, D, F8> st[DEPTH];
+  RingStep<TT, D, CK> st[DEPTH];
   u32x4 qr[DEPTH][D / 32];
   typename TT::raw skr[DEPTH];
   int btr[NBT];
@@ -734,7 +911,7 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
   bool qload = true;  // the data cursor's step starts a piece
 #pragma unroll
   for (int j = 0; j < DEPTH - 1; ++j) {
-    load_stream_step<TT, D, F8>(p, sw, cd, btr[j % NBT], lane, bs_shift, lofs, qp, qload, st[j],
+    load_stream_step<TT, D, CK>(p, sw, cd, btr[j % NBT], lane, bs_shift, lofs, qp, qload, st[j],
                                 qr[j], skr[j]);
     qload = cursor_next(cd, sw, p, hi, L, x, u0);
     if (qload) qp = query_ptrs<D, F8>(p, sw, cd, g, lane);
@@ -745,7 +922,8 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
     cursor_next(cb, sw, p, hi, L, x, u0);
   }
 
-  RowState<TT, D> rs;
+  RowState<MT, D> rs;
+  float row_f = 1.0f;  // integer pages: this row's score factor (query normalisation x key scale)
   int pc_bl = -1, pc_u = -1;  // the piece being computed
   int pc_kh = 0, pc_total = 0;
   int full_lo = 0, full_hi = 0;  // steps [t, t + 32) inside [full_lo, full_hi) need no masks
@@ -755,9 +933,17 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
     const int P = lane_of(sw.P, pc_bl), n = lane_of(sw.q.n, pc_bl);
     const bool final = P >= pc_u * L && P + n <= (pc_u + 1) * L;
     const int64_t slot = (int64_t)pc_u + b;
-    store_rows<TT, D>(rs, p, pc_kh, lane_of(sw.q.s0, pc_bl), 0, g * lane_of(sw.q.nq, pc_bl), g, c,
-                      G, pc_sink, final,
-                      [&](int64_t, int, int rloc) { return (slot * p.kv_heads + pc_kh) * 16 + rloc; });
+    float vsc[D / 16];  // integer pages: value scales of the lane's output dims
+    if constexpr (INT) {
+#pragma unroll
+      for (int j = 0; j < D / 16; ++j)
+        vsc[j] = p.v_quant == PA_QUANT_PER_CHANNEL ? p.v_scale[(int64_t)pc_kh * D + (D / 16) * c + j]
+                                                   : p.v_scale[0];
+    }
+    store_rows<MT, D, TT>(rs, p, pc_kh, lane_of(sw.q.s0, pc_bl), 0, g * lane_of(sw.q.nq, pc_bl), g,
+                          c, G, pc_sink, final,
+                          [&](int64_t, int, int rloc) { return (slot * p.kv_heads + pc_kh) * 16 + rloc; },
+                          false, INT ? vsc : nullptr);
   };
 
   for (int k = 0; k < K; k += U) {
@@ -768,7 +954,7 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
       const int sd_slot = (i + DEPTH - 1) % DEPTH;
       const int bt_use = (i + DEPTH - 1) % NBT, bt_load = (i + BA) % NBT;
       const int cs = i % DEPTH;  // ring slot of the step computed now
-      load_stream_step<TT, D, F8>(p, sw, cd, btr[bt_use], lane, bs_shift, lofs, qp, qload,
+      load_stream_step<TT, D, CK>(p, sw, cd, btr[bt_use], lane, bs_shift, lofs, qp, qload,
                                   st[sd_slot], qr[sd_slot], skr[sd_slot]);
       qload = cursor_next(cd, sw, p, hi, L, x, u0);
       if (qload) qp = query_ptrs<D, F8>(p, sw, cd, g, lane);
@@ -792,8 +978,11 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
           // its window and, when causal, the keys up to itself.
           full_lo = p.window > 0 ? pastb + nq - p.window : 0;
           full_hi = p.causal ? pastb + 1 : pc_total;
+          if constexpr (INT)
+            row_f = int_query<TT, D>(rs, qr[cs], p, pc_kh, G);
+          else
 #pragma unroll
-          for (int q = 0; q < D / 32; ++q) rs.qv[q] = __builtin_bit_cast(vec8, qr[cs][q]);
+            for (int q = 0; q < D / 32; ++q) rs.qv[q] = __builtin_bit_cast(vec8, qr[cs][q]);
 #pragma unroll
           for (int j = 0; j < D / 16; ++j) rs.o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
           rs.m_run = kNegInf;
@@ -801,7 +990,8 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
         }
         const int t0 = cc.t;
         const bool masked = !(t0 >= full_lo && t0 + 32 <= full_hi);
-        auto run = [&](Step<D>& cur, float ksA, float ksB, float vsA, float vsB) {
+        // (generic: instantiated only for pages in the activation dtype, where it is called)
+        auto run = [&](auto& cur, float ksA, float ksB, float vsA, float vsB) {
           if (t0 + 32 > pc_total) {
             // Value rows past the sequence end (re-read rows) take no part, even if not finite.
 #pragma unroll
@@ -810,10 +1000,24 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
               if (pos >= pc_total) cur.v[e] = VRow<D>{};
             }
           }
-          compute_step<TT, D, CAP, F8>(rs, cur, t0, pc_total, G, p.scale_log2, p.scale,
-                                       p.softcap, ksA, ksB, vsA, vsB, masked);
+          compute_step<TT, D, CAP, false>(rs, cur, t0, pc_total, G, p.scale_log2, p.scale,
+                                          p.softcap, ksA, ksB, vsA, vsB, masked);
         };
-        if constexpr (F8) {
+        if constexpr (INT) {
+          // Codes are finite: rows past the end weigh in with probability 0 as they are.
+          auto& cur = st[cs];
+          attend_step_ops<MT, D, CAP, true, true, false>(
+              rs,
+              [&](int tile, int s) {
+                if constexpr (CK == kDcI8) return key_operand_i8<D>(cur, tile, s);
+                else return key_operand_i4<D>(cur, tile, s);
+              },
+              [&](int j) {
+                if constexpr (CK == kDcI8) return value_operand_i8<D>(cur, j);
+                else return value_operand_i4<D>(cur, j);
+              },
+              t0, pc_total, G, p.scale_log2, p.scale, p.softcap, row_f, row_f, 1.f, 1.f, masked);
+        } else if constexpr (F8) {
           // Page scales of tiles A and B (lanes 0..3); a tile wholly past the end weighs zero
           // (its page id, and so its scale, is not a real one).
           Step8<D>& cur = st[cs];
@@ -867,7 +1071,7 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
 #ifndef PA_DECODE_DEPTH8
 #define PA_DECODE_DEPTH8 3
 #endif
-template <typename TT, int D, bool CAP, bool F8>
+template <typename TT, int D, bool CAP, int CK>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 decode_balanced_kernel(const AttnParams p) {
   // Workgroup = W wavefronts (one per SIMD of a CU) for W consecutive kv-heads of one segment:
@@ -911,7 +1115,7 @@ decode_balanced_kernel(const AttnParams p) {
     const int chunk_total = __builtin_amdgcn_readlane(incl, 63);
     const int lo = max(gs, carry), hi = min(ge, carry + chunk_total);
     if (lo < hi)
-      stream_range<TT, D, CAP, F8, F8 ? PA_DECODE_DEPTH8 : (D > 128 ? 1 : PA_DECODE_DEPTH)>(p, sw, lo, hi, L, x,
+      stream_range<TT, D, CAP, CK, CK != kDcT ? PA_DECODE_DEPTH8 : (D > 128 ? 1 : PA_DECODE_DEPTH)>(p, sw, lo, hi, L, x,
                                                                            u0, lane);
     carry += chunk_total;
   }
@@ -950,25 +1154,33 @@ balanced_merge_kernel(const AttnParams p) {
   merge_pieces<TT, D>(p, b, kh, s0, g * nq, g, f, nparts, lane);
 }
 
+template <typename TT, int D, bool CAP>
+void launch_balanced_ck(const AttnParams& p, dim3 grid, dim3 block, int ck, hipStream_t s) {
+  switch (ck) {
+    case kDcFp8: hipLaunchKernelGGL((decode_balanced_kernel<TT, D, CAP, kDcFp8>), grid, block, 0, s, p); break;
+    case kDcI8: hipLaunchKernelGGL((decode_balanced_kernel<TT, D, CAP, kDcI8>), grid, block, 0, s, p); break;
+    case kDcI4: hipLaunchKernelGGL((decode_balanced_kernel<TT, D, CAP, kDcI4>), grid, block, 0, s, p); break;
+    default: hipLaunchKernelGGL((decode_balanced_kernel<TT, D, CAP, kDcT>), grid, block, 0, s, p); break;
+  }
+}
+
+// ck: DecodeCache kind of the pages (the streaming decode); the chunked kernel takes kDcT only.
 template <typename TT, int D>
-hipError_t launch_d(const AttnParams& p, dim3 grid, dim3 block, bool balanced, bool f8,
+hipError_t launch_d(const AttnParams& p, dim3 grid, dim3 block, bool balanced, int ck,
                     hipStream_t s) {
   if constexpr (D != 64 && D != 128) {
     // Heads 96 / 256: the streaming decode on pages in the activation dtype only.
-    if (!balanced || f8) return hipErrorInvalidValue;
+    if (!balanced || ck != kDcT) return hipErrorInvalidValue;
     if (p.softcap > 0.0f)
-      hipLaunchKernelGGL((decode_balanced_kernel<TT, D, true, false>), grid, block, 0, s, p);
+      hipLaunchKernelGGL((decode_balanced_kernel<TT, D, true, kDcT>), grid, block, 0, s, p);
     else
-      hipLaunchKernelGGL((decode_balanced_kernel<TT, D, false, false>), grid, block, 0, s, p);
+      hipLaunchKernelGGL((decode_balanced_kernel<TT, D, false, kDcT>), grid, block, 0, s, p);
     return hipGetLastError();
   } else if (balanced) {
-    if (p.softcap > 0.0f) {
-      if (f8) hipLaunchKernelGGL((decode_balanced_kernel<TT, D, true, true>), grid, block, 0, s, p);
-      else hipLaunchKernelGGL((decode_balanced_kernel<TT, D, true, false>), grid, block, 0, s, p);
-    } else {
-      if (f8) hipLaunchKernelGGL((decode_balanced_kernel<TT, D, false, true>), grid, block, 0, s, p);
-      else hipLaunchKernelGGL((decode_balanced_kernel<TT, D, false, false>), grid, block, 0, s, p);
-    }
+    if (p.softcap > 0.0f)
+      launch_balanced_ck<TT, D, true>(p, grid, block, ck, s);
+    else
+      launch_balanced_ck<TT, D, false>(p, grid, block, ck, s);
   } else if (p.ng > 1) {
     // NG row groups per wavefront: 4 at d=64, 2 at d=128 (what fits the register file).
     constexpr int NG = D == 64 ? 4 : 2;
@@ -986,13 +1198,13 @@ hipError_t launch_d(const AttnParams& p, dim3 grid, dim3 block, bool balanced, b
 }
 
 template <typename TT>
-hipError_t launch_t(const AttnParams& p, dim3 grid, dim3 block, bool balanced, bool f8,
+hipError_t launch_t(const AttnParams& p, dim3 grid, dim3 block, bool balanced, int ck,
                     hipStream_t s) {
   switch (p.head_dim) {
-    case 64: return launch_d<TT, 64>(p, grid, block, balanced, f8, s);
-    case 96: return launch_d<TT, 96>(p, grid, block, balanced, f8, s);
-    case 128: return launch_d<TT, 128>(p, grid, block, balanced, f8, s);
-    case 256: return launch_d<TT, 256>(p, grid, block, balanced, f8, s);
+    case 64: return launch_d<TT, 64>(p, grid, block, balanced, ck, s);
+    case 96: return launch_d<TT, 96>(p, grid, block, balanced, ck, s);
+    case 128: return launch_d<TT, 128>(p, grid, block, balanced, ck, s);
+    case 256: return launch_d<TT, 256>(p, grid, block, balanced, ck, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -1004,8 +1216,10 @@ bool balanced_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype, int bl
   if (head_dim != 64 && head_dim != 96 && head_dim != 128 && head_dim != 256) return false;
   if (block_size <= 0 || (block_size & (block_size - 1)) != 0) return false;
   if (cache_dtype == act) return true;
-  return cache_dtype == PA_DTYPE_FP8_E4M3 && block_size >= 16 &&
-         (head_dim == 64 || head_dim == 128);
+  // byte-coded pages (fp8, int8, int4): 16-key tiles inside one page, heads 64 / 128
+  return (cache_dtype == PA_DTYPE_FP8_E4M3 || cache_dtype == PA_DTYPE_INT8 ||
+          cache_dtype == PA_DTYPE_INT4) &&
+         block_size >= 16 && (head_dim == 64 || head_dim == 128);
 }
 
 bool decode_mfma_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype) {
@@ -1027,8 +1241,8 @@ hipError_t launch_decode_mfma(const AttnParams& p, pa_dtype act, pa_dtype cache_
   const int row_groups = (int)std::min<int64_t>(((int64_t)g * mq + rows_per_wave - 1) / rows_per_wave,
                                                 (int64_t)(INT32_MAX / p.kv_heads));
   dim3 grid(p.kv_heads * row_groups, p.max_splits, p.batch);
-  if (act == PA_DTYPE_FLOAT16) return launch_t<TF16>(p, grid, dim3(64), false, false, s);
-  return launch_t<TBF16>(p, grid, dim3(64), false, false, s);
+  if (act == PA_DTYPE_FLOAT16) return launch_t<TF16>(p, grid, dim3(64), false, kDcT, s);
+  return launch_t<TBF16>(p, grid, dim3(64), false, kDcT, s);
 }
 
 // The partial merge of the balanced decode, for the head size of the decode launch.
@@ -1050,17 +1264,24 @@ hipError_t launch_merge(const AttnParams& p, hipStream_t s) {
 hipError_t launch_decode_balanced(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
                                   hipStream_t s) {
   if (!balanced_supported(p.head_dim, act, cache_dtype, p.block_size)) return hipErrorInvalidValue;
-  const bool f8 = cache_dtype == PA_DTYPE_FP8_E4M3;
-  if (f8 != (p.read_all_from_cache != 0)) return hipErrorInvalidValue;
-  if (f8 && (p.k_scale == nullptr || p.v_scale == nullptr || p.linear_cap > 0))
+  const int ck = cache_dtype == PA_DTYPE_FP8_E4M3 ? kDcFp8
+                 : cache_dtype == PA_DTYPE_INT8   ? kDcI8
+                 : cache_dtype == PA_DTYPE_INT4   ? kDcI4
+                                                  : kDcT;
+  const bool coded = ck != kDcT;
+  if (coded != (p.read_all_from_cache != 0)) return hipErrorInvalidValue;
+  if (coded && (p.k_scale == nullptr || p.v_scale == nullptr || p.linear_cap > 0))
+    return hipErrorInvalidValue;
+  if (ck >= kDcI8 && ((p.k_quant != PA_QUANT_PER_TENSOR && p.k_quant != PA_QUANT_PER_CHANNEL) ||
+                      (p.v_quant != PA_QUANT_PER_TENSOR && p.v_quant != PA_QUANT_PER_CHANNEL)))
     return hipErrorInvalidValue;
   if (p.batch <= 0) return hipSuccess;
   if (p.part_o == nullptr || p.mix < 1 || p.mix > p.kv_heads || p.max_splits % p.mix != 0)
     return hipErrorInvalidValue;
   const int W = p.kv_heads % 4 == 0 ? 4 : p.kv_heads % 2 == 0 ? 2 : 1;
   dim3 grid((p.kv_heads / W) * (p.max_splits / p.mix)), block(64 * W);
-  hipError_t e = (act == PA_DTYPE_FLOAT16) ? launch_t<TF16>(p, grid, block, true, f8, s)
-                                           : launch_t<TBF16>(p, grid, block, true, f8, s);
+  hipError_t e = (act == PA_DTYPE_FLOAT16) ? launch_t<TF16>(p, grid, block, true, ck, s)
+                                           : launch_t<TBF16>(p, grid, block, true, ck, s);
   if (e != hipSuccess) return e;
   return act == PA_DTYPE_FLOAT16 ? launch_merge<TF16>(p, s) : launch_merge<TBF16>(p, s);
 }

@@ -287,8 +287,10 @@ __device__ __forceinline__ void step_probs(RowState<TT, D>& rs, const float (&x)
   TT::split8(pv, phi, plo8);
 }
 
-template <typename TT, int D, bool CAP, bool SC, bool MASK = true, typename KeyOp,
-          typename ValueOp>
+// SPLIT = false: P enters the P.V product once, rounded to T (fp16 keeps 11 bits; used for
+// integer pages, whose value operands are exact small integers).
+template <typename TT, int D, bool CAP, bool SC, bool MASK = true, bool SPLIT = true,
+          typename KeyOp, typename ValueOp>
 __device__ __forceinline__ void attend_step_ops(RowState<TT, D>& rs, KeyOp kop, ValueOp vop,
                                                 int t0, int end, int G, float scale_log2,
                                                 float scale, float cap, float ksA, float ksB,
@@ -299,13 +301,27 @@ __device__ __forceinline__ void attend_step_ops(RowState<TT, D>& rs, KeyOp kop, 
   const float lmax = step_scores<TT, D, CAP, SC, MASK>(rs, kop, t0, end, G, scale_log2, scale,
                                                        cap, ksA, ksB, x, masked);
   if (__any(needs_rescale(rs, lmax))) rescale_rows(rs, lmax, G);
-  vec8 phi, plo8;
-  step_probs<TT, D, false, SC>(rs, x, scale_log2, vsA, vsB, phi, plo8);
+  if constexpr (SPLIT) {
+    vec8 phi, plo8;
+    step_probs<TT, D, false, SC>(rs, x, scale_log2, vsA, vsB, phi, plo8);
 #pragma unroll
-  for (int j = 0; j < DL; ++j) {
-    const vec8 vb = vop(j);
-    rs.o[j] = TT::mfma(phi, vb, rs.o[j]);
-    rs.o[j] = TT::mfma(plo8, vb, rs.o[j]);
+    for (int j = 0; j < DL; ++j) {
+      const vec8 vb = vop(j);
+      rs.o[j] = TT::mfma(phi, vb, rs.o[j]);
+      rs.o[j] = TT::mfma(plo8, vb, rs.o[j]);
+    }
+  } else {
+    const float msafe = (rs.m_run == kNegInf) ? 0.0f : rs.m_run;
+    float pv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      pv[e] = __builtin_amdgcn_exp2f(x[e] - msafe);
+      rs.l_part += pv[e];
+      if constexpr (SC) pv[e] *= (e < 4) ? vsA : vsB;
+    }
+    const vec8 pp = TT::cvt8(pv);
+#pragma unroll
+    for (int j = 0; j < DL; ++j) rs.o[j] = TT::mfma(pp, vop(j), rs.o[j]);
   }
 }
 
@@ -462,11 +478,13 @@ __device__ __forceinline__ void init_rows(RowState<TT, D>& rs, const AttnParams&
 // with any visible key) with e folded into the row's (m, l) as (m + e, l * 2^-e).  A log-sum-exp
 // merge over (m, l, O) gives the same result for either form: the factors 2^e cancel between
 // the weighted O and the denominator, the sink term included.
-template <typename TT, int D, typename PartIndex>
+// TO: the output type (the products' type TT unless they run in another one); vsc: per-dim
+// factors of the lane's DL output dims in final rows (integer pages' value scales), or null.
+template <typename TT, int D, typename TO = TT, typename PartIndex>
 __device__ __forceinline__ void store_rows(const RowState<TT, D>& rs, const AttnParams& p, int kh,
                                            int s0, int row0, int R, int g, int c, int G,
                                            float sink_c, bool final, PartIndex part_index,
-                                           bool half_part = false) {
+                                           bool half_part = false, const float* vsc = nullptr) {
   constexpr int DL = D / 16;
   float l_row = rs.l_part + __shfl_xor(rs.l_part, 16, 64);
   l_row += __shfl_xor(l_row, 32, 64);
@@ -494,11 +512,11 @@ __device__ __forceinline__ void store_rows(const RowState<TT, D>& rs, const Attn
     const int64_t t = s0 + oqi;
     if (final) {
       const float f = finalize_factor(mi, li, si);
-      typename TT::raw vals[DL];
+      typename TO::raw vals[DL];
 #pragma unroll
-      for (int j = 0; j < DL; ++j) vals[j] = TT::from_f32(rs.o[j][i] * f);
-      typename TT::raw* dst =
-          reinterpret_cast<typename TT::raw*>(p.out) + (t * p.num_heads + oh) * D + DL * c;
+      for (int j = 0; j < DL; ++j) vals[j] = TO::from_f32(rs.o[j][i] * f * (vsc ? vsc[j] : 1.0f));
+      typename TO::raw* dst =
+          reinterpret_cast<typename TO::raw*>(p.out) + (t * p.num_heads + oh) * D + DL * c;
       if constexpr (DL == 8) {
         u32x4 pk;
 #pragma unroll

@@ -156,7 +156,7 @@ def test_paged_integer_bfloat16(bits):
     check_op(reference_case(bits, 16, dtype=BF16))
 
 
-# a decode batch at the Llama-3-8B head geometry on integer pages (VALU kernel), both widths
+# a decode batch at the Llama-3-8B head geometry on integer pages (streaming matrix-core decode)
 @pytest.mark.parametrize("bits", [8, 4])
 def test_paged_integer_decode_batch(bits):
     rng = np.random.default_rng(bits)
