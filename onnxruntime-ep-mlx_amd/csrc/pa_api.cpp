@@ -138,7 +138,19 @@ struct Plan {
   // Planned prefill: items (sequence, row block, kv-head), row blocks per sequence.
   int64_t plan_items = 0;
   int plan_rbs = 0;
+  // Planned head-128 prefill with value images: 64-key steps and maxima chunks per
+  // (sequence, kv-head) of the image region (0: no images).
+  int img_steps = 0, img_chunks = 0;
 };
+
+// Value images of the planned head-128 prefill: taken when every 64-key step of values is read
+// by at least kImgMinRowBlocks row blocks (the images are written once and read by each), within
+// kImgMaxBytes of workspace.  PA_PREFILL_IMAGES=0 at build time keeps the in-loop conversion.
+#ifndef PA_PREFILL_IMAGES
+#define PA_PREFILL_IMAGES 1
+#endif
+constexpr int64_t kImgMinRowBlocks = 4;
+constexpr int64_t kImgMaxBytes = (int64_t)1 << 31;
 
 int max_ctx_bound(const pa_cache* c, const pa_batch* b) {
   int64_t v = (int64_t)b->max_blocks * c->block_size;
@@ -224,6 +236,14 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
       pl.plan_items = units;
       pl.plan_rbs = (int)rbs;
       pl.part_rows = (size_t)units * 2 * pa::kPrefillRows;
+      if (PA_PREFILL_IMAGES && c->head_dim == 128 && rbs >= kImgMinRowBlocks) {
+        const int64_t steps = ((int64_t)ctx + 63) / 64;
+        if ((int64_t)b->batch * c->kv_heads * steps * pa::kImgStepBytes <= kImgMaxBytes &&
+            steps <= 65535 && b->batch <= 65535) {
+          pl.img_steps = (int)steps;
+          pl.img_chunks = (int)(((int64_t)ctx + pa::kImgChunkKeys - 1) / pa::kImgChunkKeys);
+        }
+      }
       return pl;
     } else if (units >= target) {
       chunk = (int)std::min<int64_t>(((int64_t)ctx + 31) / 32 * 32, INT32_MAX / 2);
@@ -271,12 +291,21 @@ size_t part_o_bytes(const pa_cache* c, const Plan& pl) {
 
 // Workspace: [partial O | partial (m, l)].
 // Planned prefill adds [unit list (2 per item, 4 int32 each) | unit count | split flag per item].
-size_t workspace_for(const pa_cache* c, const pa_batch*, const pa_attn*, const Plan& pl) {
+// Value images add [images | scales | maxima slots].
+size_t plan_bytes(const Plan& pl) {
+  return align256((size_t)pl.plan_items * 2 * 4 * sizeof(int32_t)) + 256 +
+         align256((size_t)pl.plan_items * sizeof(int32_t));
+}
+size_t image_bytes(const pa_cache* c, const pa_batch* b, const Plan& pl) {
+  if (pl.img_steps == 0) return 0;
+  const size_t hb = (size_t)b->batch * c->kv_heads;
+  return align256(hb * pl.img_steps * pa::kImgStepBytes) + align256(hb * 4 * sizeof(int32_t)) +
+         align256(hb * pl.img_chunks * 4 * sizeof(int32_t));
+}
+size_t workspace_for(const pa_cache* c, const pa_batch* b, const pa_attn*, const Plan& pl) {
   if (pl.part_rows == 0) return 0;
   size_t n = part_o_bytes(c, pl) + align256(pl.part_rows * 2 * sizeof(float));
-  if (pl.plan_items > 0)
-    n += align256((size_t)pl.plan_items * 2 * 4 * sizeof(int32_t)) + 256 +
-         align256((size_t)pl.plan_items * sizeof(int32_t));
+  if (pl.plan_items > 0) n += plan_bytes(pl) + image_bytes(c, b, pl);
   return n;
 }
 
@@ -368,6 +397,17 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
     p.plan_rbs = pl.plan_rbs;
     p.plan_slots = 2 * device_cus();
     p.plan_step = pa::prefill_key_step(c->head_dim);
+    if (pl.img_steps > 0) {
+      const size_t hb = (size_t)b->batch * c->kv_heads;
+      char* img = base + plan_bytes(pl) - align256((size_t)pl.plan_items * 2 * 4 * sizeof(int32_t));
+      p.vimg = img;
+      img += align256(hb * pl.img_steps * pa::kImgStepBytes);
+      p.vscale = reinterpret_cast<int32_t*>(img);
+      img += align256(hb * 4 * sizeof(int32_t));
+      p.vmax = reinterpret_cast<int32_t*>(img);
+      p.img_steps = pl.img_steps;
+      p.img_chunks = pl.img_chunks;
+    }
   }
   p.num_blocks = c->num_blocks;
   p.block_size = c->block_size;

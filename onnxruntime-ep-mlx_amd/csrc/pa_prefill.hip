@@ -572,7 +572,62 @@ __device__ __forceinline__ void mx_store(MxBuf& buf, MxStage& st, int wave, int 
   buf.vs[wave] = s_run;  // every lane writes the same word: no branch
 }
 
-template <typename TT, bool CAP>
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Wait for every outstanding vector-memory operation of this wavefront (the step's direct LDS
+// loads) -- vmcnt(0), expcnt and lgkmcnt left at their maxima.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Image staging: this wavefront's quarter of the step at t0 goes straight from memory to LDS
+// buffer `buf` (direct LDS loads, 16 bytes per lane, lane l at byte 16 l of a 1 KiB item), with
+// no register round trip:
+//   key items (kb = wave / 2, ks = 4 (wave % 2) + i): lane l reads key 32 kb + l % 32, bytes
+//   32 ks + 16 (l / 32) of its row slice -- the score A-operand image;
+//   value items (t = wave, nt): 1 KiB each, contiguous in the step's value image.
+// Keys come from the pages (16-key groups share a page) under the same conditions as mx_load;
+// other steps address every key row on its own.
+template <typename TT>
+__device__ __forceinline__ void img_issue(const WaveInfo& w, PageWindow& pw, MxBuf& buf, int wave,
+                                          int lane, int t0, const char* vimg_hb) {
+  constexpr int D = 128;
+  const int kb = wave >> 1;
+  const bool paged = w.bs % 16 == 0 && (t0 + kMxKeys <= w.cache_limit || w.cache_limit >= w.total) &&
+                     (w.lin_row0 < 0 || t0 + kMxKeys <= w.lin_cap);
+  const char* kp;
+  if (paged) {
+    int64_t grp[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int t = t0 + 32 * kb + 16 * q;
+      if (w.lin_row0 >= 0) {
+        grp[q] = w.lin_row0 + t;
+        continue;
+      }
+      const int bi = min(div_bs(t, w), w.max_blocks - 1);
+      if (bi < pw.first || bi >= pw.first + 64) window_at(pw, w, bi, lane);
+      int64_t blk = __builtin_amdgcn_readlane(pw.ids, bi - pw.first);
+      blk = min(max(blk, (int64_t)0), w.num_blocks - 1);
+      grp[q] = blk * w.bs + mod_bs(t, w);
+    }
+    const int64_t row = ((lane & 16) ? grp[1] : grp[0]) + (lane & 15);
+    kp = w.kc + row * w.rowb + w.hoff + 16 * (lane >> 5);
+  } else {
+    kp = row_ptr(w, t0 + 32 * kb + (lane & 31), false, D) + 16 * (lane >> 5);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ks = 4 * (wave & 1) + i;
+    __builtin_amdgcn_global_load_lds(kp + 32 * ks, (lds_ptr_t)&buf.k[kb][ks][0], 16, 0, 0);
+  }
+  const char* vp = vimg_hb + (int64_t)(t0 / kMxKeys) * kImgStepBytes + 4096 * wave + 16 * lane;
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt)
+    __builtin_amdgcn_global_load_lds(vp + 1024 * nt, (lds_ptr_t)&buf.v[wave][nt][0], 16, 0, 0);
+}
+
+// IMG: value operands from the per-(sequence, kv-head) value images (AttnParams::vimg), staged
+// by direct LDS loads one step ahead; otherwise loaded, converted and regrouped in the loop.
+template <typename TT, bool CAP, bool IMG>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 prefill_mx_kernel(const AttnParams p) {
   constexpr int D = 128, ROWS = kPrefillRows;
@@ -673,7 +728,19 @@ prefill_mx_kernel(const AttnParams p) {
   PageWindow pw;
   window_at(pw, w, min(div_bs(t_first, w), w.max_blocks - 1), lane);
   MxStage st;
-  if (nsteps > 0) {
+  const char* vimg_hb = nullptr;
+  if constexpr (IMG) {
+    // the image scales of this (sequence, kv-head): fixed for the whole key range
+    const int64_t hb = (int64_t)b * p.kv_heads + kh;
+    vimg_hb = p.vimg + hb * p.img_steps * (int64_t)kImgStepBytes;
+    const int4 s4 = *reinterpret_cast<const int4*>(p.vscale + hb * 4);
+    sv[0] = __builtin_amdgcn_readfirstlane(s4.x);
+    sv[1] = __builtin_amdgcn_readfirstlane(s4.y);
+    sv[2] = __builtin_amdgcn_readfirstlane(s4.z);
+    sv[3] = __builtin_amdgcn_readfirstlane(s4.w);
+    if (nsteps > 0) img_issue<TT>(w, pw, lds[0], wave, lane, t_first, vimg_hb);
+    wait_vmem();
+  } else if (nsteps > 0) {
     mx_load<TT>(w, pw, wave, lane, t_first, st);
     mx_store<TT>(lds[0], st, wave, lane, t_first, total, s_stage);
     if (nsteps > 1) mx_load<TT>(w, pw, wave, lane, t_first + kMxKeys, st);
@@ -682,6 +749,10 @@ prefill_mx_kernel(const AttnParams p) {
   for (int k = 0; k < nsteps; ++k) {
     const int t0 = t_first + kMxKeys * k;
     MxBuf& cur = lds[k & 1];
+    // image staging: step k + 1 into the other buffer (every wavefront finished reading it
+    // before the barrier that ended iteration k - 1)
+    if constexpr (IMG)
+      if (k + 1 < nsteps) img_issue<TT>(w, pw, lds[(k + 1) & 1], wave, lane, t0 + kMxKeys, vimg_hb);
     if (t0 < any_hi && t0 + kMxKeys > any_lo) {
       // scores: two 32-key blocks, their accumulation chains interleaved
       f32x16 sc[2];
@@ -729,7 +800,7 @@ prefill_mx_kernel(const AttnParams p) {
         for (int nt = 0; nt < 4; ++nt) o[nt] *= alpha;
       }
       // value scales of this step: the output quarters follow a raised s exactly
-      {
+      if constexpr (!IMG) {
         const int4 vs4 = *reinterpret_cast<const int4*>(cur.vs);
         const int vsn[4] = {__builtin_amdgcn_readfirstlane(vs4.x),
                             __builtin_amdgcn_readfirstlane(vs4.y),
@@ -766,10 +837,14 @@ prefill_mx_kernel(const AttnParams p) {
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt)
-          o[nt] = mfma32<TF16>(cur.v[t][nt][mx_vslot(lane)], pb[t], o[nt]);
+          o[nt] = mfma32<TF16>(cur.v[t][nt][IMG ? lane : mx_vslot(lane)], pb[t], o[nt]);
     }
-    if (k + 1 < nsteps) mx_store<TT>(lds[(k + 1) & 1], st, wave, lane, t0 + kMxKeys, total, s_stage);
-    if (k + 2 < nsteps) mx_load<TT>(w, pw, wave, lane, t0 + 2 * kMxKeys, st);
+    if constexpr (IMG) {
+      wait_vmem();
+    } else {
+      if (k + 1 < nsteps) mx_store<TT>(lds[(k + 1) & 1], st, wave, lane, t0 + kMxKeys, total, s_stage);
+      if (k + 2 < nsteps) mx_load<TT>(w, pw, wave, lane, t0 + 2 * kMxKeys, st);
+    }
     __syncthreads();
   }
 
@@ -887,8 +962,143 @@ __device__ __forceinline__ ItemKeys item_keys(const AttnParams& p, int i) {
 // halves at a 32-key boundary.  Units are ordered by a counting sort on their 32-key step count
 // (LDS histogram, descending); the order inside a bucket is whatever the atomics give, which
 // changes nothing in the results (every unit writes its own rows or partial).
+//
+// With bf16 value images, workgroups 1.. of the same launch run the value maxima pass
+// (vmax_chunk), which needs nothing from the plan: it costs no launch of its own and runs on
+// other CUs while workgroup 0 plans.
+template <int NT>
+__device__ __forceinline__ void vmax_chunk(const AttnParams& p, int id) {
+  constexpr int D = 128;
+  static_assert(NT % 64 == 0 && NT >= 64, "whole wavefronts");
+  const int c = id % p.img_chunks;
+  const int kh = (id / p.img_chunks) % p.kv_heads;
+  const int b = id / (p.img_chunks * p.kv_heads);
+  if (b >= p.batch) return;
+  const int s0 = min(max(p.cum[b], 0), p.num_tokens);
+  const int s1 = min(max(p.cum[b + 1], s0), p.num_tokens);
+  const int pastb = clamped_past(p, b, s1 - s0);
+  const int total = pastb + (s1 - s0);
+  const WaveInfo w = make_wave(p, D, b, kh, s0, pastb, total);
+  __shared__ int qmax[4];
+  const int tid = threadIdx.x;
+  if (tid < 4) qmax[tid] = 0;
+  // thread: 16-byte piece tid % 16 of the 256-byte value slice (quarter (tid % 16) / 4) of every
+  // (NT / 16)-th row of the chunk
+  uint32_t mx = 0;
+  for (int r = tid >> 4; r < kImgChunkKeys; r += NT / 16) {
+    const int pos = c * kImgChunkKeys + r;
+    if (pos >= total) break;
+    const u32x4 x = ld16(row_ptr(w, pos, true, D) + 16 * (tid & 15));
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      mx = __builtin_bit_cast(uint32_t,
+                              __builtin_elementwise_max(__builtin_bit_cast(u16x2, mx),
+                                                        __builtin_bit_cast(u16x2, x[m] & 0x7fff7fffu)));
+  }
+  int e = (int)(max(mx & 0xffffu, mx >> 16) >> 7);
+  // lanes that differ in bits 0, 1, 4, 5 hold the same quarter
+  e = max(e, __shfl_xor(e, 1, 64));
+  e = max(e, __shfl_xor(e, 2, 64));
+  e = max(e, __shfl_xor(e, 16, 64));
+  e = max(e, __shfl_xor(e, 32, 64));
+  __syncthreads();
+  if ((tid & 63) < 16 && (tid & 3) == 0) atomicMax(&qmax[(tid & 15) >> 2], e);
+  __syncthreads();
+  if (tid < 4) p.vmax[(((int64_t)b * p.kv_heads + kh) * p.img_chunks + c) * 4 + tid] = qmax[tid];
+}
+
+// Value operand images (AttnParams::vimg): one workgroup per (64-key step, kv-head, sequence).
+// The step's value rows (zero at or past the sequence end) are converted to fp16 under the
+// (sequence, kv-head)'s quarter scales 2^-s -- bf16 values: s from the maxima pass, so the
+// quarter's largest value lies in [2^14, 2^15) of fp16 (exact conversion; values below 2^-29 of
+// it lose bits in the fp16 subnormal range); fp16 values: s = 0 -- staged in LDS and regrouped
+// into the P.V A-operand layout of prefill_mx_kernel: item (t, nt) of the step, lane l holds dim
+// 32 nt + l % 32 of keys 16 t + 4 h + e and then 16 t + 8 + 4 h + e (e < 4, h = l / 32).
+// Workgroup 0 of a (sequence, kv-head) also stores the scales for the prefill kernel.
+template <typename TT>
+__global__ __launch_bounds__(256) void prefill_vimage_kernel(const AttnParams p) {
+  constexpr int D = 128;
+  const int j = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+  const int s0 = min(max(p.cum[b], 0), p.num_tokens);
+  const int s1 = min(max(p.cum[b + 1], s0), p.num_tokens);
+  const int pastb = clamped_past(p, b, s1 - s0);
+  const int total = pastb + (s1 - s0);
+  if (j * kMxKeys >= total || s1 == s0) return;
+  const int64_t hb = (int64_t)b * p.kv_heads + kh;
+  const WaveInfo w = make_wave(p, D, b, kh, s0, pastb, total);
+  __shared__ int qs[4];
+  __shared__ uint32_t rows[kMxKeys][D / 2 + 1];  // fp16 rows, one word = two dims
+  const int tid = threadIdx.x;
+  if (tid < 4) {
+    int s = 0;
+    if constexpr (std::is_same<TT, TBF16>::value) {
+      int emax = 0;
+      for (int c = 0; c < p.img_chunks; ++c)
+        emax = max(emax, p.vmax[(hb * p.img_chunks + c) * 4 + tid]);
+      s = max(emax - 141, -112);
+    }
+    qs[tid] = s;
+    if (j == 0) p.vscale[hb * 4 + tid] = s;
+  }
+  // the row slices: thread -> row tid / 4, quarter tid % 4 (64 bytes)
+  const int r = tid >> 2, q = tid & 3;
+  const int pos = j * kMxKeys + r;
+  u32x4 x[4];
+  if (pos < total) {
+    const char* src = row_ptr(w, pos, true, D) + 64 * q;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = ld16(src + 16 * i);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = u32x4{0u, 0u, 0u, 0u};
+  }
+  __syncthreads();
+  if constexpr (std::is_same<TT, TBF16>::value) {
+    // bf16 exponent E -> fp16 exponent E - 112 - s: subtract (112 + s) << 7 from the magnitude
+    // bits (saturating: values below the fp16 range flush towards zero), shift into place
+    const unsigned short bias = (unsigned short)((112 + qs[q]) << 7);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        u16x2 a = __builtin_bit_cast(u16x2, x[i][m] & 0x7fff7fffu);
+        a = __builtin_elementwise_sub_sat(a, u16x2{bias, bias});
+        a = a << (unsigned short)3;
+        x[i][m] = (x[i][m] & 0x80008000u) | __builtin_bit_cast(uint32_t, a);
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) rows[r][16 * q + 4 * i + m] = x[i][m];
+  __syncthreads();
+  // regroup: task (t, h, nt, dim pair dp) -> slots of lanes 32 h + 2 dp (+1) of item (t, nt)
+  char* dst = p.vimg + (hb * p.img_steps + j) * (int64_t)kImgStepBytes;
+#pragma unroll
+  for (int rep = 0; rep < 2; ++rep) {
+    const int task = tid + 256 * rep;
+    const int dp = task & 15, h = (task >> 4) & 1, nt = (task >> 5) & 3, t = task >> 7;
+    u32x4 lo, hi;
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) {
+      // elements 2 e2, 2 e2 + 1: keys 16 t + 4 h + (e & 3) + 8 (e >> 2)
+      const int ka = 16 * t + 4 * h + ((2 * e2) & 3) + 8 * ((2 * e2) >> 2);
+      const uint32_t wa = rows[ka][16 * nt + dp], wb = rows[ka + 1][16 * nt + dp];
+      lo[e2] = __builtin_amdgcn_perm(wb, wa, 0x05040100u);
+      hi[e2] = __builtin_amdgcn_perm(wb, wa, 0x07060302u);
+    }
+    u32x4* o = reinterpret_cast<u32x4*>(dst + (4 * t + nt) * 1024) + 32 * h + 2 * dp;
+    o[0] = lo;
+    o[1] = hi;
+  }
+}
+
 template <int NT>
 __global__ __launch_bounds__(NT) void prefill_plan_kernel(const AttnParams p) {
+  if (blockIdx.x > 0) {
+    vmax_chunk<NT>(p, (int)blockIdx.x - 1);
+    return;
+  }
   constexpr int NB = 1024;  // buckets of 32-key steps (the last one holds everything longer)
   __shared__ int hist[NB];
   __shared__ unsigned long long total_keys;
@@ -1046,10 +1256,17 @@ template <typename TT, int D>
 hipError_t launch_d(const AttnParams& p, dim3 grid, hipStream_t s) {
   constexpr int NG = kPrefillGroups;
   if constexpr (D == 128) {
-    if (p.softcap > 0.0f)
-      hipLaunchKernelGGL((prefill_mx_kernel<TT, true>), grid, dim3(256), 0, s, p);
-    else
-      hipLaunchKernelGGL((prefill_mx_kernel<TT, false>), grid, dim3(256), 0, s, p);
+    const bool cap = p.softcap > 0.0f;
+    if (p.vimg != nullptr) {
+      if (cap)
+        hipLaunchKernelGGL((prefill_mx_kernel<TT, true, true>), grid, dim3(256), 0, s, p);
+      else
+        hipLaunchKernelGGL((prefill_mx_kernel<TT, false, true>), grid, dim3(256), 0, s, p);
+    } else if (cap) {
+      hipLaunchKernelGGL((prefill_mx_kernel<TT, true, false>), grid, dim3(256), 0, s, p);
+    } else {
+      hipLaunchKernelGGL((prefill_mx_kernel<TT, false, false>), grid, dim3(256), 0, s, p);
+    }
     return hipGetLastError();
   }
   if (p.softcap > 0.0f)
@@ -1095,7 +1312,23 @@ hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype ca
       !p.plan_split || !p.part_o || !p.part_ml || p.max_splits != 1)
     return hipErrorInvalidValue;
   if ((int64_t)p.plan_items * (kPrefillRows / kPrefillMergeRows) > INT32_MAX) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((prefill_plan_kernel<1024>), dim3(1), dim3(1024), 0, s, p);
+  // Value images (head 128): the maxima pass rides in the plan launch (bf16 values only), then
+  // one workgroup per (64-key step, kv-head, sequence) writes the images.
+  const bool img = p.vimg != nullptr;
+  if (img && (p.head_dim != 128 || !p.vscale || !p.vmax || p.img_steps <= 0 || p.img_chunks <= 0 ||
+              p.img_steps > 65535 || p.kv_heads > 65535 || p.batch > 65535))
+    return hipErrorInvalidValue;
+  const int64_t nmax = img && act == PA_DTYPE_BFLOAT16
+                           ? (int64_t)p.batch * p.kv_heads * p.img_chunks : 0;
+  if (nmax + 1 > INT32_MAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((prefill_plan_kernel<1024>), dim3((unsigned)(1 + nmax)), dim3(1024), 0, s, p);
+  if (img) {
+    const dim3 ig(p.img_steps, p.kv_heads, p.batch);
+    if (act == PA_DTYPE_FLOAT16)
+      hipLaunchKernelGGL((prefill_vimage_kernel<TF16>), ig, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((prefill_vimage_kernel<TBF16>), ig, dim3(256), 0, s, p);
+  }
   const dim3 grid(2 * p.plan_items, 1);
   hipError_t e = act == PA_DTYPE_FLOAT16 ? launch_t<TF16>(p, grid, s) : launch_t<TBF16>(p, grid, s);
   if (e != hipSuccess) return e;

@@ -1,0 +1,107 @@
+"""GPU parity of the planned head-128 prefill over value images.
+
+When every 64-key step of values is read by at least four 128-row blocks (g * max_query_len >=
+512 grouped query rows per sequence) the planned launch converts the value rows once per
+(sequence, kv-head) into fp16 P.V operand images under per-quarter power-of-two scales (from a
+maxima pass over all the sequence's values), and the prefill kernel stages keys (from the pages)
+and value images into LDS with direct loads.  Checked against the oracle rounded to T
+(rel-L2 <= 2e-3) and against its float64 result (<= 4e-3), twice per case (bit-identical calls):
+both activation dtypes, values far above and below the fp16 range, a few rows 1000x larger than
+the rest late in long sequences (the scale covers every chunk of the maxima pass), block sizes
+32 and 8 (keys addressed row by row), new rows read from the inputs instead of the pages,
+softcap + window, sink logits, an empty sequence, ragged chunks and a 7:1 head group.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import _oracle as orc
+from _oracle import BF16, F16
+from pa_cases import make_case, to_torch, from_torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(case, dtype, nq, new_rows_in_cache):
+    import torch
+    import onnxruntime_ep_mlx_amd as ep
+    H = case["num_heads"]
+    t = {n: to_torch(case[n], dtype) for n in ("query", "key", "value", "key_cache",
+                                               "value_cache")}
+    I = {n: torch.from_numpy(case[n]).cuda() for n in ("cum", "past", "block_table")}
+    if new_rows_in_cache:
+        ep.reshape_and_cache(t["key"], t["value"], t["key_cache"], t["value_cache"], I["cum"],
+                             I["past"], I["block_table"])
+    hs = to_torch(case["head_sink"], dtype) if case.get("head_sink") is not None else None
+    outs = [ep.attention(t["query"], t["key"], t["value"], t["key_cache"], t["value_cache"],
+                         I["cum"], I["past"], I["block_table"], num_heads=H, max_query_len=nq,
+                         kind=2, head_sink=hs, softcap=case["softcap"],
+                         local_window_size=case["local_window_size"],
+                         new_rows_in_cache=new_rows_in_cache) for _ in range(2)]
+    torch.cuda.synchronize()
+    return outs
+
+
+def _check(case, dtype, nq, new_rows_in_cache):
+    import torch
+    ref, ref_t, _, _ = orc.paged_attention_op(case)
+    outs = _run(case, dtype, nq, new_rows_in_cache)
+    for out in outs:
+        got = orc.decode(from_torch(out, dtype), dtype)
+        err_t = orc.rel_l2(got, orc.decode(ref_t, dtype))
+        err64 = orc.rel_l2(got.astype(np.float64), ref)
+        assert err_t <= 2e-3, err_t
+        assert err64 <= 4e-3, err64
+    assert torch.equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("dtype,bs,in_cache,vstd,softcap,window,sink,hot", [
+    (BF16, 16, True, None, 0.0, -1, True, None),
+    (F16, 16, True, None, 0.0, -1, True, None),
+    (BF16, 16, True, 1e6, 0.0, -1, False, None),
+    (BF16, 16, True, 1e-6, 0.0, -1, False, None),
+    (BF16, 16, True, None, 0.0, -1, False, 1000.0),
+    (BF16, 32, True, None, 30.0, 2900, True, None),
+    (BF16, 8, False, None, 0.0, -1, False, None),
+    (F16, 8, False, None, 0.0, -1, True, None)],
+    ids=["bf16_sink", "f16_sink", "bf16_large_v", "bf16_tiny_v", "bf16_hot_rows",
+         "bf16_block32_softcap_window", "bf16_block8_new_rows_from_inputs",
+         "f16_block8_new_rows_from_inputs_sink"])
+def test_prefill_images(dtype, bs, in_cache, vstd, softcap, window, sink, hot):
+    rng = np.random.default_rng(5 + bs)
+    B, H, KV, d, nq = 24, 32, 8, 128, 128  # g * nq = 512 rows: 4 row blocks per sequence
+    new_lens = np.full(B, nq)
+    new_lens[3] = 0
+    new_lens[9] = 77
+    past = rng.integers(0, 600, size=B)
+    past[[4, 20]] = [2900, 4000]  # items over the split threshold
+    past[11] = 0
+    mb = int((past.max() + nq + bs - 1) // bs)
+    case = make_case(H, KV, d, B * mb, bs, B, dtype=dtype, seed=5 + bs, new_lens=new_lens,
+                     past=past, max_blocks=mb, std=1.0, value_std=vstd, softcap=softcap,
+                     window=window, head_sink=(rng.standard_normal(H) if sink else None))
+    if hot is not None:
+        # rows 2000..2015 and 3500..3515 of the two long sequences (maxima chunks 3 and 6)
+        vc = orc.decode(case["value_cache"], dtype)
+        for b in (4, 20):
+            for pos in (2000, 3500):
+                if pos < past[b]:
+                    blk = case["block_table"][b, pos // bs]
+                    vc[blk, pos % bs: pos % bs + 16] *= hot
+        case["value_cache"] = orc.encode(vc, dtype)
+    _check(case, dtype, nq, in_cache)
+
+
+def test_prefill_images_group7_ragged():
+    """Qwen-style 7:1 head groups (28 query / 4 kv heads), ragged 100..200-token chunks (up to
+    11 row blocks per sequence), pasts up to 3000."""
+    rng = np.random.default_rng(41)
+    B, H, KV, d, bs = 16, 28, 4, 128, 16
+    new_lens = rng.integers(100, 201, size=B)
+    past = rng.integers(0, 3000, size=B)
+    nq = int(new_lens.max())
+    mb = int((past.max() + nq + bs - 1) // bs)
+    case = make_case(H, KV, d, B * mb, bs, B, dtype=BF16, seed=41, new_lens=new_lens,
+                     past=past, max_blocks=mb, std=1.0)
+    _check(case, BF16, nq, True)
