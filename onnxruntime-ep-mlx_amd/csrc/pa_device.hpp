@@ -346,21 +346,22 @@ struct AttnParams {
   int32_t* plan;
   int32_t* plan_info;
   int32_t* plan_split;
-  // Value operand images of the planned head-128 prefill (vimg != NULL): the value rows of every
-  // 64-key step of (sequence b, kv-head kh), converted to fp16 and regrouped once into the
-  // P.V A-operand layout, at vimg + ((b * kv_heads + kh) * img_steps + step) * kImgStepBytes;
-  // vscale[(b * kv_heads + kh) * 4 + q] is the power-of-two exponent s of 32-dim quarter q
-  // (image element = value * 2^-s); vmax[((b * kv_heads + kh) * img_chunks + c) * 4 + q] the
-  // largest biased exponent of |value| in quarter q over keys [kImgChunkKeys * c, + kImgChunkKeys).
+  // Operand images of the planned head-128 prefill (vimg != NULL): for every 64-key step of
+  // (sequence b, kv-head kh), the key rows gathered and the value rows converted to fp16,
+  // both laid out as the prefill kernel's LDS operands, at
+  // vimg + ((b * kv_heads + kh) * img_steps + step) * kImgStepBytes;
+  // vscale[(b * kv_heads + kh) * 4 + q] is the power-of-two exponent s of 32-dim quarter q of the
+  // values (image element = value * 2^-s); vmax[((b * kv_heads + kh) * img_chunks + c) * 4 + q]
+  // the largest biased exponent of |value| in quarter q over keys [kImgChunkKeys * c, + kImgChunkKeys).
   char* vimg;
   int32_t* vscale;
   int32_t* vmax;
   int32_t img_steps, img_chunks;
 };
 
-// Value image geometry of the planned head-128 prefill: 64 keys x 128 dims of fp16 per step,
-// the maxima pass covers kImgChunkKeys keys per workgroup.
-constexpr int kImgStepBytes = 64 * 128 * 2;
+// Image geometry of the planned head-128 prefill: 64 keys x 128 dims of 16-bit keys and values
+// per step, the maxima pass covers kImgChunkKeys keys per workgroup.
+constexpr int kImgStepBytes = 2 * 64 * 128 * 2;
 constexpr int kImgChunkKeys = 512;
 
 // Final normalisation shared by every attention kernel: the factor that turns an output

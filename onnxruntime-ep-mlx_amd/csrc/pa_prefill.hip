@@ -578,53 +578,22 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // loads) -- vmcnt(0), expcnt and lgkmcnt left at their maxima.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// Image staging: this wavefront's quarter of the step at t0 goes straight from memory to LDS
-// buffer `buf` (direct LDS loads, 16 bytes per lane, lane l at byte 16 l of a 1 KiB item), with
-// no register round trip:
-//   key items (kb = wave / 2, ks = 4 (wave % 2) + i): lane l reads key 32 kb + l % 32, bytes
-//   32 ks + 16 (l / 32) of its row slice -- the score A-operand image;
-//   value items (t = wave, nt): 1 KiB each, contiguous in the step's value image.
-// Keys come from the pages (16-key groups share a page) under the same conditions as mx_load;
-// other steps address every key row on its own.
-template <typename TT>
-__device__ __forceinline__ void img_issue(const WaveInfo& w, PageWindow& pw, MxBuf& buf, int wave,
-                                          int lane, int t0, const char* vimg_hb) {
-  constexpr int D = 128;
-  const int kb = wave >> 1;
-  const bool paged = w.bs % 16 == 0 && (t0 + kMxKeys <= w.cache_limit || w.cache_limit >= w.total) &&
-                     (w.lin_row0 < 0 || t0 + kMxKeys <= w.lin_cap);
-  const char* kp;
-  if (paged) {
-    int64_t grp[2];
+// Image staging: this wavefront's quarter of the step at t0 goes straight from the step's
+// operand image (AttnParams::vimg, the LDS buffer image byte for byte) to LDS buffer `buf`:
+// 8 direct LDS loads of 1 KiB items, 16 bytes per lane, no register round trip.
+__device__ __forceinline__ void img_issue(MxBuf& buf, int wave, int lane, int t0,
+                                          const char* img_hb) {
+  static_assert(sizeof(MxBuf::k) + sizeof(MxBuf::v) == kImgStepBytes, "image = LDS operands");
+  const char* src = img_hb + (int64_t)(t0 / kMxKeys) * kImgStepBytes + 8192 * wave + 16 * lane;
+  char* dst = reinterpret_cast<char*>(&buf.k[0][0][0]) + 8192 * wave;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int t = t0 + 32 * kb + 16 * q;
-      if (w.lin_row0 >= 0) {
-        grp[q] = w.lin_row0 + t;
-        continue;
-      }
-      const int bi = min(div_bs(t, w), w.max_blocks - 1);
-      if (bi < pw.first || bi >= pw.first + 64) window_at(pw, w, bi, lane);
-      int64_t blk = __builtin_amdgcn_readlane(pw.ids, bi - pw.first);
-      blk = min(max(blk, (int64_t)0), w.num_blocks - 1);
-      grp[q] = blk * w.bs + mod_bs(t, w);
-    }
-    const int64_t row = ((lane & 16) ? grp[1] : grp[0]) + (lane & 15);
-    kp = w.kc + row * w.rowb + w.hoff + 16 * (lane >> 5);
-  } else {
-    kp = row_ptr(w, t0 + 32 * kb + (lane & 31), false, D) + 16 * (lane >> 5);
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int ks = 4 * (wave & 1) + i;
-    __builtin_amdgcn_global_load_lds(kp + 32 * ks, (lds_ptr_t)&buf.k[kb][ks][0], 16, 0, 0);
-  }
-  const char* vp = vimg_hb + (int64_t)(t0 / kMxKeys) * kImgStepBytes + 4096 * wave + 16 * lane;
-#pragma unroll
-  for (int nt = 0; nt < 4; ++nt)
-    __builtin_amdgcn_global_load_lds(vp + 1024 * nt, (lds_ptr_t)&buf.v[wave][nt][0], 16, 0, 0);
+  for (int i = 0; i < 8; ++i)
+    __builtin_amdgcn_global_load_lds(src + 1024 * i, (lds_ptr_t)(dst + 1024 * i), 16, 0, 0);
 }
 
+#ifndef PA_MX_SGB
+#define PA_MX_SGB 0
+#endif
 // IMG: value operands from the per-(sequence, kv-head) value images (AttnParams::vimg), staged
 // by direct LDS loads one step ahead; otherwise loaded, converted and regrouped in the loop.
 template <typename TT, bool CAP, bool IMG>
@@ -723,129 +692,165 @@ prefill_mx_kernel(const AttnParams p) {
   // scale of the quarter it stages (bf16 values; fp16 values are used unscaled).
   constexpr int kS0 = std::is_same<TT, TBF16>::value ? -112 : 0;
   int sv[4] = {kS0, kS0, kS0, kS0};
-  int s_stage = kS0;
 
-  PageWindow pw;
-  window_at(pw, w, min(div_bs(t_first, w), w.max_blocks - 1), lane);
-  MxStage st;
-  const char* vimg_hb = nullptr;
+  // Scores of the step at t0 from LDS buffer `buf`: two 32-key blocks, their accumulation chains
+  // interleaved.
+  auto scores = [&](const MxBuf& buf, f32x16(&sc)[2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sc[kb][i] = 0.0f;
+#if PA_MX_SGB
+    // operands of k-step ks + PA_MX_SGB read while the products of k-step ks run
+    u32x4 ka[8][2];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) ka[ks][kb] = buf.k[kb][ks][lane];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) sc[kb] = mfma32<TT>(ka[ks][kb], qv[ks], sc[kb]);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * PA_MX_SGB, 0);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      if (ks + PA_MX_SGB < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    }
+#else
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) sc[kb] = mfma32<TT>(buf.k[kb][ks][lane], qv[ks], sc[kb]);
+#endif
+  };
+  // Online softmax of the step at t0 over its scores, then O += P . V from buffer `buf`.
+  auto attend = [&](const f32x16(&sc)[2], int t0, const MxBuf& buf) __attribute__((always_inline)) {
+    float x[2][16];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float v = sc[kb][i];
+        if constexpr (CAP) v = p.softcap * tanhf(v * scale / p.softcap) * kLog2e;
+        x[kb][i] = v;
+      }
+    // per-score position tests only on steps some row does not see whole (one scalar branch)
+    if (!(t0 >= all_lo && t0 + kMxKeys <= all_hi)) {
+      const int base = t0 + 4 * h;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int pos = base + 32 * kb + 8 * (i >> 2) + (i & 3);
+          x[kb][i] = (pos < end && pos >= vis_lo && pos < vis_hi) ? x[kb][i] : kNegInf;
+        }
+    }
+    float lmax = kNegInf;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) lmax = fmaxf(lmax, x[kb][i]);
+    lmax = fmaxf(lmax, other_half(lmax));
+    if constexpr (!CAP) lmax *= scale_log2;
+    if (__any(lmax > m_run + 8.0f)) {
+      const float m_new = fmaxf(m_run, lmax);
+      const float alpha = (m_run == kNegInf || m_new == kNegInf) ? 1.0f : exp2f(m_run - m_new);
+      l_part *= alpha;
+      m_run = m_new;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) o[nt] *= alpha;
+    }
+    // value scales of this step: the output quarters follow a raised s exactly
+    if constexpr (!IMG) {
+      const int4 vs4 = *reinterpret_cast<const int4*>(buf.vs);
+      const int vsn[4] = {__builtin_amdgcn_readfirstlane(vs4.x),
+                          __builtin_amdgcn_readfirstlane(vs4.y),
+                          __builtin_amdgcn_readfirstlane(vs4.z),
+                          __builtin_amdgcn_readfirstlane(vs4.w)};
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+        if (vsn[nt] != sv[nt]) {
+          const float f = __builtin_ldexpf(1.0f, sv[nt] - vsn[nt]);
+          o[nt] *= f;
+          sv[nt] = vsn[nt];
+        }
+    }
+    const float msafe = (m_run == kNegInf) ? 0.0f : m_run;
+    u32x4 pb[4];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      float pv[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        pv[i] = __builtin_amdgcn_exp2f(CAP ? x[kb][i] - msafe
+                                           : __builtin_fmaf(x[kb][i], scale_log2, -msafe));
+        l_part += pv[i];
+      }
+#pragma unroll
+      for (int half = 0; half < 2; ++half)
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          pb[2 * kb + half][m] = __builtin_bit_cast(
+              uint32_t, __builtin_convertvector(
+                            f32x2v{pv[8 * half + 2 * m], pv[8 * half + 2 * m + 1]}, f16x2v));
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+        o[nt] = mfma32<TF16>(buf.v[t][nt][IMG ? lane : mx_vslot(lane)], pb[t], o[nt]);
+  };
+  // Steps some row of this wavefront sees.
+  auto seen = [&](int t0) { return t0 < any_hi && t0 + kMxKeys > any_lo; };
+
   if constexpr (IMG) {
-    // the image scales of this (sequence, kv-head): fixed for the whole key range
     const int64_t hb = (int64_t)b * p.kv_heads + kh;
-    vimg_hb = p.vimg + hb * p.img_steps * (int64_t)kImgStepBytes;
+    const char* img_hb = p.vimg + hb * p.img_steps * (int64_t)kImgStepBytes;
+    // the image scales of this (sequence, kv-head): fixed for the whole key range
     const int4 s4 = *reinterpret_cast<const int4*>(p.vscale + hb * 4);
     sv[0] = __builtin_amdgcn_readfirstlane(s4.x);
     sv[1] = __builtin_amdgcn_readfirstlane(s4.y);
     sv[2] = __builtin_amdgcn_readfirstlane(s4.z);
     sv[3] = __builtin_amdgcn_readfirstlane(s4.w);
-    if (nsteps > 0) img_issue<TT>(w, pw, lds[0], wave, lane, t_first, vimg_hb);
+    // Direct LDS loads of step k + 1 into the other buffer while step k computes (every
+    // wavefront finished reading that buffer before the barrier that ended iteration k - 1).
+    if (nsteps > 0) img_issue(lds[0], wave, lane, t_first, img_hb);
     wait_vmem();
-  } else if (nsteps > 0) {
-    mx_load<TT>(w, pw, wave, lane, t_first, st);
-    mx_store<TT>(lds[0], st, wave, lane, t_first, total, s_stage);
-    if (nsteps > 1) mx_load<TT>(w, pw, wave, lane, t_first + kMxKeys, st);
-  }
-  __syncthreads();
-  for (int k = 0; k < nsteps; ++k) {
-    const int t0 = t_first + kMxKeys * k;
-    MxBuf& cur = lds[k & 1];
-    // image staging: step k + 1 into the other buffer (every wavefront finished reading it
-    // before the barrier that ended iteration k - 1)
-    if constexpr (IMG)
-      if (k + 1 < nsteps) img_issue<TT>(w, pw, lds[(k + 1) & 1], wave, lane, t0 + kMxKeys, vimg_hb);
-    if (t0 < any_hi && t0 + kMxKeys > any_lo) {
-      // scores: two 32-key blocks, their accumulation chains interleaved
-      f32x16 sc[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sc[kb][i] = 0.0f;
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) sc[kb] = mfma32<TT>(cur.k[kb][ks][lane], qv[ks], sc[kb]);
-      float x[2][16];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float v = sc[kb][i];
-          if constexpr (CAP) v = p.softcap * tanhf(v * scale / p.softcap) * kLog2e;
-          x[kb][i] = v;
-        }
-      // per-score position tests only on steps some row does not see whole (one scalar branch)
-      if (!(t0 >= all_lo && t0 + kMxKeys <= all_hi)) {
-        const int base = t0 + 4 * h;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int pos = base + 32 * kb + 8 * (i >> 2) + (i & 3);
-            x[kb][i] = (pos < end && pos >= vis_lo && pos < vis_hi) ? x[kb][i] : kNegInf;
-          }
+    __syncthreads();
+    for (int k = 0; k < nsteps; ++k) {
+      const int t0 = t_first + kMxKeys * k;
+      if (k + 1 < nsteps) img_issue(lds[(k + 1) & 1], wave, lane, t0 + kMxKeys, img_hb);
+      if (seen(t0)) {
+        f32x16 sc[2];
+        scores(lds[k & 1], sc);
+        attend(sc, t0, lds[k & 1]);
       }
-      float lmax = kNegInf;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) lmax = fmaxf(lmax, x[kb][i]);
-      lmax = fmaxf(lmax, other_half(lmax));
-      if constexpr (!CAP) lmax *= scale_log2;
-      if (__any(lmax > m_run + 8.0f)) {
-        const float m_new = fmaxf(m_run, lmax);
-        const float alpha = (m_run == kNegInf || m_new == kNegInf) ? 1.0f : exp2f(m_run - m_new);
-        l_part *= alpha;
-        m_run = m_new;
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) o[nt] *= alpha;
-      }
-      // value scales of this step: the output quarters follow a raised s exactly
-      if constexpr (!IMG) {
-        const int4 vs4 = *reinterpret_cast<const int4*>(cur.vs);
-        const int vsn[4] = {__builtin_amdgcn_readfirstlane(vs4.x),
-                            __builtin_amdgcn_readfirstlane(vs4.y),
-                            __builtin_amdgcn_readfirstlane(vs4.z),
-                            __builtin_amdgcn_readfirstlane(vs4.w)};
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
-          if (vsn[nt] != sv[nt]) {
-            const float f = __builtin_ldexpf(1.0f, sv[nt] - vsn[nt]);
-            o[nt] *= f;
-            sv[nt] = vsn[nt];
-          }
-      }
-      const float msafe = (m_run == kNegInf) ? 0.0f : m_run;
-      u32x4 pb[4];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        float pv[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          pv[i] = __builtin_amdgcn_exp2f(CAP ? x[kb][i] - msafe
-                                             : __builtin_fmaf(x[kb][i], scale_log2, -msafe));
-          l_part += pv[i];
-        }
-#pragma unroll
-        for (int half = 0; half < 2; ++half)
-#pragma unroll
-          for (int m = 0; m < 4; ++m)
-            pb[2 * kb + half][m] = __builtin_bit_cast(
-                uint32_t, __builtin_convertvector(
-                              f32x2v{pv[8 * half + 2 * m], pv[8 * half + 2 * m + 1]}, f16x2v));
-      }
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
-          o[nt] = mfma32<TF16>(cur.v[t][nt][IMG ? lane : mx_vslot(lane)], pb[t], o[nt]);
-    }
-    if constexpr (IMG) {
       wait_vmem();
-    } else {
-      if (k + 1 < nsteps) mx_store<TT>(lds[(k + 1) & 1], st, wave, lane, t0 + kMxKeys, total, s_stage);
-      if (k + 2 < nsteps) mx_load<TT>(w, pw, wave, lane, t0 + 2 * kMxKeys, st);
+      __syncthreads();
+    }
+  } else {
+    PageWindow pw;
+    window_at(pw, w, min(div_bs(t_first, w), w.max_blocks - 1), lane);
+    MxStage st;
+    int s_stage = kS0;
+    if (nsteps > 0) {
+      mx_load<TT>(w, pw, wave, lane, t_first, st);
+      mx_store<TT>(lds[0], st, wave, lane, t_first, total, s_stage);
+      if (nsteps > 1) mx_load<TT>(w, pw, wave, lane, t_first + kMxKeys, st);
     }
     __syncthreads();
+    for (int k = 0; k < nsteps; ++k) {
+      const int t0 = t_first + kMxKeys * k;
+      if (seen(t0)) {
+        f32x16 sc[2];
+        scores(lds[k & 1], sc);
+        attend(sc, t0, lds[k & 1]);
+      }
+      if (k + 1 < nsteps) mx_store<TT>(lds[(k + 1) & 1], st, wave, lane, t0 + kMxKeys, total, s_stage);
+      if (k + 2 < nsteps) mx_load<TT>(w, pw, wave, lane, t0 + 2 * kMxKeys, st);
+      __syncthreads();
+    }
   }
 
   // Epilogue: row r's output in true units is o[nt] * 2^sv[nt]; lanes l and l ^ 32 hold dims
@@ -1007,16 +1012,21 @@ __device__ __forceinline__ void vmax_chunk(const AttnParams& p, int id) {
   if (tid < 4) p.vmax[(((int64_t)b * p.kv_heads + kh) * p.img_chunks + c) * 4 + tid] = qmax[tid];
 }
 
-// Value operand images (AttnParams::vimg): one workgroup per (64-key step, kv-head, sequence).
-// The step's value rows (zero at or past the sequence end) are converted to fp16 under the
-// (sequence, kv-head)'s quarter scales 2^-s -- bf16 values: s from the maxima pass, so the
-// quarter's largest value lies in [2^14, 2^15) of fp16 (exact conversion; values below 2^-29 of
-// it lose bits in the fp16 subnormal range); fp16 values: s = 0 -- staged in LDS and regrouped
-// into the P.V A-operand layout of prefill_mx_kernel: item (t, nt) of the step, lane l holds dim
-// 32 nt + l % 32 of keys 16 t + 4 h + e and then 16 t + 8 + 4 h + e (e < 4, h = l / 32).
+// Operand images (AttnParams::vimg): one workgroup per (64-key step, kv-head, sequence) writes
+// the step's LDS operand buffer of prefill_mx_kernel byte for byte, so the kernel's staging is a
+// plain copy:
+//   keys (16 KiB): item (kb, ks), lane l holds bytes 32 ks + 16 (l / 32) .. + 15 of the row slice
+//   of key 32 kb + l % 32 -- the rows gathered from the pages (or the caller's new rows), zero at
+//   or past the sequence end;
+//   values (16 KiB): the rows (zero at or past the end) converted to fp16 under the (sequence,
+//   kv-head)'s quarter scales 2^-s -- bf16 values: s from the maxima pass, so the quarter's
+//   largest value lies in [2^14, 2^15) of fp16 (exact conversion; values below 2^-29 of it lose
+//   bits in the fp16 subnormal range); fp16 values: s = 0 -- and regrouped through LDS into the
+//   P.V A-operand layout: item (t, nt), lane l holds dim 32 nt + l % 32 of keys 16 t + 4 h + e
+//   and then 16 t + 8 + 4 h + e (e < 4, h = l / 32).
 // Workgroup 0 of a (sequence, kv-head) also stores the scales for the prefill kernel.
 template <typename TT>
-__global__ __launch_bounds__(256) void prefill_vimage_kernel(const AttnParams p) {
+__global__ __launch_bounds__(256) void prefill_image_kernel(const AttnParams p) {
   constexpr int D = 128;
   const int j = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
   const int s0 = min(max(p.cum[b], 0), p.num_tokens);
@@ -1027,7 +1037,7 @@ __global__ __launch_bounds__(256) void prefill_vimage_kernel(const AttnParams p)
   const int64_t hb = (int64_t)b * p.kv_heads + kh;
   const WaveInfo w = make_wave(p, D, b, kh, s0, pastb, total);
   __shared__ int qs[4];
-  __shared__ uint32_t rows[kMxKeys][D / 2 + 1];  // fp16 rows, one word = two dims
+  __shared__ uint32_t rows[kMxKeys][D / 2 + 1];  // fp16 value rows, one word = two dims
   const int tid = threadIdx.x;
   if (tid < 4) {
     int s = 0;
@@ -1040,17 +1050,28 @@ __global__ __launch_bounds__(256) void prefill_vimage_kernel(const AttnParams p)
     qs[tid] = s;
     if (j == 0) p.vscale[hb * 4 + tid] = s;
   }
-  // the row slices: thread -> row tid / 4, quarter tid % 4 (64 bytes)
+  // row slices: thread -> key row tid / 4, bytes 64 (tid % 4) .. + 63 (dims 32 q .. 32 q + 31)
   const int r = tid >> 2, q = tid & 3;
   const int pos = j * kMxKeys + r;
-  u32x4 x[4];
-  if (pos < total) {
-    const char* src = row_ptr(w, pos, true, D) + 64 * q;
+  const bool live = pos < total;
+  u32x4 kx[4], vx[4];
+  {
+    const char* ks = live ? row_ptr(w, pos, false, D) + 64 * q : nullptr;
+    const char* vs = live ? row_ptr(w, pos, true, D) + 64 * q : nullptr;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = ld16(src + 16 * i);
-  } else {
+    for (int i = 0; i < 4; ++i) {
+      kx[i] = live ? ld16(ks + 16 * i) : u32x4{0u, 0u, 0u, 0u};
+      vx[i] = live ? ld16(vs + 16 * i) : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  char* dst = p.vimg + (hb * p.img_steps + j) * (int64_t)kImgStepBytes;
+  // keys: 16-byte chunk dc = 4 q + i of row r -> item (kb = r / 32, ks = dc / 2), lane
+  // 32 (dc % 2) + r % 32
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = u32x4{0u, 0u, 0u, 0u};
+  for (int i = 0; i < 4; ++i) {
+    const int dc = 4 * q + i;
+    *reinterpret_cast<u32x4*>(dst + ((((r >> 5) * 8 + (dc >> 1)) * 64) + 32 * (dc & 1) + (r & 31)) * 16) =
+        kx[i];
   }
   __syncthreads();
   if constexpr (std::is_same<TT, TBF16>::value) {
@@ -1061,19 +1082,19 @@ __global__ __launch_bounds__(256) void prefill_vimage_kernel(const AttnParams p)
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
-        u16x2 a = __builtin_bit_cast(u16x2, x[i][m] & 0x7fff7fffu);
+        u16x2 a = __builtin_bit_cast(u16x2, vx[i][m] & 0x7fff7fffu);
         a = __builtin_elementwise_sub_sat(a, u16x2{bias, bias});
         a = a << (unsigned short)3;
-        x[i][m] = (x[i][m] & 0x80008000u) | __builtin_bit_cast(uint32_t, a);
+        vx[i][m] = (vx[i][m] & 0x80008000u) | __builtin_bit_cast(uint32_t, a);
       }
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int m = 0; m < 4; ++m) rows[r][16 * q + 4 * i + m] = x[i][m];
+    for (int m = 0; m < 4; ++m) rows[r][16 * q + 4 * i + m] = vx[i][m];
   __syncthreads();
-  // regroup: task (t, h, nt, dim pair dp) -> slots of lanes 32 h + 2 dp (+1) of item (t, nt)
-  char* dst = p.vimg + (hb * p.img_steps + j) * (int64_t)kImgStepBytes;
+  // value regroup: task (t, h, nt, dim pair dp) -> slots of lanes 32 h + 2 dp (+1) of item (t, nt)
+  char* vdst = dst + kImgStepBytes / 2;
 #pragma unroll
   for (int rep = 0; rep < 2; ++rep) {
     const int task = tid + 256 * rep;
@@ -1087,7 +1108,7 @@ __global__ __launch_bounds__(256) void prefill_vimage_kernel(const AttnParams p)
       lo[e2] = __builtin_amdgcn_perm(wb, wa, 0x05040100u);
       hi[e2] = __builtin_amdgcn_perm(wb, wa, 0x07060302u);
     }
-    u32x4* o = reinterpret_cast<u32x4*>(dst + (4 * t + nt) * 1024) + 32 * h + 2 * dp;
+    u32x4* o = reinterpret_cast<u32x4*>(vdst + (4 * t + nt) * 1024) + 32 * h + 2 * dp;
     o[0] = lo;
     o[1] = hi;
   }
@@ -1312,8 +1333,8 @@ hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype ca
       !p.plan_split || !p.part_o || !p.part_ml || p.max_splits != 1)
     return hipErrorInvalidValue;
   if ((int64_t)p.plan_items * (kPrefillRows / kPrefillMergeRows) > INT32_MAX) return hipErrorInvalidValue;
-  // Value images (head 128): the maxima pass rides in the plan launch (bf16 values only), then
-  // one workgroup per (64-key step, kv-head, sequence) writes the images.
+  // Operand images (head 128): the value maxima pass rides in the plan launch (bf16 values
+  // only), then one workgroup per (64-key step, kv-head, sequence) writes the images.
   const bool img = p.vimg != nullptr;
   if (img && (p.head_dim != 128 || !p.vscale || !p.vmax || p.img_steps <= 0 || p.img_chunks <= 0 ||
               p.img_steps > 65535 || p.kv_heads > 65535 || p.batch > 65535))
@@ -1325,9 +1346,9 @@ hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype ca
   if (img) {
     const dim3 ig(p.img_steps, p.kv_heads, p.batch);
     if (act == PA_DTYPE_FLOAT16)
-      hipLaunchKernelGGL((prefill_vimage_kernel<TF16>), ig, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((prefill_image_kernel<TF16>), ig, dim3(256), 0, s, p);
     else
-      hipLaunchKernelGGL((prefill_vimage_kernel<TBF16>), ig, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((prefill_image_kernel<TBF16>), ig, dim3(256), 0, s, p);
   }
   const dim3 grid(2 * p.plan_items, 1);
   hipError_t e = act == PA_DTYPE_FLOAT16 ? launch_t<TF16>(p, grid, s) : launch_t<TBF16>(p, grid, s);
