@@ -838,6 +838,21 @@ bool host_slots_distinct(const pa_paged_attention_io* io) {
   const int32_t* past = io->host_past_seqlens;
   const int32_t* bt = io->host_block_table;
   const int64_t bs = io->cache.block_size;
+  // Sufficient and cheap (about T / block_size + B entries): no block id appears twice among the
+  // block-table entries that cover the new positions, so no two slots (block * bs + row) meet.
+  {
+    std::vector<int32_t> blocks;
+    blocks.reserve((size_t)std::max(io->num_tokens, 0) / std::max<int64_t>(bs, 1) + 2 * io->batch);
+    for (int b = 0; b < io->batch; ++b) {
+      if (cum[b + 1] <= cum[b]) continue;
+      const int64_t first = (int64_t)past[b], last = first + (cum[b + 1] - cum[b]) - 1;
+      for (int64_t bi = first / bs; bi <= last / bs; ++bi)
+        blocks.push_back(bt[(int64_t)b * io->max_blocks + bi]);
+    }
+    std::sort(blocks.begin(), blocks.end());
+    if (std::adjacent_find(blocks.begin(), blocks.end()) == blocks.end()) return true;
+  }
+  // Otherwise compare the slots themselves (shared blocks whose written rows differ).
   std::vector<int64_t> slots;
   slots.reserve((size_t)std::max(io->num_tokens, 0));
   for (int b = 0; b < io->batch; ++b)

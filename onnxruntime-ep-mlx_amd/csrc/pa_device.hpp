@@ -357,6 +357,7 @@ struct AttnParams {
   int32_t* vscale;
   int32_t* vmax;
   int32_t img_steps, img_chunks;
+  int32_t plan_vmax_groups;  // workgroups of the plan launch that run the value maxima pass
 };
 
 // Image geometry of the planned head-128 prefill: 64 keys x 128 dims of 16-bit keys and values

@@ -594,6 +594,7 @@ __device__ __forceinline__ void img_issue(MxBuf& buf, int wave, int lane, int t0
 #ifndef PA_MX_SGB
 #define PA_MX_SGB 0
 #endif
+
 // IMG: value operands from the per-(sequence, kv-head) value images (AttnParams::vimg), staged
 // by direct LDS loads one step ahead; otherwise loaded, converted and regrouped in the loop.
 template <typename TT, bool CAP, bool IMG>
@@ -785,15 +786,17 @@ prefill_mx_kernel(const AttnParams p) {
       for (int i = 0; i < 16; ++i) {
         pv[i] = __builtin_amdgcn_exp2f(CAP ? x[kb][i] - msafe
                                            : __builtin_fmaf(x[kb][i], scale_log2, -msafe));
-        l_part += pv[i];
       }
 #pragma unroll
       for (int half = 0; half < 2; ++half)
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
-          pb[2 * kb + half][m] = __builtin_bit_cast(
-              uint32_t, __builtin_convertvector(
-                            f32x2v{pv[8 * half + 2 * m], pv[8 * half + 2 * m + 1]}, f16x2v));
+        for (int m = 0; m < 4; ++m) {
+          const f16x2v ph = __builtin_convertvector(
+              f32x2v{pv[8 * half + 2 * m], pv[8 * half + 2 * m + 1]}, f16x2v);
+          pb[2 * kb + half][m] = __builtin_bit_cast(uint32_t, ph);
+          // the row sum adds the fp16 probabilities the P.V product takes
+          l_part = __builtin_amdgcn_fdot2(ph, f16x2v{(_Float16)1.0f, (_Float16)1.0f}, l_part, false);
+        }
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -968,9 +971,9 @@ __device__ __forceinline__ ItemKeys item_keys(const AttnParams& p, int i) {
 // (LDS histogram, descending); the order inside a bucket is whatever the atomics give, which
 // changes nothing in the results (every unit writes its own rows or partial).
 //
-// With bf16 value images, workgroups 1.. of the same launch run the value maxima pass
-// (vmax_chunk), which needs nothing from the plan: it costs no launch of its own and runs on
-// other CUs while workgroup 0 plans.
+// With operand images, workgroups 1.. of the same launch run the value maxima pass (vmax_chunk,
+// bf16 values) and write the key half of the images (key_image), neither of which needs anything
+// from the plan: they cost no launch of their own and run on other CUs while workgroup 0 plans.
 template <int NT>
 __device__ __forceinline__ void vmax_chunk(const AttnParams& p, int id) {
   constexpr int D = 128;
@@ -989,17 +992,21 @@ __device__ __forceinline__ void vmax_chunk(const AttnParams& p, int id) {
   if (tid < 4) qmax[tid] = 0;
   // thread: 16-byte piece tid % 16 of the 256-byte value slice (quarter (tid % 16) / 4) of every
   // (NT / 16)-th row of the chunk
+  constexpr int RPT = kImgChunkKeys / (NT / 16);  // rows per thread
+  u32x4 x[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int pos = c * kImgChunkKeys + (tid >> 4) + (NT / 16) * i;
+    x[i] = pos < total ? ld16(row_ptr(w, pos, true, D) + 16 * (tid & 15)) : u32x4{0u, 0u, 0u, 0u};
+  }
   uint32_t mx = 0;
-  for (int r = tid >> 4; r < kImgChunkKeys; r += NT / 16) {
-    const int pos = c * kImgChunkKeys + r;
-    if (pos >= total) break;
-    const u32x4 x = ld16(row_ptr(w, pos, true, D) + 16 * (tid & 15));
+#pragma unroll
+  for (int i = 0; i < RPT; ++i)
 #pragma unroll
     for (int m = 0; m < 4; ++m)
       mx = __builtin_bit_cast(uint32_t,
                               __builtin_elementwise_max(__builtin_bit_cast(u16x2, mx),
-                                                        __builtin_bit_cast(u16x2, x[m] & 0x7fff7fffu)));
-  }
+                                                        __builtin_bit_cast(u16x2, x[i][m] & 0x7fff7fffu)));
   int e = (int)(max(mx & 0xffffu, mx >> 16) >> 7);
   // lanes that differ in bits 0, 1, 4, 5 hold the same quarter
   e = max(e, __shfl_xor(e, 1, 64));
@@ -1012,18 +1019,51 @@ __device__ __forceinline__ void vmax_chunk(const AttnParams& p, int id) {
   if (tid < 4) p.vmax[(((int64_t)b * p.kv_heads + kh) * p.img_chunks + c) * 4 + tid] = qmax[tid];
 }
 
-// Operand images (AttnParams::vimg): one workgroup per (64-key step, kv-head, sequence) writes
-// the step's LDS operand buffer of prefill_mx_kernel byte for byte, so the kernel's staging is a
-// plain copy:
-//   keys (16 KiB): item (kb, ks), lane l holds bytes 32 ks + 16 (l / 32) .. + 15 of the row slice
-//   of key 32 kb + l % 32 -- the rows gathered from the pages (or the caller's new rows), zero at
-//   or past the sequence end;
-//   values (16 KiB): the rows (zero at or past the end) converted to fp16 under the (sequence,
-//   kv-head)'s quarter scales 2^-s -- bf16 values: s from the maxima pass, so the quarter's
-//   largest value lies in [2^14, 2^15) of fp16 (exact conversion; values below 2^-29 of it lose
-//   bits in the fp16 subnormal range); fp16 values: s = 0 -- and regrouped through LDS into the
-//   P.V A-operand layout: item (t, nt), lane l holds dim 32 nt + l % 32 of keys 16 t + 4 h + e
-//   and then 16 t + 8 + 4 h + e (e < 4, h = l / 32).
+// Key half of the operand images: NT / 256 consecutive 64-key steps of (sequence b, kv-head kh)
+// per workgroup of the plan launch (they need nothing from the plan or the value maxima).  Thread:
+// key row (t % 256) / 4 of step t / 256, bytes 64 (t % 4) .. + 63 of the row slice, whose 16-byte
+// chunk dc = 4 (t % 4) + i goes to item (kb = row / 32, ks = dc / 2), lane 32 (dc % 2) + row % 32;
+// rows at or past the sequence end are zero.
+template <int NT>
+__device__ __forceinline__ void key_image(const AttnParams& p, int id) {
+  constexpr int D = 128, SPW = NT / 256;
+  const int nj = (p.img_steps + SPW - 1) / SPW;
+  const int jb = id % nj, kh = (id / nj) % p.kv_heads, b = id / (nj * p.kv_heads);
+  if (b >= p.batch) return;
+  const int s0 = min(max(p.cum[b], 0), p.num_tokens);
+  const int s1 = min(max(p.cum[b + 1], s0), p.num_tokens);
+  const int pastb = clamped_past(p, b, s1 - s0);
+  const int total = pastb + (s1 - s0);
+  const int tid = threadIdx.x;
+  const int j = jb * SPW + tid / 256;
+  if (s1 == s0 || j >= p.img_steps || j * kMxKeys >= total) return;
+  const WaveInfo w = make_wave(p, D, b, kh, s0, pastb, total);
+  const int r = (tid & 255) >> 2, q = tid & 3;
+  const int pos = j * kMxKeys + r;
+  const bool live = pos < total;
+  const char* src = live ? row_ptr(w, pos, false, D) + 64 * q : nullptr;
+  u32x4 kx[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) kx[i] = live ? ld16(src + 16 * i) : u32x4{0u, 0u, 0u, 0u};
+  char* dst = p.vimg + (((int64_t)b * p.kv_heads + kh) * p.img_steps + j) * (int64_t)kImgStepBytes;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int dc = 4 * q + i;
+    *reinterpret_cast<u32x4*>(dst + ((((r >> 5) * 8 + (dc >> 1)) * 64) + 32 * (dc & 1) + (r & 31)) * 16) =
+        kx[i];
+  }
+}
+
+// Operand images (AttnParams::vimg): each 64-key step of (sequence, kv-head) holds the step's LDS
+// operand buffer of prefill_mx_kernel byte for byte, so the kernel's staging is a plain copy:
+//   keys (16 KiB, written by key_image in the plan launch): item (kb, ks), lane l holds bytes
+//   32 ks + 16 (l / 32) .. + 15 of the row slice of key 32 kb + l % 32;
+//   values (16 KiB, this kernel, one workgroup per (step, kv-head, sequence)): the rows (zero at or
+//   past the end) converted to fp16 under the (sequence, kv-head)'s quarter scales 2^-s -- bf16
+//   values: s from the maxima pass, so the quarter's largest value lies in [2^14, 2^15) of fp16
+//   (exact conversion; values below 2^-29 of it lose bits in the fp16 subnormal range); fp16
+//   values: s = 0 -- and regrouped through LDS into the P.V A-operand layout: item (t, nt), lane l
+//   holds dim 32 nt + l % 32 of keys 16 t + 4 h + e and then 16 t + 8 + 4 h + e (e < 4, h = l / 32).
 // Workgroup 0 of a (sequence, kv-head) also stores the scales for the prefill kernel.
 template <typename TT>
 __global__ __launch_bounds__(256) void prefill_image_kernel(const AttnParams p) {
@@ -1054,25 +1094,13 @@ __global__ __launch_bounds__(256) void prefill_image_kernel(const AttnParams p) 
   const int r = tid >> 2, q = tid & 3;
   const int pos = j * kMxKeys + r;
   const bool live = pos < total;
-  u32x4 kx[4], vx[4];
+  u32x4 vx[4];
   {
-    const char* ks = live ? row_ptr(w, pos, false, D) + 64 * q : nullptr;
     const char* vs = live ? row_ptr(w, pos, true, D) + 64 * q : nullptr;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      kx[i] = live ? ld16(ks + 16 * i) : u32x4{0u, 0u, 0u, 0u};
-      vx[i] = live ? ld16(vs + 16 * i) : u32x4{0u, 0u, 0u, 0u};
-    }
+    for (int i = 0; i < 4; ++i) vx[i] = live ? ld16(vs + 16 * i) : u32x4{0u, 0u, 0u, 0u};
   }
   char* dst = p.vimg + (hb * p.img_steps + j) * (int64_t)kImgStepBytes;
-  // keys: 16-byte chunk dc = 4 q + i of row r -> item (kb = r / 32, ks = dc / 2), lane
-  // 32 (dc % 2) + r % 32
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int dc = 4 * q + i;
-    *reinterpret_cast<u32x4*>(dst + ((((r >> 5) * 8 + (dc >> 1)) * 64) + 32 * (dc & 1) + (r & 31)) * 16) =
-        kx[i];
-  }
   __syncthreads();
   if constexpr (std::is_same<TT, TBF16>::value) {
     // bf16 exponent E -> fp16 exponent E - 112 - s: subtract (112 + s) << 7 from the magnitude
@@ -1117,7 +1145,12 @@ __global__ __launch_bounds__(256) void prefill_image_kernel(const AttnParams p) 
 template <int NT>
 __global__ __launch_bounds__(NT) void prefill_plan_kernel(const AttnParams p) {
   if (blockIdx.x > 0) {
-    vmax_chunk<NT>(p, (int)blockIdx.x - 1);
+    const int id = (int)blockIdx.x - 1;
+    const int nmax = p.plan_vmax_groups;
+    if (id < nmax)
+      vmax_chunk<NT>(p, id);
+    else
+      key_image<NT>(p, id - nmax);
     return;
   }
   constexpr int NB = 1024;  // buckets of 32-key steps (the last one holds everything longer)
@@ -1127,9 +1160,17 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(const AttnParams p) {
   for (int i = tid; i < NB; i += NT) hist[i] = 0;
   if (tid == 0) total_keys = 0;
   __syncthreads();
+  // The key ranges of this thread's first kCached items stay in registers for the later passes
+  // (each costs two dependent metadata loads).
+  constexpr int kCached = 4;
+  ItemKeys cached[kCached];
+  auto keys = [&](int j, int i) { return j < kCached ? cached[j] : item_keys(p, i); };
   unsigned long long mine = 0;
-  for (int i = tid; i < p.plan_items; i += NT) {
+  for (int i = tid, j = 0; i < p.plan_items; i += NT, ++j) {
     const ItemKeys k = item_keys(p, i);
+#pragma unroll
+    for (int c = 0; c < kCached; ++c)
+      if (c == j) cached[c] = k;
     if (k.end >= 0) mine += (unsigned long long)(k.end - k.first);
   }
   // Wave sums first: one LDS atomic per wavefront instead of one per thread on one address.
@@ -1148,8 +1189,8 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(const AttnParams p) {
   auto mid_of = [&](const ItemKeys& k) {
     return k.first + (((k.end - k.first + step - 1) / step + 1) / 2) * step;
   };
-  for (int i = tid; i < p.plan_items; i += NT) {
-    const ItemKeys k = item_keys(p, i);
+  for (int i = tid, j = 0; i < p.plan_items; i += NT, ++j) {
+    const ItemKeys k = keys(j, i);
     if (k.end < 0) {
       p.plan_split[i] = 0;
       continue;
@@ -1194,8 +1235,8 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(const AttnParams p) {
   }
   __syncthreads();
   int4* plan = reinterpret_cast<int4*>(p.plan);
-  for (int i = tid; i < p.plan_items; i += NT) {
-    const ItemKeys k = item_keys(p, i);
+  for (int i = tid, j = 0; i < p.plan_items; i += NT, ++j) {
+    const ItemKeys k = keys(j, i);
     if (k.end < 0) continue;
     if (split_of(k)) {
       const int mid = mid_of(k);
@@ -1339,10 +1380,17 @@ hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype ca
   if (img && (p.head_dim != 128 || !p.vscale || !p.vmax || p.img_steps <= 0 || p.img_chunks <= 0 ||
               p.img_steps > 65535 || p.kv_heads > 65535 || p.batch > 65535))
     return hipErrorInvalidValue;
+  constexpr int kPlanThreads = 1024;
   const int64_t nmax = img && act == PA_DTYPE_BFLOAT16
                            ? (int64_t)p.batch * p.kv_heads * p.img_chunks : 0;
-  if (nmax + 1 > INT32_MAX) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((prefill_plan_kernel<1024>), dim3((unsigned)(1 + nmax)), dim3(1024), 0, s, p);
+  const int64_t nkey = img ? (int64_t)p.batch * p.kv_heads *
+                                 ((p.img_steps + kPlanThreads / 256 - 1) / (kPlanThreads / 256))
+                           : 0;
+  if (nmax + nkey + 1 > INT32_MAX) return hipErrorInvalidValue;
+  AttnParams pp = p;
+  pp.plan_vmax_groups = (int32_t)nmax;
+  hipLaunchKernelGGL((prefill_plan_kernel<kPlanThreads>), dim3((unsigned)(1 + nmax + nkey)),
+                     dim3(kPlanThreads), 0, s, pp);
   if (img) {
     const dim3 ig(p.img_steps, p.kv_heads, p.batch);
     if (act == PA_DTYPE_FLOAT16)
