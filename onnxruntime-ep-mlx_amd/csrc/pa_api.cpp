@@ -138,9 +138,9 @@ struct Plan {
   // Planned prefill: items (sequence, row block, kv-head), row blocks per sequence.
   int64_t plan_items = 0;
   int plan_rbs = 0;
-  // Planned head-128 prefill with value images: 64-key steps and maxima chunks per
-  // (sequence, kv-head) of the image region (0: no images).
-  int img_steps = 0, img_chunks = 0;
+  // Planned head-128 prefill with operand images: 64-key steps per (sequence, kv-head) of the
+  // image region (0: no images).
+  int img_steps = 0;
 };
 
 // Value images of the planned head-128 prefill: taken when every 64-key step of values is read
@@ -171,8 +171,10 @@ int device_cus() {
   return n;
 }
 
+// images: the planned head-128 prefill may use operand images (off where the workspace is
+// bounded, pa_paged_attention_static).
 Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype act, int kind,
-               int chunk, bool linear = false, int linear_cap = 0) {
+               int chunk, bool linear = false, int linear_cap = 0, bool images = true) {
   Plan pl{};
   // The LATENT layout (values = leading dims of the key rows) runs on the VALU kernel.
   if (c->value_cache == nullptr || (a->v_head_size > 0 && a->v_head_size != c->head_dim))
@@ -236,12 +238,11 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
       pl.plan_items = units;
       pl.plan_rbs = (int)rbs;
       pl.part_rows = (size_t)units * 2 * pa::kPrefillRows;
-      if (PA_PREFILL_IMAGES && c->head_dim == 128 && rbs >= kImgMinRowBlocks) {
+      if (PA_PREFILL_IMAGES && images && c->head_dim == 128 && rbs >= kImgMinRowBlocks) {
         const int64_t steps = ((int64_t)ctx + 63) / 64;
         if ((int64_t)b->batch * c->kv_heads * steps * pa::kImgStepBytes <= kImgMaxBytes &&
             steps <= 65535 && b->batch <= 65535) {
           pl.img_steps = (int)steps;
-          pl.img_chunks = (int)(((int64_t)ctx + pa::kImgChunkKeys - 1) / pa::kImgChunkKeys);
         }
       }
       return pl;
@@ -291,7 +292,7 @@ size_t part_o_bytes(const pa_cache* c, const Plan& pl) {
 
 // Workspace: [partial O | partial (m, l)].
 // Planned prefill adds [unit list (2 per item, 4 int32 each) | unit count | split flag per item].
-// Value images add [images | scales | maxima slots].
+// Operand images add [images | step value exponents].
 size_t plan_bytes(const Plan& pl) {
   return align256((size_t)pl.plan_items * 2 * 4 * sizeof(int32_t)) + 256 +
          align256((size_t)pl.plan_items * sizeof(int32_t));
@@ -299,8 +300,8 @@ size_t plan_bytes(const Plan& pl) {
 size_t image_bytes(const pa_cache* c, const pa_batch* b, const Plan& pl) {
   if (pl.img_steps == 0) return 0;
   const size_t hb = (size_t)b->batch * c->kv_heads;
-  return align256(hb * pl.img_steps * pa::kImgStepBytes) + align256(hb * 4 * sizeof(int32_t)) +
-         align256(hb * pl.img_chunks * 4 * sizeof(int32_t));
+  return align256(hb * pl.img_steps * pa::kImgStepBytes) +
+         align256(hb * pl.img_steps * sizeof(int32_t));
 }
 size_t workspace_for(const pa_cache* c, const pa_batch* b, const pa_attn*, const Plan& pl) {
   if (pl.part_rows == 0) return 0;
@@ -318,6 +319,7 @@ struct RunOpts {
   const void* bias = nullptr;
   int bias_b = 0, bias_h = 0, bias_rows = 0, bias_cols = 0;
   bool smooth_softmax = false;
+  bool images = true;  // operand images allowed (see make_plan)
 };
 
 // The kernel family a call with these options runs: a bias or per-sequence key counts (which
@@ -361,7 +363,8 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
   if (!(a->softcap >= 0.0f) || !std::isfinite(a->softcap))
     return fail(PA_ERR_INVALID_ARGUMENT, "softcap must be finite and non-negative");
   kind = effective_kind(kind, opts);
-  Plan pl = make_plan(c, b, a, act, kind, chunk, opts.linear_cap > 0, opts.linear_cap);
+  Plan pl = make_plan(c, b, a, act, kind, chunk, opts.linear_cap > 0, opts.linear_cap,
+                      opts.images);
   if (opts.linear_cap > 0 && !(pl.balanced || pl.kind == 2 || pl.kind == 3))
     return fail(PA_ERR_UNSUPPORTED,
                 "contiguous caches run on the streaming decode, prefill or VALU kernels only");
@@ -402,11 +405,8 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
       char* img = base + plan_bytes(pl) - align256((size_t)pl.plan_items * 2 * 4 * sizeof(int32_t));
       p.vimg = img;
       img += align256(hb * pl.img_steps * pa::kImgStepBytes);
-      p.vscale = reinterpret_cast<int32_t*>(img);
-      img += align256(hb * 4 * sizeof(int32_t));
-      p.vmax = reinterpret_cast<int32_t*>(img);
+      p.vstep = reinterpret_cast<int32_t*>(img);
       p.img_steps = pl.img_steps;
-      p.img_chunks = pl.img_chunks;
     }
   }
   p.num_blocks = c->num_blocks;
@@ -694,7 +694,8 @@ struct OpLayout {
   pa_attn attn;
 };
 
-int op_layout(const pa_paged_attention_node* n, const pa_paged_attention_io* io, OpLayout* L) {
+int op_layout(const pa_paged_attention_node* n, const pa_paged_attention_io* io, OpLayout* L,
+              bool images = true) {
   if (!n || !io) return fail(PA_ERR_INVALID_ARGUMENT, "node/io is NULL");
   if (n->num_heads <= 0 || n->kv_num_heads <= 0 || n->num_heads % n->kv_num_heads != 0)
     return fail(PA_ERR_INVALID_ARGUMENT, "PagedAttention: bad num_heads/kv_num_heads");
@@ -769,7 +770,9 @@ int op_layout(const pa_paged_attention_node* n, const pa_paged_attention_io* io,
   a.is_causal = n->is_causal;
   a.head_sink = io->head_sink;
   a.v_head_size = L->v_head;
-  L->total = L->attn_off + pa_attention_workspace_bytes_ex(&io->cache, &b, &a, io->dtype, 0, 0);
+  L->total = L->attn_off +
+             workspace_for(&io->cache, &b, &a,
+                           make_plan(&io->cache, &b, &a, io->dtype, 0, 0, false, 0, images));
   return PA_OK;
 }
 
@@ -903,10 +906,12 @@ size_t pa_paged_attention_workspace_bytes(const pa_paged_attention_node* node,
   return L.total;
 }
 
-int pa_paged_attention(const pa_paged_attention_node* n, const pa_paged_attention_io* io,
-                       void* workspace, size_t workspace_bytes, pa_stream_t stream) {
+// The operator entry; images: see make_plan.
+static int paged_attention_impl(const pa_paged_attention_node* n, const pa_paged_attention_io* io,
+                                void* workspace, size_t workspace_bytes, pa_stream_t stream,
+                                bool images) {
   OpLayout L;
-  int rc = op_layout(n, io, &L);
+  int rc = op_layout(n, io, &L, images);
   if (rc) return rc;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (io->host_cumulative_sequence_length && (rc = validate_host_metadata(n, io))) return rc;
@@ -938,6 +943,7 @@ int pa_paged_attention(const pa_paged_attention_node* n, const pa_paged_attentio
     x.copy_rows = true;
   }
   RunOpts opts;
+  opts.images = images;
   const bool distinct = io->slot_mapping == nullptr &&
                         io->host_cumulative_sequence_length != nullptr && host_slots_distinct(io);
   if (distinct) L.batch.flags |= PA_BATCH_SLOTS_DISTINCT;
@@ -955,6 +961,11 @@ int pa_paged_attention(const pa_paged_attention_node* n, const pa_paged_attentio
                      ws + L.attn_off, workspace_bytes - L.attn_off, 0, 0, s, opts);
   if (rc) return rc;
   return copy_cache_outputs(io, s);
+}
+
+int pa_paged_attention(const pa_paged_attention_node* n, const pa_paged_attention_io* io,
+                       void* workspace, size_t workspace_bytes, pa_stream_t stream) {
+  return paged_attention_impl(n, io, workspace, workspace_bytes, stream, true);
 }
 
 // ------------------------------------------------------------------------------ no-alloc entry
@@ -994,6 +1005,12 @@ int pa_paged_attention_static(const pa_paged_attention_node* n, const pa_paged_a
   OpLayout L;
   int rc = op_layout(n, io, &L);
   if (rc) return rc;
+  // A planned prefill whose operand images do not fit the scratch runs without them.
+  bool images = true;
+  if (L.total > PA_STATIC_SCRATCH_BYTES) {
+    images = false;
+    if ((rc = op_layout(n, io, &L, false))) return rc;
+  }
   if (L.total > PA_STATIC_SCRATCH_BYTES)
     return fail(PA_ERR_UNSUPPORTED,
                 "pa_paged_attention_static: the call needs %zu bytes of workspace, more than the "
@@ -1001,7 +1018,7 @@ int pa_paged_attention_static(const pa_paged_attention_node* n, const pa_paged_a
                 L.total, (size_t)PA_STATIC_SCRATCH_BYTES);
   void* ws = nullptr;
   if ((rc = static_scratch(&ws))) return rc;
-  return pa_paged_attention(n, io, ws, PA_STATIC_SCRATCH_BYTES, stream);
+  return paged_attention_impl(n, io, ws, PA_STATIC_SCRATCH_BYTES, stream, images);
 }
 
 // ------------------------------------------------------------------------------ GQA

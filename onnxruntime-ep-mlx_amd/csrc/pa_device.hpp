@@ -347,23 +347,18 @@ struct AttnParams {
   int32_t* plan_info;
   int32_t* plan_split;
   // Operand images of the planned head-128 prefill (vimg != NULL): for every 64-key step of
-  // (sequence b, kv-head kh), the key rows gathered and the value rows converted to fp16,
-  // both laid out as the prefill kernel's LDS operands, at
-  // vimg + ((b * kv_heads + kh) * img_steps + step) * kImgStepBytes;
-  // vscale[(b * kv_heads + kh) * 4 + q] is the power-of-two exponent s of 32-dim quarter q of the
-  // values (image element = value * 2^-s); vmax[((b * kv_heads + kh) * img_chunks + c) * 4 + q]
-  // the largest biased exponent of |value| in quarter q over keys [kImgChunkKeys * c, + kImgChunkKeys).
+  // (sequence b, kv-head kh), the key rows gathered and the value rows converted to fp16, both
+  // laid out as the prefill kernel's LDS operands, at
+  // vimg + ((b * kv_heads + kh) * img_steps + step) * kImgStepBytes; vstep[same index] is the
+  // step's power-of-two value exponent s (image element = value * 2^-s).
   char* vimg;
-  int32_t* vscale;
-  int32_t* vmax;
-  int32_t img_steps, img_chunks;
-  int32_t plan_vmax_groups;  // workgroups of the plan launch that run the value maxima pass
+  int32_t* vstep;
+  int32_t img_steps;
 };
 
 // Image geometry of the planned head-128 prefill: 64 keys x 128 dims of 16-bit keys and values
-// per step, the maxima pass covers kImgChunkKeys keys per workgroup.
+// per step.
 constexpr int kImgStepBytes = 2 * 64 * 128 * 2;
-constexpr int kImgChunkKeys = 512;
 
 // Final normalisation shared by every attention kernel: the factor that turns an output
 // accumulated relative to running max m (log2 units) with running sum l into the result,

@@ -418,6 +418,18 @@ __device__ __forceinline__ float other_half(float x) {
   return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
 }
 
+// Largest step below the accumulator's exponent that the planned prefill's images take through
+// the probabilities (scaled by at most 2^-kImgPShift, so probabilities down to 2^(kImgPShift - 14)
+// of the lazy maximum stay fp16-normal).
+constexpr int kImgPShift = 4;
+
+// Maximum of a float over the wavefront (butterfly).
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
 // Maximum of a non-negative value over the wavefront (DPP row steps, then the row broadcasts).
 __device__ __forceinline__ int wave_max_nonneg(int v) {
   v = max(v, __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
@@ -591,9 +603,6 @@ __device__ __forceinline__ void img_issue(MxBuf& buf, int wave, int lane, int t0
     __builtin_amdgcn_global_load_lds(src + 1024 * i, (lds_ptr_t)(dst + 1024 * i), 16, 0, 0);
 }
 
-#ifndef PA_MX_SGB
-#define PA_MX_SGB 0
-#endif
 
 // IMG: value operands from the per-(sequence, kv-head) value images (AttnParams::vimg), staged
 // by direct LDS loads one step ahead; otherwise loaded, converted and regrouped in the loop.
@@ -701,32 +710,16 @@ prefill_mx_kernel(const AttnParams p) {
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) sc[kb][i] = 0.0f;
-#if PA_MX_SGB
-    // operands of k-step ks + PA_MX_SGB read while the products of k-step ks run
-    u32x4 ka[8][2];
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) ka[ks][kb] = buf.k[kb][ks][lane];
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) sc[kb] = mfma32<TT>(ka[ks][kb], qv[ks], sc[kb]);
-    __builtin_amdgcn_sched_group_barrier(0x100, 2 * PA_MX_SGB, 0);
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      if (ks + PA_MX_SGB < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-    }
-#else
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) sc[kb] = mfma32<TT>(buf.k[kb][ks][lane], qv[ks], sc[kb]);
-#endif
   };
   // Online softmax of the step at t0 over its scores, then O += P . V from buffer `buf`.
-  auto attend = [&](const f32x16(&sc)[2], int t0, const MxBuf& buf) __attribute__((always_inline)) {
+  // IMG: the accumulator's value exponent (output in units of 2^s_acc; no step seen yet: far below
+  // any step's) -- each step's image holds its values in units of 2^sj.
+  int s_acc = -(1 << 29);
+  auto attend = [&](const f32x16(&sc)[2], int t0, const MxBuf& buf, int sj) __attribute__((always_inline)) {
     float x[2][16];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -777,7 +770,47 @@ prefill_mx_kernel(const AttnParams p) {
           sv[nt] = vsn[nt];
         }
     }
-    const float msafe = (m_run == kNegInf) ? 0.0f : m_run;
+    // IMG: bring the step's values and the accumulator to one exponent.  A step up to
+    // kImgPShift below the accumulator enters through its probabilities, scaled by 2^-dsh (exact:
+    // an offset in the exponent, and row sums weigh the fp16 probabilities by 2^dsh); otherwise
+    // the accumulator moves to the step's exponent by an exact power of two -- upwards only while
+    // that cannot overflow, which a step 2^-100 below output values that large could need: such a
+    // step's values are negligible against the output and count in the row sums only.
+    int dsh = 0;
+    bool pv_on = true;
+    if constexpr (IMG) {
+      int d = __builtin_amdgcn_readfirstlane(s_acc - sj);
+      bool up_ok = true;
+      if (d > 84) {  // moving up by 2^d: only if the largest |output| stays below 2^120
+        float om = 0.0f;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) om = fmaxf(om, fabsf(o[nt][i]));
+        om = wave_max_f(om);
+        up_ok = __builtin_amdgcn_readfirstlane(__builtin_ldexpf(om, min(d, 300)) <= 0x1p120f ? 1 : 0);
+      }
+      if (d < 0 || (d > kImgPShift && up_ok)) {
+        const float f = __builtin_ldexpf(1.0f, d);
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) o[nt] *= f;
+        s_acc = sj;
+        d = 0;
+      }
+      pv_on = d <= kImgPShift;
+      dsh = pv_on ? d : 0;
+    }
+    if (IMG && !pv_on) {
+      const float m0 = (m_run == kNegInf) ? 0.0f : m_run;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          l_part += __builtin_amdgcn_exp2f(CAP ? x[kb][i] - m0 : __builtin_fmaf(x[kb][i], scale_log2, -m0));
+      return;
+    }
+    const float msafe = ((m_run == kNegInf) ? 0.0f : m_run) + (float)dsh;
+    const _Float16 lw = (_Float16)(float)(1 << dsh);
     u32x4 pb[4];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -795,7 +828,7 @@ prefill_mx_kernel(const AttnParams p) {
               f32x2v{pv[8 * half + 2 * m], pv[8 * half + 2 * m + 1]}, f16x2v);
           pb[2 * kb + half][m] = __builtin_bit_cast(uint32_t, ph);
           // the row sum adds the fp16 probabilities the P.V product takes
-          l_part = __builtin_amdgcn_fdot2(ph, f16x2v{(_Float16)1.0f, (_Float16)1.0f}, l_part, false);
+          l_part = __builtin_amdgcn_fdot2(ph, f16x2v{lw, lw}, l_part, false);
         }
     }
 #pragma unroll
@@ -810,28 +843,35 @@ prefill_mx_kernel(const AttnParams p) {
   if constexpr (IMG) {
     const int64_t hb = (int64_t)b * p.kv_heads + kh;
     const char* img_hb = p.vimg + hb * p.img_steps * (int64_t)kImgStepBytes;
-    // the image scales of this (sequence, kv-head): fixed for the whole key range
-    const int4 s4 = *reinterpret_cast<const int4*>(p.vscale + hb * 4);
-    sv[0] = __builtin_amdgcn_readfirstlane(s4.x);
-    sv[1] = __builtin_amdgcn_readfirstlane(s4.y);
-    sv[2] = __builtin_amdgcn_readfirstlane(s4.z);
-    sv[3] = __builtin_amdgcn_readfirstlane(s4.w);
+    const int32_t* vstep_hb = p.vstep + hb * p.img_steps;
     // Direct LDS loads of step k + 1 into the other buffer while step k computes (every
     // wavefront finished reading that buffer before the barrier that ended iteration k - 1).
-    if (nsteps > 0) img_issue(lds[0], wave, lane, t_first, img_hb);
+    // The value exponent of step k + 1 is loaded with its operands, at the start of iteration k,
+    // so its latency hides under the step's compute like theirs.
+    int sj = 0, sj_next = 0;
+    if (nsteps > 0) {
+      img_issue(lds[0], wave, lane, t_first, img_hb);
+      sj_next = vstep_hb[t_first / kMxKeys];
+    }
     wait_vmem();
     __syncthreads();
     for (int k = 0; k < nsteps; ++k) {
       const int t0 = t_first + kMxKeys * k;
-      if (k + 1 < nsteps) img_issue(lds[(k + 1) & 1], wave, lane, t0 + kMxKeys, img_hb);
+      sj = __builtin_amdgcn_readfirstlane(sj_next);
+      if (k + 1 < nsteps) {
+        img_issue(lds[(k + 1) & 1], wave, lane, t0 + kMxKeys, img_hb);
+        sj_next = vstep_hb[t0 / kMxKeys + 1];
+      }
       if (seen(t0)) {
         f32x16 sc[2];
         scores(lds[k & 1], sc);
-        attend(sc, t0, lds[k & 1]);
+        attend(sc, t0, lds[k & 1], sj);
       }
       wait_vmem();
       __syncthreads();
     }
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) sv[nt] = s_acc;
   } else {
     PageWindow pw;
     window_at(pw, w, min(div_bs(t_first, w), w.max_blocks - 1), lane);
@@ -848,7 +888,7 @@ prefill_mx_kernel(const AttnParams p) {
       if (seen(t0)) {
         f32x16 sc[2];
         scores(lds[k & 1], sc);
-        attend(sc, t0, lds[k & 1]);
+        attend(sc, t0, lds[k & 1], 0);
       }
       if (k + 1 < nsteps) mx_store<TT>(lds[(k + 1) & 1], st, wave, lane, t0 + kMxKeys, total, s_stage);
       if (k + 2 < nsteps) mx_load<TT>(w, pw, wave, lane, t0 + 2 * kMxKeys, st);
@@ -971,141 +1011,85 @@ __device__ __forceinline__ ItemKeys item_keys(const AttnParams& p, int i) {
 // (LDS histogram, descending); the order inside a bucket is whatever the atomics give, which
 // changes nothing in the results (every unit writes its own rows or partial).
 //
-// With operand images, workgroups 1.. of the same launch run the value maxima pass (vmax_chunk,
-// bf16 values) and write the key half of the images (key_image), neither of which needs anything
-// from the plan: they cost no launch of their own and run on other CUs while workgroup 0 plans.
-template <int NT>
-__device__ __forceinline__ void vmax_chunk(const AttnParams& p, int id) {
-  constexpr int D = 128;
-  static_assert(NT % 64 == 0 && NT >= 64, "whole wavefronts");
-  const int c = id % p.img_chunks;
-  const int kh = (id / p.img_chunks) % p.kv_heads;
-  const int b = id / (p.img_chunks * p.kv_heads);
-  if (b >= p.batch) return;
-  const int s0 = min(max(p.cum[b], 0), p.num_tokens);
-  const int s1 = min(max(p.cum[b + 1], s0), p.num_tokens);
-  const int pastb = clamped_past(p, b, s1 - s0);
-  const int total = pastb + (s1 - s0);
-  const WaveInfo w = make_wave(p, D, b, kh, s0, pastb, total);
-  __shared__ int qmax[4];
-  const int tid = threadIdx.x;
-  if (tid < 4) qmax[tid] = 0;
-  // thread: 16-byte piece tid % 16 of the 256-byte value slice (quarter (tid % 16) / 4) of every
-  // (NT / 16)-th row of the chunk
-  constexpr int RPT = kImgChunkKeys / (NT / 16);  // rows per thread
-  u32x4 x[RPT];
-#pragma unroll
-  for (int i = 0; i < RPT; ++i) {
-    const int pos = c * kImgChunkKeys + (tid >> 4) + (NT / 16) * i;
-    x[i] = pos < total ? ld16(row_ptr(w, pos, true, D) + 16 * (tid & 15)) : u32x4{0u, 0u, 0u, 0u};
-  }
-  uint32_t mx = 0;
-#pragma unroll
-  for (int i = 0; i < RPT; ++i)
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-      mx = __builtin_bit_cast(uint32_t,
-                              __builtin_elementwise_max(__builtin_bit_cast(u16x2, mx),
-                                                        __builtin_bit_cast(u16x2, x[i][m] & 0x7fff7fffu)));
-  int e = (int)(max(mx & 0xffffu, mx >> 16) >> 7);
-  // lanes that differ in bits 0, 1, 4, 5 hold the same quarter
-  e = max(e, __shfl_xor(e, 1, 64));
-  e = max(e, __shfl_xor(e, 2, 64));
-  e = max(e, __shfl_xor(e, 16, 64));
-  e = max(e, __shfl_xor(e, 32, 64));
-  __syncthreads();
-  if ((tid & 63) < 16 && (tid & 3) == 0) atomicMax(&qmax[(tid & 15) >> 2], e);
-  __syncthreads();
-  if (tid < 4) p.vmax[(((int64_t)b * p.kv_heads + kh) * p.img_chunks + c) * 4 + tid] = qmax[tid];
-}
-
-// Key half of the operand images: NT / 256 consecutive 64-key steps of (sequence b, kv-head kh)
-// per workgroup of the plan launch (they need nothing from the plan or the value maxima).  Thread:
-// key row (t % 256) / 4 of step t / 256, bytes 64 (t % 4) .. + 63 of the row slice, whose 16-byte
-// chunk dc = 4 (t % 4) + i goes to item (kb = row / 32, ks = dc / 2), lane 32 (dc % 2) + row % 32;
-// rows at or past the sequence end are zero.
-template <int NT>
-__device__ __forceinline__ void key_image(const AttnParams& p, int id) {
-  constexpr int D = 128, SPW = NT / 256;
-  const int nj = (p.img_steps + SPW - 1) / SPW;
-  const int jb = id % nj, kh = (id / nj) % p.kv_heads, b = id / (nj * p.kv_heads);
-  if (b >= p.batch) return;
-  const int s0 = min(max(p.cum[b], 0), p.num_tokens);
-  const int s1 = min(max(p.cum[b + 1], s0), p.num_tokens);
-  const int pastb = clamped_past(p, b, s1 - s0);
-  const int total = pastb + (s1 - s0);
-  const int tid = threadIdx.x;
-  const int j = jb * SPW + tid / 256;
-  if (s1 == s0 || j >= p.img_steps || j * kMxKeys >= total) return;
-  const WaveInfo w = make_wave(p, D, b, kh, s0, pastb, total);
-  const int r = (tid & 255) >> 2, q = tid & 3;
-  const int pos = j * kMxKeys + r;
-  const bool live = pos < total;
-  const char* src = live ? row_ptr(w, pos, false, D) + 64 * q : nullptr;
-  u32x4 kx[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) kx[i] = live ? ld16(src + 16 * i) : u32x4{0u, 0u, 0u, 0u};
-  char* dst = p.vimg + (((int64_t)b * p.kv_heads + kh) * p.img_steps + j) * (int64_t)kImgStepBytes;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int dc = 4 * q + i;
-    *reinterpret_cast<u32x4*>(dst + ((((r >> 5) * 8 + (dc >> 1)) * 64) + 32 * (dc & 1) + (r & 31)) * 16) =
-        kx[i];
-  }
-}
+// With operand images, workgroups 1.. of the same launch write the images (image_steps), which
+// need nothing from the plan: they cost no launch of their own and run on other CUs while
+// workgroup 0 plans.
 
 // Operand images (AttnParams::vimg): each 64-key step of (sequence, kv-head) holds the step's LDS
 // operand buffer of prefill_mx_kernel byte for byte, so the kernel's staging is a plain copy:
-//   keys (16 KiB, written by key_image in the plan launch): item (kb, ks), lane l holds bytes
-//   32 ks + 16 (l / 32) .. + 15 of the row slice of key 32 kb + l % 32;
-//   values (16 KiB, this kernel, one workgroup per (step, kv-head, sequence)): the rows (zero at or
-//   past the end) converted to fp16 under the (sequence, kv-head)'s quarter scales 2^-s -- bf16
-//   values: s from the maxima pass, so the quarter's largest value lies in [2^14, 2^15) of fp16
-//   (exact conversion; values below 2^-29 of it lose bits in the fp16 subnormal range); fp16
-//   values: s = 0 -- and regrouped through LDS into the P.V A-operand layout: item (t, nt), lane l
-//   holds dim 32 nt + l % 32 of keys 16 t + 4 h + e and then 16 t + 8 + 4 h + e (e < 4, h = l / 32).
-// Workgroup 0 of a (sequence, kv-head) also stores the scales for the prefill kernel.
-template <typename TT>
-__global__ __launch_bounds__(256) void prefill_image_kernel(const AttnParams p) {
-  constexpr int D = 128;
-  const int j = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+//   keys (16 KiB): item (kb, ks), lane l holds bytes 32 ks + 16 (l / 32) .. + 15 of the row slice
+//   of key 32 kb + l % 32 -- the rows gathered from the pages (or the caller's new rows);
+//   values (16 KiB): the rows converted to fp16 under the step's scale 2^-s -- bf16 values: s puts
+//   the step's largest |value| into [2^14, 2^15) of fp16 (exact conversion; values below 2^-29 of
+//   it lose bits in the fp16 subnormal range); fp16 values: s = 0 -- regrouped through LDS into
+//   the P.V A-operand layout: item (t, nt), lane l holds dim 32 nt + l % 32 of keys 16 t + 4 h + e
+//   and then 16 t + 8 + 4 h + e (e < 4, h = l / 32).
+// Rows at or past the sequence end are zero.  NT / 256 consecutive steps per workgroup, 256
+// threads each: thread (row r = (t % 256) / 4, q = t % 4) moves bytes 64 q .. 64 q + 63 of key and
+// value row r; key chunk dc = 4 q + i goes to item (kb = r / 32, ks = dc / 2), lane
+// 32 (dc % 2) + r % 32.  The step's exponent goes to vstep.
+template <typename TT, int NT>
+__device__ __forceinline__ void image_steps(const AttnParams& p, int id) {
+  constexpr int D = 128, SPW = NT / 256;
+  __shared__ uint32_t rows[SPW][kMxKeys][D / 2 + 1];  // fp16 value rows, one word = two dims
+  __shared__ int emax[SPW];
+  const int nj = (p.img_steps + SPW - 1) / SPW;
+  const int jb = id % nj, kh = (id / nj) % p.kv_heads, b = id / (nj * p.kv_heads);
+  if (b >= p.batch) return;  // whole workgroup
   const int s0 = min(max(p.cum[b], 0), p.num_tokens);
   const int s1 = min(max(p.cum[b + 1], s0), p.num_tokens);
   const int pastb = clamped_past(p, b, s1 - s0);
   const int total = pastb + (s1 - s0);
-  if (j * kMxKeys >= total || s1 == s0) return;
-  const int64_t hb = (int64_t)b * p.kv_heads + kh;
+  const int tid = threadIdx.x, grp = tid / 256;
+  const int j = jb * SPW + grp;
+  const bool step_live = s1 > s0 && j < p.img_steps && j * kMxKeys < total;
   const WaveInfo w = make_wave(p, D, b, kh, s0, pastb, total);
-  __shared__ int qs[4];
-  __shared__ uint32_t rows[kMxKeys][D / 2 + 1];  // fp16 value rows, one word = two dims
-  const int tid = threadIdx.x;
-  if (tid < 4) {
-    int s = 0;
-    if constexpr (std::is_same<TT, TBF16>::value) {
-      int emax = 0;
-      for (int c = 0; c < p.img_chunks; ++c)
-        emax = max(emax, p.vmax[(hb * p.img_chunks + c) * 4 + tid]);
-      s = max(emax - 141, -112);
-    }
-    qs[tid] = s;
-    if (j == 0) p.vscale[hb * 4 + tid] = s;
-  }
-  // row slices: thread -> key row tid / 4, bytes 64 (tid % 4) .. + 63 (dims 32 q .. 32 q + 31)
-  const int r = tid >> 2, q = tid & 3;
+  const int r = (tid & 255) >> 2, q = tid & 3;
   const int pos = j * kMxKeys + r;
-  const bool live = pos < total;
-  u32x4 vx[4];
+  const bool live = step_live && pos < total;
+  if (tid < SPW) emax[tid] = 0;
+  u32x4 kx[4], vx[4];
   {
+    const char* ks = live ? row_ptr(w, pos, false, D) + 64 * q : nullptr;
     const char* vs = live ? row_ptr(w, pos, true, D) + 64 * q : nullptr;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) vx[i] = live ? ld16(vs + 16 * i) : u32x4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < 4; ++i) {
+      kx[i] = live ? ld16(ks + 16 * i) : u32x4{0u, 0u, 0u, 0u};
+      vx[i] = live ? ld16(vs + 16 * i) : u32x4{0u, 0u, 0u, 0u};
+    }
   }
+  const int64_t hb = (int64_t)b * p.kv_heads + kh;
   char* dst = p.vimg + (hb * p.img_steps + j) * (int64_t)kImgStepBytes;
-  __syncthreads();
+  if (step_live) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int dc = 4 * q + i;
+      *reinterpret_cast<u32x4*>(dst + ((((r >> 5) * 8 + (dc >> 1)) * 64) + 32 * (dc & 1) + (r & 31)) * 16) =
+          kx[i];
+    }
+  }
+  // the step's largest biased exponent of |value| (bf16; every wavefront of a group, then LDS)
+  int e = 0;
   if constexpr (std::is_same<TT, TBF16>::value) {
+    uint32_t mx = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        mx = __builtin_bit_cast(uint32_t,
+                                __builtin_elementwise_max(__builtin_bit_cast(u16x2, mx),
+                                                          __builtin_bit_cast(u16x2, vx[i][m] & 0x7fff7fffu)));
+    e = wave_max_nonneg((int)(max(mx & 0xffffu, mx >> 16) >> 7));
+  }
+  __syncthreads();
+  if ((tid & 63) == 0) atomicMax(&emax[grp], e);
+  __syncthreads();
+  // bf16: s = emax - 141 puts the largest value into [2^14, 2^15) of fp16; fp16: s = 0
+  const int sc = std::is_same<TT, TBF16>::value ? max(emax[grp] - 141, -112) : 0;
+  if (std::is_same<TT, TBF16>::value) {
     // bf16 exponent E -> fp16 exponent E - 112 - s: subtract (112 + s) << 7 from the magnitude
     // bits (saturating: values below the fp16 range flush towards zero), shift into place
-    const unsigned short bias = (unsigned short)((112 + qs[q]) << 7);
+    const unsigned short bias = (unsigned short)((112 + sc) << 7);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -1119,20 +1103,22 @@ __global__ __launch_bounds__(256) void prefill_image_kernel(const AttnParams p) 
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int m = 0; m < 4; ++m) rows[r][16 * q + 4 * i + m] = vx[i][m];
+    for (int m = 0; m < 4; ++m) rows[grp][r][16 * q + 4 * i + m] = vx[i][m];
   __syncthreads();
+  if (!step_live) return;
+  if ((tid & 255) == 0) p.vstep[hb * p.img_steps + j] = sc;
   // value regroup: task (t, h, nt, dim pair dp) -> slots of lanes 32 h + 2 dp (+1) of item (t, nt)
   char* vdst = dst + kImgStepBytes / 2;
 #pragma unroll
   for (int rep = 0; rep < 2; ++rep) {
-    const int task = tid + 256 * rep;
+    const int task = (tid & 255) + 256 * rep;
     const int dp = task & 15, h = (task >> 4) & 1, nt = (task >> 5) & 3, t = task >> 7;
     u32x4 lo, hi;
 #pragma unroll
     for (int e2 = 0; e2 < 4; ++e2) {
       // elements 2 e2, 2 e2 + 1: keys 16 t + 4 h + (e & 3) + 8 (e >> 2)
       const int ka = 16 * t + 4 * h + ((2 * e2) & 3) + 8 * ((2 * e2) >> 2);
-      const uint32_t wa = rows[ka][16 * nt + dp], wb = rows[ka + 1][16 * nt + dp];
+      const uint32_t wa = rows[grp][ka][16 * nt + dp], wb = rows[grp][ka + 1][16 * nt + dp];
       lo[e2] = __builtin_amdgcn_perm(wb, wa, 0x05040100u);
       hi[e2] = __builtin_amdgcn_perm(wb, wa, 0x07060302u);
     }
@@ -1142,16 +1128,13 @@ __global__ __launch_bounds__(256) void prefill_image_kernel(const AttnParams p) 
   }
 }
 
-template <int NT>
+template <int NT, typename TT, bool IMG>
 __global__ __launch_bounds__(NT) void prefill_plan_kernel(const AttnParams p) {
-  if (blockIdx.x > 0) {
-    const int id = (int)blockIdx.x - 1;
-    const int nmax = p.plan_vmax_groups;
-    if (id < nmax)
-      vmax_chunk<NT>(p, id);
-    else
-      key_image<NT>(p, id - nmax);
-    return;
+  if constexpr (IMG) {
+    if (blockIdx.x > 0) {
+      image_steps<TT, NT>(p, (int)blockIdx.x - 1);
+      return;
+    }
   }
   constexpr int NB = 1024;  // buckets of 32-key steps (the last one holds everything longer)
   __shared__ int hist[NB];
@@ -1374,30 +1357,25 @@ hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype ca
       !p.plan_split || !p.part_o || !p.part_ml || p.max_splits != 1)
     return hipErrorInvalidValue;
   if ((int64_t)p.plan_items * (kPrefillRows / kPrefillMergeRows) > INT32_MAX) return hipErrorInvalidValue;
-  // Operand images (head 128): the value maxima pass rides in the plan launch (bf16 values
-  // only), then one workgroup per (64-key step, kv-head, sequence) writes the images.
-  const bool img = p.vimg != nullptr;
-  if (img && (p.head_dim != 128 || !p.vscale || !p.vmax || p.img_steps <= 0 || p.img_chunks <= 0 ||
-              p.img_steps > 65535 || p.kv_heads > 65535 || p.batch > 65535))
-    return hipErrorInvalidValue;
+  // Operand images (head 128): written by workgroups 1.. of the plan launch.
   constexpr int kPlanThreads = 1024;
-  const int64_t nmax = img && act == PA_DTYPE_BFLOAT16
-                           ? (int64_t)p.batch * p.kv_heads * p.img_chunks : 0;
-  const int64_t nkey = img ? (int64_t)p.batch * p.kv_heads *
+  const bool img = p.vimg != nullptr;
+  if (img && (p.head_dim != 128 || !p.vstep || p.img_steps <= 0))
+    return hipErrorInvalidValue;
+  const int64_t nimg = img ? (int64_t)p.batch * p.kv_heads *
                                  ((p.img_steps + kPlanThreads / 256 - 1) / (kPlanThreads / 256))
                            : 0;
-  if (nmax + nkey + 1 > INT32_MAX) return hipErrorInvalidValue;
-  AttnParams pp = p;
-  pp.plan_vmax_groups = (int32_t)nmax;
-  hipLaunchKernelGGL((prefill_plan_kernel<kPlanThreads>), dim3((unsigned)(1 + nmax + nkey)),
-                     dim3(kPlanThreads), 0, s, pp);
-  if (img) {
-    const dim3 ig(p.img_steps, p.kv_heads, p.batch);
-    if (act == PA_DTYPE_FLOAT16)
-      hipLaunchKernelGGL((prefill_image_kernel<TF16>), ig, dim3(256), 0, s, p);
-    else
-      hipLaunchKernelGGL((prefill_image_kernel<TBF16>), ig, dim3(256), 0, s, p);
-  }
+  if (nimg + 1 > INT32_MAX) return hipErrorInvalidValue;
+  const dim3 pg((unsigned)(1 + nimg));
+  if (!img)
+    hipLaunchKernelGGL((prefill_plan_kernel<kPlanThreads, TBF16, false>), pg, dim3(kPlanThreads), 0,
+                       s, p);
+  else if (act == PA_DTYPE_FLOAT16)
+    hipLaunchKernelGGL((prefill_plan_kernel<kPlanThreads, TF16, true>), pg, dim3(kPlanThreads), 0,
+                       s, p);
+  else
+    hipLaunchKernelGGL((prefill_plan_kernel<kPlanThreads, TBF16, true>), pg, dim3(kPlanThreads), 0,
+                       s, p);
   const dim3 grid(2 * p.plan_items, 1);
   hipError_t e = act == PA_DTYPE_FLOAT16 ? launch_t<TF16>(p, grid, s) : launch_t<TBF16>(p, grid, s);
   if (e != hipSuccess) return e;

@@ -3,9 +3,12 @@ static scratch) against pa_paged_attention with a caller workspace, through the 
 
 Two calls in a row on the same scratch, the second with a smaller input: a planned prefill
 (unit list, split flags and fp16 partials in the scratch) and then a small decode batch (balanced
-split-K partials), plus a decode followed by an even smaller one.  Outputs and caches must be
-bit-identical to the caller-workspace entry's, which runs the same kernels.  A call whose
-workspace exceeds the scratch is rejected on the host before any device work.
+split-K partials), plus a decode followed by an even smaller one.  Caches must be bit-identical to
+the caller-workspace entry's; so must the decode outputs, which run the same kernels.  The
+prefill's operand images (about 55 MB here) do not fit beside its partials in the scratch, so the
+static entry runs that planned prefill with the in-loop value conversion: its output must agree
+with the caller-workspace entry's within the parity bar (rel-L2 <= 2e-3).  A call whose workspace
+exceeds the scratch even so is rejected on the host before any device work.
 """
 from __future__ import annotations
 
@@ -42,8 +45,14 @@ def _decode_case(B, seed):
 def _same(case):
     a = run_gpu_op(case)
     b = run_gpu_op(case, static_scratch=True)
-    for x, y, what in zip(a, b, ("output", "key cache", "value cache")):
+    for x, y, what in zip(a[1:], b[1:], ("key cache", "value cache")):
         assert np.array_equal(x, y), what
+    dt = case["dtype"]
+    if int(case["cum"][-1]) <= 64:
+        assert np.array_equal(a[0], b[0]), "output"
+    else:  # planned prefill: without operand images in the scratch
+        err = orc.rel_l2(orc.decode(b[0], dt), orc.decode(a[0], dt))
+        assert err <= 2e-3, err
     if int(case["cum"][-1]) <= 64:  # decode batches: the oracle too (the prefill one is slow)
         ref, ref_t, _, _ = orc.paged_attention_op(case)
         err = orc.rel_l2(orc.decode(b[0], case["dtype"]), orc.decode(ref_t, case["dtype"]))
@@ -78,4 +87,9 @@ def test_static_entry_rejects_workspace_beyond_scratch():
     rc = lib.pa_paged_attention_static(C.byref(node), C.byref(io), None)
     assert rc == capi.PA_ERR_UNSUPPORTED
     msg = lib.pa_last_error().decode()
-    assert "static scratch" in msg and str(need) in msg, msg
+    assert "static scratch" in msg, msg
+    # the reported need is the call's without operand images (at most the full need), still
+    # beyond the scratch
+    import re
+    got = int(re.search(r"needs (\d+) bytes", msg).group(1))
+    assert capi.PA_STATIC_SCRATCH_BYTES < got <= need, msg
