@@ -149,6 +149,9 @@ struct Plan {
 #ifndef PA_PREFILL_IMAGES
 #define PA_PREFILL_IMAGES 1
 #endif
+#ifndef PA_IMG_WAVES
+#define PA_IMG_WAVES 2
+#endif
 constexpr int64_t kImgMinRowBlocks = 4;
 constexpr int64_t kImgMaxBytes = (int64_t)1 << 31;
 
@@ -239,7 +242,7 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
       pl.plan_rbs = (int)rbs;
       pl.part_rows = (size_t)units * 2 * pa::kPrefillRows;
       if (PA_PREFILL_IMAGES && images && c->head_dim == 128 && rbs >= kImgMinRowBlocks) {
-        const int64_t steps = ((int64_t)ctx + 63) / 64;
+        const int64_t steps = ((int64_t)ctx + pa::kImgKeys - 1) / pa::kImgKeys;
         if ((int64_t)b->batch * c->kv_heads * steps * pa::kImgStepBytes <= kImgMaxBytes &&
             steps <= 65535 && b->batch <= 65535) {
           pl.img_steps = (int)steps;
@@ -398,8 +401,9 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
     p.plan_split = reinterpret_cast<int32_t*>(base + 256);
     p.plan_items = (int32_t)pl.plan_items;
     p.plan_rbs = pl.plan_rbs;
-    p.plan_slots = 2 * device_cus();
-    p.plan_step = pa::prefill_key_step(c->head_dim);
+    // workgroups resident per CU: two, three for the 32-key image kernel (148 VGPRs, 33 KB LDS)
+    p.plan_slots = (pl.img_steps > 0 && pa::kImgKeys == 32 ? PA_IMG_WAVES : 2) * device_cus();
+    p.plan_step = pl.img_steps > 0 ? pa::kImgKeys : pa::prefill_key_step(c->head_dim);
     if (pl.img_steps > 0) {
       const size_t hb = (size_t)b->batch * c->kv_heads;
       char* img = base + plan_bytes(pl) - align256((size_t)pl.plan_items * 2 * 4 * sizeof(int32_t));

@@ -356,9 +356,14 @@ struct AttnParams {
   int32_t img_steps;
 };
 
-// Image geometry of the planned head-128 prefill: 64 keys x 128 dims of 16-bit keys and values
-// per step.
-constexpr int kImgStepBytes = 2 * 64 * 128 * 2;
+// Image geometry of the planned head-128 prefill: kImgKeys keys x 128 dims of 16-bit keys and
+// values per step (the prefill kernel's key step over images: 32 or 64).
+#ifndef PA_IMG_KEYS
+#define PA_IMG_KEYS 64
+#endif
+constexpr int kImgKeys = PA_IMG_KEYS;
+static_assert(kImgKeys == 32 || kImgKeys == 64, "image steps of one or two 32-key blocks");
+constexpr int kImgStepBytes = 2 * kImgKeys * 128 * 2;
 
 // Final normalisation shared by every attention kernel: the factor that turns an output
 // accumulated relative to running max m (log2 units) with running sum l into the result,

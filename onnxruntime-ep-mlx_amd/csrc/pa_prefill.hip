@@ -441,7 +441,7 @@ __device__ __forceinline__ int wave_max_nonneg(int v) {
   return __builtin_amdgcn_readlane(v, 63);
 }
 
-// One LDS buffer: the operand images of a 64-key step.
+// One LDS buffer: the operand images of a step of 32 KB keys (KB = 2 for the in-loop staging).
 //   k[kb][ks][lane]: key 32 kb + lane % 32, dims 16 ks + 8 (lane / 32) .. + 7 (score A operand)
 //   v[t][nt][slot]:  slot mx_vslot(lane) holds dim 32 nt + lane % 32, keys
 //                    16 t + {4 h + e, 8 + 4 h + e}, h = lane / 32 (output A operand, fp16)
@@ -449,12 +449,14 @@ __device__ __forceinline__ int wave_max_nonneg(int v) {
 // Every staging write and every operand read touches 16 distinct 16-byte bank groups per
 // 16 lanes (the value slots are XOR-swizzled for the staging writes; mx_vslot keeps the reads a
 // permutation of the image).
-struct MxBuf {
-  u32x4 k[2][8][64];
-  u32x4 v[4][4][64];
+template <int KB>
+struct MxBufT {
+  u32x4 k[KB][8][64];
+  u32x4 v[2 * KB][4][64];
   int vs[4];
   int pad[12];
 };
+using MxBuf = MxBufT<2>;
 
 __device__ __forceinline__ int mx_vslot(int lane) { return lane ^ ((lane >> 4) & 3); }
 
@@ -592,26 +594,35 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70)
 
 // Image staging: this wavefront's quarter of the step at t0 goes straight from the step's
 // operand image (AttnParams::vimg, the LDS buffer image byte for byte) to LDS buffer `buf`:
-// 8 direct LDS loads of 1 KiB items, 16 bytes per lane, no register round trip.
-__device__ __forceinline__ void img_issue(MxBuf& buf, int wave, int lane, int t0,
+// direct LDS loads of 1 KiB items (4 KB per wavefront), 16 bytes per lane, no register round trip.
+template <int KB>
+__device__ __forceinline__ void img_issue(MxBufT<KB>& buf, int wave, int lane, int t0,
                                           const char* img_hb) {
-  static_assert(sizeof(MxBuf::k) + sizeof(MxBuf::v) == kImgStepBytes, "image = LDS operands");
-  const char* src = img_hb + (int64_t)(t0 / kMxKeys) * kImgStepBytes + 8192 * wave + 16 * lane;
-  char* dst = reinterpret_cast<char*>(&buf.k[0][0][0]) + 8192 * wave;
+  static_assert(sizeof(MxBufT<KB>::k) + sizeof(MxBufT<KB>::v) == kImgStepBytes,
+                "image = LDS operands");
+  constexpr int PW = kImgStepBytes / 4;  // bytes per wavefront
+  const char* src = img_hb + (int64_t)(t0 / kImgKeys) * kImgStepBytes + PW * wave + 16 * lane;
+  char* dst = reinterpret_cast<char*>(&buf.k[0][0][0]) + PW * wave;
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < PW / 1024; ++i)
     __builtin_amdgcn_global_load_lds(src + 1024 * i, (lds_ptr_t)(dst + 1024 * i), 16, 0, 0);
 }
 
 
 // IMG: value operands from the per-(sequence, kv-head) value images (AttnParams::vimg), staged
 // by direct LDS loads one step ahead; otherwise loaded, converted and regrouped in the loop.
+#ifndef PA_IMG_WAVES
+#define PA_IMG_WAVES 2
+#endif
 template <typename TT, bool CAP, bool IMG>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, IMG ? PA_IMG_WAVES : 2))) void
 prefill_mx_kernel(const AttnParams p) {
   constexpr int D = 128, ROWS = kPrefillRows;
   static_assert(ROWS == 128, "four wavefronts of 32 rows");
-  __shared__ MxBuf lds[2];
+  // key blocks of 32 per step: image steps of kImgKeys keys, or 64 keys staged in the loop
+  constexpr int KB = IMG ? kImgKeys / 32 : 2, KEYS = 32 * KB;
+  using Buf = MxBufT<KB>;
+  __shared__ Buf lds[2];
   int rb, kh, b, split = blockIdx.y, part = 0, item = 0, ustart = 0, uend = 0;
   if (p.plan_items > 0) {
     const int nunits = p.plan_info[0];
@@ -658,9 +669,9 @@ prefill_mx_kernel(const AttnParams p) {
   const int r_last = min(row0 + ROWS, R) - 1;
   const int hi_all = p.causal ? pastb + r_last / g + 1 : total;
   const int lo_all = p.window > 0 ? max(0, pastb + row0 / g - p.window + 1) : 0;
-  const int t_first = max(start, (lo_all / kMxKeys) * kMxKeys);
+  const int t_first = max(start, (lo_all / KEYS) * KEYS);
   const int t_last = min(end, hi_all);
-  const int nsteps = t_last > t_first ? (t_last - t_first + kMxKeys - 1) / kMxKeys : 0;
+  const int nsteps = t_last > t_first ? (t_last - t_first + KEYS - 1) / KEYS : 0;
 
   const WaveInfo w = make_wave(p, D, b, kh, s0, pastb, total);
   // This lane's query row and the keys it sees.
@@ -705,24 +716,24 @@ prefill_mx_kernel(const AttnParams p) {
 
   // Scores of the step at t0 from LDS buffer `buf`: two 32-key blocks, their accumulation chains
   // interleaved.
-  auto scores = [&](const MxBuf& buf, f32x16(&sc)[2]) __attribute__((always_inline)) {
+  auto scores = [&](const Buf& buf, f32x16(&sc)[KB]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) sc[kb][i] = 0.0f;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) sc[kb] = mfma32<TT>(buf.k[kb][ks][lane], qv[ks], sc[kb]);
+      for (int kb = 0; kb < KB; ++kb) sc[kb] = mfma32<TT>(buf.k[kb][ks][lane], qv[ks], sc[kb]);
   };
   // Online softmax of the step at t0 over its scores, then O += P . V from buffer `buf`.
   // IMG: the accumulator's value exponent (output in units of 2^s_acc; no step seen yet: far below
   // any step's) -- each step's image holds its values in units of 2^sj.
   int s_acc = -(1 << 29);
-  auto attend = [&](const f32x16(&sc)[2], int t0, const MxBuf& buf, int sj) __attribute__((always_inline)) {
-    float x[2][16];
+  auto attend = [&](const f32x16(&sc)[KB], int t0, const Buf& buf, int sj) __attribute__((always_inline)) {
+    float x[KB][16];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         float v = sc[kb][i];
@@ -730,10 +741,10 @@ prefill_mx_kernel(const AttnParams p) {
         x[kb][i] = v;
       }
     // per-score position tests only on steps some row does not see whole (one scalar branch)
-    if (!(t0 >= all_lo && t0 + kMxKeys <= all_hi)) {
+    if (!(t0 >= all_lo && t0 + KEYS <= all_hi)) {
       const int base = t0 + 4 * h;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int pos = base + 32 * kb + 8 * (i >> 2) + (i & 3);
@@ -742,7 +753,7 @@ prefill_mx_kernel(const AttnParams p) {
     }
     float lmax = kNegInf;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) lmax = fmaxf(lmax, x[kb][i]);
     lmax = fmaxf(lmax, other_half(lmax));
@@ -803,7 +814,7 @@ prefill_mx_kernel(const AttnParams p) {
     if (IMG && !pv_on) {
       const float m0 = (m_run == kNegInf) ? 0.0f : m_run;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i)
           l_part += __builtin_amdgcn_exp2f(CAP ? x[kb][i] - m0 : __builtin_fmaf(x[kb][i], scale_log2, -m0));
@@ -811,9 +822,9 @@ prefill_mx_kernel(const AttnParams p) {
     }
     const float msafe = ((m_run == kNegInf) ? 0.0f : m_run) + (float)dsh;
     const _Float16 lw = (_Float16)(float)(1 << dsh);
-    u32x4 pb[4];
+    u32x4 pb[2 * KB];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < KB; ++kb) {
       float pv[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
@@ -832,13 +843,13 @@ prefill_mx_kernel(const AttnParams p) {
         }
     }
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < 2 * KB; ++t)
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt)
         o[nt] = mfma32<TF16>(buf.v[t][nt][IMG ? lane : mx_vslot(lane)], pb[t], o[nt]);
   };
   // Steps some row of this wavefront sees.
-  auto seen = [&](int t0) { return t0 < any_hi && t0 + kMxKeys > any_lo; };
+  auto seen = [&](int t0) { return t0 < any_hi && t0 + KEYS > any_lo; };
 
   if constexpr (IMG) {
     const int64_t hb = (int64_t)b * p.kv_heads + kh;
@@ -851,19 +862,19 @@ prefill_mx_kernel(const AttnParams p) {
     int sj = 0, sj_next = 0;
     if (nsteps > 0) {
       img_issue(lds[0], wave, lane, t_first, img_hb);
-      sj_next = vstep_hb[t_first / kMxKeys];
+      sj_next = vstep_hb[t_first / KEYS];
     }
     wait_vmem();
     __syncthreads();
     for (int k = 0; k < nsteps; ++k) {
-      const int t0 = t_first + kMxKeys * k;
+      const int t0 = t_first + KEYS * k;
       sj = __builtin_amdgcn_readfirstlane(sj_next);
       if (k + 1 < nsteps) {
-        img_issue(lds[(k + 1) & 1], wave, lane, t0 + kMxKeys, img_hb);
-        sj_next = vstep_hb[t0 / kMxKeys + 1];
+        img_issue(lds[(k + 1) & 1], wave, lane, t0 + KEYS, img_hb);
+        sj_next = vstep_hb[t0 / KEYS + 1];
       }
       if (seen(t0)) {
-        f32x16 sc[2];
+        f32x16 sc[KB];
         scores(lds[k & 1], sc);
         attend(sc, t0, lds[k & 1], sj);
       }
@@ -880,18 +891,18 @@ prefill_mx_kernel(const AttnParams p) {
     if (nsteps > 0) {
       mx_load<TT>(w, pw, wave, lane, t_first, st);
       mx_store<TT>(lds[0], st, wave, lane, t_first, total, s_stage);
-      if (nsteps > 1) mx_load<TT>(w, pw, wave, lane, t_first + kMxKeys, st);
+      if (nsteps > 1) mx_load<TT>(w, pw, wave, lane, t_first + KEYS, st);
     }
     __syncthreads();
     for (int k = 0; k < nsteps; ++k) {
-      const int t0 = t_first + kMxKeys * k;
+      const int t0 = t_first + KEYS * k;
       if (seen(t0)) {
-        f32x16 sc[2];
+        f32x16 sc[KB];
         scores(lds[k & 1], sc);
         attend(sc, t0, lds[k & 1], 0);
       }
-      if (k + 1 < nsteps) mx_store<TT>(lds[(k + 1) & 1], st, wave, lane, t0 + kMxKeys, total, s_stage);
-      if (k + 2 < nsteps) mx_load<TT>(w, pw, wave, lane, t0 + 2 * kMxKeys, st);
+      if (k + 1 < nsteps) mx_store<TT>(lds[(k + 1) & 1], st, wave, lane, t0 + KEYS, total, s_stage);
+      if (k + 2 < nsteps) mx_load<TT>(w, pw, wave, lane, t0 + 2 * KEYS, st);
       __syncthreads();
     }
   }
@@ -1015,8 +1026,9 @@ __device__ __forceinline__ ItemKeys item_keys(const AttnParams& p, int i) {
 // need nothing from the plan: they cost no launch of their own and run on other CUs while
 // workgroup 0 plans.
 
-// Operand images (AttnParams::vimg): each 64-key step of (sequence, kv-head) holds the step's LDS
-// operand buffer of prefill_mx_kernel byte for byte, so the kernel's staging is a plain copy:
+// Operand images (AttnParams::vimg): each kImgKeys-key step of (sequence, kv-head) holds the
+// step's LDS operand buffer of prefill_mx_kernel byte for byte, so the kernel's staging is a plain
+// copy:
 //   keys (16 KiB): item (kb, ks), lane l holds bytes 32 ks + 16 (l / 32) .. + 15 of the row slice
 //   of key 32 kb + l % 32 -- the rows gathered from the pages (or the caller's new rows);
 //   values (16 KiB): the rows converted to fp16 under the step's scale 2^-s -- bf16 values: s puts
@@ -1024,48 +1036,61 @@ __device__ __forceinline__ ItemKeys item_keys(const AttnParams& p, int i) {
 //   it lose bits in the fp16 subnormal range); fp16 values: s = 0 -- regrouped through LDS into
 //   the P.V A-operand layout: item (t, nt), lane l holds dim 32 nt + l % 32 of keys 16 t + 4 h + e
 //   and then 16 t + 8 + 4 h + e (e < 4, h = l / 32).
-// Rows at or past the sequence end are zero.  NT / 256 consecutive steps per workgroup, 256
-// threads each: thread (row r = (t % 256) / 4, q = t % 4) moves bytes 64 q .. 64 q + 63 of key and
-// value row r; key chunk dc = 4 q + i goes to item (kb = r / 32, ks = dc / 2), lane
-// 32 (dc % 2) + r % 32.  The step's exponent goes to vstep.
-template <typename TT, int NT>
-__device__ __forceinline__ void image_steps(const AttnParams& p, int id) {
-  constexpr int D = 128, SPW = NT / 256;
-  __shared__ uint32_t rows[SPW][kMxKeys][D / 2 + 1];  // fp16 value rows, one word = two dims
-  __shared__ int emax[SPW];
+// Rows at or past the sequence end are zero.  Steps of kImgKeys keys, NT / 256 consecutive
+// steps per workgroup, 256 threads each: thread (row r, piece q) moves 16-byte chunks
+// dc = CH q .. CH q + CH - 1 of key and value row r; key chunk dc goes to item (kb = r / 32,
+// ks = dc / 2), lane 32 (dc % 2) + r % 32.  The step's exponent goes to vstep.
+// One group of NT / 256 image steps of one (sequence, kv-head): id -> (step group, kv-head,
+// sequence); the rows are loaded into registers by img_load and written out by img_store.
+template <int NT>
+struct ImgGroup {
+  static constexpr int KEYS = kImgKeys, PCS = 256 / KEYS, CH = 16 / PCS;
+  u32x4 kx[CH], vx[CH];
+  int64_t hb;
+  int j, r, q;
+  bool step_live;
+};
+
+template <int NT>
+__device__ __forceinline__ void img_load(const AttnParams& p, int id, ImgGroup<NT>& g) {
+  constexpr int D = 128, SPW = NT / 256, KEYS = kImgKeys, PCS = ImgGroup<NT>::PCS;
+  constexpr int CH = ImgGroup<NT>::CH;
   const int nj = (p.img_steps + SPW - 1) / SPW;
-  const int jb = id % nj, kh = (id / nj) % p.kv_heads, b = id / (nj * p.kv_heads);
-  if (b >= p.batch) return;  // whole workgroup
+  const int jb = id % nj, kh = (id / nj) % p.kv_heads, b = min(id / (nj * p.kv_heads), p.batch - 1);
   const int s0 = min(max(p.cum[b], 0), p.num_tokens);
   const int s1 = min(max(p.cum[b + 1], s0), p.num_tokens);
   const int pastb = clamped_past(p, b, s1 - s0);
   const int total = pastb + (s1 - s0);
-  const int tid = threadIdx.x, grp = tid / 256;
-  const int j = jb * SPW + grp;
-  const bool step_live = s1 > s0 && j < p.img_steps && j * kMxKeys < total;
+  const int tid = threadIdx.x;
+  g.j = jb * SPW + tid / 256;
+  g.step_live = s1 > s0 && g.j < p.img_steps && g.j * KEYS < total;
+  g.hb = (int64_t)b * p.kv_heads + kh;
+  g.r = (tid & 255) / PCS;
+  g.q = tid % PCS;
   const WaveInfo w = make_wave(p, D, b, kh, s0, pastb, total);
-  const int r = (tid & 255) >> 2, q = tid & 3;
-  const int pos = j * kMxKeys + r;
-  const bool live = step_live && pos < total;
-  if (tid < SPW) emax[tid] = 0;
-  u32x4 kx[4], vx[4];
-  {
-    const char* ks = live ? row_ptr(w, pos, false, D) + 64 * q : nullptr;
-    const char* vs = live ? row_ptr(w, pos, true, D) + 64 * q : nullptr;
+  const int pos = g.j * KEYS + g.r;
+  const bool live = g.step_live && pos < total;
+  const char* ks = live ? row_ptr(w, pos, false, D) + 16 * CH * g.q : nullptr;
+  const char* vs = live ? row_ptr(w, pos, true, D) + 16 * CH * g.q : nullptr;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      kx[i] = live ? ld16(ks + 16 * i) : u32x4{0u, 0u, 0u, 0u};
-      vx[i] = live ? ld16(vs + 16 * i) : u32x4{0u, 0u, 0u, 0u};
-    }
+  for (int i = 0; i < CH; ++i) {
+    g.kx[i] = live ? ld16(ks + 16 * i) : u32x4{0u, 0u, 0u, 0u};
+    g.vx[i] = live ? ld16(vs + 16 * i) : u32x4{0u, 0u, 0u, 0u};
   }
-  const int64_t hb = (int64_t)b * p.kv_heads + kh;
-  char* dst = p.vimg + (hb * p.img_steps + j) * (int64_t)kImgStepBytes;
-  if (step_live) {
+}
+
+template <typename TT, int NT>
+__device__ __forceinline__ void img_store(const AttnParams& p, ImgGroup<NT>& g,
+                                          uint32_t (*rows)[kImgKeys][65], int* emax) {
+  constexpr int KB = kImgKeys / 32, CH = ImgGroup<NT>::CH;
+  const int tid = threadIdx.x, grp = tid / 256, r = g.r, q = g.q;
+  char* dst = p.vimg + (g.hb * p.img_steps + g.j) * (int64_t)kImgStepBytes;
+  if (g.step_live) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int dc = 4 * q + i;
+    for (int i = 0; i < CH; ++i) {
+      const int dc = CH * q + i;
       *reinterpret_cast<u32x4*>(dst + ((((r >> 5) * 8 + (dc >> 1)) * 64) + 32 * (dc & 1) + (r & 31)) * 16) =
-          kx[i];
+          g.kx[i];
     }
   }
   // the step's largest biased exponent of |value| (bf16; every wavefront of a group, then LDS)
@@ -1073,14 +1098,15 @@ __device__ __forceinline__ void image_steps(const AttnParams& p, int id) {
   if constexpr (std::is_same<TT, TBF16>::value) {
     uint32_t mx = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < CH; ++i)
 #pragma unroll
       for (int m = 0; m < 4; ++m)
         mx = __builtin_bit_cast(uint32_t,
                                 __builtin_elementwise_max(__builtin_bit_cast(u16x2, mx),
-                                                          __builtin_bit_cast(u16x2, vx[i][m] & 0x7fff7fffu)));
+                                                          __builtin_bit_cast(u16x2, g.vx[i][m] & 0x7fff7fffu)));
     e = wave_max_nonneg((int)(max(mx & 0xffffu, mx >> 16) >> 7));
   }
+  if (tid < NT / 256) emax[tid] = 0;
   __syncthreads();
   if ((tid & 63) == 0) atomicMax(&emax[grp], e);
   __syncthreads();
@@ -1091,41 +1117,57 @@ __device__ __forceinline__ void image_steps(const AttnParams& p, int id) {
     // bits (saturating: values below the fp16 range flush towards zero), shift into place
     const unsigned short bias = (unsigned short)((112 + sc) << 7);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < CH; ++i)
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
-        u16x2 a = __builtin_bit_cast(u16x2, vx[i][m] & 0x7fff7fffu);
+        u16x2 a = __builtin_bit_cast(u16x2, g.vx[i][m] & 0x7fff7fffu);
         a = __builtin_elementwise_sub_sat(a, u16x2{bias, bias});
         a = a << (unsigned short)3;
-        vx[i][m] = (vx[i][m] & 0x80008000u) | __builtin_bit_cast(uint32_t, a);
+        g.vx[i][m] = (g.vx[i][m] & 0x80008000u) | __builtin_bit_cast(uint32_t, a);
       }
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < CH; ++i)
 #pragma unroll
-    for (int m = 0; m < 4; ++m) rows[grp][r][16 * q + 4 * i + m] = vx[i][m];
+    for (int m = 0; m < 4; ++m) rows[grp][r][4 * (CH * q + i) + m] = g.vx[i][m];
   __syncthreads();
-  if (!step_live) return;
-  if ((tid & 255) == 0) p.vstep[hb * p.img_steps + j] = sc;
-  // value regroup: task (t, h, nt, dim pair dp) -> slots of lanes 32 h + 2 dp (+1) of item (t, nt)
-  char* vdst = dst + kImgStepBytes / 2;
+  if (g.step_live) {
+    if ((tid & 255) == 0) p.vstep[g.hb * p.img_steps + g.j] = sc;
+    // value regroup: task (t, h, nt, dim pair dp) -> slots of lanes 32 h + 2 dp (+1) of item
+    // (t, nt)
+    char* vdst = dst + kImgStepBytes / 2;
 #pragma unroll
-  for (int rep = 0; rep < 2; ++rep) {
-    const int task = (tid & 255) + 256 * rep;
-    const int dp = task & 15, h = (task >> 4) & 1, nt = (task >> 5) & 3, t = task >> 7;
-    u32x4 lo, hi;
+    for (int rep = 0; rep < KB; ++rep) {
+      const int task = (tid & 255) + 256 * rep;
+      const int dp = task & 15, h = (task >> 4) & 1, nt = (task >> 5) & 3, t = task >> 7;
+      u32x4 lo, hi;
 #pragma unroll
-    for (int e2 = 0; e2 < 4; ++e2) {
-      // elements 2 e2, 2 e2 + 1: keys 16 t + 4 h + (e & 3) + 8 (e >> 2)
-      const int ka = 16 * t + 4 * h + ((2 * e2) & 3) + 8 * ((2 * e2) >> 2);
-      const uint32_t wa = rows[grp][ka][16 * nt + dp], wb = rows[grp][ka + 1][16 * nt + dp];
-      lo[e2] = __builtin_amdgcn_perm(wb, wa, 0x05040100u);
-      hi[e2] = __builtin_amdgcn_perm(wb, wa, 0x07060302u);
+      for (int e2 = 0; e2 < 4; ++e2) {
+        // elements 2 e2, 2 e2 + 1: keys 16 t + 4 h + (e & 3) + 8 (e >> 2)
+        const int ka = 16 * t + 4 * h + ((2 * e2) & 3) + 8 * ((2 * e2) >> 2);
+        const uint32_t wa = rows[grp][ka][16 * nt + dp], wb = rows[grp][ka + 1][16 * nt + dp];
+        lo[e2] = __builtin_amdgcn_perm(wb, wa, 0x05040100u);
+        hi[e2] = __builtin_amdgcn_perm(wb, wa, 0x07060302u);
+      }
+      u32x4* o = reinterpret_cast<u32x4*>(vdst + (4 * t + nt) * 1024) + 32 * h + 2 * dp;
+      o[0] = lo;
+      o[1] = hi;
     }
-    u32x4* o = reinterpret_cast<u32x4*>(vdst + (4 * t + nt) * 1024) + 32 * h + 2 * dp;
-    o[0] = lo;
-    o[1] = hi;
   }
+}
+
+// Image workgroup `id`: one group of NT / 256 steps.  (A persistent variant, each workgroup
+// loading its next group before writing the current one, measured no faster.)
+template <typename TT, int NT>
+__device__ __forceinline__ void image_steps(const AttnParams& p, int id) {
+  constexpr int SPW = NT / 256;
+  __shared__ uint32_t rows[SPW][kImgKeys][65];  // fp16 value rows, one word = two dims
+  __shared__ int emax[SPW];
+  const int nj = (p.img_steps + SPW - 1) / SPW;
+  if (id >= nj * p.kv_heads * p.batch) return;
+  ImgGroup<NT> g;
+  img_load<NT>(p, id, g);
+  img_store<TT, NT>(p, g, rows, emax);
 }
 
 template <int NT, typename TT, bool IMG>
