@@ -143,7 +143,7 @@ struct Plan {
   int img_steps = 0;
 };
 
-// Value images of the planned head-128 prefill: taken when every 64-key step of values is read
+// Operand images of the planned prefill: taken when every key step of the images is read
 // by at least kImgMinRowBlocks row blocks (the images are written once and read by each), within
 // kImgMaxBytes of workspace.  PA_PREFILL_IMAGES=0 at build time keeps the in-loop conversion.
 #ifndef PA_PREFILL_IMAGES
@@ -241,9 +241,11 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
       pl.plan_items = units;
       pl.plan_rbs = (int)rbs;
       pl.part_rows = (size_t)units * 2 * pa::kPrefillRows;
-      if (PA_PREFILL_IMAGES && images && c->head_dim == 128 && rbs >= kImgMinRowBlocks) {
-        const int64_t steps = ((int64_t)ctx + pa::kImgKeys - 1) / pa::kImgKeys;
-        if ((int64_t)b->batch * c->kv_heads * steps * pa::kImgStepBytes <= kImgMaxBytes &&
+      if (PA_PREFILL_IMAGES && images && pa::img_head(c->head_dim) && rbs >= kImgMinRowBlocks) {
+        const int ik = pa::img_keys(c->head_dim);
+        const int64_t steps = ((int64_t)ctx + ik - 1) / ik;
+        if ((int64_t)b->batch * c->kv_heads * steps * pa::img_step_bytes(c->head_dim) <=
+                kImgMaxBytes &&
             steps <= 65535 && b->batch <= 65535) {
           pl.img_steps = (int)steps;
         }
@@ -303,7 +305,7 @@ size_t plan_bytes(const Plan& pl) {
 size_t image_bytes(const pa_cache* c, const pa_batch* b, const Plan& pl) {
   if (pl.img_steps == 0) return 0;
   const size_t hb = (size_t)b->batch * c->kv_heads;
-  return align256(hb * pl.img_steps * pa::kImgStepBytes) +
+  return align256(hb * pl.img_steps * pa::img_step_bytes(c->head_dim)) +
          align256(hb * pl.img_steps * sizeof(int32_t));
 }
 size_t workspace_for(const pa_cache* c, const pa_batch* b, const pa_attn*, const Plan& pl) {
@@ -402,13 +404,14 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
     p.plan_items = (int32_t)pl.plan_items;
     p.plan_rbs = pl.plan_rbs;
     // workgroups resident per CU: two, three for the 32-key image kernel (148 VGPRs, 33 KB LDS)
-    p.plan_slots = (pl.img_steps > 0 && pa::kImgKeys == 32 ? PA_IMG_WAVES : 2) * device_cus();
-    p.plan_step = pl.img_steps > 0 ? pa::kImgKeys : pa::prefill_key_step(c->head_dim);
+    p.plan_slots = (pl.img_steps > 0 && pa::img_keys(c->head_dim) == 32 && c->head_dim <= 128
+                        ? PA_IMG_WAVES : 2) * device_cus();
+    p.plan_step = pl.img_steps > 0 ? pa::img_keys(c->head_dim) : pa::prefill_key_step(c->head_dim);
     if (pl.img_steps > 0) {
       const size_t hb = (size_t)b->batch * c->kv_heads;
       char* img = base + plan_bytes(pl) - align256((size_t)pl.plan_items * 2 * 4 * sizeof(int32_t));
       p.vimg = img;
-      img += align256(hb * pl.img_steps * pa::kImgStepBytes);
+      img += align256(hb * pl.img_steps * pa::img_step_bytes(c->head_dim));
       p.vstep = reinterpret_cast<int32_t*>(img);
       p.img_steps = pl.img_steps;
     }

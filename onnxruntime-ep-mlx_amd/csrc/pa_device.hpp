@@ -346,24 +346,29 @@ struct AttnParams {
   int32_t* plan;
   int32_t* plan_info;
   int32_t* plan_split;
-  // Operand images of the planned head-128 prefill (vimg != NULL): for every 64-key step of
-  // (sequence b, kv-head kh), the key rows gathered and the value rows converted to fp16, both
+  // Operand images of the planned prefill (vimg != NULL): for every img_keys(head_dim)-key step
+  // of (sequence b, kv-head kh), the key rows gathered and the value rows converted to fp16, both
   // laid out as the prefill kernel's LDS operands, at
-  // vimg + ((b * kv_heads + kh) * img_steps + step) * kImgStepBytes; vstep[same index] is the
-  // step's power-of-two value exponent s (image element = value * 2^-s).
+  // vimg + ((b * kv_heads + kh) * img_steps + step) * img_step_bytes(head_dim); vstep[same index]
+  // is the step's power-of-two value exponent s (image element = value * 2^-s).
   char* vimg;
   int32_t* vstep;
   int32_t img_steps;
 };
 
-// Image geometry of the planned head-128 prefill: kImgKeys keys x 128 dims of 16-bit keys and
-// values per step (the prefill kernel's key step over images: 32 or 64).
+// Image geometry of the planned prefill: kImgKeys keys x d dims of 16-bit keys and values per
+// step (the prefill kernel's key step over images: 32 or 64).
 #ifndef PA_IMG_KEYS
 #define PA_IMG_KEYS 64
 #endif
 constexpr int kImgKeys = PA_IMG_KEYS;
 static_assert(kImgKeys == 32 || kImgKeys == 64, "image steps of one or two 32-key blocks");
-constexpr int kImgStepBytes = 2 * kImgKeys * 128 * 2;
+// Keys per image step at head size d (head 256: 32, so a step's operands and the output rows
+// fit the register budget of two wavefronts per SIMD), and the bytes of one step's image.
+__host__ __device__ constexpr int img_keys(int d) { return d > 128 ? 32 : kImgKeys; }
+__host__ __device__ constexpr int img_step_bytes(int d) { return 2 * img_keys(d) * d * 2; }
+// Heads the planned prefill runs over operand images.
+__host__ __device__ constexpr bool img_head(int d) { return d == 64 || d == 128 || d == 256; }
 
 // Final normalisation shared by every attention kernel: the factor that turns an output
 // accumulated relative to running max m (log2 units) with running sum l into the result,

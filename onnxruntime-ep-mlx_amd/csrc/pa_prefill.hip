@@ -449,10 +449,10 @@ __device__ __forceinline__ int wave_max_nonneg(int v) {
 // Every staging write and every operand read touches 16 distinct 16-byte bank groups per
 // 16 lanes (the value slots are XOR-swizzled for the staging writes; mx_vslot keeps the reads a
 // permutation of the image).
-template <int KB>
+template <int KB, int D = 128>
 struct MxBufT {
-  u32x4 k[KB][8][64];
-  u32x4 v[2 * KB][4][64];
+  u32x4 k[KB][D / 16][64];
+  u32x4 v[2 * KB][D / 32][64];
   int vs[4];
   int pad[12];
 };
@@ -595,13 +595,14 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70)
 // Image staging: this wavefront's quarter of the step at t0 goes straight from the step's
 // operand image (AttnParams::vimg, the LDS buffer image byte for byte) to LDS buffer `buf`:
 // direct LDS loads of 1 KiB items (4 KB per wavefront), 16 bytes per lane, no register round trip.
-template <int KB>
-__device__ __forceinline__ void img_issue(MxBufT<KB>& buf, int wave, int lane, int t0,
+template <int KB, int D>
+__device__ __forceinline__ void img_issue(MxBufT<KB, D>& buf, int wave, int lane, int t0,
                                           const char* img_hb) {
-  static_assert(sizeof(MxBufT<KB>::k) + sizeof(MxBufT<KB>::v) == kImgStepBytes,
+  constexpr int SB = img_step_bytes(D);
+  static_assert(sizeof(MxBufT<KB, D>::k) + sizeof(MxBufT<KB, D>::v) == SB && 32 * KB == img_keys(D),
                 "image = LDS operands");
-  constexpr int PW = kImgStepBytes / 4;  // bytes per wavefront
-  const char* src = img_hb + (int64_t)(t0 / kImgKeys) * kImgStepBytes + PW * wave + 16 * lane;
+  constexpr int PW = SB / 4;  // bytes per wavefront
+  const char* src = img_hb + (int64_t)(t0 / img_keys(D)) * SB + PW * wave + 16 * lane;
   char* dst = reinterpret_cast<char*>(&buf.k[0][0][0]) + PW * wave;
 #pragma unroll
   for (int i = 0; i < PW / 1024; ++i)
@@ -614,14 +615,16 @@ __device__ __forceinline__ void img_issue(MxBufT<KB>& buf, int wave, int lane, i
 #ifndef PA_IMG_WAVES
 #define PA_IMG_WAVES 2
 #endif
-template <typename TT, bool CAP, bool IMG>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, IMG ? PA_IMG_WAVES : 2))) void
+template <typename TT, bool CAP, bool IMG, int D = 128>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, IMG && D <= 128 ? PA_IMG_WAVES : 2))) void
 prefill_mx_kernel(const AttnParams p) {
-  constexpr int D = 128, ROWS = kPrefillRows;
+  constexpr int ROWS = kPrefillRows;
   static_assert(ROWS == 128, "four wavefronts of 32 rows");
-  // key blocks of 32 per step: image steps of kImgKeys keys, or 64 keys staged in the loop
-  constexpr int KB = IMG ? kImgKeys / 32 : 2, KEYS = 32 * KB;
-  using Buf = MxBufT<KB>;
+  static_assert(IMG ? img_head(D) : D == 128, "images at heads 64 / 128 / 256, in-loop staging at 128");
+  // key blocks of 32 per step: image steps of img_keys(D) keys, or 64 keys staged in the loop;
+  // KS 16-dim k-steps of the score product, NQ 32-dim output tiles
+  constexpr int KB = IMG ? img_keys(D) / 32 : 2, KEYS = 32 * KB, KS = D / 16, NQ = D / 32;
+  using Buf = MxBufT<KB, D>;
   __shared__ Buf lds[2];
   int rb, kh, b, split = blockIdx.y, part = 0, item = 0, ustart = 0, uend = 0;
   if (p.plan_items > 0) {
@@ -683,12 +686,12 @@ prefill_mx_kernel(const AttnParams p) {
   const int vis_hi = rvalid ? (p.causal ? rpos + 1 : total) : -1;
   const uint32_t qxor = p.scale < 0.0f ? 0x80008000u : 0u;
   const float scale = fabsf(p.scale), scale_log2 = fabsf(p.scale_log2);
-  u32x4 qv[8];
+  u32x4 qv[KS];
   {
     const char* qrow = reinterpret_cast<const char*>(p.q) +
                        (((int64_t)(s0 + qi) * p.num_heads + head) * D + 8 * h) * 2;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
+    for (int ks = 0; ks < KS; ++ks)
       qv[ks] = rvalid ? (ld16(qrow + 32 * ks) ^ qxor) : u32x4{0u, 0u, 0u, 0u};
   }
   // Keys visible to some row [any_lo, any_hi) and to every row [all_lo, all_hi) of the wave.
@@ -703,16 +706,18 @@ prefill_mx_kernel(const AttnParams p) {
       all_lo = p.window > 0 ? pastb + ql - p.window + 1 : 0;
     }
   }
-  f32x16 o[4];
+  f32x16 o[NQ];
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt)
+  for (int nt = 0; nt < NQ; ++nt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[nt][i] = 0.0f;
   float m_run = kNegInf, l_part = 0.0f;
   // Value scale exponents the output quarters are accumulated in, and this wavefront's running
   // scale of the quarter it stages (bf16 values; fp16 values are used unscaled).
   constexpr int kS0 = std::is_same<TT, TBF16>::value ? -112 : 0;
-  int sv[4] = {kS0, kS0, kS0, kS0};
+  int sv[NQ];
+#pragma unroll
+  for (int nt = 0; nt < NQ; ++nt) sv[nt] = kS0;
 
   // Scores of the step at t0 from LDS buffer `buf`: two 32-key blocks, their accumulation chains
   // interleaved.
@@ -722,7 +727,7 @@ prefill_mx_kernel(const AttnParams p) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) sc[kb][i] = 0.0f;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
+    for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) sc[kb] = mfma32<TT>(buf.k[kb][ks][lane], qv[ks], sc[kb]);
   };
@@ -764,7 +769,7 @@ prefill_mx_kernel(const AttnParams p) {
       l_part *= alpha;
       m_run = m_new;
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) o[nt] *= alpha;
+      for (int nt = 0; nt < NQ; ++nt) o[nt] *= alpha;
     }
     // value scales of this step: the output quarters follow a raised s exactly
     if constexpr (!IMG) {
@@ -795,7 +800,7 @@ prefill_mx_kernel(const AttnParams p) {
       if (d > 84) {  // moving up by 2^d: only if the largest |output| stays below 2^120
         float om = 0.0f;
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
+        for (int nt = 0; nt < NQ; ++nt)
 #pragma unroll
           for (int i = 0; i < 16; ++i) om = fmaxf(om, fabsf(o[nt][i]));
         om = wave_max_f(om);
@@ -804,7 +809,7 @@ prefill_mx_kernel(const AttnParams p) {
       if (d < 0 || (d > kImgPShift && up_ok)) {
         const float f = __builtin_ldexpf(1.0f, d);
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) o[nt] *= f;
+        for (int nt = 0; nt < NQ; ++nt) o[nt] *= f;
         s_acc = sj;
         d = 0;
       }
@@ -845,7 +850,7 @@ prefill_mx_kernel(const AttnParams p) {
 #pragma unroll
     for (int t = 0; t < 2 * KB; ++t)
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
+      for (int nt = 0; nt < NQ; ++nt)
         o[nt] = mfma32<TF16>(buf.v[t][nt][IMG ? lane : mx_vslot(lane)], pb[t], o[nt]);
   };
   // Steps some row of this wavefront sees.
@@ -853,7 +858,7 @@ prefill_mx_kernel(const AttnParams p) {
 
   if constexpr (IMG) {
     const int64_t hb = (int64_t)b * p.kv_heads + kh;
-    const char* img_hb = p.vimg + hb * p.img_steps * (int64_t)kImgStepBytes;
+    const char* img_hb = p.vimg + hb * p.img_steps * (int64_t)img_step_bytes(D);
     const int32_t* vstep_hb = p.vstep + hb * p.img_steps;
     // Direct LDS loads of step k + 1 into the other buffer while step k computes (every
     // wavefront finished reading that buffer before the barrier that ended iteration k - 1).
@@ -882,7 +887,7 @@ prefill_mx_kernel(const AttnParams p) {
       __syncthreads();
     }
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) sv[nt] = s_acc;
+    for (int nt = 0; nt < NQ; ++nt) sv[nt] = s_acc;
   } else {
     PageWindow pw;
     window_at(pw, w, min(div_bs(t_first, w), w.max_blocks - 1), lane);
@@ -917,7 +922,7 @@ prefill_mx_kernel(const AttnParams p) {
     const float f = finalize_factor(m_run, l_row, sink_c);
     typename TT::raw* dst = reinterpret_cast<typename TT::raw*>(p.out) + (tok * p.num_heads + head) * D;
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
+    for (int nt = 0; nt < NQ; ++nt) {
       const float fq = __builtin_ldexpf(f, sv[nt]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -934,7 +939,7 @@ prefill_mx_kernel(const AttnParams p) {
     const int64_t pi = (tok * p.num_heads + head) * p.max_splits + split;
     float* dstf = p.part_o + pi * D;
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
+    for (int nt = 0; nt < NQ; ++nt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         f32x4 v4;
@@ -950,7 +955,7 @@ prefill_mx_kernel(const AttnParams p) {
     // fp16 partial row scaled by 2^-e (e from the row's largest |O|), e folded into (m, l)
     float mx = 0.0f;
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
+    for (int nt = 0; nt < NQ; ++nt) {
       float q = 0.0f;
 #pragma unroll
       for (int i = 0; i < 16; ++i) q = fmaxf(q, fabsf(o[nt][i]));
@@ -961,7 +966,7 @@ prefill_mx_kernel(const AttnParams p) {
     const int64_t pi = ((int64_t)item * 2 + part - 1) * ROWS + (r - row0);
     char* dstb = reinterpret_cast<char*>(p.part_o) + pi * D * 2;
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
+    for (int nt = 0; nt < NQ; ++nt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         u32x2 pk;
@@ -1026,35 +1031,38 @@ __device__ __forceinline__ ItemKeys item_keys(const AttnParams& p, int i) {
 // need nothing from the plan: they cost no launch of their own and run on other CUs while
 // workgroup 0 plans.
 
-// Operand images (AttnParams::vimg): each kImgKeys-key step of (sequence, kv-head) holds the
+// Operand images (AttnParams::vimg): each img_keys(D)-key step of (sequence, kv-head) holds the
 // step's LDS operand buffer of prefill_mx_kernel byte for byte, so the kernel's staging is a plain
 // copy:
-//   keys (16 KiB): item (kb, ks), lane l holds bytes 32 ks + 16 (l / 32) .. + 15 of the row slice
-//   of key 32 kb + l % 32 -- the rows gathered from the pages (or the caller's new rows);
-//   values (16 KiB): the rows converted to fp16 under the step's scale 2^-s -- bf16 values: s puts
+//   keys (img_keys(D) x D x 2 bytes): item (kb, ks), lane l holds bytes 32 ks + 16 (l / 32) ..
+//   + 15 of the row slice of key 32 kb + l % 32 -- the rows gathered from the pages (or the
+//   caller's new rows);
+//   values (as many bytes): the rows converted to fp16 under the step's scale 2^-s -- bf16 values: s puts
 //   the step's largest |value| into [2^14, 2^15) of fp16 (exact conversion; values below 2^-29 of
 //   it lose bits in the fp16 subnormal range); fp16 values: s = 0 -- regrouped through LDS into
 //   the P.V A-operand layout: item (t, nt), lane l holds dim 32 nt + l % 32 of keys 16 t + 4 h + e
 //   and then 16 t + 8 + 4 h + e (e < 4, h = l / 32).
-// Rows at or past the sequence end are zero.  Steps of kImgKeys keys, NT / 256 consecutive
+// Rows at or past the sequence end are zero.  Steps of img_keys(D) keys, NT / 256 consecutive
 // steps per workgroup, 256 threads each: thread (row r, piece q) moves 16-byte chunks
 // dc = CH q .. CH q + CH - 1 of key and value row r; key chunk dc goes to item (kb = r / 32,
 // ks = dc / 2), lane 32 (dc % 2) + r % 32.  The step's exponent goes to vstep.
 // One group of NT / 256 image steps of one (sequence, kv-head): id -> (step group, kv-head,
 // sequence); the rows are loaded into registers by img_load and written out by img_store.
-template <int NT>
+template <int NT, int D>
 struct ImgGroup {
-  static constexpr int KEYS = kImgKeys, PCS = 256 / KEYS, CH = 16 / PCS;
+  // PCS threads per row, each moving CH of the row's D / 8 16-byte chunks
+  static constexpr int KEYS = img_keys(D), PCS = 256 / KEYS, CH = (D / 8) / PCS;
+  static_assert(CH * PCS * 8 == D, "whole chunks per thread");
   u32x4 kx[CH], vx[CH];
   int64_t hb;
   int j, r, q;
   bool step_live;
 };
 
-template <int NT>
-__device__ __forceinline__ void img_load(const AttnParams& p, int id, ImgGroup<NT>& g) {
-  constexpr int D = 128, SPW = NT / 256, KEYS = kImgKeys, PCS = ImgGroup<NT>::PCS;
-  constexpr int CH = ImgGroup<NT>::CH;
+template <int NT, int D>
+__device__ __forceinline__ void img_load(const AttnParams& p, int id, ImgGroup<NT, D>& g) {
+  constexpr int SPW = NT / 256, KEYS = img_keys(D), PCS = ImgGroup<NT, D>::PCS;
+  constexpr int CH = ImgGroup<NT, D>::CH;
   const int nj = (p.img_steps + SPW - 1) / SPW;
   const int jb = id % nj, kh = (id / nj) % p.kv_heads, b = min(id / (nj * p.kv_heads), p.batch - 1);
   const int s0 = min(max(p.cum[b], 0), p.num_tokens);
@@ -1079,17 +1087,18 @@ __device__ __forceinline__ void img_load(const AttnParams& p, int id, ImgGroup<N
   }
 }
 
-template <typename TT, int NT>
-__device__ __forceinline__ void img_store(const AttnParams& p, ImgGroup<NT>& g,
-                                          uint32_t (*rows)[kImgKeys][65], int* emax) {
-  constexpr int KB = kImgKeys / 32, CH = ImgGroup<NT>::CH;
+template <typename TT, int NT, int D>
+__device__ __forceinline__ void img_store(const AttnParams& p, ImgGroup<NT, D>& g,
+                                          uint32_t (*rows)[img_keys(D)][D / 2 + 1], int* emax) {
+  constexpr int KB = img_keys(D) / 32, CH = ImgGroup<NT, D>::CH, NQ = D / 32;
+  constexpr int SB = img_step_bytes(D);
   const int tid = threadIdx.x, grp = tid / 256, r = g.r, q = g.q;
-  char* dst = p.vimg + (g.hb * p.img_steps + g.j) * (int64_t)kImgStepBytes;
+  char* dst = p.vimg + (g.hb * p.img_steps + g.j) * (int64_t)SB;
   if (g.step_live) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int dc = CH * q + i;
-      *reinterpret_cast<u32x4*>(dst + ((((r >> 5) * 8 + (dc >> 1)) * 64) + 32 * (dc & 1) + (r & 31)) * 16) =
+      *reinterpret_cast<u32x4*>(dst + ((((r >> 5) * (D / 16) + (dc >> 1)) * 64) + 32 * (dc & 1) + (r & 31)) * 16) =
           g.kx[i];
     }
   }
@@ -1135,11 +1144,13 @@ __device__ __forceinline__ void img_store(const AttnParams& p, ImgGroup<NT>& g,
     if ((tid & 255) == 0) p.vstep[g.hb * p.img_steps + g.j] = sc;
     // value regroup: task (t, h, nt, dim pair dp) -> slots of lanes 32 h + 2 dp (+1) of item
     // (t, nt)
-    char* vdst = dst + kImgStepBytes / 2;
+    char* vdst = dst + SB / 2;
+    constexpr int NTASK = 64 * KB * NQ;  // (t < 2 KB, h < 2, nt < NQ, dp < 16)
 #pragma unroll
-    for (int rep = 0; rep < KB; ++rep) {
+    for (int rep = 0; rep < (NTASK + 255) / 256; ++rep) {
       const int task = (tid & 255) + 256 * rep;
-      const int dp = task & 15, h = (task >> 4) & 1, nt = (task >> 5) & 3, t = task >> 7;
+      if (task >= NTASK) break;
+      const int dp = task & 15, h = (task >> 4) & 1, nt = (task >> 5) % NQ, t = (task >> 5) / NQ;
       u32x4 lo, hi;
 #pragma unroll
       for (int e2 = 0; e2 < 4; ++e2) {
@@ -1149,7 +1160,7 @@ __device__ __forceinline__ void img_store(const AttnParams& p, ImgGroup<NT>& g,
         lo[e2] = __builtin_amdgcn_perm(wb, wa, 0x05040100u);
         hi[e2] = __builtin_amdgcn_perm(wb, wa, 0x07060302u);
       }
-      u32x4* o = reinterpret_cast<u32x4*>(vdst + (4 * t + nt) * 1024) + 32 * h + 2 * dp;
+      u32x4* o = reinterpret_cast<u32x4*>(vdst + (NQ * t + nt) * 1024) + 32 * h + 2 * dp;
       o[0] = lo;
       o[1] = hi;
     }
@@ -1158,23 +1169,23 @@ __device__ __forceinline__ void img_store(const AttnParams& p, ImgGroup<NT>& g,
 
 // Image workgroup `id`: one group of NT / 256 steps.  (A persistent variant, each workgroup
 // loading its next group before writing the current one, measured no faster.)
-template <typename TT, int NT>
+template <typename TT, int NT, int D>
 __device__ __forceinline__ void image_steps(const AttnParams& p, int id) {
   constexpr int SPW = NT / 256;
-  __shared__ uint32_t rows[SPW][kImgKeys][65];  // fp16 value rows, one word = two dims
+  __shared__ uint32_t rows[SPW][img_keys(D)][D / 2 + 1];  // fp16 value rows, one word = two dims
   __shared__ int emax[SPW];
   const int nj = (p.img_steps + SPW - 1) / SPW;
   if (id >= nj * p.kv_heads * p.batch) return;
-  ImgGroup<NT> g;
-  img_load<NT>(p, id, g);
-  img_store<TT, NT>(p, g, rows, emax);
+  ImgGroup<NT, D> g;
+  img_load<NT, D>(p, id, g);
+  img_store<TT, NT, D>(p, g, rows, emax);
 }
 
-template <int NT, typename TT, bool IMG>
+template <int NT, typename TT, int IMGD>
 __global__ __launch_bounds__(NT) void prefill_plan_kernel(const AttnParams p) {
-  if constexpr (IMG) {
+  if constexpr (IMGD > 0) {  // head size of the operand images
     if (blockIdx.x > 0) {
-      image_steps<TT, NT>(p, (int)blockIdx.x - 1);
+      image_steps<TT, NT, IMGD>(p, (int)blockIdx.x - 1);
       return;
     }
   }
@@ -1342,14 +1353,18 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnParams p) 
 template <typename TT, int D>
 hipError_t launch_d(const AttnParams& p, dim3 grid, hipStream_t s) {
   constexpr int NG = kPrefillGroups;
+  if constexpr (img_head(D)) {
+    if (p.vimg != nullptr) {
+      if (p.softcap > 0.0f)
+        hipLaunchKernelGGL((prefill_mx_kernel<TT, true, true, D>), grid, dim3(256), 0, s, p);
+      else
+        hipLaunchKernelGGL((prefill_mx_kernel<TT, false, true, D>), grid, dim3(256), 0, s, p);
+      return hipGetLastError();
+    }
+  }
   if constexpr (D == 128) {
     const bool cap = p.softcap > 0.0f;
-    if (p.vimg != nullptr) {
-      if (cap)
-        hipLaunchKernelGGL((prefill_mx_kernel<TT, true, true>), grid, dim3(256), 0, s, p);
-      else
-        hipLaunchKernelGGL((prefill_mx_kernel<TT, false, true>), grid, dim3(256), 0, s, p);
-    } else if (cap) {
+    if (cap) {
       hipLaunchKernelGGL((prefill_mx_kernel<TT, true, false>), grid, dim3(256), 0, s, p);
     } else {
       hipLaunchKernelGGL((prefill_mx_kernel<TT, false, false>), grid, dim3(256), 0, s, p);
@@ -1399,25 +1414,37 @@ hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype ca
       !p.plan_split || !p.part_o || !p.part_ml || p.max_splits != 1)
     return hipErrorInvalidValue;
   if ((int64_t)p.plan_items * (kPrefillRows / kPrefillMergeRows) > INT32_MAX) return hipErrorInvalidValue;
-  // Operand images (head 128): written by workgroups 1.. of the plan launch.
+  // Operand images: written by workgroups 1.. of the plan launch.
   constexpr int kPlanThreads = 1024;
   const bool img = p.vimg != nullptr;
-  if (img && (p.head_dim != 128 || !p.vstep || p.img_steps <= 0))
+  if (img && (!img_head(p.head_dim) || !p.vstep || p.img_steps <= 0))
     return hipErrorInvalidValue;
   const int64_t nimg = img ? (int64_t)p.batch * p.kv_heads *
                                  ((p.img_steps + kPlanThreads / 256 - 1) / (kPlanThreads / 256))
                            : 0;
   if (nimg + 1 > INT32_MAX) return hipErrorInvalidValue;
   const dim3 pg((unsigned)(1 + nimg));
-  if (!img)
-    hipLaunchKernelGGL((prefill_plan_kernel<kPlanThreads, TBF16, false>), pg, dim3(kPlanThreads), 0,
-                       s, p);
-  else if (act == PA_DTYPE_FLOAT16)
-    hipLaunchKernelGGL((prefill_plan_kernel<kPlanThreads, TF16, true>), pg, dim3(kPlanThreads), 0,
-                       s, p);
-  else
-    hipLaunchKernelGGL((prefill_plan_kernel<kPlanThreads, TBF16, true>), pg, dim3(kPlanThreads), 0,
-                       s, p);
+  auto plan = [&](auto tt, auto dd) {
+    using T_ = decltype(tt);
+    constexpr int D_ = decltype(dd)::value;
+    hipLaunchKernelGGL((prefill_plan_kernel<kPlanThreads, T_, D_>), pg, dim3(kPlanThreads), 0, s, p);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  if (!img) {
+    plan(TBF16{}, I0{});
+  } else {
+    auto by_head = [&](auto tt) {
+      switch (p.head_dim) {
+        case 64: plan(tt, std::integral_constant<int, 64>{}); break;
+        case 128: plan(tt, std::integral_constant<int, 128>{}); break;
+        default: plan(tt, std::integral_constant<int, 256>{}); break;
+      }
+    };
+    if (act == PA_DTYPE_FLOAT16)
+      by_head(TF16{});
+    else
+      by_head(TBF16{});
+  }
   const dim3 grid(2 * p.plan_items, 1);
   hipError_t e = act == PA_DTYPE_FLOAT16 ? launch_t<TF16>(p, grid, s) : launch_t<TBF16>(p, grid, s);
   if (e != hipSuccess) return e;

@@ -1,4 +1,4 @@
-"""GPU parity of the planned head-128 prefill over operand images.
+"""GPU parity of the planned prefill over operand images (heads 64, 128 and 256).
 
 When every 64-key step of values is read by at least four 128-row blocks (g * max_query_len >=
 512 grouped query rows per sequence) the plan launch writes, once per (sequence, kv-head) and
@@ -65,23 +65,33 @@ def _check(case, dtype, nq, new_rows_in_cache):
     assert torch.equal(outs[0], outs[1])
 
 
-@pytest.mark.parametrize("dtype,bs,in_cache,vstd,softcap,window,sink,hot", [
-    (BF16, 16, True, None, 0.0, -1, True, None),
-    (F16, 16, True, None, 0.0, -1, True, None),
-    (BF16, 16, True, 1e6, 0.0, -1, False, None),
-    (BF16, 16, True, 1e-6, 0.0, -1, False, None),
-    (BF16, 16, True, None, 0.0, -1, False, 1000.0),
-    (BF16, 16, True, None, 0.0, -1, False, 2.0 ** 100),
-    (BF16, 32, True, None, 30.0, 2900, True, None),
-    (BF16, 8, False, None, 0.0, -1, False, None),
-    (F16, 8, False, None, 0.0, -1, True, None)],
+@pytest.mark.parametrize("d,dtype,bs,in_cache,vstd,softcap,window,sink,hot", [
+    (128, BF16, 16, True, None, 0.0, -1, True, None),
+    (128, F16, 16, True, None, 0.0, -1, True, None),
+    (128, BF16, 16, True, 1e6, 0.0, -1, False, None),
+    (128, BF16, 16, True, 1e-6, 0.0, -1, False, None),
+    (128, BF16, 16, True, None, 0.0, -1, False, 1000.0),
+    (128, BF16, 16, True, None, 0.0, -1, False, 2.0 ** 100),
+    (128, BF16, 32, True, None, 30.0, 2900, True, None),
+    (128, BF16, 8, False, None, 0.0, -1, False, None),
+    (128, F16, 8, False, None, 0.0, -1, True, None),
+    (64, BF16, 16, True, None, 0.0, -1, True, None),
+    (64, F16, 8, False, None, 30.0, 2900, False, None),
+    (64, BF16, 16, True, None, 0.0, -1, False, 2.0 ** 100),
+    (256, BF16, 16, True, None, 0.0, -1, True, None),
+    (256, F16, 32, True, None, 30.0, 2900, False, None),
+    (256, BF16, 8, False, 1e6, 0.0, -1, True, None),
+    (256, BF16, 16, True, None, 0.0, -1, False, 1000.0)],
     ids=["bf16_sink", "f16_sink", "bf16_large_v", "bf16_tiny_v", "bf16_hot_rows",
          "bf16_extreme_rows",
          "bf16_block32_softcap_window", "bf16_block8_new_rows_from_inputs",
-         "f16_block8_new_rows_from_inputs_sink"])
-def test_prefill_images(dtype, bs, in_cache, vstd, softcap, window, sink, hot):
+         "f16_block8_new_rows_from_inputs_sink", "d64_bf16_sink",
+         "d64_f16_block8_softcap_window", "d64_bf16_extreme_rows", "d256_bf16_sink",
+         "d256_f16_block32_softcap_window", "d256_bf16_block8_large_v_sink",
+         "d256_bf16_hot_rows"])
+def test_prefill_images(d, dtype, bs, in_cache, vstd, softcap, window, sink, hot):
     rng = np.random.default_rng(5 + bs)
-    B, H, KV, d, nq = 24, 32, 8, 128, 128  # g * nq = 512 rows: 4 row blocks per sequence
+    B, H, KV, nq = 24, 32, 8, 128  # g * nq = 512 rows: 4 row blocks per sequence
     new_lens = np.full(B, nq)
     new_lens[3] = 0
     new_lens[9] = 77
@@ -93,7 +103,7 @@ def test_prefill_images(dtype, bs, in_cache, vstd, softcap, window, sink, hot):
                      past=past, max_blocks=mb, std=1.0, value_std=vstd, softcap=softcap,
                      window=window, head_sink=(rng.standard_normal(H) if sink else None))
     if hot is not None:
-        # rows 2000..2015 and 3500..3515 of the two long sequences (64-key steps 31 and 54)
+        # rows 2000..2015 and 3500..3515 of the two long sequences (in the middle and late)
         vc = orc.decode(case["value_cache"], dtype)
         for b in (4, 20):
             for pos in (2000, 3500):
