@@ -368,7 +368,9 @@ static_assert(kImgKeys == 32 || kImgKeys == 64, "image steps of one or two 32-ke
 __host__ __device__ constexpr int img_keys(int d) { return d > 128 ? 32 : kImgKeys; }
 __host__ __device__ constexpr int img_step_bytes(int d) { return 2 * img_keys(d) * d * 2; }
 // Heads the planned prefill runs over operand images.
-__host__ __device__ constexpr bool img_head(int d) { return d == 64 || d == 128 || d == 256; }
+__host__ __device__ constexpr bool img_head(int d) {
+  return d == 64 || d == 96 || d == 128 || d == 256;
+}
 
 // Final normalisation shared by every attention kernel: the factor that turns an output
 // accumulated relative to running max m (log2 units) with running sum l into the result,

@@ -620,7 +620,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, IMG && D
 prefill_mx_kernel(const AttnParams p) {
   constexpr int ROWS = kPrefillRows;
   static_assert(ROWS == 128, "four wavefronts of 32 rows");
-  static_assert(IMG ? img_head(D) : D == 128, "images at heads 64 / 128 / 256, in-loop staging at 128");
+  static_assert(IMG ? img_head(D) : D == 128, "images at heads 64 / 96 / 128 / 256, in-loop staging at 128");
   // key blocks of 32 per step: image steps of img_keys(D) keys, or 64 keys staged in the loop;
   // KS 16-dim k-steps of the score product, NQ 32-dim output tiles
   constexpr int KB = IMG ? img_keys(D) / 32 : 2, KEYS = 32 * KB, KS = D / 16, NQ = D / 32;
@@ -1290,10 +1290,16 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(const AttnParams p) {
 // partials are fp16 rows scaled by a power of two folded into their (m, l) (store_rows with
 // half_part): the log-sum-exp merge below takes them as they are.
 constexpr int kPrefillMergeRows = 32;
+// Threads of a merge workgroup at head size D: D / 8 per row, as many rows per pass as divide
+// kPrefillMergeRows within 256 threads (head 96: 12 x 16 = 192).
+__host__ __device__ constexpr int merge_rows_per_pass(int D) {
+  return (256 / (D / 8)) >= 32 ? 32 : (256 / (D / 8)) >= 16 ? 16 : 8;
+}
+__host__ __device__ constexpr int merge_threads(int D) { return (D / 8) * merge_rows_per_pass(D); }
 template <typename TT, int D>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnParams p) {
   constexpr int QPR = D / 8;              // lanes per row, 8 elements (16 bytes of fp16) each
-  constexpr int RPP = 256 / QPR;          // rows per pass
+  constexpr int RPP = merge_rows_per_pass(D);  // rows per pass
   constexpr int NP = kPrefillMergeRows / RPP;
   static_assert(kPrefillRows % kPrefillMergeRows == 0 && kPrefillMergeRows % RPP == 0, "merge tiling");
   constexpr int CH = kPrefillRows / kPrefillMergeRows;
@@ -1392,11 +1398,12 @@ hipError_t launch_t(const AttnParams& p, dim3 grid, hipStream_t s) {
 // The merge of the planned prefill's split items (heads whose rows tile the merge workgroup).
 template <typename TT>
 hipError_t launch_prefill_merge(const AttnParams& p, hipStream_t s) {
-  const dim3 grid(p.plan_items * (kPrefillRows / kPrefillMergeRows)), block(256);
+  const dim3 grid(p.plan_items * (kPrefillRows / kPrefillMergeRows));
   switch (p.head_dim) {
-    case 64: hipLaunchKernelGGL((prefill_merge_kernel<TT, 64>), grid, block, 0, s, p); break;
-    case 128: hipLaunchKernelGGL((prefill_merge_kernel<TT, 128>), grid, block, 0, s, p); break;
-    case 256: hipLaunchKernelGGL((prefill_merge_kernel<TT, 256>), grid, block, 0, s, p); break;
+    case 64: hipLaunchKernelGGL((prefill_merge_kernel<TT, 64>), grid, dim3(merge_threads(64)), 0, s, p); break;
+    case 96: hipLaunchKernelGGL((prefill_merge_kernel<TT, 96>), grid, dim3(merge_threads(96)), 0, s, p); break;
+    case 128: hipLaunchKernelGGL((prefill_merge_kernel<TT, 128>), grid, dim3(merge_threads(128)), 0, s, p); break;
+    case 256: hipLaunchKernelGGL((prefill_merge_kernel<TT, 256>), grid, dim3(merge_threads(256)), 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -1436,6 +1443,7 @@ hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype ca
     auto by_head = [&](auto tt) {
       switch (p.head_dim) {
         case 64: plan(tt, std::integral_constant<int, 64>{}); break;
+        case 96: plan(tt, std::integral_constant<int, 96>{}); break;
         case 128: plan(tt, std::integral_constant<int, 128>{}); break;
         default: plan(tt, std::integral_constant<int, 256>{}); break;
       }
@@ -1458,9 +1466,9 @@ bool prefill_mfma_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype) {
   return head_dim == 64 || head_dim == 96 || head_dim == 128 || head_dim == 256;
 }
 
-// The planned launch merges split items with D/8 lanes per row: heads whose rows tile that.
+// The planned launch merges split items with D/8 lanes per row (merge_threads).
 bool prefill_planned_supported(int head_dim) {
-  return head_dim == 64 || head_dim == 128 || head_dim == 256;
+  return head_dim == 64 || head_dim == 96 || head_dim == 128 || head_dim == 256;
 }
 
 // Grid: one workgroup per (row block, sequence, kv-head) and context chunk (p.max_splits

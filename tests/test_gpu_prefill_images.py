@@ -1,4 +1,4 @@
-"""GPU parity of the planned prefill over operand images (heads 64, 128 and 256).
+"""GPU parity of the planned prefill over operand images (heads 64, 96, 128 and 256).
 
 When every 64-key step of values is read by at least four 128-row blocks (g * max_query_len >=
 512 grouped query rows per sequence) the plan launch writes, once per (sequence, kv-head) and
@@ -81,14 +81,18 @@ def _check(case, dtype, nq, new_rows_in_cache):
     (256, BF16, 16, True, None, 0.0, -1, True, None),
     (256, F16, 32, True, None, 30.0, 2900, False, None),
     (256, BF16, 8, False, 1e6, 0.0, -1, True, None),
-    (256, BF16, 16, True, None, 0.0, -1, False, 1000.0)],
+    (256, BF16, 16, True, None, 0.0, -1, False, 1000.0),
+    (96, BF16, 16, True, None, 0.0, -1, True, None),
+    (96, F16, 8, False, 300.0, 30.0, 2900, False, None),
+    (96, BF16, 32, True, None, 0.0, -1, False, 2.0 ** 100)],
     ids=["bf16_sink", "f16_sink", "bf16_large_v", "bf16_tiny_v", "bf16_hot_rows",
          "bf16_extreme_rows",
          "bf16_block32_softcap_window", "bf16_block8_new_rows_from_inputs",
          "f16_block8_new_rows_from_inputs_sink", "d64_bf16_sink",
          "d64_f16_block8_softcap_window", "d64_bf16_extreme_rows", "d256_bf16_sink",
          "d256_f16_block32_softcap_window", "d256_bf16_block8_large_v_sink",
-         "d256_bf16_hot_rows"])
+         "d256_bf16_hot_rows", "d96_bf16_sink", "d96_f16_block8_large_v_softcap_window",
+         "d96_bf16_block32_extreme_rows"])
 def test_prefill_images(d, dtype, bs, in_cache, vstd, softcap, window, sink, hot):
     rng = np.random.default_rng(5 + bs)
     B, H, KV, nq = 24, 32, 8, 128  # g * nq = 512 rows: 4 row blocks per sequence
