@@ -609,7 +609,6 @@ __device__ __forceinline__ void img_issue(MxBufT<KB, D>& buf, int wave, int lane
     __builtin_amdgcn_global_load_lds(src + 1024 * i, (lds_ptr_t)(dst + 1024 * i), 16, 0, 0);
 }
 
-
 // IMG: value operands from the per-(sequence, kv-head) value images (AttnParams::vimg), staged
 // by direct LDS loads one step ahead; otherwise loaded, converted and regrouped in the loop.
 #ifndef PA_IMG_WAVES
@@ -745,15 +744,20 @@ prefill_mx_kernel(const AttnParams p) {
         if constexpr (CAP) v = p.softcap * tanhf(v * scale / p.softcap) * kLog2e;
         x[kb][i] = v;
       }
-    // per-score position tests only on steps some row does not see whole (one scalar branch)
+    // per-score position tests only on steps some row does not see whole (one scalar branch):
+    // key positions [vis_lo, min(end, vis_hi)) of this row, one unsigned range test each (three
+    // compares per score kept their masks in scalar registers and spilled them).  Differences
+    // taken modulo 2^32: the span is below 3 * 2^30 and a position below vis_lo lands above it.
     if (!(t0 >= all_lo && t0 + KEYS <= all_hi)) {
-      const int base = t0 + 4 * h;
+      const int hi_pos = min(end, vis_hi);
+      const unsigned span = hi_pos > vis_lo ? (unsigned)hi_pos - (unsigned)vis_lo : 0u;
+      const unsigned rel = (unsigned)(t0 + 4 * h) - (unsigned)vis_lo;
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int pos = base + 32 * kb + 8 * (i >> 2) + (i & 3);
-          x[kb][i] = (pos < end && pos >= vis_lo && pos < vis_hi) ? x[kb][i] : kNegInf;
+          const unsigned off = 32 * kb + 8 * (i >> 2) + (i & 3);
+          x[kb][i] = (rel + off < span) ? x[kb][i] : kNegInf;
         }
     }
     float lmax = kNegInf;
