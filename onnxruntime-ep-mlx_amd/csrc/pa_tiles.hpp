@@ -222,13 +222,18 @@ __device__ __forceinline__ float step_scores(const RowState<TT, D>& rs, KeyOp ko
   }
   // `masked` (wave-uniform) is false when the caller knows every key of the step is visible to
   // every valid row: one scalar branch instead of the per-score position tests.
+  // Positions [vis_lo, min(end, vis_hi)) of the row: one unsigned range test per score, the
+  // differences taken modulo 2^32 (the span is below 3 * 2^30, a position below vis_lo lands
+  // above it); three compares per score kept their masks in scalar registers.
   if constexpr (MASK) {
     if (masked) {
+      const int hi_pos = min(end, rs.vis_hi);
+      const unsigned span = hi_pos > rs.vis_lo ? (unsigned)hi_pos - (unsigned)rs.vis_lo : 0u;
+      const unsigned rel = (unsigned)(t0 + 4 * G) - (unsigned)rs.vis_lo;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int pos = t0 + 16 * (e >> 2) + 4 * G + (e & 3);
-        const bool vis = pos < end && pos >= rs.vis_lo && pos < rs.vis_hi;
-        x[e] = vis ? x[e] : kNegInf;
+        const unsigned off = 16 * (e >> 2) + (e & 3);
+        x[e] = (rel + off < span) ? x[e] : kNegInf;
       }
     }
   }
