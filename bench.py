@@ -423,7 +423,9 @@ def other_config_line(args, w, ms_step, attn_ms, kv_bytes, cpu=None):
             "roofline": {
                 "bound": "mfma", "achieved": round(tf_attn, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(tf_attn / MFMA_BF16_PEAK_TFLOPS, 4),
-                "traffic": None, "kernel": "pa_attention (prefill_kernel, LDS-shared K/V steps)",
+                "traffic": load_traffic("prefill_c4_traffic.json") if w["d"] == 128 else None,
+                "kernel": "pa_attention (planned prefill over operand images: plan + image "
+                          "launch, prefill_mx_kernel, merge of split items)",
                 "us_per_launch": round(attn_ms * 1e3, 1)},
         }
     gbs = kv_bytes / (ms_step * 1e-3) / 1e9
