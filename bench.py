@@ -42,6 +42,10 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup-ms", type=float, default=200.0,
+                    help="after the --warmup steps, further untimed steps until this much wall "
+                         "time has passed: the first ~20 ms of sustained load after an idle GPU "
+                         "run ~10 %% slower (C4: 290 vs 255-260 us per step)")
     ap.add_argument("--seed", type=int, default=3)
     ap.add_argument("--chunk", type=int, default=0, help="split-K chunk (0 = library default)")
     ap.add_argument("--cpu-sample", type=int, default=16, help="sequences in the CPU sample")
@@ -401,7 +405,7 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 def other_config_line(args, w, ms_step, attn_ms, kv_bytes, cpu=None):
     """JSON line of BASELINE.json configs 4 and 5 (not the driver's default line)."""
     common = {"n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-              "ms_per_step": round(ms_step, 4), "us_per_step": round(ms_step * 1e3, 1),
+              "warmup_extra_steps": args.warmup_extra, "ms_per_step": round(ms_step, 4), "us_per_step": round(ms_step * 1e3, 1),
               "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
               "cpu_baseline": cpu}
     if args.config == "c4":
@@ -488,6 +492,13 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    extra, t_w = 0, time.perf_counter()
+    while (time.perf_counter() - t_w) * 1e3 < args.warmup_ms:
+        for _ in range(10):
+            step()
+        torch.cuda.synchronize()
+        extra += 10
+    args.warmup_extra = extra
 
     # whole-step timing
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -531,6 +542,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_extra_steps": args.warmup_extra,
         "ms_per_step": round(ms_step, 4),
         "us_per_step": round(ms_step * 1e3, 1),
         "tokens_per_s": round(w["B"] / (ms_step * 1e-3), 1),
