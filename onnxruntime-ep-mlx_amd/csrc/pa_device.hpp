@@ -372,6 +372,18 @@ __host__ __device__ constexpr bool img_head(int d) {
   return d == 64 || d == 96 || d == 128 || d == 256;
 }
 
+// Softcapped score in log2 units for the matrix-core kernels: cap * tanh(y) * log2(e), y = v * k
+// with k = scale / cap, from the identity tanh(y) = sign(y) (1 - e) / (1 + e), e = exp(-2 |y|):
+// one exponential and one reciprocal (about one ulp each, ~2^-22 absolute in tanh: far below
+// the resolution of bf16 / fp16 scores) instead of a division and the library tanh per score.
+// |y| large: e = 0, tanh = +-1; NaN stays NaN.
+__device__ __forceinline__ float softcap_log2(float v, float k, float cap_log2) {
+  const float y = v * k;
+  const float e = __builtin_amdgcn_exp2f(-2.0f * kLog2e * fabsf(y));
+  const float t = (1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e);
+  return __builtin_copysignf(t, y) * cap_log2;
+}
+
 // Final normalisation shared by every attention kernel: the factor that turns an output
 // accumulated relative to running max m (log2 units) with running sum l into the result,
 // folding in an optional sink logit that only enters the denominator.

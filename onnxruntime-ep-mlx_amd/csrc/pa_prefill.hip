@@ -685,6 +685,7 @@ prefill_mx_kernel(const AttnParams p) {
   const int vis_hi = rvalid ? (p.causal ? rpos + 1 : total) : -1;
   const uint32_t qxor = p.scale < 0.0f ? 0x80008000u : 0u;
   const float scale = fabsf(p.scale), scale_log2 = fabsf(p.scale_log2);
+  const float cap_k = CAP ? scale / p.softcap : 0.0f, cap_l2 = p.softcap * kLog2e;
   u32x4 qv[KS];
   {
     const char* qrow = reinterpret_cast<const char*>(p.q) +
@@ -741,7 +742,7 @@ prefill_mx_kernel(const AttnParams p) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         float v = sc[kb][i];
-        if constexpr (CAP) v = p.softcap * tanhf(v * scale / p.softcap) * kLog2e;
+        if constexpr (CAP) v = softcap_log2(v, cap_k, cap_l2);
         x[kb][i] = v;
       }
     // per-score position tests only on steps some row does not see whole (one scalar branch):

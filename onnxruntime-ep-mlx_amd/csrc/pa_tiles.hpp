@@ -210,11 +210,12 @@ __device__ __forceinline__ float step_scores(const RowState<TT, D>& rs, KeyOp ko
   // only their maximum here and enters each exponent through one FMA in step_probs.
   static_assert(!FOLD || (!CAP && !SC), "FOLD takes plain scaled scores");
   const float xa = SC ? ksA * scale_log2 : scale_log2, xb = SC ? ksB * scale_log2 : scale_log2;
+  const float cap_k = CAP ? scale / cap : 0.0f, cap_l2 = cap * kLog2e;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float sv = (e < 4) ? sa[e & 3] : sb[e & 3];
     if constexpr (CAP)
-      x[e] = cap * tanhf(sv * scale / cap) * kLog2e;
+      x[e] = softcap_log2(sv, cap_k, cap_l2);
     else if constexpr (FOLD)
       x[e] = sv;
     else
