@@ -195,9 +195,13 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
                       !(linear && c->dtype != act) &&
                       (int64_t)c->num_blocks * c->block_size <= (int64_t)UINT32_MAX &&
                       (int64_t)std::max(b->batch, 0) * (cap / 32 + 2) < (int64_t)INT32_MAX;
+  // Integer pages (int8 / int4 codes): multi-token batches on the planned prefill over operand
+  // images of the codes when the images may be used and fit (else the VALU kernel).
+  const bool intc = PA_PREFILL_IMAGES && images &&
+                    pa::prefill_int_supported(c->head_dim, act, c->dtype);
   // Contiguous caches: the streaming decode, the LDS-shared prefill kernels, or VALU.
   if (kind == 0 && linear)
-    kind = bal_ok ? 1 : pa::prefill_mfma_supported(c->head_dim, act, c->dtype) ? 2 : 3;
+    kind = bal_ok ? 1 : (pa::prefill_mfma_supported(c->head_dim, act, c->dtype) || intc) ? 2 : 3;
   if (kind == 0) {
     if (bal_ok || (mfma && (int64_t)g * mq <= 16))
       kind = 1;
@@ -205,9 +209,14 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
       kind = 2;
     else if (mfma)
       kind = 1;
+    else if (intc)
+      kind = 2;
     else
       kind = 3;
   }
+  // integer pages run the prefill kernel only over images, i.e. the planned launch
+  if (kind == 2 && pa::prefill_int_supported(c->head_dim, act, c->dtype) && (!intc || chunk > 0))
+    kind = 3;
   pl.kind = kind;
   pl.balanced = kind == 1 && bal_ok;
   if (kind == 4) pl.kind = 1;
@@ -232,7 +241,7 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
     const int64_t rbs = ((int64_t)g * mq + pa::kPrefillRows - 1) / pa::kPrefillRows;
     const int64_t units = (int64_t)b->batch * c->kv_heads * rbs;
     const int64_t target = 2 * (int64_t)device_cus();
-    if (units >= target && units <= (int64_t)INT32_MAX / 4 &&
+    if ((units >= target || intc) && units <= (int64_t)INT32_MAX / 4 &&
         pa::prefill_planned_supported(c->head_dim)) {
       // Enough workgroups for every slot: planned units, longest first, long items split in two
       // (the tail of uneven row blocks otherwise idles ~28% of the slots at the C4 shape).
@@ -241,7 +250,8 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
       pl.plan_items = units;
       pl.plan_rbs = (int)rbs;
       pl.part_rows = (size_t)units * 2 * pa::kPrefillRows;
-      if (PA_PREFILL_IMAGES && images && pa::img_head(c->head_dim) && rbs >= kImgMinRowBlocks) {
+      if (PA_PREFILL_IMAGES && images && pa::img_head(c->head_dim) &&
+          (rbs >= kImgMinRowBlocks || intc)) {
         const int ik = pa::img_keys(c->head_dim);
         const int64_t steps = ((int64_t)ctx + ik - 1) / ik;
         if ((int64_t)b->batch * c->kv_heads * steps * pa::img_step_bytes(c->head_dim) <=
@@ -250,7 +260,9 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
           pl.img_steps = (int)steps;
         }
       }
-      return pl;
+      if (!(intc && pl.img_steps == 0)) return pl;
+      pl = Plan{};  // integer pages whose images do not fit: see below
+      pl.kind = 2;
     } else if (units >= target) {
       chunk = (int)std::min<int64_t>(((int64_t)ctx + 31) / 32 * 32, INT32_MAX / 2);
     } else {
@@ -260,6 +272,12 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
       chunk = (int)std::min<int64_t>(std::max<int64_t>((ch + step - 1) / step * step, 256),
                                      INT32_MAX / 2);
     }
+  }
+  // Integer pages that did not get the planned launch over images: the VALU kernel.
+  if (pl.kind == 2 && pa::prefill_int_supported(c->head_dim, act, c->dtype)) {
+    kind = 3;
+    pl.kind = 3;
+    pl.ng = 1;
   }
   if (chunk <= 0) {
     // Work units without split-K: (sequence, kv-head, row groups) for the MFMA kernel,
@@ -363,13 +381,18 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
           pa::balanced_supported(c->head_dim, act, c->dtype, c->block_size)))
       return fail(PA_ERR_UNSUPPORTED, "decode MFMA kernel does not cover this dtype/head_dim");
   }
-  if (kind == 2 && !pa::prefill_mfma_supported(c->head_dim, act, c->dtype))
+  if (kind == 2 && !pa::prefill_mfma_supported(c->head_dim, act, c->dtype) &&
+      !pa::prefill_int_supported(c->head_dim, act, c->dtype))
     return fail(PA_ERR_UNSUPPORTED, "prefill MFMA kernel does not cover this dtype/head_dim");
   if (!(a->softcap >= 0.0f) || !std::isfinite(a->softcap))
     return fail(PA_ERR_INVALID_ARGUMENT, "softcap must be finite and non-negative");
   kind = effective_kind(kind, opts);
   Plan pl = make_plan(c, b, a, act, kind, chunk, opts.linear_cap > 0, opts.linear_cap,
                       opts.images);
+  if (kind == 2 && pl.kind != 2 && pa::prefill_int_supported(c->head_dim, act, c->dtype))
+    return fail(PA_ERR_UNSUPPORTED,
+                "prefill MFMA kernel: integer pages run on it over operand images only (planned "
+                "launch, automatic chunking, images within the workspace)");
   if (opts.linear_cap > 0 && !(pl.balanced || pl.kind == 2 || pl.kind == 3))
     return fail(PA_ERR_UNSUPPORTED,
                 "contiguous caches run on the streaming decode, prefill or VALU kernels only");

@@ -614,9 +614,14 @@ __device__ __forceinline__ void img_issue(MxBufT<KB, D>& buf, int wave, int lane
 #ifndef PA_IMG_WAVES
 #define PA_IMG_WAVES 2
 #endif
-template <typename TT, bool CAP, bool IMG, int D = 128>
+// INTC: integer pages (images of fp16 codes): per-channel / per-tensor key scales fold into the
+// query, normalised per row by a power of two whose exponent joins the row's softmax scale; the
+// scores run on fp16 products; value scales multiply the output per dim before normalisation.
+template <typename TT, bool CAP, bool IMG, int D = 128, bool INTC = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, IMG && D <= 128 ? PA_IMG_WAVES : 2))) void
 prefill_mx_kernel(const AttnParams p) {
+  static_assert(!INTC || IMG, "integer pages over images only");
+  using KT = typename std::conditional<INTC, TF16, TT>::type;  // score operand type
   constexpr int ROWS = kPrefillRows;
   static_assert(ROWS == 128, "four wavefronts of 32 rows");
   static_assert(IMG ? img_head(D) : D == 128, "images at heads 64 / 96 / 128 / 256, in-loop staging at 128");
@@ -684,8 +689,11 @@ prefill_mx_kernel(const AttnParams p) {
   const int vis_lo = p.window > 0 ? rpos - p.window + 1 : 0;
   const int vis_hi = rvalid ? (p.causal ? rpos + 1 : total) : -1;
   const uint32_t qxor = p.scale < 0.0f ? 0x80008000u : 0u;
-  const float scale = fabsf(p.scale), scale_log2 = fabsf(p.scale_log2);
-  const float cap_k = CAP ? scale / p.softcap : 0.0f, cap_l2 = p.softcap * kLog2e;
+  const float scale = fabsf(p.scale);
+  // the row's log2-domain score scale and softcap factor (per lane for integer pages)
+  float scale_log2 = fabsf(p.scale_log2);
+  float cap_k = CAP ? scale / p.softcap : 0.0f;
+  const float cap_l2 = p.softcap * kLog2e;
   u32x4 qv[KS];
   {
     const char* qrow = reinterpret_cast<const char*>(p.q) +
@@ -693,6 +701,44 @@ prefill_mx_kernel(const AttnParams p) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
       qv[ks] = rvalid ? (ld16(qrow + 32 * ks) ^ qxor) : u32x4{0u, 0u, 0u, 0u};
+    if constexpr (INTC) {
+      // q * key scale in fp32 (dims 16 ks + 8 h + e of this lane), scaled by 2^-er so the bound
+      // max|q| (the row) x max|scale| (the kv-head) lies below 2^14, then fp16 (RNE), one product
+      // at a time: scores = 2^er * (q16 . codes)
+      const bool kpc = p.k_quant == PA_QUANT_PER_CHANNEL;
+      float mq = 0.0f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          mq = fmaxf(mq, fabsf(TT::to_f32((uint16_t)(qv[ks][e >> 1] >> (16 * (e & 1))))));
+      mq = fmaxf(mq, other_half(mq));
+      float ms = 0.0f;
+      if (kpc) {
+        for (int d = lane; d < D; d += 64) ms = fmaxf(ms, fabsf(p.k_scale[(int64_t)kh * D + d]));
+        ms = wave_max_f(ms);
+      } else {
+        ms = fabsf(p.k_scale[0]);
+      }
+      const float bound = mq * ms;
+      const int er = bound > 0.0f ? __builtin_amdgcn_frexp_expf(bound) - 14 : 0;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const int d0 = 16 * ks + 8 * h + 2 * m;
+          const float s0v = p.k_scale[kpc ? (int64_t)kh * D + d0 : 0];
+          const float s1v = p.k_scale[kpc ? (int64_t)kh * D + d0 + 1 : 0];
+          const float a = TT::to_f32((uint16_t)qv[ks][m]) * s0v;
+          const float c = TT::to_f32((uint16_t)(qv[ks][m] >> 16)) * s1v;
+          const f16x2v ph = __builtin_convertvector(
+              f32x2v{__builtin_ldexpf(a, -er), __builtin_ldexpf(c, -er)}, f16x2v);
+          qv[ks][m] = __builtin_bit_cast(uint32_t, ph);
+          __builtin_amdgcn_sched_barrier(0);  // the scale loads a pair at a time (registers)
+        }
+      scale_log2 = __builtin_ldexpf(scale_log2, er);
+      cap_k = __builtin_ldexpf(cap_k, er);
+    }
   }
   // Keys visible to some row [any_lo, any_hi) and to every row [all_lo, all_hi) of the wave.
   int any_lo = 0, any_hi = -1, all_lo = 0, all_hi = -1;
@@ -729,7 +775,7 @@ prefill_mx_kernel(const AttnParams p) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) sc[kb] = mfma32<TT>(buf.k[kb][ks][lane], qv[ks], sc[kb]);
+      for (int kb = 0; kb < KB; ++kb) sc[kb] = mfma32<KT>(buf.k[kb][ks][lane], qv[ks], sc[kb]);
   };
   // Online softmax of the step at t0 over its scores, then O += P . V from buffer `buf`.
   // IMG: the accumulator's value exponent (output in units of 2^s_acc; no step seen yet: far below
@@ -919,6 +965,18 @@ prefill_mx_kernel(const AttnParams p) {
 
   // Epilogue: row r's output in true units is o[nt] * 2^sv[nt]; lanes l and l ^ 32 hold dims
   // 8 i + 4 h + j of each quarter.
+  if constexpr (INTC) {  // value scales per dim (per channel) or one per tensor
+    const bool vpc = p.v_quant == PA_QUANT_PER_CHANNEL;
+#pragma unroll
+    for (int nt = 0; nt < NQ; ++nt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          o[nt][4 * i + j] *= p.v_scale[vpc ? (int64_t)kh * D + 32 * nt + 8 * i + 4 * h + j : 0];
+      __builtin_amdgcn_sched_barrier(0);  // the scale loads one quarter at a time (registers)
+    }
+  }
   const float l_row = l_part + other_half(l_part);
   if (!rvalid) return;
   const int64_t tok = s0 + qi;
@@ -1064,7 +1122,46 @@ struct ImgGroup {
   bool step_live;
 };
 
-template <int NT, int D>
+// Page codes of integer caches (KC: kImgI8 / kImgI4) load as 32-bit words and widen exactly to
+// fp16 (int8 codes; int4 nibbles, low nibble first, biased by +8), so the images hold the codes
+// and the scales apply outside the products.
+constexpr int kImgT = 0, kImgI8 = 1, kImgI4 = 2;
+template <int KC>
+__device__ __forceinline__ uint32_t f16_pair(int a, int b) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)a) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)b) << 16);
+}
+template <int KC, int CH>
+__device__ __forceinline__ void load_codes(const char* row, bool live, u32x4 (&x)[CH]) {
+  if constexpr (KC == kImgI8) {
+    // 8 codes per 16-byte fp16 chunk: two words
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      uint32_t w[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        w[k] = live ? reinterpret_cast<const uint32_t*>(row)[2 * i + k] : 0u;
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int c0 = (int8_t)(w[k] & 0xff), c1 = (int8_t)((w[k] >> 8) & 0xff);
+        const int c2 = (int8_t)((w[k] >> 16) & 0xff), c3 = (int8_t)(w[k] >> 24);
+        x[i][2 * k] = f16_pair<KC>(c0, c1);
+        x[i][2 * k + 1] = f16_pair<KC>(c2, c3);
+      }
+    }
+  } else {
+    // 8 codes per chunk: one word of nibbles
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const uint32_t w = live ? reinterpret_cast<const uint32_t*>(row)[i] : 0x88888888u;
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        x[i][k] = f16_pair<KC>((int)((w >> (8 * k)) & 15u) - 8, (int)((w >> (8 * k + 4)) & 15u) - 8);
+    }
+  }
+}
+
+template <int NT, int D, int KC>
 __device__ __forceinline__ void img_load(const AttnParams& p, int id, ImgGroup<NT, D>& g) {
   constexpr int SPW = NT / 256, KEYS = img_keys(D), PCS = ImgGroup<NT, D>::PCS;
   constexpr int CH = ImgGroup<NT, D>::CH;
@@ -1080,23 +1177,37 @@ __device__ __forceinline__ void img_load(const AttnParams& p, int id, ImgGroup<N
   g.hb = (int64_t)b * p.kv_heads + kh;
   g.r = (tid & 255) / PCS;
   g.q = tid % PCS;
-  const WaveInfo w = make_wave(p, D, b, kh, s0, pastb, total);
+  WaveInfo w = make_wave(p, D, b, kh, s0, pastb, total);
   const int pos = g.j * KEYS + g.r;
   const bool live = g.step_live && pos < total;
-  const char* ks = live ? row_ptr(w, pos, false, D) + 16 * CH * g.q : nullptr;
-  const char* vs = live ? row_ptr(w, pos, true, D) + 16 * CH * g.q : nullptr;
+  if constexpr (KC == kImgT) {
+    const char* ks = live ? row_ptr(w, pos, false, D) + 16 * CH * g.q : nullptr;
+    const char* vs = live ? row_ptr(w, pos, true, D) + 16 * CH * g.q : nullptr;
 #pragma unroll
-  for (int i = 0; i < CH; ++i) {
-    g.kx[i] = live ? ld16(ks + 16 * i) : u32x4{0u, 0u, 0u, 0u};
-    g.vx[i] = live ? ld16(vs + 16 * i) : u32x4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < CH; ++i) {
+      g.kx[i] = live ? ld16(ks + 16 * i) : u32x4{0u, 0u, 0u, 0u};
+      g.vx[i] = live ? ld16(vs + 16 * i) : u32x4{0u, 0u, 0u, 0u};
+    }
+  } else {
+    // code rows: D bytes (int8) or D / 2 (int4) per kv-head
+    constexpr int RB = KC == kImgI8 ? D : D / 2;
+    w.rowb = w.lin_row0 >= 0 ? RB : (int64_t)p.kv_heads * RB;
+    w.hoff = w.lin_row0 >= 0 ? 0 : (int64_t)kh * RB;
+    const int cb = (KC == kImgI8 ? 8 : 4) * CH * g.q;  // bytes before this thread's codes
+    const char* ks = live ? row_ptr(w, pos, false, D) + cb : nullptr;
+    const char* vs = live ? row_ptr(w, pos, true, D) + cb : nullptr;
+    load_codes<KC, CH>(ks, live, g.kx);
+    load_codes<KC, CH>(vs, live, g.vx);
   }
 }
 
-template <typename TT, int NT, int D>
+template <typename TT, int NT, int D, int KC>
 __device__ __forceinline__ void img_store(const AttnParams& p, ImgGroup<NT, D>& g,
                                           uint32_t (*rows)[img_keys(D)][D / 2 + 1], int* emax) {
   constexpr int KB = img_keys(D) / 32, CH = ImgGroup<NT, D>::CH, NQ = D / 32;
   constexpr int SB = img_step_bytes(D);
+  // bf16 pages take a per-step scale; fp16 pages and integer codes (exact in fp16) go as they are
+  constexpr bool BF = std::is_same<TT, TBF16>::value && KC == kImgT;
   const int tid = threadIdx.x, grp = tid / 256, r = g.r, q = g.q;
   char* dst = p.vimg + (g.hb * p.img_steps + g.j) * (int64_t)SB;
   if (g.step_live) {
@@ -1109,7 +1220,7 @@ __device__ __forceinline__ void img_store(const AttnParams& p, ImgGroup<NT, D>& 
   }
   // the step's largest biased exponent of |value| (bf16; every wavefront of a group, then LDS)
   int e = 0;
-  if constexpr (std::is_same<TT, TBF16>::value) {
+  if constexpr (BF) {
     uint32_t mx = 0;
 #pragma unroll
     for (int i = 0; i < CH; ++i)
@@ -1125,8 +1236,8 @@ __device__ __forceinline__ void img_store(const AttnParams& p, ImgGroup<NT, D>& 
   if ((tid & 63) == 0) atomicMax(&emax[grp], e);
   __syncthreads();
   // bf16: s = emax - 141 puts the largest value into [2^14, 2^15) of fp16; fp16: s = 0
-  const int sc = std::is_same<TT, TBF16>::value ? max(emax[grp] - 141, -112) : 0;
-  if (std::is_same<TT, TBF16>::value) {
+  const int sc = BF ? max(emax[grp] - 141, -112) : 0;
+  if constexpr (BF) {
     // bf16 exponent E -> fp16 exponent E - 112 - s: subtract (112 + s) << 7 from the magnitude
     // bits (saturating: values below the fp16 range flush towards zero), shift into place
     const unsigned short bias = (unsigned short)((112 + sc) << 7);
@@ -1174,7 +1285,7 @@ __device__ __forceinline__ void img_store(const AttnParams& p, ImgGroup<NT, D>& 
 
 // Image workgroup `id`: one group of NT / 256 steps.  (A persistent variant, each workgroup
 // loading its next group before writing the current one, measured no faster.)
-template <typename TT, int NT, int D>
+template <typename TT, int NT, int D, int KC>
 __device__ __forceinline__ void image_steps(const AttnParams& p, int id) {
   constexpr int SPW = NT / 256;
   __shared__ uint32_t rows[SPW][img_keys(D)][D / 2 + 1];  // fp16 value rows, one word = two dims
@@ -1182,15 +1293,15 @@ __device__ __forceinline__ void image_steps(const AttnParams& p, int id) {
   const int nj = (p.img_steps + SPW - 1) / SPW;
   if (id >= nj * p.kv_heads * p.batch) return;
   ImgGroup<NT, D> g;
-  img_load<NT, D>(p, id, g);
-  img_store<TT, NT, D>(p, g, rows, emax);
+  img_load<NT, D, KC>(p, id, g);
+  img_store<TT, NT, D, KC>(p, g, rows, emax);
 }
 
-template <int NT, typename TT, int IMGD>
+template <int NT, typename TT, int IMGD, int KC = kImgT>
 __global__ __launch_bounds__(NT) void prefill_plan_kernel(const AttnParams p) {
-  if constexpr (IMGD > 0) {  // head size of the operand images
+  if constexpr (IMGD > 0) {  // head size of the operand images; KC: the pages' element kind
     if (blockIdx.x > 0) {
-      image_steps<TT, NT, IMGD>(p, (int)blockIdx.x - 1);
+      image_steps<TT, NT, IMGD, KC>(p, (int)blockIdx.x - 1);
       return;
     }
   }
@@ -1362,17 +1473,24 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnParams p) 
 }
 
 template <typename TT, int D>
-hipError_t launch_d(const AttnParams& p, dim3 grid, hipStream_t s) {
+hipError_t launch_d(const AttnParams& p, dim3 grid, hipStream_t s, bool intc = false) {
   constexpr int NG = kPrefillGroups;
   if constexpr (img_head(D)) {
     if (p.vimg != nullptr) {
-      if (p.softcap > 0.0f)
+      if (intc) {
+        if (p.softcap > 0.0f)
+          hipLaunchKernelGGL((prefill_mx_kernel<TT, true, true, D, true>), grid, dim3(256), 0, s, p);
+        else
+          hipLaunchKernelGGL((prefill_mx_kernel<TT, false, true, D, true>), grid, dim3(256), 0, s, p);
+      } else if (p.softcap > 0.0f) {
         hipLaunchKernelGGL((prefill_mx_kernel<TT, true, true, D>), grid, dim3(256), 0, s, p);
-      else
+      } else {
         hipLaunchKernelGGL((prefill_mx_kernel<TT, false, true, D>), grid, dim3(256), 0, s, p);
+      }
       return hipGetLastError();
     }
   }
+  if (intc) return hipErrorInvalidValue;  // integer pages run over images only
   if constexpr (D == 128) {
     const bool cap = p.softcap > 0.0f;
     if (cap) {
@@ -1390,12 +1508,12 @@ hipError_t launch_d(const AttnParams& p, dim3 grid, hipStream_t s) {
 }
 
 template <typename TT>
-hipError_t launch_t(const AttnParams& p, dim3 grid, hipStream_t s) {
+hipError_t launch_t(const AttnParams& p, dim3 grid, hipStream_t s, bool intc = false) {
   switch (p.head_dim) {
-    case 64: return launch_d<TT, 64>(p, grid, s);
-    case 96: return launch_d<TT, 96>(p, grid, s);
-    case 128: return launch_d<TT, 128>(p, grid, s);
-    case 256: return launch_d<TT, 256>(p, grid, s);
+    case 64: return launch_d<TT, 64>(p, grid, s, intc);
+    case 96: return launch_d<TT, 96>(p, grid, s, intc);
+    case 128: return launch_d<TT, 128>(p, grid, s, intc);
+    case 256: return launch_d<TT, 256>(p, grid, s, intc);
     default: return hipErrorInvalidValue;
   }
 }
@@ -1420,7 +1538,11 @@ hipError_t launch_prefill_merge(const AttnParams& p, hipStream_t s) {
 // (workgroups past the planned count exit at once), then the merge of the split items.
 hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
                                   hipStream_t s) {
-  if (!prefill_mfma_supported(p.head_dim, act, cache_dtype) || !prefill_planned_supported(p.head_dim))
+  // integer pages: over operand images of their codes only
+  const bool intc = prefill_int_supported(p.head_dim, act, cache_dtype);
+  if (intc ? (p.vimg == nullptr || !p.k_scale || !p.v_scale)
+           : (!prefill_mfma_supported(p.head_dim, act, cache_dtype) ||
+              !prefill_planned_supported(p.head_dim)))
     return hipErrorInvalidValue;
   if (p.plan_items <= 0 || p.plan_rbs <= 0 || !p.plan || !p.plan_info ||
       !p.plan_split || !p.part_o || !p.part_ml || p.max_splits != 1)
@@ -1436,21 +1558,30 @@ hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype ca
                            : 0;
   if (nimg + 1 > INT32_MAX) return hipErrorInvalidValue;
   const dim3 pg((unsigned)(1 + nimg));
-  auto plan = [&](auto tt, auto dd) {
+  auto plan = [&](auto tt, auto dd, auto kc) {
     using T_ = decltype(tt);
-    constexpr int D_ = decltype(dd)::value;
-    hipLaunchKernelGGL((prefill_plan_kernel<kPlanThreads, T_, D_>), pg, dim3(kPlanThreads), 0, s, p);
+    constexpr int D_ = decltype(dd)::value, KC_ = decltype(kc)::value;
+    hipLaunchKernelGGL((prefill_plan_kernel<kPlanThreads, T_, D_, KC_>), pg, dim3(kPlanThreads), 0,
+                       s, p);
   };
   using I0 = std::integral_constant<int, 0>;
   if (!img) {
-    plan(TBF16{}, I0{});
+    plan(TBF16{}, I0{}, I0{});
   } else {
+    auto by_kind = [&](auto tt, auto dd) {
+      if (cache_dtype == PA_DTYPE_INT8)
+        plan(tt, dd, std::integral_constant<int, kImgI8>{});
+      else if (cache_dtype == PA_DTYPE_INT4)
+        plan(tt, dd, std::integral_constant<int, kImgI4>{});
+      else
+        plan(tt, dd, std::integral_constant<int, kImgT>{});
+    };
     auto by_head = [&](auto tt) {
       switch (p.head_dim) {
-        case 64: plan(tt, std::integral_constant<int, 64>{}); break;
-        case 96: plan(tt, std::integral_constant<int, 96>{}); break;
-        case 128: plan(tt, std::integral_constant<int, 128>{}); break;
-        default: plan(tt, std::integral_constant<int, 256>{}); break;
+        case 64: by_kind(tt, std::integral_constant<int, 64>{}); break;
+        case 96: by_kind(tt, std::integral_constant<int, 96>{}); break;
+        case 128: by_kind(tt, std::integral_constant<int, 128>{}); break;
+        default: by_kind(tt, std::integral_constant<int, 256>{}); break;
       }
     };
     if (act == PA_DTYPE_FLOAT16)
@@ -1459,10 +1590,18 @@ hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype ca
       by_head(TBF16{});
   }
   const dim3 grid(2 * p.plan_items, 1);
-  hipError_t e = act == PA_DTYPE_FLOAT16 ? launch_t<TF16>(p, grid, s) : launch_t<TBF16>(p, grid, s);
+  hipError_t e = act == PA_DTYPE_FLOAT16 ? launch_t<TF16>(p, grid, s, intc)
+                                         : launch_t<TBF16>(p, grid, s, intc);
   if (e != hipSuccess) return e;
   return act == PA_DTYPE_FLOAT16 ? launch_prefill_merge<TF16>(p, s)
                                  : launch_prefill_merge<TBF16>(p, s);
+}
+
+// Integer pages (int8 / int4 codes with fp32 scales) on the planned prefill over operand images.
+bool prefill_int_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype) {
+  if (act != PA_DTYPE_FLOAT16 && act != PA_DTYPE_BFLOAT16) return false;
+  if (cache_dtype != PA_DTYPE_INT8 && cache_dtype != PA_DTYPE_INT4) return false;
+  return img_head(head_dim);
 }
 
 bool prefill_mfma_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype) {
