@@ -58,8 +58,8 @@ def parse():
     ap.add_argument("--head-dim", type=int, default=128, choices=(64, 96, 128, 256),
                     help="c3 / c4: the same batch at another head size (128 = the config)")
     ap.add_argument("--cache-dtype", default="bf16", choices=("bf16", "int8", "int4"),
-                    help="c3 only: the same decode batch over int8 / int4 pages with per-channel "
-                         "fp32 scales (bf16 = config 3)")
+                    help="c3 / c4: the same batch over int8 / int4 pages with per-channel "
+                         "fp32 scales (bf16 = the config)")
     return ap.parse_args()
 
 
@@ -122,10 +122,12 @@ def build_workload(torch, ep, seed, d=128, cache="bf16"):
     return w
 
 
-def build_prefill_workload(torch, seed=4, d=128):
+def build_prefill_workload(torch, seed=4, d=128, cache="bf16"):
     """bf16, 8 sequences each appending a 512-token chunk over a cached
     context U[0, 4096], 28 query / 4 kv heads, d 128, block 16, causal within the chunk, packed
-    cumulative_sequence_length, values N(0,1).  No rotary (the config names none)."""
+    cumulative_sequence_length, values N(0,1).  No rotary (the config names none).
+    cache int8 / int4: the same batch over integer pages (codes uniform over the code range,
+    per-channel fp32 scales [KV, d] of U[0.5, 1.5) / 64)."""
     import numpy as np
     rng = np.random.default_rng(seed)
     B, H, KV, bs, chunk = 8, 28, 4, 16, 512
@@ -135,11 +137,21 @@ def build_prefill_workload(torch, seed=4, d=128):
     bt = rng.permutation(nb).astype(np.int32).reshape(B, mb)
     dev = torch.device("cuda", 0)
     g = torch.Generator(device=dev).manual_seed(seed)
-    kc = torch.randn((nb, bs, KV, d), generator=g, device=dev).to(torch.bfloat16)
-    vc = torch.randn((nb, bs, KV, d), generator=g, device=dev).to(torch.bfloat16)
+    ks = vs = None
+    if cache == "bf16":
+        kc = torch.randn((nb, bs, KV, d), generator=g, device=dev).to(torch.bfloat16)
+        vc = torch.randn((nb, bs, KV, d), generator=g, device=dev).to(torch.bfloat16)
+    else:
+        width, dt = (d, torch.int8) if cache == "int8" else (d // 2, torch.uint8)
+        lo, hi = (-128, 128) if cache == "int8" else (0, 256)
+        kc = torch.randint(lo, hi, (nb, bs, KV, width), generator=g, device=dev, dtype=dt)
+        vc = torch.randint(lo, hi, (nb, bs, KV, width), generator=g, device=dev, dtype=dt)
+        ks = (torch.rand((KV, d), generator=g, device=dev) + 0.5) / 64.0
+        vs = (torch.rand((KV, d), generator=g, device=dev) + 0.5) / 64.0
     T = B * chunk
     w = dict(B=B, T=T, mq=chunk, H=H, KV=KV, d=d, bs=bs, nb=nb, ctx=past + chunk, bt_np=bt,
-             kc=kc, vc=vc, cos=None, sin=None, ks=None, vs=None,
+             kc=kc, vc=vc, cos=None, sin=None, ks=ks, vs=vs, cache=cache,
+             quant="NONE" if cache == "bf16" else "PER_CHANNEL",
              q=torch.randn((T, H * d), generator=g, device=dev).to(torch.bfloat16),
              k=torch.randn((T, KV * d), generator=g, device=dev).to(torch.bfloat16),
              v=torch.randn((T, KV * d), generator=g, device=dev).to(torch.bfloat16))
@@ -427,7 +439,8 @@ def other_config_line(args, w, ms_step, attn_ms, kv_bytes, cpu=None):
             "roofline": {
                 "bound": "mfma", "achieved": round(tf_attn, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(tf_attn / MFMA_BF16_PEAK_TFLOPS, 4),
-                "traffic": load_traffic("prefill_c4_traffic.json") if w["d"] == 128 else None,
+                "traffic": (load_traffic("prefill_c4_traffic.json")
+                            if w["d"] == 128 and w.get("cache", "bf16") == "bf16" else None),
                 "kernel": "pa_attention (planned prefill over operand images: plan + image "
                           "launch, prefill_mx_kernel, merge of split items)",
                 "us_per_launch": round(attn_ms * 1e3, 1)},
@@ -469,9 +482,13 @@ def main():
         w = build_workload(torch, ep, args.seed, args.head_dim, args.cache_dtype)
         step = Step(torch, ep, w, args.chunk, kind=1 if args.cache_dtype == "bf16" else 0)
     elif args.config == "c4":
-        w = build_prefill_workload(torch, d=args.head_dim)
+        w = build_prefill_workload(torch, d=args.head_dim, cache=args.cache_dtype)
         step = Step(torch, ep, w, args.chunk, kind=0)
     else:
+        if args.cache_dtype != "bf16":
+            print("bench.py: --cache-dtype applies to c3 and c4 (c5 is the e4m3 config)",
+                  file=sys.stderr)
+            sys.exit(2)
         w = build_fp8_workload(torch)
         step = Step(torch, ep, w, args.chunk, kind=0)
     # bytes per K or V element: fp8 / int8 pages 1, int4 pages 1/2, bf16 2
@@ -529,8 +546,15 @@ def main():
 
     if args.config != "c3":
         line = other_config_line(args, w, ms_step, attn_ms, kv_bytes, cpu)
-        if w["d"] != 128:  # not config 4 itself: say so in the line
-            line["metric"] += f" (head_dim {w['d']} variant of config 4)"
+        cache = w.get("cache", "bf16")
+        if w["d"] != 128 or cache != "bf16":  # not config 4 itself: say so in the line
+            what = f"head_dim {w['d']}" + ("" if cache == "bf16" else f", {cache} pages")
+            line["metric"] += f" ({what} variant of config 4)"
+            line["config"]["cache_dtype"] = cache
+            if cache != "bf16":
+                line["dtype"] = f"bf16 x {cache} (fp16 code images, fp16 MFMA)"
+                line["data"] = ("synthetic (seeded uniform integer codes, per-channel scales; "
+                                "N(0,1) bf16 q/k/v; random block tables)")
         print(json.dumps(line), flush=True)
         return
 
@@ -575,7 +599,9 @@ def main():
                                       "split-K paged attention per step")
         line["config"]["cache_dtype"] = w["cache"]
         if w["cache"] != "bf16":
-            line["roofline"]["kernel"] = "pa_attention (attn_generic_kernel + split_reduce_kernel)"
+            if w["d"] not in (64, 128):  # byte-coded pages stream at heads 64 / 128 only
+                line["roofline"]["kernel"] = ("pa_attention (attn_generic_kernel + "
+                                              "split_reduce_kernel)")
             line["dtype"] = f"bf16 x {w['cache']}"
     print(json.dumps(line), flush=True)
 
