@@ -195,10 +195,12 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
                       !(linear && c->dtype != act) &&
                       (int64_t)c->num_blocks * c->block_size <= (int64_t)UINT32_MAX &&
                       (int64_t)std::max(b->batch, 0) * (cap / 32 + 2) < (int64_t)INT32_MAX;
-  // Integer pages (int8 / int4 codes): multi-token batches on the planned prefill over operand
-  // images of the codes when the images may be used and fit (else the VALU kernel).
+  // Byte-coded pages (int8 / int4 codes, fp8 e4m3 paged): multi-token batches on the planned
+  // prefill over operand images of the pages when the images may be used and fit (else the VALU
+  // kernel).
   const bool intc = PA_PREFILL_IMAGES && images &&
-                    pa::prefill_int_supported(c->head_dim, act, c->dtype);
+                    pa::prefill_coded_supported(c->head_dim, act, c->dtype) &&
+                    !(linear && c->dtype == PA_DTYPE_FP8_E4M3);
   // Contiguous caches: the streaming decode, the LDS-shared prefill kernels, or VALU.
   if (kind == 0 && linear)
     kind = bal_ok ? 1 : (pa::prefill_mfma_supported(c->head_dim, act, c->dtype) || intc) ? 2 : 3;
@@ -214,8 +216,8 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
     else
       kind = 3;
   }
-  // integer pages run the prefill kernel only over images, i.e. the planned launch
-  if (kind == 2 && pa::prefill_int_supported(c->head_dim, act, c->dtype) && (!intc || chunk > 0))
+  // byte-coded pages run the prefill kernel only over images, i.e. the planned launch
+  if (kind == 2 && pa::prefill_coded_supported(c->head_dim, act, c->dtype) && (!intc || chunk > 0))
     kind = 3;
   pl.kind = kind;
   pl.balanced = kind == 1 && bal_ok;
@@ -261,7 +263,7 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
         }
       }
       if (!(intc && pl.img_steps == 0)) return pl;
-      pl = Plan{};  // integer pages whose images do not fit: see below
+      pl = Plan{};  // byte-coded pages whose images do not fit: see below
       pl.kind = 2;
     } else if (units >= target) {
       chunk = (int)std::min<int64_t>(((int64_t)ctx + 31) / 32 * 32, INT32_MAX / 2);
@@ -273,8 +275,8 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
                                      INT32_MAX / 2);
     }
   }
-  // Integer pages that did not get the planned launch over images: the VALU kernel.
-  if (pl.kind == 2 && pa::prefill_int_supported(c->head_dim, act, c->dtype)) {
+  // Byte-coded pages that did not get the planned launch over images: the VALU kernel.
+  if (pl.kind == 2 && pa::prefill_coded_supported(c->head_dim, act, c->dtype)) {
     kind = 3;
     pl.kind = 3;
     pl.ng = 1;
@@ -382,16 +384,16 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
       return fail(PA_ERR_UNSUPPORTED, "decode MFMA kernel does not cover this dtype/head_dim");
   }
   if (kind == 2 && !pa::prefill_mfma_supported(c->head_dim, act, c->dtype) &&
-      !pa::prefill_int_supported(c->head_dim, act, c->dtype))
+      !pa::prefill_coded_supported(c->head_dim, act, c->dtype))
     return fail(PA_ERR_UNSUPPORTED, "prefill MFMA kernel does not cover this dtype/head_dim");
   if (!(a->softcap >= 0.0f) || !std::isfinite(a->softcap))
     return fail(PA_ERR_INVALID_ARGUMENT, "softcap must be finite and non-negative");
   kind = effective_kind(kind, opts);
   Plan pl = make_plan(c, b, a, act, kind, chunk, opts.linear_cap > 0, opts.linear_cap,
                       opts.images);
-  if (kind == 2 && pl.kind != 2 && pa::prefill_int_supported(c->head_dim, act, c->dtype))
+  if (kind == 2 && pl.kind != 2 && pa::prefill_coded_supported(c->head_dim, act, c->dtype))
     return fail(PA_ERR_UNSUPPORTED,
-                "prefill MFMA kernel: integer pages run on it over operand images only (planned "
+                "prefill MFMA kernel: byte-coded pages run on it over operand images only (planned "
                 "launch, automatic chunking, images within the workspace)");
   if (opts.linear_cap > 0 && !(pl.balanced || pl.kind == 2 || pl.kind == 3))
     return fail(PA_ERR_UNSUPPORTED,

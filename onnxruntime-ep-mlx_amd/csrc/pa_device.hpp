@@ -430,7 +430,7 @@ bool decode_mfma_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype);
 // pages, pages in the activation dtype or (d 64 / 128) fp8 e4m3 with at least 16 rows per page.
 bool balanced_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype, int block_size);
 bool prefill_mfma_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype);
-bool prefill_int_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype);
+bool prefill_coded_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype);
 bool prefill_planned_supported(int head_dim);
 
 }  // namespace pa

@@ -617,11 +617,14 @@ __device__ __forceinline__ void img_issue(MxBufT<KB, D>& buf, int wave, int lane
 // INTC: integer pages (images of fp16 codes): per-channel / per-tensor key scales fold into the
 // query, normalised per row by a power of two whose exponent joins the row's softmax scale; the
 // scores run on fp16 products; value scales multiply the output per dim before normalisation.
-template <typename TT, bool CAP, bool IMG, int D = 128, bool INTC = false>
+// F8S: fp8 pages (images of the dequantised rows in fp16, keys and values each under a per-step
+// power of two): the query rows go to fp16 under a per-row power of two as for INTC, and each
+// step's key exponent joins the softmax scale of the step.
+template <typename TT, bool CAP, bool IMG, int D = 128, bool INTC = false, bool F8S = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, IMG && D <= 128 ? PA_IMG_WAVES : 2))) void
 prefill_mx_kernel(const AttnParams p) {
-  static_assert(!INTC || IMG, "integer pages over images only");
-  using KT = typename std::conditional<INTC, TF16, TT>::type;  // score operand type
+  static_assert(!(INTC || F8S) || IMG, "byte-coded pages over images only");
+  using KT = typename std::conditional<INTC || F8S, TF16, TT>::type;  // score operand type
   constexpr int ROWS = kPrefillRows;
   static_assert(ROWS == 128, "four wavefronts of 32 rows");
   static_assert(IMG ? img_head(D) : D == 128, "images at heads 64 / 96 / 128 / 256, in-loop staging at 128");
@@ -701,11 +704,12 @@ prefill_mx_kernel(const AttnParams p) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
       qv[ks] = rvalid ? (ld16(qrow + 32 * ks) ^ qxor) : u32x4{0u, 0u, 0u, 0u};
-    if constexpr (INTC) {
+    if constexpr (INTC || F8S) {
       // q * key scale in fp32 (dims 16 ks + 8 h + e of this lane), scaled by 2^-er so the bound
       // max|q| (the row) x max|scale| (the kv-head) lies below 2^14, then fp16 (RNE), one product
-      // at a time: scores = 2^er * (q16 . codes)
-      const bool kpc = p.k_quant == PA_QUANT_PER_CHANNEL;
+      // at a time: scores = 2^er * (q16 . codes).  fp8 pages: no scale here (the images hold the
+      // dequantised keys), max|scale| = 1.
+      const bool kpc = INTC && p.k_quant == PA_QUANT_PER_CHANNEL;
       float mq = 0.0f;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
@@ -713,12 +717,15 @@ prefill_mx_kernel(const AttnParams p) {
         for (int e = 0; e < 8; ++e)
           mq = fmaxf(mq, fabsf(TT::to_f32((uint16_t)(qv[ks][e >> 1] >> (16 * (e & 1))))));
       mq = fmaxf(mq, other_half(mq));
-      float ms = 0.0f;
-      if (kpc) {
-        for (int d = lane; d < D; d += 64) ms = fmaxf(ms, fabsf(p.k_scale[(int64_t)kh * D + d]));
-        ms = wave_max_f(ms);
-      } else {
-        ms = fabsf(p.k_scale[0]);
+      float ms = 1.0f;
+      if constexpr (INTC) {
+        if (kpc) {
+          ms = 0.0f;
+          for (int d = lane; d < D; d += 64) ms = fmaxf(ms, fabsf(p.k_scale[(int64_t)kh * D + d]));
+          ms = wave_max_f(ms);
+        } else {
+          ms = fabsf(p.k_scale[0]);
+        }
       }
       const float bound = mq * ms;
       const int er = bound > 0.0f ? __builtin_amdgcn_frexp_expf(bound) - 14 : 0;
@@ -727,8 +734,8 @@ prefill_mx_kernel(const AttnParams p) {
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
           const int d0 = 16 * ks + 8 * h + 2 * m;
-          const float s0v = p.k_scale[kpc ? (int64_t)kh * D + d0 : 0];
-          const float s1v = p.k_scale[kpc ? (int64_t)kh * D + d0 + 1 : 0];
+          const float s0v = INTC ? p.k_scale[kpc ? (int64_t)kh * D + d0 : 0] : 1.0f;
+          const float s1v = INTC ? p.k_scale[kpc ? (int64_t)kh * D + d0 + 1 : 0] : 1.0f;
           const float a = TT::to_f32((uint16_t)qv[ks][m]) * s0v;
           const float c = TT::to_f32((uint16_t)(qv[ks][m] >> 16)) * s1v;
           const f16x2v ph = __builtin_convertvector(
@@ -781,14 +788,17 @@ prefill_mx_kernel(const AttnParams p) {
   // IMG: the accumulator's value exponent (output in units of 2^s_acc; no step seen yet: far below
   // any step's) -- each step's image holds its values in units of 2^sj.
   int s_acc = -(1 << 29);
-  auto attend = [&](const f32x16(&sc)[KB], int t0, const Buf& buf, int sj) __attribute__((always_inline)) {
+  auto attend = [&](const f32x16(&sc)[KB], int t0, const Buf& buf, int sj, int ek) __attribute__((always_inline)) {
+    // the step's score scale (fp8 pages: its keys are in units of 2^ek)
+    const float sl2 = F8S ? __builtin_ldexpf(scale_log2, ek) : scale_log2;
+    const float ck = F8S ? __builtin_ldexpf(cap_k, ek) : cap_k;
     float x[KB][16];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         float v = sc[kb][i];
-        if constexpr (CAP) v = softcap_log2(v, cap_k, cap_l2);
+        if constexpr (CAP) v = softcap_log2(v, ck, cap_l2);
         x[kb][i] = v;
       }
     // per-score position tests only on steps some row does not see whole (one scalar branch):
@@ -813,7 +823,7 @@ prefill_mx_kernel(const AttnParams p) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) lmax = fmaxf(lmax, x[kb][i]);
     lmax = fmaxf(lmax, other_half(lmax));
-    if constexpr (!CAP) lmax *= scale_log2;
+    if constexpr (!CAP) lmax *= sl2;
     if (__any(lmax > m_run + 8.0f)) {
       const float m_new = fmaxf(m_run, lmax);
       const float alpha = (m_run == kNegInf || m_new == kNegInf) ? 1.0f : exp2f(m_run - m_new);
@@ -873,7 +883,7 @@ prefill_mx_kernel(const AttnParams p) {
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i)
-          l_part += __builtin_amdgcn_exp2f(CAP ? x[kb][i] - m0 : __builtin_fmaf(x[kb][i], scale_log2, -m0));
+          l_part += __builtin_amdgcn_exp2f(CAP ? x[kb][i] - m0 : __builtin_fmaf(x[kb][i], sl2, -m0));
       return;
     }
     const float msafe = ((m_run == kNegInf) ? 0.0f : m_run) + (float)dsh;
@@ -885,7 +895,7 @@ prefill_mx_kernel(const AttnParams p) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         pv[i] = __builtin_amdgcn_exp2f(CAP ? x[kb][i] - msafe
-                                           : __builtin_fmaf(x[kb][i], scale_log2, -msafe));
+                                           : __builtin_fmaf(x[kb][i], sl2, -msafe));
       }
 #pragma unroll
       for (int half = 0; half < 2; ++half)
@@ -925,6 +935,11 @@ prefill_mx_kernel(const AttnParams p) {
     for (int k = 0; k < nsteps; ++k) {
       const int t0 = t_first + KEYS * k;
       sj = __builtin_amdgcn_readfirstlane(sj_next);
+      int ek = 0;
+      if constexpr (F8S) {  // fp8 pages: key exponent above, value exponent below
+        ek = sj >> 16;
+        sj = (int)(int16_t)(sj & 0xffff);
+      }
       if (k + 1 < nsteps) {
         img_issue(lds[(k + 1) & 1], wave, lane, t0 + KEYS, img_hb);
         sj_next = vstep_hb[t0 / KEYS + 1];
@@ -932,7 +947,7 @@ prefill_mx_kernel(const AttnParams p) {
       if (seen(t0)) {
         f32x16 sc[KB];
         scores(lds[k & 1], sc);
-        attend(sc, t0, lds[k & 1], sj);
+        attend(sc, t0, lds[k & 1], sj, ek);
       }
       wait_vmem();
       __syncthreads();
@@ -955,7 +970,7 @@ prefill_mx_kernel(const AttnParams p) {
       if (seen(t0)) {
         f32x16 sc[KB];
         scores(lds[k & 1], sc);
-        attend(sc, t0, lds[k & 1], 0);
+        attend(sc, t0, lds[k & 1], 0, 0);
       }
       if (k + 1 < nsteps) mx_store<TT>(lds[(k + 1) & 1], st, wave, lane, t0 + KEYS, total, s_stage);
       if (k + 2 < nsteps) mx_load<TT>(w, pw, wave, lane, t0 + 2 * KEYS, st);
@@ -1117,6 +1132,7 @@ struct ImgGroup {
   static constexpr int KEYS = img_keys(D), PCS = 256 / KEYS, CH = (D / 8) / PCS;
   static_assert(CH * PCS * 8 == D, "whole chunks per thread");
   u32x4 kx[CH], vx[CH];
+  float ks, vs;  // fp8 pages: the row's key / value page scales
   int64_t hb;
   int j, r, q;
   bool step_live;
@@ -1124,8 +1140,10 @@ struct ImgGroup {
 
 // Page codes of integer caches (KC: kImgI8 / kImgI4) load as 32-bit words and widen exactly to
 // fp16 (int8 codes; int4 nibbles, low nibble first, biased by +8), so the images hold the codes
-// and the scales apply outside the products.
-constexpr int kImgT = 0, kImgI8 = 1, kImgI4 = 2;
+// and the scales apply outside the products.  fp8 pages (kImgF8) load their e4m3 codes (words 0
+// and 1 of each chunk) and the row's page scales; img_store dequantises them (code x scale in
+// fp32) and writes keys and values as fp16 under per-step powers of two.
+constexpr int kImgT = 0, kImgI8 = 1, kImgI4 = 2, kImgF8 = 3;
 template <int KC>
 __device__ __forceinline__ uint32_t f16_pair(int a, int b) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)a) |
@@ -1189,16 +1207,72 @@ __device__ __forceinline__ void img_load(const AttnParams& p, int id, ImgGroup<N
       g.vx[i] = live ? ld16(vs + 16 * i) : u32x4{0u, 0u, 0u, 0u};
     }
   } else {
-    // code rows: D bytes (int8) or D / 2 (int4) per kv-head
-    constexpr int RB = KC == kImgI8 ? D : D / 2;
+    // code rows: D bytes (int8, fp8) or D / 2 (int4) per kv-head
+    constexpr int RB = KC == kImgI4 ? D / 2 : D;
     w.rowb = w.lin_row0 >= 0 ? RB : (int64_t)p.kv_heads * RB;
     w.hoff = w.lin_row0 >= 0 ? 0 : (int64_t)kh * RB;
-    const int cb = (KC == kImgI8 ? 8 : 4) * CH * g.q;  // bytes before this thread's codes
+    const int cb = (KC == kImgI4 ? 4 : 8) * CH * g.q;  // bytes before this thread's codes
     const char* ks = live ? row_ptr(w, pos, false, D) + cb : nullptr;
     const char* vs = live ? row_ptr(w, pos, true, D) + cb : nullptr;
-    load_codes<KC, CH>(ks, live, g.kx);
-    load_codes<KC, CH>(vs, live, g.vx);
+    if constexpr (KC == kImgF8) {
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        const u32x2 kw = live ? reinterpret_cast<const u32x2*>(ks)[i] : u32x2{0u, 0u};
+        const u32x2 vw = live ? reinterpret_cast<const u32x2*>(vs)[i] : u32x2{0u, 0u};
+        g.kx[i] = u32x4{kw[0], kw[1], 0u, 0u};
+        g.vx[i] = u32x4{vw[0], vw[1], 0u, 0u};
+      }
+      // page scales of the row's block (paged caches only: every row is read from the pages)
+      g.ks = g.vs = 0.0f;
+      if (live) {
+        const int bi = min(div_bs(pos, w), w.max_blocks - 1);
+        const int64_t blk = min(max((int64_t)w.bt[bi], (int64_t)0), w.num_blocks - 1);
+        g.ks = p.k_scale[blk * p.kv_heads + kh];
+        g.vs = p.v_scale[blk * p.kv_heads + kh];
+      }
+    } else {
+      load_codes<KC, CH>(ks, live, g.kx);
+      load_codes<KC, CH>(vs, live, g.vx);
+    }
   }
+}
+
+// fp8 pages: the largest |e4m3 code| of a thread's chunks (the magnitude order of e4m3 is the
+// integer order of its low seven bits; 0x7f, NaN, counts as the largest), then as fp32.
+template <int CH>
+__device__ __forceinline__ float f8_chunks_absmax(const u32x4 (&x)[CH]) {
+  using u8x4 = unsigned char __attribute__((ext_vector_type(4)));
+  u8x4 m = u8x4{0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < CH; ++i)
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      m = __builtin_elementwise_max(m, __builtin_bit_cast(u8x4, x[i][k] & 0x7f7f7f7fu));
+  const unsigned c = max(max((unsigned)m[0], (unsigned)m[1]), max((unsigned)m[2], (unsigned)m[3]));
+  return e4m3_to_f32(c);
+}
+
+// fp8 pages: 8 e4m3 codes (words 0, 1 of x) times f (page scale x 2^-s) as 4 fp16 pairs (RNE).
+// Each code pair widens exactly to fp16 with one v_cvt_scalef32_pk_f16_fp8 at scale 1.0 (the
+// decode's widening: every e4m3 value is an fp16 value, NaN stays NaN), then to fp32.
+__device__ __forceinline__ u32x4 f8_chunk_f16(const u32x4& x, float f) {
+  const f16x2v c[4] = {
+      __builtin_bit_cast(f16x2v, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x[0], 1.0f, false)),
+      __builtin_bit_cast(f16x2v, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x[0], 1.0f, true)),
+      __builtin_bit_cast(f16x2v, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x[1], 1.0f, false)),
+      __builtin_bit_cast(f16x2v, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x[1], 1.0f, true))};
+  u32x4 o;
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+    o[m] = __builtin_bit_cast(
+        uint32_t, __builtin_convertvector(f32x2v{(float)c[m][0] * f, (float)c[m][1] * f}, f16x2v));
+  return o;
+}
+
+// Exponent s of a step whose largest |value| is mx: mx * 2^-s lies in [2^14, 2^15) of fp16; the
+// biased form (s + 256 > 0, 0 for a step of zeros) takes the group maximum as an integer.
+__device__ __forceinline__ int f8_step_exp_biased(float mx) {
+  return mx > 0.0f ? __builtin_amdgcn_frexp_expf(mx) - 15 + 256 : 0;
 }
 
 template <typename TT, int NT, int D, int KC>
@@ -1210,16 +1284,21 @@ __device__ __forceinline__ void img_store(const AttnParams& p, ImgGroup<NT, D>& 
   constexpr bool BF = std::is_same<TT, TBF16>::value && KC == kImgT;
   const int tid = threadIdx.x, grp = tid / 256, r = g.r, q = g.q;
   char* dst = p.vimg + (g.hb * p.img_steps + g.j) * (int64_t)SB;
-  if (g.step_live) {
+  auto store_keys = [&]() {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int dc = CH * q + i;
       *reinterpret_cast<u32x4*>(dst + ((((r >> 5) * (D / 16) + (dc >> 1)) * 64) + 32 * (dc & 1) + (r & 31)) * 16) =
           g.kx[i];
     }
-  }
+  };
+  if (KC != kImgF8 && g.step_live) store_keys();
   // the step's largest biased exponent of |value| (bf16; every wavefront of a group, then LDS)
-  int e = 0;
+  int e = 0, ek = 0;
+  if constexpr (KC == kImgF8) {  // values and keys: exponents of the dequantised maxima
+    e = wave_max_nonneg(f8_step_exp_biased(f8_chunks_absmax<CH>(g.vx) * fabsf(g.vs)));
+    ek = wave_max_nonneg(f8_step_exp_biased(f8_chunks_absmax<CH>(g.kx) * fabsf(g.ks)));
+  }
   if constexpr (BF) {
     uint32_t mx = 0;
 #pragma unroll
@@ -1231,12 +1310,28 @@ __device__ __forceinline__ void img_store(const AttnParams& p, ImgGroup<NT, D>& 
                                                           __builtin_bit_cast(u16x2, g.vx[i][m] & 0x7fff7fffu)));
     e = wave_max_nonneg((int)(max(mx & 0xffffu, mx >> 16) >> 7));
   }
-  if (tid < NT / 256) emax[tid] = 0;
+  if (tid < 2 * (NT / 256)) emax[tid] = 0;
   __syncthreads();
-  if ((tid & 63) == 0) atomicMax(&emax[grp], e);
+  if ((tid & 63) == 0) {
+    atomicMax(&emax[grp], e);
+    if (KC == kImgF8) atomicMax(&emax[NT / 256 + grp], ek);
+  }
   __syncthreads();
   // bf16: s = emax - 141 puts the largest value into [2^14, 2^15) of fp16; fp16: s = 0
-  const int sc = BF ? max(emax[grp] - 141, -112) : 0;
+  int sc = BF ? max(emax[grp] - 141, -112) : 0;
+  if constexpr (KC == kImgF8) {
+    // fp8: code x page scale x 2^-s in fp16 (keys under their own s), both exponents to vstep
+    const int sv = emax[grp] > 0 ? emax[grp] - 256 : 0;
+    const int sk = emax[NT / 256 + grp] > 0 ? emax[NT / 256 + grp] - 256 : 0;
+    const float fk = __builtin_ldexpf(g.ks, -sk), fv = __builtin_ldexpf(g.vs, -sv);
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      g.kx[i] = f8_chunk_f16(g.kx[i], fk);
+      g.vx[i] = f8_chunk_f16(g.vx[i], fv);
+    }
+    if (g.step_live) store_keys();
+    sc = (int)((uint32_t)sk << 16 | ((uint32_t)sv & 0xffffu));
+  }
   if constexpr (BF) {
     // bf16 exponent E -> fp16 exponent E - 112 - s: subtract (112 + s) << 7 from the magnitude
     // bits (saturating: values below the fp16 range flush towards zero), shift into place
@@ -1289,7 +1384,7 @@ template <typename TT, int NT, int D, int KC>
 __device__ __forceinline__ void image_steps(const AttnParams& p, int id) {
   constexpr int SPW = NT / 256;
   __shared__ uint32_t rows[SPW][img_keys(D)][D / 2 + 1];  // fp16 value rows, one word = two dims
-  __shared__ int emax[SPW];
+  __shared__ int emax[2 * SPW];  // per step: value exponent, then (fp8 pages) key exponent
   const int nj = (p.img_steps + SPW - 1) / SPW;
   if (id >= nj * p.kv_heads * p.batch) return;
   ImgGroup<NT, D> g;
@@ -1472,16 +1567,24 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const AttnParams p) 
   }
 }
 
+// Page kinds of the prefill launch: pages in the activation dtype, integer codes, fp8 codes.
+constexpr int kPkT = 0, kPkInt = 1, kPkF8 = 2;
+
 template <typename TT, int D>
-hipError_t launch_d(const AttnParams& p, dim3 grid, hipStream_t s, bool intc = false) {
+hipError_t launch_d(const AttnParams& p, dim3 grid, hipStream_t s, int pk = kPkT) {
   constexpr int NG = kPrefillGroups;
   if constexpr (img_head(D)) {
     if (p.vimg != nullptr) {
-      if (intc) {
+      if (pk == kPkInt) {
         if (p.softcap > 0.0f)
           hipLaunchKernelGGL((prefill_mx_kernel<TT, true, true, D, true>), grid, dim3(256), 0, s, p);
         else
           hipLaunchKernelGGL((prefill_mx_kernel<TT, false, true, D, true>), grid, dim3(256), 0, s, p);
+      } else if (pk == kPkF8) {
+        if (p.softcap > 0.0f)
+          hipLaunchKernelGGL((prefill_mx_kernel<TT, true, true, D, false, true>), grid, dim3(256), 0, s, p);
+        else
+          hipLaunchKernelGGL((prefill_mx_kernel<TT, false, true, D, false, true>), grid, dim3(256), 0, s, p);
       } else if (p.softcap > 0.0f) {
         hipLaunchKernelGGL((prefill_mx_kernel<TT, true, true, D>), grid, dim3(256), 0, s, p);
       } else {
@@ -1490,7 +1593,7 @@ hipError_t launch_d(const AttnParams& p, dim3 grid, hipStream_t s, bool intc = f
       return hipGetLastError();
     }
   }
-  if (intc) return hipErrorInvalidValue;  // integer pages run over images only
+  if (pk != kPkT) return hipErrorInvalidValue;  // byte-coded pages run over images only
   if constexpr (D == 128) {
     const bool cap = p.softcap > 0.0f;
     if (cap) {
@@ -1508,12 +1611,12 @@ hipError_t launch_d(const AttnParams& p, dim3 grid, hipStream_t s, bool intc = f
 }
 
 template <typename TT>
-hipError_t launch_t(const AttnParams& p, dim3 grid, hipStream_t s, bool intc = false) {
+hipError_t launch_t(const AttnParams& p, dim3 grid, hipStream_t s, int pk = kPkT) {
   switch (p.head_dim) {
-    case 64: return launch_d<TT, 64>(p, grid, s, intc);
-    case 96: return launch_d<TT, 96>(p, grid, s, intc);
-    case 128: return launch_d<TT, 128>(p, grid, s, intc);
-    case 256: return launch_d<TT, 256>(p, grid, s, intc);
+    case 64: return launch_d<TT, 64>(p, grid, s, pk);
+    case 96: return launch_d<TT, 96>(p, grid, s, pk);
+    case 128: return launch_d<TT, 128>(p, grid, s, pk);
+    case 256: return launch_d<TT, 256>(p, grid, s, pk);
     default: return hipErrorInvalidValue;
   }
 }
@@ -1538,9 +1641,10 @@ hipError_t launch_prefill_merge(const AttnParams& p, hipStream_t s) {
 // (workgroups past the planned count exit at once), then the merge of the split items.
 hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
                                   hipStream_t s) {
-  // integer pages: over operand images of their codes only
-  const bool intc = prefill_int_supported(p.head_dim, act, cache_dtype);
-  if (intc ? (p.vimg == nullptr || !p.k_scale || !p.v_scale)
+  // byte-coded pages (integer, fp8): over operand images of their rows only
+  const bool coded = prefill_coded_supported(p.head_dim, act, cache_dtype);
+  const int pk = !coded ? kPkT : cache_dtype == PA_DTYPE_FP8_E4M3 ? kPkF8 : kPkInt;
+  if (coded ? (p.vimg == nullptr || !p.k_scale || !p.v_scale)
            : (!prefill_mfma_supported(p.head_dim, act, cache_dtype) ||
               !prefill_planned_supported(p.head_dim)))
     return hipErrorInvalidValue;
@@ -1573,6 +1677,8 @@ hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype ca
         plan(tt, dd, std::integral_constant<int, kImgI8>{});
       else if (cache_dtype == PA_DTYPE_INT4)
         plan(tt, dd, std::integral_constant<int, kImgI4>{});
+      else if (cache_dtype == PA_DTYPE_FP8_E4M3)
+        plan(tt, dd, std::integral_constant<int, kImgF8>{});
       else
         plan(tt, dd, std::integral_constant<int, kImgT>{});
     };
@@ -1590,17 +1696,20 @@ hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype ca
       by_head(TBF16{});
   }
   const dim3 grid(2 * p.plan_items, 1);
-  hipError_t e = act == PA_DTYPE_FLOAT16 ? launch_t<TF16>(p, grid, s, intc)
-                                         : launch_t<TBF16>(p, grid, s, intc);
+  hipError_t e = act == PA_DTYPE_FLOAT16 ? launch_t<TF16>(p, grid, s, pk)
+                                         : launch_t<TBF16>(p, grid, s, pk);
   if (e != hipSuccess) return e;
   return act == PA_DTYPE_FLOAT16 ? launch_prefill_merge<TF16>(p, s)
                                  : launch_prefill_merge<TBF16>(p, s);
 }
 
-// Integer pages (int8 / int4 codes with fp32 scales) on the planned prefill over operand images.
-bool prefill_int_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype) {
+// Byte-coded pages (int8 / int4 codes with fp32 scales, fp8 e4m3 with per-(block, kv-head)
+// scales) on the planned prefill over operand images.
+bool prefill_coded_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype) {
   if (act != PA_DTYPE_FLOAT16 && act != PA_DTYPE_BFLOAT16) return false;
-  if (cache_dtype != PA_DTYPE_INT8 && cache_dtype != PA_DTYPE_INT4) return false;
+  if (cache_dtype != PA_DTYPE_INT8 && cache_dtype != PA_DTYPE_INT4 &&
+      cache_dtype != PA_DTYPE_FP8_E4M3)
+    return false;
   return img_head(head_dim);
 }
 

@@ -136,5 +136,5 @@ def test_int_prefill_kernel_level_kinds(d, bits, dtype):
     for out in (mx, valu):
         got = orc.decode(from_torch(out, dtype), dtype).astype(np.float64)
         _check_rows(got, ref, None, c["cum"], dtype)
-    with pytest.raises(Exception, match="integer pages"):
+    with pytest.raises(Exception, match="over operand images only"):
         _attention(c, kc, vc, 2, chunk=64)
