@@ -57,9 +57,9 @@ def parse():
                     help="c3 (default): BASELINE.json config 3; c4 / c5: configs 4 / 5")
     ap.add_argument("--head-dim", type=int, default=128, choices=(64, 96, 128, 256),
                     help="c3 / c4: the same batch at another head size (128 = the config)")
-    ap.add_argument("--cache-dtype", default="bf16", choices=("bf16", "int8", "int4"),
+    ap.add_argument("--cache-dtype", default="bf16", choices=("bf16", "int8", "int4", "fp8"),
                     help="c3 / c4: the same batch over int8 / int4 pages with per-channel "
-                         "fp32 scales (bf16 = the config)")
+                         "fp32 scales (bf16 = the config); c4 also over fp8 e4m3 pages")
     return ap.parse_args()
 
 
@@ -127,7 +127,8 @@ def build_prefill_workload(torch, seed=4, d=128, cache="bf16"):
     context U[0, 4096], 28 query / 4 kv heads, d 128, block 16, causal within the chunk, packed
     cumulative_sequence_length, values N(0,1).  No rotary (the config names none).
     cache int8 / int4: the same batch over integer pages (codes uniform over the code range,
-    per-channel fp32 scales [KV, d] of U[0.5, 1.5) / 64)."""
+    per-channel fp32 scales [KV, d] of U[0.5, 1.5) / 64); fp8: over e4m3 pages, N(0,1) quantised
+    with scale amax / 448 per (block, kv-head) as config 5 draws them."""
     import numpy as np
     rng = np.random.default_rng(seed)
     B, H, KV, bs, chunk = 8, 28, 4, 16, 512
@@ -141,6 +142,15 @@ def build_prefill_workload(torch, seed=4, d=128, cache="bf16"):
     if cache == "bf16":
         kc = torch.randn((nb, bs, KV, d), generator=g, device=dev).to(torch.bfloat16)
         vc = torch.randn((nb, bs, KV, d), generator=g, device=dev).to(torch.bfloat16)
+    elif cache == "fp8":
+        kc = torch.empty((nb, bs, KV, d), dtype=torch.float8_e4m3fn, device=dev)
+        vc = torch.empty_like(kc)
+        ks = torch.empty((nb, KV), dtype=torch.float32, device=dev)
+        vs = torch.empty_like(ks)
+        for t, sc in ((kc, ks), (vc, vs)):
+            x = torch.randn((nb, bs, KV, d), generator=g, device=dev)
+            sc.copy_((x.abs().amax(dim=(1, 3)) / 448.0).clamp_min(1e-12))
+            t.copy_((x / sc[:, None, :, None]).to(torch.float8_e4m3fn))
     else:
         width, dt = (d, torch.int8) if cache == "int8" else (d // 2, torch.uint8)
         lo, hi = (-128, 128) if cache == "int8" else (0, 256)
@@ -151,7 +161,7 @@ def build_prefill_workload(torch, seed=4, d=128, cache="bf16"):
     T = B * chunk
     w = dict(B=B, T=T, mq=chunk, H=H, KV=KV, d=d, bs=bs, nb=nb, ctx=past + chunk, bt_np=bt,
              kc=kc, vc=vc, cos=None, sin=None, ks=ks, vs=vs, cache=cache,
-             quant="NONE" if cache == "bf16" else "PER_CHANNEL",
+             quant="PER_CHANNEL" if cache in ("int8", "int4") else "NONE",
              q=torch.randn((T, H * d), generator=g, device=dev).to(torch.bfloat16),
              k=torch.randn((T, KV * d), generator=g, device=dev).to(torch.bfloat16),
              v=torch.randn((T, KV * d), generator=g, device=dev).to(torch.bfloat16))
@@ -475,6 +485,13 @@ def main():
               "(decode shards by sequence or kv-head with no exchange between GPUs)",
               file=sys.stderr)
         sys.exit(2)
+    if args.config == "c5" and args.cache_dtype != "bf16":
+        print("bench.py: --cache-dtype applies to c3 and c4 (c5 is the e4m3 config)",
+              file=sys.stderr)
+        sys.exit(2)
+    if args.config == "c3" and args.cache_dtype == "fp8":
+        print("bench.py: the fp8 decode batch is config 5 (--config c5)", file=sys.stderr)
+        sys.exit(2)
     import torch
     import onnxruntime_ep_mlx_amd as ep
     torch.cuda.set_device(0)
@@ -485,10 +502,6 @@ def main():
         w = build_prefill_workload(torch, d=args.head_dim, cache=args.cache_dtype)
         step = Step(torch, ep, w, args.chunk, kind=0)
     else:
-        if args.cache_dtype != "bf16":
-            print("bench.py: --cache-dtype applies to c3 and c4 (c5 is the e4m3 config)",
-                  file=sys.stderr)
-            sys.exit(2)
         w = build_fp8_workload(torch)
         step = Step(torch, ep, w, args.chunk, kind=0)
     # bytes per K or V element: fp8 / int8 pages 1, int4 pages 1/2, bf16 2
@@ -551,10 +564,14 @@ def main():
             what = f"head_dim {w['d']}" + ("" if cache == "bf16" else f", {cache} pages")
             line["metric"] += f" ({what} variant of config 4)"
             line["config"]["cache_dtype"] = cache
-            if cache != "bf16":
+            if cache in ("int8", "int4"):
                 line["dtype"] = f"bf16 x {cache} (fp16 code images, fp16 MFMA)"
                 line["data"] = ("synthetic (seeded uniform integer codes, per-channel scales; "
                                 "N(0,1) bf16 q/k/v; random block tables)")
+            elif cache == "fp8":
+                line["dtype"] = "bf16 x e4m3 (fp16 images of the dequantised rows, fp16 MFMA)"
+                line["data"] = ("synthetic (seeded N(0,1) quantised to e4m3 with amax/448 "
+                                "block scales; N(0,1) bf16 q/k/v; random block tables)")
         print(json.dumps(line), flush=True)
         return
 
