@@ -458,6 +458,80 @@ __global__ __launch_bounds__(256) void copy_append_kernel(const AppendParams p, 
   }
 }
 
+// Quantising append for byte-coded pages (int8, int4, fp8 e4m3): no rotary or norm, paged,
+// every token's slot distinct, 16-bit activations, head_dim % 8 == 0.  One wavefront per token,
+// lane l takes elements 8 l .. 8 l + 7 of each 512-element piece of the token's key and value rows
+// (all kv-heads, contiguous in the input and in the slot): one 16-byte load per row, the codes
+// of int_code / f32_to_e4m3_sat (the per-row kernel's arithmetic, so the bytes are identical),
+// one 8-byte (int8, fp8) or 4-byte (int4) store.  The first piece's rows load before the slot
+// lookup resolves.
+template <typename TT, int CK>
+__global__ __launch_bounds__(256) void quant_append_kernel(const AppendParams p) {
+  static_assert(CK != kCacheT, "byte-coded pages");
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= p.num_tokens) return;  // whole wavefront
+  const int D = p.head_dim, n = p.kv_heads * D;
+  using raw = typename TT::raw;
+  const raw* ks = reinterpret_cast<const raw*>(p.key) + (int64_t)t * p.k_ld;
+  const raw* vs = reinterpret_cast<const raw*>(p.value) + (int64_t)t * p.v_ld;
+  u32x4 kx = u32x4{0u, 0u, 0u, 0u}, vx = kx;
+  if (8 * lane < n) {
+    kx = *reinterpret_cast<const u32x4*>(ks + 8 * lane);
+    vx = *reinterpret_cast<const u32x4*>(vs + 8 * lane);
+  }
+  const SeqPos sp = seq_pos_of_token(p.cum, p.past, p.batch, t);
+  const int64_t pos = (int64_t)max(sp.past, 0) + (t - sp.start);
+  int64_t slot = p.slot_mapping ? (int64_t)p.slot_mapping[t] : slot_at(p, sp.b, pos);
+  if (slot >= p.num_blocks * p.block_size) slot = -1;
+  if (slot < 0) return;
+  constexpr int EB = CK == kCacheI4 ? 4 : 8;  // code bytes per 8 elements
+  uint8_t* kd = reinterpret_cast<uint8_t*>(p.key_cache) + slot * (int64_t)(n / 8 * EB);
+  uint8_t* vd = reinterpret_cast<uint8_t*>(p.value_cache) + slot * (int64_t)(n / 8 * EB);
+  const int64_t blk = slot / p.block_size;
+  const bool recip = p.quant_reciprocal != 0;
+  const bool kpc = p.k_quant == PA_QUANT_PER_CHANNEL, vpc = p.v_quant == PA_QUANT_PER_CHANNEL;
+  for (int e0 = 8 * lane; e0 < n; e0 += 512) {
+    if (e0 != 8 * lane) {
+      kx = *reinterpret_cast<const u32x4*>(ks + e0);
+      vx = *reinterpret_cast<const u32x4*>(vs + e0);
+    }
+    const int kh = e0 / D;
+#pragma unroll
+    for (int side = 0; side < 2; ++side) {
+      const u32x4 x = side ? vx : kx;
+      const float* sc = side ? p.v_scale : p.k_scale;
+      const bool pc = side ? vpc : kpc;
+      uint32_t code[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float v = TT::to_f32((uint16_t)(x[i >> 1] >> (16 * (i & 1))));
+        if constexpr (CK == kCacheFp8) {
+          const float s8 = sc[blk * p.kv_heads + kh];
+          code[i] = s8 == 0.0f ? 0u : f32_to_e4m3_sat(v / s8);
+        } else {
+          const float si = sc[pc ? e0 + i : 0];  // per channel: [kv_heads, D] = element order
+          code[i] = CK == kCacheI4
+                        ? (uint32_t)(int_code(v, si, recip, -8.0f, 7.0f) + 8)
+                        : (uint32_t)(uint8_t)(int8_t)int_code(v, si, recip, -128.0f, 127.0f);
+        }
+      }
+      uint8_t* dst = (side ? vd : kd) + e0 / 8 * EB;
+      if constexpr (CK == kCacheI4) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w |= (code[2 * j] | (code[2 * j + 1] << 4)) << (8 * j);
+        *reinterpret_cast<uint32_t*>(dst) = w;
+      } else {
+        u32x2 w = u32x2{0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i >> 2] |= (code[i] & 0xffu) << (8 * (i & 3));
+        *reinterpret_cast<u32x2*>(dst) = w;
+      }
+    }
+  }
+}
+
 }  // namespace
 
 template <typename TT>
@@ -498,6 +572,35 @@ hipError_t launch_rotary_append(const AppendParams& p, pa_dtype act, pa_dtype ca
     if ((align & 15) == 0 && row_bytes <= kCopyChunks * 64 * 16) {
       hipLaunchKernelGGL(copy_append_kernel, dim3((p.num_tokens + 3) / 4), dim3(256), 0, s, p,
                          (int)row_bytes);
+      return hipGetLastError();
+    }
+  }
+  const bool coded = cache_dtype == PA_DTYPE_INT8 || cache_dtype == PA_DTYPE_INT4 ||
+                     cache_dtype == PA_DTYPE_FP8_E4M3;
+  if (coded && (act == PA_DTYPE_FLOAT16 || act == PA_DTYPE_BFLOAT16) && !transform &&
+      p.linear_cap <= 0 && p.slots_distinct && p.key && p.value && p.key_cache &&
+      p.value_cache && p.k_scale && p.v_scale && !p.v_out && p.head_dim % 8 == 0) {
+    // 16-byte input rows, 8-byte (int4: 4-byte) code rows
+    const uintptr_t in_align = (uintptr_t)p.key | (uintptr_t)p.value | (uintptr_t)(p.k_ld * 2) |
+                               (uintptr_t)(p.v_ld * 2);
+    const uintptr_t out_align = (uintptr_t)p.key_cache | (uintptr_t)p.value_cache;
+    if ((in_align & 15) == 0 && (out_align & (cache_dtype == PA_DTYPE_INT4 ? 3 : 7)) == 0) {
+      const dim3 qg((p.num_tokens + 3) / 4);
+      const bool h = act == PA_DTYPE_FLOAT16;
+      switch (cache_dtype) {
+        case PA_DTYPE_INT8:
+          if (h) hipLaunchKernelGGL((quant_append_kernel<TF16, kCacheI8>), qg, dim3(256), 0, s, p);
+          else hipLaunchKernelGGL((quant_append_kernel<TBF16, kCacheI8>), qg, dim3(256), 0, s, p);
+          break;
+        case PA_DTYPE_INT4:
+          if (h) hipLaunchKernelGGL((quant_append_kernel<TF16, kCacheI4>), qg, dim3(256), 0, s, p);
+          else hipLaunchKernelGGL((quant_append_kernel<TBF16, kCacheI4>), qg, dim3(256), 0, s, p);
+          break;
+        default:
+          if (h) hipLaunchKernelGGL((quant_append_kernel<TF16, kCacheFp8>), qg, dim3(256), 0, s, p);
+          else hipLaunchKernelGGL((quant_append_kernel<TBF16, kCacheFp8>), qg, dim3(256), 0, s, p);
+          break;
+      }
       return hipGetLastError();
     }
   }

@@ -138,3 +138,9 @@ def test_fp8_prefill_kernel_level_kinds(d, dtype):
     for out in (mx, valu):
         got = orc.decode(from_torch(out, dtype), dtype).astype(np.float64)
         _check_rows(got, ref, c["cum"], dtype)
+
+
+# rows of 768 and 1024 elements over all kv-heads: the append quantises them in two pieces
+@pytest.mark.parametrize("d", [96, 128])
+def test_fp8_prefill_wide_rows(d):
+    check_op(fp8_case(d, BF16, H=16, KV=8, new_lens=[40, 3, 0, 77], past=[100, 5, 9, 300]))

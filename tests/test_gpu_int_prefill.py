@@ -138,3 +138,10 @@ def test_int_prefill_kernel_level_kinds(d, bits, dtype):
         _check_rows(got, ref, None, c["cum"], dtype)
     with pytest.raises(Exception, match="over operand images only"):
         _attention(c, kc, vc, 2, chunk=64)
+
+
+# rows of 768 and 1024 elements over all kv-heads: the append quantises them in two pieces
+@pytest.mark.parametrize("d,bits", [(96, 8), (128, 4), (128, 8)])
+def test_int_prefill_wide_rows(d, bits):
+    check_op(prefill_case(d, bits, "channel", BF16, H=16, KV=8, new_lens=[40, 3, 0, 77],
+                          past=[100, 5, 9, 300]))
