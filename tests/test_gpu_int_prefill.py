@@ -145,3 +145,15 @@ def test_int_prefill_kernel_level_kinds(d, bits, dtype):
 def test_int_prefill_wide_rows(d, bits):
     check_op(prefill_case(d, bits, "channel", BF16, H=16, KV=8, new_lens=[40, 3, 0, 77],
                           past=[100, 5, 9, 300]))
+
+
+# GroupQueryAttention over contiguous integer caches ([B, KV, cap, d] codes): multi-token
+# queries at heads 64-256 run the same image prefill, the images gathered from the present rows
+@pytest.mark.parametrize("bits,d,present", [(8, 128, "shared"), (4, 64, "new"), (8, 256, "new"),
+                                            (4, 96, "shared")])
+def test_int_gqa_contiguous_multi_token(bits, d, present):
+    from gqa_cases import gqa_case
+    from test_gpu_gqa_forms import check as gqa_check
+    c = gqa_case(BF16, 3, 64, 16, 4, d, [200, 63, 150], cap=256, seed=bits + d,
+                 cache_dtype=I8 if bits == 8 else I4, modes=(PER_CHANNEL, PER_TENSOR), std=0.5)
+    gqa_check(c, present=present)
