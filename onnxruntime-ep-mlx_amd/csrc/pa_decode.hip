@@ -116,8 +116,10 @@ __device__ __forceinline__ typename TT::vec8 value_operand8(const Step8<D>& r, i
 // Integer pages (kv_cache.rs:222-256: values are code x scale).  The products run in fp16 on the
 // exact codes: 0x64XX is the fp16 value 1024 + XX, so a biased code byte XX becomes its code with
 // one packed subtraction -- int8: XX = code ^ 0x80, minus 1152; int4: XX = nibble = code + 8,
-// minus 1032 (both exact: the results are small integers).  The scales enter outside the
-// products: per-tensor key scales in the score scale, per-channel ones in the query operands,
+// minus 1032 (both exact: the results are small integers).  Key operands skip the subtraction:
+// they hold code + bias, and the bias times the row's query sum (int_query's offset, the same for
+// every key of the row) leaves each score in the FMA that scales it.  The scales enter outside
+// the products: per-tensor key scales in the score scale, per-channel ones in the query operands,
 // value scales in the epilogue (balanced_merge_kernel for split rows).
 typedef _Float16 f16x2c __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t f16pair_sub(uint32_t w, float bias) {
@@ -132,11 +134,11 @@ __device__ __forceinline__ f16x8 key_operand_i8(const Step8<D>& r, int tile, int
   const u32x4& w = r.k[tile][s >> 1];
   const int t = s & 1;
   const uint32_t a = w[2 * t] ^ 0x80808080u, b = w[2 * t + 1] ^ 0x80808080u;
-  u32x4 o;
-  o[0] = f16pair_sub(__builtin_amdgcn_perm(0x64646464u, a, 0x04010400u), 1152.f);
-  o[1] = f16pair_sub(__builtin_amdgcn_perm(0x64646464u, a, 0x04030402u), 1152.f);
-  o[2] = f16pair_sub(__builtin_amdgcn_perm(0x64646464u, b, 0x04010400u), 1152.f);
-  o[3] = f16pair_sub(__builtin_amdgcn_perm(0x64646464u, b, 0x04030402u), 1152.f);
+  u32x4 o;  // code + 1152
+  o[0] = __builtin_amdgcn_perm(0x64646464u, a, 0x04010400u);
+  o[1] = __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u);
+  o[2] = __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u);
+  o[3] = __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u);
   return __builtin_bit_cast(f16x8, o);
 }
 
@@ -174,11 +176,11 @@ template <int D>
 __device__ __forceinline__ f16x8 key_operand_i4(const Step4<D>& r, int tile, int s) {
   const uint32_t x = r.k[tile][s >> 1][s & 1];
   const uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
-  u32x4 o;
+  u32x4 o;  // code + 1032
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     const uint32_t sel = 0x0c000c00u | ((uint32_t)(4 + m) << 16) | (uint32_t)m;
-    o[m] = f16pair_sub(__builtin_amdgcn_perm(hi, lo, sel) | 0x64006400u, 1032.f);
+    o[m] = __builtin_amdgcn_perm(hi, lo, sel) | 0x64006400u;
   }
   return __builtin_bit_cast(f16x8, o);
 }
@@ -201,9 +203,11 @@ __device__ __forceinline__ f16x8 value_operand_i4(const Step4<D>& r, int j) {
 // of its largest |value| (so the row fits fp16 and keeps 11 bits), and the returned factor
 // 2^(e - 14) -- times a per-tensor key scale -- restores the scores.  Lanes c, c + 16, c + 32,
 // c + 48 hold row c; the lane's dims of k-step q are 64 (q / 2) + 16 G + 8 (q % 2) .. + 7.
+// koff: bias x the sum of the row's fp16 query operands (the key operands hold code + bias).
 template <typename TT, int D>
 __device__ __forceinline__ float int_query(RowState<TF16, D>& rs, const u32x4 (&qr)[D / 32],
-                                           const AttnParams& p, int kh, int G) {
+                                           const AttnParams& p, int kh, int G, float bias,
+                                           float& koff) {
   const bool pc = p.k_quant == PA_QUANT_PER_CHANNEL;
   float qf[D / 32][8];
   float mx = 0.0f;
@@ -232,13 +236,19 @@ __device__ __forceinline__ float int_query(RowState<TF16, D>& rs, const u32x4 (&
   mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
   const int ex = mx > 0.0f ? max(__builtin_amdgcn_frexp_expf(mx), -100) : 0;
   const float up = __builtin_ldexpf(1.0f, 14 - ex);
+  float qsum = 0.0f;
 #pragma unroll
   for (int q = 0; q < D / 32; ++q) {
     float t[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) t[e] = qf[q][e] * up;
     rs.qv[q] = TF16::cvt8(t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qsum += (float)rs.qv[q][e];
   }
+  qsum += __shfl_xor(qsum, 16, 64);
+  qsum += __shfl_xor(qsum, 32, 64);
+  koff = bias * qsum;
   return __builtin_ldexpf(1.0f, ex - 14) * (pc ? 1.0f : p.k_scale[0]);
 }
 
@@ -924,6 +934,7 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
 
   RowState<MT, D> rs;
   float row_f = 1.0f;  // integer pages: this row's score factor (query normalisation x key scale)
+  float koff = 0.0f;   // integer pages: the key-operand bias times the row's query sum
   int pc_bl = -1, pc_u = -1;  // the piece being computed
   int pc_kh = 0, pc_total = 0;
   int full_lo = 0, full_hi = 0;  // steps [t, t + 32) inside [full_lo, full_hi) need no masks
@@ -979,7 +990,8 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
           full_lo = p.window > 0 ? pastb + nq - p.window : 0;
           full_hi = p.causal ? pastb + 1 : pc_total;
           if constexpr (INT)
-            row_f = int_query<TT, D>(rs, qr[cs], p, pc_kh, G);
+            row_f = int_query<TT, D>(rs, qr[cs], p, pc_kh, G, CK == kDcI8 ? 1152.f : 1032.f,
+                                     koff);
           else
 #pragma unroll
             for (int q = 0; q < D / 32; ++q) rs.qv[q] = __builtin_bit_cast(vec8, qr[cs][q]);
@@ -1006,7 +1018,7 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
         if constexpr (INT) {
           // Codes are finite: rows past the end weigh in with probability 0 as they are.
           auto& cur = st[cs];
-          attend_step_ops<MT, D, CAP, true, true, false>(
+          attend_step_ops<MT, D, CAP, true, true, false, true>(
               rs,
               [&](int tile, int s) {
                 if constexpr (CK == kDcI8) return key_operand_i8<D>(cur, tile, s);
@@ -1016,7 +1028,8 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
                 if constexpr (CK == kDcI8) return value_operand_i8<D>(cur, j);
                 else return value_operand_i4<D>(cur, j);
               },
-              t0, pc_total, G, p.scale_log2, p.scale, p.softcap, row_f, row_f, 1.f, 1.f, masked);
+              t0, pc_total, G, p.scale_log2, p.scale, p.softcap, row_f, row_f, 1.f, 1.f, masked,
+              koff);
         } else if constexpr (F8) {
           // Page scales of tiles A and B (lanes 0..3); a tile wholly past the end weighs zero
           // (its page id, and so its scale, is not a real one).

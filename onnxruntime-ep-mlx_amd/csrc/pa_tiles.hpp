@@ -189,11 +189,12 @@ struct RowState {
 // Scores of the step in log2 units (masked to -inf where not visible); returns this lane's max.
 //
 // `kop(tile, s)` returns the key operand of k-step s of tile 0 (keys t0..t0+15) or 1.
-template <typename TT, int D, bool CAP, bool SC, bool MASK, bool FOLD = false, typename KeyOp>
+template <typename TT, int D, bool CAP, bool SC, bool MASK, bool FOLD = false, bool KOFF = false,
+          typename KeyOp>
 __device__ __forceinline__ float step_scores(const RowState<TT, D>& rs, KeyOp kop, int t0,
                                              int end, int G, float scale_log2, float scale,
                                              float cap, float ksA, float ksB, float (&x)[8],
-                                             bool masked = true) {
+                                             bool masked = true, float koff = 0.0f) {
   constexpr int KS = D / 32;
   f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -201,15 +202,28 @@ __device__ __forceinline__ float step_scores(const RowState<TT, D>& rs, KeyOp ko
     sa = TT::mfma(kop(0, s), rs.qv[s], sa);
     sb = TT::mfma(kop(1, s), rs.qv[s], sb);
   }
+  // KOFF: every score of the row carries koff (key operands offset by a constant): removed in
+  // the FMA that applies the tile's factor.
+  static_assert(!KOFF || SC, "offset keys come with page factors");
   if constexpr (SC && CAP) {
-    sa *= ksA;
-    sb *= ksB;
+    if constexpr (KOFF) {
+      const float ka = koff * ksA, kb = koff * ksB;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sa[e] = __builtin_fmaf(sa[e], ksA, -ka);
+        sb[e] = __builtin_fmaf(sb[e], ksB, -kb);
+      }
+    } else {
+      sa *= ksA;
+      sb *= ksB;
+    }
   }
   // Page scales (SC) fold into the log2-domain score scale: one product per tile.  FOLD (no
   // softcap, no page scales, scale_log2 >= 0): x keeps the raw products, the scale multiplies
   // only their maximum here and enters each exponent through one FMA in step_probs.
   static_assert(!FOLD || (!CAP && !SC), "FOLD takes plain scaled scores");
   const float xa = SC ? ksA * scale_log2 : scale_log2, xb = SC ? ksB * scale_log2 : scale_log2;
+  const float kxa = KOFF ? koff * xa : 0.0f, kxb = KOFF ? koff * xb : 0.0f;
   const float cap_k = CAP ? scale / cap : 0.0f, cap_l2 = cap * kLog2e;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -218,6 +232,8 @@ __device__ __forceinline__ float step_scores(const RowState<TT, D>& rs, KeyOp ko
       x[e] = softcap_log2(sv, cap_k, cap_l2);
     else if constexpr (FOLD)
       x[e] = sv;
+    else if constexpr (KOFF)
+      x[e] = __builtin_fmaf(sv, (e < 4) ? xa : xb, -((e < 4) ? kxa : kxb));
     else
       x[e] = sv * ((e < 4) ? xa : xb);
   }
@@ -296,16 +312,17 @@ __device__ __forceinline__ void step_probs(RowState<TT, D>& rs, const float (&x)
 // SPLIT = false: P enters the P.V product once, rounded to T (fp16 keeps 11 bits; used for
 // integer pages, whose value operands are exact small integers).
 template <typename TT, int D, bool CAP, bool SC, bool MASK = true, bool SPLIT = true,
-          typename KeyOp, typename ValueOp>
+          bool KOFF = false, typename KeyOp, typename ValueOp>
 __device__ __forceinline__ void attend_step_ops(RowState<TT, D>& rs, KeyOp kop, ValueOp vop,
                                                 int t0, int end, int G, float scale_log2,
                                                 float scale, float cap, float ksA, float ksB,
-                                                float vsA, float vsB, bool masked = true) {
+                                                float vsA, float vsB, bool masked = true,
+                                                float koff = 0.0f) {
   using vec8 = typename TT::vec8;
   constexpr int DL = D / 16;
   float x[8];
-  const float lmax = step_scores<TT, D, CAP, SC, MASK>(rs, kop, t0, end, G, scale_log2, scale,
-                                                       cap, ksA, ksB, x, masked);
+  const float lmax = step_scores<TT, D, CAP, SC, MASK, false, KOFF>(
+      rs, kop, t0, end, G, scale_log2, scale, cap, ksA, ksB, x, masked, koff);
   if (__any(needs_rescale(rs, lmax))) rescale_rows(rs, lmax, G);
   if constexpr (SPLIT) {
     vec8 phi, plo8;
