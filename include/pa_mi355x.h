@@ -119,6 +119,12 @@ typedef struct pa_batch {
    * without a device read.  0 means "unknown" and is treated as num_tokens. */
   int32_t max_query_len;
   uint32_t flags; /* PA_BATCH_* bits */
+  /* Host-known upper bound of past + new tokens of any one sequence.  It sizes the operand images
+   * of the planned prefill (part of the workspace) by the live context instead of the block-table
+   * capacity.  0 means "unknown" and is treated as max_blocks * block_size.  The caller
+   * guarantees the bound: the query rows of a sequence whose context exceeds it may be left
+   * unwritten (no access outside the buffers). */
+  int32_t max_context_len;
 } pa_batch;
 
 /* The caller guarantees that every new key/value row was written to its block-table slot on
@@ -274,6 +280,13 @@ typedef struct pa_paged_attention_io {
    * it are left unwritten (no access outside the buffers).  0 without host metadata: the bound
    * is num_tokens. */
   int32_t max_query_len;
+  /* Host-known bound on past + new tokens of any one sequence (max of past[b] + cum[b+1] -
+   * cum[b]); 0 = unknown.  It sizes the workspace's operand images of multi-token batches by the
+   * live context rather than by max_blocks * block_size.  With host metadata the exact maximum is
+   * used and a smaller bound is refused (PA_ERR_INVALID_ARGUMENT); without it the caller
+   * guarantees the bound, and query rows of a sequence beyond it may be left unwritten (no access
+   * outside the buffers).  0 without host metadata: the block-table capacity. */
+  int32_t max_context_len;
 } pa_paged_attention_io;
 
 /* Workspace bytes for one call.  The size depends on the shapes (num_tokens, batch,

@@ -254,8 +254,11 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
       pl.part_rows = (size_t)units * 2 * pa::kPrefillRows;
       if (PA_PREFILL_IMAGES && images && pa::img_head(c->head_dim) &&
           (rbs >= kImgMinRowBlocks || intc)) {
+        // images of the live context: the caller's bound on past + new tokens, else the capacity
         const int ik = pa::img_keys(c->head_dim);
-        const int64_t steps = ((int64_t)ctx + ik - 1) / ik;
+        const int64_t live =
+            b->max_context_len > 0 ? std::min<int64_t>(b->max_context_len, ctx) : (int64_t)ctx;
+        const int64_t steps = (live + ik - 1) / ik;
         if ((int64_t)b->batch * c->kv_heads * steps * pa::img_step_bytes(c->head_dim) <=
                 kImgMaxBytes &&
             steps <= 65535 && b->batch <= 65535) {
@@ -794,6 +797,19 @@ int op_layout(const pa_paged_attention_node* n, const pa_paged_attention_io* io,
     b.max_query_len = std::max(mq, 1);
   }
   if (b.max_query_len == 0) b.max_query_len = std::max(io->num_tokens, 1);
+  // Context bound (past + new tokens of any sequence): the host metadata's maximum, else the
+  // caller's, else 0 (the block-table capacity).
+  if (io->max_context_len < 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "max_context_len must be non-negative");
+  b.max_context_len = io->max_context_len;
+  if (io->host_cumulative_sequence_length && io->host_past_seqlens) {
+    int64_t mc = 1;
+    for (int i = 0; i < io->batch; ++i)
+      mc = std::max<int64_t>(mc, (int64_t)io->host_past_seqlens[i] +
+                                     io->host_cumulative_sequence_length[i + 1] -
+                                     io->host_cumulative_sequence_length[i]);
+    b.max_context_len = (int32_t)std::min<int64_t>(mc, INT32_MAX);
+  }
   pa_attn& a = L->attn;
   a.num_heads = n->num_heads;
   a.scale = n->scale;
@@ -832,6 +848,12 @@ int validate_host_metadata(const pa_paged_attention_node* n, const pa_paged_atte
         return fail(PA_ERR_INVALID_ARGUMENT,
                     "PagedAttention: a sequence has more new tokens (%d) than max_query_len (%d)",
                     cum[i + 1] - cum[i], io->max_query_len);
+  if (io->max_context_len > 0)
+    for (int i = 0; i < B; ++i)
+      if ((int64_t)past[i] + cum[i + 1] - cum[i] > io->max_context_len)
+        return fail(PA_ERR_INVALID_ARGUMENT,
+                    "PagedAttention: a sequence has more tokens (%lld) than max_context_len (%d)",
+                    (long long)past[i] + cum[i + 1] - cum[i], io->max_context_len);
   const int64_t nb = io->cache.num_blocks, bs = io->cache.block_size;
   if (io->slot_mapping) {
     const int32_t* sm = io->host_slot_mapping;
@@ -1182,6 +1204,8 @@ int gqa_layout(const pa_gqa_node* n, const pa_gqa_io* io, GqaLayout* L) {
   b.num_tokens = (int32_t)T;
   b.max_query_len = io->seq;
   b.flags = PA_BATCH_NEW_ROWS_IN_CACHE | PA_BATCH_SLOTS_DISTINCT;
+  // every sequence's keys: at most total_sequence_length (host value), within the capacity
+  b.max_context_len = (int32_t)std::max<int64_t>(1, std::min<int64_t>(total, L->cap_p));
   pa_attn& a = L->attn;
   a = pa_attn{};
   a.num_heads = n->num_heads;

@@ -1091,6 +1091,9 @@ __device__ __forceinline__ ItemKeys item_keys(const AttnParams& p, int i) {
   if (row0 >= R) return ItemKeys{0, -1};
   const int pastb = clamped_past(p, b, s1 - s0);
   const int total = pastb + (s1 - s0);
+  // Operand images cover img_steps steps of every (sequence, kv-head): a sequence with more keys
+  // (beyond the caller's context bound) gets no work, so nothing reads past its images.
+  if (p.img_steps > 0 && total > p.img_steps * p.plan_step) return ItemKeys{0, -1};
   const int r_last = min(row0 + kPrefillRows, R) - 1;
   const int hi = p.causal ? pastb + r_last / g + 1 : total;
   const int lo = p.window > 0 ? max(0, pastb + row0 / g - p.window + 1) : 0;
@@ -1238,7 +1241,9 @@ __device__ __forceinline__ void img_load(const AttnParams& p, int id, ImgGroup<N
 }
 
 // fp8 pages: the largest |e4m3 code| of a thread's chunks (the magnitude order of e4m3 is the
-// integer order of its low seven bits; 0x7f, NaN, counts as the largest), then as fp32.
+// integer order of its low seven bits), then as fp32.  A NaN code (0x7f) counts as the largest
+// finite magnitude, 0x7e = 448, so the step's exponent still keeps its finite values in fp16 range
+// (the NaN itself converts to an fp16 NaN).
 template <int CH>
 __device__ __forceinline__ float f8_chunks_absmax(const u32x4 (&x)[CH]) {
   using u8x4 = unsigned char __attribute__((ext_vector_type(4)));
@@ -1249,7 +1254,7 @@ __device__ __forceinline__ float f8_chunks_absmax(const u32x4 (&x)[CH]) {
     for (int k = 0; k < 2; ++k)
       m = __builtin_elementwise_max(m, __builtin_bit_cast(u8x4, x[i][k] & 0x7f7f7f7fu));
   const unsigned c = max(max((unsigned)m[0], (unsigned)m[1]), max((unsigned)m[2], (unsigned)m[3]));
-  return e4m3_to_f32(c);
+  return e4m3_to_f32(min(c, 0x7eu));
 }
 
 // fp8 pages: 8 e4m3 codes (words 0, 1 of x) times f (page scale x 2^-s) as 4 fp16 pairs (RNE).

@@ -69,7 +69,7 @@ class PaBatch(C.Structure):
         ("cumulative_sequence_length", C.c_void_p), ("past_seqlens", C.c_void_p),
         ("block_table", C.c_void_p), ("slot_mapping", C.c_void_p),
         ("batch", C.c_int32), ("max_blocks", C.c_int32), ("num_tokens", C.c_int32),
-        ("max_query_len", C.c_int32), ("flags", C.c_uint32),
+        ("max_query_len", C.c_int32), ("flags", C.c_uint32), ("max_context_len", C.c_int32),
     ]
 
 
@@ -109,7 +109,7 @@ class PaIO(C.Structure):
         ("host_cumulative_sequence_length", C.c_void_p), ("host_past_seqlens", C.c_void_p),
         ("host_block_table", C.c_void_p), ("host_slot_mapping", C.c_void_p),
         ("output", C.c_void_p), ("key_cache_out", C.c_void_p), ("value_cache_out", C.c_void_p),
-        ("max_query_len", C.c_int32),
+        ("max_query_len", C.c_int32), ("max_context_len", C.c_int32),
     ]
 
 

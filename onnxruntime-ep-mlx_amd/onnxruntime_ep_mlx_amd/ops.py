@@ -110,14 +110,16 @@ def cache_desc(key_cache: torch.Tensor, value_cache: torch.Tensor,
 
 def batch_desc(cum: torch.Tensor, past: torch.Tensor, block_table: torch.Tensor,
                num_tokens: int, slot_mapping: torch.Tensor | None = None,
-               max_query_len: int = 0, flags: int = 0) -> capi.PaBatch:
+               max_query_len: int = 0, flags: int = 0,
+               max_context_len: int = 0) -> capi.PaBatch:
     for name, t in (("cumulative_sequence_length", cum), ("past_seqlens", past),
                     ("block_table", block_table), ("slot_mapping", slot_mapping)):
         if t is not None and t.dtype != torch.int32:
             raise ValueError(f"input {name} must be int32")
         _contig(name, t)
     return capi.PaBatch(_ptr(cum), _ptr(past), _ptr(block_table), _ptr(slot_mapping),
-                        cum.numel() - 1, block_table.shape[1], num_tokens, max_query_len, flags)
+                        cum.numel() - 1, block_table.shape[1], num_tokens, max_query_len, flags,
+                        max_context_len)
 
 
 def attn_desc(num_heads: int, scale: float = 0.0, softcap: float = 0.0,
@@ -237,15 +239,18 @@ def rotary_append(query, key, value, key_cache, value_cache, cum, past, block_ta
 def attention(q, k_new, v_new, key_cache, value_cache, cum, past, block_table, *, num_heads,
               scale=0.0, softcap=0.0, local_window_size=-1, is_causal=1, head_sink=None,
               k_scale=None, v_scale=None, max_query_len=0, kind=0, chunk=0, out=None,
-              new_rows_in_cache=False, k_quant_type="NONE", v_quant_type="NONE"):
+              new_rows_in_cache=False, k_quant_type="NONE", v_quant_type="NONE",
+              max_context_len=0):
     """Attention over the (already appended) paged cache; kind/chunk force a kernel family.
-    new_rows_in_cache: the caller appended k_new/v_new into distinct block-table slots."""
+    new_rows_in_cache: the caller appended k_new/v_new into distinct block-table slots.
+    max_context_len: bound on every sequence's past + new tokens (0 = the block-table capacity)."""
     lib = capi.load()
     cache = cache_desc(key_cache, value_cache, k_scale, v_scale,
                        head_dim=q.shape[-1] // num_heads, k_quant_type=k_quant_type,
                        v_quant_type=v_quant_type)
     batch = batch_desc(cum, past, block_table, q.shape[0], None, max_query_len,
-                       capi.PA_BATCH_NEW_ROWS_IN_CACHE if new_rows_in_cache else 0)
+                       capi.PA_BATCH_NEW_ROWS_IN_CACHE if new_rows_in_cache else 0,
+                       max_context_len)
     attn = attn_desc(num_heads, scale, softcap, local_window_size, is_causal, head_sink)
     act = pa_dtype(q.dtype)
     nbytes = lib.pa_attention_workspace_bytes_ex(C.byref(cache), C.byref(batch), C.byref(attn),
@@ -268,7 +273,7 @@ def paged_attention(query, key, value, key_cache, value_cache, cumulative_sequen
                     k_quant_type="NONE", v_quant_type="NONE", v_head_size=0,
                     kv_cache_layout="SEPARATE", validate=True, output=None,
                     key_cache_out=None, value_cache_out=None, max_query_len=0,
-                    static_scratch=False):
+                    max_context_len=0, static_scratch=False):
     """com.microsoft::PagedAttention on MI355X (operator-level entry, pa_paged_attention).
 
     ``attention_metadata`` is accepted and ignored, like the reference
@@ -285,7 +290,9 @@ def paged_attention(query, key, value, key_cache, value_cache, cumulative_sequen
     ``value_cache_out`` given as tensors of their own receive a copy of the updated caches
     (outputs bound onto the inputs need nothing), and are returned in place of the inputs.
     ``max_query_len`` (0 = derive it) bounds every sequence's new tokens: it picks the kernel
-    family without a device read when ``validate`` is False.
+    family without a device read when ``validate`` is False.  ``max_context_len`` (0 = derive
+    it from the host metadata, else the block-table capacity) bounds every sequence's past + new
+    tokens: it sizes the operand images of multi-token batches by the live context.
     ``static_scratch``: call pa_paged_attention_static, which allocates nothing (its workspace
     is the library's per-GPU static scratch, shared by every call on that GPU).
     """
@@ -331,7 +338,7 @@ def paged_attention(query, key, value, key_cache, value_cache, cumulative_sequen
         _ptr(slot_mapping), _ptr(head_sink), _ptr(q_norm_weight), _ptr(k_norm_weight),
         _ptr(host.get("cum")), _ptr(host.get("past")), _ptr(host.get("bt")),
         _ptr(host.get("slots")), _ptr(output), _ptr(key_cache_out), _ptr(value_cache_out),
-        max_query_len)
+        max_query_len, max_context_len)
     if static_scratch:
         capi.check(lib.pa_paged_attention_static(C.byref(node), C.byref(io),
                                                  _stream(query.device)))

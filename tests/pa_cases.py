@@ -142,7 +142,7 @@ QUANT_NAMES = {0: "NONE", PER_TENSOR: "PER_TENSOR", PER_CHANNEL: "PER_CHANNEL"}
 
 
 def run_gpu_op(case: dict, validate=True, device="cuda", packed=False, max_query_len=0,
-               cache_outputs="omitted", static_scratch=False):
+               cache_outputs="omitted", static_scratch=False, max_context_len=0):
     """Run the operator-level entry (pa_paged_attention) on the GPU for a case.  packed: hand
     Q, K and V over as one [T, (H + 2 KV) * d] query with key = value = None.
     cache_outputs: "omitted" (outputs 1/2 absent), "aliased" (bound onto the input caches) or
@@ -182,7 +182,7 @@ def run_gpu_op(case: dict, validate=True, device="cuda", packed=False, max_query
         v_head_size=case.get("v_head_size", 0),
         kv_cache_layout="LATENT" if case.get("latent") else "SEPARATE", validate=validate,
         key_cache_out=kco, value_cache_out=vco, max_query_len=max_query_len,
-        static_scratch=static_scratch)
+        max_context_len=max_context_len, static_scratch=static_scratch)
     torch.cuda.synchronize()
     res = (from_torch(out, dt), from_torch(kc, cdt), None if vc is None else from_torch(vc, cdt))
     if cache_outputs == "separate":

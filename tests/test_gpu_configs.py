@@ -82,7 +82,13 @@ def _run(ep, torch, c, kc, vc, rows=None):
     return from_torch(out, BF16)
 
 
-def test_c3_full_batch_sampled_oracle_and_properties():
+def test_c3_full_batch_oracle_and_properties():
+    """BASELINE.json config 3 (B=64, 32q/8kv, d 128, bf16, ctx U[512,8192], RoPE theta 500000)
+    through pa_paged_attention.  Every sequence against the oracle: its pages gathered after the
+    step (the oracle re-appends the new row into its slot, so its cache equals the device pages
+    only if the device wrote the same rotated row), all 32 heads; the whole pool through
+    properties: only the 64 appended rows changed, a second call bit-identical, a subset re-run
+    as its own batch agrees."""
     import torch
     import onnxruntime_ep_mlx_amd as ep
     c = _c3_inputs()
@@ -91,21 +97,16 @@ def test_c3_full_batch_sampled_oracle_and_properties():
     kc = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).to(torch.bfloat16)
     vc = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).to(torch.bfloat16)
     kc0, vc0 = kc.clone(), vc.clone()
-    sample = [0, 17, 38, 63]
-    blocks = {}
-    for b in sample:
-        n = (int(c["ctx"][b]) + c["bs"] - 1) // c["bs"]
-        ids = torch.from_numpy(c["bt"][b, :n].astype(np.int64)).cuda()
-        blocks[b] = (from_torch(kc.index_select(0, ids), BF16),
-                     from_torch(vc.index_select(0, ids), BF16))
 
     out = _run(ep, torch, c, kc, vc)
     kc1, vc1 = kc.clone(), vc.clone()
 
-    # 1. sampled sequences against the oracle (pages gathered before the step)
-    for b in sample:
-        kb, vb = blocks[b]
-        n = kb.shape[0]
+    # 1. every sequence against the oracle
+    for b in range(c["B"]):
+        n = (int(c["ctx"][b]) + c["bs"] - 1) // c["bs"]
+        ids = torch.from_numpy(c["bt"][b, :n].astype(np.int64)).cuda()
+        kb = from_torch(kc1.index_select(0, ids), BF16)
+        vb = from_torch(vc1.index_select(0, ids), BF16)
         sub = dict(num_heads=c["H"], kv_num_heads=c["KV"], head_dim=c["d"], dtype=BF16,
                    cache_dtype=BF16, cum=np.array([0, 1], np.int32),
                    past=np.array([c["past"][b]], np.int32),
@@ -116,9 +117,9 @@ def test_c3_full_batch_sampled_oracle_and_properties():
         ref, ref_t, kc_ref, vc_ref = orc.paged_attention_op(sub)
         err = orc.rel_l2(orc.decode(out[b:b + 1], BF16), orc.decode(ref_t, BF16))
         assert err <= 2e-3, (b, err)
-        ids = torch.from_numpy(c["bt"][b, :n].astype(np.int64)).cuda()
-        assert np.array_equal(from_torch(kc1.index_select(0, ids), BF16), kc_ref), b
-        assert np.array_equal(from_torch(vc1.index_select(0, ids), BF16), vc_ref), b
+        assert orc.rel_l2(orc.decode(out[b:b + 1], BF16), ref) <= 4e-3, b
+        assert np.array_equal(kb, kc_ref), b
+        assert np.array_equal(vb, vc_ref), b
 
     # 2. only the 64 appended rows changed
     diff = (kc1.view(torch.int16) != kc0.view(torch.int16)).reshape(-1, c["KV"] * c["d"])
@@ -134,8 +135,9 @@ def test_c3_full_batch_sampled_oracle_and_properties():
     out2 = _run(ep, torch, c, kc, vc)
     assert np.array_equal(out, out2)
 
-    # 4. batch independence: the sampled sequences as their own batch (a smaller batch picks a
-    # different split-K chunk, so agreement is to fp32 summation order, not bit-exact)
+    # 4. batch independence: a subset as its own batch (a smaller batch picks a different split
+    # of the keys, so agreement is to fp32 summation order, not bit-exact)
+    sample = [0, 17, 38, 63]
     out3 = _run(ep, torch, c, kc, vc, rows=sample)
     err = orc.rel_l2(orc.decode(out3, BF16), orc.decode(out[sample], BF16))
     assert err <= 1e-3, err
@@ -161,9 +163,9 @@ def test_c4_full_workload_planned_prefill():
     """BASELINE.json config 4 at its workload (bench.py --config c4: seed 4, 8 x 512-token chunks,
     past U[0,4096], 28q/4kv, d 128, block 16, bf16) through pa_paged_attention, which takes the
     planned prefill (896 row-block items >= 2 per CU, items over the split threshold run as two
-    halves).  Checks: the whole pool bit-exact after the append; the sequences with the shortest
-    and the longest past fully (28 heads x 512 rows) against the oracle; every sequence against
-    the independent chunked decode kernel (kind 4); two calls bit-identical."""
+    halves).  Checks: the whole pool bit-exact after the append; every sequence fully (28 heads
+    x 512 rows) against the oracle; every sequence against the chunked decode kernel (kind 4)
+    too; two calls bit-identical."""
     import torch
     import onnxruntime_ep_mlx_amd as ep
     bench = _bench()
@@ -194,8 +196,8 @@ def test_c4_full_workload_planned_prefill():
     for b in range(B):
         rows = slice(int(cum[b]), int(cum[b + 1]))
         assert orc.rel_l2(got[rows], alt[rows]) <= 2e-3, b
-    # shortest and longest past against the oracle (pages gathered from the pre-step pool)
-    for b in (int(np.argmin(past)), int(np.argmax(past))):
+    # every sequence against the oracle (pages gathered from the pre-step pool)
+    for b in range(B):
         n = (int(w["ctx"][b]) + bs - 1) // bs
         ids = np.asarray(w["bt_np"][b, :n])
         rows = slice(int(cum[b]), int(cum[b + 1]))
@@ -210,10 +212,11 @@ def test_c4_full_workload_planned_prefill():
 
 def test_c5_full_batch_fp8():
     """BASELINE.json config 5 at its batch (bench.py --config c5: B=16, 64q/8kv, d 128, ctx
-    32768, e4m3 pages with per-(block, kv-head) scales) through pa_paged_attention.  Three sampled
-    sequences against the oracle (pages and scales gathered before the step, the appended row
-    bytes included); the full batch through properties: only the 16 appended rows of the pages
-    changed, two calls bit-identical, the sampled sequences re-run as their own batch agree."""
+    32768, e4m3 pages with per-(block, kv-head) scales) through pa_paged_attention.  Every
+    sequence against the oracle: its pages and scales gathered after the step (the oracle
+    re-quantises the new row into its slot, so its pages equal the device's only if the device
+    wrote the same codes); the full batch through properties: only the 16 appended rows of the
+    pages changed, two calls bit-identical, a subset re-run as its own batch agrees."""
     import torch
     import onnxruntime_ep_mlx_amd as ep
     from _oracle import E4M3
@@ -221,12 +224,7 @@ def test_c5_full_batch_fp8():
     w = bench.build_fp8_workload(torch, seed=5)
     B, H, KV, d, bs = w["B"], w["H"], w["KV"], w["d"], w["bs"]
     past = w["past"].cpu().numpy()
-    sample = [0, 7, 15]
     n = (int(w["ctx"][0]) + bs - 1) // bs
-    pages = {b: tuple(from_torch(_gather(torch, w[p].view(torch.uint8), w["bt_np"][b], n), E4M3)
-                      for p in ("kc", "vc")) +
-                tuple(_gather(torch, w[s], w["bt_np"][b], n).cpu().numpy() for s in ("ks", "vs"))
-             for b in sample}
     kc0 = w["kc"].view(torch.uint8).clone()
 
     def run(rows=None):
@@ -244,8 +242,10 @@ def test_c5_full_batch_fp8():
 
     out = run()
     q, k, v = (from_torch(w[t], BF16) for t in ("q", "k", "v"))
-    for b in sample:
-        kb, vb, ksb, vsb = pages[b]
+    for b in range(B):
+        kb, vb = (from_torch(_gather(torch, w[p].view(torch.uint8), w["bt_np"][b], n), E4M3)
+                  for p in ("kc", "vc"))
+        ksb, vsb = (_gather(torch, w[s], w["bt_np"][b], n).cpu().numpy() for s in ("ks", "vs"))
         sub = dict(num_heads=H, kv_num_heads=KV, head_dim=d, dtype=BF16, cache_dtype=E4M3,
                    cum=np.array([0, 1], np.int32), past=past[b:b + 1].copy(),
                    block_table=np.arange(n, dtype=np.int32)[None], query=q[b:b + 1],
@@ -253,14 +253,14 @@ def test_c5_full_batch_fp8():
                    k_scale=ksb.copy(), v_scale=vsb.copy())
         ref, ref_t, kc_ref, vc_ref = orc.paged_attention_op(sub)
         assert orc.rel_l2(orc.decode(out[b:b + 1], BF16), orc.decode(ref_t, BF16)) <= 2e-3, b
-        got_k = from_torch(_gather(torch, w["kc"].view(torch.uint8), w["bt_np"][b], n), E4M3)
-        got_v = from_torch(_gather(torch, w["vc"].view(torch.uint8), w["bt_np"][b], n), E4M3)
-        assert np.array_equal(got_k, kc_ref) and np.array_equal(got_v, vc_ref), b
+        assert orc.rel_l2(orc.decode(out[b:b + 1], BF16), ref) <= 4e-3, b
+        assert np.array_equal(kb, kc_ref) and np.array_equal(vb, vc_ref), b
     # only the appended rows changed
     diff = (w["kc"].view(torch.uint8) != kc0).reshape(-1, KV * d)
     changed = set(torch.nonzero(diff.any(dim=1)).flatten().cpu().numpy().tolist())
     expect = {int(w["bt_np"][b, int(past[b]) // bs]) * bs + int(past[b]) % bs for b in range(B)}
     assert changed <= expect
     assert np.array_equal(run(), out)
+    sample = [0, 7, 15]
     err = orc.rel_l2(orc.decode(run(sample), BF16), orc.decode(out[sample], BF16))
     assert err <= 1e-3, err
