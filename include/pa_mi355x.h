@@ -337,8 +337,24 @@ int pa_paged_attention_static(const pa_paged_attention_node* node,
  * "GroupQueryAttention:".  Integer present caches (cache_dtype PA_DTYPE_INT8 / PA_DTYPE_INT4,
  * "kv_cache_bit_width" 8 / 4) encode the new rows as sat(RNE(x * (1 / scale))) with a zero scale
  * read as 1 (the MLAS reciprocal rule, kv_cache.rs:183-190) and attend over code * scale.
- * fp16/bf16 head 64/128 decode batches (num_heads/kv_heads * seq <= 16) without a bias run on the
- * streaming matrix-core decode; everything else on the VALU kernel. */
+ * sliding_window_cache = 1 (attention.rs:1139-1368): past_key / past_value are rings of capacity
+ * past_capacity >= local_window_size > 0 (present_capacity must equal it; the present is the
+ * past buffer itself or one of its own, never omitted; kv_seq == seq).  A sequence of length L
+ * holds its last ring_end(L) rows at rows [0, ring_end(L)): L while L <= capacity, else L less
+ * whole multiples of gap = capacity - window + 1.  A call with p = length - seq past rows
+ * attends the staged view [the ring's ring_end(p) rows | the seq new rows] under the causal
+ * window (new row i at absolute position p + i, rotated there; RoPE in fp32 with position ids or
+ * a bias; bias columns at absolute positions) and writes the present [the view's last
+ * ring_end(p + seq) rows | zero codes].  The view lives in the workspace.
+ * qk_output = 1 / 2 (attention.rs:771-785, :833-839; not with sliding_window_cache): output_qk
+ * receives, per (sequence, head, query row), the scaled, softcapped, biased scores where the row
+ * sees the key (1) or the probabilities with the sink in the denominator (2), 0 elsewhere and in
+ * the columns past the sequence's length; computed on the VALU after the attention.
+ * Kernels: fp16/bf16 decode batches at heads 64/96/128/256 (num_heads/kv_heads * seq <= 16) over
+ * caches in the activation dtype run the streaming matrix-core decode; multi-token batches at
+ * those heads, and every batch over int8 / int4 presents, the matrix-core prefill (integer codes
+ * over operand images); a bias, ragged first prompts (sequences shorter than seq), fp32
+ * activations and other head sizes the VALU kernel. */
 typedef struct pa_gqa_node {
   int32_t num_heads;          /* "num_heads" */
   int32_t kv_num_heads;       /* "kv_num_heads" */
@@ -350,6 +366,8 @@ typedef struct pa_gqa_node {
   int32_t is_causal;          /* "causal" (1) */
   float qk_norm_epsilon;      /* "qk_norm_epsilon" (1e-6) */
   int32_t smooth_softmax;     /* "smooth_softmax" == 1: a zero sink logit for every head */
+  int32_t sliding_window_cache; /* "sliding_window_cache" (0): ring caches, see below */
+  int32_t qk_output;          /* "qk_output" (0): 1 scores, 2 probabilities into output_qk */
 } pa_gqa_node;
 
 typedef struct pa_gqa_io {
@@ -391,6 +409,8 @@ typedef struct pa_gqa_io {
   const float* v_scale;
   int32_t k_quant_type;      /* PA_QUANT_* ("k_quant_type" / "v_quant_type") */
   int32_t v_quant_type;
+  void* output_qk;           /* output 3 [batch, num_heads, seq, total_sequence_length] in T
+                                (qk_output 1 / 2), else NULL */
 } pa_gqa_io;
 
 size_t pa_group_query_attention_workspace_bytes(const pa_gqa_node* node, const pa_gqa_io* io);

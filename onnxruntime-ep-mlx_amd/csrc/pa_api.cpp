@@ -346,6 +346,7 @@ struct RunOpts {
   const int32_t* key_limit = nullptr;
   const void* bias = nullptr;
   int bias_b = 0, bias_h = 0, bias_rows = 0, bias_cols = 0;
+  const int32_t* bias_col_off = nullptr;  // per-sequence bias column offsets (sliding rings)
   bool smooth_softmax = false;
   bool images = true;  // operand images allowed (see make_plan)
 };
@@ -478,6 +479,7 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
   p.bias_h = opts.bias_h;
   p.bias_rows = opts.bias_rows;
   p.bias_cols = opts.bias_cols;
+  p.bias_col_off = opts.bias_col_off;
   p.smooth_softmax = opts.smooth_softmax ? 1 : 0;
 
   hipError_t e;
@@ -583,6 +585,7 @@ struct AppendExtra {
   const int64_t* position_ids = nullptr;
   bool pos_offset_form = false;
   bool rope_fp32 = false;
+  int ring_cap = 0, ring_window = 0;  // sliding_window_cache rings (see AppendParams)
 };
 
 static int rotary_append_impl(const pa_cache* c, const pa_batch* b, int32_t num_heads,
@@ -650,6 +653,8 @@ static int rotary_append_impl(const pa_cache* c, const pa_batch* b, int32_t num_
   p.position_ids = x.position_ids;
   p.pos_offset_form = x.pos_offset_form ? 1 : 0;
   p.rope_fp32 = x.rope_fp32 ? 1 : 0;
+  p.ring_cap = x.ring_cap;
+  p.ring_window = x.ring_window;
   p.seqlens_k = x.seqlens_k;
   p.meta_out = x.meta_out;
   p.q_ld = x.q_ld ? x.q_ld : (int64_t)num_heads * c->head_dim;
@@ -1094,8 +1099,11 @@ struct GqaLayout {
   bool ragged;      // some sequence may be shorter than the query rows (per-sequence key counts)
   int cap_in;       // past capacity (0 without a past)
   int cap_p;        // present capacity
+  bool sliding;     // sliding_window_cache: past and present are rings of capacity cap_in
+  int view_cap;     // sliding: rows per (sequence, kv-head) of the staged view (cap_in + seq)
   size_t row_bytes; // bytes of one stored row of one kv-head
-  size_t q_bytes, k_bytes, v_bytes, meta_off, pres_off, pres_side, attn_off, total;
+  size_t q_bytes, k_bytes, v_bytes, meta_off, pres_off, pres_side, view_off, view_side, attn_off,
+      total;
   pa_cache cache;
   pa_batch batch;
   pa_attn attn;
@@ -1103,7 +1111,8 @@ struct GqaLayout {
 };
 
 // group_query_attention_op / gqa_batched (attention.rs:932-1454, :586-848): shapes, caches and the
-// workspace [rotated q | rotated k | packed v | metadata | present (when omitted) | attention].
+// workspace [rotated q | rotated k | packed v | metadata | present (when omitted) | staged view
+// (sliding_window_cache) | attention].
 int gqa_layout(const pa_gqa_node* n, const pa_gqa_io* io, GqaLayout* L) {
   if (!n || !io) return fail(PA_ERR_INVALID_ARGUMENT, "node/io is NULL");
   if (n->num_heads <= 0 || n->kv_num_heads <= 0 || n->num_heads % n->kv_num_heads != 0)
@@ -1118,7 +1127,7 @@ int gqa_layout(const pa_gqa_node* n, const pa_gqa_io* io, GqaLayout* L) {
     return fail(PA_ERR_INVALID_ARGUMENT,
                 "GroupQueryAttention: batch and sequence length must be positive");
   if ((io->kv_seq != io->seq && io->kv_seq != 0) ||
-      (io->kv_seq == 0 && (L->packed || io->past_key == nullptr)))
+      (io->kv_seq == 0 && (L->packed || io->past_key == nullptr || n->sliding_window_cache)))
     return fail(PA_ERR_INVALID_ARGUMENT,
                 "GroupQueryAttention: K/V must match Q sequence or be empty with paired "
                 "non-sliding past");
@@ -1151,7 +1160,26 @@ int gqa_layout(const pa_gqa_node* n, const pa_gqa_io* io, GqaLayout* L) {
                 "or neither");
   L->in_ws = io->present_key == nullptr;
   const int64_t grown = std::max<int64_t>(L->cap_in, total);
-  if (L->shared) {
+  L->sliding = n->sliding_window_cache != 0;
+  L->view_cap = 0;
+  if (L->sliding) {
+    // rings of the past's capacity (attention.rs:1146-1165, claim :2455-2473)
+    if (n->local_window_size <= 0 || !io->past_key || io->past_capacity < n->local_window_size)
+      return fail(PA_ERR_INVALID_ARGUMENT,
+                  "GroupQueryAttention: sliding cache requires 0 < local_window_size <= capacity");
+    if (L->in_ws)
+      return fail(PA_ERR_INVALID_ARGUMENT,
+                  "GroupQueryAttention: sliding_window_cache requires present key/value outputs");
+    if (!L->shared && io->present_capacity != io->past_capacity)
+      return fail(PA_ERR_INVALID_ARGUMENT,
+                  "GroupQueryAttention: sliding present must be [batch,kv_num_heads,past "
+                  "capacity,head]");
+    if (n->qk_output != 0)
+      return fail(PA_ERR_UNSUPPORTED,
+                  "GroupQueryAttention: sliding_window_cache with QK diagnostics is unsupported");
+    L->cap_p = L->cap_in;
+    L->view_cap = L->cap_in + io->seq;
+  } else if (L->shared) {
     L->cap_p = L->cap_in;
   } else if (!L->in_ws) {
     if (io->present_capacity != grown)
@@ -1162,8 +1190,12 @@ int gqa_layout(const pa_gqa_node* n, const pa_gqa_io* io, GqaLayout* L) {
   } else {
     L->cap_p = (int)grown;
   }
-  if ((int64_t)io->batch * n->kv_num_heads * L->cap_p > (int64_t)INT32_MAX)
+  if ((int64_t)io->batch * n->kv_num_heads * std::max(L->cap_p, L->view_cap) > (int64_t)INT32_MAX)
     return fail(PA_ERR_UNSUPPORTED, "GroupQueryAttention: present cache has more than 2^31 rows");
+  if (n->qk_output < 0 || n->qk_output > 2 || (n->qk_output != 0) != (io->output_qk != nullptr))
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "GroupQueryAttention: qk_output must be 0, 1 or 2 and enabled exactly when "
+                "output_qk is present");
   L->head = io->query_hidden / qheads;
   L->transform = (n->do_rotary != 0) || io->q_norm_weight != nullptr || L->packed;
   const int64_t T = (int64_t)io->batch * io->seq;
@@ -1173,7 +1205,7 @@ int gqa_layout(const pa_gqa_node* n, const pa_gqa_io* io, GqaLayout* L) {
   L->k_bytes = (L->transform && kv_rows) ? align256((size_t)T * n->kv_num_heads * L->head * es) : 0;
   L->v_bytes = L->packed ? align256((size_t)T * n->kv_num_heads * L->head * es) : 0;
   L->meta_off = L->q_bytes + L->k_bytes + L->v_bytes;
-  L->pres_off = L->meta_off + align256((size_t)(3 * io->batch + 1) * sizeof(int32_t));
+  L->pres_off = L->meta_off + align256((size_t)pa::meta_ints(io->batch) * sizeof(int32_t));
   pa_cache& c = L->cache;
   c = pa_cache{};
   c.dtype = io->cache_dtype == 0 ? io->dtype : io->cache_dtype;
@@ -1185,12 +1217,16 @@ int gqa_layout(const pa_gqa_node* n, const pa_gqa_io* io, GqaLayout* L) {
                 "GroupQueryAttention: packed INT4 requires an even logical head size");
   L->row_bytes = cache_head_bytes(c.dtype, L->head);
   L->pres_side = L->in_ws ? align256((size_t)io->batch * n->kv_num_heads * L->cap_p * L->row_bytes) : 0;
-  L->attn_off = L->pres_off + 2 * L->pres_side;
+  L->view_off = L->pres_off + 2 * L->pres_side;
+  L->view_side = L->sliding ? align256((size_t)io->batch * n->kv_num_heads * L->view_cap * L->row_bytes) : 0;
+  L->attn_off = L->view_off + 2 * L->view_side;
+  // rows the attention addresses per (sequence, kv-head): the present, or the staged view
+  const int lin_cap = L->sliding ? L->view_cap : L->cap_p;
   // The cache pointers are set per call (the present may live in the workspace).
   c.key_cache = io->present_key ? io->present_key : const_cast<void*>(io->query);
   c.value_cache = io->present_value ? io->present_value : const_cast<void*>(io->query);
   c.block_size = 16;  // geometry for the plan only: rows are addressed contiguously
-  c.num_blocks = ((int64_t)io->batch * n->kv_num_heads * L->cap_p + 15) / 16;
+  c.num_blocks = ((int64_t)io->batch * n->kv_num_heads * lin_cap + 15) / 16;
   c.kv_heads = n->kv_num_heads;
   c.head_dim = L->head;
   c.k_scale = io->k_scale;
@@ -1204,8 +1240,10 @@ int gqa_layout(const pa_gqa_node* n, const pa_gqa_io* io, GqaLayout* L) {
   b.num_tokens = (int32_t)T;
   b.max_query_len = io->seq;
   b.flags = PA_BATCH_NEW_ROWS_IN_CACHE | PA_BATCH_SLOTS_DISTINCT;
-  // every sequence's keys: at most total_sequence_length (host value), within the capacity
-  b.max_context_len = (int32_t)std::max<int64_t>(1, std::min<int64_t>(total, L->cap_p));
+  // every sequence's keys: at most total_sequence_length (host value), within the capacity; the
+  // staged view of a ring holds at most its capacity plus the new rows
+  b.max_context_len = L->sliding ? lin_cap
+                                 : (int32_t)std::max<int64_t>(1, std::min<int64_t>(total, L->cap_p));
   pa_attn& a = L->attn;
   a = pa_attn{};
   a.num_heads = n->num_heads;
@@ -1217,11 +1255,11 @@ int gqa_layout(const pa_gqa_node* n, const pa_gqa_io* io, GqaLayout* L) {
   RunOpts& o = L->opts;
   o = RunOpts{};
   o.new_rows_in_cache = true;
-  o.linear_cap = L->cap_p;
+  o.linear_cap = lin_cap;
   // A first prompt (total == seq) may hold sequences shorter than the query rows (right-padded
   // rows): their key counts come from seqlens_k (VALU kernel).  Otherwise every sequence has
   // query_past + seq keys and any kernel family serves it.  The pointer is set per call.
-  L->ragged = total == io->seq;
+  L->ragged = total == io->seq && !L->sliding;  // rings: every sequence has length >= seq
   if (L->ragged && io->host_seqlens_k) {
     L->ragged = false;
     for (int b = 0; b < io->batch; ++b) L->ragged |= io->host_seqlens_k[b] + 1 < io->seq;
@@ -1243,6 +1281,17 @@ int validate_gqa_lengths(const pa_gqa_io* io, const GqaLayout& L) {
   const int32_t* len = io->host_seqlens_k;
   const int64_t total = io->total_sequence_length;
   bool bad = false;
+  if (L.sliding) {  // attention.rs:1142-1151
+    int64_t mx = -1;
+    for (int b = 0; b < io->batch; ++b) {
+      const int64_t v = len[b];
+      bad |= v < 0 || v >= total || v + 1 < io->seq;
+      mx = std::max(mx, v);
+    }
+    if (bad || mx != total - 1)
+      return fail(PA_ERR_INVALID_ARGUMENT, "GroupQueryAttention: invalid sliding sequence lengths");
+    return PA_OK;
+  }
   int64_t mx = -1;
   for (int b = 0; b < io->batch && !bad; ++b) {
     const int64_t v = len[b];
@@ -1323,8 +1372,10 @@ int pa_group_query_attention(const pa_gqa_node* n, const pa_gqa_io* io, void* wo
       !((io->bias_batch == 1 || io->bias_batch == io->batch) &&
         (io->bias_heads == 1 || io->bias_heads == n->num_heads)))
     return fail(PA_ERR_INVALID_ARGUMENT,
-                "GroupQueryAttention: attention_bias must broadcast to "
-                "[batch,heads,sequence,total]");
+                L.sliding ? "GroupQueryAttention: sliding attention_bias requires absolute "
+                            "total_sequence_length columns"
+                          : "GroupQueryAttention: attention_bias must broadcast to "
+                            "[batch,heads,sequence,total]");
   if (workspace_bytes < L.total || !workspace)
     return fail(PA_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes, got %zu", L.total,
                 workspace_bytes);
@@ -1332,16 +1383,39 @@ int pa_group_query_attention(const pa_gqa_node* n, const pa_gqa_io* io, void* wo
   char* ws = reinterpret_cast<char*>(workspace);
   int32_t* meta = reinterpret_cast<int32_t*>(ws + L.meta_off);
   L.batch.cumulative_sequence_length = meta;
-  L.batch.past_seqlens = meta + io->batch + 1;
+  L.batch.past_seqlens = meta + pa::meta_past(io->batch);
   L.batch.block_table = meta;  // unused for contiguous caches
-  L.opts.key_limit = L.ragged ? meta + 2 * io->batch + 1 : nullptr;
+  L.opts.key_limit = L.ragged ? meta + pa::meta_keys(io->batch) : nullptr;
   if (L.in_ws) {
     L.cache.key_cache = ws + L.pres_off;
     L.cache.value_cache = ws + L.pres_off + L.pres_side;
   }
+  // A ring's staged view: [the ring's rows before the call | the new rows] per (sequence,
+  // kv-head); the attention reads it and the present is written from it afterwards.
+  pa::RingParams ring{};
+  if (L.sliding) {
+    L.cache.key_cache = ws + L.view_off;
+    L.cache.value_cache = ws + L.view_off + L.view_side;
+    L.opts.bias_col_off = meta + pa::meta_colofs(io->batch);
+    ring.seqlens_k = io->seqlens_k;
+    ring.row_bytes = (int64_t)L.row_bytes;
+    ring.batch = io->batch;
+    ring.kv_heads = n->kv_num_heads;
+    ring.seq = io->seq;
+    ring.cap = L.cap_in;
+    ring.window = n->local_window_size;
+    ring.zero = L.cache.dtype == PA_DTYPE_INT4 ? 0x88888888u : 0u;
+    ring.src_k = reinterpret_cast<const char*>(io->past_key);
+    ring.src_v = reinterpret_cast<const char*>(io->past_value);
+    ring.dst_k = reinterpret_cast<char*>(L.cache.key_cache);
+    ring.dst_v = reinterpret_cast<char*>(L.cache.value_cache);
+    ring.present = 0;
+    hipError_t e = pa::launch_ring_move(ring, s);
+    if (e != hipSuccess) return hip_fail(e, "sliding-window staging");
+  }
   // The present starts as [past rows | zero codes] unless it is the past buffer itself
   // (gqa_batched builds [stored | past tail | zeros], attention.rs:790-818).
-  if (!L.shared) {
+  if (!L.shared && !L.sliding) {
     const size_t pitch = (size_t)L.cap_p * L.row_bytes;
     const size_t keep = (size_t)std::min(L.cap_in, L.cap_p) * L.row_bytes;
     const size_t rows = (size_t)io->batch * n->kv_num_heads;
@@ -1364,8 +1438,12 @@ int pa_group_query_attention(const pa_gqa_node* n, const pa_gqa_io* io, void* wo
   const void* key = io->kv_seq ? io->key : nullptr;
   const void* value = io->kv_seq ? io->value : nullptr;
   AppendExtra x;
-  x.linear_cap = L.cap_p;
+  x.linear_cap = L.sliding ? L.view_cap : L.cap_p;
   x.seq = io->seq;
+  if (L.sliding) {
+    x.ring_cap = L.cap_in;
+    x.ring_window = n->local_window_size;
+  }
   x.kv_rows = io->kv_seq != 0;
   x.seqlens_k = io->seqlens_k;
   x.meta_out = meta;
@@ -1374,8 +1452,11 @@ int pa_group_query_attention(const pa_gqa_node* n, const pa_gqa_io* io, void* wo
     x.position_ids = io->position_ids;
     x.pos_offset_form = io->total_sequence_length == io->seq;
   }
-  // gqa_rope_f32 for position ids or an empty key/value (attention.rs:716-720)
-  x.rope_fp32 = n->do_rotary && (io->position_ids != nullptr || io->kv_seq == 0);
+  // gqa_rope_f32 for position ids or an empty key/value (attention.rs:716-720); on rings for
+  // position ids or a bias (:1222-1228)
+  x.rope_fp32 = n->do_rotary &&
+                (io->position_ids != nullptr ||
+                 (L.sliding ? io->attention_bias != nullptr : io->kv_seq == 0));
   if (L.packed) {
     const size_t es = elem_size(io->dtype);
     const char* qkv = reinterpret_cast<const char*>(io->query);
@@ -1394,8 +1475,47 @@ int pa_group_query_attention(const pa_gqa_node* n, const pa_gqa_io* io, void* wo
   const void* q = L.transform ? q_rot : io->query;
   const void* kn = k_rot ? k_rot : (key ? key : io->query);
   const void* vn = L.packed ? v_rows : (value ? value : io->query);
-  return run_attention(&L.cache, &L.batch, &L.attn, io->dtype, q, kn, vn, io->output,
-                       ws + L.attn_off, workspace_bytes - L.attn_off, 0, 0, s, L.opts);
+  rc = run_attention(&L.cache, &L.batch, &L.attn, io->dtype, q, kn, vn, io->output,
+                     ws + L.attn_off, workspace_bytes - L.attn_off, 0, 0, s, L.opts);
+  if (rc) return rc;
+  if (L.sliding) {  // the present ring: the view's last rows, then zero codes
+    ring.present = 1;
+    ring.src_k = reinterpret_cast<const char*>(L.cache.key_cache);
+    ring.src_v = reinterpret_cast<const char*>(L.cache.value_cache);
+    ring.dst_k = reinterpret_cast<char*>(io->present_key);
+    ring.dst_v = reinterpret_cast<char*>(io->present_value);
+    hipError_t e = pa::launch_ring_move(ring, s);
+    if (e != hipSuccess) return hip_fail(e, "sliding-window present");
+  }
+  if (n->qk_output != 0) {  // output 3: scores or probabilities over the present
+    pa::AttnParams p{};
+    p.q = q;
+    p.key_cache = L.cache.key_cache;
+    p.k_scale = L.cache.k_scale;
+    p.k_quant = L.cache.k_quant_type;
+    p.past = L.batch.past_seqlens;
+    p.head_sink = io->head_sink;
+    p.smooth_softmax = n->smooth_softmax == 1 ? 1 : 0;
+    p.bias = io->attention_bias;
+    p.bias_b = io->bias_batch;
+    p.bias_h = io->bias_heads;
+    p.bias_rows = io->seq;
+    p.bias_cols = (int32_t)io->total_sequence_length;
+    p.num_heads = n->num_heads;
+    p.kv_heads = n->kv_num_heads;
+    p.head_dim = L.head;
+    p.batch = io->batch;
+    p.max_query_len = io->seq;
+    p.linear_cap = L.cap_p;
+    p.scale = n->scale != 0.0f ? n->scale : 1.0f / std::sqrt((float)L.head);
+    p.softcap = n->softcap;
+    p.window = n->local_window_size;
+    p.causal = n->is_causal ? 1 : 0;
+    hipError_t e = pa::launch_gqa_qk(p, io->dtype, L.cache.dtype, io->output_qk, n->qk_output,
+                                     io->total_sequence_length, meta + pa::meta_keys(io->batch), s);
+    if (e != hipSuccess) return hip_fail(e, "output_qk");
+  }
+  return PA_OK;
 }
 
 // ------------------------------------------------------------------------------ claim
@@ -1573,9 +1693,9 @@ int pa_paged_attention_claim(const pa_node_info* n, char* reason, size_t reason_
   return 1;
 }
 
-// group_query_attention_claim (attention.rs:2407-2628) + kv_cache::claim for contiguous caches
-// (kv_cache.rs:16-108, scales at inputs 12/13), restricted to what pa_group_query_attention
-// executes: sliding_window_cache and the output_qk diagnostics are declined.
+// group_query_attention_claim (attention.rs:2407-2754) + kv_cache::claim for contiguous caches
+// (kv_cache.rs:16-108, scales at inputs 12/13), check for check in the reference's order, with
+// its messages; head sizes beyond the VALU kernel's 640 are declined.
 int pa_group_query_attention_claim(const pa_gqa_node_info* n, char* reason, size_t reason_len) {
   auto deny = [&](const char* fmt, ...) {
     if (reason && reason_len) {
@@ -1612,7 +1732,15 @@ int pa_group_query_attention_claim(const pa_gqa_node_info* n, char* reason, size
   if (n->num_inputs == 7 && do_rotary)
     return deny("7-input GroupQueryAttention requires do_rotary=0 because cos/sin caches are "
                 "absent");
-  if (sliding) return deny("sliding_window_cache is not executed by this build");
+  if (sliding) {
+    if (window <= 0) return deny("sliding_window_cache=1 requires local_window_size > 0");
+    if (!(out_present(1) && out_present(2)))
+      return deny("sliding_window_cache requires present key/value outputs");
+    if (!(present(3) && n->input_rank[3] == 4 && shape(3, 2) >= window))
+      return deny("sliding-window key cache capacity must be at least local_window_size");
+    if (!(present(4) && n->input_rank[4] == 4 && shape(4, 2) >= window))
+      return deny("sliding-window value cache capacity must be at least local_window_size");
+  }
   const bool packed = present(0) && !present(1) && !present(2);
   if (!packed && !(present(0) && present(1) && present(2)))
     return deny("Q/K/V must be either all separate or packed in input 0 with inputs 1 and 2 "
@@ -1686,6 +1814,9 @@ int pa_group_query_attention_claim(const pa_gqa_node_info* n, char* reason, size
   if (n->kv_cache_bit_width == 4 && head % 2 != 0)
     return deny("GQA packed INT4 requires an even logical head size (pinned CheckPast byte "
                 "geometry)");
+  if (sliding && n->kv_cache_bit_width != 0 &&
+      head % (n->kv_cache_bit_width == 4 ? 32 : 16) != 0)
+    return deny("sliding integer cache rows must satisfy pinned 16-byte alignment");
   const int64_t cache_head = n->kv_cache_bit_width == 4 ? (head + 1) / 2 : head;
   const int64_t qb = shape(0, 0), qs = shape(0, 1);
   if (has_bias &&
@@ -1742,7 +1873,14 @@ int pa_group_query_attention_claim(const pa_gqa_node_info* n, char* reason, size
   const int qk = n->qk_output;
   if (!(qk >= 0 && qk <= 2 && (qk != 0) == out_present(3)))
     return deny("qk_output must be 0, 1 or 2 and enabled exactly when output_qk is present");
-  if (qk != 0) return deny("output_qk diagnostics are not executed by this build");
+  if (sliding && qk != 0) return deny("sliding_window_cache with QK diagnostics is unsupported");
+  if (qk != 0 &&
+      !(n->output_dtype[3] == out_dt && n->output_rank[3] == 4 &&
+        (n->output_shape[3][0] < 0 || qb < 0 || n->output_shape[3][0] == qb) &&
+        (n->output_shape[3][1] < 0 || n->output_shape[3][1] == nh) &&
+        (n->output_shape[3][2] < 0 || qs < 0 || n->output_shape[3][2] == qs)))
+    return deny("output_qk must be [batch,num_heads,sequence_length,total_sequence_length] in "
+                "activation dtype");
   if (!std::isfinite(n->softcap) || n->softcap < 0.0f)
     return deny("softcap must be finite and non-negative");
   return 1;

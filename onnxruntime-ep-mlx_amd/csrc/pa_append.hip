@@ -43,12 +43,6 @@ __device__ __forceinline__ int64_t slot_at(const AppendParams& p, int b, int64_t
   return blk * p.block_size + logical % p.block_size;
 }
 
-// Per-lane slot of token u (the last-writer scan; u differs between lanes).
-__device__ __forceinline__ int64_t token_slot_lane(const AppendParams& p, int u) {
-  if (p.slot_mapping) return (int64_t)p.slot_mapping[u];
-  const int b = seq_of_token_lane(p.cum, p.batch, u);
-  return slot_at(p, b, (int64_t)max(p.past[b], 0) + (u - p.cum[b]));
-}
 
 // Last-writer rule without a slot mapping: whether a later token writes `slot` (block blk =
 // slot / bs, offset slot % bs) of token position `pos` in sequence b.  A later token u can only
@@ -269,16 +263,29 @@ __global__ __launch_bounds__(256) void rotary_append_kernel(const AppendParams p
     pos = (int64_t)qp + j;
     kv_store = p.gqa_kv_rows != 0 && j < len - qp;
     rpos = pos;
+    if (p.ring_cap > 0) {  // sliding_window_cache: row before + j of the staged view
+      const RingGeom rg = ring_geom(len, p.gqa_seq, p.ring_cap, p.ring_window);
+      pos = (int64_t)rg.before + j;
+      rpos = (int64_t)rg.p + j;
+      kv_store = p.gqa_kv_rows != 0;
+    }
     if (p.position_ids)
       rpos = p.pos_offset_form ? p.position_ids[0] + j
                                : p.position_ids[(int64_t)seq_b * p.gqa_seq + j];
     if (p.meta_out && t == 0 && blockIdx.y == 0)
       for (int i = threadIdx.x; i <= p.batch; i += blockDim.x) {
-        p.meta_out[i] = i * p.gqa_seq;  // cum
+        p.meta_out[kMetaCum + i] = i * p.gqa_seq;  // cum
         if (i < p.batch) {
           const int li = p.seqlens_k[i] + 1;
-          p.meta_out[p.batch + 1 + i] = max(li - p.gqa_seq, 0);  // past (query_past)
-          p.meta_out[2 * p.batch + 1 + i] = li;                   // key count
+          if (p.ring_cap > 0) {
+            const RingGeom rg = ring_geom(li, p.gqa_seq, p.ring_cap, p.ring_window);
+            p.meta_out[meta_past(p.batch) + i] = rg.before;                 // past (view rows)
+            p.meta_out[meta_keys(p.batch) + i] = rg.before + p.gqa_seq;     // key count
+            p.meta_out[meta_colofs(p.batch) + i] = rg.p - rg.before;        // bias column offset
+          } else {
+            p.meta_out[meta_past(p.batch) + i] = max(li - p.gqa_seq, 0);  // past (query_past)
+            p.meta_out[meta_keys(p.batch) + i] = li;                       // key count
+          }
         }
       }
   } else {
@@ -551,6 +558,65 @@ void launch_append_t(const AppendParams& p, pa_dtype cache_dtype, dim3 grid, dim
       hipLaunchKernelGGL((rotary_append_kernel<TT, kCacheT>), grid, block, 0, s, p);
       break;
   }
+}
+
+// ------------------------------------------------------------------- sliding_window_cache rings
+// Byte moves of the GroupQueryAttention ring (attention.rs:1139-1368), one workgroup per
+// (sequence, kv-head, chunk of rows), 16 bytes per thread when rows are 16-byte multiples (else
+// one byte).  stage: history rows [0, before) of the past ring -> rows [0, before) of the staged
+// view (capacity cap + seq); present: rows [0, after) of the present ring <- view rows
+// [seed, seed + after), rows [after, cap) <- zero codes (int4: 0x88).  The present may be the past
+// buffer itself: the present pass runs after the attention, and reads only the view.
+constexpr int kRingRowsPerGroup = 64;
+template <bool V16>
+__global__ __launch_bounds__(256) void ring_move_kernel(RingParams r) {
+  const int bh = blockIdx.x, b = bh / r.kv_heads;
+  const int len = r.seqlens_k[b] + 1;
+  const RingGeom g = ring_geom(len, r.seq, r.cap, r.window);
+  const int row0 = blockIdx.y * kRingRowsPerGroup;
+  const int64_t rb = r.row_bytes;
+  for (int side = 0; side < 2; ++side) {
+    const char* src = side ? r.src_v : r.src_k;
+    char* dst = side ? r.dst_v : r.dst_k;
+    const int64_t spitch = (int64_t)(r.present ? r.cap + r.seq : r.cap) * rb;  // rows of a (b, kh)
+    const int64_t dpitch = (int64_t)(r.present ? r.cap : r.cap + r.seq) * rb;
+    src += bh * spitch;
+    dst += bh * dpitch;
+    // rows [row0, row1) of this group: stage copies [0, before); present copies [0, after) from
+    // view row seed and zero-fills [after, cap)
+    const int nrows = r.present ? r.cap : g.before;
+    const int row1 = min(row0 + kRingRowsPerGroup, nrows);
+    if (row0 >= row1) continue;
+    const int copy_end = r.present ? min(row1, g.after) : row1;
+    const int64_t soff = r.present ? (int64_t)g.seed * rb : 0;
+    constexpr int U = V16 ? 16 : 1;
+    const int64_t a0 = row0 * rb, a_copy = max((int64_t)copy_end * rb, a0), a1 = row1 * rb;
+    for (int64_t o = a0 + (int64_t)threadIdx.x * U; o < a1; o += 256 * U) {
+      if constexpr (V16) {
+        u32x4 v = u32x4{r.zero, r.zero, r.zero, r.zero};
+        if (o < a_copy) v = *reinterpret_cast<const u32x4*>(src + soff + o);
+        *reinterpret_cast<u32x4*>(dst + o) = v;
+      } else {
+        dst[o] = o < a_copy ? src[soff + o] : (char)(r.zero & 0xff);
+      }
+    }
+  }
+}
+
+hipError_t launch_ring_move(const RingParams& r, hipStream_t s) {
+  if (r.batch <= 0 || r.kv_heads <= 0 || r.cap <= 0 || r.window <= 0 || r.window > r.cap ||
+      r.seq <= 0 || r.row_bytes <= 0)
+    return hipErrorInvalidValue;
+  // rows of a group: present [0, cap); stage [0, before) with before <= cap
+  const dim3 grid((unsigned)((int64_t)r.batch * r.kv_heads),
+                  (r.cap + kRingRowsPerGroup - 1) / kRingRowsPerGroup);
+  const uintptr_t al = (uintptr_t)r.src_k | (uintptr_t)r.src_v | (uintptr_t)r.dst_k |
+                       (uintptr_t)r.dst_v | (uintptr_t)r.row_bytes;
+  if ((al & 15) == 0)
+    hipLaunchKernelGGL((ring_move_kernel<true>), grid, dim3(256), 0, s, r);
+  else
+    hipLaunchKernelGGL((ring_move_kernel<false>), grid, dim3(256), 0, s, r);
+  return hipGetLastError();
 }
 
 hipError_t launch_rotary_append(const AppendParams& p, pa_dtype act, pa_dtype cache_dtype,

@@ -110,6 +110,8 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
                    ((((int64_t)(p.bias_b == 1 ? 0 : b) * p.bias_h + (p.bias_h == 1 ? 0 : h)) *
                          p.bias_rows + (t - s0)) * p.bias_cols)
              : nullptr;
+  // bias column of key position pos: pos + the sequence's offset (sliding-window rings)
+  const int64_t bias_off = p.bias_col_off ? p.bias_col_off[b] : 0;
 
   const int64_t row = (int64_t)p.kv_heads * D;
   // Cache rows in storage units: int4 holds two channels per byte.
@@ -170,7 +172,7 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
     }
     float s = wave_sum(part) * p.scale;
     if (cap > 0.0f) s = cap * tanhf(s / cap);
-    if (bias_row) s += TT::to_f32(bias_row[pos]);
+    if (bias_row) s += TT::to_f32(bias_row[min(max(pos + bias_off, (int64_t)0), (int64_t)p.bias_cols - 1)]);
     float x = s * kLog2e;
     float mn = fmaxf(m, x);
     float alpha = (m == kNegInf) ? 0.0f : exp2f(m - mn);
@@ -302,6 +304,117 @@ hipError_t launch_generic_t(const AttnParams& p, pa_dtype cache_dtype, hipStream
                                   : launch_generic_ne<TT, 10>(p, cache_dtype, s);
 }
 
+// ------------------------------------------------------------------------------ output_qk
+// GroupQueryAttention's QK diagnostics (output 3, attention.rs:771-785, :833-839) over a
+// contiguous present [batch, kv_heads, linear_cap, D]: row (b, h, i) of qk [batch, num_heads,
+// seq, cols] holds, for key j < the sequence's key count, the score s_j = scale * q.k_j
+// (softcapped, plus the bias) where row i sees key j (mode 1), or its probability
+// exp(s_j - m) / (sum of the visible exp(s - m) + exp(sink - m)) (mode 2), and 0 everywhere else
+// (masked keys, columns past the key count).  One workgroup per row, keys spread over the
+// threads, each a full dot product in fp32 from the row in LDS; mode 2 takes a maxima-and-sums
+// pass before the writing pass.  Rows sit at b * seq + i of q (seq = max_query_len); past[b] is
+// the sequence's query_past and keys[b] its key count.
+constexpr int kQkThreads = 256;
+template <typename TT, typename CT>
+__global__ __launch_bounds__(kQkThreads) void gqa_qk_kernel(const AttnParams p, void* qk, int mode,
+                                                            int64_t cols, const int32_t* keys) {
+  const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  const int S = p.max_query_len, D = p.head_dim, g = p.num_heads / p.kv_heads, kh = h / g;
+  __shared__ float qs[kMaxHeadDim];
+  __shared__ float red_m[kQkThreads / 64], red_l[kQkThreads / 64];
+  const int64_t t = (int64_t)b * S + i;
+  for (int e = tid; e < D; e += kQkThreads)
+    qs[e] = TT::to_f32(reinterpret_cast<const typename TT::raw*>(p.q)[(t * p.num_heads + h) * D + e]);
+  __syncthreads();
+  const int64_t qp = max(p.past[b], 0);
+  const int64_t length = min((int64_t)max(keys[b], 0), (int64_t)p.linear_cap);
+  int64_t hi = length, lo = 0;
+  if (p.causal) hi = min(hi, qp + i + 1);
+  if (p.window > 0) lo = max((int64_t)0, min(qp + i, length - 1) - p.window + 1);
+  const int Dc = std::is_same<CT, I4Cache>::value ? (D + 1) >> 1 : D;
+  const int64_t base0 = ((int64_t)b * p.kv_heads + kh) * p.linear_cap * Dc;
+  const bool kpc = p.k_quant == PA_QUANT_PER_CHANNEL;
+  const typename TT::raw* bias_row =
+      p.bias ? reinterpret_cast<const typename TT::raw*>(p.bias) +
+                   ((((int64_t)(p.bias_b == 1 ? 0 : b) * p.bias_h + (p.bias_h == 1 ? 0 : h)) *
+                         p.bias_rows + i) * p.bias_cols)
+             : nullptr;
+  auto score = [&](int64_t j) {
+    float dot = 0.0f;
+    for (int e = 0; e < D; ++e) {
+      const float ks = kIntCache<CT> ? p.k_scale[kpc ? (int64_t)kh * D + e : 0] : 1.0f;
+      dot += qs[e] * CacheRead<CT>::at(p.key_cache, base0 + j * Dc, e, ks);
+    }
+    float sc = dot * p.scale;
+    if (p.softcap > 0.0f) sc = p.softcap * tanhf(sc / p.softcap);
+    if (bias_row) sc += TT::to_f32(bias_row[min(j, (int64_t)p.bias_cols - 1)]);
+    return sc;
+  };
+  // mode 2: the row's maximum (with the sink) and denominator, in base 2
+  float m = kNegInf, l = 0.0f;
+  if (mode == 2) {
+    for (int64_t j = lo + tid; j < hi; j += kQkThreads) {
+      const float x = score(j) * kLog2e, mn = fmaxf(m, x);
+      l = l * (m == kNegInf ? 0.0f : exp2f(m - mn)) + exp2f(x - mn);
+      m = mn;
+    }
+    // combine (m, l) over the wavefront, then over the wavefronts
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float m2 = __shfl_xor(m, o, 64), l2 = __shfl_xor(l, o, 64), mn = fmaxf(m, m2);
+      l = (mn == kNegInf) ? 0.0f
+                          : l * (m == kNegInf ? 0.0f : exp2f(m - mn)) +
+                                l2 * (m2 == kNegInf ? 0.0f : exp2f(m2 - mn));
+      m = mn;
+    }
+    if ((tid & 63) == 0) red_m[tid >> 6] = m, red_l[tid >> 6] = l;
+    __syncthreads();
+    m = kNegInf;
+    l = 0.0f;
+    for (int w = 0; w < kQkThreads / 64; ++w) {
+      const float mn = fmaxf(m, red_m[w]);
+      l = (mn == kNegInf) ? 0.0f
+                          : l * (m == kNegInf ? 0.0f : exp2f(m - mn)) +
+                                red_l[w] * (red_m[w] == kNegInf ? 0.0f : exp2f(red_m[w] - mn));
+      m = mn;
+    }
+    const float sk = sink_logit<TT>(p, h);
+    const float mm = fmaxf(m, sk);
+    l = (mm == kNegInf) ? 0.0f
+                        : l * (m == kNegInf ? 0.0f : exp2f(m - mm)) +
+                              (sk == kNegInf ? 0.0f : exp2f(sk - mm));
+    m = mm;
+  }
+  typename TT::raw* row = reinterpret_cast<typename TT::raw*>(qk) + ((((int64_t)b * p.num_heads + h) * S + i) * cols);
+  for (int64_t j = tid; j < cols; j += kQkThreads) {
+    float v = 0.0f;
+    if (j >= lo && j < hi) {
+      const float sc = score(j);
+      v = mode == 1 ? sc : (l > 0.0f ? exp2f(sc * kLog2e - m) / l : 0.0f);
+    }
+    row[j] = TT::from_f32(v);
+  }
+}
+
+template <typename TT>
+hipError_t launch_qk_t(const AttnParams& p, pa_dtype cache_dtype, void* qk, int mode, int64_t cols,
+                       const int32_t* keys, hipStream_t s) {
+  const dim3 grid(p.max_query_len, p.num_heads, p.batch), block(kQkThreads);
+  switch (cache_dtype) {
+    case PA_DTYPE_INT8:
+      hipLaunchKernelGGL((gqa_qk_kernel<TT, I8Cache>), grid, block, 0, s, p, qk, mode, cols, keys);
+      break;
+    case PA_DTYPE_INT4:
+      hipLaunchKernelGGL((gqa_qk_kernel<TT, I4Cache>), grid, block, 0, s, p, qk, mode, cols, keys);
+      break;
+    default:
+      if (cache_dtype != TT::code) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((gqa_qk_kernel<TT, TT>), grid, block, 0, s, p, qk, mode, cols, keys);
+      break;
+  }
+  return hipGetLastError();
+}
+
 template <typename TT>
 void launch_reduce_t(const AttnParams& p, hipStream_t s) {
   dim3 grid(p.num_heads, p.num_tokens), block(64);
@@ -322,6 +435,20 @@ hipError_t launch_attn_generic(const AttnParams& p, pa_dtype act, pa_dtype cache
     case PA_DTYPE_FLOAT16: return launch_generic_t<TF16>(p, cache_dtype, s);
     case PA_DTYPE_BFLOAT16: return launch_generic_t<TBF16>(p, cache_dtype, s);
     case PA_DTYPE_FLOAT32: return launch_generic_t<TF32>(p, cache_dtype, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_gqa_qk(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype, void* qk,
+                         int mode, int64_t cols, const int32_t* keys, hipStream_t s) {
+  if (p.batch <= 0 || p.max_query_len <= 0) return hipSuccess;
+  if (p.head_dim > kMaxHeadDim || p.linear_cap <= 0 || (mode != 1 && mode != 2) || cols <= 0 ||
+      !keys || !qk || p.max_query_len > 65535 || p.num_heads > 65535 || p.batch > 65535)
+    return hipErrorInvalidValue;
+  switch (act) {
+    case PA_DTYPE_FLOAT16: return launch_qk_t<TF16>(p, cache_dtype, qk, mode, cols, keys, s);
+    case PA_DTYPE_BFLOAT16: return launch_qk_t<TBF16>(p, cache_dtype, qk, mode, cols, keys, s);
+    case PA_DTYPE_FLOAT32: return launch_qk_t<TF32>(p, cache_dtype, qk, mode, cols, keys, s);
     default: return hipErrorInvalidValue;
   }
 }

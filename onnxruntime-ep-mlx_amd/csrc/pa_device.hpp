@@ -215,19 +215,6 @@ __device__ __forceinline__ SeqPos seq_pos_of_token(const int32_t* cum, const int
   return SeqPos{lo + k, __shfl(cj, k, 64), __shfl(pj, k, 64)};
 }
 
-// Per-lane form (t may differ between lanes, or lanes may be inactive): binary search.
-__device__ __forceinline__ int seq_of_token_lane(const int32_t* cum, int batch, int t) {
-  int lo = 0, hi = batch - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (__ldg(&cum[mid]) <= t)
-      lo = mid;
-    else
-      hi = mid - 1;
-  }
-  return lo;
-}
-
 // ------------------------------------------------------------------------------ parameters
 struct AppendParams {
   const void* query;
@@ -283,7 +270,44 @@ struct AppendParams {
   // (zero scale read as 1).
   int32_t k_quant, v_quant;
   int32_t quant_reciprocal;
+  // GroupQueryAttention sliding_window_cache (ring_cap > 0, linear mode): a sequence of length
+  // len has p = len - gqa_seq past rows, of which the ring holds before = ring_end(p); row j
+  // rotates at position p + j and is stored at row before + j of the staged view (capacity
+  // linear_cap = ring_cap + gqa_seq).  meta_out then also receives the ring geometry
+  // (ring_meta).
+  int32_t ring_cap, ring_window;
 };
+
+// Rows a sliding_window_cache ring of capacity cap and window w holds for a sequence of len rows
+// (attention.rs:1166-1181): len while it fits, else len less whole multiples of gap = cap - w + 1.
+__host__ __device__ __forceinline__ int ring_end(int64_t len, int cap, int w) {
+  if (len <= cap) return (int)len;
+  const int64_t gap = (int64_t)cap - w + 1;
+  return (int)(len - gap * ((len - cap + gap - 1) / gap));
+}
+
+// Ring geometry of one sequence: p past rows (absolute), `before` held before the call, `after`
+// after it, and the staged-view row of the present's first row (seed = before - (after - seq)).
+struct RingGeom {
+  int p, before, after, seed;
+};
+__host__ __device__ __forceinline__ RingGeom ring_geom(int len, int seq, int cap, int w) {
+  RingGeom g;
+  g.p = len - seq > 0 ? len - seq : 0;
+  g.before = ring_end(g.p, cap, w);
+  g.after = ring_end((int64_t)g.p + seq, cap, w);
+  g.seed = g.before - (g.after - seq);
+  return g;
+}
+
+// Metadata the append writes for the attention (GroupQueryAttention, meta_out): cum [B + 1],
+// past [B], key count [B], then for rings the bias column offset p - before [B] (a view row's
+// absolute position minus the row), seed [B] and after [B].
+constexpr int kMetaCum = 0;
+__host__ __device__ constexpr int meta_past(int B) { return B + 1; }
+__host__ __device__ constexpr int meta_keys(int B) { return 2 * B + 1; }
+__host__ __device__ constexpr int meta_colofs(int B) { return 3 * B + 1; }
+__host__ __device__ constexpr int meta_ints(int B) { return 4 * B + 1; }
 
 struct AttnParams {
   const void* q;
@@ -342,6 +366,9 @@ struct AttnParams {
   const int32_t* key_limit;
   const void* bias;
   int32_t bias_b, bias_h, bias_rows, bias_cols;
+  // bias column of key position pos of sequence b: pos + bias_col_off[b] (sliding_window_cache:
+  // the staged view's rows are not absolute positions); NULL: pos
+  const int32_t* bias_col_off;
   int32_t smooth_softmax;
   int32_t* plan;
   int32_t* plan_info;
@@ -411,6 +438,20 @@ constexpr int kPrefillRows = 64 * kPrefillGroups;
 inline int prefill_key_step(int head_dim) { return head_dim == 128 ? 64 : 32; }
 
 // Launchers (defined in the .hip files).
+// GroupQueryAttention sliding_window_cache ring moves (pa_append.hip): present == 0 stages the
+// past ring's history rows into the view; present == 1 writes the present ring from the view.
+struct RingParams {
+  const int32_t* seqlens_k;
+  const char* src_k;
+  const char* src_v;
+  char* dst_k;
+  char* dst_v;
+  int64_t row_bytes;  // bytes of one stored row of one kv-head
+  int32_t batch, kv_heads, seq, cap, window;
+  int32_t present;
+  uint32_t zero;  // zero code in every byte (int4: 0x88888888)
+};
+hipError_t launch_ring_move(const RingParams& r, hipStream_t s);
 hipError_t launch_rotary_append(const AppendParams& p, pa_dtype act, pa_dtype cache_dtype,
                                 hipStream_t s);
 hipError_t launch_attn_generic(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
@@ -425,6 +466,10 @@ hipError_t launch_prefill_mfma(const AttnParams& p, pa_dtype act, pa_dtype cache
 hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
                                   hipStream_t s);
 hipError_t launch_split_reduce(const AttnParams& p, pa_dtype act, hipStream_t s);
+// GroupQueryAttention output_qk diagnostics (pa_attn_generic.hip): mode 1 scores, 2 probabilities
+// into qk [batch, num_heads, max_query_len, cols]; keys[b]: the sequence's key count.
+hipError_t launch_gqa_qk(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype, void* qk,
+                         int mode, int64_t cols, const int32_t* keys, hipStream_t s);
 bool decode_mfma_supported(int head_dim, pa_dtype act, pa_dtype cache_dtype);
 // Balanced (streaming) decode: fp16/bf16 activations, d in {64, 96, 128, 256}, power-of-two
 // pages, pages in the activation dtype or (d 64 / 128) fp8 e4m3 with at least 16 rows per page.

@@ -119,6 +119,7 @@ class PaGqaNode(C.Structure):
         ("softcap", C.c_float), ("local_window_size", C.c_int32), ("do_rotary", C.c_int32),
         ("rotary_interleaved", C.c_int32), ("is_causal", C.c_int32),
         ("qk_norm_epsilon", C.c_float), ("smooth_softmax", C.c_int32),
+        ("sliding_window_cache", C.c_int32), ("qk_output", C.c_int32),
     ]
 
 
@@ -141,6 +142,7 @@ class PaGqaIO(C.Structure):
         ("output", C.c_void_p),
         ("cache_dtype", C.c_int), ("k_scale", C.c_void_p), ("v_scale", C.c_void_p),
         ("k_quant_type", C.c_int32), ("v_quant_type", C.c_int32),
+        ("output_qk", C.c_void_p),
     ]
 
 

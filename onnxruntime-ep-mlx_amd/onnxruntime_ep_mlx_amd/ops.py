@@ -359,7 +359,7 @@ def group_query_attention(query, key, value, past_key, past_value, seqlens_k,
                           do_rotary=0, rotary_interleaved=0, is_causal=1, qk_norm_epsilon=1e-6,
                           smooth_softmax=0, k_quant_type="NONE", v_quant_type="NONE",
                           present="new", present_key=None, present_value=None, validate=True,
-                          output=None):
+                          output=None, sliding_window_cache=0, qk_output=0, output_qk=None):
     """com.microsoft::GroupQueryAttention on MI355X (pa_group_query_attention), inputs in the
     operator's order (query, key, value, past_key, past_value, seqlens_k,
     total_sequence_length, cos_cache, sin_cache, position_ids, attention_bias, head_sink,
@@ -374,7 +374,10 @@ def group_query_attention(query, key, value, past_key, past_value, seqlens_k,
     (outputs bound onto the inputs: capacity stays), "omitted" returns None for both;
     ``present_key``/``present_value`` given explicitly are used as the "new" buffers.
     ``validate``: copy seqlens_k (and position_ids) to the host for the reference's checks.
-    Returns (output, present_key, present_value)."""
+    ``sliding_window_cache``: the caches are rings of the past capacity (``local_window_size``
+    > 0); "new" presents then take the past's capacity.  ``qk_output`` 1 / 2 writes the
+    scores / probabilities [B, H, S, total] into ``output_qk`` (allocated when None).
+    Returns (output, present_key, present_value), plus output_qk when ``qk_output`` is set."""
     lib = capi.load()
     if query.dim() != 3:
         raise ValueError("query must have rank 3 [batch, sequence, hidden]")
@@ -404,7 +407,7 @@ def group_query_attention(query, key, value, past_key, past_value, seqlens_k,
             raise ValueError("GroupQueryAttention: present='shared' needs past_key/past_value")
         present_key, present_value = past_key, past_value
     elif present == "new" and present_key is None:
-        shape = (B, kv_num_heads, max(past_cap, total), width)
+        shape = (B, kv_num_heads, past_cap if sliding_window_cache else max(past_cap, total), width)
         present_key = torch.empty(shape, dtype=cache_dt, device=query.device)
         present_value = torch.empty(shape, dtype=cache_dt, device=query.device)
     elif present == "omitted":
@@ -415,8 +418,11 @@ def group_query_attention(query, key, value, past_key, past_value, seqlens_k,
     if output is None:
         output = query.new_empty((B, S, num_heads * head))
     cache_code = 0 if cache_dt == query.dtype else pa_dtype(cache_dt)
+    if qk_output and output_qk is None:
+        output_qk = query.new_empty((B, num_heads, S, total))
     node = capi.PaGqaNode(num_heads, kv_num_heads, scale, softcap, local_window_size, do_rotary,
-                          rotary_interleaved, is_causal, qk_norm_epsilon, smooth_softmax)
+                          rotary_interleaved, is_causal, qk_norm_epsilon, smooth_softmax,
+                          int(sliding_window_cache), int(qk_output))
     rot = do_rotary and cos_cache is not None
     io = capi.PaGqaIO(
         dtype=pa_dtype(query.dtype), batch=B, seq=S, query_hidden=query.shape[2], kv_seq=kv_seq,
@@ -437,7 +443,7 @@ def group_query_attention(query, key, value, past_key, past_value, seqlens_k,
         head_sink=_ptr(head_sink), q_norm_weight=_ptr(q_norm_weight),
         k_norm_weight=_ptr(k_norm_weight), output=_ptr(output), cache_dtype=cache_code,
         k_scale=_ptr(k_scale), v_scale=_ptr(v_scale), k_quant_type=_quant(k_quant_type),
-        v_quant_type=_quant(v_quant_type))
+        v_quant_type=_quant(v_quant_type), output_qk=_ptr(output_qk) if qk_output else None)
     if attention_bias is not None and (attention_bias.dim() != 4
                                        or attention_bias.shape[2] != S
                                        or attention_bias.shape[3] != total):
@@ -447,6 +453,8 @@ def group_query_attention(query, key, value, past_key, past_value, seqlens_k,
     ws = _ws.get(max(nbytes, 1), query.device)
     capi.check(lib.pa_group_query_attention(C.byref(node), C.byref(io), _ptr(ws), nbytes,
                                             _stream(query.device)))
+    if qk_output:
+        return output, present_key, present_value, output_qk
     return output, present_key, present_value
 
 

@@ -768,9 +768,15 @@ static int gqa_one_sequence(const orc_gqa_args* a, int b, double* out) {
         double* o = out + qb;
         for (int e = 0; e < d; ++e) o[e] = 0.0;
         double l = sink == -INFINITY ? 0.0 : exp(sink - m);
+        for (int p = lo; p < hi; ++p) l += exp(sc[p] - m);
+        if (a->qk_mode) {
+          /* diagnostics row (b, h, i): visible logits or probabilities, zero elsewhere */
+          double* qk = a->qk_out + (((int64_t)b * H + h) * S + i) * a->total;
+          for (int64_t p = 0; p < a->total; ++p) qk[p] = 0.0;
+          for (int p = lo; p < hi; ++p) qk[p] = a->qk_mode == 1 ? sc[p] : exp(sc[p] - m) / l;
+        }
         for (int p = lo; p < hi; ++p) {
           const double wgt = exp(sc[p] - m);
-          l += wgt;
           const int64_t r = ((int64_t)b * KV + kh) * Pc + p;
           if (quant)
             orc_int_decode_row((const uint8_t*)a->present_v + r * w, d,
@@ -790,12 +796,158 @@ static int gqa_one_sequence(const orc_gqa_args* a, int b, double* out) {
   return rc;
 }
 
+/* sliding_window_cache (attention.rs:1139-1330).  The ring of capacity C holds the last
+ * cache_end(L) rows of a sequence of length L at [0, cache_end(L)): cache_end(L) = L while
+ * L <= C, else L - gap * ceil((L - C) / gap) with gap = C - window + 1 (:1166-1181).  A call with
+ * p = length - S past rows attends its S new rows over the staged view [past rows [0, before) |
+ * new rows] (before = cache_end(p)) with the causal window of causal_window_mask (:1288-1290;
+ * the reference narrows the view to the kept rows when that holds the window, :1183-1192, which
+ * masks the same keys), bias columns at absolute positions p - before + j (:1292-1301), and
+ * writes the present [the last after = cache_end(p + S) rows of the view | zero codes]
+ * (:1338-1368).  RoPE rotates at absolute positions p + i, in fp32 with position ids or a bias
+ * (:1222-1228). */
+static int cache_end(int64_t L, int C, int W) {
+  if (L <= C) return (int)L;
+  const int64_t gap = (int64_t)C - W + 1, over = L - C;
+  return (int)(L - gap * ((over + gap - 1) / gap));
+}
+
+static int gqa_sliding_sequence(const orc_gqa_args* a, int b, double* out) {
+  const int S = a->seq, H = a->num_heads, KV = a->kv_heads, d = a->head_dim;
+  const int dt = a->dtype, g = H / KV, C = a->past_cap, W = a->window;
+  const int cdt = a->cache_dtype ? a->cache_dtype : dt;
+  const int quant = is_int_dt(cdt), bits = cdt == ORC_I8 ? 8 : 4;
+  const int w = quant ? cache_width(cdt, d) : d;
+  const size_t row_bytes = quant ? (size_t)w : (size_t)w * esize(dt);
+  const int f32rope = a->position_ids != NULL || a->bias != NULL;
+  const int kpc = a->k_mode == ORC_QUANT_PER_CHANNEL, vpc = a->v_mode == ORC_QUANT_PER_CHANNEL;
+  if (!a->past_k || a->present_cap != C || W <= 0 || W > C || a->kv_seq != S) return 7;
+  const int length = a->seqlens_k[b] + 1;
+  const int p = length - S;
+  if (p < 0) return 7;
+  const int before = cache_end(p, C, W), after = cache_end((int64_t)p + S, C, W);
+  const int seed = before - (after - S); /* view row of the present's first row */
+  const int L = before + S;               /* rows of the staged view */
+  uint8_t* view_k = (uint8_t*)malloc((size_t)KV * L * row_bytes);
+  uint8_t* view_v = (uint8_t*)malloc((size_t)KV * L * row_bytes);
+  float* row = (float*)malloc((size_t)d * sizeof(float));
+  float* qrow = (float*)malloc((size_t)d * sizeof(float));
+  double* sc = (double*)malloc((size_t)L * sizeof(double));
+  int rc = 0;
+  if (!view_k || !view_v || !row || !qrow || !sc) rc = 4;
+  for (int kh = 0; kh < KV && !rc; ++kh)
+    for (int side = 0; side < 2; ++side) {
+      const uint8_t* src = (const uint8_t*)(side ? a->past_v : a->past_k);
+      uint8_t* view = side ? view_v : view_k;
+      memcpy(view + (size_t)kh * L * row_bytes, src + ((size_t)b * KV + kh) * C * row_bytes,
+             (size_t)before * row_bytes);
+    }
+  /* the new rows, normalised, rotated and encoded as stored */
+  for (int j = 0; j < S && !rc; ++j) {
+    int64_t rp = (int64_t)p + j;
+    if (a->position_ids)
+      rp = a->total == S ? a->position_ids[0] + j : a->position_ids[(int64_t)b * S + j];
+    if (a->cos_cache && (rp < 0 || rp >= a->cos_rows)) {
+      rc = 6;
+      break;
+    }
+    for (int kh = 0; kh < KV; ++kh) {
+      const int64_t src = (((int64_t)b * S + j) * KV + kh) * d;
+      for (int side = 0; side < 2; ++side) {
+        const void* in = side ? a->value : a->key;
+        for (int e = 0; e < d; ++e) row[e] = ld(in, src + e, dt);
+        if (!side && a->k_norm) norm_row(row, d, a->k_norm, a->norm_eps, dt);
+        if (!side && a->cos_cache)
+          rope_row(row, rp, a->cos_cache, a->sin_cache, a->rot_half, a->interleaved, f32rope, dt);
+        uint8_t* dst = (side ? view_v : view_k) + ((size_t)kh * L + before + j) * row_bytes;
+        if (quant) {
+          const float* s = side ? a->v_scale : a->k_scale;
+          const int pc = side ? vpc : kpc;
+          orc_int_encode_row(row, d, pc ? s + (int64_t)kh * d : s, pc, bits, 1, dst);
+        } else {
+          for (int e = 0; e < d; ++e) st(dst, e, row[e], dt);
+        }
+      }
+    }
+  }
+  /* attention of the S query rows over the view */
+  for (int i = 0; i < S && !rc; ++i) {
+    int64_t rp = (int64_t)p + i;
+    if (a->position_ids)
+      rp = a->total == S ? a->position_ids[0] + i : a->position_ids[(int64_t)b * S + i];
+    const int qpos = before + i;
+    const int lo = qpos - W + 1 > 0 ? qpos - W + 1 : 0, hi = qpos + 1;
+    for (int h = 0; h < H; ++h) {
+      const int kh = h / g;
+      const int64_t qb = (((int64_t)b * S + i) * H + h) * d;
+      for (int e = 0; e < d; ++e) qrow[e] = ld(a->query, qb + e, dt);
+      if (a->q_norm) norm_row(qrow, d, a->q_norm, a->norm_eps, dt);
+      if (a->cos_cache)
+        rope_row(qrow, rp, a->cos_cache, a->sin_cache, a->rot_half, a->interleaved, f32rope, dt);
+      double m = -INFINITY;
+      for (int j = lo; j < hi; ++j) {
+        const uint8_t* kr = view_k + ((size_t)kh * L + j) * row_bytes;
+        if (quant)
+          orc_int_decode_row(kr, d, kpc ? a->k_scale + (int64_t)kh * d : a->k_scale, kpc, bits, row);
+        else
+          for (int e = 0; e < d; ++e) row[e] = ld(kr, e, dt);
+        double dot = 0.0;
+        for (int e = 0; e < d; ++e) dot += (double)qrow[e] * (double)row[e];
+        double s = (double)a->scale * dot;
+        if (a->softcap > 0.0f) s = (double)a->softcap * tanh(s / (double)a->softcap);
+        if (a->bias) {
+          const int bb = a->bias_b == 1 ? 0 : b, bh = a->bias_h == 1 ? 0 : h;
+          const int64_t col = (int64_t)p - before + j; /* absolute key position */
+          s += (double)ld(a->bias, (((int64_t)bb * a->bias_h + bh) * S + i) * a->total + col, dt);
+        }
+        sc[j] = s;
+        if (s > m) m = s;
+      }
+      double sink = -INFINITY;
+      if (a->head_sink) sink = (double)ld(a->head_sink, h, dt);
+      else if (a->smooth) sink = 0.0;
+      if (sink > m) m = sink;
+      double* o = out + qb;
+      for (int e = 0; e < d; ++e) o[e] = 0.0;
+      double l = sink == -INFINITY ? 0.0 : exp(sink - m);
+      for (int j = lo; j < hi; ++j) {
+        const double wgt = exp(sc[j] - m);
+        l += wgt;
+        const uint8_t* vr = view_v + ((size_t)kh * L + j) * row_bytes;
+        if (quant)
+          orc_int_decode_row(vr, d, vpc ? a->v_scale + (int64_t)kh * d : a->v_scale, vpc, bits, row);
+        else
+          for (int e = 0; e < d; ++e) row[e] = ld(vr, e, dt);
+        for (int e = 0; e < d; ++e) o[e] += wgt * (double)row[e];
+      }
+      if (l != 0.0)
+        for (int e = 0; e < d; ++e) o[e] /= l;
+    }
+  }
+  /* present: the last `after` rows of the view, then zero codes */
+  for (int kh = 0; kh < KV && !rc; ++kh)
+    for (int side = 0; side < 2; ++side) {
+      const uint8_t* view = side ? view_v : view_k;
+      uint8_t* dst = (uint8_t*)(side ? a->present_v : a->present_k) +
+                     ((size_t)b * KV + kh) * C * row_bytes;
+      memcpy(dst, view + ((size_t)kh * L + seed) * row_bytes, (size_t)after * row_bytes);
+      memset(dst + (size_t)after * row_bytes, cdt == ORC_I4 ? 0x88 : 0,
+             (size_t)(C - after) * row_bytes);
+    }
+  free(view_k);
+  free(view_v);
+  free(row);
+  free(qrow);
+  free(sc);
+  return rc;
+}
+
 int orc_gqa_batched(const orc_gqa_args* a, double* out) {
   int rc = 0;
   /* sequences are independent (each writes its own present rows and output rows) */
   #pragma omp parallel for schedule(dynamic, 1) reduction(max : rc)
   for (int b = 0; b < a->batch; ++b) {
-    int r = gqa_one_sequence(a, b, out);
+    int r = a->sliding ? gqa_sliding_sequence(a, b, out) : gqa_one_sequence(a, b, out);
     if (r > rc) rc = r;
   }
   return rc;

@@ -167,6 +167,13 @@ typedef struct orc_gqa_args {
   const float* k_scale;
   const float* v_scale;
   int k_mode, v_mode;
+  /* sliding_window_cache (attention.rs:1139-1330): past and present are rings of capacity
+   * past_cap (present_cap must equal it) holding the last cache_end(length) rows; window > 0 */
+  int sliding;
+  /* qk_output (attention.rs:771-785): 1 the visible logits (scaled, softcapped, biased; 0 where
+   * masked), 2 the probabilities, into qk_out [B, H, S, total] (columns >= length are 0) */
+  int qk_mode;
+  double* qk_out;
 } orc_gqa_args;
 int orc_gqa_batched(const orc_gqa_args* a, double* out);
 

@@ -42,6 +42,7 @@ class GqaArgs(C.Structure):
         ("scale", C.c_float), ("softcap", C.c_float), ("window", C.c_int), ("causal", C.c_int),
         ("cache_dtype", C.c_int), ("k_scale", C.c_void_p), ("v_scale", C.c_void_p),
         ("k_mode", C.c_int), ("v_mode", C.c_int),
+        ("sliding", C.c_int), ("qk_mode", C.c_int), ("qk_out", C.c_void_p),
     ]
 
 
@@ -252,15 +253,18 @@ def gqa_batched(dtype, q, k, v, past_k, past_v, seqlens_k, total, H, KV, d, *, s
                 present_cap=None, softcap=0.0, window=-1, causal=1, cos=None, sin=None,
                 interleaved=0, position_ids=None, bias=None, head_sink=None, smooth=0,
                 q_norm=None, k_norm=None, norm_eps=1e-6, cache_dtype=0, k_scale=None,
-                v_scale=None, k_mode=0, v_mode=0):
+                v_scale=None, k_mode=0, v_mode=0, sliding=0, qk_mode=0):
     """orc_gqa_batched: every GroupQueryAttention form on contiguous caches.  q [B, S, H*d];
-    k/v [B, kv_seq, KV*d] or None (kv_seq 0); past_k/v [B, KV, cap, w] or None.
-    Returns (out float64 [B, S, H*d], present_k, present_v)."""
+    k/v [B, kv_seq, KV*d] or None (kv_seq 0); past_k/v [B, KV, cap, w] or None.  sliding: the
+    sliding_window_cache ring (present capacity = past capacity); qk_mode 1 / 2: output_qk.
+    Returns (out float64 [B, S, H*d], present_k, present_v), plus the float64 diagnostics
+    [B, H, S, total] when qk_mode is set."""
     B, S = q.shape[0], q.shape[1]
     kv_seq = 0 if k is None else k.shape[1]
     cap = 0 if past_k is None else past_k.shape[2]
     if present_cap is None:
-        present_cap = max(cap, int(total))
+        present_cap = cap if sliding else max(cap, int(total))
+    qk = np.zeros((B, H, S, int(total)), np.float64) if qk_mode else None
     w = d if not cache_dtype else (d if cache_dtype == I8 else (d + 1) // 2)
     raw = RAW[cache_dtype or dtype]
     pres_k = np.zeros((B, KV, present_cap, w), raw)
@@ -288,9 +292,12 @@ def gqa_batched(dtype, q, k, v, past_k, past_v, seqlens_k, total, H, KV, d, *, s
                 smooth=smooth, q_norm=ptr(q_norm), k_norm=ptr(k_norm), norm_eps=norm_eps,
                 scale=scale, softcap=softcap, window=window, causal=causal,
                 cache_dtype=cache_dtype, k_scale=ptr(k_scale, np.float32),
-                v_scale=ptr(v_scale, np.float32), k_mode=k_mode, v_mode=v_mode)
+                v_scale=ptr(v_scale, np.float32), k_mode=k_mode, v_mode=v_mode,
+                sliding=sliding, qk_mode=qk_mode, qk_out=None if qk is None else qk.ctypes.data)
     rc = lib().orc_gqa_batched(C.byref(a), out.ctypes.data)
     assert rc == 0, rc
+    if qk_mode:
+        return out, pres_k, pres_v, qk
     return out, pres_k, pres_v
 
 

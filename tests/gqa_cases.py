@@ -52,6 +52,7 @@ def gqa_case(dtype, B, S, H, KV, d, seqlens, *, cap=None, kv_seq=None, total=Non
 
 
 def run_oracle(c, present_cap=None):
+    """The oracle on a case: (out, present_k, present_v) (+ the diagnostics with qk_mode)."""
     return orc.gqa_batched(
         c["dtype"], c["q"], c["k"], c["v"], c["pk"], c["pv"], c["seqlens"], c["total"], c["H"],
         c["KV"], c["d"], scale=c["scale"], present_cap=present_cap, softcap=c["softcap"],
@@ -59,7 +60,8 @@ def run_oracle(c, present_cap=None):
         position_ids=c.get("pid"), bias=c.get("bias"), head_sink=c.get("sink"),
         smooth=c["smooth"], q_norm=c.get("q_norm"), k_norm=c.get("k_norm"),
         cache_dtype=c["cache_dtype"], k_scale=c.get("k_scale"), v_scale=c.get("v_scale"),
-        k_mode=c.get("k_mode", 0), v_mode=c.get("v_mode", 0))
+        k_mode=c.get("k_mode", 0), v_mode=c.get("v_mode", 0), sliding=c.get("sliding", 0),
+        qk_mode=c.get("qk_mode", 0))
 
 
 FORMS = {

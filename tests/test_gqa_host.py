@@ -97,11 +97,33 @@ def _with(mutate):
 
 
 @pytest.mark.parametrize("mutate,reason", [
-    # forms this build declines
-    (lambda n: (setattr(n, "sliding_window_cache", 1), setattr(n, "local_window_size", 64)),
-     "sliding_window_cache is not executed by this build"),
+    # sliding_window_cache and output_qk rules (attention.rs:2455-2473, :2589-2590, :2730-2748)
+    (lambda n: setattr(n, "sliding_window_cache", 1),
+     "sliding_window_cache=1 requires local_window_size > 0"),
+    (lambda n: (setattr(n, "sliding_window_cache", 1), setattr(n, "local_window_size", 64),
+                setattr(n, "num_outputs", 1)),
+     "sliding_window_cache requires present key/value outputs"),
+    (lambda n: (setattr(n, "sliding_window_cache", 1), setattr(n, "local_window_size", 8192)),
+     "sliding-window key cache capacity must be at least local_window_size"),
+    (lambda n: (setattr(n, "sliding_window_cache", 1), setattr(n, "local_window_size", 64),
+                n.input_shape[4].__setitem__(2, 32)),
+     "sliding-window value cache capacity must be at least local_window_size"),
+    (lambda n: (setattr(n, "sliding_window_cache", 1), setattr(n, "local_window_size", 64),
+                n.input_shape[3].__setitem__(2, -1)),
+     "sliding-window key cache capacity must be at least local_window_size"),
+    (lambda n: (setattr(n, "sliding_window_cache", 1), setattr(n, "local_window_size", 64),
+                setattr(n, "qk_output", 1), setattr(n, "num_outputs", 4),
+                n.output_present.__setitem__(3, 1), n.output_dtype.__setitem__(3, BF16),
+                n.output_rank.__setitem__(3, 4)),
+     "sliding_window_cache with QK diagnostics is unsupported"),
+    (lambda n: (setattr(n, "qk_output", 2), setattr(n, "num_outputs", 4),
+                n.output_present.__setitem__(3, 1), n.output_dtype.__setitem__(3, BF16),
+                n.output_rank.__setitem__(3, 4), n.output_shape[3].__setitem__(1, 16)),
+     "output_qk must be [batch,num_heads,sequence_length,total_sequence_length]"),
     (lambda n: (setattr(n, "qk_output", 1), setattr(n, "num_outputs", 4),
-                n.output_present.__setitem__(3, 1)), "output_qk diagnostics are not executed"),
+                n.output_present.__setitem__(3, 1), n.output_dtype.__setitem__(3, F32),
+                n.output_rank.__setitem__(3, 4)),
+     "output_qk must be [batch,num_heads,sequence_length,total_sequence_length]"),
     # the reference's own reasons
     (lambda n: setattr(n, "num_outputs", 5), "requires 1 to 4 outputs"),
     (lambda n: n.output_present.__setitem__(2, 0), "present_key and present_value must both"),
@@ -145,6 +167,39 @@ def _with(mutate):
 def test_claim_declines_with_reasons(mutate, reason):
     ok, why = group_query_attention_claim(_with(mutate))
     assert not ok and reason in why, why
+
+
+def test_claim_accepts_sliding_and_qk_forms():
+    n = _node()
+    n.sliding_window_cache, n.local_window_size = 1, 4096
+    assert group_query_attention_claim(n)[0]
+    for mode in (1, 2):
+        n = _node()
+        n.qk_output, n.num_outputs = mode, 4
+        n.output_present[3] = 1
+        n.output_dtype[3] = BF16
+        n.output_rank[3] = 4
+        for j, v in enumerate([4, 32, 1, -1]):  # total_sequence_length symbolic
+            n.output_shape[3][j] = v
+        assert group_query_attention_claim(n)[0], group_query_attention_claim(n)[1]
+
+
+def test_claim_sliding_integer_alignment():
+    """Sliding integer rings need 16-byte rows (attention.rs:2589-2590): head % 16 for int8,
+    head % 32 for int4."""
+    for bits, dt, head, ok in ((8, capi.PA_INT8_DTYPE, 16, True), (8, capi.PA_INT8_DTYPE, 24, False),
+                               (4, capi.PA_UINT8_DTYPE, 32, True), (4, capi.PA_UINT8_DTYPE, 48, False),
+                               (4, capi.PA_UINT8_DTYPE, 16, False)):
+        n = _node(cache_dtype=dt, d=head, rotary=False)
+        n.kv_cache_bit_width = bits
+        n.k_quant_type = n.v_quant_type = capi.PA_QUANT_PER_TENSOR
+        _set_input(n, 12, F32, [1])
+        _set_input(n, 13, F32, [1])
+        n.sliding_window_cache, n.local_window_size = 1, 8
+        got, why = group_query_attention_claim(n)
+        assert got == ok, (bits, head, why)
+        if not ok:
+            assert "pinned 16-byte alignment" in why, why
 
 
 def test_claim_integer_cache_rules():
