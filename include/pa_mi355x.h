@@ -191,12 +191,19 @@ size_t pa_attention_workspace_bytes_ex(const pa_cache* cache, const pa_batch* ba
  * paged_attention.rs:46-74).  fp8 and integer caches read every position from the pages (the
  * quantised rule of attention.rs:4192-4194).  q: [num_tokens, num_heads*head_dim]; out
  * likewise.
- * Dispatch: fp16/bf16 with head_dim 64 or 128 run on matrix cores: the balanced (stream-K)
- * decode kernel when (num_heads/kv_heads) * max_query_len <= 16 and the block size is a power
- * of two (fp8 pages too); otherwise, with cache dtype = T, the LDS-shared prefill kernel
- * (128 grouped query rows per workgroup; planned longest-first units with split halves once the
- * batch has at least two row blocks per compute unit); fp32 activations, other head sizes and
- * integer pages use the VALU kernel.  batch->max_query_len = 0 is read as num_tokens. */
+ * Dispatch (fp16/bf16 activations at head sizes 64, 96, 128 and 256 run on matrix cores):
+ *   - decode batches, (num_heads/kv_heads) * max_query_len <= 16 with a power-of-two block size:
+ *     the streaming (stream-K) decode over pages in T, and at heads 64/128 over fp8, int8 and
+ *     int4 pages of at least 16 rows;
+ *   - other batches over pages in T: the LDS-shared prefill kernel (128 grouped query rows per
+ *     workgroup; the planned launch -- longest-first units, long items split in two -- once the
+ *     batch fills two workgroups per compute unit, over operand images when each (sequence,
+ *     kv-head) has at least 4 row blocks);
+ *   - other batches over fp8 / int8 / int4 pages: the planned prefill over operand images (fp16
+ *     rows of the live context, within 2 GiB of workspace);
+ *   - fp32 activations, other head sizes, the LATENT layout and forced split-K chunks over
+ *     byte-coded pages: the VALU kernel.
+ * batch->max_query_len = 0 is read as num_tokens. */
 int pa_attention(const pa_cache* cache, const pa_batch* batch, const pa_attn* attn,
                  pa_dtype act_dtype, const void* q, const void* k_new, const void* v_new,
                  void* out, void* workspace, size_t workspace_bytes, pa_stream_t stream);

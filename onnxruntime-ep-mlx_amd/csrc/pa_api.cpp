@@ -63,7 +63,7 @@ bool is_act(pa_dtype d) {
 
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
-// Largest head size any kernel serves (the VALU kernel; matrix cores take 64 and 128).
+// Largest head size any kernel serves (the VALU kernel; matrix cores take 64, 96, 128, 256).
 constexpr int kMaxHeadDim = 640;
 
 // ---------------------------------------------------------------------------- descriptor checks
@@ -329,7 +329,16 @@ size_t image_bytes(const pa_cache* c, const pa_batch* b, const Plan& pl) {
   if (pl.img_steps == 0) return 0;
   const size_t hb = (size_t)b->batch * c->kv_heads;
   return align256(hb * pl.img_steps * pa::img_step_bytes(c->head_dim)) +
-         align256(hb * pl.img_steps * sizeof(int32_t));
+         align256(hb * pl.img_steps * sizeof(int32_t)) + align256(hb * sizeof(int32_t));
+}
+
+// Per-call number of the image writer's wide-step flags (AttnParams::img_wide): never 0, so a
+// zeroed flag array reads as "no wide step".
+int32_t next_img_epoch() {
+  static std::atomic<uint32_t> epoch{0};
+  uint32_t e = epoch.fetch_add(1, std::memory_order_relaxed) + 1;
+  if ((e & 0x7fffffffu) == 0) e = epoch.fetch_add(1, std::memory_order_relaxed) + 1;
+  return (int32_t)(e & 0x7fffffffu);
 }
 size_t workspace_for(const pa_cache* c, const pa_batch* b, const pa_attn*, const Plan& pl) {
   if (pl.part_rows == 0) return 0;
@@ -442,6 +451,9 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
       p.vimg = img;
       img += align256(hb * pl.img_steps * pa::img_step_bytes(c->head_dim));
       p.vstep = reinterpret_cast<int32_t*>(img);
+      img += align256(hb * pl.img_steps * sizeof(int32_t));
+      p.img_wide = reinterpret_cast<int32_t*>(img);
+      p.img_epoch = next_img_epoch();
       p.img_steps = pl.img_steps;
     }
   }

@@ -381,6 +381,10 @@ struct AttnParams {
   char* vimg;
   int32_t* vstep;
   int32_t img_steps;
+  // per (sequence, kv-head): set to img_epoch (a per-call number) by the image writer when a step
+  // of the pair is wide (bf16 values kept raw, see the image writer); any other value: none
+  int32_t* img_wide;
+  int32_t img_epoch;
 };
 
 // Image geometry of the planned prefill: kImgKeys keys x d dims of 16-bit keys and values per

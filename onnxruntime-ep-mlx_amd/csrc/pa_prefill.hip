@@ -393,6 +393,7 @@ prefill_kernel(const AttnParams p) {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
 
 constexpr int kMxKeys = 64;  // keys per step
@@ -422,6 +423,12 @@ __device__ __forceinline__ float other_half(float x) {
 // the probabilities (scaled by at most 2^-kImgPShift, so probabilities down to 2^(kImgPShift - 14)
 // of the lazy maximum stay fp16-normal).
 constexpr int kImgPShift = 4;
+// Wide steps of bf16 value images: a step whose nonzero values span kImgWideSpan or more binades
+// (some would go subnormal in fp16 under the step's single exponent) keeps its values as raw bf16
+// and is tagged in its exponent word (vstep = s + kImgWideTag); the prefill kernel takes its P.V
+// product in bf16 with the probabilities split into bf16 hi + lo parts.
+constexpr int kImgWideSpan = 29;
+constexpr int kImgWideTag = 1 << 24;
 
 // Maximum of a float over the wavefront (butterfly).
 __device__ __forceinline__ float wave_max_f(float v) {
@@ -625,6 +632,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, IMG && D
 prefill_mx_kernel(const AttnParams p) {
   static_assert(!(INTC || F8S) || IMG, "byte-coded pages over images only");
   using KT = typename std::conditional<INTC || F8S, TF16, TT>::type;  // score operand type
+  // bf16 pages over images: steps may be wide (raw bf16 values, see kImgWideTag).  Head 256 keeps
+  // one loop (its image kernel is at the register limit; a second loop instance spills).
+  constexpr bool kWide = IMG && !INTC && !F8S && std::is_same<TT, TBF16>::value && D <= 128;
   constexpr int ROWS = kPrefillRows;
   static_assert(ROWS == 128, "four wavefronts of 32 rows");
   static_assert(IMG ? img_head(D) : D == 128, "images at heads 64 / 96 / 128 / 256, in-loop staging at 128");
@@ -788,7 +798,11 @@ prefill_mx_kernel(const AttnParams p) {
   // IMG: the accumulator's value exponent (output in units of 2^s_acc; no step seen yet: far below
   // any step's) -- each step's image holds its values in units of 2^sj.
   int s_acc = -(1 << 29);
-  auto attend = [&](const f32x16(&sc)[KB], int t0, const Buf& buf, int sj, int ek) __attribute__((always_inline)) {
+  // WT: std::true_type in the loop instance for (sequence, kv-head) pairs with wide steps (see
+  // kImgWideTag), std::false_type otherwise (the branch on a step's tag costs the common loop
+  // registers, so it lives in a loop of its own)
+  auto attend = [&](auto WT, const f32x16(&sc)[KB], int t0, const Buf& buf, int sj, int ek) __attribute__((always_inline)) {
+    constexpr bool kWideLoop = kWide && decltype(WT)::value;
     // the step's score scale (fp8 pages: its keys are in units of 2^ek)
     const float sl2 = F8S ? __builtin_ldexpf(scale_log2, ek) : scale_log2;
     const float ck = F8S ? __builtin_ldexpf(cap_k, ek) : cap_k;
@@ -855,7 +869,12 @@ prefill_mx_kernel(const AttnParams p) {
     // step's values are negligible against the output and count in the row sums only.
     int dsh = 0;
     bool pv_on = true;
+    bool wide = false;
     if constexpr (IMG) {
+      if constexpr (kWideLoop) {  // raw bf16 values (see kImgWideTag); sj is the step's exponent
+        wide = sj > kImgWideTag / 2;
+        if (wide) sj -= kImgWideTag;
+      }
       int d = __builtin_amdgcn_readfirstlane(s_acc - sj);
       bool up_ok = true;
       if (d > 84) {  // moving up by 2^d: only if the largest |output| stays below 2^120
@@ -885,6 +904,52 @@ prefill_mx_kernel(const AttnParams p) {
         for (int i = 0; i < 16; ++i)
           l_part += __builtin_amdgcn_exp2f(CAP ? x[kb][i] - m0 : __builtin_fmaf(x[kb][i], sl2, -m0));
       return;
+    }
+    if constexpr (kWideLoop) {
+      if (wide) {
+        // P.V in bf16 against the raw bf16 values: the probabilities in units of 2^-s_acc (the
+        // output's units; exact powers of two) as bf16 hi parts, then the remainders as bf16 lo
+        // parts (about 16 bits together), one operand set at a time in the registers the fp16
+        // path uses; the row sum takes the probabilities themselves
+        const float m0 = (m_run == kNegInf) ? 0.0f : m_run;
+        // the value operands through an index the compiler cannot equate with the fp16 path's,
+        // so their LDS reads are not hoisted above the branch (all of them live at once)
+        int vl = lane;
+        asm volatile("" : "+v"(vl));
+        u32x4 pw[2 * KB];
+#pragma unroll
+        for (int part = 0; part < 2; ++part) {
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+              float pe[2];
+#pragma unroll
+              for (int j = 0; j < 2; ++j) {
+                const float xv = x[kb][2 * m + j];
+                const float pv = __builtin_amdgcn_exp2f(CAP ? xv - m0 : __builtin_fmaf(xv, sl2, -m0));
+                if (part == 0) l_part += pv;
+                pe[j] = __builtin_ldexpf(pv, -s_acc);
+              }
+              // hi = RNE bf16 of pe; lo = bf16 of pe - hi (hi read back exactly from its bits)
+              const uint32_t hw = __builtin_bit_cast(
+                  uint32_t, __builtin_convertvector(f32x2v{pe[0], pe[1]}, bf16x2v));
+              uint32_t w = hw;
+              if (part == 1) {
+                const float h0 = __builtin_bit_cast(float, hw << 16);
+                const float h1 = __builtin_bit_cast(float, hw & 0xffff0000u);
+                w = __builtin_bit_cast(uint32_t,
+                                       __builtin_convertvector(f32x2v{pe[0] - h0, pe[1] - h1}, bf16x2v));
+              }
+              pw[2 * kb + (m >> 2)][m & 3] = w;
+            }
+#pragma unroll
+          for (int t = 0; t < 2 * KB; ++t)
+#pragma unroll
+            for (int nt = 0; nt < NQ; ++nt) o[nt] = mfma32<TBF16>(buf.v[t][nt][vl], pw[t], o[nt]);
+        }
+        return;
+      }
     }
     const float msafe = ((m_run == kNegInf) ? 0.0f : m_run) + (float)dsh;
     const _Float16 lw = (_Float16)(float)(1 << dsh);
@@ -925,33 +990,41 @@ prefill_mx_kernel(const AttnParams p) {
     // wavefront finished reading that buffer before the barrier that ended iteration k - 1).
     // The value exponent of step k + 1 is loaded with its operands, at the start of iteration k,
     // so its latency hides under the step's compute like theirs.
-    int sj = 0, sj_next = 0;
-    if (nsteps > 0) {
-      img_issue(lds[0], wave, lane, t_first, img_hb);
-      sj_next = vstep_hb[t_first / KEYS];
-    }
-    wait_vmem();
-    __syncthreads();
-    for (int k = 0; k < nsteps; ++k) {
-      const int t0 = t_first + KEYS * k;
-      sj = __builtin_amdgcn_readfirstlane(sj_next);
-      int ek = 0;
-      if constexpr (F8S) {  // fp8 pages: key exponent above, value exponent below
-        ek = sj >> 16;
-        sj = (int)(int16_t)(sj & 0xffff);
-      }
-      if (k + 1 < nsteps) {
-        img_issue(lds[(k + 1) & 1], wave, lane, t0 + KEYS, img_hb);
-        sj_next = vstep_hb[t0 / KEYS + 1];
-      }
-      if (seen(t0)) {
-        f32x16 sc[KB];
-        scores(lds[k & 1], sc);
-        attend(sc, t0, lds[k & 1], sj, ek);
+    auto steps = [&](auto WT) __attribute__((always_inline)) {
+      int sj = 0, sj_next = 0;
+      if (nsteps > 0) {
+        img_issue(lds[0], wave, lane, t_first, img_hb);
+        sj_next = vstep_hb[t_first / KEYS];
       }
       wait_vmem();
       __syncthreads();
-    }
+      for (int k = 0; k < nsteps; ++k) {
+        const int t0 = t_first + KEYS * k;
+        sj = __builtin_amdgcn_readfirstlane(sj_next);
+        int ek = 0;
+        if constexpr (F8S) {  // fp8 pages: key exponent above, value exponent below
+          ek = sj >> 16;
+          sj = (int)(int16_t)(sj & 0xffff);
+        }
+        if (k + 1 < nsteps) {
+          img_issue(lds[(k + 1) & 1], wave, lane, t0 + KEYS, img_hb);
+          sj_next = vstep_hb[t0 / KEYS + 1];
+        }
+        if (seen(t0)) {
+          f32x16 sc[KB];
+          scores(lds[k & 1], sc);
+          attend(WT, sc, t0, lds[k & 1], sj, ek);
+        }
+        wait_vmem();
+        __syncthreads();
+      }
+    };
+    // pairs whose images hold a wide step (flag == this call's epoch) take the loop that reads
+    // the step tags; stale flags of earlier calls hold other epochs
+    if (kWide && __builtin_amdgcn_readfirstlane(p.img_wide[hb]) == p.img_epoch)
+      steps(std::true_type{});
+    else
+      steps(std::false_type{});
 #pragma unroll
     for (int nt = 0; nt < NQ; ++nt) sv[nt] = s_acc;
   } else {
@@ -970,7 +1043,7 @@ prefill_mx_kernel(const AttnParams p) {
       if (seen(t0)) {
         f32x16 sc[KB];
         scores(lds[k & 1], sc);
-        attend(sc, t0, lds[k & 1], 0, 0);
+        attend(std::false_type{}, sc, t0, lds[k & 1], 0, 0);
       }
       if (k + 1 < nsteps) mx_store<TT>(lds[(k + 1) & 1], st, wave, lane, t0 + KEYS, total, s_stage);
       if (k + 2 < nsteps) mx_load<TT>(w, pw, wave, lane, t0 + 2 * KEYS, st);
@@ -1305,25 +1378,33 @@ __device__ __forceinline__ void img_store(const AttnParams& p, ImgGroup<NT, D>& 
     ek = wave_max_nonneg(f8_step_exp_biased(f8_chunks_absmax<CH>(g.kx) * fabsf(g.ks)));
   }
   if constexpr (BF) {
-    uint32_t mx = 0;
+    // largest magnitude and smallest nonzero magnitude (zeros read as 0x7fff), as bit patterns
+    uint32_t mx = 0, mn = 0x7fff7fffu;
 #pragma unroll
     for (int i = 0; i < CH; ++i)
 #pragma unroll
-      for (int m = 0; m < 4; ++m)
-        mx = __builtin_bit_cast(uint32_t,
-                                __builtin_elementwise_max(__builtin_bit_cast(u16x2, mx),
-                                                          __builtin_bit_cast(u16x2, g.vx[i][m] & 0x7fff7fffu)));
+      for (int m = 0; m < 4; ++m) {
+        const u16x2 a = __builtin_bit_cast(u16x2, g.vx[i][m] & 0x7fff7fffu);
+        mx = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, mx), a));
+        const u16x2 z = __builtin_bit_cast(u16x2, (a == (unsigned short)0)) & (unsigned short)0x7fff;
+        mn = __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(u16x2, mn), a + z));
+      }
     e = wave_max_nonneg((int)(max(mx & 0xffffu, mx >> 16) >> 7));
+    // 255 - the smallest nonzero biased exponent (a max, so the group reduction is one atomicMax)
+    ek = wave_max_nonneg(255 - (int)(min(mn & 0xffffu, mn >> 16) >> 7));
   }
   if (tid < 2 * (NT / 256)) emax[tid] = 0;
   __syncthreads();
   if ((tid & 63) == 0) {
     atomicMax(&emax[grp], e);
-    if (KC == kImgF8) atomicMax(&emax[NT / 256 + grp], ek);
+    if (KC == kImgF8 || BF) atomicMax(&emax[NT / 256 + grp], ek);
   }
   __syncthreads();
-  // bf16: s = emax - 141 puts the largest value into [2^14, 2^15) of fp16; fp16: s = 0
+  // bf16: s = emax - 141 puts the largest value into [2^14, 2^15) of fp16; fp16: s = 0.  A wide
+  // bf16 step (nonzero values kImgWideSpan or more binades apart) keeps its values as they are.
   int sc = BF ? max(emax[grp] - 141, -112) : 0;
+  // (heads up to 128: the prefill kernel at head 256 has no loop for wide steps)
+  const bool wide = BF && D <= 128 && emax[grp] - (255 - emax[NT / 256 + grp]) >= kImgWideSpan;
   if constexpr (KC == kImgF8) {
     // fp8: code x page scale x 2^-s in fp16 (keys under their own s), both exponents to vstep
     const int sv = emax[grp] > 0 ? emax[grp] - 256 : 0;
@@ -1337,7 +1418,11 @@ __device__ __forceinline__ void img_store(const AttnParams& p, ImgGroup<NT, D>& 
     if (g.step_live) store_keys();
     sc = (int)((uint32_t)sk << 16 | ((uint32_t)sv & 0xffffu));
   }
-  if constexpr (BF) {
+  if (wide) {
+    sc += kImgWideTag;
+    if (g.step_live && (tid & 255) == 0) p.img_wide[g.hb] = p.img_epoch;
+  }
+  if (BF && !wide) {
     // bf16 exponent E -> fp16 exponent E - 112 - s: subtract (112 + s) << 7 from the magnitude
     // bits (saturating: values below the fp16 range flush towards zero), shift into place
     const unsigned short bias = (unsigned short)((112 + sc) << 7);
@@ -1599,7 +1684,11 @@ hipError_t launch_d(const AttnParams& p, dim3 grid, hipStream_t s, int pk = kPkT
     }
   }
   if (pk != kPkT) return hipErrorInvalidValue;  // byte-coded pages run over images only
-  if constexpr (D == 128) {
+  // Head 128 without images: fp16 pages on the 32x32 kernel with in-loop staging (fp16 values as
+  // they are); bf16 pages on prefill_kernel below, whose P.V takes the raw bf16 values (hi + lo
+  // probabilities) -- the in-loop fp16 conversion of bf16 values keeps a running power of two per
+  // quarter, under which values 2^-29 below the largest seen so far lose bits.
+  if constexpr (D == 128 && !std::is_same<TT, TBF16>::value) {
     const bool cap = p.softcap > 0.0f;
     if (cap) {
       hipLaunchKernelGGL((prefill_mx_kernel<TT, true, false>), grid, dim3(256), 0, s, p);

@@ -130,3 +130,37 @@ def test_prefill_images_group7_ragged():
     case = make_case(H, KV, d, B * mb, bs, B, dtype=BF16, seed=41, new_lens=new_lens,
                      past=past, max_blocks=mb, std=1.0)
     _check(case, BF16, nq, True)
+
+
+@pytest.mark.parametrize("d,B", [(128, 16), (64, 16), (96, 16), (128, 4), (256, 4)],
+                         ids=["d128_images", "d64_images", "d96_images", "d128_in_loop",
+                              "d256_in_loop"])
+def test_step_with_a_huge_low_probability_value(d, B):
+    """One key per (sequence, kv-head) carries a value row 2^40 times the others with a score
+    ~42 below them (probability ~2^-60): its image step must not lose the ordinary values of
+    the same step, which hold the attention mass of every row (a single exponent per step would
+    put them 2^-40 below the step's largest value, under fp16's range).  Such steps keep raw bf16
+    values and take their P.V product in bf16.  16 sequences fill the planned launch over images
+    (heads 64/96/128; head 256 keeps one exponent per step: values more than 2^-29 below a step's
+    largest lose bits there); 4 sequences take the grid launch without images, whose kernel
+    multiplies raw bf16 values.  Per-sequence bars."""
+    rng = np.random.default_rng(77 + d)
+    H, KV, nq, bs = 32, 8, 128, 16
+    past = np.resize(np.array([300, 450, 120, 600]), B)
+    mb = int((past.max() + nq + bs - 1) // bs)
+    case = make_case(H, KV, d, B * mb, bs, B, dtype=BF16, seed=77 + d, new_lens=np.full(B, nq),
+                     past=past, max_blocks=mb, std=1.0)
+    q = orc.decode(case["query"], BF16).reshape(-1, H, d)
+    q[:, :, 0] = 4.0
+    case["query"] = orc.encode(q.reshape(-1, H * d), BF16)
+    kc = orc.decode(case["key_cache"], BF16)
+    vc = orc.decode(case["value_cache"], BF16)
+    for b in range(B):
+        pos = 100
+        blk, row = case["block_table"][b, pos // bs], pos % bs
+        kc[blk, row] = 0.0
+        kc[blk, row, :, 0] = -120.0 * np.sqrt(d / 128.0)
+        vc[blk, row] = rng.standard_normal((KV, d)) * 2.0 ** 40
+    case["key_cache"] = orc.encode(kc, BF16)
+    case["value_cache"] = orc.encode(vc, BF16)
+    _check(case, BF16, nq, True)
