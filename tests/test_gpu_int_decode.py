@@ -115,3 +115,32 @@ def test_int_kernel_level_streaming_decode(bits):
     assert np.array_equal(a, b)
     got = orc.decode(a, BF16).astype(np.float64)
     assert orc.rel_l2(got, orc.decode(ref_t, BF16)) <= 2e-3
+
+
+# Precision of the bias-carrying key operands: scores are sums of q~ x (code + bias) (bias 1152
+# for int8, 1032 for int4) with bias x sum(q~) taken off afterwards, so the fp32 rounding of the
+# sums scales with bias x sum|q~| rather than with the score.  Peaky softmaxes (queries 8x larger,
+# logits spanning tens of units) and keys at code 0 except one outlier channel (per-tensor int4,
+# scores nearly all from that channel) put the most weight on that rounding.
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("modes", [(PER_TENSOR, PER_TENSOR), (PER_CHANNEL, PER_CHANNEL)],
+                         ids=["tensor", "channel"])
+def test_int_decode_peaky_softmax(bits, modes):
+    case = int_case(bits, 128, seed=bits * 7 + modes[0], modes=modes, B=6, H=16, KV=4)
+    q = orc.decode(case["query"], BF16) * 8.0
+    case["query"] = orc.encode(q, BF16)
+    check(case)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_int4_per_tensor_outlier_channel(d):
+    case = int_case(4, d, seed=31 + d, modes=(PER_TENSOR, PER_TENSOR), B=6, H=16, KV=4)
+    kc = np.full_like(case["key_cache"], 0x88)  # code 0 in both nibbles
+    rng = np.random.default_rng(d)
+    codes = rng.integers(-8, 8, size=kc.shape[:3])  # channel 0 (low nibble of byte 0)
+    kc[..., 0] = ((codes + 8) | (8 << 4)).astype(np.uint8)
+    case["key_cache"] = kc
+    q = orc.decode(case["query"], BF16).reshape(case["query"].shape[0], 16, d)
+    q[:, :, 0] *= 16.0  # the outlier channel dominates the scores
+    case["query"] = orc.encode(q.reshape(-1, 16 * d), BF16)
+    check(case)
