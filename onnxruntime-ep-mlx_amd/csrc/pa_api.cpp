@@ -189,10 +189,10 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
   // numbers the 32-key steps of the whole batch with 32-bit indices: every sequence is clamped
   // to the cache capacity on the device, so batch * (capacity / 32 + 1) bounds the step count.
   const int64_t cap = linear_cap > 0 ? linear_cap : (int64_t)b->max_blocks * c->block_size;
-  // (contiguous caches: pages in the activation dtype only)
+  // (contiguous caches: in the activation dtype or integer codes)
   const bool bal_ok = (int64_t)g * mq <= 16 &&
                       pa::balanced_supported(c->head_dim, act, c->dtype, c->block_size) &&
-                      !(linear && c->dtype != act) &&
+                      !(linear && c->dtype != act && !is_int_cache(c->dtype)) &&
                       (int64_t)c->num_blocks * c->block_size <= (int64_t)UINT32_MAX &&
                       (int64_t)std::max(b->batch, 0) * (cap / 32 + 2) < (int64_t)INT32_MAX;
   // Byte-coded pages (int8 / int4 codes, fp8 e4m3 paged): multi-token batches on the planned
@@ -360,9 +360,10 @@ struct RunOpts {
   bool images = true;  // operand images allowed (see make_plan)
 };
 
-// The kernel family a call with these options runs: a bias or per-sequence key counts (which
-// only the VALU kernel takes) send it to the VALU kernel.
-int effective_kind(int kind, const RunOpts& o) { return (o.bias || o.key_limit) ? 3 : kind; }
+// Operand images for a call with these options: not with a bias (the matrix-core kernels that
+// take one -- the streaming decode and prefill_kernel -- read the cache rows themselves), so
+// byte-coded multi-token batches with a bias run on the VALU kernel.
+bool plan_images(const RunOpts& o) { return o.images && o.bias == nullptr; }
 
 int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype act,
                   const void* q, const void* kn, const void* vn, void* out, void* ws,
@@ -401,9 +402,8 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
     return fail(PA_ERR_UNSUPPORTED, "prefill MFMA kernel does not cover this dtype/head_dim");
   if (!(a->softcap >= 0.0f) || !std::isfinite(a->softcap))
     return fail(PA_ERR_INVALID_ARGUMENT, "softcap must be finite and non-negative");
-  kind = effective_kind(kind, opts);
   Plan pl = make_plan(c, b, a, act, kind, chunk, opts.linear_cap > 0, opts.linear_cap,
-                      opts.images);
+                      plan_images(opts));
   if (kind == 2 && pl.kind != 2 && pa::prefill_coded_supported(c->head_dim, act, c->dtype))
     return fail(PA_ERR_UNSUPPORTED,
                 "prefill MFMA kernel: byte-coded pages run on it over operand images only (planned "
@@ -441,9 +441,12 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
     p.plan_split = reinterpret_cast<int32_t*>(base + 256);
     p.plan_items = (int32_t)pl.plan_items;
     p.plan_rbs = pl.plan_rbs;
-    // workgroups resident per CU: two, three for the 32-key image kernel (148 VGPRs, 33 KB LDS)
+    // workgroups resident per CU: two, three for the 32-key image kernel (148 VGPRs, 33 KB LDS),
+    // one for the bias kernel from head 128 on
     p.plan_slots = (pl.img_steps > 0 && pa::img_keys(c->head_dim) == 32 && c->head_dim <= 128
-                        ? PA_IMG_WAVES : 2) * device_cus();
+                        ? PA_IMG_WAVES
+                    : opts.bias && c->head_dim >= 128 ? 1
+                                                      : 2) * device_cus();
     p.plan_step = pl.img_steps > 0 ? pa::img_keys(c->head_dim) : pa::prefill_key_step(c->head_dim);
     if (pl.img_steps > 0) {
       const size_t hb = (size_t)b->batch * c->kv_heads;
@@ -1099,8 +1102,8 @@ namespace {
 size_t attention_ws(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype act,
                     const RunOpts& o) {
   return workspace_for(c, b, a,
-                       make_plan(c, b, a, act, effective_kind(0, o), 0, o.linear_cap > 0,
-                                 o.linear_cap));
+                       make_plan(c, b, a, act, 0, 0, o.linear_cap > 0, o.linear_cap,
+                                 plan_images(o)));
 }
 
 struct GqaLayout {

@@ -20,6 +20,18 @@
 namespace pa {
 namespace {
 
+// gqa_rope_f32 terms: fp32 products and their sum or difference, each rounded on its own (the
+// pragma above keeps them apart; the HIP __f*_rn helpers are compiled outside it, and their
+// products and sums were fused -- down to one fp16 rounding of a*c - b*s through v_fma_mix).
+__device__ __forceinline__ float rot_sub32(float a, float c, float b, float s) {
+  const float x = a * c, y = b * s;
+  return x - y;
+}
+__device__ __forceinline__ float rot_add32(float a, float c, float b, float s) {
+  const float x = a * c, y = b * s;
+  return x + y;
+}
+
 template <typename TT>
 __device__ __forceinline__ float ldv(const void* p, int64_t i) {
   return TT::to_f32(reinterpret_cast<const typename TT::raw*>(p)[i]);
@@ -145,8 +157,8 @@ __device__ void process_row(const AppendParams& p, const void* src, int64_t src_
     float a = fetch(e1), b = fetch(e2);
     float o1, o2;
     if (p.rope_fp32) {  // each operation rounded to fp32, one rounding to T (gqa_rope_f32)
-      o1 = rnd<TT>(__fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s)));
-      o2 = rnd<TT>(__fadd_rn(__fmul_rn(b, c), __fmul_rn(a, s)));
+      o1 = rnd<TT>(rot_sub32(a, c, b, s));
+      o2 = rnd<TT>(rot_add32(b, c, a, s));
     } else {
       o1 = rnd<TT>(rnd<TT>(a * c) - rnd<TT>(b * s));
       o2 = rnd<TT>(rnd<TT>(b * c) + rnd<TT>(a * s));
@@ -212,8 +224,7 @@ __device__ void int_row(const AppendParams& p, const void* src, int64_t sbase, v
     const float s = ldv<TT>(p.sin_cache, pos * half + i);
     const float a = fetch(e1), b = fetch(e2);
     if (p.rope_fp32)
-      return first ? rnd<TT>(__fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s)))
-                   : rnd<TT>(__fadd_rn(__fmul_rn(b, c), __fmul_rn(a, s)));
+      return first ? rnd<TT>(rot_sub32(a, c, b, s)) : rnd<TT>(rot_add32(b, c, a, s));
     return first ? rnd<TT>(rnd<TT>(a * c) - rnd<TT>(b * s))
                  : rnd<TT>(rnd<TT>(b * c) + rnd<TT>(a * s));
   };

@@ -365,7 +365,7 @@ decode_chunked_kernel(const AttnParams p) {
   const int nq = s1 - s0;
   if (nq <= 0) return;
   const int pastb = clamped_past(p, b, nq);
-  const int total = pastb + nq;
+  const int total = seq_total(p, b, pastb, nq);
   const int start = split * p.chunk;
   if (start >= total) return;
   const int end = min(start + p.chunk, total);
@@ -443,8 +443,9 @@ __device__ __forceinline__ SeqSteps seq_steps(const AttnParams& p, int b) {
   const bool any = q.nq > 0;
   q.pastb = any ? min(max(pb, 0), cap - q.nq) : 0;
   q.total = any ? q.pastb + q.nq : 0;
+  if (p.key_limit && any) q.total = min(q.total, max(p.key_limit[bb], 0));
   q.first = (any && p.window > 0) ? (max(0, q.pastb - p.window + 1) / 32) * 32 : 0;
-  q.n = any ? (q.total - q.first + 31) / 32 : 0;
+  q.n = any ? max(q.total - q.first + 31, 0) / 32 : 0;
   return q;
 }
 
@@ -702,12 +703,15 @@ __device__ __forceinline__ uint64_t tile_row_bytes(const AttnParams& p, const Cu
   return row0 * rowb;
 }
 
-// Cache kinds of the streaming decode: pages in the activation dtype, fp8 e4m3, int8, int4.
-enum DecodeCache { kDcT = 0, kDcFp8 = 1, kDcI8 = 2, kDcI4 = 3 };
+// Cache kinds of the streaming decode: pages in the activation dtype, fp8 e4m3, int8, int4;
+// kDcLin marks integer codes in a contiguous cache and kDcBias an additive attention bias
+// (GroupQueryAttention presents and attention_bias).
+enum DecodeCache { kDcT = 0, kDcFp8 = 1, kDcI8 = 2, kDcI4 = 3, kDcLin = 4, kDcBias = 8 };
 
 template <typename TT, int D, int CK>
 using RingStep = typename std::conditional<
-    CK == kDcT, Step<D>, typename std::conditional<CK == kDcI4, Step4<D>, Step8<D>>::type>::type;
+    (CK & 3) == kDcT, Step<D>,
+    typename std::conditional<(CK & 3) == kDcI4, Step4<D>, Step8<D>>::type>::type;
 
 // Per-lane constants of the streaming loads.
 struct LaneOffs {
@@ -723,13 +727,14 @@ struct LaneOffs {
 struct QueryPtrs {
   const char* q;
   const char* sink;
+  BiasRow br;  // BIAS: the bias row of row r
 };
-template <int D, bool F8>  // F8: the query layout of byte-coded pages (fp8, int8, int4)
+template <int D, bool F8, bool BIAS = false>  // F8: the query layout of byte-coded pages
 __device__ __forceinline__ QueryPtrs query_ptrs(const AttnParams& p, const SeqWin& sw,
                                                 const Cursor& c, int g, int lane) {
   const int cl = lane & 15, G = lane >> 4;
   const int s0 = lane_of(sw.q.s0, c.bl), nq = lane_of(sw.q.nq, c.bl);
-  const int r = min(cl, g * nq - 1);
+  const int r = max(min(cl, g * nq - 1), 0);
   const int rq = r / g, rh = r - rq * g;
   QueryPtrs o;
   o.q = reinterpret_cast<const char*>(p.q) +
@@ -737,6 +742,7 @@ __device__ __forceinline__ QueryPtrs query_ptrs(const AttnParams& p, const SeqWi
   // Sink logit input of that row's head (a harmless read of the query when there is none).
   o.sink = p.head_sink ? reinterpret_cast<const char*>(p.head_sink) + (c.kh * g + rh) * 2
                        : reinterpret_cast<const char*>(p.q);
+  if constexpr (BIAS) o.br = bias_row_of(p, sw.base + c.bl, c.kh * g + rh, rq);
   return o;
 }
 
@@ -794,6 +800,49 @@ __device__ __forceinline__ void load_step4(const AttnParams& p, const Cursor& c,
   }
 }
 
+// Contiguous integer caches [batch, kv_heads, cap, RB bytes] (GroupQueryAttention presents):
+// the same per-lane pieces as load_step8 / load_step4, addressed per lane from the rows of
+// (sequence, kv-head); rows past the sequence end re-read its last row (finite codes, weighted
+// zero), so no load leaves the sequence's rows.
+template <int D, int CK, typename ST>
+__device__ __forceinline__ void load_step_linear(const AttnParams& p, const SeqWin& sw,
+                                                 const Cursor& c, int lane, ST& st) {
+  constexpr int RB = CK == kDcI4 ? D / 2 : D;  // bytes per row
+  const int cl = lane & 15, G = lane >> 4;
+  const int last = c.total - 1;
+  const int64_t r0 = ((int64_t)(sw.base + c.bl) * p.kv_heads + c.kh) * p.linear_cap;
+  const char* kc = reinterpret_cast<const char*>(p.key_cache) + r0 * RB;
+  const char* vc = reinterpret_cast<const char*>(p.value_cache) + r0 * RB;
+#pragma unroll
+  for (int tile = 0; tile < 2; ++tile) {
+    const int tp = c.t + 16 * tile;
+    const char* kr = kc + (int64_t)min(tp + cl, last) * RB;
+#pragma unroll
+    for (int h = 0; h < D / 64; ++h) {
+      if constexpr (CK == kDcI4)
+        st.k[tile][h] = ld8s(kr + 8 * G + 32 * h);
+      else
+        st.k[tile][h] = ld16s(kr + 16 * G + 64 * h);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const char* vr = vc + (int64_t)min(tp + 4 * G + e, last) * RB + (RB / 16) * cl;
+      if constexpr (CK == kDcI4) {
+        if constexpr (D == 128)
+          st.v[4 * tile + e] = ld4s(vr);
+        else
+          st.v[4 * tile + e] =
+              (uint32_t)__builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(vr));
+      } else {
+        if constexpr (D == 128)
+          st.v[4 * tile + e].w = ld8s(vr);
+        else
+          st.v[4 * tile + e].w = ld4s(vr);
+      }
+    }
+  }
+}
+
 // All loads of one step: K and V rows of both 16-key tiles and the query rows of the step's
 // (sequence, kv-head).  Every path issues the same number of loads, so the compiler's vmcnt
 // waits only drain the step about to be computed.  Rows past the sequence end re-read the last
@@ -804,12 +853,17 @@ __device__ __forceinline__ void load_stream_step(const AttnParams& p, const SeqW
                                                  const LaneOffs& lo, const QueryPtrs& qp,
                                                  bool qload, RingStep<TT, D, CK>& st,
                                                  u32x4 (&qv)[D / 32], typename TT::raw& sk) {
-  constexpr bool F8 = CK != kDcT;  // byte-coded pages: the fp8 query layout
+  constexpr bool F8 = (CK & 3) != kDcT;  // byte-coded pages: the fp8 query layout
   const int cl = lane & 15, G = lane >> 4;
-  if constexpr (CK == kDcFp8 || CK == kDcI8) {
-    load_step8<D, CK == kDcFp8>(p, c, btl, lane, bs_shift, lo, st);
-  } else if constexpr (CK == kDcI4) {
-    load_step4<D>(p, c, btl, lane, bs_shift, lo, st);
+  if constexpr ((CK & kDcLin) != 0) {
+    load_step_linear<D, CK & 3>(p, sw, c, lane, st);
+  } else if constexpr (CK == kDcI8 || CK == kDcI4) {
+    if constexpr (CK == kDcI8)
+      load_step8<D, false>(p, c, btl, lane, bs_shift, lo, st);
+    else
+      load_step4<D>(p, c, btl, lane, bs_shift, lo, st);
+  } else if constexpr (CK == kDcFp8) {
+    load_step8<D, true>(p, c, btl, lane, bs_shift, lo, st);
   } else {
     constexpr int DL = D / 16;
     const uint32_t hoff = (uint32_t)c.kh * D * 2;
@@ -883,8 +937,10 @@ __device__ __forceinline__ void load_stream_step(const AttnParams& p, const SeqW
 template <typename TT, int D, bool CAP, int CK, int DEPTH>
 __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& sw, int lo, int hi,
                                              int L, int x, int u0, int lane) {
-  constexpr bool F8 = CK != kDcT;        // byte-coded pages (fp8 query layout)
-  constexpr bool INT = CK >= kDcI8;      // integer codes: fp16 products
+  constexpr bool F8 = (CK & 3) != kDcT;  // byte-coded pages (fp8 query layout)
+  constexpr bool BIAS = (CK & kDcBias) != 0;  // additive bias (GroupQueryAttention)
+  constexpr bool INT = (CK & 3) >= kDcI8;  // integer codes: fp16 products
+  constexpr int CB = CK & 3;               // the code kind (kDcLin: contiguous addressing)
   using MT = typename std::conditional<INT, TF16, TT>::type;  // the products' type
   using vec8 = typename MT::vec8;
   const int c = lane & 15, G = lane >> 4;
@@ -892,10 +948,10 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
   const int bs_shift = __builtin_ctz(p.block_size);  // power of two (host dispatch)
   const int K = hi - lo;
   // bytes per row of one kv-head, and of one key chunk / value slice unit
-  constexpr int RB = CK == kDcT ? 2 * D : CK == kDcI4 ? D / 2 : D;
+  constexpr int RB = CB == kDcT ? 2 * D : CB == kDcI4 ? D / 2 : D;
   LaneOffs lofs;
   lofs.rowb = (uint32_t)p.kv_heads * RB;
-  lofs.koff = (uint32_t)c * lofs.rowb + (CK == kDcI4 ? 8 : 16) * G;
+  lofs.koff = (uint32_t)c * lofs.rowb + (CB == kDcI4 ? 8 : 16) * G;
   lofs.voff = (uint32_t)(4 * G) * lofs.rowb + (uint32_t)(RB / 16) * c;
 
   // Block ids run BA steps ahead of the compute in a ring of NBT entries: 2 * (DEPTH - 1) ahead
@@ -907,10 +963,11 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
   constexpr int U = DEPTH > 1 ? DEPTH : 2;
   Cursor cc = cursor_at(sw, p, lo, L, x, u0);
   Cursor cd = cc, cb = cc;
-  QueryPtrs qp = query_ptrs<D, F8>(p, sw, cd, g, lane);
+  QueryPtrs qp = query_ptrs<D, F8, BIAS>(p, sw, cd, g, lane);
   RingStep<TT, D, CK> st[DEPTH];
   u32x4 qr[DEPTH][D / 32];
   typename TT::raw skr[DEPTH];
+  uint32_t braw[BIAS ? DEPTH : 1][4];  // BIAS: the lane's 8 bias values of each ring step
   int btr[NBT];
   // Prologue: block ids of steps 0 .. DEPTH-2, their rows, block ids of steps DEPTH-1 .. BA-1.
 #pragma unroll
@@ -923,8 +980,9 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
   for (int j = 0; j < DEPTH - 1; ++j) {
     load_stream_step<TT, D, CK>(p, sw, cd, btr[j % NBT], lane, bs_shift, lofs, qp, qload, st[j],
                                 qr[j], skr[j]);
+    if constexpr (BIAS) bias_load(qp.br, cd.t, G, braw[j]);
     qload = cursor_next(cd, sw, p, hi, L, x, u0);
-    if (qload) qp = query_ptrs<D, F8>(p, sw, cd, g, lane);
+    if (qload) qp = query_ptrs<D, F8, BIAS>(p, sw, cd, g, lane);
   }
 #pragma unroll
   for (int j = DEPTH - 1; j < BA; ++j) {
@@ -967,8 +1025,9 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
       const int cs = i % DEPTH;  // ring slot of the step computed now
       load_stream_step<TT, D, CK>(p, sw, cd, btr[bt_use], lane, bs_shift, lofs, qp, qload,
                                   st[sd_slot], qr[sd_slot], skr[sd_slot]);
+      if constexpr (BIAS) bias_load(qp.br, cd.t, G, braw[BIAS ? sd_slot : 0]);
       qload = cursor_next(cd, sw, p, hi, L, x, u0);
-      if (qload) qp = query_ptrs<D, F8>(p, sw, cd, g, lane);
+      if (qload) qp = query_ptrs<D, F8, BIAS>(p, sw, cd, g, lane);
       btr[bt_load] = load_step_blocks(p, sw, cb, lane, bs_shift);
       cursor_next(cb, sw, p, hi, L, x, u0);
       if (k + i < K) {
@@ -988,9 +1047,9 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
           // Every valid row (positions pastb .. pastb + nq - 1) sees keys [full_lo, full_hi):
           // its window and, when causal, the keys up to itself.
           full_lo = p.window > 0 ? pastb + nq - p.window : 0;
-          full_hi = p.causal ? pastb + 1 : pc_total;
+          full_hi = p.causal ? min(pastb + 1, pc_total) : pc_total;
           if constexpr (INT)
-            row_f = int_query<TT, D>(rs, qr[cs], p, pc_kh, G, CK == kDcI8 ? 1152.f : 1032.f,
+            row_f = int_query<TT, D>(rs, qr[cs], p, pc_kh, G, CB == kDcI8 ? 1152.f : 1032.f,
                                      koff);
           else
 #pragma unroll
@@ -1015,21 +1074,23 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
           compute_step<TT, D, CAP, false>(rs, cur, t0, pc_total, G, p.scale_log2, p.scale,
                                           p.softcap, ksA, ksB, vsA, vsB, masked);
         };
+        float bx[8];  // BIAS: the step's bias in log2 units
+        if constexpr (BIAS) bias_log2<TT>(braw[cs], bx);
         if constexpr (INT) {
           // Codes are finite: rows past the end weigh in with probability 0 as they are.
           auto& cur = st[cs];
-          attend_step_ops<MT, D, CAP, true, true, false, true>(
+          attend_step_ops<MT, D, CAP, true, true, false, true, BIAS>(
               rs,
               [&](int tile, int s) {
-                if constexpr (CK == kDcI8) return key_operand_i8<D>(cur, tile, s);
+                if constexpr (CB == kDcI8) return key_operand_i8<D>(cur, tile, s);
                 else return key_operand_i4<D>(cur, tile, s);
               },
               [&](int j) {
-                if constexpr (CK == kDcI8) return value_operand_i8<D>(cur, j);
+                if constexpr (CB == kDcI8) return value_operand_i8<D>(cur, j);
                 else return value_operand_i4<D>(cur, j);
               },
               t0, pc_total, G, p.scale_log2, p.scale, p.softcap, row_f, row_f, 1.f, 1.f, masked,
-              koff);
+              koff, bx);
         } else if constexpr (F8) {
           // Page scales of tiles A and B (lanes 0..3); a tile wholly past the end weighs zero
           // (its page id, and so its scale, is not a real one).
@@ -1052,6 +1113,13 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
               b_live ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc, 1)) : 0.f,
               __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc, 2)),
               b_live ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc, 3)) : 0.f, masked);
+        } else if constexpr (BIAS) {
+          Step<D>& cur = st[cs];
+          clear_tail_rows<D>(cur, t0, pc_total, G);
+          attend_step_ops<TT, D, CAP, false, true, true, false, true>(
+              rs, [&](int tile, int s) { return __builtin_bit_cast(vec8, cur.k[tile][s]); },
+              [&](int j) { return value_operand<TT, D>(cur, j); }, t0, pc_total, G, p.scale_log2,
+              p.scale, p.softcap, 1.f, 1.f, 1.f, 1.f, masked, 0.0f, bx);
         } else {
           run(st[cs], 1.f, 1.f, 1.f, 1.f);
         }
@@ -1128,7 +1196,7 @@ decode_balanced_kernel(const AttnParams p) {
     const int chunk_total = __builtin_amdgcn_readlane(incl, 63);
     const int lo = max(gs, carry), hi = min(ge, carry + chunk_total);
     if (lo < hi)
-      stream_range<TT, D, CAP, CK, CK != kDcT ? PA_DECODE_DEPTH8 : (D > 128 ? 1 : PA_DECODE_DEPTH)>(p, sw, lo, hi, L, x,
+      stream_range<TT, D, CAP, CK, (CK & 3) != kDcT ? PA_DECODE_DEPTH8 : (D > 128 ? 1 : PA_DECODE_DEPTH)>(p, sw, lo, hi, L, x,
                                                                            u0, lane);
     carry += chunk_total;
   }
@@ -1173,6 +1241,11 @@ void launch_balanced_ck(const AttnParams& p, dim3 grid, dim3 block, int ck, hipS
     case kDcFp8: hipLaunchKernelGGL((decode_balanced_kernel<TT, D, CAP, kDcFp8>), grid, block, 0, s, p); break;
     case kDcI8: hipLaunchKernelGGL((decode_balanced_kernel<TT, D, CAP, kDcI8>), grid, block, 0, s, p); break;
     case kDcI4: hipLaunchKernelGGL((decode_balanced_kernel<TT, D, CAP, kDcI4>), grid, block, 0, s, p); break;
+    case kDcI8 | kDcLin: hipLaunchKernelGGL((decode_balanced_kernel<TT, D, CAP, kDcI8 | kDcLin>), grid, block, 0, s, p); break;
+    case kDcI4 | kDcLin: hipLaunchKernelGGL((decode_balanced_kernel<TT, D, CAP, kDcI4 | kDcLin>), grid, block, 0, s, p); break;
+    case kDcBias: hipLaunchKernelGGL((decode_balanced_kernel<TT, D, CAP, kDcBias>), grid, block, 0, s, p); break;
+    case kDcI8 | kDcLin | kDcBias: hipLaunchKernelGGL((decode_balanced_kernel<TT, D, CAP, kDcI8 | kDcLin | kDcBias>), grid, block, 0, s, p); break;
+    case kDcI4 | kDcLin | kDcBias: hipLaunchKernelGGL((decode_balanced_kernel<TT, D, CAP, kDcI4 | kDcLin | kDcBias>), grid, block, 0, s, p); break;
     default: hipLaunchKernelGGL((decode_balanced_kernel<TT, D, CAP, kDcT>), grid, block, 0, s, p); break;
   }
 }
@@ -1183,11 +1256,17 @@ hipError_t launch_d(const AttnParams& p, dim3 grid, dim3 block, bool balanced, i
                     hipStream_t s) {
   if constexpr (D != 64 && D != 128) {
     // Heads 96 / 256: the streaming decode on pages in the activation dtype only.
-    if (!balanced || ck != kDcT) return hipErrorInvalidValue;
-    if (p.softcap > 0.0f)
+    if (!balanced || (ck != kDcT && ck != kDcBias)) return hipErrorInvalidValue;
+    if (ck == kDcBias) {
+      if (p.softcap > 0.0f)
+        hipLaunchKernelGGL((decode_balanced_kernel<TT, D, true, kDcBias>), grid, block, 0, s, p);
+      else
+        hipLaunchKernelGGL((decode_balanced_kernel<TT, D, false, kDcBias>), grid, block, 0, s, p);
+    } else if (p.softcap > 0.0f) {
       hipLaunchKernelGGL((decode_balanced_kernel<TT, D, true, kDcT>), grid, block, 0, s, p);
-    else
+    } else {
       hipLaunchKernelGGL((decode_balanced_kernel<TT, D, false, kDcT>), grid, block, 0, s, p);
+    }
     return hipGetLastError();
   } else if (balanced) {
     if (p.softcap > 0.0f)
@@ -1277,15 +1356,23 @@ hipError_t launch_merge(const AttnParams& p, hipStream_t s) {
 hipError_t launch_decode_balanced(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
                                   hipStream_t s) {
   if (!balanced_supported(p.head_dim, act, cache_dtype, p.block_size)) return hipErrorInvalidValue;
-  const int ck = cache_dtype == PA_DTYPE_FP8_E4M3 ? kDcFp8
-                 : cache_dtype == PA_DTYPE_INT8   ? kDcI8
-                 : cache_dtype == PA_DTYPE_INT4   ? kDcI4
-                                                  : kDcT;
+  int ck = cache_dtype == PA_DTYPE_FP8_E4M3 ? kDcFp8
+           : cache_dtype == PA_DTYPE_INT8   ? kDcI8
+           : cache_dtype == PA_DTYPE_INT4   ? kDcI4
+                                            : kDcT;
   const bool coded = ck != kDcT;
   if (coded != (p.read_all_from_cache != 0)) return hipErrorInvalidValue;
-  if (coded && (p.k_scale == nullptr || p.v_scale == nullptr || p.linear_cap > 0))
+  // contiguous caches: in the activation dtype or integer codes (GroupQueryAttention presents)
+  if (coded && (p.k_scale == nullptr || p.v_scale == nullptr ||
+                (p.linear_cap > 0 && ck == kDcFp8)))
     return hipErrorInvalidValue;
-  if (ck >= kDcI8 && ((p.k_quant != PA_QUANT_PER_TENSOR && p.k_quant != PA_QUANT_PER_CHANNEL) ||
+  if (ck >= kDcI8 && p.linear_cap > 0) ck |= kDcLin;
+  // an additive bias (GroupQueryAttention): caches in the activation dtype or integer codes
+  if (p.bias != nullptr) {
+    if (ck == kDcFp8 || (ck >= kDcI8 && p.linear_cap <= 0)) return hipErrorInvalidValue;
+    ck |= kDcBias;
+  }
+  if ((ck & 3) >= kDcI8 && ((p.k_quant != PA_QUANT_PER_TENSOR && p.k_quant != PA_QUANT_PER_CHANNEL) ||
                       (p.v_quant != PA_QUANT_PER_TENSOR && p.v_quant != PA_QUANT_PER_CHANNEL)))
     return hipErrorInvalidValue;
   if (p.batch <= 0) return hipSuccess;

@@ -210,10 +210,12 @@ __device__ __forceinline__ void store_quarter(u32x4 (*buf)[64], Quarter<D>& q, i
 }
 
 // Two workgroups per CU; one at head 256, whose row state and step operands need the larger
-// register budget.
-template <typename TT, int D, bool CAP, int NG>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D > 128 ? 1 : 2,
-                                                                     D > 128 ? 1 : 2))) void
+// register budget.  BIAS: GroupQueryAttention's additive attention bias (AttnParams::bias), each
+// lane's 8 values per group and step loaded one step ahead (one workgroup per CU from head 128
+// on: two spilled ~25 registers).
+template <typename TT, int D, bool CAP, int NG, bool BIAS = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
+    (D > 128 || (BIAS && D == 128)) ? 1 : 2, (D > 128 || (BIAS && D == 128)) ? 1 : 2))) void
 prefill_kernel(const AttnParams p) {
   using vec8 = typename TT::vec8;
   constexpr int KS = D / 32, DL = D / 16, NI = 2 * KS + DL;
@@ -252,7 +254,7 @@ prefill_kernel(const AttnParams p) {
   const int row0 = rb * ROWS;
   if (row0 >= R) return;
   const int pastb = clamped_past(p, b, nq);
-  const int total = pastb + nq;
+  const int total = seq_total(p, b, pastb, nq);
   int start, end;
   bool single;
   if (p.plan_items > 0) {
@@ -295,6 +297,18 @@ prefill_kernel(const AttnParams p) {
     all_lo = p.window > 0 ? pastb + ql - p.window + 1 : 0;
   }
 
+  // bias rows of this lane in each group (rows past R read row R - 1: never stored)
+  BiasRow brow[NG];
+  uint32_t bnext[BIAS ? NG : 1][4];
+  if constexpr (BIAS) {
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+      const int r = min(wrow0 + 16 * j + c, R - 1);
+      brow[j] = bias_row_of(p, b, kh * g + r % g, r / g);
+      if (nsteps > 0) bias_load(brow[j], t_first, G, bnext[j]);
+    }
+  }
+
   PageWindow pw;
   window_at(pw, w, min(div_bs(t_first, w), w.max_blocks - 1), lane);
   const RoleGeom rg = role_geom<D>(wave, c, G);
@@ -307,6 +321,14 @@ prefill_kernel(const AttnParams p) {
   __syncthreads();
   for (int k = 0; k < nsteps; ++k) {
     const int t0 = t_first + 32 * k;
+    float bx[NG][8];
+    if constexpr (BIAS) {
+#pragma unroll
+      for (int j = 0; j < NG; ++j) {
+        bias_log2<TT>(bnext[j], bx[j]);
+        if (k + 1 < nsteps) bias_load(brow[j], t0 + 32, G, bnext[j]);
+      }
+    }
     if constexpr (D > 128) {
       // Heads above 128: operands read from LDS where they are used (the row state of two
       // groups already takes most of the register file).
@@ -317,11 +339,11 @@ prefill_kernel(const AttnParams p) {
         };
         auto vl = [&](int n) { return __builtin_bit_cast(vec8, lds[bsel][2 * KS + n][lane]); };
         if (t0 >= all_lo && t0 + 32 <= all_hi)
-          attend_groups_ops<TT, D, CAP, false, NG>(rs, kl, vl, t0, end, G, scale_log2, scale,
-                                                   p.softcap);
+          attend_groups_ops<TT, D, CAP, false, NG, BIAS>(rs, kl, vl, t0, end, G, scale_log2,
+                                                         scale, p.softcap, bx);
         else
-          attend_groups_ops<TT, D, CAP, true, NG>(rs, kl, vl, t0, end, G, scale_log2, scale,
-                                                  p.softcap);
+          attend_groups_ops<TT, D, CAP, true, NG, BIAS>(rs, kl, vl, t0, end, G, scale_log2,
+                                                        scale, p.softcap, bx);
       }
     } else if (t0 < any_hi && t0 + 32 > any_lo) {
       u32x4 kop[2][KS];
@@ -334,11 +356,11 @@ prefill_kernel(const AttnParams p) {
       for (int j = 0; j < DL; ++j) vop[j] = lds[k & 1][2 * KS + j][lane];
       auto vb = [&](int n) { return __builtin_bit_cast(vec8, vop[n]); };
       if (t0 >= all_lo && t0 + 32 <= all_hi)
-        attend_groups<TT, D, CAP, false, NG>(rs, kop, vb, t0, end, G, scale_log2, scale,
-                                             p.softcap);
+        attend_groups<TT, D, CAP, false, NG, BIAS>(rs, kop, vb, t0, end, G, scale_log2, scale,
+                                                   p.softcap, bx);
       else
-        attend_groups<TT, D, CAP, true, NG>(rs, kop, vb, t0, end, G, scale_log2, scale,
-                                            p.softcap);
+        attend_groups<TT, D, CAP, true, NG, BIAS>(rs, kop, vb, t0, end, G, scale_log2, scale,
+                                                  p.softcap, bx);
     }
     if (k + 1 < nsteps) store_quarter<D>(lds[(k + 1) & 1], q, wave, t0 + 32, total, lane, G);
     if (k + 2 < nsteps) load_quarter<D>(w, pw, rg, wave, t0 + 64, lane, q);
@@ -672,7 +694,7 @@ prefill_mx_kernel(const AttnParams p) {
   const int row0 = rb * ROWS;
   if (row0 >= R) return;
   const int pastb = clamped_past(p, b, nq);
-  const int total = pastb + nq;
+  const int total = seq_total(p, b, pastb, nq);
   int start, end;
   bool single;
   if (p.plan_items > 0) {
@@ -1163,7 +1185,7 @@ __device__ __forceinline__ ItemKeys item_keys(const AttnParams& p, int i) {
   const int row0 = rb * kPrefillRows;
   if (row0 >= R) return ItemKeys{0, -1};
   const int pastb = clamped_past(p, b, s1 - s0);
-  const int total = pastb + (s1 - s0);
+  const int total = seq_total(p, b, pastb, s1 - s0);
   // Operand images cover img_steps steps of every (sequence, kv-head): a sequence with more keys
   // (beyond the caller's context bound) gets no work, so nothing reads past its images.
   if (p.img_steps > 0 && total > p.img_steps * p.plan_step) return ItemKeys{0, -1};
@@ -1264,7 +1286,7 @@ __device__ __forceinline__ void img_load(const AttnParams& p, int id, ImgGroup<N
   const int s0 = min(max(p.cum[b], 0), p.num_tokens);
   const int s1 = min(max(p.cum[b + 1], s0), p.num_tokens);
   const int pastb = clamped_past(p, b, s1 - s0);
-  const int total = pastb + (s1 - s0);
+  const int total = seq_total(p, b, pastb, s1 - s0);
   const int tid = threadIdx.x;
   g.j = jb * SPW + tid / 256;
   g.step_live = s1 > s0 && g.j < p.img_steps && g.j * KEYS < total;
@@ -1663,6 +1685,16 @@ constexpr int kPkT = 0, kPkInt = 1, kPkF8 = 2;
 template <typename TT, int D>
 hipError_t launch_d(const AttnParams& p, dim3 grid, hipStream_t s, int pk = kPkT) {
   constexpr int NG = kPrefillGroups;
+  if (p.bias != nullptr) {
+    // GroupQueryAttention's additive bias: prefill_kernel at every head size, pages in the
+    // activation dtype, no operand images
+    if (p.vimg != nullptr || pk != kPkT) return hipErrorInvalidValue;
+    if (p.softcap > 0.0f)
+      hipLaunchKernelGGL((prefill_kernel<TT, D, true, NG, true>), grid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((prefill_kernel<TT, D, false, NG, true>), grid, dim3(256), 0, s, p);
+    return hipGetLastError();
+  }
   if constexpr (img_head(D)) {
     if (p.vimg != nullptr) {
       if (pk == kPkInt) {

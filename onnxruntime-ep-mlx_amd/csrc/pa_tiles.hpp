@@ -189,12 +189,15 @@ struct RowState {
 // Scores of the step in log2 units (masked to -inf where not visible); returns this lane's max.
 //
 // `kop(tile, s)` returns the key operand of k-step s of tile 0 (keys t0..t0+15) or 1.
+// BIAS: bx[e] (an additive bias in log2 units for score e of the lane: key t0 + 16 (e / 4) +
+// 4 G + e % 4) is added after the scale and softcap, before the position masks.
 template <typename TT, int D, bool CAP, bool SC, bool MASK, bool FOLD = false, bool KOFF = false,
-          typename KeyOp>
+          bool BIAS = false, typename KeyOp>
 __device__ __forceinline__ float step_scores(const RowState<TT, D>& rs, KeyOp kop, int t0,
                                              int end, int G, float scale_log2, float scale,
                                              float cap, float ksA, float ksB, float (&x)[8],
-                                             bool masked = true, float koff = 0.0f) {
+                                             bool masked = true, float koff = 0.0f,
+                                             const float* bx = nullptr) {
   constexpr int KS = D / 32;
   f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -221,7 +224,7 @@ __device__ __forceinline__ float step_scores(const RowState<TT, D>& rs, KeyOp ko
   // Page scales (SC) fold into the log2-domain score scale: one product per tile.  FOLD (no
   // softcap, no page scales, scale_log2 >= 0): x keeps the raw products, the scale multiplies
   // only their maximum here and enters each exponent through one FMA in step_probs.
-  static_assert(!FOLD || (!CAP && !SC), "FOLD takes plain scaled scores");
+  static_assert(!FOLD || (!CAP && !SC && !BIAS), "FOLD takes plain scaled scores");
   const float xa = SC ? ksA * scale_log2 : scale_log2, xb = SC ? ksB * scale_log2 : scale_log2;
   const float kxa = KOFF ? koff * xa : 0.0f, kxb = KOFF ? koff * xb : 0.0f;
   const float cap_k = CAP ? scale / cap : 0.0f, cap_l2 = cap * kLog2e;
@@ -236,6 +239,7 @@ __device__ __forceinline__ float step_scores(const RowState<TT, D>& rs, KeyOp ko
       x[e] = __builtin_fmaf(sv, (e < 4) ? xa : xb, -((e < 4) ? kxa : kxb));
     else
       x[e] = sv * ((e < 4) ? xa : xb);
+    if constexpr (BIAS) x[e] += bx[e];
   }
   // `masked` (wave-uniform) is false when the caller knows every key of the step is visible to
   // every valid row: one scalar branch instead of the per-score position tests.
@@ -312,17 +316,17 @@ __device__ __forceinline__ void step_probs(RowState<TT, D>& rs, const float (&x)
 // SPLIT = false: P enters the P.V product once, rounded to T (fp16 keeps 11 bits; used for
 // integer pages, whose value operands are exact small integers).
 template <typename TT, int D, bool CAP, bool SC, bool MASK = true, bool SPLIT = true,
-          bool KOFF = false, typename KeyOp, typename ValueOp>
+          bool KOFF = false, bool BIAS = false, typename KeyOp, typename ValueOp>
 __device__ __forceinline__ void attend_step_ops(RowState<TT, D>& rs, KeyOp kop, ValueOp vop,
                                                 int t0, int end, int G, float scale_log2,
                                                 float scale, float cap, float ksA, float ksB,
                                                 float vsA, float vsB, bool masked = true,
-                                                float koff = 0.0f) {
+                                                float koff = 0.0f, const float* bx = nullptr) {
   using vec8 = typename TT::vec8;
   constexpr int DL = D / 16;
   float x[8];
-  const float lmax = step_scores<TT, D, CAP, SC, MASK, false, KOFF>(
-      rs, kop, t0, end, G, scale_log2, scale, cap, ksA, ksB, x, masked, koff);
+  const float lmax = step_scores<TT, D, CAP, SC, MASK, false, KOFF, BIAS>(
+      rs, kop, t0, end, G, scale_log2, scale, cap, ksA, ksB, x, masked, koff, bx);
   if (__any(needs_rescale(rs, lmax))) rescale_rows(rs, lmax, G);
   if constexpr (SPLIT) {
     vec8 phi, plo8;
@@ -361,20 +365,25 @@ __device__ __forceinline__ void attend_step(RowState<TT, D>& rs, const u32x4 (&k
 
 // NG row groups against the same step: all scores first, one branch for the rare rescale, then
 // every group's probabilities and PV MFMAs in one block, each value operand built once.
-// Without softcap the scale folds into the exponents (step_scores FOLD), which takes
+// Without softcap or bias the scale folds into the exponents (step_scores FOLD), which takes
 // scale_log2 >= 0: the caller moves the sign of a negative scale into the query operands.
-template <typename TT, int D, bool CAP, bool MASK, int NG, typename KeyOp, typename ValueOp>
+// BIAS: bx[j] holds group j's additive bias of the lane's scores (log2 units, step_scores).
+template <typename TT, int D, bool CAP, bool MASK, int NG, bool BIAS = false, typename KeyOp,
+          typename ValueOp>
 __device__ __forceinline__ void attend_groups_ops(RowState<TT, D> (&rs)[NG], KeyOp kop,
                                                   ValueOp vop, int t0, int end, int G,
-                                                  float scale_log2, float scale, float cap) {
+                                                  float scale_log2, float scale, float cap,
+                                                  const float (*bx)[8] = nullptr) {
   using vec8 = typename TT::vec8;
   constexpr int DL = D / 16;
+  constexpr bool FOLD = !CAP && !BIAS;
   float x[NG][8], lmax[NG];
   bool any = false;
 #pragma unroll
   for (int j = 0; j < NG; ++j) {
-    lmax[j] = step_scores<TT, D, CAP, false, MASK, !CAP>(rs[j], kop, t0, end, G, scale_log2,
-                                                         scale, cap, 1.f, 1.f, x[j]);
+    lmax[j] = step_scores<TT, D, CAP, false, MASK, FOLD, false, BIAS>(
+        rs[j], kop, t0, end, G, scale_log2, scale, cap, 1.f, 1.f, x[j], true, 0.0f,
+        BIAS ? bx[j] : nullptr);
     any = any || needs_rescale(rs[j], lmax[j]);
   }
   if (__any(any)) {
@@ -385,7 +394,7 @@ __device__ __forceinline__ void attend_groups_ops(RowState<TT, D> (&rs)[NG], Key
   vec8 phi[NG], plo[NG];
 #pragma unroll
   for (int j = 0; j < NG; ++j)
-    step_probs<TT, D, !CAP, false>(rs[j], x[j], scale_log2, 1.f, 1.f, phi[j], plo[j]);
+    step_probs<TT, D, FOLD, false>(rs[j], x[j], scale_log2, 1.f, 1.f, phi[j], plo[j]);
 #pragma unroll
   for (int n = 0; n < DL; ++n) {
     const vec8 vb = vop(n);
@@ -397,15 +406,15 @@ __device__ __forceinline__ void attend_groups_ops(RowState<TT, D> (&rs)[NG], Key
   }
 }
 
-template <typename TT, int D, bool CAP, bool MASK, int NG, typename ValueOp>
+template <typename TT, int D, bool CAP, bool MASK, int NG, bool BIAS = false, typename ValueOp>
 __device__ __forceinline__ void attend_groups(RowState<TT, D> (&rs)[NG],
                                               const u32x4 (&k)[2][D / 32], ValueOp vop, int t0,
                                               int end, int G, float scale_log2, float scale,
-                                              float cap) {
+                                              float cap, const float (*bx)[8] = nullptr) {
   using vec8 = typename TT::vec8;
-  attend_groups_ops<TT, D, CAP, MASK, NG>(
+  attend_groups_ops<TT, D, CAP, MASK, NG, BIAS>(
       rs, [&](int tile, int s) { return __builtin_bit_cast(vec8, k[tile][s]); }, vop, t0, end, G,
-      scale_log2, scale, cap);
+      scale_log2, scale, cap, bx);
 }
 
 // One 32-key step held in registers as loaded (value rows regrouped here).
@@ -428,6 +437,46 @@ __device__ __forceinline__ int clamped_past(const AttnParams& p, int b, int nq) 
                       ? p.linear_cap
                       : (int)min((int64_t)p.max_blocks * p.block_size, (int64_t)(INT32_MAX / 2));
   return min(max(p.past[b], 0), max(cap - nq, 0));
+}
+
+// Keys of sequence b: past + query rows, bounded by key_limit[b] when given (GroupQueryAttention
+// first prompts whose sequences are shorter than the padded query rows).
+__device__ __forceinline__ int seq_total(const AttnParams& p, int b, int pastb, int nq) {
+  const int t = pastb + nq;
+  return p.key_limit ? min(t, max(p.key_limit[b], 0)) : t;
+}
+
+// GroupQueryAttention's additive bias [bias_b, bias_h, bias_rows, bias_cols] in T for one query
+// row: query qi of sequence b at head h (a size-1 batch or head dimension broadcasts); key
+// position pos reads column pos + off clamped into [0, cols), the VALU kernel's rule.
+struct BiasRow {
+  const uint16_t* row;
+  int off, last;
+};
+__device__ __forceinline__ BiasRow bias_row_of(const AttnParams& p, int b, int h, int qi) {
+  const int64_t r = ((int64_t)(p.bias_b == 1 ? 0 : b) * p.bias_h + (p.bias_h == 1 ? 0 : h)) *
+                        p.bias_rows + qi;
+  BiasRow br;
+  br.row = reinterpret_cast<const uint16_t*>(p.bias) + r * p.bias_cols;
+  br.off = p.bias_col_off ? p.bias_col_off[b] : 0;
+  br.last = p.bias_cols - 1;
+  return br;
+}
+// The bias of this lane's 8 scores of a 32-key step (keys t0 + 16 (e / 4) + 4 G + e % 4) as
+// stored (two per word), and in log2 units.
+__device__ __forceinline__ void bias_load(const BiasRow& br, int t0, int G, uint32_t (&raw)[4]) {
+  uint32_t v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    v[e] = br.row[min(max(t0 + 16 * (e >> 2) + 4 * G + (e & 3) + br.off, 0), br.last)];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) raw[i] = v[2 * i] | (v[2 * i + 1] << 16);
+}
+template <typename TT>
+__device__ __forceinline__ void bias_log2(const uint32_t (&raw)[4], float (&bx)[8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    bx[e] = TT::to_f32((typename TT::raw)(raw[e >> 1] >> (16 * (e & 1)))) * kLog2e;
 }
 
 __device__ __forceinline__ WaveInfo make_wave(const AttnParams& p, int D, int b, int kh, int s0,
