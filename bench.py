@@ -60,6 +60,12 @@ def parse():
     ap.add_argument("--cache-dtype", default="bf16", choices=("bf16", "int8", "int4", "fp8"),
                     help="c3 / c4: the same batch over int8 / int4 pages with per-channel "
                          "fp32 scales (bf16 = the config); c4 also over fp8 e4m3 pages")
+    ap.add_argument("--gqa", action="store_true",
+                    help="c3 only: the same decode batch through GroupQueryAttention "
+                         "(pa_group_query_attention) over contiguous presents [64, 8, 8192, 128] "
+                         "updated in place, --cache-dtype bf16 / int8 / int4")
+    ap.add_argument("--bias", action="store_true",
+                    help="with --gqa: an attention_bias [64, 1, 1, total] (bf16 N(0,1))")
     return ap.parse_args()
 
 
@@ -205,6 +211,115 @@ def build_fp8_workload(torch, seed=5):
     w["past"] = torch.full((B,), ctx - 1, dtype=torch.int32, device=dev)
     w["bt"] = torch.from_numpy(bt).to(dev)
     return w
+
+
+class GqaStep:
+    """GroupQueryAttention over the config 3 decode batch: contiguous presents [B, KV, 8192, d]
+    (bf16, or int8 / int4 codes with per-channel scales) updated in place, seqlens_k = ctx - 1,
+    one new token per sequence rotated at position ctx - 1; one ctypes call per step."""
+
+    def __init__(self, torch, w, cache, bias):
+        import numpy as np
+        from onnxruntime_ep_mlx_amd import _capi as capi
+        self.lib, self.capi = capi.load(), capi
+        dev = torch.device("cuda", 0)
+        g = torch.Generator(device=dev).manual_seed(11)
+        B, H, KV, d, cap = w["B"], w["H"], w["KV"], w["d"], 8192
+        if cache == "bf16":
+            self.pk = torch.empty((B, KV, cap, d), dtype=torch.bfloat16, device=dev)
+            self.pv = torch.empty_like(self.pk)
+            for t in (self.pk, self.pv):
+                for b in range(0, B, 8):
+                    t[b:b + 8] = torch.randn((8, KV, cap, d), generator=g,
+                                             device=dev).to(torch.bfloat16)
+            ks = vs = None
+            code, quant = 0, capi.PA_QUANT_NONE
+        else:
+            width, dt = (d, torch.int8) if cache == "int8" else (d // 2, torch.uint8)
+            lo, hi = (-128, 128) if cache == "int8" else (0, 256)
+            self.pk = torch.randint(lo, hi, (B, KV, cap, width), generator=g, device=dev,
+                                    dtype=dt)
+            self.pv = torch.randint(lo, hi, (B, KV, cap, width), generator=g, device=dev,
+                                    dtype=dt)
+            ks = (torch.rand((KV, d), generator=g, device=dev) + 0.5) / 64.0
+            vs = (torch.rand((KV, d), generator=g, device=dev) + 0.5) / 64.0
+            code = capi.PA_DTYPE_INT8 if cache == "int8" else capi.PA_DTYPE_INT4
+            quant = capi.PA_QUANT_PER_CHANNEL
+        self.keep = [ks, vs]
+        self.seqlens = torch.from_numpy((w["ctx"] - 1).astype(np.int32)).to(dev)
+        self.host = np.ascontiguousarray((w["ctx"] - 1).astype(np.int32))
+        self.q = w["q"].view(B, 1, H * d)
+        self.k = w["k"].view(B, 1, KV * d)
+        self.v = w["v"].view(B, 1, KV * d)
+        self.out = torch.empty_like(self.q)
+        total = int(w["ctx"].max())  # the longest sequence after the new token
+        self.bias = (torch.randn((B, 1, 1, total), generator=g, device=dev).to(torch.bfloat16)
+                     if bias else None)
+        ptr = lambda t: None if t is None else t.data_ptr()
+        self.node = capi.PaGqaNode(H, KV, 0.0, 0.0, -1, 1, 0, 1, 1e-6, 0, 0, 0)
+        self.io = capi.PaGqaIO(
+            dtype=capi.PA_DTYPE_BFLOAT16, batch=B, seq=1, query_hidden=H * d, kv_seq=1,
+            query=ptr(self.q), key=ptr(self.k), value=ptr(self.v), past_key=ptr(self.pk),
+            past_value=ptr(self.pv), past_capacity=cap, present_key=ptr(self.pk),
+            present_value=ptr(self.pv), present_capacity=cap, seqlens_k=ptr(self.seqlens),
+            host_seqlens_k=self.host.ctypes.data, total_sequence_length=total,
+            cos_cache=ptr(w["cos"]), sin_cache=ptr(w["sin"]),
+            rotary_positions=w["cos"].shape[0], rotary_half=w["cos"].shape[1],
+            attention_bias=ptr(self.bias), bias_batch=B if bias else 0,
+            bias_heads=1 if bias else 0, output=ptr(self.out), cache_dtype=code,
+            k_scale=ptr(ks), v_scale=ptr(vs), k_quant_type=quant, v_quant_type=quant)
+        self.ws_bytes = self.lib.pa_group_query_attention_workspace_bytes(C.byref(self.node),
+                                                                         C.byref(self.io))
+        self.ws = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=dev)
+        self.stream = torch.cuda.current_stream().cuda_stream
+
+    def __call__(self):
+        self.capi.check(self.lib.pa_group_query_attention(
+            C.byref(self.node), C.byref(self.io), self.ws.data_ptr(), self.ws_bytes,
+            self.stream))
+
+
+def gqa_main(args, torch, ep):
+    """--gqa: the config 3 decode batch through GroupQueryAttention (a variant line, not the
+    driver's default line).  value = KV bytes of the codes or rows read per step / step time."""
+    w = build_workload(torch, ep, args.seed, 128, "bf16")
+    step = GqaStep(torch, w, args.cache_dtype, args.bias)
+    elem = {"bf16": 2, "int8": 1, "int4": 0.5}[args.cache_dtype]
+    kv_bytes = float(w["ctx"].sum()) * w["KV"] * w["d"] * 2 * elem
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t_w = time.perf_counter()
+    while (time.perf_counter() - t_w) * 1e3 < args.warmup_ms:
+        for _ in range(10):
+            step()
+        torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    gbs = kv_bytes / (ms * 1e-3) / 1e9
+    what = f"{args.cache_dtype} presents" + (", attention_bias [64,1,1,total]" if args.bias else "")
+    print(json.dumps({
+        "metric": f"GroupQueryAttention decode GB/s (KV bytes), config 3 batch, {what}",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "us_per_step": round(ms * 1e3, 1),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16" if args.cache_dtype == "bf16" else f"bf16 x {args.cache_dtype}",
+        "data": "synthetic (seeded N(0,1) bf16 rows or uniform codes; N(0,1) q/k/v)",
+        "config": {"workload": "pa_group_query_attention: RoPE + present append + streaming "
+                               "decode over contiguous presents, one token per sequence",
+                   "batch": w["B"], "num_heads": w["H"], "kv_heads": w["KV"], "head_dim": w["d"],
+                   "present_capacity": 8192, "ctx": "U[512,8192]",
+                   "sum_ctx": int(w["ctx"].sum()), "kv_bytes_per_step": int(kv_bytes),
+                   "cache_dtype": args.cache_dtype, "attention_bias": bool(args.bias)},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "whole GroupQueryAttention call (append + decode + merge)"},
+        "cpu_baseline": None}), flush=True)
 
 
 class Step:
@@ -492,9 +607,19 @@ def main():
     if args.config == "c3" and args.cache_dtype == "fp8":
         print("bench.py: the fp8 decode batch is config 5 (--config c5)", file=sys.stderr)
         sys.exit(2)
+    if args.gqa and (args.config != "c3" or args.cache_dtype == "fp8" or args.head_dim != 128):
+        print("bench.py: --gqa takes the config 3 batch at head 128 with bf16 / int8 / int4 "
+              "presents", file=sys.stderr)
+        sys.exit(2)
+    if args.bias and not args.gqa:
+        print("bench.py: --bias applies to --gqa", file=sys.stderr)
+        sys.exit(2)
     import torch
     import onnxruntime_ep_mlx_amd as ep
     torch.cuda.set_device(0)
+    if args.gqa:
+        gqa_main(args, torch, ep)
+        return
     if args.config == "c3":
         w = build_workload(torch, ep, args.seed, args.head_dim, args.cache_dtype)
         step = Step(torch, ep, w, args.chunk, kind=1 if args.cache_dtype == "bf16" else 0)

@@ -357,11 +357,14 @@ int pa_paged_attention_static(const pa_paged_attention_node* node,
  * receives, per (sequence, head, query row), the scaled, softcapped, biased scores where the row
  * sees the key (1) or the probabilities with the sink in the denominator (2), 0 elsewhere and in
  * the columns past the sequence's length; computed on the VALU after the attention.
- * Kernels: fp16/bf16 decode batches at heads 64/96/128/256 (num_heads/kv_heads * seq <= 16) over
- * caches in the activation dtype run the streaming matrix-core decode; multi-token batches at
- * those heads, and every batch over int8 / int4 presents, the matrix-core prefill (integer codes
- * over operand images); a bias, ragged first prompts (sequences shorter than seq), fp32
- * activations and other head sizes the VALU kernel. */
+ * Kernels: fp16/bf16 decode batches (num_heads/kv_heads * seq <= 16) run the streaming
+ * matrix-core decode -- heads 64/96/128/256 over presents in the activation dtype, heads 64/128
+ * over int8 / int4 presents (codes read per lane from the contiguous rows) -- with or without an
+ * attention_bias; multi-token batches at those heads run the matrix-core prefill (int8 / int4
+ * presents over operand images of the codes; with a bias prefill_kernel, which takes it at every
+ * head size, over presents in the activation dtype); ragged first prompts (sequences shorter than
+ * seq) bound each sequence's keys on the same kernels.  fp32 activations, other head sizes and a
+ * bias on a multi-token batch over int8 / int4 presents run the VALU kernel. */
 typedef struct pa_gqa_node {
   int32_t num_heads;          /* "num_heads" */
   int32_t kv_num_heads;       /* "kv_num_heads" */
