@@ -64,6 +64,10 @@ def parse():
                     help="c3 only: the same decode batch through GroupQueryAttention "
                          "(pa_group_query_attention) over contiguous presents [64, 8, 8192, 128] "
                          "updated in place, --cache-dtype bf16 / int8 / int4")
+    ap.add_argument("--latent", type=int, default=0, metavar="HEADS",
+                    help="c3 only: the config 3 contexts through the LATENT layout (MLA: one "
+                         "kv-head of 576-dim rows, values = their first 512 dims, RoPE on the last "
+                         "64) with HEADS query heads (16 or 128)")
     ap.add_argument("--bias", action="store_true",
                     help="with --gqa: an attention_bias [64, 1, 1, total] (bf16 N(0,1))")
     return ap.parse_args()
@@ -277,6 +281,104 @@ class GqaStep:
         self.capi.check(self.lib.pa_group_query_attention(
             C.byref(self.node), C.byref(self.io), self.ws.data_ptr(), self.ws_bytes,
             self.stream))
+
+
+class LatentStep:
+    """The config 3 decode contexts (B=64, ctx U[512,8192] seed 3, block 16) through the LATENT
+    layout: one kv-head of 576-dim key rows whose first 512 dims are the values (MLA), H query
+    heads, RoPE (theta 10000) on dims 512..575, one new row per sequence; one ctypes call per step
+    (pa_paged_attention)."""
+
+    def __init__(self, torch, seed, H):
+        import numpy as np
+        from onnxruntime_ep_mlx_amd import _capi as capi
+        from onnxruntime_ep_mlx_amd.ops import cache_desc
+        self.lib, self.capi = capi.load(), capi
+        rng = np.random.default_rng(seed)
+        B, D, VD, bs = 64, 576, 512, 16
+        self.ctx = rng.integers(512, 8193, size=B).astype(np.int32)
+        mb = 8192 // bs
+        nb = int(sum((int(c) + bs - 1) // bs for c in self.ctx)) + 64
+        perm = rng.permutation(nb).astype(np.int32)
+        bt = np.zeros((B, mb), np.int32)
+        used = 0
+        for b in range(B):
+            n = (int(self.ctx[b]) + bs - 1) // bs
+            bt[b, :n] = perm[used:used + n]
+            bt[b, n:] = perm[used]
+            used += n
+        dev = torch.device("cuda", 0)
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.kc = torch.randn((nb, bs, 1, D), generator=g, device=dev).to(torch.bfloat16)
+        half = 32
+        inv = 1.0 / (10000.0 ** (torch.arange(half, dtype=torch.float64) / half))
+        ang = torch.arange(8192 + 8, dtype=torch.float64)[:, None] * inv[None, :]
+        self.cos = ang.cos().to(torch.bfloat16).to(dev)
+        self.sin = ang.sin().to(torch.bfloat16).to(dev)
+        self.q = torch.randn((B, H * D), generator=g, device=dev).to(torch.bfloat16)
+        self.k = torch.randn((B, D), generator=g, device=dev).to(torch.bfloat16)
+        self.out = torch.empty((B, H * VD), dtype=torch.bfloat16, device=dev)
+        self.cum = torch.arange(B + 1, dtype=torch.int32, device=dev)
+        self.past = torch.from_numpy(self.ctx - 1).to(dev)
+        self.bt = torch.from_numpy(bt).to(dev)
+        self.host = {"cum": np.arange(B + 1, dtype=np.int32),
+                     "past": np.ascontiguousarray(self.ctx - 1), "bt": bt}
+        self.node = capi.PaNode(H, 1, float(1 / np.sqrt(192)), 0.0, -1, 1, 0, VD, 1, 1e-6, VD, 1)
+        self.io = capi.PaIO(
+            capi.PA_DTYPE_BFLOAT16, B, H * D, self.q.data_ptr(), self.k.data_ptr(), None,
+            cache_desc(self.kc, None, head_dim=D), self.cum.data_ptr(), self.past.data_ptr(),
+            self.bt.data_ptr(), B, mb, self.cos.data_ptr(), self.sin.data_ptr(),
+            self.cos.shape[0], half, None, None, None, None, self.host["cum"].ctypes.data,
+            self.host["past"].ctypes.data, self.host["bt"].ctypes.data, None,
+            self.out.data_ptr())
+        self.ws_bytes = self.lib.pa_paged_attention_workspace_bytes(C.byref(self.node),
+                                                                    C.byref(self.io))
+        self.ws = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=dev)
+        self.stream = torch.cuda.current_stream().cuda_stream
+
+    def __call__(self):
+        self.capi.check(self.lib.pa_paged_attention(C.byref(self.node), C.byref(self.io),
+                                                    self.ws.data_ptr(), self.ws_bytes,
+                                                    self.stream))
+
+
+def latent_main(args, torch):
+    """--latent H: a variant line (not the driver's default line).  value = latent-row bytes read
+    per step (sum ctx x 576 x 2, each row once for all heads) / step time."""
+    step = LatentStep(torch, args.seed, args.latent)
+    kv_bytes = float(step.ctx.sum()) * 576 * 2
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t_w = time.perf_counter()
+    while (time.perf_counter() - t_w) * 1e3 < args.warmup_ms:
+        for _ in range(10):
+            step()
+        torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    gbs = kv_bytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": f"LATENT (MLA 576/512) paged decode GB/s (latent-row bytes), config 3 "
+                  f"contexts, {args.latent} query heads",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "us_per_step": round(ms * 1e3, 1),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16 latent rows and queries; random block tables)",
+        "config": {"workload": "pa_paged_attention, kv_cache_layout LATENT: RoPE + append of one "
+                               "latent row per sequence + attention of every head over the rows",
+                   "batch": 64, "num_heads": args.latent, "kv_heads": 1, "head_dim": 576,
+                   "v_head_size": 512, "block_size": 16, "ctx": "U[512,8192]",
+                   "sum_ctx": int(step.ctx.sum()), "latent_bytes_per_step": int(kv_bytes)},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "whole call (append + latent_kernel + split_reduce_kernel)"},
+        "cpu_baseline": None}), flush=True)
 
 
 def gqa_main(args, torch, ep):
@@ -611,6 +713,10 @@ def main():
         print("bench.py: --gqa takes the config 3 batch at head 128 with bf16 / int8 / int4 "
               "presents", file=sys.stderr)
         sys.exit(2)
+    if args.latent and (args.config != "c3" or args.gqa or args.latent not in (16, 128)):
+        print("bench.py: --latent takes 16 or 128 heads over the config 3 contexts",
+              file=sys.stderr)
+        sys.exit(2)
     if args.bias and not args.gqa:
         print("bench.py: --bias applies to --gqa", file=sys.stderr)
         sys.exit(2)
@@ -619,6 +725,9 @@ def main():
     torch.cuda.set_device(0)
     if args.gqa:
         gqa_main(args, torch, ep)
+        return
+    if args.latent:
+        latent_main(args, torch)
         return
     if args.config == "c3":
         w = build_workload(torch, ep, args.seed, args.head_dim, args.cache_dtype)

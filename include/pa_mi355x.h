@@ -201,7 +201,11 @@ size_t pa_attention_workspace_bytes_ex(const pa_cache* cache, const pa_batch* ba
  *     kv-head) has at least 4 row blocks);
  *   - other batches over fp8 / int8 / int4 pages: the planned prefill over operand images (fp16
  *     rows of the live context, within 2 GiB of workspace);
- *   - fp32 activations, other head sizes, the LATENT layout and forced split-K chunks over
+ *   - the LATENT layout (one kv-head, values = the first v_head_size key dims) with the cache in
+ *     the activation dtype, key rows of a multiple of 32 dims up to 640 and values of 128, 256
+ *     or 512 dims (MLA 576 / 512): its matrix-core kernel, all heads served by one read of each
+ *     row per 16 grouped query rows;
+ *   - fp32 activations, other head sizes, other LATENT shapes and forced split-K chunks over
  *     byte-coded pages: the VALU kernel.
  * batch->max_query_len = 0 is read as num_tokens. */
 int pa_attention(const pa_cache* cache, const pa_batch* batch, const pa_attn* attn,
@@ -213,7 +217,8 @@ int pa_attention(const pa_cache* cache, const pa_batch* batch, const pa_attn* at
  * grouped query rows, else chunked split-K), 2 = LDS-shared prefill kernel (planned launch when
  * the batch fills the GPU and chunk_tokens is 0, else split-K chunks), 3 = generic VALU,
  * 4 = decode MFMA with chunked split-K forced.  A kind that does not cover the dtype / head size
- * returns PA_ERR_UNSUPPORTED.
+ * returns PA_ERR_UNSUPPORTED.  The LATENT layout takes 0 (its matrix-core kernel where that
+ * covers the shape) or 3.
  * chunk_tokens: split-K chunk for the chunked/generic kernels (multiple of 32; 0 = automatic). */
 int pa_attention_ex(const pa_cache* cache, const pa_batch* batch, const pa_attn* attn,
                     pa_dtype act_dtype, const void* q, const void* k_new, const void* v_new,

@@ -153,6 +153,10 @@ struct Plan {
 #define PA_IMG_WAVES 2
 #endif
 constexpr int64_t kImgMinRowBlocks = 4;
+// LATENT kernel: context chunks sized for this many workgroups per CU
+#ifndef PA_LATENT_TARGET
+#define PA_LATENT_TARGET 2
+#endif
 constexpr int64_t kImgMaxBytes = (int64_t)1 << 31;
 
 int max_ctx_bound(const pa_cache* c, const pa_batch* b) {
@@ -179,9 +183,15 @@ int device_cus() {
 Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype act, int kind,
                int chunk, bool linear = false, int linear_cap = 0, bool images = true) {
   Plan pl{};
-  // The LATENT layout (values = leading dims of the key rows) runs on the VALU kernel.
-  if (c->value_cache == nullptr || (a->v_head_size > 0 && a->v_head_size != c->head_dim))
-    kind = 3;
+  // The LATENT layout (values = leading dims of the key rows): its matrix-core kernel (kind 5)
+  // where it covers the head sizes and dtypes, else the VALU kernel.
+  if (c->value_cache == nullptr || (a->v_head_size > 0 && a->v_head_size != c->head_dim)) {
+    const int vd = a->v_head_size > 0 ? a->v_head_size : c->head_dim;
+    kind = (kind == 0 && c->kv_heads == 1 &&
+            pa::latent_mfma_supported(c->head_dim, vd, act, c->dtype))
+               ? 5
+               : 3;
+  }
   const int g = a->num_heads / c->kv_heads;
   const int mq = b->max_query_len > 0 ? b->max_query_len : std::max(b->num_tokens, 1);
   const bool mfma = pa::decode_mfma_supported(c->head_dim, act, c->dtype);
@@ -289,10 +299,13 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
     // (token, head) for the VALU kernel.  Split the context only when they cannot fill the
     // GPU (~2048 one-per-SIMD wavefronts for NG = 4, ~4096 otherwise).
     const int64_t rows_pw = 16 * pl.ng;
+    // LATENT kernel: workgroups of 4 wavefronts per 16 grouped rows, one or two per CU
     const int64_t units =
-        pl.kind == 1 ? (int64_t)b->batch * c->kv_heads * (((int64_t)g * mq + rows_pw - 1) / rows_pw)
-                     : (int64_t)std::max(b->num_tokens, 1) * a->num_heads;
-    const int64_t target = pl.ng > 1 ? 2048 : 4096;
+        pl.kind == 1   ? (int64_t)b->batch * c->kv_heads * (((int64_t)g * mq + rows_pw - 1) / rows_pw)
+        : pl.kind == 5 ? (int64_t)b->batch * (((int64_t)g * mq + 15) / 16)
+                       : (int64_t)std::max(b->num_tokens, 1) * a->num_heads;
+    const int64_t target =
+        pl.kind == 5 ? PA_LATENT_TARGET * (int64_t)device_cus() : pl.ng > 1 ? 2048 : 4096;
     if (units >= target) {
       chunk = (int)std::min<int64_t>(((int64_t)ctx + 31) / 32 * 32, INT32_MAX / 2);
     } else {
@@ -303,6 +316,9 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
     }
   }
   chunk = std::max(32, chunk / 32 * 32);
+  // the LATENT kernel holds one window of 64 page ids per chunk
+  if (pl.kind == 5 && c->block_size >= 16)
+    chunk = std::min(chunk, std::max(32, 63 * c->block_size / 32 * 32));
   pl.chunk = chunk;
   pl.max_splits = (int)std::max<int64_t>(1, ((int64_t)ctx + chunk - 1) / chunk);
   pl.part_rows = pl.max_splits > 1
@@ -387,7 +403,9 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
     return fail(PA_ERR_INVALID_ARGUMENT, "q/k_new/v_new/out pointers are NULL");
   if (kind < 0 || kind > 4) return fail(PA_ERR_INVALID_ARGUMENT, "unknown kernel kind %d", kind);
   if (latent && kind != 0 && kind != 3)
-    return fail(PA_ERR_UNSUPPORTED, "the LATENT layout runs on the VALU kernel only");
+    return fail(PA_ERR_UNSUPPORTED,
+                "the LATENT layout runs on its matrix-core kernel (automatic choice) or the VALU "
+                "kernel only");
   if (kind == 4 && !pa::decode_mfma_supported(c->head_dim, act, c->dtype))
     return fail(PA_ERR_UNSUPPORTED, "decode MFMA kernel does not cover this dtype/head_dim");
   if (kind == 1 && !pa::decode_mfma_supported(c->head_dim, act, c->dtype)) {
@@ -509,6 +527,7 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
       e = pl.plan_items > 0 ? pa::launch_prefill_planned(p, act, c->dtype, s)
                             : pa::launch_prefill_mfma(p, act, c->dtype, s);
       break;
+    case 5: e = pa::launch_latent(p, act, c->dtype, s); break;
     default: e = pa::launch_attn_generic(p, act, c->dtype, s); break;
   }
   if (e != hipSuccess) return hip_fail(e, "attention kernel launch");

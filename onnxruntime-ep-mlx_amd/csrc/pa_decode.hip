@@ -126,6 +126,12 @@ __device__ __forceinline__ uint32_t f16pair_sub(uint32_t w, float bias) {
   const f16x2c v = __builtin_bit_cast(f16x2c, w) - f16x2c{(_Float16)bias, (_Float16)bias};
   return __builtin_bit_cast(uint32_t, v);
 }
+// w * a + b on both fp16 halves (exact here: w / 16 and the difference are fp16 integers).
+__device__ __forceinline__ uint32_t f16pair_fma(uint32_t w, float a, float b) {
+  const f16x2c v = __builtin_bit_cast(f16x2c, w) * f16x2c{(_Float16)a, (_Float16)a} +
+                   f16x2c{(_Float16)b, (_Float16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
 
 // int8 pages: Step8 layout (one byte per code).  Key operand of k-step s: words 2 (s & 1) and
 // 2 (s & 1) + 1 of chunk s / 2, as in key_operand8.
@@ -185,15 +191,22 @@ __device__ __forceinline__ f16x8 key_operand_i4(const Step4<D>& r, int tile, int
   return __builtin_bit_cast(f16x8, o);
 }
 
+// Value operand of N-tile j: byte j / 2 of value rows 2m and 2m + 1 into the two halves of word
+// m (one byte permute), the nibble of dim j kept in place under the exponent of 1024 (one
+// and-or): low nibbles (even j) read 1024 + code + 8, high nibbles (odd j) 1024 + 16 (code + 8),
+// both brought back to the exact code by one packed fp16 operation.
 template <int D>
 __device__ __forceinline__ f16x8 value_operand_i4(const Step4<D>& r, int j) {
-  const int sh = 4 * (j & 1), byte = j >> 1;
+  const int byte = j >> 1;
   const uint32_t sel = 0x0c000c00u | ((uint32_t)(4 + byte) << 16) | (uint32_t)byte;
   u32x4 o;
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    const uint32_t lo = (r.v[2 * m] >> sh) & 0x0F0F0F0Fu, hi = (r.v[2 * m + 1] >> sh) & 0x0F0F0F0Fu;
-    o[m] = f16pair_sub(__builtin_amdgcn_perm(hi, lo, sel) | 0x64006400u, 1032.f);
+    const uint32_t t = __builtin_amdgcn_perm(r.v[2 * m + 1], r.v[2 * m], sel);
+    if (j & 1)
+      o[m] = f16pair_fma((t & 0x00F000F0u) | 0x64006400u, 0.0625f, -72.f);
+    else
+      o[m] = f16pair_sub((t & 0x000F000Fu) | 0x64006400u, 1032.f);
   }
   return __builtin_bit_cast(f16x8, o);
 }

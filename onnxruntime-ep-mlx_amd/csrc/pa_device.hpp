@@ -470,6 +470,9 @@ hipError_t launch_prefill_mfma(const AttnParams& p, pa_dtype act, pa_dtype cache
 hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype,
                                   hipStream_t s);
 hipError_t launch_split_reduce(const AttnParams& p, pa_dtype act, hipStream_t s);
+// LATENT layout on matrix cores (pa_latent.hip); partials merged by launch_split_reduce.
+bool latent_mfma_supported(int head_dim, int v_head_dim, pa_dtype act, pa_dtype cache_dtype);
+hipError_t launch_latent(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype, hipStream_t s);
 // GroupQueryAttention output_qk diagnostics (pa_attn_generic.hip): mode 1 scores, 2 probabilities
 // into qk [batch, num_heads, max_query_len, cols]; keys[b]: the sequence's key count.
 hipError_t launch_gqa_qk(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype, void* qk,

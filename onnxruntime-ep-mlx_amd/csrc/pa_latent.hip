@@ -1,0 +1,328 @@
+// pa_latent.hip — the LATENT cache layout on gfx950 matrix cores.
+//
+// Replaces the reference's latent route (kv_cache_layout = "LATENT", attention.rs:4058-4062,
+// :4210-4213): one kv-head whose key rows of D dims (e.g. 576 = 512 latent + 64 rotary dims) are
+// also the value rows, values being their first VD dims; every query head attends the same rows.
+//
+// Work unit: one workgroup of 4 wavefronts per (sequence, block of 16 grouped query rows,
+// context chunk).  Rows r = (query token r / H, head r % H), MFMA column c = row row0 + c.  The
+// four wavefronts split the head dims instead of the rows: wavefront w
+//   - computes the partial scores of its quarter of the k-steps (dims 32 s .. 32 s + 31 for
+//     s in [KS w / 4, KS (w + 1) / 4), KS = D / 32) with 16x16x32 MFMAs, K tile x Q^T;
+//   - adds the four partial score tiles read back from LDS (one barrier per step, two buffers),
+//     in the same order in every wavefront, so all four hold the same scores and run the same
+//     online softmax;
+//   - accumulates P . V for its quarter of the value dims (VD / 4 columns), P split into hi + lo
+//     16-bit parts, from value-row slices read straight from the cache rows.
+// Each key byte is read once per workgroup for the scores; the value dims are the first VD key
+// dims, read a second time in the value layout (the same workgroup at the same time: L2 hits).
+// Steps of 32 keys are loaded two steps ahead into a three-slot register ring.  Partials of split
+// chunks go to the workspace at row (token * H + head) * max_splits + split (stride D), merged by
+// split_reduce_kernel as the VALU kernel's are.
+#include "pa_tiles.hpp"
+
+namespace pa {
+namespace {
+
+constexpr int kLatMaxKw = 5;  // k-steps per wavefront for D <= 640
+
+// Value operand of N-tile j (8 keys x head dim (DW/16) c + j) from the eight value-row slices
+// of a step, as value_operand does for a Step.
+template <typename TT, int DW>
+__device__ __forceinline__ typename TT::vec8 lat_value_operand(const VRow<DW> (&v)[8], int j) {
+  u32x4 w;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const uint32_t lo = v[2 * m].word(j >> 1), hi = v[2 * m + 1].word(j >> 1);
+    w[m] = __builtin_amdgcn_perm(hi, lo, (j & 1) ? 0x07060302u : 0x05040100u);
+  }
+  return __builtin_bit_cast(typename TT::vec8, w);
+}
+
+template <int DW>
+struct LatStep {
+  u32x4 k[2][kLatMaxKw];  // this wavefront's key k-steps of tiles A / B (row c, dims 32 s + 8 G)
+  VRow<DW> v[8];          // value rows 4 G + e of tile A (e < 4) and B (e >= 4), its dims
+};
+
+// Two workgroups per CU at 128 value dims; one from 256 on (the ring of five key k-steps and
+// eight value-row slices per slot takes ~300 registers at 256, ~400 at 512).
+template <typename TT, int DW, bool CAP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DW > 32 ? 1 : 2,
+                                                                     DW > 32 ? 1 : 2))) void
+latent_kernel(const AttnParams p) {
+  using vec8 = typename TT::vec8;
+  constexpr int DL = DW / 16;  // N-tiles (and value dims per lane) of a wavefront
+  __shared__ f32x4 part[2][4][2][64];  // partial score tiles: [buffer][wavefront][tile][lane]
+  const int rb = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, c = lane & 15, G = lane >> 4;
+  const int D = p.head_dim, KS = D / 32;
+  const int ks0 = (KS * wave) / 4, nks = (KS * (wave + 1)) / 4 - ks0;
+  // Everything up to the step loop is uniform over the workgroup (barriers inside the loop).
+  const int s0 = min(max(p.cum[b], 0), p.num_tokens);
+  const int s1 = min(max(p.cum[b + 1], s0), p.num_tokens);
+  const int nq = s1 - s0;
+  const int H = p.num_heads;  // one kv-head: g = H rows per query token
+  const int R = H * nq;
+  const int row0 = rb * 16;
+  if (nq <= 0 || row0 >= R) return;
+  const int pastb = clamped_past(p, b, nq);
+  const int total = seq_total(p, b, pastb, nq);
+  const int start = split * p.chunk;
+  if (start >= total) return;
+  const int end = min(start + p.chunk, total);
+  const bool single = start == 0 && end == total;
+  if (!single && p.part_o == nullptr) return;
+  const int r_last = min(row0 + 16, R) - 1;
+  const int hi_any = p.causal ? pastb + r_last / H + 1 : total;
+  const int lo_any = p.window > 0 ? max(0, pastb + row0 / H - p.window + 1) : 0;
+  const int t_first = max(start, (lo_any / 32) * 32);
+  const int t_last = min(end, hi_any);
+  const int nsteps = t_last > t_first ? (t_last - t_first + 31) / 32 : 0;
+  // keys every row of the block sees: steps inside need no position tests
+  const int all_hi = min(end, p.causal ? pastb + row0 / H + 1 : total);
+  const int all_lo = p.window > 0 ? pastb + r_last / H - p.window + 1 : 0;
+
+  const WaveInfo w = make_wave(p, D, b, 0, s0, pastb, total);
+  // This lane's query row (MFMA column c) and the keys it sees.
+  const int r = row0 + c;
+  const bool rvalid = r < R;
+  const int qi = rvalid ? r / H : 0, head = rvalid ? r % H : 0;
+  const int rpos = pastb + qi;
+  RowState<TT, DW> rs;
+  rs.vis_lo = p.window > 0 ? rpos - p.window + 1 : 0;
+  rs.vis_hi = rvalid ? (p.causal ? rpos + 1 : total) : -1;
+  rs.m_run = kNegInf;
+  rs.l_part = 0.0f;
+#pragma unroll
+  for (int j = 0; j < DL; ++j) rs.o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // A negative scale moves its sign into the query operands.
+  const uint32_t qxor = p.scale < 0.0f ? 0x80008000u : 0u;
+  const float scale = fabsf(p.scale), scale_log2 = fabsf(p.scale_log2);
+  const float cap_k = CAP ? scale / p.softcap : 0.0f, cap_l2 = p.softcap * kLog2e;
+  // Every wavefront runs kLatMaxKw k-steps: those past its own (k >= nks) read k-step KS - 1
+  // again against zero query operands, so the loop carries no branch around loads or MFMAs.
+  vec8 qv[kLatMaxKw];
+  int kofs[kLatMaxKw];  // byte offset of the lane's 16 bytes of each k-step in a key row
+  {
+    const char* qrow =
+        reinterpret_cast<const char*>(p.q) + (((int64_t)(s0 + qi) * H + head) * D) * 2 + 16 * G;
+#pragma unroll
+    for (int k = 0; k < kLatMaxKw; ++k) {
+      kofs[k] = 64 * min(ks0 + k, KS - 1) + 16 * G;
+      const u32x4 v = (k < nks && rvalid) ? (ld16(qrow + 64 * (ks0 + k)) ^ qxor)
+                                          : u32x4{0u, 0u, 0u, 0u};
+      qv[k] = __builtin_bit_cast(vec8, v);
+    }
+  }
+
+  // Page ids of the chunk: one block-table window of 64 entries (the host keeps a chunk within
+  // 64 blocks of 16 or more rows).
+  PageWindow pw;
+  window_at(pw, w, min(div_bs(t_first, w), w.max_blocks - 1), lane);
+  const int vcol = 2 * (DW * wave + DL * c);  // byte offset of this lane's value dims in a row
+  // The sequence's last row (PAGED steps): value rows past the end read it again, so every value
+  // operand is a finite cache row and needs no masking (their probabilities are 0).
+  const char* last_row;
+  {
+    const int bi = min(div_bs(total - 1, w), w.max_blocks - 1);
+    int64_t blk = __builtin_amdgcn_readlane(pw.ids, min(max(bi - pw.first, 0), 63));
+    blk = min(max(blk, (int64_t)0), w.num_blocks - 1);
+    last_row = w.kc + (blk * w.bs + mod_bs(total - 1, w)) * w.rowb;
+  }
+  // PAGED: 16-key tiles wholly in the pages (block size a multiple of 16, every row of the chunk
+  // in the cache): one page id per tile; else row by row (new rows from the batch, other block
+  // sizes; rows past the end read the last row).
+  auto load = [&](auto PAGED, LatStep<DW>& st, int t0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int T = 0; T < 2; ++T) {
+      const int t = t0 + 16 * T;
+      const char* kr;
+      const char* vr[4];
+      if constexpr (decltype(PAGED)::value) {
+        const int bi = min(div_bs(t, w), w.max_blocks - 1);
+        int64_t blk = __builtin_amdgcn_readlane(pw.ids, min(max(bi - pw.first, 0), 63));
+        blk = min(max(blk, (int64_t)0), w.num_blocks - 1);
+        const char* tb = w.kc + (blk * w.bs + mod_bs(t, w)) * w.rowb;
+        kr = tb + (int64_t)c * w.rowb;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          vr[e] = t + 4 * G + e < total ? tb + (int64_t)(4 * G + e) * w.rowb : last_row;
+      } else {
+        kr = row_ptr(w, t + c, false, D);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) vr[e] = row_ptr(w, t + 4 * G + e, false, D);
+      }
+#pragma unroll
+      for (int k = 0; k < kLatMaxKw; ++k) st.k[T][k] = ld16s(kr + kofs[k]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) st.v[4 * T + e] = ld_vrow_s<DW>(vr[e] + vcol);
+    }
+  };
+  auto compute = [&](LatStep<DW>& st, int k) {
+    const int t0 = t_first + 32 * k;
+    f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < kLatMaxKw; ++kk) {
+      sa = TT::mfma(__builtin_bit_cast(vec8, st.k[0][kk]), qv[kk], sa);
+      sb = TT::mfma(__builtin_bit_cast(vec8, st.k[1][kk]), qv[kk], sb);
+    }
+    const int buf = k & 1;
+    part[buf][wave][0][lane] = sa;
+    part[buf][wave][1][lane] = sb;
+    __syncthreads();
+    f32x4 fa = part[buf][0][0][lane], fb = part[buf][0][1][lane];
+#pragma unroll
+    for (int u = 1; u < 4; ++u) {
+      fa += part[buf][u][0][lane];
+      fb += part[buf][u][1][lane];
+    }
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float sv = e < 4 ? fa[e & 3] : fb[e & 3];
+      x[e] = CAP ? softcap_log2(sv, cap_k, cap_l2) : sv * scale_log2;
+    }
+    if (!(t0 >= all_lo && t0 + 32 <= all_hi)) {
+      // positions [vis_lo, min(end, vis_hi)) of the row, one unsigned range test per score
+      const int hi_pos = min(end, rs.vis_hi);
+      const unsigned span = hi_pos > rs.vis_lo ? (unsigned)hi_pos - (unsigned)rs.vis_lo : 0u;
+      const unsigned rel = (unsigned)(t0 + 4 * G) - (unsigned)rs.vis_lo;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const unsigned off = 16 * (e >> 2) + (e & 3);
+        x[e] = (rel + off < span) ? x[e] : kNegInf;
+      }
+    }
+    float lmax = kNegInf;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) lmax = fmaxf(lmax, x[e]);
+    if (__any(needs_rescale(rs, lmax))) rescale_rows(rs, lmax, G);
+    vec8 phi, plo;
+    step_probs<TT, DW, false, false>(rs, x, scale_log2, 1.f, 1.f, phi, plo);
+#pragma unroll
+    for (int j = 0; j < DL; ++j) {
+      const vec8 vb = lat_value_operand<TT, DW>(st.v, j);
+      rs.o[j] = TT::mfma(phi, vb, rs.o[j]);
+      rs.o[j] = TT::mfma(plo, vb, rs.o[j]);
+    }
+  };
+
+  // Three-slot ring: the rows of step k + 2 are issued before step k is computed.
+  auto steps = [&](auto PAGED) __attribute__((always_inline)) {
+    LatStep<DW> st[3];
+    if (nsteps > 0) load(PAGED, st[0], t_first);
+    if (nsteps > 1) load(PAGED, st[1], t_first + 32);
+    for (int k = 0; k < nsteps; k += 3) {
+      if (k + 2 < nsteps) load(PAGED, st[2], t_first + 32 * (k + 2));
+      compute(st[0], k);
+      if (k + 1 < nsteps) {
+        if (k + 3 < nsteps) load(PAGED, st[0], t_first + 32 * (k + 3));
+        compute(st[1], k + 1);
+      }
+      if (k + 2 < nsteps) {
+        if (k + 4 < nsteps) load(PAGED, st[1], t_first + 32 * (k + 4));
+        compute(st[2], k + 2);
+      }
+    }
+  };
+  // every row the steps read below the sequence end in the pages, pages of whole 16-key tiles,
+  // one window of page ids (rows past the end are zeroed or masked)
+  if (w.bs % 16 == 0 && w.cache_limit >= min(w.total, t_first + 32 * nsteps) &&
+      div_bs(t_first + 32 * nsteps - 1, w) - pw.first < 64)
+    steps(std::true_type{});
+  else
+    steps(std::false_type{});
+
+  // Rows 4 G + i of this lane's O registers: this wavefront's DW value dims of each row.
+  float l_row = rs.l_part + __shfl_xor(rs.l_part, 16, 64);
+  l_row += __shfl_xor(l_row, 32, 64);
+  const int VD = 4 * DW;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int rr = row0 + 4 * G + i;
+    const float mi = __shfl(rs.m_run, 4 * G + i, 64);
+    const float li = __shfl(l_row, 4 * G + i, 64);
+    if (rr >= R) continue;
+    const int oh = rr % H;
+    const int64_t t = s0 + rr / H;
+    if (single) {
+      const float f = finalize_factor(mi, li, sink_logit<TT>(p, oh));
+      typename TT::raw vals[DL];
+#pragma unroll
+      for (int j = 0; j < DL; ++j) vals[j] = TT::from_f32(rs.o[j][i] * f);
+      typename TT::raw* dst = reinterpret_cast<typename TT::raw*>(p.out) +
+                              (t * H + oh) * VD + DW * wave + DL * c;
+      if constexpr (DL == 8) {
+        u32x4 pk;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          pk[m] = (uint32_t)vals[2 * m] | ((uint32_t)vals[2 * m + 1] << 16);
+        *reinterpret_cast<u32x4*>(dst) = pk;
+      } else {
+#pragma unroll
+        for (int j = 0; j < DL; ++j) dst[j] = vals[j];
+      }
+    } else {
+      const int64_t pi = (t * H + oh) * p.max_splits + split;
+      float* dst = p.part_o + pi * D + DW * wave + DL * c;
+#pragma unroll
+      for (int j = 0; j < DL; ++j) dst[j] = rs.o[j][i];
+      if (wave == 0 && c == 0) {
+        p.part_ml[pi * 2 + 0] = mi;
+        p.part_ml[pi * 2 + 1] = li;
+      }
+    }
+  }
+}
+
+template <typename TT, int DW>
+void launch_lat_dw(const AttnParams& p, dim3 grid, hipStream_t s) {
+  if (p.softcap > 0.0f)
+    hipLaunchKernelGGL((latent_kernel<TT, DW, true>), grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((latent_kernel<TT, DW, false>), grid, dim3(256), 0, s, p);
+}
+
+template <typename TT>
+void launch_lat_t(const AttnParams& p, dim3 grid, hipStream_t s) {
+  switch (p.v_head_dim) {
+    case 128: launch_lat_dw<TT, 32>(p, grid, s); break;
+    case 256: launch_lat_dw<TT, 64>(p, grid, s); break;
+    default: launch_lat_dw<TT, 128>(p, grid, s); break;
+  }
+}
+
+}  // namespace
+
+// Key rows of D = 32 k dims up to 640 (5 k-steps per wavefront), values = their first 128, 256 or
+// 512 dims, 16-bit activations with the cache in the same type.
+bool latent_mfma_supported(int head_dim, int v_head_dim, pa_dtype act, pa_dtype cache_dtype) {
+  if (act != PA_DTYPE_FLOAT16 && act != PA_DTYPE_BFLOAT16) return false;
+  if (cache_dtype != act) return false;
+  if (head_dim % 32 != 0 || head_dim > 32 * 4 * kLatMaxKw) return false;
+  return (v_head_dim == 128 || v_head_dim == 256 || v_head_dim == 512) && v_head_dim <= head_dim;
+}
+
+// Grid: one workgroup per (16 grouped query rows, context chunk, sequence).
+hipError_t launch_latent(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype, hipStream_t s) {
+  if (!latent_mfma_supported(p.head_dim, p.v_head_dim, act, cache_dtype) || p.kv_heads != 1 ||
+      !p.v_from_key)
+    return hipErrorInvalidValue;
+  if (p.batch <= 0 || p.num_tokens <= 0) return hipSuccess;
+  if (p.chunk < 32 || p.chunk % 32 != 0 || p.max_splits < 1 || p.max_splits > 65535 ||
+      p.batch > 65535)
+    return hipErrorInvalidValue;
+  const int mq = p.max_query_len > 0 ? p.max_query_len : p.num_tokens;
+  const int64_t rbs = ((int64_t)p.num_heads * mq + 15) / 16;
+  if (rbs > INT32_MAX) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)rbs, p.max_splits, p.batch);
+  if (act == PA_DTYPE_FLOAT16)
+    launch_lat_t<TF16>(p, grid, s);
+  else
+    launch_lat_t<TBF16>(p, grid, s);
+  return hipGetLastError();
+}
+
+}  // namespace pa

@@ -59,28 +59,6 @@ __device__ __forceinline__ void load_piece(uint32_t* r, const char* ptr) {
   }
 }
 
-// Block-table window: lane i holds the page id of block first + i.
-struct PageWindow {
-  int first;
-  int ids;
-};
-
-__device__ __forceinline__ void window_at(PageWindow& pw, const WaveInfo& w, int bi, int lane) {
-  pw.first = bi;
-  pw.ids = w.bt[min(bi + lane, w.max_blocks - 1)];
-}
-
-// Byte offset (from the cache base) of the first row of the 16-key tile starting at key t.
-__device__ __forceinline__ int64_t tile_base(const WaveInfo& w, PageWindow& pw, int t, int lane,
-                                             int D) {
-  if (w.lin_row0 >= 0) return (w.lin_row0 + t) * w.rowb;  // contiguous cache
-  const int bi = min(div_bs(t, w), w.max_blocks - 1);
-  if (bi < pw.first || bi >= pw.first + 64) window_at(pw, w, bi, lane);
-  int64_t blk = __builtin_amdgcn_readlane(pw.ids, bi - pw.first);
-  blk = min(max(blk, (int64_t)0), w.num_blocks - 1);
-  return (blk * w.bs + mod_bs(t, w)) * w.rowb + w.hoff;
-}
-
 // Per-lane geometry of a role: piece s sits at row `row0 + s * row_step` of the tile and byte
 // `col0 + (s >> 1) * col_a + (s & 1) * col_b` of that row's kv-head slice.
 struct RoleGeom {

@@ -136,6 +136,28 @@ __device__ __forceinline__ const char* row_ptr(const WaveInfo& w, int pos, bool 
   return (value ? w.vn : w.kn) + tok * w.rowb + w.hoff;
 }
 
+// Block-table window: lane i holds the page id of block first + i.
+struct PageWindow {
+  int first;
+  int ids;
+};
+
+__device__ __forceinline__ void window_at(PageWindow& pw, const WaveInfo& w, int bi, int lane) {
+  pw.first = bi;
+  pw.ids = w.bt[min(bi + lane, w.max_blocks - 1)];
+}
+
+// Byte offset (from the cache base) of the first row of the 16-key tile starting at key t.
+__device__ __forceinline__ int64_t tile_base(const WaveInfo& w, PageWindow& pw, int t, int lane,
+                                             int D) {
+  if (w.lin_row0 >= 0) return (w.lin_row0 + t) * w.rowb;  // contiguous cache
+  const int bi = min(div_bs(t, w), w.max_blocks - 1);
+  if (bi < pw.first || bi >= pw.first + 64) window_at(pw, w, bi, lane);
+  int64_t blk = __builtin_amdgcn_readlane(pw.ids, bi - pw.first);
+  blk = min(max(blk, (int64_t)0), w.num_blocks - 1);
+  return (blk * w.bs + mod_bs(t, w)) * w.rowb + w.hoff;
+}
+
 // Regroup 8 value rows (lane holds DL dims of each) into the MFMA B-operand of N-tile j:
 // 8 keys x head dim DL*c + j.
 template <typename TT, int D>

@@ -68,3 +68,65 @@ def test_latent_mla_sized_heads(new_lens):
                          rotary_offset=512, theta=10000.0, scale=float(1 / np.sqrt(192)),
                          std=1.0)
     check_latent(c)
+
+
+# The LATENT matrix-core kernel (pa_latent.hip: four wavefronts split the score k-steps and the
+# value dims of a 16-row block): MLA heads in both dtypes, 16 and 128 query heads, decode and
+# ragged prefill batches, pages of 8 / 16 / 32 / 64 rows (8: rows addressed one by one), split
+# contexts, softcap / window / sink, a negative scale, and values of 128 / 256 dims.
+@pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("H", [16, 128])
+@pytest.mark.parametrize("new_lens", [[1, 1, 1, 1], [7, 1, 33, 2]], ids=["decode", "prefill"])
+def test_latent_mfma_mla(dtype, H, new_lens):
+    rng = np.random.default_rng(H + len(new_lens) + sum(new_lens) + dtype)
+    past = rng.integers(0, 700, 4)
+    c = make_latent_case(H, 576, 512, 4 * 48, 16, 4, dtype=dtype, seed=int(past.sum()) + H,
+                         new_lens=new_lens, past=past, max_blocks=48, do_rotary=1, rot_dim=64,
+                         rotary_offset=512, theta=10000.0, scale=float(1 / np.sqrt(192)),
+                         std=1.0)
+    check_latent(c)
+
+
+@pytest.mark.parametrize("bs", [8, 32, 64])
+def test_latent_mfma_block_sizes(bs):
+    rng = np.random.default_rng(bs)
+    mb = 768 // bs
+    past = rng.integers(100, 700, 3)
+    c = make_latent_case(16, 576, 512, 3 * mb, bs, 3, dtype=BF16, seed=bs, new_lens=[1, 3, 1],
+                         past=past, max_blocks=mb, do_rotary=1, rot_dim=64, rotary_offset=512,
+                         scale=float(1 / np.sqrt(192)), std=1.0)
+    check_latent(c)
+
+
+@pytest.mark.parametrize("window,softcap,sink", [(100, 0.0, False), (-1, 30.0, True),
+                                                 (37, 20.0, True)])
+def test_latent_mfma_masks_softcap_sink(window, softcap, sink):
+    c = make_latent_case(16, 576, 512, 3 * 48, 16, 3, dtype=BF16, seed=window + 3,
+                         new_lens=[1, 9, 2], past=[600, 250, 0], max_blocks=48, do_rotary=1,
+                         rot_dim=64, rotary_offset=512, scale=float(1 / np.sqrt(192)), std=1.0,
+                         window=window, softcap=softcap,
+                         head_sink=np.linspace(-1, 1, 16) if sink else None)
+    check_latent(c)
+
+
+def test_latent_mfma_long_context_splits():
+    # contexts of ~6000 keys: split into chunks, partials merged by split_reduce_kernel
+    c = make_latent_case(16, 576, 512, 2 * 400, 16, 2, dtype=BF16, seed=41, new_lens=[1, 1],
+                         past=[6390, 5000], max_blocks=400, do_rotary=1, rot_dim=64,
+                         rotary_offset=512, scale=float(1 / np.sqrt(192)), std=1.0)
+    check_latent(c)
+
+
+def test_latent_mfma_negative_scale():
+    c = make_latent_case(16, 576, 512, 3 * 48, 16, 3, dtype=F16, seed=43, new_lens=[1, 4, 1],
+                         past=[300, 20, 700], max_blocks=48, scale=-0.05, std=1.0)
+    check_latent(c)
+
+
+@pytest.mark.parametrize("d,vd", [(320, 256), (192, 128), (512, 512)])
+def test_latent_mfma_value_sizes(d, vd):
+    c = make_latent_case(32, d, vd, 3 * 48, 16, 3, dtype=BF16, seed=d + vd, new_lens=[1, 5, 2],
+                         past=[500, 80, 3], max_blocks=48, do_rotary=1,
+                         rot_dim=d - vd if d > vd else 64, rotary_offset=vd if d > vd else 0,
+                         scale=float(1 / np.sqrt(d)), std=1.0)
+    check_latent(c)
