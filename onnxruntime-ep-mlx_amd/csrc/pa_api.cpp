@@ -302,7 +302,8 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
     // LATENT kernel: workgroups of 4 wavefronts per 16 grouped rows, one or two per CU
     const int64_t units =
         pl.kind == 1   ? (int64_t)b->batch * c->kv_heads * (((int64_t)g * mq + rows_pw - 1) / rows_pw)
-        : pl.kind == 5 ? (int64_t)b->batch * (((int64_t)g * mq + 15) / 16)
+        : pl.kind == 5 ? (int64_t)b->batch * (((int64_t)g * mq + 16 * pa::latent_row_groups(g, mq) - 1) /
+                                             (16 * pa::latent_row_groups(g, mq)))
                        : (int64_t)std::max(b->num_tokens, 1) * a->num_heads;
     const int64_t target =
         pl.kind == 5 ? PA_LATENT_TARGET * (int64_t)device_cus() : pl.ng > 1 ? 2048 : 4096;

@@ -472,6 +472,8 @@ hipError_t launch_prefill_planned(const AttnParams& p, pa_dtype act, pa_dtype ca
 hipError_t launch_split_reduce(const AttnParams& p, pa_dtype act, hipStream_t s);
 // LATENT layout on matrix cores (pa_latent.hip); partials merged by launch_split_reduce.
 bool latent_mfma_supported(int head_dim, int v_head_dim, pa_dtype act, pa_dtype cache_dtype);
+// 16-row groups per LATENT workgroup for H heads and max_query_len mq.
+inline int latent_row_groups(int heads, int mq) { return (int64_t)heads * mq >= 32 ? 2 : 1; }
 hipError_t launch_latent(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype, hipStream_t s);
 // GroupQueryAttention output_qk diagnostics (pa_attn_generic.hip): mode 1 scores, 2 probabilities
 // into qk [batch, num_heads, max_query_len, cols]; keys[b]: the sequence's key count.

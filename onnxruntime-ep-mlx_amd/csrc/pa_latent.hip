@@ -4,8 +4,10 @@
 // :4210-4213): one kv-head whose key rows of D dims (e.g. 576 = 512 latent + 64 rotary dims) are
 // also the value rows, values being their first VD dims; every query head attends the same rows.
 //
-// Work unit: one workgroup of 4 wavefronts per (sequence, block of 16 grouped query rows,
-// context chunk).  Rows r = (query token r / H, head r % H), MFMA column c = row row0 + c.  The
+// Work unit: one workgroup of 4 wavefronts per (sequence, block of 16 NG grouped query rows,
+// context chunk): NG = 2 row groups once a sequence has 32 or more rows, so a row is read once for
+// 32 heads.  Rows r = (query token r / H, head r % H), MFMA column c of group j = row row0 + 16 j +
+// c.  The
 // four wavefronts split the head dims instead of the rows: wavefront w
 //   - computes the partial scores of its quarter of the k-steps (dims 32 s .. 32 s + 31 for
 //     s in [KS w / 4, KS (w + 1) / 4), KS = D / 32) with 16x16x32 MFMAs, K tile x Q^T;
@@ -47,13 +49,14 @@ struct LatStep {
 
 // Two workgroups per CU at 128 value dims; one from 256 on (the ring of five key k-steps and
 // eight value-row slices per slot takes ~300 registers at 256, ~400 at 512).
-template <typename TT, int DW, bool CAP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DW > 32 ? 1 : 2,
-                                                                     DW > 32 ? 1 : 2))) void
+template <typename TT, int DW, bool CAP, int NG>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DW > 32 || NG > 1 ? 1 : 2,
+                                                                     DW > 32 || NG > 1 ? 1 : 2))) void
 latent_kernel(const AttnParams p) {
   using vec8 = typename TT::vec8;
   constexpr int DL = DW / 16;  // N-tiles (and value dims per lane) of a wavefront
-  __shared__ f32x4 part[2][4][2][64];  // partial score tiles: [buffer][wavefront][tile][lane]
+  // partial score tiles: [buffer][wavefront][row group][tile][lane]
+  __shared__ f32x4 part[2][4][NG][2][64];
   const int rb = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, c = lane & 15, G = lane >> 4;
@@ -65,7 +68,7 @@ latent_kernel(const AttnParams p) {
   const int nq = s1 - s0;
   const int H = p.num_heads;  // one kv-head: g = H rows per query token
   const int R = H * nq;
-  const int row0 = rb * 16;
+  const int row0 = rb * 16 * NG;
   if (nq <= 0 || row0 >= R) return;
   const int pastb = clamped_past(p, b, nq);
   const int total = seq_total(p, b, pastb, nq);
@@ -74,7 +77,7 @@ latent_kernel(const AttnParams p) {
   const int end = min(start + p.chunk, total);
   const bool single = start == 0 && end == total;
   if (!single && p.part_o == nullptr) return;
-  const int r_last = min(row0 + 16, R) - 1;
+  const int r_last = min(row0 + 16 * NG, R) - 1;
   const int hi_any = p.causal ? pastb + r_last / H + 1 : total;
   const int lo_any = p.window > 0 ? max(0, pastb + row0 / H - p.window + 1) : 0;
   const int t_first = max(start, (lo_any / 32) * 32);
@@ -85,35 +88,38 @@ latent_kernel(const AttnParams p) {
   const int all_lo = p.window > 0 ? pastb + r_last / H - p.window + 1 : 0;
 
   const WaveInfo w = make_wave(p, D, b, 0, s0, pastb, total);
-  // This lane's query row (MFMA column c) and the keys it sees.
-  const int r = row0 + c;
-  const bool rvalid = r < R;
-  const int qi = rvalid ? r / H : 0, head = rvalid ? r % H : 0;
-  const int rpos = pastb + qi;
-  RowState<TT, DW> rs;
-  rs.vis_lo = p.window > 0 ? rpos - p.window + 1 : 0;
-  rs.vis_hi = rvalid ? (p.causal ? rpos + 1 : total) : -1;
-  rs.m_run = kNegInf;
-  rs.l_part = 0.0f;
-#pragma unroll
-  for (int j = 0; j < DL; ++j) rs.o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // This lane's query row in each row group (MFMA column c of group j: row row0 + 16 j + c)
+  // and the keys it sees.
   // A negative scale moves its sign into the query operands.
   const uint32_t qxor = p.scale < 0.0f ? 0x80008000u : 0u;
   const float scale = fabsf(p.scale), scale_log2 = fabsf(p.scale_log2);
   const float cap_k = CAP ? scale / p.softcap : 0.0f, cap_l2 = p.softcap * kLog2e;
   // Every wavefront runs kLatMaxKw k-steps: those past its own (k >= nks) read k-step KS - 1
   // again against zero query operands, so the loop carries no branch around loads or MFMAs.
-  vec8 qv[kLatMaxKw];
+  RowState<TT, DW> rs[NG];
+  vec8 qv[NG][kLatMaxKw];
   int kofs[kLatMaxKw];  // byte offset of the lane's 16 bytes of each k-step in a key row
-  {
+#pragma unroll
+  for (int k = 0; k < kLatMaxKw; ++k) kofs[k] = 64 * min(ks0 + k, KS - 1) + 16 * G;
+#pragma unroll
+  for (int j = 0; j < NG; ++j) {
+    const int r = row0 + 16 * j + c;
+    const bool rvalid = r < R;
+    const int qi = rvalid ? r / H : 0, head = rvalid ? r % H : 0;
+    const int rpos = pastb + qi;
+    rs[j].vis_lo = p.window > 0 ? rpos - p.window + 1 : 0;
+    rs[j].vis_hi = rvalid ? (p.causal ? rpos + 1 : total) : -1;
+    rs[j].m_run = kNegInf;
+    rs[j].l_part = 0.0f;
+#pragma unroll
+    for (int n = 0; n < DL; ++n) rs[j].o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
     const char* qrow =
         reinterpret_cast<const char*>(p.q) + (((int64_t)(s0 + qi) * H + head) * D) * 2 + 16 * G;
 #pragma unroll
     for (int k = 0; k < kLatMaxKw; ++k) {
-      kofs[k] = 64 * min(ks0 + k, KS - 1) + 16 * G;
       const u32x4 v = (k < nks && rvalid) ? (ld16(qrow + 64 * (ks0 + k)) ^ qxor)
                                           : u32x4{0u, 0u, 0u, 0u};
-      qv[k] = __builtin_bit_cast(vec8, v);
+      qv[j][k] = __builtin_bit_cast(vec8, v);
     }
   }
 
@@ -162,50 +168,63 @@ latent_kernel(const AttnParams p) {
   };
   auto compute = [&](LatStep<DW>& st, int k) {
     const int t0 = t_first + 32 * k;
-    f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kk = 0; kk < kLatMaxKw; ++kk) {
-      sa = TT::mfma(__builtin_bit_cast(vec8, st.k[0][kk]), qv[kk], sa);
-      sb = TT::mfma(__builtin_bit_cast(vec8, st.k[1][kk]), qv[kk], sb);
-    }
     const int buf = k & 1;
-    part[buf][wave][0][lane] = sa;
-    part[buf][wave][1][lane] = sb;
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+      f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < kLatMaxKw; ++kk) {
+        if (kk < nks) {
+          sa = TT::mfma(__builtin_bit_cast(vec8, st.k[0][kk]), qv[j][kk], sa);
+          sb = TT::mfma(__builtin_bit_cast(vec8, st.k[1][kk]), qv[j][kk], sb);
+        }
+      }
+      part[buf][wave][j][0][lane] = sa;
+      part[buf][wave][j][1][lane] = sb;
+    }
     __syncthreads();
-    f32x4 fa = part[buf][0][0][lane], fb = part[buf][0][1][lane];
+    const bool masked = !(t0 >= all_lo && t0 + 32 <= all_hi);
+    vec8 phi[NG], plo[NG];
 #pragma unroll
-    for (int u = 1; u < 4; ++u) {
-      fa += part[buf][u][0][lane];
-      fb += part[buf][u][1][lane];
-    }
-    float x[8];
+    for (int j = 0; j < NG; ++j) {
+      f32x4 fa = part[buf][0][j][0][lane], fb = part[buf][0][j][1][lane];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float sv = e < 4 ? fa[e & 3] : fb[e & 3];
-      x[e] = CAP ? softcap_log2(sv, cap_k, cap_l2) : sv * scale_log2;
-    }
-    if (!(t0 >= all_lo && t0 + 32 <= all_hi)) {
-      // positions [vis_lo, min(end, vis_hi)) of the row, one unsigned range test per score
-      const int hi_pos = min(end, rs.vis_hi);
-      const unsigned span = hi_pos > rs.vis_lo ? (unsigned)hi_pos - (unsigned)rs.vis_lo : 0u;
-      const unsigned rel = (unsigned)(t0 + 4 * G) - (unsigned)rs.vis_lo;
+      for (int u = 1; u < 4; ++u) {
+        fa += part[buf][u][j][0][lane];
+        fb += part[buf][u][j][1][lane];
+      }
+      float x[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const unsigned off = 16 * (e >> 2) + (e & 3);
-        x[e] = (rel + off < span) ? x[e] : kNegInf;
+        const float sv = e < 4 ? fa[e & 3] : fb[e & 3];
+        x[e] = CAP ? softcap_log2(sv, cap_k, cap_l2) : sv * scale_log2;
       }
+      if (masked) {
+        // positions [vis_lo, min(end, vis_hi)) of the row, one unsigned range test per score
+        const int hi_pos = min(end, rs[j].vis_hi);
+        const unsigned span =
+            hi_pos > rs[j].vis_lo ? (unsigned)hi_pos - (unsigned)rs[j].vis_lo : 0u;
+        const unsigned rel = (unsigned)(t0 + 4 * G) - (unsigned)rs[j].vis_lo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const unsigned off = 16 * (e >> 2) + (e & 3);
+          x[e] = (rel + off < span) ? x[e] : kNegInf;
+        }
+      }
+      float lmax = kNegInf;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) lmax = fmaxf(lmax, x[e]);
+      if (__any(needs_rescale(rs[j], lmax))) rescale_rows(rs[j], lmax, G);
+      step_probs<TT, DW, false, false>(rs[j], x, scale_log2, 1.f, 1.f, phi[j], plo[j]);
     }
-    float lmax = kNegInf;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) lmax = fmaxf(lmax, x[e]);
-    if (__any(needs_rescale(rs, lmax))) rescale_rows(rs, lmax, G);
-    vec8 phi, plo;
-    step_probs<TT, DW, false, false>(rs, x, scale_log2, 1.f, 1.f, phi, plo);
+    for (int n = 0; n < DL; ++n) {
+      const vec8 vb = lat_value_operand<TT, DW>(st.v, n);
 #pragma unroll
-    for (int j = 0; j < DL; ++j) {
-      const vec8 vb = lat_value_operand<TT, DW>(st.v, j);
-      rs.o[j] = TT::mfma(phi, vb, rs.o[j]);
-      rs.o[j] = TT::mfma(plo, vb, rs.o[j]);
+      for (int j = 0; j < NG; ++j) {
+        rs[j].o[n] = TT::mfma(phi[j], vb, rs[j].o[n]);
+        rs[j].o[n] = TT::mfma(plo[j], vb, rs[j].o[n]);
+      }
     }
   };
 
@@ -235,62 +254,71 @@ latent_kernel(const AttnParams p) {
   else
     steps(std::false_type{});
 
-  // Rows 4 G + i of this lane's O registers: this wavefront's DW value dims of each row.
-  float l_row = rs.l_part + __shfl_xor(rs.l_part, 16, 64);
-  l_row += __shfl_xor(l_row, 32, 64);
+  // Rows 4 G + i of this lane's O registers in each group: this wavefront's DW value dims.
   const int VD = 4 * DW;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int rr = row0 + 4 * G + i;
-    const float mi = __shfl(rs.m_run, 4 * G + i, 64);
-    const float li = __shfl(l_row, 4 * G + i, 64);
-    if (rr >= R) continue;
-    const int oh = rr % H;
-    const int64_t t = s0 + rr / H;
-    if (single) {
-      const float f = finalize_factor(mi, li, sink_logit<TT>(p, oh));
-      typename TT::raw vals[DL];
+  for (int j = 0; j < NG; ++j) {
+    float l_row = rs[j].l_part + __shfl_xor(rs[j].l_part, 16, 64);
+    l_row += __shfl_xor(l_row, 32, 64);
 #pragma unroll
-      for (int j = 0; j < DL; ++j) vals[j] = TT::from_f32(rs.o[j][i] * f);
-      typename TT::raw* dst = reinterpret_cast<typename TT::raw*>(p.out) +
-                              (t * H + oh) * VD + DW * wave + DL * c;
-      if constexpr (DL == 8) {
-        u32x4 pk;
+    for (int i = 0; i < 4; ++i) {
+      const int rr = row0 + 16 * j + 4 * G + i;
+      const float mi = __shfl(rs[j].m_run, 4 * G + i, 64);
+      const float li = __shfl(l_row, 4 * G + i, 64);
+      if (rr >= R) continue;
+      const int oh = rr % H;
+      const int64_t t = s0 + rr / H;
+      if (single) {
+        const float f = finalize_factor(mi, li, sink_logit<TT>(p, oh));
+        typename TT::raw vals[DL];
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
-          pk[m] = (uint32_t)vals[2 * m] | ((uint32_t)vals[2 * m + 1] << 16);
-        *reinterpret_cast<u32x4*>(dst) = pk;
+        for (int n = 0; n < DL; ++n) vals[n] = TT::from_f32(rs[j].o[n][i] * f);
+        typename TT::raw* dst = reinterpret_cast<typename TT::raw*>(p.out) +
+                                (t * H + oh) * VD + DW * wave + DL * c;
+        if constexpr (DL == 8) {
+          u32x4 pk;
+#pragma unroll
+          for (int m = 0; m < 4; ++m)
+            pk[m] = (uint32_t)vals[2 * m] | ((uint32_t)vals[2 * m + 1] << 16);
+          *reinterpret_cast<u32x4*>(dst) = pk;
+        } else {
+#pragma unroll
+          for (int n = 0; n < DL; ++n) dst[n] = vals[n];
+        }
       } else {
+        const int64_t pi = (t * H + oh) * p.max_splits + split;
+        float* dst = p.part_o + pi * D + DW * wave + DL * c;
 #pragma unroll
-        for (int j = 0; j < DL; ++j) dst[j] = vals[j];
-      }
-    } else {
-      const int64_t pi = (t * H + oh) * p.max_splits + split;
-      float* dst = p.part_o + pi * D + DW * wave + DL * c;
-#pragma unroll
-      for (int j = 0; j < DL; ++j) dst[j] = rs.o[j][i];
-      if (wave == 0 && c == 0) {
-        p.part_ml[pi * 2 + 0] = mi;
-        p.part_ml[pi * 2 + 1] = li;
+        for (int n = 0; n < DL; ++n) dst[n] = rs[j].o[n][i];
+        if (wave == 0 && c == 0) {
+          p.part_ml[pi * 2 + 0] = mi;
+          p.part_ml[pi * 2 + 1] = li;
+        }
       }
     }
   }
 }
 
 template <typename TT, int DW>
-void launch_lat_dw(const AttnParams& p, dim3 grid, hipStream_t s) {
-  if (p.softcap > 0.0f)
-    hipLaunchKernelGGL((latent_kernel<TT, DW, true>), grid, dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL((latent_kernel<TT, DW, false>), grid, dim3(256), 0, s, p);
+void launch_lat_dw(const AttnParams& p, dim3 grid, int ng, hipStream_t s) {
+  if (ng == 2) {
+    if (p.softcap > 0.0f)
+      hipLaunchKernelGGL((latent_kernel<TT, DW, true, 2>), grid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((latent_kernel<TT, DW, false, 2>), grid, dim3(256), 0, s, p);
+  } else if (p.softcap > 0.0f) {
+    hipLaunchKernelGGL((latent_kernel<TT, DW, true, 1>), grid, dim3(256), 0, s, p);
+  } else {
+    hipLaunchKernelGGL((latent_kernel<TT, DW, false, 1>), grid, dim3(256), 0, s, p);
+  }
 }
 
 template <typename TT>
-void launch_lat_t(const AttnParams& p, dim3 grid, hipStream_t s) {
+void launch_lat_t(const AttnParams& p, dim3 grid, int ng, hipStream_t s) {
   switch (p.v_head_dim) {
-    case 128: launch_lat_dw<TT, 32>(p, grid, s); break;
-    case 256: launch_lat_dw<TT, 64>(p, grid, s); break;
-    default: launch_lat_dw<TT, 128>(p, grid, s); break;
+    case 128: launch_lat_dw<TT, 32>(p, grid, ng, s); break;
+    case 256: launch_lat_dw<TT, 64>(p, grid, ng, s); break;
+    default: launch_lat_dw<TT, 128>(p, grid, ng, s); break;
   }
 }
 
@@ -315,13 +343,14 @@ hipError_t launch_latent(const AttnParams& p, pa_dtype act, pa_dtype cache_dtype
       p.batch > 65535)
     return hipErrorInvalidValue;
   const int mq = p.max_query_len > 0 ? p.max_query_len : p.num_tokens;
-  const int64_t rbs = ((int64_t)p.num_heads * mq + 15) / 16;
+  const int ng = latent_row_groups(p.num_heads, mq);
+  const int64_t rbs = ((int64_t)p.num_heads * mq + 16 * ng - 1) / (16 * ng);
   if (rbs > INT32_MAX) return hipErrorInvalidValue;
   const dim3 grid((unsigned)rbs, p.max_splits, p.batch);
   if (act == PA_DTYPE_FLOAT16)
-    launch_lat_t<TF16>(p, grid, s);
+    launch_lat_t<TF16>(p, grid, ng, s);
   else
-    launch_lat_t<TBF16>(p, grid, s);
+    launch_lat_t<TBF16>(p, grid, ng, s);
   return hipGetLastError();
 }
 
