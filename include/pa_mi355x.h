@@ -200,7 +200,8 @@ size_t pa_attention_workspace_bytes_ex(const pa_cache* cache, const pa_batch* ba
  *     batch fills two workgroups per compute unit, over operand images when each (sequence,
  *     kv-head) has at least 4 row blocks);
  *   - other batches over fp8 / int8 / int4 pages: the planned prefill over operand images (fp16
- *     rows of the live context, within 2 GiB of workspace);
+ *     rows of the live context, within 2 GiB of workspace; larger batches run it on groups of
+ *     sequences whose images fit, one launch per group);
  *   - the LATENT layout (one kv-head, values = the first v_head_size key dims) with the cache in
  *     the activation dtype, key rows of a multiple of 32 dims up to 640 and values of 128, 256
  *     or 512 dims (MLA 576 / 512): its matrix-core kernel, all heads served by one read of each

@@ -141,7 +141,16 @@ struct Plan {
   // Planned head-128 prefill with operand images: 64-key steps per (sequence, kv-head) of the
   // image region (0: no images).
   int img_steps = 0;
+  // Byte-coded pages whose images of the whole batch exceed the image limit: the planned launch
+  // runs on groups of sub_batch sequences in turn, the workspace sized for one group (0: the
+  // whole batch in one launch).
+  int sub_batch = 0;
 };
+
+// Sequences one planned launch covers.
+int64_t plan_batch(const pa_batch* b, const Plan& pl) {
+  return pl.sub_batch > 0 ? std::min<int64_t>(pl.sub_batch, b->batch) : b->batch;
+}
 
 // Operand images of the planned prefill: taken when every key step of the images is read
 // by at least kImgMinRowBlocks row blocks (the images are written once and read by each), within
@@ -269,10 +278,17 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
         const int64_t live =
             b->max_context_len > 0 ? std::min<int64_t>(b->max_context_len, ctx) : (int64_t)ctx;
         const int64_t steps = (live + ik - 1) / ik;
-        if ((int64_t)b->batch * c->kv_heads * steps * pa::img_step_bytes(c->head_dim) <=
-                kImgMaxBytes &&
-            steps <= 65535 && b->batch <= 65535) {
+        const int64_t per_seq = (int64_t)c->kv_heads * steps * pa::img_step_bytes(c->head_dim);
+        if ((int64_t)b->batch * per_seq <= kImgMaxBytes && steps <= 65535 &&
+            b->batch <= 65535) {
           pl.img_steps = (int)steps;
+        } else if (intc && !linear && per_seq <= kImgMaxBytes && steps <= 65535) {
+          // byte-coded pages: groups of sequences whose images fit, one planned launch each
+          pl.sub_batch = (int)std::min<int64_t>(kImgMaxBytes / per_seq, 65535);
+          pl.img_steps = (int)steps;
+          const int64_t sub_units = (int64_t)pl.sub_batch * c->kv_heads * rbs;
+          pl.plan_items = sub_units;
+          pl.part_rows = (size_t)sub_units * 2 * pa::kPrefillRows;
         }
       }
       if (!(intc && pl.img_steps == 0)) return pl;
@@ -344,7 +360,7 @@ size_t plan_bytes(const Plan& pl) {
 }
 size_t image_bytes(const pa_cache* c, const pa_batch* b, const Plan& pl) {
   if (pl.img_steps == 0) return 0;
-  const size_t hb = (size_t)b->batch * c->kv_heads;
+  const size_t hb = (size_t)plan_batch(b, pl) * c->kv_heads;
   return align256(hb * pl.img_steps * pa::img_step_bytes(c->head_dim)) +
          align256(hb * pl.img_steps * sizeof(int32_t)) + align256(hb * sizeof(int32_t));
 }
@@ -468,7 +484,7 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
                                                       : 2) * device_cus();
     p.plan_step = pl.img_steps > 0 ? pa::img_keys(c->head_dim) : pa::prefill_key_step(c->head_dim);
     if (pl.img_steps > 0) {
-      const size_t hb = (size_t)b->batch * c->kv_heads;
+      const size_t hb = (size_t)plan_batch(b, pl) * c->kv_heads;
       char* img = base + plan_bytes(pl) - align256((size_t)pl.plan_items * 2 * 4 * sizeof(int32_t));
       p.vimg = img;
       img += align256(hb * pl.img_steps * pa::img_step_bytes(c->head_dim));
@@ -525,8 +541,27 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
   switch (pl.kind) {
     case 1: e = pa::launch_decode_mfma(p, act, c->dtype, s); break;
     case 2:
-      e = pl.plan_items > 0 ? pa::launch_prefill_planned(p, act, c->dtype, s)
-                            : pa::launch_prefill_mfma(p, act, c->dtype, s);
+      if (pl.sub_batch > 0) {
+        // groups of sequences in turn over the same workspace (cum holds absolute token
+        // offsets, so q / k / v / out stay as they are)
+        e = hipSuccess;
+        for (int64_t b0 = 0; b0 < b->batch && e == hipSuccess; b0 += pl.sub_batch) {
+          pa::AttnParams q = p;
+          const int nb = (int)std::min<int64_t>(pl.sub_batch, b->batch - b0);
+          q.cum = p.cum + b0;
+          q.past = p.past + b0;
+          q.block_table = p.block_table + b0 * p.max_blocks;
+          q.batch = nb;
+          q.plan_items = (int32_t)((int64_t)nb * c->kv_heads * pl.plan_rbs);
+          if (p.key_limit) q.key_limit = p.key_limit + b0;
+          // fresh wide-step flags: the image slots are reused by every group
+          if (b0 > 0) q.img_epoch = next_img_epoch();
+          e = pa::launch_prefill_planned(q, act, c->dtype, s);
+        }
+      } else {
+        e = pl.plan_items > 0 ? pa::launch_prefill_planned(p, act, c->dtype, s)
+                              : pa::launch_prefill_mfma(p, act, c->dtype, s);
+      }
       break;
     case 5: e = pa::launch_latent(p, act, c->dtype, s); break;
     default: e = pa::launch_attn_generic(p, act, c->dtype, s); break;

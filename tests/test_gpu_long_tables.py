@@ -7,6 +7,8 @@ kv-head), 32 KiB per step at head 128) are sized by the live context: the host m
 longest past + new tokens, or the caller's max_context_len.  Sized by the block-table capacity,
 16 sequences x 8 kv-heads x 1,024 steps would need 4 GiB -- beyond the 2 GiB image limit -- and
 these batches would fall to the VALU kernel; now they run the matrix-core prefill over images.
+Where the caller's bound itself makes the images too large, the planned prefill runs on groups
+of sequences whose images fit, one launch per group over the same image region.
 The block tables repeat valid pool blocks past each sequence's live pages (the reference's
 validation checks only the blocks a sequence needs, attention.rs:3975-3987).
 
@@ -21,7 +23,7 @@ import pytest
 
 import _oracle as orc
 from _oracle import BF16, E4M3, F16, I4, I8
-from pa_cases import make_case, run_gpu_op
+from pa_cases import QUANT_NAMES, from_torch, make_case, run_gpu_op, to_torch
 
 pytestmark = pytest.mark.gpu
 
@@ -90,3 +92,37 @@ def test_context_bound_below_a_sequence_leaves_its_rows():
           flush=True)
     out, kc, vc = run_gpu_op(case, validate=False, max_query_len=mq, max_context_len=mc)
     _check(case, out, kc, vc, skip=(b_long,))
+
+
+@pytest.mark.parametrize("cache_dtype,dtype", [(E4M3, BF16), (I8, BF16), (I4, F16)],
+                         ids=["fp8-bf16", "int8-bf16", "int4-fp16"])
+def test_oversized_images_run_in_sequence_groups(cache_dtype, dtype):
+    """The caller bounds the context by the whole block-table span (65,536 positions): images of
+    12 sequences x 8 kv-heads x 1,024 64-key steps (3 GiB) exceed the 2 GiB image limit, so the
+    planned prefill runs on groups of 8 and 4 sequences over one 2 GiB image region instead of
+    dropping to the VALU kernel.  The kernel-level call that admits only the planned prefill
+    (kind 2 over byte-coded pages) gives the operator's output bit for bit."""
+    import torch
+    import onnxruntime_ep_mlx_amd as ep
+    case = long_table_case(cache_dtype, dtype, B=12, seed=11)
+    assert "cos_cache" not in case
+    mq = int(np.diff(case["cum"]).max())
+    mc = SPAN_BLOCKS * 16
+    print(f"grouped-images case {orc.NAMES[cache_dtype]} act={orc.NAMES[dtype]} B=12 KV=8 "
+          f"bound={mc}", flush=True)
+    out, kc, vc = run_gpu_op(case, validate=False, max_query_len=mq, max_context_len=mc)
+    _check(case, out, kc, vc)
+    # the same attention through the kernel-level entry on the updated caches
+    cdt = case["cache_dtype"]
+    t = {n: to_torch(case[n], dtype) for n in ("query", "key", "value")}
+    I = {n: torch.from_numpy(np.ascontiguousarray(case[n], np.int32)).cuda()
+         for n in ("cum", "past", "block_table")}
+    again = ep.attention(t["query"], t["key"], t["value"], to_torch(kc, cdt), to_torch(vc, cdt),
+                         I["cum"], I["past"], I["block_table"], num_heads=case["num_heads"],
+                         k_scale=torch.from_numpy(case["k_scale"]).cuda(),
+                         v_scale=torch.from_numpy(case["v_scale"]).cuda(),
+                         k_quant_type=QUANT_NAMES[case.get("k_quant", 0)],
+                         v_quant_type=QUANT_NAMES[case.get("v_quant", 0)],
+                         max_query_len=mq, kind=2, new_rows_in_cache=True, max_context_len=mc)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out, from_torch(again, dtype))

@@ -4,9 +4,9 @@ The planned prefill writes operand images (fp16 key and value rows laid out as t
 operands, 32 KiB per 64-key step of every (sequence, kv-head) at head 128) into the workspace.
 They are sized by the live context of the call -- the host metadata's longest past + new tokens,
 the caller's max_context_len, or GroupQueryAttention's total_sequence_length -- not by the
-block-table or present capacity.  A capacity-sized region could exceed the 2 GiB image limit and
-send byte-coded pages (int8 / int4 / fp8) to the VALU kernel; these cases check that the image
-region is planned and has the live size.
+block-table or present capacity.  These cases check that the image region is planned and has the
+live size, and that a region beyond the 2 GiB image limit (byte-coded pages: int8 / int4 / fp8)
+is planned for groups of sequences that fit it rather than dropped.
 """
 from __future__ import annotations
 
@@ -86,10 +86,14 @@ def test_paged_images_follow_the_callers_context_bound():
     n = lib.pa_paged_attention_workspace_bytes(C.byref(node), C.byref(io))
     live = 16 * 8 * 17 * STEP_BYTES
     assert live <= n < live + (256 << 20), n
-    # without a bound the images cover the block-table capacity: beyond the limit, no images
+    # without a bound the images cover the block-table capacity (65,536 positions: 1,024 steps,
+    # 256 MiB per sequence), 4 GiB for the batch: the planned launch runs on groups of 8
+    # sequences, the workspace holding the images of one group (2 GiB) and its plan
     node0, io0, keep0 = _paged(past, 64, 4096, host=False, bound=0)
     n0 = lib.pa_paged_attention_workspace_bytes(C.byref(node0), C.byref(io0))
-    assert n0 < live, n0
+    group = 8 * 8 * 1024 * STEP_BYTES
+    assert group == 1 << 31
+    assert group <= n0 < group + (64 << 20), n0
 
 
 def test_context_bound_below_the_host_metadata_is_refused():
