@@ -486,32 +486,46 @@ __device__ __forceinline__ int64_t total_steps(const AttnParams& p, int lane) {
 __device__ __forceinline__ int64_t seg_len(int64_t S, int nseg) { return (S + nseg - 1) / nseg; }
 
 // Merge the nparts partials of (sequence b, kv-head kh), stored at slots f+b .. f+nparts-1+b,
-// into the final rows.  Lane l handles row l/4 and a quarter of the head dims.  Pieces are taken
-// four at a time with every load of a batch issued before any is used (indices clamped into
-// range, surplus pieces weighted zero), so a merge costs one memory round trip per batch.
+// into the final rows.  Thread t (of 256) handles row t / 16 and DS = D / 16 consecutive head
+// dims.  Up to KB pieces are loaded together (every load issued before any is used; indices
+// clamped into range, surplus pieces weighted zero), so a sequence of up to KB partials -- at
+// the config 3 batch every one -- costs one memory round trip.
 template <typename TT, int D>
 __device__ __forceinline__ void merge_pieces(const AttnParams& p, int b, int kh, int s0, int R,
-                                             int g, int f, int nparts, int lane) {
-  constexpr int DQ = D / 4;   // dims per lane
-  constexpr int NV = DQ / 4;  // float4 loads per lane and piece
-  constexpr int KB = D > 128 ? 2 : 4;  // pieces per batch (register budget)
-  const int r = lane >> 2, quarter = lane & 3;
+                                             int g, int f, int nparts, int tid) {
+  constexpr int DS = D / 16;           // dims per thread
+  constexpr int KB = D > 128 ? 6 : 96 / DS;  // pieces per batch (~96 registers of partials)
+  static_assert(DS % 2 == 0, "pairs of dims");
+  const int r = tid >> 4, slice = tid & 15;
   if (r >= R) return;
   float M = kNegInf, lsum = 0.0f;
-  f32x4 acc[NV];
+  float acc[DS];
 #pragma unroll
-  for (int v = 0; v < NV; ++v) acc[v] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int e = 0; e < DS; ++e) acc[e] = 0.0f;
   for (int k0 = 0; k0 < nparts; k0 += KB) {
     float2 ml[KB];
-    f32x4 o[KB][NV];
+    float o[KB][DS];
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
       const int k = min(k0 + j, nparts - 1);
       const int64_t row = (((int64_t)f + k + b) * p.kv_heads + kh) * 16 + r;
       ml[j] = *reinterpret_cast<const float2*>(p.part_ml + row * 2);
-      const f32x4* src = reinterpret_cast<const f32x4*>(p.part_o + row * D + quarter * DQ);
+      const float* src = p.part_o + row * D + slice * DS;
+      if constexpr (DS % 4 == 0) {
 #pragma unroll
-      for (int v = 0; v < NV; ++v) o[j][v] = src[v];
+        for (int v = 0; v < DS / 4; ++v) {
+          const f32x4 x = reinterpret_cast<const f32x4*>(src)[v];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[j][4 * v + e] = x[e];
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < DS / 2; ++v) {
+          const float2 x = reinterpret_cast<const float2*>(src)[v];
+          o[j][2 * v] = x.x;
+          o[j][2 * v + 1] = x.y;
+        }
+      }
     }
     float mn = M;
 #pragma unroll
@@ -521,13 +535,13 @@ __device__ __forceinline__ void merge_pieces(const AttnParams& p, int b, int kh,
     const float a = (M == kNegInf) ? 0.0f : exp2f(M - mn);
     lsum *= a;
 #pragma unroll
-    for (int v = 0; v < NV; ++v) acc[v] *= a;
+    for (int e = 0; e < DS; ++e) acc[e] *= a;
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
       const float w = (k0 + j < nparts && ml[j].x != kNegInf) ? exp2f(ml[j].x - mn) : 0.0f;
       lsum += ml[j].y * w;
 #pragma unroll
-      for (int v = 0; v < NV; ++v) acc[v] += o[j][v] * w;
+      for (int e = 0; e < DS; ++e) acc[e] += o[j][e] * w;
     }
     M = mn;
   }
@@ -538,23 +552,25 @@ __device__ __forceinline__ void merge_pieces(const AttnParams& p, int b, int kh,
     // integer pages: the partials are in code units; scale each output dim
     const bool pc = p.v_quant == PA_QUANT_PER_CHANNEL;
 #pragma unroll
-    for (int v = 0; v < NV; ++v)
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        acc[v][e] *= pc ? p.v_scale[(int64_t)kh * D + quarter * DQ + 4 * v + e] : p.v_scale[0];
+    for (int e = 0; e < DS; ++e)
+      acc[e] *= pc ? p.v_scale[(int64_t)kh * D + slice * DS + e] : p.v_scale[0];
   }
-  u32x4* out = reinterpret_cast<u32x4*>(reinterpret_cast<typename TT::raw*>(p.out) +
-                                        (t * p.num_heads + h) * D + quarter * DQ);
+  uint32_t w[DS / 2];
 #pragma unroll
-  for (int v = 0; v < NV; v += 2) {
-    u32x4 w;
+  for (int m = 0; m < DS / 2; ++m)
+    w[m] = (uint32_t)TT::from_f32(acc[2 * m] * fct) |
+           ((uint32_t)TT::from_f32(acc[2 * m + 1] * fct) << 16);
+  uint32_t* out = reinterpret_cast<uint32_t*>(reinterpret_cast<typename TT::raw*>(p.out) +
+                                              (t * p.num_heads + h) * D + slice * DS);
+  if constexpr (DS % 8 == 0) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const f32x4 x = acc[v + e / 2];
-      const float lo = x[(e & 1) * 2] * fct, hi = x[(e & 1) * 2 + 1] * fct;
-      w[e] = (uint32_t)TT::from_f32(lo) | ((uint32_t)TT::from_f32(hi) << 16);
-    }
-    out[v / 2] = w;
+    for (int v = 0; v < DS / 8; ++v)
+      reinterpret_cast<u32x4*>(out)[v] = u32x4{w[4 * v], w[4 * v + 1], w[4 * v + 2], w[4 * v + 3]};
+  } else if constexpr (DS == 4) {
+    *reinterpret_cast<u32x2*>(out) = u32x2{w[0], w[1]};
+  } else {
+#pragma unroll
+    for (int m = 0; m < DS / 2; ++m) out[m] = w[m];
   }
 }
 
@@ -1219,10 +1235,9 @@ decode_balanced_kernel(const AttnParams p) {
 // A device-scope fence per piece inside the decode kernel (to let the last piece merge) writes
 // back the XCD's L2 and measured far slower than this separate launch.
 template <typename TT, int D>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void
-balanced_merge_kernel(const AttnParams p) {
+__global__ __launch_bounds__(256) void balanced_merge_kernel(const AttnParams p) {
   const int kh = blockIdx.x, b = blockIdx.y;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
   const int nseg = p.max_splits;
   const int g = p.num_heads / p.kv_heads;
   // Prefix of steps up to b, b's own metadata and the total, one parallel pass over sequences.
@@ -1245,7 +1260,7 @@ balanced_merge_kernel(const AttnParams p) {
   const int f = (int)(Pb / seg_l);
   const int nparts = (int)((Pb + nb - 1) / seg_l) - f + 1;
   if (nparts <= 1) return;  // written directly by the decode kernel
-  merge_pieces<TT, D>(p, b, kh, s0, g * nq, g, f, nparts, lane);
+  merge_pieces<TT, D>(p, b, kh, s0, g * nq, g, f, nparts, (int)threadIdx.x);
 }
 
 template <typename TT, int D, bool CAP>
@@ -1353,7 +1368,7 @@ hipError_t launch_decode_mfma(const AttnParams& p, pa_dtype act, pa_dtype cache_
 // The partial merge of the balanced decode, for the head size of the decode launch.
 template <typename TT>
 hipError_t launch_merge(const AttnParams& p, hipStream_t s) {
-  const dim3 grid(p.kv_heads, p.batch), block(64);
+  const dim3 grid(p.kv_heads, p.batch), block(256);
   switch (p.head_dim) {
     case 64: hipLaunchKernelGGL((balanced_merge_kernel<TT, 64>), grid, block, 0, s, p); break;
     case 96: hipLaunchKernelGGL((balanced_merge_kernel<TT, 96>), grid, block, 0, s, p); break;
