@@ -188,9 +188,11 @@ int device_cus() {
 }
 
 // images: the planned head-128 prefill may use operand images (off where the workspace is
-// bounded, pa_paged_attention_static).
+// bounded, pa_paged_attention_static).  bias: GroupQueryAttention's attention bias is present
+// (its streaming decode runs one wavefront per SIMD at every cache dtype).
 Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype act, int kind,
-               int chunk, bool linear = false, int linear_cap = 0, bool images = true) {
+               int chunk, bool linear = false, int linear_cap = 0, bool images = true,
+               bool bias = false) {
   Plan pl{};
   // The LATENT layout (values = leading dims of the key rows): its matrix-core kernel (kind 5)
   // where it covers the head sizes and dtypes, else the VALU kernel.
@@ -245,10 +247,11 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
   const int ctx = std::max(
       linear_cap > 0 ? std::min(linear_cap, INT32_MAX / 2) : max_ctx_bound(c, b), 1);
   if (pl.balanced) {
-    // One wavefront per SIMD on every CU, each walking kDecodeMix sub-segments.
+    // decode_waves wavefronts per SIMD on every CU, each walking kDecodeMix sub-segments.
     pl.chunk = 32;
     pl.mix = std::min(kDecodeMix, c->kv_heads);
-    pl.max_splits = pl.mix * std::max(1, 4 * device_cus() / c->kv_heads);
+    const int waves = bias ? 1 : pa::decode_waves(c->dtype);
+    pl.max_splits = pl.mix * std::max(1, 4 * waves * device_cus() / c->kv_heads);
     pl.part_rows = (size_t)(pl.max_splits + b->batch) * c->kv_heads * 16;
     return pl;
   }
@@ -438,7 +441,7 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
   if (!(a->softcap >= 0.0f) || !std::isfinite(a->softcap))
     return fail(PA_ERR_INVALID_ARGUMENT, "softcap must be finite and non-negative");
   Plan pl = make_plan(c, b, a, act, kind, chunk, opts.linear_cap > 0, opts.linear_cap,
-                      plan_images(opts));
+                      plan_images(opts), opts.bias != nullptr);
   if (kind == 2 && pl.kind != 2 && pa::prefill_coded_supported(c->head_dim, act, c->dtype))
     return fail(PA_ERR_UNSUPPORTED,
                 "prefill MFMA kernel: byte-coded pages run on it over operand images only (planned "
@@ -1158,7 +1161,7 @@ size_t attention_ws(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_d
                     const RunOpts& o) {
   return workspace_for(c, b, a,
                        make_plan(c, b, a, act, 0, 0, o.linear_cap > 0, o.linear_cap,
-                                 plan_images(o)));
+                                 plan_images(o), o.bias != nullptr));
 }
 
 struct GqaLayout {

@@ -398,6 +398,22 @@ static_assert(kImgKeys == 32 || kImgKeys == 64, "image steps of one or two 32-ke
 // fit the register budget of two wavefronts per SIMD), and the bytes of one step's image.
 __host__ __device__ constexpr int img_keys(int d) { return d > 128 ? 32 : kImgKeys; }
 __host__ __device__ constexpr int img_step_bytes(int d) { return 2 * img_keys(d) * d * 2; }
+// Wavefronts per SIMD of the streaming decode over caches of this dtype (the grid holds that many
+// segments per SIMD).  int4 codes: two -- their decode is bound by instruction issue (the code
+// widening), and a second wavefront fills the first one's memory waits; its kernel fits 256
+// VGPRs without spilling (the bias variant keeps one wavefront per SIMD and runs the grid in two
+// rounds).  int8 at two spills ~34 VGPRs and stays at one.
+#ifndef PA_DECODE_WAVES_I4
+#define PA_DECODE_WAVES_I4 2
+#endif
+#ifndef PA_DECODE_WAVES_I8
+#define PA_DECODE_WAVES_I8 1
+#endif
+__host__ __device__ constexpr int decode_waves(int cache_dtype) {
+  return cache_dtype == PA_DTYPE_INT4 ? PA_DECODE_WAVES_I4
+         : cache_dtype == PA_DTYPE_INT8 ? PA_DECODE_WAVES_I8
+                                        : 1;
+}
 // Heads the planned prefill runs over operand images.
 __host__ __device__ constexpr bool img_head(int d) {
   return d == 64 || d == 96 || d == 128 || d == 256;
