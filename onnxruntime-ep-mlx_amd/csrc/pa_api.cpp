@@ -250,7 +250,7 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
     // decode_waves wavefronts per SIMD on every CU, each walking kDecodeMix sub-segments.
     pl.chunk = 32;
     pl.mix = std::min(kDecodeMix, c->kv_heads);
-    const int waves = bias ? 1 : pa::decode_waves(c->dtype);
+    const int waves = bias ? 1 : pa::decode_waves(c->dtype, c->head_dim);
     pl.max_splits = pl.mix * std::max(1, 4 * waves * device_cus() / c->kv_heads);
     pl.part_rows = (size_t)(pl.max_splits + b->batch) * c->kv_heads * 16;
     return pl;

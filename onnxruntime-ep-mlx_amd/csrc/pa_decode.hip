@@ -736,6 +736,13 @@ __device__ __forceinline__ uint64_t tile_row_bytes(const AttnParams& p, const Cu
 // kDcLin marks integer codes in a contiguous cache and kDcBias an additive attention bias
 // (GroupQueryAttention presents and attention_bias).
 enum DecodeCache { kDcT = 0, kDcFp8 = 1, kDcI8 = 2, kDcI4 = 3, kDcLin = 4, kDcBias = 8 };
+// The cache dtype of a decode form (kDcT: -1, caches in the activation dtype).
+constexpr int decode_cache_dtype(int ck) {
+  return (ck & 3) == kDcI4 ? PA_DTYPE_INT4
+         : (ck & 3) == kDcI8 ? PA_DTYPE_INT8
+         : (ck & 3) == kDcFp8 ? PA_DTYPE_FP8_E4M3
+                              : -1;
+}
 
 template <typename TT, int D, int CK>
 using RingStep = typename std::conditional<
@@ -1191,8 +1198,8 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
 #endif
 template <typename TT, int D, bool CAP, int CK>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
-    (CK & kDcBias) ? 1 : decode_waves((CK & 3) == kDcI4 ? PA_DTYPE_INT4 : (CK & 3) == kDcI8 ? PA_DTYPE_INT8 : 0),
-    (CK & kDcBias) ? 1 : decode_waves((CK & 3) == kDcI4 ? PA_DTYPE_INT4 : (CK & 3) == kDcI8 ? PA_DTYPE_INT8 : 0)))) void
+    (CK & kDcBias) ? 1 : decode_waves(decode_cache_dtype(CK), D),
+    (CK & kDcBias) ? 1 : decode_waves(decode_cache_dtype(CK), D)))) void
 decode_balanced_kernel(const AttnParams p) {
   // Workgroup = W wavefronts (one per SIMD of a CU) for W consecutive kv-heads of one segment:
   // the kv-head slices of each page row are then fetched through one CU together, which the

@@ -409,10 +409,23 @@ __host__ __device__ constexpr int img_step_bytes(int d) { return 2 * img_keys(d)
 #ifndef PA_DECODE_WAVES_I8
 #define PA_DECODE_WAVES_I8 1
 #endif
-__host__ __device__ constexpr int decode_waves(int cache_dtype) {
-  return cache_dtype == PA_DTYPE_INT4 ? PA_DECODE_WAVES_I4
-         : cache_dtype == PA_DTYPE_INT8 ? PA_DECODE_WAVES_I8
-                                        : 1;
+// Pages in the activation dtype: two at head 64 (201 VGPRs; its 8 KiB steps keep few bytes in
+// flight per wavefront: C3-shaped batch 113.5 -> 100.8 us per launch), one at head 96 (two: 163.5
+// -> 170.0 us) and at heads 128 / 256 (bound by what the memory system delivers; above 256
+// VGPRs).
+#ifndef PA_DECODE_WAVES_D96
+#define PA_DECODE_WAVES_D96 1
+#endif
+#ifndef PA_DECODE_WAVES_D64
+#define PA_DECODE_WAVES_D64 2
+#endif
+__host__ __device__ constexpr int decode_waves(int cache_dtype, int head_dim) {
+  return cache_dtype == PA_DTYPE_INT4        ? PA_DECODE_WAVES_I4
+         : cache_dtype == PA_DTYPE_INT8      ? PA_DECODE_WAVES_I8
+         : cache_dtype == PA_DTYPE_FP8_E4M3  ? 1
+         : head_dim == 96                    ? PA_DECODE_WAVES_D96
+         : head_dim == 64                    ? PA_DECODE_WAVES_D64
+                                             : 1;
 }
 // Heads the planned prefill runs over operand images.
 __host__ __device__ constexpr bool img_head(int d) {
