@@ -413,6 +413,10 @@ __host__ __device__ constexpr int img_step_bytes(int d) { return 2 * img_keys(d)
 // flight per wavefront: C3-shaped batch 113.5 -> 100.8 us per launch), one at head 96 (two: 163.5
 // -> 170.0 us) and at heads 128 / 256 (bound by what the memory system delivers; above 256
 // VGPRs).
+// fp8 pages: one (two at ring depth 2, 229 VGPRs: C5 launch 185.6 -> 201.4 us).
+#ifndef PA_DECODE_WAVES_F8
+#define PA_DECODE_WAVES_F8 1
+#endif
 #ifndef PA_DECODE_WAVES_D96
 #define PA_DECODE_WAVES_D96 1
 #endif
@@ -422,7 +426,7 @@ __host__ __device__ constexpr int img_step_bytes(int d) { return 2 * img_keys(d)
 __host__ __device__ constexpr int decode_waves(int cache_dtype, int head_dim) {
   return cache_dtype == PA_DTYPE_INT4        ? PA_DECODE_WAVES_I4
          : cache_dtype == PA_DTYPE_INT8      ? PA_DECODE_WAVES_I8
-         : cache_dtype == PA_DTYPE_FP8_E4M3  ? 1
+         : cache_dtype == PA_DTYPE_FP8_E4M3  ? PA_DECODE_WAVES_F8
          : head_dim == 96                    ? PA_DECODE_WAVES_D96
          : head_dim == 64                    ? PA_DECODE_WAVES_D64
                                              : 1;
