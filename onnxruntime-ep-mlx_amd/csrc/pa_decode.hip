@@ -169,18 +169,20 @@ __device__ __forceinline__ f16x8 value_operand_i8(const Step8<D>& r, int j) {
   return __builtin_bit_cast(f16x8, o);
 }
 
-// int4 pages: rows of D/2 bytes, byte i = dims 2i (low nibble) and 2i + 1 (high nibble).  Key
-// chunk h of a lane: dims 64h + 16G .. +15 in 8 bytes; value row e: the lane's D/16 dims in
-// D/32 bytes (D = 64: two bytes in the low half of the word).
+// int4 pages: rows of D/2 bytes, byte i = dims 2i (low nibble) and 2i + 1 (high nibble).  Keys:
+// lane group G holds the D/4 dims (D/4) G .. of its row in one D/8-byte piece (16 lanes x 4
+// groups read whole row slices), word s of it = the 8 dims (D/4) G + 8 s .. of k-step s (the
+// query operands take the same dims); value row e: the lane's D/16 dims in D/32 bytes (D = 64:
+// two bytes in the low half of the word).
 template <int D>
 struct Step4 {
-  u32x2 k[2][D / 64];
+  uint32_t k[2][D / 32];
   uint32_t v[8];
 };
 
 template <int D>
 __device__ __forceinline__ f16x8 key_operand_i4(const Step4<D>& r, int tile, int s) {
-  const uint32_t x = r.k[tile][s >> 1][s & 1];
+  const uint32_t x = r.k[tile][s];
   const uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
   u32x4 o;  // code + 1032
 #pragma unroll
@@ -215,9 +217,10 @@ __device__ __forceinline__ f16x8 value_operand_i4(const Step4<D>& r, int j) {
 // query dims they meet (q_d * s_d, fp32); the row is then scaled by 2^(14 - e), e the exponent
 // of its largest |value| (so the row fits fp16 and keeps 11 bits), and the returned factor
 // 2^(e - 14) -- times a per-tensor key scale -- restores the scores.  Lanes c, c + 16, c + 32,
-// c + 48 hold row c; the lane's dims of k-step q are 64 (q / 2) + 16 G + 8 (q % 2) .. + 7.
+// c + 48 hold row c; the lane's dims of k-step q are 64 (q / 2) + 16 G + 8 (q % 2) .. + 7 (int8),
+// (D / 4) G + 8 q .. + 7 (int4).
 // koff: bias x the sum of the row's fp16 query operands (the key operands hold code + bias).
-template <typename TT, int D>
+template <typename TT, int D, bool I4>
 __device__ __forceinline__ float int_query(RowState<TF16, D>& rs, const u32x4 (&qr)[D / 32],
                                            const AttnParams& p, int kh, int G, float bias,
                                            float& koff) {
@@ -228,7 +231,8 @@ __device__ __forceinline__ float int_query(RowState<TF16, D>& rs, const u32x4 (&
   for (int q = 0; q < D / 32; ++q) {
     float sc[8];
     if (pc) {
-      const float* sp = p.k_scale + (int64_t)kh * D + 64 * (q >> 1) + 16 * G + 8 * (q & 1);
+      const float* sp = p.k_scale + (int64_t)kh * D + (I4 ? (D / 4) * G + 8 * q
+                                                           : 64 * (q >> 1) + 16 * G + 8 * (q & 1));
       const f32x4 a = *reinterpret_cast<const f32x4*>(sp);
       const f32x4 b = *reinterpret_cast<const f32x4*>(sp + 4);
 #pragma unroll
@@ -758,14 +762,16 @@ struct LaneOffs {
 // Per-lane pointers of the query row and sink logit the data cursor's (sequence, kv-head)
 // needs; recomputed only when that cursor changes sequence or kv-head.  MFMA column c is row
 // r = c (rows past R repeat the last one; their scores never reach an output).  Query k-step q
-// covers dims 32q + 8G .. (bf16 pages) or 64(q/2) + 16G + 8(q%2) .. (fp8 pages, matching the
-// key chunks); the lane part of that offset is folded in here, the q part is a constant.
+// covers dims 32q + 8G .. (bf16 pages), 64(q/2) + 16G + 8(q%2) .. (fp8 / int8 pages, matching
+// the key chunks) or (D/4)G + 8q .. (int4 pages); the lane part of that offset is folded in
+// here, the q part is a constant.
 struct QueryPtrs {
   const char* q;
   const char* sink;
   BiasRow br;  // BIAS: the bias row of row r
 };
-template <int D, bool F8, bool BIAS = false>  // F8: the query layout of byte-coded pages
+// QL: the query layout (0 pages in T, 1 fp8 / int8 pages, 2 int4 pages)
+template <int D, int QL, bool BIAS = false>
 __device__ __forceinline__ QueryPtrs query_ptrs(const AttnParams& p, const SeqWin& sw,
                                                 const Cursor& c, int g, int lane) {
   const int cl = lane & 15, G = lane >> 4;
@@ -774,7 +780,8 @@ __device__ __forceinline__ QueryPtrs query_ptrs(const AttnParams& p, const SeqWi
   const int rq = r / g, rh = r - rq * g;
   QueryPtrs o;
   o.q = reinterpret_cast<const char*>(p.q) +
-        ((int64_t)(s0 + rq) * p.num_heads + c.kh * g + rh) * D * 2 + (F8 ? 32 : 16) * G;
+        ((int64_t)(s0 + rq) * p.num_heads + c.kh * g + rh) * D * 2 +
+        (QL == 1 ? 32 : QL == 2 ? D / 2 : 16) * G;
   // Sink logit input of that row's head (a harmless read of the query when there is none).
   o.sink = p.head_sink ? reinterpret_cast<const char*>(p.head_sink) + (c.kh * g + rh) * 2
                        : reinterpret_cast<const char*>(p.q);
@@ -823,8 +830,15 @@ __device__ __forceinline__ void load_step4(const AttnParams& p, const Cursor& c,
     int64_t blk;
     const uint64_t off = tile_row_bytes(p, c, btl, tile, bs_shift, lo.rowb, blk) + hoff;
     const __amdgpu_buffer_rsrc_t rk = rows_rsrc(kc + off), rv = rows_rsrc(vc + off);
+    if constexpr (D == 128) {
+      const u32x4 x = bld16(rk, lo.koff, 0);
 #pragma unroll
-    for (int h = 0; h < D / 64; ++h) st.k[tile][h] = bld8(rk, lo.koff + 32 * h, 0);
+      for (int m = 0; m < 4; ++m) st.k[tile][m] = x[m];
+    } else {
+      const u32x2 x = bld8(rk, lo.koff, 0);
+      st.k[tile][0] = x[0];
+      st.k[tile][1] = x[1];
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       if constexpr (D == 128)
@@ -853,12 +867,19 @@ __device__ __forceinline__ void load_step_linear(const AttnParams& p, const SeqW
   for (int tile = 0; tile < 2; ++tile) {
     const int tp = c.t + 16 * tile;
     const char* kr = kc + (int64_t)min(tp + cl, last) * RB;
+    if constexpr (CK == kDcI4) {
+      if constexpr (D == 128) {
+        const u32x4 x = ld16s(kr + 16 * G);
 #pragma unroll
-    for (int h = 0; h < D / 64; ++h) {
-      if constexpr (CK == kDcI4)
-        st.k[tile][h] = ld8s(kr + 8 * G + 32 * h);
-      else
-        st.k[tile][h] = ld16s(kr + 16 * G + 64 * h);
+        for (int m = 0; m < 4; ++m) st.k[tile][m] = x[m];
+      } else {
+        const u32x2 x = ld8s(kr + 8 * G);
+        st.k[tile][0] = x[0];
+        st.k[tile][1] = x[1];
+      }
+    } else {
+#pragma unroll
+      for (int h = 0; h < D / 64; ++h) st.k[tile][h] = ld16s(kr + 16 * G + 64 * h);
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -889,7 +910,7 @@ __device__ __forceinline__ void load_stream_step(const AttnParams& p, const SeqW
                                                  const LaneOffs& lo, const QueryPtrs& qp,
                                                  bool qload, RingStep<TT, D, CK>& st,
                                                  u32x4 (&qv)[D / 32], typename TT::raw& sk) {
-  constexpr bool F8 = (CK & 3) != kDcT;  // byte-coded pages: the fp8 query layout
+  constexpr int QL = (CK & 3) == kDcT ? 0 : (CK & 3) == kDcI4 ? 2 : 1;  // query layout
   const int cl = lane & 15, G = lane >> 4;
   if constexpr ((CK & kDcLin) != 0) {
     load_step_linear<D, CK & 3>(p, sw, c, lane, st);
@@ -958,7 +979,7 @@ __device__ __forceinline__ void load_stream_step(const AttnParams& p, const SeqW
   if (qload) {
 #pragma unroll
     for (int q = 0; q < D / 32; ++q)
-      qv[q] = ld16(qp.q + (F8 ? 128 * (q >> 1) + 16 * (q & 1) : 64 * q));
+      qv[q] = ld16(qp.q + (QL == 1 ? 128 * (q >> 1) + 16 * (q & 1) : QL == 2 ? 16 * q : 64 * q));
     sk = *reinterpret_cast<const typename TT::raw*>(qp.sink);
   }
 }
@@ -973,7 +994,8 @@ __device__ __forceinline__ void load_stream_step(const AttnParams& p, const SeqW
 template <typename TT, int D, bool CAP, int CK, int DEPTH>
 __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& sw, int lo, int hi,
                                              int L, int x, int u0, int lane) {
-  constexpr bool F8 = (CK & 3) != kDcT;  // byte-coded pages (fp8 query layout)
+  constexpr bool F8 = (CK & 3) != kDcT;  // byte-coded pages
+  constexpr int QL = (CK & 3) == kDcT ? 0 : (CK & 3) == kDcI4 ? 2 : 1;  // query layout
   constexpr bool BIAS = (CK & kDcBias) != 0;  // additive bias (GroupQueryAttention)
   constexpr bool INT = (CK & 3) >= kDcI8;  // integer codes: fp16 products
   constexpr int CB = CK & 3;               // the code kind (kDcLin: contiguous addressing)
@@ -987,7 +1009,7 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
   constexpr int RB = CB == kDcT ? 2 * D : CB == kDcI4 ? D / 2 : D;
   LaneOffs lofs;
   lofs.rowb = (uint32_t)p.kv_heads * RB;
-  lofs.koff = (uint32_t)c * lofs.rowb + (CB == kDcI4 ? 8 : 16) * G;
+  lofs.koff = (uint32_t)c * lofs.rowb + (CB == kDcI4 ? D / 8 : 16) * G;
   lofs.voff = (uint32_t)(4 * G) * lofs.rowb + (uint32_t)(RB / 16) * c;
 
   // Block ids run BA steps ahead of the compute in a ring of NBT entries: 2 * (DEPTH - 1) ahead
@@ -999,7 +1021,7 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
   constexpr int U = DEPTH > 1 ? DEPTH : 2;
   Cursor cc = cursor_at(sw, p, lo, L, x, u0);
   Cursor cd = cc, cb = cc;
-  QueryPtrs qp = query_ptrs<D, F8, BIAS>(p, sw, cd, g, lane);
+  QueryPtrs qp = query_ptrs<D, QL, BIAS>(p, sw, cd, g, lane);
   RingStep<TT, D, CK> st[DEPTH];
   u32x4 qr[DEPTH][D / 32];
   typename TT::raw skr[DEPTH];
@@ -1018,7 +1040,7 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
                                 qr[j], skr[j]);
     if constexpr (BIAS) bias_load(qp.br, cd.t, G, braw[j]);
     qload = cursor_next(cd, sw, p, hi, L, x, u0);
-    if (qload) qp = query_ptrs<D, F8, BIAS>(p, sw, cd, g, lane);
+    if (qload) qp = query_ptrs<D, QL, BIAS>(p, sw, cd, g, lane);
   }
 #pragma unroll
   for (int j = DEPTH - 1; j < BA; ++j) {
@@ -1063,7 +1085,7 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
                                   st[sd_slot], qr[sd_slot], skr[sd_slot]);
       if constexpr (BIAS) bias_load(qp.br, cd.t, G, braw[BIAS ? sd_slot : 0]);
       qload = cursor_next(cd, sw, p, hi, L, x, u0);
-      if (qload) qp = query_ptrs<D, F8, BIAS>(p, sw, cd, g, lane);
+      if (qload) qp = query_ptrs<D, QL, BIAS>(p, sw, cd, g, lane);
       btr[bt_load] = load_step_blocks(p, sw, cb, lane, bs_shift);
       cursor_next(cb, sw, p, hi, L, x, u0);
       if (k + i < K) {
@@ -1085,7 +1107,7 @@ __device__ __forceinline__ void stream_range(const AttnParams& p, const SeqWin& 
           full_lo = p.window > 0 ? pastb + nq - p.window : 0;
           full_hi = p.causal ? min(pastb + 1, pc_total) : pc_total;
           if constexpr (INT)
-            row_f = int_query<TT, D>(rs, qr[cs], p, pc_kh, G, CB == kDcI8 ? 1152.f : 1032.f,
+            row_f = int_query<TT, D, CB == kDcI4>(rs, qr[cs], p, pc_kh, G, CB == kDcI8 ? 1152.f : 1032.f,
                                      koff);
           else
 #pragma unroll
