@@ -818,7 +818,8 @@ __device__ __forceinline__ void load_step8(const AttnParams& p, const Cursor& c,
   }
 }
 
-// int4 pages: per tile D/64 8-byte key chunks and four D/32-byte value row slices per lane.
+// int4 pages: per tile one D/8-byte key piece (the lane group's D/4 dims) and four D/32-byte
+// value row slices per lane.
 template <int D>
 __device__ __forceinline__ void load_step4(const AttnParams& p, const Cursor& c, int btl, int lane,
                                            int bs_shift, const LaneOffs& lo, Step4<D>& st) {
