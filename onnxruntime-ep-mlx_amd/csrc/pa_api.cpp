@@ -187,12 +187,57 @@ int device_cus() {
   return n;
 }
 
+// Per-sequence query and past lengths from host metadata (pa_paged_attention's host_* inputs),
+// when the caller gave them: they size the LATENT kernel's context chunks.
+struct HostLens {
+  const int32_t* cum = nullptr;
+  const int32_t* past = nullptr;
+};
+
+#ifndef PA_LATENT_PLAN
+#define PA_LATENT_PLAN 1
+#endif
+constexpr int kLatPlanMaxBatch = 4096;  // batches beyond this keep the capacity rule (host cost)
+
+// LATENT kernel: the context chunk (a multiple of 32 keys in [256, cap]) that minimises the
+// estimated launch time for the host's per-sequence key counts, in units of one 32-key step of a
+// workgroup: the work of all workgroups spread over `slots` resident ones, plus half a
+// workgroup's length for the last dispatch round, plus the partial rows of split sequences (fp32
+// O, m, l written by the kernel and read by the merge) priced as key bytes.  0 when no chunk is
+// better than a whole context (never: a split of the longest sequence always balances better).
+int latent_chunk(const pa_cache* c, const pa_batch* b, const pa_attn* a, const HostLens& hl,
+                 int ng, int64_t slots, int cap) {
+  const int D = c->head_dim;
+  const int64_t H = a->num_heads;
+  double best = 0.0;
+  int pick = 0;
+  for (int ch = 256; ch <= cap; ch += 32) {
+    int64_t work = 0, part_rows = 0;
+    for (int i = 0; i < b->batch; ++i) {
+      const int64_t nq = (int64_t)hl.cum[i + 1] - hl.cum[i];
+      if (nq <= 0) continue;
+      const int64_t tot = std::max<int64_t>((int64_t)std::max(hl.past[i], 0) + nq, 1);
+      const int64_t rbs = (H * nq + 16 * ng - 1) / (16 * ng);
+      const int64_t n = (tot + ch - 1) / ch;
+      work += rbs * ((tot + 31) / 32 + n);  // steps + one step of set-up per workgroup
+      if (n > 1) part_rows += n * H * nq;
+    }
+    const double merge = (double)part_rows * (D * 4 + 8) * 2 / ((double)slots * 32 * D * 2);
+    const double est = (double)work / (double)slots + (ch / 32 + 1) * 0.5 + merge;
+    if (pick == 0 || est < best) {
+      best = est;
+      pick = ch;
+    }
+  }
+  return pick;
+}
+
 // images: the planned head-128 prefill may use operand images (off where the workspace is
 // bounded, pa_paged_attention_static).  bias: GroupQueryAttention's attention bias is present
 // (its streaming decode runs one wavefront per SIMD at every cache dtype).
 Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype act, int kind,
                int chunk, bool linear = false, int linear_cap = 0, bool images = true,
-               bool bias = false) {
+               bool bias = false, const HostLens& hl = HostLens()) {
   Plan pl{};
   // The LATENT layout (values = leading dims of the key rows): its matrix-core kernel (kind 5)
   // where it covers the head sizes and dtypes, else the VALU kernel.
@@ -326,7 +371,15 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
                        : (int64_t)std::max(b->num_tokens, 1) * a->num_heads;
     const int64_t target =
         pl.kind == 5 ? PA_LATENT_TARGET * (int64_t)device_cus() : pl.ng > 1 ? 2048 : 4096;
-    if (units >= target) {
+    if (pl.kind == 5 && PA_LATENT_PLAN && hl.cum && hl.past && b->batch <= kLatPlanMaxBatch &&
+        c->block_size >= 16) {
+      // workgroups resident per CU: two at 128 value dims with one row group, else one
+      const int vd = a->v_head_size > 0 ? a->v_head_size : c->head_dim;
+      const int ng = pa::latent_row_groups(g, mq);
+      const int64_t slots = (vd <= 128 && ng == 1 ? 2 : 1) * (int64_t)device_cus();
+      chunk = latent_chunk(c, b, a, hl, ng, slots,
+                           std::max(256, 63 * c->block_size / 32 * 32));
+    } else if (units >= target) {
       chunk = (int)std::min<int64_t>(((int64_t)ctx + 31) / 32 * 32, INT32_MAX / 2);
     } else {
       const int64_t splits = (target + units - 1) / units;
@@ -394,6 +447,7 @@ struct RunOpts {
   const int32_t* bias_col_off = nullptr;  // per-sequence bias column offsets (sliding rings)
   bool smooth_softmax = false;
   bool images = true;  // operand images allowed (see make_plan)
+  HostLens host;       // host metadata lengths (LATENT chunk sizing)
 };
 
 // Operand images for a call with these options: not with a bias (the matrix-core kernels that
@@ -441,7 +495,7 @@ int run_attention(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dty
   if (!(a->softcap >= 0.0f) || !std::isfinite(a->softcap))
     return fail(PA_ERR_INVALID_ARGUMENT, "softcap must be finite and non-negative");
   Plan pl = make_plan(c, b, a, act, kind, chunk, opts.linear_cap > 0, opts.linear_cap,
-                      plan_images(opts), opts.bias != nullptr);
+                      plan_images(opts), opts.bias != nullptr, opts.host);
   if (kind == 2 && pl.kind != 2 && pa::prefill_coded_supported(c->head_dim, act, c->dtype))
     return fail(PA_ERR_UNSUPPORTED,
                 "prefill MFMA kernel: byte-coded pages run on it over operand images only (planned "
@@ -898,7 +952,10 @@ int op_layout(const pa_paged_attention_node* n, const pa_paged_attention_io* io,
   a.v_head_size = L->v_head;
   L->total = L->attn_off +
              workspace_for(&io->cache, &b, &a,
-                           make_plan(&io->cache, &b, &a, io->dtype, 0, 0, false, 0, images));
+                           make_plan(&io->cache, &b, &a, io->dtype, 0, 0, false, 0, images,
+                                     false,
+                                     HostLens{io->host_cumulative_sequence_length,
+                                              io->host_past_seqlens}));
   return PA_OK;
 }
 
@@ -1076,6 +1133,7 @@ static int paged_attention_impl(const pa_paged_attention_node* n, const pa_paged
   }
   RunOpts opts;
   opts.images = images;
+  opts.host = HostLens{io->host_cumulative_sequence_length, io->host_past_seqlens};
   const bool distinct = io->slot_mapping == nullptr &&
                         io->host_cumulative_sequence_length != nullptr && host_slots_distinct(io);
   if (distinct) L.batch.flags |= PA_BATCH_SLOTS_DISTINCT;

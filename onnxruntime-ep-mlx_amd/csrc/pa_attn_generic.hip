@@ -255,7 +255,28 @@ __global__ __launch_bounds__(64) void split_reduce_kernel(const AttnParams p) {
       wl = (ms == kNegInf) ? 0.0f : exp2f(ms - M);
     }
     const int n = min(64, nsplit - s0);
-    for (int k = 0; k < n; ++k) {
+    // Four split rows per round: their loads are issued together (a chain of one row at a time
+    // left the wavefront waiting a memory latency per row); the sums keep the split order.
+    int k = 0;
+    for (; k + 4 <= n; k += 4) {
+      float v[4][NE];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float* row = po + (int64_t)(s0 + k + u) * D;
+#pragma unroll
+        for (int q = 0; q < NE; ++q) {
+          const int e = lane + 64 * q;
+          v[u][q] = e < VD ? row[e] : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float wk = __shfl(wl, k + u, 64);
+#pragma unroll
+        for (int q = 0; q < NE; ++q) acc[q] += v[u][q] * wk;
+      }
+    }
+    for (; k < n; ++k) {
       const float wk = __shfl(wl, k, 64);
       const float* row = po + (int64_t)(s0 + k) * D;
 #pragma unroll

@@ -15,18 +15,77 @@
 //     in the same order in every wavefront, so all four hold the same scores and run the same
 //     online softmax;
 //   - accumulates P . V for its quarter of the value dims (VD / 4 columns), P split into hi + lo
-//     16-bit parts, from value-row slices read straight from the cache rows.
-// Each key byte is read once per workgroup for the scores; the value dims are the first VD key
-// dims, read a second time in the value layout (the same workgroup at the same time: L2 hits).
-// Steps of 32 keys are loaded two steps ahead into a three-slot register ring.  Partials of split
-// chunks go to the workspace at row (token * H + head) * max_splits + split (stride D), merged by
-// split_reduce_kernel as the VALU kernel's are.
+//     16-bit parts, from value-row slices of the step's rows.
+// Paged steps (block size a multiple of 16, every row in the pages) go through a three-slot LDS
+// ring: each 32-row step is copied to LDS by direct loads of whole 128-byte lines, two steps
+// ahead, and both the key operands and the value-row slices are read from there, so every row
+// byte leaves HBM once per workgroup.  Other steps (new rows from the batch, other block sizes)
+// use a three-slot register ring loaded straight from the rows (key pieces of 64 bytes per row
+// and instruction, the value slices read a second time: L2 hits).  Partials of split chunks go
+// to the workspace at row (token * H + head) * max_splits + split (stride D), merged by
+// split_reduce_kernel as the VALU kernel's are.  The chunk length comes from the host's
+// per-sequence lengths when the caller gives them (pa_api.cpp, latent_chunk).
 #include "pa_tiles.hpp"
 
 namespace pa {
 namespace {
 
-constexpr int kLatMaxKw = 5;  // k-steps per wavefront for D <= 640
+constexpr int kLatMaxKs = 20;  // k-steps of 32 dims in a key row: D <= 640
+
+#ifndef PA_LATENT_DEPTH
+#define PA_LATENT_DEPTH 3  // register ring slots: steps loaded DEPTH - 1 ahead of the compute
+#endif
+#ifndef PA_LATENT_LDS
+#define PA_LATENT_LDS 1  // paged steps staged in LDS by direct loads (else the register ring)
+#endif
+constexpr int kLatLdsSlots = 3;                   // LDS ring: steps issued two ahead
+constexpr int kLatSlotChunks = 32 * kLatMaxKs * 4;  // 16-byte pieces of a 32-row step, D <= 640
+
+// One direct LDS load: 16 bytes per lane from src to LDS byte address lds + 16 * lane.  Written
+// as inline assembly so that the compiler's memory-counter bookkeeping does not see it: the
+// builtin form made every later LDS read and barrier wait for all outstanding direct loads (the
+// prefetched steps included).  The kernel waits for these loads itself (lat_wait_vm) before the
+// barrier that publishes a step.
+// M0 (the LDS base of the load) is a reserved register: the compiler sets it before each
+// instruction of its own that reads it and this kernel has none, so the clobber is declared for
+// the record and its warning silenced.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lat_dma16(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Wait until at most n of this wavefront's vector-memory operations are outstanding (n is
+// wave-uniform; the s_waitcnt immediate must be a constant).  Encoding: vmcnt in bits 3:0 and
+// 15:14, expcnt (7) and lgkmcnt (15) left at their maxima.
+__device__ __forceinline__ void lat_wait_vm(int n) {
+#define LAT_VM(k) \
+  case k:         \
+    __builtin_amdgcn_s_waitcnt(((k) & 15) | (((k) >> 4) << 14) | 0x0F70); \
+    break;
+  switch (n) {
+    LAT_VM(1) LAT_VM(2) LAT_VM(3) LAT_VM(4) LAT_VM(5) LAT_VM(6) LAT_VM(7) LAT_VM(8) LAT_VM(9)
+    LAT_VM(10) LAT_VM(11) LAT_VM(12) LAT_VM(13) LAT_VM(14) LAT_VM(15) LAT_VM(16) LAT_VM(17)
+    LAT_VM(18) LAT_VM(19) LAT_VM(20)
+    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+  }
+#undef LAT_VM
+}
+
+// Piece x of row r of an LDS step slot sits at position x ^ (r & 7) within the row's leading
+// multiple of 8 pieces: the 16 rows an MFMA operand read touches spread over the banks.
+__device__ __forceinline__ int lat_swz(int x, int r, int cpr8) { return x < cpr8 ? x ^ (r & 7) : x; }
+
+template <int DW>
+__device__ __forceinline__ VRow<DW> lat_lds_vrow(const char* p) {
+  VRow<DW> v;
+  __builtin_memcpy(&v, p, sizeof(v));
+  return v;
+}
 
 // Value operand of N-tile j (8 keys x head dim (DW/16) c + j) from the eight value-row slices
 // of a step, as value_operand does for a Step.
@@ -41,27 +100,38 @@ __device__ __forceinline__ typename TT::vec8 lat_value_operand(const VRow<DW> (&
   return __builtin_bit_cast(typename TT::vec8, w);
 }
 
-template <int DW>
+template <int DW, int KW>
 struct LatStep {
-  u32x4 k[2][kLatMaxKw];  // this wavefront's key k-steps of tiles A / B (row c, dims 32 s + 8 G)
+  u32x4 k[2][KW];          // this wavefront's key k-steps of tiles A / B (row c, dims 32 s + 8 G)
   VRow<DW> v[8];          // value rows 4 G + e of tile A (e < 4) and B (e >= 4), its dims
 };
 
-// Two workgroups per CU at 128 value dims; one from 256 on (the ring of five key k-steps and
-// eight value-row slices per slot takes ~300 registers at 256, ~400 at 512).
-template <typename TT, int DW, bool CAP, int NG>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DW > 32 || NG > 1 ? 1 : 2,
-                                                                     DW > 32 || NG > 1 ? 1 : 2))) void
+// NW wavefronts per workgroup, each with VD / NW value dims (DW).  With the register ring:
+// two workgroups per CU at 128 value dims, one from 256 on (the ring of five key k-steps and
+// eight value-row slices per slot takes ~300 registers at 256, ~400 at 512).  With the LDS ring
+// (LDSK, 120 KiB of steps): one workgroup per CU.  (Eight wavefronts of 64 value dims, two per
+// SIMD with the register ring, measured 6 % slower at 512 value dims.)
+template <int DW, int NG, int NW, bool LDSK>
+constexpr int lat_waves_per_simd() {
+  return LDSK ? 1 : (DW > 32 || NG > 1 ? 1 : 2);
+}
+
+template <typename TT, int DW, bool CAP, int NG, int NW, bool LDSK>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
+    lat_waves_per_simd<DW, NG, NW, LDSK>(), lat_waves_per_simd<DW, NG, NW, LDSK>()))) void
 latent_kernel(const AttnParams p) {
   using vec8 = typename TT::vec8;
   constexpr int DL = DW / 16;  // N-tiles (and value dims per lane) of a wavefront
+  constexpr int KW = (kLatMaxKs + NW - 1) / NW;  // k-steps per wavefront, at most
   // partial score tiles: [buffer][wavefront][row group][tile][lane]
-  __shared__ f32x4 part[2][4][NG][2][64];
+  __shared__ f32x4 part[2][NW][NG][2][64];
+  // LDS ring of paged steps: slot = 32 rows of D / 8 16-byte pieces (row-major, swizzled)
+  __shared__ u32x4 lring[LDSK ? kLatLdsSlots * kLatSlotChunks : 1];
   const int rb = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, c = lane & 15, G = lane >> 4;
   const int D = p.head_dim, KS = D / 32;
-  const int ks0 = (KS * wave) / 4, nks = (KS * (wave + 1)) / 4 - ks0;
+  const int ks0 = (KS * wave) / NW, nks = (KS * (wave + 1)) / NW - ks0;
   // Everything up to the step loop is uniform over the workgroup (barriers inside the loop).
   const int s0 = min(max(p.cum[b], 0), p.num_tokens);
   const int s1 = min(max(p.cum[b + 1], s0), p.num_tokens);
@@ -94,13 +164,13 @@ latent_kernel(const AttnParams p) {
   const uint32_t qxor = p.scale < 0.0f ? 0x80008000u : 0u;
   const float scale = fabsf(p.scale), scale_log2 = fabsf(p.scale_log2);
   const float cap_k = CAP ? scale / p.softcap : 0.0f, cap_l2 = p.softcap * kLog2e;
-  // Every wavefront runs kLatMaxKw k-steps: those past its own (k >= nks) read k-step KS - 1
+  // Every wavefront runs KW k-steps: those past its own (k >= nks) read k-step KS - 1
   // again against zero query operands, so the loop carries no branch around loads or MFMAs.
   RowState<TT, DW> rs[NG];
-  vec8 qv[NG][kLatMaxKw];
-  int kofs[kLatMaxKw];  // byte offset of the lane's 16 bytes of each k-step in a key row
+  vec8 qv[NG][KW];
+  int kofs[KW];  // byte offset of the lane's 16 bytes of each k-step in a key row
 #pragma unroll
-  for (int k = 0; k < kLatMaxKw; ++k) kofs[k] = 64 * min(ks0 + k, KS - 1) + 16 * G;
+  for (int k = 0; k < KW; ++k) kofs[k] = 64 * min(ks0 + k, KS - 1) + 16 * G;
 #pragma unroll
   for (int j = 0; j < NG; ++j) {
     const int r = row0 + 16 * j + c;
@@ -116,7 +186,7 @@ latent_kernel(const AttnParams p) {
     const char* qrow =
         reinterpret_cast<const char*>(p.q) + (((int64_t)(s0 + qi) * H + head) * D) * 2 + 16 * G;
 #pragma unroll
-    for (int k = 0; k < kLatMaxKw; ++k) {
+    for (int k = 0; k < KW; ++k) {
       const u32x4 v = (k < nks && rvalid) ? (ld16(qrow + 64 * (ks0 + k)) ^ qxor)
                                           : u32x4{0u, 0u, 0u, 0u};
       qv[j][k] = __builtin_bit_cast(vec8, v);
@@ -140,7 +210,7 @@ latent_kernel(const AttnParams p) {
   // PAGED: 16-key tiles wholly in the pages (block size a multiple of 16, every row of the chunk
   // in the cache): one page id per tile; else row by row (new rows from the batch, other block
   // sizes; rows past the end read the last row).
-  auto load = [&](auto PAGED, LatStep<DW>& st, int t0) __attribute__((always_inline)) {
+  auto load = [&](auto PAGED, LatStep<DW, KW>& st, int t0) __attribute__((always_inline)) {
 #pragma unroll
     for (int T = 0; T < 2; ++T) {
       const int t = t0 + 16 * T;
@@ -161,19 +231,19 @@ latent_kernel(const AttnParams p) {
         for (int e = 0; e < 4; ++e) vr[e] = row_ptr(w, t + 4 * G + e, false, D);
       }
 #pragma unroll
-      for (int k = 0; k < kLatMaxKw; ++k) st.k[T][k] = ld16s(kr + kofs[k]);
+      for (int k = 0; k < KW; ++k) st.k[T][k] = ld16s(kr + kofs[k]);
 #pragma unroll
       for (int e = 0; e < 4; ++e) st.v[4 * T + e] = ld_vrow_s<DW>(vr[e] + vcol);
     }
   };
-  auto compute = [&](LatStep<DW>& st, int k) {
+  auto compute = [&](LatStep<DW, KW>& st, int k) {
     const int t0 = t_first + 32 * k;
     const int buf = k & 1;
 #pragma unroll
     for (int j = 0; j < NG; ++j) {
       f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kk = 0; kk < kLatMaxKw; ++kk) {
+      for (int kk = 0; kk < KW; ++kk) {
         if (kk < nks) {
           sa = TT::mfma(__builtin_bit_cast(vec8, st.k[0][kk]), qv[j][kk], sa);
           sb = TT::mfma(__builtin_bit_cast(vec8, st.k[1][kk]), qv[j][kk], sb);
@@ -189,7 +259,7 @@ latent_kernel(const AttnParams p) {
     for (int j = 0; j < NG; ++j) {
       f32x4 fa = part[buf][0][j][0][lane], fb = part[buf][0][j][1][lane];
 #pragma unroll
-      for (int u = 1; u < 4; ++u) {
+      for (int u = 1; u < NW; ++u) {
         fa += part[buf][u][j][0][lane];
         fb += part[buf][u][j][1][lane];
       }
@@ -228,34 +298,115 @@ latent_kernel(const AttnParams p) {
     }
   };
 
-  // Three-slot ring: the rows of step k + 2 are issued before step k is computed.
+  // Three-slot ring: the rows of step k + 2 are issued before step k is computed.  Every slot
+  // is loaded unconditionally (steps past the last one read the last step again, in bounds), so
+  // the loads carry no branch and the compiler's memory-counter waits stay exact: a load
+  // skipped on one path made it wait for every outstanding load, the prefetch included.
   auto steps = [&](auto PAGED) __attribute__((always_inline)) {
-    LatStep<DW> st[3];
-    if (nsteps > 0) load(PAGED, st[0], t_first);
-    if (nsteps > 1) load(PAGED, st[1], t_first + 32);
-    for (int k = 0; k < nsteps; k += 3) {
-      if (k + 2 < nsteps) load(PAGED, st[2], t_first + 32 * (k + 2));
-      compute(st[0], k);
-      if (k + 1 < nsteps) {
-        if (k + 3 < nsteps) load(PAGED, st[0], t_first + 32 * (k + 3));
-        compute(st[1], k + 1);
+    constexpr int DEPTH = PA_LATENT_DEPTH;
+    LatStep<DW, KW> st[DEPTH];
+    const int last = t_first + 32 * (nsteps - 1);
+    auto at = [&](int k) { return min(t_first + 32 * k, last); };
+#pragma unroll
+    for (int i = 0; i < DEPTH - 1; ++i) load(PAGED, st[i], at(i));
+    for (int k = 0; k < nsteps; k += DEPTH) {
+#pragma unroll
+      for (int i = 0; i < DEPTH; ++i) {
+        load(PAGED, st[(i + DEPTH - 1) % DEPTH], at(k + i + DEPTH - 1));
+        if (i == 0 || k + i < nsteps) compute(st[i], k + i);
       }
-      if (k + 2 < nsteps) {
-        if (k + 4 < nsteps) load(PAGED, st[1], t_first + 32 * (k + 4));
-        compute(st[2], k + 2);
+    }
+  };
+  // LDS-staged paged steps.  Each 32-row step goes to an LDS slot by direct loads (16 bytes per
+  // lane, whole 128-byte lines of the page rows per instruction): wavefront w fetches pieces
+  // [w D, (w + 1) D) of the slot's 4 D, i.e. ceil(D / 64) loads per step.  The operands are then
+  // read from LDS in the register-ring layout (keys: row c of a tile, k-step pieces; values: the
+  // wavefront's value-dim slice of eight rows) and computed as there.  Steps are issued two
+  // ahead; before step k each wavefront waits for its own loads of step k (the count of its
+  // later loads still allowed outstanding), then the workgroup barrier makes every wavefront's
+  // pieces visible and frees the slot of step k - 1 for step k + 2.
+  auto lds_steps = [&]() __attribute__((always_inline)) {
+    const int CPR = D / 8, CPR8 = CPR & ~7;
+    const int NIW = (D + 63) / 64;  // direct loads per wavefront and step (D % 64 is 0 or 32)
+    int pk[kLatMaxKs / 2];          // per load: (row offset in its page + piece offset) << 5 | row
+#pragma unroll
+    for (int i = 0; i < kLatMaxKs / 2; ++i) {
+      const int s = wave * D + 64 * i + lane;
+      const int r = min(s / CPR, 31), xp = s - (s / CPR) * CPR;
+      pk[i] = (((r & 15) * (int)w.rowb + 16 * lat_swz(xp, r, CPR8)) << 5) | r;
+    }
+    char* const lbase = reinterpret_cast<char*>(&lring[0]);
+    // LDS byte address of the ring (the address-space-3 pointer's value)
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lbase;
+    auto issue = [&](int k) __attribute__((always_inline)) {
+      const int t0 = t_first + 32 * k;
+      const char* tb[2];
+#pragma unroll
+      for (int T = 0; T < 2; ++T) {
+        const int t = t0 + 16 * T;
+        const int bi = min(div_bs(t, w), w.max_blocks - 1);
+        int64_t blk = __builtin_amdgcn_readlane(pw.ids, min(max(bi - pw.first, 0), 63));
+        blk = min(max(blk, (int64_t)0), w.num_blocks - 1);
+        tb[T] = w.kc + (blk * w.bs + mod_bs(t, w)) * w.rowb;
       }
+      const uint32_t ldst = __builtin_amdgcn_readfirstlane(
+          lds0 + (k % kLatLdsSlots) * (kLatSlotChunks * 16) + wave * D * 16);
+#pragma unroll
+      for (int i = 0; i < kLatMaxKs / 2; ++i) {
+        if (i < NIW && 64 * i + lane < D) {
+          const int r = pk[i] & 31, off = pk[i] >> 5;
+          // rows past the sequence end read the last row (finite values under probability 0)
+          const char* src = t0 + r < total ? (r < 16 ? tb[0] : tb[1]) + off
+                                           : last_row + (off - (r & 15) * (int)w.rowb);
+          lat_dma16(src, ldst + 1024 * i);
+        }
+      }
+    };
+    auto fill = [&](LatStep<DW, KW>& st, int k) __attribute__((always_inline)) {
+      const char* const sb = lbase + (k % kLatLdsSlots) * (kLatSlotChunks * 16);
+#pragma unroll
+      for (int T = 0; T < 2; ++T) {
+        const int r = 16 * T + c;
+#pragma unroll
+        for (int kk = 0; kk < KW; ++kk) {
+          const int x = 4 * min(ks0 + kk, KS - 1) + G;
+          st.k[T][kk] = *reinterpret_cast<const u32x4*>(sb + (r * CPR + lat_swz(x, r, CPR8)) * 16);
+        }
+      }
+      const int vb = vcol >> 4, vw = vcol & 15;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int r = 16 * (e >> 2) + 4 * G + (e & 3);
+        st.v[e] = lat_lds_vrow<DW>(sb + (r * CPR + lat_swz(vb, r, CPR8)) * 16 + vw);
+      }
+    };
+#pragma unroll
+    for (int i = 0; i < kLatLdsSlots - 1; ++i)
+      if (i < nsteps) issue(i);
+    for (int k = 0; k < nsteps; ++k) {
+      lat_wait_vm(min(kLatLdsSlots - 2, nsteps - 1 - k) * NIW);
+      __syncthreads();
+      if (k + kLatLdsSlots - 1 < nsteps) issue(k + kLatLdsSlots - 1);
+      LatStep<DW, KW> st;
+      fill(st, k);
+      compute(st, k);
     }
   };
   // every row the steps read below the sequence end in the pages, pages of whole 16-key tiles,
   // one window of page ids (rows past the end are zeroed or masked)
-  if (w.bs % 16 == 0 && w.cache_limit >= min(w.total, t_first + 32 * nsteps) &&
-      div_bs(t_first + 32 * nsteps - 1, w) - pw.first < 64)
-    steps(std::true_type{});
-  else
+  if (nsteps <= 0) {
+  } else if (w.bs % 16 == 0 && w.cache_limit >= min(w.total, t_first + 32 * nsteps) &&
+             div_bs(t_first + 32 * nsteps - 1, w) - pw.first < 64) {
+    if constexpr (LDSK)
+      lds_steps();
+    else
+      steps(std::true_type{});
+  } else {
     steps(std::false_type{});
+  }
 
   // Rows 4 G + i of this lane's O registers in each group: this wavefront's DW value dims.
-  const int VD = 4 * DW;
+  const int VD = NW * DW;
 #pragma unroll
   for (int j = 0; j < NG; ++j) {
     float l_row = rs[j].l_part + __shfl_xor(rs[j].l_part, 16, 64);
@@ -299,37 +450,38 @@ latent_kernel(const AttnParams p) {
   }
 }
 
-template <typename TT, int DW>
+template <typename TT, int DW, int NW>
 void launch_lat_dw(const AttnParams& p, dim3 grid, int ng, hipStream_t s) {
+  const dim3 block(64 * NW);
   if (ng == 2) {
     if (p.softcap > 0.0f)
-      hipLaunchKernelGGL((latent_kernel<TT, DW, true, 2>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((latent_kernel<TT, DW, true, 2, NW, PA_LATENT_LDS != 0>), grid, block, 0, s, p);
     else
-      hipLaunchKernelGGL((latent_kernel<TT, DW, false, 2>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((latent_kernel<TT, DW, false, 2, NW, PA_LATENT_LDS != 0>), grid, block, 0, s, p);
   } else if (p.softcap > 0.0f) {
-    hipLaunchKernelGGL((latent_kernel<TT, DW, true, 1>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((latent_kernel<TT, DW, true, 1, NW, PA_LATENT_LDS != 0>), grid, block, 0, s, p);
   } else {
-    hipLaunchKernelGGL((latent_kernel<TT, DW, false, 1>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((latent_kernel<TT, DW, false, 1, NW, PA_LATENT_LDS != 0>), grid, block, 0, s, p);
   }
 }
 
 template <typename TT>
 void launch_lat_t(const AttnParams& p, dim3 grid, int ng, hipStream_t s) {
   switch (p.v_head_dim) {
-    case 128: launch_lat_dw<TT, 32>(p, grid, ng, s); break;
-    case 256: launch_lat_dw<TT, 64>(p, grid, ng, s); break;
-    default: launch_lat_dw<TT, 128>(p, grid, ng, s); break;
+    case 128: launch_lat_dw<TT, 32, 4>(p, grid, ng, s); break;
+    case 256: launch_lat_dw<TT, 64, 4>(p, grid, ng, s); break;
+    default: launch_lat_dw<TT, 128, 4>(p, grid, ng, s); break;
   }
 }
 
 }  // namespace
 
-// Key rows of D = 32 k dims up to 640 (5 k-steps per wavefront), values = their first 128, 256 or
-// 512 dims, 16-bit activations with the cache in the same type.
+// Key rows of D = 32 k dims up to 640, values = their first 128, 256 or 512 dims, 16-bit
+// activations with the cache in the same type.
 bool latent_mfma_supported(int head_dim, int v_head_dim, pa_dtype act, pa_dtype cache_dtype) {
   if (act != PA_DTYPE_FLOAT16 && act != PA_DTYPE_BFLOAT16) return false;
   if (cache_dtype != act) return false;
-  if (head_dim % 32 != 0 || head_dim > 32 * 4 * kLatMaxKw) return false;
+  if (head_dim % 32 != 0 || head_dim > 32 * kLatMaxKs) return false;
   return (v_head_dim == 128 || v_head_dim == 256 || v_head_dim == 512) && v_head_dim <= head_dim;
 }
 
