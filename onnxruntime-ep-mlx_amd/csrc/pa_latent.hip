@@ -38,8 +38,19 @@ constexpr int kLatMaxKs = 20;  // k-steps of 32 dims in a key row: D <= 640
 #ifndef PA_LATENT_LDS
 #define PA_LATENT_LDS 1  // paged steps staged in LDS by direct loads (else the register ring)
 #endif
-constexpr int kLatLdsSlots = 3;                   // LDS ring: steps issued two ahead
-constexpr int kLatSlotChunks = 32 * kLatMaxKs * 4;  // 16-byte pieces of a 32-row step, D <= 640
+#ifndef PA_LATENT_LDS_SLOTS1
+#define PA_LATENT_LDS_SLOTS1 4
+#endif
+// LDS ring of paged steps: slots of 32 rows x D / 8 16-byte pieces for D <= 576 (the MLA
+// 576-dim rows): four slots (steps issued three ahead) with one row group, whose partial-score
+// buffer leaves exactly that room in the 160 KiB, three with two.  Longer rows take the
+// register ring.
+constexpr int kLatLdsMaxD = 576;
+constexpr int kLatSlotChunks = 32 * kLatLdsMaxD / 8;
+template <int NG>
+constexpr int lat_lds_slots() {
+  return NG == 1 ? PA_LATENT_LDS_SLOTS1 : 3;
+}
 
 // One direct LDS load: 16 bytes per lane from src to LDS byte address lds + 16 * lane.  Written
 // as inline assembly so that the compiler's memory-counter bookkeeping does not see it: the
@@ -126,6 +137,7 @@ latent_kernel(const AttnParams p) {
   // partial score tiles: [buffer][wavefront][row group][tile][lane]
   __shared__ f32x4 part[2][NW][NG][2][64];
   // LDS ring of paged steps: slot = 32 rows of D / 8 16-byte pieces (row-major, swizzled)
+  constexpr int kLatLdsSlots = lat_lds_slots<NG>();
   __shared__ u32x4 lring[LDSK ? kLatLdsSlots * kLatSlotChunks : 1];
   const int rb = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -396,7 +408,7 @@ latent_kernel(const AttnParams p) {
   // one window of page ids (rows past the end are zeroed or masked)
   if (nsteps <= 0) {
   } else if (w.bs % 16 == 0 && w.cache_limit >= min(w.total, t_first + 32 * nsteps) &&
-             div_bs(t_first + 32 * nsteps - 1, w) - pw.first < 64) {
+             div_bs(t_first + 32 * nsteps - 1, w) - pw.first < 64 && (!LDSK || D <= kLatLdsMaxD)) {
     if constexpr (LDSK)
       lds_steps();
     else
