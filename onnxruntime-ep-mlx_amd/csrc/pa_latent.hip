@@ -347,30 +347,61 @@ latent_kernel(const AttnParams p) {
       const int r = min(s / CPR, 31), xp = s - (s / CPR) * CPR;
       pk[i] = (((r & 15) * (int)w.rowb + 16 * lat_swz(xp, r, CPR8)) << 5) | r;
     }
+    // the same plan split for the common case: offsets, and a bit per load for rows 16..31
+    int poff[kLatMaxKs / 2];
+    uint32_t hi16 = 0;
+#pragma unroll
+    for (int i = 0; i < kLatMaxKs / 2; ++i) {
+      poff[i] = pk[i] >> 5;
+      hi16 |= (uint32_t)((pk[i] & 31) >= 16) << i;
+    }
     char* const lbase = reinterpret_cast<char*>(&lring[0]);
     // LDS byte address of the ring (the address-space-3 pointer's value)
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lbase;
+    // Page cursor of the next step to issue (steps are issued once each, in order): block-table
+    // index and row in the block of its first key, advanced by 32 keys per step.
+    int cur_bi = div_bs(t_first, w), cur_ob = mod_bs(t_first, w);
     auto issue = [&](int k) __attribute__((always_inline)) {
       const int t0 = t_first + 32 * k;
       const char* tb[2];
 #pragma unroll
       for (int T = 0; T < 2; ++T) {
-        const int t = t0 + 16 * T;
-        const int bi = min(div_bs(t, w), w.max_blocks - 1);
+        int bi = cur_bi, ob = cur_ob + 16 * T;
+        if (ob >= w.bs) {  // the block size is a multiple of 16
+          ob -= w.bs;
+          ++bi;
+        }
+        bi = min(bi, w.max_blocks - 1);
         int64_t blk = __builtin_amdgcn_readlane(pw.ids, min(max(bi - pw.first, 0), 63));
         blk = min(max(blk, (int64_t)0), w.num_blocks - 1);
-        tb[T] = w.kc + (blk * w.bs + mod_bs(t, w)) * w.rowb;
+        tb[T] = w.kc + (blk * w.bs + ob) * w.rowb;
+      }
+      cur_ob += 32;
+      while (cur_ob >= w.bs) {  // at most twice (block size >= 16)
+        cur_ob -= w.bs;
+        ++cur_bi;
       }
       const uint32_t ldst = __builtin_amdgcn_readfirstlane(
           lds0 + (k % kLatLdsSlots) * (kLatSlotChunks * 16) + wave * D * 16);
+      if (D % 64 == 0 && t0 + 32 <= total) {
+        // every lane loads, every row of the step is a sequence row
 #pragma unroll
-      for (int i = 0; i < kLatMaxKs / 2; ++i) {
-        if (i < NIW && 64 * i + lane < D) {
-          const int r = pk[i] & 31, off = pk[i] >> 5;
-          // rows past the sequence end read the last row (finite values under probability 0)
-          const char* src = t0 + r < total ? (r < 16 ? tb[0] : tb[1]) + off
-                                           : last_row + (off - (r & 15) * (int)w.rowb);
-          lat_dma16(src, ldst + 1024 * i);
+        for (int i = 0; i < kLatMaxKs / 2; ++i) {
+          if (i < NIW) {
+            const char* src = ((hi16 >> i) & 1u ? tb[1] : tb[0]) + poff[i];
+            lat_dma16(src, ldst + 1024 * i);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < kLatMaxKs / 2; ++i) {
+          if (i < NIW && 64 * i + lane < D) {
+            const int r = pk[i] & 31, off = pk[i] >> 5;
+            // rows past the sequence end read the last row (finite values under probability 0)
+            const char* src = t0 + r < total ? (r < 16 ? tb[0] : tb[1]) + off
+                                             : last_row + (off - (r & 15) * (int)w.rowb);
+            lat_dma16(src, ldst + 1024 * i);
+          }
         }
       }
     };
@@ -396,7 +427,14 @@ latent_kernel(const AttnParams p) {
     for (int i = 0; i < kLatLdsSlots - 1; ++i)
       if (i < nsteps) issue(i);
     for (int k = 0; k < nsteps; ++k) {
-      lat_wait_vm(min(kLatLdsSlots - 2, nsteps - 1 - k) * NIW);
+      const int later = min(kLatLdsSlots - 2, nsteps - 1 - k) * NIW;  // loads issued after step k's
+      // 576-dim rows in the steady state (four or three slots): no search for the immediate
+      if (NIW == 9 && later == 18)
+        __builtin_amdgcn_s_waitcnt((18 & 15) | ((18 >> 4) << 14) | 0x0F70);
+      else if (NIW == 9 && later == 9)
+        __builtin_amdgcn_s_waitcnt(9 | 0x0F70);
+      else
+        lat_wait_vm(later);
       __syncthreads();
       if (k + kLatLdsSlots - 1 < nsteps) issue(k + kLatLdsSlots - 1);
       LatStep<DW, KW> st;
