@@ -214,6 +214,10 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
   }
 }
 
+#ifndef PA_MERGE_ROUND
+#define PA_MERGE_ROUND 4  // eight per round measured slower (more registers, fewer waves)
+#endif
+
 // Merge the per-chunk partials of one (token, head): global max, rescaled sums, divide.
 // Partial rows have stride head_dim; outputs hold v_head_dim values per head.
 template <typename TT, int NE>
@@ -255,13 +259,15 @@ __global__ __launch_bounds__(64) void split_reduce_kernel(const AttnParams p) {
       wl = (ms == kNegInf) ? 0.0f : exp2f(ms - M);
     }
     const int n = min(64, nsplit - s0);
-    // Four split rows per round: their loads are issued together (a chain of one row at a time
-    // left the wavefront waiting a memory latency per row); the sums keep the split order.
+    // PA_MERGE_ROUND split rows per round: their loads are issued together (a chain of one row
+    // at a time left the wavefront waiting a memory latency per row); the sums keep the split
+    // order.
+    constexpr int RND = PA_MERGE_ROUND;
     int k = 0;
-    for (; k + 4 <= n; k += 4) {
-      float v[4][NE];
+    for (; k + RND <= n; k += RND) {
+      float v[RND][NE];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < RND; ++u) {
         const float* row = po + (int64_t)(s0 + k + u) * D;
 #pragma unroll
         for (int q = 0; q < NE; ++q) {
@@ -270,7 +276,7 @@ __global__ __launch_bounds__(64) void split_reduce_kernel(const AttnParams p) {
         }
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < RND; ++u) {
         const float wk = __shfl(wl, k + u, 64);
 #pragma unroll
         for (int q = 0; q < NE; ++q) acc[q] += v[u][q] * wk;
