@@ -81,7 +81,8 @@ __device__ __forceinline__ void lat_wait_vm(int n) {
   switch (n) {
     LAT_VM(1) LAT_VM(2) LAT_VM(3) LAT_VM(4) LAT_VM(5) LAT_VM(6) LAT_VM(7) LAT_VM(8) LAT_VM(9)
     LAT_VM(10) LAT_VM(11) LAT_VM(12) LAT_VM(13) LAT_VM(14) LAT_VM(15) LAT_VM(16) LAT_VM(17)
-    LAT_VM(18) LAT_VM(19) LAT_VM(20)
+    LAT_VM(18) LAT_VM(19) LAT_VM(20) LAT_VM(21) LAT_VM(22) LAT_VM(23) LAT_VM(24) LAT_VM(25)
+    LAT_VM(26) LAT_VM(27) LAT_VM(28) LAT_VM(29) LAT_VM(30)
     default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
   }
 #undef LAT_VM
@@ -248,7 +249,9 @@ latent_kernel(const AttnParams p) {
       for (int e = 0; e < 4; ++e) st.v[4 * T + e] = ld_vrow_s<DW>(vr[e] + vcol);
     }
   };
-  auto compute = [&](LatStep<DW, KW>& st, int k) {
+  // mid(): between the partial-score writes and their reads -- the workgroup barrier, with
+  // whatever the caller's ring does at it
+  auto compute = [&](LatStep<DW, KW>& st, int k, auto&& mid) {
     const int t0 = t_first + 32 * k;
     const int buf = k & 1;
 #pragma unroll
@@ -264,7 +267,7 @@ latent_kernel(const AttnParams p) {
       part[buf][wave][j][0][lane] = sa;
       part[buf][wave][j][1][lane] = sb;
     }
-    __syncthreads();
+    mid();
     const bool masked = !(t0 >= all_lo && t0 + 32 <= all_hi);
     vec8 phi[NG], plo[NG];
 #pragma unroll
@@ -325,7 +328,7 @@ latent_kernel(const AttnParams p) {
 #pragma unroll
       for (int i = 0; i < DEPTH; ++i) {
         load(PAGED, st[(i + DEPTH - 1) % DEPTH], at(k + i + DEPTH - 1));
-        if (i == 0 || k + i < nsteps) compute(st[i], k + i);
+        if (i == 0 || k + i < nsteps) compute(st[i], k + i, [] { __syncthreads(); });
       }
     }
   };
@@ -424,10 +427,12 @@ latent_kernel(const AttnParams p) {
       }
     };
 #pragma unroll
-    for (int i = 0; i < kLatLdsSlots - 1; ++i)
+    for (int i = 0; i < kLatLdsSlots; ++i)
       if (i < nsteps) issue(i);
-    for (int k = 0; k < nsteps; ++k) {
-      const int later = min(kLatLdsSlots - 2, nsteps - 1 - k) * NIW;  // loads issued after step k's
+    // One barrier per step: the one between the partial-score writes and reads of step k also
+    // publishes step k + 1's pieces (each wavefront waits for its own loads first) and frees
+    // the slot step k was read from (its operands are in registers by then) for step k + S.
+    auto wait_loads = [&](int later) __attribute__((always_inline)) {
       // 576-dim rows in the steady state (four or three slots): no search for the immediate
       if (NIW == 9 && later == 18)
         __builtin_amdgcn_s_waitcnt((18 & 15) | ((18 >> 4) << 14) | 0x0F70);
@@ -435,11 +440,17 @@ latent_kernel(const AttnParams p) {
         __builtin_amdgcn_s_waitcnt(9 | 0x0F70);
       else
         lat_wait_vm(later);
-      __syncthreads();
-      if (k + kLatLdsSlots - 1 < nsteps) issue(k + kLatLdsSlots - 1);
+    };
+    wait_loads(min(kLatLdsSlots - 1, nsteps - 1) * NIW);  // loads issued after step 0's
+    __syncthreads();
+    for (int k = 0; k < nsteps; ++k) {
       LatStep<DW, KW> st;
       fill(st, k);
-      compute(st, k);
+      compute(st, k, [&] {
+        if (k + 1 < nsteps) wait_loads(min(kLatLdsSlots - 2, nsteps - 2 - k) * NIW);
+        __syncthreads();
+        if (k + kLatLdsSlots < nsteps) issue(k + kLatLdsSlots);
+      });
     }
   };
   // every row the steps read below the sequence end in the pages, pages of whole 16-key tiles,
