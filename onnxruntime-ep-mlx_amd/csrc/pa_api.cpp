@@ -197,13 +197,19 @@ struct HostLens {
 #ifndef PA_LATENT_PLAN
 #define PA_LATENT_PLAN 1
 #endif
+// Price of a partial-row byte against a key byte in latent_chunk: the merge streams its rows
+// slower than the kernel streams keys (MLA decode at 16 heads, config 3 contexts: weight 1
+// 142.2 us per step, 2 137.8 us, 3 137.4 us).
+#ifndef PA_LATENT_MERGE_W
+#define PA_LATENT_MERGE_W 3.0
+#endif
 constexpr int kLatPlanMaxBatch = 4096;  // batches beyond this keep the capacity rule (host cost)
 
 // LATENT kernel: the context chunk (a multiple of 32 keys in [256, cap]) that minimises the
 // estimated launch time for the host's per-sequence key counts, in units of one 32-key step of a
 // workgroup: the work of all workgroups spread over `slots` resident ones, plus half a
 // workgroup's length for the last dispatch round, plus the partial rows of split sequences (fp32
-// O, m, l written by the kernel and read by the merge) priced as key bytes.  0 when no chunk is
+// O, m, l written by the kernel and read by the merge) priced as PA_LATENT_MERGE_W key bytes.  0 when no chunk is
 // better than a whole context (never: a split of the longest sequence always balances better).
 int latent_chunk(const pa_cache* c, const pa_batch* b, const pa_attn* a, const HostLens& hl,
                  int ng, int64_t slots, int cap) {
@@ -222,7 +228,8 @@ int latent_chunk(const pa_cache* c, const pa_batch* b, const pa_attn* a, const H
       work += rbs * ((tot + 31) / 32 + n);  // steps + one step of set-up per workgroup
       if (n > 1) part_rows += n * H * nq;
     }
-    const double merge = (double)part_rows * (D * 4 + 8) * 2 / ((double)slots * 32 * D * 2);
+    const double merge =
+        PA_LATENT_MERGE_W * (double)part_rows * (D * 4 + 8) * 2 / ((double)slots * 32 * D * 2);
     const double est = (double)work / (double)slots + (ch / 32 + 1) * 0.5 + merge;
     if (pick == 0 || est < best) {
       best = est;
