@@ -209,8 +209,7 @@ constexpr int kLatPlanMaxBatch = 4096;  // batches beyond this keep the capacity
 // estimated launch time for the host's per-sequence key counts, in units of one 32-key step of a
 // workgroup: the work of all workgroups spread over `slots` resident ones, plus half a
 // workgroup's length for the last dispatch round, plus the partial rows of split sequences (fp32
-// O, m, l written by the kernel and read by the merge) priced as PA_LATENT_MERGE_W key bytes.  0 when no chunk is
-// better than a whole context (never: a split of the longest sequence always balances better).
+// O, m, l written by the kernel and read by the merge) priced as PA_LATENT_MERGE_W key bytes.
 int latent_chunk(const pa_cache* c, const pa_batch* b, const pa_attn* a, const HostLens& hl,
                  int ng, int64_t slots, int cap) {
   const int D = c->head_dim;
