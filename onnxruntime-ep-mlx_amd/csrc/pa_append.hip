@@ -166,6 +166,24 @@ __device__ void process_row(const AppendParams& p, const void* src, int64_t src_
     put(e1, o1);
     put(e2, o2);
   }
+  // Elements outside the rotated range: plain copies.  16-bit rows with 16-byte aligned pieces
+  // (e.g. the LATENT layout's 512 latent dims beside a 64-dim rotary range) move 8 elements per
+  // lane and access, the bits unchanged; otherwise element by element.
+  using raw = typename TT::raw;
+  const int rot_lo = off, rot_hi = off + 2 * half;
+  if (sizeof(raw) == 2 && !norm_w && !q8 && D % 8 == 0 && rot_lo % 8 == 0 && rot_hi % 8 == 0 &&
+      ((src_base | dst_base | (dst2 ? dst2_base : 0)) & 7) == 0 &&
+      ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst) |
+        reinterpret_cast<uintptr_t>(dst2)) & 15) == 0) {
+    const raw* s16 = reinterpret_cast<const raw*>(src) + src_base;
+    for (int e = 8 * lane; e < D; e += 512) {
+      if (e >= rot_lo && e < rot_hi) continue;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(s16 + e);
+      if (dst) *reinterpret_cast<u32x4*>(reinterpret_cast<raw*>(dst) + dst_base + e) = v;
+      if (dst2) *reinterpret_cast<u32x4*>(reinterpret_cast<raw*>(dst2) + dst2_base + e) = v;
+    }
+    return;
+  }
   for (int e = lane; e < D; e += 64) {
     if (e >= off && e < off + 2 * half) continue;
     put(e, fetch(e));
