@@ -249,39 +249,18 @@ latent_kernel(const AttnParams p) {
       for (int e = 0; e < 4; ++e) st.v[4 * T + e] = ld_vrow_s<DW>(vr[e] + vcol);
     }
   };
-  // mid(): between the partial-score writes and their reads -- the workgroup barrier, with
-  // whatever the caller's ring does at it
-  auto compute = [&](LatStep<DW, KW>& st, int k, auto&& mid) {
+  // Softmax and P . V of step k from its full score tiles (fa: keys t0 .. t0 + 15, fb: the next
+  // 16) and the value-row slices in st.
+  auto finish = [&](LatStep<DW, KW>& st, int k, const f32x4 (&fa)[NG], const f32x4 (&fb)[NG]) {
     const int t0 = t_first + 32 * k;
-    const int buf = k & 1;
-#pragma unroll
-    for (int j = 0; j < NG; ++j) {
-      f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < KW; ++kk) {
-        if (kk < nks) {
-          sa = TT::mfma(__builtin_bit_cast(vec8, st.k[0][kk]), qv[j][kk], sa);
-          sb = TT::mfma(__builtin_bit_cast(vec8, st.k[1][kk]), qv[j][kk], sb);
-        }
-      }
-      part[buf][wave][j][0][lane] = sa;
-      part[buf][wave][j][1][lane] = sb;
-    }
-    mid();
     const bool masked = !(t0 >= all_lo && t0 + 32 <= all_hi);
     vec8 phi[NG], plo[NG];
 #pragma unroll
     for (int j = 0; j < NG; ++j) {
-      f32x4 fa = part[buf][0][j][0][lane], fb = part[buf][0][j][1][lane];
-#pragma unroll
-      for (int u = 1; u < NW; ++u) {
-        fa += part[buf][u][j][0][lane];
-        fb += part[buf][u][j][1][lane];
-      }
       float x[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float sv = e < 4 ? fa[e & 3] : fb[e & 3];
+        const float sv = e < 4 ? fa[j][e & 3] : fb[j][e & 3];
         x[e] = CAP ? softcap_log2(sv, cap_k, cap_l2) : sv * scale_log2;
       }
       if (masked) {
@@ -311,6 +290,38 @@ latent_kernel(const AttnParams p) {
         rs[j].o[n] = TT::mfma(plo[j], vb, rs[j].o[n]);
       }
     }
+  };
+  // Partial scores of this wavefront's k-steps, summed across the wavefronts through LDS.
+  // mid(): between the partial-score writes and their reads -- the workgroup barrier, with
+  // whatever the caller's ring does at it.
+  auto compute = [&](LatStep<DW, KW>& st, int k, auto&& mid) {
+    const int buf = k & 1;
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+      f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KW; ++kk) {
+        if (kk < nks) {
+          sa = TT::mfma(__builtin_bit_cast(vec8, st.k[0][kk]), qv[j][kk], sa);
+          sb = TT::mfma(__builtin_bit_cast(vec8, st.k[1][kk]), qv[j][kk], sb);
+        }
+      }
+      part[buf][wave][j][0][lane] = sa;
+      part[buf][wave][j][1][lane] = sb;
+    }
+    mid();
+    f32x4 fa[NG], fb[NG];
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+      fa[j] = part[buf][0][j][0][lane];
+      fb[j] = part[buf][0][j][1][lane];
+#pragma unroll
+      for (int u = 1; u < NW; ++u) {
+        fa[j] += part[buf][u][j][0][lane];
+        fb[j] += part[buf][u][j][1][lane];
+      }
+    }
+    finish(st, k, fa, fb);
   };
 
   // Three-slot ring: the rows of step k + 2 are issued before step k is computed.  Every slot
@@ -443,14 +454,15 @@ latent_kernel(const AttnParams p) {
     };
     wait_loads(min(kLatLdsSlots - 1, nsteps - 1) * NIW);  // loads issued after step 0's
     __syncthreads();
+    auto next = [&](int k) __attribute__((always_inline)) {
+      if (k + 1 < nsteps) wait_loads(min(kLatLdsSlots - 2, nsteps - 2 - k) * NIW);
+      __syncthreads();
+      if (k + kLatLdsSlots < nsteps) issue(k + kLatLdsSlots);
+    };
     for (int k = 0; k < nsteps; ++k) {
       LatStep<DW, KW> st;
       fill(st, k);
-      compute(st, k, [&] {
-        if (k + 1 < nsteps) wait_loads(min(kLatLdsSlots - 2, nsteps - 2 - k) * NIW);
-        __syncthreads();
-        if (k + kLatLdsSlots < nsteps) issue(k + kLatLdsSlots);
-      });
+      compute(st, k, [&] { next(k); });
     }
   };
   // every row the steps read below the sequence end in the pages, pages of whole 16-key tiles,
