@@ -1,5 +1,5 @@
-"""The structs of include/pa_mi355x.h against their ctypes mirrors (and the Rust mirrors shown in
-INTEGRATION.md): same field names in the same order, same offsets, same sizes.
+"""The structs of include/pa_mi355x.h against their ctypes mirrors (and the Rust mirrors in the
+repository's integration notes): same field names in the same order, same offsets, same sizes.
 
 The header is compiled with gcc into a small program that prints sizeof/offsetof of every field
 the header declares; the field lists come from parsing the header itself, so a field added to
@@ -34,7 +34,9 @@ MIRRORS = {
     "pa_gqa_node_info": capi.PaGqaNodeInfo,
 }
 
-# header struct -> Rust mirror name in INTEGRATION.md
+NOTES = "INTEGRATION.md"  # the integration notes at the repository root
+
+# header struct -> Rust mirror name in the integration notes
 RUST_MIRRORS = {
     "pa_cache": "PaCache",
     "pa_paged_attention_node": "PaNode",
@@ -108,9 +110,9 @@ def test_ctypes_mirror_matches_header(struct, c_layout):
 
 
 def rust_struct_fields(name: str) -> list[str]:
-    text = (ROOT / "INTEGRATION.md").read_text()
+    text = (ROOT / NOTES).read_text()
     m = re.search(r"pub struct " + name + r" \{(.*?)\n\}", text, flags=re.S)
-    assert m, f"Rust mirror {name} not found in INTEGRATION.md"
+    assert m, f"Rust mirror {name} not found in {NOTES}"
     body = re.sub(r"//[^\n]*", "", m.group(1))
     return re.findall(r"pub (\w+):", body)
 
