@@ -203,6 +203,14 @@ struct HostLens {
 #ifndef PA_LATENT_MERGE_W
 #define PA_LATENT_MERGE_W 3.0
 #endif
+// Resident workgroups assumed by latent_chunk, in multiples of the real count: the estimate
+// leaves out each workgroup's fixed cost (query load, first steps' latency, partial rows), and
+// a doubled count picks the chunk that measured best (MLA decode at 16 heads, config 3
+// contexts, step: x1 (chunk 640) 135.8 us, x2 (480) 124.9 us, x3 (416) 139.9 us, x4 (352)
+// 152.6 us; 128 heads unchanged at the 992-key cap).
+#ifndef PA_LATENT_SLOTS_X
+#define PA_LATENT_SLOTS_X 2.0
+#endif
 constexpr int kLatPlanMaxBatch = 4096;  // batches beyond this keep the capacity rule (host cost)
 
 // LATENT kernel: the context chunk (a multiple of 32 keys in [256, cap]) that minimises the
@@ -382,7 +390,8 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
       // workgroups resident per CU: two at 128 value dims with one row group, else one
       const int vd = a->v_head_size > 0 ? a->v_head_size : c->head_dim;
       const int ng = pa::latent_row_groups(g, mq);
-      const int64_t slots = (vd <= 128 && ng == 1 ? 2 : 1) * (int64_t)device_cus();
+      const int64_t slots =
+          (int64_t)(PA_LATENT_SLOTS_X * (vd <= 128 && ng == 1 ? 2 : 1) * device_cus());
       chunk = latent_chunk(c, b, a, hl, ng, slots,
                            std::max(256, 63 * c->block_size / 32 * 32));
     } else if (units >= target) {
