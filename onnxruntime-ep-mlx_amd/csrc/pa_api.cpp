@@ -211,6 +211,9 @@ struct HostLens {
 #ifndef PA_LATENT_SLOTS_X
 #define PA_LATENT_SLOTS_X 2.0
 #endif
+#ifndef PA_LATENT_ODD_SPLITS
+#define PA_LATENT_ODD_SPLITS 1
+#endif
 constexpr int kLatPlanMaxBatch = 4096;  // batches beyond this keep the capacity rule (host cost)
 
 // LATENT kernel: the context chunk (a multiple of 32 keys in [256, cap]) that minimises the
@@ -409,6 +412,14 @@ Plan make_plan(const pa_cache* c, const pa_batch* b, const pa_attn* a, pa_dtype 
     chunk = std::min(chunk, std::max(32, 63 * c->block_size / 32 * 32));
   pl.chunk = chunk;
   pl.max_splits = (int)std::max<int64_t>(1, ((int64_t)ctx + chunk - 1) / chunk);
+  // LATENT grid (row blocks, splits, sequences): workgroups go to the 8 XCDs round-robin by
+  // linear id, so with an even split count the same splits of every sequence land on the same
+  // XCDs (the early splits, which every sequence has, piling onto some of them).  An odd count
+  // (the extra workgroups exit at once) cycles each split over all XCDs: 16-head MLA decode over
+  // the config 3 contexts at 512-key chunks (16 splits) 160.3 -> 128.6 us per step.
+  if (pl.kind == 5 && PA_LATENT_ODD_SPLITS && pl.max_splits > 1 && pl.max_splits % 2 == 0 &&
+      pl.max_splits < 65535)
+    ++pl.max_splits;
   pl.part_rows = pl.max_splits > 1
                      ? (size_t)std::max(b->num_tokens, 0) * a->num_heads * pl.max_splits
                      : 0;
