@@ -215,15 +215,19 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
 }
 
 #ifndef PA_MERGE_ROUND
-#define PA_MERGE_ROUND 4  // eight per round measured slower (more registers, fewer waves)
+#define PA_MERGE_ROUND 4  // eight per round measured slower
 #endif
 
 // Merge the per-chunk partials of one (token, head): global max, rescaled sums, divide.
-// Partial rows have stride head_dim; outputs hold v_head_dim values per head.
+// Partial rows have stride head_dim; outputs hold v_head_dim values per head.  A workgroup of
+// four wavefronts per (head, token): thread x takes the value elements x, x + 256, ... (NE of
+// them), so each thread's loads of a round of split rows are few and all in flight together;
+// every wavefront computes the split weights itself (no exchange between them).  Each element
+// sums its split rows in split order.
 template <typename TT, int NE>
-__global__ __launch_bounds__(64) void split_reduce_kernel(const AttnParams p) {
+__global__ __launch_bounds__(256) void split_reduce_kernel(const AttnParams p) {
   const int h = blockIdx.x, t = blockIdx.y;
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int D = p.head_dim;
   const int VD = p.v_head_dim;
   const int b = seq_of_token(p.cum, p.batch, t);
@@ -259,9 +263,7 @@ __global__ __launch_bounds__(64) void split_reduce_kernel(const AttnParams p) {
       wl = (ms == kNegInf) ? 0.0f : exp2f(ms - M);
     }
     const int n = min(64, nsplit - s0);
-    // PA_MERGE_ROUND split rows per round: their loads are issued together (a chain of one row
-    // at a time left the wavefront waiting a memory latency per row); the sums keep the split
-    // order.
+    // PA_MERGE_ROUND split rows per round, their loads issued together
     constexpr int RND = PA_MERGE_ROUND;
     int k = 0;
     for (; k + RND <= n; k += RND) {
@@ -271,7 +273,7 @@ __global__ __launch_bounds__(64) void split_reduce_kernel(const AttnParams p) {
         const float* row = po + (int64_t)(s0 + k + u) * D;
 #pragma unroll
         for (int q = 0; q < NE; ++q) {
-          const int e = lane + 64 * q;
+          const int e = tid + 256 * q;
           v[u][q] = e < VD ? row[e] : 0.0f;
         }
       }
@@ -287,14 +289,14 @@ __global__ __launch_bounds__(64) void split_reduce_kernel(const AttnParams p) {
       const float* row = po + (int64_t)(s0 + k) * D;
 #pragma unroll
       for (int q = 0; q < NE; ++q) {
-        const int e = lane + 64 * q;
+        const int e = tid + 256 * q;
         if (e < VD) acc[q] += row[e] * wk;
       }
     }
   }
 #pragma unroll
   for (int q = 0; q < NE; ++q) {
-    const int e = lane + 64 * q;
+    const int e = tid + 256 * q;
     if (e < VD) out[((int64_t)t * p.num_heads + h) * VD + e] = TT::from_f32(acc[q] * f);
   }
 }
@@ -444,11 +446,11 @@ hipError_t launch_qk_t(const AttnParams& p, pa_dtype cache_dtype, void* qk, int 
 
 template <typename TT>
 void launch_reduce_t(const AttnParams& p, hipStream_t s) {
-  dim3 grid(p.num_heads, p.num_tokens), block(64);
-  if (ne_covers<4>(p.head_dim))
-    hipLaunchKernelGGL((split_reduce_kernel<TT, 4>), grid, block, 0, s, p);
+  dim3 grid(p.num_heads, p.num_tokens), block(256);
+  if (p.v_head_dim <= 256)
+    hipLaunchKernelGGL((split_reduce_kernel<TT, 1>), grid, block, 0, s, p);
   else
-    hipLaunchKernelGGL((split_reduce_kernel<TT, 10>), grid, block, 0, s, p);
+    hipLaunchKernelGGL((split_reduce_kernel<TT, 3>), grid, block, 0, s, p);
 }
 
 }  // namespace
