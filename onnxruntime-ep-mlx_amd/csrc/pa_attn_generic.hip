@@ -220,12 +220,13 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const AttnParams p) {
 
 // Merge the per-chunk partials of one (token, head): global max, rescaled sums, divide.
 // Partial rows have stride head_dim; outputs hold v_head_dim values per head.  A workgroup of
-// four wavefronts per (head, token): thread x takes the value elements x, x + 256, ... (NE of
-// them), so each thread's loads of a round of split rows are few and all in flight together;
-// every wavefront computes the split weights itself (no exchange between them).  Each element
-// sums its split rows in split order.
-template <typename TT, int NE>
-__global__ __launch_bounds__(256) void split_reduce_kernel(const AttnParams p) {
+// NT threads (one or four wavefronts) per (head, token): thread x takes the value elements x,
+// x + NT, ... (NE of them); with four wavefronts each thread's loads of a round of split rows
+// are few and all in flight together (few (head, token) pairs), with one the workgroups are
+// cheaper (many pairs).  Every wavefront computes the split weights itself (no exchange between
+// them).  Each element sums its split rows in split order.
+template <typename TT, int NE, int NT>
+__global__ __launch_bounds__(NT) void split_reduce_kernel(const AttnParams p) {
   const int h = blockIdx.x, t = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
   const int D = p.head_dim;
@@ -273,7 +274,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const AttnParams p) {
         const float* row = po + (int64_t)(s0 + k + u) * D;
 #pragma unroll
         for (int q = 0; q < NE; ++q) {
-          const int e = tid + 256 * q;
+          const int e = tid + NT * q;
           v[u][q] = e < VD ? row[e] : 0.0f;
         }
       }
@@ -289,14 +290,14 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const AttnParams p) {
       const float* row = po + (int64_t)(s0 + k) * D;
 #pragma unroll
       for (int q = 0; q < NE; ++q) {
-        const int e = tid + 256 * q;
+        const int e = tid + NT * q;
         if (e < VD) acc[q] += row[e] * wk;
       }
     }
   }
 #pragma unroll
   for (int q = 0; q < NE; ++q) {
-    const int e = tid + 256 * q;
+    const int e = tid + NT * q;
     if (e < VD) out[((int64_t)t * p.num_heads + h) * VD + e] = TT::from_f32(acc[q] * f);
   }
 }
@@ -446,11 +447,20 @@ hipError_t launch_qk_t(const AttnParams& p, pa_dtype cache_dtype, void* qk, int 
 
 template <typename TT>
 void launch_reduce_t(const AttnParams& p, hipStream_t s) {
-  dim3 grid(p.num_heads, p.num_tokens), block(256);
-  if (p.v_head_dim <= 256)
-    hipLaunchKernelGGL((split_reduce_kernel<TT, 1>), grid, block, 0, s, p);
-  else
-    hipLaunchKernelGGL((split_reduce_kernel<TT, 3>), grid, block, 0, s, p);
+  dim3 grid(p.num_heads, p.num_tokens);
+  // four wavefronts per pair up to 4096 pairs (16 per CU), one beyond (LATENT decode at 16
+  // heads, 1024 pairs: merge 14.4 -> 8.4 us; at 128 heads, 8192 pairs: 22.3 us with one,
+  // 26.7 us with four)
+  if ((int64_t)p.num_heads * p.num_tokens <= 4096) {
+    if (p.v_head_dim <= 256)
+      hipLaunchKernelGGL((split_reduce_kernel<TT, 1, 256>), grid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((split_reduce_kernel<TT, 3, 256>), grid, dim3(256), 0, s, p);
+  } else if (p.v_head_dim <= 256) {
+    hipLaunchKernelGGL((split_reduce_kernel<TT, 4, 64>), grid, dim3(64), 0, s, p);
+  } else {
+    hipLaunchKernelGGL((split_reduce_kernel<TT, 10, 64>), grid, dim3(64), 0, s, p);
+  }
 }
 
 }  // namespace
