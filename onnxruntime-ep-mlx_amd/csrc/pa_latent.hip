@@ -16,10 +16,12 @@
 //     online softmax;
 //   - accumulates P . V for its quarter of the value dims (VD / 4 columns), P split into hi + lo
 //     16-bit parts, from value-row slices of the step's rows.
-// Paged steps (block size a multiple of 16, every row in the pages) go through a three-slot LDS
-// ring: each 32-row step is copied to LDS by direct loads of whole 128-byte lines, two steps
-// ahead, and both the key operands and the value-row slices are read from there, so every row
-// byte leaves HBM once per workgroup.  Other steps (new rows from the batch, other block sizes)
+// Paged steps (block size a multiple of 16, every row in the pages, rows of at most 576 dims) go
+// through an LDS ring of four slots (one row group) or three (two): each 32-row step is copied
+// to LDS by direct loads of whole 128-byte lines, every slot but the one being read in flight,
+// and both the key operands and the value-row slices are read from there, so every row byte
+// leaves HBM once per workgroup; the step's one barrier (the partial-score exchange) also
+// publishes the next step.  Other steps (new rows from the batch, other block sizes, longer rows)
 // use a three-slot register ring loaded straight from the rows (key pieces of 64 bytes per row
 // and instruction, the value slices read a second time: L2 hits).  Partials of split chunks go
 // to the workspace at row (token * H + head) * max_splits + split (stride D), merged by
