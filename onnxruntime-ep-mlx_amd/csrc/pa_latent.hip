@@ -17,11 +17,10 @@
 //   - accumulates P . V for its quarter of the value dims (VD / 4 columns), P split into hi + lo
 //     16-bit parts, from value-row slices of the step's rows.
 // Paged steps (block size a multiple of 16, every row in the pages, rows of at most 576 dims) go
-// through an LDS ring of four slots (one row group) or three (two): each 32-row step is copied
-// to LDS by direct loads of whole 128-byte lines, every slot but the one being read in flight,
-// and both the key operands and the value-row slices are read from there, so every row byte
-// leaves HBM once per workgroup; the step's one barrier (the partial-score exchange) also
-// publishes the next step.  Other steps (new rows from the batch, other block sizes, longer rows)
+// through a three-slot LDS ring: each 32-row step is copied to LDS by direct loads of whole
+// 128-byte lines, every slot but the one being read in flight, and both the key operands and
+// the value-row slices are read from there, so every row byte leaves HBM once per workgroup;
+// the step's one barrier (the partial-score exchange) also publishes the next step.  Other steps (new rows from the batch, other block sizes, longer rows)
 // use a three-slot register ring loaded straight from the rows (key pieces of 64 bytes per row
 // and instruction, the value slices read a second time: L2 hits).  Partials of split chunks go
 // to the workspace at row (token * H + head) * max_splits + split (stride D), merged by
@@ -41,12 +40,13 @@ constexpr int kLatMaxKs = 20;  // k-steps of 32 dims in a key row: D <= 640
 #define PA_LATENT_LDS 1  // paged steps staged in LDS by direct loads (else the register ring)
 #endif
 #ifndef PA_LATENT_LDS_SLOTS1
-#define PA_LATENT_LDS_SLOTS1 4
+#define PA_LATENT_LDS_SLOTS1 3
 #endif
 // LDS ring of paged steps: slots of 32 rows x D / 8 16-byte pieces for D <= 576 (the MLA
-// 576-dim rows): four slots (steps issued three ahead) with one row group, whose partial-score
-// buffer leaves exactly that room in the 160 KiB, three with two.  Longer rows take the
-// register ring.
+// 576-dim rows), three of them (124 KiB of LDS with one row group's partial-score buffer, 140
+// KiB with two).  Four slots with one row group (exactly the 160 KiB) measured the same once
+// every slot prefetches (16-head step 118.4 against 117.9 us).  Longer rows take the register
+// ring.
 constexpr int kLatLdsMaxD = 576;
 constexpr int kLatSlotChunks = 32 * kLatLdsMaxD / 8;
 template <int NG>
